@@ -1,0 +1,146 @@
+/*
+ * sgsa.h -- C ABI of libsgsa_hip.so, the MI355X (gfx950) SGSA layer-forward
+ * library.  Plain pointers and sizes only; every entry point is asynchronous
+ * on the caller's HIP stream (passed as void*, NULL = default stream), never
+ * allocates device memory and never synchronises.  Device buffers are owned
+ * by the caller.
+ *
+ * Layouts (the reference's, modelings/sgsa_ops/naive.py:24-29):
+ *   q, k, v, sparse_k, sparse_v, k_hat, v_hat, write_key, out : [B,T,H,D], D contiguous
+ *   beta, gamma, alpha, budget                                : [B,T,H] fp32
+ *   initial_state, final_state                                : [B,H,D,D] fp32 (key-major)
+ *   indices, scores, weights                                  : [B,H,Tq,top_k]
+ *   top2 : [B,H,Tq,2]   counts : [B,H,Tq]   diag : [SGSA_NDIAG,B,H,Tq]
+ * dtype: SGSA_F32 or SGSA_BF16 for q/k/v-like tensors; everything else is
+ * fp32 (int32 for indices/counts).  D <= 128.
+ *
+ * Return value: SGSA_OK (0) or an sgsa_status; sgsa_last_error() gives the
+ * message of the last failure on the calling thread.  Unsupported input is an
+ * error, never a silent fallback.
+ */
+#ifndef SGSA_H_
+#define SGSA_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SGSA_ABI_VERSION 1
+#define SGSA_NDIAG 10
+
+enum sgsa_status {
+  SGSA_OK = 0,
+  SGSA_ERR_INVALID_ARG = 1,
+  SGSA_ERR_UNSUPPORTED = 2,
+  SGSA_ERR_HIP = 3,
+  SGSA_ERR_WORKSPACE = 4
+};
+
+enum sgsa_dtype { SGSA_F32 = 0, SGSA_BF16 = 1 };
+
+/* Order of the diagnostics planes written by sgsa_sparse_gather
+ * (modelings/modeling_sgsa.py:385-404). */
+enum sgsa_diag {
+  SGSA_DIAG_SCORE_MARGIN = 0,
+  SGSA_DIAG_CONCENTRATION = 1,
+  SGSA_DIAG_MAX_CONFIDENCE = 2,
+  SGSA_DIAG_NOVELTY = 3,
+  SGSA_DIAG_WRITE_CONFLICT = 4,
+  SGSA_DIAG_ENTROPY = 5,
+  SGSA_DIAG_AVG_DISTANCE = 6,
+  SGSA_DIAG_LOCAL_RATIO = 7,
+  SGSA_DIAG_SINK_RATIO = 8,
+  SGSA_DIAG_REMOTE_RATIO = 9
+};
+
+int sgsa_abi_version(void);
+const char* sgsa_status_string(int status);
+const char* sgsa_last_error(void);
+
+/* ---- chunked gated-delta-rule core ------------------------------------------
+ * Replaces chunk_sgsa_fwd (modelings/sgsa_ops/chunk_fwd.py:12-131), reached
+ * through chunk_sgsa / ChunkSGSAFunction.forward (modelings/sgsa_ops/chunk.py:
+ * 104-148, :17-56).  sparse_k, sparse_v, alpha: all three NULL = no sparse
+ * write (chunk.py:123).  initial_state NULL = zeros; final_state NULL = not
+ * requested.  chunk_size is accepted for signature compatibility; the kernels
+ * always use 64-token chunks (the result does not depend on it beyond
+ * rounding).  Needs sgsa_chunk_fwd_workspace_size() bytes of workspace. */
+int sgsa_chunk_fwd_workspace_size(int B, int T, int H, int D, int has_sparse, size_t* bytes);
+int sgsa_chunk_fwd(int dtype, int B, int T, int H, int D, int chunk_size,
+                   const void* q, const void* k, const void* v,
+                   const float* beta, const float* gamma,
+                   const void* sparse_k, const void* sparse_v, const float* alpha,
+                   const float* initial_state,
+                   void* out, float* final_state,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- score GEMM + exact token top-k ----------------------------------------
+ * Replaces the dense scores and the per-row top-k loop of
+ * SparseRetriever.forward / _masked_topk (modelings/modeling_sgsa.py:420-428,
+ * :144-165) and of TopKSparseKVReuseAttention.forward
+ * (modelings/hybrid_dense_delta_topk.py:343-349).  score = (q.k)/scale for
+ * scale_mode 0 (retriever: scale = sqrt(D)), (q.k)*scale for scale_mode 1
+ * (hybrid: scale = 1/sqrt(D)).  Query row r sits at key position r+q_offset;
+ * causal keeps keys <= that position.  Each row gets
+ * counts = min(top_k, valid keys) selected slots, ties broken by lowest key
+ * index; slots >= counts hold index 0 and score -FLT_MAX (:151-153).
+ * sorted = 0: selected slots in ascending key index; sorted = 1: (score desc,
+ * index asc) as torch.topk(sorted=True) with the lowest-index tie rule.
+ * top2 (may be NULL) receives the two largest valid scores (-FLT_MAX if absent). */
+int sgsa_score_topk(int dtype, int B, int Tq, int Tk, int H, int D, int top_k,
+                    int causal, int q_offset, float scale, int scale_mode,
+                    const void* q, const void* k,
+                    int32_t* indices, float* scores, float* top2, int32_t* counts,
+                    int sorted, void* stream);
+
+/* Known-answer hook: writes the exact fp32 scores sgsa_score_topk selects on,
+ * for query rows [row0, row0+rows), to out [B,H,rows,Tk]; keys outside the
+ * causal range get -FLT_MAX. */
+int sgsa_score_dump(int dtype, int B, int Tq, int Tk, int H, int D,
+                    int causal, int q_offset, float scale, int scale_mode,
+                    const void* q, const void* k, int row0, int rows, float* out, void* stream);
+
+/* ---- sparse gather + weights + diagnostics + write gate ---------------------
+ * Replaces the softmax/gather of SparseRetriever._token_only
+ * (modelings/modeling_sgsa.py:126-134), its _diagnostics (:361-405), the write
+ * key and alpha gate of SGSAStateLayer (:546-552, :497-504), and the V-only
+ * gather of TopKSparseKVReuseAttention (hybrid_dense_delta_topk.py:350-356;
+ * pass k = NULL, k_hat = NULL).  Consumes sgsa_score_topk's output (either
+ * order).  self_key [B,Tq,H,D]: key of each query token (the retriever's
+ * self_key = k, :459); needed for diag and for the gate.  budget NULL = no
+ * gate (write_key/alpha untouched); else alpha = alpha_max * concentration *
+ * novelty * sigmoid(budget), clipped (:497-504), write_mode 0 direct / 1
+ * residual.  weights, diag, k_hat, write_key, alpha may be NULL.  workspace:
+ * >= 256 bytes when diag is requested, else may be NULL. */
+int sgsa_sparse_gather(int dtype, int B, int Tq, int Tk, int H, int D, int top_k, int q_offset,
+                       const void* k, const void* v, const void* self_key,
+                       const int32_t* indices, const float* scores, const float* top2,
+                       const int32_t* counts,
+                       const float* budget, int write_mode, float alpha_max, float tau_c,
+                       int local_window, int sink_size,
+                       void* k_hat, void* v_hat, void* write_key, float* alpha,
+                       float* weights, float* diag,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- whole SGSA layer forward ------------------------------------------------
+ * The attention half of SGSABlock.forward (modelings/modeling_sgsa.py:669-684)
+ * with the projections as inputs: token top-k retrieval on (q_ret, k, v)
+ * (causal, scale sqrt(D)), write key + alpha gate from budget logits, then
+ * chunk_sgsa(q, k, v, beta, gamma, write_key, v_hat, alpha, initial_state)
+ * (:584-596).  out [B,T,H,D] dtype; final_state [B,H,D,D] fp32 or NULL. */
+int sgsa_layer_fwd_workspace_size(int dtype, int B, int T, int H, int D, int top_k, size_t* bytes);
+int sgsa_layer_fwd(int dtype, int B, int T, int H, int D, int top_k, int chunk_size,
+                   const void* q, const void* k, const void* v, const void* q_ret,
+                   const float* beta, const float* gamma, const float* budget,
+                   const float* initial_state, int write_mode, float alpha_max, float tau_c,
+                   void* out, float* final_state,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SGSA_H_ */

@@ -1,0 +1,509 @@
+"""CPU restatement of the SGSA layer-forward hot path.
+
+TEST INFRASTRUCTURE ONLY.  This module is the checker the HIP kernels are
+compared against.  Only ``tests/``, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py`` may import it; nothing under
+``sgsa_amd/`` may, and the product path never falls back to it.
+
+Everything here is plain PyTorch on the CPU, written from the reference's
+behaviour (FAndromedA/sgsa, paths relative to the repository root):
+
+* ``naive_recurrent_sgsa``  -- modelings/sgsa_ops/naive.py:10-57
+* ``chunk_sgsa_fwd``        -- modelings/sgsa_ops/chunk_fwd.py:12-131 (torch branch)
+* ``masked_topk``           -- modelings/modeling_sgsa.py:144-165, with the
+                               tie rule fixed to (score desc, index asc)
+* ``token_topk_retrieval``  -- modelings/modeling_sgsa.py:407-474, token_only
+                               mode :113-142, diagnostics :361-405
+* ``write_key`` / ``compute_alpha`` -- modelings/modeling_sgsa.py:543-552, :497-504
+* ``topk_kv_reuse_attention`` -- modelings/hybrid_dense_delta_topk.py:330-358
+                               (V-only gather, ``finfo.min`` masking, no valid mask)
+* ``make_inputs``           -- the seeded synthetic inputs of the benchmark configs
+
+How each function is pinned (tests/test_oracle.py):
+
+* recurrence: T=1 and T=2 closed forms written out by hand, the GDN transition
+  form ``S_t = g_t (I - b k k^T) S_{t-1} + b k v^T`` (an algebraically different
+  statement), decay-only and exact-overwrite special cases, and a planted
+  mistake (sparse residual read from the updated state) that must fail;
+* chunk form: equality with the recurrence for several chunk sizes including
+  a ragged tail (the reference's own 1e-5 test), and state continuation;
+* top-k: brute force with Python ``sorted`` on tiny rows with ties and -0.0,
+  causality, the t<k row counts and the padded-slot convention;
+* retrieval/diagnostics/gate: explicit Python loops on tiny inputs, sums of
+  weights, k_hat parallel/orthogonal novelty limits, alpha range and clip.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Dict, Optional, Tuple
+
+import torch
+import torch.nn.functional as F
+
+Tensor = torch.Tensor
+
+__all__ = [
+    "naive_recurrent_sgsa",
+    "chunk_sgsa_fwd",
+    "topk_lowest_index",
+    "masked_topk",
+    "token_topk_retrieval",
+    "write_key",
+    "compute_alpha",
+    "sgsa_layer_forward",
+    "topk_kv_reuse_attention",
+    "make_inputs",
+    "CONFIGS",
+]
+
+
+# ---------------------------------------------------------------------------
+# Recurrence (parity target)
+# ---------------------------------------------------------------------------
+
+def naive_recurrent_sgsa(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    beta: Tensor,
+    gamma: Tensor,
+    sparse_k: Optional[Tensor] = None,
+    sparse_v: Optional[Tensor] = None,
+    alpha: Optional[Tensor] = None,
+    initial_state: Optional[Tensor] = None,
+    output_final_state: bool = False,
+) -> Tuple[Tensor, Optional[Tensor]]:
+    """Token-by-token SGSA recurrence (modelings/sgsa_ops/naive.py:34-57).
+
+    Per token: ``base = gamma_t * S``; the local residual and the sparse
+    residual both read ``base`` (naive.py:40-53); output ``o_t = S^T q_t``
+    (naive.py:55).  Shapes: q,k,v,sparse_* [B,T,H,D]; beta,gamma,alpha [B,T,H];
+    state [B,H,Dk,Dv].  Computes in the dtype of ``q``.
+    """
+    bsz, seq_len, heads, dk = q.shape
+    dv = v.shape[-1]
+    if initial_state is None:
+        state = q.new_zeros(bsz, heads, dk, dv)
+    else:
+        state = initial_state.to(q.dtype).clone()
+    has_sparse = sparse_k is not None and sparse_v is not None and alpha is not None
+    outs = []
+    for t in range(seq_len):
+        base = gamma[:, t, :, None, None] * state
+        k_t, v_t = k[:, t], v[:, t]
+        pred = torch.einsum("bhde,bhd->bhe", base, k_t)
+        state = base + k_t[..., :, None] * ((v_t - pred) * beta[:, t, :, None])[..., None, :]
+        if has_sparse:
+            sk, sv = sparse_k[:, t], sparse_v[:, t]
+            pred_s = torch.einsum("bhde,bhd->bhe", base, sk)
+            state = state + sk[..., :, None] * ((sv - pred_s) * alpha[:, t, :, None])[..., None, :]
+        outs.append(torch.einsum("bhde,bhd->bhe", state, q[:, t]))
+    out = torch.stack(outs, dim=1) if outs else q.new_zeros(bsz, 0, heads, dv)
+    return out, (state if output_final_state else None)
+
+
+def chunk_sgsa_fwd(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    beta: Tensor,
+    gamma: Tensor,
+    sparse_k: Optional[Tensor] = None,
+    sparse_v: Optional[Tensor] = None,
+    alpha: Optional[Tensor] = None,
+    initial_state: Optional[Tensor] = None,
+    chunk_size: int = 64,
+    output_final_state: bool = False,
+) -> Tuple[Tensor, Optional[Tensor]]:
+    """Chunked SGSA forward, torch branch of modelings/sgsa_ops/chunk_fwd.py:12-131.
+
+    Virtual samples interleave (local, sparse) per token (chunk_fwd.py:53-56);
+    ``D`` is the inclusive chunk-local cumprod of ``gamma.clamp_min(1e-6)``
+    (:46, :70-71); ``rhs = nu - D_tau * (kappa S0)`` (:73-74); the transition
+    ``T_ij = 1[tau_j < tau_i] lam_j D_tau_i / max(D_tau_j, 1e-6) (kappa_i . kappa_j)``
+    (:86-87) is solved with ``solve_triangular`` (:89); readout uses the
+    ``tau_i <= t`` mask (:120); the final state is :109-115.  The state is
+    carried in the compute dtype (fp32 for low-precision inputs).
+    """
+    bsz, seq_len, heads, dk = q.shape
+    dv = v.shape[-1]
+    cdt = torch.float32 if q.dtype in (torch.float16, torch.bfloat16) else q.dtype
+    state = (q.new_zeros(bsz, heads, dk, dv, dtype=cdt) if initial_state is None
+             else initial_state.to(cdt))
+    has_sparse = sparse_k is not None and sparse_v is not None and alpha is not None
+    outs = []
+    for start in range(0, seq_len, chunk_size):
+        end = min(start + chunk_size, seq_len)
+        n = end - start
+        qc = q[:, start:end].to(cdt)
+        kc = k[:, start:end].to(cdt)
+        vc = v[:, start:end].to(cdt)
+        bc = beta[:, start:end].to(cdt)
+        gc = gamma[:, start:end].to(cdt).clamp_min(1e-6)
+        if has_sparse:
+            kap = torch.stack((kc, sparse_k[:, start:end].to(cdt)), 2).reshape(bsz, 2 * n, heads, dk)
+            nu = torch.stack((vc, sparse_v[:, start:end].to(cdt)), 2).reshape(bsz, 2 * n, heads, dv)
+            lam = torch.stack((bc, alpha[:, start:end].to(cdt)), 2).reshape(bsz, 2 * n, heads)
+            tau = torch.arange(n).repeat_interleave(2)
+        else:
+            kap, nu, lam, tau = kc, vc, bc, torch.arange(n)
+        kap = kap.transpose(1, 2)           # [B,H,M,Dk]
+        nu = nu.transpose(1, 2)             # [B,H,M,Dv]
+        lam = lam.transpose(1, 2)           # [B,H,M]
+        qh = qc.transpose(1, 2)             # [B,H,n,Dk]
+        prefix = torch.cumprod(gc.transpose(1, 2), dim=-1)   # [B,H,n]
+        ptau = prefix[..., tau]                              # [B,H,M]
+        rhs = nu - ptau[..., None] * torch.einsum("bhde,bhmd->bhme", state, kap)
+        gram = kap @ kap.transpose(-1, -2)
+        dep = (tau[None, :] < tau[:, None]).to(cdt)
+        decay = ptau[..., :, None] / ptau[..., None, :].clamp_min(1e-6)
+        trans = dep * lam[..., None, :] * decay * gram
+        eye = torch.eye(kap.shape[2], dtype=cdt)
+        resid = torch.linalg.solve_triangular(trans + eye, rhs, upper=False)
+        # readout: o_t = D_t S0^T q_t + sum_{tau_i <= t} lam_i D_t / D_tau_i (q_t.kappa_i) R_i
+        read_mask = (tau[None, :] <= torch.arange(n)[:, None]).to(cdt)          # [n,M]
+        read_w = read_mask * lam[..., None, :] * (prefix[..., :, None] / ptau[..., None, :].clamp_min(1e-6))
+        qk = qh @ kap.transpose(-1, -2)                                         # [B,H,n,M]
+        o = prefix[..., None] * (qh @ state) + (qk * read_w) @ resid
+        outs.append(o.transpose(1, 2).to(q.dtype))
+        final = prefix[..., -1]
+        tail = final[..., None] / ptau.clamp_min(1e-6)
+        state = final[..., None, None] * state + kap.transpose(-1, -2) @ (resid * (lam * tail)[..., None])
+    out = torch.cat(outs, dim=1) if outs else q.new_zeros(bsz, 0, heads, dv)
+    return out, (state if output_final_state else None)
+
+
+# ---------------------------------------------------------------------------
+# Retrieval (token_only)
+# ---------------------------------------------------------------------------
+
+def topk_lowest_index(x: Tensor, k: int) -> Tuple[Tensor, Tensor]:
+    """Exact top-k of each row of a 2-D tensor, ordered (value desc, index asc).
+
+    ``torch.topk`` is used only for the k-th value (which is tie-independent);
+    membership then takes every element above it plus the lowest-index elements
+    equal to it, and a stable descending sort orders the result.  -0.0 and +0.0
+    compare equal, as IEEE comparison (and torch.topk) treat them.
+    """
+    rows, n = x.shape
+    if k == 0 or rows == 0:
+        return x.new_zeros(rows, k), torch.zeros(rows, k, dtype=torch.long)
+    kth = torch.topk(x, k, dim=-1, largest=True, sorted=True).values[:, k - 1:k]
+    above = x > kth
+    eq = x == kth
+    need = k - above.sum(-1, keepdim=True)
+    eq_rank = torch.cumsum(eq.to(torch.int64), dim=-1) - 1
+    sel = above | (eq & (eq_rank < need))
+    idx = torch.nonzero(sel)[:, 1].reshape(rows, k)            # ascending per row
+    vals = x.gather(1, idx)
+    order = torch.sort(vals, dim=-1, descending=True, stable=True).indices
+    return vals.gather(1, order), idx.gather(1, order)
+
+
+def masked_topk(scores: Tensor, valid_mask: Tensor, topk: int) -> Tuple[Tensor, Tensor, Tensor]:
+    """Fixed-size masked top-k (modelings/modeling_sgsa.py:144-165).
+
+    Invalid entries are filled with ``finfo(dtype).min`` (:150, :158).  The row
+    count ``k_q = min(topk, max(valid_count, 1))`` uses the maximum valid count
+    over (B,H) (:159-160).  Slots >= k_q keep score=min, index=0, valid=False
+    (:151-153).  Ties are broken by lowest index (the reference leaves this to
+    torch.topk; the port fixes it).
+    scores/valid_mask: [B,H,Q,K].  Returns scores [B,H,Q,topk], int64 indices,
+    bool valid.
+    """
+    bsz, heads, qn, kn = scores.shape
+    fmin = torch.finfo(scores.dtype).min
+    masked = scores.masked_fill(~valid_mask, fmin)
+    vc = valid_mask.sum(-1).amax(dim=(0, 1))                          # [Q]
+    kq = torch.clamp(torch.clamp(vc, min=1), max=topk)                # [Q]
+    vals, idx = topk_lowest_index(masked.reshape(-1, kn), topk)
+    vals = vals.reshape(bsz, heads, qn, topk)
+    idx = idx.reshape(bsz, heads, qn, topk)
+    valid = valid_mask.gather(-1, idx)
+    slot = torch.arange(topk)
+    live = slot[None, None, None, :] < kq[None, None, :, None]
+    vals = torch.where(live, vals, torch.full_like(vals, fmin))
+    idx = torch.where(live, idx, torch.zeros_like(idx))
+    valid = valid & live
+    return vals, idx, valid
+
+
+def token_topk_retrieval(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    top_k: int,
+    causal: bool = True,
+    attention_mask: Optional[Tensor] = None,
+    tau_c: float = 0.1,
+    local_window: int = 64,
+    sink_size: int = 8,
+    eps: float = 1e-6,
+    block_rows: int = 256,
+) -> Dict[str, object]:
+    """Token top-k retrieval (SparseRetriever.forward, modelings/modeling_sgsa.py:407-474).
+
+    Scores ``q k^T / sqrt(d)`` (:420) are computed query-block by query-block
+    (the reference materialises [B,H,T,T]); valid mask is causal & key/query
+    padding (:421-428); weights are ``softmax(fp32 scores) * valid`` renormalised
+    with ``clamp_min(eps)`` (:126-128); k_hat/v_hat are weighted sums of the
+    selected rows (:130-134).  Diagnostics follow :361-405 with
+    ``self_key = k`` (:459).  Inputs [B,T,H,D]; k_hat/v_hat returned [B,T,H,D];
+    everything else [B,H,T,*].
+    """
+    bsz, seq_len, heads, dk = q.shape
+    dtype = q.dtype
+    qh, kh, vh = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
+    topk = min(top_k, seq_len)
+    sc = math.sqrt(dk)
+    out_scores = []
+    out_idx = []
+    out_w = []
+    out_kh = []
+    out_vh = []
+    pos = torch.arange(seq_len)
+    key_valid = attention_mask.to(torch.bool) if attention_mask is not None else None
+    for r0 in range(0, seq_len, block_rows):
+        r1 = min(seq_len, r0 + block_rows)
+        scores = torch.matmul(qh[:, :, r0:r1], kh.transpose(-2, -1)) / sc
+        if causal:
+            valid = (pos[None, :] <= pos[r0:r1, None])[None, None].expand(bsz, heads, -1, -1)
+        else:
+            valid = torch.ones(bsz, heads, r1 - r0, seq_len, dtype=torch.bool)
+        if key_valid is not None:
+            valid = valid & key_valid[:, None, None, :] & key_valid[:, None, r0:r1, None]
+        ts, ti, tv = masked_topk(scores, valid, topk)
+        w = F.softmax(ts.float(), dim=-1).to(dtype)
+        w = w * tv.to(dtype)
+        w = w / w.sum(-1, keepdim=True).clamp_min(eps)
+        gk = kh[:, :, None, :, :].expand(-1, -1, r1 - r0, -1, -1).gather(
+            3, ti[..., None].expand(-1, -1, -1, -1, dk))
+        gv = vh[:, :, None, :, :].expand(-1, -1, r1 - r0, -1, -1).gather(
+            3, ti[..., None].expand(-1, -1, -1, -1, vh.shape[-1]))
+        out_kh.append((w[..., None] * gk).sum(3))
+        out_vh.append((w[..., None] * gv).sum(3))
+        out_scores.append(ts)
+        out_idx.append(ti)
+        out_w.append(w)
+    scores = torch.cat(out_scores, 2)
+    idx = torch.cat(out_idx, 2)
+    weights = torch.cat(out_w, 2)
+    k_hat = torch.cat(out_kh, 2)                   # [B,H,T,D]
+    v_hat = torch.cat(out_vh, 2)
+    diag = retrieval_diagnostics(scores, weights, idx, k_hat, kh, tau_c, local_window, sink_size, eps)
+    return {
+        "indices": idx,
+        "block_indices": None,
+        "weights": weights,
+        "scores": scores,
+        "k_hat": k_hat.transpose(1, 2),
+        "v_hat": v_hat.transpose(1, 2),
+        "diagnostics": diag,
+    }
+
+
+def retrieval_diagnostics(
+    scores: Tensor,
+    weights: Tensor,
+    indices: Tensor,
+    k_hat: Tensor,
+    self_key: Tensor,
+    tau_c: float = 0.1,
+    local_window: int = 64,
+    sink_size: int = 8,
+    eps: float = 1e-6,
+) -> Dict[str, Tensor]:
+    """SparseRetriever._diagnostics (modelings/modeling_sgsa.py:361-405).  [B,H,T,*] layout."""
+    if scores.shape[-1] >= 2:
+        margin = scores[..., 0] - scores[..., 1]
+    else:
+        margin = torch.zeros_like(scores[..., 0])
+    concentration = torch.sigmoid(margin / max(tau_c, eps))
+    max_conf = weights.max(dim=-1).values
+    dot = (k_hat * self_key).sum(-1)
+    self_norm = self_key.norm(dim=-1).clamp_min(eps)
+    kh_norm = k_hat.norm(dim=-1).clamp_min(eps)
+    proj = dot / (self_norm * self_norm + eps)
+    k_perp = k_hat - proj[..., None] * self_key
+    novelty = (k_perp.norm(dim=-1) / (kh_norm + eps)).clamp(0.0, 1.0)
+    conflict = (dot / (self_norm * kh_norm + eps)).clamp(-1.0, 1.0)
+    wc = weights.clamp_min(eps)
+    entropy = -(wc * wc.log()).sum(-1)
+    out = {
+        "score_margin": margin,
+        "concentration": concentration,
+        "max_confidence": max_conf,
+        "novelty": novelty,
+        "write_conflict": conflict,
+        "entropy": entropy,
+    }
+    seq_len = int(indices.max().item()) + 1 if indices.numel() > 0 else 1
+    qpos = torch.arange(indices.shape[2]).view(1, 1, -1, 1)
+    dist = (qpos - indices).clamp_min(0)
+    out["avg_distance"] = dist.float().mean(-1) / max(seq_len, 1)
+    out["local_ratio"] = (dist <= local_window).float().mean(-1)
+    out["sink_ratio"] = (indices < sink_size).float().mean(-1)
+    out["remote_ratio"] = ((dist > local_window) & (indices >= sink_size)).float().mean(-1)
+    return out
+
+
+# ---------------------------------------------------------------------------
+# Write gate (SGSAStateLayer)
+# ---------------------------------------------------------------------------
+
+def write_key(k_hat: Tensor, k: Tensor, mode: str = "direct", eps: float = 1e-6) -> Tensor:
+    """Write key of SGSAStateLayer.forward (modelings/modeling_sgsa.py:546-551)."""
+    if mode == "direct":
+        return k_hat
+    if mode == "residual":
+        dot = (k_hat * k).sum(-1)
+        nsq = (k * k).sum(-1).clamp_min(eps)
+        return k_hat - (dot / nsq)[..., None] * k
+    raise ValueError(f"unknown write mode {mode!r}")
+
+
+def compute_alpha(
+    concentration: Tensor,
+    novelty: Tensor,
+    budget_logits: Tensor,
+    wkey: Tensor,
+    v_hat: Tensor,
+    alpha_max: float = 0.25,
+) -> Tensor:
+    """SGSAStateLayer._compute_alpha (modelings/modeling_sgsa.py:497-504).
+
+    concentration/novelty [B,H,T]; budget_logits [B,T,H] (the output of
+    ``budget_proj``, before the sigmoid); wkey/v_hat [B,T,H,D].  Returns [B,T,H].
+    """
+    c = concentration.transpose(1, 2)
+    n = novelty.transpose(1, 2).clamp(0.0, 1.0)
+    a = alpha_max * c * n * torch.sigmoid(budget_logits)
+    proxy = a * v_hat.norm(dim=-1) * wkey.norm(dim=-1)
+    clip = torch.clamp(1.0 / proxy.clamp_min(1.0), max=1.0)
+    return a * clip
+
+
+def sgsa_layer_forward(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    q_ret: Tensor,
+    beta: Tensor,
+    gamma: Tensor,
+    budget_logits: Tensor,
+    top_k: int,
+    initial_state: Optional[Tensor] = None,
+    write_mode: str = "direct",
+    alpha_max: float = 0.25,
+    tau_c: float = 0.1,
+    use_chunk: bool = False,
+    chunk_size: int = 64,
+    block_rows: int = 256,
+) -> Dict[str, Tensor]:
+    """Op-level SGSA layer forward: retrieval -> gate -> state update.
+
+    Mirrors SGSABlock.forward's attention half (modelings/modeling_sgsa.py:669-684)
+    with the projections taken as inputs: retrieval on (q_ret, k, v), write key
+    and alpha (:546-552), then the recurrent state update (naive.py, or the
+    chunk form when ``use_chunk``).  Inputs are upcast to fp32.
+    """
+    f = lambda x: None if x is None else x.float()
+    q, k, v, q_ret, beta, gamma, budget_logits = map(f, (q, k, v, q_ret, beta, gamma, budget_logits))
+    ret = token_topk_retrieval(q_ret, k, v, top_k, tau_c=tau_c, block_rows=block_rows)
+    wk = write_key(ret["k_hat"], k, write_mode)
+    alpha = compute_alpha(ret["diagnostics"]["concentration"], ret["diagnostics"]["novelty"],
+                          budget_logits, wk, ret["v_hat"], alpha_max)
+    if use_chunk:
+        o, st = chunk_sgsa_fwd(q, k, v, beta, gamma, wk, ret["v_hat"], alpha,
+                               f(initial_state), chunk_size, True)
+    else:
+        o, st = naive_recurrent_sgsa(q, k, v, beta, gamma, wk, ret["v_hat"], alpha,
+                                     f(initial_state), True)
+    return {"o": o, "final_state": st, "write_key": wk, "v_hat": ret["v_hat"],
+            "alpha": alpha, "retrieval": ret}
+
+
+# ---------------------------------------------------------------------------
+# Hybrid top-k KV reuse (V-only)
+# ---------------------------------------------------------------------------
+
+def topk_kv_reuse_attention(query: Tensor, key: Tensor, value: Tensor, top_k: int,
+                            attention_mask: Optional[Tensor] = None) -> Tuple[Tensor, Tensor, Tensor]:
+    """Core of TopKSparseKVReuseAttention.forward (modelings/hybrid_dense_delta_topk.py:343-356).
+
+    query [B,H,Q,D] (RoPE already applied), key/value [B,H,K,D]; queries sit at
+    positions K-Q .. K-1 (:153-156).  Scores are multiplied by 1/sqrt(d) (:343-344),
+    masked with ``finfo.min`` (:346) and every row keeps ``min(top_k, K)`` slots
+    (:348-349) with no valid mask; probabilities are a fp32 softmax (:350).
+    Returns (attended [B,H,Q,D], indices [B,H,Q,k], probs [B,H,Q,k]).
+    """
+    bsz, heads, qn, d = query.shape
+    kn = key.shape[-2]
+    scale = 1.0 / math.sqrt(d)
+    scores = torch.matmul(query, key.transpose(-2, -1)) * scale
+    qpos = torch.arange(kn - qn, kn)[:, None]
+    masked = torch.arange(kn)[None, :] > qpos
+    masked = masked[None, None].expand(bsz, heads, -1, -1)
+    if attention_mask is not None:
+        masked = masked | ~attention_mask.to(torch.bool)[:, None, None, :]
+    scores = scores.masked_fill(masked, torch.finfo(scores.dtype).min)
+    kk = min(top_k, kn)
+    vals, idx = topk_lowest_index(scores.reshape(-1, kn), kk)
+    vals = vals.reshape(bsz, heads, qn, kk)
+    idx = idx.reshape(bsz, heads, qn, kk)
+    probs = F.softmax(vals.float(), dim=-1).to(query.dtype)
+    gv = value[:, :, None].expand(-1, -1, qn, -1, -1).gather(3, idx[..., None].expand(-1, -1, -1, -1, d))
+    return (probs[..., None] * gv).sum(3), idx, probs
+
+
+# ---------------------------------------------------------------------------
+# Synthetic inputs
+# ---------------------------------------------------------------------------
+
+CONFIGS = {
+    0: dict(B=1, H=4, T=512, D=64, chunk=64, top_k=32, dtype=torch.float32),
+    1: dict(B=4, H=16, T=8192, D=128, chunk=64, top_k=256, dtype=torch.bfloat16),
+    "north_star": dict(B=1, H=16, T=32768, D=128, chunk=64, top_k=2048, dtype=torch.bfloat16),
+    3: dict(B=1, H=16, T=65536, D=128, chunk=64, top_k=2048, dtype=torch.bfloat16, heavy_tail=True),
+}
+
+
+def make_inputs(B: int, T: int, H: int, D: int, dtype=torch.float32, seed: int = 0,
+                heavy_tail: bool = False, with_budget: bool = True) -> Dict[str, Tensor]:
+    """Seeded synthetic inputs, drawn in a fixed order on a CPU generator.
+
+    q,k,v ~ N(0,1) [B,T,H,D]; beta = sigmoid(N(0,1)); g = logsigmoid(N(0,1)+4)
+    and gamma = exp(g); budget logits ~ N(0,1); q and k are L2-normalised per
+    head.  Low-precision configs round to ``dtype``; the returned fp32 copies
+    (``*_f32``) are those rounded values upcast, so the oracle and the kernels
+    see identical inputs.  With ``heavy_tail`` 1% of key positions per (b,h)
+    (``randperm`` on the same generator) are scaled x8 in a separate
+    retrieval-key tensor ``k_ret``; the state key stays unit-norm.
+    """
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, T, H, D, generator=g)
+    k = torch.randn(B, T, H, D, generator=g)
+    v = torch.randn(B, T, H, D, generator=g)
+    beta = torch.sigmoid(torch.randn(B, T, H, generator=g))
+    glog = F.logsigmoid(torch.randn(B, T, H, generator=g) + 4.0)
+    gamma = torch.exp(glog)
+    budget = torch.randn(B, T, H, generator=g) if with_budget else None
+    q = q / q.norm(dim=-1, keepdim=True)
+    k = k / k.norm(dim=-1, keepdim=True)
+    k_ret = k
+    if heavy_tail:
+        k_ret = k.clone()
+        n = int(round(0.01 * T))
+        for b in range(B):
+            for h in range(H):
+                sel = torch.randperm(T, generator=g)[:n]
+                k_ret[b, sel, h] *= 8.0
+    out = {"q": q, "k": k, "v": v, "beta": beta, "gamma": gamma, "g": glog, "budget": budget,
+           "k_ret": k_ret}
+    if dtype != torch.float32:
+        for name in ("q", "k", "v", "k_ret"):
+            out[name] = out[name].to(dtype)
+    for name in ("q", "k", "v", "k_ret"):
+        out[name + "_f32"] = out[name].float()
+    return out

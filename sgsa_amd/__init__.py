@@ -1,0 +1,25 @@
+"""SGSA layer forward on AMD MI355X (gfx950): HIP kernels behind a C ABI.
+
+Public entry points mirror FAndromedA/sgsa:
+  chunk_sgsa            -- modelings/sgsa_ops/chunk.py:104-148
+  SparseRetriever       -- modelings/modeling_sgsa.py:90-474 (token_only mode)
+  sparse_retrieve       -- functional form of SparseRetriever.forward
+  sgsa_layer_forward    -- retrieval + write gate + chunked state update in one call
+The compiled library (libsgsa_hip.so) is required; there is no fallback path.
+"""
+
+from .ops import ChunkSGSAFunction, chunk_sgsa, chunk_sgsa_fwd
+from .retrieval import SparseRetriever, score_dump, score_topk, sparse_retrieve
+from .layer import LayerWorkspace, sgsa_layer_forward
+
+__all__ = [
+    "ChunkSGSAFunction",
+    "chunk_sgsa",
+    "chunk_sgsa_fwd",
+    "SparseRetriever",
+    "score_topk",
+    "score_dump",
+    "sparse_retrieve",
+    "sgsa_layer_forward",
+    "LayerWorkspace",
+]

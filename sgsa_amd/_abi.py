@@ -1,0 +1,101 @@
+"""ctypes binding of libsgsa_hip.so (the C ABI declared in include/sgsa.h).
+
+The library is loaded from the package directory; if it is missing this
+raises -- there is no fallback implementation.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libsgsa_hip.so")
+
+SGSA_F32 = 0
+SGSA_BF16 = 1
+NDIAG = 10
+DIAG_NAMES = (
+    "score_margin",
+    "concentration",
+    "max_confidence",
+    "novelty",
+    "write_conflict",
+    "entropy",
+    "avg_distance",
+    "local_ratio",
+    "sink_ratio",
+    "remote_ratio",
+)
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_F = ctypes.c_float
+_SZ = ctypes.c_size_t
+
+# name -> (restype, argtypes)
+SIGNATURES = {
+    "sgsa_abi_version": (_I, []),
+    "sgsa_status_string": (ctypes.c_char_p, [_I]),
+    "sgsa_last_error": (ctypes.c_char_p, []),
+    "sgsa_chunk_fwd_workspace_size": (_I, [_I, _I, _I, _I, _I, ctypes.POINTER(_SZ)]),
+    "sgsa_chunk_fwd": (_I, [_I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),
+    "sgsa_score_topk": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _I, _F, _I, _P, _P, _P, _P, _P, _P, _I, _P]),
+    "sgsa_score_dump": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _F, _I, _P, _P, _I, _I, _P, _P]),
+    "sgsa_sparse_gather": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _I, _F, _F,
+                                _I, _I, _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),
+    "sgsa_layer_fwd_workspace_size": (_I, [_I, _I, _I, _I, _I, _I, ctypes.POINTER(_SZ)]),
+    "sgsa_layer_fwd": (_I, [_I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _I, _F, _F, _P, _P,
+                            _P, _SZ, _P]),
+}
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load (once) and return the HIP library with typed entry points."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is not built; run `python -m sgsa_amd.build`")
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = handle
+    return _lib
+
+
+class SGSAError(RuntimeError):
+    pass
+
+
+def check(status: int) -> None:
+    if status == 0:
+        return
+    L = lib()
+    msg = f"{L.sgsa_status_string(status).decode()}: {L.sgsa_last_error().decode()}"
+    if status in (1, 2, 4):
+        raise ValueError(msg)
+    raise SGSAError(msg)
+
+
+def ptr(t: Optional[torch.Tensor]):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def stream_of(t: torch.Tensor):
+    if t.is_cuda:
+        return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+    return None
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.float32:
+        return SGSA_F32
+    if dt == torch.bfloat16:
+        return SGSA_BF16
+    raise ValueError(f"unsupported dtype {dt}: the SGSA kernels take float32 or bfloat16")

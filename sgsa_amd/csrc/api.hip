@@ -1,0 +1,251 @@
+// C ABI of libsgsa_hip.so (declared in include/sgsa.h): argument validation,
+// workspace carving and kernel dispatch.  Validation runs on the host before
+// any HIP call, so the error paths are testable without a GPU.
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string>
+
+#include "../../include/sgsa.h"
+#include "kernels.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int status, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return status;
+}
+
+int hip_status(hipError_t e, const char* where) {
+  if (e == hipSuccess) return SGSA_OK;
+  return fail(SGSA_ERR_HIP, "%s: %s", where, hipGetErrorString(e));
+}
+
+constexpr size_t kAlign = 256;
+size_t align_up(size_t x) { return (x + kAlign - 1) & ~(kAlign - 1); }
+
+size_t dtype_size(int dtype) { return dtype == SGSA_F32 ? 4 : 2; }
+
+int check_dtype(int dtype) {
+  if (dtype != SGSA_F32 && dtype != SGSA_BF16) return fail(SGSA_ERR_INVALID_ARG, "dtype %d is not SGSA_F32 or SGSA_BF16", dtype);
+  return SGSA_OK;
+}
+
+int check_dims(int B, int T, int H, int D) {
+  if (B <= 0 || T <= 0 || H <= 0 || D <= 0) return fail(SGSA_ERR_INVALID_ARG, "shape B=%d T=%d H=%d D=%d must be positive", B, T, H, D);
+  if (D > 128) return fail(SGSA_ERR_UNSUPPORTED, "head dim D=%d > 128 is not supported", D);
+  if ((long)B * T * H * D > (1L << 40)) return fail(SGSA_ERR_UNSUPPORTED, "tensor too large");
+  if ((long)B * T > 0x7fffffffL) return fail(SGSA_ERR_UNSUPPORTED, "B*T too large for 32-bit token indexing");
+  return SGSA_OK;
+}
+
+#define REQUIRE(ptr) \
+  do { if ((ptr) == nullptr) return fail(SGSA_ERR_INVALID_ARG, "%s must not be NULL", #ptr); } while (0)
+
+struct LayerWs {
+  size_t idx, sc, top2, cnt, wk, vh, al, misc, chunk, total;
+};
+
+LayerWs layer_ws(int dtype, int B, int T, int H, int D, int top_k) {
+  LayerWs w{};
+  const size_t rows = (size_t)B * H * T;
+  const size_t kk = (size_t)(top_k < T ? top_k : T);
+  size_t off = 0;
+  w.idx = off; off = align_up(off + rows * kk * 4);
+  w.sc = off; off = align_up(off + rows * kk * 4);
+  w.top2 = off; off = align_up(off + rows * 2 * 4);
+  w.cnt = off; off = align_up(off + rows * 4);
+  w.wk = off; off = align_up(off + (size_t)B * T * H * D * dtype_size(dtype));
+  w.vh = off; off = align_up(off + (size_t)B * T * H * D * dtype_size(dtype));
+  w.al = off; off = align_up(off + (size_t)B * T * H * 4);
+  w.misc = off; off = align_up(off + 256);
+  w.chunk = off; off = align_up(off + sgsa::chunk_workspace_bytes(B, T, H, 1));
+  w.total = off + kAlign;
+  return w;
+}
+
+}  // namespace
+
+extern "C" {
+
+int sgsa_abi_version(void) { return SGSA_ABI_VERSION; }
+
+const char* sgsa_status_string(int status) {
+  switch (status) {
+    case SGSA_OK: return "ok";
+    case SGSA_ERR_INVALID_ARG: return "invalid argument";
+    case SGSA_ERR_UNSUPPORTED: return "unsupported shape or option";
+    case SGSA_ERR_HIP: return "HIP runtime error";
+    case SGSA_ERR_WORKSPACE: return "workspace too small";
+    default: return "unknown status";
+  }
+}
+
+const char* sgsa_last_error(void) { return g_last_error.c_str(); }
+
+int sgsa_chunk_fwd_workspace_size(int B, int T, int H, int D, int has_sparse, size_t* bytes) {
+  REQUIRE(bytes);
+  if (int s = check_dims(B, T, H, D)) return s;
+  *bytes = sgsa::chunk_workspace_bytes(B, T, H, has_sparse ? 1 : 0);
+  return SGSA_OK;
+}
+
+int sgsa_chunk_fwd(int dtype, int B, int T, int H, int D, int chunk_size, const void* q, const void* k,
+                   const void* v, const float* beta, const float* gamma, const void* sparse_k,
+                   const void* sparse_v, const float* alpha, const float* initial_state, void* out,
+                   float* final_state, void* workspace, size_t workspace_bytes, void* stream) {
+  if (int s = check_dtype(dtype)) return s;
+  if (int s = check_dims(B, T, H, D)) return s;
+  if (chunk_size <= 0) return fail(SGSA_ERR_INVALID_ARG, "chunk_size=%d must be positive", chunk_size);
+  REQUIRE(q); REQUIRE(k); REQUIRE(v); REQUIRE(beta); REQUIRE(gamma); REQUIRE(out); REQUIRE(workspace);
+  const int nsp = (sparse_k != nullptr) + (sparse_v != nullptr) + (alpha != nullptr);
+  if (nsp != 0 && nsp != 3) return fail(SGSA_ERR_INVALID_ARG, "sparse_k, sparse_v and alpha must be given together");
+  const size_t need = sgsa::chunk_workspace_bytes(B, T, H, nsp == 3);
+  if (workspace_bytes < need) return fail(SGSA_ERR_WORKSPACE, "workspace %zu < %zu bytes", workspace_bytes, need);
+  sgsa::ChunkArgs a{};
+  a.dtype = dtype; a.B = B; a.T = T; a.H = H; a.D = D;
+  a.q = q; a.k = k; a.v = v; a.beta = beta; a.gamma = gamma;
+  a.sparse_k = nsp == 3 ? sparse_k : nullptr;
+  a.sparse_v = nsp == 3 ? sparse_v : nullptr;
+  a.alpha = nsp == 3 ? alpha : nullptr;
+  a.initial_state = initial_state; a.out = out; a.final_state = final_state; a.workspace = workspace;
+  return hip_status(sgsa::launch_chunk_fwd(a, (hipStream_t)stream), "sgsa_chunk_fwd");
+}
+
+static int validate_topk(int dtype, int B, int Tq, int Tk, int H, int D, int top_k, int scale_mode, float scale) {
+  if (int s = check_dtype(dtype)) return s;
+  if (int s = check_dims(B, Tq, H, D)) return s;
+  if (int s = check_dims(B, Tk, H, D)) return s;
+  if (top_k <= 0) return fail(SGSA_ERR_INVALID_ARG, "top_k=%d must be positive", top_k);
+  if (top_k > Tk) return fail(SGSA_ERR_INVALID_ARG, "top_k=%d exceeds the key length %d (pass min(top_k, Tk))", top_k, Tk);
+  if (scale_mode != 0 && scale_mode != 1) return fail(SGSA_ERR_INVALID_ARG, "scale_mode must be 0 (divide) or 1 (multiply)");
+  if (!(scale > 0.f) || !isfinite(scale)) return fail(SGSA_ERR_INVALID_ARG, "scale must be positive and finite");
+  return SGSA_OK;
+}
+
+int sgsa_score_topk(int dtype, int B, int Tq, int Tk, int H, int D, int top_k, int causal, int q_offset,
+                    float scale, int scale_mode, const void* q, const void* k, int32_t* indices, float* scores,
+                    float* top2, int32_t* counts, int sorted, void* stream) {
+  if (int s = validate_topk(dtype, B, Tq, Tk, H, D, top_k, scale_mode, scale)) return s;
+  REQUIRE(q); REQUIRE(k); REQUIRE(indices); REQUIRE(scores);
+  if (sorted && counts == nullptr) return fail(SGSA_ERR_INVALID_ARG, "sorted output needs counts");
+  if (q_offset < 0) return fail(SGSA_ERR_INVALID_ARG, "q_offset must be >= 0");
+  if (top_k > 4096 && sorted) return fail(SGSA_ERR_UNSUPPORTED, "sorted output supports top_k <= 4096");
+  sgsa::TopkArgs a{};
+  a.dtype = dtype; a.B = B; a.Tq = Tq; a.Tk = Tk; a.H = H; a.D = D; a.top_k = top_k;
+  a.causal = causal ? 1 : 0; a.q_offset = q_offset; a.scale = scale; a.scale_mode = scale_mode;
+  a.q = q; a.k = k; a.indices = indices; a.scores = scores; a.top2 = top2; a.counts = counts;
+  hipStream_t st = (hipStream_t)stream;
+  if (int s = hip_status(sgsa::launch_score_topk(a, st), "sgsa_score_topk")) return s;
+  if (sorted) return hip_status(sgsa::launch_sort_rows(indices, scores, (long)B * H * Tq, top_k, counts, st), "sgsa_score_topk(sort)");
+  return SGSA_OK;
+}
+
+int sgsa_score_dump(int dtype, int B, int Tq, int Tk, int H, int D, int causal, int q_offset, float scale,
+                    int scale_mode, const void* q, const void* k, int row0, int rows, float* out, void* stream) {
+  if (int s = validate_topk(dtype, B, Tq, Tk, H, D, 1, scale_mode, scale)) return s;
+  REQUIRE(q); REQUIRE(k); REQUIRE(out);
+  if (row0 < 0 || rows <= 0 || row0 + rows > Tq) return fail(SGSA_ERR_INVALID_ARG, "row range [%d,%d) outside [0,%d)", row0, row0 + rows, Tq);
+  sgsa::TopkArgs a{};
+  a.dtype = dtype; a.B = B; a.Tq = Tq; a.Tk = Tk; a.H = H; a.D = D; a.top_k = 1;
+  a.causal = causal ? 1 : 0; a.q_offset = q_offset; a.scale = scale; a.scale_mode = scale_mode;
+  a.q = q; a.k = k; a.dump = out; a.dump_row0 = row0; a.dump_rows = rows;
+  return hip_status(sgsa::launch_score_topk(a, (hipStream_t)stream), "sgsa_score_dump");
+}
+
+int sgsa_sparse_gather(int dtype, int B, int Tq, int Tk, int H, int D, int top_k, int q_offset, const void* k,
+                       const void* v, const void* self_key, const int32_t* indices, const float* scores,
+                       const float* top2, const int32_t* counts, const float* budget, int write_mode,
+                       float alpha_max, float tau_c, int local_window, int sink_size, void* k_hat, void* v_hat,
+                       void* write_key, float* alpha, float* weights, float* diag, void* workspace,
+                       size_t workspace_bytes, void* stream) {
+  if (int s = check_dtype(dtype)) return s;
+  if (int s = check_dims(B, Tq, H, D)) return s;
+  if (int s = check_dims(B, Tk, H, D)) return s;
+  if (top_k <= 0) return fail(SGSA_ERR_INVALID_ARG, "top_k=%d must be positive", top_k);
+  REQUIRE(v); REQUIRE(indices); REQUIRE(scores); REQUIRE(top2); REQUIRE(counts); REQUIRE(v_hat);
+  if (write_mode != 0 && write_mode != 1) return fail(SGSA_ERR_INVALID_ARG, "write_mode must be 0 (direct) or 1 (residual)");
+  if ((diag != nullptr || budget != nullptr) && self_key == nullptr)
+    return fail(SGSA_ERR_INVALID_ARG, "self_key is required for diagnostics and for the write gate");
+  if ((diag != nullptr || budget != nullptr) && k == nullptr)
+    return fail(SGSA_ERR_INVALID_ARG, "diagnostics and the write gate need k (the K gather)");
+  if (k_hat != nullptr && k == nullptr) return fail(SGSA_ERR_INVALID_ARG, "k_hat requested without k");
+  if (budget != nullptr && (alpha == nullptr)) return fail(SGSA_ERR_INVALID_ARG, "the write gate needs an alpha output");
+  if (write_mode == 1 && budget != nullptr && write_key == nullptr)
+    return fail(SGSA_ERR_INVALID_ARG, "residual write mode needs a write_key output");
+  if (diag != nullptr && (workspace == nullptr || workspace_bytes < 256))
+    return fail(SGSA_ERR_WORKSPACE, "diagnostics need a workspace of at least 256 bytes");
+  sgsa::GatherArgs a{};
+  a.dtype = dtype; a.B = B; a.Tq = Tq; a.Tk = Tk; a.H = H; a.D = D; a.top_k = top_k; a.q_offset = q_offset;
+  a.k = k; a.v = v; a.self_key = self_key; a.indices = indices; a.scores = scores; a.top2 = top2; a.counts = counts;
+  a.use_valid = 1; a.tau_c = tau_c; a.eps = 1e-6f; a.local_window = local_window; a.sink_size = sink_size;
+  a.budget = budget; a.write_mode = write_mode; a.alpha_max = alpha_max;
+  a.k_hat = k_hat; a.v_hat = v_hat; a.write_key = write_key; a.alpha = alpha; a.weights = weights; a.diag = diag;
+  a.max_index = diag ? (int32_t*)workspace : nullptr;
+  return hip_status(sgsa::launch_sparse_gather(a, (hipStream_t)stream), "sgsa_sparse_gather");
+}
+
+int sgsa_layer_fwd_workspace_size(int dtype, int B, int T, int H, int D, int top_k, size_t* bytes) {
+  REQUIRE(bytes);
+  if (int s = check_dtype(dtype)) return s;
+  if (int s = check_dims(B, T, H, D)) return s;
+  if (top_k <= 0) return fail(SGSA_ERR_INVALID_ARG, "top_k=%d must be positive", top_k);
+  *bytes = layer_ws(dtype, B, T, H, D, top_k).total;
+  return SGSA_OK;
+}
+
+int sgsa_layer_fwd(int dtype, int B, int T, int H, int D, int top_k, int chunk_size, const void* q, const void* k,
+                   const void* v, const void* q_ret, const float* beta, const float* gamma, const float* budget,
+                   const float* initial_state, int write_mode, float alpha_max, float tau_c, void* out,
+                   float* final_state, void* workspace, size_t workspace_bytes, void* stream) {
+  if (int s = check_dtype(dtype)) return s;
+  if (int s = check_dims(B, T, H, D)) return s;
+  if (top_k <= 0) return fail(SGSA_ERR_INVALID_ARG, "top_k=%d must be positive", top_k);
+  if (chunk_size <= 0) return fail(SGSA_ERR_INVALID_ARG, "chunk_size=%d must be positive", chunk_size);
+  if (write_mode != 0 && write_mode != 1) return fail(SGSA_ERR_INVALID_ARG, "write_mode must be 0 (direct) or 1 (residual)");
+  REQUIRE(q); REQUIRE(k); REQUIRE(v); REQUIRE(q_ret); REQUIRE(beta); REQUIRE(gamma); REQUIRE(budget);
+  REQUIRE(out); REQUIRE(workspace);
+  const LayerWs L = layer_ws(dtype, B, T, H, D, top_k);
+  if (workspace_bytes < L.total) return fail(SGSA_ERR_WORKSPACE, "workspace %zu < %zu bytes", workspace_bytes, L.total);
+  char* base = (char*)(((uintptr_t)workspace + kAlign - 1) & ~(uintptr_t)(kAlign - 1));
+  const int kk = top_k < T ? top_k : T;
+  int32_t* idx = (int32_t*)(base + L.idx);
+  float* sc = (float*)(base + L.sc);
+  float* t2 = (float*)(base + L.top2);
+  int32_t* cnt = (int32_t*)(base + L.cnt);
+  void* wk = base + L.wk;
+  void* vh = base + L.vh;
+  float* al = (float*)(base + L.al);
+  hipStream_t st = (hipStream_t)stream;
+
+  sgsa::TopkArgs ta{};
+  ta.dtype = dtype; ta.B = B; ta.Tq = T; ta.Tk = T; ta.H = H; ta.D = D; ta.top_k = kk; ta.causal = 1;
+  ta.q_offset = 0; ta.scale = (float)sqrt((double)D); ta.scale_mode = 0;
+  ta.q = q_ret; ta.k = k; ta.indices = idx; ta.scores = sc; ta.top2 = t2; ta.counts = cnt;
+  if (int s = hip_status(sgsa::launch_score_topk(ta, st), "sgsa_layer_fwd(topk)")) return s;
+
+  sgsa::GatherArgs ga{};
+  ga.dtype = dtype; ga.B = B; ga.Tq = T; ga.Tk = T; ga.H = H; ga.D = D; ga.top_k = kk; ga.q_offset = 0;
+  ga.k = k; ga.v = v; ga.self_key = k; ga.indices = idx; ga.scores = sc; ga.top2 = t2; ga.counts = cnt;
+  ga.use_valid = 1; ga.tau_c = tau_c; ga.eps = 1e-6f; ga.local_window = 64; ga.sink_size = 8;
+  ga.budget = budget; ga.write_mode = write_mode; ga.alpha_max = alpha_max;
+  ga.k_hat = write_mode == 0 ? wk : nullptr; ga.v_hat = vh; ga.write_key = write_mode == 1 ? wk : nullptr;
+  ga.alpha = al;
+  if (int s = hip_status(sgsa::launch_sparse_gather(ga, st), "sgsa_layer_fwd(gather)")) return s;
+
+  sgsa::ChunkArgs ca{};
+  ca.dtype = dtype; ca.B = B; ca.T = T; ca.H = H; ca.D = D;
+  ca.q = q; ca.k = k; ca.v = v; ca.beta = beta; ca.gamma = gamma;
+  ca.sparse_k = wk; ca.sparse_v = vh; ca.alpha = al; ca.initial_state = initial_state;
+  ca.out = out; ca.final_state = final_state; ca.workspace = base + L.chunk;
+  return hip_status(sgsa::launch_chunk_fwd(ca, st), "sgsa_layer_fwd(chunk)");
+}
+
+}  // extern "C"

@@ -1,0 +1,304 @@
+// K2: sparse top-k gather with softmax weights, retrieval diagnostics and
+// the SGSA write gate, fused into one pass per query row.
+//
+// Replaces, per query row:
+//   weights = softmax(fp32 scores) * valid / max(sum, eps)
+//                                        modelings/modeling_sgsa.py:126-128
+//   k_hat, v_hat = sum_i w_i K[idx_i], sum_i w_i V[idx_i]        :130-134
+//   margin, concentration, max_confidence, novelty, write_conflict,
+//   entropy, distance ratios                                     :361-405
+//   write key (direct | residual) and alpha gate     :546-552, :497-504
+//   V-only variant for the hybrid KV reuse  hybrid_dense_delta_topk.py:350-356
+// without the reference's [B,H,T,k,D] expand+gather temporary.
+//
+// One wave per query row.  The row's slot list (int32 index + fp32 score,
+// ascending key index from K1) is read 64 slots at a time, one slot per lane;
+// weights are exp(s - s_max) with s_max the row maximum from K1.  The wave is
+// then split into groups of LPR lanes, each lane owning 16 B of a key row, and
+// walks the 64 slots with every group fetching a different K and V row, so a
+// wave keeps 2 x 16 rows of 16 B loads in flight per unrolled step.
+#include "common.h"
+#include "kernels.h"
+
+#include <float.h>
+
+namespace sgsa {
+
+namespace {
+
+template <typename X, bool VEC> struct GatherShape {
+  static constexpr int NE = VEC ? 16 / (int)sizeof(X) : 2;   // elements per lane
+};
+
+template <typename X, bool VEC>
+__device__ __forceinline__ void load_row(const X* __restrict__ base, long rowoff, int sub, int D, int lpr,
+                                         float (&x)[GatherShape<X, VEC>::NE]) {
+  constexpr int NE = GatherShape<X, VEC>::NE;
+  if constexpr (VEC) {
+    const int d0 = sub * NE;
+    if (d0 < D) {
+      const uint4 raw = *reinterpret_cast<const uint4*>(base + rowoff + d0);
+      if constexpr (sizeof(X) == 2) {
+        const uint32_t u[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          x[2 * i] = __uint_as_float(u[i] << 16);
+          x[2 * i + 1] = __uint_as_float(u[i] & 0xffff0000u);
+        }
+      } else {
+        x[0] = __uint_as_float(raw.x); x[1] = __uint_as_float(raw.y);
+        x[2] = __uint_as_float(raw.z); x[3] = __uint_as_float(raw.w);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < NE; ++i) x[i] = 0.f;
+    }
+  } else {
+#pragma unroll
+    for (int m = 0; m < NE; ++m) {
+      const int d = sub + lpr * m;
+      x[m] = d < D ? ld(base, rowoff + d) : 0.f;
+    }
+  }
+}
+
+template <typename X, bool VEC>
+__device__ __forceinline__ int elem_d(int sub, int m, int lpr) {
+  return VEC ? sub * GatherShape<X, VEC>::NE + m : sub + lpr * m;
+}
+
+}  // namespace
+
+template <typename X, bool VEC>
+__global__ __launch_bounds__(256) void sparse_gather_kernel(GatherArgs a, int lpr) {
+  constexpr int NE = GatherShape<X, VEC>::NE;
+  const int lane = threadIdx.x & 63;
+  const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);     // over B*H*Tq
+  const long nrows = (long)a.B * a.H * a.Tq;
+  if (row >= nrows) return;
+  const int Tq = a.Tq, Tk = a.Tk, H = a.H, D = a.D, topk = a.top_k;
+  const int bh = (int)(row / Tq), qr = (int)(row % Tq);
+  const int b = bh / H, h = bh % H;
+  const int pos = qr + a.q_offset;
+  const int grp = lane / lpr, sub = lane % lpr;
+  const int rpi = 64 / lpr;    // key rows per step
+
+  const int kq = a.counts[row];
+  const float s0 = a.top2[2 * row];
+  const int32_t* idxp = a.indices + row * topk;
+  const float* scp = a.scores + row * topk;
+  const uint8_t* vp = a.slot_valid ? a.slot_valid + row * topk : nullptr;
+  const X* K = reinterpret_cast<const X*>(a.k);
+  const X* V = reinterpret_cast<const X*>(a.v);
+
+  float ak[NE], av[NE];
+#pragma unroll
+  for (int i = 0; i < NE; ++i) { ak[i] = 0.f; av[i] = 0.f; }
+  float esum = 0.f;
+
+  for (int base = 0; base < kq; base += 64) {
+    const int slot = base + lane;
+    int j = 0;
+    float wgt = 0.f;
+    if (slot < kq) {
+      j = idxp[slot];
+      const bool ok = vp ? (vp[slot] != 0) : true;
+      wgt = ok ? __expf(scp[slot] - s0) : 0.f;
+    }
+    esum += wgt;
+    const int nstep = min(64, kq - base);
+#pragma unroll 4
+    for (int it = 0; it * rpi < nstep; ++it) {
+      const int src = it * rpi + grp;
+      const int jj = __shfl(j, src, 64);
+      const float ww = __shfl(wgt, src, 64);
+      if (src < nstep && ww != 0.f) {
+        const long off = ((long)(b * Tk + jj) * H + h) * D;
+        float xv[NE];
+        load_row<X, VEC>(V, off, sub, D, lpr, xv);
+        if (K) {
+          float xk[NE];
+          load_row<X, VEC>(K, off, sub, D, lpr, xk);
+#pragma unroll
+          for (int i = 0; i < NE; ++i) ak[i] += ww * xk[i];
+        }
+#pragma unroll
+        for (int i = 0; i < NE; ++i) av[i] += ww * xv[i];
+      }
+    }
+  }
+  // combine the groups (lanes with equal `sub`)
+  for (int o = lpr; o < 64; o <<= 1) {
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+      ak[i] += __shfl_xor(ak[i], o, 64);
+      av[i] += __shfl_xor(av[i], o, 64);
+    }
+  }
+  const float E = wave_sum(esum);
+  const float inv = E > 0.f ? 1.f / E : 0.f;
+#pragma unroll
+  for (int i = 0; i < NE; ++i) { ak[i] *= inv; av[i] *= inv; }
+
+  // ---- per-row scalars (group 0 lanes hold the row vectors) ----
+  const long qoff = ((long)(b * Tq + qr) * H + h) * D;
+  float kt[NE];
+  if (a.self_key != nullptr && (a.diag != nullptr || a.budget != nullptr)) {
+    load_row<X, VEC>(reinterpret_cast<const X*>(a.self_key), qoff, sub, D, lpr, kt);
+  } else {
+#pragma unroll
+    for (int i = 0; i < NE; ++i) kt[i] = 0.f;
+  }
+  float pdot = 0.f, pkk = 0.f, phh = 0.f, pvv = 0.f;
+  if (grp == 0) {
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+      pdot += ak[i] * kt[i];
+      pkk += kt[i] * kt[i];
+      phh += ak[i] * ak[i];
+      pvv += av[i] * av[i];
+    }
+  }
+  const float dot = wave_sum(pdot), kk2 = wave_sum(pkk), hh2 = wave_sum(phh), vv2 = wave_sum(pvv);
+  const float eps = a.eps;
+
+  float margin = 0.f;
+  if (topk >= 2) margin = s0 - a.top2[2 * row + 1];
+  const float conc = 1.f / (1.f + expf(-(margin / fmaxf(a.tau_c, eps))));
+  const float self_norm = fmaxf(sqrtf(kk2), eps);
+  const float kh_norm = fmaxf(sqrtf(hh2), eps);
+  const float proj = dot / (self_norm * self_norm + eps);
+  float pperp = 0.f;
+  if (grp == 0) {
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+      const float dlt = ak[i] - proj * kt[i];
+      pperp += dlt * dlt;
+    }
+  }
+  const float perp = sqrtf(wave_sum(pperp));
+  const float novelty = fminf(fmaxf(perp / (kh_norm + eps), 0.f), 1.f);
+
+  // ---- write gate ----
+  float wk[NE];
+#pragma unroll
+  for (int i = 0; i < NE; ++i) wk[i] = ak[i];
+  float alpha_v = 0.f;
+  if (a.budget != nullptr) {
+    float wnorm2 = hh2;
+    if (a.write_mode == 1) {
+      const float c = dot / fmaxf(kk2, eps);
+      float pw = 0.f;
+#pragma unroll
+      for (int i = 0; i < NE; ++i) {
+        wk[i] = ak[i] - c * kt[i];
+        pw += grp == 0 ? wk[i] * wk[i] : 0.f;
+      }
+      wnorm2 = wave_sum(pw);
+    }
+    const float bud = a.budget[(long)(b * Tq + qr) * H + h];
+    float al = a.alpha_max * conc * novelty * (1.f / (1.f + expf(-bud)));
+    const float prox = al * sqrtf(vv2) * sqrtf(wnorm2);
+    const float clip = fminf(1.f / fmaxf(prox, 1.f), 1.f);
+    alpha_v = al * clip;
+  }
+
+  // ---- stores of the row vectors ----
+  if (grp == 0) {
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+      const int d = elem_d<X, VEC>(sub, i, lpr);
+      if (d >= D) continue;
+      if (a.k_hat) st(reinterpret_cast<X*>(a.k_hat), qoff + d, ak[i]);
+      st(reinterpret_cast<X*>(a.v_hat), qoff + d, av[i]);
+      if (a.write_key) st(reinterpret_cast<X*>(a.write_key), qoff + d, wk[i]);
+    }
+  }
+  if (a.alpha && lane == 0) a.alpha[(long)(b * Tq + qr) * H + h] = alpha_v;
+
+  // ---- second pass over the slot list: weights, entropy, distance stats ----
+  if (a.diag != nullptr || a.weights != nullptr) {
+    float ent = 0.f, dsum = 0.f, nloc = 0.f, nsink = 0.f, nrem = 0.f;
+    int imax = 0;
+    for (int base = 0; base < topk; base += 64) {
+      const int slot = base + lane;
+      if (slot >= topk) break;
+      int j = 0;
+      float wv = 0.f;
+      if (slot < kq) {
+        j = idxp[slot];
+        const bool ok = vp ? (vp[slot] != 0) : true;
+        wv = ok ? __expf(scp[slot] - s0) * inv : 0.f;
+      }
+      if (a.weights) a.weights[row * topk + slot] = wv;
+      const float wc = fmaxf(wv, eps);
+      ent += wc * logf(wc);
+      const int dist = max(pos - j, 0);
+      dsum += (float)dist;
+      nloc += dist <= a.local_window ? 1.f : 0.f;
+      nsink += j < a.sink_size ? 1.f : 0.f;
+      nrem += (dist > a.local_window && j >= a.sink_size) ? 1.f : 0.f;
+      imax = max(imax, j);
+    }
+    if (a.diag != nullptr) {
+      ent = wave_sum(ent);
+      dsum = wave_sum(dsum);
+      nloc = wave_sum(nloc);
+      nsink = wave_sum(nsink);
+      nrem = wave_sum(nrem);
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) imax = max(imax, __shfl_xor(imax, o, 64));
+      if (lane == 0) {
+        const long plane = (long)a.B * a.H * a.Tq;
+        const float inv_k = 1.f / (float)topk;
+        float* dg = a.diag;
+        dg[0 * plane + row] = margin;
+        dg[1 * plane + row] = conc;
+        dg[2 * plane + row] = kq > 0 ? inv : 0.f;
+        dg[3 * plane + row] = novelty;
+        dg[4 * plane + row] = fminf(fmaxf(dot / (self_norm * kh_norm + eps), -1.f), 1.f);
+        dg[5 * plane + row] = -ent;
+        dg[6 * plane + row] = dsum * inv_k;    // divided by (max index + 1) in finish_diag
+        dg[7 * plane + row] = nloc * inv_k;
+        dg[8 * plane + row] = nsink * inv_k;
+        dg[9 * plane + row] = nrem * inv_k;
+        atomicMax(a.max_index, imax);
+      }
+    }
+  }
+}
+
+// avg_distance /= max(max_index + 1, 1)  (modelings/modeling_sgsa.py:395, :401)
+__global__ void finish_diag_kernel(float* __restrict__ avgd, long n, const int32_t* __restrict__ max_index) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) avgd[i] = avgd[i] / (float)max(*max_index + 1, 1);
+}
+
+__global__ void zero_int_kernel(int32_t* p) { *p = 0; }
+
+hipError_t launch_sparse_gather(const GatherArgs& a, hipStream_t st) {
+  const long nrows = (long)a.B * a.H * a.Tq;
+  const dim3 grid((unsigned)((nrows + 3) / 4));
+  if (a.diag) zero_int_kernel<<<1, 1, 0, st>>>(a.max_index);
+  const int epv = 16 / (a.dtype == DT_F32 ? 4 : 2);
+  bool vec = (a.D % epv) == 0;
+  auto aligned = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
+  vec = vec && aligned(a.v) && (a.k == nullptr || aligned(a.k)) && (a.self_key == nullptr || aligned(a.self_key));
+  if (vec) {
+    int lpr = 1;
+    while (lpr * epv < a.D) lpr <<= 1;
+    if (a.dtype == DT_F32) sparse_gather_kernel<float, true><<<grid, 256, 0, st>>>(a, lpr);
+    else sparse_gather_kernel<bf16_t, true><<<grid, 256, 0, st>>>(a, lpr);
+  } else {
+    if (a.dtype == DT_F32) sparse_gather_kernel<float, false><<<grid, 256, 0, st>>>(a, 64);
+    else sparse_gather_kernel<bf16_t, false><<<grid, 256, 0, st>>>(a, 64);
+  }
+  if (a.diag) {
+    const long plane = nrows;
+    finish_diag_kernel<<<dim3((unsigned)((plane + 255) / 256)), 256, 0, st>>>(a.diag + 6 * plane, plane,
+                                                                            a.max_index);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace sgsa

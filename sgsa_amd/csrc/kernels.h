@@ -1,0 +1,88 @@
+// Internal host-side interface between the C ABI (api.cpp) and the kernel
+// translation units.  Not installed; the public interface is include/sgsa.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace sgsa {
+
+enum DType { DT_F32 = 0, DT_BF16 = 1 };
+
+struct ChunkArgs {
+  int dtype;
+  int B, T, H, D;
+  const void* q;
+  const void* k;
+  const void* v;
+  const float* beta;
+  const float* gamma;
+  const void* sparse_k;   // nullptr together with sparse_v/alpha: no sparse write
+  const void* sparse_v;
+  const float* alpha;
+  const float* initial_state;   // [B,H,D,D] fp32 or nullptr
+  void* out;                    // [B,T,H,D] dtype
+  float* final_state;           // [B,H,D,D] fp32 or nullptr
+  void* workspace;
+};
+
+size_t chunk_workspace_bytes(int B, int T, int H, int has_sparse);
+hipError_t launch_chunk_fwd(const ChunkArgs& a, hipStream_t st);
+
+struct TopkArgs {
+  int dtype;
+  int B, Tq, Tk, H, D;
+  int top_k;          // slots per row actually written (topk_dim)
+  int causal;
+  int q_offset;       // query row r sits at key position r + q_offset
+  float scale;        // score = acc / scale (scale_mode 0) or acc * scale (scale_mode 1)
+  int scale_mode;
+  const void* q;      // [B,Tq,H,D]
+  const void* k;      // [B,Tk,H,D]
+  const uint8_t* key_mask;   // [B,Tk] (1 = valid) or nullptr
+  const int32_t* row_kq;     // [Tq] slots to fill per query row, or nullptr (derived)
+  int32_t* indices;   // [B,H,Tq,top_k]
+  float* scores;      // [B,H,Tq,top_k]
+  float* top2;        // [B,H,Tq,2] or nullptr
+  int32_t* counts;    // [B,H,Tq] valid selected slots, or nullptr
+  float* dump;        // score-dump mode: [B,H,dump_rows,Tk]; nullptr = select mode
+  int dump_row0, dump_rows;
+};
+
+hipError_t launch_score_topk(const TopkArgs& a, hipStream_t st);
+hipError_t launch_sort_rows(int32_t* indices, float* scores, long rows, int top_k, const int32_t* counts,
+                            hipStream_t st);
+
+struct GatherArgs {
+  int dtype;
+  int B, Tq, Tk, H, D;
+  int top_k;                 // slots per row (topk_dim)
+  int q_offset;              // query row r sits at key position r + q_offset
+  const void* k;             // [B,Tk,H,D]  (nullptr: V-only gather)
+  const void* v;             // [B,Tk,H,D]
+  const void* self_key;      // [B,Tq,H,D] key of the query token (diagnostics / residual key), or nullptr
+  const int32_t* indices;    // [B,H,Tq,top_k]
+  const float* scores;       // [B,H,Tq,top_k]
+  const float* top2;         // [B,H,Tq,2]
+  const int32_t* counts;     // [B,H,Tq] valid slots (prefix) per row
+  const uint8_t* slot_valid; // [B,H,Tq,top_k] or nullptr (all slots < counts valid)
+  int use_valid;             // 1: weights are multiplied by validity and renormalised (retriever)
+  float tau_c, eps;
+  int local_window, sink_size;
+  const float* budget;       // [B,Tq,H] budget logits -> alpha gate, or nullptr
+  int write_mode;            // 0 direct, 1 residual
+  float alpha_max;
+  void* k_hat;               // [B,Tq,H,D] dtype or nullptr
+  void* v_hat;               // [B,Tq,H,D] dtype
+  void* write_key;           // [B,Tq,H,D] dtype or nullptr
+  float* alpha;              // [B,Tq,H] or nullptr
+  float* weights;            // [B,H,Tq,top_k] or nullptr
+  float* diag;               // [NDIAG,B,H,Tq] or nullptr
+  int32_t* max_index;        // 1 int scratch (diagnostics); required when diag != nullptr
+};
+
+constexpr int NDIAG = 10;
+hipError_t launch_sparse_gather(const GatherArgs& a, hipStream_t st);
+
+}  // namespace sgsa

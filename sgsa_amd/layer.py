@@ -1,0 +1,89 @@
+"""Whole SGSA layer forward in one C-ABI call (sgsa_layer_fwd).
+
+The attention half of SGSABlock.forward (modelings/modeling_sgsa.py:669-684)
+with the projections taken as inputs: token top-k retrieval on (q_ret, k, v),
+the write key and alpha gate of SGSAStateLayer (:546-552, :497-504) from the
+budget logits, then the chunked state update (:584-596).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Tuple
+
+import torch
+
+from . import _abi
+
+Tensor = torch.Tensor
+
+_WRITE_MODES = {"direct": 0, "residual": 1}
+
+
+class LayerWorkspace:
+    """Reusable device workspace for sgsa_layer_fwd, grown on demand."""
+
+    def __init__(self) -> None:
+        self.buf: Optional[Tensor] = None
+
+    def get(self, nbytes: int, device) -> Tensor:
+        if self.buf is None or self.buf.numel() < nbytes or self.buf.device != device:
+            self.buf = torch.empty(nbytes, device=device, dtype=torch.uint8)
+        return self.buf
+
+
+def layer_workspace_bytes(dtype: torch.dtype, B: int, T: int, H: int, D: int, top_k: int) -> int:
+    n = ctypes.c_size_t()
+    _abi.check(_abi.lib().sgsa_layer_fwd_workspace_size(_abi.dtype_code(dtype), B, T, H, D, int(top_k),
+                                                        ctypes.byref(n)))
+    return n.value
+
+
+def sgsa_layer_forward(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    q_ret: Tensor,
+    beta: Tensor,
+    gamma: Tensor,
+    budget_logits: Tensor,
+    top_k: int,
+    initial_state: Optional[Tensor] = None,
+    write_mode: str = "direct",
+    alpha_max: float = 0.25,
+    tau_c: float = 0.1,
+    chunk_size: int = 64,
+    output_final_state: bool = True,
+    workspace: Optional[LayerWorkspace] = None,
+    out: Optional[Tensor] = None,
+) -> Tuple[Tensor, Optional[Tensor]]:
+    """q,k,v,q_ret [B,T,H,D] (float32 or bfloat16); beta,gamma,budget_logits [B,T,H].
+
+    Returns (o [B,T,H,D] in q.dtype, final state [B,H,D,D] float32 or None).
+    """
+    if not q.is_cuda:
+        raise ValueError("sgsa_layer_forward: the SGSA kernels run on a ROCm GPU; got CPU tensors")
+    B, T, H, D = q.shape
+    for name, t in (("k", k), ("v", v), ("q_ret", q_ret)):
+        if t.shape != q.shape or t.dtype != q.dtype:
+            raise ValueError(f"{name} must match q in shape and dtype")
+    for name, t in (("beta", beta), ("gamma", gamma), ("budget_logits", budget_logits)):
+        if t.shape != (B, T, H):
+            raise ValueError(f"{name} has shape {tuple(t.shape)}, expected {(B, T, H)}")
+    if write_mode not in _WRITE_MODES:
+        raise ValueError(f"write_mode must be one of {sorted(_WRITE_MODES)}")
+    dev = q.device
+    qc, kc, vc, rc = (t.contiguous() for t in (q, k, v, q_ret))
+    bc, gc, uc = (t.float().contiguous() for t in (beta, gamma, budget_logits))
+    h0 = initial_state.float().contiguous() if initial_state is not None else None
+    if out is None:
+        out = torch.empty_like(qc)
+    ht = torch.empty(B, H, D, D, device=dev, dtype=torch.float32) if output_final_state else None
+    nbytes = layer_workspace_bytes(q.dtype, B, T, H, D, top_k)
+    ws = (workspace or LayerWorkspace()).get(nbytes, dev)
+    _abi.check(_abi.lib().sgsa_layer_fwd(
+        _abi.dtype_code(q.dtype), B, T, H, D, int(top_k), int(chunk_size),
+        _abi.ptr(qc), _abi.ptr(kc), _abi.ptr(vc), _abi.ptr(rc), _abi.ptr(bc), _abi.ptr(gc), _abi.ptr(uc),
+        _abi.ptr(h0), _WRITE_MODES[write_mode], float(alpha_max), float(tau_c), _abi.ptr(out), _abi.ptr(ht),
+        _abi.ptr(ws), ws.numel(), _abi.stream_of(qc)))
+    return out, ht

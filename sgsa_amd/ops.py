@@ -1,0 +1,146 @@
+"""Drop-in ``chunk_sgsa`` backed by the gfx950 HIP kernels.
+
+Same signature and return as modelings/sgsa_ops/chunk.py:104-148, so callers
+such as SGSAStateLayer.forward (modelings/modeling_sgsa.py:584-596) work by
+swapping the import.  Differences, all deliberate:
+
+* the final state is returned in float32 (the reference casts it to q.dtype,
+  chunk_fwd.py:129);
+* ``use_triton`` is accepted and ignored; ``chunk_size`` is accepted, the
+  kernels always use 64-token chunks (the result depends on it only through
+  rounding);
+* decay ratios are exp(log-cumsum differences) rather than ratios of clamped
+  prefix products (chunk_fwd.py:86, :110, :121), which follows the recurrent
+  definition (naive.py:40) also where a chunk-local prefix falls below 1e-6;
+* unsupported input (CPU tensors, float16, D > 128) raises instead of falling
+  back to another implementation.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Tuple
+
+import torch
+
+from . import _abi
+
+Tensor = torch.Tensor
+
+
+def _check_layout(name: str, t: Tensor, shape, device) -> None:
+    if tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} has shape {tuple(t.shape)}, expected {tuple(shape)}")
+    if t.device != device:
+        raise ValueError(f"{name} is on {t.device}, expected {device}")
+
+
+def chunk_sgsa_fwd(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    beta: Tensor,
+    gamma: Tensor,
+    sparse_k: Optional[Tensor] = None,
+    sparse_v: Optional[Tensor] = None,
+    alpha: Optional[Tensor] = None,
+    initial_state: Optional[Tensor] = None,
+    chunk_size: int = 64,
+    output_final_state: bool = False,
+    use_triton: bool = True,
+) -> Tuple[Tensor, Optional[Tensor]]:
+    """Forward body (replaces modelings/sgsa_ops/chunk_fwd.py:12-131)."""
+    if not q.is_cuda:
+        raise ValueError("chunk_sgsa: the SGSA kernels run on a ROCm GPU; got CPU tensors")
+    B, T, H, D = q.shape
+    dev = q.device
+    for name, t in (("k", k), ("v", v)):
+        _check_layout(name, t, (B, T, H, D), dev)
+    for name, t in (("beta", beta), ("gamma", gamma)):
+        _check_layout(name, t, (B, T, H), dev)
+    has_sparse = sparse_k is not None and sparse_v is not None and alpha is not None
+    if has_sparse:
+        _check_layout("sparse_k", sparse_k, (B, T, H, D), dev)
+        _check_layout("sparse_v", sparse_v, (B, T, H, D), dev)
+        _check_layout("alpha", alpha, (B, T, H), dev)
+    dt = q.dtype
+    code = _abi.dtype_code(dt)
+    cast = lambda t: t.to(dt).contiguous()
+    qc, kc, vc = cast(q), cast(k), cast(v)
+    bc = beta.float().contiguous()
+    gc = gamma.float().contiguous()
+    skc = cast(sparse_k) if has_sparse else None
+    svc = cast(sparse_v) if has_sparse else None
+    ac = alpha.float().contiguous() if has_sparse else None
+    h0 = None
+    if initial_state is not None:
+        _check_layout("initial_state", initial_state, (B, H, D, D), dev)
+        h0 = initial_state.float().contiguous()
+    out = torch.empty_like(qc)
+    ht = torch.empty(B, H, D, D, device=dev, dtype=torch.float32) if output_final_state else None
+    L = _abi.lib()
+    nbytes = ctypes.c_size_t()
+    _abi.check(L.sgsa_chunk_fwd_workspace_size(B, T, H, D, int(has_sparse), ctypes.byref(nbytes)))
+    ws = torch.empty(nbytes.value, device=dev, dtype=torch.uint8)
+    _abi.check(L.sgsa_chunk_fwd(code, B, T, H, D, int(chunk_size), _abi.ptr(qc), _abi.ptr(kc), _abi.ptr(vc),
+                                _abi.ptr(bc), _abi.ptr(gc), _abi.ptr(skc), _abi.ptr(svc), _abi.ptr(ac),
+                                _abi.ptr(h0), _abi.ptr(out), _abi.ptr(ht), _abi.ptr(ws), nbytes.value,
+                                _abi.stream_of(qc)))
+    return out, ht
+
+
+class ChunkSGSAFunction(torch.autograd.Function):
+    """Autograd wrapper with the reference's argument list (modelings/sgsa_ops/chunk.py:13-101).
+
+    Only the forward is native.  The backward (chunk_bwd.py, a torch recompute
+    in the reference) is not part of this library and raises.
+    """
+
+    @staticmethod
+    def forward(ctx, q, k, v, beta, gamma, sparse_k, sparse_v, alpha, initial_state, has_sparse,
+                has_initial_state, chunk_size, output_final_state, use_triton):
+        out, final = chunk_sgsa_fwd(
+            q, k, v, beta, gamma,
+            sparse_k if has_sparse else None,
+            sparse_v if has_sparse else None,
+            alpha if has_sparse else None,
+            initial_state if has_initial_state else None,
+            chunk_size, output_final_state, use_triton)
+        return out, final
+
+    @staticmethod
+    def backward(ctx, do, dht):
+        raise NotImplementedError("chunk_sgsa backward is not implemented by the HIP library (forward only)")
+
+
+def chunk_sgsa(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    beta: Tensor,
+    gamma: Tensor,
+    sparse_k: Optional[Tensor] = None,
+    sparse_v: Optional[Tensor] = None,
+    alpha: Optional[Tensor] = None,
+    initial_state: Optional[Tensor] = None,
+    chunk_size: int = 64,
+    output_final_state: bool = False,
+    use_triton: bool = True,
+) -> Tuple[Tensor, Optional[Tensor]]:
+    """Chunked Sparse-Guided State Attention core (modelings/sgsa_ops/chunk.py:104-148).
+
+    q,k,v,sparse_k,sparse_v: [B,T,H,D]; beta,gamma,alpha: [B,T,H];
+    initial_state: [B,H,D,D].  The sparse write is used iff sparse_k, sparse_v
+    and alpha are all given (chunk.py:123).  Returns (o [B,T,H,D] in q.dtype,
+    final state [B,H,D,D] float32 or None).
+    """
+    has_sparse = sparse_k is not None and sparse_v is not None and alpha is not None
+    has_init = initial_state is not None
+    empty = torch.empty(0, device=q.device, dtype=q.dtype)
+    return ChunkSGSAFunction.apply(
+        q, k, v, beta, gamma,
+        sparse_k if sparse_k is not None else empty,
+        sparse_v if sparse_v is not None else empty,
+        alpha if alpha is not None else torch.empty(0, device=q.device, dtype=beta.dtype),
+        initial_state if has_init else empty,
+        has_sparse, has_init, chunk_size, output_final_state, use_triton)

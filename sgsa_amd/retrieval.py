@@ -1,0 +1,143 @@
+"""Token top-k sparse retrieval on gfx950 (SparseRetriever, token_only mode).
+
+``sparse_retrieve`` returns the dict of SparseRetriever.forward
+(modelings/modeling_sgsa.py:407-474) computed by two HIP kernels: the score
+GEMM + exact top-k (sgsa_score_topk) and the gather + weights + diagnostics
+(sgsa_sparse_gather).  Indices are int64 as in the reference (:152); weights
+are returned in the input dtype (:126-128); ties in the top-k are broken by
+the lowest key index.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from typing import Dict, Optional
+
+import torch
+import torch.nn as nn
+
+from . import _abi
+
+Tensor = torch.Tensor
+
+
+def score_topk(q: Tensor, k: Tensor, top_k: int, causal: bool = True, q_offset: int = 0,
+               scale: Optional[float] = None, scale_mode: int = 0, sorted: bool = True):
+    """Exact top-k over causal scores without materialising them.
+
+    q [B,Tq,H,D], k [B,Tk,H,D].  Returns (indices int32 [B,H,Tq,kk],
+    scores float32 [B,H,Tq,kk], top2 float32 [B,H,Tq,2], counts int32 [B,H,Tq])
+    with kk = min(top_k, Tk).
+    """
+    if not q.is_cuda:
+        raise ValueError("score_topk: the SGSA kernels run on a ROCm GPU; got CPU tensors")
+    B, Tq, H, D = q.shape
+    Tk = k.shape[1]
+    if k.shape != (B, Tk, H, D) or k.dtype != q.dtype:
+        raise ValueError(f"k shape/dtype {tuple(k.shape)}/{k.dtype} does not match q {tuple(q.shape)}/{q.dtype}")
+    kk = min(int(top_k), Tk)
+    if scale is None:
+        scale = math.sqrt(D) if scale_mode == 0 else 1.0 / math.sqrt(D)
+    qc, kc = q.contiguous(), k.contiguous()
+    dev = q.device
+    idx = torch.empty(B, H, Tq, kk, device=dev, dtype=torch.int32)
+    sc = torch.empty(B, H, Tq, kk, device=dev, dtype=torch.float32)
+    top2 = torch.empty(B, H, Tq, 2, device=dev, dtype=torch.float32)
+    cnt = torch.empty(B, H, Tq, device=dev, dtype=torch.int32)
+    _abi.check(_abi.lib().sgsa_score_topk(
+        _abi.dtype_code(q.dtype), B, Tq, Tk, H, D, kk, int(causal), int(q_offset), float(scale), int(scale_mode),
+        _abi.ptr(qc), _abi.ptr(kc), _abi.ptr(idx), _abi.ptr(sc), _abi.ptr(top2), _abi.ptr(cnt), int(sorted),
+        _abi.stream_of(qc)))
+    return idx, sc, top2, cnt
+
+
+def score_dump(q: Tensor, k: Tensor, row0: int, rows: int, causal: bool = True, q_offset: int = 0,
+               scale: Optional[float] = None, scale_mode: int = 0) -> Tensor:
+    """The exact fp32 scores score_topk selects on, for query rows [row0, row0+rows): [B,H,rows,Tk]."""
+    B, Tq, H, D = q.shape
+    Tk = k.shape[1]
+    if scale is None:
+        scale = math.sqrt(D) if scale_mode == 0 else 1.0 / math.sqrt(D)
+    qc, kc = q.contiguous(), k.contiguous()
+    out = torch.empty(B, H, rows, Tk, device=q.device, dtype=torch.float32)
+    _abi.check(_abi.lib().sgsa_score_dump(
+        _abi.dtype_code(q.dtype), B, Tq, Tk, H, D, int(causal), int(q_offset), float(scale), int(scale_mode),
+        _abi.ptr(qc), _abi.ptr(kc), int(row0), int(rows), _abi.ptr(out), _abi.stream_of(qc)))
+    return out
+
+
+def sparse_retrieve(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    top_k: int,
+    causal: bool = True,
+    attention_mask: Optional[Tensor] = None,
+    tau_c: float = 0.1,
+    local_window: int = 64,
+    sink_size: int = 8,
+    sorted: bool = True,
+    return_weights: bool = True,
+    return_diagnostics: bool = True,
+) -> Dict[str, object]:
+    """Token-only retrieval; the dict of SparseRetriever.forward (modeling_sgsa.py:467-474).
+
+    q,k,v: [B,T,H,D].  k_hat/v_hat are [B,T,H,D]; indices/weights [B,H,T,kk];
+    diagnostics [B,H,T] each.  Padding masks are not supported yet.
+    """
+    if attention_mask is not None:
+        raise NotImplementedError("sparse_retrieve: attention_mask is not supported by the HIP retrieval yet")
+    B, T, H, D = q.shape
+    if v.shape != k.shape or v.dtype != k.dtype:
+        raise ValueError("v must match k in shape and dtype")
+    idx, sc, top2, cnt = score_topk(q, k, top_k, causal=causal, sorted=sorted)
+    kk = idx.shape[-1]
+    kc, vc = k.contiguous(), v.contiguous()
+    dev = q.device
+    k_hat = torch.empty(B, T, H, D, device=dev, dtype=q.dtype)
+    v_hat = torch.empty_like(k_hat)
+    weights = torch.empty(B, H, T, kk, device=dev, dtype=torch.float32) if return_weights else None
+    diag = torch.empty(_abi.NDIAG, B, H, T, device=dev, dtype=torch.float32) if return_diagnostics else None
+    ws = torch.empty(256, device=dev, dtype=torch.uint8)
+    _abi.check(_abi.lib().sgsa_sparse_gather(
+        _abi.dtype_code(q.dtype), B, T, T, H, D, kk, 0,
+        _abi.ptr(kc), _abi.ptr(vc), _abi.ptr(kc), _abi.ptr(idx), _abi.ptr(sc), _abi.ptr(top2), _abi.ptr(cnt),
+        None, 0, 0.0, float(tau_c), int(local_window), int(sink_size),
+        _abi.ptr(k_hat), _abi.ptr(v_hat), None, None, _abi.ptr(weights), _abi.ptr(diag),
+        _abi.ptr(ws), 256, _abi.stream_of(kc)))
+    out = {
+        "indices": idx.long(),
+        "block_indices": None,
+        "weights": weights.to(q.dtype) if weights is not None else None,
+        "k_hat": k_hat,
+        "v_hat": v_hat,
+        "diagnostics": ({n: diag[i] for i, n in enumerate(_abi.DIAG_NAMES)} if diag is not None else {}),
+        "scores": sc,
+        "counts": cnt,
+    }
+    return out
+
+
+class SparseRetriever(nn.Module):
+    """SparseRetriever (modelings/modeling_sgsa.py:90-474) for ``retrieval_mode='token_only'``.
+
+    Takes any config object with ``top_k``, ``tau_c``, ``local_window``,
+    ``sink_size`` and ``retrieval_mode`` attributes (the reference's SGSAConfig).
+    """
+
+    def __init__(self, config) -> None:
+        super().__init__()
+        mode = getattr(config, "retrieval_mode", "token_only")
+        if mode != "token_only":
+            raise NotImplementedError(f"retrieval_mode={mode!r}: only token_only is implemented on gfx950")
+        self.top_k = config.top_k
+        self.tau_c = getattr(config, "tau_c", 0.1)
+        self.local_window = getattr(config, "local_window", 64)
+        self.sink_size = getattr(config, "sink_size", 8)
+
+    def forward(self, q: Tensor, k: Tensor, v: Tensor, causal: bool = True,
+                attention_mask: Optional[Tensor] = None) -> Dict[str, object]:
+        r = sparse_retrieve(q, k, v, self.top_k, causal=causal, attention_mask=attention_mask, tau_c=self.tau_c,
+                            local_window=self.local_window, sink_size=self.sink_size)
+        return {key: r[key] for key in ("indices", "block_indices", "weights", "k_hat", "v_hat", "diagnostics")}

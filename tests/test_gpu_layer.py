@@ -1,0 +1,86 @@
+"""GPU parity of the retrieval (K1+K2) and of the whole layer forward.
+
+Oracle: oracle/sgsa_oracle.py (fp32 CPU restatement of modeling_sgsa.py and
+the recurrent core).  Inputs are the benchmark distributions (make_inputs);
+bf16 runs feed the oracle the bf16-rounded values.
+"""
+
+import pytest
+import torch
+
+from oracle import sgsa_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+sgsa_amd = pytest.importorskip("sgsa_amd")
+
+
+def _close(got, ref, rel, name=""):
+    got = got.detach().float().cpu()
+    ref = ref.detach().float().cpu()
+    scale = ref.abs().max().clamp_min(1e-12)
+    err = (got - ref).abs().max() / scale
+    assert torch.isfinite(got).all(), f"{name}: non-finite"
+    assert err <= rel, f"{name}: max error {err:.3e} relative to max|ref| {scale:.3e} exceeds {rel:.1e}"
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-4), (torch.bfloat16, 2e-2)])
+def test_retrieval_matches_oracle(dev, dtype, tol):
+    B, T, H, D, k = 1, 512, 4, 64, 32
+    x = O.make_inputs(B, T, H, D, dtype=dtype, seed=0)
+    ret = O.token_topk_retrieval(x["q_f32"], x["k_f32"], x["v_f32"], k)
+    got = sgsa_amd.sparse_retrieve(x["q"].to(dev), x["k"].to(dev), x["v"].to(dev), k)
+    torch.cuda.synchronize()
+    gi = got["indices"].cpu()
+    mism = (gi != ret["indices"]).any(-1).float().mean().item()
+    assert mism < 0.01, f"{mism:.3%} of rows select a different key set"
+    _close(got["k_hat"], ret["k_hat"], tol, "k_hat")
+    _close(got["v_hat"], ret["v_hat"], tol, "v_hat")
+    _close(got["weights"], ret["weights"], tol, "weights")
+    for name in ("concentration", "max_confidence", "novelty", "write_conflict", "entropy",
+                 "avg_distance", "local_ratio", "sink_ratio", "remote_ratio"):
+        _close(got["diagnostics"][name], ret["diagnostics"][name], max(tol, 1e-4), name)
+    # margins: row 0 has a finfo.min second slot in both
+    gm, rm = got["diagnostics"]["score_margin"].cpu(), ret["diagnostics"]["score_margin"]
+    _close(gm[..., 1:], rm[..., 1:], max(tol, 1e-4), "score_margin")
+
+
+def test_retrieval_causality_and_shapes(dev):
+    # scripts/sgsa_sanity_checks.py:22-39
+    B, T, H, D, k = 2, 12, 4, 24, 4
+    g = torch.Generator().manual_seed(1)
+    q, kk, v = (torch.randn(B, T, H, D, generator=g).to(dev) for _ in range(3))
+    out = sgsa_amd.SparseRetriever(type("C", (), {"top_k": k, "retrieval_mode": "token_only"})())(q, kk, v)
+    pos = torch.arange(T, device=dev).view(1, 1, T, 1)
+    assert torch.all(out["indices"] <= pos)
+    assert out["k_hat"].shape == (B, T, H, D) and out["v_hat"].shape == (B, T, H, D)
+    assert out["diagnostics"]["score_margin"].shape == (B, H, T)
+    assert out["indices"].dtype == torch.int64
+
+
+@pytest.mark.parametrize("dtype,tol,dims", [
+    (torch.float32, 1e-4, (1, 512, 4, 64, 32)),       # config 0
+    (torch.bfloat16, 2e-2, (1, 1024, 2, 128, 256)),
+])
+@pytest.mark.parametrize("write_mode", ["direct", "residual"])
+def test_layer_forward_matches_recurrent_oracle(dev, dtype, tol, dims, write_mode):
+    B, T, H, D, k = dims
+    x = O.make_inputs(B, T, H, D, dtype=dtype, seed=0)
+    ref = O.sgsa_layer_forward(x["q_f32"], x["k_f32"], x["v_f32"], x["q_f32"], x["beta"], x["gamma"],
+                               x["budget"], k, write_mode=write_mode)
+    o, st = sgsa_amd.sgsa_layer_forward(x["q"].to(dev), x["k"].to(dev), x["v"].to(dev), x["q"].to(dev),
+                                        x["beta"].to(dev), x["gamma"].to(dev), x["budget"].to(dev), k,
+                                        write_mode=write_mode)
+    torch.cuda.synchronize()
+    _close(o, ref["o"], tol, "o")
+    _close(st, ref["final_state"], tol, "final_state")
+
+
+def test_layer_forward_deterministic(dev):
+    B, T, H, D, k = 1, 700, 2, 128, 64
+    x = O.make_inputs(B, T, H, D, dtype=torch.bfloat16, seed=3)
+    args = [x[n].to(dev) for n in ("q", "k", "v", "q", "beta", "gamma", "budget")]
+    o1, s1 = sgsa_amd.sgsa_layer_forward(*args, k)
+    o2, s2 = sgsa_amd.sgsa_layer_forward(*args, k)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2) and torch.equal(s1, s2)

@@ -1,0 +1,284 @@
+"""Pins the CPU oracle (oracle/sgsa_oracle.py) before anything is compared with it.
+
+Each check is chosen so that a plausible mistake in the oracle (a dropped term,
+the sparse residual read from the wrong state, an off-by-one decay, a wrong tie
+order) fails at least one of them.  The reference ships no golden vectors for
+this path (its tests are the chunk==recurrent equalities of
+tests/test_sgsa_core.py:25-50 and the causality checks of
+scripts/sgsa_sanity_checks.py:22-39), so these are closed forms, algebraic
+restatements, invariants and brute force.
+"""
+
+import math
+
+import pytest
+import torch
+
+from oracle import sgsa_oracle as O
+
+
+def _inputs(seed=0, B=2, T=9, H=3, D=5, dtype=torch.float64):
+    # Same draw shape as the reference's _random_inputs (tests/test_sgsa_core.py:11-22).
+    g = torch.Generator().manual_seed(seed)
+    r = lambda *s: torch.randn(*s, generator=g, dtype=dtype)
+    q, k, v, sk, sv = (r(B, T, H, D) for _ in range(5))
+    beta = torch.sigmoid(r(B, T, H))
+    gamma = torch.sigmoid(r(B, T, H))
+    alpha = 0.25 * torch.sigmoid(r(B, T, H))
+    return q, k, v, sk, sv, beta, gamma, alpha
+
+
+# ---------------------------------------------------------------- recurrence
+
+def _one_step_by_hand(S, q, k, v, sk, sv, b, g, a, sparse_reads_base=True):
+    """Scalar loops, one token, one head: the recurrence written out element-wise."""
+    d, e = len(k), len(v)
+    base = [[g * S[i][j] for j in range(e)] for i in range(d)]
+    pred = [sum(base[i][j] * k[i] for i in range(d)) for j in range(e)]
+    new = [[base[i][j] + k[i] * b * (v[j] - pred[j]) for j in range(e)] for i in range(d)]
+    src = base if sparse_reads_base else new
+    pred_s = [sum(src[i][j] * sk[i] for i in range(d)) for j in range(e)]
+    new = [[new[i][j] + sk[i] * a * (sv[j] - pred_s[j]) for j in range(e)] for i in range(d)]
+    o = [sum(new[i][j] * q[i] for i in range(d)) for j in range(e)]
+    return new, o
+
+
+def test_recurrence_two_tokens_by_hand():
+    q, k, v, sk, sv, beta, gamma, alpha = _inputs(B=1, T=2, H=1, D=3)
+    S0 = torch.randn(1, 1, 3, 3, generator=torch.Generator().manual_seed(7), dtype=torch.float64)
+    out, st = O.naive_recurrent_sgsa(q, k, v, beta, gamma, sk, sv, alpha, S0, True)
+    S = S0[0, 0].tolist()
+    outs = []
+    for t in range(2):
+        S, o = _one_step_by_hand(S, q[0, t, 0].tolist(), k[0, t, 0].tolist(), v[0, t, 0].tolist(),
+                                 sk[0, t, 0].tolist(), sv[0, t, 0].tolist(), float(beta[0, t, 0]),
+                                 float(gamma[0, t, 0]), float(alpha[0, t, 0]))
+        outs.append(o)
+    torch.testing.assert_close(out[0, :, 0], torch.tensor(outs, dtype=torch.float64), rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(st[0, 0], torch.tensor(S, dtype=torch.float64), rtol=1e-12, atol=1e-12)
+    # the planted mistake (sparse residual read from the updated state) must be detectable
+    S_bad = S0[0, 0].tolist()
+    S_bad, _ = _one_step_by_hand(S_bad, q[0, 0, 0].tolist(), k[0, 0, 0].tolist(), v[0, 0, 0].tolist(),
+                                 sk[0, 0, 0].tolist(), sv[0, 0, 0].tolist(), float(beta[0, 0, 0]),
+                                 float(gamma[0, 0, 0]), float(alpha[0, 0, 0]), sparse_reads_base=False)
+    _, st1 = O.naive_recurrent_sgsa(q[:, :1], k[:, :1], v[:, :1], beta[:, :1], gamma[:, :1],
+                                    sk[:, :1], sv[:, :1], alpha[:, :1], S0, True)
+    assert (st1[0, 0] - torch.tensor(S_bad, dtype=torch.float64)).abs().max() > 1e-3
+
+
+def test_recurrence_matches_transition_matrix_form():
+    # S_t = g (I - b k k^T - a s s^T) S_{t-1} + b k v^T + a s w^T  (both residuals read g*S)
+    q, k, v, sk, sv, beta, gamma, alpha = _inputs(seed=3, B=1, T=7, H=2, D=4)
+    S0 = torch.randn(1, 2, 4, 4, generator=torch.Generator().manual_seed(1), dtype=torch.float64)
+    out, st = O.naive_recurrent_sgsa(q, k, v, beta, gamma, sk, sv, alpha, S0, True)
+    eye = torch.eye(4, dtype=torch.float64)
+    for h in range(2):
+        S = S0[0, h].clone()
+        for t in range(7):
+            kt, st_, vt, sv_t = k[0, t, h], sk[0, t, h], v[0, t, h], sv[0, t, h]
+            b, g, a = beta[0, t, h], gamma[0, t, h], alpha[0, t, h]
+            A = g * (eye - b * torch.outer(kt, kt) - a * torch.outer(st_, st_))
+            S = A @ S + b * torch.outer(kt, vt) + a * torch.outer(st_, sv_t)
+            torch.testing.assert_close(out[0, t, h], S.T @ q[0, t, h], rtol=1e-10, atol=1e-10)
+        torch.testing.assert_close(st[0, h], S, rtol=1e-10, atol=1e-10)
+
+
+def test_recurrence_special_cases():
+    q, k, v, sk, sv, beta, gamma, alpha = _inputs(seed=5, B=1, T=6, H=2, D=4)
+    S0 = torch.randn(1, 2, 4, 4, generator=torch.Generator().manual_seed(2), dtype=torch.float64)
+    zero = torch.zeros_like(beta)
+    # decay only: o_t = c^(t+1) S0^T q_t
+    c = 0.9
+    out, _ = O.naive_recurrent_sgsa(q, k, v, zero, torch.full_like(gamma, c), sk, sv, zero, S0, False)
+    for t in range(6):
+        exp = (c ** (t + 1)) * torch.einsum("bhde,bhd->bhe", S0, q[:, t])
+        torch.testing.assert_close(out[:, t], exp, rtol=1e-12, atol=1e-12)
+    # exact overwrite: unit key, beta=1, gamma=1, no sparse write => S^T k = v after the step
+    kk = k[:, :1] / k[:, :1].norm(dim=-1, keepdim=True)
+    _, st = O.naive_recurrent_sgsa(q[:, :1], kk, v[:, :1], torch.ones_like(beta[:, :1]),
+                                   torch.ones_like(gamma[:, :1]), None, None, None, S0, True)
+    torch.testing.assert_close(torch.einsum("bhde,bhd->bhe", st, kk[:, 0]), v[:, 0], rtol=1e-12, atol=1e-12)
+    # no sparse arguments == sparse write with alpha = 0
+    o1, s1 = O.naive_recurrent_sgsa(q, k, v, beta, gamma, None, None, None, S0, True)
+    o2, s2 = O.naive_recurrent_sgsa(q, k, v, beta, gamma, sk, sv, zero, S0, True)
+    torch.testing.assert_close(o1, o2, rtol=0, atol=0)
+    torch.testing.assert_close(s1, s2, rtol=0, atol=0)
+
+
+def test_state_continuation():
+    q, k, v, sk, sv, beta, gamma, alpha = _inputs(seed=9, T=10)
+    full, sf = O.naive_recurrent_sgsa(q, k, v, beta, gamma, sk, sv, alpha, None, True)
+    a, sa = O.naive_recurrent_sgsa(q[:, :4], k[:, :4], v[:, :4], beta[:, :4], gamma[:, :4],
+                                   sk[:, :4], sv[:, :4], alpha[:, :4], None, True)
+    b, sb = O.naive_recurrent_sgsa(q[:, 4:], k[:, 4:], v[:, 4:], beta[:, 4:], gamma[:, 4:],
+                                   sk[:, 4:], sv[:, 4:], alpha[:, 4:], sa, True)
+    torch.testing.assert_close(torch.cat([a, b], 1), full, rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(sb, sf, rtol=1e-12, atol=1e-12)
+
+
+# ---------------------------------------------------------------- chunk form
+
+@pytest.mark.parametrize("chunk", [1, 2, 3, 4, 5, 16])
+@pytest.mark.parametrize("sparse", [False, True])
+def test_chunk_matches_recurrent_fp64(chunk, sparse):
+    q, k, v, sk, sv, beta, gamma, alpha = _inputs(seed=chunk)
+    S0 = torch.randn(2, 3, 5, 5, generator=torch.Generator().manual_seed(4), dtype=torch.float64)
+    kw = dict(sparse_k=sk, sparse_v=sv, alpha=alpha) if sparse else {}
+    ro, rs = O.naive_recurrent_sgsa(q, k, v, beta, gamma, initial_state=S0, output_final_state=True, **kw)
+    co, cs = O.chunk_sgsa_fwd(q, k, v, beta, gamma, initial_state=S0, chunk_size=chunk,
+                              output_final_state=True, **kw)
+    torch.testing.assert_close(co, ro, rtol=1e-10, atol=1e-10)
+    torch.testing.assert_close(cs, rs, rtol=1e-10, atol=1e-10)
+
+
+def test_chunk_matches_recurrent_fp32_reference_tolerance():
+    # the reference's own check: chunk_size=4, T=9 (ragged), 1e-5 (tests/test_sgsa_core.py:34-50)
+    q, k, v, sk, sv, beta, gamma, alpha = (x.float() for x in _inputs())
+    ro, rs = O.naive_recurrent_sgsa(q, k, v, beta, gamma, sk, sv, alpha, None, True)
+    co, cs = O.chunk_sgsa_fwd(q, k, v, beta, gamma, sk, sv, alpha, None, 4, True)
+    torch.testing.assert_close(co, ro, rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(cs, rs, rtol=1e-5, atol=1e-5)
+
+
+# ---------------------------------------------------------------- top-k
+
+def _brute_topk(row, k):
+    order = sorted(range(len(row)), key=lambda j: (-row[j], j))[:k]
+    return [row[j] for j in order], order
+
+
+def test_topk_lowest_index_brute_force_with_ties():
+    g = torch.Generator().manual_seed(0)
+    for trial in range(40):
+        n = int(torch.randint(1, 40, (1,), generator=g))
+        k = int(torch.randint(1, n + 1, (1,), generator=g))
+        # small integer values force many ties
+        x = torch.randint(-3, 4, (3, n), generator=g).to(torch.float32) * 0.25
+        vals, idx = O.topk_lowest_index(x, k)
+        for r in range(3):
+            bv, bi = _brute_topk(x[r].tolist(), k)
+            assert idx[r].tolist() == bi
+            assert vals[r].tolist() == bv
+
+
+def test_topk_signed_zero_is_a_tie():
+    x = torch.tensor([[0.0, -0.0, 0.0, -1.0, -0.0]])
+    vals, idx = O.topk_lowest_index(x, 3)
+    assert idx[0].tolist() == [0, 1, 2]
+
+
+def test_masked_topk_causal_rows_and_padding():
+    g = torch.Generator().manual_seed(1)
+    B, H, T, k = 2, 3, 12, 5
+    s = torch.randn(B, H, T, T, generator=g)
+    pos = torch.arange(T)
+    valid = (pos[None, :] <= pos[:, None])[None, None].expand(B, H, -1, -1)
+    vals, idx, ok = O.masked_topk(s, valid, k)
+    fmin = torch.finfo(torch.float32).min
+    for t in range(T):
+        kq = min(k, t + 1)
+        assert ok[:, :, t, :kq].all() and not ok[:, :, t, kq:].any()
+        assert (idx[:, :, t, kq:] == 0).all() and (vals[:, :, t, kq:] == fmin).all()
+        assert (idx[:, :, t, :kq] <= t).all()
+        for b in range(B):
+            for h in range(H):
+                bv, bi = _brute_topk(s[b, h, t, :t + 1].tolist(), kq)
+                assert idx[b, h, t, :kq].tolist() == bi
+
+
+# ---------------------------------------------------------------- retrieval, diagnostics, gate
+
+def test_retrieval_by_explicit_loops():
+    g = torch.Generator().manual_seed(2)
+    B, T, H, D, k = 1, 7, 2, 4, 3
+    q, kk, v = (torch.randn(B, T, H, D, generator=g, dtype=torch.float64) for _ in range(3))
+    ret = O.token_topk_retrieval(q, kk, v, k, block_rows=3)
+    for h in range(H):
+        for t in range(T):
+            s = [sum(q[0, t, h, d].item() * kk[0, j, h, d].item() for d in range(D)) / math.sqrt(D)
+                 for j in range(t + 1)]
+            kq = min(k, t + 1)
+            bv, bi = _brute_topk(s, kq)
+            m = max(bv)
+            e = [math.exp(x - m) for x in bv]
+            w = [x / sum(e) for x in e]
+            assert ret["indices"][0, h, t, :kq].tolist() == bi
+            torch.testing.assert_close(ret["weights"][0, h, t, :kq], torch.tensor(w, dtype=torch.float64))
+            exp_k = sum(w[i] * kk[0, bi[i], h] for i in range(kq))
+            exp_v = sum(w[i] * v[0, bi[i], h] for i in range(kq))
+            torch.testing.assert_close(ret["k_hat"][0, t, h], exp_k)
+            torch.testing.assert_close(ret["v_hat"][0, t, h], exp_v)
+            margin = (bv[0] - bv[1]) if kq >= 2 else None
+            if margin is not None:
+                torch.testing.assert_close(ret["diagnostics"]["score_margin"][0, h, t],
+                                           torch.tensor(margin, dtype=torch.float64))
+    # row 0 with k >= 2: the second slot is finfo.min, so concentration saturates at 1
+    assert torch.all(ret["diagnostics"]["concentration"][:, :, 0] == 1.0)
+
+
+def test_diagnostics_novelty_limits():
+    key = torch.tensor([[[[1.0, 2.0, 0.0]]]])
+    par = 3.0 * key
+    orth = torch.tensor([[[[2.0, -1.0, 5.0]]]])
+    sc = torch.tensor([[[[1.0, 0.5]]]])
+    w = torch.tensor([[[[0.6, 0.4]]]])
+    idx = torch.zeros(1, 1, 1, 2, dtype=torch.long)
+    d_par = O.retrieval_diagnostics(sc, w, idx, par, key)
+    d_orth = O.retrieval_diagnostics(sc, w, idx, orth, key)
+    assert float(d_par["novelty"]) < 1e-5
+    assert abs(float(d_orth["novelty"]) - 1.0) < 1e-5
+    assert abs(float(d_par["write_conflict"]) - 1.0) < 1e-5
+    assert abs(float(d_orth["write_conflict"])) < 1e-5
+    torch.testing.assert_close(d_par["concentration"], torch.sigmoid(torch.tensor([[[0.5 / 0.1]]])))
+    torch.testing.assert_close(d_par["entropy"], torch.tensor([[[-(0.6 * math.log(0.6) + 0.4 * math.log(0.4))]]]))
+
+
+def test_alpha_range_and_clip():
+    g = torch.Generator().manual_seed(3)
+    B, T, H, D = 2, 5, 3, 4
+    conc = torch.rand(B, H, T, generator=g)
+    nov = torch.rand(B, H, T, generator=g)
+    budget = torch.randn(B, T, H, generator=g)
+    wk = 10 * torch.randn(B, T, H, D, generator=g)
+    vh = 10 * torch.randn(B, T, H, D, generator=g)
+    a = O.compute_alpha(conc, nov, budget, wk, vh, 0.25)
+    assert torch.all(a >= 0) and torch.all(a <= 0.25 + 1e-7)
+    raw = 0.25 * conc.transpose(1, 2) * nov.transpose(1, 2) * torch.sigmoid(budget)
+    prox = raw * vh.norm(dim=-1) * wk.norm(dim=-1)
+    clipped = prox > 1
+    assert clipped.any()
+    torch.testing.assert_close((a * vh.norm(dim=-1) * wk.norm(dim=-1))[clipped],
+                               torch.ones(int(clipped.sum())))
+    torch.testing.assert_close(a[~clipped], raw[~clipped])
+
+
+def test_residual_write_key_is_orthogonal():
+    # scripts/sgsa_sanity_checks.py:72-76
+    g = torch.Generator().manual_seed(4)
+    kh, k = torch.randn(2, 6, 3, 8, generator=g), torch.randn(2, 6, 3, 8, generator=g)
+    wk = O.write_key(kh, k, "residual")
+    assert (wk * k).sum(-1).abs().mean() < 1e-5
+
+
+def test_kv_reuse_causal_offset_and_probs():
+    g = torch.Generator().manual_seed(5)
+    B, H, Q, K, D = 1, 2, 3, 8, 4
+    qh = torch.randn(B, H, Q, D, generator=g)
+    kh = torch.randn(B, H, K, D, generator=g)
+    vh = torch.randn(B, H, K, D, generator=g)
+    out, idx, p = O.topk_kv_reuse_attention(qh, kh, vh, 4)
+    for r in range(Q):
+        pos = K - Q + r
+        s = (qh[0, 0, r] @ kh[0, 0].T) * (1.0 / math.sqrt(D))
+        s[pos + 1:] = torch.finfo(torch.float32).min
+        _, bi = _brute_topk(s.tolist(), 4)
+        assert idx[0, 0, r].tolist() == bi
+    torch.testing.assert_close(p.sum(-1), torch.ones(B, H, Q))
+
+
+def test_make_inputs_shapes_and_rounding():
+    x = O.make_inputs(1, 16, 2, 8, dtype=torch.bfloat16, heavy_tail=True)
+    assert x["q"].dtype == torch.bfloat16 and x["q_f32"].dtype == torch.float32
+    assert torch.equal(x["q"].float(), x["q_f32"])
+    n = (x["k_ret_f32"].norm(dim=-1) > 4).sum()
+    assert int(n) == 2 * round(0.01 * 16)
