@@ -241,6 +241,7 @@ def token_topk_retrieval(
     sink_size: int = 8,
     eps: float = 1e-6,
     block_rows: int = 256,
+    rows: Optional[Tuple[int, int]] = None,
 ) -> Dict[str, object]:
     """Token top-k retrieval (SparseRetriever.forward, modelings/modeling_sgsa.py:407-474).
 
@@ -250,7 +251,8 @@ def token_topk_retrieval(
     with ``clamp_min(eps)`` (:126-128); k_hat/v_hat are weighted sums of the
     selected rows (:130-134).  Diagnostics follow :361-405 with
     ``self_key = k`` (:459).  Inputs [B,T,H,D]; k_hat/v_hat returned [B,T,H,D];
-    everything else [B,H,T,*].
+    everything else [B,H,T,*].  ``rows=(r0, r1)`` restricts the work to those
+    query rows (used to time a bounded sample); outputs then cover only them.
     """
     bsz, seq_len, heads, dk = q.shape
     dtype = q.dtype
@@ -264,8 +266,9 @@ def token_topk_retrieval(
     out_vh = []
     pos = torch.arange(seq_len)
     key_valid = attention_mask.to(torch.bool) if attention_mask is not None else None
-    for r0 in range(0, seq_len, block_rows):
-        r1 = min(seq_len, r0 + block_rows)
+    row_lo, row_hi = rows if rows is not None else (0, seq_len)
+    for r0 in range(row_lo, row_hi, block_rows):
+        r1 = min(row_hi, r0 + block_rows)
         scores = torch.matmul(qh[:, :, r0:r1], kh.transpose(-2, -1)) / sc
         if causal:
             valid = (pos[None, :] <= pos[r0:r1, None])[None, None].expand(bsz, heads, -1, -1)
@@ -291,7 +294,8 @@ def token_topk_retrieval(
     weights = torch.cat(out_w, 2)
     k_hat = torch.cat(out_kh, 2)                   # [B,H,T,D]
     v_hat = torch.cat(out_vh, 2)
-    diag = retrieval_diagnostics(scores, weights, idx, k_hat, kh, tau_c, local_window, sink_size, eps)
+    diag = retrieval_diagnostics(scores, weights, idx, k_hat, kh[:, :, row_lo:row_hi], tau_c, local_window,
+                                 sink_size, eps, row_offset=row_lo)
     return {
         "indices": idx,
         "block_indices": None,
@@ -313,8 +317,12 @@ def retrieval_diagnostics(
     local_window: int = 64,
     sink_size: int = 8,
     eps: float = 1e-6,
+    row_offset: int = 0,
 ) -> Dict[str, Tensor]:
-    """SparseRetriever._diagnostics (modelings/modeling_sgsa.py:361-405).  [B,H,T,*] layout."""
+    """SparseRetriever._diagnostics (modelings/modeling_sgsa.py:361-405).  [B,H,T,*] layout.
+
+    ``row_offset`` is the query position of the first row (0 for a full pass).
+    """
     if scores.shape[-1] >= 2:
         margin = scores[..., 0] - scores[..., 1]
     else:
@@ -339,7 +347,7 @@ def retrieval_diagnostics(
         "entropy": entropy,
     }
     seq_len = int(indices.max().item()) + 1 if indices.numel() > 0 else 1
-    qpos = torch.arange(indices.shape[2]).view(1, 1, -1, 1)
+    qpos = torch.arange(row_offset, row_offset + indices.shape[2]).view(1, 1, -1, 1)
     dist = (qpos - indices).clamp_min(0)
     out["avg_distance"] = dist.float().mean(-1) / max(seq_len, 1)
     out["local_ratio"] = (dist <= local_window).float().mean(-1)
