@@ -9,7 +9,8 @@
 // [16w, 16w+16) so all per-row state (histograms, counters) is wave-private.
 // Score tiles of 64 keys are recomputed with MFMA in every pass (K tile staged
 // in LDS, q fragments held in registers), fp32 accumulation, then
-// score = acc / scale (retriever) or acc * scale (hybrid).
+// score = acc * (1/scale) (retriever, reciprocal rounded once on the host) or
+// acc * scale (hybrid).
 //
 // Selection is an exact radix select over order-preserving uint32 keys of the
 // fp32 scores (-0.0 folded onto +0.0): up to four 8-bit digit passes build a
@@ -24,6 +25,8 @@
 #include "kernels.h"
 
 #include <float.h>
+
+#include <type_traits>
 
 namespace sgsa {
 
@@ -61,24 +64,6 @@ __device__ __forceinline__ void load_k_tile(typename KTile<X>::T* ks, const X* _
   }
 }
 
-// Vectorised variant for D == DP rows (16 B per lane per load).
-template <typename X>
-__device__ __forceinline__ void load_k_tile_vec(typename KTile<X>::T* ks, const X* __restrict__ k, int b, int h,
-                                                int j0, int Tk, int H) {
-  constexpr int P = KTile<X>::PITCH;
-  constexpr int EPV = 16 / sizeof(X);          // elements per 16 B
-  constexpr int VPR = DP / EPV;                // vectors per row
-  for (int e = threadIdx.x; e < KT * VPR; e += blockDim.x) {
-    const int r = e / VPR, cv = e % VPR, j = j0 + r;
-    uint4 x = make_uint4(0, 0, 0, 0);
-    if (j < Tk) {
-      const long off = ((long)(b * Tk + j) * H + h) * DP + cv * EPV;
-      x = *reinterpret_cast<const uint4*>(reinterpret_cast<const X*>(k) + off);
-    }
-    *reinterpret_cast<uint4*>(ks + r * P + cv * EPV) = x;
-  }
-}
-
 struct RowInfo {
   uint32_t pfx, msk;
   int need, done;
@@ -86,18 +71,22 @@ struct RowInfo {
 
 }  // namespace
 
-template <typename X, bool DUMP>
-__global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb) {
+template <typename X, bool DUMP, bool C16>
+__global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb, float mscale) {
   constexpr int P = KTile<X>::PITCH;
   constexpr bool BF = sizeof(X) == 2;
-  constexpr int NQF = BF ? DP / 32 : DP / 4;   // q fragments per lane
+  constexpr int NQF = BF ? DP / 32 : DP / 4;          // q fragments per lane
+  constexpr int EPV = 16 / (int)sizeof(X);             // elements per 16 B vector
+  constexpr int VPR = DP / EPV;                        // vectors per K row
+  constexpr int NPF = KT * VPR / 256;                  // prefetch vectors per thread
+  constexpr int HW = DUMP ? 1 : (C16 ? NBIN / 2 : NBIN);   // histogram words per row
   __shared__ __align__(16) typename KTile<X>::T ks[KT * P];
-  __shared__ uint32_t hist[DUMP ? 1 : 4][16][NBIN];
+  __shared__ uint32_t hist[4][16][HW];
   __shared__ RowInfo rinfo[4][16];
 
   const int BH = a.B * a.H;
   const int bid = blockIdx.x;
-  const int bh = bid % BH;
+  const int bh = bid % BH;   // with B*H a multiple of 8, a head always lands on the same XCD
   int qb = nqb - 1 - bid / BH;   // heaviest (latest) query blocks first
   if (DUMP) qb = (a.dump_row0 / QB) + bid / BH;
   const int b = bh / a.H, h = bh % a.H;
@@ -105,6 +94,7 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb) {
   const int lr = lane & 15, lg = lane >> 4;
   const int r0 = qb * QB;
   const int Tq = a.Tq, Tk = a.Tk, H = a.H, D = a.D;
+  const X* kbase = reinterpret_cast<const X*>(a.k);
 
   // q fragments (A operand rows r0+16w+lr)
   typedef typename std::conditional<BF, bf16x8, float>::type QF;
@@ -129,64 +119,77 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb) {
     }
   }
 
-  // per-row bookkeeping for the 4 rows this lane holds in the accumulator (rows 4*lg+e)
-  int pos[4];       // query key-position
+  // rows this lane holds in the accumulator: 4*lg + e
   int nvalid[4];
   bool live[4];
-  int maxpos = -1;
+  int minvalid = 0x7fffffff;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const int qr = r0 + 16 * w + 4 * lg + e;
     live[e] = qr < Tq;
-    pos[e] = qr + a.q_offset;
     int nv = Tk;
-    if (a.causal) nv = min(Tk, pos[e] + 1);
+    if (a.causal) nv = min(Tk, qr + a.q_offset + 1);
     if (nv < 0) nv = 0;
     nvalid[e] = live[e] ? nv : 0;
+    if (live[e]) minvalid = min(minvalid, nvalid[e]);
   }
-  // keys this block must visit
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) minvalid = min(minvalid, __shfl_xor(minvalid, o, 64));
   int kend = Tk;
   if (a.causal && !DUMP) {
     const int last = min(Tq, r0 + QB) - 1 + a.q_offset;
     kend = min(Tk, last + 1);
   }
-  (void)maxpos;
-  const int ntile = (kend + KT - 1) / KT;
+  const int ntile = DUMP ? (Tk + KT - 1) / KT : (kend + KT - 1) / KT;
   const bool vec = (D == DP);
 
-  auto compute_tile = [&](int kt, f4* acc) {
+  uint4 pf[NPF];
+  auto issue = [&](int kt) __attribute__((always_inline)) {
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
-      f4 c = f4_zero();
-#pragma unroll
-      for (int s = 0; s < NQF; ++s) {
-        if constexpr (BF) {
-          const uint4 raw = *reinterpret_cast<const uint4*>(&ks[(16 * nt + lr) * P + 32 * s + 8 * lg]);
-          c = mma_bf16(qf[s], __builtin_bit_cast(bf16x8, raw), c);
-        } else {
-          c = mma_f32(qf[s], ks[(16 * nt + lr) * P + 4 * s + lg], c);
-        }
-      }
-      acc[nt] = c;
+    for (int i = 0; i < NPF; ++i) {
+      const int e = tid + 256 * i, r = e / VPR, cv = e % VPR, j = kt * KT + r;
+      pf[i] = make_uint4(0, 0, 0, 0);
+      if (j < Tk) pf[i] = *reinterpret_cast<const uint4*>(kbase + ((long)(b * Tk + j) * H + h) * DP + cv * EPV);
     }
   };
-  auto to_score = [&](float x) -> float {
-    const float s = a.scale_mode == 0 ? x / a.scale : x * a.scale;
-    return s + 0.0f;
+  auto commit = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < NPF; ++i) {
+      const int e = tid + 256 * i, r = e / VPR, cv = e % VPR;
+      *reinterpret_cast<uint4*>(ks + r * P + cv * EPV) = pf[i];
+    }
   };
-  auto stage = [&](int kt) {
-    __syncthreads();
-    if (vec) load_k_tile_vec<X>(ks, reinterpret_cast<const X*>(a.k), b, h, kt * KT, Tk, H);
-    else load_k_tile<X>(ks, reinterpret_cast<const X*>(a.k), b, h, kt * KT, Tk, H, D);
-    __syncthreads();
+  // Runs fn(kt, acc) for every key tile with the score tile in acc; K tiles are
+  // prefetched one tile ahead into registers.
+  auto sweep = [&](auto&& fn) __attribute__((always_inline)) {
+    if (vec) issue(0);
+    for (int kt = 0; kt < ntile; ++kt) {
+      __syncthreads();
+      if (vec) commit();
+      else load_k_tile<X>(ks, kbase, b, h, kt * KT, Tk, H, D);
+      __syncthreads();
+      if (vec && kt + 1 < ntile) issue(kt + 1);
+      f4 acc[4];
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+        f4 c = f4_zero();
+#pragma unroll
+        for (int s = 0; s < NQF; ++s) {
+          if constexpr (BF) {
+            const uint4 raw = *reinterpret_cast<const uint4*>(&ks[(16 * nt + lr) * P + 32 * s + 8 * lg]);
+            c = mma_bf16(qf[s], __builtin_bit_cast(bf16x8, raw), c);
+          } else {
+            c = mma_f32(qf[s], ks[(16 * nt + lr) * P + 4 * s + lg], c);
+          }
+        }
+        acc[nt] = c * mscale + 0.0f;   // fold -0.0 onto +0.0
+      }
+      fn(kt, acc);
+    }
   };
 
   if constexpr (DUMP) {
-    const int ntd = (Tk + KT - 1) / KT;
-    for (int kt = 0; kt < ntd; ++kt) {
-      stage(kt);
-      f4 acc[4];
-      compute_tile(kt, acc);
+    sweep([&](int kt, f4* acc) __attribute__((always_inline)) {
 #pragma unroll
       for (int nt = 0; nt < 4; ++nt) {
         const int j = kt * KT + 16 * nt + lr;
@@ -194,12 +197,10 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb) {
         for (int e = 0; e < 4; ++e) {
           const int qr = r0 + 16 * w + 4 * lg + e;
           if (!live[e] || j >= Tk || qr < a.dump_row0 || qr >= a.dump_row0 + a.dump_rows) continue;
-          const bool ok = j < nvalid[e] || !a.causal;
-          const float s = ok ? to_score(acc[nt][e]) : -FLT_MAX;
-          a.dump[((long)bh * a.dump_rows + (qr - a.dump_row0)) * Tk + j] = s;
+          a.dump[((long)bh * a.dump_rows + (qr - a.dump_row0)) * Tk + j] = j < nvalid[e] ? acc[nt][e] : -FLT_MAX;
         }
       }
-    }
+    });
     return;
   }
 
@@ -208,22 +209,18 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb) {
   if (lane < 16) {
     const int qr = r0 + 16 * w + lane;
     int nv = 0;
-    if (qr < Tq) {
-      nv = Tk;
-      if (a.causal) nv = max(0, min(Tk, qr + a.q_offset + 1));
-    }
-    int kq = min(topk, nv);
+    if (qr < Tq) nv = a.causal ? max(0, min(Tk, qr + a.q_offset + 1)) : Tk;
     RowInfo ri;
-    ri.pfx = 0; ri.msk = 0; ri.need = kq;
+    ri.pfx = 0; ri.msk = 0; ri.need = min(topk, nv);
     ri.done = (nv <= topk) ? 1 : 0;
     rinfo[w][lane] = ri;
   }
-  for (int i = lane; i < 16 * NBIN; i += 64) (&hist[w][0][0])[i] = 0;
+  for (int i = lane; i < 16 * HW; i += 64) (&hist[w][0][0])[i] = 0;
   __syncthreads();
 
   uint32_t pfx[4], msk[4];
   int need[4], done[4];
-  auto reload = [&]() {
+  auto reload = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const RowInfo ri = rinfo[w][4 * lg + e];
@@ -236,22 +233,26 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb) {
     int mine = 0;
 #pragma unroll
     for (int e = 0; e < 4; ++e) mine |= !done[e];
+    const bool wave_busy = __ballot(mine) != 0;
     if (!__syncthreads_or(mine)) break;
-    for (int kt = 0; kt < ntile; ++kt) {
-      stage(kt);
-      f4 acc[4];
-      compute_tile(kt, acc);
+    sweep([&](int kt, f4* acc) __attribute__((always_inline)) {
+      if (!wave_busy) return;
+      const bool full = (kt + 1) * KT <= minvalid;
 #pragma unroll
       for (int nt = 0; nt < 4; ++nt) {
         const int j = kt * KT + 16 * nt + lr;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          if (done[e] || j >= nvalid[e]) continue;
-          const uint32_t key = f32_order_key(to_score(acc[nt][e]));
-          if ((key & msk[e]) == pfx[e]) atomicAdd(&hist[w][4 * lg + e][(key >> sh) & 255u], 1u);
+          const uint32_t key = f32_order_key(acc[nt][e]);
+          const bool ok = !done[e] && (full || j < nvalid[e]) && (key & msk[e]) == pfx[e];
+          if (ok) {
+            const uint32_t bin = (key >> sh) & 255u;
+            if constexpr (C16) atomicAdd(&hist[w][4 * lg + e][bin >> 1], 1u << ((bin & 1u) << 4));
+            else atomicAdd(&hist[w][4 * lg + e][bin], 1u);
+          }
         }
       }
-    }
+    });
     __syncthreads();
     // resolve one digit per unfinished row of this wave
     for (int rr = 0; rr < 16; ++rr) {
@@ -259,8 +260,13 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb) {
       if (ri.done) continue;
       // lane l covers bins 255-4l .. 252-4l (descending)
       uint32_t c[4];
+      if constexpr (C16) {
+        const uint32_t w0 = hist[w][rr][127 - 2 * lane], w1 = hist[w][rr][126 - 2 * lane];
+        c[0] = w0 >> 16; c[1] = w0 & 0xffffu; c[2] = w1 >> 16; c[3] = w1 & 0xffffu;
+      } else {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) c[q] = hist[w][rr][255 - 4 * lane - q];
+        for (int q = 0; q < 4; ++q) c[q] = hist[w][rr][255 - 4 * lane - q];
+      }
       const uint32_t loc = c[0] + c[1] + c[2] + c[3];
       uint32_t inc = loc;
 #pragma unroll
@@ -296,8 +302,13 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb) {
         ri.done = (cnt == (uint32_t)ri.need || sh == 0) ? 1 : 0;
         rinfo[w][rr] = ri;
       }
+      if constexpr (C16) {
+        hist[w][rr][127 - 2 * lane] = 0;
+        hist[w][rr][126 - 2 * lane] = 0;
+      } else {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) hist[w][rr][255 - 4 * lane - q] = 0;
+        for (int q = 0; q < 4; ++q) hist[w][rr][255 - 4 * lane - q] = 0;
+      }
     }
     __syncthreads();
     reload();
@@ -309,17 +320,18 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb) {
 #pragma unroll
   for (int e = 0; e < 4; ++e) { outc[e] = 0; eqc[e] = 0; m1[e] = -FLT_MAX; m2[e] = -FLT_MAX; }
   const uint32_t lower = (1u << lr) - 1u;
-  for (int kt = 0; kt < ntile; ++kt) {
-    stage(kt);
-    f4 acc[4];
-    compute_tile(kt, acc);
+  long rowbase[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) rowbase[e] = ((long)bh * Tq + (r0 + 16 * w + 4 * lg + e)) * topk;
+  sweep([&](int kt, f4* acc) __attribute__((always_inline)) {
+    const bool full = (kt + 1) * KT <= minvalid;
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) {
       const int j = kt * KT + 16 * nt + lr;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const bool ok = j < nvalid[e];
-        const float s = to_score(acc[nt][e]);
+        const bool ok = full || j < nvalid[e];
+        const float s = acc[nt][e];
         const uint32_t key = f32_order_key(s);
         const uint32_t km = key & msk[e];
         const bool eq = ok && km == pfx[e];
@@ -328,19 +340,17 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb) {
         const uint32_t sb = (uint32_t)(__ballot(sel) >> (16 * lg)) & 0xffffu;
         const int slot = outc[e] + __popc(sb & lower);
         if (sel && slot < topk) {
-          const long row = ((long)bh * Tq + (r0 + 16 * w + 4 * lg + e));
-          a.indices[row * topk + slot] = j;
-          a.scores[row * topk + slot] = s;
+          a.indices[rowbase[e] + slot] = j;
+          a.scores[rowbase[e] + slot] = s;
         }
-        if (ok) {
-          if (s > m1[e]) { m2[e] = m1[e]; m1[e] = s; }
-          else if (s > m2[e]) m2[e] = s;
-        }
+        const float so = ok ? s : -FLT_MAX;   // running top-2 with multiplicity
+        m2[e] = fmaxf(m2[e], fminf(m1[e], so));
+        m1[e] = fmaxf(m1[e], so);
         outc[e] += __popc(sb);
         eqc[e] += __popc(eqb);
       }
     }
-  }
+  });
   // merge top-2 over the 16 lanes holding each row, then pad and write counts
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
@@ -351,10 +361,10 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb) {
       m1[e] = hi; m2[e] = lo;
     }
     if (!live[e]) continue;
-    const long row = ((long)bh * Tq + (r0 + 16 * w + 4 * lg + e));
+    const long row = rowbase[e] / topk;
     for (int p = outc[e] + lr; p < topk; p += 16) {
-      a.indices[row * topk + p] = 0;
-      a.scores[row * topk + p] = -FLT_MAX;
+      a.indices[rowbase[e] + p] = 0;
+      a.scores[rowbase[e] + p] = -FLT_MAX;
     }
     if (lr == 0) {
       if (a.counts) a.counts[row] = outc[e];
@@ -408,17 +418,26 @@ __global__ __launch_bounds__(256) void sort_rows_kernel(int32_t* __restrict__ in
 hipError_t launch_score_topk(const TopkArgs& a, hipStream_t st) {
   const int nqb = (a.Tq + QB - 1) / QB;
   const int BH = a.B * a.H;
+  // score = acc / scale is evaluated as acc * (1/scale) with the reciprocal
+  // rounded once on the host; scale_mode 1 multiplies by scale directly.
+  const float ms = a.scale_mode == 0 ? (float)(1.0 / (double)a.scale) : a.scale;
   if (a.dump) {
     const int qb0 = a.dump_row0 / QB;
     const int qb1 = (a.dump_row0 + a.dump_rows + QB - 1) / QB;
     const dim3 grid((unsigned)(BH * (qb1 - qb0)));
-    if (a.dtype == DT_F32) score_topk_kernel<float, true><<<grid, 256, 0, st>>>(a, nqb);
-    else score_topk_kernel<bf16_t, true><<<grid, 256, 0, st>>>(a, nqb);
+    if (a.dtype == DT_F32) score_topk_kernel<float, true, true><<<grid, 256, 0, st>>>(a, nqb, ms);
+    else score_topk_kernel<bf16_t, true, true><<<grid, 256, 0, st>>>(a, nqb, ms);
     return hipGetLastError();
   }
   const dim3 grid((unsigned)(BH * nqb));
-  if (a.dtype == DT_F32) score_topk_kernel<float, false><<<grid, 256, 0, st>>>(a, nqb);
-  else score_topk_kernel<bf16_t, false><<<grid, 256, 0, st>>>(a, nqb);
+  const bool c16 = a.Tk <= 65535;   // 16-bit histogram counters cannot overflow
+  if (a.dtype == DT_F32) {
+    if (c16) score_topk_kernel<float, false, true><<<grid, 256, 0, st>>>(a, nqb, ms);
+    else score_topk_kernel<float, false, false><<<grid, 256, 0, st>>>(a, nqb, ms);
+  } else {
+    if (c16) score_topk_kernel<bf16_t, false, true><<<grid, 256, 0, st>>>(a, nqb, ms);
+    else score_topk_kernel<bf16_t, false, false><<<grid, 256, 0, st>>>(a, nqb, ms);
+  }
   return hipGetLastError();
 }
 
