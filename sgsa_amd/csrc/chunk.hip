@@ -21,8 +21,8 @@
 //                      the fp32 state recurrence; stores R and the chunk-start
 //                      states.
 //   chunk_out    (K5)  parallel over all chunks: the readout.
-// All contractions use v_mfma_f32_16x16x4_f32 with fp32 operands (the state
-// stays fp32 end to end).  The head dimension is padded to DP=128 in LDS and
+// This file is the fp32-input path: all contractions use v_mfma_f32_16x16x4_f32
+// with fp32 operands.  bf16 inputs take chunk_bf16.hip.  The head dimension is padded to DP=128 in LDS and
 // in the workspace; padded rows/columns are zero and never stored.
 #include "common.h"
 #include "kernels.h"
@@ -437,7 +437,9 @@ size_t chunk_workspace_bytes(int B, int T, int H, int has_sparse) {
   const long wu = BH * NT * M * DP;         // W, U, R each
   const long hs = BH * NT * DP * DP;        // chunk-start states
   const long lgd = BH * NT * L;
-  return sizeof(float) * (3 * wu + hs + lgd) + 256 * 5;
+  const size_t f32 = sizeof(float) * (3 * wu + hs + lgd) + 256 * 5;
+  const size_t b16 = chunk_bf16_workspace_bytes(B, T, H, has_sparse);
+  return f32 > b16 ? f32 : b16;
 }
 
 template <typename X, bool SP>
@@ -468,9 +470,9 @@ static hipError_t launch_chunk_t(const ChunkArgs& a, hipStream_t st) {
 }
 
 hipError_t launch_chunk_fwd(const ChunkArgs& a, hipStream_t st) {
+  if (a.dtype == DT_BF16) return launch_chunk_bf16(a, st);
   const bool sp = a.sparse_k != nullptr;
-  if (a.dtype == DT_F32) return sp ? launch_chunk_t<float, true>(a, st) : launch_chunk_t<float, false>(a, st);
-  return sp ? launch_chunk_t<bf16_t, true>(a, st) : launch_chunk_t<bf16_t, false>(a, st);
+  return sp ? launch_chunk_t<float, true>(a, st) : launch_chunk_t<float, false>(a, st);
 }
 
 }  // namespace sgsa

@@ -27,8 +27,10 @@ struct ChunkArgs {
   void* workspace;
 };
 
-size_t chunk_workspace_bytes(int B, int T, int H, int has_sparse);
+size_t chunk_workspace_bytes(int B, int T, int H, int has_sparse);   // covers both paths
+size_t chunk_bf16_workspace_bytes(int B, int T, int H, int has_sparse);
 hipError_t launch_chunk_fwd(const ChunkArgs& a, hipStream_t st);
+hipError_t launch_chunk_bf16(const ChunkArgs& a, hipStream_t st);
 
 struct TopkArgs {
   int dtype;

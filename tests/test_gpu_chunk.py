@@ -110,3 +110,18 @@ def test_chunk_deterministic(dev):
     o1, s1 = _run(dev, torch.bfloat16, q, k, v, sk, sv, beta, gamma, alpha, None, True)
     o2, s2 = _run(dev, torch.bfloat16, q, k, v, sk, sv, beta, gamma, alpha, None, True)
     assert torch.equal(o1, o2) and torch.equal(s1, s2)
+
+
+@pytest.mark.parametrize("dims", [(1, 333, 2, 128), (2, 130, 2, 96), (1, 64, 3, 40)])
+@pytest.mark.parametrize("sparse", [False, True])
+def test_chunk_bf16_initial_state_and_shapes(dev, dims, sparse):
+    B, T, H, D = dims
+    q, k, v, sk, sv, beta, gamma, alpha = _norm_inputs(6, B, T, H, D)
+    rb = lambda t: t.to(torch.bfloat16).float()
+    q, k, v, sk, sv = map(rb, (q, k, v, sk, sv))
+    h0 = 0.1 * torch.randn(B, H, D, D, generator=torch.Generator().manual_seed(8))
+    kw = dict(sparse_k=sk, sparse_v=sv, alpha=alpha) if sparse else {}
+    ro, rs = O.naive_recurrent_sgsa(q, k, v, beta, gamma, initial_state=h0, output_final_state=True, **kw)
+    out, st = _run(dev, torch.bfloat16, q, k, v, sk, sv, beta, gamma, alpha, h0, sparse)
+    _close(out, ro, 2e-2)
+    _close(st, rs, 2e-2)
