@@ -121,6 +121,12 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--T", type=int, default=NORTH_STAR["T"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run one plain 256 MiB fp32 copy kernel (torch.neg) first; its PMC byte counters "
+                         "give the scale factor for the traffic of the SGSA kernels")
+    ap.add_argument("--traffic-from", default=os.path.join(ROOT, "profiles", "hbm_traffic_north_star_pmc.md"),
+                    help="committed PMC summary whose 'gather_hbm_bytes_per_launch:' line gives the measured "
+                         "L2-to-fabric bytes of one gather launch at the north-star shape")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on exactly one GPU (got --gpus {args.gpus}); the SGSA layer shards by head, "
@@ -181,6 +187,13 @@ def main() -> int:
         if events is not None:
             events[-1].record(cur)
 
+    if args.copy_calibration:
+        src = torch.ones(64 * 1024 * 1024, device=dev, dtype=torch.float32)
+        dst = torch.empty_like(src)
+        torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        log("copy calibration: 268435456 bytes read, 268435456 bytes written (torch.neg)")
+        del src, dst
     log(f"warmup {args.warmup} steps")
     for _ in range(args.warmup):
         step()
@@ -200,6 +213,12 @@ def main() -> int:
     log(f"ms/step {ms_step:.3f}  stages {json.dumps({n: round(v, 3) for n, v in stage_ms.items()})}")
 
     gbytes = gather_bytes(B, H, T, D, kk)
+    traffic = None
+    if args.traffic_from and os.path.exists(args.traffic_from) and (B, T, H, D, kk) == (1, 32768, 16, 128, 2048):
+        with open(args.traffic_from) as f:
+            for line in f:
+                if line.startswith("gather_hbm_bytes_per_launch:"):
+                    traffic = int(line.split(":", 1)[1])
     g_s = stage_ms["gather_gate"] / 1000.0
     achieved = gbytes / g_s / 1e9
     roofline = {
@@ -209,7 +228,7 @@ def main() -> int:
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4),
-        "traffic": None,
+        "traffic": traffic,
         "algorithmic_bytes": gbytes,
     }
     result = {

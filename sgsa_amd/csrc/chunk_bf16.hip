@@ -13,7 +13,7 @@
 // 16-byte loads (row-major W, transposed kappa / S / R).
 //
 // K3 chunk_intra_bf16  grid (NT, B*H)      Gram, T, (I+T)^-1, W = A D_tau kappa, U = A nu, kappa^T
-// K4 chunk_state_bf16  grid (DP/16, B*H)   sequential state pass; fragments of chunk c+1 are
+// K4 chunk_state_bf16  grid (B*H, DP/16)   sequential state pass; fragments of chunk c+1 are
 //                                          prefetched into registers while chunk c is processed
 // K5 chunk_out_bf16    grid (NT, B*H)      o = D Q S + P R
 #include "common.h"
@@ -300,7 +300,10 @@ __global__ __launch_bounds__(256) void chunk_state_bf16(
   __shared__ float lam[M];
   __shared__ float logd[L];
 
-  const int cs = blockIdx.x, bh = blockIdx.y;
+  // grid (B*H, DP/16): the column slices of one head are B*H blocks apart, so
+  // with B*H a multiple of 8 they share an XCD (and its L2) and read each
+  // chunk's W / kappa^T once from the fabric.
+  const int bh = blockIdx.x, cs = blockIdx.y;
   const int b = bh / H, h = bh % H;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int lr = lane & 15, lg = lane >> 4;
@@ -594,7 +597,7 @@ static hipError_t launch_bf16_t(const ChunkArgs& a, hipStream_t st) {
   const bf16_t* sk = (const bf16_t*)a.sparse_k;
   const bf16_t* sv = (const bf16_t*)a.sparse_v;
   chunk_intra_bf16<SP><<<dim3(NT, BH), 256, 0, st>>>(k, v, sk, sv, a.beta, a.alpha, a.gamma, a.T, a.H, a.D, NT, ws);
-  chunk_state_bf16<SP><<<dim3(DP / 16, BH), 256, 0, st>>>(a.beta, a.alpha, a.initial_state, a.T, a.H, a.D, NT, ws,
+  chunk_state_bf16<SP><<<dim3(BH, DP / 16), 256, 0, st>>>(a.beta, a.alpha, a.initial_state, a.T, a.H, a.D, NT, ws,
                                                          a.final_state);
   chunk_out_bf16<SP><<<dim3(NT, BH), 256, 0, st>>>(q, k, sk, a.beta, a.alpha, a.T, a.H, a.D, NT, ws,
                                                    (bf16_t*)a.out);
