@@ -148,7 +148,6 @@ def main() -> int:
     bd, gd, ud = (t.to(dev).contiguous() for t in (beta, gamma, budget))
     idx = torch.empty(B, H, T, kk, device=dev, dtype=torch.int32)
     sc = torch.empty(B, H, T, kk, device=dev, dtype=torch.float32)
-    top2 = torch.empty(B, H, T, 2, device=dev, dtype=torch.float32)
     cnt = torch.empty(B, H, T, device=dev, dtype=torch.int32)
     wk = torch.empty(B, T, H, D, device=dev, dtype=bf)
     vh = torch.empty_like(wk)
@@ -159,17 +158,20 @@ def main() -> int:
     L = _abi.lib()
     _abi.check(L.sgsa_chunk_fwd_workspace_size(B, T, H, D, 1, ctypes.byref(nbytes)))
     ws = torch.empty(nbytes.value, device=dev, dtype=torch.uint8)
+    tbytes = ctypes.c_size_t()
+    _abi.check(L.sgsa_score_topk_workspace_size(B, T, H, ctypes.byref(tbytes)))
+    tws = torch.empty(tbytes.value, device=dev, dtype=torch.uint8)
     P = _abi.ptr
     stream = _abi.stream_of(qd)
     scale = math.sqrt(D)
 
     def k1():
         _abi.check(L.sgsa_score_topk(_abi.SGSA_BF16, B, T, T, H, D, kk, 1, 0, scale, 0, P(qd), P(kd), P(idx),
-                                     P(sc), P(top2), P(cnt), 0, stream))
+                                     P(sc), None, P(cnt), 0, P(tws), tbytes.value, stream))
 
     def k2():
         _abi.check(L.sgsa_sparse_gather(_abi.SGSA_BF16, B, T, T, H, D, kk, 0, P(kd), P(vd), P(kd), P(idx), P(sc),
-                                        P(top2), P(cnt), P(ud), 0, 0.25, 0.1, 64, 8, P(wk), P(vh), None, P(al),
+                                        None, P(cnt), P(ud), 0, 0.25, 0.1, 64, 8, P(wk), P(vh), None, P(al),
                                         None, None, None, 0, stream))
 
     def k345():

@@ -87,14 +87,17 @@ int sgsa_chunk_fwd(int dtype, int B, int T, int H, int D, int chunk_size,
  * causal keeps keys <= that position.  Each row gets
  * counts = min(top_k, valid keys) selected slots, ties broken by lowest key
  * index; slots >= counts hold index 0 and score -FLT_MAX (:151-153).
- * sorted = 0: selected slots in ascending key index; sorted = 1: (score desc,
- * index asc) as torch.topk(sorted=True) with the lowest-index tie rule.
- * top2 (may be NULL) receives the two largest valid scores (-FLT_MAX if absent). */
+ * sorted = 0: the selected slots in a deterministic order (not sorted);
+ * sorted = 1: (score desc, index asc) as torch.topk(sorted=True) with the
+ * lowest-index tie rule.  top2 (may be NULL) receives the two largest valid
+ * scores (-FLT_MAX if absent).  Needs sgsa_score_topk_workspace_size() bytes
+ * of workspace (per-row candidate lists). */
+int sgsa_score_topk_workspace_size(int B, int Tq, int H, size_t* bytes);
 int sgsa_score_topk(int dtype, int B, int Tq, int Tk, int H, int D, int top_k,
                     int causal, int q_offset, float scale, int scale_mode,
                     const void* q, const void* k,
                     int32_t* indices, float* scores, float* top2, int32_t* counts,
-                    int sorted, void* stream);
+                    int sorted, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Known-answer hook: writes the exact fp32 scores sgsa_score_topk selects on,
  * for query rows [row0, row0+rows), to out [B,H,rows,Tk]; keys outside the
@@ -109,7 +112,8 @@ int sgsa_score_dump(int dtype, int B, int Tq, int Tk, int H, int D,
  * key and alpha gate of SGSAStateLayer (:546-552, :497-504), and the V-only
  * gather of TopKSparseKVReuseAttention (hybrid_dense_delta_topk.py:350-356;
  * pass k = NULL, k_hat = NULL).  Consumes sgsa_score_topk's output (either
- * order).  self_key [B,Tq,H,D]: key of each query token (the retriever's
+ * order).  top2 may be NULL: the row maximum is then tracked with an
+ * online-softmax rescale.  self_key [B,Tq,H,D]: key of each query token (the retriever's
  * self_key = k, :459); needed for diag and for the gate.  budget NULL = no
  * gate (write_key/alpha untouched); else alpha = alpha_max * concentration *
  * novelty * sigmoid(budget), clipped (:497-504), write_mode 0 direct / 1

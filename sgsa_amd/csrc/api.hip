@@ -50,7 +50,7 @@ int check_dims(int B, int T, int H, int D) {
   do { if ((ptr) == nullptr) return fail(SGSA_ERR_INVALID_ARG, "%s must not be NULL", #ptr); } while (0)
 
 struct LayerWs {
-  size_t idx, sc, top2, cnt, wk, vh, al, misc, chunk, total;
+  size_t idx, sc, cnt, wk, vh, al, misc, topk, chunk, total;
 };
 
 LayerWs layer_ws(int dtype, int B, int T, int H, int D, int top_k) {
@@ -60,12 +60,12 @@ LayerWs layer_ws(int dtype, int B, int T, int H, int D, int top_k) {
   size_t off = 0;
   w.idx = off; off = align_up(off + rows * kk * 4);
   w.sc = off; off = align_up(off + rows * kk * 4);
-  w.top2 = off; off = align_up(off + rows * 2 * 4);
   w.cnt = off; off = align_up(off + rows * 4);
   w.wk = off; off = align_up(off + (size_t)B * T * H * D * dtype_size(dtype));
   w.vh = off; off = align_up(off + (size_t)B * T * H * D * dtype_size(dtype));
   w.al = off; off = align_up(off + (size_t)B * T * H * 4);
   w.misc = off; off = align_up(off + 256);
+  w.topk = off; off = align_up(off + sgsa::topk_workspace_bytes(B, T, H));
   w.chunk = off; off = align_up(off + sgsa::chunk_workspace_bytes(B, T, H, 1));
   w.total = off + kAlign;
   return w;
@@ -130,11 +130,21 @@ static int validate_topk(int dtype, int B, int Tq, int Tk, int H, int D, int top
   return SGSA_OK;
 }
 
+int sgsa_score_topk_workspace_size(int B, int Tq, int H, size_t* bytes) {
+  REQUIRE(bytes);
+  if (int s = check_dims(B, Tq, H, 1)) return s;
+  *bytes = sgsa::topk_workspace_bytes(B, Tq, H);
+  return SGSA_OK;
+}
+
 int sgsa_score_topk(int dtype, int B, int Tq, int Tk, int H, int D, int top_k, int causal, int q_offset,
                     float scale, int scale_mode, const void* q, const void* k, int32_t* indices, float* scores,
-                    float* top2, int32_t* counts, int sorted, void* stream) {
+                    float* top2, int32_t* counts, int sorted, void* workspace, size_t workspace_bytes,
+                    void* stream) {
   if (int s = validate_topk(dtype, B, Tq, Tk, H, D, top_k, scale_mode, scale)) return s;
-  REQUIRE(q); REQUIRE(k); REQUIRE(indices); REQUIRE(scores);
+  REQUIRE(q); REQUIRE(k); REQUIRE(indices); REQUIRE(scores); REQUIRE(workspace);
+  const size_t need_ws = sgsa::topk_workspace_bytes(B, Tq, H);
+  if (workspace_bytes < need_ws) return fail(SGSA_ERR_WORKSPACE, "workspace %zu < %zu bytes", workspace_bytes, need_ws);
   if (sorted && counts == nullptr) return fail(SGSA_ERR_INVALID_ARG, "sorted output needs counts");
   if (q_offset < 0) return fail(SGSA_ERR_INVALID_ARG, "q_offset must be >= 0");
   if (top_k > 4096 && sorted) return fail(SGSA_ERR_UNSUPPORTED, "sorted output supports top_k <= 4096");
@@ -142,6 +152,7 @@ int sgsa_score_topk(int dtype, int B, int Tq, int Tk, int H, int D, int top_k, i
   a.dtype = dtype; a.B = B; a.Tq = Tq; a.Tk = Tk; a.H = H; a.D = D; a.top_k = top_k;
   a.causal = causal ? 1 : 0; a.q_offset = q_offset; a.scale = scale; a.scale_mode = scale_mode;
   a.q = q; a.k = k; a.indices = indices; a.scores = scores; a.top2 = top2; a.counts = counts;
+  a.workspace = workspace;
   hipStream_t st = (hipStream_t)stream;
   if (int s = hip_status(sgsa::launch_score_topk(a, st), "sgsa_score_topk")) return s;
   if (sorted) return hip_status(sgsa::launch_sort_rows(indices, scores, (long)B * H * Tq, top_k, counts, st), "sgsa_score_topk(sort)");
@@ -170,7 +181,7 @@ int sgsa_sparse_gather(int dtype, int B, int Tq, int Tk, int H, int D, int top_k
   if (int s = check_dims(B, Tq, H, D)) return s;
   if (int s = check_dims(B, Tk, H, D)) return s;
   if (top_k <= 0) return fail(SGSA_ERR_INVALID_ARG, "top_k=%d must be positive", top_k);
-  REQUIRE(v); REQUIRE(indices); REQUIRE(scores); REQUIRE(top2); REQUIRE(counts); REQUIRE(v_hat);
+  REQUIRE(v); REQUIRE(indices); REQUIRE(scores); REQUIRE(counts); REQUIRE(v_hat);
   if (write_mode != 0 && write_mode != 1) return fail(SGSA_ERR_INVALID_ARG, "write_mode must be 0 (direct) or 1 (residual)");
   if ((diag != nullptr || budget != nullptr) && self_key == nullptr)
     return fail(SGSA_ERR_INVALID_ARG, "self_key is required for diagnostics and for the write gate");
@@ -218,7 +229,6 @@ int sgsa_layer_fwd(int dtype, int B, int T, int H, int D, int top_k, int chunk_s
   const int kk = top_k < T ? top_k : T;
   int32_t* idx = (int32_t*)(base + L.idx);
   float* sc = (float*)(base + L.sc);
-  float* t2 = (float*)(base + L.top2);
   int32_t* cnt = (int32_t*)(base + L.cnt);
   void* wk = base + L.wk;
   void* vh = base + L.vh;
@@ -228,12 +238,13 @@ int sgsa_layer_fwd(int dtype, int B, int T, int H, int D, int top_k, int chunk_s
   sgsa::TopkArgs ta{};
   ta.dtype = dtype; ta.B = B; ta.Tq = T; ta.Tk = T; ta.H = H; ta.D = D; ta.top_k = kk; ta.causal = 1;
   ta.q_offset = 0; ta.scale = (float)sqrt((double)D); ta.scale_mode = 0;
-  ta.q = q_ret; ta.k = k; ta.indices = idx; ta.scores = sc; ta.top2 = t2; ta.counts = cnt;
+  ta.q = q_ret; ta.k = k; ta.indices = idx; ta.scores = sc; ta.top2 = nullptr; ta.counts = cnt;
+  ta.workspace = base + L.topk;
   if (int s = hip_status(sgsa::launch_score_topk(ta, st), "sgsa_layer_fwd(topk)")) return s;
 
   sgsa::GatherArgs ga{};
   ga.dtype = dtype; ga.B = B; ga.Tq = T; ga.Tk = T; ga.H = H; ga.D = D; ga.top_k = kk; ga.q_offset = 0;
-  ga.k = k; ga.v = v; ga.self_key = k; ga.indices = idx; ga.scores = sc; ga.top2 = t2; ga.counts = cnt;
+  ga.k = k; ga.v = v; ga.self_key = k; ga.indices = idx; ga.scores = sc; ga.top2 = nullptr; ga.counts = cnt;
   ga.use_valid = 1; ga.tau_c = tau_c; ga.eps = 1e-6f; ga.local_window = 64; ga.sink_size = 8;
   ga.budget = budget; ga.write_mode = write_mode; ga.alpha_max = alpha_max;
   ga.k_hat = write_mode == 0 ? wk : nullptr; ga.v_hat = vh; ga.write_key = write_mode == 1 ? wk : nullptr;

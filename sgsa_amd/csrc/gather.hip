@@ -13,7 +13,8 @@
 //
 // One wave per query row.  The row's slot list (int32 index + fp32 score,
 // ascending key index from K1) is read 64 slots at a time, one slot per lane;
-// weights are exp(s - s_max) with s_max the row maximum from K1.  The wave is
+// weights are exp(s - m) with m the row maximum, taken from K1 or kept as a
+// running maximum with an online-softmax rescale of the partial sums.  The wave is
 // then split into groups of LPR lanes, each lane owning 16 B of a key row, and
 // walks the 64 slots with every group fetching a different K and V row, so a
 // wave keeps 2 x 16 rows of 16 B loads in flight per unrolled step.
@@ -84,7 +85,9 @@ __global__ __launch_bounds__(256) void sparse_gather_kernel(GatherArgs a, int lp
   const int rpi = 64 / lpr;    // key rows per step
 
   const int kq = a.counts[row];
-  const float s0 = a.top2[2 * row];
+  const bool fixed_max = a.top2 != nullptr;
+  float mrun = fixed_max ? a.top2[2 * row] : -INFINITY;   // running max of the row's valid scores
+  float t1 = -FLT_MAX, t2 = -FLT_MAX;                      // running top-2 (online mode)
   const int32_t* idxp = a.indices + row * topk;
   const float* scp = a.scores + row * topk;
   const uint8_t* vp = a.slot_valid ? a.slot_valid + row * topk : nullptr;
@@ -99,12 +102,27 @@ __global__ __launch_bounds__(256) void sparse_gather_kernel(GatherArgs a, int lp
   for (int base = 0; base < kq; base += 64) {
     const int slot = base + lane;
     int j = 0;
-    float wgt = 0.f;
+    float sc = -INFINITY;
     if (slot < kq) {
       j = idxp[slot];
       const bool ok = vp ? (vp[slot] != 0) : true;
-      wgt = ok ? __expf(scp[slot] - s0) : 0.f;
+      if (ok) sc = scp[slot];
     }
+    if (!fixed_max) {
+      // online-softmax merge: rescale what was accumulated under the old max
+      const float bm = wave_max(sc);
+      if (bm > mrun) {
+        const float f = (mrun == -INFINITY) ? 0.f : __expf(mrun - bm);
+        esum *= f;
+#pragma unroll
+        for (int i = 0; i < NE; ++i) { ak[i] *= f; av[i] *= f; }
+        mrun = bm;
+      }
+      const float so = sc == -INFINITY ? -FLT_MAX : sc;
+      t2 = fmaxf(t2, fminf(t1, so));
+      t1 = fmaxf(t1, so);
+    }
+    const float wgt = sc == -INFINITY ? 0.f : __expf(sc - mrun);
     esum += wgt;
     const int nstep = min(64, kq - base);
 #pragma unroll 4
@@ -135,6 +153,19 @@ __global__ __launch_bounds__(256) void sparse_gather_kernel(GatherArgs a, int lp
       av[i] += __shfl_xor(av[i], o, 64);
     }
   }
+  float s0 = mrun, s1;
+  if (fixed_max) {
+    s1 = a.top2[2 * row + 1];
+  } else {
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const float b1 = __shfl_xor(t1, o, 64), b2 = __shfl_xor(t2, o, 64);
+      const float hi = fmaxf(t1, b1), lo = fmaxf(fminf(t1, b1), fmaxf(t2, b2));
+      t1 = hi; t2 = lo;
+    }
+    s0 = kq > 0 ? t1 : -FLT_MAX;
+    s1 = t2;
+  }
   const float E = wave_sum(esum);
   const float inv = E > 0.f ? 1.f / E : 0.f;
 #pragma unroll
@@ -163,7 +194,7 @@ __global__ __launch_bounds__(256) void sparse_gather_kernel(GatherArgs a, int lp
   const float eps = a.eps;
 
   float margin = 0.f;
-  if (topk >= 2) margin = s0 - a.top2[2 * row + 1];
+  if (topk >= 2) margin = s0 - s1;
   const float conc = 1.f / (1.f + expf(-(margin / fmaxf(a.tau_c, eps))));
   const float self_norm = fmaxf(sqrtf(kk2), eps);
   const float kh_norm = fmaxf(sqrtf(hh2), eps);
@@ -228,7 +259,7 @@ __global__ __launch_bounds__(256) void sparse_gather_kernel(GatherArgs a, int lp
       if (slot < kq) {
         j = idxp[slot];
         const bool ok = vp ? (vp[slot] != 0) : true;
-        wv = ok ? __expf(scp[slot] - s0) * inv : 0.f;
+        wv = ok ? __expf(scp[slot] - mrun) * inv : 0.f;
       }
       if (a.weights) a.weights[row * topk + slot] = wv;
       const float wc = fmaxf(wv, eps);

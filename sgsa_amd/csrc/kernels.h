@@ -50,7 +50,14 @@ struct TopkArgs {
   int32_t* counts;    // [B,H,Tq] valid selected slots, or nullptr
   float* dump;        // score-dump mode: [B,H,dump_rows,Tk]; nullptr = select mode
   int dump_row0, dump_rows;
+  void* workspace;    // topk_workspace_bytes(): candidate lists + per-head key norms
+  uint2* scratch;     // set by the launcher
+  int* flags;         // set by the launcher
+  const float* kmax;  // set by the launcher
 };
+
+constexpr int TOPK_CAP = 512;   // collected threshold-bin candidates per row
+size_t topk_workspace_bytes(int B, int Tq, int H);
 
 hipError_t launch_score_topk(const TopkArgs& a, hipStream_t st);
 hipError_t launch_sort_rows(int32_t* indices, float* scores, long rows, int top_k, const int32_t* counts,
@@ -66,7 +73,7 @@ struct GatherArgs {
   const void* self_key;      // [B,Tq,H,D] key of the query token (diagnostics / residual key), or nullptr
   const int32_t* indices;    // [B,H,Tq,top_k]
   const float* scores;       // [B,H,Tq,top_k]
-  const float* top2;         // [B,H,Tq,2]
+  const float* top2;         // [B,H,Tq,2] row max / second max, or nullptr (online max)
   const int32_t* counts;     // [B,H,Tq] valid slots (prefix) per row
   const uint8_t* slot_valid; // [B,H,Tq,top_k] or nullptr (all slots < counts valid)
   int use_valid;             // 1: weights are multiplied by validity and renormalised (retriever)

@@ -6,21 +6,32 @@
 // ever materialising the [T,T] score matrix.
 //
 // Work unit: one (batch, head) and a block of 64 query rows; wave w owns rows
-// [16w, 16w+16) so all per-row state (histograms, counters) is wave-private.
-// Score tiles of 64 keys are recomputed with MFMA in every pass (K tile staged
-// in LDS, q fragments held in registers), fp32 accumulation, then
-// score = acc * (1/scale) (retriever, reciprocal rounded once on the host) or
-// acc * scale (hybrid).
+// [16w, 16w+16), so every per-row counter and histogram is wave-private.  Score
+// tiles of 64 keys are recomputed with MFMA in each pass (K tiles prefetched
+// one ahead into registers, staged in LDS; q fragments stay in registers),
+// fp32 accumulation, score = acc * (1/scale) with the reciprocal rounded once
+// on the host (retriever) or acc * scale (hybrid).
 //
-// Selection is an exact radix select over order-preserving uint32 keys of the
-// fp32 scores (-0.0 folded onto +0.0): up to four 8-bit digit passes build a
-// per-row 256-bin histogram of the still-tied candidates, each pass fixing one
-// digit of the k-th key; a row leaves early once its threshold bin holds
-// exactly the number still needed.  A final pass emits, in ascending key
-// index order, every candidate above the threshold prefix plus the first
-// `need` candidates equal to it (ordered ballot ranks), so ties are broken by
-// lowest index.  Output rows are therefore in ascending index order; the
-// optional sort kernel reorders them to (score desc, index asc).
+// Exact selection in two sweeps for typical rows:
+//   pass A  a 256-bin histogram per row of bin(s) = clamp(int(s*iw + 128), 0, 255),
+//           iw = 128 / (|q_row| * max_j |k_j| * scale): a monotone map of the
+//           score (any iw keeps the selection exact; the Cauchy-Schwarz bound
+//           only makes the bins informative).  The threshold bin b*, the count
+//           above it and the number `need` still to take from it follow.
+//   pass B  emits every candidate with bin > b* in ascending key index and
+//           appends the candidates of bin b* (in index order) to a per-row
+//           scratch list of at most TOPK_CAP entries.
+//   resolve an exact radix select over the order-preserving uint32 keys of the
+//           collected scores (-0.0 folded onto +0.0) finds the need-th largest;
+//           the winners -- keys above it, then equal keys in index order -- are
+//           appended.  Ties are therefore broken by lowest index.
+// Rows whose b* holds exactly `need` candidates skip the scratch.  A block
+// with a row whose b* holds more than TOPK_CAP candidates (coarse bins, mass
+// ties) is flagged and redone by a second launch of the kernel that selects
+// with up to four 8-bit radix digit passes over the keys, then emits.  The output
+// order of a row is deterministic (emitted part in index order, then the
+// resolved part in index order); the sort kernel reorders rows to
+// (score desc, index asc) when requested.
 #include "common.h"
 #include "kernels.h"
 
@@ -36,6 +47,8 @@ constexpr int QB = 64;        // query rows per block
 constexpr int KT = 64;        // keys per tile
 constexpr int DP = 128;       // padded head dim
 constexpr int NBIN = 256;
+
+enum RowMode { SELECT_ALL = 0, BIN_ALL = 1, COLLECT = 2, RADIX = 3 };
 
 template <typename X> struct KTile;
 template <> struct KTile<bf16_t> {
@@ -65,13 +78,104 @@ __device__ __forceinline__ void load_k_tile(typename KTile<X>::T* ks, const X* _
 }
 
 struct RowInfo {
-  uint32_t pfx, msk;
-  int need, done;
+  float iw;          // bin scale
+  int bstar;         // threshold bin
+  int need;          // still to take at the current resolution
+  int mode;          // RowMode
+  uint32_t pfx, msk; // RADIX key prefix inside b*
+  int done;          // RADIX resolution finished
+  float th0, th1;    // pass B: select s >= th1; collect th0 <= s < th1
 };
+
+__device__ __forceinline__ int score_bin(float s, float iw) {
+  return (int)__builtin_amdgcn_fmed3f(fmaf(s, iw, 128.0f), 0.0f, 255.0f);
+}
+
+__device__ __forceinline__ float key_to_f32(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+// Smallest float s with score_bin(s, iw) >= bt (1 <= bt <= 255), by bisection over
+// the order-preserving keys between -inf and +inf (score_bin is monotone in s).
+__device__ __forceinline__ float bin_lower_edge(int bt, float iw) {
+  uint32_t lo = 0x007fffffu, hi = 0xff800000u;   // keys of -inf and +inf
+  while (hi - lo > 1u) {
+    const uint32_t mid = lo + ((hi - lo) >> 1);
+    if (score_bin(key_to_f32(mid), iw) >= bt) hi = mid;
+    else lo = mid;
+  }
+  return key_to_f32(hi);
+}
+
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Over 256 counts laid out as lane l <-> bins 255-4l .. 252-4l (descending),
+// finds the bin holding the `need`-th largest element.  Wave-uniform results.
+__device__ __forceinline__ void find_bin(const uint32_t (&c)[4], int lane, uint32_t need, int& bin, uint32_t& above,
+                                         uint32_t& cnt) {
+  const uint32_t loc = c[0] + c[1] + c[2] + c[3];
+  uint32_t inc = loc;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t n = __shfl_up(inc, o, 64);
+    if (lane >= o) inc += n;
+  }
+  const uint32_t exc = inc - loc;
+  const bool hit = exc < need && need <= inc;
+  const uint64_t bal = __ballot(hit);
+  const int src = bal ? __ffsll((unsigned long long)bal) - 1 : 0;
+  int b = 0;
+  uint32_t ab = 0, ct = 0;
+  if (hit) {
+    uint32_t cum = exc;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (ct == 0 && cum + c[q] >= need) {
+        b = 255 - 4 * lane - q;
+        ab = cum;
+        ct = c[q];
+      }
+      if (ct == 0) cum += c[q];
+    }
+  }
+  bin = __shfl(b, src, 64);
+  above = __shfl(ab, src, 64);
+  cnt = __shfl(ct, src, 64);
+}
 
 }  // namespace
 
-template <typename X, bool DUMP, bool C16>
+// Max |k_j| per (b,h): the denominator of the pass-A bin scale.  grid (B*H), 256 threads.
+template <typename X>
+__global__ __launch_bounds__(256) void key_norm_max_kernel(const X* __restrict__ k, int Tk, int H, int D,
+                                                           float* __restrict__ kmax) {
+  __shared__ float red[4];
+  const int bh = blockIdx.x, b = bh / H, h = bh % H;
+  float m = 0.f;
+  for (int j = threadIdx.x; j < Tk; j += blockDim.x) {
+    const X* row = k + ((long)(b * Tk + j) * H + h) * D;
+    float s = 0.f;
+    for (int d = 0; d < D; ++d) {
+      const float x = ld(row, d);
+      s = fmaf(x, x, s);
+    }
+    m = fmaxf(m, s);
+  }
+  m = wave_max(m);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) kmax[bh] = sqrtf(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
+}
+
+// FB = false: the two-pass select; a block with a row whose threshold bin holds
+// more than TOPK_CAP candidates sets flags[block] and returns without output.
+// FB = true: re-runs exactly the flagged blocks with 8-bit radix digit passes
+// over the order-preserving keys (up to 4 passes + emit).
+template <typename X, bool DUMP, bool C16, bool TOP2, bool FB>
 __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb, float mscale) {
   constexpr int P = KTile<X>::PITCH;
   constexpr bool BF = sizeof(X) == 2;
@@ -80,9 +184,13 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb, fl
   constexpr int VPR = DP / EPV;                        // vectors per K row
   constexpr int NPF = KT * VPR / 256;                  // prefetch vectors per thread
   constexpr int HW = DUMP ? 1 : (C16 ? NBIN / 2 : NBIN);   // histogram words per row
+  constexpr int HWA = HW < 16 ? 16 : HW;               // >= 256 words per wave for the resolve
+  constexpr int CAPL = TOPK_CAP / 64;                  // collected entries per lane in the resolve
   __shared__ __align__(16) typename KTile<X>::T ks[KT * P];
-  __shared__ uint32_t hist[4][16][HW];
+  __shared__ uint32_t hist[4][16][HWA];
   __shared__ RowInfo rinfo[4][16];
+  __shared__ int rowcnt[4][16][2];   // emitted count, collected count
+  __shared__ float qnorm[4][16];
 
   const int BH = a.B * a.H;
   const int bid = blockIdx.x;
@@ -96,10 +204,11 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb, fl
   const int Tq = a.Tq, Tk = a.Tk, H = a.H, D = a.D;
   const X* kbase = reinterpret_cast<const X*>(a.k);
 
-  // q fragments (A operand rows r0+16w+lr)
+  // q fragments (A operand rows r0+16w+lr) and their norms
   typedef typename std::conditional<BF, bf16x8, float>::type QF;
   QF qf[NQF];
   {
+    float qn2 = 0.f;
     const int qr = r0 + 16 * w + lr;
     const X* qp = reinterpret_cast<const X*>(a.q) + ((long)(b * Tq + (qr < Tq ? qr : 0)) * H + h) * D;
 #pragma unroll
@@ -110,13 +219,19 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb, fl
         for (int j = 0; j < 8; ++j) {
           const int d = 32 * s + 8 * lg + j;
           raw[j] = (qr < Tq && d < D) ? reinterpret_cast<const uint16_t*>(qp)[d] : (uint16_t)0;
+          const float x = bf16_to_f32(raw[j]);
+          qn2 = fmaf(x, x, qn2);
         }
         qf[s] = __builtin_bit_cast(bf16x8, raw);
       } else {
         const int d = 4 * s + lg;
         qf[s] = (qr < Tq && d < D) ? reinterpret_cast<const float*>(qp)[d] : 0.f;
+        qn2 = fmaf(qf[s], qf[s], qn2);
       }
     }
+    qn2 += __shfl_xor(qn2, 16, 64);
+    qn2 += __shfl_xor(qn2, 32, 64);
+    if (!DUMP && lg == 0) qnorm[w][lr] = sqrtf(qn2);
   }
 
   // rows this lane holds in the accumulator: 4*lg + e
@@ -159,8 +274,7 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb, fl
       *reinterpret_cast<uint4*>(ks + r * P + cv * EPV) = pf[i];
     }
   };
-  // Runs fn(kt, acc) for every key tile with the score tile in acc; K tiles are
-  // prefetched one tile ahead into registers.
+  // Runs fn(kt, acc) for every key tile with the score tile in acc.
   auto sweep = [&](auto&& fn) __attribute__((always_inline)) {
     if (vec) issue(0);
     for (int kt = 0; kt < ntile; ++kt) {
@@ -204,35 +318,118 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb, fl
     return;
   }
 
-  // ---- radix select -------------------------------------------------------
   const int topk = a.top_k;
+  if constexpr (FB) {
+    if (a.flags[bid] == 0) return;   // block-uniform
+  }
+  __syncthreads();   // qnorm visible
   if (lane < 16) {
     const int qr = r0 + 16 * w + lane;
     int nv = 0;
     if (qr < Tq) nv = a.causal ? max(0, min(Tk, qr + a.q_offset + 1)) : Tk;
     RowInfo ri;
-    ri.pfx = 0; ri.msk = 0; ri.need = min(topk, nv);
-    ri.done = (nv <= topk) ? 1 : 0;
+    const float bound = qnorm[w][lane] * a.kmax[bh] * fabsf(mscale) * 1.001f;
+    ri.iw = (bound > 0.f && bound < FLT_MAX) ? 128.0f / bound : 0.f;
+    ri.bstar = -1;
+    ri.need = min(topk, nv);
+    ri.mode = (nv <= topk) ? SELECT_ALL : (FB ? RADIX : BIN_ALL);
+    ri.pfx = 0; ri.msk = 0; ri.done = (FB && nv > topk) ? 0 : 1; ri.th0 = -INFINITY; ri.th1 = -INFINITY;
     rinfo[w][lane] = ri;
   }
-  for (int i = lane; i < 16 * HW; i += 64) (&hist[w][0][0])[i] = 0;
+  for (int i = lane; i < 16 * HWA; i += 64) (&hist[w][0][0])[i] = 0;
   __syncthreads();
 
+  float iw[4];
+  int mode[4], bstar[4], need[4], rdone[4];
   uint32_t pfx[4], msk[4];
-  int need[4], done[4];
   auto reload = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const RowInfo ri = rinfo[w][4 * lg + e];
-      pfx[e] = ri.pfx; msk[e] = ri.msk; need[e] = ri.need; done[e] = ri.done;
+      iw[e] = ri.iw; mode[e] = ri.mode; bstar[e] = ri.bstar; need[e] = ri.need;
+      pfx[e] = ri.pfx; msk[e] = ri.msk; rdone[e] = ri.done;
     }
   };
   reload();
 
-  for (int sh = 24; sh >= 0; sh -= 8) {
+  auto read_counts = [&](int rr, uint32_t (&c)[4]) __attribute__((always_inline)) {
+    if constexpr (C16) {
+      const uint32_t w0 = hist[w][rr][127 - 2 * lane], w1 = hist[w][rr][126 - 2 * lane];
+      c[0] = w0 >> 16; c[1] = w0 & 0xffffu; c[2] = w1 >> 16; c[3] = w1 & 0xffffu;
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) c[q] = hist[w][rr][255 - 4 * lane - q];
+    }
+  };
+  auto clear_counts = [&](int rr) __attribute__((always_inline)) {
+    if constexpr (C16) {
+      hist[w][rr][127 - 2 * lane] = 0;
+      hist[w][rr][126 - 2 * lane] = 0;
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) hist[w][rr][255 - 4 * lane - q] = 0;
+    }
+  };
+  auto bump = [&](int row, uint32_t bin) __attribute__((always_inline)) {
+    if constexpr (C16) atomicAdd(&hist[w][row][bin >> 1], 1u << ((bin & 1u) << 4));
+    else atomicAdd(&hist[w][row][bin], 1u);
+  };
+
+  // ---- pass A: score-bin histogram -------------------------------------------
+  if constexpr (!FB) {
     int mine = 0;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) mine |= !done[e];
+    for (int e = 0; e < 4; ++e) mine |= (mode[e] != SELECT_ALL);
+    const bool wave_busy = __ballot(mine) != 0;
+    if (__syncthreads_or(mine)) {
+      sweep([&](int kt, f4* acc) __attribute__((always_inline)) {
+        if (!wave_busy) return;
+        const bool full = (kt + 1) * KT <= minvalid;
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) {
+          const int j = kt * KT + 16 * nt + lr;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            if (live[e] && mode[e] != SELECT_ALL && (full || j < nvalid[e]))
+              bump(4 * lg + e, (uint32_t)score_bin(acc[nt][e], iw[e]));
+          }
+        }
+      });
+      __syncthreads();
+      for (int rr = 0; rr < 16; ++rr) {
+        RowInfo ri = rinfo[w][rr];
+        if (ri.mode == SELECT_ALL) continue;
+        uint32_t c[4];
+        read_counts(rr, c);
+        int bin;
+        uint32_t above, cnt;
+        find_bin(c, lane, (uint32_t)ri.need, bin, above, cnt);
+        if (lane == 0) {
+          ri.bstar = bin;
+          ri.need -= (int)above;
+          if (cnt == (uint32_t)ri.need) ri.mode = BIN_ALL;
+          else if (cnt <= (uint32_t)TOPK_CAP) ri.mode = COLLECT;
+          else ri.mode = RADIX;
+          rinfo[w][rr] = ri;
+        }
+        clear_counts(rr);
+      }
+      __syncthreads();
+      reload();
+    }
+    int overflow = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) overflow |= (mode[e] == RADIX);
+    overflow = __syncthreads_or(overflow);
+    if (tid == 0) a.flags[bid] = overflow;
+    if (overflow) return;   // block-uniform; the fallback launch redoes this block
+  }
+
+  // ---- fallback: radix digits over the keys ---------------------------------
+  if constexpr (FB) for (int sh = 24; sh >= 0; sh -= 8) {
+    int mine = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) mine |= (mode[e] == RADIX && !rdone[e]);
     const bool wave_busy = __ballot(mine) != 0;
     if (!__syncthreads_or(mine)) break;
     sweep([&](int kt, f4* acc) __attribute__((always_inline)) {
@@ -243,58 +440,22 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb, fl
         const int j = kt * KT + 16 * nt + lr;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const uint32_t key = f32_order_key(acc[nt][e]);
-          const bool ok = !done[e] && (full || j < nvalid[e]) && (key & msk[e]) == pfx[e];
-          if (ok) {
-            const uint32_t bin = (key >> sh) & 255u;
-            if constexpr (C16) atomicAdd(&hist[w][4 * lg + e][bin >> 1], 1u << ((bin & 1u) << 4));
-            else atomicAdd(&hist[w][4 * lg + e][bin], 1u);
-          }
+          const float s = acc[nt][e];
+          const uint32_t key = f32_order_key(s);
+          if (live[e] && mode[e] == RADIX && !rdone[e] && (full || j < nvalid[e]) && (key & msk[e]) == pfx[e])
+            bump(4 * lg + e, (key >> sh) & 255u);
         }
       }
     });
     __syncthreads();
-    // resolve one digit per unfinished row of this wave
     for (int rr = 0; rr < 16; ++rr) {
       RowInfo ri = rinfo[w][rr];
-      if (ri.done) continue;
-      // lane l covers bins 255-4l .. 252-4l (descending)
+      if (ri.mode != RADIX || ri.done) continue;
       uint32_t c[4];
-      if constexpr (C16) {
-        const uint32_t w0 = hist[w][rr][127 - 2 * lane], w1 = hist[w][rr][126 - 2 * lane];
-        c[0] = w0 >> 16; c[1] = w0 & 0xffffu; c[2] = w1 >> 16; c[3] = w1 & 0xffffu;
-      } else {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) c[q] = hist[w][rr][255 - 4 * lane - q];
-      }
-      const uint32_t loc = c[0] + c[1] + c[2] + c[3];
-      uint32_t inc = loc;
-#pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t n = __shfl_up(inc, o, 64);
-        if (lane >= o) inc += n;
-      }
-      const uint32_t exc = inc - loc;
-      const bool hit = exc < (uint32_t)ri.need && (uint32_t)ri.need <= inc;
-      const uint64_t bal = __ballot(hit);
-      const int src = __ffsll((unsigned long long)bal) - 1;
-      int bin = 0;
-      uint32_t above = 0, cnt = 0;
-      if (hit) {
-        uint32_t cum = exc;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          if (cnt == 0 && cum + c[q] >= (uint32_t)ri.need) {
-            bin = 255 - 4 * lane - q;
-            above = cum;
-            cnt = c[q];
-          }
-          if (cnt == 0) cum += c[q];
-        }
-      }
-      bin = __shfl(bin, src, 64);
-      above = __shfl(above, src, 64);
-      cnt = __shfl(cnt, src, 64);
+      read_counts(rr, c);
+      int bin;
+      uint32_t above, cnt;
+      find_bin(c, lane, (uint32_t)ri.need, bin, above, cnt);
       if (lane == 0) {
         ri.pfx |= (uint32_t)bin << sh;
         ri.msk |= 0xffu << sh;
@@ -302,73 +463,207 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb, fl
         ri.done = (cnt == (uint32_t)ri.need || sh == 0) ? 1 : 0;
         rinfo[w][rr] = ri;
       }
-      if constexpr (C16) {
-        hist[w][rr][127 - 2 * lane] = 0;
-        hist[w][rr][126 - 2 * lane] = 0;
-      } else {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) hist[w][rr][255 - 4 * lane - q] = 0;
-      }
+      clear_counts(rr);
     }
     __syncthreads();
     reload();
   }
 
-  // ---- emit pass ------------------------------------------------------------
-  int outc[4], eqc[4];
+  // ---- thresholds for pass B -------------------------------------------------
+  if (lane < 16) {
+    RowInfo ri = rinfo[w][lane];
+    float t0 = -INFINITY, t1 = -INFINITY;
+    if (FB && ri.mode == RADIX) {
+      t0 = INFINITY; t1 = INFINITY;   // every candidate goes through the key path
+    } else if (!FB && ri.mode != SELECT_ALL) {
+      const float lo_b = ri.bstar > 0 ? bin_lower_edge(ri.bstar, ri.iw) : -INFINITY;
+      const float hi_b = ri.bstar < NBIN - 1 ? bin_lower_edge(ri.bstar + 1, ri.iw) : INFINITY;
+      if (ri.mode == BIN_ALL) { t0 = lo_b; t1 = lo_b; }
+      else { t0 = lo_b; t1 = hi_b; }   // COLLECT
+    }
+    ri.th0 = t0; ri.th1 = t1;
+    rinfo[w][lane] = ri;
+  }
+  __syncthreads();
+
+  // ---- pass B: emit above b*, collect b* -------------------------------------
+  float th0[4], th1[4];
+  int outc[4], colc[4];
   float m1[4], m2[4];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) { outc[e] = 0; eqc[e] = 0; m1[e] = -FLT_MAX; m2[e] = -FLT_MAX; }
+  for (int e = 0; e < 4; ++e) {
+    th0[e] = rinfo[w][4 * lg + e].th0;
+    th1[e] = rinfo[w][4 * lg + e].th1;
+    outc[e] = 0; colc[e] = 0; m1[e] = -FLT_MAX; m2[e] = -FLT_MAX;
+  }
+  const int grow0 = bh * Tq + r0 + 16 * w + 4 * lg;   // global row of e = 0
   const uint32_t lower = (1u << lr) - 1u;
-  long rowbase[4];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) rowbase[e] = ((long)bh * Tq + (r0 + 16 * w + 4 * lg + e)) * topk;
-  sweep([&](int kt, f4* acc) __attribute__((always_inline)) {
-    const bool full = (kt + 1) * KT <= minvalid;
-#pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
-      const int j = kt * KT + 16 * nt + lr;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const bool ok = full || j < nvalid[e];
-        const float s = acc[nt][e];
-        const uint32_t key = f32_order_key(s);
-        const uint32_t km = key & msk[e];
-        const bool eq = ok && km == pfx[e];
-        const uint32_t eqb = (uint32_t)(__ballot(eq) >> (16 * lg)) & 0xffffu;
-        const bool sel = ok && (km > pfx[e] || (eq && eqc[e] + __popc(eqb & lower) < need[e]));
-        const uint32_t sb = (uint32_t)(__ballot(sel) >> (16 * lg)) & 0xffffu;
-        const int slot = outc[e] + __popc(sb & lower);
-        if (sel && slot < topk) {
-          a.indices[rowbase[e] + slot] = j;
-          a.scores[rowbase[e] + slot] = s;
-        }
-        const float so = ok ? s : -FLT_MAX;   // running top-2 with multiplicity
-        m2[e] = fmaxf(m2[e], fminf(m1[e], so));
-        m1[e] = fmaxf(m1[e], so);
-        outc[e] += __popc(sb);
-        eqc[e] += __popc(eqb);
+  uint2* scratch = a.scratch;
+  auto emit = [&](int e, int j, float s, bool sel, bool col) __attribute__((always_inline)) {
+    const uint32_t sm = (uint32_t)(__ballot(sel) >> (16 * lg)) & 0xffffu;
+    const uint32_t cm = (uint32_t)(__ballot(col) >> (16 * lg)) & 0xffffu;
+    const long row = (long)(grow0 + e);
+    if (sel) {
+      const int slot = outc[e] + __popc(sm & lower);
+      if (slot < topk) {
+        a.indices[row * topk + slot] = j;
+        a.scores[row * topk + slot] = s;
       }
     }
-  });
-  // merge top-2 over the 16 lanes holding each row, then pad and write counts
+    if (col) {
+      const int slot = colc[e] + __popc(cm & lower);
+      if (slot < TOPK_CAP) scratch[row * TOPK_CAP + slot] = make_uint2(__float_as_uint(s), (uint32_t)j);
+    }
+    outc[e] += __popc(sm);
+    colc[e] += __popc(cm);
+  };
+  auto top2_update = [&](int e, bool ok, float s) __attribute__((always_inline)) {
+    if constexpr (TOP2) {
+      const float so = ok ? s : -FLT_MAX;   // running top-2 with multiplicity
+      m2[e] = fmaxf(m2[e], fminf(m1[e], so));
+      m1[e] = fmaxf(m1[e], so);
+    }
+  };
+  if constexpr (!FB) {
+    sweep([&](int kt, f4* acc) __attribute__((always_inline)) {
+      const bool full = (kt + 1) * KT <= minvalid;
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+        const int j = kt * KT + 16 * nt + lr;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const bool ok = live[e] && (full || j < nvalid[e]);
+          const float s = acc[nt][e];
+          const bool sel = ok && s >= th1[e];
+          const bool col = ok && s >= th0[e] && s < th1[e];
+          emit(e, j, s, sel, col);
+          top2_update(e, ok, s);
+        }
+      }
+    });
+  } else {
+    int eqc[4] = {0, 0, 0, 0};
+    sweep([&](int kt, f4* acc) __attribute__((always_inline)) {
+      const bool full = (kt + 1) * KT <= minvalid;
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+        const int j = kt * KT + 16 * nt + lr;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const bool ok = live[e] && (full || j < nvalid[e]);
+          const float s = acc[nt][e];
+          bool sel = ok && s >= th1[e];
+          const bool col = ok && s >= th0[e] && s < th1[e];
+          const uint32_t km = f32_order_key(s) & msk[e];
+          const bool inb = ok && mode[e] == RADIX;
+          const bool eq = inb && km == pfx[e];
+          const uint32_t eqm = (uint32_t)(__ballot(eq) >> (16 * lg)) & 0xffffu;
+          sel = sel || (inb && (km > pfx[e] || (eq && eqc[e] + __popc(eqm & lower) < need[e])));
+          eqc[e] += __popc(eqm);
+          emit(e, j, s, sel, col);
+          top2_update(e, ok, s);
+        }
+      }
+    });
+  }
+  if (lr == 0) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      rowcnt[w][4 * lg + e][0] = outc[e];
+      rowcnt[w][4 * lg + e][1] = colc[e];
+    }
+  }
+  __syncthreads();
+
+  // ---- resolve collected rows: exact threshold among <= TOPK_CAP scores -----
+  uint32_t* h256 = &hist[w][0][0];   // 256 words of this wave's histogram area
+  if constexpr (!FB) for (int rr = 0; rr < 16; ++rr) {
+    const RowInfo ri = rinfo[w][rr];
+    if (ri.mode != COLLECT) continue;
+    const long row = (long)bh * Tq + (r0 + 16 * w + rr);
+    const int n = min(rowcnt[w][rr][1], TOPK_CAP);
+    int base = rowcnt[w][rr][0];
+    uint32_t key[CAPL];
+    int idx[CAPL];
+#pragma unroll
+    for (int m = 0; m < CAPL; ++m) {
+      const int p = 64 * m + lane;
+      key[m] = 0; idx[m] = 0;
+      if (p < n) {
+        const uint2 v = scratch[row * TOPK_CAP + p];
+        key[m] = f32_order_key(__uint_as_float(v.x));
+        idx[m] = (int)v.y;
+      }
+    }
+    uint32_t rp = 0, rm = 0;
+    uint32_t rneed = (uint32_t)ri.need;
+    for (int sh = 24; sh >= 0; sh -= 8) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) h256[4 * lane + q] = 0;
+      wave_lds_sync();
+#pragma unroll
+      for (int m = 0; m < CAPL; ++m) {
+        if (64 * m + lane < n && (key[m] & rm) == rp) atomicAdd(&h256[(key[m] >> sh) & 255u], 1u);
+      }
+      wave_lds_sync();
+      uint32_t c[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) c[q] = h256[255 - 4 * lane - q];
+      int bin;
+      uint32_t above, cnt;
+      find_bin(c, lane, rneed, bin, above, cnt);
+      rp |= (uint32_t)bin << sh;
+      rm |= 0xffu << sh;
+      rneed -= above;
+      wave_lds_sync();
+      if (cnt == rneed) break;
+    }
+    int eqn = 0;
+    const uint64_t below = (1ull << lane) - 1ull;
+#pragma unroll
+    for (int m = 0; m < CAPL; ++m) {
+      const bool valid = 64 * m + lane < n;
+      const uint32_t km = key[m] & rm;
+      const bool eq = valid && km == rp;
+      const uint64_t eb = __ballot(eq);
+      const int rank = __popcll(eb & below);
+      const bool sel = valid && (km > rp || (eq && eqn + rank < (int)rneed));
+      const uint64_t sb = __ballot(sel);
+      if (sel) {
+        const int slot = base + __popcll(sb & below);
+        if (slot < topk) {
+          a.indices[row * topk + slot] = idx[m];
+          a.scores[row * topk + slot] = key_to_f32(key[m]);
+        }
+      }
+      base += __popcll(sb);
+      eqn += __popcll(eb);
+    }
+    if (lane == 0) rowcnt[w][rr][0] = base;
+  }
+  __syncthreads();
+
+  // ---- merge top-2, pad, counts --------------------------------------------
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
+    const long rowg = (long)(grow0 + e);
+    if constexpr (TOP2) {
 #pragma unroll
-    for (int o = 1; o < 16; o <<= 1) {
-      const float b1 = __shfl_xor(m1[e], o, 64), b2 = __shfl_xor(m2[e], o, 64);
-      const float hi = fmaxf(m1[e], b1), lo = fmaxf(fminf(m1[e], b1), fmaxf(m2[e], b2));
-      m1[e] = hi; m2[e] = lo;
+      for (int o = 1; o < 16; o <<= 1) {
+        const float b1 = __shfl_xor(m1[e], o, 64), b2 = __shfl_xor(m2[e], o, 64);
+        const float hi = fmaxf(m1[e], b1), lo = fmaxf(fminf(m1[e], b1), fmaxf(m2[e], b2));
+        m1[e] = hi; m2[e] = lo;
+      }
     }
     if (!live[e]) continue;
-    const long row = rowbase[e] / topk;
-    for (int p = outc[e] + lr; p < topk; p += 16) {
-      a.indices[rowbase[e] + p] = 0;
-      a.scores[rowbase[e] + p] = -FLT_MAX;
+    const int oc = min(rowcnt[w][4 * lg + e][0], topk);
+    for (int p = oc + lr; p < topk; p += 16) {
+      a.indices[rowg * topk + p] = 0;
+      a.scores[rowg * topk + p] = -FLT_MAX;
     }
     if (lr == 0) {
-      if (a.counts) a.counts[row] = outc[e];
-      if (a.top2) { a.top2[2 * row] = m1[e]; a.top2[2 * row + 1] = m2[e]; }
+      if (a.counts) a.counts[rowg] = oc;
+      if constexpr (TOP2) { a.top2[2 * rowg] = m1[e]; a.top2[2 * rowg + 1] = m2[e]; }
     }
   }
 }
@@ -408,14 +703,19 @@ __global__ __launch_bounds__(256) void sort_rows_kernel(int32_t* __restrict__ in
   }
   for (int i = threadIdx.x; i < n; i += blockDim.x) {
     const unsigned long long key = sk[i];
-    const uint32_t ok = (uint32_t)(key >> 32);
-    const uint32_t u = (ok & 0x80000000u) ? (ok & 0x7fffffffu) : ~ok;
     ip[i] = (int32_t)(0xffffffffu - (uint32_t)(key & 0xffffffffu));
-    sp[i] = __uint_as_float(u);
+    sp[i] = key_to_f32((uint32_t)(key >> 32));
   }
 }
 
-hipError_t launch_score_topk(const TopkArgs& a, hipStream_t st) {
+size_t topk_workspace_bytes(int B, int Tq, int H) {
+  const size_t nqb = (Tq + QB - 1) / QB;
+  return (size_t)B * H * Tq * TOPK_CAP * sizeof(uint2) + (((size_t)B * H * nqb * sizeof(int) + 255) & ~(size_t)255) +
+         (size_t)B * H * sizeof(float) + 512;
+}
+
+hipError_t launch_score_topk(const TopkArgs& a0, hipStream_t st) {
+  TopkArgs a = a0;
   const int nqb = (a.Tq + QB - 1) / QB;
   const int BH = a.B * a.H;
   // score = acc / scale is evaluated as acc * (1/scale) with the reciprocal
@@ -425,19 +725,36 @@ hipError_t launch_score_topk(const TopkArgs& a, hipStream_t st) {
     const int qb0 = a.dump_row0 / QB;
     const int qb1 = (a.dump_row0 + a.dump_rows + QB - 1) / QB;
     const dim3 grid((unsigned)(BH * (qb1 - qb0)));
-    if (a.dtype == DT_F32) score_topk_kernel<float, true, true><<<grid, 256, 0, st>>>(a, nqb, ms);
-    else score_topk_kernel<bf16_t, true, true><<<grid, 256, 0, st>>>(a, nqb, ms);
+    if (a.dtype == DT_F32) score_topk_kernel<float, true, true, false, false><<<grid, 256, 0, st>>>(a, nqb, ms);
+    else score_topk_kernel<bf16_t, true, true, false, false><<<grid, 256, 0, st>>>(a, nqb, ms);
     return hipGetLastError();
   }
+  // workspace: [scratch lists | block flags | kmax]
+  char* ws = (char*)(((uintptr_t)a.workspace + 255) & ~(uintptr_t)255);
+  a.scratch = (uint2*)ws;
+  ws += (size_t)BH * a.Tq * TOPK_CAP * sizeof(uint2);
+  a.flags = (int*)ws;
+  ws += ((size_t)BH * nqb * sizeof(int) + 255) & ~(size_t)255;
+  float* kmax = (float*)ws;
+  a.kmax = kmax;
+  if (a.dtype == DT_F32) key_norm_max_kernel<float><<<dim3(BH), 256, 0, st>>>((const float*)a.k, a.Tk, a.H, a.D, kmax);
+  else key_norm_max_kernel<bf16_t><<<dim3(BH), 256, 0, st>>>((const bf16_t*)a.k, a.Tk, a.H, a.D, kmax);
   const dim3 grid((unsigned)(BH * nqb));
   const bool c16 = a.Tk <= 65535;   // 16-bit histogram counters cannot overflow
+  const bool t2 = a.top2 != nullptr;
+#define SGSA_TOPK_LAUNCH(XT, C, T2)                                                   \
+  do {                                                                                \
+    score_topk_kernel<XT, false, C, T2, false><<<grid, 256, 0, st>>>(a, nqb, ms);     \
+    score_topk_kernel<XT, false, C, T2, true><<<grid, 256, 0, st>>>(a, nqb, ms);      \
+  } while (0)
   if (a.dtype == DT_F32) {
-    if (c16) score_topk_kernel<float, false, true><<<grid, 256, 0, st>>>(a, nqb, ms);
-    else score_topk_kernel<float, false, false><<<grid, 256, 0, st>>>(a, nqb, ms);
+    if (c16) { if (t2) SGSA_TOPK_LAUNCH(float, true, true); else SGSA_TOPK_LAUNCH(float, true, false); }
+    else { if (t2) SGSA_TOPK_LAUNCH(float, false, true); else SGSA_TOPK_LAUNCH(float, false, false); }
   } else {
-    if (c16) score_topk_kernel<bf16_t, false, true><<<grid, 256, 0, st>>>(a, nqb, ms);
-    else score_topk_kernel<bf16_t, false, false><<<grid, 256, 0, st>>>(a, nqb, ms);
+    if (c16) { if (t2) SGSA_TOPK_LAUNCH(bf16_t, true, true); else SGSA_TOPK_LAUNCH(bf16_t, true, false); }
+    else { if (t2) SGSA_TOPK_LAUNCH(bf16_t, false, true); else SGSA_TOPK_LAUNCH(bf16_t, false, false); }
   }
+#undef SGSA_TOPK_LAUNCH
   return hipGetLastError();
 }
 

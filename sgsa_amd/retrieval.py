@@ -45,10 +45,14 @@ def score_topk(q: Tensor, k: Tensor, top_k: int, causal: bool = True, q_offset: 
     sc = torch.empty(B, H, Tq, kk, device=dev, dtype=torch.float32)
     top2 = torch.empty(B, H, Tq, 2, device=dev, dtype=torch.float32)
     cnt = torch.empty(B, H, Tq, device=dev, dtype=torch.int32)
-    _abi.check(_abi.lib().sgsa_score_topk(
+    L = _abi.lib()
+    nbytes = ctypes.c_size_t()
+    _abi.check(L.sgsa_score_topk_workspace_size(B, Tq, H, ctypes.byref(nbytes)))
+    ws = torch.empty(nbytes.value, device=dev, dtype=torch.uint8)
+    _abi.check(L.sgsa_score_topk(
         _abi.dtype_code(q.dtype), B, Tq, Tk, H, D, kk, int(causal), int(q_offset), float(scale), int(scale_mode),
         _abi.ptr(qc), _abi.ptr(kc), _abi.ptr(idx), _abi.ptr(sc), _abi.ptr(top2), _abi.ptr(cnt), int(sorted),
-        _abi.stream_of(qc)))
+        _abi.ptr(ws), nbytes.value, _abi.stream_of(qc)))
     return idx, sc, top2, cnt
 
 

@@ -277,8 +277,8 @@ def test_kv_reuse_causal_offset_and_probs():
 
 
 def test_make_inputs_shapes_and_rounding():
-    x = O.make_inputs(1, 16, 2, 8, dtype=torch.bfloat16, heavy_tail=True)
+    x = O.make_inputs(1, 300, 2, 8, dtype=torch.bfloat16, heavy_tail=True)
     assert x["q"].dtype == torch.bfloat16 and x["q_f32"].dtype == torch.float32
     assert torch.equal(x["q"].float(), x["q_f32"])
     n = (x["k_ret_f32"].norm(dim=-1) > 4).sum()
-    assert int(n) == 2 * round(0.01 * 16)
+    assert int(n) == 2 * round(0.01 * 300) and int(n) > 0
