@@ -6,8 +6,11 @@
 A step is one SGSA layer forward over the batch at the north-star shape
 (B=1, H=16, T=32768, d=128, top-k=2048, chunk 64, bf16 inputs, fp32 state):
   K1 sgsa_score_topk   causal score GEMM + exact top-k (ascending-index rows)
-  K2 sgsa_sparse_gather K/V gather + softmax weights + concentration/novelty +
-                        write gate (alpha)
+  K2 sgsa_sparse_gather_tiled  top-k weighted K/V sums (K/V streamed through
+                        LDS, weights applied with MFMA) + concentration/novelty +
+                        write gate (alpha); --gather direct uses the per-row
+                        gather kernel instead, and the other form is timed
+                        once for comparison
   K3-K5 sgsa_chunk_fwd  chunked gated-delta-rule update with the sparse write
 Inputs are synthetic (seed 0, the benchmark distribution) and resident in HBM
 before timing.  Per-stage durations come from HIP events recorded on the
@@ -125,8 +128,10 @@ def main() -> int:
                     help="run one plain 256 MiB fp32 copy kernel (torch.neg) first; its PMC byte counters "
                          "give the scale factor for the traffic of the SGSA kernels")
     ap.add_argument("--traffic-from", default=os.path.join(ROOT, "profiles", "hbm_traffic_north_star_pmc.md"),
-                    help="committed PMC summary whose 'gather_hbm_bytes_per_launch:' line gives the measured "
-                         "L2-to-fabric bytes of one gather launch at the north-star shape")
+                    help="committed PMC summary whose 'hbm_bytes_per_launch <kernel>:' lines give the measured "
+                         "L2-to-fabric bytes of one launch at the north-star shape")
+    ap.add_argument("--gather", choices=("tiled", "direct"), default="tiled",
+                    help="K2 form in the timed step: LDS-tiled MFMA (default) or per-row 16-byte gathers")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on exactly one GPU (got --gpus {args.gpus}); the SGSA layer shards by head, "
@@ -149,6 +154,8 @@ def main() -> int:
     idx = torch.empty(B, H, T, kk, device=dev, dtype=torch.int32)
     sc = torch.empty(B, H, T, kk, device=dev, dtype=torch.float32)
     cnt = torch.empty(B, H, T, device=dev, dtype=torch.int32)
+    top2 = torch.empty(B, H, T, 2, device=dev, dtype=torch.float32)
+    spl = torch.empty(B, H, T, device=dev, dtype=torch.int32)
     wk = torch.empty(B, T, H, D, device=dev, dtype=bf)
     vh = torch.empty_like(wk)
     al = torch.empty(B, T, H, device=dev, dtype=torch.float32)
@@ -167,18 +174,23 @@ def main() -> int:
 
     def k1():
         _abi.check(L.sgsa_score_topk(_abi.SGSA_BF16, B, T, T, H, D, kk, 1, 0, scale, 0, P(qd), P(kd), P(idx),
-                                     P(sc), None, P(cnt), 0, P(tws), tbytes.value, stream))
+                                     P(sc), P(top2), P(cnt), P(spl), 0, P(tws), tbytes.value, stream))
 
-    def k2():
+    def k2_tiled():
+        _abi.check(L.sgsa_sparse_gather_tiled(B, T, H, D, kk, P(kd), P(vd), P(idx), P(sc), P(top2), P(cnt),
+                                              P(spl), P(ud), 0, 0.25, 0.1, P(wk), P(vh), None, P(al), stream))
+
+    def k2_direct():
         _abi.check(L.sgsa_sparse_gather(_abi.SGSA_BF16, B, T, T, H, D, kk, 0, P(kd), P(vd), P(kd), P(idx), P(sc),
-                                        None, P(cnt), P(ud), 0, 0.25, 0.1, 64, 8, P(wk), P(vh), None, P(al),
+                                        P(top2), P(cnt), P(ud), 0, 0.25, 0.1, 64, 8, P(wk), P(vh), None, P(al),
                                         None, None, None, 0, stream))
 
     def k345():
         _abi.check(L.sgsa_chunk_fwd(_abi.SGSA_BF16, B, T, H, D, cfg["chunk"], P(qd), P(kd), P(vd), P(bd), P(gd),
                                     P(wk), P(vh), P(al), None, P(out), P(ht), P(ws), nbytes.value, stream))
 
-    stages = (("score_topk", k1), ("gather_gate", k2), ("chunk", k345))
+    k2_main, k2_other = (k2_tiled, k2_direct) if args.gather == "tiled" else (k2_direct, k2_tiled)
+    stages = (("score_topk", k1), ("gather_gate", k2_main), ("chunk", k345))
     cur = torch.cuda.current_stream(dev)
 
     def step(events=None):
@@ -214,25 +226,46 @@ def main() -> int:
     assert torch.isfinite(out.float()).all() and torch.isfinite(ht).all(), "non-finite layer output"
     log(f"ms/step {ms_step:.3f}  stages {json.dumps({n: round(v, 3) for n, v in stage_ms.items()})}")
 
-    gbytes = gather_bytes(B, H, T, D, kk)
-    traffic = None
+    # the other K2 form on the same top-k lists, for comparison (outside the timed steps)
+    other_ms = None
+    if args.steps > 0:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        k2_other()
+        e0.record(cur)
+        for _ in range(3):
+            k2_other()
+        e1.record(cur)
+        torch.cuda.synchronize()
+        other_ms = e0.elapsed_time(e1) / 3
+        log(f"gather ({'direct' if args.gather == 'tiled' else 'tiled'}) for comparison: {other_ms:.3f} ms")
+
+    measured = {}
     if args.traffic_from and os.path.exists(args.traffic_from) and (B, T, H, D, kk) == (1, 32768, 16, 128, 2048):
         with open(args.traffic_from) as f:
             for line in f:
-                if line.startswith("gather_hbm_bytes_per_launch:"):
-                    traffic = int(line.split(":", 1)[1])
-    g_s = stage_ms["gather_gate"] / 1000.0
-    achieved = gbytes / g_s / 1e9
-    roofline = {
-        "kernel": "sparse_gather_kernel (K2)",
-        "bound": "hbm",
-        "achieved": round(achieved, 1),
-        "peak": HBM_PEAK_GBS,
-        "unit": "GB/s",
-        "frac": round(achieved / HBM_PEAK_GBS, 4),
-        "traffic": traffic,
-        "algorithmic_bytes": gbytes,
+                if line.startswith("hbm_bytes_per_launch "):
+                    name, val = line[len("hbm_bytes_per_launch "):].split(":", 1)
+                    measured[name.strip()] = int(val)
+    gbytes = gather_bytes(B, H, T, D, kk)
+    f_score = B * H * T * (T + 1) * D               # causal score GEMM, one pass
+    f_chunk = B * H * ((T + 63) // 64) * 23.77e6     # chunk contractions (K3 + K5 + K4)
+    gather_kernel = "gather_tile_kernel" if args.gather == "tiled" else "sparse_gather_kernel"
+    rooflines = {
+        "score_topk": {"kernel": "score_topk_kernel (K1)", "bound": "mfma",
+                       "achieved": round(f_score / (stage_ms["score_topk"] / 1000.0) / 1e12, 2),
+                       "peak": 2500.0, "unit": "TFLOP/s", "traffic": measured.get("score_topk_kernel"),
+                       "algorithmic_flops": f_score},
+        "gather_gate": {"kernel": f"{gather_kernel} (K2)", "bound": "hbm",
+                        "achieved": round(gbytes / (stage_ms["gather_gate"] / 1000.0) / 1e9, 1),
+                        "peak": HBM_PEAK_GBS, "unit": "GB/s", "traffic": measured.get(gather_kernel),
+                        "algorithmic_bytes": gbytes},
+        "chunk": {"kernel": "chunk_intra/state/out (K3-K5)", "bound": "mfma",
+                  "achieved": round(f_chunk / (stage_ms["chunk"] / 1000.0) / 1e12, 2),
+                  "peak": 2500.0, "unit": "TFLOP/s", "traffic": None, "algorithmic_flops": f_chunk},
     }
+    for r in rooflines.values():
+        r["frac"] = round(r["achieved"] / r["peak"], 4)
+    dominant = max(stage_ms, key=stage_ms.get)
     result = {
         "metric": METRIC,
         "value": round(B * T / (ms_step / 1000.0), 1),
@@ -247,9 +280,11 @@ def main() -> int:
         "dtype": "bf16",
         "data": "synthetic",
         "config": {"workload": "sgsa_layer_fwd", "B": B, "T": T, "H": H, "D": D, "top_k": top_k,
-                   "chunk": cfg["chunk"], "state": "fp32"},
+                   "chunk": cfg["chunk"], "state": "fp32", "gather": args.gather},
         "stage_ms": {n: round(v, 3) for n, v in stage_ms.items()},
-        "roofline": roofline,
+        "gather_other_form_ms": round(other_ms, 3) if other_ms is not None else None,
+        "roofline": rooflines[dominant],
+        "rooflines": rooflines,
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:

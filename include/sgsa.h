@@ -87,7 +87,9 @@ int sgsa_chunk_fwd(int dtype, int B, int T, int H, int D, int chunk_size,
  * causal keeps keys <= that position.  Each row gets
  * counts = min(top_k, valid keys) selected slots, ties broken by lowest key
  * index; slots >= counts hold index 0 and score -FLT_MAX (:151-153).
- * sorted = 0: the selected slots in a deterministic order (not sorted);
+ * sorted = 0: the selected slots in a deterministic order made of two runs
+ * that each ascend in key index; split (may be NULL) receives the length of
+ * the first run [B,H,Tq];
  * sorted = 1: (score desc, index asc) as torch.topk(sorted=True) with the
  * lowest-index tie rule.  top2 (may be NULL) receives the two largest valid
  * scores (-FLT_MAX if absent).  Needs sgsa_score_topk_workspace_size() bytes
@@ -97,7 +99,7 @@ int sgsa_score_topk(int dtype, int B, int Tq, int Tk, int H, int D, int top_k,
                     int causal, int q_offset, float scale, int scale_mode,
                     const void* q, const void* k,
                     int32_t* indices, float* scores, float* top2, int32_t* counts,
-                    int sorted, void* workspace, size_t workspace_bytes, void* stream);
+                    int32_t* split, int sorted, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Known-answer hook: writes the exact fp32 scores sgsa_score_topk selects on,
  * for query rows [row0, row0+rows), to out [B,H,rows,Tk]; keys outside the
@@ -128,6 +130,17 @@ int sgsa_sparse_gather(int dtype, int B, int Tq, int Tk, int H, int D, int top_k
                        void* k_hat, void* v_hat, void* write_key, float* alpha,
                        float* weights, float* diag,
                        void* workspace, size_t workspace_bytes, void* stream);
+
+/* Tiled form of sgsa_sparse_gather for the layer path (bf16, D = 128, causal,
+ * Tq = Tk = T): streams K/V through LDS in 64-key tiles and applies the exact
+ * top-k weights with MFMA.  Needs the unsorted output of sgsa_score_topk with
+ * top2 and split; computes k_hat, v_hat, the write key and alpha (no
+ * weights / diagnostics outputs).  Same references as sgsa_sparse_gather. */
+int sgsa_sparse_gather_tiled(int B, int T, int H, int D, int top_k, const void* k, const void* v,
+                             const int32_t* indices, const float* scores, const float* top2,
+                             const int32_t* counts, const int32_t* split, const float* budget,
+                             int write_mode, float alpha_max, float tau_c, void* k_hat, void* v_hat,
+                             void* write_key, float* alpha, void* stream);
 
 /* ---- whole SGSA layer forward ------------------------------------------------
  * The attention half of SGSABlock.forward (modelings/modeling_sgsa.py:669-684)

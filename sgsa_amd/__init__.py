@@ -9,7 +9,7 @@ The compiled library (libsgsa_hip.so) is required; there is no fallback path.
 """
 
 from .ops import ChunkSGSAFunction, chunk_sgsa, chunk_sgsa_fwd
-from .retrieval import SparseRetriever, score_dump, score_topk, sparse_retrieve
+from .retrieval import SparseRetriever, gather_gate, score_dump, score_topk, sparse_retrieve
 from .layer import LayerWorkspace, sgsa_layer_forward
 
 __all__ = [
@@ -19,6 +19,7 @@ __all__ = [
     "SparseRetriever",
     "score_topk",
     "score_dump",
+    "gather_gate",
     "sparse_retrieve",
     "sgsa_layer_forward",
     "LayerWorkspace",

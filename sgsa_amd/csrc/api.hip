@@ -50,7 +50,7 @@ int check_dims(int B, int T, int H, int D) {
   do { if ((ptr) == nullptr) return fail(SGSA_ERR_INVALID_ARG, "%s must not be NULL", #ptr); } while (0)
 
 struct LayerWs {
-  size_t idx, sc, cnt, wk, vh, al, misc, topk, chunk, total;
+  size_t idx, sc, cnt, top2, split, wk, vh, al, misc, topk, chunk, total;
 };
 
 LayerWs layer_ws(int dtype, int B, int T, int H, int D, int top_k) {
@@ -61,6 +61,8 @@ LayerWs layer_ws(int dtype, int B, int T, int H, int D, int top_k) {
   w.idx = off; off = align_up(off + rows * kk * 4);
   w.sc = off; off = align_up(off + rows * kk * 4);
   w.cnt = off; off = align_up(off + rows * 4);
+  w.top2 = off; off = align_up(off + rows * 2 * 4);
+  w.split = off; off = align_up(off + rows * 4);
   w.wk = off; off = align_up(off + (size_t)B * T * H * D * dtype_size(dtype));
   w.vh = off; off = align_up(off + (size_t)B * T * H * D * dtype_size(dtype));
   w.al = off; off = align_up(off + (size_t)B * T * H * 4);
@@ -139,19 +141,20 @@ int sgsa_score_topk_workspace_size(int B, int Tq, int H, size_t* bytes) {
 
 int sgsa_score_topk(int dtype, int B, int Tq, int Tk, int H, int D, int top_k, int causal, int q_offset,
                     float scale, int scale_mode, const void* q, const void* k, int32_t* indices, float* scores,
-                    float* top2, int32_t* counts, int sorted, void* workspace, size_t workspace_bytes,
-                    void* stream) {
+                    float* top2, int32_t* counts, int32_t* split, int sorted, void* workspace,
+                    size_t workspace_bytes, void* stream) {
   if (int s = validate_topk(dtype, B, Tq, Tk, H, D, top_k, scale_mode, scale)) return s;
   REQUIRE(q); REQUIRE(k); REQUIRE(indices); REQUIRE(scores); REQUIRE(workspace);
   const size_t need_ws = sgsa::topk_workspace_bytes(B, Tq, H);
   if (workspace_bytes < need_ws) return fail(SGSA_ERR_WORKSPACE, "workspace %zu < %zu bytes", workspace_bytes, need_ws);
   if (sorted && counts == nullptr) return fail(SGSA_ERR_INVALID_ARG, "sorted output needs counts");
+  if (sorted && split != nullptr) return fail(SGSA_ERR_INVALID_ARG, "split describes the unsorted order; pass NULL with sorted=1");
   if (q_offset < 0) return fail(SGSA_ERR_INVALID_ARG, "q_offset must be >= 0");
   if (top_k > 4096 && sorted) return fail(SGSA_ERR_UNSUPPORTED, "sorted output supports top_k <= 4096");
   sgsa::TopkArgs a{};
   a.dtype = dtype; a.B = B; a.Tq = Tq; a.Tk = Tk; a.H = H; a.D = D; a.top_k = top_k;
   a.causal = causal ? 1 : 0; a.q_offset = q_offset; a.scale = scale; a.scale_mode = scale_mode;
-  a.q = q; a.k = k; a.indices = indices; a.scores = scores; a.top2 = top2; a.counts = counts;
+  a.q = q; a.k = k; a.indices = indices; a.scores = scores; a.top2 = top2; a.counts = counts; a.split = split;
   a.workspace = workspace;
   hipStream_t st = (hipStream_t)stream;
   if (int s = hip_status(sgsa::launch_score_topk(a, st), "sgsa_score_topk")) return s;
@@ -203,6 +206,28 @@ int sgsa_sparse_gather(int dtype, int B, int Tq, int Tk, int H, int D, int top_k
   return hip_status(sgsa::launch_sparse_gather(a, (hipStream_t)stream), "sgsa_sparse_gather");
 }
 
+int sgsa_sparse_gather_tiled(int B, int T, int H, int D, int top_k, const void* k, const void* v,
+                             const int32_t* indices, const float* scores, const float* top2,
+                             const int32_t* counts, const int32_t* split, const float* budget, int write_mode,
+                             float alpha_max, float tau_c, void* k_hat, void* v_hat, void* write_key,
+                             float* alpha, void* stream) {
+  if (int s = check_dims(B, T, H, D)) return s;
+  if (D != 128) return fail(SGSA_ERR_UNSUPPORTED, "the tiled gather needs D == 128 (got %d)", D);
+  if (top_k <= 0 || top_k > T) return fail(SGSA_ERR_INVALID_ARG, "top_k=%d must be in [1, T]", top_k);
+  REQUIRE(k); REQUIRE(v); REQUIRE(indices); REQUIRE(scores); REQUIRE(top2); REQUIRE(counts); REQUIRE(split);
+  REQUIRE(v_hat);
+  if (write_mode != 0 && write_mode != 1) return fail(SGSA_ERR_INVALID_ARG, "write_mode must be 0 (direct) or 1 (residual)");
+  if (budget != nullptr && alpha == nullptr) return fail(SGSA_ERR_INVALID_ARG, "the write gate needs an alpha output");
+  if (write_mode == 1 && budget != nullptr && write_key == nullptr)
+    return fail(SGSA_ERR_INVALID_ARG, "residual write mode needs a write_key output");
+  sgsa::GatherArgs g{};
+  g.dtype = SGSA_BF16; g.B = B; g.Tq = T; g.Tk = T; g.H = H; g.D = D; g.top_k = top_k; g.q_offset = 0;
+  g.k = k; g.v = v; g.self_key = k; g.indices = indices; g.scores = scores; g.top2 = top2; g.counts = counts;
+  g.use_valid = 1; g.tau_c = tau_c; g.eps = 1e-6f; g.budget = budget; g.write_mode = write_mode;
+  g.alpha_max = alpha_max; g.k_hat = k_hat; g.v_hat = v_hat; g.write_key = write_key; g.alpha = alpha;
+  return hip_status(sgsa::launch_sparse_gather_staged(g, split, (hipStream_t)stream), "sgsa_sparse_gather_tiled");
+}
+
 int sgsa_layer_fwd_workspace_size(int dtype, int B, int T, int H, int D, int top_k, size_t* bytes) {
   REQUIRE(bytes);
   if (int s = check_dtype(dtype)) return s;
@@ -230,6 +255,9 @@ int sgsa_layer_fwd(int dtype, int B, int T, int H, int D, int top_k, int chunk_s
   int32_t* idx = (int32_t*)(base + L.idx);
   float* sc = (float*)(base + L.sc);
   int32_t* cnt = (int32_t*)(base + L.cnt);
+  float* t2 = (float*)(base + L.top2);
+  int32_t* spl = (int32_t*)(base + L.split);
+  const bool tiled = dtype == SGSA_BF16 && D == 128;
   void* wk = base + L.wk;
   void* vh = base + L.vh;
   float* al = (float*)(base + L.al);
@@ -238,7 +266,8 @@ int sgsa_layer_fwd(int dtype, int B, int T, int H, int D, int top_k, int chunk_s
   sgsa::TopkArgs ta{};
   ta.dtype = dtype; ta.B = B; ta.Tq = T; ta.Tk = T; ta.H = H; ta.D = D; ta.top_k = kk; ta.causal = 1;
   ta.q_offset = 0; ta.scale = (float)sqrt((double)D); ta.scale_mode = 0;
-  ta.q = q_ret; ta.k = k; ta.indices = idx; ta.scores = sc; ta.top2 = nullptr; ta.counts = cnt;
+  ta.q = q_ret; ta.k = k; ta.indices = idx; ta.scores = sc; ta.counts = cnt;
+  ta.top2 = tiled ? t2 : nullptr; ta.split = tiled ? spl : nullptr;
   ta.workspace = base + L.topk;
   if (int s = hip_status(sgsa::launch_score_topk(ta, st), "sgsa_layer_fwd(topk)")) return s;
 
@@ -249,7 +278,12 @@ int sgsa_layer_fwd(int dtype, int B, int T, int H, int D, int top_k, int chunk_s
   ga.budget = budget; ga.write_mode = write_mode; ga.alpha_max = alpha_max;
   ga.k_hat = write_mode == 0 ? wk : nullptr; ga.v_hat = vh; ga.write_key = write_mode == 1 ? wk : nullptr;
   ga.alpha = al;
-  if (int s = hip_status(sgsa::launch_sparse_gather(ga, st), "sgsa_layer_fwd(gather)")) return s;
+  if (tiled) {
+    ga.top2 = t2;
+    if (int s = hip_status(sgsa::launch_sparse_gather_staged(ga, spl, st), "sgsa_layer_fwd(gather)")) return s;
+  } else {
+    if (int s = hip_status(sgsa::launch_sparse_gather(ga, st), "sgsa_layer_fwd(gather)")) return s;
+  }
 
   sgsa::ChunkArgs ca{};
   ca.dtype = dtype; ca.B = B; ca.T = T; ca.H = H; ca.D = D;

@@ -48,6 +48,7 @@ struct TopkArgs {
   float* scores;      // [B,H,Tq,top_k]
   float* top2;        // [B,H,Tq,2] or nullptr
   int32_t* counts;    // [B,H,Tq] valid selected slots, or nullptr
+  int32_t* split;     // [B,H,Tq] length of the leading ascending-index run, or nullptr
   float* dump;        // score-dump mode: [B,H,dump_rows,Tk]; nullptr = select mode
   int dump_row0, dump_rows;
   void* workspace;    // topk_workspace_bytes(): candidate lists + per-head key norms
@@ -93,5 +94,8 @@ struct GatherArgs {
 
 constexpr int NDIAG = 10;
 hipError_t launch_sparse_gather(const GatherArgs& a, hipStream_t st);
+// LDS-staged variant for the fused layer path: bf16, D = 128, rows whose
+// slots [0, split) ascend in key index; no weights/diag outputs.
+hipError_t launch_sparse_gather_staged(const GatherArgs& a, const int32_t* split, hipStream_t st);
 
 }  // namespace sgsa

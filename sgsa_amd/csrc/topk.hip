@@ -190,6 +190,7 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb, fl
   __shared__ uint32_t hist[4][16][HWA];
   __shared__ RowInfo rinfo[4][16];
   __shared__ int rowcnt[4][16][2];   // emitted count, collected count
+  __shared__ int run1[4][16];        // length of the leading ascending run
   __shared__ float qnorm[4][16];
 
   const int BH = a.B * a.H;
@@ -571,6 +572,7 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb, fl
     for (int e = 0; e < 4; ++e) {
       rowcnt[w][4 * lg + e][0] = outc[e];
       rowcnt[w][4 * lg + e][1] = colc[e];
+      run1[w][4 * lg + e] = outc[e];
     }
   }
   __syncthreads();
@@ -663,6 +665,7 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb, fl
     }
     if (lr == 0) {
       if (a.counts) a.counts[rowg] = oc;
+      if (a.split) a.split[rowg] = min(run1[w][4 * lg + e], oc);
       if constexpr (TOP2) { a.top2[2 * rowg] = m1[e]; a.top2[2 * rowg + 1] = m2[e]; }
     }
   }

@@ -23,12 +23,14 @@ Tensor = torch.Tensor
 
 
 def score_topk(q: Tensor, k: Tensor, top_k: int, causal: bool = True, q_offset: int = 0,
-               scale: Optional[float] = None, scale_mode: int = 0, sorted: bool = True):
+               scale: Optional[float] = None, scale_mode: int = 0, sorted: bool = True,
+               return_split: bool = False):
     """Exact top-k over causal scores without materialising them.
 
     q [B,Tq,H,D], k [B,Tk,H,D].  Returns (indices int32 [B,H,Tq,kk],
     scores float32 [B,H,Tq,kk], top2 float32 [B,H,Tq,2], counts int32 [B,H,Tq])
-    with kk = min(top_k, Tk).
+    with kk = min(top_k, Tk); with ``return_split`` (unsorted output only) also
+    the length of each row's first ascending run.
     """
     if not q.is_cuda:
         raise ValueError("score_topk: the SGSA kernels run on a ROCm GPU; got CPU tensors")
@@ -45,15 +47,52 @@ def score_topk(q: Tensor, k: Tensor, top_k: int, causal: bool = True, q_offset: 
     sc = torch.empty(B, H, Tq, kk, device=dev, dtype=torch.float32)
     top2 = torch.empty(B, H, Tq, 2, device=dev, dtype=torch.float32)
     cnt = torch.empty(B, H, Tq, device=dev, dtype=torch.int32)
+    spl = torch.empty(B, H, Tq, device=dev, dtype=torch.int32) if return_split else None
     L = _abi.lib()
     nbytes = ctypes.c_size_t()
     _abi.check(L.sgsa_score_topk_workspace_size(B, Tq, H, ctypes.byref(nbytes)))
     ws = torch.empty(nbytes.value, device=dev, dtype=torch.uint8)
     _abi.check(L.sgsa_score_topk(
         _abi.dtype_code(q.dtype), B, Tq, Tk, H, D, kk, int(causal), int(q_offset), float(scale), int(scale_mode),
-        _abi.ptr(qc), _abi.ptr(kc), _abi.ptr(idx), _abi.ptr(sc), _abi.ptr(top2), _abi.ptr(cnt), int(sorted),
-        _abi.ptr(ws), nbytes.value, _abi.stream_of(qc)))
+        _abi.ptr(qc), _abi.ptr(kc), _abi.ptr(idx), _abi.ptr(sc), _abi.ptr(top2), _abi.ptr(cnt), _abi.ptr(spl),
+        int(sorted), _abi.ptr(ws), nbytes.value, _abi.stream_of(qc)))
+    if return_split:
+        return idx, sc, top2, cnt, spl
     return idx, sc, top2, cnt
+
+
+def gather_gate(k: Tensor, v: Tensor, idx: Tensor, sc: Tensor, top2: Tensor, cnt: Tensor,
+                budget_logits: Tensor, split: Optional[Tensor] = None, write_mode: str = "direct",
+                alpha_max: float = 0.25, tau_c: float = 0.1):
+    """K2 of the layer path on top of ``score_topk`` output: (write key, v_hat, alpha).
+
+    With ``split`` (unsorted top-k output, bf16, D=128) the tiled kernel runs;
+    without it, the direct row gather.  k, v: [B,T,H,D]; budget_logits [B,T,H].
+    """
+    B, T, H, D = k.shape
+    kk = idx.shape[-1]
+    mode = {"direct": 0, "residual": 1}[write_mode]
+    kc, vc = k.contiguous(), v.contiguous()
+    dev = k.device
+    wk = torch.empty(B, T, H, D, device=dev, dtype=k.dtype)
+    vh = torch.empty_like(wk)
+    al = torch.empty(B, T, H, device=dev, dtype=torch.float32)
+    bud = budget_logits.float().contiguous()
+    L = _abi.lib()
+    khat = wk if mode == 0 else None
+    wkey = wk if mode == 1 else None
+    if split is not None:
+        _abi.check(L.sgsa_sparse_gather_tiled(
+            B, T, H, D, kk, _abi.ptr(kc), _abi.ptr(vc), _abi.ptr(idx), _abi.ptr(sc), _abi.ptr(top2),
+            _abi.ptr(cnt), _abi.ptr(split), _abi.ptr(bud), mode, float(alpha_max), float(tau_c),
+            _abi.ptr(khat), _abi.ptr(vh), _abi.ptr(wkey), _abi.ptr(al), _abi.stream_of(kc)))
+    else:
+        _abi.check(L.sgsa_sparse_gather(
+            _abi.dtype_code(k.dtype), B, T, T, H, D, kk, 0, _abi.ptr(kc), _abi.ptr(vc), _abi.ptr(kc),
+            _abi.ptr(idx), _abi.ptr(sc), _abi.ptr(top2), _abi.ptr(cnt), _abi.ptr(bud), mode, float(alpha_max),
+            float(tau_c), 64, 8, _abi.ptr(khat), _abi.ptr(vh), _abi.ptr(wkey), _abi.ptr(al), None, None, None, 0,
+            _abi.stream_of(kc)))
+    return wk, vh, al
 
 
 def score_dump(q: Tensor, k: Tensor, row0: int, rows: int, causal: bool = True, q_offset: int = 0,

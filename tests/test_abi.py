@@ -60,16 +60,16 @@ def test_workspace_size_queries():
      "workspace"),
     (lambda L, p: L.sgsa_chunk_fwd(0, 1, 0, 1, 64, 64, p, p, p, p, p, None, None, None, None, p, None, p, 1 << 30, None),
      "positive"),
-    (lambda L, p: L.sgsa_score_topk(1, 1, 16, 16, 2, 64, 32, 1, 0, 8.0, 0, p, p, p, p, None, None, 0, p, 1 << 30, None),
+    (lambda L, p: L.sgsa_score_topk(1, 1, 16, 16, 2, 64, 32, 1, 0, 8.0, 0, p, p, p, p, None, None, None, 0, p, 1 << 30, None),
      "exceeds"),
-    (lambda L, p: L.sgsa_score_topk(1, 1, 16, 16, 2, 64, 4, 1, 0, 8.0, 2, p, p, p, p, None, None, 0, p, 1 << 30, None),
+    (lambda L, p: L.sgsa_score_topk(1, 1, 16, 16, 2, 64, 4, 1, 0, 8.0, 2, p, p, p, p, None, None, None, 0, p, 1 << 30, None),
      "scale_mode"),
-    (lambda L, p: L.sgsa_score_topk(1, 1, 16, 16, 2, 64, 4, 1, 0, 8.0, 0, p, None, p, p, None, None, 0, p, 1 << 30, None),
+    (lambda L, p: L.sgsa_score_topk(1, 1, 16, 16, 2, 64, 4, 1, 0, 8.0, 0, p, None, p, p, None, None, None, 0, p, 1 << 30, None),
      "k must not be NULL"),
-    (lambda L, p: L.sgsa_score_topk(1, 1, 16, 16, 2, 64, 4, 1, 0, 8.0, 0, p, p, p, p, None, None, 1, p, 1 << 30,
+    (lambda L, p: L.sgsa_score_topk(1, 1, 16, 16, 2, 64, 4, 1, 0, 8.0, 0, p, p, p, p, None, None, None, 1, p, 1 << 30,
                                     None),
      "counts"),
-    (lambda L, p: L.sgsa_score_topk(1, 1, 16, 16, 2, 64, 4, 1, 0, 8.0, 0, p, p, p, p, None, p, 0, p, 64, None),
+    (lambda L, p: L.sgsa_score_topk(1, 1, 16, 16, 2, 64, 4, 1, 0, 8.0, 0, p, p, p, p, None, p, None, 0, p, 64, None),
      "workspace"),
     (lambda L, p: L.sgsa_score_dump(1, 1, 16, 16, 2, 64, 1, 0, 8.0, 0, p, p, 10, 10, p, None),
      "row range"),

@@ -84,3 +84,20 @@ def test_layer_forward_deterministic(dev):
     o2, s2 = sgsa_amd.sgsa_layer_forward(*args, k)
     torch.cuda.synchronize()
     assert torch.equal(o1, o2) and torch.equal(s1, s2)
+
+
+@pytest.mark.parametrize("write_mode", ["direct", "residual"])
+@pytest.mark.parametrize("dims", [(1, 2100, 2, 128, 256), (2, 700, 3, 128, 64)])
+def test_tiled_gather_matches_direct_gather(dev, write_mode, dims):
+    # the LDS-tiled MFMA form of K2 against the row-gather form on the same top-k lists
+    B, T, H, D, k = dims
+    x = O.make_inputs(B, T, H, D, dtype=torch.bfloat16, seed=5)
+    q, kk, v, bud = x["q"].to(dev), x["k"].to(dev), x["v"].to(dev), x["budget"].to(dev)
+    idx, sc, top2, cnt, spl = sgsa_amd.score_topk(q, kk, k, sorted=False, return_split=True)
+    wk_t, vh_t, al_t = sgsa_amd.gather_gate(kk, v, idx, sc, top2, cnt, bud, split=spl, write_mode=write_mode)
+    wk_d, vh_d, al_d = sgsa_amd.gather_gate(kk, v, idx, sc, top2, cnt, bud, split=None, write_mode=write_mode)
+    torch.cuda.synchronize()
+    assert (spl <= cnt).all() and (spl >= 0).all()
+    _close(wk_t, wk_d, 1e-2, "write_key")
+    _close(vh_t, vh_d, 1e-2, "v_hat")
+    _close(al_t, al_d, 1e-2, "alpha")
