@@ -131,8 +131,8 @@ int sgsa_sparse_gather(int dtype, int B, int Tq, int Tk, int H, int D, int top_k
                        float* weights, float* diag,
                        void* workspace, size_t workspace_bytes, void* stream);
 
-/* Tiled form of sgsa_sparse_gather for the layer path (bf16, D = 128, causal,
- * Tq = Tk = T): streams K/V through LDS in 64-key tiles and applies the exact
+/* Tiled form of sgsa_sparse_gather for the layer path (bf16, D = 128,
+ * top_k % 4 == 0, causal, Tq = Tk = T): streams K/V through LDS in 64-key tiles and applies the exact
  * top-k weights with MFMA.  Needs the unsorted output of sgsa_score_topk with
  * top2 and split; computes k_hat, v_hat, the write key and alpha (no
  * weights / diagnostics outputs).  Same references as sgsa_sparse_gather. */

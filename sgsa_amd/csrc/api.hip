@@ -214,6 +214,7 @@ int sgsa_sparse_gather_tiled(int B, int T, int H, int D, int top_k, const void* 
   if (int s = check_dims(B, T, H, D)) return s;
   if (D != 128) return fail(SGSA_ERR_UNSUPPORTED, "the tiled gather needs D == 128 (got %d)", D);
   if (top_k <= 0 || top_k > T) return fail(SGSA_ERR_INVALID_ARG, "top_k=%d must be in [1, T]", top_k);
+  if (top_k % 4 != 0) return fail(SGSA_ERR_UNSUPPORTED, "the tiled gather needs top_k %% 4 == 0 (got %d)", top_k);
   REQUIRE(k); REQUIRE(v); REQUIRE(indices); REQUIRE(scores); REQUIRE(top2); REQUIRE(counts); REQUIRE(split);
   REQUIRE(v_hat);
   if (write_mode != 0 && write_mode != 1) return fail(SGSA_ERR_INVALID_ARG, "write_mode must be 0 (direct) or 1 (residual)");
@@ -257,7 +258,7 @@ int sgsa_layer_fwd(int dtype, int B, int T, int H, int D, int top_k, int chunk_s
   int32_t* cnt = (int32_t*)(base + L.cnt);
   float* t2 = (float*)(base + L.top2);
   int32_t* spl = (int32_t*)(base + L.split);
-  const bool tiled = dtype == SGSA_BF16 && D == 128;
+  const bool tiled = dtype == SGSA_BF16 && D == 128 && kk % 4 == 0;
   void* wk = base + L.wk;
   void* vh = base + L.vh;
   float* al = (float*)(base + L.al);

@@ -13,9 +13,13 @@
 //
 // Slot lists come from K1: per row, slots [0, split) ascend in key index and
 // slots [split, count) ascend in key index, so each row keeps two cursors that
-// advance monotonically with the tile index.  Weights are exp(s - m) with the
-// row maximum m from K1 (top2); the softmax denominator is summed in fp32
-// from the unrounded weights.
+// advance monotonically with the tile index.  The four lanes of a row hold a
+// 32-slot window of each run in registers (16-byte loads, issued right after
+// the tile that consumed the previous window, so their latency overlaps the
+// MFMA work and the next K/V tile); a row that exhausts a window inside one
+// tile reloads it and goes round again.  Weights are exp(s - m) with the row
+// maximum m from K1 (top2); the softmax denominator is summed in fp32 from the
+// unrounded weights.  Requires top_k % 4 == 0 (16-byte aligned windows).
 #include "common.h"
 #include "kernels.h"
 
@@ -37,6 +41,59 @@ __device__ __forceinline__ void wave_lds_sync() {
 }
 
 __device__ __forceinline__ bf16x8 as_bf8(uint4 u) { return __builtin_bit_cast(bf16x8, u); }
+
+// One ascending run of a row's slot list.  Lane quarter lg holds positions
+// base + 16h + 4lg + e (h = 0, 1; e = 0..3) of the window.
+struct SlotRun {
+  int c, end, base;
+  int4 ix[2];
+  float4 sc[2];
+};
+
+// (Re)load the 32-slot window at the cursor.  Always issues the same four
+// loads (addresses clamped into the row) so the wait counts stay static;
+// positions at or past `end` are masked when consumed.
+__device__ __forceinline__ void slot_window(SlotRun& r, const int* __restrict__ idxp,
+                                            const float* __restrict__ scp, int lg, int topk) {
+  r.base = r.c & ~3;
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) {
+    const int p = min(r.base + 16 * hh + 4 * lg, topk - 4);
+    r.ix[hh] = *reinterpret_cast<const int4*>(idxp + p);
+    r.sc[hh] = *reinterpret_cast<const float4*>(scp + p);
+  }
+}
+
+// Scatter the window's slots with key in [t0, t1) into this wave's P rows.
+// Returns the lane's consumed count; `stop` is set when a held slot lies at or
+// beyond t1 (the row is done with this tile).
+__device__ __forceinline__ int slot_consume(const SlotRun& r, int t0, int t1, int lg, float m, uint16_t* prow,
+                                            float& esum, bool& stop) {
+  int n = 0;
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) {
+    const int js[4] = {r.ix[hh].x, r.ix[hh].y, r.ix[hh].z, r.ix[hh].w};
+    const float ss[4] = {r.sc[hh].x, r.sc[hh].y, r.sc[hh].z, r.sc[hh].w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int pos = r.base + 16 * hh + 4 * lg + e;
+      if (pos >= r.c && pos < r.end) {
+        const int j = js[e];
+        if (j < t1) {
+          ++n;
+          if (j >= t0) {
+            const float wv = __expf(ss[e] - m);
+            esum += wv;
+            prow[j - t0] = f32_to_bf16(wv);
+          }
+        } else {
+          stop = true;
+        }
+      }
+    }
+  }
+  return n;
+}
 
 }  // namespace
 
@@ -71,7 +128,6 @@ __global__ __launch_bounds__(256) void gather_tile_kernel(GatherArgs a, const in
     end1 = min(split[rg], end2);
     m = a.top2[2 * rg];
   }
-  int c1 = 0, c2 = end1;
   float esum = 0.f;
 
   int kend = Tk;
@@ -84,25 +140,35 @@ __global__ __launch_bounds__(256) void gather_tile_kernel(GatherArgs a, const in
   // ---- K/V tile staging (transposed), register prefetch one tile ahead -----
   // thread t: key pair kp = t % 32 (keys 2kp, 2kp+1), 8-dim chunks c = t/32 and c+8
   const int kp = tid & 31, cq = tid >> 5;
+  // Loads are unconditional (key index clamped into [0, Tk)) so every thread
+  // issues the same number of memory operations per tile; keys past Tk are
+  // zeroed at commit.
   uint4 pk[2][2], pv[2][2];   // [chunk half][key of the pair]
+  uint32_t pmask[2];          // all-ones for keys < Tk
   auto issue = [&](int kt) __attribute__((always_inline)) {
 #pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-      const int c = cq + 8 * hh;
+    for (int u = 0; u < 2; ++u) {
+      const int j = kt * KT + 2 * kp + u;
+      pmask[u] = j < Tk ? 0xffffffffu : 0u;
+      const int jc = min(j, Tk - 1);
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int j = kt * KT + 2 * kp + u;
-        pk[hh][u] = make_uint4(0, 0, 0, 0);
-        pv[hh][u] = make_uint4(0, 0, 0, 0);
-        if (j < Tk) {
-          const long off = ((long)(b * Tk + j) * H + h) * DP + 8 * c;
-          pk[hh][u] = *reinterpret_cast<const uint4*>(K + off);
-          pv[hh][u] = *reinterpret_cast<const uint4*>(V + off);
-        }
+      for (int hh = 0; hh < 2; ++hh) {
+        const long off = ((long)(b * Tk + jc) * H + h) * DP + 8 * (cq + 8 * hh);
+        pk[hh][u] = *reinterpret_cast<const uint4*>(K + off);
+        pv[hh][u] = *reinterpret_cast<const uint4*>(V + off);
       }
     }
   };
   auto commit = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const uint32_t mk = pmask[u];
+        pk[hh][u] = make_uint4(pk[hh][u].x & mk, pk[hh][u].y & mk, pk[hh][u].z & mk, pk[hh][u].w & mk);
+        pv[hh][u] = make_uint4(pv[hh][u].x & mk, pv[hh][u].y & mk, pv[hh][u].z & mk, pv[hh][u].w & mk);
+      }
+    }
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
       const int c = cq + 8 * hh;
@@ -129,62 +195,47 @@ __global__ __launch_bounds__(256) void gather_tile_kernel(GatherArgs a, const in
 #pragma unroll
   for (int n = 0; n < DP / 16; ++n) { ok_[n] = f4_zero(); ov_[n] = f4_zero(); }
   uint16_t* Pw = P[w];
+  uint16_t* prw = Pw + lr * PT;
   const int* idxp = a.indices + pbase;
   const float* scp = a.scores + pbase;
+  SlotRun run1, run2;
+  run1.c = 0; run1.end = end1;
+  run2.c = end1; run2.end = end2;
+  issue(0);   // same order as in the loop: K/V tile, then the slot windows
+  slot_window(run1, idxp, scp, lg, topk);
+  slot_window(run2, idxp, scp, lg, topk);
 
-  issue(0);
   for (int kt = 0; kt < ntile; ++kt) {
     const int t0 = kt * KT, t1 = t0 + KT;
     __syncthreads();           // previous tile's K/V and P reads are done
     commit();
     // clear this wave's P rows (16 x PT bf16 = 144 uint4)
     for (int e = lane; e < 16 * PT / 8; e += 64) reinterpret_cast<uint4*>(Pw)[e] = make_uint4(0, 0, 0, 0);
-    if (kt + 1 < ntile) issue(kt + 1);
+    issue(min(kt + 1, ntile - 1));   // unconditional: keeps the wait counts static
     wave_lds_sync();
-    // scatter this tile's weights: run 1 (8 slots per row per round), run 2 (4 slots per round)
-    for (;;) {
-      int n1 = 0;
-      bool full1 = false;
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int p = c1 + lg + 4 * i;
-        if (p < end1) {
-          const int j = idxp[p];
-          if (j < t1) {
-            ++n1;
-            if (j >= t0)
-            {
-              const float wv = __expf(scp[p] - m);
-              esum += wv;
-              Pw[lr * PT + (j - t0)] = f32_to_bf16(wv);
-            }
-          }
-        }
-      }
+    // scatter this tile's weights from both runs and reload each window behind
+    // it; the first pass uses windows loaded during the previous tile
+    auto scatter_pass = [&]() __attribute__((always_inline)) -> bool {
+      bool stop1 = false, stop2 = false;
+      int n1 = slot_consume(run1, t0, t1, lg, m, prw, esum, stop1);
+      int n2 = slot_consume(run2, t0, t1, lg, m, prw, esum, stop2);
       n1 += __shfl_xor(n1, 16, 64);
       n1 += __shfl_xor(n1, 32, 64);
-      c1 += n1;
-      full1 = (n1 == 8);
-      int n2 = 0;
-      {
-        const int p = c2 + lg;
-        if (p < end2) {
-          const int j = idxp[p];
-          if (j < t1) {
-            ++n2;
-            if (j >= t0) {
-              const float wv = __expf(scp[p] - m);
-              esum += wv;
-              Pw[lr * PT + (j - t0)] = f32_to_bf16(wv);
-            }
-          }
-        }
-      }
       n2 += __shfl_xor(n2, 16, 64);
       n2 += __shfl_xor(n2, 32, 64);
-      c2 += n2;
-      const bool more = (full1 && c1 < end1) || (n2 == 4 && c2 < end2);
-      if (__ballot(more) == 0) break;
+      const uint64_t s1 = __ballot(stop1), s2 = __ballot(stop2);
+      stop1 = ((s1 >> lr) | (s1 >> (lr + 16)) | (s1 >> (lr + 32)) | (s1 >> (lr + 48))) & 1;
+      stop2 = ((s2 >> lr) | (s2 >> (lr + 16)) | (s2 >> (lr + 32)) | (s2 >> (lr + 48))) & 1;
+      run1.c += n1;
+      run2.c += n2;
+      slot_window(run1, idxp, scp, lg, topk);
+      slot_window(run2, idxp, scp, lg, topk);
+      // a row that consumed its whole window without meeting t1 may have more keys in this tile
+      return (!stop1 && run1.c < run1.end) || (!stop2 && run2.c < run2.end);
+    };
+    if (__ballot(scatter_pass())) {
+      while (__ballot(scatter_pass())) {
+      }
     }
     __syncthreads();           // K/V tile committed by all threads; P rows written
     // k_hat += P K, v_hat += P V  (P: 16 rows x 64 keys, K/V: 64 keys x 128 dims)

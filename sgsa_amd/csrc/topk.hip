@@ -47,6 +47,7 @@ constexpr int QB = 64;        // query rows per block
 constexpr int KT = 64;        // keys per tile
 constexpr int DP = 128;       // padded head dim
 constexpr int NBIN = 256;
+constexpr int KNCH = 32;      // partial key-norm maxima per (batch, head)
 
 enum RowMode { SELECT_ALL = 0, BIN_ALL = 1, COLLECT = 2, RADIX = 3 };
 
@@ -150,25 +151,31 @@ __device__ __forceinline__ void find_bin(const uint32_t (&c)[4], int lane, uint3
 }  // namespace
 
 // Max |k_j| per (b,h): the denominator of the pass-A bin scale.  grid (B*H), 256 threads.
+// Squared key-norm maxima of one (batch, head): block (bh, c) covers rows
+// j = c (mod KNCH), 16 lanes per row; kmax2[bh * KNCH + c] = max_j |k_j|^2.
 template <typename X>
 __global__ __launch_bounds__(256) void key_norm_max_kernel(const X* __restrict__ k, int Tk, int H, int D,
-                                                           float* __restrict__ kmax) {
+                                                           float* __restrict__ kmax2) {
   __shared__ float red[4];
-  const int bh = blockIdx.x, b = bh / H, h = bh % H;
+  const int bh = blockIdx.x / KNCH, c = blockIdx.x % KNCH, b = bh / H, h = bh % H;
+  const int sub = threadIdx.x & 15, rw = threadIdx.x >> 4;
   float m = 0.f;
-  for (int j = threadIdx.x; j < Tk; j += blockDim.x) {
-    const X* row = k + ((long)(b * Tk + j) * H + h) * D;
+  for (int j0 = c; j0 < Tk; j0 += KNCH * 16) {   // trip count uniform over the block
+    const int j = j0 + KNCH * rw;
     float s = 0.f;
-    for (int d = 0; d < D; ++d) {
-      const float x = ld(row, d);
-      s = fmaf(x, x, s);
+    if (j < Tk) {
+      const X* row = k + ((long)(b * Tk + j) * H + h) * D;
+      for (int d = sub; d < D; d += 16) {
+        const float x = ld(row, d);
+        s = fmaf(x, x, s);
+      }
     }
-    m = fmaxf(m, s);
+    m = fmaxf(m, group_sum(s, 16));
   }
   m = wave_max(m);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
   __syncthreads();
-  if (threadIdx.x == 0) kmax[bh] = sqrtf(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
+  if (threadIdx.x == 0) kmax2[blockIdx.x] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
 }
 
 // FB = false: the two-pass select; a block with a row whose threshold bin holds
@@ -324,12 +331,14 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb, fl
     if (a.flags[bid] == 0) return;   // block-uniform
   }
   __syncthreads();   // qnorm visible
+  float kmx2 = lane < KNCH ? a.kmax[(long)bh * KNCH + lane] : 0.f;
+  const float kmx = sqrtf(wave_max(kmx2));
   if (lane < 16) {
     const int qr = r0 + 16 * w + lane;
     int nv = 0;
     if (qr < Tq) nv = a.causal ? max(0, min(Tk, qr + a.q_offset + 1)) : Tk;
     RowInfo ri;
-    const float bound = qnorm[w][lane] * a.kmax[bh] * fabsf(mscale) * 1.001f;
+    const float bound = qnorm[w][lane] * kmx * fabsf(mscale) * 1.001f;
     ri.iw = (bound > 0.f && bound < FLT_MAX) ? 128.0f / bound : 0.f;
     ri.bstar = -1;
     ri.need = min(topk, nv);
@@ -714,7 +723,7 @@ __global__ __launch_bounds__(256) void sort_rows_kernel(int32_t* __restrict__ in
 size_t topk_workspace_bytes(int B, int Tq, int H) {
   const size_t nqb = (Tq + QB - 1) / QB;
   return (size_t)B * H * Tq * TOPK_CAP * sizeof(uint2) + (((size_t)B * H * nqb * sizeof(int) + 255) & ~(size_t)255) +
-         (size_t)B * H * sizeof(float) + 512;
+         (size_t)B * H * KNCH * sizeof(float) + 512;
 }
 
 hipError_t launch_score_topk(const TopkArgs& a0, hipStream_t st) {
@@ -740,8 +749,9 @@ hipError_t launch_score_topk(const TopkArgs& a0, hipStream_t st) {
   ws += ((size_t)BH * nqb * sizeof(int) + 255) & ~(size_t)255;
   float* kmax = (float*)ws;
   a.kmax = kmax;
-  if (a.dtype == DT_F32) key_norm_max_kernel<float><<<dim3(BH), 256, 0, st>>>((const float*)a.k, a.Tk, a.H, a.D, kmax);
-  else key_norm_max_kernel<bf16_t><<<dim3(BH), 256, 0, st>>>((const bf16_t*)a.k, a.Tk, a.H, a.D, kmax);
+  const dim3 kgrid((unsigned)(BH * KNCH));
+  if (a.dtype == DT_F32) key_norm_max_kernel<float><<<kgrid, 256, 0, st>>>((const float*)a.k, a.Tk, a.H, a.D, kmax);
+  else key_norm_max_kernel<bf16_t><<<kgrid, 256, 0, st>>>((const bf16_t*)a.k, a.Tk, a.H, a.D, kmax);
   const dim3 grid((unsigned)(BH * nqb));
   const bool c16 = a.Tk <= 65535;   // 16-bit histogram counters cannot overflow
   const bool t2 = a.top2 != nullptr;
