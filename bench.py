@@ -131,7 +131,8 @@ def main() -> int:
                     help="committed PMC summary whose 'hbm_bytes_per_launch <kernel>:' lines give the measured "
                          "L2-to-fabric bytes of one launch at the north-star shape")
     ap.add_argument("--gather", choices=("tiled", "direct"), default="tiled",
-                    help="K2 form in the timed step: LDS-tiled MFMA (default) or per-row 16-byte gathers")
+                    help="timed step: the fused layer path (K1 tile lists -> LDS-tiled MFMA K2 -> chunk, what "
+                         "sgsa_layer_fwd runs; default) or K1 row lists -> per-row 16-byte gathers -> chunk")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on exactly one GPU (got --gpus {args.gpus}); the SGSA layer shards by head, "
@@ -155,7 +156,6 @@ def main() -> int:
     sc = torch.empty(B, H, T, kk, device=dev, dtype=torch.float32)
     cnt = torch.empty(B, H, T, device=dev, dtype=torch.int32)
     top2 = torch.empty(B, H, T, 2, device=dev, dtype=torch.float32)
-    spl = torch.empty(B, H, T, device=dev, dtype=torch.int32)
     wk = torch.empty(B, T, H, D, device=dev, dtype=bf)
     vh = torch.empty_like(wk)
     al = torch.empty(B, T, H, device=dev, dtype=torch.float32)
@@ -168,17 +168,25 @@ def main() -> int:
     tbytes = ctypes.c_size_t()
     _abi.check(L.sgsa_score_topk_workspace_size(B, T, H, ctypes.byref(tbytes)))
     tws = torch.empty(tbytes.value, device=dev, dtype=torch.uint8)
+    lbytes, obytes = ctypes.c_size_t(), ctypes.c_size_t()
+    _abi.check(L.sgsa_topk_lists_size(B, T, H, kk, ctypes.byref(lbytes), ctypes.byref(obytes)))
+    tl = torch.empty(lbytes.value, device=dev, dtype=torch.uint8)
+    toff = torch.empty(obytes.value // 4, device=dev, dtype=torch.int32)
     P = _abi.ptr
     stream = _abi.stream_of(qd)
     scale = math.sqrt(D)
 
-    def k1():
+    def k1_rows():
         _abi.check(L.sgsa_score_topk(_abi.SGSA_BF16, B, T, T, H, D, kk, 1, 0, scale, 0, P(qd), P(kd), P(idx),
-                                     P(sc), P(top2), P(cnt), P(spl), 0, P(tws), tbytes.value, stream))
+                                     P(sc), P(top2), P(cnt), None, 0, P(tws), tbytes.value, stream))
+
+    def k1_lists():
+        _abi.check(L.sgsa_score_topk_lists(B, T, H, D, kk, P(qd), P(kd), P(tl), P(toff), P(top2), P(cnt),
+                                           P(tws), tbytes.value, stream))
 
     def k2_tiled():
-        _abi.check(L.sgsa_sparse_gather_tiled(B, T, H, D, kk, P(kd), P(vd), P(idx), P(sc), P(top2), P(cnt),
-                                              P(spl), P(ud), 0, 0.25, 0.1, P(wk), P(vh), None, P(al), stream))
+        _abi.check(L.sgsa_sparse_gather_lists(B, T, H, D, kk, P(kd), P(vd), P(tl), P(toff), P(top2), P(cnt),
+                                              P(ud), 0, 0.25, 0.1, P(wk), P(vh), None, P(al), stream))
 
     def k2_direct():
         _abi.check(L.sgsa_sparse_gather(_abi.SGSA_BF16, B, T, T, H, D, kk, 0, P(kd), P(vd), P(kd), P(idx), P(sc),
@@ -189,8 +197,12 @@ def main() -> int:
         _abi.check(L.sgsa_chunk_fwd(_abi.SGSA_BF16, B, T, H, D, cfg["chunk"], P(qd), P(kd), P(vd), P(bd), P(gd),
                                     P(wk), P(vh), P(al), None, P(out), P(ht), P(ws), nbytes.value, stream))
 
-    k2_main, k2_other = (k2_tiled, k2_direct) if args.gather == "tiled" else (k2_direct, k2_tiled)
-    stages = (("score_topk", k1), ("gather_gate", k2_main), ("chunk", k345))
+    if args.gather == "tiled":
+        stages = (("score_topk", k1_lists), ("gather_gate", k2_tiled), ("chunk", k345))
+        other = (k1_rows, k2_direct)
+    else:
+        stages = (("score_topk", k1_rows), ("gather_gate", k2_direct), ("chunk", k345))
+        other = (k1_lists, k2_tiled)
     cur = torch.cuda.current_stream(dev)
 
     def step(events=None):
@@ -226,14 +238,30 @@ def main() -> int:
     assert torch.isfinite(out.float()).all() and torch.isfinite(ht).all(), "non-finite layer output"
     log(f"ms/step {ms_step:.3f}  stages {json.dumps({n: round(v, 3) for n, v in stage_ms.items()})}")
 
-    # the other K2 form on the same top-k lists, for comparison (outside the timed steps)
+    if args.gather == "tiled":
+        # the timed step is exactly sgsa_layer_fwd: same kernels, same order, bit-identical result
+        lbytes_ws = ctypes.c_size_t()
+        _abi.check(L.sgsa_layer_fwd_workspace_size(_abi.SGSA_BF16, B, T, H, D, kk, ctypes.byref(lbytes_ws)))
+        out_l, ht_l = torch.empty_like(out), torch.empty_like(ht)
+        del ws
+        lws = torch.empty(lbytes_ws.value, device=dev, dtype=torch.uint8)
+        _abi.check(L.sgsa_layer_fwd(_abi.SGSA_BF16, B, T, H, D, kk, cfg["chunk"], P(qd), P(kd), P(vd), P(qd),
+                                    P(bd), P(gd), P(ud), None, 0, 0.25, 0.1, P(out_l), P(ht_l), P(lws),
+                                    lbytes_ws.value, stream))
+        torch.cuda.synchronize()
+        assert torch.equal(out, out_l) and torch.equal(ht, ht_l), "timed step differs from sgsa_layer_fwd"
+        log("timed step reproduces sgsa_layer_fwd bit for bit")
+        del lws, out_l, ht_l
+
+    # the other K1/K2 form, for comparison (outside the timed steps)
     other_ms = None
     if args.steps > 0:
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        k2_other()
+        other[0]()
+        other[1]()
         e0.record(cur)
         for _ in range(3):
-            k2_other()
+            other[1]()
         e1.record(cur)
         torch.cuda.synchronize()
         other_ms = e0.elapsed_time(e1) / 3
@@ -250,10 +278,11 @@ def main() -> int:
     f_score = B * H * T * (T + 1) * D               # causal score GEMM, one pass
     f_chunk = B * H * ((T + 63) // 64) * 23.77e6     # chunk contractions (K3 + K5 + K4)
     gather_kernel = "gather_tile_kernel" if args.gather == "tiled" else "sparse_gather_kernel"
+    topk_kernel = "score_topk_kernel"
     rooflines = {
-        "score_topk": {"kernel": "score_topk_kernel (K1)", "bound": "mfma",
+        "score_topk": {"kernel": f"{topk_kernel} (K1)", "bound": "mfma",
                        "achieved": round(f_score / (stage_ms["score_topk"] / 1000.0) / 1e12, 2),
-                       "peak": 2500.0, "unit": "TFLOP/s", "traffic": measured.get("score_topk_kernel"),
+                       "peak": 2500.0, "unit": "TFLOP/s", "traffic": measured.get(topk_kernel),
                        "algorithmic_flops": f_score},
         "gather_gate": {"kernel": f"{gather_kernel} (K2)", "bound": "hbm",
                         "achieved": round(gbytes / (stage_ms["gather_gate"] / 1000.0) / 1e9, 1),

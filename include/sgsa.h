@@ -142,6 +142,30 @@ int sgsa_sparse_gather_tiled(int B, int T, int H, int D, int top_k, const void* 
                              int write_mode, float alpha_max, float tau_c, void* k_hat, void* v_hat,
                              void* write_key, float* alpha, void* stream);
 
+/* ---- layer-path building blocks: tile lists ----------------------------------
+ * The fused layer (sgsa_layer_fwd, bf16 with D = 128) does not materialise
+ * per-row index/score lists: K1 writes, for every 64-row block, every 16-row
+ * wave of it and every 64-key tile, the selected (score, row, key) entries of
+ * that tile, which is the order the tiled gather consumes them in.  These
+ * entries run the two halves separately (causal, Tq = Tk = T, scores
+ * q.k / sqrt(D) as in the retriever, modelings/modeling_sgsa.py:420-428,
+ * :144-165, :126-134).  Layout: region r = ((b*H + h) * ceil(T/64) + block)
+ * * 4 + wave holds 16 * (min(top_k,T) + 512) 8-byte entries {float score,
+ * uint32 row_in_wave << 8 | key_in_tile} (the score of a candidate that lost
+ * the threshold tie-break is -inf) and ceil(T/64) + 1 int32 tile offsets. */
+int sgsa_topk_lists_size(int B, int T, int H, int top_k, size_t* list_bytes, size_t* offset_bytes);
+/* bf16 q, k [B,T,H,D]; top2 [B,H,T,2], counts [B,H,T]; workspace as sgsa_score_topk. */
+int sgsa_score_topk_lists(int B, int T, int H, int D, int top_k, const void* q, const void* k,
+                          void* lists, int32_t* offsets, float* top2, int32_t* counts,
+                          void* workspace, size_t workspace_bytes, void* stream);
+/* The tiled gather (D = 128) on those lists: k_hat or write key, v_hat, alpha
+ * (same outputs and references as sgsa_sparse_gather_tiled). */
+int sgsa_sparse_gather_lists(int B, int T, int H, int D, int top_k, const void* k, const void* v,
+                             const void* lists, const int32_t* offsets, const float* top2,
+                             const int32_t* counts, const float* budget, int write_mode,
+                             float alpha_max, float tau_c, void* k_hat, void* v_hat,
+                             void* write_key, float* alpha, void* stream);
+
 /* ---- whole SGSA layer forward ------------------------------------------------
  * The attention half of SGSABlock.forward (modelings/modeling_sgsa.py:669-684)
  * with the projections as inputs: token top-k retrieval on (q_ret, k, v)
@@ -155,6 +179,18 @@ int sgsa_layer_fwd(int dtype, int B, int T, int H, int D, int top_k, int chunk_s
                    const float* initial_state, int write_mode, float alpha_max, float tau_c,
                    void* out, float* final_state,
                    void* workspace, size_t workspace_bytes, void* stream);
+
+/* The retrieval half of sgsa_layer_fwd on its own: the token top-k over
+ * (q_ret, k, v), the write key (write_mode 0: k_hat; 1: k_hat minus its
+ * projection on k) and the alpha gate -- the sparse_k / sparse_v / alpha that
+ * SGSABlock.forward hands to chunk_sgsa (modelings/modeling_sgsa.py:669-684,
+ * :546-552).  Same kernels and workspace (sgsa_layer_fwd_workspace_size) as
+ * sgsa_layer_fwd.  write_key / v_hat [B,T,H,D] dtype, alpha [B,T,H] fp32. */
+int sgsa_layer_retrieve(int dtype, int B, int T, int H, int D, int top_k,
+                        const void* q_ret, const void* k, const void* v, const float* budget,
+                        int write_mode, float alpha_max, float tau_c,
+                        void* write_key, void* v_hat, float* alpha,
+                        void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -5,12 +5,14 @@ Public entry points mirror FAndromedA/sgsa:
   SparseRetriever       -- modelings/modeling_sgsa.py:90-474 (token_only mode)
   sparse_retrieve       -- functional form of SparseRetriever.forward
   sgsa_layer_forward    -- retrieval + write gate + chunked state update in one call
+  sgsa_layer_retrieve   -- its retrieval half: (write key, v_hat, alpha)
 The compiled library (libsgsa_hip.so) is required; there is no fallback path.
 """
 
 from .ops import ChunkSGSAFunction, chunk_sgsa, chunk_sgsa_fwd
-from .retrieval import SparseRetriever, gather_gate, score_dump, score_topk, sparse_retrieve
-from .layer import LayerWorkspace, sgsa_layer_forward
+from .retrieval import (SparseRetriever, gather_gate, gather_lists, score_dump, score_topk, score_topk_lists,
+                        sparse_retrieve)
+from .layer import LayerWorkspace, sgsa_layer_forward, sgsa_layer_retrieve
 
 __all__ = [
     "ChunkSGSAFunction",
@@ -20,7 +22,10 @@ __all__ = [
     "score_topk",
     "score_dump",
     "gather_gate",
+    "gather_lists",
+    "score_topk_lists",
     "sparse_retrieve",
     "sgsa_layer_forward",
+    "sgsa_layer_retrieve",
     "LayerWorkspace",
 ]

@@ -51,6 +51,7 @@ int check_dims(int B, int T, int H, int D) {
 
 struct LayerWs {
   size_t idx, sc, cnt, top2, split, wk, vh, al, misc, topk, chunk, total;
+  bool lists;   // bf16, D = 128: K1 writes tile lists (idx/sc regions) for the tiled K2
 };
 
 LayerWs layer_ws(int dtype, int B, int T, int H, int D, int top_k) {
@@ -58,8 +59,14 @@ LayerWs layer_ws(int dtype, int B, int T, int H, int D, int top_k) {
   const size_t rows = (size_t)B * H * T;
   const size_t kk = (size_t)(top_k < T ? top_k : T);
   size_t off = 0;
-  w.idx = off; off = align_up(off + rows * kk * 4);
-  w.sc = off; off = align_up(off + rows * kk * 4);
+  w.lists = dtype == SGSA_BF16 && D == 128;
+  if (w.lists) {
+    w.idx = off; off = align_up(off + sgsa::topk_list_bytes(B, T, H, (int)kk));
+    w.sc = off; off = align_up(off + sgsa::topk_list_off_bytes(B, T, T, H));
+  } else {
+    w.idx = off; off = align_up(off + rows * kk * 4);
+    w.sc = off; off = align_up(off + rows * kk * 4);
+  }
   w.cnt = off; off = align_up(off + rows * 4);
   w.top2 = off; off = align_up(off + rows * 2 * 4);
   w.split = off; off = align_up(off + rows * 4);
@@ -162,6 +169,55 @@ int sgsa_score_topk(int dtype, int B, int Tq, int Tk, int H, int D, int top_k, i
   return SGSA_OK;
 }
 
+int sgsa_topk_lists_size(int B, int T, int H, int top_k, size_t* list_bytes, size_t* offset_bytes) {
+  REQUIRE(list_bytes); REQUIRE(offset_bytes);
+  if (int s = check_dims(B, T, H, 1)) return s;
+  if (top_k <= 0) return fail(SGSA_ERR_INVALID_ARG, "top_k=%d must be positive", top_k);
+  const int kk = top_k < T ? top_k : T;
+  *list_bytes = sgsa::topk_list_bytes(B, T, H, kk);
+  *offset_bytes = sgsa::topk_list_off_bytes(B, T, T, H);
+  return SGSA_OK;
+}
+
+int sgsa_score_topk_lists(int B, int T, int H, int D, int top_k, const void* q, const void* k, void* lists,
+                          int32_t* offsets, float* top2, int32_t* counts, void* workspace, size_t workspace_bytes,
+                          void* stream) {
+  if (int s = check_dims(B, T, H, D)) return s;
+  if (top_k <= 0) return fail(SGSA_ERR_INVALID_ARG, "top_k=%d must be positive", top_k);
+  REQUIRE(q); REQUIRE(k); REQUIRE(lists); REQUIRE(offsets); REQUIRE(top2); REQUIRE(counts); REQUIRE(workspace);
+  const size_t need_ws = sgsa::topk_workspace_bytes(B, T, H);
+  if (workspace_bytes < need_ws) return fail(SGSA_ERR_WORKSPACE, "workspace %zu < %zu bytes", workspace_bytes, need_ws);
+  sgsa::TopkArgs a{};
+  a.dtype = SGSA_BF16; a.B = B; a.Tq = T; a.Tk = T; a.H = H; a.D = D; a.top_k = top_k < T ? top_k : T;
+  a.causal = 1; a.q_offset = 0; a.scale = (float)sqrt((double)D); a.scale_mode = 0;
+  a.q = q; a.k = k; a.top2 = top2; a.counts = counts;
+  a.tl_list = reinterpret_cast<uint2*>(lists); a.tl_off = offsets;
+  a.workspace = workspace;
+  return hip_status(sgsa::launch_score_topk(a, (hipStream_t)stream), "sgsa_score_topk_lists");
+}
+
+int sgsa_sparse_gather_lists(int B, int T, int H, int D, int top_k, const void* k, const void* v, const void* lists,
+                             const int32_t* offsets, const float* top2, const int32_t* counts, const float* budget,
+                             int write_mode, float alpha_max, float tau_c, void* k_hat, void* v_hat,
+                             void* write_key, float* alpha, void* stream) {
+  if (int s = check_dims(B, T, H, D)) return s;
+  if (D != 128) return fail(SGSA_ERR_UNSUPPORTED, "the tiled gather needs D == 128 (got %d)", D);
+  if (top_k <= 0) return fail(SGSA_ERR_INVALID_ARG, "top_k=%d must be positive", top_k);
+  REQUIRE(k); REQUIRE(v); REQUIRE(lists); REQUIRE(offsets); REQUIRE(top2); REQUIRE(counts); REQUIRE(v_hat);
+  if (write_mode != 0 && write_mode != 1) return fail(SGSA_ERR_INVALID_ARG, "write_mode must be 0 (direct) or 1 (residual)");
+  if (budget != nullptr && alpha == nullptr) return fail(SGSA_ERR_INVALID_ARG, "the write gate needs an alpha output");
+  if (write_mode == 1 && budget != nullptr && write_key == nullptr)
+    return fail(SGSA_ERR_INVALID_ARG, "residual write mode needs a write_key output");
+  sgsa::GatherArgs g{};
+  g.dtype = SGSA_BF16; g.B = B; g.Tq = T; g.Tk = T; g.H = H; g.D = D; g.top_k = top_k < T ? top_k : T;
+  g.q_offset = 0; g.k = k; g.v = v; g.self_key = k; g.top2 = top2; g.counts = counts;
+  g.use_valid = 1; g.tau_c = tau_c; g.eps = 1e-6f; g.budget = budget; g.write_mode = write_mode;
+  g.alpha_max = alpha_max; g.k_hat = k_hat; g.v_hat = v_hat; g.write_key = write_key; g.alpha = alpha;
+  return hip_status(sgsa::launch_sparse_gather_lists(g, reinterpret_cast<const uint2*>(lists), offsets,
+                                                     (hipStream_t)stream),
+                    "sgsa_sparse_gather_lists");
+}
+
 int sgsa_score_dump(int dtype, int B, int Tq, int Tk, int H, int D, int causal, int q_offset, float scale,
                     int scale_mode, const void* q, const void* k, int row0, int rows, float* out, void* stream) {
   if (int s = validate_topk(dtype, B, Tq, Tk, H, D, 1, scale_mode, scale)) return s;
@@ -238,53 +294,92 @@ int sgsa_layer_fwd_workspace_size(int dtype, int B, int T, int H, int D, int top
   return SGSA_OK;
 }
 
+}  // extern "C"
+
+namespace {
+
+// K1 + K2 of the layer path into (wk, vh, al); the workspace is laid out by layer_ws.
+int layer_retrieve_impl(const LayerWs& L, char* base, int dtype, int B, int T, int H, int D, int top_k,
+                        const void* q_ret, const void* k, const void* v, const float* budget, int write_mode,
+                        float alpha_max, float tau_c, void* wk, void* vh, float* al, hipStream_t st,
+                        const char* who) {
+  const int kk = top_k < T ? top_k : T;
+  int32_t* cnt = (int32_t*)(base + L.cnt);
+  float* t2 = (float*)(base + L.top2);
+
+  sgsa::TopkArgs ta{};
+  ta.dtype = dtype; ta.B = B; ta.Tq = T; ta.Tk = T; ta.H = H; ta.D = D; ta.top_k = kk; ta.causal = 1;
+  ta.q_offset = 0; ta.scale = (float)sqrt((double)D); ta.scale_mode = 0;
+  ta.q = q_ret; ta.k = k; ta.counts = cnt;
+  if (L.lists) {
+    ta.tl_list = reinterpret_cast<uint2*>(base + L.idx);
+    ta.tl_off = reinterpret_cast<int32_t*>(base + L.sc);
+    ta.top2 = t2;
+  } else {
+    ta.indices = (int32_t*)(base + L.idx); ta.scores = (float*)(base + L.sc);
+  }
+  ta.workspace = base + L.topk;
+  if (int s = hip_status(sgsa::launch_score_topk(ta, st), who)) return s;
+
+  sgsa::GatherArgs ga{};
+  ga.dtype = dtype; ga.B = B; ga.Tq = T; ga.Tk = T; ga.H = H; ga.D = D; ga.top_k = kk; ga.q_offset = 0;
+  ga.k = k; ga.v = v; ga.self_key = k; ga.counts = cnt;
+  ga.use_valid = 1; ga.tau_c = tau_c; ga.eps = 1e-6f; ga.local_window = 64; ga.sink_size = 8;
+  ga.budget = budget; ga.write_mode = write_mode; ga.alpha_max = alpha_max;
+  ga.k_hat = write_mode == 0 ? wk : nullptr; ga.v_hat = vh; ga.write_key = write_mode == 1 ? wk : nullptr;
+  ga.alpha = al;
+  if (L.lists) {
+    ga.top2 = t2;
+    return hip_status(sgsa::launch_sparse_gather_lists(ga, ta.tl_list, ta.tl_off, st), who);
+  }
+  ga.indices = ta.indices; ga.scores = ta.scores; ga.top2 = nullptr;
+  return hip_status(sgsa::launch_sparse_gather(ga, st), who);
+}
+
+int layer_check(int dtype, int B, int T, int H, int D, int top_k, int write_mode) {
+  if (int s = check_dtype(dtype)) return s;
+  if (int s = check_dims(B, T, H, D)) return s;
+  if (top_k <= 0) return fail(SGSA_ERR_INVALID_ARG, "top_k=%d must be positive", top_k);
+  if (write_mode != 0 && write_mode != 1) return fail(SGSA_ERR_INVALID_ARG, "write_mode must be 0 (direct) or 1 (residual)");
+  return SGSA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int sgsa_layer_retrieve(int dtype, int B, int T, int H, int D, int top_k, const void* q_ret, const void* k,
+                        const void* v, const float* budget, int write_mode, float alpha_max, float tau_c,
+                        void* write_key, void* v_hat, float* alpha, void* workspace, size_t workspace_bytes,
+                        void* stream) {
+  if (int s = layer_check(dtype, B, T, H, D, top_k, write_mode)) return s;
+  REQUIRE(q_ret); REQUIRE(k); REQUIRE(v); REQUIRE(budget); REQUIRE(write_key); REQUIRE(v_hat); REQUIRE(alpha);
+  REQUIRE(workspace);
+  const LayerWs L = layer_ws(dtype, B, T, H, D, top_k);
+  if (workspace_bytes < L.total) return fail(SGSA_ERR_WORKSPACE, "workspace %zu < %zu bytes", workspace_bytes, L.total);
+  char* base = (char*)(((uintptr_t)workspace + kAlign - 1) & ~(uintptr_t)(kAlign - 1));
+  return layer_retrieve_impl(L, base, dtype, B, T, H, D, top_k, q_ret, k, v, budget, write_mode, alpha_max, tau_c,
+                             write_key, v_hat, alpha, (hipStream_t)stream, "sgsa_layer_retrieve");
+}
+
 int sgsa_layer_fwd(int dtype, int B, int T, int H, int D, int top_k, int chunk_size, const void* q, const void* k,
                    const void* v, const void* q_ret, const float* beta, const float* gamma, const float* budget,
                    const float* initial_state, int write_mode, float alpha_max, float tau_c, void* out,
                    float* final_state, void* workspace, size_t workspace_bytes, void* stream) {
-  if (int s = check_dtype(dtype)) return s;
-  if (int s = check_dims(B, T, H, D)) return s;
-  if (top_k <= 0) return fail(SGSA_ERR_INVALID_ARG, "top_k=%d must be positive", top_k);
+  if (int s = layer_check(dtype, B, T, H, D, top_k, write_mode)) return s;
   if (chunk_size <= 0) return fail(SGSA_ERR_INVALID_ARG, "chunk_size=%d must be positive", chunk_size);
-  if (write_mode != 0 && write_mode != 1) return fail(SGSA_ERR_INVALID_ARG, "write_mode must be 0 (direct) or 1 (residual)");
   REQUIRE(q); REQUIRE(k); REQUIRE(v); REQUIRE(q_ret); REQUIRE(beta); REQUIRE(gamma); REQUIRE(budget);
   REQUIRE(out); REQUIRE(workspace);
   const LayerWs L = layer_ws(dtype, B, T, H, D, top_k);
   if (workspace_bytes < L.total) return fail(SGSA_ERR_WORKSPACE, "workspace %zu < %zu bytes", workspace_bytes, L.total);
   char* base = (char*)(((uintptr_t)workspace + kAlign - 1) & ~(uintptr_t)(kAlign - 1));
-  const int kk = top_k < T ? top_k : T;
-  int32_t* idx = (int32_t*)(base + L.idx);
-  float* sc = (float*)(base + L.sc);
-  int32_t* cnt = (int32_t*)(base + L.cnt);
-  float* t2 = (float*)(base + L.top2);
-  int32_t* spl = (int32_t*)(base + L.split);
-  const bool tiled = dtype == SGSA_BF16 && D == 128 && kk % 4 == 0;
   void* wk = base + L.wk;
   void* vh = base + L.vh;
   float* al = (float*)(base + L.al);
   hipStream_t st = (hipStream_t)stream;
-
-  sgsa::TopkArgs ta{};
-  ta.dtype = dtype; ta.B = B; ta.Tq = T; ta.Tk = T; ta.H = H; ta.D = D; ta.top_k = kk; ta.causal = 1;
-  ta.q_offset = 0; ta.scale = (float)sqrt((double)D); ta.scale_mode = 0;
-  ta.q = q_ret; ta.k = k; ta.indices = idx; ta.scores = sc; ta.counts = cnt;
-  ta.top2 = tiled ? t2 : nullptr; ta.split = tiled ? spl : nullptr;
-  ta.workspace = base + L.topk;
-  if (int s = hip_status(sgsa::launch_score_topk(ta, st), "sgsa_layer_fwd(topk)")) return s;
-
-  sgsa::GatherArgs ga{};
-  ga.dtype = dtype; ga.B = B; ga.Tq = T; ga.Tk = T; ga.H = H; ga.D = D; ga.top_k = kk; ga.q_offset = 0;
-  ga.k = k; ga.v = v; ga.self_key = k; ga.indices = idx; ga.scores = sc; ga.top2 = nullptr; ga.counts = cnt;
-  ga.use_valid = 1; ga.tau_c = tau_c; ga.eps = 1e-6f; ga.local_window = 64; ga.sink_size = 8;
-  ga.budget = budget; ga.write_mode = write_mode; ga.alpha_max = alpha_max;
-  ga.k_hat = write_mode == 0 ? wk : nullptr; ga.v_hat = vh; ga.write_key = write_mode == 1 ? wk : nullptr;
-  ga.alpha = al;
-  if (tiled) {
-    ga.top2 = t2;
-    if (int s = hip_status(sgsa::launch_sparse_gather_staged(ga, spl, st), "sgsa_layer_fwd(gather)")) return s;
-  } else {
-    if (int s = hip_status(sgsa::launch_sparse_gather(ga, st), "sgsa_layer_fwd(gather)")) return s;
-  }
+  if (int s = layer_retrieve_impl(L, base, dtype, B, T, H, D, top_k, q_ret, k, v, budget, write_mode, alpha_max,
+                                  tau_c, wk, vh, al, st, "sgsa_layer_fwd(retrieve)"))
+    return s;
 
   sgsa::ChunkArgs ca{};
   ca.dtype = dtype; ca.B = B; ca.T = T; ca.H = H; ca.D = D;

@@ -1,25 +1,32 @@
 // K2t: top-k weighted K/V sum by streaming K/V tiles through LDS (bf16, D = 128).
 //
-// Same result as K2 (gather.hip) for the fused layer path -- k_hat, v_hat, the
-// write key and the alpha gate (modelings/modeling_sgsa.py:126-134, :369-381,
-// :497-504, :546-551) -- computed the MI355X way: instead of fetching each of
-// the ~2048 selected K and V rows of every query row from HBM/L2 with 16-byte
-// gathers, a block of 64 query rows walks the causal key range once in tiles
-// of 64 keys.  Each tile of K and V is read from HBM with coalesced 16-byte
-// loads (prefetched one tile ahead into registers) and stored transposed in
-// LDS; the exact top-k weights of the tile form a sparse 64x64 block P built
-// from the rows' slot lists; then k_hat += P K and v_hat += P V run on
+// Same result as K2 (gather.hip) -- k_hat, v_hat, the write key and the alpha
+// gate (modelings/modeling_sgsa.py:126-134, :369-381, :497-504, :546-551) --
+// computed the MI355X way: instead of fetching each of the ~2048 selected K
+// and V rows of every query row from HBM/L2 with 16-byte gathers, a block of
+// query rows walks the causal key range once in tiles of 64 keys.  Each tile
+// of K and V is read with coalesced 16-byte loads (prefetched one tile ahead
+// into registers) and stored transposed in LDS; the exact top-k weights of the
+// tile form a sparse block P; then k_hat += P K and v_hat += P V run on
 // v_mfma_f32_16x16x32_bf16 (P rounded to bf16, weights in (0,1]).
 //
-// Slot lists come from K1: per row, slots [0, split) ascend in key index and
-// slots [split, count) ascend in key index, so each row keeps two cursors that
-// advance monotonically with the tile index.  The four lanes of a row hold a
-// 32-slot window of each run in registers (16-byte loads, issued right after
-// the tile that consumed the previous window, so their latency overlaps the
-// MFMA work and the next K/V tile); a row that exhausts a window inside one
-// tile reloads it and goes round again.  Weights are exp(s - m) with the row
-// maximum m from K1 (top2); the softmax denominator is summed in fp32 from the
-// unrounded weights.  Requires top_k % 4 == 0 (16-byte aligned windows).
+// Two kernels, by where the selection comes from:
+//  * gather_list_kernel (layer path): K1 wrote, per 16-row wave and per key
+//    tile, the selected (score, row, key) entries.  A block owns 128 rows,
+//    each wave 32 (two MFMA row tiles sharing every K/V operand read from
+//    LDS); each tile's entries are read with coalesced loads issued one tile
+//    ahead and scattered into P without branches.  The softmax denominator
+//    is P times a ones vector on the same MFMA, i.e. the sum of the bf16
+//    weights that the numerators use.
+//  * gather_tile_kernel (sgsa_sparse_gather_tiled): per-row slot lists of
+//    K1's row output, 64-row blocks, 16 rows per wave.  Per row, slots
+//    [0, split) and [split, count) each ascend in key index, so each row keeps
+//    two cursors that advance monotonically with the tile index.  The four
+//    lanes of a row hold a 32-slot window of each run in registers (16-byte
+//    loads, reloaded behind the consumed part); a row that exhausts a window
+//    inside one tile reloads it and goes round again.  Weights are exp(s - m)
+//    with the row maximum m from K1 (top2), the denominator summed in fp32
+//    from the unrounded weights.  Requires top_k % 4 == 0.
 #include "common.h"
 #include "kernels.h"
 
@@ -29,7 +36,8 @@ namespace sgsa {
 
 namespace {
 
-constexpr int QB = 64;
+constexpr int QB = 64;     // rows per block, slot-list kernel
+constexpr int QL = 128;    // rows per block, tile-list kernel
 constexpr int KT = 64;
 constexpr int DP = 128;
 constexpr int PT = KT + 8;   // pitch (bf16) of the transposed K/V tiles and of P
@@ -64,88 +72,47 @@ __device__ __forceinline__ void slot_window(SlotRun& r, const int* __restrict__ 
   }
 }
 
-// Scatter the window's slots with key in [t0, t1) into this wave's P rows.
+// Scatter half HH of the window (positions base + 16HH + 4lg + e) with key in
+// [t0, t1) into this wave's P row, without branches: lanes with nothing to
+// write store into a padding column (`junk`, never read by the MFMA).
 // Returns the lane's consumed count; `stop` is set when a held slot lies at or
 // beyond t1 (the row is done with this tile).
-__device__ __forceinline__ int slot_consume(const SlotRun& r, int t0, int t1, int lg, float m, uint16_t* prow,
-                                            float& esum, bool& stop) {
+template <int HH>
+__device__ __forceinline__ int slot_half(const SlotRun& r, int t0, int t1, int lg, float m, uint16_t* prow, int junk,
+                                         float& esum, int& stop) {
+  const int js[4] = {r.ix[HH].x, r.ix[HH].y, r.ix[HH].z, r.ix[HH].w};
+  const float ss[4] = {r.sc[HH].x, r.sc[HH].y, r.sc[HH].z, r.sc[HH].w};
+  const int p0 = r.base + 16 * HH + 4 * lg - r.c;
+  const unsigned span = (unsigned)(r.end - r.c);
   int n = 0;
 #pragma unroll
-  for (int hh = 0; hh < 2; ++hh) {
-    const int js[4] = {r.ix[hh].x, r.ix[hh].y, r.ix[hh].z, r.ix[hh].w};
-    const float ss[4] = {r.sc[hh].x, r.sc[hh].y, r.sc[hh].z, r.sc[hh].w};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int pos = r.base + 16 * hh + 4 * lg + e;
-      if (pos >= r.c && pos < r.end) {
-        const int j = js[e];
-        if (j < t1) {
-          ++n;
-          if (j >= t0) {
-            const float wv = __expf(ss[e] - m);
-            esum += wv;
-            prow[j - t0] = f32_to_bf16(wv);
-          }
-        } else {
-          stop = true;
-        }
-      }
-    }
+  for (int e = 0; e < 4; ++e) {
+    const int inr = (unsigned)(p0 + e) < span;
+    const int j = js[e];
+    const int below = j < t1;
+    const int take = inr & below;
+    stop |= inr & (below ^ 1);
+    n += take;
+    const bool hit = take && j >= t0;
+    const float wv = __expf(ss[e] - m);
+    esum += hit ? wv : 0.f;
+    prow[hit ? j - t0 : junk] = f32_to_bf16(wv);
   }
   return n;
 }
 
-}  // namespace
 
-__global__ __launch_bounds__(256) void gather_tile_kernel(GatherArgs a, const int32_t* __restrict__ split,
-                                                          int nqb) {
-  __shared__ __align__(16) uint16_t Kt[DP * PT];
-  __shared__ __align__(16) uint16_t Vt[DP * PT];
-  __shared__ __align__(16) uint16_t P[4][16 * PT];
-  __shared__ float rowE[4][16];
-
-  const int BH = a.B * a.H;
-  const int bid = blockIdx.x;
-  const int bh = bid % BH;
-  const int qb = nqb - 1 - bid / BH;    // heaviest query blocks first
-  const int b = bh / a.H, h = bh % a.H;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int lr = lane & 15, lg = lane >> 4;
-  const int Tq = a.Tq, Tk = a.Tk, H = a.H, topk = a.top_k;
-  const int r0 = qb * QB;
-  const uint16_t* K = reinterpret_cast<const uint16_t*>(a.k);
-  const uint16_t* V = reinterpret_cast<const uint16_t*>(a.v);
-
-  // ---- slot-list ownership: lane -> (row = r0 + 16w + lr, quarter lg) -------
-  const int prow = r0 + 16 * w + lr;
-  const bool plive = prow < Tq;
-  const long pbase = ((long)bh * Tq + (plive ? prow : 0)) * topk;
-  int end1 = 0, end2 = 0;
-  float m = 0.f;
-  if (plive) {
-    const long rg = (long)bh * Tq + prow;
-    end2 = a.counts[rg];
-    end1 = min(split[rg], end2);
-    m = a.top2[2 * rg];
-  }
-  float esum = 0.f;
-
-  int kend = Tk;
-  {
-    const int last = min(Tq, r0 + QB) - 1 + a.q_offset;
-    kend = min(Tk, last + 1);
-  }
-  const int ntile = (kend + KT - 1) / KT;
-
-  // ---- K/V tile staging (transposed), register prefetch one tile ahead -----
-  // thread t: key pair kp = t % 32 (keys 2kp, 2kp+1), 8-dim chunks c = t/32 and c+8
-  const int kp = tid & 31, cq = tid >> 5;
-  // Loads are unconditional (key index clamped into [0, Tk)) so every thread
-  // issues the same number of memory operations per tile; keys past Tk are
-  // zeroed at commit.
+// Transposed K/V tile staging for 256 threads: thread t loads keys 2kp, 2kp+1
+// (kp = t % 32), 8-dim chunks cq = t / 32 and cq + 8, of one 64-key tile.  The
+// loads are unconditional (key index clamped into [0, Tk)) so every thread
+// issues the same number of memory operations per tile; keys past Tk are
+// zeroed at commit.
+struct KVStage {
   uint4 pk[2][2], pv[2][2];   // [chunk half][key of the pair]
   uint32_t pmask[2];          // all-ones for keys < Tk
-  auto issue = [&](int kt) __attribute__((always_inline)) {
+
+  __device__ __forceinline__ void issue(const uint16_t* __restrict__ K, const uint16_t* __restrict__ V, int b, int h,
+                                        int H, int Tk, int kt, int kp, int cq) {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int j = kt * KT + 2 * kp + u;
@@ -158,8 +125,9 @@ __global__ __launch_bounds__(256) void gather_tile_kernel(GatherArgs a, const in
         pv[hh][u] = *reinterpret_cast<const uint4*>(V + off);
       }
     }
-  };
-  auto commit = [&]() __attribute__((always_inline)) {
+  }
+
+  __device__ __forceinline__ void commit(uint16_t* Kt, uint16_t* Vt, int kp, int cq) {
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
 #pragma unroll
@@ -179,100 +147,37 @@ __global__ __launch_bounds__(256) void gather_tile_kernel(GatherArgs a, const in
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         // dims 8c+2i (low halves) and 8c+2i+1 (high halves) of keys 2kp, 2kp+1
-        const uint32_t klo = (k0[i] & 0xffffu) | (k1[i] << 16);
-        const uint32_t khi = (k0[i] >> 16) | (k1[i] & 0xffff0000u);
-        const uint32_t vlo = (v0[i] & 0xffffu) | (v1[i] << 16);
-        const uint32_t vhi = (v0[i] >> 16) | (v1[i] & 0xffff0000u);
-        *reinterpret_cast<uint32_t*>(&Kt[(8 * c + 2 * i) * PT + 2 * kp]) = klo;
-        *reinterpret_cast<uint32_t*>(&Kt[(8 * c + 2 * i + 1) * PT + 2 * kp]) = khi;
-        *reinterpret_cast<uint32_t*>(&Vt[(8 * c + 2 * i) * PT + 2 * kp]) = vlo;
-        *reinterpret_cast<uint32_t*>(&Vt[(8 * c + 2 * i + 1) * PT + 2 * kp]) = vhi;
-      }
-    }
-  };
-
-  f4 ok_[DP / 16], ov_[DP / 16];
-#pragma unroll
-  for (int n = 0; n < DP / 16; ++n) { ok_[n] = f4_zero(); ov_[n] = f4_zero(); }
-  uint16_t* Pw = P[w];
-  uint16_t* prw = Pw + lr * PT;
-  const int* idxp = a.indices + pbase;
-  const float* scp = a.scores + pbase;
-  SlotRun run1, run2;
-  run1.c = 0; run1.end = end1;
-  run2.c = end1; run2.end = end2;
-  issue(0);   // same order as in the loop: K/V tile, then the slot windows
-  slot_window(run1, idxp, scp, lg, topk);
-  slot_window(run2, idxp, scp, lg, topk);
-
-  for (int kt = 0; kt < ntile; ++kt) {
-    const int t0 = kt * KT, t1 = t0 + KT;
-    __syncthreads();           // previous tile's K/V and P reads are done
-    commit();
-    // clear this wave's P rows (16 x PT bf16 = 144 uint4)
-    for (int e = lane; e < 16 * PT / 8; e += 64) reinterpret_cast<uint4*>(Pw)[e] = make_uint4(0, 0, 0, 0);
-    issue(min(kt + 1, ntile - 1));   // unconditional: keeps the wait counts static
-    wave_lds_sync();
-    // scatter this tile's weights from both runs and reload each window behind
-    // it; the first pass uses windows loaded during the previous tile
-    auto scatter_pass = [&]() __attribute__((always_inline)) -> bool {
-      bool stop1 = false, stop2 = false;
-      int n1 = slot_consume(run1, t0, t1, lg, m, prw, esum, stop1);
-      int n2 = slot_consume(run2, t0, t1, lg, m, prw, esum, stop2);
-      n1 += __shfl_xor(n1, 16, 64);
-      n1 += __shfl_xor(n1, 32, 64);
-      n2 += __shfl_xor(n2, 16, 64);
-      n2 += __shfl_xor(n2, 32, 64);
-      const uint64_t s1 = __ballot(stop1), s2 = __ballot(stop2);
-      stop1 = ((s1 >> lr) | (s1 >> (lr + 16)) | (s1 >> (lr + 32)) | (s1 >> (lr + 48))) & 1;
-      stop2 = ((s2 >> lr) | (s2 >> (lr + 16)) | (s2 >> (lr + 32)) | (s2 >> (lr + 48))) & 1;
-      run1.c += n1;
-      run2.c += n2;
-      slot_window(run1, idxp, scp, lg, topk);
-      slot_window(run2, idxp, scp, lg, topk);
-      // a row that consumed its whole window without meeting t1 may have more keys in this tile
-      return (!stop1 && run1.c < run1.end) || (!stop2 && run2.c < run2.end);
-    };
-    if (__ballot(scatter_pass())) {
-      while (__ballot(scatter_pass())) {
-      }
-    }
-    __syncthreads();           // K/V tile committed by all threads; P rows written
-    // k_hat += P K, v_hat += P V  (P: 16 rows x 64 keys, K/V: 64 keys x 128 dims)
-#pragma unroll
-    for (int s = 0; s < KT / 32; ++s) {
-      const uint4 pa = *reinterpret_cast<const uint4*>(&Pw[lr * PT + 32 * s + 8 * lg]);
-#pragma unroll
-      for (int n = 0; n < DP / 16; ++n) {
-        const uint4 kb = *reinterpret_cast<const uint4*>(&Kt[(16 * n + lr) * PT + 32 * s + 8 * lg]);
-        const uint4 vb = *reinterpret_cast<const uint4*>(&Vt[(16 * n + lr) * PT + 32 * s + 8 * lg]);
-        ok_[n] = mma_bf16(as_bf8(pa), as_bf8(kb), ok_[n]);
-        ov_[n] = mma_bf16(as_bf8(pa), as_bf8(vb), ov_[n]);
+        *reinterpret_cast<uint32_t*>(&Kt[(8 * c + 2 * i) * PT + 2 * kp]) = __builtin_amdgcn_perm(k1[i], k0[i], 0x05040100u);
+        *reinterpret_cast<uint32_t*>(&Kt[(8 * c + 2 * i + 1) * PT + 2 * kp]) = __builtin_amdgcn_perm(k1[i], k0[i], 0x07060302u);
+        *reinterpret_cast<uint32_t*>(&Vt[(8 * c + 2 * i) * PT + 2 * kp]) = __builtin_amdgcn_perm(v1[i], v0[i], 0x05040100u);
+        *reinterpret_cast<uint32_t*>(&Vt[(8 * c + 2 * i + 1) * PT + 2 * kp]) = __builtin_amdgcn_perm(v1[i], v0[i], 0x07060302u);
       }
     }
   }
+};
 
-  // ---- epilogue: normalise, gate, write key, stores ------------------------
-  esum += __shfl_xor(esum, 16, 64);
-  esum += __shfl_xor(esum, 32, 64);
-  if (lg == 0) rowE[w][lr] = esum;
-  wave_lds_sync();
+// Normalise one 16-row MFMA tile of k_hat / v_hat sums (row 4lg + e of the
+// tile in register e, column 16n + lr) by the row denominators E[e], then the
+// gate: concentration from the top-2 margin, novelty of k_hat against the
+// token's own key, the (residual) write key and alpha
+// (modelings/modeling_sgsa.py:126-134, :369-381, :497-504, :546-551).
+__device__ __forceinline__ void tile_epilogue(const GatherArgs& a, const f4 (&ok)[DP / 16], const f4 (&ov)[DP / 16],
+                                              const float (&E)[4], int row0, int bh, int b, int h, int lr, int lg) {
+  const int Tq = a.Tq, H = a.H;
   const float eps = a.eps;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    const int rl = 4 * lg + e;
-    const int row = r0 + 16 * w + rl;
+    const int row = row0 + 4 * lg + e;
     const bool live = row < Tq;
     const long rg = (long)bh * Tq + (live ? row : 0);
-    const float E = rowE[w][rl];
-    const float inv = E > 0.f ? 1.f / E : 0.f;
+    const float inv = E[e] > 0.f ? 1.f / E[e] : 0.f;
     const long qoff = ((long)(b * Tq + (live ? row : 0)) * H + h) * DP;
     float kh[DP / 16], vh[DP / 16], ks[DP / 16];
     float pdot = 0.f, pkk = 0.f, phh = 0.f, pvv = 0.f;
 #pragma unroll
     for (int n = 0; n < DP / 16; ++n) {
-      kh[n] = ok_[n][e] * inv;
-      vh[n] = ov_[n][e] * inv;
+      kh[n] = ok[n][e] * inv;
+      vh[n] = ov[n][e] * inv;
       ks[n] = live ? bf16_to_f32(reinterpret_cast<const uint16_t*>(a.self_key)[qoff + 16 * n + lr]) : 0.f;
       pdot += kh[n] * ks[n];
       pkk += ks[n] * ks[n];
@@ -283,7 +188,7 @@ __global__ __launch_bounds__(256) void gather_tile_kernel(GatherArgs a, const in
                 vv2 = group_sum(pvv, 16);
     const int kq = live ? a.counts[rg] : 0;
     float margin = 0.f;
-    if (topk >= 2 && live) margin = a.top2[2 * rg] - a.top2[2 * rg + 1];
+    if (a.top_k >= 2 && live) margin = a.top2[2 * rg] - a.top2[2 * rg + 1];
     if (kq == 0) margin = 0.f;
     const float conc = 1.f / (1.f + expf(-(margin / fmaxf(a.tau_c, eps))));
     const float self_norm = fmaxf(sqrtf(kk2), eps);
@@ -329,9 +234,289 @@ __global__ __launch_bounds__(256) void gather_tile_kernel(GatherArgs a, const in
   }
 }
 
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Slot-list form (sgsa_sparse_gather_tiled)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void gather_tile_kernel(GatherArgs a, const int32_t* __restrict__ split, int nqb) {
+  __shared__ __align__(16) uint16_t Kt[DP * PT];
+  __shared__ __align__(16) uint16_t Vt[DP * PT];
+  __shared__ __align__(16) uint16_t P[4][16 * PT];
+  __shared__ float rowE[4][16];
+
+  const int BH = a.B * a.H;
+  const int bid = blockIdx.x;
+  const int bh = bid % BH;
+  const int qb = nqb - 1 - bid / BH;    // heaviest query blocks first
+  const int b = bh / a.H, h = bh % a.H;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int Tq = a.Tq, Tk = a.Tk, H = a.H, topk = a.top_k;
+  const int r0 = qb * QB;
+  const uint16_t* K = reinterpret_cast<const uint16_t*>(a.k);
+  const uint16_t* V = reinterpret_cast<const uint16_t*>(a.v);
+
+  // ---- slot-list ownership: lane -> (row = r0 + 16w + lr, quarter lg) -------
+  const int prow = r0 + 16 * w + lr;
+  const bool plive = prow < Tq;
+  const long pbase = ((long)bh * Tq + (plive ? prow : 0)) * topk;
+  int end1 = 0, end2 = 0;
+  float m = 0.f;
+  if (plive) {
+    const long rg = (long)bh * Tq + prow;
+    end2 = a.counts[rg];
+    end1 = min(split[rg], end2);
+    m = a.top2[2 * rg];
+  }
+  float esum = 0.f;
+
+  const int kend = min(Tk, min(Tq, r0 + QB) + a.q_offset);
+  const int ntile = (kend + KT - 1) / KT;
+  const int kp = tid & 31, cq = tid >> 5;
+  KVStage kv;
+
+  f4 ok_[DP / 16], ov_[DP / 16];
+#pragma unroll
+  for (int n = 0; n < DP / 16; ++n) { ok_[n] = f4_zero(); ov_[n] = f4_zero(); }
+  uint16_t* Pw = P[w];
+  uint16_t* prw = Pw + lr * PT;
+  const int junk = KT + lg;   // padding column of the P row
+  const int* idxp = a.indices + pbase;
+  const float* scp = a.scores + pbase;
+  SlotRun run1, run2;
+  run1.c = 0; run1.end = end1;
+  run2.c = end1; run2.end = end2;
+  kv.issue(K, V, b, h, H, Tk, 0, kp, cq);
+  slot_window(run1, idxp, scp, lg, topk);
+  slot_window(run2, idxp, scp, lg, topk);
+  // Nothing outstanding on entry: the loop head then only waits for the K/V
+  // tile, not for the slot windows reloaded after it.
+  __builtin_amdgcn_s_waitcnt(0);
+
+  for (int kt = 0; kt < ntile; ++kt) {
+    const int t0 = kt * KT, t1 = t0 + KT;
+    __syncthreads();           // previous tile's K/V and P reads are done
+    kv.commit(Kt, Vt, kp, cq);
+    // clear this wave's P rows (16 x PT bf16 = 144 uint4)
+    for (int e = lane; e < 16 * PT / 8; e += 64) reinterpret_cast<uint4*>(Pw)[e] = make_uint4(0, 0, 0, 0);
+    kv.issue(K, V, b, h, H, Tk, min(kt + 1, ntile - 1), kp, cq);   // unconditional: static wait counts
+    wave_lds_sync();
+    // scatter this tile's weights from both runs and reload each window behind
+    // it; the first pass uses windows loaded during the previous tile
+    auto scatter_pass = [&]() __attribute__((always_inline)) -> bool {
+      int stop1 = 0, stop2 = 0;
+      int n1 = slot_half<0>(run1, t0, t1, lg, m, prw, junk, esum, stop1);
+      int n2 = slot_half<0>(run2, t0, t1, lg, m, prw, junk, esum, stop2);
+      // the second half matters only to rows that neither stopped nor ran out in the first
+      const uint64_t h1 = __ballot(stop1), h2 = __ballot(stop2);
+      const bool s1 = ((h1 >> lr) | (h1 >> (lr + 16)) | (h1 >> (lr + 32)) | (h1 >> (lr + 48))) & 1;
+      const bool s2 = ((h2 >> lr) | (h2 >> (lr + 16)) | (h2 >> (lr + 32)) | (h2 >> (lr + 48))) & 1;
+      if (__ballot((!s1 && run1.end > run1.base + 16) || (!s2 && run2.end > run2.base + 16))) {
+        n1 += slot_half<1>(run1, t0, t1, lg, m, prw, junk, esum, stop1);
+        n2 += slot_half<1>(run2, t0, t1, lg, m, prw, junk, esum, stop2);
+      }
+      n1 += __shfl_xor(n1, 16, 64);
+      n1 += __shfl_xor(n1, 32, 64);
+      n2 += __shfl_xor(n2, 16, 64);
+      n2 += __shfl_xor(n2, 32, 64);
+      const uint64_t g1 = __ballot(stop1), g2 = __ballot(stop2);
+      const bool f1 = ((g1 >> lr) | (g1 >> (lr + 16)) | (g1 >> (lr + 32)) | (g1 >> (lr + 48))) & 1;
+      const bool f2 = ((g2 >> lr) | (g2 >> (lr + 16)) | (g2 >> (lr + 32)) | (g2 >> (lr + 48))) & 1;
+      run1.c += n1;
+      run2.c += n2;
+      slot_window(run1, idxp, scp, lg, topk);
+      slot_window(run2, idxp, scp, lg, topk);
+      // a row that consumed its whole window without meeting t1 may have more keys in this tile
+      return (!f1 && run1.c < run1.end) || (!f2 && run2.c < run2.end);
+    };
+    if (__ballot(scatter_pass())) {
+      while (__ballot(scatter_pass())) {
+      }
+    }
+    __syncthreads();           // K/V tile committed by all threads; P rows written
+    // k_hat += P K, v_hat += P V  (P: 16 rows x 64 keys, K/V: 64 keys x 128 dims)
+#pragma unroll
+    for (int s = 0; s < KT / 32; ++s) {
+      const uint4 pa = *reinterpret_cast<const uint4*>(&Pw[lr * PT + 32 * s + 8 * lg]);
+#pragma unroll
+      for (int n = 0; n < DP / 16; ++n) {
+        const uint4 kb = *reinterpret_cast<const uint4*>(&Kt[(16 * n + lr) * PT + 32 * s + 8 * lg]);
+        const uint4 vb = *reinterpret_cast<const uint4*>(&Vt[(16 * n + lr) * PT + 32 * s + 8 * lg]);
+        ok_[n] = mma_bf16(as_bf8(pa), as_bf8(kb), ok_[n]);
+        ov_[n] = mma_bf16(as_bf8(pa), as_bf8(vb), ov_[n]);
+      }
+    }
+  }
+
+  esum += __shfl_xor(esum, 16, 64);
+  esum += __shfl_xor(esum, 32, 64);
+  if (lg == 0) rowE[w][lr] = esum;
+  wave_lds_sync();
+  float E[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) E[e] = rowE[w][4 * lg + e];
+  tile_epilogue(a, ok_, ov_, E, r0 + 16 * w, bh, b, h, lr, lg);
+}
+
+// ---------------------------------------------------------------------------
+// Tile-list form (layer path)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256, 2) void gather_list_kernel(GatherArgs a, const uint2* __restrict__ tl,
+                                                          const int32_t* __restrict__ toff, int nqb2, int nqb,
+                                                          int ntmax) {
+  __shared__ __align__(16) uint16_t Kt[DP * PT];
+  __shared__ __align__(16) uint16_t Vt[DP * PT];
+  __shared__ __align__(16) uint16_t P[4][32 * PT];
+  __shared__ float mrow[4][32];
+
+  const int BH = a.B * a.H;
+  const int bid = blockIdx.x;
+  const int bh = bid % BH;
+  const int qb2 = nqb2 - 1 - bid / BH;   // heaviest row blocks first
+  const int b = bh / a.H, h = bh % a.H;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int Tq = a.Tq, Tk = a.Tk, H = a.H, topk = a.top_k;
+  const int r0 = qb2 * QL;
+  const int wr0 = r0 + 32 * w;   // first row of this wave
+  const uint16_t* K = reinterpret_cast<const uint16_t*>(a.k);
+  const uint16_t* V = reinterpret_cast<const uint16_t*>(a.v);
+
+  const int kend = min(Tk, min(Tq, r0 + QL) + a.q_offset);
+  const int ntile = (kend + KT - 1) / KT;
+  const int kp = tid & 31, cq = tid >> 5;
+  KVStage kv;
+
+  // The wave's rows are the two 16-row waves 2(w&1), 2(w&1)+1 of K1's 64-row
+  // block qb64; their lists end at that block's own last tile nt64.
+  const int qb64 = 2 * qb2 + (w >> 1);
+  const bool rvalid = qb64 < nqb;
+  const int nt64 = rvalid ? (min(Tk, min(Tq, 64 * qb64 + 64) + a.q_offset) + KT - 1) / KT : 0;
+  const int tlcap = 16 * (topk + TOPK_CAP);
+  const long reg0 = ((long)bh * nqb + (rvalid ? qb64 : 0)) * 4 + 2 * (w & 1);
+  const uint2* tlr[2] = {tl + reg0 * tlcap, tl + (reg0 + 1) * tlcap};
+  const int32_t* tor[2] = {toff + reg0 * (ntmax + 1), toff + (reg0 + 1) * (ntmax + 1)};
+
+  if (lane < 32) {
+    const int row = wr0 + lane;
+    mrow[w][lane] = row < Tq ? a.top2[2 * ((long)bh * Tq + row)] : 0.f;
+  }
+
+  // tile offsets, 64 at a time in one register per list, picked with readlane
+  int ofb[2] = {-(1 << 20), -(1 << 20)}, ofr[2] = {0, 0};
+  auto off_at = [&](int mt, int i) __attribute__((always_inline)) -> int {
+    if (!rvalid) return 0;
+    i = min(i, nt64);
+    if (i < ofb[mt] || i >= ofb[mt] + 64) {   // wave-uniform
+      ofb[mt] = i;
+      ofr[mt] = tor[mt][min(i + lane, nt64)];
+    }
+    return __builtin_amdgcn_readlane(ofr[mt], i - ofb[mt]);
+  };
+  constexpr int NPE = 2;               // entries prefetched per lane and list: the first 128 of a tile
+  uint2 pe[2][NPE], pn[2][NPE];        // [list][i]: this tile / the next tile
+  int c0[2] = {0, 0}, c1[2] = {0, 0};  // entry ranges of this tile
+  auto entries = [&](uint2 (&d)[NPE], int mt, int e0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < NPE; ++i) d[i] = tlr[mt][min(max(e0 + 64 * i + lane, 0), tlcap - 1)];
+  };
+  uint16_t* Pw = P[w];
+  // scatter one entry of list mt without branches on the LDS address: invalid
+  // lanes store into a padding column that the MFMA never reads
+  auto scat = [&](uint2 en, int mt, bool valid) __attribute__((always_inline)) {
+    const int rr = 16 * mt + ((en.y >> 8) & 15), kk = en.y & 63;
+    const float wv = __expf(__uint_as_float(en.x) - mrow[w][rr]);
+    Pw[valid ? rr * PT + kk : (16 * mt + lr) * PT + KT + lg] = f32_to_bf16(wv);
+  };
+
+  f4 ok_[2][DP / 16], ov_[2][DP / 16], es[2];
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt) {
+    es[mt] = f4_zero();
+#pragma unroll
+    for (int n = 0; n < DP / 16; ++n) { ok_[mt][n] = f4_zero(); ov_[mt][n] = f4_zero(); }
+  }
+  const uint4 ones4 = make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u);   // bf16 1.0 x 8
+
+  wave_lds_sync();   // mrow
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt) {
+    c0[mt] = off_at(mt, 0);
+    c1[mt] = off_at(mt, 1);
+    entries(pe[mt], mt, c0[mt]);
+  }
+  kv.issue(K, V, b, h, H, Tk, 0, kp, cq);
+  __builtin_amdgcn_s_waitcnt(0);   // nothing outstanding on entry: static wait counts in the loop
+
+  for (int kt = 0; kt < ntile; ++kt) {
+    __syncthreads();           // previous tile's K/V and P reads are done
+    kv.commit(Kt, Vt, kp, cq);
+    // clear this wave's P rows (32 x PT bf16 = 288 uint4)
+    for (int e = lane; e < 32 * PT / 8; e += 64) reinterpret_cast<uint4*>(Pw)[e] = make_uint4(0, 0, 0, 0);
+    kv.issue(K, V, b, h, H, Tk, min(kt + 1, ntile - 1), kp, cq);   // unconditional: static wait counts
+    int n0[2], n1[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      n0[mt] = off_at(mt, kt + 1);
+      n1[mt] = off_at(mt, kt + 2);
+      entries(pn[mt], mt, n0[mt]);
+    }
+    wave_lds_sync();
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+      for (int i = 0; i < NPE; ++i) {
+        if (c0[mt] + 64 * i < c1[mt]) scat(pe[mt][i], mt, c0[mt] + 64 * i + lane < c1[mt]);   // wave-uniform skip
+      }
+      for (int e0 = c0[mt] + 64 * NPE; e0 < c1[mt]; e0 += 64) {   // dense tiles: the rest, loaded here
+        const uint2 en = tlr[mt][min(max(e0 + lane, 0), tlcap - 1)];
+        scat(en, mt, e0 + lane < c1[mt]);
+      }
+#pragma unroll
+      for (int i = 0; i < NPE; ++i) pe[mt][i] = pn[mt][i];
+      c0[mt] = n0[mt];
+      c1[mt] = n1[mt];
+    }
+    __syncthreads();           // K/V tile committed by all threads; P rows written
+    // k_hat += P K, v_hat += P V, E += P 1  (two 16-row tiles share each K/V operand)
+#pragma unroll
+    for (int s = 0; s < KT / 32; ++s) {
+      const uint4 pa0 = *reinterpret_cast<const uint4*>(&Pw[lr * PT + 32 * s + 8 * lg]);
+      const uint4 pa1 = *reinterpret_cast<const uint4*>(&Pw[(16 + lr) * PT + 32 * s + 8 * lg]);
+#pragma unroll
+      for (int n = 0; n < DP / 16; ++n) {
+        const uint4 kb = *reinterpret_cast<const uint4*>(&Kt[(16 * n + lr) * PT + 32 * s + 8 * lg]);
+        const uint4 vb = *reinterpret_cast<const uint4*>(&Vt[(16 * n + lr) * PT + 32 * s + 8 * lg]);
+        ok_[0][n] = mma_bf16(as_bf8(pa0), as_bf8(kb), ok_[0][n]);
+        ok_[1][n] = mma_bf16(as_bf8(pa1), as_bf8(kb), ok_[1][n]);
+        ov_[0][n] = mma_bf16(as_bf8(pa0), as_bf8(vb), ov_[0][n]);
+        ov_[1][n] = mma_bf16(as_bf8(pa1), as_bf8(vb), ov_[1][n]);
+      }
+      es[0] = mma_bf16(as_bf8(pa0), as_bf8(ones4), es[0]);
+      es[1] = mma_bf16(as_bf8(pa1), as_bf8(ones4), es[1]);
+    }
+  }
+
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt) {
+    const float E[4] = {es[mt][0], es[mt][1], es[mt][2], es[mt][3]};
+    tile_epilogue(a, ok_[mt], ov_[mt], E, wr0 + 16 * mt, bh, b, h, lr, lg);
+  }
+}
+
 hipError_t launch_sparse_gather_staged(const GatherArgs& a, const int32_t* split, hipStream_t st) {
   const int nqb = (a.Tq + QB - 1) / QB;
   gather_tile_kernel<<<dim3((unsigned)(a.B * a.H * nqb)), 256, 0, st>>>(a, split, nqb);
+  return hipGetLastError();
+}
+
+hipError_t launch_sparse_gather_lists(const GatherArgs& a, const uint2* tl_list, const int32_t* tl_off,
+                                      hipStream_t st) {
+  const int nqb = (a.Tq + QB - 1) / QB;
+  const int nqb2 = (a.Tq + QL - 1) / QL;
+  const int ntmax = (a.Tk + KT - 1) / KT;
+  gather_list_kernel<<<dim3((unsigned)(a.B * a.H * nqb2)), 256, 0, st>>>(a, tl_list, tl_off, nqb2, nqb, ntmax);
   return hipGetLastError();
 }
 

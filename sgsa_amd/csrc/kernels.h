@@ -51,6 +51,9 @@ struct TopkArgs {
   int32_t* split;     // [B,H,Tq] length of the leading ascending-index run, or nullptr
   float* dump;        // score-dump mode: [B,H,dump_rows,Tk]; nullptr = select mode
   int dump_row0, dump_rows;
+  uint2* tl_list;     // layer path (bf16): per-wave tile lists, topk_list_bytes(); nullptr otherwise
+  int32_t* tl_off;    // per-wave tile start offsets, topk_list_off_bytes()
+  int tl_ntmax;       // set by the launcher: key tiles per row block
   void* workspace;    // topk_workspace_bytes(): candidate lists + per-head key norms
   uint2* scratch;     // set by the launcher
   int* flags;         // set by the launcher
@@ -59,6 +62,11 @@ struct TopkArgs {
 
 constexpr int TOPK_CAP = 512;   // collected threshold-bin candidates per row
 size_t topk_workspace_bytes(int B, int Tq, int H);
+// Tile-list layout shared by the layer-path K1 and K2: one region per
+// (batch*head, 64-row block, wave) of 16 * (top_k + TOPK_CAP) entries and of
+// ceil(Tk / 64) + 1 tile offsets.
+size_t topk_list_bytes(int B, int Tq, int H, int top_k);
+size_t topk_list_off_bytes(int B, int Tq, int Tk, int H);
 
 hipError_t launch_score_topk(const TopkArgs& a, hipStream_t st);
 hipError_t launch_sort_rows(int32_t* indices, float* scores, long rows, int top_k, const int32_t* counts,
@@ -97,5 +105,8 @@ hipError_t launch_sparse_gather(const GatherArgs& a, hipStream_t st);
 // LDS-staged variant for the fused layer path: bf16, D = 128, rows whose
 // slots [0, split) ascend in key index; no weights/diag outputs.
 hipError_t launch_sparse_gather_staged(const GatherArgs& a, const int32_t* split, hipStream_t st);
+// Layer path: the same kernel fed by the tile lists of the list-mode K1.
+hipError_t launch_sparse_gather_lists(const GatherArgs& a, const uint2* tl_list, const int32_t* tl_off,
+                                      hipStream_t st);
 
 }  // namespace sgsa

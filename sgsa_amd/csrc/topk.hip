@@ -182,7 +182,7 @@ __global__ __launch_bounds__(256) void key_norm_max_kernel(const X* __restrict__
 // more than TOPK_CAP candidates sets flags[block] and returns without output.
 // FB = true: re-runs exactly the flagged blocks with 8-bit radix digit passes
 // over the order-preserving keys (up to 4 passes + emit).
-template <typename X, bool DUMP, bool C16, bool TOP2, bool FB>
+template <typename X, bool DUMP, bool C16, bool TOP2, bool FB, bool LIST>
 __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb, float mscale) {
   constexpr int P = KTile<X>::PITCH;
   constexpr bool BF = sizeof(X) == 2;
@@ -509,13 +509,42 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb, fl
   const int grow0 = bh * Tq + r0 + 16 * w + 4 * lg;   // global row of e = 0
   const uint32_t lower = (1u << lr) - 1u;
   uint2* scratch = a.scratch;
-  auto emit = [&](int e, int j, float s, bool sel, bool col) __attribute__((always_inline)) {
+  // LIST: the wave's tile list (layer path) -- entries (score, row << 8 | key in
+  // tile) grouped by key tile in ascending tile order, toff[kt] = first entry of
+  // tile kt, toff[ntile] = end.  Threshold-bin candidates get an entry as well;
+  // the resolve overwrites the score of those not selected with -inf.
+  const int tlcap = 16 * (topk + TOPK_CAP);
+  const long lreg = ((long)bh * nqb + qb) * 4 + w;
+  uint2* tl = LIST ? a.tl_list + lreg * tlcap : nullptr;
+  int32_t* toff = LIST ? a.tl_off + lreg * (a.tl_ntmax + 1) : nullptr;
+  int woff = 0;
+  auto emit = [&](int e, int kk, int j, float s, bool sel, bool col) __attribute__((always_inline)) {
+    if constexpr (LIST) {
+      const bool cand = sel || col;
+      const uint64_t cb = __ballot(cand);
+      const uint32_t cbr = (uint32_t)(cb >> (16 * lg)) & 0xffffu;
+      const uint32_t cm = (uint32_t)(__ballot(col) >> (16 * lg)) & 0xffffu;
+      if (cand) {
+        const int pos = woff + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(cb >> 32),
+                                                              __builtin_amdgcn_mbcnt_lo((uint32_t)cb, 0u));
+        if (pos < tlcap) tl[pos] = make_uint2(__float_as_uint(s), (uint32_t)(((4 * lg + e) << 8) | kk));
+        if (col) {
+          const int slot = colc[e] + __popc(cm & lower);
+          if (slot < TOPK_CAP)
+            scratch[(long)(grow0 + e) * TOPK_CAP + slot] = make_uint2(__float_as_uint(s), (uint32_t)pos);
+        }
+      }
+      woff += __popcll(cb);
+      outc[e] += __popc(cbr & ~cm);
+      colc[e] += __popc(cm);
+      return;
+    }
     const uint32_t sm = (uint32_t)(__ballot(sel) >> (16 * lg)) & 0xffffu;
     const uint32_t cm = (uint32_t)(__ballot(col) >> (16 * lg)) & 0xffffu;
     const long row = (long)(grow0 + e);
     if (sel) {
       const int slot = outc[e] + __popc(sm & lower);
-      if (slot < topk) {
+      if (!LIST && slot < topk) {
         a.indices[row * topk + slot] = j;
         a.scores[row * topk + slot] = s;
       }
@@ -536,6 +565,9 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb, fl
   };
   if constexpr (!FB) {
     sweep([&](int kt, f4* acc) __attribute__((always_inline)) {
+      if constexpr (LIST) {
+        if (lane == 0) toff[kt] = woff;
+      }
       const bool full = (kt + 1) * KT <= minvalid;
 #pragma unroll
       for (int nt = 0; nt < 4; ++nt) {
@@ -546,7 +578,7 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb, fl
           const float s = acc[nt][e];
           const bool sel = ok && s >= th1[e];
           const bool col = ok && s >= th0[e] && s < th1[e];
-          emit(e, j, s, sel, col);
+          emit(e, 16 * nt + lr, j, s, sel, col);
           top2_update(e, ok, s);
         }
       }
@@ -554,6 +586,9 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb, fl
   } else {
     int eqc[4] = {0, 0, 0, 0};
     sweep([&](int kt, f4* acc) __attribute__((always_inline)) {
+      if constexpr (LIST) {
+        if (lane == 0) toff[kt] = woff;
+      }
       const bool full = (kt + 1) * KT <= minvalid;
 #pragma unroll
       for (int nt = 0; nt < 4; ++nt) {
@@ -570,11 +605,14 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb, fl
           const uint32_t eqm = (uint32_t)(__ballot(eq) >> (16 * lg)) & 0xffffu;
           sel = sel || (inb && (km > pfx[e] || (eq && eqc[e] + __popc(eqm & lower) < need[e])));
           eqc[e] += __popc(eqm);
-          emit(e, j, s, sel, col);
+          emit(e, 16 * nt + lr, j, s, sel, col);
           top2_update(e, ok, s);
         }
       }
     });
+  }
+  if constexpr (LIST) {
+    if (lane == 0) toff[ntile] = woff;
   }
   if (lr == 0) {
 #pragma unroll
@@ -640,7 +678,9 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb, fl
       const int rank = __popcll(eb & below);
       const bool sel = valid && (km > rp || (eq && eqn + rank < (int)rneed));
       const uint64_t sb = __ballot(sel);
-      if (sel) {
+      if constexpr (LIST) {
+        if (valid && !sel && idx[m] >= 0 && idx[m] < tlcap) tl[idx[m]].x = 0xff800000u;   // -inf: weight 0
+      } else if (sel) {
         const int slot = base + __popcll(sb & below);
         if (slot < topk) {
           a.indices[row * topk + slot] = idx[m];
@@ -668,7 +708,7 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb, fl
     }
     if (!live[e]) continue;
     const int oc = min(rowcnt[w][4 * lg + e][0], topk);
-    for (int p = oc + lr; p < topk; p += 16) {
+    if (!LIST) for (int p = oc + lr; p < topk; p += 16) {
       a.indices[rowg * topk + p] = 0;
       a.scores[rowg * topk + p] = -FLT_MAX;
     }
@@ -726,6 +766,16 @@ size_t topk_workspace_bytes(int B, int Tq, int H) {
          (size_t)B * H * KNCH * sizeof(float) + 512;
 }
 
+size_t topk_list_bytes(int B, int Tq, int H, int top_k) {
+  const size_t nqb = (Tq + QB - 1) / QB;
+  return (size_t)B * H * nqb * 4 * 16 * (size_t)(top_k + TOPK_CAP) * sizeof(uint2);
+}
+
+size_t topk_list_off_bytes(int B, int Tq, int Tk, int H) {
+  const size_t nqb = (Tq + QB - 1) / QB;
+  return (size_t)B * H * nqb * 4 * (size_t)((Tk + KT - 1) / KT + 1) * sizeof(int32_t);
+}
+
 hipError_t launch_score_topk(const TopkArgs& a0, hipStream_t st) {
   TopkArgs a = a0;
   const int nqb = (a.Tq + QB - 1) / QB;
@@ -737,8 +787,8 @@ hipError_t launch_score_topk(const TopkArgs& a0, hipStream_t st) {
     const int qb0 = a.dump_row0 / QB;
     const int qb1 = (a.dump_row0 + a.dump_rows + QB - 1) / QB;
     const dim3 grid((unsigned)(BH * (qb1 - qb0)));
-    if (a.dtype == DT_F32) score_topk_kernel<float, true, true, false, false><<<grid, 256, 0, st>>>(a, nqb, ms);
-    else score_topk_kernel<bf16_t, true, true, false, false><<<grid, 256, 0, st>>>(a, nqb, ms);
+    if (a.dtype == DT_F32) score_topk_kernel<float, true, true, false, false, false><<<grid, 256, 0, st>>>(a, nqb, ms);
+    else score_topk_kernel<bf16_t, true, true, false, false, false><<<grid, 256, 0, st>>>(a, nqb, ms);
     return hipGetLastError();
   }
   // workspace: [scratch lists | block flags | kmax]
@@ -755,10 +805,22 @@ hipError_t launch_score_topk(const TopkArgs& a0, hipStream_t st) {
   const dim3 grid((unsigned)(BH * nqb));
   const bool c16 = a.Tk <= 65535;   // 16-bit histogram counters cannot overflow
   const bool t2 = a.top2 != nullptr;
+  if (a.tl_list != nullptr) {   // layer path: tile lists (bf16, top-2 required)
+    a.tl_ntmax = (a.Tk + KT - 1) / KT;
+    if (a.dtype != DT_BF16 || !t2) return hipErrorInvalidValue;
+    if (c16) {
+      score_topk_kernel<bf16_t, false, true, true, false, true><<<grid, 256, 0, st>>>(a, nqb, ms);
+      score_topk_kernel<bf16_t, false, true, true, true, true><<<grid, 256, 0, st>>>(a, nqb, ms);
+    } else {
+      score_topk_kernel<bf16_t, false, false, true, false, true><<<grid, 256, 0, st>>>(a, nqb, ms);
+      score_topk_kernel<bf16_t, false, false, true, true, true><<<grid, 256, 0, st>>>(a, nqb, ms);
+    }
+    return hipGetLastError();
+  }
 #define SGSA_TOPK_LAUNCH(XT, C, T2)                                                   \
   do {                                                                                \
-    score_topk_kernel<XT, false, C, T2, false><<<grid, 256, 0, st>>>(a, nqb, ms);     \
-    score_topk_kernel<XT, false, C, T2, true><<<grid, 256, 0, st>>>(a, nqb, ms);      \
+    score_topk_kernel<XT, false, C, T2, false, false><<<grid, 256, 0, st>>>(a, nqb, ms);     \
+    score_topk_kernel<XT, false, C, T2, true, false><<<grid, 256, 0, st>>>(a, nqb, ms);      \
   } while (0)
   if (a.dtype == DT_F32) {
     if (c16) { if (t2) SGSA_TOPK_LAUNCH(float, true, true); else SGSA_TOPK_LAUNCH(float, true, false); }

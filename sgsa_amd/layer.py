@@ -87,3 +87,45 @@ def sgsa_layer_forward(
         _abi.ptr(h0), _WRITE_MODES[write_mode], float(alpha_max), float(tau_c), _abi.ptr(out), _abi.ptr(ht),
         _abi.ptr(ws), ws.numel(), _abi.stream_of(qc)))
     return out, ht
+
+
+def sgsa_layer_retrieve(
+    q_ret: Tensor,
+    k: Tensor,
+    v: Tensor,
+    budget_logits: Tensor,
+    top_k: int,
+    write_mode: str = "direct",
+    alpha_max: float = 0.25,
+    tau_c: float = 0.1,
+    workspace: Optional[LayerWorkspace] = None,
+) -> Tuple[Tensor, Tensor, Tensor]:
+    """The retrieval half of ``sgsa_layer_forward`` (sgsa_layer_retrieve): the
+    (write key, v_hat, alpha) that the layer feeds to the chunked update.
+
+    q_ret, k, v [B,T,H,D] (float32 or bfloat16); budget_logits [B,T,H].
+    Returns write_key / v_hat [B,T,H,D] in the input dtype and alpha [B,T,H] float32.
+    """
+    if not q_ret.is_cuda:
+        raise ValueError("sgsa_layer_retrieve: the SGSA kernels run on a ROCm GPU; got CPU tensors")
+    B, T, H, D = q_ret.shape
+    for name, t in (("k", k), ("v", v)):
+        if t.shape != q_ret.shape or t.dtype != q_ret.dtype:
+            raise ValueError(f"{name} must match q_ret in shape and dtype")
+    if budget_logits.shape != (B, T, H):
+        raise ValueError(f"budget_logits has shape {tuple(budget_logits.shape)}, expected {(B, T, H)}")
+    if write_mode not in _WRITE_MODES:
+        raise ValueError(f"write_mode must be one of {sorted(_WRITE_MODES)}")
+    dev = q_ret.device
+    rc, kc, vc = (t.contiguous() for t in (q_ret, k, v))
+    uc = budget_logits.float().contiguous()
+    wk = torch.empty_like(kc)
+    vh = torch.empty_like(kc)
+    al = torch.empty(B, T, H, device=dev, dtype=torch.float32)
+    nbytes = layer_workspace_bytes(q_ret.dtype, B, T, H, D, top_k)
+    ws = (workspace or LayerWorkspace()).get(nbytes, dev)
+    _abi.check(_abi.lib().sgsa_layer_retrieve(
+        _abi.dtype_code(q_ret.dtype), B, T, H, D, int(top_k), _abi.ptr(rc), _abi.ptr(kc), _abi.ptr(vc),
+        _abi.ptr(uc), _WRITE_MODES[write_mode], float(alpha_max), float(tau_c), _abi.ptr(wk), _abi.ptr(vh),
+        _abi.ptr(al), _abi.ptr(ws), ws.numel(), _abi.stream_of(rc)))
+    return wk, vh, al

@@ -95,6 +95,53 @@ def gather_gate(k: Tensor, v: Tensor, idx: Tensor, sc: Tensor, top2: Tensor, cnt
     return wk, vh, al
 
 
+def score_topk_lists(q: Tensor, k: Tensor, top_k: int):
+    """K1 of the fused layer: the causal top-k of q.k/sqrt(D) written as tile
+    lists (see include/sgsa.h) instead of per-row index/score lists.
+
+    q, k [B,T,H,D] bfloat16.  Returns (lists uint8 buffer, offsets int32,
+    top2 float32 [B,H,T,2], counts int32 [B,H,T]).
+    """
+    if not q.is_cuda:
+        raise ValueError("score_topk_lists: the SGSA kernels run on a ROCm GPU; got CPU tensors")
+    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or k.shape != q.shape:
+        raise ValueError("score_topk_lists takes bfloat16 q and k of equal shape")
+    B, T, H, D = q.shape
+    qc, kc = q.contiguous(), k.contiguous()
+    dev = q.device
+    L = _abi.lib()
+    lb, ob, wb = ctypes.c_size_t(), ctypes.c_size_t(), ctypes.c_size_t()
+    _abi.check(L.sgsa_topk_lists_size(B, T, H, int(top_k), ctypes.byref(lb), ctypes.byref(ob)))
+    _abi.check(L.sgsa_score_topk_workspace_size(B, T, H, ctypes.byref(wb)))
+    lists = torch.empty(lb.value, device=dev, dtype=torch.uint8)
+    offs = torch.empty(ob.value // 4, device=dev, dtype=torch.int32)
+    top2 = torch.empty(B, H, T, 2, device=dev, dtype=torch.float32)
+    cnt = torch.empty(B, H, T, device=dev, dtype=torch.int32)
+    ws = torch.empty(wb.value, device=dev, dtype=torch.uint8)
+    _abi.check(L.sgsa_score_topk_lists(B, T, H, D, int(top_k), _abi.ptr(qc), _abi.ptr(kc), _abi.ptr(lists),
+                                       _abi.ptr(offs), _abi.ptr(top2), _abi.ptr(cnt), _abi.ptr(ws), wb.value,
+                                       _abi.stream_of(qc)))
+    return lists, offs, top2, cnt
+
+
+def gather_lists(k: Tensor, v: Tensor, lists: Tensor, offs: Tensor, top2: Tensor, cnt: Tensor,
+                 budget_logits: Tensor, top_k: int, write_mode: str = "direct", alpha_max: float = 0.25,
+                 tau_c: float = 0.1):
+    """K2 of the fused layer on ``score_topk_lists`` output: (write key, v_hat, alpha)."""
+    B, T, H, D = k.shape
+    mode = {"direct": 0, "residual": 1}[write_mode]
+    kc, vc = k.contiguous(), v.contiguous()
+    wk = torch.empty_like(kc)
+    vh = torch.empty_like(kc)
+    al = torch.empty(B, T, H, device=k.device, dtype=torch.float32)
+    bud = budget_logits.float().contiguous()
+    _abi.check(_abi.lib().sgsa_sparse_gather_lists(
+        B, T, H, D, int(top_k), _abi.ptr(kc), _abi.ptr(vc), _abi.ptr(lists), _abi.ptr(offs), _abi.ptr(top2),
+        _abi.ptr(cnt), _abi.ptr(bud), mode, float(alpha_max), float(tau_c), _abi.ptr(wk if mode == 0 else None),
+        _abi.ptr(vh), _abi.ptr(wk if mode == 1 else None), _abi.ptr(al), _abi.stream_of(kc)))
+    return wk, vh, al
+
+
 def score_dump(q: Tensor, k: Tensor, row0: int, rows: int, causal: bool = True, q_offset: int = 0,
                scale: Optional[float] = None, scale_mode: int = 0) -> Tensor:
     """The exact fp32 scores score_topk selects on, for query rows [row0, row0+rows): [B,H,rows,Tk]."""

@@ -101,3 +101,42 @@ def test_tiled_gather_matches_direct_gather(dev, write_mode, dims):
     _close(wk_t, wk_d, 1e-2, "write_key")
     _close(vh_t, vh_d, 1e-2, "v_hat")
     _close(al_t, al_d, 1e-2, "alpha")
+
+
+@pytest.mark.parametrize("dtype,tol,dims", [
+    (torch.float32, 1e-4, (1, 512, 4, 64, 32)),        # direct gather
+    (torch.bfloat16, 2e-2, (1, 1024, 2, 128, 256)),    # tile lists (D = 128)
+    (torch.bfloat16, 2e-2, (2, 700, 3, 128, 64)),      # tile lists, ragged last row block
+    (torch.bfloat16, 2e-2, (1, 300, 2, 64, 40)),       # direct gather, bf16
+])
+@pytest.mark.parametrize("write_mode", ["direct", "residual"])
+def test_layer_retrieve_matches_oracle(dev, dtype, tol, dims, write_mode):
+    # the (write key, v_hat, alpha) that the layer feeds to the chunked update
+    B, T, H, D, k = dims
+    x = O.make_inputs(B, T, H, D, dtype=dtype, seed=2)
+    ref = O.sgsa_layer_forward(x["q_f32"], x["k_f32"], x["v_f32"], x["q_f32"], x["beta"], x["gamma"],
+                               x["budget"], k, write_mode=write_mode)
+    wk, vh, al = sgsa_amd.sgsa_layer_retrieve(x["q"].to(dev), x["k"].to(dev), x["v"].to(dev), x["budget"].to(dev),
+                                              k, write_mode=write_mode)
+    torch.cuda.synchronize()
+    _close(wk, ref["write_key"], tol, "write_key")
+    _close(vh, ref["v_hat"], tol, "v_hat")
+    _close(al, ref["alpha"], max(tol, 1e-4), "alpha")
+
+
+def test_layer_forward_carries_the_sparse_write(dev):
+    # the sparse write must be visible in o: closer to the full reference than
+    # to the reference without it (budget -> -inf gives alpha = 0)
+    B, T, H, D, k = 1, 512, 2, 128, 64
+    x = O.make_inputs(B, T, H, D, dtype=torch.bfloat16, seed=7)
+    bud = torch.full_like(x["budget"], 6.0)   # sigmoid ~ 1: large gates
+    args = (x["q_f32"], x["k_f32"], x["v_f32"], x["q_f32"], x["beta"], x["gamma"])
+    ref = O.sgsa_layer_forward(*args, bud, k, alpha_max=0.9)["o"]
+    ref0 = O.sgsa_layer_forward(*args, torch.full_like(bud, -1e4), k, alpha_max=0.9)["o"]
+    o, _ = sgsa_amd.sgsa_layer_forward(x["q"].to(dev), x["k"].to(dev), x["v"].to(dev), x["q"].to(dev),
+                                       x["beta"].to(dev), x["gamma"].to(dev), bud.to(dev), k, alpha_max=0.9)
+    torch.cuda.synchronize()
+    o = o.float().cpu()
+    gap = (ref - ref0).abs().max()
+    assert gap > 0.05 * ref.abs().max(), "the sparse write is too small to test"
+    assert (o - ref).abs().max() < 0.25 * gap

@@ -156,3 +156,71 @@ def test_topk_large_rows_subset(dev):
     i_s, s_s, _, c_s = sgsa_amd.score_topk(q, kk, k, sorted=True)
     torch.cuda.synchronize()
     _check_rows(i_s, s_s, c_s, top2, dump.cpu(), k, row0=T - 64)
+
+
+def _decode_tile_lists(lists, offs, B, T, H, top_k):
+    """(mask [B*H,T,T] of selected (row, key), scores at those) from the layer-path tile lists."""
+    nqb = ntm = (T + 63) // 64
+    kk = min(top_k, T)
+    cap = 16 * (kk + 512)
+    R = B * H * nqb * 4
+    ent = lists.view(torch.int32).view(R, cap, 2).cpu()
+    off = offs.view(R, ntm + 1).cpu().long()
+    mask = torch.zeros(B * H, T, T, dtype=torch.bool)
+    smat = torch.zeros(B * H, T, T)
+    for r in range(R):
+        bh, qb, w = r // (nqb * 4), (r // 4) % nqb, r % 4
+        ntile = (min(T, qb * 64 + 64) + 63) // 64
+        n = int(off[r, ntile])
+        if n == 0:
+            continue
+        e = ent[r, :n]
+        tile = torch.searchsorted(off[r, 1:ntile + 1].contiguous(), torch.arange(n), right=True)
+        key = tile * 64 + (e[:, 1] & 63).long()
+        row = qb * 64 + 16 * w + (e[:, 1] >> 8).long()
+        s = e[:, 0].contiguous().view(torch.float32)
+        keep = s != float("-inf")
+        assert not mask[bh, row[keep], key[keep]].any(), "a (row, key) appears twice"
+        mask[bh, row[keep], key[keep]] = True
+        smat[bh, row[keep], key[keep]] = s[keep]
+    return mask, smat
+
+
+@pytest.mark.parametrize("case", ["random", "ties", "mass_ties", "heavy_tail", "d64"])
+def test_tile_lists_hold_the_exact_selection(dev, case):
+    # the layer-path K1 (tile lists) selects exactly what the row-list K1 selects
+    B, T, H, D, k = 1, 2100, 2, 128, 256
+    g = torch.Generator().manual_seed(21)
+    if case == "random":
+        q, kk = torch.randn(B, T, H, D, generator=g), torch.randn(B, T, H, D, generator=g)
+    elif case == "ties":
+        base = torch.randn(5, H, D, generator=g)
+        kk = base[torch.randint(0, 5, (T,), generator=g)][None]
+        q = torch.randn(B, T, H, D, generator=g)
+    elif case == "mass_ties":   # threshold bin beyond the candidate cap: radix fallback blocks
+        base = torch.randn(2, H, D, generator=g)
+        kk = base[torch.randint(0, 2, (T,), generator=g)][None]
+        q = torch.randn(B, T, H, D, generator=g)
+    elif case == "heavy_tail":
+        x = O.make_inputs(B, T, H, D, dtype=torch.float32, seed=12, heavy_tail=True, with_budget=False)
+        q, kk = x["q"], x["k_ret"]
+    else:
+        B, T, H, D, k = 2, 700, 3, 64, 100
+        q, kk = torch.randn(B, T, H, D, generator=g), torch.randn(B, T, H, D, generator=g)
+    q, kk = q.to(dev, torch.bfloat16).contiguous(), kk.to(dev, torch.bfloat16).contiguous()
+    lists, offs, t2l, cl = sgsa_amd.score_topk_lists(q, kk, k)
+    idx, sc, t2, cnt = sgsa_amd.score_topk(q, kk, k, sorted=False)
+    torch.cuda.synchronize()
+    assert torch.equal(cl.cpu(), cnt.cpu()), "counts differ"
+    assert torch.equal(t2l.cpu(), t2.cpu()), "top2 differs"
+    mask, smat = _decode_tile_lists(lists, offs, B, T, H, k)
+    ref = torch.zeros_like(mask)
+    rsc = torch.zeros_like(smat)
+    kq = min(k, T)
+    ic, sg, cc = idx.cpu().long().view(B * H, T, kq), sc.cpu().view(B * H, T, kq), cnt.cpu().view(B * H, T)
+    live = torch.arange(kq)[None, None, :] < cc[..., None]
+    bi, ri, si = live.nonzero(as_tuple=True)
+    ref[bi, ri, ic[bi, ri, si]] = True
+    rsc[bi, ri, ic[bi, ri, si]] = sg[bi, ri, si]
+    assert torch.equal(mask, ref), f"selected sets differ in {(mask != ref).sum().item()} (row, key) pairs"
+    assert torch.equal(smat[mask], rsc[mask]), "selected scores differ"
