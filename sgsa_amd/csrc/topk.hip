@@ -381,7 +381,7 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb, fl
     }
   };
   auto bump = [&](int row, uint32_t bin) __attribute__((always_inline)) {
-    if constexpr (C16) atomicAdd(&hist[w][row][bin >> 1], 1u << ((bin & 1u) << 4));
+    if constexpr (C16) atomicAdd(&hist[w][row][bin >> 1], 1u + (bin & 1u) * 0xffffu);   // low / high half
     else atomicAdd(&hist[w][row][bin], 1u);
   };
 
@@ -392,16 +392,27 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb, fl
     for (int e = 0; e < 4; ++e) mine |= (mode[e] != SELECT_ALL);
     const bool wave_busy = __ballot(mine) != 0;
     if (__syncthreads_or(mine)) {
+      bool hrow[4];   // rows of this lane that build a histogram
+#pragma unroll
+      for (int e = 0; e < 4; ++e) hrow[e] = live[e] && mode[e] != SELECT_ALL;
       sweep([&](int kt, f4* acc) __attribute__((always_inline)) {
         if (!wave_busy) return;
-        const bool full = (kt + 1) * KT <= minvalid;
+        if ((kt + 1) * KT <= minvalid) {   // every key of the tile is valid for every live row
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt) {
-          const int j = kt * KT + 16 * nt + lr;
+          for (int nt = 0; nt < 4; ++nt) {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            if (live[e] && mode[e] != SELECT_ALL && (full || j < nvalid[e]))
-              bump(4 * lg + e, (uint32_t)score_bin(acc[nt][e], iw[e]));
+            for (int e = 0; e < 4; ++e) {
+              if (hrow[e]) bump(4 * lg + e, (uint32_t)score_bin(acc[nt][e], iw[e]));
+            }
+          }
+        } else {
+#pragma unroll
+          for (int nt = 0; nt < 4; ++nt) {
+            const int j = kt * KT + 16 * nt + lr;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              if (hrow[e] && j < nvalid[e]) bump(4 * lg + e, (uint32_t)score_bin(acc[nt][e], iw[e]));
+            }
           }
         }
       });
@@ -519,26 +530,6 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb, fl
   int32_t* toff = LIST ? a.tl_off + lreg * (a.tl_ntmax + 1) : nullptr;
   int woff = 0;
   auto emit = [&](int e, int kk, int j, float s, bool sel, bool col) __attribute__((always_inline)) {
-    if constexpr (LIST) {
-      const bool cand = sel || col;
-      const uint64_t cb = __ballot(cand);
-      const uint32_t cbr = (uint32_t)(cb >> (16 * lg)) & 0xffffu;
-      const uint32_t cm = (uint32_t)(__ballot(col) >> (16 * lg)) & 0xffffu;
-      if (cand) {
-        const int pos = woff + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(cb >> 32),
-                                                              __builtin_amdgcn_mbcnt_lo((uint32_t)cb, 0u));
-        if (pos < tlcap) tl[pos] = make_uint2(__float_as_uint(s), (uint32_t)(((4 * lg + e) << 8) | kk));
-        if (col) {
-          const int slot = colc[e] + __popc(cm & lower);
-          if (slot < TOPK_CAP)
-            scratch[(long)(grow0 + e) * TOPK_CAP + slot] = make_uint2(__float_as_uint(s), (uint32_t)pos);
-        }
-      }
-      woff += __popcll(cb);
-      outc[e] += __popc(cbr & ~cm);
-      colc[e] += __popc(cm);
-      return;
-    }
     const uint32_t sm = (uint32_t)(__ballot(sel) >> (16 * lg)) & 0xffffu;
     const uint32_t cm = (uint32_t)(__ballot(col) >> (16 * lg)) & 0xffffu;
     const long row = (long)(grow0 + e);
@@ -563,11 +554,64 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb, fl
       m1[e] = fmaxf(m1[e], so);
     }
   };
-  if constexpr (!FB) {
-    sweep([&](int kt, f4* acc) __attribute__((always_inline)) {
-      if constexpr (LIST) {
-        if (lane == 0) toff[kt] = woff;
+  // LIST emission of one score: every candidate (s >= th0: selected or in the
+  // threshold bin) gets the next entry of the wave's list in lane order; those
+  // in the threshold bin also go to the row's scratch list with the entry index.
+  const uint32_t rk0 = ((uint32_t)(4 * lg) << 8) | (uint32_t)lr;
+  auto emit_list = [&](int e, int nt, float s, bool cand, auto cols) __attribute__((always_inline)) {
+    const uint64_t cb = __ballot(cand);
+    const int pos = min(woff + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(cb >> 32),
+                                                              __builtin_amdgcn_mbcnt_lo((uint32_t)cb, 0u)),
+                        tlcap - 1);
+    if (cand) tl[pos] = make_uint2(__float_as_uint(s), rk0 + (uint32_t)((e << 8) + 16 * nt));
+    woff += __popcll(cb);
+    if constexpr (!decltype(cols)::value) return;
+    const bool col = cand && s < th1[e];
+    const uint64_t cm = __ballot(col);
+    if (cm != 0) {   // wave-uniform
+      const uint32_t grp = (uint32_t)(cm >> (16 * lg)) & 0xffffu;
+      if (col) {
+        const int slot = colc[e] + __popc(grp & lower);
+        if (slot < TOPK_CAP) scratch[(long)(grow0 + e) * TOPK_CAP + slot] = make_uint2(__float_as_uint(s), (uint32_t)pos);
       }
+      colc[e] += __popc(grp);
+    }
+  };
+  // running top-2 (m1 >= m2): med3 gives the new second before m1 moves
+  auto top2_fast = [&](int e, float x) __attribute__((always_inline)) {
+    m2[e] = __builtin_amdgcn_fmed3f(m1[e], m2[e], x);
+    m1[e] = fmaxf(m1[e], x);
+  };
+  if constexpr (!FB && LIST) {
+    sweep([&](int kt, f4* acc) __attribute__((always_inline)) {
+      if (lane == 0) toff[kt] = woff;
+      if ((kt + 1) * KT <= minvalid) {
+        // full tile: every key is valid for every live row
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float s = acc[nt][e];
+            emit_list(e, nt, s, live[e] && s >= th0[e], std::true_type{});
+            top2_fast(e, s);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) {
+          const int j = kt * KT + 16 * nt + lr;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const bool ok = live[e] && j < nvalid[e];
+            const float s = acc[nt][e];
+            emit_list(e, nt, s, ok && s >= th0[e], std::true_type{});
+            top2_fast(e, ok ? s : -FLT_MAX);
+          }
+        }
+      }
+    });
+  } else if constexpr (!FB) {
+    sweep([&](int kt, f4* acc) __attribute__((always_inline)) {
       const bool full = (kt + 1) * KT <= minvalid;
 #pragma unroll
       for (int nt = 0; nt < 4; ++nt) {
@@ -605,7 +649,8 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb, fl
           const uint32_t eqm = (uint32_t)(__ballot(eq) >> (16 * lg)) & 0xffffu;
           sel = sel || (inb && (km > pfx[e] || (eq && eqc[e] + __popc(eqm & lower) < need[e])));
           eqc[e] += __popc(eqm);
-          emit(e, 16 * nt + lr, j, s, sel, col);
+          if constexpr (LIST) emit_list(e, nt, s, sel, std::false_type{});
+          else emit(e, 16 * nt + lr, j, s, sel, col);
           top2_update(e, ok, s);
         }
       }
@@ -707,7 +752,8 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb, fl
       }
     }
     if (!live[e]) continue;
-    const int oc = min(rowcnt[w][4 * lg + e][0], topk);
+    // LIST: every row selects exactly min(top_k, valid keys)
+    const int oc = LIST ? min(topk, nvalid[e]) : min(rowcnt[w][4 * lg + e][0], topk);
     if (!LIST) for (int p = oc + lr; p < topk; p += 16) {
       a.indices[rowg * topk + p] = 0;
       a.scores[rowg * topk + p] = -FLT_MAX;
