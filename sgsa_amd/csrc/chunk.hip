@@ -81,7 +81,7 @@ __global__ __launch_bounds__(256) void chunk_intra_kernel(
 
   const int c = blockIdx.x, bh = blockIdx.y;
   const int b = bh / H, h = bh % H;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform
   const int lr = lane & 15, lg = lane >> 4;
   const int t0 = c * L;
 
@@ -233,7 +233,7 @@ __global__ __launch_bounds__(256) void chunk_state_kernel(
 
   const int cs = blockIdx.x, bh = blockIdx.y;
   const int b = bh / H, h = bh % H;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform
   const int lr = lane & 15, lg = lane >> 4;
   const int col = 16 * cs + lr;
 
@@ -350,7 +350,7 @@ __global__ __launch_bounds__(256) void chunk_out_kernel(
 
   const int c = blockIdx.x, bh = blockIdx.y;
   const int b = bh / H, h = bh % H;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform
   const int lr = lane & 15, lg = lane >> 4;
   const int t0 = c * L;
 

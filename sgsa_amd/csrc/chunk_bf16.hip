@@ -106,7 +106,7 @@ __global__ __launch_bounds__(256) void chunk_intra_bf16(
 
   const int c = blockIdx.x, bh = blockIdx.y;
   const int b = bh / H, h = bh % H;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform
   const int lr = lane & 15, lg = lane >> 4;
   const int t0 = c * L;
   const long cidx = (long)bh * NT + c;
@@ -305,7 +305,7 @@ __global__ __launch_bounds__(256) void chunk_state_bf16(
   // chunk's W / kappa^T once from the fabric.
   const int bh = blockIdx.x, cs = blockIdx.y;
   const int b = bh / H, h = bh % H;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform
   const int lr = lane & 15, lg = lane >> 4;
   const int col = 16 * cs + lr;
 
@@ -473,7 +473,7 @@ __global__ __launch_bounds__(256) void chunk_out_bf16(
 
   const int c = blockIdx.x, bh = blockIdx.y;
   const int b = bh / H, h = bh % H;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform
   const int lr = lane & 15, lg = lane >> 4;
   const int t0 = c * L;
   const long cidx = (long)bh * NT + c;

@@ -91,4 +91,7 @@ __device__ __forceinline__ float group_sum(float v, int w) {
 
 __device__ __forceinline__ int popc64(uint64_t x) { return __popcll(x); }
 
+// Wave ballot straight from the predicate's lane mask (no int round trip).
+__device__ __forceinline__ uint64_t ballot64(bool p) { return __builtin_amdgcn_ballot_w64(p); }
+
 }  // namespace sgsa

@@ -250,7 +250,7 @@ __global__ __launch_bounds__(256) void gather_tile_kernel(GatherArgs a, const in
   const int bh = bid % BH;
   const int qb = nqb - 1 - bid / BH;    // heaviest query blocks first
   const int b = bh / a.H, h = bh % a.H;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform
   const int lr = lane & 15, lg = lane >> 4;
   const int Tq = a.Tq, Tk = a.Tk, H = a.H, topk = a.top_k;
   const int r0 = qb * QB;
@@ -309,10 +309,10 @@ __global__ __launch_bounds__(256) void gather_tile_kernel(GatherArgs a, const in
       int n1 = slot_half<0>(run1, t0, t1, lg, m, prw, junk, esum, stop1);
       int n2 = slot_half<0>(run2, t0, t1, lg, m, prw, junk, esum, stop2);
       // the second half matters only to rows that neither stopped nor ran out in the first
-      const uint64_t h1 = __ballot(stop1), h2 = __ballot(stop2);
+      const uint64_t h1 = ballot64(stop1), h2 = ballot64(stop2);
       const bool s1 = ((h1 >> lr) | (h1 >> (lr + 16)) | (h1 >> (lr + 32)) | (h1 >> (lr + 48))) & 1;
       const bool s2 = ((h2 >> lr) | (h2 >> (lr + 16)) | (h2 >> (lr + 32)) | (h2 >> (lr + 48))) & 1;
-      if (__ballot((!s1 && run1.end > run1.base + 16) || (!s2 && run2.end > run2.base + 16))) {
+      if (ballot64((!s1 && run1.end > run1.base + 16) || (!s2 && run2.end > run2.base + 16))) {
         n1 += slot_half<1>(run1, t0, t1, lg, m, prw, junk, esum, stop1);
         n2 += slot_half<1>(run2, t0, t1, lg, m, prw, junk, esum, stop2);
       }
@@ -320,7 +320,7 @@ __global__ __launch_bounds__(256) void gather_tile_kernel(GatherArgs a, const in
       n1 += __shfl_xor(n1, 32, 64);
       n2 += __shfl_xor(n2, 16, 64);
       n2 += __shfl_xor(n2, 32, 64);
-      const uint64_t g1 = __ballot(stop1), g2 = __ballot(stop2);
+      const uint64_t g1 = ballot64(stop1), g2 = ballot64(stop2);
       const bool f1 = ((g1 >> lr) | (g1 >> (lr + 16)) | (g1 >> (lr + 32)) | (g1 >> (lr + 48))) & 1;
       const bool f2 = ((g2 >> lr) | (g2 >> (lr + 16)) | (g2 >> (lr + 32)) | (g2 >> (lr + 48))) & 1;
       run1.c += n1;
@@ -330,8 +330,8 @@ __global__ __launch_bounds__(256) void gather_tile_kernel(GatherArgs a, const in
       // a row that consumed its whole window without meeting t1 may have more keys in this tile
       return (!f1 && run1.c < run1.end) || (!f2 && run2.c < run2.end);
     };
-    if (__ballot(scatter_pass())) {
-      while (__ballot(scatter_pass())) {
+    if (ballot64(scatter_pass())) {
+      while (ballot64(scatter_pass())) {
       }
     }
     __syncthreads();           // K/V tile committed by all threads; P rows written
@@ -375,7 +375,7 @@ __global__ __launch_bounds__(256, 2) void gather_list_kernel(GatherArgs a, const
   const int bh = bid % BH;
   const int qb2 = nqb2 - 1 - bid / BH;   // heaviest row blocks first
   const int b = bh / a.H, h = bh % a.H;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform
   const int lr = lane & 15, lg = lane >> 4;
   const int Tq = a.Tq, Tk = a.Tk, H = a.H, topk = a.top_k;
   const int r0 = qb2 * QL;

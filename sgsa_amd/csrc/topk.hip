@@ -127,7 +127,7 @@ __device__ __forceinline__ void find_bin(const uint32_t (&c)[4], int lane, uint3
   }
   const uint32_t exc = inc - loc;
   const bool hit = exc < need && need <= inc;
-  const uint64_t bal = __ballot(hit);
+  const uint64_t bal = ballot64(hit);
   const int src = bal ? __ffsll((unsigned long long)bal) - 1 : 0;
   int b = 0;
   uint32_t ab = 0, ct = 0;
@@ -206,7 +206,7 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb, fl
   int qb = nqb - 1 - bid / BH;   // heaviest (latest) query blocks first
   if (DUMP) qb = (a.dump_row0 / QB) + bid / BH;
   const int b = bh / a.H, h = bh % a.H;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform
   const int lr = lane & 15, lg = lane >> 4;
   const int r0 = qb * QB;
   const int Tq = a.Tq, Tk = a.Tk, H = a.H, D = a.D;
@@ -390,7 +390,7 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb, fl
     int mine = 0;
 #pragma unroll
     for (int e = 0; e < 4; ++e) mine |= (mode[e] != SELECT_ALL);
-    const bool wave_busy = __ballot(mine) != 0;
+    const bool wave_busy = ballot64(mine) != 0;
     if (__syncthreads_or(mine)) {
       bool hrow[4];   // rows of this lane that build a histogram
 #pragma unroll
@@ -451,7 +451,7 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb, fl
     int mine = 0;
 #pragma unroll
     for (int e = 0; e < 4; ++e) mine |= (mode[e] == RADIX && !rdone[e]);
-    const bool wave_busy = __ballot(mine) != 0;
+    const bool wave_busy = ballot64(mine) != 0;
     if (!__syncthreads_or(mine)) break;
     sweep([&](int kt, f4* acc) __attribute__((always_inline)) {
       if (!wave_busy) return;
@@ -530,8 +530,8 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb, fl
   int32_t* toff = LIST ? a.tl_off + lreg * (a.tl_ntmax + 1) : nullptr;
   int woff = 0;
   auto emit = [&](int e, int kk, int j, float s, bool sel, bool col) __attribute__((always_inline)) {
-    const uint32_t sm = (uint32_t)(__ballot(sel) >> (16 * lg)) & 0xffffu;
-    const uint32_t cm = (uint32_t)(__ballot(col) >> (16 * lg)) & 0xffffu;
+    const uint32_t sm = (uint32_t)(ballot64(sel) >> (16 * lg)) & 0xffffu;
+    const uint32_t cm = (uint32_t)(ballot64(col) >> (16 * lg)) & 0xffffu;
     const long row = (long)(grow0 + e);
     if (sel) {
       const int slot = outc[e] + __popc(sm & lower);
@@ -559,15 +559,15 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb, fl
   // in the threshold bin also go to the row's scratch list with the entry index.
   const uint32_t rk0 = ((uint32_t)(4 * lg) << 8) | (uint32_t)lr;
   auto emit_list = [&](int e, int nt, float s, bool cand, auto cols) __attribute__((always_inline)) {
-    const uint64_t cb = __ballot(cand);
-    const int pos = min(woff + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(cb >> 32),
-                                                              __builtin_amdgcn_mbcnt_lo((uint32_t)cb, 0u)),
-                        tlcap - 1);
+    const uint64_t cb = ballot64(cand);
+    const uint32_t pos = min((uint32_t)woff + __builtin_amdgcn_mbcnt_hi((uint32_t)(cb >> 32),
+                                                                        __builtin_amdgcn_mbcnt_lo((uint32_t)cb, 0u)),
+                             (uint32_t)tlcap - 1u);
     if (cand) tl[pos] = make_uint2(__float_as_uint(s), rk0 + (uint32_t)((e << 8) + 16 * nt));
-    woff += __popcll(cb);
+    woff = __builtin_amdgcn_readfirstlane(woff + __popcll(cb));
     if constexpr (!decltype(cols)::value) return;
     const bool col = cand && s < th1[e];
-    const uint64_t cm = __ballot(col);
+    const uint64_t cm = ballot64(col);
     if (cm != 0) {   // wave-uniform
       const uint32_t grp = (uint32_t)(cm >> (16 * lg)) & 0xffffu;
       if (col) {
@@ -646,7 +646,7 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb, fl
           const uint32_t km = f32_order_key(s) & msk[e];
           const bool inb = ok && mode[e] == RADIX;
           const bool eq = inb && km == pfx[e];
-          const uint32_t eqm = (uint32_t)(__ballot(eq) >> (16 * lg)) & 0xffffu;
+          const uint32_t eqm = (uint32_t)(ballot64(eq) >> (16 * lg)) & 0xffffu;
           sel = sel || (inb && (km > pfx[e] || (eq && eqc[e] + __popc(eqm & lower) < need[e])));
           eqc[e] += __popc(eqm);
           if constexpr (LIST) emit_list(e, nt, s, sel, std::false_type{});
@@ -719,10 +719,10 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb, fl
       const bool valid = 64 * m + lane < n;
       const uint32_t km = key[m] & rm;
       const bool eq = valid && km == rp;
-      const uint64_t eb = __ballot(eq);
+      const uint64_t eb = ballot64(eq);
       const int rank = __popcll(eb & below);
       const bool sel = valid && (km > rp || (eq && eqn + rank < (int)rneed));
-      const uint64_t sb = __ballot(sel);
+      const uint64_t sb = ballot64(sel);
       if constexpr (LIST) {
         if (valid && !sel && idx[m] >= 0 && idx[m] < tlcap) tl[idx[m]].x = 0xff800000u;   // -inf: weight 0
       } else if (sel) {
