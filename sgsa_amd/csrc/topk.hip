@@ -558,6 +558,12 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb, fl
   // threshold bin) gets the next entry of the wave's list in lane order; those
   // in the threshold bin also go to the row's scratch list with the entry index.
   const uint32_t rk0 = ((uint32_t)(4 * lg) << 8) | (uint32_t)lr;
+  const uint64_t grp_mask = 0xffffull << (16 * lg);   // the 16 lanes of this lane's row group
+  float th0e[4];                                       // th0 with dead rows folded in (+inf)
+#pragma unroll
+  for (int e = 0; e < 4; ++e) th0e[e] = live[e] ? th0[e] : INFINITY;
+  // Candidate test = one compare; the entry position = ballot + mbcnt against the
+  // wave-uniform running offset; the threshold-bin mask is formed on scalar masks.
   auto emit_list = [&](int e, int nt, float s, bool cand, auto cols) __attribute__((always_inline)) {
     const uint64_t cb = ballot64(cand);
     const uint32_t pos = min((uint32_t)woff + __builtin_amdgcn_mbcnt_hi((uint32_t)(cb >> 32),
@@ -566,15 +572,15 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb, fl
     if (cand) tl[pos] = make_uint2(__float_as_uint(s), rk0 + (uint32_t)((e << 8) + 16 * nt));
     woff = __builtin_amdgcn_readfirstlane(woff + __popcll(cb));
     if constexpr (!decltype(cols)::value) return;
-    const bool col = cand && s < th1[e];
-    const uint64_t cm = ballot64(col);
+    const uint64_t cm = cb & ballot64(s < th1[e]);
     if (cm != 0) {   // wave-uniform
-      const uint32_t grp = (uint32_t)(cm >> (16 * lg)) & 0xffffu;
-      if (col) {
-        const int slot = colc[e] + __popc(grp & lower);
-        if (slot < TOPK_CAP) scratch[(long)(grow0 + e) * TOPK_CAP + slot] = make_uint2(__float_as_uint(s), (uint32_t)pos);
+      const uint64_t gm = cm & grp_mask;
+      if (cand && s < th1[e]) {
+        const int slot = colc[e] + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(gm >> 32),
+                                                                  __builtin_amdgcn_mbcnt_lo((uint32_t)gm, 0u));
+        if (slot < TOPK_CAP) scratch[(long)(grow0 + e) * TOPK_CAP + slot] = make_uint2(__float_as_uint(s), pos);
       }
-      colc[e] += __popc(grp);
+      colc[e] += __popcll(gm);
     }
   };
   // running top-2 (m1 >= m2): med3 gives the new second before m1 moves
@@ -592,7 +598,7 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb, fl
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const float s = acc[nt][e];
-            emit_list(e, nt, s, live[e] && s >= th0[e], std::true_type{});
+            emit_list(e, nt, s, s >= th0e[e], std::true_type{});
             top2_fast(e, s);
           }
         }
@@ -604,7 +610,7 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb, fl
           for (int e = 0; e < 4; ++e) {
             const bool ok = live[e] && j < nvalid[e];
             const float s = acc[nt][e];
-            emit_list(e, nt, s, ok && s >= th0[e], std::true_type{});
+            emit_list(e, nt, s, s >= th0e[e] && j < nvalid[e], std::true_type{});
             top2_fast(e, ok ? s : -FLT_MAX);
           }
         }
