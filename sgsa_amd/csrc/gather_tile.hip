@@ -463,16 +463,25 @@ __global__ __launch_bounds__(256, 2) void gather_list_kernel(GatherArgs a, const
       entries(pn[mt], mt, n0[mt]);
     }
     wave_lds_sync();
+    // the prefetched entries of both lists, without branches (independent LDS reads batch)
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
-      for (int i = 0; i < NPE; ++i) {
-        if (c0[mt] + 64 * i < c1[mt]) scat(pe[mt][i], mt, c0[mt] + 64 * i + lane < c1[mt]);   // wave-uniform skip
+      for (int i = 0; i < NPE; ++i) scat(pe[mt][i], mt, c0[mt] + 64 * i + lane < c1[mt]);
+    }
+    // dense tiles: the rest, four loads in flight at a time
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      for (int e0 = c0[mt] + 64 * NPE; e0 < c1[mt]; e0 += 256) {
+        uint2 en[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) en[i] = tlr[mt][min(max(e0 + 64 * i + lane, 0), tlcap - 1)];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) scat(en[i], mt, e0 + 64 * i + lane < c1[mt]);
       }
-      for (int e0 = c0[mt] + 64 * NPE; e0 < c1[mt]; e0 += 64) {   // dense tiles: the rest, loaded here
-        const uint2 en = tlr[mt][min(max(e0 + lane, 0), tlcap - 1)];
-        scat(en, mt, e0 + lane < c1[mt]);
-      }
+    }
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
       for (int i = 0; i < NPE; ++i) pe[mt][i] = pn[mt][i];
       c0[mt] = n0[mt];
@@ -480,18 +489,27 @@ __global__ __launch_bounds__(256, 2) void gather_list_kernel(GatherArgs a, const
     }
     __syncthreads();           // K/V tile committed by all threads; P rows written
     // k_hat += P K, v_hat += P V, E += P 1  (two 16-row tiles share each K/V operand)
+    // Operand reads are software-pipelined by hand: the K/V fragments of step
+    // n+1 are in flight while step n multiplies (the accumulators leave too few
+    // registers for the compiler to hoist them on its own).
 #pragma unroll
     for (int s = 0; s < KT / 32; ++s) {
-      const uint4 pa0 = *reinterpret_cast<const uint4*>(&Pw[lr * PT + 32 * s + 8 * lg]);
-      const uint4 pa1 = *reinterpret_cast<const uint4*>(&Pw[(16 + lr) * PT + 32 * s + 8 * lg]);
+      const int cofs = 32 * s + 8 * lg;
+      const uint4 pa0 = *reinterpret_cast<const uint4*>(&Pw[lr * PT + cofs]);
+      const uint4 pa1 = *reinterpret_cast<const uint4*>(&Pw[(16 + lr) * PT + cofs]);
+      uint4 kb[2], vb[2];
+      kb[0] = *reinterpret_cast<const uint4*>(&Kt[lr * PT + cofs]);
+      vb[0] = *reinterpret_cast<const uint4*>(&Vt[lr * PT + cofs]);
 #pragma unroll
       for (int n = 0; n < DP / 16; ++n) {
-        const uint4 kb = *reinterpret_cast<const uint4*>(&Kt[(16 * n + lr) * PT + 32 * s + 8 * lg]);
-        const uint4 vb = *reinterpret_cast<const uint4*>(&Vt[(16 * n + lr) * PT + 32 * s + 8 * lg]);
-        ok_[0][n] = mma_bf16(as_bf8(pa0), as_bf8(kb), ok_[0][n]);
-        ok_[1][n] = mma_bf16(as_bf8(pa1), as_bf8(kb), ok_[1][n]);
-        ov_[0][n] = mma_bf16(as_bf8(pa0), as_bf8(vb), ov_[0][n]);
-        ov_[1][n] = mma_bf16(as_bf8(pa1), as_bf8(vb), ov_[1][n]);
+        if (n + 1 < DP / 16) {
+          kb[(n + 1) & 1] = *reinterpret_cast<const uint4*>(&Kt[(16 * (n + 1) + lr) * PT + cofs]);
+          vb[(n + 1) & 1] = *reinterpret_cast<const uint4*>(&Vt[(16 * (n + 1) + lr) * PT + cofs]);
+        }
+        ok_[0][n] = mma_bf16(as_bf8(pa0), as_bf8(kb[n & 1]), ok_[0][n]);
+        ok_[1][n] = mma_bf16(as_bf8(pa1), as_bf8(kb[n & 1]), ok_[1][n]);
+        ov_[0][n] = mma_bf16(as_bf8(pa0), as_bf8(vb[n & 1]), ov_[0][n]);
+        ov_[1][n] = mma_bf16(as_bf8(pa1), as_bf8(vb[n & 1]), ov_[1][n]);
       }
       es[0] = mma_bf16(as_bf8(pa0), as_bf8(ones4), es[0]);
       es[1] = mma_bf16(as_bf8(pa1), as_bf8(ones4), es[1]);
