@@ -415,7 +415,7 @@ __global__ __launch_bounds__(256, 2) void gather_list_kernel(GatherArgs a, const
     return __builtin_amdgcn_readlane(ofr[mt], i - ofb[mt]);
   };
   constexpr int NPE = 2;               // entries prefetched per lane and list: the first 128 of a tile
-  uint2 pe[2][NPE], pn[2][NPE];        // [list][i]: this tile / the next tile
+  uint2 pe[2][NPE];                    // [list][i]; reloaded for the next tile right after the scatter
   int c0[2] = {0, 0}, c1[2] = {0, 0};  // entry ranges of this tile
   auto entries = [&](uint2 (&d)[NPE], int mt, int e0) __attribute__((always_inline)) {
 #pragma unroll
@@ -455,13 +455,6 @@ __global__ __launch_bounds__(256, 2) void gather_list_kernel(GatherArgs a, const
     // clear this wave's P rows (32 x PT bf16 = 288 uint4)
     for (int e = lane; e < 32 * PT / 8; e += 64) reinterpret_cast<uint4*>(Pw)[e] = make_uint4(0, 0, 0, 0);
     kv.issue(K, V, b, h, H, Tk, min(kt + 1, ntile - 1), kp, cq);   // unconditional: static wait counts
-    int n0[2], n1[2];
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      n0[mt] = off_at(mt, kt + 1);
-      n1[mt] = off_at(mt, kt + 2);
-      entries(pn[mt], mt, n0[mt]);
-    }
     wave_lds_sync();
     // the prefetched entries of both lists, without branches (independent LDS reads batch)
 #pragma unroll
@@ -480,12 +473,13 @@ __global__ __launch_bounds__(256, 2) void gather_list_kernel(GatherArgs a, const
         for (int i = 0; i < 4; ++i) scat(en[i], mt, e0 + 64 * i + lane < c1[mt]);
       }
     }
+    // the next tile's first entries go straight into the registers just consumed
+    // (no copies, so no wait on loads still in flight)
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
-#pragma unroll
-      for (int i = 0; i < NPE; ++i) pe[mt][i] = pn[mt][i];
-      c0[mt] = n0[mt];
-      c1[mt] = n1[mt];
+      c0[mt] = off_at(mt, kt + 1);
+      c1[mt] = off_at(mt, kt + 2);
+      entries(pe[mt], mt, c0[mt]);
     }
     __syncthreads();           // K/V tile committed by all threads; P rows written
     // k_hat += P K, v_hat += P V, E += P 1  (two 16-row tiles share each K/V operand)
