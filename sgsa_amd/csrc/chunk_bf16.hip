@@ -324,8 +324,15 @@ __global__ __launch_bounds__(256) void chunk_state_bf16(
   f4 uu[RTW];
   uint4 nwh[RTW][KS], nwl[RTW][KS], nkt[2][KSM];
   f4 nuu[RTW];
+  float nlogd = 0.f, nlam = 0.f;   // this thread's log-decay / write-strength entries of the next chunk
   auto fetch = [&](int c) __attribute__((always_inline)) {
     const long cidx = (long)bh * NT + c;
+    if (tid < L) nlogd = ws.logd[cidx * L + tid];
+    if (tid < M) {
+      const int t = c * L + samp_t<SP>(tid);
+      nlam = 0.f;
+      if (t < T) nlam = samp_r<SP>(tid) ? alpha[(long)(b * T + t) * H + h] : beta[(long)(b * T + t) * H + h];
+    }
     const uint16_t* Wh = ws.Whi + cidx * M * DP;
     const uint16_t* Wl = ws.Wlo + cidx * M * DP;
     const float* Uc = ws.U + cidx * M * DP;
@@ -349,6 +356,8 @@ __global__ __launch_bounds__(256) void chunk_state_bf16(
     }
   };
   auto take = [&]() __attribute__((always_inline)) {
+    if (tid < L) logd[tid] = nlogd;
+    if (tid < M) lam[tid] = nlam;
 #pragma unroll
     for (int u = 0; u < RTW; ++u) {
       uu[u] = nuu[u];
@@ -365,16 +374,8 @@ __global__ __launch_bounds__(256) void chunk_state_bf16(
   fetch(0);
   for (int c = 0; c < NT; ++c) {
     const long cidx = (long)bh * NT + c;
-    const int t0 = c * L;
-    take();
+    take();   // logd / lam of this chunk into LDS (the previous chunk's readers passed a barrier)
     if (c + 1 < NT) fetch(c + 1);
-    if (tid < L) logd[tid] = ws.logd[cidx * L + tid];
-    if (tid < M) {
-      const int t = t0 + samp_t<SP>(tid);
-      float lm = 0.f;
-      if (t < T) lm = samp_r<SP>(tid) ? alpha[(long)(b * T + t) * H + h] : beta[(long)(b * T + t) * H + h];
-      lam[tid] = lm;
-    }
     // chunk-start state: LDS operand copy and workspace copy (both transposed, hi/lo)
     uint16_t* STh = ws.STh + cidx * DP * DP;
     uint16_t* STl = ws.STl + cidx * DP * DP;
