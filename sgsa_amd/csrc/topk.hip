@@ -88,9 +88,13 @@ struct RowInfo {
   float th0, th1;    // pass B: select s >= th1; collect th0 <= s < th1
 };
 
-__device__ __forceinline__ int score_bin(float s, float iw) {
-  return (int)__builtin_amdgcn_fmed3f(fmaf(s, iw, 128.0f), 0.0f, 255.0f);
+// bin(s) = round(s * iw + 128) clamped to [0, 255], read from the mantissa of
+// 2^23 + x (no float-to-int conversion).  Monotone non-decreasing in s, which is
+// all the exact select needs; NaN lands in bin 0.
+__device__ __forceinline__ uint32_t score_bin_bits(float s, float iw) {
+  return __float_as_uint(__builtin_amdgcn_fmed3f(fmaf(s, iw, 8388736.0f), 8388608.0f, 8388863.0f));
 }
+__device__ __forceinline__ int score_bin(float s, float iw) { return (int)(score_bin_bits(s, iw) & 255u); }
 
 __device__ __forceinline__ float key_to_f32(uint32_t k) {
   return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
@@ -380,9 +384,10 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb, fl
       for (int q = 0; q < 4; ++q) hist[w][rr][255 - 4 * lane - q] = 0;
     }
   };
-  auto bump = [&](int row, uint32_t bin) __attribute__((always_inline)) {
-    if constexpr (C16) atomicAdd(&hist[w][row][bin >> 1], 1u + (bin & 1u) * 0xffffu);   // low / high half
-    else atomicAdd(&hist[w][row][bin], 1u);
+  // bits: score_bin_bits (bin in the low 8 bits)
+  auto bump = [&](int row, uint32_t bits) __attribute__((always_inline)) {
+    if constexpr (C16) atomicAdd(&hist[w][row][(bits & 0xfeu) >> 1], 1u + (bits & 1u) * 0xffffu);   // low / high half
+    else atomicAdd(&hist[w][row][bits & 0xffu], 1u);
   };
 
   // ---- pass A: score-bin histogram -------------------------------------------
@@ -402,7 +407,7 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb, fl
           for (int nt = 0; nt < 4; ++nt) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              if (hrow[e]) bump(4 * lg + e, (uint32_t)score_bin(acc[nt][e], iw[e]));
+              if (hrow[e]) bump(4 * lg + e, score_bin_bits(acc[nt][e], iw[e]));
             }
           }
         } else {
@@ -411,7 +416,7 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb, fl
             const int j = kt * KT + 16 * nt + lr;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              if (hrow[e] && j < nvalid[e]) bump(4 * lg + e, (uint32_t)score_bin(acc[nt][e], iw[e]));
+              if (hrow[e] && j < nvalid[e]) bump(4 * lg + e, score_bin_bits(acc[nt][e], iw[e]));
             }
           }
         }
