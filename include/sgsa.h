@@ -142,6 +142,20 @@ int sgsa_sparse_gather_tiled(int B, int T, int H, int D, int top_k, const void* 
                              int write_mode, float alpha_max, float tau_c, void* k_hat, void* v_hat,
                              void* write_key, float* alpha, void* stream);
 
+/* ---- recurrent form (decode step) -----------------------------------------------
+ * fused_recurrent_sgsa (modelings/sgsa_ops/recurrent.py:138-175, Triton kernel
+ * recurrent_fwd_triton.py:25-145) with the semantics of naive_recurrent_sgsa
+ * (naive.py:34-57): token by token, decay first, both writes read the decayed
+ * state, o_t = S^T q_t.  q, k, v, sparse_k, sparse_v [B,T,H,D] (dtype);
+ * beta, gamma, alpha [B,T,H] fp32; sparse_k / sparse_v / alpha all NULL or all
+ * given; initial_state / final_state [B,H,D,D] fp32 or NULL; out [B,T,H,D]
+ * in dtype.  T = 1 is one decode step.  No workspace. */
+int sgsa_recurrent_fwd(int dtype, int B, int T, int H, int D,
+                       const void* q, const void* k, const void* v,
+                       const float* beta, const float* gamma,
+                       const void* sparse_k, const void* sparse_v, const float* alpha,
+                       const float* initial_state, void* out, float* final_state, void* stream);
+
 /* ---- layer-path building blocks: tile lists ----------------------------------
  * The fused layer (sgsa_layer_fwd, bf16 with D = 128) does not materialise
  * per-row index/score lists: K1 writes, for every 64-row block, every 16-row

@@ -6,6 +6,7 @@ Public entry points mirror FAndromedA/sgsa:
   sparse_retrieve       -- functional form of SparseRetriever.forward
   sgsa_layer_forward    -- retrieval + write gate + chunked state update in one call
   sgsa_layer_retrieve   -- its retrieval half: (write key, v_hat, alpha)
+  fused_recurrent_sgsa  -- token-by-token recurrence (decode step), recurrent.py:138-175
 The compiled library (libsgsa_hip.so) is required; there is no fallback path.
 """
 
@@ -13,11 +14,13 @@ from .ops import ChunkSGSAFunction, chunk_sgsa, chunk_sgsa_fwd
 from .retrieval import (SparseRetriever, gather_gate, gather_lists, score_dump, score_topk, score_topk_lists,
                         sparse_retrieve)
 from .layer import LayerWorkspace, sgsa_layer_forward, sgsa_layer_retrieve
+from .recurrent import fused_recurrent_sgsa
 
 __all__ = [
     "ChunkSGSAFunction",
     "chunk_sgsa",
     "chunk_sgsa_fwd",
+    "fused_recurrent_sgsa",
     "SparseRetriever",
     "score_topk",
     "score_dump",

@@ -139,6 +139,22 @@ static int validate_topk(int dtype, int B, int Tq, int Tk, int H, int D, int top
   return SGSA_OK;
 }
 
+int sgsa_recurrent_fwd(int dtype, int B, int T, int H, int D, const void* q, const void* k, const void* v,
+                       const float* beta, const float* gamma, const void* sparse_k, const void* sparse_v,
+                       const float* alpha, const float* initial_state, void* out, float* final_state, void* stream) {
+  if (int s = check_dtype(dtype)) return s;
+  if (int s = check_dims(B, T, H, D)) return s;
+  REQUIRE(q); REQUIRE(k); REQUIRE(v); REQUIRE(beta); REQUIRE(gamma); REQUIRE(out);
+  const int ns = (sparse_k != nullptr) + (sparse_v != nullptr) + (alpha != nullptr);
+  if (ns != 0 && ns != 3) return fail(SGSA_ERR_INVALID_ARG, "sparse_k, sparse_v and alpha must be given together");
+  sgsa::RecurrentArgs a{};
+  a.dtype = dtype; a.B = B; a.T = T; a.H = H; a.D = D;
+  a.q = q; a.k = k; a.v = v; a.beta = beta; a.gamma = gamma;
+  a.sparse_k = sparse_k; a.sparse_v = sparse_v; a.alpha = alpha;
+  a.initial_state = initial_state; a.out = out; a.final_state = final_state;
+  return hip_status(sgsa::launch_recurrent(a, (hipStream_t)stream), "sgsa_recurrent_fwd");
+}
+
 int sgsa_score_topk_workspace_size(int B, int Tq, int H, size_t* bytes) {
   REQUIRE(bytes);
   if (int s = check_dims(B, Tq, H, 1)) return s;

@@ -32,6 +32,23 @@ size_t chunk_bf16_workspace_bytes(int B, int T, int H, int has_sparse);
 hipError_t launch_chunk_fwd(const ChunkArgs& a, hipStream_t st);
 hipError_t launch_chunk_bf16(const ChunkArgs& a, hipStream_t st);
 
+struct RecurrentArgs {
+  int dtype;
+  int B, T, H, D;
+  const void* q;              // [B,T,H,D]
+  const void* k;
+  const void* v;
+  const float* beta;          // [B,T,H]
+  const float* gamma;
+  const void* sparse_k;       // [B,T,H,D] or nullptr (no sparse write)
+  const void* sparse_v;
+  const float* alpha;         // [B,T,H]
+  const float* initial_state; // [B,H,D,D] fp32 or nullptr
+  void* out;                  // [B,T,H,D] in the input dtype
+  float* final_state;         // [B,H,D,D] fp32 or nullptr
+};
+hipError_t launch_recurrent(const RecurrentArgs& a, hipStream_t st);
+
 struct TopkArgs {
   int dtype;
   int B, Tq, Tk, H, D;

@@ -1,0 +1,69 @@
+"""Drop-in ``fused_recurrent_sgsa`` backed by the gfx950 HIP recurrent kernel.
+
+Same signature and return as modelings/sgsa_ops/recurrent.py:138-175 (the
+function the layer's "recurrent" / "fused_recurrent" backends call,
+modelings/modeling_sgsa.py:570-582), with the semantics of
+naive_recurrent_sgsa (naive.py:34-57).  T = 1 is one decode step: pass the
+previous final state as ``initial_state``.  The final state is float32, as on
+the reference's Triton path (recurrent_fwd_triton.py:121-123); ``use_triton``
+is accepted and ignored; unsupported input raises.
+"""
+
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+
+from . import _abi
+from .ops import _check_layout
+
+Tensor = torch.Tensor
+
+
+def fused_recurrent_sgsa(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    beta: Tensor,
+    gamma: Tensor,
+    sparse_k: Optional[Tensor] = None,
+    sparse_v: Optional[Tensor] = None,
+    alpha: Optional[Tensor] = None,
+    initial_state: Optional[Tensor] = None,
+    output_final_state: bool = False,
+    use_triton: bool = True,
+) -> Tuple[Tensor, Optional[Tensor]]:
+    """q, k, v [B,T,H,D]; beta, gamma [B,T,H]; state [B,H,D,D] (float32 out)."""
+    if not q.is_cuda:
+        raise ValueError("fused_recurrent_sgsa: the SGSA kernels run on a ROCm GPU; got CPU tensors")
+    B, T, H, D = q.shape
+    dev = q.device
+    for name, t in (("k", k), ("v", v)):
+        _check_layout(name, t, (B, T, H, D), dev)
+    for name, t in (("beta", beta), ("gamma", gamma)):
+        _check_layout(name, t, (B, T, H), dev)
+    has_sparse = sparse_k is not None and sparse_v is not None and alpha is not None
+    if has_sparse:
+        _check_layout("sparse_k", sparse_k, (B, T, H, D), dev)
+        _check_layout("sparse_v", sparse_v, (B, T, H, D), dev)
+        _check_layout("alpha", alpha, (B, T, H), dev)
+    dt = q.dtype
+    code = _abi.dtype_code(dt)
+    cast = lambda t: t.to(dt).contiguous()
+    qc, kc, vc = cast(q), cast(k), cast(v)
+    bc = beta.float().contiguous()
+    gc = gamma.float().contiguous()
+    skc = cast(sparse_k) if has_sparse else None
+    svc = cast(sparse_v) if has_sparse else None
+    ac = alpha.float().contiguous() if has_sparse else None
+    h0 = None
+    if initial_state is not None:
+        _check_layout("initial_state", initial_state, (B, H, D, D), dev)
+        h0 = initial_state.float().contiguous()
+    out = torch.empty_like(qc)
+    ht = torch.empty(B, H, D, D, device=dev, dtype=torch.float32) if output_final_state else None
+    _abi.check(_abi.lib().sgsa_recurrent_fwd(
+        code, B, T, H, D, _abi.ptr(qc), _abi.ptr(kc), _abi.ptr(vc), _abi.ptr(bc), _abi.ptr(gc), _abi.ptr(skc),
+        _abi.ptr(svc), _abi.ptr(ac), _abi.ptr(h0), _abi.ptr(out), _abi.ptr(ht), _abi.stream_of(qc)))
+    return out, ht

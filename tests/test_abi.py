@@ -82,6 +82,15 @@ def test_workspace_size_queries():
     (lambda L, p: L.sgsa_layer_fwd(1, 1, 16, 2, 64, 4, 64, p, p, p, p, p, p, p, None, 3, 0.25, 0.1, p, None, p,
                                    1 << 30, None),
      "write_mode"),
+    (lambda L, p: L.sgsa_recurrent_fwd(1, 1, 16, 2, 64, p, p, p, p, p, p, None, p, None, p, None, None),
+     "together"),
+    (lambda L, p: L.sgsa_recurrent_fwd(0, 1, 16, 2, 160, p, p, p, p, p, None, None, None, None, p, None, None),
+     "D=160"),
+    (lambda L, p: L.sgsa_sparse_gather_lists(1, 16, 2, 64, 4, p, p, p, p, p, p, None, 0, 0.25, 0.1, p, p, None, None,
+                                             None),
+     "D == 128"),
+    (lambda L, p: L.sgsa_score_topk_lists(1, 16, 2, 64, 4, p, p, p, p, p, p, p, 16, None),
+     "workspace"),
 ])
 def test_argument_validation(call, needle):
     abi, L = _lib()

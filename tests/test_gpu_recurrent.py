@@ -1,0 +1,101 @@
+"""GPU parity of the recurrent form (K6): fused_recurrent_sgsa / decode steps.
+
+Oracle: oracle/sgsa_oracle.py naive_recurrent_sgsa (fp32 restatement of
+modelings/sgsa_ops/naive.py:34-57).  bf16 runs feed the oracle the
+bf16-rounded inputs.
+"""
+
+import pytest
+import torch
+
+from oracle import sgsa_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+sgsa_amd = pytest.importorskip("sgsa_amd")
+
+
+def _close(got, ref, rel, name=""):
+    got = got.detach().float().cpu()
+    ref = ref.detach().float().cpu()
+    scale = ref.abs().max().clamp_min(1e-12)
+    err = (got - ref).abs().max() / scale
+    assert torch.isfinite(got).all(), f"{name}: non-finite"
+    assert err <= rel, f"{name}: max error {err:.3e} relative to max|ref| {scale:.3e} exceeds {rel:.1e}"
+
+
+def _inputs(B, T, H, D, seed, sparse=True, h0=True):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, T, H, D, generator=g)
+    k = torch.nn.functional.normalize(torch.randn(B, T, H, D, generator=g), dim=-1)
+    v = torch.randn(B, T, H, D, generator=g)
+    beta = torch.sigmoid(torch.randn(B, T, H, generator=g))
+    gamma = torch.exp(torch.nn.functional.logsigmoid(torch.randn(B, T, H, generator=g) + 4.0))
+    sk = torch.nn.functional.normalize(torch.randn(B, T, H, D, generator=g), dim=-1) if sparse else None
+    sv = torch.randn(B, T, H, D, generator=g) if sparse else None
+    al = 0.25 * torch.rand(B, T, H, generator=g) if sparse else None
+    s0 = 0.1 * torch.randn(B, H, D, D, generator=g) if h0 else None
+    return q, k, v, beta, gamma, sk, sv, al, s0
+
+
+@pytest.mark.parametrize("dims,sparse,h0", [
+    ((2, 37, 3, 64), True, True),
+    ((1, 50, 2, 128), True, False),
+    ((2, 23, 2, 40), False, True),
+    ((1, 9, 3, 5), True, True),          # the reference's tiny ragged head dim
+])
+def test_recurrent_fp32_matches_oracle(dev, dims, sparse, h0):
+    B, T, H, D = dims
+    q, k, v, beta, gamma, sk, sv, al, s0 = _inputs(B, T, H, D, seed=1, sparse=sparse, h0=h0)
+    ro, rs = O.naive_recurrent_sgsa(q, k, v, beta, gamma, sk, sv, al, s0, True)
+    d = lambda t: None if t is None else t.to(dev)
+    o, st = sgsa_amd.fused_recurrent_sgsa(d(q), d(k), d(v), d(beta), d(gamma), d(sk), d(sv), d(al), d(s0),
+                                          output_final_state=True)
+    torch.cuda.synchronize()
+    _close(o, ro, 1e-4, "o")
+    _close(st, rs, 1e-4, "final_state")
+    assert st.dtype == torch.float32
+
+
+def test_recurrent_bf16_matches_oracle(dev):
+    B, T, H, D = 2, 64, 4, 128
+    q, k, v, beta, gamma, sk, sv, al, s0 = _inputs(B, T, H, D, seed=2)
+    bf = lambda t: t.to(torch.bfloat16)
+    q, k, v, sk, sv = map(bf, (q, k, v, sk, sv))
+    f = lambda t: t.float()
+    ro, rs = O.naive_recurrent_sgsa(f(q), f(k), f(v), beta, gamma, f(sk), f(sv), al, s0, True)
+    d = lambda t: t.to(dev)
+    o, st = sgsa_amd.fused_recurrent_sgsa(d(q), d(k), d(v), d(beta), d(gamma), d(sk), d(sv), d(al), d(s0),
+                                          output_final_state=True)
+    torch.cuda.synchronize()
+    assert o.dtype == torch.bfloat16
+    _close(o, ro, 2e-2, "o")
+    _close(st, rs, 2e-2, "final_state")
+
+
+def test_decode_steps_equal_one_pass(dev):
+    # T single-token calls carrying the state give the one-pass result bit for bit
+    B, T, H, D = 2, 20, 3, 128
+    q, k, v, beta, gamma, sk, sv, al, s0 = (None if t is None else t.to(dev) for t in _inputs(B, T, H, D, seed=3))
+    o1, s1 = sgsa_amd.fused_recurrent_sgsa(q, k, v, beta, gamma, sk, sv, al, s0, output_final_state=True)
+    st = s0
+    outs = []
+    for t in range(T):
+        sl = slice(t, t + 1)
+        o, st = sgsa_amd.fused_recurrent_sgsa(q[:, sl], k[:, sl], v[:, sl], beta[:, sl], gamma[:, sl], sk[:, sl],
+                                              sv[:, sl], al[:, sl], st, output_final_state=True)
+        outs.append(o)
+    torch.cuda.synchronize()
+    assert torch.equal(torch.cat(outs, 1), o1)
+    assert torch.equal(st, s1)
+
+
+def test_recurrent_agrees_with_chunk_form(dev):
+    # the two kernel families compute the same recurrence
+    B, T, H, D = 1, 200, 2, 128
+    q, k, v, beta, gamma, sk, sv, al, s0 = (None if t is None else t.to(dev) for t in _inputs(B, T, H, D, seed=4))
+    o1, s1 = sgsa_amd.fused_recurrent_sgsa(q, k, v, beta, gamma, sk, sv, al, s0, output_final_state=True)
+    o2, s2 = sgsa_amd.chunk_sgsa(q, k, v, beta, gamma, sk, sv, al, s0, output_final_state=True)
+    torch.cuda.synchronize()
+    _close(o1, o2, 1e-4, "o")
+    _close(s1, s2, 1e-4, "final_state")
