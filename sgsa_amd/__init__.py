@@ -7,6 +7,7 @@ Public entry points mirror FAndromedA/sgsa:
   sgsa_layer_forward    -- retrieval + write gate + chunked state update in one call
   sgsa_layer_retrieve   -- its retrieval half: (write key, v_hat, alpha)
   fused_recurrent_sgsa  -- token-by-token recurrence (decode step), recurrent.py:138-175
+  sgsa_decode_step      -- one generated token: retrieval over the KV cache, gate, recurrent update
 The compiled library (libsgsa_hip.so) is required; there is no fallback path.
 """
 
@@ -15,12 +16,14 @@ from .retrieval import (SparseRetriever, gather_gate, gather_lists, score_dump, 
                         sparse_retrieve)
 from .layer import LayerWorkspace, sgsa_layer_forward, sgsa_layer_retrieve
 from .recurrent import fused_recurrent_sgsa
+from .decode import sgsa_decode_step
 
 __all__ = [
     "ChunkSGSAFunction",
     "chunk_sgsa",
     "chunk_sgsa_fwd",
     "fused_recurrent_sgsa",
+    "sgsa_decode_step",
     "SparseRetriever",
     "score_topk",
     "score_dump",

@@ -1,0 +1,88 @@
+"""One SGSA decode step: the new token's retrieval over the KV cache, its write
+key and gate, and the recurrent state update -- the token-by-token form of
+SGSABlock.forward's attention half (modelings/modeling_sgsa.py:669-684) with
+the recurrent backend (:570-582).
+
+The caller appends the new token's key and value to the cache first; the
+token sits at cache position Tc - 1 and retrieves over keys [0, Tc - 1]
+(causal).  Three C-ABI calls on the current stream: sgsa_score_topk (one
+query row, q_offset = Tc - 1), sgsa_sparse_gather (weights, k_hat / write
+key, v_hat, alpha) and sgsa_recurrent_fwd (T = 1).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from typing import Tuple
+
+import torch
+
+from . import _abi
+from .recurrent import fused_recurrent_sgsa
+
+Tensor = torch.Tensor
+
+_WRITE_MODES = {"direct": 0, "residual": 1}
+
+
+def sgsa_decode_step(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    q_ret: Tensor,
+    beta: Tensor,
+    gamma: Tensor,
+    budget_logits: Tensor,
+    k_cache: Tensor,
+    v_cache: Tensor,
+    state: Tensor,
+    top_k: int,
+    write_mode: str = "direct",
+    alpha_max: float = 0.25,
+    tau_c: float = 0.1,
+) -> Tuple[Tensor, Tensor]:
+    """q, k, v, q_ret [B,1,H,D]; beta, gamma, budget_logits [B,1,H];
+    k_cache, v_cache [B,Tc,H,D] (ending with this token); state [B,H,D,D] fp32.
+
+    Returns (o [B,1,H,D] in q.dtype, new state [B,H,D,D] fp32).
+    """
+    if not q.is_cuda:
+        raise ValueError("sgsa_decode_step: the SGSA kernels run on a ROCm GPU; got CPU tensors")
+    B, one, H, D = q.shape
+    if one != 1:
+        raise ValueError(f"sgsa_decode_step takes one token per sequence, got T={one}")
+    Tc = k_cache.shape[1]
+    if k_cache.shape != (B, Tc, H, D) or v_cache.shape != (B, Tc, H, D):
+        raise ValueError("k_cache / v_cache must be [B, Tc, H, D] like q")
+    if write_mode not in _WRITE_MODES:
+        raise ValueError(f"write_mode must be one of {sorted(_WRITE_MODES)}")
+    dt = q.dtype
+    dev = q.device
+    kk = min(int(top_k), Tc)
+    rc, kc, vc, kn = (t.to(dt).contiguous() for t in (q_ret, k_cache, v_cache, k))
+    L = _abi.lib()
+    # 1. top-k of the new query over the cache (causal: position Tc - 1)
+    idx = torch.empty(B, H, 1, kk, device=dev, dtype=torch.int32)
+    sc = torch.empty(B, H, 1, kk, device=dev, dtype=torch.float32)
+    top2 = torch.empty(B, H, 1, 2, device=dev, dtype=torch.float32)
+    cnt = torch.empty(B, H, 1, device=dev, dtype=torch.int32)
+    nb = ctypes.c_size_t()
+    _abi.check(L.sgsa_score_topk_workspace_size(B, 1, H, ctypes.byref(nb)))
+    tws = torch.empty(nb.value, device=dev, dtype=torch.uint8)
+    _abi.check(L.sgsa_score_topk(_abi.dtype_code(dt), B, 1, Tc, H, D, kk, 1, Tc - 1, math.sqrt(D), 0,
+                                 _abi.ptr(rc), _abi.ptr(kc), _abi.ptr(idx), _abi.ptr(sc), _abi.ptr(top2),
+                                 _abi.ptr(cnt), None, 0, _abi.ptr(tws), nb.value, _abi.stream_of(rc)))
+    # 2. weights, k_hat / write key, v_hat and the gate for that row
+    mode = _WRITE_MODES[write_mode]
+    wk = torch.empty(B, 1, H, D, device=dev, dtype=dt)
+    vh = torch.empty_like(wk)
+    al = torch.empty(B, 1, H, device=dev, dtype=torch.float32)
+    bud = budget_logits.float().contiguous()
+    _abi.check(L.sgsa_sparse_gather(
+        _abi.dtype_code(dt), B, 1, Tc, H, D, kk, Tc - 1, _abi.ptr(kc), _abi.ptr(vc), _abi.ptr(kn), _abi.ptr(idx),
+        _abi.ptr(sc), _abi.ptr(top2), _abi.ptr(cnt), _abi.ptr(bud), mode, float(alpha_max), float(tau_c), 64, 8,
+        _abi.ptr(wk if mode == 0 else None), _abi.ptr(vh), _abi.ptr(wk if mode == 1 else None), _abi.ptr(al),
+        None, None, None, 0, _abi.stream_of(kc)))
+    # 3. the recurrent update for this token
+    return fused_recurrent_sgsa(q, k, v, beta, gamma, wk, vh, al, state, output_final_state=True)

@@ -99,3 +99,26 @@ def test_recurrent_agrees_with_chunk_form(dev):
     torch.cuda.synchronize()
     _close(o1, o2, 1e-4, "o")
     _close(s1, s2, 1e-4, "final_state")
+
+
+@pytest.mark.parametrize("dtype,tol,D", [(torch.float32, 1e-4, 64), (torch.bfloat16, 2e-2, 128)])
+@pytest.mark.parametrize("write_mode", ["direct", "residual"])
+def test_decode_steps_match_the_layer_oracle(dev, dtype, tol, D, write_mode):
+    # the last 6 tokens generated one at a time (retrieval over the growing cache,
+    # gate, recurrent update) reproduce the full-sequence layer at those positions
+    B, T, H, k, n = 2, 200, 2, 32, 6
+    x = O.make_inputs(B, T, H, D, dtype=dtype, seed=8)
+    args = lambda sl: (x["q_f32"][:, sl], x["k_f32"][:, sl], x["v_f32"][:, sl], x["q_f32"][:, sl],
+                       x["beta"][:, sl], x["gamma"][:, sl], x["budget"][:, sl])
+    full = O.sgsa_layer_forward(*args(slice(0, T)), k, write_mode=write_mode)
+    prev = O.sgsa_layer_forward(*args(slice(0, T - n)), k, write_mode=write_mode)
+    st = prev["final_state"].to(dev)
+    d = lambda t: t.to(dev)
+    for t in range(T - n, T):
+        sl = slice(t, t + 1)
+        o, st = sgsa_amd.sgsa_decode_step(d(x["q"][:, sl]), d(x["k"][:, sl]), d(x["v"][:, sl]), d(x["q"][:, sl]),
+                                          d(x["beta"][:, sl]), d(x["gamma"][:, sl]), d(x["budget"][:, sl]),
+                                          d(x["k"][:, :t + 1]), d(x["v"][:, :t + 1]), st, k, write_mode=write_mode)
+        torch.cuda.synchronize()
+        _close(o, full["o"][:, sl], tol, f"o[{t}]")
+    _close(st, full["final_state"], tol, "final_state")
