@@ -187,7 +187,7 @@ __global__ __launch_bounds__(256) void key_norm_max_kernel(const X* __restrict__
 // FB = true: re-runs exactly the flagged blocks with 8-bit radix digit passes
 // over the order-preserving keys (up to 4 passes + emit).
 template <typename X, bool DUMP, bool C16, bool TOP2, bool FB, bool LIST>
-__global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb, float mscale) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LIST && !FB ? 3 : 1))) void score_topk_kernel(TopkArgs a, int nqb, float mscale) {
   constexpr int P = KTile<X>::PITCH;
   constexpr bool BF = sizeof(X) == 2;
   constexpr int NQF = BF ? DP / 32 : DP / 4;          // q fragments per lane
@@ -386,7 +386,9 @@ __global__ __launch_bounds__(256) void score_topk_kernel(TopkArgs a, int nqb, fl
   };
   // bits: score_bin_bits (bin in the low 8 bits)
   auto bump = [&](int row, uint32_t bits) __attribute__((always_inline)) {
-    if constexpr (C16) atomicAdd(&hist[w][row][(bits & 0xfeu) >> 1], 1u + (bits & 1u) * 0xffffu);   // low / high half
+    // C16: word bin >> 1, half bin & 1; the increment's shift 16 (bin & 1) equals
+    // (bits << 4) mod 32, and the shift instruction reads only those 5 bits
+    if constexpr (C16) atomicAdd(&hist[w][row][__builtin_amdgcn_ubfe(bits, 1, 7)], 1u << ((bits << 4) & 31u));
     else atomicAdd(&hist[w][row][bits & 0xffu], 1u);
   };
 
