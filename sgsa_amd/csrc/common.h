@@ -93,5 +93,9 @@ __device__ __forceinline__ int popc64(uint64_t x) { return __popcll(x); }
 
 // Wave ballot straight from the predicate's lane mask (no int round trip).
 __device__ __forceinline__ uint64_t ballot64(bool p) { return __builtin_amdgcn_ballot_w64(p); }
+// Number of set bits of m below this lane.
+__device__ __forceinline__ uint32_t lane_rank(uint64_t m) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
 
 }  // namespace sgsa

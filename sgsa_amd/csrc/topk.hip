@@ -561,34 +561,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LIST && !FB
       m1[e] = fmaxf(m1[e], so);
     }
   };
-  // LIST emission of one score: every candidate (s >= th0: selected or in the
-  // threshold bin) gets the next entry of the wave's list in lane order; those
-  // in the threshold bin also go to the row's scratch list with the entry index.
+  // LIST entries: {score, row_in_wave << 8 | key_in_tile}.  Every candidate
+  // (s >= th0: selected or in the threshold bin) gets the next entry of the
+  // wave's list in lane order; the position is a ballot + mbcnt against the
+  // wave-uniform running offset.
   const uint32_t rk0 = ((uint32_t)(4 * lg) << 8) | (uint32_t)lr;
-  const uint64_t grp_mask = 0xffffull << (16 * lg);   // the 16 lanes of this lane's row group
   float th0e[4];                                       // th0 with dead rows folded in (+inf)
 #pragma unroll
   for (int e = 0; e < 4; ++e) th0e[e] = live[e] ? th0[e] : INFINITY;
-  // Candidate test = one compare; the entry position = ballot + mbcnt against the
-  // wave-uniform running offset; the threshold-bin mask is formed on scalar masks.
-  auto emit_list = [&](int e, int nt, float s, bool cand, auto cols) __attribute__((always_inline)) {
+  // direct emission (radix fallback launch: no threshold bin)
+  auto emit_list = [&](int e, int nt, float s, bool cand) __attribute__((always_inline)) {
     const uint64_t cb = ballot64(cand);
-    const uint32_t pos = min((uint32_t)woff + __builtin_amdgcn_mbcnt_hi((uint32_t)(cb >> 32),
-                                                                        __builtin_amdgcn_mbcnt_lo((uint32_t)cb, 0u)),
-                             (uint32_t)tlcap - 1u);
+    const uint32_t pos = min((uint32_t)woff + lane_rank(cb), (uint32_t)tlcap - 1u);
     if (cand) tl[pos] = make_uint2(__float_as_uint(s), rk0 + (uint32_t)((e << 8) + 16 * nt));
     woff = __builtin_amdgcn_readfirstlane(woff + __popcll(cb));
-    if constexpr (!decltype(cols)::value) return;
-    const uint64_t cm = cb & ballot64(s < th1[e]);
-    if (cm != 0) {   // wave-uniform
-      const uint64_t gm = cm & grp_mask;
-      if (cand && s < th1[e]) {
-        const int slot = colc[e] + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(gm >> 32),
-                                                                  __builtin_amdgcn_mbcnt_lo((uint32_t)gm, 0u));
-        if (slot < TOPK_CAP) scratch[(long)(grow0 + e) * TOPK_CAP + slot] = make_uint2(__float_as_uint(s), pos);
-      }
-      colc[e] += __popcll(gm);
-    }
   };
   // running top-2 (m1 >= m2): med3 gives the new second before m1 moves
   auto top2_fast = [&](int e, float x) __attribute__((always_inline)) {
@@ -596,8 +582,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LIST && !FB
     m1[e] = fmaxf(m1[e], x);
   };
   if constexpr (!FB && LIST) {
+    // A tile's candidates are first gathered in LDS -- the wave's histogram area,
+    // idle between pass A and the resolve, holds a whole tile (16 rows x 64 keys)
+    // -- and then written to the wave's list with full-wave stores.  Bit 31 of
+    // a buffered entry marks a threshold-bin candidate; the flush also gives it
+    // a slot in its row's scratch list (an LDS counter per row), so the slot
+    // order within a row is arbitrary and the resolve breaks ties by position.
+    static_assert(16 * HWA >= 2 * 16 * KT, "a tile's candidates must fit the histogram area");
+    uint2* ebuf = reinterpret_cast<uint2*>(&hist[w][0][0]);
+    const long srow0 = (long)bh * Tq + r0 + 16 * w;   // global row of the wave's row 0
+    if (lane < 16) rowcnt[w][lane][1] = 0;
+    int tcnt = 0;
+    auto emit_buf = [&](int e, int nt, float s, bool cand) __attribute__((always_inline)) {
+      const uint64_t cb = ballot64(cand);
+      if (cand)
+        ebuf[(uint32_t)tcnt + lane_rank(cb)] =
+            make_uint2(__float_as_uint(s), rk0 + (uint32_t)((e << 8) + 16 * nt) + (s < th1[e] ? 0x80000000u : 0u));
+      tcnt = __builtin_amdgcn_readfirstlane(tcnt + __popcll(cb));
+    };
     sweep([&](int kt, f4* acc) __attribute__((always_inline)) {
+      // A row holds at most top_k + TOPK_CAP candidates of which at most TOPK_CAP
+      // in its threshold bin, so neither list can fill up; the bounds below only
+      // keep one tile's writes inside the regions whatever the inputs.
+      woff = min(woff, tlcap - 16 * KT);
       if (lane == 0) toff[kt] = woff;
+      tcnt = 0;
       if ((kt + 1) * KT <= minvalid) {
         // full tile: every key is valid for every live row
 #pragma unroll
@@ -605,7 +614,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LIST && !FB
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const float s = acc[nt][e];
-            emit_list(e, nt, s, s >= th0e[e], std::true_type{});
+            emit_buf(e, nt, s, s >= th0e[e]);
             top2_fast(e, s);
           }
         }
@@ -617,11 +626,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LIST && !FB
           for (int e = 0; e < 4; ++e) {
             const bool ok = live[e] && j < nvalid[e];
             const float s = acc[nt][e];
-            emit_list(e, nt, s, s >= th0e[e] && j < nvalid[e], std::true_type{});
+            emit_buf(e, nt, s, s >= th0e[e] && j < nvalid[e]);
             top2_fast(e, ok ? s : -FLT_MAX);
           }
         }
       }
+      // flush, two chunks of 64 per step (LDS accesses of one wave complete in order)
+      auto flush_one = [&](bool ok, uint2 ent, int c) __attribute__((always_inline)) {
+        const bool col = ok && (ent.y >> 31) != 0u;
+        ent.y &= 0x7fffffffu;
+        const uint32_t pos = (uint32_t)(woff + c + lane);
+        if (ok) tl[pos] = ent;
+        if (col) {
+          const int r = (int)(ent.y >> 8);   // row in wave
+          const int slot = (int)atomicAdd((uint32_t*)&rowcnt[w][r][1], 1u);
+          if (slot < TOPK_CAP) scratch[(srow0 + r) * TOPK_CAP + slot] = make_uint2(ent.x, pos);
+        }
+      };
+      for (int c0 = 0; c0 < tcnt; c0 += 128) {
+        const bool ok0 = c0 + lane < tcnt, ok1 = c0 + 64 + lane < tcnt;
+        const uint2 e0 = ok0 ? ebuf[c0 + lane] : make_uint2(0u, 0u);
+        const uint2 e1 = ok1 ? ebuf[c0 + 64 + lane] : make_uint2(0u, 0u);
+        flush_one(ok0, e0, c0);
+        flush_one(ok1, e1, c0 + 64);
+      }
+      woff = __builtin_amdgcn_readfirstlane(woff + tcnt);
     });
   } else if constexpr (!FB) {
     sweep([&](int kt, f4* acc) __attribute__((always_inline)) {
@@ -662,7 +691,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LIST && !FB
           const uint32_t eqm = (uint32_t)(ballot64(eq) >> (16 * lg)) & 0xffffu;
           sel = sel || (inb && (km > pfx[e] || (eq && eqc[e] + __popc(eqm & lower) < need[e])));
           eqc[e] += __popc(eqm);
-          if constexpr (LIST) emit_list(e, nt, s, sel, std::false_type{});
+          if constexpr (LIST) emit_list(e, nt, s, sel);
           else emit(e, 16 * nt + lr, j, s, sel, col);
           top2_update(e, ok, s);
         }
@@ -676,7 +705,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LIST && !FB
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       rowcnt[w][4 * lg + e][0] = outc[e];
-      rowcnt[w][4 * lg + e][1] = colc[e];
+      if (!LIST || FB) rowcnt[w][4 * lg + e][1] = colc[e];
       run1[w][4 * lg + e] = outc[e];
     }
   }
@@ -725,16 +754,46 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LIST && !FB
       wave_lds_sync();
       if (cnt == rneed) break;
     }
-    int eqn = 0;
+    // Keys equal to the threshold key: the rneed with the smallest idx win (idx
+    // is the key index, or in LIST mode the entry position, which grows with the
+    // key index within a row).  Only when more are equal than needed does a radix
+    // select over ~idx find the cut; the slot order of the scratch list is free.
+    uint32_t neq = 0;
+#pragma unroll
+    for (int m = 0; m < CAPL; ++m) neq += (uint32_t)__popcll(ballot64(64 * m + lane < n && (key[m] & rm) == rp));
+    uint32_t ip = 0, im = 0;
+    if (neq > rneed) {
+      uint32_t need2 = rneed;
+      for (int sh = 24; sh >= 0; sh -= 8) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) h256[4 * lane + q] = 0;
+        wave_lds_sync();
+#pragma unroll
+        for (int m = 0; m < CAPL; ++m) {
+          const uint32_t ik = ~(uint32_t)idx[m];
+          if (64 * m + lane < n && (key[m] & rm) == rp && (ik & im) == ip) atomicAdd(&h256[(ik >> sh) & 255u], 1u);
+        }
+        wave_lds_sync();
+        uint32_t c[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) c[q] = h256[255 - 4 * lane - q];
+        int bin;
+        uint32_t above, cnt;
+        find_bin(c, lane, need2, bin, above, cnt);
+        ip |= (uint32_t)bin << sh;
+        im |= 0xffu << sh;
+        need2 -= above;
+        wave_lds_sync();
+        if (cnt == need2) break;
+      }
+    }
     const uint64_t below = (1ull << lane) - 1ull;
 #pragma unroll
     for (int m = 0; m < CAPL; ++m) {
       const bool valid = 64 * m + lane < n;
       const uint32_t km = key[m] & rm;
       const bool eq = valid && km == rp;
-      const uint64_t eb = ballot64(eq);
-      const int rank = __popcll(eb & below);
-      const bool sel = valid && (km > rp || (eq && eqn + rank < (int)rneed));
+      const bool sel = valid && (km > rp || (eq && (neq <= rneed || ((~(uint32_t)idx[m]) & im) >= ip)));
       const uint64_t sb = ballot64(sel);
       if constexpr (LIST) {
         if (valid && !sel && idx[m] >= 0 && idx[m] < tlcap) tl[idx[m]].x = 0xff800000u;   // -inf: weight 0
@@ -746,7 +805,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LIST && !FB
         }
       }
       base += __popcll(sb);
-      eqn += __popcll(eb);
     }
     if (lane == 0) rowcnt[w][rr][0] = base;
   }
