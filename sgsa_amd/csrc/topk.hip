@@ -877,6 +877,472 @@ __global__ __launch_bounds__(256) void sort_rows_kernel(int32_t* __restrict__ in
   }
 }
 
+// ---------------------------------------------------------------------------
+// K1, tile-list form (layer path: bf16, D = 128, top-2 required).
+//
+// The same selection as score_topk_kernel<..., LIST = true>, with pass A laid
+// out so that no K tile goes through LDS.  The K tiles are re-read from L2 for
+// every 64-row block; staging them (global -> VGPR -> LDS -> VGPR, two barriers
+// a tile) for 16 rows per wave cost more than the histogram arithmetic.  In
+// pass A wave w owns keys [16w, 16w+16) of every 64-key tile for all 64 rows of
+// the block: its 16 keys are the MFMA A operand, loaded straight into registers
+// one tile ahead, and the block's q rows are the B operand, resident in
+// registers.  The product C[key][row] puts 4 keys of 4 rows (16g + lr) in each
+// lane and all four waves bump the same 64 row histograms.  Each product sums
+// the same 32 dims per instruction as score_topk_kernel, so the fp32 scores
+// are identical.  MFMA row rho of the A operand holds key rho/4 + 4 (rho%4).
+//
+// Pass B keeps score_topk_kernel's layout (wave w: rows 16w.., K tile in LDS):
+// every score of a row is then in one wave, which keeps the emission buffer,
+// its flush to the tile list and the top-2 wave-private.
+// A block with a row whose threshold bin overflows is flagged for the radix
+// fallback launch of score_topk_kernel<..., FB = true, LIST = true>, which
+// writes the same lists.
+// ---------------------------------------------------------------------------
+template <bool C16>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void score_topk_tiles_kernel(
+    TopkArgs a, int nqb, float mscale) {
+  constexpr int HW = C16 ? NBIN / 2 : NBIN;   // histogram words per row
+  constexpr int CAPL = TOPK_CAP / 64;
+  constexpr int PB = DP + 8;                  // LDS pitch of a K row (272 B keeps 16 B alignment)
+  __shared__ __align__(16) uint32_t hist[64][HW];   // rows of the block; pass B: emission buffers
+  __shared__ RowInfo rinfo[4][16];
+  __shared__ int colcnt[4][16];                     // threshold-bin candidates collected per row
+  __shared__ float qnorm[4][16];
+  __shared__ __align__(16) uint16_t ks[KT * PB];    // pass B: the K tile
+
+  const int BH = a.B * a.H;
+  const int bid = blockIdx.x;
+  const int bh = bid % BH;
+  const int qb = nqb - 1 - bid / BH;   // heaviest (latest) query blocks first
+  const int b = bh / a.H, h = bh % a.H;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lr = lane & 15, lg = lane >> 4;
+  const int r0 = qb * QB;
+  const int Tq = a.Tq, Tk = a.Tk, H = a.H;
+  const uint16_t* kb = reinterpret_cast<const uint16_t*>(a.k);
+  const int topk = a.top_k;
+
+  // B operand: q^T of the block's rows; lane holds row r0 + 16g + lr, dims 32s + 8lg + [0, 8)
+  bf16x8 qf[4][4];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int qr = r0 + 16 * g + lr;
+    const uint16_t* qp = reinterpret_cast<const uint16_t*>(a.q) + ((long)(b * Tq + (qr < Tq ? qr : 0)) * H + h) * DP;
+    float qn2 = 0.f;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      u16x8 raw;
+      if (qr < Tq) raw = *reinterpret_cast<const u16x8*>(qp + 32 * s + 8 * lg);
+      else raw = (u16x8){0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float x = bf16_to_f32(raw[j]);
+        qn2 = fmaf(x, x, qn2);
+      }
+      qf[g][s] = __builtin_bit_cast(bf16x8, raw);
+    }
+    qn2 += __shfl_xor(qn2, 16, 64);
+    qn2 += __shfl_xor(qn2, 32, 64);
+    if (g == w && lg == 0) qnorm[w][lr] = sqrtf(qn2);
+  }
+
+  // the lane's rows r0 + 16g + lr
+  int nvalid[4];
+  bool live[4];
+  int minvalid = 0x7fffffff;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int qr = r0 + 16 * g + lr;
+    live[g] = qr < Tq;
+    int nv = Tk;
+    if (a.causal) nv = min(Tk, qr + a.q_offset + 1);
+    if (nv < 0) nv = 0;
+    nvalid[g] = live[g] ? nv : 0;
+    if (live[g]) minvalid = min(minvalid, nvalid[g]);
+  }
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) minvalid = min(minvalid, __shfl_xor(minvalid, o, 64));
+  int kend = Tk;
+  if (a.causal) kend = min(Tk, min(Tq, r0 + QB) - 1 + a.q_offset + 1);
+  const int ntile = (kend + KT - 1) / KT;
+
+  // A operand: the wave's 16 keys of a tile; MFMA row lr holds key lr/4 + 4 (lr%4)
+  const int krow = (lr >> 2) + 4 * (lr & 3);
+  bf16x8 kf[4];
+  auto kload = [&](int kt) __attribute__((always_inline)) {
+    const int j = kt * KT + 16 * w + krow;
+    const bool okj = j < Tk;
+    const uint16_t* p = kb + ((long)(b * Tk + (okj ? j : 0)) * H + h) * DP + 8 * lg;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      u16x8 raw = *reinterpret_cast<const u16x8*>(p + 32 * s);
+      if (!okj) raw = (u16x8){0, 0, 0, 0, 0, 0, 0, 0};
+      kf[s] = __builtin_bit_cast(bf16x8, raw);
+    }
+  };
+  // fn(kt, acc): acc[g][i] = score of row r0 + 16g + lr against key kt*64 + 16w + lg + 4i
+  auto sweep = [&](auto&& fn) __attribute__((always_inline)) {
+    kload(0);
+    for (int kt = 0; kt < ntile; ++kt) {
+      f4 acc[4];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        f4 c = f4_zero();
+#pragma unroll
+        for (int s = 0; s < 4; ++s) c = mma_bf16(kf[s], qf[g][s], c);
+        acc[g] = c * mscale + 0.0f;   // fold -0.0 onto +0.0
+      }
+      if (kt + 1 < ntile) kload(kt + 1);
+      fn(kt, acc);
+    }
+  };
+
+  // row set-up (wave w: rows r0 + 16w + lane)
+  __syncthreads();   // qnorm visible
+  float kmx2 = lane < KNCH ? a.kmax[(long)bh * KNCH + lane] : 0.f;
+  const float kmx = sqrtf(wave_max(kmx2));
+  if (lane < 16) {
+    const int qr = r0 + 16 * w + lane;
+    int nv = 0;
+    if (qr < Tq) nv = a.causal ? max(0, min(Tk, qr + a.q_offset + 1)) : Tk;
+    RowInfo ri;
+    const float bound = qnorm[w][lane] * kmx * fabsf(mscale) * 1.001f;
+    ri.iw = (bound > 0.f && bound < FLT_MAX) ? 128.0f / bound : 0.f;
+    ri.bstar = -1;
+    ri.need = min(topk, nv);
+    ri.mode = (nv <= topk) ? SELECT_ALL : BIN_ALL;
+    ri.pfx = 0; ri.msk = 0; ri.done = 1; ri.th0 = -INFINITY; ri.th1 = -INFINITY;
+    rinfo[w][lane] = ri;
+    colcnt[w][lane] = 0;
+  }
+  for (int i = tid; i < 64 * HW; i += 256) (&hist[0][0])[i] = 0;
+  __syncthreads();
+
+  float iw[4];
+  int mode[4];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) { iw[g] = rinfo[g][lr].iw; mode[g] = rinfo[g][lr].mode; }
+
+  // ---- pass A: block-shared row histograms ------------------------------------
+  {
+    int mine = 0;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) mine |= (live[g] && mode[g] != SELECT_ALL);
+    if (__syncthreads_or(mine)) {
+      bool hrow[4];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) hrow[g] = live[g] && mode[g] != SELECT_ALL;
+      auto bump = [&](int row, uint32_t bits) __attribute__((always_inline)) {
+        // C16: word bin >> 1, half bin & 1; the shift 16 (bin & 1) is (bits << 4) mod 32
+        if constexpr (C16) atomicAdd(&hist[row][__builtin_amdgcn_ubfe(bits, 1, 7)], 1u << ((bits << 4) & 31u));
+        else atomicAdd(&hist[row][bits & 0xffu], 1u);
+      };
+      sweep([&](int kt, f4* acc) __attribute__((always_inline)) {
+        if ((kt + 1) * KT <= minvalid) {
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (hrow[g]) bump(16 * g + lr, score_bin_bits(acc[g][i], iw[g]));
+          }
+        } else {
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int j = kt * KT + 16 * w + lg + 4 * i;
+              if (hrow[g] && j < nvalid[g]) bump(16 * g + lr, score_bin_bits(acc[g][i], iw[g]));
+            }
+          }
+        }
+      });
+      __syncthreads();
+      for (int rr = 0; rr < 16; ++rr) {
+        RowInfo ri = rinfo[w][rr];
+        if (ri.mode == SELECT_ALL) continue;
+        const uint32_t* hr = hist[16 * w + rr];
+        uint32_t c[4];
+        if constexpr (C16) {
+          const uint32_t w0 = hr[127 - 2 * lane], w1 = hr[126 - 2 * lane];
+          c[0] = w0 >> 16; c[1] = w0 & 0xffffu; c[2] = w1 >> 16; c[3] = w1 & 0xffffu;
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) c[q] = hr[255 - 4 * lane - q];
+        }
+        int bin;
+        uint32_t above, cnt;
+        find_bin(c, lane, (uint32_t)ri.need, bin, above, cnt);
+        if (lane == 0) {
+          ri.bstar = bin;
+          ri.need -= (int)above;
+          if (cnt == (uint32_t)ri.need) ri.mode = BIN_ALL;
+          else if (cnt <= (uint32_t)TOPK_CAP) ri.mode = COLLECT;
+          else ri.mode = RADIX;
+          rinfo[w][rr] = ri;
+        }
+      }
+    }
+    __syncthreads();
+    int overflow = 0;
+    if (lane < 16) overflow = rinfo[w][lane].mode == RADIX;
+    overflow = __syncthreads_or(overflow);
+    if (tid == 0) a.flags[bid] = overflow;
+    if (overflow) return;   // block-uniform; the fallback launch redoes this block
+  }
+
+  // ---- thresholds for pass B ---------------------------------------------------
+  if (lane < 16) {
+    RowInfo ri = rinfo[w][lane];
+    float t0 = -INFINITY, t1 = -INFINITY;
+    if (ri.mode != SELECT_ALL) {
+      const float lo_b = ri.bstar > 0 ? bin_lower_edge(ri.bstar, ri.iw) : -INFINITY;
+      const float hi_b = ri.bstar < NBIN - 1 ? bin_lower_edge(ri.bstar + 1, ri.iw) : INFINITY;
+      if (ri.mode == BIN_ALL) { t0 = lo_b; t1 = lo_b; }
+      else { t0 = lo_b; t1 = hi_b; }   // COLLECT
+    }
+    ri.th0 = t0; ri.th1 = t1;
+    rinfo[w][lane] = ri;
+  }
+  __syncthreads();
+
+  // ---- pass B: wave w takes rows r0 + 16w + 4lg + e against the K tile in LDS --
+  // (every score of a row is then in one wave, which keeps the emission, the
+  // flush and the top-2 wave-private).  A operand: the wave's row group of qf.
+  bf16x8 qa[4] = {qf[0][0], qf[0][1], qf[0][2], qf[0][3]};
+#pragma unroll
+  for (int g = 1; g < 4; ++g) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) qa[s] = g == w ? qf[g][s] : qa[s];
+  }
+  float th0e[4], th1[4], m1[4], m2[4];
+  int nv4[4];
+  bool live4[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int rr = 4 * lg + e, qr = r0 + 16 * w + rr;
+    live4[e] = qr < Tq;
+    int nv = Tk;
+    if (a.causal) nv = min(Tk, qr + a.q_offset + 1);
+    if (nv < 0) nv = 0;
+    nv4[e] = live4[e] ? nv : 0;
+    th0e[e] = live4[e] ? rinfo[w][rr].th0 : INFINITY;   // dead rows take nothing
+    th1[e] = rinfo[w][rr].th1;
+    m1[e] = -FLT_MAX; m2[e] = -FLT_MAX;
+  }
+  uint4 pf[4];   // the next tile: 64 keys x 16 vectors of 16 B over 256 threads
+  auto issue = [&](int kt) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = tid + 256 * i, r = e >> 4, cv = e & 15, j = kt * KT + r;
+      pf[i] = make_uint4(0, 0, 0, 0);
+      if (j < Tk) pf[i] = *reinterpret_cast<const uint4*>(kb + ((long)(b * Tk + j) * H + h) * DP + cv * 8);
+    }
+  };
+  auto sweepB = [&](auto&& fn) __attribute__((always_inline)) {
+    issue(0);
+    for (int kt = 0; kt < ntile; ++kt) {
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int e = tid + 256 * i;
+        *reinterpret_cast<uint4*>(ks + (e >> 4) * PB + (e & 15) * 8) = pf[i];
+      }
+      __syncthreads();
+      if (kt + 1 < ntile) issue(kt + 1);
+      f4 acc[4];
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+        f4 c = f4_zero();
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const uint4 raw = *reinterpret_cast<const uint4*>(&ks[(16 * nt + lr) * PB + 32 * s + 8 * lg]);
+          c = mma_bf16(qa[s], __builtin_bit_cast(bf16x8, raw), c);
+        }
+        acc[nt] = c * mscale + 0.0f;   // fold -0.0 onto +0.0
+      }
+      fn(kt, acc);
+    }
+  };
+  const int tlcap = 16 * (topk + TOPK_CAP);
+  const long lreg = ((long)bh * nqb + qb) * 4 + w;
+  uint2* tl = a.tl_list + lreg * tlcap;
+  int32_t* toff = a.tl_off + lreg * (a.tl_ntmax + 1);
+  const long srow0 = (long)bh * Tq + r0 + 16 * w;    // global row of the wave's row 0
+  uint2* scratch = a.scratch;
+  // A tile's candidates are gathered in LDS -- the wave's 16 histogram rows hold
+  // 16 rows x 64 keys -- and written with full-wave stores.  Bit 31 of a
+  // buffered entry marks a threshold-bin candidate; the flush also gives it a
+  // slot in its row's scratch list (an LDS counter per row), so the slot order
+  // within a row is arbitrary and the resolve breaks ties by list position.
+  static_assert(16 * HW >= 2 * 16 * KT, "a tile's candidates must fit the wave's histogram rows");
+  uint2* ebuf = reinterpret_cast<uint2*>(&hist[16 * w][0]);
+  const uint32_t rk0 = ((uint32_t)(4 * lg) << 8) | (uint32_t)lr;
+  int woff = 0, tcnt = 0;
+  auto emit_buf = [&](int e, int nt, float sc, bool cand) __attribute__((always_inline)) {
+    const uint64_t cb = ballot64(cand);
+    if (cand)
+      ebuf[(uint32_t)tcnt + lane_rank(cb)] =
+          make_uint2(__float_as_uint(sc), rk0 + (uint32_t)((e << 8) + 16 * nt) + (sc < th1[e] ? 0x80000000u : 0u));
+    tcnt = __builtin_amdgcn_readfirstlane(tcnt + __popcll(cb));
+  };
+  auto top2_fast = [&](int e, float x) __attribute__((always_inline)) {
+    m2[e] = __builtin_amdgcn_fmed3f(m1[e], m2[e], x);
+    m1[e] = fmaxf(m1[e], x);
+  };
+  sweepB([&](int kt, f4* acc) __attribute__((always_inline)) {
+    // A row holds at most top_k + TOPK_CAP candidates, so the list cannot fill
+    // up; the bound only keeps one tile's writes inside the region whatever the inputs.
+    woff = min(woff, tlcap - 16 * KT);
+    if (lane == 0) toff[kt] = woff;
+    tcnt = 0;
+    if ((kt + 1) * KT <= minvalid) {
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float sc = acc[nt][e];
+          emit_buf(e, nt, sc, sc >= th0e[e]);
+          top2_fast(e, sc);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+        const int j = kt * KT + 16 * nt + lr;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float sc = acc[nt][e];
+          emit_buf(e, nt, sc, sc >= th0e[e] && j < nv4[e]);
+          top2_fast(e, live4[e] && j < nv4[e] ? sc : -FLT_MAX);
+        }
+      }
+    }
+    // flush, two chunks of 64 per step (LDS accesses of one wave complete in order)
+    auto flush_one = [&](bool ok, uint2 ent, int c) __attribute__((always_inline)) {
+      const bool col = ok && (ent.y >> 31) != 0u;
+      ent.y &= 0x7fffffffu;
+      const uint32_t pos = (uint32_t)(woff + c + lane);
+      if (ok) tl[pos] = ent;
+      if (col) {
+        const int r = (int)(ent.y >> 8);   // row in wave
+        const int slot = (int)atomicAdd((uint32_t*)&colcnt[w][r], 1u);
+        if (slot < TOPK_CAP) scratch[(srow0 + r) * TOPK_CAP + slot] = make_uint2(ent.x, pos);
+      }
+    };
+    for (int c0 = 0; c0 < tcnt; c0 += 128) {
+      const bool ok0 = c0 + lane < tcnt, ok1 = c0 + 64 + lane < tcnt;
+      const uint2 e0 = ok0 ? ebuf[c0 + lane] : make_uint2(0u, 0u);
+      const uint2 e1 = ok1 ? ebuf[c0 + 64 + lane] : make_uint2(0u, 0u);
+      flush_one(ok0, e0, c0);
+      flush_one(ok1, e1, c0 + 64);
+    }
+    woff = __builtin_amdgcn_readfirstlane(woff + tcnt);
+  });
+  if (lane == 0) toff[ntile] = woff;
+
+  // ---- resolve the collected rows of the wave ----------------------------------
+  uint32_t* h256 = &hist[16 * w][0];   // 256 words of the wave's histogram rows
+  for (int rr = 0; rr < 16; ++rr) {
+    const RowInfo ri = rinfo[w][rr];
+    if (ri.mode != COLLECT) continue;
+    const long row = srow0 + rr;
+    const int n = min(colcnt[w][rr], TOPK_CAP);
+    uint32_t key[CAPL];
+    int idx[CAPL];
+#pragma unroll
+    for (int m = 0; m < CAPL; ++m) {
+      const int p = 64 * m + lane;
+      key[m] = 0; idx[m] = 0;
+      if (p < n) {
+        const uint2 v = scratch[row * TOPK_CAP + p];
+        key[m] = f32_order_key(__uint_as_float(v.x));
+        idx[m] = (int)v.y;
+      }
+    }
+    uint32_t rp = 0, rm = 0;
+    uint32_t rneed = (uint32_t)ri.need;
+    for (int sh = 24; sh >= 0; sh -= 8) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) h256[4 * lane + q] = 0;
+      wave_lds_sync();
+#pragma unroll
+      for (int m = 0; m < CAPL; ++m) {
+        if (64 * m + lane < n && (key[m] & rm) == rp) atomicAdd(&h256[(key[m] >> sh) & 255u], 1u);
+      }
+      wave_lds_sync();
+      uint32_t c[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) c[q] = h256[255 - 4 * lane - q];
+      int bin;
+      uint32_t above, cnt;
+      find_bin(c, lane, rneed, bin, above, cnt);
+      rp |= (uint32_t)bin << sh;
+      rm |= 0xffu << sh;
+      rneed -= above;
+      wave_lds_sync();
+      if (cnt == rneed) break;
+    }
+    // equal keys at the threshold: the rneed with the smallest list position
+    // (positions grow with the key index within a row)
+    uint32_t neq = 0;
+#pragma unroll
+    for (int m = 0; m < CAPL; ++m) neq += (uint32_t)__popcll(ballot64(64 * m + lane < n && (key[m] & rm) == rp));
+    uint32_t ip = 0, im = 0;
+    if (neq > rneed) {
+      uint32_t need2 = rneed;
+      for (int sh = 24; sh >= 0; sh -= 8) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) h256[4 * lane + q] = 0;
+        wave_lds_sync();
+#pragma unroll
+        for (int m = 0; m < CAPL; ++m) {
+          const uint32_t ik = ~(uint32_t)idx[m];
+          if (64 * m + lane < n && (key[m] & rm) == rp && (ik & im) == ip) atomicAdd(&h256[(ik >> sh) & 255u], 1u);
+        }
+        wave_lds_sync();
+        uint32_t c[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) c[q] = h256[255 - 4 * lane - q];
+        int bin;
+        uint32_t above, cnt;
+        find_bin(c, lane, need2, bin, above, cnt);
+        ip |= (uint32_t)bin << sh;
+        im |= 0xffu << sh;
+        need2 -= above;
+        wave_lds_sync();
+        if (cnt == need2) break;
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < CAPL; ++m) {
+      const bool valid = 64 * m + lane < n;
+      const uint32_t km = key[m] & rm;
+      const bool eq = valid && km == rp;
+      const bool sel = valid && (km > rp || (eq && (neq <= rneed || ((~(uint32_t)idx[m]) & im) >= ip)));
+      if (valid && !sel && idx[m] >= 0 && idx[m] < tlcap) tl[idx[m]].x = 0xff800000u;   // -inf: weight 0
+    }
+  }
+
+  // ---- top-2 over the row's 16 lanes, counts -----------------------------------
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) {
+      const float b1 = __shfl_xor(m1[e], o, 64), b2 = __shfl_xor(m2[e], o, 64);
+      const float hi = fmaxf(m1[e], b1), lo = fmaxf(fminf(m1[e], b1), fmaxf(m2[e], b2));
+      m1[e] = hi; m2[e] = lo;
+    }
+    if (lr == 0 && live4[e]) {
+      const long rowg = srow0 + 4 * lg + e;
+      if (a.counts) a.counts[rowg] = min(topk, nv4[e]);
+      if (a.split) a.split[rowg] = 0;
+      a.top2[2 * rowg] = m1[e];
+      a.top2[2 * rowg + 1] = m2[e];
+    }
+  }
+}
+
 size_t topk_workspace_bytes(int B, int Tq, int H) {
   const size_t nqb = (Tq + QB - 1) / QB;
   return (size_t)B * H * Tq * TOPK_CAP * sizeof(uint2) + (((size_t)B * H * nqb * sizeof(int) + 255) & ~(size_t)255) +
@@ -925,11 +1391,14 @@ hipError_t launch_score_topk(const TopkArgs& a0, hipStream_t st) {
   if (a.tl_list != nullptr) {   // layer path: tile lists (bf16, top-2 required)
     a.tl_ntmax = (a.Tk + KT - 1) / KT;
     if (a.dtype != DT_BF16 || !t2) return hipErrorInvalidValue;
+    const bool regs = a.D == DP;   // K fragments straight into registers (D = 128)
     if (c16) {
-      score_topk_kernel<bf16_t, false, true, true, false, true><<<grid, 256, 0, st>>>(a, nqb, ms);
+      if (regs) score_topk_tiles_kernel<true><<<grid, 256, 0, st>>>(a, nqb, ms);
+      else score_topk_kernel<bf16_t, false, true, true, false, true><<<grid, 256, 0, st>>>(a, nqb, ms);
       score_topk_kernel<bf16_t, false, true, true, true, true><<<grid, 256, 0, st>>>(a, nqb, ms);
     } else {
-      score_topk_kernel<bf16_t, false, false, true, false, true><<<grid, 256, 0, st>>>(a, nqb, ms);
+      if (regs) score_topk_tiles_kernel<false><<<grid, 256, 0, st>>>(a, nqb, ms);
+      else score_topk_kernel<bf16_t, false, false, true, false, true><<<grid, 256, 0, st>>>(a, nqb, ms);
       score_topk_kernel<bf16_t, false, false, true, true, true><<<grid, 256, 0, st>>>(a, nqb, ms);
     }
     return hipGetLastError();
