@@ -93,6 +93,19 @@ __device__ __forceinline__ int popc64(uint64_t x) { return __popcll(x); }
 
 // Wave ballot straight from the predicate's lane mask (no int round trip).
 __device__ __forceinline__ uint64_t ballot64(bool p) { return __builtin_amdgcn_ballot_w64(p); }
+// Inclusive prefix sum over the 64 lanes: row_shr 1/2/4/8 within each row of 16
+// lanes (lanes past the row edge read 0), then row_bcast 15 adds the last lane
+// of rows 0 and 2 to rows 1 and 3 and row_bcast 31 adds lane 31 to rows 2 and 3.
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x) {
+  int v = (int)x;
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, true);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, true);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, true);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, true);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);
+  return (uint32_t)v;
+}
 // Number of set bits of m below this lane.
 __device__ __forceinline__ uint32_t lane_rank(uint64_t m) {
   return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));

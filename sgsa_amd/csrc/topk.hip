@@ -123,16 +123,11 @@ __device__ __forceinline__ void wave_lds_sync() {
 __device__ __forceinline__ void find_bin(const uint32_t (&c)[4], int lane, uint32_t need, int& bin, uint32_t& above,
                                          uint32_t& cnt) {
   const uint32_t loc = c[0] + c[1] + c[2] + c[3];
-  uint32_t inc = loc;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const uint32_t n = __shfl_up(inc, o, 64);
-    if (lane >= o) inc += n;
-  }
+  const uint32_t inc = wave_incl_scan(loc);
   const uint32_t exc = inc - loc;
   const bool hit = exc < need && need <= inc;
   const uint64_t bal = ballot64(hit);
-  const int src = bal ? __ffsll((unsigned long long)bal) - 1 : 0;
+  const int src = bal ? (int)__builtin_ctzll(bal) : 0;   // wave-uniform
   int b = 0;
   uint32_t ab = 0, ct = 0;
   if (hit) {
@@ -147,9 +142,9 @@ __device__ __forceinline__ void find_bin(const uint32_t (&c)[4], int lane, uint3
       if (ct == 0) cum += c[q];
     }
   }
-  bin = __shfl(b, src, 64);
-  above = __shfl(ab, src, 64);
-  cnt = __shfl(ct, src, 64);
+  bin = __builtin_amdgcn_readlane(b, src);
+  above = (uint32_t)__builtin_amdgcn_readlane((int)ab, src);
+  cnt = (uint32_t)__builtin_amdgcn_readlane((int)ct, src);
 }
 
 }  // namespace
@@ -731,9 +726,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LIST && !FB
         idx[m] = (int)v.y;
       }
     }
-    uint32_t rp = 0, rm = 0;
+    // every collected key lies in [key(th0), key(th1) - 1]: the bytes those two
+    // share are the same for all of them and need no pass
+    const uint32_t klo = f32_order_key(ri.th0), dif = klo ^ (f32_order_key(ri.th1) - 1u);
+    uint32_t rm = 0;
+    int sh = 24;
+    while (sh > 0 && (dif >> sh) == 0u) { rm |= 0xffu << sh; sh -= 8; }
+    uint32_t rp = klo & rm;
     uint32_t rneed = (uint32_t)ri.need;
-    for (int sh = 24; sh >= 0; sh -= 8) {
+    for (; sh >= 0; sh -= 8) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) h256[4 * lane + q] = 0;
       wave_lds_sync();
@@ -1260,9 +1261,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void s
         idx[m] = (int)v.y;
       }
     }
-    uint32_t rp = 0, rm = 0;
+    // every collected key lies in [key(th0), key(th1) - 1]: the bytes those two
+    // share are the same for all of them and need no pass
+    const uint32_t klo = f32_order_key(ri.th0), dif = klo ^ (f32_order_key(ri.th1) - 1u);
+    uint32_t rm = 0;
+    int sh = 24;
+    while (sh > 0 && (dif >> sh) == 0u) { rm |= 0xffu << sh; sh -= 8; }
+    uint32_t rp = klo & rm;
     uint32_t rneed = (uint32_t)ri.need;
-    for (int sh = 24; sh >= 0; sh -= 8) {
+    for (; sh >= 0; sh -= 8) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) h256[4 * lane + q] = 0;
       wave_lds_sync();
