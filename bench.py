@@ -278,7 +278,7 @@ def main() -> int:
     f_score = B * H * T * (T + 1) * D               # causal score GEMM, one pass
     f_chunk = B * H * ((T + 63) // 64) * 23.77e6     # chunk contractions (K3 + K5 + K4)
     gather_kernel = "gather_list_kernel" if args.gather == "tiled" else "sparse_gather_kernel"
-    topk_kernel = "score_topk_kernel"
+    topk_kernel = "score_topk_tiles_kernel" if args.gather == "tiled" else "score_topk_kernel"
     rooflines = {
         "score_topk": {"kernel": f"{topk_kernel} (K1)", "bound": "mfma",
                        "achieved": round(f_score / (stage_ms["score_topk"] / 1000.0) / 1e12, 2),
