@@ -15,6 +15,9 @@ behaviour (FAndromedA/sgsa, paths relative to the repository root):
 * ``token_topk_retrieval``  -- modelings/modeling_sgsa.py:407-474, token_only
                                mode :113-142, diagnostics :361-405
 * ``write_key`` / ``compute_alpha`` -- modelings/modeling_sgsa.py:543-552, :497-504
+* ``rms_norm`` / ``gated_mlp`` / ``sgsa_model_forward`` -- the causal LM around the
+                               layer, modelings/modeling_sgsa.py:634-749 (RMSNorm and
+                               GatedMLP as restated in hybrid_dense_delta_topk.py:94-117)
 * ``topk_kv_reuse_attention`` -- modelings/hybrid_dense_delta_topk.py:330-358
                                (V-only gather, ``finfo.min`` masking, no valid mask)
 * ``make_inputs``           -- the seeded synthetic inputs of the benchmark configs
@@ -30,7 +33,11 @@ How each function is pinned (tests/test_oracle.py):
 * top-k: brute force with Python ``sorted`` on tiny rows with ties and -0.0,
   causality, the t<k row counts and the padded-slot convention;
 * retrieval/diagnostics/gate: explicit Python loops on tiny inputs, sums of
-  weights, k_hat parallel/orthogonal novelty limits, alpha range and clip.
+  weights, k_hat parallel/orthogonal novelty limits, alpha range and clip;
+* model: RMSNorm and the SwiGLU MLP against scalar loops; a model with no
+  layers is lm_head(norm(embedding + position)); one layer with zeroed o_proj
+  and MLP leaves the residual stream unchanged, and with zeroed MLP equals the
+  stream plus o_proj of the layer oracle's output.
 """
 
 from __future__ import annotations
@@ -430,6 +437,71 @@ def sgsa_layer_forward(
                                      f(initial_state), True)
     return {"o": o, "final_state": st, "write_key": wk, "v_hat": ret["v_hat"],
             "alpha": alpha, "retrieval": ret}
+
+
+# ---------------------------------------------------------------------------
+# The causal LM around the layer (SGSABlock / SGSAForCausalLM)
+# ---------------------------------------------------------------------------
+
+def rms_norm(x: Tensor, weight: Tensor, eps: float) -> Tensor:
+    """x * rsqrt(mean(x^2) + eps) * weight: the fla-core RMSNorm that modeling_sgsa.py:40
+    imports, as the reference restates it in modelings/hybrid_dense_delta_topk.py:94-103."""
+    return x * torch.rsqrt(x.pow(2).mean(dim=-1, keepdim=True) + eps) * weight
+
+
+def gated_mlp(x: Tensor, w_gate: Tensor, w_up: Tensor, w_down: Tensor) -> Tensor:
+    """down(silu(gate x) * up x): fla-core GatedMLP with SwiGLU (modeling_sgsa.py:651-657), as
+    restated in modelings/hybrid_dense_delta_topk.py:106-117."""
+    return (F.silu(x @ w_gate.T) * (x @ w_up.T)) @ w_down.T
+
+
+def sgsa_model_forward(params: Dict[str, Tensor], input_ids: Tensor, *, num_layers: int, num_heads: int,
+                       top_k: int, eps: float = 1e-6, write_mode: str = "direct", alpha_max: float = 0.25,
+                       tau_c: float = 0.1, sparse_output_lambda: float = 0.0,
+                       act_dtype: Optional[torch.dtype] = None) -> Tensor:
+    """Logits of SGSAForCausalLM.forward (modelings/modeling_sgsa.py:735-749) in fp32.
+
+    ``params`` uses the parameter names of sgsa_amd.model.SGSAForCausalLM, which follow
+    the reference's modules: embedding + learned position embedding (:739), per block
+    (:669-709) RMSNorm, q/k/v/q_ret projections, the gates of SGSAStateLayer
+    (beta = sigmoid(.).clamp_min(1e-4), gamma = sigmoid(.), budget logits; :584-585,
+    :501), the token_only retrieval and state update (``sgsa_layer_forward``), o_proj,
+    the optional sparse output (:689-692), the residual MLP (:695), then the final
+    RMSNorm and lm_head (:746).
+
+    ``act_dtype`` (e.g. bfloat16) rounds every activation a model in that dtype stores
+    -- each projection, norm, MLP product and residual sum -- while the arithmetic
+    stays fp32, so that a low-precision model is compared on the inputs it actually
+    feeds each layer.
+    """
+    P = {k: v.float() for k, v in params.items()}
+    r = (lambda x: x) if act_dtype is None else (lambda x: x.to(act_dtype).float())
+    B, T = input_ids.shape
+    h = r(P["embed_tokens.weight"][input_ids] + P["pos_embed.weight"][:T][None])
+    C = h.shape[-1]
+    H, D = num_heads, C // num_heads
+    for i in range(num_layers):
+        w = lambda n: P[f"layers.{i}.{n}"]
+        n = r(rms_norm(h, w("input_norm.weight"), eps))
+        q = r(n @ w("q_proj.weight").T).view(B, T, H, D)
+        k = r(n @ w("k_proj.weight").T).view(B, T, H, D)
+        v = r(n @ w("v_proj.weight").T).view(B, T, H, D)
+        q_ret = r(n @ w("q_ret_proj.weight").T).view(B, T, H, D)
+        beta = torch.sigmoid(r(n @ w("beta_proj.weight").T + w("beta_proj.bias"))).clamp_min(1e-4)
+        gamma = torch.sigmoid(r(n @ w("gamma_proj.weight").T + w("gamma_proj.bias")))
+        budget = r(n @ w("budget_proj.weight").T + w("budget_proj.bias"))
+        lay = sgsa_layer_forward(q, k, v, q_ret, beta, gamma, budget, top_k, write_mode=write_mode,
+                                 alpha_max=alpha_max, tau_c=tau_c)
+        out = r(r(lay["o"]).reshape(B, T, C) @ w("o_proj.weight").T)
+        if sparse_output_lambda > 0:
+            sp = r(r(lay["v_hat"]).reshape(B, T, C) @ w("sparse_out_proj.weight").T)
+            out = r(out + r(sparse_output_lambda * sp))
+        h = r(h + out)
+        m = r(rms_norm(h, w("post_attn_norm.weight"), eps))
+        gate, up = r(m @ w("mlp.gate_proj.weight").T), r(m @ w("mlp.up_proj.weight").T)
+        h = r(h + r(r(r(F.silu(gate)) * up) @ w("mlp.down_proj.weight").T))
+    head = P.get("lm_head.weight", P["embed_tokens.weight"])
+    return r(r(rms_norm(h, P["norm.weight"], eps)) @ head.T)
 
 
 # ---------------------------------------------------------------------------

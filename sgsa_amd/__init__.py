@@ -8,6 +8,7 @@ Public entry points mirror FAndromedA/sgsa:
   sgsa_layer_retrieve   -- its retrieval half: (write key, v_hat, alpha)
   fused_recurrent_sgsa  -- token-by-token recurrence (decode step), recurrent.py:138-175
   sgsa_decode_step      -- one generated token: retrieval over the KV cache, gate, recurrent update
+  SGSAForCausalLM       -- the causal LM around the layer, modeling_sgsa.py:634-767 (token_only, forward)
 The compiled library (libsgsa_hip.so) is required; there is no fallback path.
 """
 
@@ -17,6 +18,7 @@ from .retrieval import (SparseRetriever, gather_gate, gather_lists, score_dump, 
 from .layer import LayerWorkspace, sgsa_layer_forward, sgsa_layer_retrieve
 from .recurrent import fused_recurrent_sgsa
 from .decode import sgsa_decode_step
+from .model import SGSABlock, SGSAConfig, SGSAForCausalLM
 
 __all__ = [
     "ChunkSGSAFunction",
@@ -34,4 +36,7 @@ __all__ = [
     "sgsa_layer_forward",
     "sgsa_layer_retrieve",
     "LayerWorkspace",
+    "SGSAConfig",
+    "SGSABlock",
+    "SGSAForCausalLM",
 ]

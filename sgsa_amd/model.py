@@ -1,0 +1,191 @@
+"""The SGSA causal LM around the layer kernels: SGSABlock and SGSAForCausalLM.
+
+Mirrors modelings/modeling_sgsa.py:634-767 (SGSABlock, SGSAForCausalLM) for the
+token_only retrieval mode with the chunked state backend:
+
+  h   = embed(ids) + pos_embed(positions)                            (:739-743)
+  per block (:669-709):
+    n = RMSNorm(h);  q, k, v, q_ret = proj(n) as [B,T,H,D]
+    beta  = sigmoid(beta_proj(n)).clamp_min(1e-4);  gamma = sigmoid(gamma_proj(n))   (:584-585)
+    attended = SGSA layer(q, k, v, q_ret, beta, gamma, budget_proj(n))  -- K1, K2, K3-K5
+    h = h + o_proj(attended) [+ lambda * sparse_out_proj(v_hat)]
+    h = h + down(silu(gate(m)) * up(m)),  m = RMSNorm(h)
+  logits = lm_head(RMSNorm(h))   (lm_head tied to the embedding by default)
+
+The layer core runs in the HIP library (sgsa_layer_forward); the projections,
+norms and the MLP are plain GEMMs and elementwise ops left to PyTorch
+(rocBLAS / hipBLASLt).  RMSNorm and GatedMLP are the fla-core modules the
+reference imports (modeling_sgsa.py:40-41); their arithmetic is the in-tree
+restatement of modelings/hybrid_dense_delta_topk.py:94-117.  Forward only.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Dict, Optional
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from .layer import LayerWorkspace, sgsa_layer_forward, sgsa_layer_retrieve
+from .ops import chunk_sgsa
+
+Tensor = torch.Tensor
+
+
+@dataclass
+class SGSAConfig:
+    """The fields of modelings/modeling_sgsa.py:47-78 that the token_only path reads."""
+
+    vocab_size: int = 32000
+    hidden_size: int = 256
+    intermediate_size: int = 512
+    num_hidden_layers: int = 2
+    num_attention_heads: int = 4
+    num_kv_heads: int = 4
+    max_position_embeddings: int = 2048
+    dropout: float = 0.0
+    layer_norm_eps: float = 1e-6
+    pad_token_id: int = 0
+    top_k: int = 16
+    retrieval_mode: str = "token_only"
+    sgsa_write_mode: str = "direct"   # direct | residual
+    alpha_max: float = 0.25
+    tau_c: float = 0.1
+    sparse_output_lambda: float = 0.0
+    tie_word_embeddings: bool = True
+    chunk_size: int = 64
+
+    @property
+    def head_dim(self) -> int:
+        if self.hidden_size % self.num_attention_heads != 0:
+            raise ValueError("hidden_size must be divisible by num_attention_heads")
+        return self.hidden_size // self.num_attention_heads
+
+
+class RMSNorm(nn.Module):
+    """x * rsqrt(mean(x^2) + eps) * weight, evaluated in fp32."""
+
+    def __init__(self, hidden_size: int, eps: float) -> None:
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(hidden_size))
+        self.eps = eps
+
+    def forward(self, x: Tensor) -> Tensor:
+        xf = x.float()
+        y = xf * torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + self.eps)
+        return (y * self.weight.float()).to(x.dtype)
+
+
+class GatedMLP(nn.Module):
+    """down(silu(gate(x)) * up(x))."""
+
+    def __init__(self, hidden_size: int, intermediate_size: int) -> None:
+        super().__init__()
+        self.gate_proj = nn.Linear(hidden_size, intermediate_size, bias=False)
+        self.up_proj = nn.Linear(hidden_size, intermediate_size, bias=False)
+        self.down_proj = nn.Linear(intermediate_size, hidden_size, bias=False)
+
+    def forward(self, x: Tensor) -> Tensor:
+        return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
+
+
+class SGSABlock(nn.Module):
+    def __init__(self, config: SGSAConfig) -> None:
+        super().__init__()
+        if config.retrieval_mode != "token_only":
+            raise ValueError("only retrieval_mode='token_only' runs on the SGSA kernels")
+        if config.num_kv_heads != config.num_attention_heads:
+            raise ValueError("the SGSA block uses one key/value head per query head")
+        if config.sgsa_write_mode not in ("direct", "residual"):
+            raise ValueError("sgsa_write_mode must be 'direct' or 'residual'")
+        if config.dropout != 0.0:
+            raise ValueError("dropout is a training feature; the forward here is inference only")
+        self.config = config
+        H, D, C = config.num_attention_heads, config.head_dim, config.hidden_size
+        self.num_heads, self.head_dim = H, D
+        self.input_norm = RMSNorm(C, config.layer_norm_eps)
+        self.post_attn_norm = RMSNorm(C, config.layer_norm_eps)
+        self.q_proj = nn.Linear(C, H * D, bias=False)
+        self.k_proj = nn.Linear(C, H * D, bias=False)
+        self.v_proj = nn.Linear(C, H * D, bias=False)
+        self.o_proj = nn.Linear(C, C, bias=False)
+        self.q_ret_proj = nn.Linear(C, H * D, bias=False)
+        self.sparse_out_proj = nn.Linear(C, C, bias=False)
+        # SGSAStateLayer's gates (modeling_sgsa.py:480-482)
+        self.beta_proj = nn.Linear(C, H, bias=True)
+        self.gamma_proj = nn.Linear(C, H, bias=True)
+        self.budget_proj = nn.Linear(C, H, bias=True)
+        self.mlp = GatedMLP(C, config.intermediate_size)
+        self._ws = LayerWorkspace()
+
+    def forward(self, h: Tensor) -> Tensor:
+        cfg = self.config
+        B, T, C = h.shape
+        H, D = self.num_heads, self.head_dim
+        n = self.input_norm(h)
+        q = self.q_proj(n).view(B, T, H, D)
+        k = self.k_proj(n).view(B, T, H, D)
+        v = self.v_proj(n).view(B, T, H, D)
+        q_ret = self.q_ret_proj(n).view(B, T, H, D)
+        beta = torch.sigmoid(self.beta_proj(n).float()).clamp_min(1e-4)
+        gamma = torch.sigmoid(self.gamma_proj(n).float())
+        budget = self.budget_proj(n).float()
+        if cfg.sparse_output_lambda > 0:
+            wk, vh, al = sgsa_layer_retrieve(q_ret, k, v, budget, cfg.top_k, cfg.sgsa_write_mode, cfg.alpha_max,
+                                             cfg.tau_c, workspace=self._ws)
+            att, _ = chunk_sgsa(q, k, v, beta, gamma, wk, vh, al)
+        else:
+            att, _ = sgsa_layer_forward(q, k, v, q_ret, beta, gamma, budget, cfg.top_k,
+                                        write_mode=cfg.sgsa_write_mode, alpha_max=cfg.alpha_max, tau_c=cfg.tau_c,
+                                        output_final_state=False, workspace=self._ws)
+        out = self.o_proj(att.reshape(B, T, C))
+        if cfg.sparse_output_lambda > 0:
+            out = out + cfg.sparse_output_lambda * self.sparse_out_proj(vh.reshape(B, T, C))
+        h = h + out
+        return h + self.mlp(self.post_attn_norm(h))
+
+
+class SGSAForCausalLM(nn.Module):
+    def __init__(self, config: SGSAConfig) -> None:
+        super().__init__()
+        self.config = config
+        self.embed_tokens = nn.Embedding(config.vocab_size, config.hidden_size, padding_idx=config.pad_token_id)
+        self.pos_embed = nn.Embedding(config.max_position_embeddings, config.hidden_size)
+        self.layers = nn.ModuleList([SGSABlock(config) for _ in range(config.num_hidden_layers)])
+        self.norm = RMSNorm(config.hidden_size, config.layer_norm_eps)
+        self.lm_head = nn.Linear(config.hidden_size, config.vocab_size, bias=False)
+        if config.tie_word_embeddings:
+            self.lm_head.weight = self.embed_tokens.weight
+
+    def init_weights(self, std: float = 0.02, qk_std: Optional[float] = None, generator=None) -> None:
+        """Normal(0, std) for every Linear / Embedding weight, zero biases (modeling_sgsa.py:727-733).
+
+        qk_std, if given, replaces std for q_proj, k_proj and q_ret_proj.  With the
+        reference's std = 0.02 at hidden size C the keys have |k|^2 ~ 0.0004 C D, and
+        the delta-rule transition 1 - beta |k|^2 leaves the unit disc once that exceeds
+        ~4 (C = 1024, D = 128 gives ~52): the state then grows without bound, in the
+        reference as here.  qk_std = 1 / sqrt(C D) keeps |k| ~ 1.
+        """
+        with torch.no_grad():
+            for name, p in self.named_parameters():
+                if name.endswith("bias"):
+                    p.zero_()
+                elif p.dim() == 1:   # norm weights
+                    p.fill_(1.0)
+                else:
+                    s = std
+                    if qk_std is not None and any(t in name for t in ("q_proj", "k_proj", "q_ret_proj")):
+                        s = qk_std
+                    p.copy_(torch.randn(p.shape, generator=generator, dtype=torch.float32) * s)
+
+    def forward(self, input_ids: Tensor) -> Dict[str, Tensor]:
+        B, T = input_ids.shape
+        if T > self.config.max_position_embeddings:
+            raise ValueError("sequence length exceeds max_position_embeddings")
+        pos = torch.arange(T, device=input_ids.device)
+        h = self.embed_tokens(input_ids) + self.pos_embed(pos)[None]
+        for layer in self.layers:
+            h = layer(h)
+        return {"logits": self.lm_head(self.norm(h))}

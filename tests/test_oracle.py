@@ -282,3 +282,87 @@ def test_make_inputs_shapes_and_rounding():
     assert torch.equal(x["q"].float(), x["q_f32"])
     n = (x["k_ret_f32"].norm(dim=-1) > 4).sum()
     assert int(n) == 2 * round(0.01 * 300) and int(n) > 0
+
+
+# --- the causal LM around the layer ------------------------------------------
+
+def test_rms_norm_and_mlp_by_scalar_loops():
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(3, 5, generator=g, dtype=torch.float64)
+    w = torch.randn(5, generator=g, dtype=torch.float64)
+    y = O.rms_norm(x, w, 1e-6)
+    for i in range(3):
+        ms = sum(float(x[i, j]) ** 2 for j in range(5)) / 5
+        for j in range(5):
+            assert abs(float(y[i, j]) - float(x[i, j]) / math.sqrt(ms + 1e-6) * float(w[j])) < 1e-12
+    wg, wu, wd = (torch.randn(s, generator=g, dtype=torch.float64) for s in ((4, 5), (4, 5), (5, 4)))
+    m = O.gated_mlp(x, wg, wu, wd)
+    for i in range(3):
+        hid = []
+        for r in range(4):
+            a = sum(float(wg[r, j]) * float(x[i, j]) for j in range(5))
+            b = sum(float(wu[r, j]) * float(x[i, j]) for j in range(5))
+            hid.append(a / (1.0 + math.exp(-a)) * b)
+        for c in range(5):
+            assert abs(float(m[i, c]) - sum(float(wd[c, r]) * hid[r] for r in range(4))) < 1e-12
+
+
+def _model_params(L, C, H, V, Tmax, I, g):
+    P = {"embed_tokens.weight": torch.randn(V, C, generator=g) * 0.5,
+         "pos_embed.weight": torch.randn(Tmax, C, generator=g) * 0.5,
+         "norm.weight": 1.0 + 0.1 * torch.randn(C, generator=g)}
+    for i in range(L):
+        p = f"layers.{i}."
+        for n in ("q_proj", "k_proj", "v_proj", "q_ret_proj"):
+            P[p + n + ".weight"] = torch.randn(C, C, generator=g) / C
+        P[p + "o_proj.weight"] = torch.randn(C, C, generator=g) / math.sqrt(C)
+        P[p + "sparse_out_proj.weight"] = torch.randn(C, C, generator=g) / math.sqrt(C)
+        for n in ("beta_proj", "gamma_proj", "budget_proj"):
+            P[p + n + ".weight"] = torch.randn(H, C, generator=g) / math.sqrt(C)
+            P[p + n + ".bias"] = torch.randn(H, generator=g)
+        P[p + "input_norm.weight"] = 1.0 + 0.1 * torch.randn(C, generator=g)
+        P[p + "post_attn_norm.weight"] = 1.0 + 0.1 * torch.randn(C, generator=g)
+        P[p + "mlp.gate_proj.weight"] = torch.randn(I, C, generator=g) / math.sqrt(C)
+        P[p + "mlp.up_proj.weight"] = torch.randn(I, C, generator=g) / math.sqrt(C)
+        P[p + "mlp.down_proj.weight"] = torch.randn(C, I, generator=g) / math.sqrt(I)
+    return P
+
+
+def test_model_without_layers_is_head_of_embeddings():
+    g = torch.Generator().manual_seed(7)
+    P = _model_params(0, 8, 2, 11, 16, 12, g)
+    ids = torch.randint(0, 11, (2, 5), generator=g)
+    got = O.sgsa_model_forward(P, ids, num_layers=0, num_heads=2, top_k=3)
+    for b in range(2):
+        for t in range(5):
+            h = P["embed_tokens.weight"][ids[b, t]] + P["pos_embed.weight"][t]
+            want = O.rms_norm(h, P["norm.weight"], 1e-6) @ P["embed_tokens.weight"].T   # tied head
+            torch.testing.assert_close(got[b, t], want)
+
+
+def test_model_residual_structure():
+    g = torch.Generator().manual_seed(8)
+    P = _model_params(1, 8, 2, 11, 16, 12, g)
+    ids = torch.randint(0, 11, (1, 7), generator=g)
+    head = lambda h: O.rms_norm(h, P["norm.weight"], 1e-6) @ P["embed_tokens.weight"].T
+    h0 = P["embed_tokens.weight"][ids] + P["pos_embed.weight"][:7][None]
+    # o_proj and the MLP's down projection zeroed: the block is the identity
+    Z = dict(P)
+    Z["layers.0.o_proj.weight"] = torch.zeros(8, 8)
+    Z["layers.0.mlp.down_proj.weight"] = torch.zeros(8, 12)
+    torch.testing.assert_close(O.sgsa_model_forward(Z, ids, num_layers=1, num_heads=2, top_k=3), head(h0))
+    # only the MLP zeroed: residual + o_proj(layer output) with the block's own projections
+    Z = dict(P)
+    Z["layers.0.mlp.down_proj.weight"] = torch.zeros(8, 12)
+    n = O.rms_norm(h0, P["layers.0.input_norm.weight"], 1e-6)
+    pr = lambda name: (n @ P[f"layers.0.{name}.weight"].T).view(1, 7, 2, 4)
+    gate = lambda name: n @ P[f"layers.0.{name}.weight"].T + P[f"layers.0.{name}.bias"]
+    lay = O.sgsa_layer_forward(pr("q_proj"), pr("k_proj"), pr("v_proj"), pr("q_ret_proj"),
+                               torch.sigmoid(gate("beta_proj")).clamp_min(1e-4), torch.sigmoid(gate("gamma_proj")),
+                               gate("budget_proj"), 3)
+    h1 = h0 + lay["o"].reshape(1, 7, 8) @ P["layers.0.o_proj.weight"].T
+    torch.testing.assert_close(O.sgsa_model_forward(Z, ids, num_layers=1, num_heads=2, top_k=3), head(h1))
+    # a different q_ret projection changes the retrieval and so the output
+    Z2 = dict(Z)
+    Z2["layers.0.q_ret_proj.weight"] = P["layers.0.q_proj.weight"] * -1.0
+    assert not torch.allclose(O.sgsa_model_forward(Z2, ids, num_layers=1, num_heads=2, top_k=3), head(h1))
