@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """SGSA layer-forward benchmark on one MI355X.
 
-    python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--no-cpu-baseline] [--workload layer|model]
 
 A step is one SGSA layer forward over the batch at the north-star shape
 (B=1, H=16, T=32768, d=128, top-k=2048, chunk 64, bf16 inputs, fp32 state):
@@ -117,6 +117,70 @@ def cpu_baseline(q, k, v, beta, gamma, budget, cfg, sample_rows=256, chunk_token
     }
 
 
+MODEL_METRIC = "SGSA 2-layer model fwd tokens/s (config 2: bf16, B=16, T=4096, hidden 1024, 8x128 heads, vocab 8192)"
+
+
+def recall_batch(B: int, T: int, vocab: int, seed: int = 0) -> torch.Tensor:
+    """Config 2's associative-recall sequences: 1024 (key, value) token pairs drawn
+    without replacement from the lower / upper half of the vocabulary, then query
+    pairs whose keys are resampled from the stored ones (each followed by its
+    value), repeated until the sequence has T tokens."""
+    g = torch.Generator().manual_seed(seed)
+    half = vocab // 2
+    seqs = []
+    for _ in range(B):
+        keys = torch.randperm(half - 1, generator=g)[:1024] + 1
+        vals = torch.randperm(half, generator=g)[:1024] + half
+        pairs = torch.stack([keys, vals], 1).reshape(-1)
+        nq = (T - pairs.numel() + 1) // 2
+        pick = torch.randint(0, 1024, (nq,), generator=g)
+        queries = torch.stack([keys[pick], vals[pick]], 1).reshape(-1)
+        seqs.append(torch.cat([pairs, queries])[:T])
+    return torch.stack(seqs)
+
+
+def run_model(args) -> int:
+    """Config 2: the 2-layer SGSA causal LM forward (sgsa_amd.SGSAForCausalLM)."""
+    import sgsa_amd
+    B, T = 16, 4096
+    cfg = sgsa_amd.SGSAConfig(vocab_size=8192, hidden_size=1024, intermediate_size=2816, num_hidden_layers=2,
+                              num_attention_heads=8, num_kv_heads=8, max_position_embeddings=T, top_k=16)
+    dev = torch.device("cuda:0")
+    model = sgsa_amd.SGSAForCausalLM(cfg)
+    model.init_weights(std=0.02, qk_std=1.0 / math.sqrt(cfg.hidden_size * cfg.head_dim),
+                       generator=torch.Generator().manual_seed(0))
+    model = model.to(device=dev, dtype=torch.bfloat16).eval()
+    ids = recall_batch(B, T, cfg.vocab_size).to(dev)
+    log(f"model: config 2, B={B} T={T}, warmup {args.warmup}")
+    with torch.no_grad():
+        for _ in range(args.warmup):
+            logits = model(ids)["logits"]
+        torch.cuda.synchronize()
+        cur = torch.cuda.current_stream()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(cur)
+        for _ in range(args.steps):
+            logits = model(ids)["logits"]
+        e1.record(cur)
+        torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / max(args.steps, 1)
+    if not torch.isfinite(logits).all():
+        log("non-finite logits")
+        return 1
+    log(f"model ms/step {ms:.3f}")
+    print(json.dumps({
+        "metric": MODEL_METRIC, "value": round(B * T / (ms / 1000.0), 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 3), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic associative-recall token ids, random-init weights",
+        "config": {"workload": "sgsa_model_fwd", "B": B, "T": T, "hidden": 1024, "heads": 8, "head_dim": 128,
+                   "vocab": 8192, "layers": 2, "intermediate": 2816, "top_k": 16,
+                   "init": "normal std 0.02; q/k/q_ret projections std 1/sqrt(hidden*head_dim)"},
+        "cpu_baseline": None,
+    }), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -133,11 +197,16 @@ def main() -> int:
     ap.add_argument("--gather", choices=("tiled", "direct"), default="tiled",
                     help="timed step: the fused layer path (K1 tile lists -> LDS-tiled MFMA K2 -> chunk, what "
                          "sgsa_layer_fwd runs; default) or K1 row lists -> per-row 16-byte gathers -> chunk")
+    ap.add_argument("--workload", choices=("layer", "model"), default="layer",
+                    help="layer: the north-star SGSA layer forward (the headline metric, default); model: "
+                         "config 2, the 2-layer SGSA causal LM forward at B=16 T=4096")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on exactly one GPU (got --gpus {args.gpus}); the SGSA layer shards by head, "
               "and no multi-GPU path is part of this build", file=sys.stderr)
         return 2
+    if args.workload == "model":
+        return run_model(args)
 
     import sgsa_amd
     from sgsa_amd import _abi
