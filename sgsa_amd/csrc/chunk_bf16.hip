@@ -240,43 +240,54 @@ __global__ __launch_bounds__(256) void chunk_intra_bf16(
   }
   __syncthreads();
 
-  // W = (A diag(D_tau)) kappa, U = A nu; wave w owns output column tiles 2w, 2w+1.
+  // W = (A diag(D_tau)) kappa, U = A nu.  Wave w owns the row blocks I = w and
+  // NB-1-w (equal k-step counts per wave) across all 8 column tiles, so the
+  // hi/lo split of each A fragment is done once and feeds 8 column tiles.
   uint16_t* Wh = ws.Whi + cidx * M * DP;
   uint16_t* Wl = ws.Wlo + cidx * M * DP;
   float* Uc = ws.U + cidx * M * DP;
-  for (int I = 0; I < NB; ++I) {
-    const int nks = (16 * (I + 1) + 31) / 32;
+  for (int ii = 0; ii < NB / 4; ++ii) {
+    const int I = ii == 0 ? w : NB - 1 - w;
+    if (I >= NB) continue;
+    const int nks = (16 * (I + 1) + 31) / 32;   // A is zero right of column 16 (I + 1)
+    f4 aw[DP / 16], au[DP / 16];
 #pragma unroll
-    for (int nn = 0; nn < 2; ++nn) {
-      const int n = 2 * w + nn;
-      f4 aw = f4_zero(), au = f4_zero();
-      for (int s = 0; s < nks; ++s) {
-        const int k0 = 32 * s + 8 * lg;
-        float xa[8], xw[8];
+    for (int n = 0; n < DP / 16; ++n) { aw[n] = f4_zero(); au[n] = f4_zero(); }
+    for (int s = 0; s < nks; ++s) {
+      const int k0 = 32 * s + 8 * lg;
+      float xa[8], xw[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          xa[j] = Tm[16 * I + lr][k0 + j];
-          xw[j] = xa[j] * dtau[k0 + j];
-        }
-        uint4 ahi, alo, whi, wlo;
-        split8(xa, ahi, alo);
-        split8(xw, whi, wlo);
+      for (int j = 0; j < 8; ++j) {
+        xa[j] = Tm[16 * I + lr][k0 + j];
+        xw[j] = xa[j] * dtau[k0 + j];
+      }
+      uint4 ahi, alo, whi, wlo;
+      split8(xa, ahi, alo);
+      split8(xw, whi, wlo);
+      // transposed products (kappa^T / nu^T as the A operand): lane (lr, lg) ends
+      // up with columns 16n + 4lg .. +3 of row 16I + lr, stored as one 8-byte
+      // (W planes) or 16-byte (U) vector; same products and order as W, U
+#pragma unroll
+      for (int n = 0; n < DP / 16; ++n) {
         const uint4 bk = *reinterpret_cast<const uint4*>(&kapT[(16 * n + lr) * PM + k0]);
         const uint4 bv = *reinterpret_cast<const uint4*>(&kap[(16 * n + lr) * PM + k0]);
-        aw = mma_bf16(as_bf8(whi), as_bf8(bk), aw);
-        aw = mma_bf16(as_bf8(wlo), as_bf8(bk), aw);
-        au = mma_bf16(as_bf8(ahi), as_bf8(bv), au);
-        au = mma_bf16(as_bf8(alo), as_bf8(bv), au);
+        aw[n] = mma_bf16(as_bf8(bk), as_bf8(whi), aw[n]);
+        aw[n] = mma_bf16(as_bf8(bk), as_bf8(wlo), aw[n]);
+        au[n] = mma_bf16(as_bf8(bv), as_bf8(ahi), au[n]);
+        au[n] = mma_bf16(as_bf8(bv), as_bf8(alo), au[n]);
       }
+    }
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const long off = (long)(16 * I + 4 * lg + e) * DP + 16 * n + lr;
-        uint16_t hi, lo;
-        split1(aw[e], hi, lo);
-        Wh[off] = hi;
-        Wl[off] = lo;
-        Uc[off] = au[e];
-      }
+    for (int n = 0; n < DP / 16; ++n) {
+      const long off = (long)(16 * I + lr) * DP + 16 * n + 4 * lg;
+      uint16_t hi[4], lo[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) split1(aw[n][e], hi[e], lo[e]);
+      *reinterpret_cast<uint2*>(Wh + off) =
+          make_uint2((uint32_t)hi[0] | ((uint32_t)hi[1] << 16), (uint32_t)hi[2] | ((uint32_t)hi[3] << 16));
+      *reinterpret_cast<uint2*>(Wl + off) =
+          make_uint2((uint32_t)lo[0] | ((uint32_t)lo[1] << 16), (uint32_t)lo[2] | ((uint32_t)lo[3] << 16));
+      *reinterpret_cast<float4*>(Uc + off) = make_float4(au[n][0], au[n][1], au[n][2], au[n][3]);
     }
   }
 }
