@@ -4,14 +4,17 @@
     python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--no-cpu-baseline] [--workload layer|model]
 
 A step is one SGSA layer forward over the batch at the north-star shape
-(B=1, H=16, T=32768, d=128, top-k=2048, chunk 64, bf16 inputs, fp32 state):
-  K1 sgsa_score_topk   causal score GEMM + exact top-k (ascending-index rows)
-  K2 sgsa_sparse_gather_tiled  top-k weighted K/V sums (K/V streamed through
-                        LDS, weights applied with MFMA) + concentration/novelty +
-                        write gate (alpha); --gather direct uses the per-row
-                        gather kernel instead, and the other form is timed
-                        once for comparison
+(B=1, H=16, T=32768, d=128, top-k=2048, chunk 64, bf16 inputs, fp32 state),
+the kernels sgsa_layer_fwd runs:
+  K1 sgsa_score_topk_thresholds   causal score GEMM + exact top-k, left as one
+                        cut per row (threshold, tie index)
+  K2 sgsa_sparse_gather_thresholds  the scores recomputed on MFMA against K/V
+                        tiles loaded straight into LDS, the cut applied, top-k
+                        weighted K/V sums + concentration/novelty + write gate
   K3-K5 sgsa_chunk_fwd  chunked gated-delta-rule update with the sparse write
+--gather tiled times the tile-list form (K1 writes the selected entries, K2
+reads them) and --gather direct the row-list form with per-row gathers; the
+K1/K2 of one other form are timed once beside the step for comparison.
 Inputs are synthetic (seed 0, the benchmark distribution) and resident in HBM
 before timing.  Per-stage durations come from HIP events recorded on the
 stream the kernels run on, inside the timed region.
@@ -194,9 +197,10 @@ def main() -> int:
     ap.add_argument("--traffic-from", default=os.path.join(ROOT, "profiles", "hbm_traffic_north_star_pmc.md"),
                     help="committed PMC summary whose 'hbm_bytes_per_launch <kernel>:' lines give the measured "
                          "L2-to-fabric bytes of one launch at the north-star shape")
-    ap.add_argument("--gather", choices=("tiled", "direct"), default="tiled",
-                    help="timed step: the fused layer path (K1 tile lists -> LDS-tiled MFMA K2 -> chunk, what "
-                         "sgsa_layer_fwd runs; default) or K1 row lists -> per-row 16-byte gathers -> chunk")
+    ap.add_argument("--gather", choices=("threshold", "tiled", "direct"), default="threshold",
+                    help="timed step: the fused layer path (K1 row thresholds -> K2 recomputing the scores on "
+                         "MFMA -> chunk, what sgsa_layer_fwd runs; default), the tile-list form (K1 tile lists -> "
+                         "LDS-tiled MFMA K2 -> chunk) or K1 row lists -> per-row 16-byte gathers -> chunk")
     ap.add_argument("--workload", choices=("layer", "model"), default="layer",
                     help="layer: the north-star SGSA layer forward (the headline metric, default); model: "
                          "config 2, the 2-layer SGSA causal LM forward at B=16 T=4096")
@@ -241,6 +245,7 @@ def main() -> int:
     _abi.check(L.sgsa_topk_lists_size(B, T, H, kk, ctypes.byref(lbytes), ctypes.byref(obytes)))
     tl = torch.empty(lbytes.value, device=dev, dtype=torch.uint8)
     toff = torch.empty(obytes.value // 4, device=dev, dtype=torch.int32)
+    thr = torch.empty(B, H, T, 2, device=dev, dtype=torch.int32)
     P = _abi.ptr
     stream = _abi.stream_of(qd)
     scale = math.sqrt(D)
@@ -252,6 +257,14 @@ def main() -> int:
     def k1_lists():
         _abi.check(L.sgsa_score_topk_lists(B, T, H, D, kk, P(qd), P(kd), P(tl), P(toff), P(top2), P(cnt),
                                            P(tws), tbytes.value, stream))
+
+    def k1_thr():
+        _abi.check(L.sgsa_score_topk_thresholds(B, T, H, D, kk, P(qd), P(kd), P(thr), P(top2), P(cnt), P(tws),
+                                                tbytes.value, stream))
+
+    def k2_thr():
+        _abi.check(L.sgsa_sparse_gather_thresholds(B, T, H, D, kk, P(qd), P(kd), P(vd), P(thr), P(top2), P(cnt),
+                                                   P(ud), 0, 0.25, 0.1, P(wk), P(vh), None, P(al), stream))
 
     def k2_tiled():
         _abi.check(L.sgsa_sparse_gather_lists(B, T, H, D, kk, P(kd), P(vd), P(tl), P(toff), P(top2), P(cnt),
@@ -266,7 +279,10 @@ def main() -> int:
         _abi.check(L.sgsa_chunk_fwd(_abi.SGSA_BF16, B, T, H, D, cfg["chunk"], P(qd), P(kd), P(vd), P(bd), P(gd),
                                     P(wk), P(vh), P(al), None, P(out), P(ht), P(ws), nbytes.value, stream))
 
-    if args.gather == "tiled":
+    if args.gather == "threshold":
+        stages = (("score_topk", k1_thr), ("gather_gate", k2_thr), ("chunk", k345))
+        other = (k1_lists, k2_tiled)
+    elif args.gather == "tiled":
         stages = (("score_topk", k1_lists), ("gather_gate", k2_tiled), ("chunk", k345))
         other = (k1_rows, k2_direct)
     else:
@@ -307,7 +323,7 @@ def main() -> int:
     assert torch.isfinite(out.float()).all() and torch.isfinite(ht).all(), "non-finite layer output"
     log(f"ms/step {ms_step:.3f}  stages {json.dumps({n: round(v, 3) for n, v in stage_ms.items()})}")
 
-    if args.gather == "tiled":
+    if args.gather == "threshold":
         # the timed step is exactly sgsa_layer_fwd: same kernels, same order, bit-identical result
         lbytes_ws = ctypes.c_size_t()
         _abi.check(L.sgsa_layer_fwd_workspace_size(_abi.SGSA_BF16, B, T, H, D, kk, ctypes.byref(lbytes_ws)))
@@ -324,17 +340,22 @@ def main() -> int:
 
     # the other K1/K2 form, for comparison (outside the timed steps)
     other_ms = None
+    other_name = {"threshold": "tiled", "tiled": "direct", "direct": "tiled"}[args.gather]
     if args.steps > 0:
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
         other[0]()
         other[1]()
-        e0.record(cur)
+        ev[0].record(cur)
+        for _ in range(3):
+            other[0]()
+        ev[1].record(cur)
         for _ in range(3):
             other[1]()
-        e1.record(cur)
+        ev[2].record(cur)
         torch.cuda.synchronize()
-        other_ms = e0.elapsed_time(e1) / 3
-        log(f"gather ({'direct' if args.gather == 'tiled' else 'tiled'}) for comparison: {other_ms:.3f} ms")
+        other_ms = {"score_topk": round(ev[0].elapsed_time(ev[1]) / 3, 3),
+                    "gather_gate": round(ev[1].elapsed_time(ev[2]) / 3, 3)}
+        log(f"{other_name} form for comparison: {json.dumps(other_ms)} ms")
 
     measured = {}
     if args.traffic_from and os.path.exists(args.traffic_from) and (B, T, H, D, kk) == (1, 32768, 16, 128, 2048):
@@ -346,8 +367,9 @@ def main() -> int:
     gbytes = gather_bytes(B, H, T, D, kk)
     f_score = B * H * T * (T + 1) * D               # causal score GEMM, one pass
     f_chunk = B * H * ((T + 63) // 64) * 23.77e6     # chunk contractions (K3 + K5 + K4)
-    gather_kernel = "gather_list_kernel" if args.gather == "tiled" else "sparse_gather_kernel"
-    topk_kernel = "score_topk_tiles_kernel" if args.gather == "tiled" else "score_topk_kernel"
+    gather_kernel = {"threshold": "gather_thr_kernel", "tiled": "gather_list_kernel",
+                     "direct": "sparse_gather_kernel"}[args.gather]
+    topk_kernel = "score_topk_kernel" if args.gather == "direct" else "score_topk_tiles_kernel"
     rooflines = {
         "score_topk": {"kernel": f"{topk_kernel} (K1)", "bound": "mfma",
                        "achieved": round(f_score / (stage_ms["score_topk"] / 1000.0) / 1e12, 2),
@@ -380,7 +402,7 @@ def main() -> int:
         "config": {"workload": "sgsa_layer_fwd", "B": B, "T": T, "H": H, "D": D, "top_k": top_k,
                    "chunk": cfg["chunk"], "state": "fp32", "gather": args.gather},
         "stage_ms": {n: round(v, 3) for n, v in stage_ms.items()},
-        "gather_other_form_ms": round(other_ms, 3) if other_ms is not None else None,
+        "other_form": {"gather": other_name, "stage_ms": other_ms},
         "roofline": rooflines[dominant],
         "rooflines": rooflines,
         "cpu_baseline": None,

@@ -180,6 +180,29 @@ int sgsa_sparse_gather_lists(int B, int T, int H, int D, int top_k, const void* 
                              float alpha_max, float tau_c, void* k_hat, void* v_hat,
                              void* write_key, float* alpha, void* stream);
 
+/* ---- layer-path building blocks: row thresholds ------------------------------
+ * What sgsa_layer_fwd runs for bf16 with D = 128.  K1 leaves, per row, only the
+ * exact cut of its top-k: thr[b,h,t] = {float th, int32 cut}; key j (causal,
+ * j <= t) is selected iff score_j > th, or score_j == th and j <= cut (the
+ * lowest indices win ties at the threshold; cut = INT32_MAX when there is no
+ * tie to break).  The gather recomputes the scores of every causal key with
+ * the same products -- bit-identical fp32 -- and applies the cut, so both
+ * halves select exactly the rows of modelings/modeling_sgsa.py:144-165
+ * (lowest-index ties) and weigh them as :126-134.  Causal, Tq = Tk = T,
+ * scores q.k / sqrt(D) (:420-428).  bf16 q, k, v [B,T,H,D]; thr [B,H,T] of
+ * 8 bytes; top2 [B,H,T,2] fp32; counts [B,H,T] int32; workspace as
+ * sgsa_score_topk. */
+int sgsa_score_topk_thresholds(int B, int T, int H, int D, int top_k, const void* q, const void* k,
+                               void* thr, float* top2, int32_t* counts, void* workspace,
+                               size_t workspace_bytes, void* stream);
+/* k_hat or write key, v_hat, alpha from those thresholds (D = 128; same outputs
+ * and references as sgsa_sparse_gather_tiled). */
+int sgsa_sparse_gather_thresholds(int B, int T, int H, int D, int top_k, const void* q, const void* k,
+                                  const void* v, const void* thr, const float* top2,
+                                  const int32_t* counts, const float* budget, int write_mode,
+                                  float alpha_max, float tau_c, void* k_hat, void* v_hat,
+                                  void* write_key, float* alpha, void* stream);
+
 /* ---- whole SGSA layer forward ------------------------------------------------
  * The attention half of SGSABlock.forward (modelings/modeling_sgsa.py:669-684)
  * with the projections as inputs: token top-k retrieval on (q_ret, k, v)

@@ -13,8 +13,8 @@ The compiled library (libsgsa_hip.so) is required; there is no fallback path.
 """
 
 from .ops import ChunkSGSAFunction, chunk_sgsa, chunk_sgsa_fwd
-from .retrieval import (SparseRetriever, gather_gate, gather_lists, score_dump, score_topk, score_topk_lists,
-                        sparse_retrieve)
+from .retrieval import (SparseRetriever, gather_gate, gather_lists, gather_thresholds, score_dump, score_topk,
+                        score_topk_lists, score_topk_thresholds, sparse_retrieve)
 from .layer import LayerWorkspace, sgsa_layer_forward, sgsa_layer_retrieve
 from .recurrent import fused_recurrent_sgsa
 from .decode import sgsa_decode_step
@@ -31,7 +31,9 @@ __all__ = [
     "score_dump",
     "gather_gate",
     "gather_lists",
+    "gather_thresholds",
     "score_topk_lists",
+    "score_topk_thresholds",
     "sparse_retrieve",
     "sgsa_layer_forward",
     "sgsa_layer_retrieve",

@@ -51,7 +51,7 @@ int check_dims(int B, int T, int H, int D) {
 
 struct LayerWs {
   size_t idx, sc, cnt, top2, split, wk, vh, al, misc, topk, chunk, total;
-  bool lists;   // bf16, D = 128: K1 writes tile lists (idx/sc regions) for the tiled K2
+  bool thr;   // bf16, D = 128: K1 leaves per-row thresholds (idx region) for the threshold K2
 };
 
 LayerWs layer_ws(int dtype, int B, int T, int H, int D, int top_k) {
@@ -59,10 +59,11 @@ LayerWs layer_ws(int dtype, int B, int T, int H, int D, int top_k) {
   const size_t rows = (size_t)B * H * T;
   const size_t kk = (size_t)(top_k < T ? top_k : T);
   size_t off = 0;
-  w.lists = dtype == SGSA_BF16 && D == 128;
-  if (w.lists) {
-    w.idx = off; off = align_up(off + sgsa::topk_list_bytes(B, T, H, (int)kk));
-    w.sc = off; off = align_up(off + sgsa::topk_list_off_bytes(B, T, T, H));
+  // (the threshold gather addresses one head's keys with 32-bit byte offsets)
+  w.thr = dtype == SGSA_BF16 && D == 128 && (long)T * H * D * 2 <= 0x7fffffffL;
+  if (w.thr) {
+    w.idx = off; off = align_up(off + rows * 8);
+    w.sc = off;
   } else {
     w.idx = off; off = align_up(off + rows * kk * 4);
     w.sc = off; off = align_up(off + rows * kk * 4);
@@ -234,6 +235,46 @@ int sgsa_sparse_gather_lists(int B, int T, int H, int D, int top_k, const void* 
                     "sgsa_sparse_gather_lists");
 }
 
+int sgsa_score_topk_thresholds(int B, int T, int H, int D, int top_k, const void* q, const void* k, void* thr,
+                               float* top2, int32_t* counts, void* workspace, size_t workspace_bytes,
+                               void* stream) {
+  if (int s = check_dims(B, T, H, D)) return s;
+  if (D != 128) return fail(SGSA_ERR_UNSUPPORTED, "the threshold form needs D == 128 (got %d)", D);
+  if (top_k <= 0) return fail(SGSA_ERR_INVALID_ARG, "top_k=%d must be positive", top_k);
+  REQUIRE(q); REQUIRE(k); REQUIRE(thr); REQUIRE(top2); REQUIRE(counts); REQUIRE(workspace);
+  const size_t need_ws = sgsa::topk_workspace_bytes(B, T, H);
+  if (workspace_bytes < need_ws) return fail(SGSA_ERR_WORKSPACE, "workspace %zu < %zu bytes", workspace_bytes, need_ws);
+  sgsa::TopkArgs a{};
+  a.dtype = SGSA_BF16; a.B = B; a.Tq = T; a.Tk = T; a.H = H; a.D = D; a.top_k = top_k < T ? top_k : T;
+  a.causal = 1; a.q_offset = 0; a.scale = (float)sqrt((double)D); a.scale_mode = 0;
+  a.q = q; a.k = k; a.top2 = top2; a.counts = counts; a.thr = reinterpret_cast<uint2*>(thr);
+  a.workspace = workspace;
+  return hip_status(sgsa::launch_score_topk(a, (hipStream_t)stream), "sgsa_score_topk_thresholds");
+}
+
+int sgsa_sparse_gather_thresholds(int B, int T, int H, int D, int top_k, const void* q, const void* k,
+                                  const void* v, const void* thr, const float* top2, const int32_t* counts,
+                                  const float* budget, int write_mode, float alpha_max, float tau_c, void* k_hat,
+                                  void* v_hat, void* write_key, float* alpha, void* stream) {
+  if (int s = check_dims(B, T, H, D)) return s;
+  if (D != 128) return fail(SGSA_ERR_UNSUPPORTED, "the threshold form needs D == 128 (got %d)", D);
+  if (top_k <= 0) return fail(SGSA_ERR_INVALID_ARG, "top_k=%d must be positive", top_k);
+  if ((long)T * H * D * 2 > 0x7fffffffL) return fail(SGSA_ERR_UNSUPPORTED, "one head's keys exceed 2 GiB of offsets");
+  REQUIRE(q); REQUIRE(k); REQUIRE(v); REQUIRE(thr); REQUIRE(top2); REQUIRE(counts); REQUIRE(v_hat);
+  if (write_mode != 0 && write_mode != 1) return fail(SGSA_ERR_INVALID_ARG, "write_mode must be 0 (direct) or 1 (residual)");
+  if (budget != nullptr && alpha == nullptr) return fail(SGSA_ERR_INVALID_ARG, "the write gate needs an alpha output");
+  if (write_mode == 1 && budget != nullptr && write_key == nullptr)
+    return fail(SGSA_ERR_INVALID_ARG, "residual write mode needs a write_key output");
+  sgsa::GatherArgs g{};
+  g.dtype = SGSA_BF16; g.B = B; g.Tq = T; g.Tk = T; g.H = H; g.D = D; g.top_k = top_k < T ? top_k : T;
+  g.q_offset = 0; g.k = k; g.v = v; g.self_key = k; g.top2 = top2; g.counts = counts;
+  g.use_valid = 1; g.tau_c = tau_c; g.eps = 1e-6f; g.budget = budget; g.write_mode = write_mode;
+  g.alpha_max = alpha_max; g.k_hat = k_hat; g.v_hat = v_hat; g.write_key = write_key; g.alpha = alpha;
+  const float ms = sgsa::score_multiplier((float)sqrt((double)D), 0);
+  return hip_status(sgsa::launch_sparse_gather_thr(g, q, reinterpret_cast<const uint2*>(thr), ms, (hipStream_t)stream),
+                    "sgsa_sparse_gather_thresholds");
+}
+
 int sgsa_score_dump(int dtype, int B, int Tq, int Tk, int H, int D, int causal, int q_offset, float scale,
                     int scale_mode, const void* q, const void* k, int row0, int rows, float* out, void* stream) {
   if (int s = validate_topk(dtype, B, Tq, Tk, H, D, 1, scale_mode, scale)) return s;
@@ -327,9 +368,8 @@ int layer_retrieve_impl(const LayerWs& L, char* base, int dtype, int B, int T, i
   ta.dtype = dtype; ta.B = B; ta.Tq = T; ta.Tk = T; ta.H = H; ta.D = D; ta.top_k = kk; ta.causal = 1;
   ta.q_offset = 0; ta.scale = (float)sqrt((double)D); ta.scale_mode = 0;
   ta.q = q_ret; ta.k = k; ta.counts = cnt;
-  if (L.lists) {
-    ta.tl_list = reinterpret_cast<uint2*>(base + L.idx);
-    ta.tl_off = reinterpret_cast<int32_t*>(base + L.sc);
+  if (L.thr) {
+    ta.thr = reinterpret_cast<uint2*>(base + L.idx);
     ta.top2 = t2;
   } else {
     ta.indices = (int32_t*)(base + L.idx); ta.scores = (float*)(base + L.sc);
@@ -344,9 +384,10 @@ int layer_retrieve_impl(const LayerWs& L, char* base, int dtype, int B, int T, i
   ga.budget = budget; ga.write_mode = write_mode; ga.alpha_max = alpha_max;
   ga.k_hat = write_mode == 0 ? wk : nullptr; ga.v_hat = vh; ga.write_key = write_mode == 1 ? wk : nullptr;
   ga.alpha = al;
-  if (L.lists) {
+  if (L.thr) {
     ga.top2 = t2;
-    return hip_status(sgsa::launch_sparse_gather_lists(ga, ta.tl_list, ta.tl_off, st), who);
+    return hip_status(sgsa::launch_sparse_gather_thr(ga, q_ret, ta.thr, sgsa::score_multiplier(ta.scale, ta.scale_mode),
+                                                     st), who);
   }
   ga.indices = ta.indices; ga.scores = ta.scores; ga.top2 = nullptr;
   return hip_status(sgsa::launch_sparse_gather(ga, st), who);

@@ -61,6 +61,23 @@ __device__ __forceinline__ f4 mma_bf16(bf16x8 a, bf16x8 b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
+// fp32 score of an accumulated q.k product: acc * (1/scale), with -0.0 folded
+// onto +0.0.  Every kernel that selects on scores or recomputes them goes
+// through this one expression, so their scores agree bit for bit.
+__device__ __forceinline__ f4 score_of(f4 acc, float mscale) {
+#pragma clang fp contract(off)
+  return acc * mscale + 0.0f;
+}
+
+// Smallest float above x (x finite or -inf; +inf stays +inf).  For scores s
+// (never -0.0 or NaN): s > x  <=>  s >= next_up(x).
+__device__ __forceinline__ float next_up(float x) {
+  uint32_t u = __float_as_uint(x);
+  if (u == 0x7f800000u) return x;
+  if (u == 0x80000000u) u = 0u;
+  return __uint_as_float((int32_t)u >= 0 ? u + 1u : u - 1u);
+}
+
 __device__ __forceinline__ f4 f4_zero() {
   f4 z = {0.f, 0.f, 0.f, 0.f};
   return z;

@@ -32,6 +32,8 @@
 
 #include <float.h>
 
+#include <type_traits>
+
 namespace sgsa {
 
 namespace {
@@ -517,6 +519,266 @@ __global__ __launch_bounds__(256, 2) void gather_list_kernel(GatherArgs a, const
   }
 }
 
+// ---------------------------------------------------------------------------
+// Threshold form (layer path): the selection is recomputed, not read.
+//
+// K1 in threshold mode leaves per row only the exact top-k cut (th, cut): key j
+// with score s is selected iff j is causal for the row and s > th, or s == th
+// and j <= cut (ties at the threshold go to the lowest indices).  This kernel
+// recomputes each tile's scores with K1's products -- A operand K rows, B
+// operand q, the same 32 dims per instruction, score_of -- so its fp32 scores
+// are K1's bit for bit, and turns them into the weights exp(s - max) without
+// leaving registers: the score accumulator C[key][row] is the A operand of
+// P K once MFMA row 4a + b of half h of a 32-key chunk holds key 8a + 4h + b.
+// The weights, and so k_hat, v_hat and the gate, equal gather_list_kernel's.
+//
+// K and V tiles go global -> LDS with direct buffer loads (no VGPR staging),
+// double-buffered.  LDS row r of a tile holds key tile_row_key(r) (the order
+// above) with a pitch of 288 bytes, and its 16-byte chunk c at slot
+// c ^ ((r >> 3) & 1): the score operand reads (16 rows, one chunk) and the
+// transposing reads (4 rows x four 8-byte pieces per 16 lanes) then hit
+// distinct banks, and the slot of chunk c + 2n is the slot of c plus 2n.  The
+// B operands of P K and P V come from ds_read_b64_tr_b16: within 16 lanes,
+// lane i gets element i % 4 of the 8 bytes that lane 4e + i / 4 addresses,
+// e = 0..3, so lanes addressing keys 8g + e, dims 16n + 4(i/4).. receive dim
+// 16n + i of four consecutive keys -- the MFMA's B layout.
+// ---------------------------------------------------------------------------
+constexpr int RP = DP + 16;            // LDS pitch (bf16) of a K/V tile row: 16 data chunks + 2 pad
+constexpr int TILE_SLOTS = KT * RP / 8;   // 16-byte slots of one tile: 1152 = 18 loads of 64 lanes
+
+__device__ __forceinline__ int tile_row_key(int r) {
+  return (r & 32) + 8 * ((r >> 2) & 3) + 4 * ((r >> 4) & 1) + (r & 3);
+}
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ s16x4 lds_read_tr(const uint16_t* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(p));
+}
+
+__global__ __launch_bounds__(256, 2) void gather_thr_kernel(GatherArgs a, const uint16_t* __restrict__ qg,
+                                                         const uint2* __restrict__ thr, float mscale, int nqb2) {
+  __shared__ __align__(16) uint16_t K0[KT * RP], V0[KT * RP], K1[KT * RP], V1[KT * RP];
+
+  const int BH = a.B * a.H;
+  const int bid = blockIdx.x;
+  const int bh = bid % BH;
+  const int qb2 = nqb2 - 1 - bid / BH;   // heaviest row blocks first
+  const int b = bh / a.H, h = bh % a.H;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform
+  const int lr = lane & 15, lg = lane >> 4;
+  const int Tq = a.Tq, Tk = a.Tk, H = a.H;
+  const int r0 = qb2 * QL;
+  const int wr0 = r0 + 32 * w;   // first row of this wave
+  const uint16_t* K = reinterpret_cast<const uint16_t*>(a.k);
+  const uint16_t* V = reinterpret_cast<const uint16_t*>(a.v);
+
+  const int kend = min(Tk, min(Tq, r0 + QL) + a.q_offset);
+  const int ntile = (kend + KT - 1) / KT;
+
+  // Direct loads.  One buffer resource per head covers its keys [0, Tk): a key
+  // past Tk reads as zeros (never selected).  Wave w issues the tile's loads
+  // w, w + 4, ... (18 per tensor); lane l of load i fills slot 64 i + l, i.e.
+  // row (64 i + l) / 18, slot (64 i + l) % 18 (slots 16, 17 are padding and
+  // re-read chunk 0).  The byte offsets within a tile do not change from tile
+  // to tile; the tile start goes into the scalar offset.
+  const long hbase = ((long)b * Tk * H + h) * DP;
+  const int rbytes = H * DP * 2;   // bytes between consecutive keys of a head
+  const int nrec = (Tk - 1) * rbytes + DP * 2;
+  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(K + hbase), 0, nrec, 0x00020000);
+  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(V + hbase), 0, nrec, 0x00020000);
+  int doff[5];
+#pragma unroll
+  for (int t = 0; t < 5; ++t) {
+    const int slot = 64 * (w + 4 * t) + lane;
+    const int r = slot / 18, p = slot % 18;
+    const int c = p < 16 ? p ^ ((r >> 3) & 1) : 0;
+    doff[t] = tile_row_key(min(r, KT - 1)) * rbytes + 16 * c;
+  }
+  // (the tile start goes into the per-lane offset, which the range check covers)
+  auto dma = [&](int kt, uint16_t* Kd, uint16_t* Vd) __attribute__((always_inline)) {
+    const int toff = kt * KT * rbytes;
+#pragma unroll
+    for (int t = 0; t < 5; ++t) {
+      const int i = w + 4 * t;
+      if (i < TILE_SLOTS / 64) {   // wave-uniform
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (__attribute__((address_space(3))) void*)(Kd + 512 * i), 16,
+                                                 doff[t] + toff, 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (__attribute__((address_space(3))) void*)(Vd + 512 * i), 16,
+                                                 doff[t] + toff, 0, 0, 0);
+      }
+    }
+  };
+  // A tile that reaches past Tk: its rows there are never selected (weight 0),
+  // but 0 * NaN is NaN, so whatever the out-of-range loads leave in LDS must be
+  // finite.  Zero the buffers once (block-uniform), before any load lands.
+  if (Tk % KT != 0) {
+    uint4* z[4] = {reinterpret_cast<uint4*>(K0), reinterpret_cast<uint4*>(V0), reinterpret_cast<uint4*>(K1),
+                   reinterpret_cast<uint4*>(V1)};
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      for (int i = tid; i < KT * RP / 8; i += 256) z[u][i] = make_uint4(0, 0, 0, 0);
+    __syncthreads();
+  }
+
+  // The lane's rows wr0 + 16 mt + lr: q (B operand of the score product), the
+  // cut, the row maximum and the causal end.  Dead rows select nothing.
+  bf16x8 qf[2][4];
+  float th[2], mx[2];
+  int cut[2], nv[2];
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt) {
+    const int row = wr0 + 16 * mt + lr;
+    const bool live = row < Tq;
+    const uint16_t* qp = qg + ((long)(b * Tq + (live ? row : 0)) * H + h) * DP + 8 * lg;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      u16x8 raw = *reinterpret_cast<const u16x8*>(qp + 32 * s);
+      if (!live) raw = (u16x8){0, 0, 0, 0, 0, 0, 0, 0};
+      qf[mt][s] = __builtin_bit_cast(bf16x8, raw);
+    }
+    th[mt] = INFINITY; cut[mt] = -1; mx[mt] = 0.f; nv[mt] = 0;
+    if (live) {
+      const long rg = (long)bh * Tq + row;
+      const uint2 t = thr[rg];
+      th[mt] = __uint_as_float(t.x);
+      cut[mt] = (int)t.y;
+      mx[mt] = a.top2[2 * rg];
+      nv[mt] = max(0, min(Tk, row + a.q_offset + 1));
+    }
+  }
+  // every key below wmin is causal for every row of the wave
+  const int wmin = wr0 + 31 < Tq ? max(0, min(Tk, wr0 + a.q_offset + 1)) : 0;
+
+  f4 ok_[2][DP / 16], ov_[2][DP / 16], es[2];
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt) {
+    es[mt] = f4_zero();
+#pragma unroll
+    for (int n = 0; n < DP / 16; ++n) { ok_[mt][n] = f4_zero(); ov_[mt][n] = f4_zero(); }
+  }
+  const uint4 ones4 = make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u);   // bf16 1.0 x 8
+
+  // score operand: row 32 sp + 16 hf + lr, chunk 4 s + lg -> slot 4 s + (lg ^ (lr >> 3))
+  const int s_off = lr * RP + 8 * (lg ^ (lr >> 3));
+  // transposing reads: row 32 sp + 16 jb + 4 lg + lr / 4, dims 16 n + 4 (lr % 4) ..
+  // -> chunk 2n + (lr % 4) / 2 at slot 2n + ((lr % 4) / 2 ^ lg / 2), byte 8 (lr % 2) in it
+  const int t_off = (4 * lg + (lr >> 2)) * RP + 8 * (((lr & 3) >> 1) ^ (lg >> 1)) + 4 * (lr & 1);
+
+  // One 32-key chunk sp of the tile in (Kc, Vc) starting at key t0: scores,
+  // weights, then k_hat += P K, v_hat += P V, E += P 1.  fast: every key is
+  // causal for every row and no row's tie cut falls inside the tile, so
+  // s >= the[mt] decides; only the weights depend on it.
+  auto chunk = [&](bool fast, const uint16_t* Kc, const uint16_t* Vc, int sp, int t0, const float (&the)[2])
+      __attribute__((always_inline)) {
+    // scores and weights one half (16 keys) at a time: A operand rows
+    // 32 sp + 16 hf + lr of the tile, the weights of keys 8 lg + 4 hf + i
+    uint32_t pw[2][4];
+    auto half = [&](int hf) __attribute__((always_inline)) {
+      f4 sc[2] = {f4_zero(), f4_zero()};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const uint4 kf = *reinterpret_cast<const uint4*>(&Kc[(32 * sp + 16 * hf) * RP + s_off + 32 * s]);
+        sc[0] = mma_bf16(as_bf8(kf), qf[0][s], sc[0]);
+        sc[1] = mma_bf16(as_bf8(kf), qf[1][s], sc[1]);
+      }
+      auto weights = [&](auto fast_t) __attribute__((always_inline)) {
+        // the score is rounded before the exponent, as K1 stores it: no fused multiply-add
+#pragma clang fp contract(off)
+        constexpr bool FAST = decltype(fast_t)::value;
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+          float p[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            // -0.0 and +0.0 compare and subtract alike, so score_of's fold is not needed here
+            const float x = sc[mt][i] * mscale;
+            bool sel;
+            if constexpr (FAST) {
+              sel = x >= the[mt];
+            } else {
+              const int j = t0 + 32 * sp + 8 * lg + 4 * hf + i;
+              sel = (j < nv[mt]) & ((x > th[mt]) | ((x == th[mt]) & (j <= cut[mt])));   // no short circuit: no branches
+            }
+            const float e = __builtin_amdgcn_exp2f((x - mx[mt]) * 1.44269504f);   // __expf(x - max)
+            p[i] = sel ? e : 0.f;
+          }
+          pw[mt][2 * hf] = (uint32_t)f32_to_bf16(p[0]) | ((uint32_t)f32_to_bf16(p[1]) << 16);
+          pw[mt][2 * hf + 1] = (uint32_t)f32_to_bf16(p[2]) | ((uint32_t)f32_to_bf16(p[3]) << 16);
+        }
+      };
+      if (fast) weights(std::true_type{});
+      else weights(std::false_type{});
+    };
+    half(0);
+    half(1);
+    const uint4 pa[2] = {make_uint4(pw[0][0], pw[0][1], pw[0][2], pw[0][3]),
+                         make_uint4(pw[1][0], pw[1][1], pw[1][2], pw[1][3])};
+    __builtin_amdgcn_sched_barrier(0);
+    // B operands one dim block ahead of the products (software pipeline kept
+    // by scheduling barriers: the accumulators leave no room for more)
+    const uint16_t* kt_ = Kc + 32 * sp * RP + t_off;
+    const uint16_t* vt_ = Vc + 32 * sp * RP + t_off;
+    auto operands = [&](int n, bf16x8& kb, bf16x8& vb) __attribute__((always_inline)) {
+      const s16x4 k0 = lds_read_tr(kt_ + 16 * n), k1 = lds_read_tr(kt_ + 16 * RP + 16 * n);
+      const s16x4 v0 = lds_read_tr(vt_ + 16 * n), v1 = lds_read_tr(vt_ + 16 * RP + 16 * n);
+      kb = __builtin_bit_cast(bf16x8, __builtin_shufflevector(k0, k1, 0, 1, 2, 3, 4, 5, 6, 7));
+      vb = __builtin_bit_cast(bf16x8, __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7));
+    };
+    bf16x8 kb[2], vb[2];
+    operands(0, kb[0], vb[0]);
+#pragma unroll
+    for (int n = 0; n < DP / 16; ++n) {
+      if (n + 1 < DP / 16) operands(n + 1, kb[(n + 1) & 1], vb[(n + 1) & 1]);
+      ok_[0][n] = mma_bf16(as_bf8(pa[0]), kb[n & 1], ok_[0][n]);
+      ok_[1][n] = mma_bf16(as_bf8(pa[1]), kb[n & 1], ok_[1][n]);
+      ov_[0][n] = mma_bf16(as_bf8(pa[0]), vb[n & 1], ov_[0][n]);
+      ov_[1][n] = mma_bf16(as_bf8(pa[1]), vb[n & 1], ov_[1][n]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    es[0] = mma_bf16(as_bf8(pa[0]), as_bf8(ones4), es[0]);
+    es[1] = mma_bf16(as_bf8(pa[1]), as_bf8(ones4), es[1]);
+  };
+
+  auto tile = [&](int kt, const uint16_t* Kc, const uint16_t* Vc) __attribute__((always_inline)) {
+    const int t0 = kt * KT;
+    float the[2];
+    bool mixed = false;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      const bool le = t0 + KT - 1 <= cut[mt], gt = t0 > cut[mt];
+      mixed |= !(le || gt);
+      the[mt] = le ? th[mt] : next_up(th[mt]);
+    }
+    const bool fast = t0 + KT <= wmin && !ballot64(mixed);
+#pragma unroll
+    for (int sp = 0; sp < KT / 32; ++sp) chunk(fast, Kc, Vc, sp, t0, the);
+  };
+
+  // Double buffering (two static buffers, so the compiler sees that the loads
+  // in flight never alias the tile being read): the loads of tile kt + 1 run
+  // while tile kt is multiplied.
+  dma(0, K0, V0);
+  for (int kt = 0; kt < ntile; kt += 2) {
+    __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): this wave's loads of tile kt are done
+    __syncthreads();                      // ... every wave's; buffer 1 is free
+    if (kt + 1 < ntile) dma(kt + 1, K1, V1);
+    tile(kt, K0, V0);
+    if (kt + 1 < ntile) {
+      __builtin_amdgcn_s_waitcnt(0x0f70);
+      __syncthreads();
+      if (kt + 2 < ntile) dma(kt + 2, K0, V0);
+      tile(kt + 1, K1, V1);
+    }
+  }
+
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt) {
+    const float E[4] = {es[mt][0], es[mt][1], es[mt][2], es[mt][3]};
+    tile_epilogue(a, ok_[mt], ov_[mt], E, wr0 + 16 * mt, bh, b, h, lr, lg);
+  }
+}
+
 hipError_t launch_sparse_gather_staged(const GatherArgs& a, const int32_t* split, hipStream_t st) {
   const int nqb = (a.Tq + QB - 1) / QB;
   gather_tile_kernel<<<dim3((unsigned)(a.B * a.H * nqb)), 256, 0, st>>>(a, split, nqb);
@@ -529,6 +791,14 @@ hipError_t launch_sparse_gather_lists(const GatherArgs& a, const uint2* tl_list,
   const int nqb2 = (a.Tq + QL - 1) / QL;
   const int ntmax = (a.Tk + KT - 1) / KT;
   gather_list_kernel<<<dim3((unsigned)(a.B * a.H * nqb2)), 256, 0, st>>>(a, tl_list, tl_off, nqb2, nqb, ntmax);
+  return hipGetLastError();
+}
+
+hipError_t launch_sparse_gather_thr(const GatherArgs& a, const void* q, const uint2* thr, float mscale,
+                                    hipStream_t st) {
+  const int nqb2 = (a.Tq + QL - 1) / QL;
+  gather_thr_kernel<<<dim3((unsigned)(a.B * a.H * nqb2)), 256, 0, st>>>(
+      a, reinterpret_cast<const uint16_t*>(q), thr, mscale, nqb2);
   return hipGetLastError();
 }
 

@@ -71,6 +71,7 @@ struct TopkArgs {
   uint2* tl_list;     // layer path (bf16): per-wave tile lists, topk_list_bytes(); nullptr otherwise
   int32_t* tl_off;    // per-wave tile start offsets, topk_list_off_bytes()
   int tl_ntmax;       // set by the launcher: key tiles per row block
+  uint2* thr;         // threshold mode (bf16, D = 128, top-2 required): [B,H,Tq] {fp32 th, cut}; no lists
   void* workspace;    // topk_workspace_bytes(): candidate lists + per-head key norms
   uint2* scratch;     // set by the launcher
   int* flags;         // set by the launcher
@@ -86,6 +87,10 @@ size_t topk_list_bytes(int B, int Tq, int H, int top_k);
 size_t topk_list_off_bytes(int B, int Tq, int Tk, int H);
 
 hipError_t launch_score_topk(const TopkArgs& a, hipStream_t st);
+// The multiplier K1 applies to q.k accumulators (score = acc * multiplier).
+inline float score_multiplier(float scale, int scale_mode) {
+  return scale_mode == 0 ? (float)(1.0 / (double)scale) : scale;
+}
 hipError_t launch_sort_rows(int32_t* indices, float* scores, long rows, int top_k, const int32_t* counts,
                             hipStream_t st);
 
@@ -125,5 +130,9 @@ hipError_t launch_sparse_gather_staged(const GatherArgs& a, const int32_t* split
 // Layer path: the same kernel fed by the tile lists of the list-mode K1.
 hipError_t launch_sparse_gather_lists(const GatherArgs& a, const uint2* tl_list, const int32_t* tl_off,
                                       hipStream_t st);
+// Layer path, threshold form: the selection recomputed from q and each row's
+// cut (score threshold, tie index) left by the threshold-mode K1.
+hipError_t launch_sparse_gather_thr(const GatherArgs& a, const void* q, const uint2* thr, float mscale,
+                                    hipStream_t st);
 
 }  // namespace sgsa

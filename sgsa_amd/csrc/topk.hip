@@ -100,6 +100,13 @@ __device__ __forceinline__ float key_to_f32(uint32_t k) {
   return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
 }
 
+// The float threshold t of a key bound: for finite scores s, s >= t <=> key(s) >= k.
+// (Keys below key(-FLT_MAX) or above key(FLT_MAX) decode to -inf/+inf or NaN;
+// no finite score has them.)
+__device__ __forceinline__ float threshold_of_key(uint32_t k) {
+  return key_to_f32(min(max(k, 0x00800000u), 0xff7fffffu));
+}
+
 // Smallest float s with score_bin(s, iw) >= bt (1 <= bt <= 255), by bisection over
 // the order-preserving keys between -inf and +inf (score_bin is monotone in s).
 __device__ __forceinline__ float bin_lower_edge(int bt, float iw) {
@@ -181,8 +188,12 @@ __global__ __launch_bounds__(256) void key_norm_max_kernel(const X* __restrict__
 // more than TOPK_CAP candidates sets flags[block] and returns without output.
 // FB = true: re-runs exactly the flagged blocks with 8-bit radix digit passes
 // over the order-preserving keys (up to 4 passes + emit).
-template <typename X, bool DUMP, bool C16, bool TOP2, bool FB, bool LIST>
+// THR (with FB and LIST): no tile lists; each row's cut goes to thr instead
+// (the fallback of the threshold-mode tiles kernel).
+template <typename X, bool DUMP, bool C16, bool TOP2, bool FB, bool LIST, bool THR = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LIST && !FB ? 3 : 1))) void score_topk_kernel(TopkArgs a, int nqb, float mscale) {
+  static_assert(!THR || (FB && LIST), "threshold output only from the list-mode fallback");
+  constexpr bool TL = LIST && !THR;   // writes tile lists
   constexpr int P = KTile<X>::PITCH;
   constexpr bool BF = sizeof(X) == 2;
   constexpr int NQF = BF ? DP / 32 : DP / 4;          // q fragments per lane
@@ -303,7 +314,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LIST && !FB
             c = mma_f32(qf[s], ks[(16 * nt + lr) * P + 4 * s + lg], c);
           }
         }
-        acc[nt] = c * mscale + 0.0f;   // fold -0.0 onto +0.0
+        acc[nt] = score_of(c, mscale);
       }
       fn(kt, acc);
     }
@@ -528,9 +539,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LIST && !FB
   // the resolve overwrites the score of those not selected with -inf.
   const int tlcap = 16 * (topk + TOPK_CAP);
   const long lreg = ((long)bh * nqb + qb) * 4 + w;
-  uint2* tl = LIST ? a.tl_list + lreg * tlcap : nullptr;
-  int32_t* toff = LIST ? a.tl_off + lreg * (a.tl_ntmax + 1) : nullptr;
+  uint2* tl = TL ? a.tl_list + lreg * tlcap : nullptr;
+  int32_t* toff = TL ? a.tl_off + lreg * (a.tl_ntmax + 1) : nullptr;
   int woff = 0;
+  int cutj[4] = {-1, -1, -1, -1};   // THR: key index of the last threshold tie selected (lane-local)
   auto emit = [&](int e, int kk, int j, float s, bool sel, bool col) __attribute__((always_inline)) {
     const uint32_t sm = (uint32_t)(ballot64(sel) >> (16 * lg)) & 0xffffu;
     const uint32_t cm = (uint32_t)(ballot64(col) >> (16 * lg)) & 0xffffu;
@@ -667,7 +679,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LIST && !FB
   } else {
     int eqc[4] = {0, 0, 0, 0};
     sweep([&](int kt, f4* acc) __attribute__((always_inline)) {
-      if constexpr (LIST) {
+      if constexpr (TL) {
         if (lane == 0) toff[kt] = woff;
       }
       const bool full = (kt + 1) * KT <= minvalid;
@@ -685,15 +697,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LIST && !FB
           const bool eq = inb && km == pfx[e];
           const uint32_t eqm = (uint32_t)(ballot64(eq) >> (16 * lg)) & 0xffffu;
           sel = sel || (inb && (km > pfx[e] || (eq && eqc[e] + __popc(eqm & lower) < need[e])));
+          if constexpr (THR) {
+            if (eq && eqc[e] + (int)__popc(eqm & lower) == need[e] - 1) cutj[e] = j;   // last tie selected
+          }
           eqc[e] += __popc(eqm);
-          if constexpr (LIST) emit_list(e, nt, s, sel);
-          else emit(e, 16 * nt + lr, j, s, sel, col);
+          if constexpr (TL) emit_list(e, nt, s, sel);
+          else if constexpr (!THR) emit(e, 16 * nt + lr, j, s, sel, col);
           top2_update(e, ok, s);
         }
       }
     });
   }
-  if constexpr (LIST) {
+  if constexpr (TL) {
     if (lane == 0) toff[ntile] = woff;
   }
   if (lr == 0) {
@@ -823,7 +838,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LIST && !FB
         m1[e] = hi; m2[e] = lo;
       }
     }
+    if constexpr (THR) {
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) cutj[e] = max(cutj[e], __shfl_xor(cutj[e], o, 64));
+    }
     if (!live[e]) continue;
+    if constexpr (THR) {
+      if (lr == 0) {
+        float th = -INFINITY;
+        int cut = 0x7fffffff;
+        if (mode[e] == RADIX) {
+          th = threshold_of_key(pfx[e]);
+          if (msk[e] == 0xffffffffu) cut = cutj[e];
+        }
+        a.thr[rowg] = make_uint2(__float_as_uint(th), (uint32_t)cut);
+      }
+    }
     // LIST: every row selects exactly min(top_k, valid keys)
     const int oc = LIST ? min(topk, nvalid[e]) : min(rowcnt[w][4 * lg + e][0], topk);
     if (!LIST) for (int p = oc + lr; p < topk; p += 16) {
@@ -900,7 +930,14 @@ __global__ __launch_bounds__(256) void sort_rows_kernel(int32_t* __restrict__ in
 // fallback launch of score_topk_kernel<..., FB = true, LIST = true>, which
 // writes the same lists.
 // ---------------------------------------------------------------------------
-template <bool C16>
+//
+// THR (threshold mode, the layer path): no lists.  Pass B runs pass A's
+// register sweep again and only collects the threshold-bin candidates (from
+// every wave into per-row LDS counters and the scratch lists); the resolve
+// then leaves each row's exact cut in thr: {fp32 threshold th, key index cut},
+// key j selected iff s > th, or s == th and j <= cut.
+// ---------------------------------------------------------------------------
+template <bool C16, bool THR>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void score_topk_tiles_kernel(
     TopkArgs a, int nqb, float mscale) {
   constexpr int HW = C16 ? NBIN / 2 : NBIN;   // histogram words per row
@@ -992,7 +1029,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void s
         f4 c = f4_zero();
 #pragma unroll
         for (int s = 0; s < 4; ++s) c = mma_bf16(kf[s], qf[g][s], c);
-        acc[g] = c * mscale + 0.0f;   // fold -0.0 onto +0.0
+        acc[g] = score_of(c, mscale);
       }
       if (kt + 1 < ntile) kload(kt + 1);
       fn(kt, acc);
@@ -1107,6 +1144,168 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void s
   }
   __syncthreads();
 
+  if constexpr (THR) {
+    // ---- pass B (threshold mode): threshold-bin candidates, top-2 --------------
+    // Lane (w, lg, lr) sees row r0 + 16g + lr against keys kt*64 + 16w + lg + 4i.
+    float tb0[4], tb1[4], m1[4], m2[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const RowInfo ri = rinfo[g][lr];
+      tb0[g] = (live[g] && ri.mode == COLLECT) ? ri.th0 : INFINITY;   // only COLLECT rows have a bin to resolve
+      tb1[g] = ri.th1;
+      m1[g] = -FLT_MAX; m2[g] = -FLT_MAX;
+    }
+    uint2* scratch = a.scratch;
+    const long srowb = (long)bh * Tq + r0;   // global row of the block's row 0
+    auto collect = [&](int g, int j, float sc) __attribute__((always_inline)) {
+      const int slot = (int)atomicAdd((uint32_t*)&colcnt[g][lr], 1u);
+      if (slot < TOPK_CAP) scratch[(srowb + 16 * g + lr) * TOPK_CAP + slot] = make_uint2(__float_as_uint(sc), (uint32_t)j);
+    };
+    sweep([&](int kt, f4* acc) __attribute__((always_inline)) {
+      const bool full = (kt + 1) * KT <= minvalid;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int j = kt * KT + 16 * w + lg + 4 * i;
+          const float sc = acc[g][i];
+          const bool ok = full || j < nvalid[g];   // nvalid is 0 for dead rows
+          m2[g] = __builtin_amdgcn_fmed3f(m1[g], m2[g], ok ? sc : -FLT_MAX);
+          m1[g] = fmaxf(m1[g], ok ? sc : -FLT_MAX);
+          if (ok & (sc >= tb0[g]) & (sc < tb1[g])) collect(g, j, sc);
+        }
+      }
+    });
+    // top-2 over the row's lanes of this wave (lg), then over the waves (LDS)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+#pragma unroll
+      for (int o = 16; o < 64; o <<= 1) {
+        const float b1 = __shfl_xor(m1[g], o, 64), b2 = __shfl_xor(m2[g], o, 64);
+        const float hi = fmaxf(m1[g], b1), lo = fmaxf(fminf(m1[g], b1), fmaxf(m2[g], b2));
+        m1[g] = hi; m2[g] = lo;
+      }
+    }
+    __syncthreads();   // candidates and counters of every wave are in place; hist is free
+    float2* t2s = reinterpret_cast<float2*>(&hist[0][0]);   // [wave][64 rows]
+    if (lg == 0) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) t2s[64 * w + 16 * g + lr] = make_float2(m1[g], m2[g]);
+    }
+    __syncthreads();
+    float2 t2 = make_float2(-FLT_MAX, -FLT_MAX);
+    if (lane < 16) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const float2 o = t2s[64 * v + 16 * w + lane];
+        const float hi = fmaxf(t2.x, o.x), lo = fmaxf(fminf(t2.x, o.x), fmaxf(t2.y, o.y));
+        t2.x = hi; t2.y = lo;
+      }
+    }
+    __syncthreads();   // hist is the resolve's histogram area from here on
+
+    // ---- resolve: the exact cut of every COLLECT row of the wave --------------
+    uint32_t* h256 = &hist[16 * w][0];
+    float thv = -INFINITY;   // lane rr < 16: row 16w + rr
+    int cutv = 0x7fffffff;
+    for (int rr = 0; rr < 16; ++rr) {
+      const RowInfo ri = rinfo[w][rr];
+      if (ri.mode == BIN_ALL && lane == rr) thv = ri.th0;   // everything from the bin's lower edge up
+      if (ri.mode != COLLECT) continue;
+      const long row = srowb + 16 * w + rr;
+      const int n = min(colcnt[w][rr], TOPK_CAP);
+      uint32_t key[CAPL];
+      int idx[CAPL];
+#pragma unroll
+      for (int m = 0; m < CAPL; ++m) {
+        const int p = 64 * m + lane;
+        key[m] = 0; idx[m] = 0;
+        if (p < n) {
+          const uint2 v = scratch[row * TOPK_CAP + p];
+          key[m] = f32_order_key(__uint_as_float(v.x));
+          idx[m] = (int)v.y;
+        }
+      }
+      const uint32_t klo = f32_order_key(ri.th0), dif = klo ^ (f32_order_key(ri.th1) - 1u);
+      uint32_t rm = 0;
+      int sh = 24;
+      while (sh > 0 && (dif >> sh) == 0u) { rm |= 0xffu << sh; sh -= 8; }
+      uint32_t rp = klo & rm;
+      uint32_t rneed = (uint32_t)ri.need;
+      for (; sh >= 0; sh -= 8) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) h256[4 * lane + q] = 0;
+        wave_lds_sync();
+#pragma unroll
+        for (int m = 0; m < CAPL; ++m) {
+          if (64 * m + lane < n && (key[m] & rm) == rp) atomicAdd(&h256[(key[m] >> sh) & 255u], 1u);
+        }
+        wave_lds_sync();
+        uint32_t c[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) c[q] = h256[255 - 4 * lane - q];
+        int bin;
+        uint32_t above, cnt;
+        find_bin(c, lane, rneed, bin, above, cnt);
+        rp |= (uint32_t)bin << sh;
+        rm |= 0xffu << sh;
+        rneed -= above;
+        wave_lds_sync();
+        if (cnt == rneed) break;
+      }
+      // Keys at the threshold key rp: the rneed with the smallest key index win;
+      // a radix select over ~index finds the last of them when more are equal.
+      uint32_t neq = 0;
+#pragma unroll
+      for (int m = 0; m < CAPL; ++m) neq += (uint32_t)__popcll(ballot64(64 * m + lane < n && (key[m] & rm) == rp));
+      uint32_t ip = 0;
+      if (neq > rneed) {
+        uint32_t im = 0, need2 = rneed;
+        for (int sh2 = 24; sh2 >= 0; sh2 -= 8) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) h256[4 * lane + q] = 0;
+          wave_lds_sync();
+#pragma unroll
+          for (int m = 0; m < CAPL; ++m) {
+            const uint32_t ik = ~(uint32_t)idx[m];
+            if (64 * m + lane < n && (key[m] & rm) == rp && (ik & im) == ip) atomicAdd(&h256[(ik >> sh2) & 255u], 1u);
+          }
+          wave_lds_sync();
+          uint32_t c[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) c[q] = h256[255 - 4 * lane - q];
+          int bin;
+          uint32_t above, cnt;
+          find_bin(c, lane, need2, bin, above, cnt);
+          ip |= (uint32_t)bin << sh2;
+          im |= 0xffu << sh2;
+          need2 -= above;
+          wave_lds_sync();
+          if (cnt == need2) break;
+        }
+      }
+      // selected: key > rp (rp's low bits are zero when the loop stopped early), or
+      // key == rp and ~index >= ip, i.e. index <= ~ip
+      if (lane == rr) {
+        thv = threshold_of_key(rp);
+        cutv = neq > rneed ? (int)~ip : 0x7fffffff;
+      }
+    }
+    if (lane < 16) {
+      const int qr = r0 + 16 * w + lane;
+      if (qr < Tq) {
+        const long rowg = srowb + 16 * w + lane;
+        const int nv = a.causal ? max(0, min(Tk, qr + a.q_offset + 1)) : Tk;
+        a.thr[rowg] = make_uint2(__float_as_uint(thv), (uint32_t)cutv);
+        if (a.counts) a.counts[rowg] = min(topk, nv);
+        if (a.split) a.split[rowg] = 0;
+        a.top2[2 * rowg] = t2.x;
+        a.top2[2 * rowg + 1] = t2.y;
+      }
+    }
+    return;
+  } else {
+
   // ---- pass B: wave w takes rows r0 + 16w + 4lg + e against the K tile in LDS --
   // (every score of a row is then in one wave, which keeps the emission, the
   // flush and the top-2 wave-private).  A operand: the wave's row group of qf.
@@ -1160,7 +1359,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void s
           const uint4 raw = *reinterpret_cast<const uint4*>(&ks[(16 * nt + lr) * PB + 32 * s + 8 * lg]);
           c = mma_bf16(qa[s], __builtin_bit_cast(bf16x8, raw), c);
         }
-        acc[nt] = c * mscale + 0.0f;   // fold -0.0 onto +0.0
+        acc[nt] = score_of(c, mscale);
       }
       fn(kt, acc);
     }
@@ -1348,6 +1547,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void s
       a.top2[2 * rowg + 1] = m2[e];
     }
   }
+  }   // !THR
 }
 
 size_t topk_workspace_bytes(int B, int Tq, int H) {
@@ -1372,7 +1572,7 @@ hipError_t launch_score_topk(const TopkArgs& a0, hipStream_t st) {
   const int BH = a.B * a.H;
   // score = acc / scale is evaluated as acc * (1/scale) with the reciprocal
   // rounded once on the host; scale_mode 1 multiplies by scale directly.
-  const float ms = a.scale_mode == 0 ? (float)(1.0 / (double)a.scale) : a.scale;
+  const float ms = score_multiplier(a.scale, a.scale_mode);
   if (a.dump) {
     const int qb0 = a.dump_row0 / QB;
     const int qb1 = (a.dump_row0 + a.dump_rows + QB - 1) / QB;
@@ -1395,16 +1595,27 @@ hipError_t launch_score_topk(const TopkArgs& a0, hipStream_t st) {
   const dim3 grid((unsigned)(BH * nqb));
   const bool c16 = a.Tk <= 65535;   // 16-bit histogram counters cannot overflow
   const bool t2 = a.top2 != nullptr;
+  if (a.thr != nullptr) {   // layer path, threshold mode (bf16, D = 128, top-2 required)
+    if (a.dtype != DT_BF16 || !t2 || a.D != DP) return hipErrorInvalidValue;
+    if (c16) {
+      score_topk_tiles_kernel<true, true><<<grid, 256, 0, st>>>(a, nqb, ms);
+      score_topk_kernel<bf16_t, false, true, true, true, true, true><<<grid, 256, 0, st>>>(a, nqb, ms);
+    } else {
+      score_topk_tiles_kernel<false, true><<<grid, 256, 0, st>>>(a, nqb, ms);
+      score_topk_kernel<bf16_t, false, false, true, true, true, true><<<grid, 256, 0, st>>>(a, nqb, ms);
+    }
+    return hipGetLastError();
+  }
   if (a.tl_list != nullptr) {   // layer path: tile lists (bf16, top-2 required)
     a.tl_ntmax = (a.Tk + KT - 1) / KT;
     if (a.dtype != DT_BF16 || !t2) return hipErrorInvalidValue;
     const bool regs = a.D == DP;   // K fragments straight into registers (D = 128)
     if (c16) {
-      if (regs) score_topk_tiles_kernel<true><<<grid, 256, 0, st>>>(a, nqb, ms);
+      if (regs) score_topk_tiles_kernel<true, false><<<grid, 256, 0, st>>>(a, nqb, ms);
       else score_topk_kernel<bf16_t, false, true, true, false, true><<<grid, 256, 0, st>>>(a, nqb, ms);
       score_topk_kernel<bf16_t, false, true, true, true, true><<<grid, 256, 0, st>>>(a, nqb, ms);
     } else {
-      if (regs) score_topk_tiles_kernel<false><<<grid, 256, 0, st>>>(a, nqb, ms);
+      if (regs) score_topk_tiles_kernel<false, false><<<grid, 256, 0, st>>>(a, nqb, ms);
       else score_topk_kernel<bf16_t, false, false, true, false, true><<<grid, 256, 0, st>>>(a, nqb, ms);
       score_topk_kernel<bf16_t, false, false, true, true, true><<<grid, 256, 0, st>>>(a, nqb, ms);
     }

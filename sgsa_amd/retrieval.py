@@ -142,6 +142,52 @@ def gather_lists(k: Tensor, v: Tensor, lists: Tensor, offs: Tensor, top2: Tensor
     return wk, vh, al
 
 
+def score_topk_thresholds(q: Tensor, k: Tensor, top_k: int):
+    """K1 of the fused layer (bf16, D = 128): the causal top-k of q.k/sqrt(D)
+    left as one exact cut per row (see include/sgsa.h).
+
+    q, k [B,T,H,D] bfloat16.  Returns (thr int32 [B,H,T,2] holding {float32 bits
+    of th, cut}, top2 float32 [B,H,T,2], counts int32 [B,H,T]): key j <= t is
+    selected iff score > th, or score == th and j <= cut.
+    """
+    if not q.is_cuda:
+        raise ValueError("score_topk_thresholds: the SGSA kernels run on a ROCm GPU; got CPU tensors")
+    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or k.shape != q.shape:
+        raise ValueError("score_topk_thresholds takes bfloat16 q and k of equal shape")
+    B, T, H, D = q.shape
+    qc, kc = q.contiguous(), k.contiguous()
+    dev = q.device
+    L = _abi.lib()
+    wb = ctypes.c_size_t()
+    _abi.check(L.sgsa_score_topk_workspace_size(B, T, H, ctypes.byref(wb)))
+    thr = torch.empty(B, H, T, 2, device=dev, dtype=torch.int32)
+    top2 = torch.empty(B, H, T, 2, device=dev, dtype=torch.float32)
+    cnt = torch.empty(B, H, T, device=dev, dtype=torch.int32)
+    ws = torch.empty(wb.value, device=dev, dtype=torch.uint8)
+    _abi.check(L.sgsa_score_topk_thresholds(B, T, H, D, int(top_k), _abi.ptr(qc), _abi.ptr(kc), _abi.ptr(thr),
+                                            _abi.ptr(top2), _abi.ptr(cnt), _abi.ptr(ws), wb.value,
+                                            _abi.stream_of(qc)))
+    return thr, top2, cnt
+
+
+def gather_thresholds(q: Tensor, k: Tensor, v: Tensor, thr: Tensor, top2: Tensor, cnt: Tensor,
+                      budget_logits: Tensor, top_k: int, write_mode: str = "direct", alpha_max: float = 0.25,
+                      tau_c: float = 0.1):
+    """K2 of the fused layer on ``score_topk_thresholds`` output: (write key, v_hat, alpha)."""
+    B, T, H, D = k.shape
+    mode = {"direct": 0, "residual": 1}[write_mode]
+    qc, kc, vc = q.contiguous(), k.contiguous(), v.contiguous()
+    wk = torch.empty_like(kc)
+    vh = torch.empty_like(kc)
+    al = torch.empty(B, T, H, device=k.device, dtype=torch.float32)
+    bud = budget_logits.float().contiguous()
+    _abi.check(_abi.lib().sgsa_sparse_gather_thresholds(
+        B, T, H, D, int(top_k), _abi.ptr(qc), _abi.ptr(kc), _abi.ptr(vc), _abi.ptr(thr), _abi.ptr(top2),
+        _abi.ptr(cnt), _abi.ptr(bud), mode, float(alpha_max), float(tau_c), _abi.ptr(wk if mode == 0 else None),
+        _abi.ptr(vh), _abi.ptr(wk if mode == 1 else None), _abi.ptr(al), _abi.stream_of(kc)))
+    return wk, vh, al
+
+
 def score_dump(q: Tensor, k: Tensor, row0: int, rows: int, causal: bool = True, q_offset: int = 0,
                scale: Optional[float] = None, scale_mode: int = 0) -> Tensor:
     """The exact fp32 scores score_topk selects on, for query rows [row0, row0+rows): [B,H,rows,Tk]."""

@@ -45,8 +45,15 @@ def test_workspace_size_queries():
     n = ctypes.c_size_t()
     assert L.sgsa_chunk_fwd_workspace_size(1, 32768, 16, 128, 1, ctypes.byref(n)) == 0
     assert n.value > 16 * 512 * 128 * 128 * 4
+    chunk = n.value
     assert L.sgsa_layer_fwd_workspace_size(1, 1, 32768, 16, 128, 2048, ctypes.byref(n)) == 0
-    assert n.value > 2 * 16 * 32768 * 2048 * 4
+    # bf16, D = 128 (threshold form): chunk workspace, K1's threshold-bin candidate
+    # lists (512 x 8 B per row), the per-row cut (8 B), write key and v_hat
+    rows = 16 * 32768
+    assert n.value > chunk + rows * 512 * 8 + rows * 8 + 2 * rows * 128 * 2
+    assert n.value < chunk + rows * 2048 * 8   # no per-row index/score lists
+    assert L.sgsa_layer_fwd_workspace_size(0, 1, 4096, 4, 64, 256, ctypes.byref(n)) == 0
+    assert n.value > 2 * 4 * 4096 * 256 * 4     # fp32: row lists (indices + scores)
 
 
 @pytest.mark.parametrize("call,needle", [

@@ -1,0 +1,99 @@
+"""GPU parity of the threshold form of the layer path (what sgsa_layer_fwd runs
+for bf16, D = 128): K1 leaves one exact cut per row, K2 recomputes the scores
+and applies it.
+
+* The cut selects exactly the rows of the row-list K1 (the lowest-index top-k
+  of K1's own fp32 scores, checked against the oracle elsewhere), applied to
+  the scores sgsa_score_dump returns -- on random, tied, mass-tied (radix
+  fallback blocks) and heavy-tailed inputs and a ragged shape.
+* K2 on the thresholds gives bit for bit the outputs of K2 on the tile lists:
+  the same scores, weights, products and gate.
+"""
+
+import pytest
+import torch
+
+from oracle import sgsa_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+sgsa_amd = pytest.importorskip("sgsa_amd")
+
+
+def _inputs(case, dev):
+    B, T, H, D, k = 1, 2100, 2, 128, 256
+    g = torch.Generator().manual_seed(33)
+    if case == "random":
+        q, kk = torch.randn(B, T, H, D, generator=g), torch.randn(B, T, H, D, generator=g)
+    elif case == "ties":   # five distinct key rows: exact score ties at every threshold
+        base = torch.randn(5, H, D, generator=g)
+        kk = base[torch.randint(0, 5, (T,), generator=g)][None]
+        q = torch.randn(B, T, H, D, generator=g)
+    elif case == "mass_ties":   # threshold bins beyond the candidate cap: radix fallback blocks
+        base = torch.randn(2, H, D, generator=g)
+        kk = base[torch.randint(0, 2, (T,), generator=g)][None]
+        q = torch.randn(B, T, H, D, generator=g)
+    elif case == "heavy_tail":
+        x = O.make_inputs(B, T, H, D, dtype=torch.float32, seed=12, heavy_tail=True, with_budget=False)
+        q, kk = x["q"], x["k_ret"]
+    else:   # ragged: T not a multiple of the 128-row gather block, B > 1
+        B, T, H, D, k = 2, 700, 3, 128, 100
+        q, kk = torch.randn(B, T, H, D, generator=g), torch.randn(B, T, H, D, generator=g)
+    v = torch.randn(B, T, H, D, generator=g)
+    bud = torch.randn(B, T, H, generator=g)
+    cast = lambda t: t.to(dev, torch.bfloat16).contiguous()
+    return cast(q), cast(kk), cast(v), bud.to(dev), k
+
+
+CASES = ["random", "ties", "mass_ties", "heavy_tail", "ragged"]
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_thresholds_select_exactly_the_row_lists(dev, case):
+    q, kk, v, _, k = _inputs(case, dev)
+    B, T, H, D = q.shape
+    thr, t2t, ct = sgsa_amd.score_topk_thresholds(q, kk, k)
+    idx, sc, t2, cnt = sgsa_amd.score_topk(q, kk, k, sorted=False)
+    dump = sgsa_amd.score_dump(q, kk, 0, T)
+    torch.cuda.synchronize()
+    assert torch.equal(ct.cpu(), cnt.cpu()), "counts differ"
+    assert torch.equal(t2t.cpu(), t2.cpu()), "top2 differs"
+    s = dump.cpu()                                              # [B,H,T,T] K1's fp32 scores
+    th = thr[..., 0].cpu().contiguous().view(torch.float32)[..., None]
+    cut = thr[..., 1].cpu().long()[..., None]
+    j = torch.arange(T)
+    causal = (j[None, :] <= j[:, None])[None, None]
+    mask = causal & ((s > th) | ((s == th) & (j[None, None, None, :] <= cut)))
+    kq = min(k, T)
+    ref = torch.zeros(B, H, T, T, dtype=torch.bool)
+    ic, cc = idx.cpu().long(), cnt.cpu()
+    live = torch.arange(kq)[None, None, None, :] < cc[..., None]
+    bi, hi, ri, si = live.nonzero(as_tuple=True)
+    ref[bi, hi, ri, ic[bi, hi, ri, si]] = True
+    assert torch.equal(mask, ref), f"selected sets differ in {(mask != ref).sum().item()} (row, key) pairs"
+    if case in ("ties", "mass_ties"):
+        assert (thr[..., 1] != 0x7fffffff).any(), "no row needed a tie cut"
+
+
+@pytest.mark.parametrize("write_mode", ["direct", "residual"])
+@pytest.mark.parametrize("case", CASES)
+def test_threshold_gather_equals_list_gather(dev, case, write_mode):
+    q, kk, v, bud, k = _inputs(case, dev)
+    thr, t2t, ct = sgsa_amd.score_topk_thresholds(q, kk, k)
+    wk_t, vh_t, al_t = sgsa_amd.gather_thresholds(q, kk, v, thr, t2t, ct, bud, k, write_mode=write_mode)
+    lists, offs, t2l, cl = sgsa_amd.score_topk_lists(q, kk, k)
+    wk_l, vh_l, al_l = sgsa_amd.gather_lists(kk, v, lists, offs, t2l, cl, bud, k, write_mode=write_mode)
+    torch.cuda.synchronize()
+    for name, a, b in (("write key", wk_t, wk_l), ("v_hat", vh_t, vh_l), ("alpha", al_t, al_l)):
+        assert torch.isfinite(a.float()).all(), f"{name}: non-finite"
+        assert torch.equal(a, b), f"{name}: differs from the tile-list gather (max {(a.float() - b.float()).abs().max():.3e})"
+
+
+def test_layer_path_is_the_threshold_form(dev):
+    # sgsa_layer_retrieve (bf16, D = 128) returns what the threshold halves return
+    q, kk, v, bud, k = _inputs("random", dev)
+    wk, vh, al = sgsa_amd.sgsa_layer_retrieve(q, kk, v, bud, k)
+    thr, t2t, ct = sgsa_amd.score_topk_thresholds(q, kk, k)
+    wk_t, vh_t, al_t = sgsa_amd.gather_thresholds(q, kk, v, thr, t2t, ct, bud, k)
+    torch.cuda.synchronize()
+    assert torch.equal(wk, wk_t) and torch.equal(vh, vh_t) and torch.equal(al, al_t)
