@@ -48,6 +48,11 @@ __device__ __forceinline__ uint32_t f32_order_key(float f) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
+// Inverse of f32_order_key.
+__device__ __forceinline__ float key_to_f32(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
 // --- MFMA fragments -------------------------------------------------------
 // v_mfma_f32_16x16x4_f32 (one block): lane l supplies A[l%16][l/16] and
 // B[l/16][l%16]; the accumulator holds C[4*(l/16)+i][l%16] in element i.

@@ -526,11 +526,14 @@ __global__ __launch_bounds__(256, 2) void gather_list_kernel(GatherArgs a, const
 // with score s is selected iff j is causal for the row and s > th, or s == th
 // and j <= cut (ties at the threshold go to the lowest indices).  This kernel
 // recomputes each tile's scores with K1's products -- A operand K rows, B
-// operand q, the same 32 dims per instruction, score_of -- so its fp32 scores
-// are K1's bit for bit, and turns them into the weights exp(s - max) without
-// leaving registers: the score accumulator C[key][row] is the A operand of
-// P K once MFMA row 4a + b of half h of a 32-key chunk holds key 8a + 4h + b.
-// The weights, and so k_hat, v_hat and the gate, equal gather_list_kernel's.
+// operand q, the same 32 dims per instruction -- so its accumulators are K1's
+// bit for bit.  The cut is applied to them exactly: per row, the smallest
+// accumulator whose fp32 score (acc * mscale) reaches th, or exceeds it, is
+// found once by bisection, and a score is then selected by one compare.  The
+// weights exp(s - max) never leave registers: exp2(acc * mscale*log2e -
+// max*log2e) (one fused multiply-add), and the score accumulator C[key][row]
+// is the A operand of P K once MFMA row 4a + b of half h of a 32-key chunk
+// holds key 8a + 4h + b.
 //
 // K and V tiles go global -> LDS with direct buffer loads (no VGPR staging),
 // double-buffered.  LDS row r of a tile holds key tile_row_key(r) (the order
@@ -551,6 +554,29 @@ __device__ __forceinline__ int tile_row_key(int r) {
 }
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// Two floats to two bf16 (round to nearest even) in one v_cvt_pk_bf16_f32; lo in bits 0-15.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, bf16x2_t));
+}
+
+// Smallest accumulator value c whose score c * mscale (one rounded fp32
+// product, monotone in c for mscale > 0) is >= t, by bisection over the
+// order-preserving keys.  t = -inf gives -inf, t = +inf gives +inf.
+__device__ __forceinline__ float acc_bound(float t, float mscale) {
+#pragma clang fp contract(off)
+  if (!(t > -INFINITY)) return -INFINITY;
+  if (!(t < INFINITY)) return INFINITY;
+  uint32_t lo = 0x007fffffu, hi = 0xff800000u;   // keys of -inf (fails) and +inf (passes)
+  while (hi - lo > 1u) {
+    const uint32_t mid = lo + ((hi - lo) >> 1);
+    if (key_to_f32(mid) * mscale >= t) hi = mid;
+    else lo = mid;
+  }
+  return key_to_f32(hi);
+}
 
 __device__ __forceinline__ s16x4 lds_read_tr(const uint16_t* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(p));
@@ -623,9 +649,13 @@ __global__ __launch_bounds__(256, 2) void gather_thr_kernel(GatherArgs a, const 
 
   // The lane's rows wr0 + 16 mt + lr: q (B operand of the score product), the
   // cut, the row maximum and the causal end.  Dead rows select nothing.
+  // Selection and weights work on the raw accumulator c (score = c * mscale):
+  // ce[mt] / cg[mt] are the smallest c with score >= th / score > th, and the
+  // weight exp(score - max) is evaluated as exp2(c * mscale*log2e - max*log2e).
   bf16x8 qf[2][4];
-  float th[2], mx[2];
+  float ce[2], cg[2], mxl[2];
   int cut[2], nv[2];
+  const float msl = mscale * 1.44269504f;
 #pragma unroll
   for (int mt = 0; mt < 2; ++mt) {
     const int row = wr0 + 16 * mt + lr;
@@ -637,15 +667,19 @@ __global__ __launch_bounds__(256, 2) void gather_thr_kernel(GatherArgs a, const 
       if (!live) raw = (u16x8){0, 0, 0, 0, 0, 0, 0, 0};
       qf[mt][s] = __builtin_bit_cast(bf16x8, raw);
     }
-    th[mt] = INFINITY; cut[mt] = -1; mx[mt] = 0.f; nv[mt] = 0;
+    float th = INFINITY, mx = 0.f;
+    cut[mt] = -1; nv[mt] = 0;
     if (live) {
       const long rg = (long)bh * Tq + row;
       const uint2 t = thr[rg];
-      th[mt] = __uint_as_float(t.x);
+      th = __uint_as_float(t.x);
       cut[mt] = (int)t.y;
-      mx[mt] = a.top2[2 * rg];
+      mx = a.top2[2 * rg];
       nv[mt] = max(0, min(Tk, row + a.q_offset + 1));
     }
+    ce[mt] = acc_bound(th, mscale);
+    cg[mt] = acc_bound(next_up(th), mscale);
+    mxl[mt] = mx * 1.44269504f;
   }
   // every key below wmin is causal for every row of the wave
   const int wmin = wr0 + 31 < Tq ? max(0, min(Tk, wr0 + a.q_offset + 1)) : 0;
@@ -668,7 +702,7 @@ __global__ __launch_bounds__(256, 2) void gather_thr_kernel(GatherArgs a, const 
   // One 32-key chunk sp of the tile in (Kc, Vc) starting at key t0: scores,
   // weights, then k_hat += P K, v_hat += P V, E += P 1.  fast: every key is
   // causal for every row and no row's tie cut falls inside the tile, so
-  // s >= the[mt] decides; only the weights depend on it.
+  // acc >= the[mt] decides; only the weights depend on it.
   auto chunk = [&](bool fast, const uint16_t* Kc, const uint16_t* Vc, int sp, int t0, const float (&the)[2])
       __attribute__((always_inline)) {
     // scores and weights one half (16 keys) at a time: A operand rows
@@ -683,28 +717,25 @@ __global__ __launch_bounds__(256, 2) void gather_thr_kernel(GatherArgs a, const 
         sc[1] = mma_bf16(as_bf8(kf), qf[1][s], sc[1]);
       }
       auto weights = [&](auto fast_t) __attribute__((always_inline)) {
-        // the score is rounded before the exponent, as K1 stores it: no fused multiply-add
-#pragma clang fp contract(off)
         constexpr bool FAST = decltype(fast_t)::value;
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
           float p[4];
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            // -0.0 and +0.0 compare and subtract alike, so score_of's fold is not needed here
-            const float x = sc[mt][i] * mscale;
+            const float c = sc[mt][i];
             bool sel;
             if constexpr (FAST) {
-              sel = x >= the[mt];
+              sel = c >= the[mt];
             } else {
               const int j = t0 + 32 * sp + 8 * lg + 4 * hf + i;
-              sel = (j < nv[mt]) & ((x > th[mt]) | ((x == th[mt]) & (j <= cut[mt])));   // no short circuit: no branches
+              sel = (j < nv[mt]) & ((c >= cg[mt]) | ((c >= ce[mt]) & (j <= cut[mt])));   // no short circuit: no branches
             }
-            const float e = __builtin_amdgcn_exp2f((x - mx[mt]) * 1.44269504f);   // __expf(x - max)
+            const float e = __builtin_amdgcn_exp2f(fmaf(c, msl, -mxl[mt]));
             p[i] = sel ? e : 0.f;
           }
-          pw[mt][2 * hf] = (uint32_t)f32_to_bf16(p[0]) | ((uint32_t)f32_to_bf16(p[1]) << 16);
-          pw[mt][2 * hf + 1] = (uint32_t)f32_to_bf16(p[2]) | ((uint32_t)f32_to_bf16(p[3]) << 16);
+          pw[mt][2 * hf] = pack_bf16x2(p[0], p[1]);
+          pw[mt][2 * hf + 1] = pack_bf16x2(p[2], p[3]);
         }
       };
       if (fast) weights(std::true_type{});
@@ -748,7 +779,7 @@ __global__ __launch_bounds__(256, 2) void gather_thr_kernel(GatherArgs a, const 
     for (int mt = 0; mt < 2; ++mt) {
       const bool le = t0 + KT - 1 <= cut[mt], gt = t0 > cut[mt];
       mixed |= !(le || gt);
-      the[mt] = le ? th[mt] : next_up(th[mt]);
+      the[mt] = le ? ce[mt] : cg[mt];
     }
     const bool fast = t0 + KT <= wmin && !ballot64(mixed);
 #pragma unroll

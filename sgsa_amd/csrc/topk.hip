@@ -96,9 +96,6 @@ __device__ __forceinline__ uint32_t score_bin_bits(float s, float iw) {
 }
 __device__ __forceinline__ int score_bin(float s, float iw) { return (int)(score_bin_bits(s, iw) & 255u); }
 
-__device__ __forceinline__ float key_to_f32(uint32_t k) {
-  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
-}
 
 // The float threshold t of a key bound: for finite scores s, s >= t <=> key(s) >= k.
 // (Keys below key(-FLT_MAX) or above key(FLT_MAX) decode to -inf/+inf or NaN;
