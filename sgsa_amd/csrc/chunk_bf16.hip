@@ -293,176 +293,322 @@ __global__ __launch_bounds__(256) void chunk_intra_bf16(
 }
 
 // ---------------------------------------------------------------------------
-// K4
+// K4: the inter-chunk state pass, segment-parallel.
+//
+// One chunk maps its start state S to D_L S + kappa^T (lambda' (U - W S)),
+// which is affine in S, so a segment of consecutive chunks maps its start
+// state to its end state as S_end = Phi S_start + P: Phi is the segment's
+// chunk maps applied to the identity with U = 0, P the same maps applied to 0
+// with U.  Three launches replace the one sequential pass over all chunks:
+//   1. chunk_seg_bf16<SEG_MAPS>: one block per (b*h, segment, P or Phi) runs
+//      the segment's chunks; all segments at once;
+//   2. chunk_seg_scan_bf16: per b*h, S_start(0) = h0 and
+//      S_start(g+1) = Phi_g S_start(g) + P_g;
+//   3. chunk_seg_bf16<SEG_FULL>: each segment reruns its chunks from its start
+//      state and writes the chunk-start states and residuals K5 reads.
+// A block owns all 128 state columns: each chunk's W, kappa^T and U cross into
+// the CU once and feed the products of all four waves.  Wave w owns state rows
+// 32w .. 32w + 31 and residual (sample) rows (M/64) w * 16 .. + M/64 * 16.
+// Products keep the fp32 state exact to about 2^-16: W, S and R' are split
+// into bf16 hi + lo (the lo * lo term is dropped).
 // ---------------------------------------------------------------------------
-template <bool SP>
-__global__ __launch_bounds__(256) void chunk_state_bf16(
-    const float* __restrict__ beta, const float* __restrict__ alpha, const float* __restrict__ h0, int T, int H,
-    int D, int NT, Bf16Ws ws, float* __restrict__ ht) {
+enum SegMode { SEG_MAPS = 0, SEG_FULL = 1 };
+
+__device__ __forceinline__ uint4 neg_bf16x8(uint4 u) {
+  return make_uint4(u.x ^ 0x80008000u, u.y ^ 0x80008000u, u.z ^ 0x80008000u, u.w ^ 0x80008000u);
+}
+
+// Number of segments of the state pass: enough (b*h, segment) blocks to fill
+// the GPU, at least 8 chunks per segment, at most 16 segments.
+inline int seg_count(int BH, int NT) {
+  int g = (256 + BH - 1) / BH;
+  g = g < 16 ? g : 16;
+  const int gmax = (NT + 7) / 8;
+  g = g < gmax ? g : gmax;
+  return g < 1 ? 1 : g;
+}
+
+// MODE SEG_MAPS: blockIdx.z 0 builds P (start 0, with U), 1 builds Phi (start
+// I, U = 0); the end state goes to sout[(z * BH + bh) * G + g] ([DP][DP] fp32).
+// MODE SEG_FULL: the start state is sinit[bh * G + g] with leading dimension
+// sld (rows and columns >= sld read as 0); chunk-start states and residuals go
+// to the workspace, and the last segment's end state to ht ([DP][DP]-padded
+// rows/cols < D, leading dimension D).
+template <bool SP, int MODE>
+__global__ __launch_bounds__(256, 1) void chunk_seg_bf16(const float* __restrict__ beta, const float* __restrict__ alpha,
+                                                       int T, int H, int D, int NT, int CPS, Bf16Ws ws,
+                                                       const float* __restrict__ sinit, int sld,
+                                                       float* __restrict__ sout, float* __restrict__ ht) {
   constexpr int M = SP ? 2 * L : L;
-  constexpr int RTW = M / 64;       // residual row tiles per wave
-  constexpr int KS = DP / 32;       // k-steps over the key dim
-  constexpr int KSM = M / 32;       // k-steps over samples
+  constexpr int RT = M / 64;      // residual row tiles per wave
+  constexpr int KS = DP / 32;     // k-steps over the key dim
+  constexpr int KSM = M / 32;     // k-steps over samples
   constexpr int PM = M + 8;
-  __shared__ __align__(16) uint16_t Sh[16 * PB];   // S slice transposed [col][row], hi
-  __shared__ __align__(16) uint16_t Sl[16 * PB];
-  __shared__ __align__(16) uint16_t Rh[16 * PM];   // R' transposed [col][sample], hi
-  __shared__ __align__(16) uint16_t Rl[16 * PM];
+  constexpr int NC = DP / 16;     // column tiles
+  __shared__ __align__(16) uint16_t Sh[DP * PB];   // S transposed [col][row], hi
+  __shared__ __align__(16) uint16_t Sl[DP * PB];
+  __shared__ __align__(16) uint16_t Rh[DP * PM];   // R' transposed [col][sample], hi
+  __shared__ __align__(16) uint16_t Rl[DP * PM];
   __shared__ float lam[M];
   __shared__ float logd[L];
 
-  // grid (B*H, DP/16): the column slices of one head are B*H blocks apart, so
-  // with B*H a multiple of 8 they share an XCD (and its L2) and read each
-  // chunk's W / kappa^T once from the fabric.
-  const int bh = blockIdx.x, cs = blockIdx.y;
+  const int bh = blockIdx.x, g = blockIdx.y, G = gridDim.y, BH = gridDim.x;
+  const bool phi = MODE == SEG_MAPS && blockIdx.z == 1;   // block-uniform
   const int b = bh / H, h = bh % H;
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform
   const int lr = lane & 15, lg = lane >> 4;
-  const int col = 16 * cs + lr;
+  const int cb = g * CPS, ce = min(NT, cb + CPS);
 
-  f4 S[2];
+  // state rows 32w + 16u + 4lg + e, columns 16n + lr
+  f4 S[2][NC];
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int row = 16 * (2 * w + u) + 4 * lg + e;
-      S[u][e] = (h0 != nullptr && row < D && col < D) ? h0[((long)bh * D + row) * D + col] : 0.f;
+    for (int n = 0; n < NC; ++n) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = 32 * w + 16 * u + 4 * lg + e, col = 16 * n + lr;
+        float x = 0.f;
+        if (MODE == SEG_MAPS) x = (phi && row == col) ? 1.f : 0.f;
+        else if (sinit != nullptr && row < sld && col < sld) x = sinit[((long)(bh * G + g) * sld + row) * sld + col];
+        S[u][n][e] = x;
+      }
     }
   }
 
-  // per-chunk operand fragments (current and prefetched next)
-  uint4 wh[RTW][KS], wl[RTW][KS], kt[2][KSM];
-  f4 uu[RTW];
-  uint4 nwh[RTW][KS], nwl[RTW][KS], nkt[2][KSM];
-  f4 nuu[RTW];
+  // Per-chunk operand fragments, one set each: W and U are reloaded for the
+  // next chunk as soon as the residual products have used them, kappa^T as
+  // soon as the state update has, so each load has the rest of a chunk to land.
+  uint4 wh[RT][KS], wl[RT][KS], kt[2][KSM];
+  f4 uu[RT][NC];
   float nlogd = 0.f, nlam = 0.f;   // this thread's log-decay / write-strength entries of the next chunk
-  auto fetch = [&](int c) __attribute__((always_inline)) {
+  const bool use_u = !phi;
+  auto load_wu = [&](int c) __attribute__((always_inline)) {
     const long cidx = (long)bh * NT + c;
-    if (tid < L) nlogd = ws.logd[cidx * L + tid];
+    const uint16_t* Wh = ws.Whi + cidx * M * DP;
+    const uint16_t* Wl = ws.Wlo + cidx * M * DP;
+    const float* Uc = ws.U + cidx * M * DP;
+#pragma unroll
+    for (int u = 0; u < RT; ++u) {
+      const int I = RT * w + u;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        wh[u][s] = neg_bf16x8(*reinterpret_cast<const uint4*>(Wh + (16 * I + lr) * DP + 32 * s + 8 * lg));
+        wl[u][s] = neg_bf16x8(*reinterpret_cast<const uint4*>(Wl + (16 * I + lr) * DP + 32 * s + 8 * lg));
+      }
+#pragma unroll
+      for (int n = 0; n < NC; ++n) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) uu[u][n][e] = use_u ? Uc[(16 * I + 4 * lg + e) * DP + 16 * n + lr] : 0.f;
+      }
+    }
+  };
+  auto load_kt = [&](int c) __attribute__((always_inline)) {
+    const uint16_t* KTc = ws.KT + ((long)bh * NT + c) * DP * M;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+#pragma unroll
+      for (int s = 0; s < KSM; ++s)
+        kt[u][s] = *reinterpret_cast<const uint4*>(KTc + (32 * w + 16 * u + lr) * M + 32 * s + 8 * lg);
+    }
+  };
+  auto load_gates = [&](int c) __attribute__((always_inline)) {
+    if (tid < L) nlogd = ws.logd[((long)bh * NT + c) * L + tid];
     if (tid < M) {
       const int t = c * L + samp_t<SP>(tid);
       nlam = 0.f;
       if (t < T) nlam = samp_r<SP>(tid) ? alpha[(long)(b * T + t) * H + h] : beta[(long)(b * T + t) * H + h];
     }
-    const uint16_t* Wh = ws.Whi + cidx * M * DP;
-    const uint16_t* Wl = ws.Wlo + cidx * M * DP;
-    const float* Uc = ws.U + cidx * M * DP;
-    const uint16_t* KTc = ws.KT + cidx * DP * M;
-#pragma unroll
-    for (int u = 0; u < RTW; ++u) {
-      const int I = RTW * w + u;
-#pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        nwh[u][s] = *reinterpret_cast<const uint4*>(Wh + (16 * I + lr) * DP + 32 * s + 8 * lg);
-        nwl[u][s] = *reinterpret_cast<const uint4*>(Wl + (16 * I + lr) * DP + 32 * s + 8 * lg);
-      }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) nuu[u][e] = Uc[(16 * I + 4 * lg + e) * DP + col];
-    }
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-#pragma unroll
-      for (int s = 0; s < KSM; ++s)
-        nkt[u][s] = *reinterpret_cast<const uint4*>(KTc + (16 * (2 * w + u) + lr) * M + 32 * s + 8 * lg);
-    }
-  };
-  auto take = [&]() __attribute__((always_inline)) {
-    if (tid < L) logd[tid] = nlogd;
-    if (tid < M) lam[tid] = nlam;
-#pragma unroll
-    for (int u = 0; u < RTW; ++u) {
-      uu[u] = nuu[u];
-#pragma unroll
-      for (int s = 0; s < KS; ++s) { wh[u][s] = nwh[u][s]; wl[u][s] = nwl[u][s]; }
-    }
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-#pragma unroll
-      for (int s = 0; s < KSM; ++s) kt[u][s] = nkt[u][s];
-    }
   };
 
-  fetch(0);
-  for (int c = 0; c < NT; ++c) {
+  if (cb < ce) {
+    load_wu(cb);
+    load_kt(cb);
+    load_gates(cb);
+  }
+  for (int c = cb; c < ce; ++c) {
     const long cidx = (long)bh * NT + c;
-    take();   // logd / lam of this chunk into LDS (the previous chunk's readers passed a barrier)
-    if (c + 1 < NT) fetch(c + 1);
-    // chunk-start state: LDS operand copy and workspace copy (both transposed, hi/lo)
-    uint16_t* STh = ws.STh + cidx * DP * DP;
-    uint16_t* STl = ws.STl + cidx * DP * DP;
+    // logd / lam of this chunk into LDS (the previous chunk's readers passed a barrier)
+    if (tid < L) logd[tid] = nlogd;
+    if (tid < M) lam[tid] = nlam;
+    if (c + 1 < ce) load_gates(c + 1);
+    // chunk-start state: LDS operand copy, and the workspace copy K5 reads (both [col][row], hi/lo)
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      ushort4 hv, lv;
-      uint16_t hh[4], ll[4];
+      const int row0 = 32 * w + 16 * u + 4 * lg;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) split1(S[u][e], hh[e], ll[e]);
-      hv = make_ushort4(hh[0], hh[1], hh[2], hh[3]);
-      lv = make_ushort4(ll[0], ll[1], ll[2], ll[3]);
-      const int row0 = 16 * (2 * w + u) + 4 * lg;
-      *reinterpret_cast<ushort4*>(&Sh[lr * PB + row0]) = hv;
-      *reinterpret_cast<ushort4*>(&Sl[lr * PB + row0]) = lv;
-      *reinterpret_cast<ushort4*>(&STh[(long)col * DP + row0]) = hv;
-      *reinterpret_cast<ushort4*>(&STl[(long)col * DP + row0]) = lv;
+      for (int n = 0; n < NC; ++n) {
+        uint16_t hh[4], ll[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) split1(S[u][n][e], hh[e], ll[e]);
+        const ushort4 hv = make_ushort4(hh[0], hh[1], hh[2], hh[3]);
+        const ushort4 lv = make_ushort4(ll[0], ll[1], ll[2], ll[3]);
+        const int col = 16 * n + lr;
+        *reinterpret_cast<ushort4*>(&Sh[col * PB + row0]) = hv;
+        *reinterpret_cast<ushort4*>(&Sl[col * PB + row0]) = lv;
+        if constexpr (MODE == SEG_FULL) {
+          *reinterpret_cast<ushort4*>(&ws.STh[cidx * DP * DP + (long)col * DP + row0]) = hv;
+          *reinterpret_cast<ushort4*>(&ws.STl[cidx * DP * DP + (long)col * DP + row0]) = lv;
+        }
+      }
     }
     __syncthreads();
 
-    // R = U - W S  (W = Wh + Wl, S = Sh + Sl; the Wl.Sl term is dropped)
-    uint16_t* RTh = ws.RTh + cidx * DP * M;
-    uint16_t* RTl = ws.RTl + cidx * DP * M;
+    // R = U - W S (the W fragments are negated: acc = U + (-W) S; Wl.Sl dropped),
+    // one 16-column tile at a time (a scheduling barrier keeps the compiler from
+    // hoisting every tile's LDS operands at once)
     const float logdL = logd[L - 1];
 #pragma unroll
-    for (int u = 0; u < RTW; ++u) {
-      const int I = RTW * w + u;
-      f4 p = f4_zero();
-#pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        const uint4 bh_ = *reinterpret_cast<const uint4*>(&Sh[lr * PB + 32 * s + 8 * lg]);
-        const uint4 bl_ = *reinterpret_cast<const uint4*>(&Sl[lr * PB + 32 * s + 8 * lg]);
-        p = mma_bf16(as_bf8(wh[u][s]), as_bf8(bh_), p);
-        p = mma_bf16(as_bf8(wh[u][s]), as_bf8(bl_), p);
-        p = mma_bf16(as_bf8(wl[u][s]), as_bf8(bh_), p);
-      }
-      const f4 r = uu[u] - p;
-      uint16_t hh[4], ll[4], h2[4], l2[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int i = 16 * I + 4 * lg + e;
-        split1(r[e], hh[e], ll[e]);
-        split1(r[e] * lam[i] * expf(logdL - logd[samp_t<SP>(i)]), h2[e], l2[e]);
-      }
+    for (int u = 0; u < RT; ++u) {
+      const int I = RT * w + u;
       const int i0 = 16 * I + 4 * lg;
-      *reinterpret_cast<ushort4*>(&RTh[(long)col * M + i0]) = make_ushort4(hh[0], hh[1], hh[2], hh[3]);
-      *reinterpret_cast<ushort4*>(&RTl[(long)col * M + i0]) = make_ushort4(ll[0], ll[1], ll[2], ll[3]);
-      *reinterpret_cast<ushort4*>(&Rh[lr * PM + i0]) = make_ushort4(h2[0], h2[1], h2[2], h2[3]);
-      *reinterpret_cast<ushort4*>(&Rl[lr * PM + i0]) = make_ushort4(l2[0], l2[1], l2[2], l2[3]);
+      float fac[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) fac[e] = lam[i0 + e] * expf(logdL - logd[samp_t<SP>(i0 + e)]);
+#pragma unroll
+      for (int n = 0; n < NC; ++n) {
+        f4 r = uu[u][n];
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          const uint4 bh_ = *reinterpret_cast<const uint4*>(&Sh[(16 * n + lr) * PB + 32 * s + 8 * lg]);
+          const uint4 bl_ = *reinterpret_cast<const uint4*>(&Sl[(16 * n + lr) * PB + 32 * s + 8 * lg]);
+          r = mma_bf16(as_bf8(wh[u][s]), as_bf8(bh_), r);
+          r = mma_bf16(as_bf8(wh[u][s]), as_bf8(bl_), r);
+          r = mma_bf16(as_bf8(wl[u][s]), as_bf8(bh_), r);
+        }
+        const int col = 16 * n + lr;
+        uint16_t hh[4], ll[4], h2[4], l2[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          split1(r[e], hh[e], ll[e]);
+          split1(r[e] * fac[e], h2[e], l2[e]);
+        }
+        if constexpr (MODE == SEG_FULL) {
+          *reinterpret_cast<ushort4*>(&ws.RTh[cidx * DP * M + (long)col * M + i0]) = make_ushort4(hh[0], hh[1], hh[2], hh[3]);
+          *reinterpret_cast<ushort4*>(&ws.RTl[cidx * DP * M + (long)col * M + i0]) = make_ushort4(ll[0], ll[1], ll[2], ll[3]);
+        }
+        *reinterpret_cast<ushort4*>(&Rh[col * PM + i0]) = make_ushort4(h2[0], h2[1], h2[2], h2[3]);
+        *reinterpret_cast<ushort4*>(&Rl[col * PM + i0]) = make_ushort4(l2[0], l2[1], l2[2], l2[3]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
+    if (c + 1 < ce) load_wu(c + 1);
     __syncthreads();
 
     // S <- D_L S + kappa^T R'
     const float DL = expf(logdL);
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      f4 acc = S[u] * DL;
+    for (int n = 0; n < NC; ++n) {
 #pragma unroll
-      for (int s = 0; s < KSM; ++s) {
-        const uint4 rh = *reinterpret_cast<const uint4*>(&Rh[lr * PM + 32 * s + 8 * lg]);
-        const uint4 rl = *reinterpret_cast<const uint4*>(&Rl[lr * PM + 32 * s + 8 * lg]);
-        acc = mma_bf16(as_bf8(kt[u][s]), as_bf8(rh), acc);
-        acc = mma_bf16(as_bf8(kt[u][s]), as_bf8(rl), acc);
+      for (int u = 0; u < 2; ++u) {
+        f4 acc = S[u][n] * DL;
+#pragma unroll
+        for (int s = 0; s < KSM; ++s) {
+          const uint4 rh = *reinterpret_cast<const uint4*>(&Rh[(16 * n + lr) * PM + 32 * s + 8 * lg]);
+          const uint4 rl = *reinterpret_cast<const uint4*>(&Rl[(16 * n + lr) * PM + 32 * s + 8 * lg]);
+          acc = mma_bf16(as_bf8(kt[u][s]), as_bf8(rh), acc);
+          acc = mma_bf16(as_bf8(kt[u][s]), as_bf8(rl), acc);
+        }
+        S[u][n] = acc;
       }
-      S[u] = acc;
+      __builtin_amdgcn_sched_barrier(0);
     }
+    if (c + 1 < ce) load_kt(c + 1);
   }
 
-  if (ht != nullptr) {
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+#pragma unroll
+    for (int n = 0; n < NC; ++n) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = 32 * w + 16 * u + 4 * lg + e, col = 16 * n + lr;
+        if constexpr (MODE == SEG_MAPS) {
+          sout[((long)((blockIdx.z * BH + bh) * G + g) * DP + row) * DP + col] = S[u][n][e];
+        } else {
+          if (ht != nullptr && g == G - 1 && row < D && col < D) ht[((long)bh * D + row) * D + col] = S[u][n][e];
+        }
+      }
+    }
+  }
+}
+
+// The segment start states: sinit[bh*G + g] for g < G, from h0 ([B*H][D][D] or
+// NULL) and the maps of chunk_seg_bf16<SEG_MAPS> (maps[0]: P, maps[1]: Phi).
+// S <- Phi S + P runs in fp32 with Phi and S split into bf16 hi + lo.
+__global__ __launch_bounds__(256, 1) void chunk_seg_scan_bf16(int G, int D, const float* __restrict__ h0,
+                                                            const float* __restrict__ maps, float* __restrict__ sinit) {
+  constexpr int NC = DP / 16;
+  constexpr int KS = DP / 32;
+  __shared__ __align__(16) uint16_t Sh[DP * PB];   // S transposed [col][row], hi
+  __shared__ __align__(16) uint16_t Sl[DP * PB];
+  const int bh = blockIdx.x, BH = gridDim.x;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lr = lane & 15, lg = lane >> 4;
+  const float* P = maps;
+  const float* Phi = maps + (long)BH * G * DP * DP;
+  f4 S[2][NC];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+#pragma unroll
+    for (int n = 0; n < NC; ++n) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = 32 * w + 16 * u + 4 * lg + e, col = 16 * n + lr;
+        S[u][n][e] = (h0 != nullptr && row < D && col < D) ? h0[((long)bh * D + row) * D + col] : 0.f;
+      }
+    }
+  }
+  for (int g = 0; g < G; ++g) {
+    float* dst = sinit + (long)(bh * G + g) * DP * DP;
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int row = 16 * (2 * w + u) + 4 * lg + e;
-        if (row < D && col < D) ht[((long)bh * D + row) * D + col] = S[u][e];
+      for (int n = 0; n < NC; ++n) {
+        const int row0 = 32 * w + 16 * u + 4 * lg, col = 16 * n + lr;
+        uint16_t hh[4], ll[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          dst[(long)(row0 + e) * DP + col] = S[u][n][e];
+          split1(S[u][n][e], hh[e], ll[e]);
+        }
+        *reinterpret_cast<ushort4*>(&Sh[col * PB + row0]) = make_ushort4(hh[0], hh[1], hh[2], hh[3]);
+        *reinterpret_cast<ushort4*>(&Sl[col * PB + row0]) = make_ushort4(ll[0], ll[1], ll[2], ll[3]);
       }
     }
+    if (g + 1 == G) break;
+    __syncthreads();
+    const float* Pg = P + (long)(bh * G + g) * DP * DP;
+    const float* Fg = Phi + (long)(bh * G + g) * DP * DP;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int rowA = 32 * w + 16 * u + lr;   // A operand row (Phi)
+      uint4 ah[KS], al[KS];
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        float x[8];
+        const float4 x0 = *reinterpret_cast<const float4*>(Fg + (long)rowA * DP + 32 * s + 8 * lg);
+        const float4 x1 = *reinterpret_cast<const float4*>(Fg + (long)rowA * DP + 32 * s + 8 * lg + 4);
+        x[0] = x0.x; x[1] = x0.y; x[2] = x0.z; x[3] = x0.w; x[4] = x1.x; x[5] = x1.y; x[6] = x1.z; x[7] = x1.w;
+        split8(x, ah[s], al[s]);
+      }
+#pragma unroll
+      for (int n = 0; n < NC; ++n) {
+        f4 acc;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] = Pg[(long)(32 * w + 16 * u + 4 * lg + e) * DP + 16 * n + lr];
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          const uint4 bh_ = *reinterpret_cast<const uint4*>(&Sh[(16 * n + lr) * PB + 32 * s + 8 * lg]);
+          const uint4 bl_ = *reinterpret_cast<const uint4*>(&Sl[(16 * n + lr) * PB + 32 * s + 8 * lg]);
+          acc = mma_bf16(as_bf8(ah[s]), as_bf8(bh_), acc);
+          acc = mma_bf16(as_bf8(ah[s]), as_bf8(bl_), acc);
+          acc = mma_bf16(as_bf8(al[s]), as_bf8(bh_), acc);
+        }
+        S[u][n] = acc;
+      }
+    }
+    __syncthreads();   // Sh/Sl are rewritten next
   }
 }
 
@@ -582,7 +728,9 @@ size_t chunk_bf16_workspace_bytes(int B, int T, int H, int has_sparse) {
   total += 2 * n * DP * DP * 2;    // STh, STl
   total += 2 * n * DP * M * 2;     // RTh, RTl
   total += n * L * 4;              // logd
-  return total + 256 * 10;
+  const size_t G = seg_count(B * H, (int)NT);
+  if (G > 1) total += 3 * (size_t)B * H * G * DP * DP * 4;   // segment maps P, Phi and start states
+  return total + 256 * 12;
 }
 
 template <bool SP>
@@ -601,16 +749,28 @@ static hipError_t launch_bf16_t(const ChunkArgs& a, hipStream_t st) {
   ws.STl = (uint16_t*)p; p = align(p + n * DP * DP * 2);
   ws.RTh = (uint16_t*)p; p = align(p + n * DP * M * 2);
   ws.RTl = (uint16_t*)p; p = align(p + n * DP * M * 2);
-  ws.logd = (float*)p;
+  ws.logd = (float*)p;    p = align(p + n * L * 4);
   const int BH = a.B * a.H;
+  const int G = seg_count(BH, NT);
+  const int CPS = (NT + G - 1) / G;
+  float* maps = (float*)p;   // [2][BH][G][DP][DP]: P, Phi
+  float* sinit = maps + 2 * (size_t)BH * G * DP * DP;
   const bf16_t* q = (const bf16_t*)a.q;
   const bf16_t* k = (const bf16_t*)a.k;
   const bf16_t* v = (const bf16_t*)a.v;
   const bf16_t* sk = (const bf16_t*)a.sparse_k;
   const bf16_t* sv = (const bf16_t*)a.sparse_v;
   chunk_intra_bf16<SP><<<dim3(NT, BH), 256, 0, st>>>(k, v, sk, sv, a.beta, a.alpha, a.gamma, a.T, a.H, a.D, NT, ws);
-  chunk_state_bf16<SP><<<dim3(BH, DP / 16), 256, 0, st>>>(a.beta, a.alpha, a.initial_state, a.T, a.H, a.D, NT, ws,
-                                                         a.final_state);
+  if (G == 1) {
+    chunk_seg_bf16<SP, SEG_FULL><<<dim3(BH, 1, 1), 256, 0, st>>>(a.beta, a.alpha, a.T, a.H, a.D, NT, NT, ws,
+                                                               a.initial_state, a.D, nullptr, a.final_state);
+  } else {
+    chunk_seg_bf16<SP, SEG_MAPS><<<dim3(BH, G, 2), 256, 0, st>>>(a.beta, a.alpha, a.T, a.H, a.D, NT, CPS, ws, nullptr,
+                                                               0, maps, nullptr);
+    chunk_seg_scan_bf16<<<dim3(BH), 256, 0, st>>>(G, a.D, a.initial_state, maps, sinit);
+    chunk_seg_bf16<SP, SEG_FULL><<<dim3(BH, G, 1), 256, 0, st>>>(a.beta, a.alpha, a.T, a.H, a.D, NT, CPS, ws, sinit,
+                                                               DP, nullptr, a.final_state);
+  }
   chunk_out_bf16<SP><<<dim3(NT, BH), 256, 0, st>>>(q, k, sk, a.beta, a.alpha, a.T, a.H, a.D, NT, ws,
                                                    (bf16_t*)a.out);
   return hipGetLastError();
