@@ -13,8 +13,10 @@
 // 16-byte loads (row-major W, transposed kappa / S / R).
 //
 // K3 chunk_intra_bf16  grid (NT, B*H)      Gram, T, (I+T)^-1, W = A D_tau kappa, U = A nu, kappa^T
-// K4 chunk_state_bf16  grid (B*H, DP/16)   sequential state pass; fragments of chunk c+1 are
-//                                          prefetched into registers while chunk c is processed
+// K4 chunk_seg_bf16    grid (B*H, G, 2|1)  state pass over G segments of chunks: per-segment affine
+//    chunk_seg_scan_bf16 grid (B*H)        maps, a scan over segments, then each segment replays its
+//                                          chunks from its start state (operands of chunk c+1 are
+//                                          prefetched into registers while chunk c is processed)
 // K5 chunk_out_bf16    grid (NT, B*H)      o = D Q S + P R
 #include "common.h"
 #include "kernels.h"
@@ -32,6 +34,15 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Workgroup barrier that orders LDS only: each wave waits for its own LDS
+// operations, not for global loads and stores still in flight (__syncthreads
+// waits for those too, which would stall register prefetches at the barrier).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 __device__ __forceinline__ bf16x8 as_bf8(uint4 u) { return __builtin_bit_cast(bf16x8, u); }
@@ -452,7 +463,7 @@ __global__ __launch_bounds__(256, 1) void chunk_seg_bf16(const float* __restrict
         }
       }
     }
-    __syncthreads();
+    lds_barrier();
 
     // R = U - W S (the W fragments are negated: acc = U + (-W) S; Wl.Sl dropped),
     // one 16-column tile at a time (a scheduling barrier keeps the compiler from
@@ -493,7 +504,7 @@ __global__ __launch_bounds__(256, 1) void chunk_seg_bf16(const float* __restrict
       }
     }
     if (c + 1 < ce) load_wu(c + 1);
-    __syncthreads();
+    lds_barrier();
 
     // S <- D_L S + kappa^T R'
     const float DL = expf(logdL);
