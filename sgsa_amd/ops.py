@@ -14,6 +14,9 @@ swapping the import.  Differences, all deliberate:
   definition (naive.py:40) also where a chunk-local prefix falls below 1e-6;
 * unsupported input (CPU tensors, float16, D > 128) raises instead of falling
   back to another implementation.
+
+The backward recomputes the forward in torch under autograd, as the
+reference's does (chunk_bwd.py:31-77); see ``backward.py``.
 """
 
 from __future__ import annotations
@@ -24,6 +27,7 @@ from typing import Optional, Tuple
 import torch
 
 from . import _abi
+from .backward import recompute_grads
 
 Tensor = torch.Tensor
 
@@ -92,8 +96,11 @@ def chunk_sgsa_fwd(
 class ChunkSGSAFunction(torch.autograd.Function):
     """Autograd wrapper with the reference's argument list (modelings/sgsa_ops/chunk.py:13-101).
 
-    Only the forward is native.  The backward (chunk_bwd.py, a torch recompute
-    in the reference) is not part of this library and raises.
+    The forward runs the HIP kernels.  The backward keeps the reference's
+    recompute semantics (chunk.py:58-101 -> chunk_bwd.py:31-77): the forward is
+    recomputed in torch under autograd (``backward.chunk_sgsa_torch``, the
+    function the kernels compute) and differentiated; it returns the 9 input
+    gradients (None for absent optionals) and None for the 5 flags.
     """
 
     @staticmethod
@@ -106,11 +113,18 @@ class ChunkSGSAFunction(torch.autograd.Function):
             alpha if has_sparse else None,
             initial_state if has_initial_state else None,
             chunk_size, output_final_state, use_triton)
+        ctx.save_for_backward(q, k, v, beta, gamma, sparse_k, sparse_v, alpha, initial_state)
+        ctx.has_sparse, ctx.has_initial_state = has_sparse, has_initial_state
         return out, final
 
     @staticmethod
     def backward(ctx, do, dht):
-        raise NotImplementedError("chunk_sgsa backward is not implemented by the HIP library (forward only)")
+        q, k, v, beta, gamma, sparse_k, sparse_v, alpha, initial_state = ctx.saved_tensors
+        hs, hi = ctx.has_sparse, ctx.has_initial_state
+        inputs = [q, k, v, beta, gamma, sparse_k if hs else None, sparse_v if hs else None, alpha if hs else None,
+                  initial_state if hi else None]
+        grads = recompute_grads(inputs, ctx.needs_input_grad[:9], do, dht)
+        return (*grads, None, None, None, None, None)
 
 
 def chunk_sgsa(

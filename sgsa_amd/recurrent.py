@@ -16,12 +16,13 @@ from typing import Optional, Tuple
 import torch
 
 from . import _abi
+from .backward import recompute_grads
 from .ops import _check_layout
 
 Tensor = torch.Tensor
 
 
-def fused_recurrent_sgsa(
+def recurrent_sgsa_fwd(
     q: Tensor,
     k: Tensor,
     v: Tensor,
@@ -32,9 +33,9 @@ def fused_recurrent_sgsa(
     alpha: Optional[Tensor] = None,
     initial_state: Optional[Tensor] = None,
     output_final_state: bool = False,
-    use_triton: bool = True,
 ) -> Tuple[Tensor, Optional[Tensor]]:
-    """q, k, v [B,T,H,D]; beta, gamma [B,T,H]; state [B,H,D,D] (float32 out)."""
+    """The HIP recurrent forward (sgsa_recurrent_fwd), no autograd.
+    q, k, v [B,T,H,D]; beta, gamma [B,T,H]; state [B,H,D,D] (float32 out)."""
     if not q.is_cuda:
         raise ValueError("fused_recurrent_sgsa: the SGSA kernels run on a ROCm GPU; got CPU tensors")
     B, T, H, D = q.shape
@@ -67,3 +68,65 @@ def fused_recurrent_sgsa(
         code, B, T, H, D, _abi.ptr(qc), _abi.ptr(kc), _abi.ptr(vc), _abi.ptr(bc), _abi.ptr(gc), _abi.ptr(skc),
         _abi.ptr(svc), _abi.ptr(ac), _abi.ptr(h0), _abi.ptr(out), _abi.ptr(ht), _abi.stream_of(qc)))
     return out, ht
+
+
+class FusedRecurrentSGSAFunction(torch.autograd.Function):
+    """Autograd wrapper of the recurrent op (modelings/sgsa_ops/recurrent.py:13-135).
+
+    The forward runs the HIP recurrent kernel.  The backward recomputes the
+    forward in torch under autograd and differentiates <o, do> + <S_T, dS_T>,
+    as the reference's does (recurrent.py:78-135); the recompute is the chunk
+    form of the same recurrence (``backward.chunk_sgsa_torch``).
+    """
+
+    @staticmethod
+    def forward(ctx, q, k, v, beta, gamma, sparse_k, sparse_v, alpha, initial_state, has_sparse,
+                has_initial_state, output_final_state):
+        out, final = recurrent_sgsa_fwd(
+            q, k, v, beta, gamma,
+            sparse_k if has_sparse else None,
+            sparse_v if has_sparse else None,
+            alpha if has_sparse else None,
+            initial_state if has_initial_state else None,
+            output_final_state)
+        ctx.save_for_backward(q, k, v, beta, gamma, sparse_k, sparse_v, alpha, initial_state)
+        ctx.has_sparse, ctx.has_initial_state = has_sparse, has_initial_state
+        return out, final
+
+    @staticmethod
+    def backward(ctx, do, dht):
+        q, k, v, beta, gamma, sparse_k, sparse_v, alpha, initial_state = ctx.saved_tensors
+        hs, hi = ctx.has_sparse, ctx.has_initial_state
+        inputs = [q, k, v, beta, gamma, sparse_k if hs else None, sparse_v if hs else None, alpha if hs else None,
+                  initial_state if hi else None]
+        grads = recompute_grads(inputs, ctx.needs_input_grad[:9], do, dht)
+        return (*grads, None, None, None)
+
+
+def fused_recurrent_sgsa(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    beta: Tensor,
+    gamma: Tensor,
+    sparse_k: Optional[Tensor] = None,
+    sparse_v: Optional[Tensor] = None,
+    alpha: Optional[Tensor] = None,
+    initial_state: Optional[Tensor] = None,
+    output_final_state: bool = False,
+    use_triton: bool = True,
+) -> Tuple[Tensor, Optional[Tensor]]:
+    """q, k, v [B,T,H,D]; beta, gamma [B,T,H]; state [B,H,D,D] (float32 out).
+    Differentiable: the backward recomputes in torch (FusedRecurrentSGSAFunction)."""
+    if not q.is_cuda:
+        raise ValueError("fused_recurrent_sgsa: the SGSA kernels run on a ROCm GPU; got CPU tensors")
+    has_sparse = sparse_k is not None and sparse_v is not None and alpha is not None
+    has_init = initial_state is not None
+    empty = torch.empty(0, device=q.device, dtype=q.dtype)
+    return FusedRecurrentSGSAFunction.apply(
+        q, k, v, beta, gamma,
+        sparse_k if has_sparse else empty,
+        sparse_v if has_sparse else empty,
+        alpha if has_sparse else torch.empty(0, device=q.device, dtype=beta.dtype),
+        initial_state if has_init else empty,
+        has_sparse, has_init, output_final_state)
