@@ -1547,6 +1547,461 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void s
   }   // !THR
 }
 
+// The largest float below x (x not -inf or NaN): s < x  <=>  s <= next_down(x)
+// for every score s that is not NaN.
+__device__ __forceinline__ float next_down(float x) {
+  const uint32_t u = __float_as_uint(x);
+  if ((u & 0x7fffffffu) == 0u) return __uint_as_float(0x80000001u);   // below +-0: -min denormal
+  return __uint_as_float((int32_t)u > 0 ? u - 1u : u + 1u);
+}
+
+// ---------------------------------------------------------------------------
+// K1, threshold form at 128 query rows per block (the layer path: bf16,
+// D = 128, counts that fit 16 bits).
+//
+// The selection of score_topk_tiles_kernel<true, THR = true> with twice the
+// rows per K tile.  Wave w owns keys [16w, 16w+16) of every 64-key tile for all
+// 128 rows of the block: its 16 keys are the MFMA A operand, loaded straight
+// into registers one tile ahead, and the block's q rows are the B operand,
+// resident in registers as 8 groups of 16 rows.  Both sweeps are bound by the
+// K bytes delivered into the CU, which this halves per score; the histogram
+// adds per score stay the same.  The operands of every product are those of the
+// 64-row kernel (A row rho holds key rho/4 + 4 (rho%4) of the wave's 16, the
+// same 32 dims per instruction), so the fp32 scores are identical.  Lane
+// (w, lg, lr) holds rows 16g + lr (g = 0..7) against keys kt*64 + 16w + lg + 4i.
+// Wave w does the per-row work (b*, thresholds, resolve, output) for row
+// groups w and w + 4.  A block with a row whose threshold bin overflows flags
+// both of its 64-row halves for the radix fallback launch of
+// score_topk_kernel<..., FB, LIST, THR>, which writes the same outputs.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nqb, float mscale) {
+  constexpr int QR = 128;
+  constexpr int NG = QR / 16;
+  constexpr int HW = NBIN / 2;   // 16-bit counter pairs per row
+  constexpr int CAPL = TOPK_CAP / 64;
+  __shared__ __align__(16) uint32_t hist[QR][HW];
+  __shared__ RowInfo rinfo[NG][16];
+  __shared__ int colcnt[NG][16];
+  __shared__ float qnorm[NG][16];
+
+  const int BH = a.B * a.H;
+  const int nqr = (a.Tq + QR - 1) / QR;
+  const int bid = blockIdx.x;
+  const int bh = bid % BH;
+  const int qb = nqr - 1 - bid / BH;   // heaviest (latest) row blocks first
+  const int b = bh / a.H, h = bh % a.H;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lr = lane & 15, lg = lane >> 4;
+  const int r0 = qb * QR;
+  const int Tq = a.Tq, Tk = a.Tk, H = a.H;
+  const uint16_t* kb = reinterpret_cast<const uint16_t*>(a.k);
+  const int topk = a.top_k;
+  // valid keys of row r0 + 16g + lr (0 for rows past Tq)
+  auto nv_of = [&](int g) __attribute__((always_inline)) {
+    const int qr = r0 + 16 * g + lr;
+    int nv = Tk;
+    if (a.causal) nv = max(0, min(Tk, qr + a.q_offset + 1));
+    return qr < Tq ? nv : 0;
+  };
+
+  // B operand: q^T of the block's rows; lane holds row r0 + 16g + lr, dims 32s + 8lg + [0, 8)
+  bf16x8 qf[NG][4];
+#pragma unroll
+  for (int g = 0; g < NG; ++g) {
+    const int qr = r0 + 16 * g + lr;
+    const uint16_t* qp = reinterpret_cast<const uint16_t*>(a.q) + ((long)(b * Tq + (qr < Tq ? qr : 0)) * H + h) * DP;
+    float qn2 = 0.f;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      u16x8 raw;
+      if (qr < Tq) raw = *reinterpret_cast<const u16x8*>(qp + 32 * s + 8 * lg);
+      else raw = (u16x8){0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float x = bf16_to_f32(raw[j]);
+        qn2 = fmaf(x, x, qn2);
+      }
+      qf[g][s] = __builtin_bit_cast(bf16x8, raw);
+    }
+    qn2 += __shfl_xor(qn2, 16, 64);
+    qn2 += __shfl_xor(qn2, 32, 64);
+    if ((g & 3) == w && lg == 0) qnorm[g][lr] = sqrtf(qn2);
+  }
+
+  // keys below minvalid are valid for every live row of the block
+  int minvalid = 0x7fffffff;
+#pragma unroll
+  for (int g = 0; g < NG; ++g)
+    if (r0 + 16 * g + lr < Tq) minvalid = min(minvalid, nv_of(g));
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) minvalid = min(minvalid, __shfl_xor(minvalid, o, 64));
+  minvalid = __builtin_amdgcn_readfirstlane(minvalid);   // block-uniform: tile tests branch on the scalar unit
+  int kend = Tk;
+  if (a.causal) kend = min(Tk, min(Tq, r0 + QR) - 1 + a.q_offset + 1);
+  const int ntile = kend > 0 ? (kend + KT - 1) / KT : 0;
+
+  // A operand: the wave's 16 keys of a tile; MFMA row lr holds key lr/4 + 4 (lr%4).
+  // Keys past Tk load key 0 instead: their scores are finite and never used (a
+  // tile with such keys is past minvalid, where every use checks j < nv <= Tk),
+  // and no select on the loaded data keeps the compiler from waiting for the
+  // prefetch right after issuing it.
+  const int krow = (lr >> 2) + 4 * (lr & 3);
+  bf16x8 kf[4];
+  auto kload = [&](int kt) __attribute__((always_inline)) {
+    const int j = kt * KT + 16 * w + krow;
+    const uint16_t* p = kb + ((long)(b * Tk + (j < Tk ? j : 0)) * H + h) * DP + 8 * lg;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) kf[s] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8*>(p + 32 * s));
+  };
+  // fn(kt, acc): acc[g][i] = score of row r0 + 16g + lr against key kt*64 + 16w + lg + 4i
+  auto sweep = [&](auto&& fn) __attribute__((always_inline)) {
+    if (ntile > 0) kload(0);
+    for (int kt = 0; kt < ntile; ++kt) {
+      f4 acc[NG];
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        f4 c = f4_zero();
+#pragma unroll
+        for (int s = 0; s < 4; ++s) c = mma_bf16(kf[s], qf[g][s], c);
+        acc[g] = score_of(c, mscale);
+      }
+      if (kt + 1 < ntile) kload(kt + 1);
+      fn(kt, acc);
+    }
+  };
+
+  // row set-up (wave w: rows of groups w and w + 4; lane < 32 -> group w + 4 (lane / 16), row lane % 16)
+  __syncthreads();   // qnorm visible
+  float kmx2 = lane < KNCH ? a.kmax[(long)bh * KNCH + lane] : 0.f;
+  const float kmx = sqrtf(wave_max(kmx2));
+  if (lane < 32) {
+    const int g = w + 4 * (lane >> 4), rr = lane & 15;
+    const int qr = r0 + 16 * g + rr;
+    int nv = 0;
+    if (qr < Tq) nv = a.causal ? max(0, min(Tk, qr + a.q_offset + 1)) : Tk;
+    RowInfo ri;
+    const float bound = qnorm[g][rr] * kmx * fabsf(mscale) * 1.001f;
+    ri.iw = (bound > 0.f && bound < FLT_MAX) ? 128.0f / bound : 0.f;
+    ri.bstar = -1;
+    ri.need = min(topk, nv);
+    ri.mode = (nv <= topk) ? SELECT_ALL : BIN_ALL;
+    ri.pfx = 0; ri.msk = 0; ri.done = 1; ri.th0 = -INFINITY; ri.th1 = -INFINITY;
+    rinfo[g][rr] = ri;
+    colcnt[g][rr] = 0;
+  }
+  for (int i = tid; i < QR * HW; i += 256) (&hist[0][0])[i] = 0;
+  __syncthreads();
+
+  // ---- pass A: block-shared row histograms and each row's top-2 ---------------
+  float m1[NG], m2[NG];   // top-2 of row 16g + lr over this lane's keys, then over the row
+#pragma unroll
+  for (int g = 0; g < NG; ++g) { m1[g] = -FLT_MAX; m2[g] = -FLT_MAX; }
+  {
+    float iw[NG];
+    uint32_t hmask = 0;   // bit g: row 16g + lr is live and needs a histogram
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      const RowInfo ri = rinfo[g][lr];
+      iw[g] = ri.iw;
+      if (r0 + 16 * g + lr < Tq && ri.mode != SELECT_ALL) hmask |= 1u << g;
+    }
+    const bool any_hist = __syncthreads_or(hmask != 0u);
+    auto bump = [&](int row, uint32_t bits) __attribute__((always_inline)) {
+      // word bin >> 1, half bin & 1; the shift 16 (bin & 1) is (bits << 4) mod 32
+      atomicAdd(&hist[row][__builtin_amdgcn_ubfe(bits, 1, 7)], 1u << ((bits << 4) & 31u));
+    };
+    auto top2 = [&](int g, float x) __attribute__((always_inline)) {
+      m2[g] = __builtin_amdgcn_fmed3f(m1[g], m2[g], x);
+      m1[g] = fmaxf(m1[g], x);
+    };
+    // Every block has a live row: the sweep gives the top-2 even where no row
+    // needs a histogram.  In full tiles every row's histogram takes the adds
+    // (rows that need none -- past Tq, or taking all their keys -- own rows
+    // nobody reads), so the adds need no per-row branch.
+    sweep([&](int kt, f4* acc) __attribute__((always_inline)) {
+      if ((kt + 1) * KT <= minvalid) {
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            top2(g, acc[g][i]);
+            if (any_hist) bump(16 * g + lr, score_bin_bits(acc[g][i], iw[g]));
+          }
+        }
+      } else {
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+          const int nv = nv_of(g);   // 0 for rows past Tq
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int j = kt * KT + 16 * w + lg + 4 * i;
+            top2(g, j < nv ? acc[g][i] : -FLT_MAX);
+            if (((hmask >> g) & 1u) && j < nv) bump(16 * g + lr, score_bin_bits(acc[g][i], iw[g]));
+          }
+        }
+      }
+    });
+    // top-2 over the row's lanes of this wave (lg)
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+#pragma unroll
+      for (int o = 16; o < 64; o <<= 1) {
+        const float b1 = __shfl_xor(m1[g], o, 64), b2 = __shfl_xor(m2[g], o, 64);
+        const float hi = fmaxf(m1[g], b1), lo = fmaxf(fminf(m1[g], b1), fmaxf(m2[g], b2));
+        m1[g] = hi; m2[g] = lo;
+      }
+    }
+    __syncthreads();
+    if (any_hist) {
+      for (int rr = 0; rr < 32; ++rr) {
+        const int g = w + 4 * (rr >> 4), r = rr & 15;
+        RowInfo ri = rinfo[g][r];
+        if (ri.mode == SELECT_ALL) continue;
+        const uint32_t* hr = hist[16 * g + r];
+        uint32_t c[4];
+        const uint32_t w0 = hr[127 - 2 * lane], w1 = hr[126 - 2 * lane];
+        c[0] = w0 >> 16; c[1] = w0 & 0xffffu; c[2] = w1 >> 16; c[3] = w1 & 0xffffu;
+        int bin;
+        uint32_t above, cnt;
+        find_bin(c, lane, (uint32_t)ri.need, bin, above, cnt);
+        if (lane == 0) {
+          ri.bstar = bin;
+          ri.need -= (int)above;
+          if (cnt == (uint32_t)ri.need) ri.mode = BIN_ALL;
+          else if (cnt <= (uint32_t)TOPK_CAP) ri.mode = COLLECT;
+          else ri.mode = RADIX;
+          rinfo[g][r] = ri;
+        }
+      }
+    }
+    __syncthreads();
+    int overflow = 0;
+    if (lane < 32) overflow = rinfo[w + 4 * (lane >> 4)][lane & 15].mode == RADIX;
+    overflow = __syncthreads_or(overflow);
+    if (tid < 2) {   // both 64-row halves, as the fallback launch indexes its blocks
+      const int q64 = 2 * qb + tid;
+      if (q64 < nqb) a.flags[(long)(nqb - 1 - q64) * BH + bh] = overflow;
+    }
+    if (overflow) return;   // block-uniform; the fallback launch redoes both halves
+  }
+
+  // top-2 over the waves, through LDS (the histograms are no longer needed)
+  float2* t2s = reinterpret_cast<float2*>(&hist[0][0]);   // [wave][128 rows]
+  if (lg == 0) {
+#pragma unroll
+    for (int g = 0; g < NG; ++g) t2s[QR * w + 16 * g + lr] = make_float2(m1[g], m2[g]);
+  }
+  __syncthreads();
+  float2 t2 = make_float2(-FLT_MAX, -FLT_MAX);   // lane < 32: row 16 (w + 4 (lane / 16)) + lane % 16
+  if (lane < 32) {
+    const int row = 16 * (w + 4 * (lane >> 4)) + (lane & 15);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const float2 o = t2s[QR * v + row];
+      const float hi = fmaxf(t2.x, o.x), lo = fmaxf(fminf(t2.x, o.x), fmaxf(t2.y, o.y));
+      t2.x = hi; t2.y = lo;
+    }
+  }
+
+  // ---- thresholds for pass B ---------------------------------------------------
+  int any_collect = 0;
+  if (lane < 32) {
+    const int g = w + 4 * (lane >> 4), r = lane & 15;
+    RowInfo ri = rinfo[g][r];
+    float t0 = -INFINITY, t1 = -INFINITY;
+    if (ri.mode != SELECT_ALL) {
+      const float lo_b = ri.bstar > 0 ? bin_lower_edge(ri.bstar, ri.iw) : -INFINITY;
+      const float hi_b = ri.bstar < NBIN - 1 ? bin_lower_edge(ri.bstar + 1, ri.iw) : INFINITY;
+      if (ri.mode == BIN_ALL) { t0 = lo_b; t1 = lo_b; }
+      else { t0 = lo_b; t1 = hi_b; }   // COLLECT
+    }
+    ri.th0 = t0; ri.th1 = t1;
+    rinfo[g][r] = ri;
+    any_collect = ri.mode == COLLECT;
+  }
+  // ---- pass B: threshold-bin candidates (blocks with a row to collect) -----------
+  uint2* scratch = a.scratch;
+  const long srowb = (long)bh * Tq + r0;   // global row of the block's row 0
+  if (__syncthreads_or(any_collect)) {
+    // candidate of row 16g + lr: th0 <= s < th1, i.e. med3(s, lo, hi) == s with
+    // lo = th0, hi = the float below th1; rows that collect nothing take
+    // lo = hi = +inf, which no finite score matches
+    float tlo[NG], thi[NG];
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      const RowInfo ri = rinfo[g][lr];
+      const bool col = r0 + 16 * g + lr < Tq && ri.mode == COLLECT;
+      tlo[g] = col ? ri.th0 : INFINITY;
+      thi[g] = col ? next_down(ri.th1) : INFINITY;
+    }
+    // A tile's candidates are staged in LDS, each lane in a column of its own
+    // (entry r of lane l at 64 r + l: a lane meets at most 32 per tile, and the
+    // histogram area is free -- 32 of its rows per wave), then each takes a slot
+    // in its row's scratch list through an LDS atomic and is stored, four
+    // entries per lane at a time.  Entry: {score bits, g << 16 | key} (the row
+    // is 16g + lr of the lane that staged and flushes it); keys fit 16 bits
+    // (Tk <= 65535 on this path).
+    uint2* ebuf = reinterpret_cast<uint2*>(&hist[32 * w][0]);
+    uint32_t* rowcnt = reinterpret_cast<uint32_t*>(&colcnt[0][0]);   // row 16g + lr at 16g + lr
+    sweep([&](int kt, f4* acc) __attribute__((always_inline)) {
+      uint32_t kc = 0;   // this lane's staged entries
+      // Where any lane of the wave has a candidate, every lane writes its entry
+      // at its next position and only candidates keep theirs (advance kc): the
+      // others are overwritten or lie past kc.  No exec-mask changes per score.
+      auto stage = [&](bool cand, int g, float sc, int j) __attribute__((always_inline)) {
+        if (ballot64(cand) != 0ull) {
+          ebuf[64 * kc + lane] = make_uint2(__float_as_uint(sc), ((uint32_t)g << 16) | (uint32_t)j);
+          kc += cand ? 1u : 0u;
+        }
+      };
+      if ((kt + 1) * KT <= minvalid) {
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float sc = acc[g][i];
+            stage(__builtin_amdgcn_fmed3f(sc, tlo[g], thi[g]) == sc, g, sc, kt * KT + 16 * w + lg + 4 * i);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+          const int nv = nv_of(g);   // 0 for rows past Tq
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int j = kt * KT + 16 * w + lg + 4 * i;
+            const float sc = acc[g][i];
+            stage((__builtin_amdgcn_fmed3f(sc, tlo[g], thi[g]) == sc) & (j < nv), g, sc, j);
+          }
+        }
+      }
+      if (ballot64(kc != 0u) != 0ull) {
+        wave_lds_sync();   // this wave's buffer writes before its reads
+        for (uint32_t r0e = 0; ballot64(r0e < kc) != 0ull; r0e += 4) {
+          uint2 e[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+            if (r0e + u < kc) e[u] = ebuf[64 * (r0e + u) + lane];
+          uint32_t slot[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+            if (r0e + u < kc) slot[u] = atomicAdd(rowcnt + 16 * (e[u].y >> 16) + lr, 1u);
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+            if (r0e + u < kc && slot[u] < (uint32_t)TOPK_CAP)
+              scratch[(srowb + 16 * (e[u].y >> 16) + lr) * TOPK_CAP + slot[u]] = make_uint2(e[u].x, e[u].y & 0xffffu);
+        }
+        wave_lds_sync();   // reads done before the next tile's writes
+      }
+    });
+  }
+  __syncthreads();   // candidates and counters of every wave are in place; hist is the resolve's area
+
+  // ---- resolve: the exact cut of every COLLECT row of the wave --------------
+  uint32_t* h256 = &hist[32 * w][0];   // 256 words of the wave's own rows
+  float thv = -INFINITY;   // lane rr < 32: row (group w + 4 (rr / 16), rr % 16)
+  int cutv = 0x7fffffff;
+  for (int rr = 0; rr < 32; ++rr) {
+    const int g = w + 4 * (rr >> 4), r = rr & 15;
+    const RowInfo ri = rinfo[g][r];
+    if (ri.mode == BIN_ALL && lane == rr) thv = ri.th0;   // everything from the bin's lower edge up
+    if (ri.mode != COLLECT) continue;
+    const long row = srowb + 16 * g + r;
+    const int n = min(colcnt[g][r], TOPK_CAP);
+    uint32_t key[CAPL];
+    int idx[CAPL];
+#pragma unroll
+    for (int m = 0; m < CAPL; ++m) {
+      const int p = 64 * m + lane;
+      key[m] = 0; idx[m] = 0;
+      if (p < n) {
+        const uint2 v = scratch[row * TOPK_CAP + p];
+        key[m] = f32_order_key(__uint_as_float(v.x));
+        idx[m] = (int)v.y;
+      }
+    }
+    // every collected key lies in [key(th0), key(th1) - 1]: the bytes those two
+    // share are the same for all of them and need no pass
+    const uint32_t klo = f32_order_key(ri.th0), dif = klo ^ (f32_order_key(ri.th1) - 1u);
+    uint32_t rm = 0;
+    int sh = 24;
+    while (sh > 0 && (dif >> sh) == 0u) { rm |= 0xffu << sh; sh -= 8; }
+    uint32_t rp = klo & rm;
+    uint32_t rneed = (uint32_t)ri.need;
+    for (; sh >= 0; sh -= 8) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) h256[4 * lane + q] = 0;
+      wave_lds_sync();
+#pragma unroll
+      for (int m = 0; m < CAPL; ++m) {
+        if (64 * m + lane < n && (key[m] & rm) == rp) atomicAdd(&h256[(key[m] >> sh) & 255u], 1u);
+      }
+      wave_lds_sync();
+      uint32_t c[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) c[q] = h256[255 - 4 * lane - q];
+      int bin;
+      uint32_t above, cnt;
+      find_bin(c, lane, rneed, bin, above, cnt);
+      rp |= (uint32_t)bin << sh;
+      rm |= 0xffu << sh;
+      rneed -= above;
+      wave_lds_sync();
+      if (cnt == rneed) break;
+    }
+    // Keys at the threshold key rp: the rneed with the smallest key index win;
+    // a radix select over ~index finds the last of them when more are equal.
+    uint32_t neq = 0;
+#pragma unroll
+    for (int m = 0; m < CAPL; ++m) neq += (uint32_t)__popcll(ballot64(64 * m + lane < n && (key[m] & rm) == rp));
+    uint32_t ip = 0;
+    if (neq > rneed) {
+      uint32_t im = 0, need2 = rneed;
+      for (int sh2 = 24; sh2 >= 0; sh2 -= 8) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) h256[4 * lane + q] = 0;
+        wave_lds_sync();
+#pragma unroll
+        for (int m = 0; m < CAPL; ++m) {
+          const uint32_t ik = ~(uint32_t)idx[m];
+          if (64 * m + lane < n && (key[m] & rm) == rp && (ik & im) == ip) atomicAdd(&h256[(ik >> sh2) & 255u], 1u);
+        }
+        wave_lds_sync();
+        uint32_t c[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) c[q] = h256[255 - 4 * lane - q];
+        int bin;
+        uint32_t above, cnt;
+        find_bin(c, lane, need2, bin, above, cnt);
+        ip |= (uint32_t)bin << sh2;
+        im |= 0xffu << sh2;
+        need2 -= above;
+        wave_lds_sync();
+        if (cnt == need2) break;
+      }
+    }
+    // selected: key > rp (rp's low bits are zero when the loop stopped early), or
+    // key == rp and ~index >= ip, i.e. index <= ~ip
+    if (lane == rr) {
+      thv = threshold_of_key(rp);
+      cutv = neq > rneed ? (int)~ip : 0x7fffffff;
+    }
+  }
+  if (lane < 32) {
+    const int g = w + 4 * (lane >> 4), r = lane & 15;
+    const int qr = r0 + 16 * g + r;
+    if (qr < Tq) {
+      const long rowg = srowb + 16 * g + r;
+      const int nv = a.causal ? max(0, min(Tk, qr + a.q_offset + 1)) : Tk;
+      a.thr[rowg] = make_uint2(__float_as_uint(thv), (uint32_t)cutv);
+      if (a.counts) a.counts[rowg] = min(topk, nv);
+      if (a.split) a.split[rowg] = 0;
+      a.top2[2 * rowg] = t2.x;
+      a.top2[2 * rowg + 1] = t2.y;
+    }
+  }
+}
+
 size_t topk_workspace_bytes(int B, int Tq, int H) {
   const size_t nqb = (Tq + QB - 1) / QB;
   return (size_t)B * H * Tq * TOPK_CAP * sizeof(uint2) + (((size_t)B * H * nqb * sizeof(int) + 255) & ~(size_t)255) +
@@ -1595,7 +2050,8 @@ hipError_t launch_score_topk(const TopkArgs& a0, hipStream_t st) {
   if (a.thr != nullptr) {   // layer path, threshold mode (bf16, D = 128, top-2 required)
     if (a.dtype != DT_BF16 || !t2 || a.D != DP) return hipErrorInvalidValue;
     if (c16) {
-      score_topk_tiles_kernel<true, true><<<grid, 256, 0, st>>>(a, nqb, ms);
+      const dim3 grid128((unsigned)(BH * ((a.Tq + 127) / 128)));
+      score_thr128_kernel<<<grid128, 256, 0, st>>>(a, nqb, ms);
       score_topk_kernel<bf16_t, false, true, true, true, true, true><<<grid, 256, 0, st>>>(a, nqb, ms);
     } else {
       score_topk_tiles_kernel<false, true><<<grid, 256, 0, st>>>(a, nqb, ms);
