@@ -80,6 +80,7 @@ __device__ __forceinline__ void load_k_tile(typename KTile<X>::T* ks, const X* _
 
 struct RowInfo {
   float iw;          // bin scale
+  float bc;          // bin offset (score_bin_bits); set by score_thr128_kernel only
   int bstar;         // threshold bin
   int need;          // still to take at the current resolution
   int mode;          // RowMode
@@ -88,13 +89,17 @@ struct RowInfo {
   float th0, th1;    // pass B: select s >= th1; collect th0 <= s < th1
 };
 
-// bin(s) = round(s * iw + 128) clamped to [0, 255], read from the mantissa of
-// 2^23 + x (no float-to-int conversion).  Monotone non-decreasing in s, which is
-// all the exact select needs; NaN lands in bin 0.
-__device__ __forceinline__ uint32_t score_bin_bits(float s, float iw) {
-  return __float_as_uint(__builtin_amdgcn_fmed3f(fmaf(s, iw, 8388736.0f), 8388608.0f, 8388863.0f));
+// bin(s) = round(s * iw + bc - 2^23) clamped to [0, 255], read from the mantissa
+// of fma(s, iw, bc) (no float-to-int conversion); bc = 2^23 + 128 centres the
+// bins on 0.  Monotone non-decreasing in s for iw > 0, which is all the exact
+// select needs; NaN lands in bin 0.
+constexpr float BIN_C0 = 8388736.0f;
+__device__ __forceinline__ uint32_t score_bin_bits(float s, float iw, float bc = BIN_C0) {
+  return __float_as_uint(__builtin_amdgcn_fmed3f(fmaf(s, iw, bc), 8388608.0f, 8388863.0f));
 }
-__device__ __forceinline__ int score_bin(float s, float iw) { return (int)(score_bin_bits(s, iw) & 255u); }
+__device__ __forceinline__ int score_bin(float s, float iw, float bc = BIN_C0) {
+  return (int)(score_bin_bits(s, iw, bc) & 255u);
+}
 
 
 // The float threshold t of a key bound: for finite scores s, s >= t <=> key(s) >= k.
@@ -106,11 +111,11 @@ __device__ __forceinline__ float threshold_of_key(uint32_t k) {
 
 // Smallest float s with score_bin(s, iw) >= bt (1 <= bt <= 255), by bisection over
 // the order-preserving keys between -inf and +inf (score_bin is monotone in s).
-__device__ __forceinline__ float bin_lower_edge(int bt, float iw) {
+__device__ __forceinline__ float bin_lower_edge(int bt, float iw, float bc = BIN_C0) {
   uint32_t lo = 0x007fffffu, hi = 0xff800000u;   // keys of -inf and +inf
   while (hi - lo > 1u) {
     const uint32_t mid = lo + ((hi - lo) >> 1);
-    if (score_bin(key_to_f32(mid), iw) >= bt) hi = mid;
+    if (score_bin(key_to_f32(mid), iw, bc) >= bt) hi = mid;
     else lo = mid;
   }
   return key_to_f32(hi);
@@ -1682,12 +1687,80 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
     RowInfo ri;
     const float bound = qnorm[g][rr] * kmx * fabsf(mscale) * 1.001f;
     ri.iw = (bound > 0.f && bound < FLT_MAX) ? 128.0f / bound : 0.f;
+    ri.bc = BIN_C0;
     ri.bstar = -1;
     ri.need = min(topk, nv);
     ri.mode = (nv <= topk) ? SELECT_ALL : BIN_ALL;
     ri.pfx = 0; ri.msk = 0; ri.done = 1; ri.th0 = -INFINITY; ri.th1 = -INFINITY;
     rinfo[g][rr] = ri;
     colcnt[g][rr] = 0;
+  }
+  __syncthreads();
+
+  // ---- the bins' range from a sample -------------------------------------------
+  // The bound above spans the Cauchy-Schwarz range; scores typically fill a
+  // third of it, so the threshold bin holds several times the keys it needs to.
+  // The min and max of each row's scores over 8 tiles spread across the sweep,
+  // widened by a quarter of their span on each side, set finer bins where they
+  // are finer than the bound's.  Any monotone map keeps the selection exact; a
+  // row it misjudges (a bin with more than TOPK_CAP keys) goes to the radix
+  // fallback like any other.
+  {
+    constexpr int NS = 8;
+    float lo[NG], hi[NG];
+#pragma unroll
+    for (int g = 0; g < NG; ++g) { lo[g] = FLT_MAX; hi[g] = -FLT_MAX; }
+    const int ns = min(ntile, NS);
+    for (int t = 0; t < ns; ++t) {
+      const int kt = (int)(((long)t * ntile) / ns);
+      kload(kt);
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        f4 c = f4_zero();
+#pragma unroll
+        for (int s = 0; s < 4; ++s) c = mma_bf16(kf[s], qf[g][s], c);
+        const f4 sc = score_of(c, mscale);
+        const int nv = nv_of(g);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const bool ok = kt * KT + 16 * w + lg + 4 * i < nv;
+          lo[g] = fminf(lo[g], ok ? sc[i] : FLT_MAX);
+          hi[g] = fmaxf(hi[g], ok ? sc[i] : -FLT_MAX);
+        }
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+#pragma unroll
+      for (int o = 16; o < 64; o <<= 1) {
+        lo[g] = fminf(lo[g], __shfl_xor(lo[g], o, 64));
+        hi[g] = fmaxf(hi[g], __shfl_xor(hi[g], o, 64));
+      }
+    }
+    float2* rg = reinterpret_cast<float2*>(&hist[0][0]);   // [wave][128 rows]
+    if (lg == 0) {
+#pragma unroll
+      for (int g = 0; g < NG; ++g) rg[QR * w + 16 * g + lr] = make_float2(lo[g], hi[g]);
+    }
+    __syncthreads();
+    if (lane < 32) {
+      const int g = w + 4 * (lane >> 4), r = lane & 15;
+      float l = FLT_MAX, h = -FLT_MAX;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const float2 o = rg[QR * v + 16 * g + r];
+        l = fminf(l, o.x); h = fmaxf(h, o.y);
+      }
+      RowInfo ri = rinfo[g][r];
+      const float sp = h - l;
+      if (l < h && sp < FLT_MAX) {
+        const float l2 = l - 0.25f * sp, iw2 = 255.0f / (1.5f * sp);
+        const float bc2 = 8388608.0f - l2 * iw2;
+        if (iw2 > ri.iw && iw2 < FLT_MAX && fabsf(bc2) < 1.0e30f) { ri.iw = iw2; ri.bc = bc2; }
+      }
+      rinfo[g][r] = ri;
+    }
+    __syncthreads();   // the range sums are read before hist is cleared
   }
   for (int i = tid; i < QR * HW; i += 256) (&hist[0][0])[i] = 0;
   __syncthreads();
@@ -1697,12 +1770,13 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
 #pragma unroll
   for (int g = 0; g < NG; ++g) { m1[g] = -FLT_MAX; m2[g] = -FLT_MAX; }
   {
-    float iw[NG];
+    float iw[NG], bc[NG];
     uint32_t hmask = 0;   // bit g: row 16g + lr is live and needs a histogram
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
       const RowInfo ri = rinfo[g][lr];
       iw[g] = ri.iw;
+      bc[g] = ri.bc;
       if (r0 + 16 * g + lr < Tq && ri.mode != SELECT_ALL) hmask |= 1u << g;
     }
     const bool any_hist = __syncthreads_or(hmask != 0u);
@@ -1725,7 +1799,7 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             top2(g, acc[g][i]);
-            if (any_hist) bump(16 * g + lr, score_bin_bits(acc[g][i], iw[g]));
+            if (any_hist) bump(16 * g + lr, score_bin_bits(acc[g][i], iw[g], bc[g]));
           }
         }
       } else {
@@ -1736,7 +1810,7 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
           for (int i = 0; i < 4; ++i) {
             const int j = kt * KT + 16 * w + lg + 4 * i;
             top2(g, j < nv ? acc[g][i] : -FLT_MAX);
-            if (((hmask >> g) & 1u) && j < nv) bump(16 * g + lr, score_bin_bits(acc[g][i], iw[g]));
+            if (((hmask >> g) & 1u) && j < nv) bump(16 * g + lr, score_bin_bits(acc[g][i], iw[g], bc[g]));
           }
         }
       }
@@ -1810,8 +1884,8 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
     RowInfo ri = rinfo[g][r];
     float t0 = -INFINITY, t1 = -INFINITY;
     if (ri.mode != SELECT_ALL) {
-      const float lo_b = ri.bstar > 0 ? bin_lower_edge(ri.bstar, ri.iw) : -INFINITY;
-      const float hi_b = ri.bstar < NBIN - 1 ? bin_lower_edge(ri.bstar + 1, ri.iw) : INFINITY;
+      const float lo_b = ri.bstar > 0 ? bin_lower_edge(ri.bstar, ri.iw, ri.bc) : -INFINITY;
+      const float hi_b = ri.bstar < NBIN - 1 ? bin_lower_edge(ri.bstar + 1, ri.iw, ri.bc) : INFINITY;
       if (ri.mode == BIN_ALL) { t0 = lo_b; t1 = lo_b; }
       else { t0 = lo_b; t1 = hi_b; }   // COLLECT
     }
