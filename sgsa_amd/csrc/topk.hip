@@ -1896,6 +1896,7 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
   // ---- pass B: threshold-bin candidates (blocks with a row to collect) -----------
   uint2* scratch = a.scratch;
   const long srowb = (long)bh * Tq + r0;   // global row of the block's row 0
+  bool full_col = false;   // pass B: a candidate found no room in its lane's staging column
   if (__syncthreads_or(any_collect)) {
     // candidate of row 16g + lr: th0 <= s < th1, i.e. med3(s, lo, hi) == s with
     // lo = th0, hi = the float below th1; rows that collect nothing take
@@ -1908,24 +1909,50 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
       tlo[g] = col ? ri.th0 : INFINITY;
       thi[g] = col ? next_down(ri.th1) : INFINITY;
     }
-    // A tile's candidates are staged in LDS, each lane in a column of its own
-    // (entry r of lane l at 64 r + l: a lane meets at most 32 per tile, and the
-    // histogram area is free -- 32 of its rows per wave), then each takes a slot
-    // in its row's scratch list through an LDS atomic and is stored, four
-    // entries per lane at a time.  Entry: {score bits, g << 16 | key} (the row
-    // is 16g + lr of the lane that staged and flushes it); keys fit 16 bits
-    // (Tk <= 65535 on this path).
+    // Candidates are staged in LDS, each lane in a column of its own (entry r of
+    // lane l at 64 r + l, 32 entries: the histogram area is free, 32 of its
+    // rows per wave), and flushed -- each takes a slot in its row's scratch list
+    // through an LDS atomic and is stored, four entries per lane at a time --
+    // after a tile that leaves some lane of the wave holding 16 or more, and
+    // after the sweep.  (Flushing every tile put the stores ahead of the next
+    // tile's K loads in the memory counter the loads are waited on.)  A tile
+    // starts with at most 15 entries per lane; a lane that still runs out of room
+    // (more than 16 of its 32 scores of one tile in threshold bins) sends the
+    // block to the radix fallback, like an overflowing bin.  Entry: {score bits,
+    // g << 16 | key}: the row is 16g + lr of the lane that staged and flushes it;
+    // keys fit 16 bits (Tk <= 65535 on this path).
     uint2* ebuf = reinterpret_cast<uint2*>(&hist[32 * w][0]);
     uint32_t* rowcnt = reinterpret_cast<uint32_t*>(&colcnt[0][0]);   // row 16g + lr at 16g + lr
+    uint32_t kc = 0;   // this lane's staged entries
+    auto flush = [&]() __attribute__((always_inline)) {
+      wave_lds_sync();   // this wave's buffer writes before its reads
+      for (uint32_t r0e = 0; ballot64(r0e < kc) != 0ull; r0e += 4) {
+        uint2 e[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          if (r0e + u < kc) e[u] = ebuf[64 * (r0e + u) + lane];
+        uint32_t slot[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          if (r0e + u < kc) slot[u] = atomicAdd(rowcnt + 16 * (e[u].y >> 16) + lr, 1u);
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          if (r0e + u < kc && slot[u] < (uint32_t)TOPK_CAP)
+            scratch[(srowb + 16 * (e[u].y >> 16) + lr) * TOPK_CAP + slot[u]] = make_uint2(e[u].x, e[u].y & 0xffffu);
+      }
+      wave_lds_sync();   // reads done before the buffer is written again
+      kc = 0;
+    };
     sweep([&](int kt, f4* acc) __attribute__((always_inline)) {
-      uint32_t kc = 0;   // this lane's staged entries
-      // Where any lane of the wave has a candidate, every lane writes its entry
-      // at its next position and only candidates keep theirs (advance kc): the
-      // others are overwritten or lie past kc.  No exec-mask changes per score.
+      // Where any lane of the wave has a candidate, every lane with room writes
+      // its entry at its next position and only candidates keep theirs (advance
+      // kc): the others are overwritten or lie past kc.
       auto stage = [&](bool cand, int g, float sc, int j) __attribute__((always_inline)) {
         if (ballot64(cand) != 0ull) {
-          ebuf[64 * kc + lane] = make_uint2(__float_as_uint(sc), ((uint32_t)g << 16) | (uint32_t)j);
-          kc += cand ? 1u : 0u;
+          const bool room = kc < 32u;
+          if (room) ebuf[64 * kc + lane] = make_uint2(__float_as_uint(sc), ((uint32_t)g << 16) | (uint32_t)j);
+          full_col |= cand & !room;
+          kc += (cand & room) ? 1u : 0u;
         }
       };
       if ((kt + 1) * KT <= minvalid) {
@@ -1949,25 +1976,16 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
           }
         }
       }
-      if (ballot64(kc != 0u) != 0ull) {
-        wave_lds_sync();   // this wave's buffer writes before its reads
-        for (uint32_t r0e = 0; ballot64(r0e < kc) != 0ull; r0e += 4) {
-          uint2 e[4];
-#pragma unroll
-          for (int u = 0; u < 4; ++u)
-            if (r0e + u < kc) e[u] = ebuf[64 * (r0e + u) + lane];
-          uint32_t slot[4];
-#pragma unroll
-          for (int u = 0; u < 4; ++u)
-            if (r0e + u < kc) slot[u] = atomicAdd(rowcnt + 16 * (e[u].y >> 16) + lr, 1u);
-#pragma unroll
-          for (int u = 0; u < 4; ++u)
-            if (r0e + u < kc && slot[u] < (uint32_t)TOPK_CAP)
-              scratch[(srowb + 16 * (e[u].y >> 16) + lr) * TOPK_CAP + slot[u]] = make_uint2(e[u].x, e[u].y & 0xffffu);
-        }
-        wave_lds_sync();   // reads done before the next tile's writes
-      }
+      if (ballot64(kc >= 16u) != 0ull) flush();
     });
+    if (ballot64(kc != 0u) != 0ull) flush();
+  }
+  if (__syncthreads_or(full_col)) {   // block-uniform: the fallback launch redoes both halves
+    if (tid < 2) {
+      const int q64 = 2 * qb + tid;
+      if (q64 < nqb) a.flags[(long)(nqb - 1 - q64) * BH + bh] = 1;
+    }
+    return;
   }
   __syncthreads();   // candidates and counters of every wave are in place; hist is the resolve's area
 

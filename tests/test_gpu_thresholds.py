@@ -5,7 +5,9 @@ and applies it.
 * The cut selects exactly the rows of the row-list K1 (the lowest-index top-k
   of K1's own fp32 scores, checked against the oracle elsewhere), applied to
   the scores sgsa_score_dump returns -- on random, tied, mass-tied (radix
-  fallback blocks) and heavy-tailed inputs and a ragged shape.
+  fallback blocks), bursts of tied keys (the 128-row kernel's candidate
+  staging overflows and the block goes to the fallback) and heavy-tailed
+  inputs and a ragged shape.
 * K2 on the thresholds gives the outputs of K2 on the tile lists: the same
   selection, and weights that differ only in the rounding of the exponent's
   argument (one fused multiply-add on the raw accumulator instead of the
@@ -35,6 +37,19 @@ def _inputs(case, dev):
         base = torch.randn(2, H, D, generator=g)
         kk = base[torch.randint(0, 2, (T,), generator=g)][None]
         q = torch.randn(B, T, H, D, generator=g)
+    elif case == "tile_burst":
+        # Queries near one key vector A, which scores far above the rest and ties
+        # exactly.  A fills key tile 1 and a quarter of every other tile, so a
+        # row's threshold bin is A's (tie cut by index) and, in K1's 128-row
+        # kernel, a lane stages a few candidates in tile 0 and then more in tile 1
+        # than its staging column holds: the block goes to the radix fallback.
+        B, T, k = 1, 500, 100
+        A = torch.randn(H, D, generator=g)
+        j = torch.arange(T)
+        is_a = ((j >= 64) & (j < 128)) | (j % 16 < 4)
+        kk = 0.05 * torch.randn(B, T, H, D, generator=g)
+        kk[:, is_a] = A
+        q = A + 0.01 * torch.randn(B, T, H, D, generator=g)
     elif case == "heavy_tail":
         x = O.make_inputs(B, T, H, D, dtype=torch.float32, seed=12, heavy_tail=True, with_budget=False)
         q, kk = x["q"], x["k_ret"]
@@ -47,7 +62,7 @@ def _inputs(case, dev):
     return cast(q), cast(kk), cast(v), bud.to(dev), k
 
 
-CASES = ["random", "ties", "mass_ties", "heavy_tail", "ragged"]
+CASES = ["random", "ties", "mass_ties", "tile_burst", "heavy_tail", "ragged"]
 
 
 @pytest.mark.parametrize("case", CASES)
@@ -73,7 +88,7 @@ def test_thresholds_select_exactly_the_row_lists(dev, case):
     bi, hi, ri, si = live.nonzero(as_tuple=True)
     ref[bi, hi, ri, ic[bi, hi, ri, si]] = True
     assert torch.equal(mask, ref), f"selected sets differ in {(mask != ref).sum().item()} (row, key) pairs"
-    if case in ("ties", "mass_ties"):
+    if case in ("ties", "mass_ties", "tile_burst"):
         assert (thr[..., 1] != 0x7fffffff).any(), "no row needed a tie cut"
 
 
