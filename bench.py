@@ -357,6 +357,21 @@ def main() -> int:
                     "gather_gate": round(ev[1].elapsed_time(ev[2]) / 3, 3)}
         log(f"{other_name} form for comparison: {json.dumps(other_ms)} ms")
 
+    # The north star's K2 is a gather of the selected K/V rows: time it beside the step (K1 row lists, then
+    # the per-row 16-byte gather), outside the timed steps, for its HBM roofline.
+    gather_form_ms = None
+    if args.steps > 0 and args.gather != "direct":
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        k1_rows()
+        k2_direct()
+        ev[0].record(cur)
+        for _ in range(2):
+            k2_direct()
+        ev[1].record(cur)
+        torch.cuda.synchronize()
+        gather_form_ms = ev[0].elapsed_time(ev[1]) / 2
+        log(f"row gather K2 (sparse_gather_kernel) on K1's row lists: {gather_form_ms:.3f} ms")
+
     measured = {}
     if args.traffic_from and os.path.exists(args.traffic_from) and (B, T, H, D, kk) == (1, 32768, 16, 128, 2048):
         with open(args.traffic_from) as f:
@@ -394,6 +409,17 @@ def main() -> int:
     }
     for r in rooflines.values():
         r["frac"] = round(r["achieved"] / r["peak"], 4)
+    if gather_form_ms is not None:
+        gk = "sparse_gather_kernel<bf16_t, true>"
+        ach = gbytes / (gather_form_ms / 1000.0) / 1e9
+        rooflines["row_gather_form"] = {
+            "kernel": f"{gk} (K2 as a gather of the selected K/V rows, timed beside the step)", "ms": round(gather_form_ms, 3),
+            "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": measured.get(gk), "algorithmic_bytes": gbytes}
+        if measured.get(gk):   # the HBM bytes it really moves, at the measured time
+            hb = measured[gk] / (gather_form_ms / 1000.0) / 1e9
+            rooflines["row_gather_form"]["hbm_GBps"] = round(hb, 1)
+            rooflines["row_gather_form"]["hbm_frac"] = round(hb / HBM_PEAK_GBS, 4)
     dominant = max(stage_ms, key=stage_ms.get)
     result = {
         "metric": METRIC,
