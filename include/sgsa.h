@@ -131,6 +131,19 @@ int sgsa_sparse_gather(int dtype, int B, int Tq, int Tk, int H, int D, int top_k
                        float* weights, float* diag,
                        void* workspace, size_t workspace_bytes, void* stream);
 
+/* Scores at given keys: for every query row and slot i < counts[row],
+ * scores[row,i] = (q_row . k[indices[row,i]]) * scale' with fp32 accumulation,
+ * where scale' is sgsa_score_topk's (1/scale, or scale for scale_mode 1).
+ * Layouts as sgsa_score_topk: q [B,Tq,H,D], k [B,Tk,H,D], indices and scores
+ * [B,H,Tq,top_k], counts [B,H,Tq]; indices outside [0,Tk) score 0.  No
+ * reference counterpart: it serves top-k reuse, where a candidate set selected
+ * once is re-scored by later queries instead of selected again
+ * (modelings/idea.md:395-401; config 4 reuses each SGSA layer's top-k over 4
+ * decode steps).  Feed the scores to sgsa_sparse_gather with top2 = NULL. */
+int sgsa_score_at(int dtype, int B, int Tq, int Tk, int H, int D, int top_k, float scale, int scale_mode,
+                  const void* q, const void* k, const int32_t* indices, const int32_t* counts,
+                  float* scores, void* stream);
+
 /* Tiled form of sgsa_sparse_gather for the layer path (bf16, D = 128,
  * top_k % 4 == 0, causal, Tq = Tk = T): streams K/V through LDS in 64-key tiles and applies the exact
  * top-k weights with MFMA.  Needs the unsorted output of sgsa_score_topk with

@@ -439,6 +439,75 @@ def sgsa_layer_forward(
             "alpha": alpha, "retrieval": ret}
 
 
+def sgsa_decode_step(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    q_ret: Tensor,
+    beta: Tensor,
+    gamma: Tensor,
+    budget_logits: Tensor,
+    k_cache: Tensor,
+    v_cache: Tensor,
+    state: Tensor,
+    top_k: int,
+    write_mode: str = "direct",
+    alpha_max: float = 0.25,
+    tau_c: float = 0.1,
+    candidates: Optional[Tuple[Tensor, Tensor]] = None,
+    eps: float = 1e-6,
+) -> Tuple[Tensor, Tensor, Tuple[Tensor, Tensor]]:
+    """One generated token of the layer, with optional top-k reuse.
+
+    The token's retrieval over the cache k_cache/v_cache [B,Tc,H,D] (ending with
+    the token; causal, so every cached key is valid), its write key and gate,
+    and one recurrent update, as ``sgsa_layer_forward`` does at that position
+    (modelings/modeling_sgsa.py:669-684 with the recurrent backend).  Without
+    ``candidates`` the keys are the exact top-k (lowest index on ties).  With
+    candidates (indices [B,H,1,n], counts [B,H,1]) selected by an earlier step,
+    those keys are re-scored for this query (modelings/idea.md:395-401) and
+    ordered by score, ties by index, before the weights, the diagnostics and
+    the gate.  Inputs are upcast to fp32.  Returns (o [B,1,H,D], state, the
+    step's candidates).
+    """
+    f = lambda x: x.float()
+    q, k, v, q_ret, beta, gamma, budget_logits, kc, vc, state = map(
+        f, (q, k, v, q_ret, beta, gamma, budget_logits, k_cache, v_cache, state))
+    B, Tc, H, D = kc.shape
+    qh = q_ret.transpose(1, 2)                                     # [B,H,1,D]
+    kh, vh = kc.transpose(1, 2), vc.transpose(1, 2)                # [B,H,Tc,D]
+    scores = torch.matmul(qh, kh.transpose(-2, -1)) / math.sqrt(D)   # [B,H,1,Tc]
+    if candidates is None:
+        kk = min(top_k, Tc)
+        ts, ti, _ = masked_topk(scores, torch.ones_like(scores, dtype=torch.bool), kk)
+        cnt = torch.full((B, H, 1), kk, dtype=torch.int32)
+        cand = (ti.to(torch.int32), cnt)
+    else:
+        cidx, cnt = candidates
+        n = int(cnt.min().item())
+        if int(cnt.max().item()) != n:
+            raise ValueError("the oracle takes candidates with one count for every row")
+        # in key-index order, so that ordering by (score desc, position asc) is (score desc, index asc)
+        ci = torch.sort(cidx[..., :n].long(), dim=-1).values
+        cs = scores.gather(-1, ci)
+        vals, pos = topk_lowest_index(cs.reshape(-1, n), n)
+        ts = vals.reshape(B, H, 1, n)
+        ti = ci.reshape(-1, n).gather(1, pos).reshape(B, H, 1, n)
+        cand = (cidx, cnt)
+    w = F.softmax(ts, dim=-1)
+    w = w / w.sum(-1, keepdim=True).clamp_min(eps)
+    gk = kh.gather(2, ti[..., 0, :, None].expand(-1, -1, -1, D))       # [B,H,n,D]
+    gv = vh.gather(2, ti[..., 0, :, None].expand(-1, -1, -1, D))
+    k_hat = (w[..., 0, :, None] * gk).sum(2)[:, :, None]               # [B,H,1,D]
+    v_hat = (w[..., 0, :, None] * gv).sum(2)[:, :, None]
+    diag = retrieval_diagnostics(ts, w, ti, k_hat, k.transpose(1, 2), tau_c, eps=eps, row_offset=Tc - 1)
+    kh_t, vh_t = k_hat.transpose(1, 2), v_hat.transpose(1, 2)          # [B,1,H,D]
+    wk = write_key(kh_t, k, write_mode)
+    alpha = compute_alpha(diag["concentration"], diag["novelty"], budget_logits, wk, vh_t, alpha_max)
+    o, st = naive_recurrent_sgsa(q, k, v, beta, gamma, wk, vh_t, alpha, state, True)
+    return o, st, cand
+
+
 # ---------------------------------------------------------------------------
 # The causal LM around the layer (SGSABlock / SGSAForCausalLM)
 # ---------------------------------------------------------------------------

@@ -319,6 +319,20 @@ int sgsa_sparse_gather(int dtype, int B, int Tq, int Tk, int H, int D, int top_k
   return hip_status(sgsa::launch_sparse_gather(a, (hipStream_t)stream), "sgsa_sparse_gather");
 }
 
+int sgsa_score_at(int dtype, int B, int Tq, int Tk, int H, int D, int top_k, float scale, int scale_mode,
+                  const void* q, const void* k, const int32_t* indices, const int32_t* counts, float* scores,
+                  void* stream) {
+  if (int s = check_dtype(dtype)) return s;
+  if (int s = check_dims(B, Tq, H, D)) return s;
+  if (int s = check_dims(B, Tk, H, D)) return s;
+  if (top_k <= 0) return fail(SGSA_ERR_INVALID_ARG, "top_k=%d must be positive", top_k);
+  if (scale_mode != 0 && scale_mode != 1) return fail(SGSA_ERR_INVALID_ARG, "scale_mode must be 0 or 1");
+  REQUIRE(q); REQUIRE(k); REQUIRE(indices); REQUIRE(counts); REQUIRE(scores);
+  return hip_status(sgsa::launch_rescore(dtype, B, Tq, Tk, H, D, top_k, q, k, indices, counts,
+                                         sgsa::score_multiplier(scale, scale_mode), scores, (hipStream_t)stream),
+                    "sgsa_score_at");
+}
+
 int sgsa_sparse_gather_tiled(int B, int T, int H, int D, int top_k, const void* k, const void* v,
                              const int32_t* indices, const float* scores, const float* top2,
                              const int32_t* counts, const int32_t* split, const float* budget, int write_mode,

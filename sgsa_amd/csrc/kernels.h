@@ -124,6 +124,11 @@ struct GatherArgs {
 
 constexpr int NDIAG = 10;
 hipError_t launch_sparse_gather(const GatherArgs& a, hipStream_t st);
+// Scores of given keys (top-k reuse across decode steps): scores[r, i] =
+// (q_r . k[indices[r, i]]) * mscale for i < counts[r].
+hipError_t launch_rescore(int dtype, int B, int Tq, int Tk, int H, int D, int top_k, const void* q, const void* k,
+                          const int32_t* indices, const int32_t* counts, float mscale, float* scores,
+                          hipStream_t st);
 // LDS-staged variant for the fused layer path: bf16, D = 128, rows whose
 // slots [0, split) ascend in key index; no weights/diag outputs.
 hipError_t launch_sparse_gather_staged(const GatherArgs& a, const int32_t* split, hipStream_t st);

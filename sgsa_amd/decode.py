@@ -8,13 +8,20 @@ token sits at cache position Tc - 1 and retrieves over keys [0, Tc - 1]
 (causal).  Three C-ABI calls on the current stream: sgsa_score_topk (one
 query row, q_offset = Tc - 1), sgsa_sparse_gather (weights, k_hat / write
 key, v_hat, alpha) and sgsa_recurrent_fwd (T = 1).
+
+Top-k reuse (modelings/idea.md:395-401; config 4 recomputes every 4 decode
+steps): a step given ``candidates`` -- the (indices, counts) an earlier step
+returned -- skips the selection and re-scores those keys for the new query
+(sgsa_score_at); the weights, gate and update then follow as usual, with the
+row maximum and top-2 taken over the re-scored set.  Keys appended since the
+candidates were selected are not among them.
 """
 
 from __future__ import annotations
 
 import ctypes
 import math
-from typing import Tuple
+from typing import Optional, Tuple
 
 import torch
 
@@ -41,11 +48,16 @@ def sgsa_decode_step(
     write_mode: str = "direct",
     alpha_max: float = 0.25,
     tau_c: float = 0.1,
-) -> Tuple[Tensor, Tensor]:
+    candidates: Optional[Tuple[Tensor, Tensor]] = None,
+    return_candidates: bool = False,
+):
     """q, k, v, q_ret [B,1,H,D]; beta, gamma, budget_logits [B,1,H];
     k_cache, v_cache [B,Tc,H,D] (ending with this token); state [B,H,D,D] fp32.
+    candidates: (indices int32 [B,H,1,n], counts int32 [B,H,1]) to re-score
+    instead of selecting (top-k reuse); indices must be < Tc.
 
-    Returns (o [B,1,H,D] in q.dtype, new state [B,H,D,D] fp32).
+    Returns (o [B,1,H,D] in q.dtype, new state [B,H,D,D] fp32), and the step's
+    candidates (selected or reused) as a third item when return_candidates.
     """
     if not q.is_cuda:
         raise ValueError("sgsa_decode_step: the SGSA kernels run on a ROCm GPU; got CPU tensors")
@@ -59,20 +71,34 @@ def sgsa_decode_step(
         raise ValueError(f"write_mode must be one of {sorted(_WRITE_MODES)}")
     dt = q.dtype
     dev = q.device
-    kk = min(int(top_k), Tc)
     rc, kc, vc, kn = (t.to(dt).contiguous() for t in (q_ret, k_cache, v_cache, k))
     L = _abi.lib()
-    # 1. top-k of the new query over the cache (causal: position Tc - 1)
-    idx = torch.empty(B, H, 1, kk, device=dev, dtype=torch.int32)
-    sc = torch.empty(B, H, 1, kk, device=dev, dtype=torch.float32)
-    top2 = torch.empty(B, H, 1, 2, device=dev, dtype=torch.float32)
-    cnt = torch.empty(B, H, 1, device=dev, dtype=torch.int32)
-    nb = ctypes.c_size_t()
-    _abi.check(L.sgsa_score_topk_workspace_size(B, 1, H, ctypes.byref(nb)))
-    tws = torch.empty(nb.value, device=dev, dtype=torch.uint8)
-    _abi.check(L.sgsa_score_topk(_abi.dtype_code(dt), B, 1, Tc, H, D, kk, 1, Tc - 1, math.sqrt(D), 0,
-                                 _abi.ptr(rc), _abi.ptr(kc), _abi.ptr(idx), _abi.ptr(sc), _abi.ptr(top2),
-                                 _abi.ptr(cnt), None, 0, _abi.ptr(tws), nb.value, _abi.stream_of(rc)))
+    if candidates is None:
+        # 1. top-k of the new query over the cache (causal: position Tc - 1)
+        kk = min(int(top_k), Tc)
+        idx = torch.empty(B, H, 1, kk, device=dev, dtype=torch.int32)
+        sc = torch.empty(B, H, 1, kk, device=dev, dtype=torch.float32)
+        top2 = torch.empty(B, H, 1, 2, device=dev, dtype=torch.float32)
+        cnt = torch.empty(B, H, 1, device=dev, dtype=torch.int32)
+        nb = ctypes.c_size_t()
+        _abi.check(L.sgsa_score_topk_workspace_size(B, 1, H, ctypes.byref(nb)))
+        tws = torch.empty(nb.value, device=dev, dtype=torch.uint8)
+        _abi.check(L.sgsa_score_topk(_abi.dtype_code(dt), B, 1, Tc, H, D, kk, 1, Tc - 1, math.sqrt(D), 0,
+                                     _abi.ptr(rc), _abi.ptr(kc), _abi.ptr(idx), _abi.ptr(sc), _abi.ptr(top2),
+                                     _abi.ptr(cnt), None, 0, _abi.ptr(tws), nb.value, _abi.stream_of(rc)))
+    else:
+        # 1'. the reused candidates, re-scored for the new query; the gather tracks
+        # the row maximum and top-2 itself (top2 = NULL)
+        idx, cnt = candidates
+        if idx.dim() != 4 or idx.shape[:3] != (B, H, 1) or idx.dtype != torch.int32 or cnt.shape != (B, H, 1) \
+                or cnt.dtype != torch.int32:
+            raise ValueError("candidates must be (int32 [B,H,1,n], int32 [B,H,1]) from an earlier step")
+        idx, cnt = idx.contiguous(), cnt.contiguous()
+        kk = idx.shape[-1]
+        sc = torch.empty(B, H, 1, kk, device=dev, dtype=torch.float32)
+        top2 = None
+        _abi.check(L.sgsa_score_at(_abi.dtype_code(dt), B, 1, Tc, H, D, kk, math.sqrt(D), 0, _abi.ptr(rc),
+                                   _abi.ptr(kc), _abi.ptr(idx), _abi.ptr(cnt), _abi.ptr(sc), _abi.stream_of(rc)))
     # 2. weights, k_hat / write key, v_hat and the gate for that row
     mode = _WRITE_MODES[write_mode]
     wk = torch.empty(B, 1, H, D, device=dev, dtype=dt)
@@ -85,4 +111,5 @@ def sgsa_decode_step(
         _abi.ptr(wk if mode == 0 else None), _abi.ptr(vh), _abi.ptr(wk if mode == 1 else None), _abi.ptr(al),
         None, None, None, 0, _abi.stream_of(kc)))
     # 3. the recurrent update for this token
-    return fused_recurrent_sgsa(q, k, v, beta, gamma, wk, vh, al, state, output_final_state=True)
+    o, st = fused_recurrent_sgsa(q, k, v, beta, gamma, wk, vh, al, state, output_final_state=True)
+    return (o, st, (idx, cnt)) if return_candidates else (o, st)

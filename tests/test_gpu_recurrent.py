@@ -122,3 +122,57 @@ def test_decode_steps_match_the_layer_oracle(dev, dtype, tol, D, write_mode):
         torch.cuda.synchronize()
         _close(o, full["o"][:, sl], tol, f"o[{t}]")
     _close(st, full["final_state"], tol, "final_state")
+
+
+@pytest.mark.parametrize("dtype,tol,D", [(torch.float32, 1e-4, 64), (torch.bfloat16, 2e-2, 128)])
+def test_decode_with_topk_reuse_matches_the_oracle(dev, dtype, tol, D):
+    # 8 generated tokens: steps 0 and 4 select their top-k over the cache, steps
+    # 1-3 and 5-7 re-score the last selection (sgsa_score_at) -- against the
+    # oracle's decode step on the same schedule
+    B, T, H, k, n = 2, 200, 2, 32, 8
+    x = O.make_inputs(B, T, H, D, dtype=dtype, seed=11)
+    args = lambda sl: (x["q_f32"][:, sl], x["k_f32"][:, sl], x["v_f32"][:, sl], x["q_f32"][:, sl],
+                       x["beta"][:, sl], x["gamma"][:, sl], x["budget"][:, sl])
+    st_ref = O.sgsa_layer_forward(*args(slice(0, T - n)), k)["final_state"]
+    st = st_ref.to(dev)
+    d = lambda t: t.to(dev)
+    cand = cand_ref = None
+    for s, t in enumerate(range(T - n, T)):
+        sl = slice(t, t + 1)
+        reuse = s % 4 != 0
+        o_ref, st_ref, c_ref = O.sgsa_decode_step(*args(sl), x["k_f32"][:, :t + 1], x["v_f32"][:, :t + 1], st_ref, k,
+                                                  candidates=cand_ref if reuse else None)
+        cand_ref = c_ref
+        o, st, c = sgsa_amd.sgsa_decode_step(d(x["q"][:, sl]), d(x["k"][:, sl]), d(x["v"][:, sl]), d(x["q"][:, sl]),
+                                             d(x["beta"][:, sl]), d(x["gamma"][:, sl]), d(x["budget"][:, sl]),
+                                             d(x["k"][:, :t + 1]), d(x["v"][:, :t + 1]), st, k,
+                                             candidates=cand if reuse else None, return_candidates=True)
+        cand = c
+        torch.cuda.synchronize()
+        _close(o, o_ref, tol, f"o[{t}] ({'reuse' if reuse else 'select'})")
+    _close(st, st_ref, tol, "final_state")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_score_at_is_the_dot_product(dev, dtype):
+    # sgsa_score_at: q . k[idx] / sqrt(D) at given keys, slots past the count untouched
+    B, Tq, Tk, H, D, n = 2, 3, 300, 2, 96, 40
+    g = torch.Generator().manual_seed(12)
+    q = torch.randn(B, Tq, H, D, generator=g).to(dtype)
+    kk = torch.randn(B, Tk, H, D, generator=g).to(dtype)
+    idx = torch.randint(0, Tk, (B, H, Tq, n), generator=g, dtype=torch.int32)
+    cnt = torch.randint(1, n + 1, (B, H, Tq), generator=g, dtype=torch.int32)
+    out = torch.full((B, H, Tq, n), 123.0, device=dev)
+    from sgsa_amd import _abi
+    qd, kd, idxd, cntd = q.to(dev).contiguous(), kk.to(dev).contiguous(), idx.to(dev), cnt.to(dev)   # kept alive
+    _abi.check(_abi.lib().sgsa_score_at(_abi.dtype_code(dtype), B, Tq, Tk, H, D, n, float(D) ** 0.5, 0,
+                                        _abi.ptr(qd), _abi.ptr(kd), _abi.ptr(idxd), _abi.ptr(cntd), _abi.ptr(out),
+                                        _abi.stream_of(out)))
+    torch.cuda.synchronize()
+    qf, kf = q.double(), kk.double()
+    ref = torch.einsum("bqhd,bhqnd->bhqn", qf, kf.permute(0, 2, 1, 3)[:, :, None].expand(-1, -1, Tq, -1, -1)
+                       .gather(3, idx.long()[..., None].expand(-1, -1, -1, -1, D))) / D ** 0.5
+    live = torch.arange(n)[None, None, None, :] < cnt[..., None]
+    got = out.cpu().double()
+    assert torch.allclose(got[live], ref[live], atol=1e-4, rtol=1e-4)
+    assert (got[~live] == 123.0).all(), "slots past the count were written"
