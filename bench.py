@@ -121,6 +121,8 @@ def cpu_baseline(q, k, v, beta, gamma, budget, cfg, sample_rows=256, chunk_token
 
 
 MODEL_METRIC = "SGSA 2-layer model fwd tokens/s (config 2: bf16, B=16, T=4096, hidden 1024, 8x128 heads, vocab 8192)"
+HYBRID_METRIC = ("hybrid decoder decode tokens/s (config 4: bf16, 24 layers 3:1 SGSA:dense GQA, hidden 2048, "
+                 "16q/4kv x 128, prefill 16384 at B=1, 256 greedy steps at B=8, top-k 2048 every 4 steps)")
 
 
 def recall_batch(B: int, T: int, vocab: int, seed: int = 0) -> torch.Tensor:
@@ -184,6 +186,60 @@ def run_model(args) -> int:
     return 0
 
 
+def run_hybrid(args) -> int:
+    """Config 4: the 24-layer hybrid decoder (sgsa_amd.hybrid), prefill then greedy decode."""
+    from sgsa_amd.hybrid import HybridConfig, HybridForCausalLM, expand_caches, rope_tables
+    T, B, steps = 16384, 8, 256
+    cfg = HybridConfig()
+    dev = torch.device("cuda:0")
+    model = HybridForCausalLM(cfg)
+    model.init_weights(std=0.02, qk_std=1.0 / math.sqrt(cfg.hidden_size * cfg.head_dim),
+                       generator=torch.Generator().manual_seed(0))
+    model = model.to(device=dev, dtype=torch.bfloat16).eval()
+    ids = torch.randint(0, cfg.vocab_size, (1, T), generator=torch.Generator().manual_seed(1)).to(dev)
+    rope = rope_tables(T + steps, cfg.head_dim, cfg.rope_theta, dev)
+    cur = torch.cuda.current_stream()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    log(f"hybrid: config 4, prefill T={T} at B=1, then {steps} decode steps at B={B}")
+    with torch.no_grad():
+        caches = model.new_cache(1, T + steps, dev, torch.bfloat16)
+        model.prefill(ids, caches, rope)   # warm-up: kernels, workspaces, GEMM plans
+        torch.cuda.synchronize()
+        ev[0].record(cur)
+        logits = model.prefill(ids, caches, rope)
+        ev[1].record(cur)
+        torch.cuda.synchronize()
+        log(f"prefill {ev[0].elapsed_time(ev[1]):.1f} ms")
+        caches = expand_caches(caches, B)
+        tok = logits[:, -1].argmax(-1).expand(B).contiguous()
+        ev[2].record(cur)
+        for s in range(steps):
+            tok = model.decode_step(tok, T + s, s, caches, rope).argmax(-1)
+            if (s + 1) % 64 == 0:
+                log(f"decode step {s + 1}")
+        ev[3].record(cur)
+        torch.cuda.synchronize()
+    pre_ms, dec_ms = ev[0].elapsed_time(ev[1]), ev[2].elapsed_time(ev[3])
+    if not torch.isfinite(logits.float()).all():
+        log("non-finite logits")
+        return 1
+    log(f"decode {dec_ms:.1f} ms for {steps} steps")
+    print(json.dumps({
+        "metric": HYBRID_METRIC, "value": round(B * steps / (dec_ms / 1000.0), 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": steps, "warmup": 1, "ms_per_step": round(dec_ms / steps, 3), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "uniform-random token ids, random-init weights",
+        "prefill": {"T": T, "B": 1, "ms": round(pre_ms, 1), "tokens_per_s": round(T / (pre_ms / 1000.0), 1)},
+        "config": {"workload": "hybrid_decoder", "layers": cfg.num_hidden_layers, "dense_every": cfg.dense_every,
+                   "hidden": cfg.hidden_size, "heads": cfg.num_attention_heads, "kv_heads": cfg.num_kv_heads,
+                   "head_dim": cfg.head_dim, "intermediate": cfg.intermediate_size, "vocab": cfg.vocab_size,
+                   "top_k": cfg.top_k, "topk_recompute_every": cfg.topk_recompute_every, "decode_batch": B,
+                   "init": "normal std 0.02; SGSA q/k/q_ret projections std 1/sqrt(hidden*head_dim)"},
+        "cpu_baseline": None,
+    }), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -201,9 +257,10 @@ def main() -> int:
                     help="timed step: the fused layer path (K1 row thresholds -> K2 recomputing the scores on "
                          "MFMA -> chunk, what sgsa_layer_fwd runs; default), the tile-list form (K1 tile lists -> "
                          "LDS-tiled MFMA K2 -> chunk) or K1 row lists -> per-row 16-byte gathers -> chunk")
-    ap.add_argument("--workload", choices=("layer", "model"), default="layer",
+    ap.add_argument("--workload", choices=("layer", "model", "hybrid"), default="layer",
                     help="layer: the north-star SGSA layer forward (the headline metric, default); model: "
-                         "config 2, the 2-layer SGSA causal LM forward at B=16 T=4096")
+                         "config 2, the 2-layer SGSA causal LM forward at B=16 T=4096; hybrid: config 4, the "
+                         "24-layer SGSA / dense-GQA decoder, prefill of 16384 tokens then 256 decode steps at B=8")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on exactly one GPU (got --gpus {args.gpus}); the SGSA layer shards by head, "
@@ -211,6 +268,8 @@ def main() -> int:
         return 2
     if args.workload == "model":
         return run_model(args)
+    if args.workload == "hybrid":
+        return run_hybrid(args)
 
     import sgsa_amd
     from sgsa_amd import _abi

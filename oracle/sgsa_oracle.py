@@ -43,7 +43,7 @@ How each function is pinned (tests/test_oracle.py):
 from __future__ import annotations
 
 import math
-from typing import Dict, Optional, Tuple
+from typing import Dict, List, Optional, Tuple
 
 import torch
 import torch.nn.functional as F
@@ -571,6 +571,108 @@ def sgsa_model_forward(params: Dict[str, Tensor], input_ids: Tensor, *, num_laye
         h = r(h + r(r(r(F.silu(gate)) * up) @ w("mlp.down_proj.weight").T))
     head = P.get("lm_head.weight", P["embed_tokens.weight"])
     return r(r(rms_norm(h, P["norm.weight"], eps)) @ head.T)
+
+
+# ---------------------------------------------------------------------------
+# Config 4: the hybrid decoder (SGSA blocks and dense GQA attention blocks)
+# ---------------------------------------------------------------------------
+
+def rope_apply(x: Tensor, pos: Tensor, theta: float = 10000.0) -> Tensor:
+    """Rotary embedding of x [B, heads, T, D] at positions pos [T], in the rotate-half
+    form of modelings/hybrid_dense_delta_topk.py:124-150 (fp32)."""
+    D = x.shape[-1]
+    inv_freq = 1.0 / (theta ** (torch.arange(0, D, 2).float() / D))
+    f = torch.outer(pos.float(), inv_freq)
+    emb = torch.cat((f, f), dim=-1)
+    rot = torch.cat((-x[..., D // 2:], x[..., :D // 2]), dim=-1)
+    return x * emb.cos() + rot * emb.sin()
+
+
+def dense_gqa_attention(q: Tensor, k: Tensor, v: Tensor, q_pos: Tensor) -> Tensor:
+    """Causal softmax attention (:178-192) with grouped key/value heads: q [B, H, Tq, D]
+    at positions q_pos [Tq]; k, v [B, Hkv, Tk, D] at positions 0 .. Tk-1; query head h
+    reads key/value head h // (H / Hkv)."""
+    H, Hkv, D = q.shape[1], k.shape[1], q.shape[-1]
+    kk = k.repeat_interleave(H // Hkv, dim=1)
+    vv = v.repeat_interleave(H // Hkv, dim=1)
+    s = torch.matmul(q, kk.transpose(-1, -2)) / math.sqrt(D)
+    s = s.masked_fill(torch.arange(k.shape[2])[None, :] > q_pos[:, None], float("-inf"))
+    return torch.matmul(torch.softmax(s, dim=-1), vv)
+
+
+def hybrid_generate(params: Dict[str, Tensor], prompt_ids: Tensor, decode_ids: Tensor, *, num_layers: int,
+                    num_heads: int, num_kv_heads: int, dense_every: int, top_k: int, recompute_every: int,
+                    rope_theta: float = 10000.0, eps: float = 1e-6, write_mode: str = "direct",
+                    alpha_max: float = 0.25, tau_c: float = 0.1) -> Tuple[Tensor, Tensor]:
+    """Logits of the config-4 hybrid decoder in fp32: the prompt [B, T] in one pass, then
+    the tokens decode_ids [B, n] one at a time (token s at position T + s).
+
+    Layer i is a dense GQA attention block when i % dense_every == 0
+    (modelings/hybrid_dense_delta_topk.py:195-244, :394-437, dense every 4th at :398)
+    and an SGSA block otherwise (SGSABlock, modelings/modeling_sgsa.py:669-709): the
+    prompt through ``sgsa_layer_forward``, each decoded token through
+    ``sgsa_decode_step``, which selects its top-k when s % recompute_every == 0 and
+    re-scores the layer's kept candidates otherwise.  ``params`` uses the names of
+    sgsa_amd.hybrid.HybridForCausalLM.  Returns (prompt logits [B, T, V], decode
+    logits [B, n, V]).
+    """
+    P = {k: v.float() for k, v in params.items()}
+    B, T = prompt_ids.shape
+    C = P["embed_tokens.weight"].shape[1]
+    H, Hkv = num_heads, num_kv_heads
+    D = C // H
+    head = P.get("lm_head.weight", P["embed_tokens.weight"])
+    caches: List[dict] = [dict() for _ in range(num_layers)]
+
+    def mlp(i, h):
+        w = lambda n: P[f"layers.{i}.{n}"]
+        m = rms_norm(h, w("post_attn_norm.weight"), eps)
+        return h + (F.silu(m @ w("mlp.gate_proj.weight").T) * (m @ w("mlp.up_proj.weight").T)) @ \
+            w("mlp.down_proj.weight").T
+
+    def run(ids: Tensor, pos0: int, step: Optional[int]) -> Tensor:
+        n_t = ids.shape[1]
+        h = P["embed_tokens.weight"][ids]
+        pos = torch.arange(pos0, pos0 + n_t)
+        for i in range(num_layers):
+            w = lambda n: P[f"layers.{i}.{n}"]
+            c = caches[i]
+            nrm = rms_norm(h, w("input_norm.weight"), eps)
+            if i % dense_every == 0:
+                q = rope_apply((nrm @ w("q_proj.weight").T).view(B, n_t, H, D).transpose(1, 2), pos, rope_theta)
+                k = rope_apply((nrm @ w("k_proj.weight").T).view(B, n_t, Hkv, D).transpose(1, 2), pos, rope_theta)
+                v = (nrm @ w("v_proj.weight").T).view(B, n_t, Hkv, D).transpose(1, 2)
+                c["k"] = k if step is None else torch.cat((c["k"], k), dim=2)
+                c["v"] = v if step is None else torch.cat((c["v"], v), dim=2)
+                att = dense_gqa_attention(q, c["k"], c["v"], pos)
+                h = h + att.transpose(1, 2).reshape(B, n_t, C) @ w("o_proj.weight").T
+            else:
+                q = (nrm @ w("q_proj.weight").T).view(B, n_t, H, D)
+                k = (nrm @ w("k_proj.weight").T).view(B, n_t, H, D)
+                v = (nrm @ w("v_proj.weight").T).view(B, n_t, H, D)
+                q_ret = (nrm @ w("q_ret_proj.weight").T).view(B, n_t, H, D)
+                beta = torch.sigmoid(nrm @ w("beta_proj.weight").T + w("beta_proj.bias")).clamp_min(1e-4)
+                gamma = torch.sigmoid(nrm @ w("gamma_proj.weight").T + w("gamma_proj.bias"))
+                budget = nrm @ w("budget_proj.weight").T + w("budget_proj.bias")
+                if step is None:
+                    lay = sgsa_layer_forward(q, k, v, q_ret, beta, gamma, budget, top_k, write_mode=write_mode,
+                                             alpha_max=alpha_max, tau_c=tau_c)
+                    o = lay["o"]
+                    c["k"], c["v"], c["state"], c["cand"] = k, v, lay["final_state"], None
+                else:
+                    c["k"] = torch.cat((c["k"], k), dim=1)
+                    c["v"] = torch.cat((c["v"], v), dim=1)
+                    select = step % recompute_every == 0 or c["cand"] is None
+                    o, c["state"], c["cand"] = sgsa_decode_step(
+                        q, k, v, q_ret, beta, gamma, budget, c["k"], c["v"], c["state"], top_k, write_mode,
+                        alpha_max, tau_c, candidates=None if select else c["cand"])
+                h = h + o.reshape(B, n_t, C) @ w("o_proj.weight").T
+            h = mlp(i, h)
+        return rms_norm(h, P["norm.weight"], eps) @ head.T
+
+    prompt_logits = run(prompt_ids, 0, None)
+    dec = [run(decode_ids[:, s:s + 1], T + s, s) for s in range(decode_ids.shape[1])]
+    return prompt_logits, (torch.cat(dec, dim=1) if dec else prompt_logits[:, :0])
 
 
 # ---------------------------------------------------------------------------

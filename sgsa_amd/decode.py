@@ -50,11 +50,15 @@ def sgsa_decode_step(
     tau_c: float = 0.1,
     candidates: Optional[Tuple[Tensor, Tensor]] = None,
     return_candidates: bool = False,
+    length: Optional[int] = None,
 ):
     """q, k, v, q_ret [B,1,H,D]; beta, gamma, budget_logits [B,1,H];
     k_cache, v_cache [B,Tc,H,D] (ending with this token); state [B,H,D,D] fp32.
     candidates: (indices int32 [B,H,1,n], counts int32 [B,H,1]) to re-score
-    instead of selecting (top-k reuse); indices must be < Tc.
+    instead of selecting (top-k reuse); indices must be < Tc.  length: the
+    number of valid cache positions when k_cache / v_cache are a preallocated
+    buffer longer than that (the token then sits at length - 1); the kernels
+    address the buffer in place.
 
     Returns (o [B,1,H,D] in q.dtype, new state [B,H,D,D] fp32), and the step's
     candidates (selected or reused) as a third item when return_candidates.
@@ -64,14 +68,20 @@ def sgsa_decode_step(
     B, one, H, D = q.shape
     if one != 1:
         raise ValueError(f"sgsa_decode_step takes one token per sequence, got T={one}")
-    Tc = k_cache.shape[1]
-    if k_cache.shape != (B, Tc, H, D) or v_cache.shape != (B, Tc, H, D):
+    Tbuf = k_cache.shape[1]
+    if k_cache.shape != (B, Tbuf, H, D) or v_cache.shape != (B, Tbuf, H, D):
         raise ValueError("k_cache / v_cache must be [B, Tc, H, D] like q")
+    Tc = Tbuf if length is None else int(length)
+    if not 1 <= Tc <= Tbuf:
+        raise ValueError(f"length={length} must be in [1, {Tbuf}]")
     if write_mode not in _WRITE_MODES:
         raise ValueError(f"write_mode must be one of {sorted(_WRITE_MODES)}")
     dt = q.dtype
     dev = q.device
-    rc, kc, vc, kn = (t.to(dt).contiguous() for t in (q_ret, k_cache, v_cache, k))
+    rc, kn = (t.to(dt).contiguous() for t in (q_ret, k))
+    # a contiguous cache of q's dtype is addressed in place (rows >= Tc are never read: the
+    # selection is causal and the indices are < Tc); anything else is copied first
+    kc, vc = (t if (t.dtype == dt and t.is_contiguous()) else t.to(dt).contiguous() for t in (k_cache, v_cache))
     L = _abi.lib()
     if candidates is None:
         # 1. top-k of the new query over the cache (causal: position Tc - 1)
@@ -83,7 +93,7 @@ def sgsa_decode_step(
         nb = ctypes.c_size_t()
         _abi.check(L.sgsa_score_topk_workspace_size(B, 1, H, ctypes.byref(nb)))
         tws = torch.empty(nb.value, device=dev, dtype=torch.uint8)
-        _abi.check(L.sgsa_score_topk(_abi.dtype_code(dt), B, 1, Tc, H, D, kk, 1, Tc - 1, math.sqrt(D), 0,
+        _abi.check(L.sgsa_score_topk(_abi.dtype_code(dt), B, 1, Tbuf, H, D, kk, 1, Tc - 1, math.sqrt(D), 0,
                                      _abi.ptr(rc), _abi.ptr(kc), _abi.ptr(idx), _abi.ptr(sc), _abi.ptr(top2),
                                      _abi.ptr(cnt), None, 0, _abi.ptr(tws), nb.value, _abi.stream_of(rc)))
     else:
@@ -97,7 +107,7 @@ def sgsa_decode_step(
         kk = idx.shape[-1]
         sc = torch.empty(B, H, 1, kk, device=dev, dtype=torch.float32)
         top2 = None
-        _abi.check(L.sgsa_score_at(_abi.dtype_code(dt), B, 1, Tc, H, D, kk, math.sqrt(D), 0, _abi.ptr(rc),
+        _abi.check(L.sgsa_score_at(_abi.dtype_code(dt), B, 1, Tbuf, H, D, kk, math.sqrt(D), 0, _abi.ptr(rc),
                                    _abi.ptr(kc), _abi.ptr(idx), _abi.ptr(cnt), _abi.ptr(sc), _abi.stream_of(rc)))
     # 2. weights, k_hat / write key, v_hat and the gate for that row
     mode = _WRITE_MODES[write_mode]
@@ -106,7 +116,7 @@ def sgsa_decode_step(
     al = torch.empty(B, 1, H, device=dev, dtype=torch.float32)
     bud = budget_logits.float().contiguous()
     _abi.check(L.sgsa_sparse_gather(
-        _abi.dtype_code(dt), B, 1, Tc, H, D, kk, Tc - 1, _abi.ptr(kc), _abi.ptr(vc), _abi.ptr(kn), _abi.ptr(idx),
+        _abi.dtype_code(dt), B, 1, Tbuf, H, D, kk, Tc - 1, _abi.ptr(kc), _abi.ptr(vc), _abi.ptr(kn), _abi.ptr(idx),
         _abi.ptr(sc), _abi.ptr(top2), _abi.ptr(cnt), _abi.ptr(bud), mode, float(alpha_max), float(tau_c), 64, 8,
         _abi.ptr(wk if mode == 0 else None), _abi.ptr(vh), _abi.ptr(wk if mode == 1 else None), _abi.ptr(al),
         None, None, None, 0, _abi.stream_of(kc)))

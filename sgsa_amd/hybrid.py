@@ -1,0 +1,335 @@
+"""Config 4: a hybrid decoder of SGSA layers and dense GQA attention layers, with
+prefill and greedy decode.
+
+Layer i is dense full attention when i % dense_every == 0 and an SGSA block
+otherwise: the 3:1 scheduling of the reference's hybrid stack
+(modelings/hybrid_dense_delta_topk.py:394-437, dense every 4th layer at :398),
+with the reference's SGSABlock (modelings/modeling_sgsa.py:634-709, here
+sgsa_amd.model.SGSABlock on the HIP kernels) as the sparse layer.
+
+* Dense layers: RMSNorm, q / k / v projections with num_kv_heads key/value heads
+  (grouped-query attention: query head h reads key/value head h // (H / Hkv)),
+  rotary embedding in the reference's rotate-half form (:124-150), causal
+  softmax attention with scores in the activation dtype and the softmax in
+  fp32 (:178-192), o_proj; then the SwiGLU MLP (:106-116).  PyTorch GEMMs.
+* SGSA layers: prefill is sgsa_layer_forward over the prompt (K1, K2, K3-K5),
+  keeping the layer's keys, values and final state; a decode step is
+  sgsa_decode_step over the cache (K1 one row, K2, K6).  Each layer selects
+  its top-k every ``topk_recompute_every`` decode steps and re-scores that
+  candidate set in between (sgsa_score_at; modelings/idea.md:395-401).
+* Caches are preallocated for prompt + decode steps: [B, Hkv, Tmax, D] keys
+  (after RoPE) and values per dense layer, [B, Tmax, H, D] keys and values plus
+  the fp32 [B, H, D, D] state and the candidate set per SGSA layer.
+
+No right-hand operand of an attention product is a transposed view: scores
+are Q K^T with K^T copied contiguous (prefill) or K Q^T with Q^T copied
+contiguous (decode), and the values are a row-major slice of the cache.
+Inference only.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import List, Optional, Tuple
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from .decode import sgsa_decode_step
+from .layer import LayerWorkspace, sgsa_layer_forward
+from .model import GatedMLP, RMSNorm, SGSABlock, SGSAConfig
+
+Tensor = torch.Tensor
+
+
+@dataclass
+class HybridConfig:
+    """Config 4 defaults: 24 layers, hidden 2048, 16 query / 4 key-value heads of 128,
+    SwiGLU 5632, vocab 32000, top-k 2048 recomputed every 4 decode steps."""
+
+    vocab_size: int = 32000
+    hidden_size: int = 2048
+    intermediate_size: int = 5632
+    num_hidden_layers: int = 24
+    num_attention_heads: int = 16
+    num_kv_heads: int = 4
+    dense_every: int = 4
+    rope_theta: float = 10000.0
+    layer_norm_eps: float = 1e-6
+    top_k: int = 2048
+    topk_recompute_every: int = 4
+    sgsa_write_mode: str = "direct"
+    alpha_max: float = 0.25
+    tau_c: float = 0.1
+    tie_word_embeddings: bool = True
+    pad_token_id: int = 0
+
+    @property
+    def head_dim(self) -> int:
+        if self.hidden_size % self.num_attention_heads != 0:
+            raise ValueError("hidden_size must be divisible by num_attention_heads")
+        return self.hidden_size // self.num_attention_heads
+
+    def is_dense(self, i: int) -> bool:
+        return i % self.dense_every == 0
+
+    def sgsa_config(self) -> SGSAConfig:
+        return SGSAConfig(vocab_size=self.vocab_size, hidden_size=self.hidden_size,
+                          intermediate_size=self.intermediate_size, num_hidden_layers=1,
+                          num_attention_heads=self.num_attention_heads, num_kv_heads=self.num_attention_heads,
+                          layer_norm_eps=self.layer_norm_eps, top_k=self.top_k,
+                          sgsa_write_mode=self.sgsa_write_mode, alpha_max=self.alpha_max, tau_c=self.tau_c)
+
+
+def rope_tables(n: int, head_dim: int, theta: float, device) -> Tuple[Tensor, Tensor]:
+    """cos, sin [n, head_dim] in fp32 (modelings/hybrid_dense_delta_topk.py:124-137)."""
+    inv_freq = 1.0 / (theta ** (torch.arange(0, head_dim, 2, device=device).float() / head_dim))
+    freqs = torch.outer(torch.arange(n, device=device, dtype=torch.float32), inv_freq)
+    emb = torch.cat((freqs, freqs), dim=-1)
+    return emb.cos(), emb.sin()
+
+
+def apply_rope(x: Tensor, cos: Tensor, sin: Tensor) -> Tensor:
+    """x [B, heads, T, D] at the positions of cos / sin [T, D] (:140-150), in x's dtype."""
+    half = x.shape[-1] // 2
+    rot = torch.cat((-x[..., half:], x[..., :half]), dim=-1)
+    return x * cos.to(x.dtype) + rot * sin.to(x.dtype)
+
+
+def gqa_attention(q: Tensor, k: Tensor, v: Tensor, pos0: int, block: int = 1024) -> Tensor:
+    """Causal attention: q [B, H, Tq, D] at positions pos0 .., k / v [B, Hkv, Tk, D]
+    with Tk >= pos0 + Tq.  Scores in q's dtype, softmax in fp32, probabilities cast
+    back (:178-192).  Query blocks of ``block`` rows read only the keys they may see.
+    Long query blocks (prefill) form Q K^T with a contiguous copy of the block's K^T
+    and a softmax over the last dimension; short ones (decode) form K Q^T, which
+    reads the cache in place."""
+    B, H, Tq, D = q.shape
+    Hkv = k.shape[1]
+    G = H // Hkv
+    out = torch.empty_like(q)
+    qg = q.reshape(B, Hkv, G, Tq, D)
+    kpos = torch.arange(k.shape[2], device=q.device)
+    if Tq >= 64:
+        for r0 in range(0, Tq, block):
+            r1 = min(Tq, r0 + block)
+            n = r1 - r0
+            kend = pos0 + r1
+            qb = qg[:, :, :, r0:r1].reshape(B, Hkv, G * n, D)
+            kt = k[:, :, :kend].transpose(-1, -2).contiguous()                                  # [B,Hkv,D,kend]
+            s = torch.matmul(qb, kt).float() * (1.0 / math.sqrt(D))                             # [B,Hkv,G*n,kend]
+            qpos = (pos0 + r0 + torch.arange(n, device=q.device)).repeat(G)
+            s = s.masked_fill(kpos[None, :kend] > qpos[:, None], float("-inf"))
+            p = torch.softmax(s, dim=-1).to(q.dtype)
+            o = torch.matmul(p, v[:, :, :kend])   # a row-major slice of the cache, not a transposed view
+            out[:, :, r0:r1] = o.view(B, Hkv, G, n, D).reshape(B, H, n, D)
+        return out
+    for r0 in range(0, Tq, block):
+        r1 = min(Tq, r0 + block)
+        n = r1 - r0
+        kend = pos0 + r1
+        qb = qg[:, :, :, r0:r1].reshape(B, Hkv, G * n, D).transpose(-1, -2).contiguous()   # [B,Hkv,D,G*n]
+        s = torch.matmul(k[:, :, :kend], qb).float() * (1.0 / math.sqrt(D))               # [B,Hkv,kend,G*n]
+        qpos = (pos0 + r0 + torch.arange(n, device=q.device)).repeat(G)                    # column -> position
+        s = s.masked_fill(kpos[:kend, None] > qpos[None, :], float("-inf"))
+        p = torch.softmax(s, dim=-2).to(q.dtype).transpose(-1, -2).contiguous()             # [B,Hkv,G*n,kend]
+        o = torch.matmul(p, v[:, :, :kend])   # [B,Hkv,G*n,D]; a row-major slice, not a transposed view
+        out[:, :, r0:r1] = o.view(B, Hkv, G, n, D).reshape(B, H, n, D)
+    return out
+
+
+class DenseGQABlock(nn.Module):
+    """Dense full-attention block of the hybrid stack (:195-244, :407-437), with grouped key/value heads."""
+
+    def __init__(self, config: HybridConfig) -> None:
+        super().__init__()
+        H, Hkv, D, C = config.num_attention_heads, config.num_kv_heads, config.head_dim, config.hidden_size
+        if H % Hkv != 0:
+            raise ValueError("num_attention_heads must be a multiple of num_kv_heads")
+        self.H, self.Hkv, self.D = H, Hkv, D
+        self.input_norm = RMSNorm(C, config.layer_norm_eps)
+        self.post_attn_norm = RMSNorm(C, config.layer_norm_eps)
+        self.q_proj = nn.Linear(C, H * D, bias=False)
+        self.k_proj = nn.Linear(C, Hkv * D, bias=False)
+        self.v_proj = nn.Linear(C, Hkv * D, bias=False)
+        self.o_proj = nn.Linear(H * D, C, bias=False)
+        self.mlp = GatedMLP(C, config.intermediate_size)
+
+    def forward_cached(self, h: Tensor, pos0: int, cache: dict, rope: Tuple[Tensor, Tensor]) -> Tensor:
+        """h [B, T, C] at positions pos0 ..; appends its keys and values to the cache."""
+        B, T, C = h.shape
+        n = self.input_norm(h)
+        q = self.q_proj(n).view(B, T, self.H, self.D).transpose(1, 2)
+        k = self.k_proj(n).view(B, T, self.Hkv, self.D).transpose(1, 2)
+        v = self.v_proj(n).view(B, T, self.Hkv, self.D).transpose(1, 2)
+        cos, sin = rope[0][pos0:pos0 + T], rope[1][pos0:pos0 + T]
+        q, k = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
+        cache["k"][:, :, pos0:pos0 + T] = k
+        cache["v"][:, :, pos0:pos0 + T] = v
+        att = gqa_attention(q, cache["k"][:, :, :pos0 + T], cache["v"][:, :, :pos0 + T], pos0)
+        h = h + self.o_proj(att.transpose(1, 2).reshape(B, T, self.H * self.D))
+        return h + self.mlp(self.post_attn_norm(h))
+
+
+class SGSADecoderBlock(SGSABlock):
+    """SGSABlock with a prefill that keeps its cache and a one-token decode step."""
+
+    def _project(self, h: Tensor):
+        B, T, C = h.shape
+        H, D = self.num_heads, self.head_dim
+        n = self.input_norm(h)
+        q = self.q_proj(n).view(B, T, H, D)
+        k = self.k_proj(n).view(B, T, H, D)
+        v = self.v_proj(n).view(B, T, H, D)
+        q_ret = self.q_ret_proj(n).view(B, T, H, D)
+        beta = torch.sigmoid(self.beta_proj(n).float()).clamp_min(1e-4)
+        gamma = torch.sigmoid(self.gamma_proj(n).float())
+        budget = self.budget_proj(n).float()
+        return q, k, v, q_ret, beta, gamma, budget
+
+    def _finish(self, h: Tensor, att: Tensor) -> Tensor:
+        B, T, C = h.shape
+        h = h + self.o_proj(att.reshape(B, T, C))
+        return h + self.mlp(self.post_attn_norm(h))
+
+    def prefill(self, h: Tensor, cache: dict) -> Tensor:
+        cfg = self.config
+        T = h.shape[1]
+        q, k, v, q_ret, beta, gamma, budget = self._project(h)
+        att, st = sgsa_layer_forward(q, k, v, q_ret, beta, gamma, budget, cfg.top_k, write_mode=cfg.sgsa_write_mode,
+                                     alpha_max=cfg.alpha_max, tau_c=cfg.tau_c, output_final_state=True,
+                                     workspace=self._ws)
+        cache["k"][:, :T] = k
+        cache["v"][:, :T] = v
+        cache["state"] = st
+        cache["cand"] = None
+        return self._finish(h, att)
+
+    def decode(self, h: Tensor, pos: int, cache: dict, select: bool) -> Tensor:
+        """h [B, 1, C] at position pos; select: recompute the top-k (else re-score the kept set)."""
+        cfg = self.config
+        q, k, v, q_ret, beta, gamma, budget = self._project(h)
+        cache["k"][:, pos:pos + 1] = k
+        cache["v"][:, pos:pos + 1] = v
+        cand = None if (select or cache["cand"] is None) else cache["cand"]
+        att, st, cand = sgsa_decode_step(q, k, v, q_ret, beta, gamma, budget, cache["k"], cache["v"],
+                                         cache["state"], cfg.top_k, write_mode=cfg.sgsa_write_mode,
+                                         alpha_max=cfg.alpha_max, tau_c=cfg.tau_c, candidates=cand,
+                                         return_candidates=True, length=pos + 1)
+        cache["state"], cache["cand"] = st, cand
+        return self._finish(h, att)
+
+
+class HybridForCausalLM(nn.Module):
+    """Embedding, the hybrid stack, final RMSNorm and (tied) LM head (:439-532)."""
+
+    def __init__(self, config: HybridConfig) -> None:
+        super().__init__()
+        self.config = config
+        self.embed_tokens = nn.Embedding(config.vocab_size, config.hidden_size, padding_idx=config.pad_token_id)
+        scfg = config.sgsa_config()
+        self.layers = nn.ModuleList([DenseGQABlock(config) if config.is_dense(i) else SGSADecoderBlock(scfg)
+                                     for i in range(config.num_hidden_layers)])
+        shared = LayerWorkspace()   # the SGSA layers run one at a time: one workspace serves them all
+        for layer in self.layers:
+            if isinstance(layer, SGSADecoderBlock):
+                layer._ws = shared
+        self.norm = RMSNorm(config.hidden_size, config.layer_norm_eps)
+        self.lm_head = nn.Linear(config.hidden_size, config.vocab_size, bias=False)
+        if config.tie_word_embeddings:
+            self.lm_head.weight = self.embed_tokens.weight
+
+    def init_weights(self, std: float = 0.02, qk_std: Optional[float] = None, generator=None) -> None:
+        """Normal(0, std) weights, zero biases, unit norms (:455-464).  qk_std replaces std for
+        the SGSA layers' q / k / q_ret projections: at std 0.02 their keys leave the delta rule's
+        stable range (|k|^2 ~ 0.0004 C D), as sgsa_amd.model.SGSAForCausalLM.init_weights explains."""
+        with torch.no_grad():
+            for name, p in self.named_parameters():
+                if name.endswith("bias"):
+                    p.zero_()
+                elif p.dim() == 1:
+                    p.fill_(1.0)
+                else:
+                    s = std
+                    layer = int(name.split(".")[1]) if name.startswith("layers.") else -1
+                    sgsa_qk = layer >= 0 and not self.config.is_dense(layer) and \
+                        any(t in name for t in ("q_proj", "k_proj", "q_ret_proj"))
+                    if qk_std is not None and sgsa_qk:
+                        s = qk_std
+                    p.copy_(torch.randn(p.shape, generator=generator, dtype=torch.float32) * s)
+
+    def new_cache(self, B: int, T_max: int, device, dtype) -> List[dict]:
+        cfg = self.config
+        H, Hkv, D = cfg.num_attention_heads, cfg.num_kv_heads, cfg.head_dim
+        caches = []
+        for i in range(cfg.num_hidden_layers):
+            if cfg.is_dense(i):
+                caches.append({"k": torch.empty(B, Hkv, T_max, D, device=device, dtype=dtype),
+                               "v": torch.empty(B, Hkv, T_max, D, device=device, dtype=dtype)})
+            else:
+                caches.append({"k": torch.empty(B, T_max, H, D, device=device, dtype=dtype),
+                               "v": torch.empty(B, T_max, H, D, device=device, dtype=dtype),
+                               "state": None, "cand": None})
+        return caches
+
+    def _head(self, h: Tensor) -> Tensor:
+        return self.lm_head(self.norm(h))
+
+    @torch.no_grad()
+    def prefill(self, input_ids: Tensor, caches: List[dict], rope: Tuple[Tensor, Tensor]) -> Tensor:
+        """Runs the prompt [B, T]; fills the caches; returns logits [B, T, V]."""
+        h = self.embed_tokens(input_ids)
+        for layer, cache in zip(self.layers, caches):
+            h = layer.forward_cached(h, 0, cache, rope) if isinstance(layer, DenseGQABlock) else layer.prefill(h, cache)
+        return self._head(h)
+
+    @torch.no_grad()
+    def decode_step(self, tokens: Tensor, pos: int, step: int, caches: List[dict],
+                    rope: Tuple[Tensor, Tensor]) -> Tensor:
+        """tokens [B] at position pos, the step-th generated token; returns logits [B, V].
+        SGSA layers select their top-k when step % topk_recompute_every == 0."""
+        select = step % self.config.topk_recompute_every == 0
+        h = self.embed_tokens(tokens[:, None])
+        for layer, cache in zip(self.layers, caches):
+            if isinstance(layer, DenseGQABlock):
+                h = layer.forward_cached(h, pos, cache, rope)
+            else:
+                h = layer.decode(h, pos, cache, select)
+        return self._head(h)[:, 0]
+
+
+def expand_caches(caches: List[dict], B: int) -> List[dict]:
+    """Caches of one sequence repeated for B sequences (prefill at B = 1, decode at B)."""
+    out = []
+    for c in caches:
+        e = {}
+        for name, t in c.items():
+            e[name] = None if t is None else (t.expand(B, *t.shape[1:]).contiguous() if t.shape[0] == 1 else t)
+        out.append(e)
+    return out
+
+
+@torch.no_grad()
+def generate(model: HybridForCausalLM, prompt: Tensor, steps: int, batch: Optional[int] = None):
+    """Greedy decoding: prefill ``prompt`` [Bp, T], then ``steps`` decode steps for ``batch``
+    sequences (the prompt's caches repeated when Bp = 1).  Step s takes the previous
+    greedy token (the prefill's for s = 0) at position T + s.  Returns (prefill logits
+    [Bp, T, V], the tokens the decode steps produced [B, steps])."""
+    cfg = model.config
+    Bp, T = prompt.shape
+    B = Bp if batch is None else batch
+    if Bp != B and Bp != 1:
+        raise ValueError("batch differs from the prompt batch, which must then be 1")
+    dev, dt = prompt.device, model.embed_tokens.weight.dtype
+    rope = rope_tables(T + steps, cfg.head_dim, cfg.rope_theta, dev)
+    caches = model.new_cache(Bp, T + steps, dev, dt)
+    logits = model.prefill(prompt, caches, rope)
+    if B != Bp:
+        caches = expand_caches(caches, B)
+    tok = logits[:, -1].argmax(-1).expand(B).contiguous() if Bp == 1 else logits[:, -1].argmax(-1)
+    out = torch.empty(B, steps, dtype=torch.long, device=dev)
+    for s in range(steps):
+        tok = model.decode_step(tok, T + s, s, caches, rope).argmax(-1)
+        out[:, s] = tok
+    return logits, out
