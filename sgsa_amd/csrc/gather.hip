@@ -334,50 +334,53 @@ hipError_t launch_sparse_gather(const GatherArgs& a, hipStream_t st) {
 
 // Scores at given keys, for top-k reuse across decode steps: for every row r
 // and slot i < counts[r], scores[r, i] = (q_r . k_{indices[r, i]}) * mscale in
-// fp32.  One wave per row; each 16-lane group takes one key per step (lane l16
-// holds dims l16 + 16 m of the query and of the key row), and the partial dot
-// products are summed over the group with lane swaps.  Indices outside [0, Tk)
-// score 0.
-template <typename X>
+// fp32.  A block takes 256 slots of one row (decode has few rows, so the slots
+// are what fills the GPU); each 16-lane group of a wave takes one key per step,
+// and with D <= 128 and D % 8 == 0 each lane reads 8 consecutive elements (16
+// bytes of bf16) of the query and the key.  Partial dot products are summed over
+// the group with lane swaps.  Indices outside [0, Tk) score 0.
+constexpr int RS_SLOTS = 256;   // slots per block
+
+template <typename X, bool VEC>
 __global__ __launch_bounds__(256) void rescore_kernel(int B, int Tq, int Tk, int H, int D, int top_k,
                                                      const X* __restrict__ q, const X* __restrict__ k,
                                                      const int32_t* __restrict__ indices,
                                                      const int32_t* __restrict__ counts, float mscale,
                                                      float* __restrict__ scores) {
-  const long nrows = (long)B * H * Tq;
-  const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= nrows) return;   // wave-uniform
+  const int nchunk = (top_k + RS_SLOTS - 1) / RS_SLOTS;
+  const long row = blockIdx.x / nchunk;
+  const int base = (blockIdx.x % nchunk) * RS_SLOTS + (threadIdx.x >> 6) * 64;   // the wave's 64 slots
   const int lane = threadIdx.x & 63, grp = lane >> 4, l16 = lane & 15;
   const int qr = (int)(row % Tq);
   const long bh = row / Tq;
   const int h = (int)(bh % H), b = (int)(bh / H);
+  const int kq = min(counts[row], top_k);
+  if (base >= kq) return;   // wave-uniform
   const long qoff = ((long)(b * Tq + qr) * H + h) * D;
+  // element e of the lane: dim VEC ? 8 l16 + e : l16 + 16 e
+  auto dim = [&](int e) { return VEC ? 8 * l16 + e : l16 + 16 * e; };
   float qv[8];
 #pragma unroll
-  for (int m = 0; m < 8; ++m) {
-    const int d = l16 + 16 * m;
-    qv[m] = d < D ? ld(q, qoff + d) : 0.f;
-  }
-  const int kq = min(counts[row], top_k);
+  for (int e = 0; e < 8; ++e) qv[e] = dim(e) < D ? ld(q, qoff + dim(e)) : 0.f;
   const int32_t* ip = indices + row * top_k;
   float* sp = scores + row * top_k;
-  for (int i0 = 0; i0 < kq; i0 += 4) {
+  const int nend = min(kq, base + 64);
+#pragma unroll 4
+  for (int i0 = base; i0 < nend; i0 += 4) {
     const int i = i0 + grp;
     float acc = 0.f;
-    if (i < kq) {
+    if (i < nend) {
       const int j = ip[i];
       if (j >= 0 && j < Tk) {
         const long koff = ((long)(b * Tk + j) * H + h) * D;
 #pragma unroll
-        for (int m = 0; m < 8; ++m) {
-          const int d = l16 + 16 * m;
-          if (d < D) acc = fmaf(qv[m], ld(k, koff + d), acc);
-        }
+        for (int e = 0; e < 8; ++e)
+          if (dim(e) < D) acc = fmaf(qv[e], ld(k, koff + dim(e)), acc);
       }
     }
 #pragma unroll
     for (int o = 1; o < 16; o <<= 1) acc += __shfl_xor(acc, o, 64);
-    if (i < kq && l16 == 0) sp[i] = acc * mscale;
+    if (i < nend && l16 == 0) sp[i] = acc * mscale;
   }
 }
 
@@ -385,13 +388,15 @@ hipError_t launch_rescore(int dtype, int B, int Tq, int Tk, int H, int D, int to
                           const int32_t* indices, const int32_t* counts, float mscale, float* scores,
                           hipStream_t st) {
   const long nrows = (long)B * H * Tq;
-  const dim3 grid((unsigned)((nrows + 3) / 4));
-  if (dtype == DT_F32)
-    rescore_kernel<float><<<grid, 256, 0, st>>>(B, Tq, Tk, H, D, top_k, (const float*)q, (const float*)k, indices,
-                                                counts, mscale, scores);
-  else
-    rescore_kernel<bf16_t><<<grid, 256, 0, st>>>(B, Tq, Tk, H, D, top_k, (const bf16_t*)q, (const bf16_t*)k,
-                                                 indices, counts, mscale, scores);
+  const long nchunk = (top_k + RS_SLOTS - 1) / RS_SLOTS;
+  const dim3 grid((unsigned)(nrows * nchunk));
+  const bool vec = D % 8 == 0;   // 8 consecutive elements per lane cover D <= 128
+#define SGSA_RESCORE(XT, V)                                                                          \
+  rescore_kernel<XT, V><<<grid, 256, 0, st>>>(B, Tq, Tk, H, D, top_k, (const XT*)q, (const XT*)k, indices, \
+                                              counts, mscale, scores)
+  if (dtype == DT_F32) { if (vec) SGSA_RESCORE(float, true); else SGSA_RESCORE(float, false); }
+  else { if (vec) SGSA_RESCORE(bf16_t, true); else SGSA_RESCORE(bf16_t, false); }
+#undef SGSA_RESCORE
   return hipGetLastError();
 }
 
