@@ -149,6 +149,34 @@ int sgsa_score_at(int dtype, int B, int Tq, int Tk, int H, int D, int top_k, flo
  * top-k weights with MFMA.  Needs the unsorted output of sgsa_score_topk with
  * top2 and split; computes k_hat, v_hat, the write key and alpha (no
  * weights / diagnostics outputs).  Same references as sgsa_sparse_gather. */
+/* ---- block retrieval modes --------------------------------------------------
+ * SparseRetriever.forward with retrieval_mode "block_only" (mode 0) or
+ * "block_token" (mode 1) on its torch path (modelings/modeling_sgsa.py:444-463;
+ * block selection :167-195, candidates :302-359, diagnostics :361-405).
+ * Scores (q.k)/sqrt(D); key block b = keys [b*block_size, (b+1)*block_size);
+ * block score = max causal score of the block (-FLT_MAX if none); each row
+ * keeps eb = min(top_blocks, nb) blocks (nb = ceil(T/block_size)), score
+ * desc, ties to the lowest index, padded with 0 (:188-195).  Candidates = the
+ * causal keys of the kept blocks; eb * min(block_size, T) <= 2048.
+ * Outputs: block_indices [B,H,T,eb]; block_scores [B,H,T,nb] (may be NULL:
+ * then held in the workspace); k_hat, v_hat [B,T,H,D]; diag
+ * [SGSA_NDIAG,B,H,T] (may be NULL; block_only leaves planes 6-9 meaningless,
+ * as the reference has no token indices there).
+ *   mode 1: indices [B,H,T,kk], kk = min(top_k, T): the masked top-k of the
+ *     candidates (:322-330), weights [B,H,T,kk] (may be NULL);
+ *   mode 0: indices unused (NULL), weights [B,H,T,T] dense (may be NULL),
+ *     margin = kept block index 0 - index 1 (:455-463).
+ * Workspace: sgsa_block_retrieve_workspace_size() bytes, with own_block_scores
+ * = 1 when block_scores is NULL. */
+int sgsa_block_retrieve_workspace_size(int B, int T, int H, int top_k, int block_size, int top_blocks, int mode,
+                                       int own_block_scores, size_t* bytes);
+int sgsa_block_retrieve(int dtype, int B, int T, int H, int D, int top_k, int block_size, int top_blocks,
+                        int mode, int causal, float tau_c, int local_window, int sink_size,
+                        const void* q, const void* k, const void* v,
+                        int32_t* indices, int32_t* block_indices, float* block_scores, float* weights,
+                        void* k_hat, void* v_hat, float* diag, void* workspace, size_t workspace_bytes,
+                        void* stream);
+
 int sgsa_sparse_gather_tiled(int B, int T, int H, int D, int top_k, const void* k, const void* v,
                              const int32_t* indices, const float* scores, const float* top2,
                              const int32_t* counts, const int32_t* split, const float* budget,

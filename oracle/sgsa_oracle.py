@@ -314,6 +314,85 @@ def token_topk_retrieval(
     }
 
 
+def block_retrieval(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    top_k: int,
+    block_size: int,
+    top_blocks: int,
+    mode: str = "block_token",
+    causal: bool = True,
+    tau_c: float = 0.1,
+    local_window: int = 64,
+    sink_size: int = 8,
+    eps: float = 1e-6,
+) -> Dict[str, object]:
+    """Block retrieval modes of SparseRetriever.forward on its torch path (no flash_moba;
+    modelings/modeling_sgsa.py:444-463), causal or not (:423-424), no padding mask.
+
+    Scores ``q k^T / sqrt(d)`` (:420).  Block b holds keys [b bs, (b+1) bs)
+    (:167-170); its score is the max over its causal keys, finfo.min when it has
+    none (:172-186); the row keeps the top ``top_blocks`` blocks through the masked
+    top-k (:188-195, lowest index on ties).  Candidates are the causal keys of the
+    kept blocks (:313-320).  ``block_token``: the masked top-k of the candidates,
+    softmax weights times validity, renormalised (:322-344).  ``block_only``:
+    softmax over every key of the row with non-candidates at finfo.min, times the
+    candidate mask, renormalised, so k_hat / v_hat are dense products (:346-359);
+    its diagnostics read the kept block indices as the selected scores and have no
+    token indices (:360-361, :455-463).  Inputs [B,T,H,D]; returns the dict of
+    token_topk_retrieval (k_hat / v_hat [B,T,H,D], the rest [B,H,T,*]).
+    """
+    if mode not in ("block_only", "block_token"):
+        raise ValueError(f"mode must be block_only or block_token, got {mode!r}")
+    B, T, H, D = q.shape
+    qh, kh, vh = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
+    scores = torch.matmul(qh, kh.transpose(-2, -1)) / math.sqrt(D)
+    pos = torch.arange(T)
+    valid = (pos[None, :] <= pos[:, None]) if causal else torch.ones(T, T, dtype=torch.bool)
+    valid = valid[None, None].expand(B, H, T, T)
+    fmin = torch.finfo(scores.dtype).min
+    block_ids = pos // block_size
+    nb = int(block_ids.max().item()) + 1
+    bscores = scores.new_full((B, H, T, nb), fmin)
+    for blk in range(nb):
+        tm = block_ids == blk
+        bscores[..., blk] = scores[..., tm].masked_fill(~valid[..., tm], fmin).max(dim=-1).values
+    bvalid = bscores > fmin / 2
+    _, bidx, _ = masked_topk(bscores, bvalid, min(top_blocks, nb))
+    in_sel = (block_ids.view(1, 1, 1, T, 1) == bidx.unsqueeze(-2)).any(dim=-1)
+    cmask = valid & in_sel
+    cscores = scores.masked_fill(~cmask, fmin)
+    if mode == "block_token":
+        ts, ti, tv = masked_topk(cscores, cmask, min(top_k, T))
+        w = F.softmax(ts.float(), dim=-1).to(scores.dtype) * tv.to(scores.dtype)
+        w = w / w.sum(-1, keepdim=True).clamp_min(eps)
+        gk = kh[:, :, None].expand(-1, -1, T, -1, -1).gather(3, ti[..., None].expand(-1, -1, -1, -1, D))
+        gv = vh[:, :, None].expand(-1, -1, T, -1, -1).gather(3, ti[..., None].expand(-1, -1, -1, -1, vh.shape[-1]))
+        k_hat, v_hat = (w[..., None] * gk).sum(3), (w[..., None] * gv).sum(3)
+        diag = retrieval_diagnostics(ts, w, ti, k_hat, kh, tau_c, local_window, sink_size, eps)
+        sel_scores, indices = ts, ti
+    else:
+        w = F.softmax(cscores.float(), dim=-1).to(scores.dtype) * cmask.to(scores.dtype)
+        w = w / w.sum(-1, keepdim=True).clamp_min(eps)
+        k_hat, v_hat = torch.matmul(w, kh), torch.matmul(w, vh)
+        sel_scores, indices = bidx.float(), None
+        diag = retrieval_diagnostics(sel_scores, w, torch.zeros(B, H, T, 1, dtype=torch.long), k_hat, kh, tau_c,
+                                     local_window, sink_size, eps)
+        for name in ("avg_distance", "local_ratio", "sink_ratio", "remote_ratio"):
+            del diag[name]
+    return {
+        "indices": indices,
+        "block_indices": bidx,
+        "block_scores": bscores,
+        "weights": w,
+        "scores": sel_scores,
+        "k_hat": k_hat.transpose(1, 2),
+        "v_hat": v_hat.transpose(1, 2),
+        "diagnostics": diag,
+    }
+
+
 def retrieval_diagnostics(
     scores: Tensor,
     weights: Tensor,

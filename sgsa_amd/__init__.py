@@ -13,7 +13,7 @@ The compiled library (libsgsa_hip.so) is required; there is no fallback path.
 """
 
 from .ops import ChunkSGSAFunction, chunk_sgsa, chunk_sgsa_fwd
-from .retrieval import (SparseRetriever, gather_gate, gather_lists, gather_thresholds, score_dump, score_topk,
+from .retrieval import (SparseRetriever, block_retrieve, gather_gate, gather_lists, gather_thresholds, score_dump, score_topk,
                         score_topk_lists, score_topk_thresholds, sparse_retrieve)
 from .layer import LayerWorkspace, sgsa_layer_forward, sgsa_layer_retrieve
 from .recurrent import fused_recurrent_sgsa
@@ -35,6 +35,7 @@ __all__ = [
     "score_topk_lists",
     "score_topk_thresholds",
     "sparse_retrieve",
+    "block_retrieve",
     "sgsa_layer_forward",
     "sgsa_layer_retrieve",
     "LayerWorkspace",

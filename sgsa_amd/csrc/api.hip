@@ -333,6 +333,107 @@ int sgsa_score_at(int dtype, int B, int Tq, int Tk, int H, int D, int top_k, flo
                     "sgsa_score_at");
 }
 
+// ---- block retrieval -----------------------------------------------------------
+namespace {
+struct BlockWs {
+  size_t bscores, ncand, bmargin, top2, counts, valid, slot_sc, slot_idx, slot_w, maxidx, total;
+};
+
+int block_dims(int B, int T, int H, int top_k, int block_size, int top_blocks, int mode, int& nb, int& eb, int& kk,
+               int& ks) {
+  if (mode != 0 && mode != 1) return fail(SGSA_ERR_INVALID_ARG, "mode must be 0 (block_only) or 1 (block_token)");
+  if (B <= 0 || T <= 0 || H <= 0) return fail(SGSA_ERR_INVALID_ARG, "B=%d T=%d H=%d must be positive", B, T, H);
+  if (block_size <= 0 || top_blocks <= 0)
+    return fail(SGSA_ERR_INVALID_ARG, "block_size=%d and top_blocks=%d must be positive", block_size, top_blocks);
+  if (mode == 1 && top_k <= 0) return fail(SGSA_ERR_INVALID_ARG, "top_k=%d must be positive", top_k);
+  nb = (T - 1) / block_size + 1;
+  eb = top_blocks < nb ? top_blocks : nb;
+  const int bsz = block_size < T ? block_size : T;
+  if ((long)eb * bsz > sgsa::BLK_MAXC)
+    return fail(SGSA_ERR_UNSUPPORTED, "top_blocks * block_size = %ld candidate keys per row exceeds %d",
+                (long)eb * bsz, sgsa::BLK_MAXC);
+  kk = mode == 1 ? (top_k < T ? top_k : T) : 0;
+  ks = eb * bsz;
+  return SGSA_OK;
+}
+
+BlockWs block_ws(int B, int T, int H, int nb, int kk, int ks, int mode, bool own_bscores, bool want_weights) {
+  const size_t rows = (size_t)B * H * T;
+  const size_t w = mode == 1 ? (size_t)kk : (size_t)ks;
+  BlockWs L{};
+  size_t o = 0;
+  auto take = [&](size_t bytes) { size_t at = o; o = align_up(o + bytes); return at; };
+  L.bscores = own_bscores ? take(rows * nb * 4) : 0;
+  L.ncand = take(rows * 4);
+  L.bmargin = take(rows * 4);
+  L.top2 = take(rows * 8);
+  L.counts = take(rows * 4);
+  L.valid = take(rows * kk);
+  L.slot_sc = take(rows * w * 4);
+  L.slot_idx = mode == 0 ? take(rows * w * 4) : 0;
+  L.slot_w = (mode == 0 && want_weights) ? take(rows * w * 4) : 0;
+  L.maxidx = take(256);
+  L.total = o;
+  return L;
+}
+}  // namespace
+
+int sgsa_block_retrieve_workspace_size(int B, int T, int H, int top_k, int block_size, int top_blocks, int mode,
+                                       int own_block_scores, size_t* bytes) {
+  int nb, eb, kk, ks;
+  if (int s = block_dims(B, T, H, top_k, block_size, top_blocks, mode, nb, eb, kk, ks)) return s;
+  REQUIRE(bytes);
+  *bytes = block_ws(B, T, H, nb, kk, ks, mode, own_block_scores != 0, true).total;
+  return SGSA_OK;
+}
+
+int sgsa_block_retrieve(int dtype, int B, int T, int H, int D, int top_k, int block_size, int top_blocks, int mode,
+                        int causal, float tau_c, int local_window, int sink_size, const void* q, const void* k,
+                        const void* v, int32_t* indices, int32_t* block_indices, float* block_scores, float* weights,
+                        void* k_hat, void* v_hat, float* diag, void* workspace, size_t workspace_bytes,
+                        void* stream) {
+  if (int s = check_dtype(dtype)) return s;
+  if (int s = check_dims(B, T, H, D)) return s;
+  int nb, eb, kk, ks;
+  if (int s = block_dims(B, T, H, top_k, block_size, top_blocks, mode, nb, eb, kk, ks)) return s;
+  REQUIRE(q); REQUIRE(k); REQUIRE(v); REQUIRE(block_indices); REQUIRE(k_hat); REQUIRE(v_hat); REQUIRE(workspace);
+  if (mode == 1 && indices == nullptr) return fail(SGSA_ERR_INVALID_ARG, "block_token needs the indices output");
+  if ((long)T * H * D * 4 > 0x7fffffffL) return fail(SGSA_ERR_UNSUPPORTED, "one head's keys exceed 2 GiB of offsets");
+  const BlockWs L = block_ws(B, T, H, nb, kk, ks, mode, block_scores == nullptr, weights != nullptr);
+  if (workspace_bytes < L.total) return fail(SGSA_ERR_WORKSPACE, "workspace %zu < %zu bytes", workspace_bytes, L.total);
+  char* base = static_cast<char*>(workspace);
+  sgsa::BlockArgs a{};
+  a.dtype = dtype; a.B = B; a.T = T; a.H = H; a.D = D;
+  a.bs = block_size; a.nb = nb; a.eb = eb; a.mode = mode; a.kk = kk; a.ks = ks; a.causal = causal ? 1 : 0;
+  a.q = q; a.k = k;
+  a.block_scores = block_scores ? block_scores : reinterpret_cast<float*>(base + L.bscores);
+  a.block_indices = block_indices;
+  a.ncand = reinterpret_cast<int32_t*>(base + L.ncand);
+  a.bmargin = mode == 0 ? reinterpret_cast<float*>(base + L.bmargin) : nullptr;
+  a.slot_idx = mode == 1 ? indices : reinterpret_cast<int32_t*>(base + L.slot_idx);
+  a.slot_sc = reinterpret_cast<float*>(base + L.slot_sc);
+  a.slot_valid = mode == 1 ? reinterpret_cast<uint8_t*>(base + L.valid) : nullptr;
+  a.top2 = reinterpret_cast<float*>(base + L.top2);
+  a.counts = reinterpret_cast<int32_t*>(base + L.counts);
+  hipStream_t st = (hipStream_t)stream;
+  if (int s = hip_status(sgsa::launch_block_select(a, st), "sgsa_block_retrieve (select)")) return s;
+
+  sgsa::GatherArgs g{};
+  g.dtype = dtype; g.B = B; g.Tq = T; g.Tk = T; g.H = H; g.D = D; g.top_k = mode == 1 ? kk : ks; g.q_offset = 0;
+  g.k = k; g.v = v; g.self_key = k; g.indices = a.slot_idx; g.scores = a.slot_sc; g.top2 = a.top2;
+  g.counts = a.counts; g.slot_valid = a.slot_valid; g.use_valid = 1; g.tau_c = tau_c; g.eps = 1e-6f;
+  g.local_window = local_window; g.sink_size = sink_size; g.k_hat = k_hat; g.v_hat = v_hat;
+  g.weights = mode == 1 ? weights : (weights ? reinterpret_cast<float*>(base + L.slot_w) : nullptr);
+  g.diag = diag; g.max_index = reinterpret_cast<int32_t*>(base + L.maxidx);
+  g.margin_in = a.bmargin;
+  g.ent_pad = mode == 0 ? (float)(T - ks) : 0.f;
+  if (int s = hip_status(sgsa::launch_sparse_gather(g, st), "sgsa_block_retrieve (gather)")) return s;
+  if (mode == 0 && weights != nullptr)
+    return hip_status(sgsa::launch_block_dense_weights(B, H, T, ks, a.slot_idx, g.weights, a.counts, weights, st),
+                      "sgsa_block_retrieve (weights)");
+  return SGSA_OK;
+}
+
 int sgsa_sparse_gather_tiled(int B, int T, int H, int D, int top_k, const void* k, const void* v,
                              const int32_t* indices, const float* scores, const float* top2,
                              const int32_t* counts, const int32_t* split, const float* budget, int write_mode,

@@ -194,7 +194,8 @@ __global__ __launch_bounds__(256) void sparse_gather_kernel(GatherArgs a, int lp
   const float eps = a.eps;
 
   float margin = 0.f;
-  if (topk >= 2) margin = s0 - s1;
+  if (a.margin_in) margin = a.margin_in[row];
+  else if (topk >= 2) margin = s0 - s1;
   const float conc = 1.f / (1.f + expf(-(margin / fmaxf(a.tau_c, eps))));
   const float self_norm = fmaxf(sqrtf(kk2), eps);
   const float kh_norm = fmaxf(sqrtf(hh2), eps);
@@ -272,7 +273,7 @@ __global__ __launch_bounds__(256) void sparse_gather_kernel(GatherArgs a, int lp
       imax = max(imax, j);
     }
     if (a.diag != nullptr) {
-      ent = wave_sum(ent);
+      ent = wave_sum(ent) + a.ent_pad * (eps * logf(eps));
       dsum = wave_sum(dsum);
       nloc = wave_sum(nloc);
       nsink = wave_sum(nsink);

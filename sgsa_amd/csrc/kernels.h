@@ -120,9 +120,40 @@ struct GatherArgs {
   float* weights;            // [B,H,Tq,top_k] or nullptr
   float* diag;               // [NDIAG,B,H,Tq] or nullptr
   int32_t* max_index;        // 1 int scratch (diagnostics); required when diag != nullptr
+  const float* margin_in;    // [B,H,Tq] score margin to report instead of top-2 (block_only), or nullptr
+  float ent_pad;             // zero-weight entries of the row beyond the slots (entropy terms of eps)
 };
 
 constexpr int NDIAG = 10;
+
+// Block retrieval (block.hip).
+constexpr int BLK_MAX_D = 128;   // head dim limit
+constexpr int BLK_MAXC = 2048;   // candidate keys per row: top_blocks * block_size
+
+struct BlockArgs {
+  int dtype;
+  int B, T, H, D;
+  int bs, nb, eb;            // block size, blocks, kept blocks min(top_blocks, nb)
+  int mode;                  // 0 block_only, 1 block_token
+  int kk;                    // block_token slots min(top_k, T)
+  int ks;                    // block_only slots eb * bs
+  int causal;
+  const void* q;             // [B,T,H,D]
+  const void* k;             // [B,T,H,D]
+  float* block_scores;       // [B,H,T,nb]
+  int32_t* block_indices;    // [B,H,T,eb]
+  int32_t* ncand;            // [B,H,T] candidate keys of each row
+  float* bmargin;            // [B,H,T] block_only margin, or nullptr
+  int32_t* slot_idx;         // [B,H,T,kk or ks]
+  float* slot_sc;            // [B,H,T,kk or ks]
+  uint8_t* slot_valid;       // [B,H,T,kk] (block_token)
+  float* top2;               // [B,H,T,2]
+  int32_t* counts;           // [B,H,T] slots handed to the gather
+};
+
+hipError_t launch_block_select(const BlockArgs& a, hipStream_t st);
+hipError_t launch_block_dense_weights(int B, int H, int T, int ks, const int32_t* idx, const float* w,
+                                      const int32_t* counts, float* dense, hipStream_t st);
 hipError_t launch_sparse_gather(const GatherArgs& a, hipStream_t st);
 // Scores of given keys (top-k reuse across decode steps): scores[r, i] =
 // (q_r . k[indices[r, i]]) * mscale for i < counts[r].

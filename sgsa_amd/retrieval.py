@@ -255,18 +255,97 @@ def sparse_retrieve(
     return out
 
 
+BLOCK_MODES = {"block_only": 0, "block_token": 1}
+
+
+def block_retrieve(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    top_k: int,
+    block_size: int,
+    top_blocks: int,
+    mode: str = "block_token",
+    causal: bool = True,
+    attention_mask: Optional[Tensor] = None,
+    tau_c: float = 0.1,
+    local_window: int = 64,
+    sink_size: int = 8,
+    return_weights: bool = True,
+    return_diagnostics: bool = True,
+    return_block_scores: bool = False,
+) -> Dict[str, object]:
+    """Block retrieval; the dict of SparseRetriever.forward for ``retrieval_mode``
+    "block_only" / "block_token" on the torch path (modelings/modeling_sgsa.py:444-474).
+
+    q,k,v: [B,T,H,D].  k_hat/v_hat [B,T,H,D]; block_indices [B,H,T,min(top_blocks, nb)];
+    block_token: indices and weights [B,H,T,min(top_k, T)]; block_only: indices None,
+    weights [B,H,T,T], and the diagnostics without the distance statistics (:455-463).
+    """
+    if attention_mask is not None:
+        raise NotImplementedError("block_retrieve: attention_mask is not supported by the HIP retrieval yet")
+    if mode not in BLOCK_MODES:
+        raise ValueError(f"mode must be one of {sorted(BLOCK_MODES)}, got {mode!r}")
+    B, T, H, D = q.shape
+    if k.shape != q.shape or v.shape != k.shape or k.dtype != q.dtype or v.dtype != k.dtype:
+        raise ValueError("q, k and v must share shape and dtype")
+    m = BLOCK_MODES[mode]
+    dev = q.device
+    nb = (T - 1) // block_size + 1 if T > 0 and block_size > 0 else 0
+    eb = min(top_blocks, nb)
+    kk = min(top_k, T)
+    qc, kc, vc = q.contiguous(), k.contiguous(), v.contiguous()
+    lib = _abi.lib()
+    n = ctypes.c_size_t()
+    _abi.check(lib.sgsa_block_retrieve_workspace_size(B, T, H, int(top_k), int(block_size), int(top_blocks), m,
+                                                      int(not return_block_scores), ctypes.byref(n)))
+    ws = torch.empty(max(n.value, 1), device=dev, dtype=torch.uint8)
+    idx = torch.empty(B, H, T, kk, device=dev, dtype=torch.int32) if m == 1 else None
+    bidx = torch.empty(B, H, T, eb, device=dev, dtype=torch.int32)
+    bsc = torch.empty(B, H, T, nb, device=dev, dtype=torch.float32) if return_block_scores else None
+    weights = None
+    if return_weights:
+        weights = torch.empty(B, H, T, kk if m == 1 else T, device=dev, dtype=torch.float32)
+    k_hat = torch.empty(B, T, H, D, device=dev, dtype=q.dtype)
+    v_hat = torch.empty_like(k_hat)
+    diag = torch.empty(_abi.NDIAG, B, H, T, device=dev, dtype=torch.float32) if return_diagnostics else None
+    _abi.check(lib.sgsa_block_retrieve(
+        _abi.dtype_code(q.dtype), B, T, H, D, int(top_k), int(block_size), int(top_blocks), m, int(causal),
+        float(tau_c), int(local_window), int(sink_size), _abi.ptr(qc), _abi.ptr(kc), _abi.ptr(vc), _abi.ptr(idx),
+        _abi.ptr(bidx), _abi.ptr(bsc), _abi.ptr(weights), _abi.ptr(k_hat), _abi.ptr(v_hat), _abi.ptr(diag),
+        _abi.ptr(ws), ws.numel(), _abi.stream_of(qc)))
+    names = _abi.DIAG_NAMES if m == 1 else _abi.DIAG_NAMES[:6]
+    out = {
+        "indices": idx.long() if idx is not None else None,
+        "block_indices": bidx.long(),
+        "weights": weights.to(q.dtype) if weights is not None else None,
+        "k_hat": k_hat,
+        "v_hat": v_hat,
+        "diagnostics": ({name: diag[i] for i, name in enumerate(names)} if diag is not None else {}),
+    }
+    if bsc is not None:
+        out["block_scores"] = bsc
+    return out
+
+
 class SparseRetriever(nn.Module):
-    """SparseRetriever (modelings/modeling_sgsa.py:90-474) for ``retrieval_mode='token_only'``.
+    """SparseRetriever (modelings/modeling_sgsa.py:90-474): ``retrieval_mode`` token_only,
+    block_only or block_token, with the torch retrieval path's semantics (the flash_moba
+    backend of :103-108 is a CUDA library this build does not have).
 
     Takes any config object with ``top_k``, ``tau_c``, ``local_window``,
-    ``sink_size`` and ``retrieval_mode`` attributes (the reference's SGSAConfig).
+    ``sink_size``, ``retrieval_mode`` and, for the block modes, ``block_size`` and
+    ``top_blocks`` attributes (the reference's SGSAConfig).
     """
 
     def __init__(self, config) -> None:
         super().__init__()
         mode = getattr(config, "retrieval_mode", "token_only")
-        if mode != "token_only":
-            raise NotImplementedError(f"retrieval_mode={mode!r}: only token_only is implemented on gfx950")
+        if mode != "token_only" and mode not in BLOCK_MODES:
+            raise ValueError(f"retrieval_mode={mode!r}: expected token_only, block_only or block_token")
+        self.mode = mode
+        self.block_size = getattr(config, "block_size", 32)
+        self.top_blocks = getattr(config, "top_blocks", 2)
         self.top_k = config.top_k
         self.tau_c = getattr(config, "tau_c", 0.1)
         self.local_window = getattr(config, "local_window", 64)
@@ -274,6 +353,11 @@ class SparseRetriever(nn.Module):
 
     def forward(self, q: Tensor, k: Tensor, v: Tensor, causal: bool = True,
                 attention_mask: Optional[Tensor] = None) -> Dict[str, object]:
+        if self.mode != "token_only":
+            r = block_retrieve(q, k, v, self.top_k, self.block_size, self.top_blocks, self.mode, causal=causal,
+                               attention_mask=attention_mask, tau_c=self.tau_c, local_window=self.local_window,
+                               sink_size=self.sink_size)
+            return {key: r[key] for key in ("indices", "block_indices", "weights", "k_hat", "v_hat", "diagnostics")}
         r = sparse_retrieve(q, k, v, self.top_k, causal=causal, attention_mask=attention_mask, tau_c=self.tau_c,
                             local_window=self.local_window, sink_size=self.sink_size)
         return {key: r[key] for key in ("indices", "block_indices", "weights", "k_hat", "v_hat", "diagnostics")}
