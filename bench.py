@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """SGSA layer-forward benchmark on one MI355X.
 
-    python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--no-cpu-baseline] [--workload layer|model]
+    python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--no-cpu-baseline] [--workload layer|model|hybrid|block]
 
 A step is one SGSA layer forward over the batch at the north-star shape
 (B=1, H=16, T=32768, d=128, top-k=2048, chunk 64, bf16 inputs, fp32 state),
@@ -240,6 +240,52 @@ def run_hybrid(args) -> int:
     return 0
 
 
+BLOCK_METRIC = ("SGSA block retrieval tokens/s (bf16, T=32k, H=16, d=128; retrieval_mode block_token with the "
+                "reference config defaults top_k 16, block_size 32, top_blocks 2)")
+
+
+def run_block(args) -> int:
+    """Block retrieval modes of SparseRetriever (sgsa_amd.block_retrieve) at the north-star shape, with the
+    reference config's defaults top_k 16, block_size 32, top_blocks 2 (modelings/modeling_sgsa.py:58-61).
+    Times block_token (the value) and block_only; block_only's dense [B,H,T,T] weights are not requested."""
+    import sgsa_amd
+    B, T, H, D = NORTH_STAR["B"], args.T, NORTH_STAR["H"], NORTH_STAR["D"]
+    top_k, bs, tb = 16, 32, 2
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+    q, k, v = (torch.randn(B, T, H, D, device=dev, generator=g).to(torch.bfloat16) for _ in range(3))
+    cur = torch.cuda.current_stream()
+    out = {}
+    for mode in ("block_token", "block_only"):
+        call = lambda: sgsa_amd.block_retrieve(q, k, v, top_k, bs, tb, mode=mode, return_weights=(mode == "block_token"))
+        for _ in range(args.warmup):
+            r = call()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(cur)
+        for _ in range(args.steps):
+            r = call()
+        e1.record(cur)
+        torch.cuda.synchronize()
+        out[mode] = e0.elapsed_time(e1) / max(args.steps, 1)
+        if not torch.isfinite(r["v_hat"].float()).all():
+            log(f"{mode}: non-finite output")
+            return 1
+        log(f"{mode} ms/call {out[mode]:.3f}")
+    ms = out["block_token"]
+    print(json.dumps({
+        "metric": BLOCK_METRIC, "value": round(B * T / (ms / 1000.0), 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 3), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic normal q/k/v",
+        "block_only_ms": round(out["block_only"], 3),
+        "config": {"workload": "sgsa_block_retrieval", "B": B, "T": T, "H": H, "D": D, "top_k": top_k,
+                   "block_size": bs, "top_blocks": tb, "outputs": "k_hat, v_hat, indices, block_indices, "
+                   "weights (block_token), diagnostics"},
+        "cpu_baseline": None,
+    }), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -257,10 +303,11 @@ def main() -> int:
                     help="timed step: the fused layer path (K1 row thresholds -> K2 recomputing the scores on "
                          "MFMA -> chunk, what sgsa_layer_fwd runs; default), the tile-list form (K1 tile lists -> "
                          "LDS-tiled MFMA K2 -> chunk) or K1 row lists -> per-row 16-byte gathers -> chunk")
-    ap.add_argument("--workload", choices=("layer", "model", "hybrid"), default="layer",
+    ap.add_argument("--workload", choices=("layer", "model", "hybrid", "block"), default="layer",
                     help="layer: the north-star SGSA layer forward (the headline metric, default); model: "
                          "config 2, the 2-layer SGSA causal LM forward at B=16 T=4096; hybrid: config 4, the "
-                         "24-layer SGSA / dense-GQA decoder, prefill of 16384 tokens then 256 decode steps at B=8")
+                         "24-layer SGSA / dense-GQA decoder, prefill of 16384 tokens then 256 decode steps at B=8; "
+                         "block: the retriever's block_token / block_only modes at the north-star shape")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on exactly one GPU (got --gpus {args.gpus}); the SGSA layer shards by head, "
@@ -270,6 +317,8 @@ def main() -> int:
         return run_model(args)
     if args.workload == "hybrid":
         return run_hybrid(args)
+    if args.workload == "block":
+        return run_block(args)
 
     import sgsa_amd
     from sgsa_amd import _abi

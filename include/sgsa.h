@@ -158,18 +158,17 @@ int sgsa_score_at(int dtype, int B, int Tq, int Tk, int H, int D, int top_k, flo
  * keeps eb = min(top_blocks, nb) blocks (nb = ceil(T/block_size)), score
  * desc, ties to the lowest index, padded with 0 (:188-195).  Candidates = the
  * causal keys of the kept blocks; eb * min(block_size, T) <= 2048.
- * Outputs: block_indices [B,H,T,eb]; block_scores [B,H,T,nb] (may be NULL:
- * then held in the workspace); k_hat, v_hat [B,T,H,D]; diag
+ * Outputs: block_indices [B,H,T,eb]; block_scores [B,H,T,nb] (may be NULL;
+ * a copy of the workspace's block-major scores); k_hat, v_hat [B,T,H,D]; diag
  * [SGSA_NDIAG,B,H,T] (may be NULL; block_only leaves planes 6-9 meaningless,
  * as the reference has no token indices there).
  *   mode 1: indices [B,H,T,kk], kk = min(top_k, T): the masked top-k of the
  *     candidates (:322-330), weights [B,H,T,kk] (may be NULL);
  *   mode 0: indices unused (NULL), weights [B,H,T,T] dense (may be NULL),
  *     margin = kept block index 0 - index 1 (:455-463).
- * Workspace: sgsa_block_retrieve_workspace_size() bytes, with own_block_scores
- * = 1 when block_scores is NULL. */
+ * Workspace: sgsa_block_retrieve_workspace_size() bytes. */
 int sgsa_block_retrieve_workspace_size(int B, int T, int H, int top_k, int block_size, int top_blocks, int mode,
-                                       int own_block_scores, size_t* bytes);
+                                       size_t* bytes);
 int sgsa_block_retrieve(int dtype, int B, int T, int H, int D, int top_k, int block_size, int top_blocks,
                         int mode, int causal, float tau_c, int local_window, int sink_size,
                         const void* q, const void* k, const void* v,

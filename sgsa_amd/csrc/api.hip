@@ -357,13 +357,13 @@ int block_dims(int B, int T, int H, int top_k, int block_size, int top_blocks, i
   return SGSA_OK;
 }
 
-BlockWs block_ws(int B, int T, int H, int nb, int kk, int ks, int mode, bool own_bscores, bool want_weights) {
+BlockWs block_ws(int B, int T, int H, int nb, int kk, int ks, int mode, bool want_weights) {
   const size_t rows = (size_t)B * H * T;
   const size_t w = mode == 1 ? (size_t)kk : (size_t)ks;
   BlockWs L{};
   size_t o = 0;
   auto take = [&](size_t bytes) { size_t at = o; o = align_up(o + bytes); return at; };
-  L.bscores = own_bscores ? take(rows * nb * 4) : 0;
+  L.bscores = take(rows * nb * 4);
   L.ncand = take(rows * 4);
   L.bmargin = take(rows * 4);
   L.top2 = take(rows * 8);
@@ -379,11 +379,11 @@ BlockWs block_ws(int B, int T, int H, int nb, int kk, int ks, int mode, bool own
 }  // namespace
 
 int sgsa_block_retrieve_workspace_size(int B, int T, int H, int top_k, int block_size, int top_blocks, int mode,
-                                       int own_block_scores, size_t* bytes) {
+                                       size_t* bytes) {
   int nb, eb, kk, ks;
   if (int s = block_dims(B, T, H, top_k, block_size, top_blocks, mode, nb, eb, kk, ks)) return s;
   REQUIRE(bytes);
-  *bytes = block_ws(B, T, H, nb, kk, ks, mode, own_block_scores != 0, true).total;
+  *bytes = block_ws(B, T, H, nb, kk, ks, mode, true).total;
   return SGSA_OK;
 }
 
@@ -399,14 +399,14 @@ int sgsa_block_retrieve(int dtype, int B, int T, int H, int D, int top_k, int bl
   REQUIRE(q); REQUIRE(k); REQUIRE(v); REQUIRE(block_indices); REQUIRE(k_hat); REQUIRE(v_hat); REQUIRE(workspace);
   if (mode == 1 && indices == nullptr) return fail(SGSA_ERR_INVALID_ARG, "block_token needs the indices output");
   if ((long)T * H * D * 4 > 0x7fffffffL) return fail(SGSA_ERR_UNSUPPORTED, "one head's keys exceed 2 GiB of offsets");
-  const BlockWs L = block_ws(B, T, H, nb, kk, ks, mode, block_scores == nullptr, weights != nullptr);
+  const BlockWs L = block_ws(B, T, H, nb, kk, ks, mode, weights != nullptr);
   if (workspace_bytes < L.total) return fail(SGSA_ERR_WORKSPACE, "workspace %zu < %zu bytes", workspace_bytes, L.total);
   char* base = static_cast<char*>(workspace);
   sgsa::BlockArgs a{};
   a.dtype = dtype; a.B = B; a.T = T; a.H = H; a.D = D;
   a.bs = block_size; a.nb = nb; a.eb = eb; a.mode = mode; a.kk = kk; a.ks = ks; a.causal = causal ? 1 : 0;
-  a.q = q; a.k = k;
-  a.block_scores = block_scores ? block_scores : reinterpret_cast<float*>(base + L.bscores);
+  a.q = q; a.k = k; a.fill_invalid = block_scores != nullptr;
+  a.block_scores = reinterpret_cast<float*>(base + L.bscores);
   a.block_indices = block_indices;
   a.ncand = reinterpret_cast<int32_t*>(base + L.ncand);
   a.bmargin = mode == 0 ? reinterpret_cast<float*>(base + L.bmargin) : nullptr;
@@ -417,6 +417,10 @@ int sgsa_block_retrieve(int dtype, int B, int T, int H, int D, int top_k, int bl
   a.counts = reinterpret_cast<int32_t*>(base + L.counts);
   hipStream_t st = (hipStream_t)stream;
   if (int s = hip_status(sgsa::launch_block_select(a, st), "sgsa_block_retrieve (select)")) return s;
+  if (block_scores != nullptr)
+    if (int s = hip_status(sgsa::launch_block_scores_transpose(a.block_scores, B, H, T, nb, block_scores, st),
+                           "sgsa_block_retrieve (block scores)"))
+      return s;
 
   sgsa::GatherArgs g{};
   g.dtype = dtype; g.B = B; g.Tq = T; g.Tk = T; g.H = H; g.D = D; g.top_k = mode == 1 ? kk : ks; g.q_offset = 0;

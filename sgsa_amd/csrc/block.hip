@@ -3,16 +3,18 @@
 // :444-463 dispatch).  Three kernels, then the row gather of gather.hip:
 //
 //   block_max_kernel     block scores: per query row and key block of
-//                        block_size keys, the max causal score (-FLT_MAX when
-//                        the block has no causal key), [B,H,T,nb] fp32;
+//   (or _mfma_kernel)    block_size keys, the max causal score (-FLT_MAX when
+//                        the block has no causal key), fp32, block-major;
 //   block_select_kernel  per row, the top `top_blocks` blocks (score desc,
 //                        lowest index on ties) and the row's candidate count;
 //   block_cand_kernel    per row, the causal keys of the kept blocks with
 //                        their scores: block_token sorts them in LDS and emits
 //                        the masked top-k slots; block_only emits them all.
 //
-// Scores here are acc * (1/sqrt(D)) with acc an fp32 fma chain over d = 0..D-1
-// in ascending order, in both the block sweep and the candidate scorer, so a
+// Scores here are acc * (1/sqrt(D)).  bf16 inputs with D % 32 == 0: acc from
+// v_mfma_f32_16x16x32_bf16 over d in steps of 32 (the MFMA sweep and scorer);
+// otherwise acc is an fp32 fma chain over d = 0..D-1 in ascending order.  The
+// block sweep and the candidate scorer of one call use the same form, so a
 // candidate's score is bit-identical to the value its block max was taken on.
 #include <float.h>
 
@@ -33,12 +35,17 @@ __device__ __forceinline__ void wave_sync_lds() {
 }
 
 // ---- block maxima ----------------------------------------------------------
-// One workgroup per (64 query rows, b, h).  The q tile stays in LDS as fp32;
-// keys come in tiles of 64 keys x 32 dims.  Thread (ty, tx) owns rows ty+16i
-// and keys tx+16j (i, j < 4).  After a key tile, its 64x64 scores go to LDS and
-// each (row, block) pair the tile touches is folded into the block score with
-// a max.  The workgroup owns its rows, and the barrier between key tiles
-// orders the read-modify-writes of a block that spans two tiles.
+// Block scores are held block-major, [B,H,nb,T] (entry (b,h,j,t) at
+// ((b*H+h)*nb + j)*T + t), so the 16 or 64 query rows of a store are
+// consecutive; the caller's [B,H,T,nb] copy is a transpose, made only on request.
+//
+// fp32 / generic sweep: one workgroup per (64 query rows, b, h).  The q tile
+// stays in LDS as fp32; keys come in tiles of 64 keys x 32 dims.  Thread
+// (ty, tx) owns rows ty+16i and keys tx+16j (i, j < 4).  After a key tile, its
+// 64x64 scores go to LDS and each (row, block) pair the tile touches is folded
+// into the block score with a max.  The workgroup owns its rows, and the
+// barrier between key tiles orders the read-modify-writes of a block that
+// spans two tiles.
 constexpr int BM_DC = 32;   // dims per key chunk
 
 template <typename X>
@@ -57,10 +64,10 @@ __global__ __launch_bounds__(256) void block_max_kernel(BlockArgs a, float mscal
     const int r = e / D, d = e % D, t = r0 + r;
     qs[r * DP + d] = t < T ? ld(Q, ((long)(b * T + t) * H + h) * D + d) : 0.f;
   }
-  float* bsc = a.block_scores + (long)bh * T * nb;
+  float* bsc = a.block_scores + (long)bh * nb * T;
   for (long e = tid; e < 64L * nb; e += 256) {
-    const int t = r0 + (int)(e / nb);
-    if (t < T) bsc[(long)t * nb + e % nb] = -FLT_MAX;
+    const int t = r0 + (int)(e % 64);
+    if (t < T) bsc[(e / 64) * T + t] = -FLT_MAX;
   }
 
   const int kend = a.causal ? min(T, r0 + 64) : T;
@@ -102,63 +109,239 @@ __global__ __launch_bounds__(256) void block_max_kernel(BlockArgs a, float mscal
     const int kt_end = min(k0 + 64, T);
     const int bA = k0 / bs, nbt = (kt_end - 1) / bs - bA + 1;
     for (int it = tid; it < 64 * nbt; it += 256) {
-      const int r = it / nbt, bb = bA + it % nbt, t = r0 + r;
+      const int r = it % 64, bb = bA + it / 64, t = r0 + r;
       if (t >= T) continue;
       const int lo = max(bb * bs, k0), hi = min(bb * bs + bs, kt_end);
       float m = -FLT_MAX;
       for (int key = lo; key < hi; ++key) m = fmaxf(m, ss[r * 65 + key - k0]);
-      float* p = bsc + (long)t * nb + bb;
+      float* p = bsc + (long)bb * T + t;
       *p = fmaxf(*p, m);
     }
   }
 }
 
+// bf16 form of the sweep on MFMA (v_mfma_f32_16x16x32_bf16), for D % 32 == 0.
+// A workgroup takes 128 query rows (wave w owns rows r0+32w..+31 as two
+// 16-row B operands, fragments in registers) and sweeps 64-key tiles; the
+// longest causal sweeps are issued first.  A key tile sits in LDS (row pitch
+// D+8 bf16, so the 16 keys of a fragment read fall in distinct banks) as four
+// 16-key A operands, and the next tile is loaded into registers while the
+// current one is multiplied.  Lane (lg, lc) ends with the scores of keys 4lg+i
+// of each 16-key column block for query lc of each row set.
+// REG (block_size % 16 == 0): every column block lies in one key block, so a
+// block's max for a query is an in-lane max over i and the column blocks, then
+// two swaps over lg; lanes lg == 0 store the queries' values (a plain store
+// when the block starts in this tile, else a max with what the same lane
+// stored for the previous tile).  Otherwise the scores go through LDS and each
+// (row, block) pair the tile touches is reduced key by key.  Blocks with no key
+// below the tile's causal end are only written when fill_invalid is set: the
+// select kernel never reads them.
+constexpr int BMM_KP = BLK_MAX_D + 8;
+constexpr int BMM_ROWS = 128;
+
+template <bool REG>
+__global__ __launch_bounds__(256) void block_max_mfma_kernel(BlockArgs a, float mscale) {
+  __shared__ __attribute__((aligned(16))) uint16_t kt[64 * BMM_KP];
+  __shared__ float ss[REG ? 1 : BMM_ROWS * 65];
+  const int D = a.D, T = a.T, H = a.H, bs = a.bs, nb = a.nb, nks = D / 32;
+  const int nrb = (T + BMM_ROWS - 1) / BMM_ROWS;
+  const int bh = blockIdx.y, b = bh / H, h = bh % H;
+  const int r0 = (nrb - 1 - (int)blockIdx.x) * BMM_ROWS;
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, lg = l >> 4, lc = l & 15;
+  const uint16_t* Q = reinterpret_cast<const uint16_t*>(a.q);
+  const uint16_t* K = reinterpret_cast<const uint16_t*>(a.k) + ((long)b * T * H + h) * D;
+  const long kstride = (long)H * D;
+
+  bf16x8 qf[2][BLK_MAX_D / 32];
+  int qrow[2];
+#pragma unroll
+  for (int rs = 0; rs < 2; ++rs) {
+    qrow[rs] = r0 + 32 * w + 16 * rs + lc;
+#pragma unroll
+    for (int s = 0; s < BLK_MAX_D / 32; ++s) {
+      u16x8 raw = {0, 0, 0, 0, 0, 0, 0, 0};
+      if (s < nks && qrow[rs] < T)
+        raw = *reinterpret_cast<const u16x8*>(Q + ((long)(b * T + qrow[rs]) * H + h) * D + 32 * s + 8 * lg);
+      qf[rs][s] = __builtin_bit_cast(bf16x8, raw);
+    }
+  }
+  float* bsc = a.block_scores + (long)bh * nb * T;
+  const int kend = a.causal ? min(T, r0 + BMM_ROWS) : T;
+  if (a.fill_invalid) {
+    const int fb = (kend + bs - 1) / bs, nfill = nb - fb;
+    for (long e = tid; e < (long)BMM_ROWS * nfill; e += 256) {
+      const int t = r0 + (int)(e % BMM_ROWS);
+      if (t < T) bsc[(fb + e / BMM_ROWS) * T + t] = -FLT_MAX;
+    }
+  }
+
+  const int cpr = D / 8;       // 16-byte chunks per key row
+  const int nch = 64 * cpr;    // chunks per tile, <= 1024
+  u16x8 pf[4];
+  auto fetch = [&](int k0) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int e = tid + 256 * u, r = e / cpr, c = e % cpr, key = k0 + r;
+      u16x8 v = {0, 0, 0, 0, 0, 0, 0, 0};
+      if (e < nch && key < T) v = *reinterpret_cast<const u16x8*>(K + key * kstride + 8 * c);
+      pf[u] = v;
+    }
+  };
+  fetch(0);
+  for (int k0 = 0; k0 < kend; k0 += 64) {
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int e = tid + 256 * u;
+      if (e < nch) *reinterpret_cast<u16x8*>(kt + (e / cpr) * BMM_KP + 8 * (e % cpr)) = pf[u];
+    }
+    __syncthreads();
+    if (k0 + 64 < kend) fetch(k0 + 64);
+    const int kt_end = min(k0 + 64, T);
+    float sc[2][4][4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      f4 acc[2] = {f4_zero(), f4_zero()};
+#pragma unroll
+      for (int s = 0; s < BLK_MAX_D / 32; ++s) {
+        if (s < nks) {
+          const bf16x8 kf = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8*>(kt + (16 * kb + lc) * BMM_KP + 32 * s + 8 * lg));
+          acc[0] = mma_bf16(kf, qf[0][s], acc[0]);
+          acc[1] = mma_bf16(kf, qf[1][s], acc[1]);
+        }
+      }
+#pragma unroll
+      for (int rs = 0; rs < 2; ++rs) {
+        const f4 v = score_of(acc[rs], mscale);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int key = k0 + 16 * kb + 4 * lg + i;
+          const bool ok = qrow[rs] < T && key < T && (!a.causal || key <= qrow[rs]);
+          sc[rs][kb][i] = ok ? v[i] : -FLT_MAX;
+        }
+      }
+    }
+    if (REG) {
+#pragma unroll
+      for (int rs = 0; rs < 2; ++rs) {
+        float run = -FLT_MAX;
+        int cur = k0 / bs;
+        auto flush = [&](int bb) {
+          float m = fmaxf(run, __shfl_xor(run, 16, 64));
+          m = fmaxf(m, __shfl_xor(m, 32, 64));
+          if (lg == 0 && qrow[rs] < T) {
+            float* p = bsc + (long)bb * T + qrow[rs];
+            *p = bb * bs >= k0 ? m : fmaxf(*p, m);
+          }
+        };
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+          const int c0 = k0 + 16 * kb;
+          if (c0 >= kt_end) break;
+          const int bb = c0 / bs;
+          if (bb != cur) {
+            flush(cur);
+            run = -FLT_MAX;
+            cur = bb;
+          }
+          run = fmaxf(run, fmaxf(fmaxf(sc[rs][kb][0], sc[rs][kb][1]), fmaxf(sc[rs][kb][2], sc[rs][kb][3])));
+        }
+        flush(cur);
+      }
+    } else {
+#pragma unroll
+      for (int rs = 0; rs < 2; ++rs)
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) ss[(32 * w + 16 * rs + lc) * 65 + 16 * kb + 4 * lg + i] = sc[rs][kb][i];
+      __syncthreads();
+      const int bA = k0 / bs, nbt = (kt_end - 1) / bs - bA + 1;
+      for (int it = tid; it < BMM_ROWS * nbt; it += 256) {
+        const int r = it % BMM_ROWS, bb = bA + it / BMM_ROWS, t = r0 + r;
+        if (t >= T) continue;
+        const int lo = max(bb * bs, k0), hi = min(bb * bs + bs, kt_end);
+        float m = -FLT_MAX;
+        for (int key = lo; key < hi; ++key) m = fmaxf(m, ss[r * 65 + key - k0]);
+        float* p = bsc + (long)bb * T + t;
+        *p = bb * bs >= k0 ? m : fmaxf(*p, m);
+      }
+    }
+  }
+}
+
+// [B,H,nb,T] -> [B,H,T,nb], for callers that ask for the block scores.
+__global__ __launch_bounds__(256) void block_scores_transpose_kernel(const float* __restrict__ src, long bhn, int T,
+                                                                     int nb, float* __restrict__ dst) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;   // over dst
+  if (i >= bhn) return;
+  const int j = (int)(i % nb);
+  const long rt = i / nb;            // bh * T + t
+  const long bh = rt / T;
+  const int t = (int)(rt % T);
+  dst[i] = src[(bh * nb + j) * T + t];
+}
+
 // ---- top blocks per row ----------------------------------------------------
-// One wave per row.  Blocks 0..lim/bs hold a key <= lim (lim = t causal, else
-// T-1); they are the valid blocks of :188-189, the same count for every (b, h)
-// of a row, so the masked top-k keeps kqb = min(eb, that count) of them
-// (:159-160) and pads the rest with index 0 (:151-152).  Each round takes the
-// best block after the previous one in (score desc, index asc) order.
+// One lane per row; the lanes of a wave take consecutive query positions, so
+// each block-score read is coalesced.  Blocks 0..lim/bs hold a key <= lim
+// (lim = t causal, else T-1); they are the valid blocks of :188-189, the same
+// count for every (b, h) of a row, so the masked top-k keeps kqb = min(eb,
+// that count) of them (:159-160) and pads the rest with index 0 (:151-152).
+// A pass keeps, in registers, the best BS_R blocks after the last one taken,
+// in (score desc, index asc) order; passes repeat until kqb are taken.
+constexpr int BS_R = 4;
+
 __global__ __launch_bounds__(256) void block_select_kernel(BlockArgs a) {
-  const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const long row = (long)blockIdx.x * 256 + threadIdx.x;
   const long nrows = (long)a.B * a.H * a.T;
   if (row >= nrows) return;
-  const int lane = threadIdx.x & 63;
-  const int t = (int)(row % a.T), bs = a.bs, eb = a.eb;
-  const int lim = a.causal ? t : a.T - 1;
+  const int T = a.T, t = (int)(row % T), bs = a.bs, eb = a.eb;
+  const long bh = row / T;
+  const int lim = a.causal ? t : T - 1;
   const int nvb = lim / bs + 1;
   const int kqb = min(eb, nvb);
-  const float* bsc = a.block_scores + row * a.nb;
+  const float* col = a.block_scores + bh * a.nb * T + t;
   int32_t* bi = a.block_indices + row * eb;
   float ls = INFINITY;
   int lj = -1, ncand = 0, first = 0, second = 0;
-  for (int s = 0; s < kqb; ++s) {
-    float bv = -INFINITY;
-    int bj = 0x7fffffff;
-    for (int j = lane; j < nvb; j += 64) {
-      const float v = bsc[j];
-      const bool after = v < ls || (v == ls && j > lj);
-      if (after && v > bv) { bv = v; bj = j; }   // j ascends per lane: ties keep the lower index
-    }
+  for (int got = 0; got < kqb;) {
+    float bv[BS_R];
+    int bj[BS_R];
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ov = __shfl_xor(bv, o, 64);
-      const int oj = __shfl_xor(bj, o, 64);
-      if (ov > bv || (ov == bv && oj < bj)) { bv = ov; bj = oj; }
+    for (int r = 0; r < BS_R; ++r) { bv[r] = -INFINITY; bj[r] = 0x7fffffff; }
+    for (int j = 0; j < nvb; ++j) {
+      float cv = col[(long)j * T];
+      if (!(cv < ls || (cv == ls && j > lj))) continue;
+      int cj = j;
+#pragma unroll
+      for (int r = 0; r < BS_R; ++r) {
+        if (cv > bv[r] || (cv == bv[r] && cj < bj[r])) {
+          const float tv = bv[r];
+          const int tj = bj[r];
+          bv[r] = cv; bj[r] = cj; cv = tv; cj = tj;
+        }
+      }
     }
-    if (bj == 0x7fffffff) bj = 0;   // only NaN scores left: keep block 0 so every key stays in range
-    ls = bv;
-    lj = bj;
-    if (lane == 0) bi[s] = bj;
-    ncand += min(bj * bs + bs, lim + 1) - bj * bs;
-    if (s == 0) first = bj;
-    if (s == 1) second = bj;
+    const int take = min(BS_R, kqb - got);
+#pragma unroll
+    for (int r = 0; r < BS_R; ++r) {
+      if (r < take) {
+        int j = bj[r];
+        if (j == 0x7fffffff) j = 0;   // only NaN scores left: keep block 0 so every key stays in range
+        bi[got + r] = j;
+        ncand += min(j * bs + bs, lim + 1) - j * bs;
+        if (got + r == 0) first = j;
+        if (got + r == 1) second = j;
+        ls = bv[r];
+        lj = j;
+      }
+    }
+    got += take;
   }
-  for (int s = kqb + lane; s < eb; s += 64) bi[s] = 0;
-  if (lane == 0) {
-    a.ncand[row] = ncand;
-    if (a.bmargin) a.bmargin[row] = eb >= 2 ? (float)first - (float)second : 0.f;
-  }
+  for (int s = kqb; s < eb; ++s) bi[s] = 0;
+  a.ncand[row] = ncand;
+  if (a.bmargin) a.bmargin[row] = eb >= 2 ? (float)first - (float)second : 0.f;
 }
 
 // q . k over d = 0..D-1 as one fp32 fma chain (16-byte loads when VEC).
@@ -210,7 +393,7 @@ template <bool VEC> struct KeyDot<bf16_t, VEC> {
 // candidate set with score -FLT_MAX and are invalid (what the masked top-k over
 // -FLT_MAX ties returns under the lowest-index rule); slots >= kq hold index 0.
 // block_only (:346-359): every candidate becomes a slot, in generation order.
-template <typename X, bool VEC, bool TOKEN>
+template <typename X, bool VEC, bool TOKEN, bool MF>
 __global__ __launch_bounds__(64) void block_cand_kernel(BlockArgs a, float mscale) {
   __shared__ float qrow[BLK_MAX_D];
   __shared__ int pre[BLK_MAXC + 1];
@@ -244,15 +427,56 @@ __global__ __launch_bounds__(64) void block_cand_kernel(BlockArgs a, float mscal
   const int ncand = run;
   wave_sync_lds();
 
-  float m1 = -FLT_MAX;
-  for (int c = lane; c < ncand; c += 64) {
+  auto key_of = [&](int c) {
     int lo = 0, hi = kqb - 1;
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
       if (pre[mid] <= c) lo = mid;
       else hi = mid - 1;
     }
-    const int key = bi[lo] * bs + (c - pre[lo]);
+    return bi[lo] * bs + (c - pre[lo]);
+  };
+  float m1 = -FLT_MAX;
+  if (MF) {
+    // 16 candidates per MFMA group as the A operand (row lc = candidate c0+lc),
+    // every B column the query: the same operand roles and instruction
+    // sequence as block_max_mfma_kernel, so the scores agree bit for bit.
+    const int nks = D / 32, lg = lane >> 4, lc = lane & 15;
+    const uint16_t* Qb = reinterpret_cast<const uint16_t*>(a.q) + ((long)(b * T + t) * H + h) * D;
+    const uint16_t* Kb = reinterpret_cast<const uint16_t*>(a.k);
+    bf16x8 qa[BLK_MAX_D / 32];
+#pragma unroll
+    for (int s = 0; s < BLK_MAX_D / 32; ++s) {
+      u16x8 raw = {0, 0, 0, 0, 0, 0, 0, 0};
+      if (s < nks) raw = *reinterpret_cast<const u16x8*>(Qb + 32 * s + 8 * lg);
+      qa[s] = __builtin_bit_cast(bf16x8, raw);
+    }
+    for (int c0 = 0; c0 < ncand; c0 += 16) {
+      const int ca = c0 + lc;   // the candidate this lane loads as A row lc
+      const int key = ca < ncand ? key_of(ca) : 0;
+      const uint16_t* kp = Kb + ((long)(b * T + key) * H + h) * D;
+      f4 acc = f4_zero();
+#pragma unroll
+      for (int s = 0; s < BLK_MAX_D / 32; ++s)
+        if (s < nks) acc = mma_bf16(__builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8*>(kp + 32 * s + 8 * lg)), qa[s], acc);
+      // accumulator element i holds A row 4lg+i, i.e. candidate c0+4lg+i; lane lc == i reports it
+      const f4 sv4 = score_of(acc, mscale);
+      const float sv = lc == 0 ? sv4[0] : lc == 1 ? sv4[1] : lc == 2 ? sv4[2] : sv4[3];
+      const int c = c0 + 4 * lg + lc;
+      const int ckey = __shfl(key, 4 * lg + lc, 64);   // key of candidate c (lane 4lg+lc loaded it)
+      if (lc < 4 && c < ncand) {
+        if (TOKEN) {
+          keys[c] = ((uint64_t)(~f32_order_key(sv)) << 32) | (uint32_t)ckey;
+        } else {
+          a.slot_idx[row * a.ks + c] = ckey;
+          a.slot_sc[row * a.ks + c] = sv;
+          m1 = fmaxf(m1, sv);
+        }
+      }
+    }
+  }
+  for (int c = MF ? ncand : lane; c < ncand; c += 64) {
+    const int key = key_of(c);
     const float s = block_score(KeyDot<X, VEC>::run(qrow, K + ((long)(b * T + key) * H + h) * D, D), mscale);
     if (TOKEN) {
       keys[c] = ((uint64_t)(~f32_order_key(s)) << 32) | (uint32_t)key;
@@ -360,29 +584,45 @@ __global__ __launch_bounds__(256) void block_dense_weights_kernel(int T, int ks,
   for (int s = threadIdx.x; s < n; s += 256) out[idx[row * ks + s]] = w[row * ks + s];
 }
 
-template <typename X>
+template <typename X, bool MF>
 static void launch_cand(const BlockArgs& a, float ms, bool vec, hipStream_t st) {
   const dim3 grid((unsigned)((long)a.B * a.H * a.T));
   if (a.mode == 1) {
-    if (vec) block_cand_kernel<X, true, true><<<grid, 64, 0, st>>>(a, ms);
-    else block_cand_kernel<X, false, true><<<grid, 64, 0, st>>>(a, ms);
+    if (vec) block_cand_kernel<X, true, true, MF><<<grid, 64, 0, st>>>(a, ms);
+    else block_cand_kernel<X, false, true, MF><<<grid, 64, 0, st>>>(a, ms);
   } else {
-    if (vec) block_cand_kernel<X, true, false><<<grid, 64, 0, st>>>(a, ms);
-    else block_cand_kernel<X, false, false><<<grid, 64, 0, st>>>(a, ms);
+    if (vec) block_cand_kernel<X, true, false, MF><<<grid, 64, 0, st>>>(a, ms);
+    else block_cand_kernel<X, false, false, MF><<<grid, 64, 0, st>>>(a, ms);
   }
+}
+
+bool block_uses_mfma(const BlockArgs& a) {
+  auto aligned = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
+  return a.dtype == DT_BF16 && a.D % 32 == 0 && aligned(a.q) && aligned(a.k);
 }
 
 hipError_t launch_block_select(const BlockArgs& a, hipStream_t st) {
   const float ms = score_multiplier((float)sqrt((double)a.D), 0);
   const dim3 g1((unsigned)((a.T + 63) / 64), (unsigned)(a.B * a.H));
-  if (a.dtype == DT_F32) block_max_kernel<float><<<g1, 256, 0, st>>>(a, ms);
+  const dim3 g2((unsigned)((a.T + BMM_ROWS - 1) / BMM_ROWS), (unsigned)(a.B * a.H));
+  const bool mf = block_uses_mfma(a);
+  if (mf && a.bs % 16 == 0) block_max_mfma_kernel<true><<<g2, 256, 0, st>>>(a, ms);
+  else if (mf) block_max_mfma_kernel<false><<<g2, 256, 0, st>>>(a, ms);
+  else if (a.dtype == DT_F32) block_max_kernel<float><<<g1, 256, 0, st>>>(a, ms);
   else block_max_kernel<bf16_t><<<g1, 256, 0, st>>>(a, ms);
   const long rows = (long)a.B * a.H * a.T;
-  block_select_kernel<<<dim3((unsigned)((rows + 3) / 4)), 256, 0, st>>>(a);
+  block_select_kernel<<<dim3((unsigned)((rows + 255) / 256)), 256, 0, st>>>(a);
   const int epv = a.dtype == DT_F32 ? 4 : 8;
   const bool vec = a.D % epv == 0 && ((uintptr_t)a.k & 15u) == 0;
-  if (a.dtype == DT_F32) launch_cand<float>(a, ms, vec, st);
-  else launch_cand<bf16_t>(a, ms, vec, st);
+  if (mf) launch_cand<bf16_t, true>(a, ms, vec, st);
+  else if (a.dtype == DT_F32) launch_cand<float, false>(a, ms, vec, st);
+  else launch_cand<bf16_t, false>(a, ms, vec, st);
+  return hipGetLastError();
+}
+
+hipError_t launch_block_scores_transpose(const float* src, int B, int H, int T, int nb, float* dst, hipStream_t st) {
+  const long n = (long)B * H * T * nb;
+  block_scores_transpose_kernel<<<dim3((unsigned)((n + 255) / 256)), 256, 0, st>>>(src, n, T, nb, dst);
   return hipGetLastError();
 }
 

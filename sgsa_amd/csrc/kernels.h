@@ -138,9 +138,10 @@ struct BlockArgs {
   int kk;                    // block_token slots min(top_k, T)
   int ks;                    // block_only slots eb * bs
   int causal;
+  int fill_invalid;          // write -FLT_MAX to blocks with no causal key (block scores are an output)
   const void* q;             // [B,T,H,D]
   const void* k;             // [B,T,H,D]
-  float* block_scores;       // [B,H,T,nb]
+  float* block_scores;       // [B,H,nb,T] (block-major)
   int32_t* block_indices;    // [B,H,T,eb]
   int32_t* ncand;            // [B,H,T] candidate keys of each row
   float* bmargin;            // [B,H,T] block_only margin, or nullptr
@@ -152,6 +153,7 @@ struct BlockArgs {
 };
 
 hipError_t launch_block_select(const BlockArgs& a, hipStream_t st);
+hipError_t launch_block_scores_transpose(const float* src, int B, int H, int T, int nb, float* dst, hipStream_t st);
 hipError_t launch_block_dense_weights(int B, int H, int T, int ks, const int32_t* idx, const float* w,
                                       const int32_t* counts, float* dense, hipStream_t st);
 hipError_t launch_sparse_gather(const GatherArgs& a, hipStream_t st);

@@ -298,7 +298,7 @@ def block_retrieve(
     lib = _abi.lib()
     n = ctypes.c_size_t()
     _abi.check(lib.sgsa_block_retrieve_workspace_size(B, T, H, int(top_k), int(block_size), int(top_blocks), m,
-                                                      int(not return_block_scores), ctypes.byref(n)))
+                                                      ctypes.byref(n)))
     ws = torch.empty(max(n.value, 1), device=dev, dtype=torch.uint8)
     idx = torch.empty(B, H, T, kk, device=dev, dtype=torch.int32) if m == 1 else None
     bidx = torch.empty(B, H, T, eb, device=dev, dtype=torch.int32)
