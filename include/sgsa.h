@@ -120,7 +120,11 @@ int sgsa_score_dump(int dtype, int B, int Tq, int Tk, int H, int D,
  * gate (write_key/alpha untouched); else alpha = alpha_max * concentration *
  * novelty * sigmoid(budget), clipped (:497-504), write_mode 0 direct / 1
  * residual.  weights, diag, k_hat, write_key, alpha may be NULL.  workspace:
- * >= 256 bytes when diag is requested, else may be NULL. */
+ * >= 256 bytes when diag is requested, else may be NULL.  Given
+ * sgsa_sparse_gather_workspace_size() bytes, calls with few rows and many
+ * slots (decode: at most 2048 rows, more than 128 slots) split each row's
+ * slots over several waves and merge the partial sums in a fixed order. */
+int sgsa_sparse_gather_workspace_size(int B, int Tq, int H, int D, int top_k, size_t* bytes);
 int sgsa_sparse_gather(int dtype, int B, int Tq, int Tk, int H, int D, int top_k, int q_offset,
                        const void* k, const void* v, const void* self_key,
                        const int32_t* indices, const float* scores, const float* top2,

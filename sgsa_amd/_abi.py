@@ -50,6 +50,7 @@ SIGNATURES = {
     "sgsa_score_dump": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _F, _I, _P, _P, _I, _I, _P, _P]),
     "sgsa_sparse_gather": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _I, _F, _F,
                                 _I, _I, _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),
+    "sgsa_sparse_gather_workspace_size": (_I, [_I, _I, _I, _I, _I, ctypes.POINTER(_SZ)]),
     "sgsa_score_at": (_I, [_I, _I, _I, _I, _I, _I, _I, _F, _I, _P, _P, _P, _P, _P, _P]),
     "sgsa_block_retrieve_workspace_size": (_I, [_I, _I, _I, _I, _I, _I, _I, ctypes.POINTER(_SZ)]),
     "sgsa_block_retrieve": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _F, _I, _I, _P, _P, _P, _P, _P, _P, _P,

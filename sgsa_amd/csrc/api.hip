@@ -316,7 +316,22 @@ int sgsa_sparse_gather(int dtype, int B, int Tq, int Tk, int H, int D, int top_k
   a.budget = budget; a.write_mode = write_mode; a.alpha_max = alpha_max;
   a.k_hat = k_hat; a.v_hat = v_hat; a.write_key = write_key; a.alpha = alpha; a.weights = weights; a.diag = diag;
   a.max_index = diag ? (int32_t*)workspace : nullptr;
+  const long rows = (long)B * H * Tq;
+  const size_t pb = sgsa::gather_part_bytes(rows, top_k, D);
+  if (pb > 0 && workspace != nullptr && workspace_bytes >= 256 + pb) {
+    a.nsplit = sgsa::gather_nsplit(rows, top_k);
+    a.split_len = sgsa::GATHER_SPLIT_LEN;
+    a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + 256);
+  }
   return hip_status(sgsa::launch_sparse_gather(a, (hipStream_t)stream), "sgsa_sparse_gather");
+}
+
+int sgsa_sparse_gather_workspace_size(int B, int Tq, int H, int D, int top_k, size_t* bytes) {
+  if (int s = check_dims(B, Tq, H, D)) return s;
+  if (top_k <= 0) return fail(SGSA_ERR_INVALID_ARG, "top_k=%d must be positive", top_k);
+  REQUIRE(bytes);
+  *bytes = 256 + sgsa::gather_part_bytes((long)B * H * Tq, top_k, D);
+  return SGSA_OK;
 }
 
 int sgsa_score_at(int dtype, int B, int Tq, int Tk, int H, int D, int top_k, float scale, int scale_mode,

@@ -70,6 +70,68 @@ __device__ __forceinline__ int elem_d(int sub, int m, int lpr) {
 
 }  // namespace
 
+// Accumulates slots [s0, s1) of one row into (ak, av, esum) with weights
+// exp(score - mrun).  Online mode (no top2) raises mrun as larger scores
+// arrive, rescaling what was accumulated, and keeps the running top-2.
+template <typename X, bool VEC>
+__device__ __forceinline__ void gather_slots(const GatherArgs& a, int s0, int s1, const int32_t* idxp,
+                                             const float* scp, const uint8_t* vp, const X* K, const X* V, int b,
+                                             int h, int grp, int sub, int lpr, bool fixed_max, float& mrun,
+                                             float& t1, float& t2, float& esum,
+                                             float (&ak)[GatherShape<X, VEC>::NE],
+                                             float (&av)[GatherShape<X, VEC>::NE]) {
+  constexpr int NE = GatherShape<X, VEC>::NE;
+  const int lane = threadIdx.x & 63;
+  const int Tk = a.Tk, H = a.H, D = a.D;
+  const int rpi = 64 / lpr;
+  for (int base = s0; base < s1; base += 64) {
+    const int slot = base + lane;
+    int j = 0;
+    float sc = -INFINITY;
+    if (slot < s1) {
+      j = idxp[slot];
+      const bool ok = vp ? (vp[slot] != 0) : true;
+      if (ok) sc = scp[slot];
+    }
+    if (!fixed_max) {
+      // online-softmax merge: rescale what was accumulated under the old max
+      const float bm = wave_max(sc);
+      if (bm > mrun) {
+        const float f = (mrun == -INFINITY) ? 0.f : __expf(mrun - bm);
+        esum *= f;
+#pragma unroll
+        for (int i = 0; i < NE; ++i) { ak[i] *= f; av[i] *= f; }
+        mrun = bm;
+      }
+      const float so = sc == -INFINITY ? -FLT_MAX : sc;
+      t2 = fmaxf(t2, fminf(t1, so));
+      t1 = fmaxf(t1, so);
+    }
+    const float wgt = sc == -INFINITY ? 0.f : __expf(sc - mrun);
+    esum += wgt;
+    const int nstep = min(64, s1 - base);
+#pragma unroll 4
+    for (int it = 0; it * rpi < nstep; ++it) {
+      const int src = it * rpi + grp;
+      const int jj = __shfl(j, src, 64);
+      const float ww = __shfl(wgt, src, 64);
+      if (src < nstep && ww != 0.f) {
+        const long off = ((long)(b * Tk + jj) * H + h) * D;
+        float xv[NE];
+        load_row<X, VEC>(V, off, sub, D, lpr, xv);
+        if (K) {
+          float xk[NE];
+          load_row<X, VEC>(K, off, sub, D, lpr, xk);
+#pragma unroll
+          for (int i = 0; i < NE; ++i) ak[i] += ww * xk[i];
+        }
+#pragma unroll
+        for (int i = 0; i < NE; ++i) av[i] += ww * xv[i];
+      }
+    }
+  }
+}
+
 template <typename X, bool VEC>
 __global__ __launch_bounds__(256) void sparse_gather_kernel(GatherArgs a, int lpr) {
   constexpr int NE = GatherShape<X, VEC>::NE;
@@ -99,49 +161,35 @@ __global__ __launch_bounds__(256) void sparse_gather_kernel(GatherArgs a, int lp
   for (int i = 0; i < NE; ++i) { ak[i] = 0.f; av[i] = 0.f; }
   float esum = 0.f;
 
-  for (int base = 0; base < kq; base += 64) {
-    const int slot = base + lane;
-    int j = 0;
-    float sc = -INFINITY;
-    if (slot < kq) {
-      j = idxp[slot];
-      const bool ok = vp ? (vp[slot] != 0) : true;
-      if (ok) sc = scp[slot];
-    }
+  if (a.nsplit == 0) {
+    gather_slots<X, VEC>(a, 0, kq, idxp, scp, vp, K, V, b, h, grp, sub, lpr, fixed_max, mrun, t1, t2, esum, ak, av);
+  } else {
+    // merge the row's partials (gather_part_kernel) in split order
+    const float* P = a.part + row * (long)a.nsplit * (4 + 2 * D);
     if (!fixed_max) {
-      // online-softmax merge: rescale what was accumulated under the old max
-      const float bm = wave_max(sc);
-      if (bm > mrun) {
-        const float f = (mrun == -INFINITY) ? 0.f : __expf(mrun - bm);
-        esum *= f;
-#pragma unroll
-        for (int i = 0; i < NE; ++i) { ak[i] *= f; av[i] *= f; }
-        mrun = bm;
-      }
-      const float so = sc == -INFINITY ? -FLT_MAX : sc;
-      t2 = fmaxf(t2, fminf(t1, so));
-      t1 = fmaxf(t1, so);
+      float mc = -INFINITY;
+      for (int c = lane; c < a.nsplit; c += 64) mc = fmaxf(mc, P[(long)c * (4 + 2 * D)]);
+      mrun = wave_max(mc);
     }
-    const float wgt = sc == -INFINITY ? 0.f : __expf(sc - mrun);
-    esum += wgt;
-    const int nstep = min(64, kq - base);
-#pragma unroll 4
-    for (int it = 0; it * rpi < nstep; ++it) {
-      const int src = it * rpi + grp;
-      const int jj = __shfl(j, src, 64);
-      const float ww = __shfl(wgt, src, 64);
-      if (src < nstep && ww != 0.f) {
-        const long off = ((long)(b * Tk + jj) * H + h) * D;
-        float xv[NE];
-        load_row<X, VEC>(V, off, sub, D, lpr, xv);
-        if (K) {
-          float xk[NE];
-          load_row<X, VEC>(K, off, sub, D, lpr, xk);
+    for (int c = 0; c < a.nsplit; ++c) {
+      const float* pc = P + (long)c * (4 + 2 * D);
+      const float f = pc[0] == -INFINITY ? 0.f : __expf(pc[0] - mrun);
+      if (lane == 0) {
+        esum += pc[1] * f;
+        const float u1 = pc[2], u2 = pc[3];
+        const float hi = fmaxf(t1, u1), lo = fmaxf(fminf(t1, u1), fmaxf(t2, u2));
+        t1 = hi;
+        t2 = lo;
+      }
+      if (grp == 0) {
 #pragma unroll
-          for (int i = 0; i < NE; ++i) ak[i] += ww * xk[i];
+        for (int i = 0; i < NE; ++i) {
+          const int d = elem_d<X, VEC>(sub, i, lpr);
+          if (d < D) {
+            ak[i] += pc[4 + d] * f;
+            av[i] += pc[4 + D + d] * f;
+          }
         }
-#pragma unroll
-        for (int i = 0; i < NE; ++i) av[i] += ww * xv[i];
       }
     }
   }
@@ -308,6 +356,69 @@ __global__ void finish_diag_kernel(float* __restrict__ avgd, long n, const int32
 
 __global__ void zero_int_kernel(int32_t* p) { *p = 0; }
 
+// Split-row form of the gather for rows with many slots and few rows (decode):
+// wave (row, c) accumulates slots [c*split_len, (c+1)*split_len) of the row
+// and writes its partial {max, sum, top-1, top-2, ak[D], av[D]}
+// (unnormalised, relative to that max); sparse_gather_kernel merges a row's
+// partials in split order, then runs its epilogue unchanged.
+template <typename X, bool VEC>
+__global__ __launch_bounds__(256) void gather_part_kernel(GatherArgs a, int lpr) {
+  constexpr int NE = GatherShape<X, VEC>::NE;
+  const int lane = threadIdx.x & 63;
+  const long wid = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const long nrows = (long)a.B * a.H * a.Tq;
+  if (wid >= nrows * a.nsplit) return;
+  const long row = wid / a.nsplit;
+  const int c = (int)(wid % a.nsplit);
+  const int Tq = a.Tq, H = a.H, D = a.D, topk = a.top_k;
+  const int bh = (int)(row / Tq);
+  const int b = bh / H, h = bh % H;
+  const int grp = lane / lpr, sub = lane % lpr;
+  const int kq = a.counts[row];
+  const bool fixed_max = a.top2 != nullptr;
+  float mrun = fixed_max ? a.top2[2 * row] : -INFINITY;
+  float t1 = -FLT_MAX, t2 = -FLT_MAX;
+  float ak[NE], av[NE];
+#pragma unroll
+  for (int i = 0; i < NE; ++i) { ak[i] = 0.f; av[i] = 0.f; }
+  float esum = 0.f;
+  const int s0 = c * a.split_len, s1 = min(kq, s0 + a.split_len);
+  gather_slots<X, VEC>(a, s0, s1, a.indices + row * topk, a.scores + row * topk,
+                       a.slot_valid ? a.slot_valid + row * topk : nullptr, reinterpret_cast<const X*>(a.k),
+                       reinterpret_cast<const X*>(a.v), b, h, grp, sub, lpr, fixed_max, mrun, t1, t2, esum, ak, av);
+  for (int o = lpr; o < 64; o <<= 1) {
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+      ak[i] += __shfl_xor(ak[i], o, 64);
+      av[i] += __shfl_xor(av[i], o, 64);
+    }
+  }
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const float b1 = __shfl_xor(t1, o, 64), b2 = __shfl_xor(t2, o, 64);
+    const float hi = fmaxf(t1, b1), lo = fmaxf(fminf(t1, b1), fmaxf(t2, b2));
+    t1 = hi; t2 = lo;
+  }
+  const float E = wave_sum(esum);
+  float* P = a.part + wid * (4 + 2 * D);
+  if (lane == 0) {
+    P[0] = mrun;
+    P[1] = E;
+    P[2] = t1;
+    P[3] = t2;
+  }
+  if (grp == 0) {
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+      const int d = elem_d<X, VEC>(sub, i, lpr);
+      if (d < D) {
+        P[4 + d] = ak[i];
+        P[4 + D + d] = av[i];
+      }
+    }
+  }
+}
+
 hipError_t launch_sparse_gather(const GatherArgs& a, hipStream_t st) {
   const long nrows = (long)a.B * a.H * a.Tq;
   const dim3 grid((unsigned)((nrows + 3) / 4));
@@ -316,6 +427,18 @@ hipError_t launch_sparse_gather(const GatherArgs& a, hipStream_t st) {
   bool vec = (a.D % epv) == 0;
   auto aligned = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
   vec = vec && aligned(a.v) && (a.k == nullptr || aligned(a.k)) && (a.self_key == nullptr || aligned(a.self_key));
+  if (a.nsplit > 0) {
+    const dim3 pgrid((unsigned)((nrows * a.nsplit + 3) / 4));
+    if (vec) {
+      int lpr = 1;
+      while (lpr * epv < a.D) lpr <<= 1;
+      if (a.dtype == DT_F32) gather_part_kernel<float, true><<<pgrid, 256, 0, st>>>(a, lpr);
+      else gather_part_kernel<bf16_t, true><<<pgrid, 256, 0, st>>>(a, lpr);
+    } else {
+      if (a.dtype == DT_F32) gather_part_kernel<float, false><<<pgrid, 256, 0, st>>>(a, 64);
+      else gather_part_kernel<bf16_t, false><<<pgrid, 256, 0, st>>>(a, 64);
+    }
+  }
   if (vec) {
     int lpr = 1;
     while (lpr * epv < a.D) lpr <<= 1;

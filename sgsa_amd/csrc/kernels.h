@@ -122,7 +122,22 @@ struct GatherArgs {
   int32_t* max_index;        // 1 int scratch (diagnostics); required when diag != nullptr
   const float* margin_in;    // [B,H,Tq] score margin to report instead of top-2 (block_only), or nullptr
   float ent_pad;             // zero-weight entries of the row beyond the slots (entropy terms of eps)
+  int nsplit;                // > 0: split-row form, nsplit partials of split_len slots per row
+  int split_len;
+  float* part;               // [B,H,Tq,nsplit,4+2D] partials (split-row form)
 };
+
+// Split-row gather: used for at most GATHER_SPLIT_ROWS rows with more than
+// GATHER_SPLIT_LEN slots; partial buffer bytes for a call.
+constexpr long GATHER_SPLIT_ROWS = 2048;
+constexpr int GATHER_SPLIT_LEN = 128;
+inline int gather_nsplit(long rows, int top_k) {
+  if (rows > GATHER_SPLIT_ROWS || top_k <= GATHER_SPLIT_LEN) return 0;
+  return (top_k + GATHER_SPLIT_LEN - 1) / GATHER_SPLIT_LEN;
+}
+inline size_t gather_part_bytes(long rows, int top_k, int D) {
+  return (size_t)rows * gather_nsplit(rows, top_k) * (4 + 2 * D) * sizeof(float);
+}
 
 constexpr int NDIAG = 10;
 

@@ -115,11 +115,14 @@ def sgsa_decode_step(
     vh = torch.empty_like(wk)
     al = torch.empty(B, 1, H, device=dev, dtype=torch.float32)
     bud = budget_logits.float().contiguous()
+    gn = ctypes.c_size_t()
+    _abi.check(L.sgsa_sparse_gather_workspace_size(B, 1, H, D, kk, ctypes.byref(gn)))
+    gws = torch.empty(gn.value, device=dev, dtype=torch.uint8)
     _abi.check(L.sgsa_sparse_gather(
         _abi.dtype_code(dt), B, 1, Tbuf, H, D, kk, Tc - 1, _abi.ptr(kc), _abi.ptr(vc), _abi.ptr(kn), _abi.ptr(idx),
         _abi.ptr(sc), _abi.ptr(top2), _abi.ptr(cnt), _abi.ptr(bud), mode, float(alpha_max), float(tau_c), 64, 8,
         _abi.ptr(wk if mode == 0 else None), _abi.ptr(vh), _abi.ptr(wk if mode == 1 else None), _abi.ptr(al),
-        None, None, None, 0, _abi.stream_of(kc)))
+        None, None, _abi.ptr(gws), gn.value, _abi.stream_of(kc)))
     # 3. the recurrent update for this token
     o, st = fused_recurrent_sgsa(q, k, v, beta, gamma, wk, vh, al, state, output_final_state=True)
     return (o, st, (idx, cnt)) if return_candidates else (o, st)
