@@ -95,6 +95,14 @@ int sgsa_chunk_fwd(int dtype, int B, int T, int H, int D, int chunk_size,
  * scores (-FLT_MAX if absent).  Needs sgsa_score_topk_workspace_size() bytes
  * of workspace (per-row candidate lists). */
 int sgsa_score_topk_workspace_size(int B, int Tq, int H, size_t* bytes);
+/* Workspace that also enables the few-row form of sgsa_score_topk: bf16,
+ * D % 32 == 0, at most 8 query rows per (b, h), B*H*Tq <= 2048 and Tk <= 32768
+ * (decode).  Each row's keys are scored by many workgroups into a [rows, Tk]
+ * buffer, then selected by an exact radix select in LDS; same results and
+ * contract, the unsorted order being one ascending run.  Equals
+ * sgsa_score_topk_workspace_size() where the form does not apply.  The
+ * workspace must be 256-byte aligned for the form to be used. */
+int sgsa_score_topk_fast_workspace_size(int dtype, int B, int Tq, int Tk, int H, int D, size_t* bytes);
 int sgsa_score_topk(int dtype, int B, int Tq, int Tk, int H, int D, int top_k,
                     int causal, int q_offset, float scale, int scale_mode,
                     const void* q, const void* k,

@@ -43,6 +43,7 @@ SIGNATURES = {
     "sgsa_chunk_fwd_workspace_size": (_I, [_I, _I, _I, _I, _I, ctypes.POINTER(_SZ)]),
     "sgsa_chunk_fwd": (_I, [_I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),
     "sgsa_score_topk_workspace_size": (_I, [_I, _I, _I, ctypes.POINTER(_SZ)]),
+    "sgsa_score_topk_fast_workspace_size": (_I, [_I, _I, _I, _I, _I, _I, ctypes.POINTER(_SZ)]),
     "sgsa_score_topk": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _I, _F, _I, _P, _P, _P, _P, _P, _P, _P, _I, _P,
                              _SZ, _P]),
     "sgsa_sparse_gather_tiled": (_I, [_I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _I, _F, _F, _P, _P, _P,

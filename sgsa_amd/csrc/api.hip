@@ -181,8 +181,29 @@ int sgsa_score_topk(int dtype, int B, int Tq, int Tk, int H, int D, int top_k, i
   a.q = q; a.k = k; a.indices = indices; a.scores = scores; a.top2 = top2; a.counts = counts; a.split = split;
   a.workspace = workspace;
   hipStream_t st = (hipStream_t)stream;
-  if (int s = hip_status(sgsa::launch_score_topk(a, st), "sgsa_score_topk")) return s;
+  const size_t base_ws = (need_ws + 255) & ~(size_t)255;
+  const size_t rows_ws = sgsa::topk_rows_bytes(a);
+  if (rows_ws > 0 && workspace_bytes >= base_ws + rows_ws && ((uintptr_t)workspace & 255u) == 0) {
+    float* sbuf = reinterpret_cast<float*>(static_cast<char*>(workspace) + base_ws);
+    if (int s = hip_status(sgsa::launch_score_topk_rows(a, sbuf, st), "sgsa_score_topk (few rows)")) return s;
+  } else if (int s = hip_status(sgsa::launch_score_topk(a, st), "sgsa_score_topk")) {
+    return s;
+  }
   if (sorted) return hip_status(sgsa::launch_sort_rows(indices, scores, (long)B * H * Tq, top_k, counts, st), "sgsa_score_topk(sort)");
+  return SGSA_OK;
+}
+
+int sgsa_score_topk_fast_workspace_size(int dtype, int B, int Tq, int Tk, int H, int D, size_t* bytes) {
+  if (int s = check_dtype(dtype)) return s;
+  if (int s = check_dims(B, Tq, H, D)) return s;
+  if (int s = check_dims(B, Tk, H, D)) return s;
+  REQUIRE(bytes);
+  sgsa::TopkArgs a{};
+  a.dtype = dtype; a.B = B; a.Tq = Tq; a.Tk = Tk; a.H = H; a.D = D;
+  static const uint4 probe{};   // aligned stand-ins: the form also needs 16-byte aligned q and k
+  a.q = &probe; a.k = &probe;
+  const size_t need_ws = (sgsa::topk_workspace_bytes(B, Tq, H) + 255) & ~(size_t)255;
+  *bytes = need_ws + sgsa::topk_rows_bytes(a);
   return SGSA_OK;
 }
 

@@ -79,6 +79,16 @@ struct TopkArgs {
 };
 
 constexpr int TOPK_CAP = 512;   // collected threshold-bin candidates per row
+
+// Few-row form of the select (topk_rows.hip): bf16, D % 32 == 0, at most
+// TR_MAX_TQ query rows per (b, h), TR_MAX_ROWS rows and TR_MAXK keys.  Extra
+// workspace (a [rows, Tk] fp32 score buffer) or 0 when the form does not apply.
+constexpr int DP_ROWS = 128;
+constexpr int TR_MAXK = 32768;
+constexpr int TR_MAX_TQ = 8;
+constexpr long TR_MAX_ROWS = 2048;
+size_t topk_rows_bytes(const TopkArgs& a);
+hipError_t launch_score_topk_rows(const TopkArgs& a, float* sbuf, hipStream_t st);
 size_t topk_workspace_bytes(int B, int Tq, int H);
 // Tile-list layout shared by the layer-path K1 and K2: one region per
 // (batch*head, 64-row block, wave) of 16 * (top_k + TOPK_CAP) entries and of

@@ -91,7 +91,7 @@ def sgsa_decode_step(
         top2 = torch.empty(B, H, 1, 2, device=dev, dtype=torch.float32)
         cnt = torch.empty(B, H, 1, device=dev, dtype=torch.int32)
         nb = ctypes.c_size_t()
-        _abi.check(L.sgsa_score_topk_workspace_size(B, 1, H, ctypes.byref(nb)))
+        _abi.check(L.sgsa_score_topk_fast_workspace_size(_abi.dtype_code(dt), B, 1, Tbuf, H, D, ctypes.byref(nb)))
         tws = torch.empty(nb.value, device=dev, dtype=torch.uint8)
         _abi.check(L.sgsa_score_topk(_abi.dtype_code(dt), B, 1, Tbuf, H, D, kk, 1, Tc - 1, math.sqrt(D), 0,
                                      _abi.ptr(rc), _abi.ptr(kc), _abi.ptr(idx), _abi.ptr(sc), _abi.ptr(top2),

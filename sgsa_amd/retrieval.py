@@ -24,13 +24,15 @@ Tensor = torch.Tensor
 
 def score_topk(q: Tensor, k: Tensor, top_k: int, causal: bool = True, q_offset: int = 0,
                scale: Optional[float] = None, scale_mode: int = 0, sorted: bool = True,
-               return_split: bool = False):
+               return_split: bool = False, fast: bool = True):
     """Exact top-k over causal scores without materialising them.
 
     q [B,Tq,H,D], k [B,Tk,H,D].  Returns (indices int32 [B,H,Tq,kk],
     scores float32 [B,H,Tq,kk], top2 float32 [B,H,Tq,2], counts int32 [B,H,Tq])
     with kk = min(top_k, Tk); with ``return_split`` (unsorted output only) also
-    the length of each row's first ascending run.
+    the length of each row's first ascending run.  ``fast`` passes the workspace
+    of sgsa_score_topk_fast_workspace_size, which lets decode-shaped calls (few
+    query rows per head) use the few-row form; ``fast=False`` keeps the row kernel.
     """
     if not q.is_cuda:
         raise ValueError("score_topk: the SGSA kernels run on a ROCm GPU; got CPU tensors")
@@ -50,7 +52,11 @@ def score_topk(q: Tensor, k: Tensor, top_k: int, causal: bool = True, q_offset: 
     spl = torch.empty(B, H, Tq, device=dev, dtype=torch.int32) if return_split else None
     L = _abi.lib()
     nbytes = ctypes.c_size_t()
-    _abi.check(L.sgsa_score_topk_workspace_size(B, Tq, H, ctypes.byref(nbytes)))
+    if fast:
+        _abi.check(L.sgsa_score_topk_fast_workspace_size(_abi.dtype_code(q.dtype), B, Tq, Tk, H, D,
+                                                         ctypes.byref(nbytes)))
+    else:
+        _abi.check(L.sgsa_score_topk_workspace_size(B, Tq, H, ctypes.byref(nbytes)))
     ws = torch.empty(nbytes.value, device=dev, dtype=torch.uint8)
     _abi.check(L.sgsa_score_topk(
         _abi.dtype_code(q.dtype), B, Tq, Tk, H, D, kk, int(causal), int(q_offset), float(scale), int(scale_mode),
