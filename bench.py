@@ -491,7 +491,7 @@ def main() -> int:
     f_score = B * H * T * (T + 1) * D               # causal score GEMM, one pass
     f_chunk = B * H * ((T + 63) // 64) * 23.77e6     # chunk contractions (K3 + K5 + K4)
     gather_kernel = {"threshold": "gather_thr_kernel", "tiled": "gather_list_kernel",
-                     "direct": "sparse_gather_kernel<bf16_t, true>"}[args.gather]
+                     "direct": "sparse_gather_kernel<bf16_t, true, false>"}[args.gather]
     topk_kernel = {"threshold": "score_thr128_kernel", "tiled": "score_topk_tiles_kernel<true, false>",
                    "direct": "score_topk_kernel<bf16_t, false, true, true, false, false, false>"}[args.gather]
     rooflines = {
@@ -518,7 +518,7 @@ def main() -> int:
     for r in rooflines.values():
         r["frac"] = round(r["achieved"] / r["peak"], 4)
     if gather_form_ms is not None:
-        gk = "sparse_gather_kernel<bf16_t, true>"
+        gk = "sparse_gather_kernel<bf16_t, true, false>"
         ach = gbytes / (gather_form_ms / 1000.0) / 1e9
         rooflines["row_gather_form"] = {
             "kernel": f"{gk} (K2 as a gather of the selected K/V rows, timed beside the step)", "ms": round(gather_form_ms, 3),

@@ -132,7 +132,7 @@ __device__ __forceinline__ void gather_slots(const GatherArgs& a, int s0, int s1
   }
 }
 
-template <typename X, bool VEC>
+template <typename X, bool VEC, bool SPLIT>
 __global__ __launch_bounds__(256) void sparse_gather_kernel(GatherArgs a, int lpr) {
   constexpr int NE = GatherShape<X, VEC>::NE;
   const int lane = threadIdx.x & 63;
@@ -161,8 +161,53 @@ __global__ __launch_bounds__(256) void sparse_gather_kernel(GatherArgs a, int lp
   for (int i = 0; i < NE; ++i) { ak[i] = 0.f; av[i] = 0.f; }
   float esum = 0.f;
 
-  if (a.nsplit == 0) {
-    gather_slots<X, VEC>(a, 0, kq, idxp, scp, vp, K, V, b, h, grp, sub, lpr, fixed_max, mrun, t1, t2, esum, ak, av);
+  if constexpr (!SPLIT) {
+    for (int base = 0; base < kq; base += 64) {
+      const int slot = base + lane;
+      int j = 0;
+      float sc = -INFINITY;
+      if (slot < kq) {
+        j = idxp[slot];
+        const bool ok = vp ? (vp[slot] != 0) : true;
+        if (ok) sc = scp[slot];
+      }
+      if (!fixed_max) {
+        // online-softmax merge: rescale what was accumulated under the old max
+        const float bm = wave_max(sc);
+        if (bm > mrun) {
+          const float f = (mrun == -INFINITY) ? 0.f : __expf(mrun - bm);
+          esum *= f;
+  #pragma unroll
+          for (int i = 0; i < NE; ++i) { ak[i] *= f; av[i] *= f; }
+          mrun = bm;
+        }
+        const float so = sc == -INFINITY ? -FLT_MAX : sc;
+        t2 = fmaxf(t2, fminf(t1, so));
+        t1 = fmaxf(t1, so);
+      }
+      const float wgt = sc == -INFINITY ? 0.f : __expf(sc - mrun);
+      esum += wgt;
+      const int nstep = min(64, kq - base);
+  #pragma unroll 4
+      for (int it = 0; it * rpi < nstep; ++it) {
+        const int src = it * rpi + grp;
+        const int jj = __shfl(j, src, 64);
+        const float ww = __shfl(wgt, src, 64);
+        if (src < nstep && ww != 0.f) {
+          const long off = ((long)(b * Tk + jj) * H + h) * D;
+          float xv[NE];
+          load_row<X, VEC>(V, off, sub, D, lpr, xv);
+          if (K) {
+            float xk[NE];
+            load_row<X, VEC>(K, off, sub, D, lpr, xk);
+  #pragma unroll
+            for (int i = 0; i < NE; ++i) ak[i] += ww * xk[i];
+          }
+  #pragma unroll
+          for (int i = 0; i < NE; ++i) av[i] += ww * xv[i];
+        }
+      }
+    }
   } else {
     // merge the row's partials (gather_part_kernel) in split order
     const float* P = a.part + row * (long)a.nsplit * (4 + 2 * D);
@@ -439,14 +484,25 @@ hipError_t launch_sparse_gather(const GatherArgs& a, hipStream_t st) {
       else gather_part_kernel<bf16_t, false><<<pgrid, 256, 0, st>>>(a, 64);
     }
   }
+  const bool sp = a.nsplit > 0;
   if (vec) {
     int lpr = 1;
     while (lpr * epv < a.D) lpr <<= 1;
-    if (a.dtype == DT_F32) sparse_gather_kernel<float, true><<<grid, 256, 0, st>>>(a, lpr);
-    else sparse_gather_kernel<bf16_t, true><<<grid, 256, 0, st>>>(a, lpr);
+    if (a.dtype == DT_F32) {
+      if (sp) sparse_gather_kernel<float, true, true><<<grid, 256, 0, st>>>(a, lpr);
+      else sparse_gather_kernel<float, true, false><<<grid, 256, 0, st>>>(a, lpr);
+    } else {
+      if (sp) sparse_gather_kernel<bf16_t, true, true><<<grid, 256, 0, st>>>(a, lpr);
+      else sparse_gather_kernel<bf16_t, true, false><<<grid, 256, 0, st>>>(a, lpr);
+    }
   } else {
-    if (a.dtype == DT_F32) sparse_gather_kernel<float, false><<<grid, 256, 0, st>>>(a, 64);
-    else sparse_gather_kernel<bf16_t, false><<<grid, 256, 0, st>>>(a, 64);
+    if (a.dtype == DT_F32) {
+      if (sp) sparse_gather_kernel<float, false, true><<<grid, 256, 0, st>>>(a, 64);
+      else sparse_gather_kernel<float, false, false><<<grid, 256, 0, st>>>(a, 64);
+    } else {
+      if (sp) sparse_gather_kernel<bf16_t, false, true><<<grid, 256, 0, st>>>(a, 64);
+      else sparse_gather_kernel<bf16_t, false, false><<<grid, 256, 0, st>>>(a, 64);
+    }
   }
   if (a.diag) {
     const long plane = nrows;
