@@ -393,11 +393,22 @@ template <bool VEC> struct KeyDot<bf16_t, VEC> {
 // candidate set with score -FLT_MAX and are invalid (what the masked top-k over
 // -FLT_MAX ties returns under the lowest-index rule); slots >= kq hold index 0.
 // block_only (:346-359): every candidate becomes a slot, in generation order.
+// LDS of block_cand_kernel, sized per launch: the query row, the kept slots'
+// prefix counts and (block_token) the sort keys of the candidates.
+constexpr size_t CAND_Q_BYTES = BLK_MAX_D * sizeof(float);
+__host__ __device__ inline size_t cand_pre_bytes(int eb) { return ((size_t)(eb + 1) * sizeof(int) + 7) & ~(size_t)7; }
+inline int cand_npad(int ks) {
+  int n = 1;
+  while (n < ks) n <<= 1;
+  return n;
+}
+
 template <typename X, bool VEC, bool TOKEN, bool MF>
 __global__ __launch_bounds__(64) void block_cand_kernel(BlockArgs a, float mscale) {
-  __shared__ float qrow[BLK_MAX_D];
-  __shared__ int pre[BLK_MAXC + 1];
-  __shared__ uint64_t keys[TOKEN ? BLK_MAXC : 1];
+  extern __shared__ __align__(16) char cand_lds[];
+  float* qrow = reinterpret_cast<float*>(cand_lds);
+  int* pre = reinterpret_cast<int*>(cand_lds + CAND_Q_BYTES);
+  uint64_t* keys = reinterpret_cast<uint64_t*>(cand_lds + CAND_Q_BYTES + cand_pre_bytes(a.eb));
   const long row = blockIdx.x;
   const int lane = threadIdx.x;
   const int T = a.T, H = a.H, D = a.D, bs = a.bs, eb = a.eb;
@@ -587,12 +598,14 @@ __global__ __launch_bounds__(256) void block_dense_weights_kernel(int T, int ks,
 template <typename X, bool MF>
 static void launch_cand(const BlockArgs& a, float ms, bool vec, hipStream_t st) {
   const dim3 grid((unsigned)((long)a.B * a.H * a.T));
+  // ncand <= ks = eb * min(bs, T): the sort needs next_pow2(ks) keys (<= BLK_MAXC)
+  const size_t lds = CAND_Q_BYTES + cand_pre_bytes(a.eb) + (a.mode == 1 ? (size_t)cand_npad(a.ks) * 8 : 0);
   if (a.mode == 1) {
-    if (vec) block_cand_kernel<X, true, true, MF><<<grid, 64, 0, st>>>(a, ms);
-    else block_cand_kernel<X, false, true, MF><<<grid, 64, 0, st>>>(a, ms);
+    if (vec) block_cand_kernel<X, true, true, MF><<<grid, 64, lds, st>>>(a, ms);
+    else block_cand_kernel<X, false, true, MF><<<grid, 64, lds, st>>>(a, ms);
   } else {
-    if (vec) block_cand_kernel<X, true, false, MF><<<grid, 64, 0, st>>>(a, ms);
-    else block_cand_kernel<X, false, false, MF><<<grid, 64, 0, st>>>(a, ms);
+    if (vec) block_cand_kernel<X, true, false, MF><<<grid, 64, lds, st>>>(a, ms);
+    else block_cand_kernel<X, false, false, MF><<<grid, 64, lds, st>>>(a, ms);
   }
 }
 

@@ -387,19 +387,31 @@ __global__ __launch_bounds__(256) void sparse_gather_kernel(GatherArgs a, int lp
         dg[7 * plane + row] = nloc * inv_k;
         dg[8 * plane + row] = nsink * inv_k;
         dg[9 * plane + row] = nrem * inv_k;
-        atomicMax(a.max_index, imax);
+        atomicMax(a.max_index + (row & (GATHER_MAXIDX_SLOTS - 1)), imax);   // spread: one word takes 1/64 of the rows
       }
     }
   }
 }
 
-// avg_distance /= max(max_index + 1, 1)  (modelings/modeling_sgsa.py:395, :401)
-__global__ void finish_diag_kernel(float* __restrict__ avgd, long n, const int32_t* __restrict__ max_index) {
+// avg_distance /= max(max_index + 1, 1)  (modelings/modeling_sgsa.py:395, :401); the largest index is the
+// max over the GATHER_MAXIDX_SLOTS words the rows spread their atomics over.
+__global__ __launch_bounds__(256) void finish_diag_kernel(float* __restrict__ avgd, long n,
+                                                          const int32_t* __restrict__ max_index) {
+  __shared__ int mx;
+  if (threadIdx.x < 64) {
+    int m = max_index[threadIdx.x & (GATHER_MAXIDX_SLOTS - 1)];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = max(m, __shfl_xor(m, o, 64));
+    if (threadIdx.x == 0) mx = m;
+  }
+  __syncthreads();
   const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) avgd[i] = avgd[i] / (float)max(*max_index + 1, 1);
+  if (i < n) avgd[i] = avgd[i] / (float)max(mx + 1, 1);
 }
 
-__global__ void zero_int_kernel(int32_t* p) { *p = 0; }
+__global__ void zero_int_kernel(int32_t* p) {
+  if (threadIdx.x < GATHER_MAXIDX_SLOTS) p[threadIdx.x] = 0;
+}
 
 // Split-row form of the gather for rows with many slots and few rows (decode):
 // wave (row, c) accumulates slots [c*split_len, (c+1)*split_len) of the row
@@ -467,7 +479,7 @@ __global__ __launch_bounds__(256) void gather_part_kernel(GatherArgs a, int lpr)
 hipError_t launch_sparse_gather(const GatherArgs& a, hipStream_t st) {
   const long nrows = (long)a.B * a.H * a.Tq;
   const dim3 grid((unsigned)((nrows + 3) / 4));
-  if (a.diag) zero_int_kernel<<<1, 1, 0, st>>>(a.max_index);
+  if (a.diag) zero_int_kernel<<<1, 64, 0, st>>>(a.max_index);
   const int epv = 16 / (a.dtype == DT_F32 ? 4 : 2);
   bool vec = (a.D % epv) == 0;
   auto aligned = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };

@@ -129,7 +129,7 @@ struct GatherArgs {
   float* alpha;              // [B,Tq,H] or nullptr
   float* weights;            // [B,H,Tq,top_k] or nullptr
   float* diag;               // [NDIAG,B,H,Tq] or nullptr
-  int32_t* max_index;        // 1 int scratch (diagnostics); required when diag != nullptr
+  int32_t* max_index;        // GATHER_MAXIDX_SLOTS ints of scratch (256 bytes, diagnostics); required with diag
   const float* margin_in;    // [B,H,Tq] score margin to report instead of top-2 (block_only), or nullptr
   float ent_pad;             // zero-weight entries of the row beyond the slots (entropy terms of eps)
   int nsplit;                // > 0: split-row form, nsplit partials of split_len slots per row
@@ -150,6 +150,7 @@ inline size_t gather_part_bytes(long rows, int top_k, int D) {
 }
 
 constexpr int NDIAG = 10;
+constexpr int GATHER_MAXIDX_SLOTS = 64;   // words the diagnostics' largest-index atomics are spread over
 
 // Block retrieval (block.hip).
 constexpr int BLK_MAX_D = 128;   // head dim limit
