@@ -270,6 +270,110 @@ __global__ __launch_bounds__(256) void block_max_mfma_kernel(BlockArgs a, float 
   }
 }
 
+// bf16 sweep for block_size 16 or 32 with the keys straight into registers
+// (the K1 threshold kernel's sweep, without its LDS): a workgroup takes 128
+// query rows, resident as eight 16-row B operands per wave, and sweeps
+// 128-key tiles; wave w takes keys [32w, 32w+32) of a tile as two 16-key A
+// operands, loaded into registers one tile ahead (MFMA row rho holds key
+// rho/4 + 4 (rho%4), so lane (lg, lr) ends with rows 16g + lr against keys
+// 32w + 16u + lg + 4i).  A wave's keys are whole blocks, so a block's max for a
+// row is an in-lane max and two swaps over lg, stored by the lanes lg == 0
+// (16 consecutive rows per store); blocks never span tiles, and nothing is
+// shared between waves.  Same operands, k-position order and score_of() as
+// block_cand_kernel's scorer, so scores agree bit for bit.
+__global__ __launch_bounds__(256, 2) void block_max_reg_kernel(BlockArgs a, float mscale) {
+  constexpr int QR = BMM_ROWS, NG = QR / 16, TK = 128;
+  const int D = a.D, T = a.T, H = a.H, bs = a.bs, nb = a.nb, nks = D / 32;
+  const int nrb = (T + QR - 1) / QR;
+  const int bh = blockIdx.y, b = bh / H, h = bh % H;
+  const int r0 = (nrb - 1 - (int)blockIdx.x) * QR;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lr = lane & 15, lg = lane >> 4;
+  const uint16_t* Q = reinterpret_cast<const uint16_t*>(a.q);
+  const uint16_t* K = reinterpret_cast<const uint16_t*>(a.k) + ((long)b * T * H + h) * D;
+  const long kstride = (long)H * D;
+
+  bf16x8 qf[NG][BLK_MAX_D / 32];
+#pragma unroll
+  for (int g = 0; g < NG; ++g) {
+    const int qr = r0 + 16 * g + lr;
+#pragma unroll
+    for (int s = 0; s < BLK_MAX_D / 32; ++s) {
+      u16x8 raw = {0, 0, 0, 0, 0, 0, 0, 0};
+      if (s < nks && qr < T) raw = *reinterpret_cast<const u16x8*>(Q + ((long)(b * T + qr) * H + h) * D + 32 * s + 8 * lg);
+      qf[g][s] = __builtin_bit_cast(bf16x8, raw);
+    }
+  }
+  float* bsc = a.block_scores + (long)bh * nb * T;
+  const int kend = a.causal ? min(T, r0 + QR) : T;
+  if (a.fill_invalid) {
+    const int fb = (kend + bs - 1) / bs, nfill = nb - fb;
+    for (long e = tid; e < (long)QR * nfill; e += 256) {
+      const int t = r0 + (int)(e % QR);
+      if (t < T) bsc[(fb + e / QR) * T + t] = -FLT_MAX;
+    }
+  }
+  const int minvalid = a.causal ? min(T, r0 + 1) : T;   // keys below it are valid for every row
+  const int ntile = (kend + TK - 1) / TK;
+  const int krow = (lr >> 2) + 4 * (lr & 3);
+  bf16x8 kf[2][BLK_MAX_D / 32];
+  auto kload = [&](int kt) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int j = kt * TK + 32 * w + 16 * u + krow;
+      const uint16_t* p = K + (long)(j < T ? j : 0) * kstride + 8 * lg;
+#pragma unroll
+      for (int s = 0; s < BLK_MAX_D / 32; ++s) {
+        u16x8 raw = {0, 0, 0, 0, 0, 0, 0, 0};
+        if (s < nks) raw = *reinterpret_cast<const u16x8*>(p + 32 * s);
+        kf[u][s] = __builtin_bit_cast(bf16x8, raw);
+      }
+    }
+  };
+  if (ntile > 0) kload(0);
+  for (int kt = 0; kt < ntile; ++kt) {
+    const int kw = kt * TK + 32 * w;   // the wave's first key
+    const bool full = kw + 32 <= minvalid;
+    float m[2][NG];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        f4 c = f4_zero();
+#pragma unroll
+        for (int s = 0; s < BLK_MAX_D / 32; ++s)
+          if (s < nks) c = mma_bf16(kf[u][s], qf[g][s], c);
+        const f4 sc = score_of(c, mscale);
+        const int qr = r0 + 16 * g + lr;
+        float mx = -FLT_MAX;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int key = kw + 16 * u + lg + 4 * i;
+          const bool ok = full || (qr < T && key < T && (!a.causal || key <= qr));
+          mx = fmaxf(mx, ok ? sc[i] : -FLT_MAX);
+        }
+        m[u][g] = mx;
+      }
+    }
+    if (kt + 1 < ntile) kload(kt + 1);
+    if (kw < kend) {   // wave-uniform: the wave's keys hold a block the rows may see
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        if (bs == 32 && u == 1) break;
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+          float v = bs == 32 ? fmaxf(m[0][g], m[1][g]) : m[u][g];
+          v = fmaxf(v, __shfl_xor(v, 16, 64));
+          v = fmaxf(v, __shfl_xor(v, 32, 64));
+          const int t = r0 + 16 * g + lr;
+          const int bb = (kw + 16 * u) / bs;
+          if (lg == 0 && t < T && kw + 16 * u < kend) bsc[(long)bb * T + t] = v;
+        }
+      }
+    }
+  }
+}
+
 // [B,H,nb,T] -> [B,H,T,nb], for callers that ask for the block scores.
 __global__ __launch_bounds__(256) void block_scores_transpose_kernel(const float* __restrict__ src, long bhn, int T,
                                                                      int nb, float* __restrict__ dst) {
@@ -619,7 +723,8 @@ hipError_t launch_block_select(const BlockArgs& a, hipStream_t st) {
   const dim3 g1((unsigned)((a.T + 63) / 64), (unsigned)(a.B * a.H));
   const dim3 g2((unsigned)((a.T + BMM_ROWS - 1) / BMM_ROWS), (unsigned)(a.B * a.H));
   const bool mf = block_uses_mfma(a);
-  if (mf && a.bs % 16 == 0) block_max_mfma_kernel<true><<<g2, 256, 0, st>>>(a, ms);
+  if (mf && (a.bs == 16 || a.bs == 32)) block_max_reg_kernel<<<g2, 256, 0, st>>>(a, ms);
+  else if (mf && a.bs % 16 == 0) block_max_mfma_kernel<true><<<g2, 256, 0, st>>>(a, ms);
   else if (mf) block_max_mfma_kernel<false><<<g2, 256, 0, st>>>(a, ms);
   else if (a.dtype == DT_F32) block_max_kernel<float><<<g1, 256, 0, st>>>(a, ms);
   else block_max_kernel<bf16_t><<<g1, 256, 0, st>>>(a, ms);

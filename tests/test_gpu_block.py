@@ -54,7 +54,7 @@ def _check(dev, B, T, H, D, dt, top_k, bs, tb, mode, causal=True, seed=0, dup=Fa
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("mode", ["block_token", "block_only"])
 @pytest.mark.parametrize("T,bs,tb,top_k", [(150, 32, 2, 16), (97, 7, 3, 12), (64, 64, 2, 8), (40, 1, 5, 6),
-                                           (33, 32, 4, 48)])
+                                           (33, 32, 4, 48), (300, 16, 3, 20), (260, 48, 2, 30)])
 def test_block_modes_match_oracle(dev, dt, mode, T, bs, tb, top_k):
     _check(dev, 2, T, 3, 64, dt, top_k, bs, tb, mode, seed=T + bs)
 
@@ -68,6 +68,8 @@ def test_block_modes_head_dim_128_and_odd(dev, mode):
 @pytest.mark.parametrize("mode", ["block_token", "block_only"])
 def test_block_modes_non_causal(dev, mode):
     _check(dev, 1, 90, 2, 32, torch.float32, 10, 16, 2, mode, causal=False, seed=7)
+    for bs in (16, 32, 64):   # the bf16 MFMA sweeps: wave-owned blocks (16, 32) and the LDS-tile form (64)
+        _check(dev, 1, 290, 2, 64, torch.bfloat16, 12, bs, 2, mode, causal=False, seed=8 + bs)
 
 
 @pytest.mark.parametrize("mode", ["block_token", "block_only"])
