@@ -188,6 +188,15 @@ int sgsa_block_retrieve(int dtype, int B, int T, int H, int D, int top_k, int bl
                         void* k_hat, void* v_hat, float* diag, void* workspace, size_t workspace_bytes,
                         void* stream);
 
+/* ---- RMSNorm of the model shells -------------------------------------------
+ * y = x * rsqrt(mean(x^2) + eps) * weight over the last dimension, in fp32,
+ * stored in x's dtype: the RMSNorm of the SGSA and hybrid stacks
+ * (modelings/hybrid_dense_delta_topk.py:94-103; the fla RMSNorm the SGSA model
+ * imports, modeling_sgsa.py:40, evaluated in fp32).  x, y [rows, C] contiguous
+ * in dtype; weight [C] in dtype (weight_f32 = 0) or fp32 (weight_f32 = 1). */
+int sgsa_rms_norm(int dtype, int weight_f32, long rows, int C, const void* x, const void* weight, float eps, void* y,
+                  void* stream);
+
 int sgsa_sparse_gather_tiled(int B, int T, int H, int D, int top_k, const void* k, const void* v,
                              const int32_t* indices, const float* scores, const float* top2,
                              const int32_t* counts, const int32_t* split, const float* budget,

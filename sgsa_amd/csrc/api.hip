@@ -474,6 +474,19 @@ int sgsa_block_retrieve(int dtype, int B, int T, int H, int D, int top_k, int bl
   return SGSA_OK;
 }
 
+int sgsa_rms_norm(int dtype, int weight_f32, long rows, int C, const void* x, const void* weight, float eps, void* y,
+                  void* stream) {
+  if (int s = check_dtype(dtype)) return s;
+  if (rows < 0 || C <= 0) return fail(SGSA_ERR_INVALID_ARG, "rows=%ld C=%d", rows, C);
+  if (rows > 0x7fffffffL) return fail(SGSA_ERR_UNSUPPORTED, "rows=%ld exceeds the grid", rows);
+  if (dtype == SGSA_F32 && !weight_f32) return fail(SGSA_ERR_INVALID_ARG, "fp32 input needs an fp32 weight");
+  if (!(eps >= 0.f)) return fail(SGSA_ERR_INVALID_ARG, "eps must be >= 0");
+  if (rows == 0) return SGSA_OK;
+  REQUIRE(x); REQUIRE(weight); REQUIRE(y);
+  return hip_status(sgsa::launch_rms_norm(dtype, weight_f32 ? 1 : 0, rows, C, x, weight, eps, y, (hipStream_t)stream),
+                    "sgsa_rms_norm");
+}
+
 int sgsa_sparse_gather_tiled(int B, int T, int H, int D, int top_k, const void* k, const void* v,
                              const int32_t* indices, const float* scores, const float* top2,
                              const int32_t* counts, const int32_t* split, const float* budget, int write_mode,

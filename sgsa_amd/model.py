@@ -28,6 +28,8 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from . import _abi
+
 from .layer import LayerWorkspace, sgsa_layer_forward, sgsa_layer_retrieve
 from .ops import chunk_sgsa
 
@@ -65,7 +67,8 @@ class SGSAConfig:
 
 
 class RMSNorm(nn.Module):
-    """x * rsqrt(mean(x^2) + eps) * weight, evaluated in fp32."""
+    """x * rsqrt(mean(x^2) + eps) * weight, evaluated in fp32 and stored in x's dtype, in one
+    HIP launch (sgsa_rms_norm; hybrid_dense_delta_topk.py:94-103)."""
 
     def __init__(self, hidden_size: int, eps: float) -> None:
         super().__init__()
@@ -73,9 +76,19 @@ class RMSNorm(nn.Module):
         self.eps = eps
 
     def forward(self, x: Tensor) -> Tensor:
-        xf = x.float()
-        y = xf * torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + self.eps)
-        return (y * self.weight.float()).to(x.dtype)
+        if not x.is_cuda:
+            raise ValueError("RMSNorm: the SGSA model runs on a ROCm GPU; got a CPU tensor")
+        xc = x.contiguous()
+        C = xc.shape[-1]
+        w = self.weight
+        if w.dtype != x.dtype and w.dtype != torch.float32:
+            w = w.float()
+        w = w.contiguous()
+        y = torch.empty_like(xc)
+        _abi.check(_abi.lib().sgsa_rms_norm(_abi.dtype_code(x.dtype), int(w.dtype == torch.float32),
+                                            xc.numel() // C, C, _abi.ptr(xc), _abi.ptr(w), float(self.eps),
+                                            _abi.ptr(y), _abi.stream_of(xc)))
+        return y
 
 
 class GatedMLP(nn.Module):

@@ -1,0 +1,36 @@
+"""GPU: the model shells' RMSNorm kernel (sgsa_rms_norm through sgsa_amd.model.RMSNorm)
+against the torch fp32 form of the same expression, x * rsqrt(mean(x^2) + eps) * w,
+stored in x's dtype (hybrid_dense_delta_topk.py:94-103 evaluated in fp32).  fp32
+within 1e-5; bf16 within one bf16 rounding (2e-2 relative)."""
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+sgsa_amd = pytest.importorskip("sgsa_amd")
+from sgsa_amd.model import RMSNorm  # noqa: E402
+
+
+@pytest.mark.parametrize("dt,wdt", [(torch.float32, torch.float32), (torch.bfloat16, torch.bfloat16),
+                                    (torch.bfloat16, torch.float32)])
+@pytest.mark.parametrize("shape", [(8, 1, 2048), (3, 77, 1000), (1, 5, 37)])
+def test_rms_norm_matches_torch(dev, dt, wdt, shape):
+    g = torch.Generator().manual_seed(shape[-1])
+    x = (3.0 * torch.randn(*shape, generator=g)).to(dt)
+    norm = RMSNorm(shape[-1], 1e-6)
+    with torch.no_grad():
+        norm.weight.copy_(1.0 + 0.1 * torch.randn(shape[-1], generator=g))
+    norm = norm.to(device=dev, dtype=wdt)
+    y = norm(x.to(dev))
+    torch.cuda.synchronize()
+    xf = x.float()
+    want = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6) * norm.weight.detach().float().cpu()
+    assert y.dtype == dt and y.shape == x.shape
+    tol = 1e-5 if dt == torch.float32 else 2e-2
+    torch.testing.assert_close(y.float().cpu(), want.to(dt).float(), atol=tol, rtol=tol)
+
+
+def test_rms_norm_rejects_cpu():
+    with pytest.raises(ValueError):
+        RMSNorm(16, 1e-6)(torch.ones(2, 16))
