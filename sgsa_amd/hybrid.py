@@ -39,7 +39,7 @@ import torch.nn.functional as F
 
 from .decode import sgsa_decode_step
 from .layer import LayerWorkspace, sgsa_layer_forward
-from .model import GatedMLP, RMSNorm, SGSABlock, SGSAConfig
+from .model import GatedMLP, RMSNorm, SGSABlock, SGSAConfig, fused_linear
 
 Tensor = torch.Tensor
 
@@ -160,9 +160,10 @@ class DenseGQABlock(nn.Module):
         """h [B, T, C] at positions pos0 ..; appends its keys and values to the cache."""
         B, T, C = h.shape
         n = self.input_norm(h)
-        q = self.q_proj(n).view(B, T, self.H, self.D).transpose(1, 2)
-        k = self.k_proj(n).view(B, T, self.Hkv, self.D).transpose(1, 2)
-        v = self.v_proj(n).view(B, T, self.Hkv, self.D).transpose(1, 2)
+        q, k, v = fused_linear(self, n, ("q_proj", "k_proj", "v_proj"))
+        q = q.reshape(B, T, self.H, self.D).transpose(1, 2)
+        k = k.reshape(B, T, self.Hkv, self.D).transpose(1, 2)
+        v = v.reshape(B, T, self.Hkv, self.D).transpose(1, 2)
         cos, sin = rope[0][pos0:pos0 + T], rope[1][pos0:pos0 + T]
         q, k = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
         cache["k"][:, :, pos0:pos0 + T] = k
@@ -174,19 +175,6 @@ class DenseGQABlock(nn.Module):
 
 class SGSADecoderBlock(SGSABlock):
     """SGSABlock with a prefill that keeps its cache and a one-token decode step."""
-
-    def _project(self, h: Tensor):
-        B, T, C = h.shape
-        H, D = self.num_heads, self.head_dim
-        n = self.input_norm(h)
-        q = self.q_proj(n).view(B, T, H, D)
-        k = self.k_proj(n).view(B, T, H, D)
-        v = self.v_proj(n).view(B, T, H, D)
-        q_ret = self.q_ret_proj(n).view(B, T, H, D)
-        beta = torch.sigmoid(self.beta_proj(n).float()).clamp_min(1e-4)
-        gamma = torch.sigmoid(self.gamma_proj(n).float())
-        budget = self.budget_proj(n).float()
-        return q, k, v, q_ret, beta, gamma, budget
 
     def _finish(self, h: Tensor, att: Tensor) -> Tensor:
         B, T, C = h.shape

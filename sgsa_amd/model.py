@@ -91,6 +91,31 @@ class RMSNorm(nn.Module):
         return y
 
 
+def fused_linear(module: nn.Module, x: Tensor, names) -> list:
+    """The outputs of the nn.Linear children ``names`` of ``module`` on the same input x.
+
+    Without autograd they come from one GEMM over the concatenated weights (views of
+    its output, split along the last dimension); the concatenation is cached on the
+    module and rebuilt when any weight or bias changes (storage or in-place version).
+    With autograd on, each projection runs on its own so gradients reach its weight.
+    """
+    lins = [getattr(module, n) for n in names]
+    if torch.is_grad_enabled():
+        return [lin(x) for lin in lins]
+    key = tuple((l.weight.data_ptr(), l.weight._version,
+                 None if l.bias is None else (l.bias.data_ptr(), l.bias._version)) for l in lins)
+    cached = module.__dict__.get("_fused_" + "_".join(names))
+    if cached is None or cached[0] != key:
+        w = torch.cat([l.weight for l in lins], 0)
+        b = None
+        if any(l.bias is not None for l in lins):
+            b = torch.cat([l.bias if l.bias is not None else l.weight.new_zeros(l.out_features) for l in lins])
+        cached = (key, w, b)
+        module.__dict__["_fused_" + "_".join(names)] = cached
+    y = F.linear(x, cached[1], cached[2])
+    return list(torch.split(y, [l.out_features for l in lins], dim=-1))
+
+
 class GatedMLP(nn.Module):
     """down(silu(gate(x)) * up(x))."""
 
@@ -101,7 +126,8 @@ class GatedMLP(nn.Module):
         self.down_proj = nn.Linear(intermediate_size, hidden_size, bias=False)
 
     def forward(self, x: Tensor) -> Tensor:
-        return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
+        gate, up = fused_linear(self, x, ("gate_proj", "up_proj"))
+        return self.down_proj(F.silu(gate) * up)
 
 
 class SGSABlock(nn.Module):
@@ -133,18 +159,22 @@ class SGSABlock(nn.Module):
         self.mlp = GatedMLP(C, config.intermediate_size)
         self._ws = LayerWorkspace()
 
-    def forward(self, h: Tensor) -> Tensor:
-        cfg = self.config
+    def _project(self, h: Tensor):
+        """q, k, v, q_ret [B,T,H,D] and beta, gamma, budget [B,T,H] (fp32) of the block's input."""
         B, T, C = h.shape
         H, D = self.num_heads, self.head_dim
         n = self.input_norm(h)
-        q = self.q_proj(n).view(B, T, H, D)
-        k = self.k_proj(n).view(B, T, H, D)
-        v = self.v_proj(n).view(B, T, H, D)
-        q_ret = self.q_ret_proj(n).view(B, T, H, D)
-        beta = torch.sigmoid(self.beta_proj(n).float()).clamp_min(1e-4)
-        gamma = torch.sigmoid(self.gamma_proj(n).float())
-        budget = self.budget_proj(n).float()
+        q, k, v, q_ret, bl, gl, ul = fused_linear(
+            self, n, ("q_proj", "k_proj", "v_proj", "q_ret_proj", "beta_proj", "gamma_proj", "budget_proj"))
+        beta = torch.sigmoid(bl.float()).clamp_min(1e-4)
+        gamma = torch.sigmoid(gl.float())
+        return (q.view(B, T, H, D), k.view(B, T, H, D), v.view(B, T, H, D), q_ret.view(B, T, H, D), beta, gamma,
+                ul.float())
+
+    def forward(self, h: Tensor) -> Tensor:
+        cfg = self.config
+        B, T, C = h.shape
+        q, k, v, q_ret, beta, gamma, budget = self._project(h)
         if cfg.sparse_output_lambda > 0:
             wk, vh, al = sgsa_layer_retrieve(q_ret, k, v, budget, cfg.top_k, cfg.sgsa_write_mode, cfg.alpha_max,
                                              cfg.tau_c, workspace=self._ws)
