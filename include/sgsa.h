@@ -197,6 +197,14 @@ int sgsa_block_retrieve(int dtype, int B, int T, int H, int D, int top_k, int bl
 int sgsa_rms_norm(int dtype, int weight_f32, long rows, int C, const void* x, const void* weight, float eps, void* y,
                   void* stream);
 
+/* The SGSA layer's gates from its gate projections' logits (SGSAStateLayer,
+ * modelings/modeling_sgsa.py:543-544 and the budget logits): beta = max(sigmoid(b), 1e-4),
+ * gamma = sigmoid(g), budget = u, as fp32 [rows, H].  Row r's logits start at
+ * logits + r * row_stride (elements of dtype): b's H values, then g's, then u's.
+ * row_stride >= 3H. */
+int sgsa_layer_gates(int dtype, long rows, int H, const void* logits, long row_stride, float* beta, float* gamma,
+                     float* budget, void* stream);
+
 int sgsa_sparse_gather_tiled(int B, int T, int H, int D, int top_k, const void* k, const void* v,
                              const int32_t* indices, const float* scores, const float* top2,
                              const int32_t* counts, const int32_t* split, const float* budget,

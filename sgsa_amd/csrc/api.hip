@@ -487,6 +487,17 @@ int sgsa_rms_norm(int dtype, int weight_f32, long rows, int C, const void* x, co
                     "sgsa_rms_norm");
 }
 
+int sgsa_layer_gates(int dtype, long rows, int H, const void* logits, long row_stride, float* beta, float* gamma,
+                     float* budget, void* stream) {
+  if (int s = check_dtype(dtype)) return s;
+  if (rows < 0 || H <= 0 || row_stride < 3L * H) return fail(SGSA_ERR_INVALID_ARG, "rows=%ld H=%d row_stride=%ld", rows, H, row_stride);
+  if (rows * H > 0x7fffffffL * 256L) return fail(SGSA_ERR_UNSUPPORTED, "rows * H exceeds the grid");
+  if (rows == 0) return SGSA_OK;
+  REQUIRE(logits); REQUIRE(beta); REQUIRE(gamma); REQUIRE(budget);
+  return hip_status(sgsa::launch_gates(dtype, logits, row_stride, rows, H, beta, gamma, budget, (hipStream_t)stream),
+                    "sgsa_layer_gates");
+}
+
 int sgsa_sparse_gather_tiled(int B, int T, int H, int D, int top_k, const void* k, const void* v,
                              const int32_t* indices, const float* scores, const float* top2,
                              const int32_t* counts, const int32_t* split, const float* budget, int write_mode,

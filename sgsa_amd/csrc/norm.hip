@@ -1,8 +1,11 @@
-// RMSNorm of the model shells (SGSAForCausalLM, the hybrid decoder) in one
-// launch per call: y = x * rsqrt(mean(x^2) + eps) * weight, evaluated in fp32
-// and stored in x's dtype.  The torch form of the same expression takes about
-// eight launches (cast, square, mean, add, rsqrt, two products, cast), which at
-// decode's few rows cost more host time than the arithmetic.
+// Small fused ops of the model shells (SGSAForCausalLM, the hybrid decoder), one
+// launch each where the torch form takes several, which at decode's few rows
+// cost more host time than the arithmetic:
+//   RMSNorm  y = x * rsqrt(mean(x^2) + eps) * weight, in fp32, stored in x's
+//            dtype (torch: cast, square, mean, add, rsqrt, two products, cast);
+//   gates    beta = max(sigmoid(b), 1e-4), gamma = sigmoid(g), budget = u in
+//            fp32 from the three H-wide logit groups of a projection row
+//            (torch: three casts, two sigmoids, a clamp).
 #include "common.h"
 #include "kernels.h"
 
@@ -27,6 +30,31 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const X* __restrict__ x, 
   const float r = 1.0f / sqrtf(mean + eps);
   X* yr = y + row * C;
   for (int c = threadIdx.x; c < C; c += 256) st(yr, c, ld(xr, c) * r * ld(w, c));
+}
+
+// One thread per (row, head).  Row r's logits start at src + r * stride: beta's
+// H, then gamma's H, then the budget's H.
+template <typename X>
+__global__ __launch_bounds__(256) void gates_kernel(const X* __restrict__ src, long stride, long rows, int H,
+                                                    float* __restrict__ beta, float* __restrict__ gamma,
+                                                    float* __restrict__ budget) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= rows * H) return;
+  const long r = i / H;
+  const int h = (int)(i % H);
+  const X* p = src + r * stride + h;
+  const float bl = ld(p, 0), gl = ld(p, H), ul = ld(p, 2 * H);
+  beta[i] = fmaxf(1.0f / (1.0f + expf(-bl)), 1e-4f);
+  gamma[i] = 1.0f / (1.0f + expf(-gl));
+  budget[i] = ul;
+}
+
+hipError_t launch_gates(int dtype, const void* src, long stride, long rows, int H, float* beta, float* gamma,
+                        float* budget, hipStream_t st) {
+  const dim3 grid((unsigned)((rows * H + 255) / 256));
+  if (dtype == DT_F32) gates_kernel<float><<<grid, 256, 0, st>>>((const float*)src, stride, rows, H, beta, gamma, budget);
+  else gates_kernel<bf16_t><<<grid, 256, 0, st>>>((const bf16_t*)src, stride, rows, H, beta, gamma, budget);
+  return hipGetLastError();
 }
 
 hipError_t launch_rms_norm(int dtype, int w_f32, long rows, int C, const void* x, const void* w, float eps, void* y,

@@ -166,10 +166,18 @@ class SGSABlock(nn.Module):
         n = self.input_norm(h)
         q, k, v, q_ret, bl, gl, ul = fused_linear(
             self, n, ("q_proj", "k_proj", "v_proj", "q_ret_proj", "beta_proj", "gamma_proj", "budget_proj"))
-        beta = torch.sigmoid(bl.float()).clamp_min(1e-4)
-        gamma = torch.sigmoid(gl.float())
+        if torch.is_grad_enabled():
+            beta = torch.sigmoid(bl.float()).clamp_min(1e-4)
+            gamma = torch.sigmoid(gl.float())
+            budget = ul.float()
+        else:
+            # bl, gl, ul are consecutive H-wide groups of one projection row: one launch for all three
+            beta, gamma, budget = (torch.empty(B, T, H, device=h.device, dtype=torch.float32) for _ in range(3))
+            _abi.check(_abi.lib().sgsa_layer_gates(_abi.dtype_code(bl.dtype), B * T, H, _abi.ptr(bl), bl.stride(-2),
+                                                   _abi.ptr(beta), _abi.ptr(gamma), _abi.ptr(budget),
+                                                   _abi.stream_of(bl)))
         return (q.view(B, T, H, D), k.view(B, T, H, D), v.view(B, T, H, D), q_ret.view(B, T, H, D), beta, gamma,
-                ul.float())
+                budget)
 
     def forward(self, h: Tensor) -> Tensor:
         cfg = self.config

@@ -34,3 +34,20 @@ def test_rms_norm_matches_torch(dev, dt, wdt, shape):
 def test_rms_norm_rejects_cpu():
     with pytest.raises(ValueError):
         RMSNorm(16, 1e-6)(torch.ones(2, 16))
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_layer_gates_match_torch(dev, dt):
+    # logits laid out as a fused projection row: [other 40 | beta H | gamma H | budget H | 5 more]
+    from sgsa_amd import _abi
+    B, T, H = 3, 7, 16
+    g = torch.Generator().manual_seed(4)
+    y = (4.0 * torch.randn(B, T, 40 + 3 * H + 5, generator=g)).to(dt).to(dev)
+    bl, gl, ul = y[..., 40:40 + H], y[..., 40 + H:40 + 2 * H], y[..., 40 + 2 * H:40 + 3 * H]
+    out = [torch.empty(B, T, H, device=dev) for _ in range(3)]
+    _abi.check(_abi.lib().sgsa_layer_gates(_abi.dtype_code(dt), B * T, H, _abi.ptr(bl), bl.stride(-2),
+                                           *(_abi.ptr(o) for o in out), _abi.stream_of(y)))
+    torch.cuda.synchronize()
+    want = (torch.sigmoid(bl.float()).clamp_min(1e-4), torch.sigmoid(gl.float()), ul.float())
+    for name, o, w in zip(("beta", "gamma", "budget"), out, want):
+        torch.testing.assert_close(o, w, atol=1e-6, rtol=1e-5, msg=name)
