@@ -197,6 +197,16 @@ int sgsa_block_retrieve(int dtype, int B, int T, int H, int D, int top_k, int bl
 int sgsa_rms_norm(int dtype, int weight_f32, long rows, int C, const void* x, const void* weight, float eps, void* y,
                   void* stream);
 
+/* Rotary embedding of a dense attention layer's q and k (rotate-half form,
+ * modelings/hybrid_dense_delta_topk.py:140-150), in x's dtype with a rounding
+ * after each product and the sum (torch's elementwise semantics).  Row (b, t)
+ * of the projection output starts at qk + (b*T + t) * row_stride: q's Hq heads
+ * of D, then k's Hk heads.  cos_table / sin_table [table_len, D] fp32, rows
+ * pos0 .. pos0+T-1 used.  q_out [B,Hq,T,D], k_out [B,Hk,T,D] contiguous. */
+int sgsa_rope_qk(int dtype, int B, int T, int Hq, int Hk, int D, int pos0, int table_len, const void* qk,
+                 long row_stride, const float* cos_table, const float* sin_table, void* q_out, void* k_out,
+                 void* stream);
+
 /* The SGSA layer's gates from its gate projections' logits (SGSAStateLayer,
  * modelings/modeling_sgsa.py:543-544 and the budget logits): beta = max(sigmoid(b), 1e-4),
  * gamma = sigmoid(g), budget = u, as fp32 [rows, H].  Row r's logits start at

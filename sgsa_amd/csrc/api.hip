@@ -487,6 +487,22 @@ int sgsa_rms_norm(int dtype, int weight_f32, long rows, int C, const void* x, co
                     "sgsa_rms_norm");
 }
 
+int sgsa_rope_qk(int dtype, int B, int T, int Hq, int Hk, int D, int pos0, int table_len, const void* qk,
+                 long row_stride, const float* cos_table, const float* sin_table, void* q_out, void* k_out,
+                 void* stream) {
+  if (int s = check_dtype(dtype)) return s;
+  if (B <= 0 || T < 0 || Hq <= 0 || Hk <= 0 || D <= 0 || D % 2 != 0)
+    return fail(SGSA_ERR_INVALID_ARG, "B=%d T=%d Hq=%d Hk=%d D=%d (D even)", B, T, Hq, Hk, D);
+  if (pos0 < 0 || (long)pos0 + T > table_len) return fail(SGSA_ERR_INVALID_ARG, "positions [%d, %d) outside the %d-row tables", pos0, pos0 + T, table_len);
+  if (row_stride < (long)(Hq + Hk) * D) return fail(SGSA_ERR_INVALID_ARG, "row_stride=%ld < (Hq+Hk)*D", row_stride);
+  if ((long)B * T * (Hq + Hk) * D > 0x7fffffffL * 256L) return fail(SGSA_ERR_UNSUPPORTED, "too many elements");
+  if (T == 0) return SGSA_OK;
+  REQUIRE(qk); REQUIRE(cos_table); REQUIRE(sin_table); REQUIRE(q_out); REQUIRE(k_out);
+  return hip_status(sgsa::launch_rope_qk(dtype, qk, row_stride, B, T, Hq, Hk, D, pos0, cos_table, sin_table, q_out,
+                                         k_out, (hipStream_t)stream),
+                    "sgsa_rope_qk");
+}
+
 int sgsa_layer_gates(int dtype, long rows, int H, const void* logits, long row_stride, float* beta, float* gamma,
                      float* budget, void* stream) {
   if (int s = check_dtype(dtype)) return s;

@@ -5,7 +5,12 @@
 //            dtype (torch: cast, square, mean, add, rsqrt, two products, cast);
 //   gates    beta = max(sigmoid(b), 1e-4), gamma = sigmoid(g), budget = u in
 //            fp32 from the three H-wide logit groups of a projection row
-//            (torch: three casts, two sigmoids, a clamp).
+//            (torch: three casts, two sigmoids, a clamp);
+//   RoPE     q and k of a dense layer rotated (rotate-half form) straight from
+//            the fused projection row into [B, heads, T, D], rounding to x's
+//            dtype after each product and the sum as torch's elementwise ops do
+//            (torch: a negation, a concatenation, two casts, two products and a
+//            sum per tensor, then the transposing copies).
 #include "common.h"
 #include "kernels.h"
 
@@ -54,6 +59,50 @@ hipError_t launch_gates(int dtype, const void* src, long stride, long rows, int 
   const dim3 grid((unsigned)((rows * H + 255) / 256));
   if (dtype == DT_F32) gates_kernel<float><<<grid, 256, 0, st>>>((const float*)src, stride, rows, H, beta, gamma, budget);
   else gates_kernel<bf16_t><<<grid, 256, 0, st>>>((const bf16_t*)src, stride, rows, H, beta, gamma, budget);
+  return hipGetLastError();
+}
+
+// One thread per output element.  Row (b, t) of the projection output starts at
+// src + (b T + t) stride: q's Hq heads of D, then k's Hk heads.
+__device__ __forceinline__ float round_to(float v, float) { return v; }
+__device__ __forceinline__ float round_to(float v, bf16_t) { return bf16_to_f32(f32_to_bf16(v)); }
+
+template <typename X>
+__global__ __launch_bounds__(256) void rope_qk_kernel(const X* __restrict__ src, long stride, int B, int T, int Hq,
+                                                      int Hk, int D, int pos0, const float* __restrict__ cosv,
+                                                      const float* __restrict__ sinv, X* __restrict__ qo,
+                                                      X* __restrict__ ko) {
+#pragma clang fp contract(off)
+  const long n = (long)B * T * (Hq + Hk) * D;
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const int d = (int)(i % D);
+  const long r = i / D;
+  const int hh = (int)(r % (Hq + Hk));
+  const long bt = r / (Hq + Hk);
+  const int t = (int)(bt % T), b = (int)(bt / T);
+  const X* xr = src + bt * stride + (long)hh * D;
+  const int half = D / 2;
+  const float x = ld(xr, d);
+  const float xr_ = d < half ? -ld(xr, d + half) : ld(xr, d - half);
+  const X tag{};
+  const float c = round_to(cosv[(long)(pos0 + t) * D + d], tag);
+  const float s = round_to(sinv[(long)(pos0 + t) * D + d], tag);
+  const float y = round_to(round_to(x * c, tag) + round_to(xr_ * s, tag), tag);
+  if (hh < Hq) st(qo, (((long)b * Hq + hh) * T + t) * D + d, y);
+  else st(ko, (((long)b * Hk + (hh - Hq)) * T + t) * D + d, y);
+}
+
+hipError_t launch_rope_qk(int dtype, const void* src, long stride, int B, int T, int Hq, int Hk, int D, int pos0,
+                          const float* cosv, const float* sinv, void* qo, void* ko, hipStream_t st) {
+  const long n = (long)B * T * (Hq + Hk) * D;
+  const dim3 grid((unsigned)((n + 255) / 256));
+  if (dtype == DT_F32)
+    rope_qk_kernel<float><<<grid, 256, 0, st>>>((const float*)src, stride, B, T, Hq, Hk, D, pos0, cosv, sinv,
+                                                (float*)qo, (float*)ko);
+  else
+    rope_qk_kernel<bf16_t><<<grid, 256, 0, st>>>((const bf16_t*)src, stride, B, T, Hq, Hk, D, pos0, cosv, sinv,
+                                                 (bf16_t*)qo, (bf16_t*)ko);
   return hipGetLastError();
 }
 

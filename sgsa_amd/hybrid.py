@@ -39,6 +39,7 @@ import torch.nn.functional as F
 
 from .decode import sgsa_decode_step
 from .layer import LayerWorkspace, sgsa_layer_forward
+from . import _abi
 from .model import GatedMLP, RMSNorm, SGSABlock, SGSAConfig, fused_linear
 
 Tensor = torch.Tensor
@@ -161,11 +162,21 @@ class DenseGQABlock(nn.Module):
         B, T, C = h.shape
         n = self.input_norm(h)
         q, k, v = fused_linear(self, n, ("q_proj", "k_proj", "v_proj"))
-        q = q.reshape(B, T, self.H, self.D).transpose(1, 2)
-        k = k.reshape(B, T, self.Hkv, self.D).transpose(1, 2)
         v = v.reshape(B, T, self.Hkv, self.D).transpose(1, 2)
-        cos, sin = rope[0][pos0:pos0 + T], rope[1][pos0:pos0 + T]
-        q, k = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
+        if torch.is_grad_enabled():
+            q = q.reshape(B, T, self.H, self.D).transpose(1, 2)
+            k = k.reshape(B, T, self.Hkv, self.D).transpose(1, 2)
+            cos, sin = rope[0][pos0:pos0 + T], rope[1][pos0:pos0 + T]
+            q, k = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
+        else:
+            # q and k are adjacent groups of one projection row: one launch rotates both into [B, heads, T, D]
+            qs = q
+            q = torch.empty(B, self.H, T, self.D, device=h.device, dtype=h.dtype)
+            k = torch.empty(B, self.Hkv, T, self.D, device=h.device, dtype=h.dtype)
+            cos_t, sin_t = rope[0].float().contiguous(), rope[1].float().contiguous()
+            _abi.check(_abi.lib().sgsa_rope_qk(_abi.dtype_code(h.dtype), B, T, self.H, self.Hkv, self.D, pos0,
+                                               cos_t.shape[0], _abi.ptr(qs), qs.stride(-2), _abi.ptr(cos_t),
+                                               _abi.ptr(sin_t), _abi.ptr(q), _abi.ptr(k), _abi.stream_of(qs)))
         cache["k"][:, :, pos0:pos0 + T] = k
         cache["v"][:, :, pos0:pos0 + T] = v
         att = gqa_attention(q, cache["k"][:, :, :pos0 + T], cache["v"][:, :, :pos0 + T], pos0)

@@ -51,3 +51,25 @@ def test_layer_gates_match_torch(dev, dt):
     want = (torch.sigmoid(bl.float()).clamp_min(1e-4), torch.sigmoid(gl.float()), ul.float())
     for name, o, w in zip(("beta", "gamma", "budget"), out, want):
         torch.testing.assert_close(o, w, atol=1e-6, rtol=1e-5, msg=name)
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("T,pos0", [(1, 40), (9, 0), (300, 17)])
+def test_rope_qk_equals_torch_rope(dev, dt, T, pos0):
+    # the fused projection row [q (Hq heads) | k (Hk heads) | v ...]; the kernel equals apply_rope bit for bit
+    from sgsa_amd import _abi
+    from sgsa_amd.hybrid import apply_rope, rope_tables
+    B, Hq, Hk, D = 2, 8, 2, 64
+    g = torch.Generator().manual_seed(T)
+    y = torch.randn(B, T, (Hq + 2 * Hk) * D, generator=g).to(dt).to(dev)
+    cos, sin = rope_tables(pos0 + T + 5, D, 10000.0, dev)
+    q = torch.empty(B, Hq, T, D, device=dev, dtype=dt)
+    k = torch.empty(B, Hk, T, D, device=dev, dtype=dt)
+    _abi.check(_abi.lib().sgsa_rope_qk(_abi.dtype_code(dt), B, T, Hq, Hk, D, pos0, cos.shape[0], _abi.ptr(y),
+                                       y.stride(-2), _abi.ptr(cos), _abi.ptr(sin), _abi.ptr(q), _abi.ptr(k),
+                                       _abi.stream_of(y)))
+    qr = y[..., :Hq * D].reshape(B, T, Hq, D).transpose(1, 2)
+    kr = y[..., Hq * D:(Hq + Hk) * D].reshape(B, T, Hk, D).transpose(1, 2)
+    c, s = cos[pos0:pos0 + T], sin[pos0:pos0 + T]
+    torch.cuda.synchronize()
+    assert torch.equal(q, apply_rope(qr, c, s)) and torch.equal(k, apply_rope(kr, c, s))
