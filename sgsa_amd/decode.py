@@ -20,6 +20,7 @@ candidates were selected are not among them.
 from __future__ import annotations
 
 import ctypes
+import functools
 import math
 from typing import Optional, Tuple
 
@@ -31,6 +32,14 @@ from .recurrent import fused_recurrent_sgsa
 Tensor = torch.Tensor
 
 _WRITE_MODES = {"direct": 0, "residual": 1}
+
+
+@functools.lru_cache(maxsize=256)
+def _workspace_size(fn: str, *args: int) -> int:
+    """Bytes from one of the library's workspace-size queries; they depend on the shapes only."""
+    n = ctypes.c_size_t()
+    _abi.check(getattr(_abi.lib(), fn)(*args, ctypes.byref(n)))
+    return n.value
 
 
 def sgsa_decode_step(
@@ -90,12 +99,11 @@ def sgsa_decode_step(
         sc = torch.empty(B, H, 1, kk, device=dev, dtype=torch.float32)
         top2 = torch.empty(B, H, 1, 2, device=dev, dtype=torch.float32)
         cnt = torch.empty(B, H, 1, device=dev, dtype=torch.int32)
-        nb = ctypes.c_size_t()
-        _abi.check(L.sgsa_score_topk_fast_workspace_size(_abi.dtype_code(dt), B, 1, Tbuf, H, D, ctypes.byref(nb)))
-        tws = torch.empty(nb.value, device=dev, dtype=torch.uint8)
+        nb = _workspace_size("sgsa_score_topk_fast_workspace_size", _abi.dtype_code(dt), B, 1, Tbuf, H, D)
+        tws = torch.empty(nb, device=dev, dtype=torch.uint8)
         _abi.check(L.sgsa_score_topk(_abi.dtype_code(dt), B, 1, Tbuf, H, D, kk, 1, Tc - 1, math.sqrt(D), 0,
                                      _abi.ptr(rc), _abi.ptr(kc), _abi.ptr(idx), _abi.ptr(sc), _abi.ptr(top2),
-                                     _abi.ptr(cnt), None, 0, _abi.ptr(tws), nb.value, _abi.stream_of(rc)))
+                                     _abi.ptr(cnt), None, 0, _abi.ptr(tws), nb, _abi.stream_of(rc)))
     else:
         # 1'. the reused candidates, re-scored for the new query; the gather tracks
         # the row maximum and top-2 itself (top2 = NULL)
@@ -115,14 +123,13 @@ def sgsa_decode_step(
     vh = torch.empty_like(wk)
     al = torch.empty(B, 1, H, device=dev, dtype=torch.float32)
     bud = budget_logits.float().contiguous()
-    gn = ctypes.c_size_t()
-    _abi.check(L.sgsa_sparse_gather_workspace_size(B, 1, H, D, kk, ctypes.byref(gn)))
-    gws = torch.empty(gn.value, device=dev, dtype=torch.uint8)
+    gn = _workspace_size("sgsa_sparse_gather_workspace_size", B, 1, H, D, kk)
+    gws = torch.empty(gn, device=dev, dtype=torch.uint8)
     _abi.check(L.sgsa_sparse_gather(
         _abi.dtype_code(dt), B, 1, Tbuf, H, D, kk, Tc - 1, _abi.ptr(kc), _abi.ptr(vc), _abi.ptr(kn), _abi.ptr(idx),
         _abi.ptr(sc), _abi.ptr(top2), _abi.ptr(cnt), _abi.ptr(bud), mode, float(alpha_max), float(tau_c), 64, 8,
         _abi.ptr(wk if mode == 0 else None), _abi.ptr(vh), _abi.ptr(wk if mode == 1 else None), _abi.ptr(al),
-        None, None, _abi.ptr(gws), gn.value, _abi.stream_of(kc)))
+        None, None, _abi.ptr(gws), gn, _abi.stream_of(kc)))
     # 3. the recurrent update for this token
     o, st = fused_recurrent_sgsa(q, k, v, beta, gamma, wk, vh, al, state, output_final_state=True)
     return (o, st, (idx, cnt)) if return_candidates else (o, st)
