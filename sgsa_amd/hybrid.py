@@ -101,8 +101,8 @@ def apply_rope(x: Tensor, cos: Tensor, sin: Tensor) -> Tensor:
 
 def gqa_attention(q: Tensor, k: Tensor, v: Tensor, pos0: int, block: int = 1024) -> Tensor:
     """Causal attention: q [B, H, Tq, D] at positions pos0 .., k / v [B, Hkv, Tk, D]
-    with Tk >= pos0 + Tq.  Scores in q's dtype, softmax in fp32, probabilities cast
-    back (:178-192).  Query blocks of ``block`` rows read only the keys they may see.
+    with Tk >= pos0 + Tq.  Scores and their 1/sqrt(D) scaling in q's dtype, softmax in
+    fp32, probabilities cast back (:178-192).  Query blocks of ``block`` rows read only the keys they may see.
     Long query blocks (prefill) form Q K^T with a contiguous copy of the block's K^T
     and a softmax over the last dimension; short ones (decode) form K Q^T, which
     reads the cache in place."""
@@ -119,7 +119,7 @@ def gqa_attention(q: Tensor, k: Tensor, v: Tensor, pos0: int, block: int = 1024)
             kend = pos0 + r1
             qb = qg[:, :, :, r0:r1].reshape(B, Hkv, G * n, D)
             kt = k[:, :, :kend].transpose(-1, -2).contiguous()                                  # [B,Hkv,D,kend]
-            s = torch.matmul(qb, kt).float() * (1.0 / math.sqrt(D))                             # [B,Hkv,G*n,kend]
+            s = (torch.matmul(qb, kt) * (1.0 / math.sqrt(D))).float()                           # [B,Hkv,G*n,kend]
             qpos = (pos0 + r0 + torch.arange(n, device=q.device)).repeat(G)
             s = s.masked_fill(kpos[None, :kend] > qpos[:, None], float("-inf"))
             p = torch.softmax(s, dim=-1).to(q.dtype)
@@ -131,7 +131,7 @@ def gqa_attention(q: Tensor, k: Tensor, v: Tensor, pos0: int, block: int = 1024)
         n = r1 - r0
         kend = pos0 + r1
         qb = qg[:, :, :, r0:r1].reshape(B, Hkv, G * n, D).transpose(-1, -2).contiguous()   # [B,Hkv,D,G*n]
-        s = torch.matmul(k[:, :, :kend], qb).float() * (1.0 / math.sqrt(D))               # [B,Hkv,kend,G*n]
+        s = (torch.matmul(k[:, :, :kend], qb) * (1.0 / math.sqrt(D))).float()             # [B,Hkv,kend,G*n]
         qpos = (pos0 + r0 + torch.arange(n, device=q.device)).repeat(G)                    # column -> position
         s = s.masked_fill(kpos[:kend, None] > qpos[None, :], float("-inf"))
         p = torch.softmax(s, dim=-2).to(q.dtype).transpose(-1, -2).contiguous()             # [B,Hkv,G*n,kend]

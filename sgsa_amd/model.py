@@ -68,7 +68,8 @@ class SGSAConfig:
 
 class RMSNorm(nn.Module):
     """x * rsqrt(mean(x^2) + eps) * weight, evaluated in fp32 and stored in x's dtype, in one
-    HIP launch (sgsa_rms_norm; hybrid_dense_delta_topk.py:94-103)."""
+    HIP launch (sgsa_rms_norm; hybrid_dense_delta_topk.py:94-103); under autograd, the same
+    arithmetic as torch ops so that gradients flow."""
 
     def __init__(self, hidden_size: int, eps: float) -> None:
         super().__init__()
@@ -78,6 +79,12 @@ class RMSNorm(nn.Module):
     def forward(self, x: Tensor) -> Tensor:
         if not x.is_cuda:
             raise ValueError("RMSNorm: the SGSA model runs on a ROCm GPU; got a CPU tensor")
+        if torch.is_grad_enabled() and (x.requires_grad or self.weight.requires_grad):
+            # Under autograd: the same fp32 arithmetic as differentiable torch ops, so
+            # gradients reach x and the norm weight (the HIP launch has no backward).
+            xf = x.float()
+            y = xf * torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + self.eps) * self.weight.float()
+            return y.to(x.dtype)
         xc = x.contiguous()
         C = xc.shape[-1]
         w = self.weight

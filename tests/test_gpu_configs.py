@@ -17,6 +17,7 @@ import pytest
 import torch
 
 from oracle import sgsa_oracle as O
+from tolerance import close, scalar_close
 
 pytestmark = pytest.mark.gpu
 
@@ -93,3 +94,146 @@ def test_config3_tile_lists_on_sampled_rows(dev):
         assert got == want, f"head {h} row {r}: {len(set(got) ^ set(want))} keys differ"
         m = torch.topk(dump, 2).values   # every sampled row has at least two keys
         assert torch.equal(top2[0, h, r].cpu(), m), f"head {h} row {r}: top-2"
+
+
+# ---------------------------------------------------------------------------
+# Config 3 through the layer path, and the threshold path past 65535 keys
+# ---------------------------------------------------------------------------
+
+def _oracle_row_on_scores(s, kf, vf, bud, r, top_k, write_mode="direct"):
+    """The oracle's retrieval of query row r of one head, given that row's causal
+    fp32 scores s [r+1]: masked_topk (modeling_sgsa.py:144-165), the renormalised
+    softmax weights and weighted sums of :126-134, retrieval_diagnostics
+    (:361-405), write_key and compute_alpha (:546-551, :497-504).  kf, vf [T, D]
+    fp32 rows of the head; bud the row's budget logit.  Returns (write key [D],
+    v_hat [D], alpha)."""
+    T = kf.shape[0]
+    kk = min(top_k, T)
+    full = torch.zeros(T)
+    full[:r + 1] = s
+    valid = (torch.arange(T) <= r).view(1, 1, 1, T)
+    vals, idx, ok = O.masked_topk(full.view(1, 1, 1, T), valid, kk)
+    w = torch.softmax(vals.float(), dim=-1) * ok.float()
+    w = w / w.sum(-1, keepdim=True).clamp_min(1e-6)
+    k_hat = (w[0, 0, 0, :, None] * kf[idx[0, 0, 0]]).sum(0)
+    v_hat = (w[0, 0, 0, :, None] * vf[idx[0, 0, 0]]).sum(0)
+    diag = O.retrieval_diagnostics(vals, w, idx, k_hat.view(1, 1, 1, -1), kf[r].view(1, 1, 1, -1), row_offset=r)
+    wk = O.write_key(k_hat.view(1, 1, 1, -1), kf[r].view(1, 1, 1, -1), write_mode)
+    al = O.compute_alpha(diag["concentration"], diag["novelty"], torch.tensor(bud).view(1, 1, 1), wk,
+                         v_hat.view(1, 1, 1, -1))
+    return wk.view(-1), v_hat, al.item()
+
+
+def _check_cut(thr, dump_row, h, r, top_k):
+    th = thr[0, h, r, 0:1].contiguous().view(torch.float32)
+    cut = int(thr[0, h, r, 1])
+    j = torch.arange(r + 1)
+    sel = ((dump_row > th) | ((dump_row == th) & (j <= cut))).nonzero()[:, 0]
+    _, want = O.topk_lowest_index(dump_row[None], min(top_k, r + 1))
+    assert torch.equal(sel, want[0].sort().values), \
+        f"head {h} row {r}: {len(set(sel.tolist()) ^ set(want[0].tolist()))} keys differ"
+    return sel
+
+
+# Config 3: 1% of the key rows x8.  The heavy tail scales the retrieval key
+# operand only (make_inputs' k_ret); the state update keeps the unit-norm keys.
+C3_ROWS = [(0, 0), (0, 65535), (1, 2047), (2, 2048), (3, 4095), (4, 16384), (5, 30001), (6, 32768),
+           (7, 40000), (8, 50000), (9, 65000), (10, 65534), (11, 12345), (12, 2049), (13, 60000), (14, 100),
+           (15, 65535)]
+
+
+@pytest.fixture(scope="module")
+def config3(dev):
+    B, T, H, D, k = 1, 65536, 16, 128, 2048
+    x = O.make_inputs(B, T, H, D, dtype=torch.bfloat16, seed=0, heavy_tail=True)
+    g = {n: x[n].to(dev) for n in ("q", "k", "k_ret", "v", "beta", "gamma", "budget")}
+    print(f"config 3 layer path B={B} T={T} H={H} D={D} k={k} (threshold K1 past 65535 keys)", flush=True)
+    wk, vh, al = sgsa_amd.sgsa_layer_retrieve(g["q"], g["k_ret"], g["v"], g["budget"], k)
+    thr, t2, cnt = sgsa_amd.score_topk_thresholds(g["q"], g["k_ret"], k)
+    o, st = sgsa_amd.chunk_sgsa(g["q"], g["k"], g["v"], g["beta"], g["gamma"], wk, vh, al, output_final_state=True)
+    torch.cuda.synchronize()
+    return {"x": x, "g": g, "k": k, "wk": wk, "vh": vh, "al": al, "thr": thr, "t2": t2, "cnt": cnt, "o": o, "st": st}
+
+
+def test_config3_layer_counts_and_cuts(config3):
+    c = config3
+    g, k = c["g"], c["k"]
+    T = g["q"].shape[1]
+    t = torch.arange(T, device=c["cnt"].device)
+    assert torch.equal(c["cnt"], torch.clamp(t + 1, max=k).int().expand_as(c["cnt"])), "counts"
+    thr = c["thr"].cpu()
+    for h, r in C3_ROWS:
+        dump = sgsa_amd.score_dump(g["q"], g["k_ret"], r, 1)[0, h, 0, :r + 1].cpu()
+        _check_cut(thr, dump, h, r, k)
+
+
+def test_config3_layer_rows_match_oracle(config3):
+    c = config3
+    x, k = c["x"], c["k"]
+    for h, r in C3_ROWS:
+        sl = lambda t: t[:, :, h:h + 1].contiguous()
+        ret = O.token_topk_retrieval(sl(x["q_f32"]), sl(x["k_ret_f32"]), sl(x["v_f32"]), k, rows=(r, r + 1))
+        wk = O.write_key(ret["k_hat"], sl(x["k_ret_f32"])[:, r:r + 1], "direct")
+        al = O.compute_alpha(ret["diagnostics"]["concentration"], ret["diagnostics"]["novelty"],
+                             sl(x["budget"])[:, r:r + 1], wk, ret["v_hat"])
+        close(c["wk"][0, r, h], wk[0, 0, 0], 2e-2, f"write key head {h} row {r}")
+        close(c["vh"][0, r, h], ret["v_hat"][0, 0, 0], 2e-2, f"v_hat head {h} row {r}")
+        scalar_close(c["al"][0, r, h].item(), al[0, 0, 0].item(), 2e-2, 1e-4, f"alpha head {h} row {r}")
+
+
+def test_config3_state_path(config3):
+    # the chunk form equals the recurrence on the same retrieval outputs (all heads),
+    # and one head equals the fp32 oracle recurrence fed those outputs
+    c = config3
+    g, x = c["g"], c["x"]
+    o2, st2 = sgsa_amd.fused_recurrent_sgsa(g["q"], g["k"], g["v"], g["beta"], g["gamma"], c["wk"], c["vh"],
+                                            c["al"], output_final_state=True)
+    torch.cuda.synchronize()
+    close(c["o"], o2, 2e-2, "o (chunk vs recurrent kernel)")
+    close(c["st"], st2, 2e-2, "final_state (chunk vs recurrent kernel)")
+    h = 6
+    sl = lambda t: t[:, :, h:h + 1].float().cpu().contiguous()
+    ro, rs = O.naive_recurrent_sgsa(sl(x["q_f32"]), sl(x["k_f32"]), sl(x["v_f32"]), sl(x["beta"]), sl(x["gamma"]),
+                                    sl(c["wk"]), sl(c["vh"]), sl(c["al"]), None, True)
+    close(c["o"][:, :, h:h + 1], ro, 2e-2, f"o head {h} vs oracle recurrence")
+    close(c["st"][:, h:h + 1], rs, 2e-2, f"final_state head {h} vs oracle recurrence")
+
+
+@pytest.mark.parametrize("case", ["heavy_tail", "mass_ties"])
+def test_thresholds_past_65535_keys(dev, case):
+    # Tk > 65535 takes score_topk_tiles_kernel<C16=false, THR=true> and, for blocks
+    # whose threshold bin overflows, the 32-bit-counter radix fallback; mass ties
+    # (keys drawn from two rows) send every block there.
+    B, T, H, D, k = 1, 65600, 2, 128, 2048
+    if case == "heavy_tail":
+        x = O.make_inputs(B, T, H, D, dtype=torch.bfloat16, seed=5, heavy_tail=True)
+        q, kr, v, bud = x["q"], x["k_ret"], x["v"], x["budget"]
+    else:
+        gen = torch.Generator().manual_seed(6)
+        base = torch.randn(2, H, D, generator=gen)
+        kr = base[torch.randint(0, 2, (T,), generator=gen)][None].to(torch.bfloat16)
+        q = torch.randn(B, T, H, D, generator=gen).to(torch.bfloat16)
+        v = torch.randn(B, T, H, D, generator=gen).to(torch.bfloat16)
+        bud = torch.randn(B, T, H, generator=gen)
+    print(f"thresholds past 65535 keys: case {case} B={B} T={T} H={H} k={k}", flush=True)
+    qd, kd, vd, bd = q.to(dev), kr.to(dev), v.to(dev), bud.to(dev)
+    thr, t2, cnt = sgsa_amd.score_topk_thresholds(qd, kd, k)
+    idx, sc, t2r, cntr = sgsa_amd.score_topk(qd, kd, k, sorted=False, fast=False)
+    wk, vh, al = sgsa_amd.gather_thresholds(qd, kd, vd, thr, t2, cnt, bd, k)
+    torch.cuda.synchronize()
+    assert torch.equal(cnt, cntr), "counts differ from the row lists"
+    assert torch.equal(t2, t2r), "top-2 differs from the row lists"
+    thr_c = thr.cpu()
+    if case == "mass_ties":
+        assert (thr[..., 1] != 0x7fffffff).any(), "no row needed a tie cut"
+    kf, vf = kr.float(), v.float()
+    for h, r in [(0, 0), (1, 2047), (0, 2048), (1, 30000), (0, 65535), (1, 65536), (0, 65599), (1, 65599)]:
+        dump = sgsa_amd.score_dump(qd, kd, r, 1)[0, h, 0, :r + 1].cpu()
+        sel = _check_cut(thr_c, dump, h, r, k)
+        n = int(cntr[0, h, r])
+        rl = idx[0, h, r, :n].long().cpu().sort().values
+        assert torch.equal(sel, rl), f"head {h} row {r}: the cut and the row list differ"
+        wk_o, vh_o, al_o = _oracle_row_on_scores(dump, kf[0, :, h], vf[0, :, h], bud[0, r, h].item(), r, k)
+        close(wk[0, r, h], wk_o, 2e-2, f"write key head {h} row {r}")
+        close(vh[0, r, h], vh_o, 2e-2, f"v_hat head {h} row {r}")
+        scalar_close(al[0, r, h].item(), al_o, 2e-2, 1e-4, f"alpha head {h} row {r}")

@@ -68,3 +68,28 @@ def test_hybrid_bf16_greedy_generation(dev):
     assert torch.isfinite(logits.float()).all()
     assert toks.shape == (3, 6) and (toks == toks[0:1]).all(), "sequences with one prompt diverged"
     assert torch.equal(toks, toks2) and torch.equal(logits, logits2), "not deterministic"
+
+
+def test_hybrid_bf16_prompt_logits_near_the_oracle(dev):
+    # bf16 activations (dense scores scaled in bf16 as hybrid_dense_delta_topk.py:186-187
+    # does) against the fp32 oracle on the same bf16 parameters: prompt and three
+    # decode steps, relative to the largest logit.  Five stacked layers, each within
+    # the layer's bf16 2e-2, and the bf16 rounding of every stored activation.
+    from sgsa_amd.hybrid import rope_tables
+    from tolerance import close
+    cfg, m = _model(dev, torch.bfloat16, seed=4)
+    g = torch.Generator().manual_seed(5)
+    B, T, n = 2, 150, 3
+    prompt = torch.randint(0, cfg.vocab_size, (B, T), generator=g)
+    dec = torch.randint(0, cfg.vocab_size, (B, n), generator=g)
+    params = {k: v.detach().float().cpu() for k, v in m.state_dict().items()}
+    ref_p, ref_d = O.hybrid_generate(params, prompt, dec, num_layers=cfg.num_hidden_layers,
+                                     num_heads=cfg.num_attention_heads, num_kv_heads=cfg.num_kv_heads,
+                                     dense_every=cfg.dense_every, top_k=cfg.top_k,
+                                     recompute_every=cfg.topk_recompute_every)
+    rope = rope_tables(T + n, cfg.head_dim, cfg.rope_theta, dev)
+    caches = m.new_cache(B, T + n, dev, torch.bfloat16)
+    close(m.prefill(prompt.to(dev), caches, rope), ref_p, 2e-2, "bf16 prompt logits")
+    for s in range(n):
+        out = m.decode_step(dec[:, s].to(dev), T + s, s, caches, rope)
+        close(out, ref_d[:, s], 2e-2, f"bf16 decode step {s}")

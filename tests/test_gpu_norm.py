@@ -22,13 +22,38 @@ def test_rms_norm_matches_torch(dev, dt, wdt, shape):
     with torch.no_grad():
         norm.weight.copy_(1.0 + 0.1 * torch.randn(shape[-1], generator=g))
     norm = norm.to(device=dev, dtype=wdt)
-    y = norm(x.to(dev))
+    with torch.no_grad():   # the HIP launch (under autograd the torch form runs)
+        y = norm(x.to(dev))
     torch.cuda.synchronize()
     xf = x.float()
     want = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6) * norm.weight.detach().float().cpu()
     assert y.dtype == dt and y.shape == x.shape
     tol = 1e-5 if dt == torch.float32 else 2e-2
     torch.testing.assert_close(y.float().cpu(), want.to(dt).float(), atol=tol, rtol=tol)
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_rms_norm_under_autograd(dev, dt):
+    # gradients reach the input and the norm weight, and the forward equals the HIP launch
+    g = torch.Generator().manual_seed(3)
+    x = (2.0 * torch.randn(4, 9, 256, generator=g)).to(dev, dt).requires_grad_(True)
+    norm = RMSNorm(256, 1e-6).to(dev)
+    with torch.no_grad():
+        norm.weight.copy_(1.0 + 0.1 * torch.randn(256, generator=g))
+        y_hip = norm(x)
+    y = norm(x)
+    assert y.grad_fn is not None
+    torch.testing.assert_close(y.float(), y_hip.float(), atol=1e-5 if dt == torch.float32 else 2e-2, rtol=1e-5)
+    gy = torch.randn(y.shape, generator=g).to(dev, dt)
+    y.backward(gy)
+    assert norm.weight.grad is not None and x.grad is not None
+    xr = x.detach().double().cpu().requires_grad_(True)
+    wr = norm.weight.detach().double().cpu().requires_grad_(True)
+    yr = xr * torch.rsqrt(xr.pow(2).mean(-1, keepdim=True) + 1e-6) * wr
+    yr.backward(gy.double().cpu())
+    tol = 1e-4 if dt == torch.float32 else 3e-2
+    torch.testing.assert_close(norm.weight.grad.double().cpu(), wr.grad, atol=tol * wr.grad.abs().max().item(), rtol=tol)
+    torch.testing.assert_close(x.grad.double().cpu(), xr.grad, atol=tol * xr.grad.abs().max().item(), rtol=tol)
 
 
 def test_rms_norm_rejects_cpu():

@@ -1,0 +1,117 @@
+"""Parity of the layer path at BASELINE.json's headline shape, the one bench.py
+times: B=1 H=16 T=32768 d=128 top-k=2048, bf16 inputs, fp32 state, seed 0.
+
+The CPU oracle cannot run all sixteen heads, so the test combines:
+  (a) the layer is its two halves: sgsa_layer_retrieve equals the threshold
+      entry points (K1 score_thr128_kernel, K2 gather_thr_kernel) bit for bit,
+      and sgsa_layer_fwd equals chunk_sgsa fed the retrieval outputs;
+  (b) on 32 sampled (head, row) pairs -- rows t < k, t = k-1, t = k, mid
+      sequence and the last row -- K1's per-row cut applied to the fp32 scores
+      sgsa_score_dump returns selects exactly the lowest-index top-k of those
+      scores (oracle.topk_lowest_index), with the same count and top-2;
+  (c) on those rows the write key, v_hat and alpha match the oracle's
+      token_topk_retrieval / write_key / compute_alpha (modeling_sgsa.py:126-134,
+      :361-405, :497-504, :546-551) within 2e-2;
+  (d) the output and final state of two whole heads match the oracle's layer
+      (fp32 recurrence, naive.py:34-57) run on that head alone within 2e-2 of
+      the largest magnitude, and 99% of their entries above 1% of it within
+      2e-2 of their own magnitude -- heads are independent in the layer.
+"""
+
+import pytest
+import torch
+
+from oracle import sgsa_oracle as O
+from tolerance import close, scalar_close
+
+pytestmark = pytest.mark.gpu
+
+sgsa_amd = pytest.importorskip("sgsa_amd")
+
+B, T, H, D, K = 1, 32768, 16, 128, 2048
+# (head, row): two rows per head, covering t < k, the k boundary, mid sequence and the end
+PAIRS = [(0, 0), (0, 32767), (1, 1), (1, 16384), (2, 63), (2, 2047), (3, 64), (3, 2048),
+         (4, 1000), (4, 2049), (5, 2046), (5, 4095), (6, 2047), (6, 4096), (7, 2048), (7, 8191),
+         (8, 3000), (8, 12345), (9, 16383), (9, 32766), (10, 20000), (10, 24575), (11, 24576), (11, 32767),
+         (12, 5000), (12, 31000), (13, 2050), (13, 16385), (14, 10000), (14, 32700), (15, 2047), (15, 32767)]
+
+
+@pytest.fixture(scope="module")
+def ns(dev):
+    x = O.make_inputs(B, T, H, D, dtype=torch.bfloat16, seed=0)
+    g = {n: x[n].to(dev) for n in ("q", "k", "v", "beta", "gamma", "budget")}
+    print(f"north-star layer B={B} T={T} H={H} D={D} k={K}", flush=True)
+    o, st = sgsa_amd.sgsa_layer_forward(g["q"], g["k"], g["v"], g["q"], g["beta"], g["gamma"], g["budget"], K)
+    wk, vh, al = sgsa_amd.sgsa_layer_retrieve(g["q"], g["k"], g["v"], g["budget"], K)
+    thr, t2, cnt = sgsa_amd.score_topk_thresholds(g["q"], g["k"], K)
+    torch.cuda.synchronize()
+    return {"x": x, "g": g, "o": o, "st": st, "wk": wk, "vh": vh, "al": al, "thr": thr, "t2": t2, "cnt": cnt}
+
+
+def test_layer_is_its_two_halves(ns):
+    g = ns["g"]
+    wk, vh, al = sgsa_amd.gather_thresholds(g["q"], g["k"], g["v"], ns["thr"], ns["t2"], ns["cnt"], g["budget"], K)
+    o2, st2 = sgsa_amd.chunk_sgsa(g["q"], g["k"], g["v"], g["beta"], g["gamma"], ns["wk"], ns["vh"], ns["al"],
+                                  output_final_state=True)
+    torch.cuda.synchronize()
+    assert torch.equal(wk, ns["wk"]) and torch.equal(vh, ns["vh"]) and torch.equal(al, ns["al"]), \
+        "sgsa_layer_retrieve differs from the threshold entry points"
+    assert torch.equal(o2, ns["o"]), "sgsa_layer_fwd output differs from chunk_sgsa on its retrieval outputs"
+    assert torch.equal(st2.float(), ns["st"]), "final states differ"
+
+
+def test_counts_on_every_row(ns):
+    t = torch.arange(T, device=ns["cnt"].device)
+    assert torch.equal(ns["cnt"], torch.clamp(t + 1, max=K).int().expand(B, H, T))
+
+
+def test_cut_selects_the_lowest_index_topk_of_the_dumped_scores(ns):
+    g = ns["g"]
+    thr, t2 = ns["thr"].cpu(), ns["t2"].cpu()
+    for r in sorted({r for _, r in PAIRS}):
+        dump = sgsa_amd.score_dump(g["q"], g["k"], r, 1)[0, :, 0, :r + 1].cpu()   # [H, r+1] fp32
+        for h in [h for h, rr in PAIRS if rr == r]:
+            s = dump[h]
+            th = thr[0, h, r, 0:1].contiguous().view(torch.float32)
+            cut = int(thr[0, h, r, 1])
+            j = torch.arange(r + 1)
+            sel = ((s > th) | ((s == th) & (j <= cut))).nonzero()[:, 0]
+            kq = min(K, r + 1)
+            _, want = O.topk_lowest_index(s[None], kq)
+            assert torch.equal(sel, want[0].sort().values), \
+                f"head {h} row {r}: {len(set(sel.tolist()) ^ set(want[0].tolist()))} keys differ"
+            valid = torch.ones(1, 1, 1, r + 1, dtype=torch.bool)
+            ov, _, _ = O.masked_topk(s.view(1, 1, 1, -1), valid, kq)
+            assert t2[0, h, r, 0] == ov[0, 0, 0, 0], f"head {h} row {r}: top-1"
+            if kq >= 2:
+                assert t2[0, h, r, 1] == ov[0, 0, 0, 1], f"head {h} row {r}: top-2"
+
+
+@pytest.mark.parametrize("write_mode", ["direct"])
+def test_sampled_rows_match_oracle_retrieval(ns, write_mode):
+    x = ns["x"]
+    for h, r in PAIRS:
+        sl = lambda t: t[:, :, h:h + 1].contiguous()
+        ret = O.token_topk_retrieval(sl(x["q_f32"]), sl(x["k_f32"]), sl(x["v_f32"]), K, rows=(r, r + 1))
+        wk = O.write_key(ret["k_hat"], sl(x["k_f32"])[:, r:r + 1], write_mode)
+        al = O.compute_alpha(ret["diagnostics"]["concentration"], ret["diagnostics"]["novelty"],
+                             sl(x["budget"])[:, r:r + 1], wk, ret["v_hat"])
+        for name, got, want in (("write key", ns["wk"][0, r, h], wk[0, 0, 0]),
+                                ("v_hat", ns["vh"][0, r, h], ret["v_hat"][0, 0, 0])):
+            close(got, want, 2e-2, f"{name} head {h} row {r}")
+        scalar_close(ns["al"][0, r, h].item(), al[0, 0, 0].item(), 2e-2, 1e-4, f"alpha head {h} row {r}")
+
+
+@pytest.mark.parametrize("h", [0, 13])
+def test_whole_head_matches_oracle_layer(ns, h):
+    x = ns["x"]
+    sl = lambda t: t[:, :, h:h + 1].contiguous()
+    print(f"oracle layer on head {h} (T={T})", flush=True)
+    ref = O.sgsa_layer_forward(sl(x["q_f32"]), sl(x["k_f32"]), sl(x["v_f32"]), sl(x["q_f32"]), sl(x["beta"]),
+                               sl(x["gamma"]), sl(x["budget"]), K)
+    # elementwise as well: 99% of the entries above 1% of the largest within 2e-2 of their own magnitude
+    close(ns["o"][:, :, h:h + 1], ref["o"], 2e-2, f"o head {h}", elem_p99=2e-2)
+    close(ns["st"][:, h:h + 1], ref["final_state"], 2e-2, f"final_state head {h}", elem_p99=2e-2)
+    close(ns["wk"][:, :, h:h + 1], ref["write_key"], 2e-2, f"write key head {h}")
+    close(ns["vh"][:, :, h:h + 1], ref["v_hat"], 2e-2, f"v_hat head {h}")
+    close(ns["al"][:, :, h:h + 1], ref["alpha"], 2e-2, f"alpha head {h}")

@@ -24,8 +24,9 @@ pytestmark = pytest.mark.gpu
 sgsa_amd = pytest.importorskip("sgsa_amd")
 
 
-def _inputs(case, dev):
-    B, T, H, D, k = 1, 2100, 2, 128, 256
+def _inputs(case, dev, big=False):
+    # big: the headline top-k (2048) at T = 8192 (ragged: T = 8100, B = 2, H = 3)
+    B, T, H, D, k = (1, 8192, 2, 128, 2048) if big else (1, 2100, 2, 128, 256)
     g = torch.Generator().manual_seed(33)
     if case == "random":
         q, kk = torch.randn(B, T, H, D, generator=g), torch.randn(B, T, H, D, generator=g)
@@ -54,7 +55,7 @@ def _inputs(case, dev):
         x = O.make_inputs(B, T, H, D, dtype=torch.float32, seed=12, heavy_tail=True, with_budget=False)
         q, kk = x["q"], x["k_ret"]
     else:   # ragged: T not a multiple of the 128-row gather block, B > 1
-        B, T, H, D, k = 2, 700, 3, 128, 100
+        B, T, H, D, k = (2, 8100, 3, 128, 2048) if big else (2, 700, 3, 128, 100)
         q, kk = torch.randn(B, T, H, D, generator=g), torch.randn(B, T, H, D, generator=g)
     v = torch.randn(B, T, H, D, generator=g)
     bud = torch.randn(B, T, H, generator=g)
@@ -63,11 +64,16 @@ def _inputs(case, dev):
 
 
 CASES = ["random", "ties", "mass_ties", "tile_burst", "heavy_tail", "ragged"]
+# (case, big): every case at its own size, and all but tile_burst (a fixed T = 500
+# construction) at top-k 2048 with T = 8192
+SIZED = [(c, False) for c in CASES] + [(c, True) for c in CASES if c != "tile_burst"]
+SIZE_IDS = [f"{c}-k2048" if big else c for c, big in SIZED]
 
 
-@pytest.mark.parametrize("case", CASES)
-def test_thresholds_select_exactly_the_row_lists(dev, case):
-    q, kk, v, _, k = _inputs(case, dev)
+@pytest.mark.parametrize("case,big", SIZED, ids=SIZE_IDS)
+def test_thresholds_select_exactly_the_row_lists(dev, case, big):
+    q, kk, v, _, k = _inputs(case, dev, big)
+    print(f"thresholds vs row lists: case {case} shape {tuple(q.shape)} k={k}", flush=True)
     B, T, H, D = q.shape
     thr, t2t, ct = sgsa_amd.score_topk_thresholds(q, kk, k)
     idx, sc, t2, cnt = sgsa_amd.score_topk(q, kk, k, sorted=False)
@@ -93,9 +99,10 @@ def test_thresholds_select_exactly_the_row_lists(dev, case):
 
 
 @pytest.mark.parametrize("write_mode", ["direct", "residual"])
-@pytest.mark.parametrize("case", CASES)
-def test_threshold_gather_equals_list_gather(dev, case, write_mode):
-    q, kk, v, bud, k = _inputs(case, dev)
+@pytest.mark.parametrize("case,big", SIZED, ids=SIZE_IDS)
+def test_threshold_gather_equals_list_gather(dev, case, big, write_mode):
+    q, kk, v, bud, k = _inputs(case, dev, big)
+    print(f"threshold gather vs list gather: case {case} shape {tuple(q.shape)} k={k} {write_mode}", flush=True)
     thr, t2t, ct = sgsa_amd.score_topk_thresholds(q, kk, k)
     wk_t, vh_t, al_t = sgsa_amd.gather_thresholds(q, kk, v, thr, t2t, ct, bud, k, write_mode=write_mode)
     lists, offs, t2l, cl = sgsa_amd.score_topk_lists(q, kk, k)
