@@ -109,6 +109,26 @@ int sgsa_score_topk(int dtype, int B, int Tq, int Tk, int H, int D, int top_k,
                     int32_t* indices, float* scores, float* top2, int32_t* counts,
                     int32_t* split, int sorted, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Scratch held by sgsa_score_topk_noalloc on each GPU it runs on (32 MiB), from
+ * its first call on that GPU until the process ends. */
+#define SGSA_NOALLOC_SCRATCH_BYTES (32u << 20)
+/* sgsa_score_topk without a workspace argument and without any device
+ * allocation.  No counterpart in the reference: it is for callers that cannot
+ * allocate -- code under HIP graph capture, tight decode/serving loops,
+ * harnesses that forbid hipMalloc.  Its workspace is a fixed per-GPU device
+ * array of SGSA_NOALLOC_SCRATCH_BYTES; it behaves as sgsa_score_topk given
+ * sgsa_score_topk_fast_workspace_size() bytes (same launches, same results)
+ * and returns SGSA_ERR_WORKSPACE when that size exceeds the array (a decode
+ * step of B*H*Tq = 128 rows over 32768 keys needs 17 MB).  Every call on one
+ * GPU shares the array: calls that overlap in time on one GPU (two streams,
+ * two host threads) race and must be serialised by the caller.  Nothing in
+ * the array needs to start at zero. */
+int sgsa_score_topk_noalloc(int dtype, int B, int Tq, int Tk, int H, int D, int top_k,
+                            int causal, int q_offset, float scale, int scale_mode,
+                            const void* q, const void* k,
+                            int32_t* indices, float* scores, float* top2, int32_t* counts,
+                            int32_t* split, int sorted, void* stream);
+
 /* Known-answer hook: writes the exact fp32 scores sgsa_score_topk selects on,
  * for query rows [row0, row0+rows), to out [B,H,rows,Tk]; keys outside the
  * causal range get -FLT_MAX. */

@@ -46,6 +46,8 @@ SIGNATURES = {
     "sgsa_score_topk_fast_workspace_size": (_I, [_I, _I, _I, _I, _I, _I, ctypes.POINTER(_SZ)]),
     "sgsa_score_topk": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _I, _F, _I, _P, _P, _P, _P, _P, _P, _P, _I, _P,
                              _SZ, _P]),
+    "sgsa_score_topk_noalloc": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _I, _F, _I, _P, _P, _P, _P, _P, _P, _P, _I,
+                                     _P]),
     "sgsa_sparse_gather_tiled": (_I, [_I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _I, _F, _F, _P, _P, _P,
                                       _P, _P]),
     "sgsa_score_dump": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _F, _I, _P, _P, _I, _I, _P, _P]),

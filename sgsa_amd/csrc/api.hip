@@ -4,6 +4,7 @@
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
+#include <mutex>
 #include <string>
 
 #include "../../include/sgsa.h"
@@ -163,25 +164,30 @@ int sgsa_score_topk_workspace_size(int B, int Tq, int H, size_t* bytes) {
   return SGSA_OK;
 }
 
-int sgsa_score_topk(int dtype, int B, int Tq, int Tk, int H, int D, int top_k, int causal, int q_offset,
-                    float scale, int scale_mode, const void* q, const void* k, int32_t* indices, float* scores,
-                    float* top2, int32_t* counts, int32_t* split, int sorted, void* workspace,
-                    size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// Argument checks of sgsa_score_topk other than the workspace.
+int score_topk_check(int dtype, int B, int Tq, int Tk, int H, int D, int top_k, int q_offset, float scale,
+                     int scale_mode, const void* q, const void* k, const int32_t* indices, const float* scores,
+                     const int32_t* counts, const int32_t* split, int sorted) {
   if (int s = validate_topk(dtype, B, Tq, Tk, H, D, top_k, scale_mode, scale)) return s;
-  REQUIRE(q); REQUIRE(k); REQUIRE(indices); REQUIRE(scores); REQUIRE(workspace);
-  const size_t need_ws = sgsa::topk_workspace_bytes(B, Tq, H);
-  if (workspace_bytes < need_ws) return fail(SGSA_ERR_WORKSPACE, "workspace %zu < %zu bytes", workspace_bytes, need_ws);
+  REQUIRE(q); REQUIRE(k); REQUIRE(indices); REQUIRE(scores);
   if (sorted && counts == nullptr) return fail(SGSA_ERR_INVALID_ARG, "sorted output needs counts");
   if (sorted && split != nullptr) return fail(SGSA_ERR_INVALID_ARG, "split describes the unsorted order; pass NULL with sorted=1");
   if (q_offset < 0) return fail(SGSA_ERR_INVALID_ARG, "q_offset must be >= 0");
   if (top_k > 4096 && sorted) return fail(SGSA_ERR_UNSUPPORTED, "sorted output supports top_k <= 4096");
-  sgsa::TopkArgs a{};
-  a.dtype = dtype; a.B = B; a.Tq = Tq; a.Tk = Tk; a.H = H; a.D = D; a.top_k = top_k;
-  a.causal = causal ? 1 : 0; a.q_offset = q_offset; a.scale = scale; a.scale_mode = scale_mode;
-  a.q = q; a.k = k; a.indices = indices; a.scores = scores; a.top2 = top2; a.counts = counts; a.split = split;
+  return SGSA_OK;
+}
+
+// The launches of sgsa_score_topk on a checked workspace: the few-row form when the
+// workspace holds its score buffer (and is 256-byte aligned), the row kernel otherwise.
+int score_topk_launch(const sgsa::TopkArgs& a0, int sorted, void* workspace, size_t workspace_bytes,
+                      hipStream_t st) {
+  sgsa::TopkArgs a = a0;
   a.workspace = workspace;
-  hipStream_t st = (hipStream_t)stream;
-  const size_t base_ws = (need_ws + 255) & ~(size_t)255;
+  const size_t base_ws = (sgsa::topk_workspace_bytes(a.B, a.Tq, a.H) + 255) & ~(size_t)255;
   const size_t rows_ws = sgsa::topk_rows_bytes(a);
   if (rows_ws > 0 && workspace_bytes >= base_ws + rows_ws && ((uintptr_t)workspace & 255u) == 0) {
     float* sbuf = reinterpret_cast<float*>(static_cast<char*>(workspace) + base_ws);
@@ -189,8 +195,89 @@ int sgsa_score_topk(int dtype, int B, int Tq, int Tk, int H, int D, int top_k, i
   } else if (int s = hip_status(sgsa::launch_score_topk(a, st), "sgsa_score_topk")) {
     return s;
   }
-  if (sorted) return hip_status(sgsa::launch_sort_rows(indices, scores, (long)B * H * Tq, top_k, counts, st), "sgsa_score_topk(sort)");
+  if (sorted)
+    return hip_status(sgsa::launch_sort_rows(a.indices, a.scores, (long)a.B * a.H * a.Tq, a.top_k, a.counts, st),
+                      "sgsa_score_topk(sort)");
   return SGSA_OK;
+}
+
+sgsa::TopkArgs score_topk_args(int dtype, int B, int Tq, int Tk, int H, int D, int top_k, int causal, int q_offset,
+                               float scale, int scale_mode, const void* q, const void* k, int32_t* indices,
+                               float* scores, float* top2, int32_t* counts, int32_t* split) {
+  sgsa::TopkArgs a{};
+  a.dtype = dtype; a.B = B; a.Tq = Tq; a.Tk = Tk; a.H = H; a.D = D; a.top_k = top_k;
+  a.causal = causal ? 1 : 0; a.q_offset = q_offset; a.scale = scale; a.scale_mode = scale_mode;
+  a.q = q; a.k = k; a.indices = indices; a.scores = scores; a.top2 = top2; a.counts = counts; a.split = split;
+  return a;
+}
+
+// ---- scratch of the allocation-free entry point ------------------------------
+// One array per GPU, held until the process ends.  Host code never passes the
+// array's name to a kernel or a copy (in host code it is a stand-in, not a device
+// address): it uses the per-device address hipGetSymbolAddress returns.
+static __device__ __align__(256) unsigned char scratch[SGSA_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's address of the scratch array, looked up once per device
+// with that device current.
+int scratch_address(void** out) {
+  int dev = -1;
+  if (int s = hip_status(hipGetDevice(&dev), "sgsa_score_topk_noalloc (hipGetDevice)")) return s;
+  if (dev < 0 || dev >= kMaxDevices) return fail(SGSA_ERR_UNSUPPORTED, "device ordinal %d beyond %d", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    if (int s = hip_status(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "sgsa_score_topk_noalloc (hipGetSymbolAddress)"))
+      return s;
+    if (p == nullptr || ((uintptr_t)p & 255u) != 0)
+      return fail(SGSA_ERR_HIP, "sgsa_score_topk_noalloc: scratch address %p is not 256-byte aligned", p);
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return SGSA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int sgsa_score_topk(int dtype, int B, int Tq, int Tk, int H, int D, int top_k, int causal, int q_offset,
+                    float scale, int scale_mode, const void* q, const void* k, int32_t* indices, float* scores,
+                    float* top2, int32_t* counts, int32_t* split, int sorted, void* workspace,
+                    size_t workspace_bytes, void* stream) {
+  if (int s = score_topk_check(dtype, B, Tq, Tk, H, D, top_k, q_offset, scale, scale_mode, q, k, indices, scores,
+                               counts, split, sorted))
+    return s;
+  REQUIRE(workspace);
+  const size_t need_ws = sgsa::topk_workspace_bytes(B, Tq, H);
+  if (workspace_bytes < need_ws) return fail(SGSA_ERR_WORKSPACE, "workspace %zu < %zu bytes", workspace_bytes, need_ws);
+  const sgsa::TopkArgs a = score_topk_args(dtype, B, Tq, Tk, H, D, top_k, causal, q_offset, scale, scale_mode, q, k,
+                                           indices, scores, top2, counts, split);
+  return score_topk_launch(a, sorted, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+int sgsa_score_topk_noalloc(int dtype, int B, int Tq, int Tk, int H, int D, int top_k, int causal, int q_offset,
+                            float scale, int scale_mode, const void* q, const void* k, int32_t* indices,
+                            float* scores, float* top2, int32_t* counts, int32_t* split, int sorted, void* stream) {
+  if (int s = score_topk_check(dtype, B, Tq, Tk, H, D, top_k, q_offset, scale, scale_mode, q, k, indices, scores,
+                               counts, split, sorted))
+    return s;
+  const sgsa::TopkArgs a = score_topk_args(dtype, B, Tq, Tk, H, D, top_k, causal, q_offset, scale, scale_mode, q, k,
+                                           indices, scores, top2, counts, split);
+  // the workspace sgsa_score_topk_fast_workspace_size asks for: the few-row form where it applies
+  const size_t base_ws = (sgsa::topk_workspace_bytes(B, Tq, H) + 255) & ~(size_t)255;
+  const size_t need = base_ws + sgsa::topk_rows_bytes(a);
+  if (need > (size_t)SGSA_NOALLOC_SCRATCH_BYTES)
+    return fail(SGSA_ERR_WORKSPACE,
+                "sgsa_score_topk_noalloc: B=%d Tq=%d Tk=%d H=%d needs %zu bytes of scratch; its fixed scratch holds "
+                "%zu (SGSA_NOALLOC_SCRATCH_BYTES); use sgsa_score_topk with a workspace", B, Tq, Tk, H, need,
+                (size_t)SGSA_NOALLOC_SCRATCH_BYTES);
+  void* ptr = nullptr;
+  if (int s = scratch_address(&ptr)) return s;
+  return score_topk_launch(a, sorted, ptr, need, (hipStream_t)stream);
 }
 
 int sgsa_score_topk_fast_workspace_size(int dtype, int B, int Tq, int Tk, int H, int D, size_t* bytes) {
