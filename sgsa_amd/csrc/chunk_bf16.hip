@@ -1,23 +1,46 @@
-// Chunked SGSA forward, bf16-input path (v_mfma_f32_16x16x32_bf16).
+// Chunked SGSA forward, bf16-input path (gfx950: v_mfma_f32_16x16x32_bf16,
+// v_mfma_f32_16x16x4_f32, ds_read_b64_tr_b16).
 //
-// Same algorithm and notation as chunk.hip (the fp32 path); the difference is
-// how each contraction maps onto bf16 MFMA without losing the fp32 state:
-//   * products of two bf16 inputs (kappa kappa^T, q kappa^T) are exact in the
-//     fp32 accumulator and use one MFMA;
-//   * an fp32 operand X (A = (I+T)^-1, the state S, the residuals R, the
-//     readout weights P) is split X = hi + lo into two bf16 planes, and
-//     X.Y = hi.Y + lo.Y (both operands fp32: hi.hi + hi.lo + lo.hi), which
-//     keeps ~16 mantissa bits;
-//   * the transition T and its blocked inverse stay in fp32 (v_mfma 16x16x4 f32).
-// Workspace planes are stored in the operand layouts the consumers read with
-// 16-byte loads (row-major W, transposed kappa / S / R).
+// Per chunk of L = 64 tokens with M = 2L virtual write samples (sample i = 2t + r:
+// r = 0 the local write k, v, beta; r = 1 the sparse write k~, v^, alpha;
+// chunk_fwd.py:49-61; without the sparse write M = L and i = t), the chunk-local
+// log-decay prefix l_t = sum_{p <= t} log max(gamma_p, 1e-6), sample keys kappa,
+// values nu and write strengths lam, and the chunk-start state S [d_k][d_v]:
 //
-// K3 chunk_intra_bf16  grid (NT, B*H)      Gram, T, (I+T)^-1, W = A D_tau kappa, U = A nu, kappa^T
-// K4 chunk_seg_bf16    grid (B*H, G, 2|1)  state pass over G segments of chunks: per-segment affine
-//    chunk_seg_scan_bf16 grid (B*H)        maps, a scan over segments, then each segment replays its
-//                                          chunks from its start state (operands of chunk c+1 are
-//                                          prefetched into registers while chunk c is processed)
-// K5 chunk_out_bf16    grid (NT, B*H)      o = D Q S + P R
+//   T_ij = 1[tau_j < tau_i] lam_j e^{l_tau_i - l_tau_j} (kappa_i . kappa_j),    A = (I + T)^-1
+//   X = kappa S,   B_i = nu_i - e^{l_tau_i} X_i,   R = A B
+//   o_t = e^{l_t} (q_t S) + sum_{tau_i <= t} lam_i e^{l_t - l_tau_i} (q_t . kappa_i) R_i
+//   S'  = e^{l_L} S + kappa^T R',   R'_i = lam_i e^{l_L - l_tau_i} R_i
+//
+// which is chunk_fwd.py:70-126 with the UT/WY inverse kept as A (R = U - W S for
+// W = A e^{l_tau} kappa and U = A nu).
+//
+// K3 chunk_inv_bf16      grid (NT, B*H)  Gram of kappa (bf16 MFMA, exact in fp32), T, and A by
+//                        blocked inversion on fp32 MFMA: each 16x16 diagonal block as the product
+//                        (I - T)(I + T^2)(I + T^4)(I + T^8) (T^16 = 0 in a block), then the
+//                        off-diagonal blocks by doubling, A_RC = -A_RR T_RC A_CC for 16-, 32- and
+//                        64-row halves.  A goes to the workspace as bf16 hi + lo planes of its
+//                        lower 16x16 tiles (36 KB per chunk), the only intermediate of the chunk.
+// K4 chunk_maps_bf16     grid (B*H, G)   the affine maps S_end = Phi S_start + P of G segments of
+//                        consecutive chunks (Phi: from I with nu = 0; P: from 0)
+//    chunk_seg_scan_bf16 grid (B*H)      the segment start states
+//    chunk_replay_bf16   grid (B*H, G)   each segment reruns its chunks from its start state and
+//                        writes the output rows; the last segment writes the final state.
+//
+// In K4 a wave owns 32 columns of the state (the value dimension).  Every product of a
+// chunk -- kappa S, A B, kappa^T R', q S, P R -- contracts over an index the wave holds
+// whole, so a wave's chain of MFMAs never waits for another wave: the accumulator tiles
+// of one product are the B operand of the next.  A 16x16x32 B operand made of two
+// accumulator tiles (rows 32s..32s+15 and 32s+16..32s+31) holds in lane (lr, lg) the k
+// rows 32s + 4lg + e and 32s + 16 + 4lg + e (e = 0..3); the A operand of such a product
+// is read in the same k order.  The shared operands of a chunk (kappa, nu and q rows, the
+// A tiles) are staged in LDS once per chunk; kappa^T operands are read from the kappa
+// rows with ds_read_b64_tr_b16.  fp32 operands (S, B, R, P, A) enter the bf16 MFMAs as
+// hi + lo bf16 pairs -- hi.Y + lo.Y against an exact bf16 Y, hi.hi + hi.lo + lo.hi
+// between two of them -- which keeps about 16 mantissa bits; the state stays fp32 in
+// registers.
+#include <type_traits>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -27,22 +50,18 @@ namespace {
 
 constexpr int L = 64;
 constexpr int DP = 128;
-constexpr int PB = DP + 8;     // bf16 LDS pitch (272 B rows)
-constexpr int PF = DP + 4;     // fp32 LDS pitch
+constexpr int PK = DP + 8;     // bf16 pitch of a staged kappa / nu / q row (272 B)
+constexpr int AP = 24;         // bf16 pitch of a staged A tile row (48 B: a tile's row reads hit distinct banks)
+constexpr int TP = 17;         // fp32 pitch of a 16x16 tile in K3
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-// Workgroup barrier that orders LDS only: each wave waits for its own LDS
-// operations, not for global loads and stores still in flight (__syncthreads
-// waits for those too, which would stall register prefetches at the barrier).
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 __device__ __forceinline__ bf16x8 as_bf8(uint4 u) { return __builtin_bit_cast(bf16x8, u); }
@@ -59,68 +78,124 @@ __device__ __forceinline__ uint4 load8(const bf16_t* row, int d0, int D, bool va
   return __builtin_bit_cast(uint4, r);
 }
 
-__device__ __forceinline__ void split8(const float (&x)[8], uint4& hi, uint4& lo) {
-  u16x8 h, l;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const uint16_t b = f32_to_bf16(x[j]);
-    h[j] = b;
-    l[j] = f32_to_bf16(x[j] - bf16_to_f32(b));
-  }
-  hi = __builtin_bit_cast(uint4, h);
-  lo = __builtin_bit_cast(uint4, l);
+// Two floats to two bf16 (round to nearest even) in one v_cvt_pk_bf16_f32; a in bits 0-15.
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, bf16x2_t));
 }
 
-__device__ __forceinline__ void split1(float x, uint16_t& hi, uint16_t& lo) {
-  hi = f32_to_bf16(x);
-  lo = f32_to_bf16(x - bf16_to_f32(hi));
+// x = hi + lo: hi the bf16 rounding of x, lo the bf16 rounding of the remainder (4 values each).
+__device__ __forceinline__ void split4(const f4& x, uint2& hi, uint2& lo) {
+  const uint32_t h0 = pack2(x[0], x[1]), h1 = pack2(x[2], x[3]);
+  hi = make_uint2(h0, h1);
+  lo = make_uint2(pack2(x[0] - __uint_as_float(h0 << 16), x[1] - __uint_as_float(h0 & 0xffff0000u)),
+                  pack2(x[2] - __uint_as_float(h1 << 16), x[3] - __uint_as_float(h1 & 0xffff0000u)));
 }
+
+__device__ __forceinline__ f4 unsplit4(uint2 hi, uint2 lo) {
+  f4 x;
+  x[0] = __uint_as_float(hi.x << 16) + __uint_as_float(lo.x << 16);
+  x[1] = __uint_as_float(hi.x & 0xffff0000u) + __uint_as_float(lo.x & 0xffff0000u);
+  x[2] = __uint_as_float(hi.y << 16) + __uint_as_float(lo.y << 16);
+  x[3] = __uint_as_float(hi.y & 0xffff0000u) + __uint_as_float(lo.y & 0xffff0000u);
+  return x;
+}
+
+// B operand from two accumulator tiles (k rows 32s + 4lg + e, then 32s + 16 + 4lg + e).
+__device__ __forceinline__ bf16x8 cat(uint2 a, uint2 b) { return as_bf8(make_uint4(a.x, a.y, b.x, b.y)); }
+
+// A operand of step s from a row-major bf16 row in LDS, in that k order.
+__device__ __forceinline__ bf16x8 rowop_p(const uint16_t* row, int s, int lg) {
+  const uint2 a = *reinterpret_cast<const uint2*>(row + 32 * s + 4 * lg);
+  const uint2 b = *reinterpret_cast<const uint2*>(row + 32 * s + 16 + 4 * lg);
+  return cat(a, b);
+}
+
+// A or B operand of step s in the MFMA's own k order (both operands read from rows).
+__device__ __forceinline__ bf16x8 rowop(const uint16_t* row, int s, int lg) {
+  return as_bf8(*reinterpret_cast<const uint4*>(row + 32 * s + 8 * lg));
+}
+
+__device__ __forceinline__ s16x4 lds_tr(const uint16_t* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(p));
+}
+
+// ds_read_b64_tr_b16: within 16 lanes, lane i receives element i % 4 of the 8 bytes
+// lane 4e + i / 4 addresses (e = 0..3).  Lane m addressing row j0 + m / 4 at column
+// d0 + 4 (m % 4) therefore hands lane i the column d0 + i of rows j0 .. j0 + 3.
+
+// e^x through v_exp_f32 (2^x): one multiply and the hardware exponential.
+__device__ __forceinline__ float fexp(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
 
 // sample i of a chunk -> (token offset, which input)
 template <bool SP> __device__ __forceinline__ int samp_t(int i) { return SP ? (i >> 1) : i; }
 template <bool SP> __device__ __forceinline__ int samp_r(int i) { return SP ? (i & 1) : 0; }
 
-}  // namespace
+__device__ __host__ constexpr int tri(int I, int J) { return I * (I + 1) / 2 + J; }
 
-struct Bf16Ws {
-  uint16_t* Whi;   // [BH,NT,M,DP]
-  uint16_t* Wlo;
-  float* U;        // [BH,NT,M,DP]
-  uint16_t* KT;    // [BH,NT,DP,M]   kappa^T
-  uint16_t* STh;   // [BH,NT,DP,DP]  chunk-start state, transposed [col][row]
-  uint16_t* STl;
-  uint16_t* RTh;   // [BH,NT,DP,M]   residuals, transposed [col][sample]
-  uint16_t* RTl;
-  float* logd;     // [BH,NT,L]
-};
+// K4 stages the kappa / nu rows of a chunk input-major: the local-write rows (tokens
+// 0..63) first, the sparse-write rows after them, shifted by 16 bytes so that the rows
+// of one sample pair sit in different banks.  Element offset of sample i's row:
+template <bool SP> __device__ __forceinline__ int krow(int i) {
+  return SP ? ((i & 1) ? (64 + (i >> 1)) * PK + 8 : (i >> 1) * PK) : i * PK;
+}
+template <int M> constexpr int krows_elems() { return M * PK + (M == 2 * L ? 8 : 0); }
+
+// kappa^T as the A operand of step s (rows: dims 16r .. 16r + 15; k: samples in the
+// accumulator k order): two transposing reads of the staged kappa rows.
+template <bool SP>
+__device__ __forceinline__ bf16x8 kapT_op(const uint16_t* kap, int r, int s, int lr, int lg) {
+  const int d = 16 * r + 4 * (lr & 3);
+  const s16x4 a = lds_tr(kap + krow<SP>(32 * s + 4 * lg + (lr >> 2)) + d);
+  const s16x4 b = lds_tr(kap + krow<SP>(32 * s + 16 + 4 * lg + (lr >> 2)) + d);
+  return __builtin_bit_cast(bf16x8, __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
 
 // ---------------------------------------------------------------------------
 // K3
 // ---------------------------------------------------------------------------
-template <bool SP>
-__global__ __launch_bounds__(256) void chunk_intra_bf16(
-    const bf16_t* __restrict__ k, const bf16_t* __restrict__ v, const bf16_t* __restrict__ sk,
-    const bf16_t* __restrict__ sv, const float* __restrict__ beta, const float* __restrict__ alpha,
-    const float* __restrict__ gamma, int T, int H, int D, int NT, Bf16Ws ws) {
-  constexpr int M = SP ? 2 * L : L;
+
+// Z = X Y for 16x16 fp32 tiles (row-major, pitch TP): four v_mfma_f32_16x16x4_f32 (lane l
+// supplies X[l%16][4s + l/16] and Y[4s + l/16][l%16]); result in the accumulator layout.
+__device__ __forceinline__ f4 mm16(const float* X, const float* Y, f4 acc, int lr, int lg) {
+#pragma unroll
+  for (int s = 0; s < 4; ++s) acc = mma_f32(X[lr * TP + 4 * s + lg], Y[(4 * s + lg) * TP + lr], acc);
+  return acc;
+}
+
+__device__ __forceinline__ void st16(float* Z, const f4& v, int lr, int lg) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) Z[(4 * lg + e) * TP + lr] = v[e];
+}
+
+__device__ __forceinline__ f4 ld16(const float* Z, int lr, int lg) {
+  f4 v;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = Z[(4 * lg + e) * TP + lr];
+  return v;
+}
+
+template <int M, bool FULL>
+__global__ __launch_bounds__(256) void chunk_inv_bf16(const bf16_t* __restrict__ k, const bf16_t* __restrict__ sk,
+                                                    const float* __restrict__ beta, const float* __restrict__ alpha,
+                                                    const float* __restrict__ gamma, int T, int H, int D, int NT,
+                                                    uint16_t* __restrict__ Aout) {
+  constexpr bool SP = M == 2 * L;
   constexpr int NB = M / 16;
-  constexpr int PM = M + 8;
-  constexpr int KAPN = (M * PB > DP * PM) ? M * PB : DP * PM;
-  __shared__ __align__(16) uint16_t kap[KAPN];        // kappa rows; later nu^T [DP][PM]
-  __shared__ __align__(16) uint16_t kapT[DP * PM];    // kappa^T
-  __shared__ __align__(16) float Tm[M][M + 4];
-  __shared__ float inv[NB][16][17];
-  __shared__ float scr[4][16][17];
+  constexpr int NTL = NB * (NB + 1) / 2;
+  constexpr int UNION = M * PK * 2;                      // bytes: kappa rows; later the product scratch
+  static_assert(4 * 4 * 16 * TP * 4 <= UNION && 16 * 16 * TP * 4 <= UNION, "scratch exceeds the union");
+  __shared__ __align__(16) unsigned char un[UNION];
+  __shared__ __align__(16) float Tt[NTL * 16 * TP];      // lower tiles of T, then of A
   __shared__ float lam[M];
-  __shared__ float dtau[M];
   __shared__ float logd[L];
+  uint16_t* kap = reinterpret_cast<uint16_t*>(un);
 
   const int c = blockIdx.x, bh = blockIdx.y;
   const int b = bh / H, h = bh % H;
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform
   const int lr = lane & 15, lg = lane >> 4;
   const int t0 = c * L;
-  const long cidx = (long)bh * NT + c;
 
   if (tid < L) {
     const int t = t0 + tid;
@@ -132,7 +207,6 @@ __global__ __launch_bounds__(256) void chunk_intra_bf16(
       if (lane >= o) x += n;
     }
     logd[tid] = x;
-    ws.logd[cidx * L + tid] = x;
   }
   if (tid < M) {
     const int t = t0 + samp_t<SP>(tid);
@@ -140,194 +214,124 @@ __global__ __launch_bounds__(256) void chunk_intra_bf16(
     if (t < T) lm = samp_r<SP>(tid) ? alpha[(long)(b * T + t) * H + h] : beta[(long)(b * T + t) * H + h];
     lam[tid] = lm;
   }
-  // kappa rows and kappa^T (16-byte chunks of 8 dims)
-  for (int e = tid; e < M * (DP / 8); e += 256) {
-    const int i = e / (DP / 8), cv = e % (DP / 8);
-    const int t = t0 + samp_t<SP>(i);
-    const bf16_t* src = samp_r<SP>(i) ? sk : k;
-    const uint4 x = load8(src + ((long)(b * T + (t < T ? t : 0)) * H + h) * D, 8 * cv, D, t < T);
-    *reinterpret_cast<uint4*>(&kap[i * PB + 8 * cv]) = x;
-    const u16x8 xs = __builtin_bit_cast(u16x8, x);
+  {
+    constexpr int NK = M * (DP / 8) / 256;   // all of a thread's loads in flight before its stores
+    uint4 kx[NK];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) kapT[(8 * cv + j) * PM + i] = xs[j];
+    for (int j = 0; j < NK; ++j) {
+      const int e = tid + 256 * j;
+      const int i = e / (DP / 8), cv = e % (DP / 8);
+      const int t = t0 + samp_t<SP>(i);
+      const bf16_t* src = samp_r<SP>(i) ? sk : k;
+      if constexpr (FULL)   // a token past T reads token T - 1: its samples have lam = 0 (zero T column)
+        kx[j] = *reinterpret_cast<const uint4*>(src + ((long)(b * T + min(t, T - 1)) * H + h) * DP + 8 * cv);
+      else kx[j] = load8(src + ((long)(b * T + (t < T ? t : 0)) * H + h) * D, 8 * cv, D, t < T);
+    }
+#pragma unroll
+    for (int j = 0; j < NK; ++j) {
+      const int e = tid + 256 * j;
+      *reinterpret_cast<uint4*>(&kap[(e / (DP / 8)) * PK + 8 * (e % (DP / 8))]) = kx[j];
+    }
   }
   __syncthreads();
-  if (tid < M) dtau[tid] = expf(logd[samp_t<SP>(tid)]);
 
-  // Gram on the lower block triangle -> transition T (fp32)
-  constexpr int NTILE = NB * (NB + 1) / 2;
-  for (int ti = w; ti < NTILE; ti += 4) {
+  // Gram on the lower tiles -> T
+  for (int ti = w; ti < NTL; ti += 4) {
     int I = 0;
-    while ((I + 1) * (I + 2) / 2 <= ti) ++I;
-    const int J = ti - I * (I + 1) / 2;
+    while (tri(I + 1, 0) <= ti) ++I;
+    const int J = ti - tri(I, 0);
     f4 acc = f4_zero();
 #pragma unroll
-    for (int s = 0; s < DP / 32; ++s) {
-      const uint4 a = *reinterpret_cast<const uint4*>(&kap[(16 * I + lr) * PB + 32 * s + 8 * lg]);
-      const uint4 bb = *reinterpret_cast<const uint4*>(&kap[(16 * J + lr) * PB + 32 * s + 8 * lg]);
-      acc = mma_bf16(as_bf8(a), as_bf8(bb), acc);
-    }
+    for (int s = 0; s < DP / 32; ++s)
+      acc = mma_bf16(rowop(kap + (16 * I + lr) * PK, s, lg), rowop(kap + (16 * J + lr) * PK, s, lg), acc);
+    const int j = 16 * J + lr, tJ = samp_t<SP>(j);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int i = 16 * I + 4 * lg + e, j = 16 * J + lr;
-      const int tI = samp_t<SP>(i), tJ = samp_t<SP>(j);
-      Tm[i][j] = (tJ < tI) ? lam[j] * expf(logd[tI] - logd[tJ]) * acc[e] : 0.f;
+      const int i = 16 * I + 4 * lg + e, tI = samp_t<SP>(i);
+      acc[e] = (tJ < tI) ? lam[j] * expf(logd[tI] - logd[tJ]) * acc[e] : 0.f;
     }
+    st16(Tt + ti * 16 * TP, acc, lr, lg);
   }
-  __syncthreads();
+  __syncthreads();   // kappa rows are dead from here on: the union becomes product scratch
 
-  // kappa^T -> workspace (consumed by K4 as the A operand of kappa^T R')
+  // Diagonal blocks: A_II = (I - T)(I + T^2)(I + T^4)(I + T^8), T strictly lower (T^16 = 0).
   {
-    uint16_t* dst = ws.KT + cidx * DP * M;
-    for (int e = tid; e < DP * (M / 8); e += 256) {
-      const int d = e / (M / 8), cv = e % (M / 8);
-      *reinterpret_cast<uint4*>(dst + d * M + 8 * cv) = *reinterpret_cast<const uint4*>(&kapT[d * PM + 8 * cv]);
-    }
-  }
-  // nu^T into the kappa buffer (kappa rows are no longer needed)
-  for (int e = tid; e < M * (DP / 8); e += 256) {
-    const int i = e / (DP / 8), cv = e % (DP / 8);
-    const int t = t0 + samp_t<SP>(i);
-    const bf16_t* src = samp_r<SP>(i) ? sv : v;
-    const uint4 x = load8(src + ((long)(b * T + (t < T ? t : 0)) * H + h) * D, 8 * cv, D, t < T);
-    const u16x8 xs = __builtin_bit_cast(u16x8, x);
+    float* sc = reinterpret_cast<float*>(un) + w * 4 * 16 * TP;   // this wave's four scratch tiles
+    float* s0 = sc;
+    float* s1 = sc + 16 * TP;
+    float* s2 = sc + 2 * 16 * TP;
+    float* s3 = sc + 3 * 16 * TP;
+    for (int Ib = w; Ib < NB; Ib += 4) {
+      float* Tb = Tt + tri(Ib, Ib) * 16 * TP;
+      const f4 t1 = ld16(Tb, lr, lg);
+      const f4 t2 = mm16(Tb, Tb, f4_zero(), lr, lg);
+      st16(s0, t2, lr, lg);
+      wave_lds_sync();
+      const f4 t3 = mm16(Tb, s0, f4_zero(), lr, lg);
+      const f4 t4 = mm16(s0, s0, f4_zero(), lr, lg);
+      st16(s1, t4, lr, lg);
+      wave_lds_sync();
+      st16(s2, mm16(s1, s1, f4_zero(), lr, lg), lr, lg);   // T^8
+      f4 p1;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) kap[(8 * cv + j) * PM + i] = xs[j];
-  }
-
-  // diagonal 16x16 inverses
-  for (int Ib = w; Ib < NB; Ib += 4) {
-    if (lane < 16) {
-      for (int i = 0; i < 16; ++i) {
-        float x = (i == lane) ? 1.f : 0.f;
-        for (int j = 0; j < i; ++j) x -= Tm[16 * Ib + i][16 * Ib + j] * inv[Ib][j][lane];
-        inv[Ib][i][lane] = x;
-      }
+      for (int e = 0; e < 4; ++e) p1[e] = (4 * lg + e == lr ? 1.f : 0.f) - t1[e] + t2[e] - t3[e];
+      st16(s3, p1, lr, lg);
+      wave_lds_sync();
+      const f4 p2 = mm16(s3, s1, p1, lr, lg);   // P1 + P1 T^4
+      st16(s0, p2, lr, lg);
+      wave_lds_sync();
+      const f4 a = mm16(s0, s2, p2, lr, lg);    // P2 + P2 T^8
+      st16(Tb, a, lr, lg);
+      wave_lds_sync();
     }
   }
   __syncthreads();
 
-  // off-diagonal blocks of A = (I+T)^-1 (fp32), written over T
-  for (int I = 1; I < NB; ++I) {
-    f4 res0 = f4_zero(), res1 = f4_zero();
+  // Off-diagonal blocks by doubling: for halves of nb tiles, rows R = (2p+1)nb.., cols
+  // C = 2p nb..: Z = T_RC A_CC, then A_RC = -A_RR Z.
+  float* Zs = reinterpret_cast<float*>(un);
 #pragma unroll
-    for (int slot = 0; slot < 2; ++slot) {
-      const int J = w + 4 * slot;
-      if (J >= I) continue;
-      f4 tmp = f4_zero();
-      for (int K = J; K < I; ++K) {
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          const float a = Tm[16 * I + lr][16 * K + 4 * s + lg];
-          const float bb = (K == J) ? inv[J][4 * s + lg][lr] : Tm[16 * K + 4 * s + lg][16 * J + lr];
-          tmp = mma_f32(a, bb, tmp);
-        }
-      }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) scr[w][4 * lg + e][lr] = tmp[e];
-      wave_lds_sync();
-      f4 r = f4_zero();
-#pragma unroll
-      for (int s = 0; s < 4; ++s) r = mma_f32(inv[I][lr][4 * s + lg], scr[w][4 * s + lg][lr], r);
-      wave_lds_sync();
-      if (slot == 0) res0 = -r; else res1 = -r;
+  for (int nb = 1; nb < NB; nb <<= 1) {
+    const int npair = NB / (2 * nb);
+    const int items = npair * nb * nb;
+    for (int it = w; it < items; it += 4) {
+      const int p = it / (nb * nb), i = (it / nb) % nb, j = it % nb;
+      const int Ri = (2 * p + 1) * nb + i, C0 = 2 * p * nb;
+      f4 z = f4_zero();
+      for (int kk = j; kk < nb; ++kk)
+        z = mm16(Tt + tri(Ri, C0 + kk) * 16 * TP, Tt + tri(C0 + kk, C0 + j) * 16 * TP, z, lr, lg);
+      st16(Zs + it * 16 * TP, z, lr, lg);
     }
     __syncthreads();
-#pragma unroll
-    for (int slot = 0; slot < 2; ++slot) {
-      const int J = w + 4 * slot;
-      if (J >= I) continue;
-      const f4 r = slot == 0 ? res0 : res1;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) Tm[16 * I + 4 * lg + e][16 * J + lr] = r[e];
+    for (int it = w; it < items; it += 4) {
+      const int p = it / (nb * nb), i = (it / nb) % nb, j = it % nb;
+      const int R0 = (2 * p + 1) * nb, C0 = 2 * p * nb;
+      f4 a = f4_zero();
+      for (int kk = 0; kk <= i; ++kk)
+        a = mm16(Tt + tri(R0 + i, R0 + kk) * 16 * TP, Zs + ((p * nb + kk) * nb + j) * 16 * TP, a, lr, lg);
+      st16(Tt + tri(R0 + i, C0 + j) * 16 * TP, -a, lr, lg);
     }
     __syncthreads();
   }
-  // complete A in Tm: diagonal blocks from inv, zeros above
-  for (int e = tid; e < M * M; e += 256) {
-    const int i = e / M, j = e % M, I = i >> 4, J = j >> 4;
-    if (J == I) Tm[i][j] = inv[I][i & 15][j & 15];
-    else if (J > I) Tm[i][j] = 0.f;
-  }
-  __syncthreads();
 
-  // W = (A diag(D_tau)) kappa, U = A nu.  Wave w owns the row blocks I = w and
-  // NB-1-w (equal k-step counts per wave) across all 8 column tiles, so the
-  // hi/lo split of each A fragment is done once and feeds 8 column tiles.
-  uint16_t* Wh = ws.Whi + cidx * M * DP;
-  uint16_t* Wl = ws.Wlo + cidx * M * DP;
-  float* Uc = ws.U + cidx * M * DP;
-  for (int ii = 0; ii < NB / 4; ++ii) {
-    const int I = ii == 0 ? w : NB - 1 - w;
-    if (I >= NB) continue;
-    const int nks = (16 * (I + 1) + 31) / 32;   // A is zero right of column 16 (I + 1)
-    f4 aw[DP / 16], au[DP / 16];
+  // A -> workspace: [NTL tiles][hi, lo][16][16] bf16
+  uint16_t* dst = Aout + ((long)bh * NT + c) * NTL * 512;
+  for (int e = tid; e < NTL * 64; e += 256) {
+    const int tl = e >> 6, r = (e >> 2) & 15, cg = e & 3;
+    const float* src = Tt + tl * 16 * TP + r * TP + 4 * cg;
+    f4 x;
 #pragma unroll
-    for (int n = 0; n < DP / 16; ++n) { aw[n] = f4_zero(); au[n] = f4_zero(); }
-    for (int s = 0; s < nks; ++s) {
-      const int k0 = 32 * s + 8 * lg;
-      float xa[8], xw[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        xa[j] = Tm[16 * I + lr][k0 + j];
-        xw[j] = xa[j] * dtau[k0 + j];
-      }
-      uint4 ahi, alo, whi, wlo;
-      split8(xa, ahi, alo);
-      split8(xw, whi, wlo);
-      // transposed products (kappa^T / nu^T as the A operand): lane (lr, lg) ends
-      // up with columns 16n + 4lg .. +3 of row 16I + lr, stored as one 8-byte
-      // (W planes) or 16-byte (U) vector; same products and order as W, U
-#pragma unroll
-      for (int n = 0; n < DP / 16; ++n) {
-        const uint4 bk = *reinterpret_cast<const uint4*>(&kapT[(16 * n + lr) * PM + k0]);
-        const uint4 bv = *reinterpret_cast<const uint4*>(&kap[(16 * n + lr) * PM + k0]);
-        aw[n] = mma_bf16(as_bf8(bk), as_bf8(whi), aw[n]);
-        aw[n] = mma_bf16(as_bf8(bk), as_bf8(wlo), aw[n]);
-        au[n] = mma_bf16(as_bf8(bv), as_bf8(ahi), au[n]);
-        au[n] = mma_bf16(as_bf8(bv), as_bf8(alo), au[n]);
-      }
-    }
-#pragma unroll
-    for (int n = 0; n < DP / 16; ++n) {
-      const long off = (long)(16 * I + lr) * DP + 16 * n + 4 * lg;
-      uint16_t hi[4], lo[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) split1(aw[n][e], hi[e], lo[e]);
-      *reinterpret_cast<uint2*>(Wh + off) =
-          make_uint2((uint32_t)hi[0] | ((uint32_t)hi[1] << 16), (uint32_t)hi[2] | ((uint32_t)hi[3] << 16));
-      *reinterpret_cast<uint2*>(Wl + off) =
-          make_uint2((uint32_t)lo[0] | ((uint32_t)lo[1] << 16), (uint32_t)lo[2] | ((uint32_t)lo[3] << 16));
-      *reinterpret_cast<float4*>(Uc + off) = make_float4(au[n][0], au[n][1], au[n][2], au[n][3]);
-    }
+    for (int q = 0; q < 4; ++q) x[q] = src[q];
+    uint2 hi, lo;
+    split4(x, hi, lo);
+    *reinterpret_cast<uint2*>(dst + tl * 512 + r * 16 + 4 * cg) = hi;
+    *reinterpret_cast<uint2*>(dst + tl * 512 + 256 + r * 16 + 4 * cg) = lo;
   }
 }
 
 // ---------------------------------------------------------------------------
-// K4: the inter-chunk state pass, segment-parallel.
-//
-// One chunk maps its start state S to D_L S + kappa^T (lambda' (U - W S)),
-// which is affine in S, so a segment of consecutive chunks maps its start
-// state to its end state as S_end = Phi S_start + P: Phi is the segment's
-// chunk maps applied to the identity with U = 0, P the same maps applied to 0
-// with U.  Three launches replace the one sequential pass over all chunks:
-//   1. chunk_seg_bf16<SEG_MAPS>: one block per (b*h, segment, P or Phi) runs
-//      the segment's chunks; all segments at once;
-//   2. chunk_seg_scan_bf16: per b*h, S_start(0) = h0 and
-//      S_start(g+1) = Phi_g S_start(g) + P_g;
-//   3. chunk_seg_bf16<SEG_FULL>: each segment reruns its chunks from its start
-//      state and writes the chunk-start states and residuals K5 reads.
-// A block owns all 128 state columns: each chunk's W, kappa^T and U cross into
-// the CU once and feed the products of all four waves.  Wave w owns state rows
-// 32w .. 32w + 31 and residual (sample) rows (M/64) w * 16 .. + M/64 * 16.
-// Products keep the fp32 state exact to about 2^-16: W, S and R' are split
-// into bf16 hi + lo (the lo * lo term is dropped).
+// K4: the state passes.
 // ---------------------------------------------------------------------------
-enum SegMode { SEG_MAPS = 0, SEG_FULL = 1 };
-
-__device__ __forceinline__ uint4 neg_bf16x8(uint4 u) {
-  return make_uint4(u.x ^ 0x80008000u, u.y ^ 0x80008000u, u.z ^ 0x80008000u, u.w ^ 0x80008000u);
-}
 
 // Number of segments of the state pass: enough (b*h, segment) blocks to fill
 // the GPU, at least 8 chunks per segment, at most 16 segments.
@@ -339,216 +343,387 @@ inline int seg_count(int BH, int NT) {
   return g < 1 ? 1 : g;
 }
 
-// MODE SEG_MAPS: blockIdx.z 0 builds P (start 0, with U), 1 builds Phi (start
-// I, U = 0); the end state goes to sout[(z * BH + bh) * G + g] ([DP][DP] fp32).
-// MODE SEG_FULL: the start state is sinit[bh * G + g] with leading dimension
-// sld (rows and columns >= sld read as 0); chunk-start states and residuals go
-// to the workspace, and the last segment's end state to ht ([DP][DP]-padded
-// rows/cols < D, leading dimension D).
-template <bool SP, int MODE>
-__global__ __launch_bounds__(256, 1) void chunk_seg_bf16(const float* __restrict__ beta, const float* __restrict__ alpha,
-                                                       int T, int H, int D, int NT, int CPS, Bf16Ws ws,
-                                                       const float* __restrict__ sinit, int sld,
-                                                       float* __restrict__ sout, float* __restrict__ ht) {
-  constexpr int M = SP ? 2 * L : L;
-  constexpr int RT = M / 64;      // residual row tiles per wave
-  constexpr int KS = DP / 32;     // k-steps over the key dim
-  constexpr int KSM = M / 32;     // k-steps over samples
-  constexpr int PM = M + 8;
-  constexpr int NC = DP / 16;     // column tiles
-  __shared__ __align__(16) uint16_t Sh[DP * PB];   // S transposed [col][row], hi
-  __shared__ __align__(16) uint16_t Sl[DP * PB];
-  __shared__ __align__(16) uint16_t Rh[DP * PM];   // R' transposed [col][sample], hi
-  __shared__ __align__(16) uint16_t Rl[DP * PM];
-  __shared__ float lam[M];
-  __shared__ float logd[L];
+// Per-chunk gate tables in LDS: the chunk-local log-decay prefix l_t, e^{l_t}, and per
+// sample the write strength lam_i and the factor lam_i e^{l_L - l_tau_i} of R'.
+template <int M>
+struct GateTab {
+  float logd[L];
+  float el[L];
+  float lam[M];
+  float fac[M];
+};
 
-  const int bh = blockIdx.x, g = blockIdx.y, G = gridDim.y, BH = gridDim.x;
-  const bool phi = MODE == SEG_MAPS && blockIdx.z == 1;   // block-uniform
-  const int b = bh / H, h = bh % H;
-  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform
-  const int lr = lane & 15, lg = lane >> 4;
-  const int cb = g * CPS, ce = min(NT, cb + CPS);
-
-  // state rows 32w + 16u + 4lg + e, columns 16n + lr
-  f4 S[2][NC];
+// Fills the tables (tokens past T: no decay, no write); wave 0 does it all, one token per
+// lane, so the factors come from the scan in registers.
+template <int M>
+__device__ __forceinline__ void stage_gates(const float* __restrict__ beta, const float* __restrict__ alpha,
+                                            const float* __restrict__ gamma, int T, int H, int b, int h, int t0,
+                                            int tid, GateTab<M>& gt) {
+  constexpr bool SP = M == 2 * L;
+  if (tid < 64) {
+    const int t = t0 + tid;
+    float x = 0.f;
+    if (t < T) x = __logf(fmaxf(gamma[(long)(b * T + t) * H + h], 1e-6f));
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
-#pragma unroll
-    for (int n = 0; n < NC; ++n) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int row = 32 * w + 16 * u + 4 * lg + e, col = 16 * n + lr;
-        float x = 0.f;
-        if (MODE == SEG_MAPS) x = (phi && row == col) ? 1.f : 0.f;
-        else if (sinit != nullptr && row < sld && col < sld) x = sinit[((long)(bh * G + g) * sld + row) * sld + col];
-        S[u][n][e] = x;
-      }
+    for (int o = 1; o < 64; o <<= 1) {
+      const float n = __shfl_up(x, o, 64);
+      if (tid >= o) x += n;
     }
-  }
-
-  // Per-chunk operand fragments, one set each: W and U are reloaded for the
-  // next chunk as soon as the residual products have used them, kappa^T as
-  // soon as the state update has, so each load has the rest of a chunk to land.
-  uint4 wh[RT][KS], wl[RT][KS], kt[2][KSM];
-  f4 uu[RT][NC];
-  float nlogd = 0.f, nlam = 0.f;   // this thread's log-decay / write-strength entries of the next chunk
-  const bool use_u = !phi;
-  auto load_wu = [&](int c) __attribute__((always_inline)) {
-    const long cidx = (long)bh * NT + c;
-    const uint16_t* Wh = ws.Whi + cidx * M * DP;
-    const uint16_t* Wl = ws.Wlo + cidx * M * DP;
-    const float* Uc = ws.U + cidx * M * DP;
+    gt.logd[tid] = x;
+    gt.el[tid] = fexp(x);
+    const float dec = fexp(__shfl(x, 63, 64) - x);   // e^{l_L - l_t}
 #pragma unroll
-    for (int u = 0; u < RT; ++u) {
-      const int I = RT * w + u;
-#pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        wh[u][s] = neg_bf16x8(*reinterpret_cast<const uint4*>(Wh + (16 * I + lr) * DP + 32 * s + 8 * lg));
-        wl[u][s] = neg_bf16x8(*reinterpret_cast<const uint4*>(Wl + (16 * I + lr) * DP + 32 * s + 8 * lg));
-      }
-#pragma unroll
-      for (int n = 0; n < NC; ++n) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) uu[u][n][e] = use_u ? Uc[(16 * I + 4 * lg + e) * DP + 16 * n + lr] : 0.f;
-      }
-    }
-  };
-  auto load_kt = [&](int c) __attribute__((always_inline)) {
-    const uint16_t* KTc = ws.KT + ((long)bh * NT + c) * DP * M;
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-#pragma unroll
-      for (int s = 0; s < KSM; ++s)
-        kt[u][s] = *reinterpret_cast<const uint4*>(KTc + (32 * w + 16 * u + lr) * M + 32 * s + 8 * lg);
-    }
-  };
-  auto load_gates = [&](int c) __attribute__((always_inline)) {
-    if (tid < L) nlogd = ws.logd[((long)bh * NT + c) * L + tid];
-    if (tid < M) {
-      const int t = c * L + samp_t<SP>(tid);
-      nlam = 0.f;
-      if (t < T) nlam = samp_r<SP>(tid) ? alpha[(long)(b * T + t) * H + h] : beta[(long)(b * T + t) * H + h];
-    }
-  };
-
-  if (cb < ce) {
-    load_wu(cb);
-    load_kt(cb);
-    load_gates(cb);
-  }
-  for (int c = cb; c < ce; ++c) {
-    const long cidx = (long)bh * NT + c;
-    // logd / lam of this chunk into LDS (the previous chunk's readers passed a barrier)
-    if (tid < L) logd[tid] = nlogd;
-    if (tid < M) lam[tid] = nlam;
-    if (c + 1 < ce) load_gates(c + 1);
-    // chunk-start state: LDS operand copy, and the workspace copy K5 reads (both [col][row], hi/lo)
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int row0 = 32 * w + 16 * u + 4 * lg;
-#pragma unroll
-      for (int n = 0; n < NC; ++n) {
-        uint16_t hh[4], ll[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) split1(S[u][n][e], hh[e], ll[e]);
-        const ushort4 hv = make_ushort4(hh[0], hh[1], hh[2], hh[3]);
-        const ushort4 lv = make_ushort4(ll[0], ll[1], ll[2], ll[3]);
-        const int col = 16 * n + lr;
-        *reinterpret_cast<ushort4*>(&Sh[col * PB + row0]) = hv;
-        *reinterpret_cast<ushort4*>(&Sl[col * PB + row0]) = lv;
-        if constexpr (MODE == SEG_FULL) {
-          *reinterpret_cast<ushort4*>(&ws.STh[cidx * DP * DP + (long)col * DP + row0]) = hv;
-          *reinterpret_cast<ushort4*>(&ws.STl[cidx * DP * DP + (long)col * DP + row0]) = lv;
-        }
-      }
-    }
-    lds_barrier();
-
-    // R = U - W S (the W fragments are negated: acc = U + (-W) S; Wl.Sl dropped),
-    // one 16-column tile at a time (a scheduling barrier keeps the compiler from
-    // hoisting every tile's LDS operands at once)
-    const float logdL = logd[L - 1];
-#pragma unroll
-    for (int u = 0; u < RT; ++u) {
-      const int I = RT * w + u;
-      const int i0 = 16 * I + 4 * lg;
-      float fac[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) fac[e] = lam[i0 + e] * expf(logdL - logd[samp_t<SP>(i0 + e)]);
-#pragma unroll
-      for (int n = 0; n < NC; ++n) {
-        f4 r = uu[u][n];
-#pragma unroll
-        for (int s = 0; s < KS; ++s) {
-          const uint4 bh_ = *reinterpret_cast<const uint4*>(&Sh[(16 * n + lr) * PB + 32 * s + 8 * lg]);
-          const uint4 bl_ = *reinterpret_cast<const uint4*>(&Sl[(16 * n + lr) * PB + 32 * s + 8 * lg]);
-          r = mma_bf16(as_bf8(wh[u][s]), as_bf8(bh_), r);
-          r = mma_bf16(as_bf8(wh[u][s]), as_bf8(bl_), r);
-          r = mma_bf16(as_bf8(wl[u][s]), as_bf8(bh_), r);
-        }
-        const int col = 16 * n + lr;
-        uint16_t hh[4], ll[4], h2[4], l2[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          split1(r[e], hh[e], ll[e]);
-          split1(r[e] * fac[e], h2[e], l2[e]);
-        }
-        if constexpr (MODE == SEG_FULL) {
-          *reinterpret_cast<ushort4*>(&ws.RTh[cidx * DP * M + (long)col * M + i0]) = make_ushort4(hh[0], hh[1], hh[2], hh[3]);
-          *reinterpret_cast<ushort4*>(&ws.RTl[cidx * DP * M + (long)col * M + i0]) = make_ushort4(ll[0], ll[1], ll[2], ll[3]);
-        }
-        *reinterpret_cast<ushort4*>(&Rh[col * PM + i0]) = make_ushort4(h2[0], h2[1], h2[2], h2[3]);
-        *reinterpret_cast<ushort4*>(&Rl[col * PM + i0]) = make_ushort4(l2[0], l2[1], l2[2], l2[3]);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    }
-    if (c + 1 < ce) load_wu(c + 1);
-    lds_barrier();
-
-    // S <- D_L S + kappa^T R'
-    const float DL = expf(logdL);
-#pragma unroll
-    for (int n = 0; n < NC; ++n) {
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        f4 acc = S[u][n] * DL;
-#pragma unroll
-        for (int s = 0; s < KSM; ++s) {
-          const uint4 rh = *reinterpret_cast<const uint4*>(&Rh[(16 * n + lr) * PM + 32 * s + 8 * lg]);
-          const uint4 rl = *reinterpret_cast<const uint4*>(&Rl[(16 * n + lr) * PM + 32 * s + 8 * lg]);
-          acc = mma_bf16(as_bf8(kt[u][s]), as_bf8(rh), acc);
-          acc = mma_bf16(as_bf8(kt[u][s]), as_bf8(rl), acc);
-        }
-        S[u][n] = acc;
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    if (c + 1 < ce) load_kt(c + 1);
-  }
-
-#pragma unroll
-  for (int u = 0; u < 2; ++u) {
-#pragma unroll
-    for (int n = 0; n < NC; ++n) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int row = 32 * w + 16 * u + 4 * lg + e, col = 16 * n + lr;
-        if constexpr (MODE == SEG_MAPS) {
-          sout[((long)((blockIdx.z * BH + bh) * G + g) * DP + row) * DP + col] = S[u][n][e];
-        } else {
-          if (ht != nullptr && g == G - 1 && row < D && col < D) ht[((long)bh * D + row) * D + col] = S[u][n][e];
-        }
-      }
+    for (int r = 0; r < (SP ? 2 : 1); ++r) {
+      const int i = SP ? 2 * tid + r : tid;
+      float lm = 0.f;
+      if (t < T) lm = r ? alpha[(long)(b * T + t) * H + h] : beta[(long)(b * T + t) * H + h];
+      gt.lam[i] = lm;
+      gt.fac[i] = lm * dec;
     }
   }
 }
 
+// Stage chunk c's shared operands in LDS: kappa rows, nu rows (USE_NU), q rows (USE_Q),
+// the A tiles (rows padded to AP), the log-decay prefix and the write strengths.  Each
+// thread issues all of its global loads before its first LDS store, so the chunk's
+// loads are in flight together.  FULL (D = DP): rows are read without conditions -- a
+// token past T reads token T - 1 instead of zeros, which is harmless: such a sample's
+// write strength is 0 (no write, no T_ij column), A rows of valid samples only involve
+// earlier samples, and it only reaches output rows t >= T, which are not stored.  For
+// D < DP, dims >= D must read as 0, and rows past T do too.
+template <int M, int NTHR, bool USE_NU, bool USE_Q, bool FULL>
+__device__ __forceinline__ void stage_chunk(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
+                                            const bf16_t* __restrict__ v, const bf16_t* __restrict__ sk,
+                                            const bf16_t* __restrict__ sv, const float* __restrict__ beta,
+                                            const float* __restrict__ alpha, const float* __restrict__ gamma,
+                                            const uint16_t* __restrict__ Ain, int T, int H, int D, int NT, int b,
+                                            int h, int bh, int c, int tid, uint16_t* kap, uint16_t* nuv,
+                                            uint16_t* qr, uint16_t* At, GateTab<M>& gt) {
+  constexpr bool SP = M == 2 * L;
+  constexpr int NB = M / 16;
+  constexpr int NTL = NB * (NB + 1) / 2;
+  constexpr int NK = M * (DP / 8) / NTHR;              // 16-byte row pieces per thread
+  constexpr int NQ = L * (DP / 8) / NTHR;
+  constexpr int NA = (NTL * 64 + NTHR - 1) / NTHR;     // 16-byte A tile pieces per thread
+  static_assert(NK * NTHR == M * (DP / 8) && NQ * NTHR == L * (DP / 8), "row pieces must divide evenly");
+  const int t0 = c * L;
+  uint4 kx[NK], nx[USE_NU ? NK : 1], qx[USE_Q ? NQ : 1], ax[NA];
+  const uint16_t* src = Ain + ((long)bh * NT + c) * NTL * 512;
+#pragma unroll
+  for (int j = 0; j < NA; ++j) {
+    const int e = tid + j * NTHR;   // tp = 2 * tile + plane, row r, 16-byte half hf
+    const int tp = e >> 5, r = (e >> 1) & 15, hf = e & 1;
+    if constexpr (NTL * 64 % NTHR == 0) ax[j] = *reinterpret_cast<const uint4*>(src + tp * 256 + r * 16 + 8 * hf);
+    else ax[j] = e < NTL * 64 ? *reinterpret_cast<const uint4*>(src + tp * 256 + r * 16 + 8 * hf) : zero4();
+  }
+#pragma unroll
+  for (int j = 0; j < NK; ++j) {
+    const int e = tid + j * NTHR;
+    const int i = e / (DP / 8), cv = e % (DP / 8);
+    const int t = t0 + samp_t<SP>(i);
+    const bool r1 = samp_r<SP>(i);
+    if constexpr (FULL) {
+      const long roff = ((long)(b * T + min(t, T - 1)) * H + h) * DP + 8 * cv;
+      kx[j] = *reinterpret_cast<const uint4*>((r1 ? sk : k) + roff);
+      if constexpr (USE_NU) nx[j] = *reinterpret_cast<const uint4*>((r1 ? sv : v) + roff);
+    } else {
+      const long roff = ((long)(b * T + (t < T ? t : 0)) * H + h) * D;
+      kx[j] = load8((r1 ? sk : k) + roff, 8 * cv, D, t < T);
+      if constexpr (USE_NU) nx[j] = load8((r1 ? sv : v) + roff, 8 * cv, D, t < T);
+    }
+  }
+  if constexpr (USE_Q) {
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) {
+      const int e = tid + j * NTHR;
+      const int i = e / (DP / 8), cv = e % (DP / 8);
+      const int t = t0 + i;
+      if constexpr (FULL) qx[j] = *reinterpret_cast<const uint4*>(q + ((long)(b * T + min(t, T - 1)) * H + h) * DP + 8 * cv);
+      else qx[j] = load8(q + ((long)(b * T + (t < T ? t : 0)) * H + h) * D, 8 * cv, D, t < T);
+    }
+  }
+  stage_gates<M>(beta, alpha, gamma, T, H, b, h, t0, tid, gt);
+#pragma unroll
+  for (int j = 0; j < NA; ++j) {
+    const int e = tid + j * NTHR;
+    const int tp = e >> 5, r = (e >> 1) & 15, hf = e & 1;
+    if (e < NTL * 64) *reinterpret_cast<uint4*>(&At[(tp * 16 + r) * AP + 8 * hf]) = ax[j];
+  }
+#pragma unroll
+  for (int j = 0; j < NK; ++j) {
+    const int e = tid + j * NTHR;
+    const int i = e / (DP / 8), cv = e % (DP / 8);
+    *reinterpret_cast<uint4*>(&kap[krow<SP>(i) + 8 * cv]) = kx[j];
+    if constexpr (USE_NU) *reinterpret_cast<uint4*>(&nuv[krow<SP>(i) + 8 * cv]) = nx[j];
+  }
+  if constexpr (USE_Q) {
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) {
+      const int e = tid + j * NTHR;
+      const int i = e / (DP / 8), cv = e % (DP / 8);
+      *reinterpret_cast<uint4*>(&qr[i * PK + 8 * cv]) = qx[j];
+    }
+  }
+}
+
+// The staging of stage_chunk for D = DP as direct-to-LDS buffer loads (buffer_load_dwordx4
+// ... lds: lane l of an instruction fills the 16 bytes at its LDS base + 16 l), which
+// hold no data registers, so all of a chunk's loads are issued back to back.  One buffer
+// resource per input covers its head's rows [0, T): a token past T reads as zeros.  A
+// 272-byte kappa / nu / q row is 17 slots (the 17th is its pad and re-reads the first);
+// a 48-byte A tile row is 3 (2 data, 1 pad).  The caller waits for the loads (vmcnt) and
+// then synchronises the block.
+template <int M, int NTHR, bool USE_NU, bool USE_Q>
+__device__ __forceinline__ void stage_chunk_dma(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
+                                                const bf16_t* __restrict__ v, const bf16_t* __restrict__ sk,
+                                                const bf16_t* __restrict__ sv, const float* __restrict__ beta,
+                                                const float* __restrict__ alpha, const float* __restrict__ gamma,
+                                                const uint16_t* __restrict__ Ain, int T, int H, int NT, int b, int h,
+                                                int bh, int c, int tid, uint16_t* kap, uint16_t* nuv, uint16_t* qr,
+                                                uint16_t* At, GateTab<M>& gt) {
+  constexpr bool SP = M == 2 * L;
+  constexpr int NB = M / 16;
+  constexpr int NTL = NB * (NB + 1) / 2;
+  constexpr int NW = NTHR / 64;
+  constexpr int RI = L * 17 / 64;            // instructions per 64 rows (17)
+  constexpr int AI = NTL * 2 * 16 * 3 / 64;  // instructions for the A tiles
+  static_assert(NTL * 2 * 16 * 3 % 64 == 0, "A tile rows must fill whole instructions");
+  const int t0 = c * L;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const long hoff = ((long)b * T * H + h) * DP;   // row 0 of this head
+  const int rbytes = H * DP * 2;
+  const int nrec = (T - 1) * rbytes + DP * 2;
+  auto rsrc = [&](const bf16_t* base) __attribute__((always_inline)) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t*>(base + hoff), 0, nrec, 0x00020000);
+  };
+  // rows of 64 tokens from one input into dst (64 rows x PK)
+  auto rows64 = [&](__amdgpu_buffer_rsrc_t rs, uint16_t* dst) __attribute__((always_inline)) {
+    for (int i = w; i < RI; i += NW) {
+      const int sl = 64 * i + lane;
+      const int row = sl / 17, pc = sl % 17;
+      const unsigned voff = (unsigned)((t0 + row) * rbytes + 16 * (pc < 16 ? pc : 0));
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(dst + 512 * i), 16,
+                                               voff, 0, 0, 0);
+    }
+  };
+  rows64(rsrc(k), kap);
+  if constexpr (SP) rows64(rsrc(sk), kap + 64 * PK + 8);
+  if constexpr (USE_NU) {
+    rows64(rsrc(v), nuv);
+    if constexpr (SP) rows64(rsrc(sv), nuv + 64 * PK + 8);
+  }
+  if constexpr (USE_Q) rows64(rsrc(q), qr);
+  {
+    const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(Ain + ((long)bh * NT + c) * NTL * 512), 0, NTL * 1024, 0x00020000);
+    for (int i = w; i < AI; i += NW) {
+      const int sl = 64 * i + lane;
+      const int row = sl / 3, pc = sl % 3;   // row = (2 tile + plane) 16 + r
+      const unsigned voff = (unsigned)(row * 32 + 16 * (pc < 2 ? pc : 0));
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ars, (__attribute__((address_space(3))) void*)(At + 512 * i), 16,
+                                               voff, 0, 0, 0);
+    }
+  }
+  stage_gates<M>(beta, alpha, gamma, T, H, b, h, t0, tid, gt);
+}
+
+// A wave's state is kept in 16-column tiles: S[r] holds S[16r + 4lg + e][col + lr] of the
+// tile's columns col .. col + 15 (r: d_k row tile).  fp32 operands enter the products as
+// Op pairs, each the B operand of one k step of 32 (hi and lo bf16 halves of two
+// accumulator tiles, in the k order of cat()).
+struct Op {
+  uint4 h, l;
+};
+
+// Tiles 2s and 2s + 1 of x as the operand of step s.
+template <int N>
+__device__ __forceinline__ void pack_ops(const f4 (&x)[N], Op (&op)[N / 2]) {
+#pragma unroll
+  for (int s = 0; s < N / 2; ++s) {
+    uint2 ha, la, hb, lb;
+    split4(x[2 * s], ha, la);
+    split4(x[2 * s + 1], hb, lb);
+    op[s].h = make_uint4(ha.x, ha.y, hb.x, hb.y);
+    op[s].l = make_uint4(la.x, la.y, lb.x, lb.y);
+  }
+}
+
+// R = A B for one 16-column tile at column col, with X = kappa S and
+// B = nu - e^{l_tau} X (nu = 0 for !USE_NU); Sop is the state tile as operands.
+template <int M, bool USE_NU>
+__device__ __forceinline__ void tile_residual(const Op (&Sop)[DP / 32], const uint16_t* kap, const uint16_t* nuv,
+                                              const uint16_t* At, const float* el, int col, int lr, int lg,
+                                              f4 (&R)[M / 16]) {
+  constexpr bool SP = M == 2 * L;
+  constexpr int NB = M / 16;
+  Op Bop[NB / 2];
+#pragma unroll
+  for (int sp = 0; sp < NB / 2; ++sp) {
+    f4 y[2];
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const int I = 2 * sp + hf;
+      f4 x = f4_zero();
+      const uint16_t* kr = kap + krow<SP>(16 * I + lr);
+#pragma unroll
+      for (int s = 0; s < DP / 32; ++s) {
+        const bf16x8 a = rowop_p(kr, s, lg);
+        x = mma_bf16(a, as_bf8(Sop[s].h), x);
+        x = mma_bf16(a, as_bf8(Sop[s].l), x);
+      }
+      float ef[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ef[e] = el[samp_t<SP>(16 * I + 4 * lg + e)];
+      if constexpr (USE_NU) {
+        const s16x4 nv = lds_tr(nuv + krow<SP>(16 * I + 4 * lg + (lr >> 2)) + col + 4 * (lr & 3));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[hf][e] = bf16_to_f32((uint16_t)nv[e]) - ef[e] * x[e];
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[hf][e] = -ef[e] * x[e];
+      }
+    }
+    uint2 ha, la, hb, lb;
+    split4(y[0], ha, la);
+    split4(y[1], hb, lb);
+    Bop[sp].h = make_uint4(ha.x, ha.y, hb.x, hb.y);
+    Bop[sp].l = make_uint4(la.x, la.y, lb.x, lb.y);
+    __builtin_amdgcn_sched_barrier(0);   // one pair of tile rows at a time
+  }
+  // tile row I takes the A tiles (I, J <= I)
+#pragma unroll
+  for (int I = 0; I < NB; ++I) {
+    R[I] = f4_zero();
+#pragma unroll
+    for (int s = 0; 2 * s <= I; ++s) {
+      const uint16_t* a0 = At + tri(I, 2 * s) * 2 * 16 * AP + lr * AP + 4 * lg;
+      const uint2 h0 = *reinterpret_cast<const uint2*>(a0);
+      const uint2 l0 = *reinterpret_cast<const uint2*>(a0 + 16 * AP);
+      uint2 h1 = make_uint2(0, 0), l1 = make_uint2(0, 0);
+      if (2 * s + 1 <= I) {
+        const uint16_t* a1 = At + tri(I, 2 * s + 1) * 2 * 16 * AP + lr * AP + 4 * lg;
+        h1 = *reinterpret_cast<const uint2*>(a1);
+        l1 = *reinterpret_cast<const uint2*>(a1 + 16 * AP);
+      }
+      const bf16x8 ah = cat(h0, h1), al = cat(l0, l1);
+      R[I] = mma_bf16(ah, as_bf8(Bop[s].h), R[I]);
+      R[I] = mma_bf16(ah, as_bf8(Bop[s].l), R[I]);
+      R[I] = mma_bf16(al, as_bf8(Bop[s].h), R[I]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// R' = lam e^{l_L - l_tau} R (the per-sample factors from the gate table) as operands.
+template <int M>
+__device__ __forceinline__ void scaled_ops(const f4 (&R)[M / 16], const float* facg, int lg, Op (&op)[M / 32]) {
+  f4 y[M / 16];
+#pragma unroll
+  for (int I = 0; I < M / 16; ++I) {
+    const float4 f = *reinterpret_cast<const float4*>(facg + 16 * I + 4 * lg);
+    y[I][0] = R[I][0] * f.x;
+    y[I][1] = R[I][1] * f.y;
+    y[I][2] = R[I][2] * f.z;
+    y[I][3] = R[I][3] * f.w;
+  }
+  pack_ops<M / 16>(y, op);
+}
+
+// S <- e^{l_L} S + kappa^T R' for one 16-column tile.
+template <int M>
+__device__ __forceinline__ void tile_update(f4 (&S)[DP / 16], const Op (&Rop)[M / 32], const uint16_t* kap, float DL,
+                                            int lr, int lg) {
+#pragma unroll
+  for (int r = 0; r < DP / 16; ++r) {
+    f4 acc = S[r] * DL;
+#pragma unroll
+    for (int s = 0; s < M / 32; ++s) {
+      const bf16x8 a = kapT_op<M == 2 * L>(kap, r, s, lr, lg);
+      acc = mma_bf16(a, as_bf8(Rop[s].h), acc);
+      acc = mma_bf16(a, as_bf8(Rop[s].l), acc);
+    }
+    S[r] = acc;
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// The chunks of segment g for one state: PHI = false runs P (start 0, with nu), PHI = true
+// runs Phi (start I, nu = 0), each wave over one 16-column tile of the state.
+template <int M, bool FULL, bool PHI>
+__device__ __forceinline__ void maps_pass(const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
+                                          const bf16_t* __restrict__ sk, const bf16_t* __restrict__ sv,
+                                          const float* __restrict__ beta, const float* __restrict__ alpha,
+                                          const float* __restrict__ gamma, int T, int H, int D, int NT, int CPS,
+                                          const uint16_t* __restrict__ Ain, float* __restrict__ dst, uint16_t* kap,
+                                          uint16_t* nuv, uint16_t* At, GateTab<M>& gt) {
+  constexpr int NB = M / 16;
+  const int bh = blockIdx.x, g = blockIdx.y;
+  const int b = bh / H, h = bh % H;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform
+  const int lr = lane & 15, lg = lane >> 4;
+  const int col = 16 * w;
+  const int cb = g * CPS, ce = min(NT, cb + CPS);
+
+  f4 S[DP / 16];
+#pragma unroll
+  for (int r = 0; r < DP / 16; ++r)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) S[r][e] = (PHI && 16 * r + 4 * lg + e == col + lr) ? 1.f : 0.f;
+
+  for (int c = cb; c < ce; ++c) {
+    __syncthreads();   // every wave is done with the previous chunk's operands
+    if constexpr (FULL) {
+      stage_chunk_dma<M, 512, !PHI, false>(nullptr, k, v, sk, sv, beta, alpha, gamma, Ain, T, H, NT, b, h, bh, c,
+                                           tid, kap, nuv, nullptr, At, gt);
+      __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): this wave's loads have landed in LDS
+    } else {
+      stage_chunk<M, 512, !PHI, false, FULL>(nullptr, k, v, sk, sv, beta, alpha, gamma, Ain, T, H, D, NT, b, h, bh,
+                                             c, tid, kap, nuv, nullptr, At, gt);
+    }
+    __syncthreads();
+    Op Sop[DP / 32];
+    pack_ops<DP / 16>(S, Sop);
+    f4 R[NB];
+    tile_residual<M, !PHI>(Sop, kap, nuv, At, gt.el, col, lr, lg, R);
+    Op Rop[NB / 2];
+    scaled_ops<M>(R, gt.fac, lg, Rop);
+    tile_update<M>(S, Rop, kap, gt.el[L - 1], lr, lg);
+  }
+#pragma unroll
+  for (int r = 0; r < DP / 16; ++r)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) dst[(long)(16 * r + 4 * lg + e) * DP + col + lr] = S[r][e];
+}
+
+// The maps of segment g: blockIdx.z = 0 builds P, 1 builds Phi; the end states go to sout
+// ([P; Phi] x [B*H][G][DP][DP] fp32).
+template <int M, bool FULL>
+__global__ __launch_bounds__(512, 1) void chunk_maps_bf16(const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
+                                                        const bf16_t* __restrict__ sk, const bf16_t* __restrict__ sv,
+                                                        const float* __restrict__ beta, const float* __restrict__ alpha,
+                                                        const float* __restrict__ gamma, int T, int H, int D, int NT,
+                                                        int CPS, const uint16_t* __restrict__ Ain,
+                                                        float* __restrict__ sout) {
+  constexpr int NB = M / 16;
+  constexpr int NTL = NB * (NB + 1) / 2;
+  __shared__ __align__(16) uint16_t kap[krows_elems<M>()];
+  __shared__ __align__(16) uint16_t nuv[krows_elems<M>()];
+  __shared__ __align__(16) uint16_t At[NTL * 2 * 16 * AP];
+  __shared__ __align__(16) GateTab<M> gt;
+  float* dst = sout + (long)((blockIdx.z * gridDim.x + blockIdx.x) * gridDim.y + blockIdx.y) * DP * DP;
+  if (blockIdx.z == 1)   // block-uniform
+    maps_pass<M, FULL, true>(k, v, sk, sv, beta, alpha, gamma, T, H, D, NT, CPS, Ain, dst, kap, nuv, At, gt);
+  else
+    maps_pass<M, FULL, false>(k, v, sk, sv, beta, alpha, gamma, T, H, D, NT, CPS, Ain, dst, kap, nuv, At, gt);
+}
+
 // The segment start states: sinit[bh*G + g] for g < G, from h0 ([B*H][D][D] or
-// NULL) and the maps of chunk_seg_bf16<SEG_MAPS> (maps[0]: P, maps[1]: Phi).
+// NULL) and the maps of chunk_maps_bf16 (maps[0]: P, maps[1]: Phi).
 // S <- Phi S + P runs in fp32 with Phi and S split into bf16 hi + lo.
 __global__ __launch_bounds__(256, 1) void chunk_seg_scan_bf16(int G, int D, const float* __restrict__ h0,
                                                             const float* __restrict__ maps, float* __restrict__ sinit) {
+  constexpr int PB = DP + 8;
   constexpr int NC = DP / 16;
   constexpr int KS = DP / 32;
   __shared__ __align__(16) uint16_t Sh[DP * PB];   // S transposed [col][row], hi
@@ -577,14 +752,12 @@ __global__ __launch_bounds__(256, 1) void chunk_seg_scan_bf16(int G, int D, cons
 #pragma unroll
       for (int n = 0; n < NC; ++n) {
         const int row0 = 32 * w + 16 * u + 4 * lg, col = 16 * n + lr;
-        uint16_t hh[4], ll[4];
+        uint2 hh, ll;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          dst[(long)(row0 + e) * DP + col] = S[u][n][e];
-          split1(S[u][n][e], hh[e], ll[e]);
-        }
-        *reinterpret_cast<ushort4*>(&Sh[col * PB + row0]) = make_ushort4(hh[0], hh[1], hh[2], hh[3]);
-        *reinterpret_cast<ushort4*>(&Sl[col * PB + row0]) = make_ushort4(ll[0], ll[1], ll[2], ll[3]);
+        for (int e = 0; e < 4; ++e) dst[(long)(row0 + e) * DP + col] = S[u][n][e];
+        split4(S[u][n], hh, ll);
+        *reinterpret_cast<uint2*>(&Sh[col * PB + row0]) = hh;
+        *reinterpret_cast<uint2*>(&Sl[col * PB + row0]) = ll;
       }
     }
     if (g + 1 == G) break;
@@ -597,11 +770,13 @@ __global__ __launch_bounds__(256, 1) void chunk_seg_scan_bf16(int G, int D, cons
       uint4 ah[KS], al[KS];
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
-        float x[8];
         const float4 x0 = *reinterpret_cast<const float4*>(Fg + (long)rowA * DP + 32 * s + 8 * lg);
         const float4 x1 = *reinterpret_cast<const float4*>(Fg + (long)rowA * DP + 32 * s + 8 * lg + 4);
-        x[0] = x0.x; x[1] = x0.y; x[2] = x0.z; x[3] = x0.w; x[4] = x1.x; x[5] = x1.y; x[6] = x1.z; x[7] = x1.w;
-        split8(x, ah[s], al[s]);
+        uint2 h0, l0, h1, l1;
+        split4((f4){x0.x, x0.y, x0.z, x0.w}, h0, l0);
+        split4((f4){x1.x, x1.y, x1.z, x1.w}, h1, l1);
+        ah[s] = make_uint4(h0.x, h0.y, h1.x, h1.y);
+        al[s] = make_uint4(l0.x, l0.y, l1.x, l1.y);
       }
 #pragma unroll
       for (int n = 0; n < NC; ++n) {
@@ -623,106 +798,147 @@ __global__ __launch_bounds__(256, 1) void chunk_seg_scan_bf16(int G, int D, cons
   }
 }
 
-// ---------------------------------------------------------------------------
-// K5
-// ---------------------------------------------------------------------------
-template <bool SP>
-__global__ __launch_bounds__(256) void chunk_out_bf16(
-    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ sk,
-    const float* __restrict__ beta, const float* __restrict__ alpha, int T, int H, int D, int NT, Bf16Ws ws,
+// Segment g reruns its chunks from its start state (sinit[bh*G + g], leading dimension
+// sld; rows / columns >= sld read as 0) and writes the output rows; the last segment
+// writes the final state to ht ([B*H][D][D], rows / columns < D).  Eight waves, one
+// 16-column tile of the state (and of the output) each.
+template <int M, bool FULL>
+__global__ __launch_bounds__(512, 1) void chunk_replay_bf16(
+    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
+    const bf16_t* __restrict__ sk, const bf16_t* __restrict__ sv, const float* __restrict__ beta,
+    const float* __restrict__ alpha, const float* __restrict__ gamma, int T, int H, int D, int NT, int CPS,
+    const uint16_t* __restrict__ Ain, const float* __restrict__ sinit, int sld, float* __restrict__ ht,
     bf16_t* __restrict__ out) {
-  constexpr int M = SP ? 2 * L : L;
-  constexpr int PM = M + 8;
-  constexpr int KS = DP / 32;
-  constexpr int KSM = M / 32;
-  __shared__ __align__(16) uint16_t Ph[4][16 * PM];
-  __shared__ __align__(16) uint16_t Pl[4][16 * PM];
-  __shared__ float lam[M];
-  __shared__ float logd[L];
+  constexpr bool SP = M == 2 * L;
+  constexpr int NB = M / 16;
+  constexpr int NTL = NB * (NB + 1) / 2;
+  __shared__ __align__(16) uint16_t kap[krows_elems<M>()];
+  __shared__ __align__(16) uint16_t nuv[krows_elems<M>()];
+  __shared__ __align__(16) uint16_t qr[L * PK];
+  __shared__ __align__(16) uint16_t At[NTL * 2 * 16 * AP];
+  __shared__ __align__(16) GateTab<M> gt;
 
-  const int c = blockIdx.x, bh = blockIdx.y;
+  const int bh = blockIdx.x, g = blockIdx.y, G = gridDim.y;
   const int b = bh / H, h = bh % H;
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform
   const int lr = lane & 15, lg = lane >> 4;
-  const int t0 = c * L;
-  const long cidx = (long)bh * NT + c;
+  const int col = 16 * w;
+  const int cb = g * CPS, ce = min(NT, cb + CPS);
 
-  if (tid < L) logd[tid] = ws.logd[cidx * L + tid];
-  if (tid < M) {
-    const int t = t0 + samp_t<SP>(tid);
-    float lm = 0.f;
-    if (t < T) lm = samp_r<SP>(tid) ? alpha[(long)(b * T + t) * H + h] : beta[(long)(b * T + t) * H + h];
-    lam[tid] = lm;
-  }
-  // q fragments: rows t0 + 16w + lr
-  uint4 qf[KS];
+  f4 S[DP / 16];
   {
-    const int t = t0 + 16 * w + lr;
-    const bf16_t* qr = q + ((long)(b * T + (t < T ? t : 0)) * H + h) * D;
+    const float* s0 = sinit != nullptr ? sinit + (long)(bh * G + g) * sld * sld : nullptr;
 #pragma unroll
-    for (int s = 0; s < KS; ++s) qf[s] = load8(qr, 32 * s + 8 * lg, D, t < T);
+    for (int r = 0; r < DP / 16; ++r)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = 16 * r + 4 * lg + e, cc = col + lr;
+        S[r][e] = (s0 != nullptr && row < sld && cc < sld) ? s0[(long)row * sld + cc] : 0.f;
+      }
   }
-  __syncthreads();
 
-  const uint16_t* STh = ws.STh + cidx * DP * DP;
-  const uint16_t* STl = ws.STl + cidx * DP * DP;
-  const uint16_t* RTh = ws.RTh + cidx * DP * M;
-  const uint16_t* RTl = ws.RTl + cidx * DP * M;
-
-  // P = mask(q kappa^T) * lam_i * D_t / D_tau_i, staged hi/lo in this wave's LDS rows
-#pragma unroll
-  for (int m = 0; m < M / 16; ++m) {
-    const int i = 16 * m + lr;
-    const int t = t0 + samp_t<SP>(i);
-    const bf16_t* kr = (samp_r<SP>(i) ? sk : k) + ((long)(b * T + (t < T ? t : 0)) * H + h) * D;
-    f4 acc = f4_zero();
-#pragma unroll
-    for (int s = 0; s < KS; ++s) acc = mma_bf16(as_bf8(qf[s]), as_bf8(load8(kr, 32 * s + 8 * lg, D, t < T)), acc);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int tt = 16 * w + 4 * lg + e;
-      const int ti = samp_t<SP>(i);
-      const float p = (ti <= tt) ? lam[i] * expf(logd[tt] - logd[ti]) * acc[e] : 0.f;
-      uint16_t hi, lo;
-      split1(p, hi, lo);
-      Ph[w][(4 * lg + e) * PM + i] = hi;
-      Pl[w][(4 * lg + e) * PM + i] = lo;
+  for (int c = cb; c < ce; ++c) {
+    __syncthreads();   // every wave is done with the previous chunk's operands
+    if constexpr (FULL) {
+      stage_chunk_dma<M, 512, true, true>(q, k, v, sk, sv, beta, alpha, gamma, Ain, T, H, NT, b, h, bh, c, tid, kap,
+                                          nuv, qr, At, gt);
+      __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): this wave's loads have landed in LDS
+    } else {
+      stage_chunk<M, 512, true, true, FULL>(q, k, v, sk, sv, beta, alpha, gamma, Ain, T, H, D, NT, b, h, bh, c, tid,
+                                            kap, nuv, qr, At, gt);
     }
+    __syncthreads();
+    Op Sop[DP / 32];
+    pack_ops<DP / 16>(S, Sop);
+    // q S for the chunk's 64 rows (rows 16 tt + 4 lg + e of the accumulator)
+    f4 qs[L / 16];
+#pragma unroll
+    for (int tt = 0; tt < L / 16; ++tt) {
+      qs[tt] = f4_zero();
+      const uint16_t* qrow = qr + (16 * tt + lr) * PK;
+#pragma unroll
+      for (int s = 0; s < DP / 32; ++s) {
+        const bf16x8 a = rowop_p(qrow, s, lg);
+        qs[tt] = mma_bf16(a, as_bf8(Sop[s].h), qs[tt]);
+        qs[tt] = mma_bf16(a, as_bf8(Sop[s].l), qs[tt]);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    f4 R[NB];
+    tile_residual<M, true>(Sop, kap, nuv, At, gt.el, col, lr, lg, R);
+    Op Rop[NB / 2];
+    pack_ops<NB>(R, Rop);
+
+    // o = e^{l_t} q S + P R, P_ti = 1[tau_i <= t] lam_i e^{l_t - l_tau_i} (q_t . kappa_i),
+    // from P^T tiles (kappa q^T) whose accumulator layout is P's A operand layout
+    const int t0 = c * L;
+#pragma unroll
+    for (int tt = 0; tt < L / 16; ++tt) {
+      const int ns = SP ? tt + 1 : tt / 2 + 1;   // k-steps over samples (samples of tokens <= 16 tt + 15)
+      const int t = 16 * tt + lr;                // P^T column of this lane
+      const uint16_t* qrow = qr + (16 * tt + lr) * PK;
+      f4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = gt.el[16 * tt + 4 * lg + e] * qs[tt][e];
+#pragma unroll
+      for (int s = 0; s < NB / 2; ++s) {
+        if (s < ns) {
+          f4 p[2];
+#pragma unroll
+          for (int hf = 0; hf < 2; ++hf) {
+            const int J = 2 * s + hf;
+            p[hf] = f4_zero();
+#pragma unroll
+            for (int s2 = 0; s2 < DP / 32; ++s2)
+              p[hf] = mma_bf16(rowop(kap + krow<SP>(16 * J + lr), s2, lg), rowop(qrow, s2, lg), p[hf]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int j = 16 * J + 4 * lg + e, tj = samp_t<SP>(j);
+              p[hf][e] = (tj <= t) ? gt.lam[j] * fexp(gt.logd[t] - gt.logd[tj]) * p[hf][e] : 0.f;
+            }
+          }
+          Op Pop[1];
+          pack_ops<2>(p, Pop);
+          o = mma_bf16(as_bf8(Pop[0].h), as_bf8(Rop[s].h), o);
+          o = mma_bf16(as_bf8(Pop[0].h), as_bf8(Rop[s].l), o);
+          o = mma_bf16(as_bf8(Pop[0].l), as_bf8(Rop[s].h), o);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int tg = t0 + 16 * tt + 4 * lg + e;
+        if (tg < T && col + lr < D) out[((long)(b * T + tg) * H + h) * D + col + lr].bits = f32_to_bf16(o[e]);
+      }
+    }
+    // R' from the residual operands (R = hi + lo to about 16 bits)
+#pragma unroll
+    for (int sp = 0; sp < NB / 2; ++sp) {
+      const float4 f0 = *reinterpret_cast<const float4*>(gt.fac + 32 * sp + 4 * lg);
+      const float4 f1 = *reinterpret_cast<const float4*>(gt.fac + 32 * sp + 16 + 4 * lg);
+      f4 y[2] = {unsplit4(make_uint2(Rop[sp].h.x, Rop[sp].h.y), make_uint2(Rop[sp].l.x, Rop[sp].l.y)),
+                 unsplit4(make_uint2(Rop[sp].h.z, Rop[sp].h.w), make_uint2(Rop[sp].l.z, Rop[sp].l.w))};
+      y[0][0] *= f0.x; y[0][1] *= f0.y; y[0][2] *= f0.z; y[0][3] *= f0.w;
+      y[1][0] *= f1.x; y[1][1] *= f1.y; y[1][2] *= f1.z; y[1][3] *= f1.w;
+      Op o1[1];
+      pack_ops<2>(y, o1);
+      Rop[sp] = o1[0];
+    }
+    tile_update<M>(S, Rop, kap, gt.el[L - 1], lr, lg);
   }
-  wave_lds_sync();
 
-  float dt[4];
+  if (ht != nullptr && g == G - 1) {
 #pragma unroll
-  for (int e = 0; e < 4; ++e) dt[e] = expf(logd[16 * w + 4 * lg + e]);
+    for (int r = 0; r < DP / 16; ++r)
 #pragma unroll
-  for (int n = 0; n < DP / 16; ++n) {
-    const int cc = 16 * n + lr;
-    f4 o1 = f4_zero();
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      const uint4 bh_ = *reinterpret_cast<const uint4*>(STh + (long)cc * DP + 32 * s + 8 * lg);
-      const uint4 bl_ = *reinterpret_cast<const uint4*>(STl + (long)cc * DP + 32 * s + 8 * lg);
-      o1 = mma_bf16(as_bf8(qf[s]), as_bf8(bh_), o1);
-      o1 = mma_bf16(as_bf8(qf[s]), as_bf8(bl_), o1);
-    }
-    f4 o2 = f4_zero();
-#pragma unroll
-    for (int s = 0; s < KSM; ++s) {
-      const uint4 ph = *reinterpret_cast<const uint4*>(&Ph[w][lr * PM + 32 * s + 8 * lg]);
-      const uint4 pl = *reinterpret_cast<const uint4*>(&Pl[w][lr * PM + 32 * s + 8 * lg]);
-      const uint4 rh = *reinterpret_cast<const uint4*>(RTh + (long)cc * M + 32 * s + 8 * lg);
-      const uint4 rl = *reinterpret_cast<const uint4*>(RTl + (long)cc * M + 32 * s + 8 * lg);
-      o2 = mma_bf16(as_bf8(ph), as_bf8(rh), o2);
-      o2 = mma_bf16(as_bf8(ph), as_bf8(rl), o2);
-      o2 = mma_bf16(as_bf8(pl), as_bf8(rh), o2);
-    }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int t = t0 + 16 * w + 4 * lg + e;
-      if (t < T && cc < D) out[((long)(b * T + t) * H + h) * D + cc].bits = f32_to_bf16(dt[e] * o1[e] + o2[e]);
-    }
+      for (int e = 0; e < 4; ++e) {
+        const int row = 16 * r + 4 * lg + e, cc = col + lr;
+        if (row < D && cc < D) ht[((long)bh * D + row) * D + cc] = S[r][e];
+      }
   }
 }
+
+}  // namespace
 
 // ---------------------------------------------------------------------------
 // Host side
@@ -730,37 +946,25 @@ __global__ __launch_bounds__(256) void chunk_out_bf16(
 
 size_t chunk_bf16_workspace_bytes(int B, int T, int H, int has_sparse) {
   const size_t NT = (T + L - 1) / L;
-  const size_t M = has_sparse ? 2 * L : L;
+  const size_t NB = has_sparse ? 2 * L / 16 : L / 16;
+  const size_t ntl = NB * (NB + 1) / 2;
   const size_t n = (size_t)B * H * NT;
-  size_t total = 0;
-  total += 2 * n * M * DP * 2;     // Whi, Wlo
-  total += n * M * DP * 4;         // U
-  total += n * DP * M * 2;         // KT
-  total += 2 * n * DP * DP * 2;    // STh, STl
-  total += 2 * n * DP * M * 2;     // RTh, RTl
-  total += n * L * 4;              // logd
+  size_t total = n * ntl * 1024;   // A tiles, hi + lo
   const size_t G = seg_count(B * H, (int)NT);
   if (G > 1) total += 3 * (size_t)B * H * G * DP * DP * 4;   // segment maps P, Phi and start states
-  return total + 256 * 12;
+  return total + 256 * 4;
 }
 
-template <bool SP>
+template <int M, bool FULL>
 static hipError_t launch_bf16_t(const ChunkArgs& a, hipStream_t st) {
+  constexpr int NB = M / 16;
+  constexpr int NTL = NB * (NB + 1) / 2;
   const int NT = (a.T + L - 1) / L;
-  const int M = SP ? 2 * L : L;
   const size_t n = (size_t)a.B * a.H * NT;
   auto align = [](char* p) { return (char*)(((uintptr_t)p + 255) & ~(uintptr_t)255); };
   char* p = align((char*)a.workspace);
-  Bf16Ws ws;
-  ws.Whi = (uint16_t*)p; p = align(p + n * M * DP * 2);
-  ws.Wlo = (uint16_t*)p; p = align(p + n * M * DP * 2);
-  ws.U = (float*)p;      p = align(p + n * M * DP * 4);
-  ws.KT = (uint16_t*)p;  p = align(p + n * DP * M * 2);
-  ws.STh = (uint16_t*)p; p = align(p + n * DP * DP * 2);
-  ws.STl = (uint16_t*)p; p = align(p + n * DP * DP * 2);
-  ws.RTh = (uint16_t*)p; p = align(p + n * DP * M * 2);
-  ws.RTl = (uint16_t*)p; p = align(p + n * DP * M * 2);
-  ws.logd = (float*)p;    p = align(p + n * L * 4);
+  uint16_t* Aws = (uint16_t*)p;
+  p = align(p + n * NTL * 1024);
   const int BH = a.B * a.H;
   const int G = seg_count(BH, NT);
   const int CPS = (NT + G - 1) / G;
@@ -771,24 +975,26 @@ static hipError_t launch_bf16_t(const ChunkArgs& a, hipStream_t st) {
   const bf16_t* v = (const bf16_t*)a.v;
   const bf16_t* sk = (const bf16_t*)a.sparse_k;
   const bf16_t* sv = (const bf16_t*)a.sparse_v;
-  chunk_intra_bf16<SP><<<dim3(NT, BH), 256, 0, st>>>(k, v, sk, sv, a.beta, a.alpha, a.gamma, a.T, a.H, a.D, NT, ws);
+  chunk_inv_bf16<M, FULL><<<dim3(NT, BH), 256, 0, st>>>(k, sk, a.beta, a.alpha, a.gamma, a.T, a.H, a.D, NT, Aws);
   if (G == 1) {
-    chunk_seg_bf16<SP, SEG_FULL><<<dim3(BH, 1, 1), 256, 0, st>>>(a.beta, a.alpha, a.T, a.H, a.D, NT, NT, ws,
-                                                               a.initial_state, a.D, nullptr, a.final_state);
+    chunk_replay_bf16<M, FULL><<<dim3(BH, 1), 512, 0, st>>>(q, k, v, sk, sv, a.beta, a.alpha, a.gamma, a.T, a.H, a.D, NT,
+                                                      NT, Aws, a.initial_state, a.D, a.final_state, (bf16_t*)a.out);
   } else {
-    chunk_seg_bf16<SP, SEG_MAPS><<<dim3(BH, G, 2), 256, 0, st>>>(a.beta, a.alpha, a.T, a.H, a.D, NT, CPS, ws, nullptr,
-                                                               0, maps, nullptr);
+    chunk_maps_bf16<M, FULL><<<dim3(BH, G, 2), 512, 0, st>>>(k, v, sk, sv, a.beta, a.alpha, a.gamma, a.T, a.H, a.D, NT, CPS,
+                                                    Aws, maps);
     chunk_seg_scan_bf16<<<dim3(BH), 256, 0, st>>>(G, a.D, a.initial_state, maps, sinit);
-    chunk_seg_bf16<SP, SEG_FULL><<<dim3(BH, G, 1), 256, 0, st>>>(a.beta, a.alpha, a.T, a.H, a.D, NT, CPS, ws, sinit,
-                                                               DP, nullptr, a.final_state);
+    chunk_replay_bf16<M, FULL><<<dim3(BH, G), 512, 0, st>>>(q, k, v, sk, sv, a.beta, a.alpha, a.gamma, a.T, a.H, a.D, NT,
+                                                      CPS, Aws, sinit, DP, a.final_state, (bf16_t*)a.out);
   }
-  chunk_out_bf16<SP><<<dim3(NT, BH), 256, 0, st>>>(q, k, sk, a.beta, a.alpha, a.T, a.H, a.D, NT, ws,
-                                                   (bf16_t*)a.out);
   return hipGetLastError();
 }
 
 hipError_t launch_chunk_bf16(const ChunkArgs& a, hipStream_t st) {
-  return a.sparse_k != nullptr ? launch_bf16_t<true>(a, st) : launch_bf16_t<false>(a, st);
+  const bool sp = a.sparse_k != nullptr;
+  // direct-to-LDS staging addresses a head's rows with 32-bit byte offsets
+  const long span = (long)(a.T + L) * a.H * DP * 2;
+  if (a.D == DP && span < 0x7fffffffL) return sp ? launch_bf16_t<2 * L, true>(a, st) : launch_bf16_t<L, true>(a, st);
+  return sp ? launch_bf16_t<2 * L, false>(a, st) : launch_bf16_t<L, false>(a, st);
 }
 
 }  // namespace sgsa
