@@ -719,82 +719,92 @@ __global__ __launch_bounds__(512, 1) void chunk_maps_bf16(const bf16_t* __restri
 }
 
 // The segment start states: sinit[bh*G + g] for g < G, from h0 ([B*H][D][D] or
-// NULL) and the maps of chunk_maps_bf16 (maps[0]: P, maps[1]: Phi).
-// S <- Phi S + P runs in fp32 with Phi and S split into bf16 hi + lo.
-__global__ __launch_bounds__(256, 1) void chunk_seg_scan_bf16(int G, int D, const float* __restrict__ h0,
-                                                            const float* __restrict__ maps, float* __restrict__ sinit) {
-  constexpr int PB = DP + 8;
-  constexpr int NC = DP / 16;
-  constexpr int KS = DP / 32;
-  __shared__ __align__(16) uint16_t Sh[DP * PB];   // S transposed [col][row], hi
-  __shared__ __align__(16) uint16_t Sl[DP * PB];
+// NULL) and the maps of chunk_maps_bf16 (maps[0]: P, maps[1]: Phi), as
+// S(g+1) = Phi_g S(g) + P_g in fp32 (Phi and S enter the MFMAs as hi + lo bf16).
+// Grid (B*H, DP/16): block y owns the 16 state columns 16y.., wave w the row tiles 2w,
+// 2w+1 of them; the column tile passes between the waves through LDS as B operands,
+// and each wave loads the next step's Phi rows and P tile while the current step runs.
+__global__ __launch_bounds__(256) void chunk_seg_scan_bf16(int G, int D, const float* __restrict__ h0,
+                                                         const float* __restrict__ maps, float* __restrict__ sinit) {
+  __shared__ __align__(16) uint4 sop[DP / 32][64][2];   // the column tile as the operand of each k step
   const int bh = blockIdx.x, BH = gridDim.x;
+  const int col = 16 * blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lr = lane & 15, lg = lane >> 4;
   const float* P = maps;
   const float* Phi = maps + (long)BH * G * DP * DP;
-  f4 S[2][NC];
+  f4 S[2];   // row tiles 2w, 2w+1: S[16(2w+u) + 4lg + e][col + lr]
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
+  for (int u = 0; u < 2; ++u)
 #pragma unroll
-    for (int n = 0; n < NC; ++n) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int row = 32 * w + 16 * u + 4 * lg + e, col = 16 * n + lr;
-        S[u][n][e] = (h0 != nullptr && row < D && col < D) ? h0[((long)bh * D + row) * D + col] : 0.f;
-      }
+    for (int e = 0; e < 4; ++e) {
+      const int row = 16 * (2 * w + u) + 4 * lg + e, cc = col + lr;
+      S[u][e] = (h0 != nullptr && row < D && cc < D) ? h0[((long)bh * D + row) * D + cc] : 0.f;
     }
-  }
+  // Phi rows of the wave's row tiles in the accumulator k order (step s: columns
+  // 32s + 4lg .. +3 and 32s + 16 + 4lg .. +3), and the P tile
+  float4 fa[2][DP / 32][2];
+  f4 pa[2];
+  auto load = [&](int g) __attribute__((always_inline)) {
+    const float* Fg = Phi + (long)(bh * G + g) * DP * DP;
+    const float* Pg = P + (long)(bh * G + g) * DP * DP;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const float* fr = Fg + (long)(16 * (2 * w + u) + lr) * DP;
+#pragma unroll
+      for (int s = 0; s < DP / 32; ++s) {
+        fa[u][s][0] = *reinterpret_cast<const float4*>(fr + 32 * s + 4 * lg);
+        fa[u][s][1] = *reinterpret_cast<const float4*>(fr + 32 * s + 16 + 4 * lg);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) pa[u][e] = Pg[(long)(16 * (2 * w + u) + 4 * lg + e) * DP + col + lr];
+    }
+  };
+  if (G > 1) load(0);
   for (int g = 0; g < G; ++g) {
     float* dst = sinit + (long)(bh * G + g) * DP * DP;
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
+    for (int u = 0; u < 2; ++u)
 #pragma unroll
-      for (int n = 0; n < NC; ++n) {
-        const int row0 = 32 * w + 16 * u + 4 * lg, col = 16 * n + lr;
-        uint2 hh, ll;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) dst[(long)(row0 + e) * DP + col] = S[u][n][e];
-        split4(S[u][n], hh, ll);
-        *reinterpret_cast<uint2*>(&Sh[col * PB + row0]) = hh;
-        *reinterpret_cast<uint2*>(&Sl[col * PB + row0]) = ll;
-      }
-    }
+      for (int e = 0; e < 4; ++e) dst[(long)(16 * (2 * w + u) + 4 * lg + e) * DP + col + lr] = S[u][e];
     if (g + 1 == G) break;
+    // this wave's row tiles 2w, 2w+1 are the halves of k step w
+    {
+      uint2 ha, la, hb, lb;
+      split4(S[0], ha, la);
+      split4(S[1], hb, lb);
+      sop[w][lane][0] = make_uint4(ha.x, ha.y, hb.x, hb.y);
+      sop[w][lane][1] = make_uint4(la.x, la.y, lb.x, lb.y);
+    }
     __syncthreads();
-    const float* Pg = P + (long)(bh * G + g) * DP * DP;
-    const float* Fg = Phi + (long)(bh * G + g) * DP * DP;
+    uint4 ah[2][DP / 32], al[2][DP / 32];
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int rowA = 32 * w + 16 * u + lr;   // A operand row (Phi)
-      uint4 ah[KS], al[KS];
+    for (int u = 0; u < 2; ++u)
 #pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        const float4 x0 = *reinterpret_cast<const float4*>(Fg + (long)rowA * DP + 32 * s + 8 * lg);
-        const float4 x1 = *reinterpret_cast<const float4*>(Fg + (long)rowA * DP + 32 * s + 8 * lg + 4);
-        uint2 h0, l0, h1, l1;
-        split4((f4){x0.x, x0.y, x0.z, x0.w}, h0, l0);
-        split4((f4){x1.x, x1.y, x1.z, x1.w}, h1, l1);
-        ah[s] = make_uint4(h0.x, h0.y, h1.x, h1.y);
-        al[s] = make_uint4(l0.x, l0.y, l1.x, l1.y);
+      for (int s2 = 0; s2 < DP / 32; ++s2) {
+        uint2 h0_, l0_, h1_, l1_;
+        const float4 x0 = fa[u][s2][0], x1 = fa[u][s2][1];
+        split4((f4){x0.x, x0.y, x0.z, x0.w}, h0_, l0_);
+        split4((f4){x1.x, x1.y, x1.z, x1.w}, h1_, l1_);
+        ah[u][s2] = make_uint4(h0_.x, h0_.y, h1_.x, h1_.y);
+        al[u][s2] = make_uint4(l0_.x, l0_.y, l1_.x, l1_.y);
       }
+    const f4 p0 = pa[0], p1 = pa[1];
+    if (g + 2 < G) load(g + 1);
+    f4 acc[2] = {p0, p1};
 #pragma unroll
-      for (int n = 0; n < NC; ++n) {
-        f4 acc;
+    for (int s2 = 0; s2 < DP / 32; ++s2) {
+      const uint4 bh_ = sop[s2][lane][0], bl_ = sop[s2][lane][1];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) acc[e] = Pg[(long)(32 * w + 16 * u + 4 * lg + e) * DP + 16 * n + lr];
-#pragma unroll
-        for (int s = 0; s < KS; ++s) {
-          const uint4 bh_ = *reinterpret_cast<const uint4*>(&Sh[(16 * n + lr) * PB + 32 * s + 8 * lg]);
-          const uint4 bl_ = *reinterpret_cast<const uint4*>(&Sl[(16 * n + lr) * PB + 32 * s + 8 * lg]);
-          acc = mma_bf16(as_bf8(ah[s]), as_bf8(bh_), acc);
-          acc = mma_bf16(as_bf8(ah[s]), as_bf8(bl_), acc);
-          acc = mma_bf16(as_bf8(al[s]), as_bf8(bh_), acc);
-        }
-        S[u][n] = acc;
+      for (int u = 0; u < 2; ++u) {
+        acc[u] = mma_bf16(as_bf8(ah[u][s2]), as_bf8(bh_), acc[u]);
+        acc[u] = mma_bf16(as_bf8(ah[u][s2]), as_bf8(bl_), acc[u]);
+        acc[u] = mma_bf16(as_bf8(al[u][s2]), as_bf8(bh_), acc[u]);
       }
     }
-    __syncthreads();   // Sh/Sl are rewritten next
+    S[0] = acc[0];
+    S[1] = acc[1];
+    __syncthreads();   // sop is rewritten next step
   }
 }
 
@@ -869,48 +879,72 @@ __global__ __launch_bounds__(512, 1) void chunk_replay_bf16(
     Op Rop[NB / 2];
     pack_ops<NB>(R, Rop);
 
-    // o = e^{l_t} q S + P R, P_ti = 1[tau_i <= t] lam_i e^{l_t - l_tau_i} (q_t . kappa_i),
-    // from P^T tiles (kappa q^T) whose accumulator layout is P's A operand layout
-    const int t0 = c * L;
-#pragma unroll
-    for (int tt = 0; tt < L / 16; ++tt) {
-      const int ns = SP ? tt + 1 : tt / 2 + 1;   // k-steps over samples (samples of tokens <= 16 tt + 15)
+    // o = e^{l_t} q S + P R, P_ti = 1[tau_i <= t] lam_i e^{l_t - l_tau_i} (q_t . kappa_i).
+    // The P operands depend only on the chunk: the waves share them out -- the operand of
+    // (row tile tt, sample step s) is built from P^T tiles 2s, 2s+1 (kappa q^T, whose
+    // accumulator layout is P's A operand layout) -- and pass them through the A tile
+    // area, free once every wave has formed R.
+    constexpr int NCB = SP ? 10 : 6;   // (tt, s) pairs: s < tt + 1 (SP) or s < tt / 2 + 1
+    uint4* pst = reinterpret_cast<uint4*>(At);   // [NCB][64 lanes][hi, lo]
+    __syncthreads();   // every wave is done with the A tiles
+    for (int cb2 = w; cb2 < NCB; cb2 += 8) {
+      int tt = 0, s0 = cb2;
+      while (s0 >= (SP ? tt + 1 : tt / 2 + 1)) { s0 -= (SP ? tt + 1 : tt / 2 + 1); ++tt; }
       const int t = 16 * tt + lr;                // P^T column of this lane
       const uint16_t* qrow = qr + (16 * tt + lr) * PK;
+      f4 p[2];
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        const int J = 2 * s0 + hf;
+        p[hf] = f4_zero();
+#pragma unroll
+        for (int s2 = 0; s2 < DP / 32; ++s2)
+          p[hf] = mma_bf16(rowop(kap + krow<SP>(16 * J + lr), s2, lg), rowop(qrow, s2, lg), p[hf]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int j = 16 * J + 4 * lg + e, tj = samp_t<SP>(j);
+          p[hf][e] = (tj <= t) ? gt.lam[j] * fexp(gt.logd[t] - gt.logd[tj]) * p[hf][e] : 0.f;
+        }
+      }
+      Op Pop[1];
+      pack_ops<2>(p, Pop);
+      pst[(cb2 * 64 + lane) * 2] = Pop[0].h;
+      pst[(cb2 * 64 + lane) * 2 + 1] = Pop[0].l;
+    }
+    __syncthreads();
+    const int t0 = c * L;
+    const bool whole = t0 + L <= T;   // block-uniform: every output row of the chunk exists
+    bf16_t* orow = out + ((long)(b * T + t0) * H + h) * D + col + lr;
+    const long ostep = (long)H * D;   // between consecutive tokens
+#pragma unroll
+    for (int tt = 0; tt < L / 16; ++tt) {
+      const int ns = SP ? tt + 1 : tt / 2 + 1;
+      const int cbase = SP ? tt * (tt + 1) / 2 : (tt < 2 ? tt : 2 + 2 * (tt - 2));
       f4 o;
 #pragma unroll
       for (int e = 0; e < 4; ++e) o[e] = gt.el[16 * tt + 4 * lg + e] * qs[tt][e];
 #pragma unroll
       for (int s = 0; s < NB / 2; ++s) {
         if (s < ns) {
-          f4 p[2];
-#pragma unroll
-          for (int hf = 0; hf < 2; ++hf) {
-            const int J = 2 * s + hf;
-            p[hf] = f4_zero();
-#pragma unroll
-            for (int s2 = 0; s2 < DP / 32; ++s2)
-              p[hf] = mma_bf16(rowop(kap + krow<SP>(16 * J + lr), s2, lg), rowop(qrow, s2, lg), p[hf]);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const int j = 16 * J + 4 * lg + e, tj = samp_t<SP>(j);
-              p[hf][e] = (tj <= t) ? gt.lam[j] * fexp(gt.logd[t] - gt.logd[tj]) * p[hf][e] : 0.f;
-            }
-          }
-          Op Pop[1];
-          pack_ops<2>(p, Pop);
-          o = mma_bf16(as_bf8(Pop[0].h), as_bf8(Rop[s].h), o);
-          o = mma_bf16(as_bf8(Pop[0].h), as_bf8(Rop[s].l), o);
-          o = mma_bf16(as_bf8(Pop[0].l), as_bf8(Rop[s].h), o);
+          const uint4 ph = pst[((cbase + s) * 64 + lane) * 2], pl = pst[((cbase + s) * 64 + lane) * 2 + 1];
+          o = mma_bf16(as_bf8(ph), as_bf8(Rop[s].h), o);
+          o = mma_bf16(as_bf8(ph), as_bf8(Rop[s].l), o);
+          o = mma_bf16(as_bf8(pl), as_bf8(Rop[s].h), o);
         }
-        __builtin_amdgcn_sched_barrier(0);
       }
+      if (FULL && whole) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int tg = t0 + 16 * tt + 4 * lg + e;
-        if (tg < T && col + lr < D) out[((long)(b * T + tg) * H + h) * D + col + lr].bits = f32_to_bf16(o[e]);
+        for (int e = 0; e < 4; ++e) orow[(16 * tt + 4 * lg + e) * ostep].bits = f32_to_bf16(o[e]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int tl = 16 * tt + 4 * lg + e;
+          if (t0 + tl < T && col + lr < D) orow[tl * ostep].bits = f32_to_bf16(o[e]);
+        }
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
+
     // R' from the residual operands (R = hi + lo to about 16 bits)
 #pragma unroll
     for (int sp = 0; sp < NB / 2; ++sp) {
@@ -982,7 +1016,7 @@ static hipError_t launch_bf16_t(const ChunkArgs& a, hipStream_t st) {
   } else {
     chunk_maps_bf16<M, FULL><<<dim3(BH, G, 2), 512, 0, st>>>(k, v, sk, sv, a.beta, a.alpha, a.gamma, a.T, a.H, a.D, NT, CPS,
                                                     Aws, maps);
-    chunk_seg_scan_bf16<<<dim3(BH), 256, 0, st>>>(G, a.D, a.initial_state, maps, sinit);
+    chunk_seg_scan_bf16<<<dim3(BH, DP / 16), 256, 0, st>>>(G, a.D, a.initial_state, maps, sinit);
     chunk_replay_bf16<M, FULL><<<dim3(BH, G), 512, 0, st>>>(q, k, v, sk, sv, a.beta, a.alpha, a.gamma, a.T, a.H, a.D, NT,
                                                       CPS, Aws, sinit, DP, a.final_state, (bf16_t*)a.out);
   }
