@@ -167,15 +167,36 @@ __global__ __launch_bounds__(256) void key_norm_max_kernel(const X* __restrict__
   __shared__ float red[4];
   const int bh = blockIdx.x / KNCH, c = blockIdx.x % KNCH, b = bh / H, h = bh % H;
   const int sub = threadIdx.x & 15, rw = threadIdx.x >> 4;
+  constexpr int EPV = 16 / (int)sizeof(X);   // elements per 16-byte load
   float m = 0.f;
+  const bool vec = D % EPV == 0 && ((uintptr_t)k & 15u) == 0;
   for (int j0 = c; j0 < Tk; j0 += KNCH * 16) {   // trip count uniform over the block
     const int j = j0 + KNCH * rw;
     float s = 0.f;
     if (j < Tk) {
       const X* row = k + ((long)(b * Tk + j) * H + h) * D;
-      for (int d = sub; d < D; d += 16) {
-        const float x = ld(row, d);
-        s = fmaf(x, x, s);
+      if (vec) {   // 16 lanes read a row in 16-byte pieces
+        for (int d = EPV * sub; d < D; d += 16 * EPV) {
+          const uint4 u = *reinterpret_cast<const uint4*>(row + d);
+          if constexpr (sizeof(X) == 2) {
+            const uint32_t wv[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const float lo = __uint_as_float(wv[q] << 16), hi = __uint_as_float(wv[q] & 0xffff0000u);
+              s = fmaf(lo, lo, s);
+              s = fmaf(hi, hi, s);
+            }
+          } else {
+            const float xs[4] = {__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z), __uint_as_float(u.w)};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) s = fmaf(xs[q], xs[q], s);
+          }
+        }
+      } else {
+        for (int d = sub; d < D; d += 16) {
+          const float x = ld(row, d);
+          s = fmaf(x, x, s);
+        }
       }
     }
     m = fmaxf(m, group_sum(s, 16));
@@ -214,6 +235,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LIST && !FB
 
   const int BH = a.B * a.H;
   const int bid = blockIdx.x;
+  if constexpr (FB) {
+    if (a.flags[bid] == 0) return;   // block-uniform: only the flagged blocks are redone
+  }
   const int bh = bid % BH;   // with B*H a multiple of 8, a head always lands on the same XCD
   int qb = nqb - 1 - bid / BH;   // heaviest (latest) query blocks first
   if (DUMP) qb = (a.dump_row0 / QB) + bid / BH;
@@ -339,9 +363,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LIST && !FB
   }
 
   const int topk = a.top_k;
-  if constexpr (FB) {
-    if (a.flags[bid] == 0) return;   // block-uniform
-  }
   __syncthreads();   // qnorm visible
   float kmx2 = lane < KNCH ? a.kmax[(long)bh * KNCH + lane] : 0.f;
   const float kmx = sqrtf(wave_max(kmx2));
