@@ -656,9 +656,8 @@ __device__ __forceinline__ void maps_pass(const bf16_t* __restrict__ k, const bf
                                           const float* __restrict__ beta, const float* __restrict__ alpha,
                                           const float* __restrict__ gamma, int T, int H, int D, int NT, int CPS,
                                           const uint16_t* __restrict__ Ain, float* __restrict__ dst, uint16_t* kap,
-                                          uint16_t* nuv, uint16_t* At, GateTab<M>& gt) {
+                                          uint16_t* nuv, uint16_t* At, GateTab<M>& gt, int bh, int g) {
   constexpr int NB = M / 16;
-  const int bh = blockIdx.x, g = blockIdx.y;
   const int b = bh / H, h = bh % H;
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform
   const int lr = lane & 15, lg = lane >> 4;
@@ -696,14 +695,17 @@ __device__ __forceinline__ void maps_pass(const bf16_t* __restrict__ k, const bf
     for (int e = 0; e < 4; ++e) dst[(long)(16 * r + 4 * lg + e) * DP + col + lr] = S[r][e];
 }
 
-// The maps of segment g: blockIdx.z = 0 builds P, 1 builds Phi; the end states go to sout
-// ([P; Phi] x [B*H][G][DP][DP] fp32).
+// The maps: one block builds P, one Phi, for each (b*h, segment) pair; the end states go
+// to sout ([P; Phi] x [B*H][G][DP][DP] fp32).  Block ids go to the XCDs round-robin, so
+// the P and Phi blocks of a pair get ids i and i + 8: the same XCD, running side by side,
+// so the second reads the chunk operands from that XCD's L2.  1-D grid of
+// 16 ceil(B*H*G / 8) blocks.
 template <int M, bool FULL>
 __global__ __launch_bounds__(512, 1) void chunk_maps_bf16(const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
                                                         const bf16_t* __restrict__ sk, const bf16_t* __restrict__ sv,
                                                         const float* __restrict__ beta, const float* __restrict__ alpha,
                                                         const float* __restrict__ gamma, int T, int H, int D, int NT,
-                                                        int CPS, const uint16_t* __restrict__ Ain,
+                                                        int CPS, int BH, int G, const uint16_t* __restrict__ Ain,
                                                         float* __restrict__ sout) {
   constexpr int NB = M / 16;
   constexpr int NTL = NB * (NB + 1) / 2;
@@ -711,11 +713,16 @@ __global__ __launch_bounds__(512, 1) void chunk_maps_bf16(const bf16_t* __restri
   __shared__ __align__(16) uint16_t nuv[krows_elems<M>()];
   __shared__ __align__(16) uint16_t At[NTL * 2 * 16 * AP];
   __shared__ __align__(16) GateTab<M> gt;
-  float* dst = sout + (long)((blockIdx.z * gridDim.x + blockIdx.x) * gridDim.y + blockIdx.y) * DP * DP;
-  if (blockIdx.z == 1)   // block-uniform
-    maps_pass<M, FULL, true>(k, v, sk, sv, beta, alpha, gamma, T, H, D, NT, CPS, Ain, dst, kap, nuv, At, gt);
+  const int pid = blockIdx.x;
+  const int z = (pid >> 3) & 1;                       // 0: P, 1: Phi
+  const int pair = (pid >> 4) * 8 + (pid & 7);        // (b*h, segment) pair, b*h fastest
+  if (pair >= BH * G) return;                         // block-uniform
+  const int bh = pair % BH, g = pair / BH;
+  float* dst = sout + (long)((z * BH + bh) * G + g) * DP * DP;
+  if (z == 1)
+    maps_pass<M, FULL, true>(k, v, sk, sv, beta, alpha, gamma, T, H, D, NT, CPS, Ain, dst, kap, nuv, At, gt, bh, g);
   else
-    maps_pass<M, FULL, false>(k, v, sk, sv, beta, alpha, gamma, T, H, D, NT, CPS, Ain, dst, kap, nuv, At, gt);
+    maps_pass<M, FULL, false>(k, v, sk, sv, beta, alpha, gamma, T, H, D, NT, CPS, Ain, dst, kap, nuv, At, gt, bh, g);
 }
 
 // The segment start states: sinit[bh*G + g] for g < G, from h0 ([B*H][D][D] or
@@ -1014,8 +1021,8 @@ static hipError_t launch_bf16_t(const ChunkArgs& a, hipStream_t st) {
     chunk_replay_bf16<M, FULL><<<dim3(BH, 1), 512, 0, st>>>(q, k, v, sk, sv, a.beta, a.alpha, a.gamma, a.T, a.H, a.D, NT,
                                                       NT, Aws, a.initial_state, a.D, a.final_state, (bf16_t*)a.out);
   } else {
-    chunk_maps_bf16<M, FULL><<<dim3(BH, G, 2), 512, 0, st>>>(k, v, sk, sv, a.beta, a.alpha, a.gamma, a.T, a.H, a.D, NT, CPS,
-                                                    Aws, maps);
+    chunk_maps_bf16<M, FULL><<<dim3(16 * ((BH * G + 7) / 8)), 512, 0, st>>>(
+        k, v, sk, sv, a.beta, a.alpha, a.gamma, a.T, a.H, a.D, NT, CPS, BH, G, Aws, maps);
     chunk_seg_scan_bf16<<<dim3(BH, DP / 16), 256, 0, st>>>(G, a.D, a.initial_state, maps, sinit);
     chunk_replay_bf16<M, FULL><<<dim3(BH, G), 512, 0, st>>>(q, k, v, sk, sv, a.beta, a.alpha, a.gamma, a.T, a.H, a.D, NT,
                                                       CPS, Aws, sinit, DP, a.final_state, (bf16_t*)a.out);
