@@ -129,6 +129,34 @@ int sgsa_score_topk_noalloc(int dtype, int B, int Tq, int Tk, int H, int D, int 
                             int32_t* indices, float* scores, float* top2, int32_t* counts,
                             int32_t* split, int sorted, void* stream);
 
+/* Masked form of sgsa_score_topk: the padding masks of SparseRetriever.forward
+ * (modelings/modeling_sgsa.py:421-428: valid = causal & key_valid &
+ * query_valid) and of TopKSparseKVReuseAttention.forward
+ * (modelings/hybrid_dense_delta_topk.py:343-349 with _merge_masks :153-175:
+ * future keys and padded keys masked, no query mask).  key_mask [B,Tk] and
+ * query_mask [B,Tq] are bytes, nonzero = valid; either may be NULL (all
+ * valid).  Row (b,h,r) has nv valid keys.  kq_rule 0 (retriever, :159-160): the
+ * row takes kq = min(top_k, max(1, max over the batch of nv)) slots; kq_rule 1
+ * (hybrid, :348): kq = top_k.  The first counts = min(kq, nv) slots hold the
+ * selected valid keys (ties to the lowest key index; sorted as
+ * sgsa_score_topk, or in an unspecified order with sorted = 0); slots
+ * [counts, kq) hold the row's lowest-index invalid keys with score -FLT_MAX
+ * (the reference fills invalid scores with finfo.min, which tie); slots >= kq
+ * hold index 0 and -FLT_MAX (:151-153).  slot_valid [B,H,Tq,top_k] (may be
+ * NULL) receives 1 for the selected slots and 0 elsewhere; fill [B,H,Tq] (may
+ * be NULL) receives kq.  kv_layout: k is [B,Tk,H,D] (0) or [B,H,Tk,D] (1, the
+ * hybrid's dense-layer KV).  counts is required; top2 as sgsa_score_topk.
+ * Needs sgsa_score_topk_masked_workspace_size() bytes (with has_key_mask or
+ * kv_layout 1 it includes a copy of the keys in valid-first order). */
+int sgsa_score_topk_masked_workspace_size(int dtype, int B, int Tq, int Tk, int H, int D, int has_key_mask,
+                                          int kv_layout, size_t* bytes);
+int sgsa_score_topk_masked(int dtype, int B, int Tq, int Tk, int H, int D, int top_k,
+                           int causal, int q_offset, float scale, int scale_mode, int kq_rule, int kv_layout,
+                           const void* q, const void* k, const uint8_t* key_mask, const uint8_t* query_mask,
+                           int32_t* indices, float* scores, uint8_t* slot_valid, float* top2,
+                           int32_t* counts, int32_t* fill, int sorted,
+                           void* workspace, size_t workspace_bytes, void* stream);
+
 /* Known-answer hook: writes the exact fp32 scores sgsa_score_topk selects on,
  * for query rows [row0, row0+rows), to out [B,H,rows,Tk]; keys outside the
  * causal range get -FLT_MAX. */
@@ -162,6 +190,23 @@ int sgsa_sparse_gather(int dtype, int B, int Tq, int Tk, int H, int D, int top_k
                        void* k_hat, void* v_hat, void* write_key, float* alpha,
                        float* weights, float* diag,
                        void* workspace, size_t workspace_bytes, void* stream);
+
+/* sgsa_sparse_gather over the output of sgsa_score_topk_masked: counts is
+ * its fill (kq slots per row); slot_valid (may be NULL) zeroes the weight of
+ * the invalid slots before the renormalisation (the retriever's
+ * softmax * valid / sum, modelings/modeling_sgsa.py:126-128).  With
+ * slot_valid = NULL every filled slot takes its softmax weight, as the
+ * hybrid's probabilities do (hybrid_dense_delta_topk.py:350): the -FLT_MAX
+ * fills weigh 0 unless a row has no valid key, which then averages its kq
+ * filled keys.  kv_layout: k and v are [B,Tk,H,D] (0) or [B,H,Tk,D] (1);
+ * self_key stays [B,Tq,H,D]. */
+int sgsa_sparse_gather_masked(int dtype, int B, int Tq, int Tk, int H, int D, int top_k, int q_offset,
+                              int kv_layout, const void* k, const void* v, const void* self_key,
+                              const int32_t* indices, const float* scores, const uint8_t* slot_valid,
+                              const float* top2, const int32_t* counts, const float* budget, int write_mode,
+                              float alpha_max, float tau_c, int local_window, int sink_size, void* k_hat,
+                              void* v_hat, void* write_key, float* alpha, float* weights, float* diag,
+                              void* workspace, size_t workspace_bytes, void* stream);
 
 /* Scores at given keys: for every query row and slot i < counts[row],
  * scores[row,i] = (q_row . k[indices[row,i]]) * scale' with fp32 accumulation,

@@ -494,17 +494,20 @@ def sgsa_layer_forward(
     use_chunk: bool = False,
     chunk_size: int = 64,
     block_rows: int = 256,
+    attention_mask: Optional[Tensor] = None,
 ) -> Dict[str, Tensor]:
     """Op-level SGSA layer forward: retrieval -> gate -> state update.
 
     Mirrors SGSABlock.forward's attention half (modelings/modeling_sgsa.py:669-684)
-    with the projections taken as inputs: retrieval on (q_ret, k, v), write key
-    and alpha (:546-552), then the recurrent state update (naive.py, or the
+    with the projections taken as inputs: retrieval on (q_ret, k, v) under the
+    optional padding mask [B,T] (:672-675 pass it to the retriever only), write
+    key and alpha (:546-552), then the recurrent state update (naive.py, or the
     chunk form when ``use_chunk``).  Inputs are upcast to fp32.
     """
     f = lambda x: None if x is None else x.float()
     q, k, v, q_ret, beta, gamma, budget_logits = map(f, (q, k, v, q_ret, beta, gamma, budget_logits))
-    ret = token_topk_retrieval(q_ret, k, v, top_k, tau_c=tau_c, block_rows=block_rows)
+    ret = token_topk_retrieval(q_ret, k, v, top_k, tau_c=tau_c, block_rows=block_rows,
+                               attention_mask=attention_mask)
     wk = write_key(ret["k_hat"], k, write_mode)
     alpha = compute_alpha(ret["diagnostics"]["concentration"], ret["diagnostics"]["novelty"],
                           budget_logits, wk, ret["v_hat"], alpha_max)

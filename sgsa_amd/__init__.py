@@ -13,12 +13,14 @@ The compiled library (libsgsa_hip.so) is required; there is no fallback path.
 """
 
 from .ops import ChunkSGSAFunction, chunk_sgsa, chunk_sgsa_fwd
-from .retrieval import (SparseRetriever, block_retrieve, gather_gate, gather_lists, gather_thresholds, score_dump, score_topk,
-                        score_topk_lists, score_topk_thresholds, sparse_retrieve)
+from .retrieval import (SparseRetriever, block_retrieve, gather_gate, gather_lists, gather_masked, gather_thresholds,
+                        masked_gather_gate, score_dump, score_topk, score_topk_lists, score_topk_masked,
+                        score_topk_thresholds, sparse_retrieve)
 from .layer import LayerWorkspace, sgsa_layer_forward, sgsa_layer_retrieve
 from .recurrent import fused_recurrent_sgsa
 from .decode import sgsa_decode_step
 from .model import SGSABlock, SGSAConfig, SGSAForCausalLM
+from .hybrid import TopKSparseKVReuseAttention, topk_kv_reuse_attention
 
 __all__ = [
     "ChunkSGSAFunction",
@@ -28,6 +30,11 @@ __all__ = [
     "sgsa_decode_step",
     "SparseRetriever",
     "score_topk",
+    "score_topk_masked",
+    "gather_masked",
+    "masked_gather_gate",
+    "topk_kv_reuse_attention",
+    "TopKSparseKVReuseAttention",
     "score_dump",
     "gather_gate",
     "gather_lists",

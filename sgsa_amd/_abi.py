@@ -48,6 +48,11 @@ SIGNATURES = {
                              _SZ, _P]),
     "sgsa_score_topk_noalloc": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _I, _F, _I, _P, _P, _P, _P, _P, _P, _P, _I,
                                      _P]),
+    "sgsa_score_topk_masked_workspace_size": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, ctypes.POINTER(_SZ)]),
+    "sgsa_score_topk_masked": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _I, _F, _I, _I, _I, _P, _P, _P, _P, _P, _P,
+                                    _P, _P, _P, _P, _I, _P, _SZ, _P]),
+    "sgsa_sparse_gather_masked": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                       _I, _F, _F, _I, _I, _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),
     "sgsa_sparse_gather_tiled": (_I, [_I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _I, _F, _F, _P, _P, _P,
                                       _P, _P]),
     "sgsa_score_dump": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _F, _I, _P, _P, _I, _I, _P, _P]),

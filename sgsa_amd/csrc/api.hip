@@ -294,6 +294,58 @@ int sgsa_score_topk_fast_workspace_size(int dtype, int B, int Tq, int Tk, int H,
   return SGSA_OK;
 }
 
+int sgsa_score_topk_masked_workspace_size(int dtype, int B, int Tq, int Tk, int H, int D, int has_key_mask,
+                                          int kv_layout, size_t* bytes) {
+  if (int s = check_dtype(dtype)) return s;
+  if (int s = check_dims(B, Tq, H, D)) return s;
+  if (int s = check_dims(B, Tk, H, D)) return s;
+  REQUIRE(bytes);
+  const int compact = (has_key_mask != 0 || kv_layout == 1) ? 1 : 0;
+  *bytes = align_up(sgsa::mask_workspace_bytes(dtype, B, Tq, Tk, H, D, compact)) +
+           align_up(sgsa::topk_workspace_bytes(B, Tq, H)) + kAlign;
+  return SGSA_OK;
+}
+
+int sgsa_score_topk_masked(int dtype, int B, int Tq, int Tk, int H, int D, int top_k, int causal, int q_offset,
+                           float scale, int scale_mode, int kq_rule, int kv_layout, const void* q, const void* k,
+                           const uint8_t* key_mask, const uint8_t* query_mask, int32_t* indices, float* scores,
+                           uint8_t* slot_valid, float* top2, int32_t* counts, int32_t* fill, int sorted,
+                           void* workspace, size_t workspace_bytes, void* stream) {
+  if (int s = score_topk_check(dtype, B, Tq, Tk, H, D, top_k, q_offset, scale, scale_mode, q, k, indices, scores,
+                               counts, nullptr, sorted))
+    return s;
+  REQUIRE(counts); REQUIRE(workspace);
+  if (kq_rule != 0 && kq_rule != 1) return fail(SGSA_ERR_INVALID_ARG, "kq_rule must be 0 (retriever) or 1 (fixed top_k)");
+  if (kv_layout != 0 && kv_layout != 1) return fail(SGSA_ERR_INVALID_ARG, "kv_layout must be 0 ([B,Tk,H,D]) or 1 ([B,H,Tk,D])");
+  if ((long)B * (Tk + 1) > 0x7fffffffL) return fail(SGSA_ERR_UNSUPPORTED, "B*(Tk+1) too large for 32-bit key counts");
+  size_t need = 0;
+  if (int s = sgsa_score_topk_masked_workspace_size(dtype, B, Tq, Tk, H, D, key_mask != nullptr, kv_layout, &need))
+    return s;
+  if (workspace_bytes < need) return fail(SGSA_ERR_WORKSPACE, "workspace %zu < %zu bytes", workspace_bytes, need);
+  const hipStream_t st = (hipStream_t)stream;
+  char* base = reinterpret_cast<char*>(((uintptr_t)workspace + kAlign - 1) & ~(uintptr_t)(kAlign - 1));
+  sgsa::MaskArgs m{};
+  m.dtype = dtype; m.B = B; m.Tq = Tq; m.Tk = Tk; m.H = H; m.D = D;
+  m.causal = causal ? 1 : 0; m.q_offset = q_offset; m.top_k = top_k; m.kq_rule = kq_rule; m.kv_hm = kv_layout;
+  m.compacted = (key_mask != nullptr || kv_layout == 1) ? 1 : 0;
+  m.key_mask = key_mask; m.query_mask = query_mask; m.k = k;
+  sgsa::mask_carve(m, base);
+  if (int s = hip_status(sgsa::launch_mask_prepare(m, st), "sgsa_score_topk_masked (mask)")) return s;
+  sgsa::TopkArgs a = score_topk_args(dtype, B, Tq, Tk, H, D, top_k, causal, q_offset, scale, scale_mode, q,
+                                     m.compacted ? m.kc : k, indices, scores, top2, counts, nullptr);
+  a.row_nv = m.nv;
+  a.row_kq = m.kq;
+  a.workspace = base + align_up(sgsa::mask_workspace_bytes(dtype, B, Tq, Tk, H, D, m.compacted));
+  if (int s = hip_status(sgsa::launch_score_topk(a, st), "sgsa_score_topk_masked")) return s;
+  if (sorted) {   // (score desc, index asc): the compaction keeps the index order
+    if (int s = hip_status(sgsa::launch_sort_rows(indices, scores, (long)B * H * Tq, top_k, counts, st),
+                           "sgsa_score_topk_masked (sort)"))
+      return s;
+  }
+  return hip_status(sgsa::launch_mask_finish(m, indices, scores, slot_valid, counts, fill, st),
+                    "sgsa_score_topk_masked (finish)");
+}
+
 int sgsa_topk_lists_size(int B, int T, int H, int top_k, size_t* list_bytes, size_t* offset_bytes) {
   REQUIRE(list_bytes); REQUIRE(offset_bytes);
   if (int s = check_dims(B, T, H, 1)) return s;
@@ -401,6 +453,20 @@ int sgsa_sparse_gather(int dtype, int B, int Tq, int Tk, int H, int D, int top_k
                        float alpha_max, float tau_c, int local_window, int sink_size, void* k_hat, void* v_hat,
                        void* write_key, float* alpha, float* weights, float* diag, void* workspace,
                        size_t workspace_bytes, void* stream) {
+  return sgsa_sparse_gather_masked(dtype, B, Tq, Tk, H, D, top_k, q_offset, 0, k, v, self_key, indices, scores,
+                                   nullptr, top2, counts, budget, write_mode, alpha_max, tau_c, local_window,
+                                   sink_size, k_hat, v_hat, write_key, alpha, weights, diag, workspace,
+                                   workspace_bytes, stream);
+}
+
+int sgsa_sparse_gather_masked(int dtype, int B, int Tq, int Tk, int H, int D, int top_k, int q_offset,
+                              int kv_layout, const void* k, const void* v, const void* self_key,
+                              const int32_t* indices, const float* scores, const uint8_t* slot_valid,
+                              const float* top2, const int32_t* counts, const float* budget, int write_mode,
+                              float alpha_max, float tau_c, int local_window, int sink_size, void* k_hat,
+                              void* v_hat, void* write_key, float* alpha, float* weights, float* diag,
+                              void* workspace, size_t workspace_bytes, void* stream) {
+  if (kv_layout != 0 && kv_layout != 1) return fail(SGSA_ERR_INVALID_ARG, "kv_layout must be 0 ([B,Tk,H,D]) or 1 ([B,H,Tk,D])");
   if (int s = check_dtype(dtype)) return s;
   if (int s = check_dims(B, Tq, H, D)) return s;
   if (int s = check_dims(B, Tk, H, D)) return s;
@@ -419,7 +485,8 @@ int sgsa_sparse_gather(int dtype, int B, int Tq, int Tk, int H, int D, int top_k
     return fail(SGSA_ERR_WORKSPACE, "diagnostics need a workspace of at least 256 bytes");
   sgsa::GatherArgs a{};
   a.dtype = dtype; a.B = B; a.Tq = Tq; a.Tk = Tk; a.H = H; a.D = D; a.top_k = top_k; a.q_offset = q_offset;
-  a.k = k; a.v = v; a.self_key = self_key; a.indices = indices; a.scores = scores; a.top2 = top2; a.counts = counts;
+  a.k = k; a.v = v; a.kv_hm = kv_layout; a.self_key = self_key; a.indices = indices; a.scores = scores; a.top2 = top2; a.counts = counts;
+  a.slot_valid = slot_valid;
   a.use_valid = 1; a.tau_c = tau_c; a.eps = 1e-6f; a.local_window = local_window; a.sink_size = sink_size;
   a.budget = budget; a.write_mode = write_mode; a.alpha_max = alpha_max;
   a.k_hat = k_hat; a.v_hat = v_hat; a.write_key = write_key; a.alpha = alpha; a.weights = weights; a.diag = diag;

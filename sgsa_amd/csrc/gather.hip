@@ -70,6 +70,11 @@ __device__ __forceinline__ int elem_d(int sub, int m, int lpr) {
 
 }  // namespace
 
+// Element offset of key / value row j of (b, h): [B,Tk,H,D] or, with kv_hm, [B,H,Tk,D].
+__device__ __forceinline__ long kv_row_offset(const GatherArgs& a, int b, int h, int j) {
+  return a.kv_hm ? (((long)b * a.H + h) * a.Tk + j) * a.D : (((long)b * a.Tk + j) * a.H + h) * a.D;
+}
+
 // Accumulates slots [s0, s1) of one row into (ak, av, esum) with weights
 // exp(score - mrun).  Online mode (no top2) raises mrun as larger scores
 // arrive, rescaling what was accumulated, and keeps the running top-2.
@@ -82,7 +87,7 @@ __device__ __forceinline__ void gather_slots(const GatherArgs& a, int s0, int s1
                                              float (&av)[GatherShape<X, VEC>::NE]) {
   constexpr int NE = GatherShape<X, VEC>::NE;
   const int lane = threadIdx.x & 63;
-  const int Tk = a.Tk, H = a.H, D = a.D;
+  const int D = a.D;
   const int rpi = 64 / lpr;
   for (int base = s0; base < s1; base += 64) {
     const int slot = base + lane;
@@ -116,7 +121,7 @@ __device__ __forceinline__ void gather_slots(const GatherArgs& a, int s0, int s1
       const int jj = __shfl(j, src, 64);
       const float ww = __shfl(wgt, src, 64);
       if (src < nstep && ww != 0.f) {
-        const long off = ((long)(b * Tk + jj) * H + h) * D;
+        const long off = kv_row_offset(a, b, h, jj);
         float xv[NE];
         load_row<X, VEC>(V, off, sub, D, lpr, xv);
         if (K) {
@@ -139,7 +144,7 @@ __global__ __launch_bounds__(256) void sparse_gather_kernel(GatherArgs a, int lp
   const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);     // over B*H*Tq
   const long nrows = (long)a.B * a.H * a.Tq;
   if (row >= nrows) return;
-  const int Tq = a.Tq, Tk = a.Tk, H = a.H, D = a.D, topk = a.top_k;
+  const int Tq = a.Tq, H = a.H, D = a.D, topk = a.top_k;
   const int bh = (int)(row / Tq), qr = (int)(row % Tq);
   const int b = bh / H, h = bh % H;
   const int pos = qr + a.q_offset;
@@ -194,7 +199,7 @@ __global__ __launch_bounds__(256) void sparse_gather_kernel(GatherArgs a, int lp
         const int jj = __shfl(j, src, 64);
         const float ww = __shfl(wgt, src, 64);
         if (src < nstep && ww != 0.f) {
-          const long off = ((long)(b * Tk + jj) * H + h) * D;
+          const long off = kv_row_offset(a, b, h, jj);
           float xv[NE];
           load_row<X, VEC>(V, off, sub, D, lpr, xv);
           if (K) {

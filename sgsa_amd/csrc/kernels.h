@@ -59,8 +59,12 @@ struct TopkArgs {
   int scale_mode;
   const void* q;      // [B,Tq,H,D]
   const void* k;      // [B,Tk,H,D]
-  const uint8_t* key_mask;   // [B,Tk] (1 = valid) or nullptr
-  const int32_t* row_kq;     // [Tq] slots to fill per query row, or nullptr (derived)
+  // Masked select (row kernel, non-list): the valid keys of row (b, r) are keys
+  // [0, row_nv[b*Tq + r]) -- a prefix, after the key compaction of mask.hip --
+  // and the row selects min(row_kq[r], row_nv) of them.  nullptr: the causal /
+  // full key range and top_k for every row.
+  const int32_t* row_nv;     // [B,Tq] or nullptr
+  const int32_t* row_kq;     // [Tq] or nullptr (only with row_nv)
   int32_t* indices;   // [B,H,Tq,top_k]
   float* scores;      // [B,H,Tq,top_k]
   float* top2;        // [B,H,Tq,2] or nullptr
@@ -77,6 +81,32 @@ struct TopkArgs {
   int* flags;         // set by the launcher
   const float* kmax;  // set by the launcher
 };
+
+// Padding masks for the select (mask.hip).
+struct MaskArgs {
+  int dtype;
+  int B, Tq, Tk, H, D;
+  int causal, q_offset;
+  int top_k;                  // slots per row of the outputs
+  int kq_rule;                // 0: kq = min(top_k, max(1, max_b nv)) per row; 1: kq = top_k
+  int kv_hm;                  // key layout: 0 [B,Tk,H,D], 1 [B,H,Tk,D]
+  int compacted;              // 1: keys copied to kc in valid-first order (needed with a key mask or kv_hm)
+  const uint8_t* key_mask;    // [B,Tk] (nonzero = valid) or nullptr
+  const uint8_t* query_mask;  // [B,Tq] or nullptr
+  const void* k;
+  // workspace (mask_carve)
+  int32_t* pc;                // [B,Tk+1] valid keys below j
+  int32_t* perm;              // [B,Tk] valid keys' indices, ascending
+  int32_t* inv;               // [B,Tk] masked keys' indices, ascending
+  int32_t* nv;                // [B,Tq] valid keys per row
+  int32_t* kq;                // [Tq] slots per row
+  void* kc;                   // [B,Tk,H,D] compacted keys (compacted only)
+};
+size_t mask_workspace_bytes(int dtype, int B, int Tq, int Tk, int H, int D, int compact);
+void mask_carve(MaskArgs& m, void* ws);
+hipError_t launch_mask_prepare(const MaskArgs& m, hipStream_t st);
+hipError_t launch_mask_finish(const MaskArgs& m, int32_t* indices, float* scores, uint8_t* slot_valid,
+                              const int32_t* counts, int32_t* fill, hipStream_t st);
 
 constexpr int TOPK_CAP = 512;   // collected threshold-bin candidates per row
 
@@ -111,6 +141,7 @@ struct GatherArgs {
   int q_offset;              // query row r sits at key position r + q_offset
   const void* k;             // [B,Tk,H,D]  (nullptr: V-only gather)
   const void* v;             // [B,Tk,H,D]
+  int kv_hm;                 // 1: k and v are [B,H,Tk,D] (row kernels only)
   const void* self_key;      // [B,Tq,H,D] key of the query token (diagnostics / residual key), or nullptr
   const int32_t* indices;    // [B,H,Tq,top_k]
   const float* scores;       // [B,H,Tq,top_k]

@@ -279,6 +279,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LIST && !FB
   }
 
   // rows this lane holds in the accumulator: 4*lg + e
+  // valid keys of query row qr (< Tq): a prefix of the keys
+  const bool masked = !DUMP && !LIST && a.row_nv != nullptr;
+  auto row_valid = [&](int qr) __attribute__((always_inline)) {
+    if (masked) return a.row_nv[(long)b * Tq + qr];
+    return a.causal ? max(0, min(Tk, qr + a.q_offset + 1)) : Tk;
+  };
   int nvalid[4];
   bool live[4];
   int minvalid = 0x7fffffff;
@@ -286,16 +292,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LIST && !FB
   for (int e = 0; e < 4; ++e) {
     const int qr = r0 + 16 * w + 4 * lg + e;
     live[e] = qr < Tq;
-    int nv = Tk;
-    if (a.causal) nv = min(Tk, qr + a.q_offset + 1);
-    if (nv < 0) nv = 0;
-    nvalid[e] = live[e] ? nv : 0;
+    nvalid[e] = live[e] ? row_valid(qr) : 0;
     if (live[e]) minvalid = min(minvalid, nvalid[e]);
   }
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) minvalid = min(minvalid, __shfl_xor(minvalid, o, 64));
   int kend = Tk;
-  if (a.causal && !DUMP) {
+  if (masked) {   // the block's largest valid prefix (QB = 64 rows, one per lane)
+    kend = r0 + lane < Tq ? row_valid(r0 + lane) : 0;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) kend = max(kend, __shfl_xor(kend, o, 64));
+  } else if (a.causal && !DUMP) {
     const int last = min(Tq, r0 + QB) - 1 + a.q_offset;
     kend = min(Tk, last + 1);
   }
@@ -368,15 +375,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LIST && !FB
   const float kmx = sqrtf(wave_max(kmx2));
   if (lane < 16) {
     const int qr = r0 + 16 * w + lane;
-    int nv = 0;
-    if (qr < Tq) nv = a.causal ? max(0, min(Tk, qr + a.q_offset + 1)) : Tk;
+    const int nv = qr < Tq ? row_valid(qr) : 0;
+    const int kr = (masked && a.row_kq != nullptr && qr < Tq) ? min(topk, a.row_kq[qr]) : topk;   // row's slots
     RowInfo ri;
     const float bound = qnorm[w][lane] * kmx * fabsf(mscale) * 1.001f;
     ri.iw = (bound > 0.f && bound < FLT_MAX) ? 128.0f / bound : 0.f;
     ri.bstar = -1;
-    ri.need = min(topk, nv);
-    ri.mode = (nv <= topk) ? SELECT_ALL : (FB ? RADIX : BIN_ALL);
-    ri.pfx = 0; ri.msk = 0; ri.done = (FB && nv > topk) ? 0 : 1; ri.th0 = -INFINITY; ri.th1 = -INFINITY;
+    ri.need = min(kr, nv);
+    ri.mode = (nv <= kr) ? SELECT_ALL : (FB ? RADIX : BIN_ALL);
+    ri.pfx = 0; ri.msk = 0; ri.done = (FB && nv > kr) ? 0 : 1; ri.th0 = -INFINITY; ri.th1 = -INFINITY;
     rinfo[w][lane] = ri;
   }
   for (int i = lane; i < 16 * HWA; i += 64) (&hist[w][0][0])[i] = 0;

@@ -41,6 +41,7 @@ from .decode import sgsa_decode_step
 from .layer import LayerWorkspace, sgsa_layer_forward
 from . import _abi
 from .model import GatedMLP, RMSNorm, SGSABlock, SGSAConfig, fused_linear
+from .retrieval import gather_masked, score_topk_masked
 
 Tensor = torch.Tensor
 
@@ -332,3 +333,82 @@ def generate(model: HybridForCausalLM, prompt: Tensor, steps: int, batch: Option
         tok = model.decode_step(tok, T + s, s, caches, rope).argmax(-1)
         out[:, s] = tok
     return logits, out
+
+
+def topk_kv_reuse_attention(query: Tensor, key: Tensor, value: Tensor, top_k: int,
+                            attention_mask: Optional[Tensor] = None) -> Tuple[Tensor, Tensor, Tensor]:
+    """Core of TopKSparseKVReuseAttention.forward (modelings/hybrid_dense_delta_topk.py:343-356)
+    on the HIP kernels: the masked select (sgsa_score_topk_masked, kq_rule 1) and
+    the V-only gather (sgsa_sparse_gather_masked), with no [B,H,Q,K] score matrix.
+
+    query [B,Q,H,D] (RoPE applied); key, value [B,H,K,D], the dense layer's KV
+    as the reference holds it; queries sit at key positions K-Q .. K-1 (:153-156);
+    attention_mask [B,K] (nonzero = real token) or None.  Scores are
+    q.k * 1/sqrt(D) (:343-344); future and padded keys are masked (:346,
+    :166-175) and every row keeps min(top_k, K) slots (:348-349), the masked
+    ones (score finfo.min, ties to the lowest index) with probability 0 unless
+    a row has no unmasked key, whose slots then share it evenly, as the fp32
+    softmax of equal scores does (:350).  Returns (attended [B,Q,H,D] in the
+    value dtype, indices int64 [B,H,Q,k], probabilities float32 [B,H,Q,k]).
+    """
+    B, Q, H, D = query.shape
+    K = key.shape[2]
+    if key.shape != (B, H, K, D) or value.shape != key.shape:
+        raise ValueError(f"key/value must be [B,H,K,D] = {(B, H, K, D)}; got {tuple(key.shape)} / {tuple(value.shape)}")
+    if Q > K:
+        raise ValueError(f"{Q} queries over {K} keys: the queries are the last Q positions of the KV")
+    idx, sc, _, top2, _, fill = score_topk_masked(query, key, top_k, key_mask=attention_mask, causal=True,
+                                                  q_offset=K - Q, scale_mode=1, kq_rule=1, kv_layout=1, sorted=True)
+    r = gather_masked(None, value, idx, sc, None, top2, fill, q_offset=K - Q, kv_layout=1, return_weights=True)
+    return r["v_hat"], idx.long(), r["weights"]
+
+
+class TopKSparseKVReuseAttention(nn.Module):
+    """Top-k sparse attention over the nearest previous dense layer's KV cache
+    (modelings/hybrid_dense_delta_topk.py:317-358): q_proj, RoPE at offset
+    K-Q, the masked top-k select and V-only gather of ``topk_kv_reuse_attention``,
+    o_proj.  Same constructor config fields (num_attention_heads, head_dim or
+    hidden_size, top_k, dropout) and forward signature.  Forward only: the
+    kernels' outputs carry no autograd graph, so the module refuses to run
+    where gradients are being recorded, and dropout on the probabilities
+    (training with dropout > 0) is not supported.
+    """
+
+    def __init__(self, config) -> None:
+        super().__init__()
+        self.config = config
+        self.num_heads = config.num_attention_heads
+        self.head_dim = config.head_dim
+        self.top_k = config.top_k
+        self.q_proj = nn.Linear(config.hidden_size, config.hidden_size, bias=False)
+        self.o_proj = nn.Linear(config.hidden_size, config.hidden_size, bias=False)
+        self.dropout_p = getattr(config, "dropout", 0.0)
+
+    def forward(self, hidden_states: Tensor, dense_kv: Tuple[Tensor, Tensor], rope: Tuple[Tensor, Tensor],
+                attention_mask: Optional[Tensor]) -> Tensor:
+        if torch.is_grad_enabled() and any(p.requires_grad for p in self.parameters()):
+            raise RuntimeError("TopKSparseKVReuseAttention runs forward-only HIP kernels; call it under "
+                               "torch.no_grad() / torch.inference_mode()")
+        if self.training and self.dropout_p > 0:
+            raise NotImplementedError("dropout on the top-k probabilities is not supported")
+        B, Q, _ = hidden_states.shape
+        key, value = dense_kv
+        K = key.shape[-2]
+        H, D = self.num_heads, self.head_dim
+        if attention_mask is not None:
+            if attention_mask.dim() != 2:
+                raise ValueError("attention_mask must have shape [batch_size, kv_len]")
+            if attention_mask.shape[-1] != K:
+                raise ValueError("attention_mask length must match the current KV length")
+        query = self.q_proj(hidden_states).view(B, Q, H, D)
+        cos, sin = rope
+        if cos.dim() == 4:   # the reference's [1, 1, S, D] tables
+            cos, sin = cos[0, 0], sin[0, 0]
+        off = K - Q
+        c = cos[off:off + Q].to(query.dtype)[None, :, None, :]
+        s = sin[off:off + Q].to(query.dtype)[None, :, None, :]
+        half = D // 2
+        query = query * c + torch.cat((-query[..., half:], query[..., :half]), dim=-1) * s
+        attended, _, _ = topk_kv_reuse_attention(query.contiguous(), key.to(query.dtype), value.to(query.dtype),
+                                                 self.top_k, attention_mask)
+        return self.o_proj(attended.reshape(B, Q, H * D))

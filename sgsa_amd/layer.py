@@ -14,6 +14,8 @@ from typing import Optional, Tuple
 import torch
 
 from . import _abi
+from .ops import chunk_sgsa_fwd
+from .retrieval import masked_gather_gate
 
 Tensor = torch.Tensor
 
@@ -56,10 +58,15 @@ def sgsa_layer_forward(
     output_final_state: bool = True,
     workspace: Optional[LayerWorkspace] = None,
     out: Optional[Tensor] = None,
+    attention_mask: Optional[Tensor] = None,
 ) -> Tuple[Tensor, Optional[Tensor]]:
     """q,k,v,q_ret [B,T,H,D] (float32 or bfloat16); beta,gamma,budget_logits [B,T,H].
 
     Returns (o [B,T,H,D] in q.dtype, final state [B,H,D,D] float32 or None).
+    attention_mask [B,T] (nonzero = real token): the retrieval masks padded
+    keys and queries (SparseRetriever.forward, modeling_sgsa.py:421-428); the
+    state update itself takes no mask (:584-596).  The masked layer runs as
+    its three entry points (masked select, masked gather + gate, chunked update).
     """
     if not q.is_cuda:
         raise ValueError("sgsa_layer_forward: the SGSA kernels run on a ROCm GPU; got CPU tensors")
@@ -72,6 +79,15 @@ def sgsa_layer_forward(
             raise ValueError(f"{name} has shape {tuple(t.shape)}, expected {(B, T, H)}")
     if write_mode not in _WRITE_MODES:
         raise ValueError(f"write_mode must be one of {sorted(_WRITE_MODES)}")
+    if attention_mask is not None:
+        wk, vh, al = masked_gather_gate(q_ret, k, v, budget_logits, top_k, attention_mask, write_mode=write_mode,
+                                        alpha_max=alpha_max, tau_c=tau_c)
+        o, ht = chunk_sgsa_fwd(q, k, v, beta, gamma, wk, vh, al, initial_state=initial_state,
+                               chunk_size=chunk_size, output_final_state=output_final_state)
+        if out is not None:
+            out.copy_(o)
+            o = out
+        return o, ht
     dev = q.device
     qc, kc, vc, rc = (t.contiguous() for t in (q, k, v, q_ret))
     bc, gc, uc = (t.float().contiguous() for t in (beta, gamma, budget_logits))
@@ -99,9 +115,11 @@ def sgsa_layer_retrieve(
     alpha_max: float = 0.25,
     tau_c: float = 0.1,
     workspace: Optional[LayerWorkspace] = None,
+    attention_mask: Optional[Tensor] = None,
 ) -> Tuple[Tensor, Tensor, Tensor]:
     """The retrieval half of ``sgsa_layer_forward`` (sgsa_layer_retrieve): the
-    (write key, v_hat, alpha) that the layer feeds to the chunked update.
+    (write key, v_hat, alpha) that the layer feeds to the chunked update
+    (with ``attention_mask`` [B,T], the masked select and gather).
 
     q_ret, k, v [B,T,H,D] (float32 or bfloat16); budget_logits [B,T,H].
     Returns write_key / v_hat [B,T,H,D] in the input dtype and alpha [B,T,H] float32.
@@ -116,6 +134,9 @@ def sgsa_layer_retrieve(
         raise ValueError(f"budget_logits has shape {tuple(budget_logits.shape)}, expected {(B, T, H)}")
     if write_mode not in _WRITE_MODES:
         raise ValueError(f"write_mode must be one of {sorted(_WRITE_MODES)}")
+    if attention_mask is not None:
+        return masked_gather_gate(q_ret, k, v, budget_logits, top_k, attention_mask, write_mode=write_mode,
+                                  alpha_max=alpha_max, tau_c=tau_c)
     dev = q_ret.device
     rc, kc, vc = (t.contiguous() for t in (q_ret, k, v))
     uc = budget_logits.float().contiguous()

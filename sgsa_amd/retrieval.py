@@ -12,7 +12,7 @@ from __future__ import annotations
 
 import ctypes
 import math
-from typing import Dict, Optional
+from typing import Dict, Optional, Tuple
 
 import torch
 import torch.nn as nn
@@ -65,6 +65,117 @@ def score_topk(q: Tensor, k: Tensor, top_k: int, causal: bool = True, q_offset: 
     if return_split:
         return idx, sc, top2, cnt, spl
     return idx, sc, top2, cnt
+
+
+def _mask_bytes(mask: Optional[Tensor], shape, name: str) -> Optional[Tensor]:
+    if mask is None:
+        return None
+    if tuple(mask.shape) != tuple(shape):
+        raise ValueError(f"{name} has shape {tuple(mask.shape)}, expected {tuple(shape)}")
+    return mask.to(torch.bool).to(torch.uint8).contiguous()
+
+
+def score_topk_masked(q: Tensor, k: Tensor, top_k: int, key_mask: Optional[Tensor] = None,
+                      query_mask: Optional[Tensor] = None, causal: bool = True, q_offset: int = 0,
+                      scale: Optional[float] = None, scale_mode: int = 0, kq_rule: int = 0,
+                      kv_layout: int = 0, sorted: bool = True):
+    """``score_topk`` with padding masks (sgsa_score_topk_masked).
+
+    q [B,Tq,H,D]; k [B,Tk,H,D] (kv_layout 0) or [B,H,Tk,D] (kv_layout 1);
+    key_mask [B,Tk] and query_mask [B,Tq] (nonzero = valid) or None.
+    kq_rule 0 gives each row min(top_k, max(1, largest valid count over the
+    batch)) slots (SparseRetriever._masked_topk, modeling_sgsa.py:159-160);
+    kq_rule 1 gives every row min(top_k, Tk) (TopKSparseKVReuseAttention,
+    hybrid_dense_delta_topk.py:348).  Returns (indices int32, scores float32,
+    slot_valid uint8, all [B,H,Tq,kk]; top2 [B,H,Tq,2]; counts int32 [B,H,Tq]
+    of valid selected slots; fill int32 [B,H,Tq] of filled slots), kk = min(top_k, Tk).
+    """
+    if not q.is_cuda:
+        raise ValueError("score_topk_masked: the SGSA kernels run on a ROCm GPU; got CPU tensors")
+    B, Tq, H, D = q.shape
+    Tk = k.shape[2] if kv_layout == 1 else k.shape[1]
+    want = (B, H, Tk, D) if kv_layout == 1 else (B, Tk, H, D)
+    if tuple(k.shape) != want or k.dtype != q.dtype:
+        raise ValueError(f"k shape/dtype {tuple(k.shape)}/{k.dtype} does not match {want}/{q.dtype}")
+    km = _mask_bytes(key_mask, (B, Tk), "key_mask")
+    qm = _mask_bytes(query_mask, (B, Tq), "query_mask")
+    kk = min(int(top_k), Tk)
+    if scale is None:
+        scale = math.sqrt(D) if scale_mode == 0 else 1.0 / math.sqrt(D)
+    qc, kc = q.contiguous(), k.contiguous()
+    dev = q.device
+    idx = torch.empty(B, H, Tq, kk, device=dev, dtype=torch.int32)
+    sc = torch.empty(B, H, Tq, kk, device=dev, dtype=torch.float32)
+    valid = torch.empty(B, H, Tq, kk, device=dev, dtype=torch.uint8)
+    top2 = torch.empty(B, H, Tq, 2, device=dev, dtype=torch.float32)
+    cnt = torch.empty(B, H, Tq, device=dev, dtype=torch.int32)
+    fill = torch.empty(B, H, Tq, device=dev, dtype=torch.int32)
+    L = _abi.lib()
+    nbytes = ctypes.c_size_t()
+    _abi.check(L.sgsa_score_topk_masked_workspace_size(_abi.dtype_code(q.dtype), B, Tq, Tk, H, D, int(km is not None),
+                                                       int(kv_layout), ctypes.byref(nbytes)))
+    ws = torch.empty(nbytes.value, device=dev, dtype=torch.uint8)
+    _abi.check(L.sgsa_score_topk_masked(
+        _abi.dtype_code(q.dtype), B, Tq, Tk, H, D, kk, int(causal), int(q_offset), float(scale), int(scale_mode),
+        int(kq_rule), int(kv_layout), _abi.ptr(qc), _abi.ptr(kc), _abi.ptr(km), _abi.ptr(qm), _abi.ptr(idx),
+        _abi.ptr(sc), _abi.ptr(valid), _abi.ptr(top2), _abi.ptr(cnt), _abi.ptr(fill), int(sorted), _abi.ptr(ws),
+        nbytes.value, _abi.stream_of(qc)))
+    return idx, sc, valid, top2, cnt, fill
+
+
+def gather_masked(k: Optional[Tensor], v: Tensor, idx: Tensor, sc: Tensor, valid: Optional[Tensor], top2: Tensor,
+                  fill: Tensor, q_offset: int = 0, kv_layout: int = 0, self_key: Optional[Tensor] = None,
+                  budget_logits: Optional[Tensor] = None, write_mode: str = "direct", alpha_max: float = 0.25,
+                  tau_c: float = 0.1, local_window: int = 64, sink_size: int = 8, return_weights: bool = False,
+                  return_diagnostics: bool = False) -> Dict[str, Optional[Tensor]]:
+    """sgsa_sparse_gather_masked over ``score_topk_masked`` output.
+
+    k (None: V-only), v: [B,Tk,H,D] (kv_layout 0) or [B,H,Tk,D] (kv_layout 1).
+    ``valid`` None: every filled slot takes its softmax weight (the hybrid's
+    probabilities); else the retriever's softmax * valid / sum.  Returns a dict
+    of k_hat / v_hat [B,Tq,H,D], write_key, alpha [B,Tq,H], weights
+    [B,H,Tq,kk] float32, diag [NDIAG,B,H,Tq] (None where not requested).
+    """
+    B, H, Tq, kk = idx.shape
+    Tk = v.shape[2] if kv_layout == 1 else v.shape[1]
+    D = v.shape[-1]
+    dev = v.device
+    kc = k.contiguous() if k is not None else None
+    vc = v.contiguous()
+    skc = self_key.contiguous() if self_key is not None else None
+    mode = {"direct": 0, "residual": 1}[write_mode]
+    k_hat = torch.empty(B, Tq, H, D, device=dev, dtype=v.dtype) if k is not None else None
+    v_hat = torch.empty(B, Tq, H, D, device=dev, dtype=v.dtype)
+    bud = budget_logits.float().contiguous() if budget_logits is not None else None
+    al = torch.empty(B, Tq, H, device=dev, dtype=torch.float32) if bud is not None else None
+    wkey = torch.empty_like(k_hat) if (bud is not None and mode == 1) else None
+    weights = torch.empty(B, H, Tq, kk, device=dev, dtype=torch.float32) if return_weights else None
+    diag = torch.empty(_abi.NDIAG, B, H, Tq, device=dev, dtype=torch.float32) if return_diagnostics else None
+    L = _abi.lib()
+    nbytes = ctypes.c_size_t()
+    _abi.check(L.sgsa_sparse_gather_workspace_size(B, Tq, H, D, kk, ctypes.byref(nbytes)))
+    ws = torch.empty(nbytes.value, device=dev, dtype=torch.uint8)
+    _abi.check(L.sgsa_sparse_gather_masked(
+        _abi.dtype_code(v.dtype), B, Tq, Tk, H, D, kk, int(q_offset), int(kv_layout), _abi.ptr(kc), _abi.ptr(vc),
+        _abi.ptr(skc), _abi.ptr(idx), _abi.ptr(sc), _abi.ptr(valid), _abi.ptr(top2), _abi.ptr(fill), _abi.ptr(bud),
+        mode, float(alpha_max), float(tau_c), int(local_window), int(sink_size), _abi.ptr(k_hat), _abi.ptr(v_hat),
+        _abi.ptr(wkey), _abi.ptr(al), _abi.ptr(weights), _abi.ptr(diag), _abi.ptr(ws), nbytes.value,
+        _abi.stream_of(vc)))
+    return {"k_hat": k_hat, "v_hat": v_hat, "write_key": (wkey if mode == 1 else k_hat), "alpha": al,
+            "weights": weights, "diag": diag}
+
+
+def masked_gather_gate(q_ret: Tensor, k: Tensor, v: Tensor, budget_logits: Tensor, top_k: int,
+                       attention_mask: Tensor, causal: bool = True, write_mode: str = "direct",
+                       alpha_max: float = 0.25, tau_c: float = 0.1) -> Tuple[Tensor, Tensor, Tensor]:
+    """Retrieval half of the SGSA layer under a padding mask [B,T] (the
+    retriever's valid = causal & key_valid & query_valid, modeling_sgsa.py:421-428):
+    (write key, v_hat, alpha) for the chunked update."""
+    idx, sc, valid, top2, cnt, fill = score_topk_masked(q_ret, k, top_k, key_mask=attention_mask,
+                                                        query_mask=attention_mask, causal=causal, sorted=False)
+    r = gather_masked(k, v, idx, sc, valid, top2, fill, self_key=k, budget_logits=budget_logits,
+                      write_mode=write_mode, alpha_max=alpha_max, tau_c=tau_c)
+    return r["write_key"], r["v_hat"], r["alpha"]
 
 
 def gather_gate(k: Tensor, v: Tensor, idx: Tensor, sc: Tensor, top2: Tensor, cnt: Tensor,
@@ -226,13 +337,32 @@ def sparse_retrieve(
     """Token-only retrieval; the dict of SparseRetriever.forward (modeling_sgsa.py:467-474).
 
     q,k,v: [B,T,H,D].  k_hat/v_hat are [B,T,H,D]; indices/weights [B,H,T,kk];
-    diagnostics [B,H,T] each.  Padding masks are not supported yet.
+    diagnostics [B,H,T] each.  attention_mask [B,T] (nonzero = real token)
+    masks padded keys and padded queries (:421-428); a row then keeps
+    min(top_k, max(1, largest valid count of that row over the batch)) slots,
+    its invalid ones pointing at its lowest-index invalid keys with weight 0
+    and the rest index 0 (:144-165).
     """
-    if attention_mask is not None:
-        raise NotImplementedError("sparse_retrieve: attention_mask is not supported by the HIP retrieval yet")
     B, T, H, D = q.shape
     if v.shape != k.shape or v.dtype != k.dtype:
         raise ValueError("v must match k in shape and dtype")
+    if attention_mask is not None:
+        idx, sc, valid, top2, cnt, fill = score_topk_masked(q, k, top_k, key_mask=attention_mask,
+                                                            query_mask=attention_mask, causal=causal, sorted=sorted)
+        r = gather_masked(k, v, idx, sc, valid, top2, fill, self_key=k, tau_c=tau_c, local_window=local_window,
+                          sink_size=sink_size, return_weights=return_weights, return_diagnostics=return_diagnostics)
+        diag = r["diag"]
+        return {
+            "indices": idx.long(),
+            "block_indices": None,
+            "weights": r["weights"].to(q.dtype) if r["weights"] is not None else None,
+            "k_hat": r["k_hat"],
+            "v_hat": r["v_hat"],
+            "diagnostics": ({n: diag[i] for i, n in enumerate(_abi.DIAG_NAMES)} if diag is not None else {}),
+            "scores": sc,
+            "counts": cnt,
+            "valid": valid.bool(),
+        }
     idx, sc, top2, cnt = score_topk(q, k, top_k, causal=causal, sorted=sorted)
     kk = idx.shape[-1]
     kc, vc = k.contiguous(), v.contiguous()

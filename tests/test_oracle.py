@@ -276,6 +276,136 @@ def test_kv_reuse_causal_offset_and_probs():
     torch.testing.assert_close(p.sum(-1), torch.ones(B, H, Q))
 
 
+# ---------------------------------------------------------------- padding masks
+
+def _padding_mask(B, T):
+    # batch 0 all real tokens, batch 1 left-padded, batch 2 right-padded with a hole
+    am = torch.ones(B, T, dtype=torch.bool)
+    am[1, :4] = False
+    am[2, T - 4:] = False
+    am[2, 3] = False
+    return am
+
+
+def test_masked_topk_padding_by_loops():
+    # _masked_topk (modeling_sgsa.py:144-165) restated per row: invalid scores are
+    # finfo.min, k_q = min(topk, max(valid count over (B,H), 1)), ties to the lowest index
+    g = torch.Generator().manual_seed(11)
+    B, H, T, k = 3, 2, 14, 5
+    s = torch.randn(B, H, T, T, generator=g)
+    am = _padding_mask(B, T)
+    pos = torch.arange(T)
+    valid = ((pos[None, :] <= pos[:, None])[None, None] & am[:, None, None, :] & am[:, None, :, None]).expand(B, H, T, T)
+    vals, idx, ok = O.masked_topk(s, valid, k)
+    fmin = torch.finfo(torch.float32).min
+    for t in range(T):
+        vc = max(sum(bool(valid[b, h, t, j]) for j in range(T)) for b in range(B) for h in range(H))
+        kq = min(k, max(vc, 1))
+        for b in range(B):
+            for h in range(H):
+                row = [s[b, h, t, j].item() if valid[b, h, t, j] else fmin for j in range(T)]
+                bv, bi = _brute_topk(row, kq)
+                assert idx[b, h, t, :kq].tolist() == bi
+                assert vals[b, h, t, :kq].tolist() == bv
+                assert ok[b, h, t, :kq].tolist() == [bool(valid[b, h, t, j]) for j in bi]
+                assert idx[b, h, t, kq:].tolist() == [0] * (k - kq)
+                assert vals[b, h, t, kq:].tolist() == [fmin] * (k - kq)
+                assert not ok[b, h, t, kq:].any()
+    # a padded query row has no valid slot; a row with fewer valid keys than
+    # k_q fills the rest with its lowest-index invalid keys
+    assert not ok[1, :, 2].any() and idx[1, 0, 2, :min(k, 3)].tolist() == list(range(min(k, 3)))
+
+
+def test_retrieval_with_padding_by_loops():
+    # float32 inputs: the reference's softmax(scores.float()) turns a float64
+    # finfo.min into -inf, and a row of them into NaN weights
+    g = torch.Generator().manual_seed(12)
+    B, T, H, D, k = 3, 11, 2, 4, 3
+    q, kk, v = (torch.randn(B, T, H, D, generator=g) for _ in range(3))
+    am = _padding_mask(B, T)
+    ret = O.token_topk_retrieval(q, kk, v, k, attention_mask=am, block_rows=4)
+    fmin = torch.finfo(torch.float32).min
+    for t in range(T):
+        ok = lambda b, j: j <= t and bool(am[b, j]) and bool(am[b, t])
+        kq = min(k, max(1, max(sum(ok(b, j) for j in range(T)) for b in range(B))))
+        for b in range(B):
+            for h in range(H):
+                row = [sum(q[b, t, h, d].item() * kk[b, j, h, d].item() for d in range(D)) / math.sqrt(D)
+                       if ok(b, j) else fmin for j in range(T)]
+                bv, bi = _brute_topk(row, kq)
+                assert ret["indices"][b, h, t, :kq].tolist() == bi
+                m = max(bv)
+                e = [math.exp(x - m) for x in bv]
+                w = [e[i] / sum(e) * (1.0 if ok(b, bi[i]) else 0.0) for i in range(kq)]
+                w = [x / max(sum(w), 1e-6) for x in w]
+                torch.testing.assert_close(ret["weights"][b, h, t, :kq], torch.tensor(w, dtype=torch.float32))
+                exp_k = sum(w[i] * kk[b, bi[i], h].double() for i in range(kq))
+                torch.testing.assert_close(ret["k_hat"][b, t, h], exp_k.float())
+                if not am[b, t]:
+                    assert ret["k_hat"][b, t, h].abs().max() == 0 and ret["v_hat"][b, t, h].abs().max() == 0
+
+
+def test_kv_reuse_padding_by_loops():
+    # TopKSparseKVReuseAttention (hybrid_dense_delta_topk.py:343-356) with _merge_masks
+    # (:153-175): a query whose visible keys are all padding averages the
+    # lowest-index keys (equal finfo.min scores, fp32 softmax)
+    g = torch.Generator().manual_seed(13)
+    B, H, Q, K, D, k = 2, 2, 4, 9, 4, 3
+    qh, kh, vh = (torch.randn(B, H, n, D, generator=g) for n in (Q, K, K))
+    am = torch.ones(B, K, dtype=torch.bool)
+    am[0, :6] = False   # query 0 of batch 0 sits at position 5: nothing visible
+    am[1, 7] = False
+    out, idx, p = O.topk_kv_reuse_attention(qh, kh, vh, k, attention_mask=am)
+    fmin = torch.finfo(torch.float32).min
+    for b in range(B):
+        for h in range(H):
+            for r in range(Q):
+                pos = K - Q + r
+                s = [(qh[b, h, r].double() @ kh[b, h, j].double()).item() / math.sqrt(D)
+                     if (j <= pos and am[b, j]) else fmin for j in range(K)]
+                bv, bi = _brute_topk(s, k)
+                assert idx[b, h, r].tolist() == bi
+                m = max(bv)
+                e = [math.exp(x - m) for x in bv]
+                pw = [x / sum(e) for x in e]
+                torch.testing.assert_close(p[b, h, r], torch.tensor(pw, dtype=torch.float32))
+                torch.testing.assert_close(out[b, h, r], sum(pw[i] * vh[b, h, bi[i]] for i in range(k)))
+    assert idx[0, 0, 0].tolist() == [0, 1, 2]
+    torch.testing.assert_close(p[0, 0, 0], torch.full((k,), 1.0 / k))
+
+
+def test_diagnostics_by_explicit_loops():
+    # _diagnostics (modeling_sgsa.py:361-405): max weight, entropy, and the distance
+    # statistics over every slot, padded ones (index 0) included, with avg_distance
+    # divided by the largest index + 1 over the whole tensor
+    g = torch.Generator().manual_seed(14)
+    B, H, T, k, D = 2, 2, 9, 4, 5
+    lw, ss, eps = 2, 1, 1e-6
+    sc = torch.randn(B, H, T, k, generator=g, dtype=torch.float64)
+    idx = torch.randint(0, T, (B, H, T, k), generator=g)
+    w = torch.rand(B, H, T, k, generator=g, dtype=torch.float64)
+    w[0, 0, 3] = 0.0
+    kh = torch.randn(B, H, T, D, generator=g, dtype=torch.float64)
+    key = torch.randn(B, H, T, D, generator=g, dtype=torch.float64)
+    d = O.retrieval_diagnostics(sc, w, idx, kh, key, local_window=lw, sink_size=ss, eps=eps)
+    imax = int(idx.max())
+    for b in range(B):
+        for h in range(H):
+            for t in range(T):
+                ws = w[b, h, t].tolist()
+                js = idx[b, h, t].tolist()
+                dist = [max(t - j, 0) for j in js]
+                assert d["max_confidence"][b, h, t].item() == max(ws)
+                ent = -sum(max(x, eps) * math.log(max(x, eps)) for x in ws)
+                assert abs(d["entropy"][b, h, t].item() - ent) < 1e-12
+                # the reference takes these means in float32 (dist.float().mean)
+                assert abs(d["avg_distance"][b, h, t].item() - sum(dist) / k / (imax + 1)) < 1e-7
+                assert d["local_ratio"][b, h, t].item() == sum(x <= lw for x in dist) / k
+                assert d["sink_ratio"][b, h, t].item() == sum(j < ss for j in js) / k
+                assert d["remote_ratio"][b, h, t].item() == sum(x > lw and j >= ss for x, j in zip(dist, js)) / k
+                assert abs(d["score_margin"][b, h, t].item() - (sc[b, h, t, 0] - sc[b, h, t, 1]).item()) < 1e-12
+
+
 def test_make_inputs_shapes_and_rounding():
     x = O.make_inputs(1, 300, 2, 8, dtype=torch.bfloat16, heavy_tail=True)
     assert x["q"].dtype == torch.bfloat16 and x["q_f32"].dtype == torch.float32
