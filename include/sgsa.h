@@ -199,14 +199,14 @@ int sgsa_sparse_gather(int dtype, int B, int Tq, int Tk, int H, int D, int top_k
  * hybrid's probabilities do (hybrid_dense_delta_topk.py:350): the -FLT_MAX
  * fills weigh 0 unless a row has no valid key, which then averages its kq
  * filled keys.  kv_layout: k and v are [B,Tk,H,D] (0) or [B,H,Tk,D] (1);
- * self_key stays [B,Tq,H,D]. */
+ * self_key stays [B,Tq,H,D].  row_stats (may be NULL): as sgsa_layer_fwd_stats. */
 int sgsa_sparse_gather_masked(int dtype, int B, int Tq, int Tk, int H, int D, int top_k, int q_offset,
                               int kv_layout, const void* k, const void* v, const void* self_key,
                               const int32_t* indices, const float* scores, const uint8_t* slot_valid,
                               const float* top2, const int32_t* counts, const float* budget, int write_mode,
                               float alpha_max, float tau_c, int local_window, int sink_size, void* k_hat,
                               void* v_hat, void* write_key, float* alpha, float* weights, float* diag,
-                              void* workspace, size_t workspace_bytes, void* stream);
+                              float* row_stats, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Scores at given keys: for every query row and slot i < counts[row],
  * scores[row,i] = (q_row . k[indices[row,i]]) * scale' with fp32 accumulation,
@@ -372,6 +372,26 @@ int sgsa_layer_retrieve(int dtype, int B, int T, int H, int D, int top_k,
                         int write_mode, float alpha_max, float tau_c,
                         void* write_key, void* v_hat, float* alpha,
                         void* workspace, size_t workspace_bytes, void* stream);
+
+/* sgsa_layer_fwd / sgsa_layer_retrieve with the per-row figures behind
+ * SGSABlock.forward's metrics (modelings/modeling_sgsa.py:697-708):
+ * alpha_out [B,T,H] fp32 (may be NULL) receives alpha ("alpha_mean");
+ * row_stats [2,B,H,T] fp32 (may be NULL) receives in plane 0 each row's
+ * largest retrieval weight (_diagnostics' max_confidence, :374,
+ * "retrieval_confidence_mean") and in plane 1 |write key| / max(|k_hat|, 1e-6)
+ * clamped to [0, 10] for write_mode 1 ("k_hat_perp_ratio_mean", :614), 0 for
+ * write_mode 0.  The means are left to the caller. */
+int sgsa_layer_fwd_stats(int dtype, int B, int T, int H, int D, int top_k, int chunk_size,
+                         const void* q, const void* k, const void* v, const void* q_ret,
+                         const float* beta, const float* gamma, const float* budget,
+                         const float* initial_state, int write_mode, float alpha_max, float tau_c,
+                         void* out, float* final_state, float* alpha_out, float* row_stats,
+                         void* workspace, size_t workspace_bytes, void* stream);
+int sgsa_layer_retrieve_stats(int dtype, int B, int T, int H, int D, int top_k,
+                              const void* q_ret, const void* k, const void* v, const float* budget,
+                              int write_mode, float alpha_max, float tau_c,
+                              void* write_key, void* v_hat, float* alpha, float* row_stats,
+                              void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -609,7 +609,8 @@ def gated_mlp(x: Tensor, w_gate: Tensor, w_up: Tensor, w_down: Tensor) -> Tensor
 def sgsa_model_forward(params: Dict[str, Tensor], input_ids: Tensor, *, num_layers: int, num_heads: int,
                        top_k: int, eps: float = 1e-6, write_mode: str = "direct", alpha_max: float = 0.25,
                        tau_c: float = 0.1, sparse_output_lambda: float = 0.0,
-                       act_dtype: Optional[torch.dtype] = None) -> Tensor:
+                       act_dtype: Optional[torch.dtype] = None, attention_mask: Optional[Tensor] = None,
+                       return_metrics: bool = False):
     """Logits of SGSAForCausalLM.forward (modelings/modeling_sgsa.py:735-749) in fp32.
 
     ``params`` uses the parameter names of sgsa_amd.model.SGSAForCausalLM, which follow
@@ -624,11 +625,21 @@ def sgsa_model_forward(params: Dict[str, Tensor], input_ids: Tensor, *, num_laye
     -- each projection, norm, MLP product and residual sum -- while the arithmetic
     stays fp32, so that a low-precision model is compared on the inputs it actually
     feeds each layer.
+
+    ``attention_mask`` [B,T] zeroes the padded embeddings (:740-741) and goes to
+    every layer's retrieval (:668-674).  ``return_metrics``: returns (logits,
+    metrics) with the per-layer metrics of :697-708 / :744-752 --
+    alpha_mean, k_hat_perp_ratio_mean ((|k_hat_perp| / max(|k_hat|, eps))
+    clamped to [0, 10], residual mode only; :546-551, :614) and
+    retrieval_confidence_mean (mean max weight, :374).
     """
     P = {k: v.float() for k, v in params.items()}
     r = (lambda x: x) if act_dtype is None else (lambda x: x.to(act_dtype).float())
     B, T = input_ids.shape
     h = r(P["embed_tokens.weight"][input_ids] + P["pos_embed.weight"][:T][None])
+    if attention_mask is not None:
+        h = h * attention_mask.to(torch.bool).float()[..., None]
+    metrics = {}
     C = h.shape[-1]
     H, D = num_heads, C // num_heads
     for i in range(num_layers):
@@ -642,7 +653,13 @@ def sgsa_model_forward(params: Dict[str, Tensor], input_ids: Tensor, *, num_laye
         gamma = torch.sigmoid(r(n @ w("gamma_proj.weight").T + w("gamma_proj.bias")))
         budget = r(n @ w("budget_proj.weight").T + w("budget_proj.bias"))
         lay = sgsa_layer_forward(q, k, v, q_ret, beta, gamma, budget, top_k, write_mode=write_mode,
-                                 alpha_max=alpha_max, tau_c=tau_c)
+                                 alpha_max=alpha_max, tau_c=tau_c, attention_mask=attention_mask)
+        kh = lay["retrieval"]["k_hat"]
+        metrics[f"layer_{i}_alpha_mean"] = lay["alpha"].mean()
+        metrics[f"layer_{i}_k_hat_perp_ratio_mean"] = (
+            (lay["write_key"].norm(dim=-1) / kh.norm(dim=-1).clamp_min(1e-6)).clamp(0.0, 10.0).mean()
+            if write_mode == "residual" else torch.zeros(()))
+        metrics[f"layer_{i}_retrieval_confidence_mean"] = lay["retrieval"]["diagnostics"]["max_confidence"].mean()
         out = r(r(lay["o"]).reshape(B, T, C) @ w("o_proj.weight").T)
         if sparse_output_lambda > 0:
             sp = r(r(lay["v_hat"]).reshape(B, T, C) @ w("sparse_out_proj.weight").T)
@@ -652,7 +669,8 @@ def sgsa_model_forward(params: Dict[str, Tensor], input_ids: Tensor, *, num_laye
         gate, up = r(m @ w("mlp.gate_proj.weight").T), r(m @ w("mlp.up_proj.weight").T)
         h = r(h + r(r(r(F.silu(gate)) * up) @ w("mlp.down_proj.weight").T))
     head = P.get("lm_head.weight", P["embed_tokens.weight"])
-    return r(r(rms_norm(h, P["norm.weight"], eps)) @ head.T)
+    logits = r(r(rms_norm(h, P["norm.weight"], eps)) @ head.T)
+    return (logits, metrics) if return_metrics else logits
 
 
 # ---------------------------------------------------------------------------

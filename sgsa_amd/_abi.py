@@ -52,7 +52,11 @@ SIGNATURES = {
     "sgsa_score_topk_masked": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _I, _F, _I, _I, _I, _P, _P, _P, _P, _P, _P,
                                     _P, _P, _P, _P, _I, _P, _SZ, _P]),
     "sgsa_sparse_gather_masked": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P,
-                                       _I, _F, _F, _I, _I, _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),
+                                       _I, _F, _F, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),
+    "sgsa_layer_fwd_stats": (_I, [_I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _I, _F, _F, _P, _P,
+                                  _P, _P, _P, _SZ, _P]),
+    "sgsa_layer_retrieve_stats": (_I, [_I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _F, _F, _P, _P, _P, _P, _P,
+                                       _SZ, _P]),
     "sgsa_sparse_gather_tiled": (_I, [_I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _I, _F, _F, _P, _P, _P,
                                       _P, _P]),
     "sgsa_score_dump": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _F, _I, _P, _P, _I, _I, _P, _P]),

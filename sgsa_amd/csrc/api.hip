@@ -455,7 +455,7 @@ int sgsa_sparse_gather(int dtype, int B, int Tq, int Tk, int H, int D, int top_k
                        size_t workspace_bytes, void* stream) {
   return sgsa_sparse_gather_masked(dtype, B, Tq, Tk, H, D, top_k, q_offset, 0, k, v, self_key, indices, scores,
                                    nullptr, top2, counts, budget, write_mode, alpha_max, tau_c, local_window,
-                                   sink_size, k_hat, v_hat, write_key, alpha, weights, diag, workspace,
+                                   sink_size, k_hat, v_hat, write_key, alpha, weights, diag, nullptr, workspace,
                                    workspace_bytes, stream);
 }
 
@@ -465,7 +465,7 @@ int sgsa_sparse_gather_masked(int dtype, int B, int Tq, int Tk, int H, int D, in
                               const float* top2, const int32_t* counts, const float* budget, int write_mode,
                               float alpha_max, float tau_c, int local_window, int sink_size, void* k_hat,
                               void* v_hat, void* write_key, float* alpha, float* weights, float* diag,
-                              void* workspace, size_t workspace_bytes, void* stream) {
+                              float* row_stats, void* workspace, size_t workspace_bytes, void* stream) {
   if (kv_layout != 0 && kv_layout != 1) return fail(SGSA_ERR_INVALID_ARG, "kv_layout must be 0 ([B,Tk,H,D]) or 1 ([B,H,Tk,D])");
   if (int s = check_dtype(dtype)) return s;
   if (int s = check_dims(B, Tq, H, D)) return s;
@@ -490,6 +490,7 @@ int sgsa_sparse_gather_masked(int dtype, int B, int Tq, int Tk, int H, int D, in
   a.use_valid = 1; a.tau_c = tau_c; a.eps = 1e-6f; a.local_window = local_window; a.sink_size = sink_size;
   a.budget = budget; a.write_mode = write_mode; a.alpha_max = alpha_max;
   a.k_hat = k_hat; a.v_hat = v_hat; a.write_key = write_key; a.alpha = alpha; a.weights = weights; a.diag = diag;
+  a.stats = row_stats;
   a.max_index = diag ? (int32_t*)workspace : nullptr;
   const long rows = (long)B * H * Tq;
   const size_t pb = sgsa::gather_part_bytes(rows, top_k, D);
@@ -707,8 +708,8 @@ namespace {
 // K1 + K2 of the layer path into (wk, vh, al); the workspace is laid out by layer_ws.
 int layer_retrieve_impl(const LayerWs& L, char* base, int dtype, int B, int T, int H, int D, int top_k,
                         const void* q_ret, const void* k, const void* v, const float* budget, int write_mode,
-                        float alpha_max, float tau_c, void* wk, void* vh, float* al, hipStream_t st,
-                        const char* who) {
+                        float alpha_max, float tau_c, void* wk, void* vh, float* al, float* stats,
+                        hipStream_t st, const char* who) {
   const int kk = top_k < T ? top_k : T;
   int32_t* cnt = (int32_t*)(base + L.cnt);
   float* t2 = (float*)(base + L.top2);
@@ -733,6 +734,7 @@ int layer_retrieve_impl(const LayerWs& L, char* base, int dtype, int B, int T, i
   ga.budget = budget; ga.write_mode = write_mode; ga.alpha_max = alpha_max;
   ga.k_hat = write_mode == 0 ? wk : nullptr; ga.v_hat = vh; ga.write_key = write_mode == 1 ? wk : nullptr;
   ga.alpha = al;
+  ga.stats = stats;
   if (L.thr) {
     ga.top2 = t2;
     return hip_status(sgsa::launch_sparse_gather_thr(ga, q_ret, ta.thr, sgsa::score_multiplier(ta.scale, ta.scale_mode),
@@ -758,6 +760,14 @@ int sgsa_layer_retrieve(int dtype, int B, int T, int H, int D, int top_k, const 
                         const void* v, const float* budget, int write_mode, float alpha_max, float tau_c,
                         void* write_key, void* v_hat, float* alpha, void* workspace, size_t workspace_bytes,
                         void* stream) {
+  return sgsa_layer_retrieve_stats(dtype, B, T, H, D, top_k, q_ret, k, v, budget, write_mode, alpha_max, tau_c,
+                                   write_key, v_hat, alpha, nullptr, workspace, workspace_bytes, stream);
+}
+
+int sgsa_layer_retrieve_stats(int dtype, int B, int T, int H, int D, int top_k, const void* q_ret, const void* k,
+                              const void* v, const float* budget, int write_mode, float alpha_max, float tau_c,
+                              void* write_key, void* v_hat, float* alpha, float* row_stats, void* workspace,
+                              size_t workspace_bytes, void* stream) {
   if (int s = layer_check(dtype, B, T, H, D, top_k, write_mode)) return s;
   REQUIRE(q_ret); REQUIRE(k); REQUIRE(v); REQUIRE(budget); REQUIRE(write_key); REQUIRE(v_hat); REQUIRE(alpha);
   REQUIRE(workspace);
@@ -765,13 +775,23 @@ int sgsa_layer_retrieve(int dtype, int B, int T, int H, int D, int top_k, const 
   if (workspace_bytes < L.total) return fail(SGSA_ERR_WORKSPACE, "workspace %zu < %zu bytes", workspace_bytes, L.total);
   char* base = (char*)(((uintptr_t)workspace + kAlign - 1) & ~(uintptr_t)(kAlign - 1));
   return layer_retrieve_impl(L, base, dtype, B, T, H, D, top_k, q_ret, k, v, budget, write_mode, alpha_max, tau_c,
-                             write_key, v_hat, alpha, (hipStream_t)stream, "sgsa_layer_retrieve");
+                             write_key, v_hat, alpha, row_stats, (hipStream_t)stream, "sgsa_layer_retrieve");
 }
 
 int sgsa_layer_fwd(int dtype, int B, int T, int H, int D, int top_k, int chunk_size, const void* q, const void* k,
                    const void* v, const void* q_ret, const float* beta, const float* gamma, const float* budget,
                    const float* initial_state, int write_mode, float alpha_max, float tau_c, void* out,
                    float* final_state, void* workspace, size_t workspace_bytes, void* stream) {
+  return sgsa_layer_fwd_stats(dtype, B, T, H, D, top_k, chunk_size, q, k, v, q_ret, beta, gamma, budget,
+                              initial_state, write_mode, alpha_max, tau_c, out, final_state, nullptr, nullptr,
+                              workspace, workspace_bytes, stream);
+}
+
+int sgsa_layer_fwd_stats(int dtype, int B, int T, int H, int D, int top_k, int chunk_size, const void* q,
+                         const void* k, const void* v, const void* q_ret, const float* beta, const float* gamma,
+                         const float* budget, const float* initial_state, int write_mode, float alpha_max,
+                         float tau_c, void* out, float* final_state, float* alpha_out, float* row_stats,
+                         void* workspace, size_t workspace_bytes, void* stream) {
   if (int s = layer_check(dtype, B, T, H, D, top_k, write_mode)) return s;
   if (chunk_size <= 0) return fail(SGSA_ERR_INVALID_ARG, "chunk_size=%d must be positive", chunk_size);
   REQUIRE(q); REQUIRE(k); REQUIRE(v); REQUIRE(q_ret); REQUIRE(beta); REQUIRE(gamma); REQUIRE(budget);
@@ -781,10 +801,10 @@ int sgsa_layer_fwd(int dtype, int B, int T, int H, int D, int top_k, int chunk_s
   char* base = (char*)(((uintptr_t)workspace + kAlign - 1) & ~(uintptr_t)(kAlign - 1));
   void* wk = base + L.wk;
   void* vh = base + L.vh;
-  float* al = (float*)(base + L.al);
+  float* al = alpha_out ? alpha_out : (float*)(base + L.al);
   hipStream_t st = (hipStream_t)stream;
   if (int s = layer_retrieve_impl(L, base, dtype, B, T, H, D, top_k, q_ret, k, v, budget, write_mode, alpha_max,
-                                  tau_c, wk, vh, al, st, "sgsa_layer_fwd(retrieve)"))
+                                  tau_c, wk, vh, al, row_stats, st, "sgsa_layer_fwd(retrieve)"))
     return s;
 
   sgsa::ChunkArgs ca{};

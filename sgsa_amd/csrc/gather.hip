@@ -313,7 +313,7 @@ __global__ __launch_bounds__(256) void sparse_gather_kernel(GatherArgs a, int lp
   float wk[NE];
 #pragma unroll
   for (int i = 0; i < NE; ++i) wk[i] = ak[i];
-  float alpha_v = 0.f;
+  float alpha_v = 0.f, perp_ratio = 0.f;
   if (a.budget != nullptr) {
     float wnorm2 = hh2;
     if (a.write_mode == 1) {
@@ -325,12 +325,17 @@ __global__ __launch_bounds__(256) void sparse_gather_kernel(GatherArgs a, int lp
         pw += grp == 0 ? wk[i] * wk[i] : 0.f;
       }
       wnorm2 = wave_sum(pw);
+      perp_ratio = fminf(fmaxf(sqrtf(wnorm2) / kh_norm, 0.f), 10.f);
     }
     const float bud = a.budget[(long)(b * Tq + qr) * H + h];
     float al = a.alpha_max * conc * novelty * (1.f / (1.f + expf(-bud)));
     const float prox = al * sqrtf(vv2) * sqrtf(wnorm2);
     const float clip = fminf(1.f / fmaxf(prox, 1.f), 1.f);
     alpha_v = al * clip;
+  }
+  if (a.stats != nullptr && lane == 0) {
+    a.stats[row] = kq > 0 ? inv : 0.f;   // the largest weight, exp(0) / E
+    a.stats[nrows + row] = perp_ratio;
   }
 
   // ---- stores of the row vectors ----

@@ -206,7 +206,7 @@ __device__ __forceinline__ void tile_epilogue(const GatherArgs& a, const f4 (&ok
     float wk[DP / 16];
 #pragma unroll
     for (int n = 0; n < DP / 16; ++n) wk[n] = kh[n];
-    float alpha_v = 0.f;
+    float alpha_v = 0.f, perp_ratio = 0.f;
     if (a.budget != nullptr) {
       float wn2 = hh2;
       if (a.write_mode == 1) {
@@ -218,6 +218,7 @@ __device__ __forceinline__ void tile_epilogue(const GatherArgs& a, const f4 (&ok
           pw += wk[n] * wk[n];
         }
         wn2 = group_sum(pw, 16);
+        perp_ratio = fminf(fmaxf(sqrtf(wn2) / kh_norm, 0.f), 10.f);
       }
       const float bud = live ? a.budget[(long)(b * Tq + row) * H + h] : 0.f;
       const float al = a.alpha_max * conc * novelty * (1.f / (1.f + expf(-bud)));
@@ -233,6 +234,10 @@ __device__ __forceinline__ void tile_epilogue(const GatherArgs& a, const f4 (&ok
       reinterpret_cast<uint16_t*>(a.v_hat)[o] = f32_to_bf16(vh[n]);
     }
     if (a.alpha && lr == 0) a.alpha[(long)(b * Tq + row) * H + h] = alpha_v;
+    if (a.stats && lr == 0) {
+      a.stats[rg] = kq > 0 ? inv : 0.f;   // the largest weight, exp(0) / E
+      a.stats[(long)a.B * H * Tq + rg] = perp_ratio;
+    }
   }
 }
 

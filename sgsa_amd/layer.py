@@ -59,6 +59,7 @@ def sgsa_layer_forward(
     workspace: Optional[LayerWorkspace] = None,
     out: Optional[Tensor] = None,
     attention_mask: Optional[Tensor] = None,
+    stats: Optional[dict] = None,
 ) -> Tuple[Tensor, Optional[Tensor]]:
     """q,k,v,q_ret [B,T,H,D] (float32 or bfloat16); beta,gamma,budget_logits [B,T,H].
 
@@ -67,6 +68,8 @@ def sgsa_layer_forward(
     keys and queries (SparseRetriever.forward, modeling_sgsa.py:421-428); the
     state update itself takes no mask (:584-596).  The masked layer runs as
     its three entry points (masked select, masked gather + gate, chunked update).
+    ``stats`` (a dict) receives "alpha" [B,T,H] and "row_stats" [2,B,H,T]
+    (sgsa_layer_fwd_stats: largest weight, write-key norm ratio per row).
     """
     if not q.is_cuda:
         raise ValueError("sgsa_layer_forward: the SGSA kernels run on a ROCm GPU; got CPU tensors")
@@ -81,7 +84,7 @@ def sgsa_layer_forward(
         raise ValueError(f"write_mode must be one of {sorted(_WRITE_MODES)}")
     if attention_mask is not None:
         wk, vh, al = masked_gather_gate(q_ret, k, v, budget_logits, top_k, attention_mask, write_mode=write_mode,
-                                        alpha_max=alpha_max, tau_c=tau_c)
+                                        alpha_max=alpha_max, tau_c=tau_c, stats=stats)
         o, ht = chunk_sgsa_fwd(q, k, v, beta, gamma, wk, vh, al, initial_state=initial_state,
                                chunk_size=chunk_size, output_final_state=output_final_state)
         if out is not None:
@@ -97,11 +100,15 @@ def sgsa_layer_forward(
     ht = torch.empty(B, H, D, D, device=dev, dtype=torch.float32) if output_final_state else None
     nbytes = layer_workspace_bytes(q.dtype, B, T, H, D, top_k)
     ws = (workspace or LayerWorkspace()).get(nbytes, dev)
-    _abi.check(_abi.lib().sgsa_layer_fwd(
+    al = rs = None
+    if stats is not None:
+        al = stats["alpha"] = torch.empty(B, T, H, device=dev, dtype=torch.float32)
+        rs = stats["row_stats"] = torch.empty(2, B, H, T, device=dev, dtype=torch.float32)
+    _abi.check(_abi.lib().sgsa_layer_fwd_stats(
         _abi.dtype_code(q.dtype), B, T, H, D, int(top_k), int(chunk_size),
         _abi.ptr(qc), _abi.ptr(kc), _abi.ptr(vc), _abi.ptr(rc), _abi.ptr(bc), _abi.ptr(gc), _abi.ptr(uc),
         _abi.ptr(h0), _WRITE_MODES[write_mode], float(alpha_max), float(tau_c), _abi.ptr(out), _abi.ptr(ht),
-        _abi.ptr(ws), ws.numel(), _abi.stream_of(qc)))
+        _abi.ptr(al), _abi.ptr(rs), _abi.ptr(ws), ws.numel(), _abi.stream_of(qc)))
     return out, ht
 
 
@@ -116,6 +123,7 @@ def sgsa_layer_retrieve(
     tau_c: float = 0.1,
     workspace: Optional[LayerWorkspace] = None,
     attention_mask: Optional[Tensor] = None,
+    stats: Optional[dict] = None,
 ) -> Tuple[Tensor, Tensor, Tensor]:
     """The retrieval half of ``sgsa_layer_forward`` (sgsa_layer_retrieve): the
     (write key, v_hat, alpha) that the layer feeds to the chunked update
@@ -136,7 +144,7 @@ def sgsa_layer_retrieve(
         raise ValueError(f"write_mode must be one of {sorted(_WRITE_MODES)}")
     if attention_mask is not None:
         return masked_gather_gate(q_ret, k, v, budget_logits, top_k, attention_mask, write_mode=write_mode,
-                                  alpha_max=alpha_max, tau_c=tau_c)
+                                  alpha_max=alpha_max, tau_c=tau_c, stats=stats)
     dev = q_ret.device
     rc, kc, vc = (t.contiguous() for t in (q_ret, k, v))
     uc = budget_logits.float().contiguous()
@@ -145,8 +153,12 @@ def sgsa_layer_retrieve(
     al = torch.empty(B, T, H, device=dev, dtype=torch.float32)
     nbytes = layer_workspace_bytes(q_ret.dtype, B, T, H, D, top_k)
     ws = (workspace or LayerWorkspace()).get(nbytes, dev)
-    _abi.check(_abi.lib().sgsa_layer_retrieve(
+    rs = None
+    if stats is not None:
+        stats["alpha"] = al
+        rs = stats["row_stats"] = torch.empty(2, B, H, T, device=dev, dtype=torch.float32)
+    _abi.check(_abi.lib().sgsa_layer_retrieve_stats(
         _abi.dtype_code(q_ret.dtype), B, T, H, D, int(top_k), _abi.ptr(rc), _abi.ptr(kc), _abi.ptr(vc),
         _abi.ptr(uc), _WRITE_MODES[write_mode], float(alpha_max), float(tau_c), _abi.ptr(wk), _abi.ptr(vh),
-        _abi.ptr(al), _abi.ptr(ws), ws.numel(), _abi.stream_of(rc)))
+        _abi.ptr(al), _abi.ptr(rs), _abi.ptr(ws), ws.numel(), _abi.stream_of(rc)))
     return wk, vh, al

@@ -3,7 +3,7 @@
 Mirrors modelings/modeling_sgsa.py:634-767 (SGSABlock, SGSAForCausalLM) for the
 token_only retrieval mode with the chunked state backend:
 
-  h   = embed(ids) + pos_embed(positions)                            (:739-743)
+  h   = (embed(ids) + pos_embed(positions)) * attention_mask         (:739-743)
   per block (:669-709):
     n = RMSNorm(h);  q, k, v, q_ret = proj(n) as [B,T,H,D]
     beta  = sigmoid(beta_proj(n)).clamp_min(1e-4);  gamma = sigmoid(gamma_proj(n))   (:584-585)
@@ -11,6 +11,9 @@ token_only retrieval mode with the chunked state backend:
     h = h + o_proj(attended) [+ lambda * sparse_out_proj(v_hat)]
     h = h + down(silu(gate(m)) * up(m)),  m = RMSNorm(h)
   logits = lm_head(RMSNorm(h))   (lm_head tied to the embedding by default)
+  loss = cross_entropy(logits[:, :-1], labels[:, 1:], ignore_index=-100)  (:758-766)
+  metrics: per layer alpha_mean, k_hat_perp_ratio_mean, retrieval_confidence_mean
+           and the path flags (:697-708, :744-752)
 
 The layer core runs in the HIP library (sgsa_layer_forward); the projections,
 norms and the MLP are plain GEMMs and elementwise ops left to PyTorch
@@ -22,7 +25,7 @@ restatement of modelings/hybrid_dense_delta_topk.py:94-117.  Forward only.
 from __future__ import annotations
 
 from dataclasses import dataclass
-from typing import Dict, Optional
+from typing import Dict, Optional, Tuple
 
 import torch
 import torch.nn as nn
@@ -186,23 +189,45 @@ class SGSABlock(nn.Module):
         return (q.view(B, T, H, D), k.view(B, T, H, D), v.view(B, T, H, D), q_ret.view(B, T, H, D), beta, gamma,
                 budget)
 
-    def forward(self, h: Tensor) -> Tensor:
+    def forward(self, h: Tensor, attention_mask: Optional[Tensor] = None) -> Tuple[Tensor, Dict[str, Tensor]]:
+        """SGSABlock.forward (modeling_sgsa.py:660-709): (hidden states, metrics).
+
+        attention_mask [B,T] (nonzero = real token) reaches the retrieval only
+        (:668-674).  The metrics are the reference's: alpha_mean,
+        k_hat_perp_ratio_mean (residual write mode, else 0),
+        retrieval_confidence_mean (mean largest retrieval weight) and the path
+        flags, of which used_torch_chunk is 1 -- the chunked update runs.
+        """
         cfg = self.config
         B, T, C = h.shape
         q, k, v, q_ret, beta, gamma, budget = self._project(h)
+        stats: Dict[str, Tensor] = {}
         if cfg.sparse_output_lambda > 0:
             wk, vh, al = sgsa_layer_retrieve(q_ret, k, v, budget, cfg.top_k, cfg.sgsa_write_mode, cfg.alpha_max,
-                                             cfg.tau_c, workspace=self._ws)
+                                             cfg.tau_c, workspace=self._ws, attention_mask=attention_mask,
+                                             stats=stats)
             att, _ = chunk_sgsa(q, k, v, beta, gamma, wk, vh, al)
         else:
             att, _ = sgsa_layer_forward(q, k, v, q_ret, beta, gamma, budget, cfg.top_k,
                                         write_mode=cfg.sgsa_write_mode, alpha_max=cfg.alpha_max, tau_c=cfg.tau_c,
-                                        output_final_state=False, workspace=self._ws)
+                                        output_final_state=False, workspace=self._ws,
+                                        attention_mask=attention_mask, stats=stats)
         out = self.o_proj(att.reshape(B, T, C))
         if cfg.sparse_output_lambda > 0:
             out = out + cfg.sparse_output_lambda * self.sparse_out_proj(vh.reshape(B, T, C))
         h = h + out
-        return h + self.mlp(self.post_attn_norm(h))
+        h = h + self.mlp(self.post_attn_norm(h))
+        rs = stats["row_stats"]
+        zero = torch.zeros((), device=h.device)
+        metrics = {
+            "alpha_mean": stats["alpha"].mean(),
+            "k_hat_perp_ratio_mean": rs[1].mean() if cfg.sgsa_write_mode == "residual" else h.new_zeros(()),
+            "retrieval_confidence_mean": rs[0].mean(),
+            "used_fla_gdn": zero,
+            "used_torch_chunk": torch.ones((), device=h.device),
+            "used_recurrent": zero,
+        }
+        return h, metrics
 
 
 class SGSAForCausalLM(nn.Module):
@@ -238,12 +263,30 @@ class SGSAForCausalLM(nn.Module):
                         s = qk_std
                     p.copy_(torch.randn(p.shape, generator=generator, dtype=torch.float32) * s)
 
-    def forward(self, input_ids: Tensor) -> Dict[str, Tensor]:
+    def forward(self, input_ids: Tensor, attention_mask: Optional[Tensor] = None,
+                labels: Optional[Tensor] = None) -> Dict[str, object]:
+        """SGSAForCausalLM.forward (modeling_sgsa.py:733-767): {"logits", "metrics"}
+        and, with labels, "loss" -- the next-token cross entropy with ignore_index
+        -100 (:758-766).  attention_mask [B,T] zeroes the padded embeddings
+        (:740-741) and masks padded keys and queries in every retrieval."""
         B, T = input_ids.shape
         if T > self.config.max_position_embeddings:
             raise ValueError("sequence length exceeds max_position_embeddings")
         pos = torch.arange(T, device=input_ids.device)
         h = self.embed_tokens(input_ids) + self.pos_embed(pos)[None]
-        for layer in self.layers:
-            h = layer(h)
-        return {"logits": self.lm_head(self.norm(h))}
+        if attention_mask is not None:
+            h = h * attention_mask.unsqueeze(-1).to(h.dtype)
+        metrics: Dict[str, Tensor] = {}
+        for i, layer in enumerate(self.layers):
+            h, m = layer(h, attention_mask=attention_mask)
+            for name in ("alpha_mean", "k_hat_perp_ratio_mean", "retrieval_confidence_mean", "used_fla_gdn",
+                         "used_torch_chunk", "used_recurrent"):
+                metrics[f"layer_{i}_{name}"] = m[name]
+        logits = self.lm_head(self.norm(h))
+        out: Dict[str, object] = {"logits": logits, "metrics": metrics}
+        if labels is not None:
+            shift_logits = logits[:, :-1, :].contiguous()
+            shift_labels = labels[:, 1:].contiguous()
+            out["loss"] = F.cross_entropy(shift_logits.view(-1, shift_logits.size(-1)), shift_labels.view(-1),
+                                          ignore_index=-100)
+        return out

@@ -127,14 +127,15 @@ def gather_masked(k: Optional[Tensor], v: Tensor, idx: Tensor, sc: Tensor, valid
                   fill: Tensor, q_offset: int = 0, kv_layout: int = 0, self_key: Optional[Tensor] = None,
                   budget_logits: Optional[Tensor] = None, write_mode: str = "direct", alpha_max: float = 0.25,
                   tau_c: float = 0.1, local_window: int = 64, sink_size: int = 8, return_weights: bool = False,
-                  return_diagnostics: bool = False) -> Dict[str, Optional[Tensor]]:
+                  return_diagnostics: bool = False, return_stats: bool = False) -> Dict[str, Optional[Tensor]]:
     """sgsa_sparse_gather_masked over ``score_topk_masked`` output.
 
     k (None: V-only), v: [B,Tk,H,D] (kv_layout 0) or [B,H,Tk,D] (kv_layout 1).
     ``valid`` None: every filled slot takes its softmax weight (the hybrid's
     probabilities); else the retriever's softmax * valid / sum.  Returns a dict
     of k_hat / v_hat [B,Tq,H,D], write_key, alpha [B,Tq,H], weights
-    [B,H,Tq,kk] float32, diag [NDIAG,B,H,Tq] (None where not requested).
+    [B,H,Tq,kk] float32, diag [NDIAG,B,H,Tq], stats [2,B,H,Tq] (largest weight;
+    |write key| / |k_hat| in residual mode) (None where not requested).
     """
     B, H, Tq, kk = idx.shape
     Tk = v.shape[2] if kv_layout == 1 else v.shape[1]
@@ -151,6 +152,7 @@ def gather_masked(k: Optional[Tensor], v: Tensor, idx: Tensor, sc: Tensor, valid
     wkey = torch.empty_like(k_hat) if (bud is not None and mode == 1) else None
     weights = torch.empty(B, H, Tq, kk, device=dev, dtype=torch.float32) if return_weights else None
     diag = torch.empty(_abi.NDIAG, B, H, Tq, device=dev, dtype=torch.float32) if return_diagnostics else None
+    stats = torch.empty(2, B, H, Tq, device=dev, dtype=torch.float32) if return_stats else None
     L = _abi.lib()
     nbytes = ctypes.c_size_t()
     _abi.check(L.sgsa_sparse_gather_workspace_size(B, Tq, H, D, kk, ctypes.byref(nbytes)))
@@ -159,22 +161,27 @@ def gather_masked(k: Optional[Tensor], v: Tensor, idx: Tensor, sc: Tensor, valid
         _abi.dtype_code(v.dtype), B, Tq, Tk, H, D, kk, int(q_offset), int(kv_layout), _abi.ptr(kc), _abi.ptr(vc),
         _abi.ptr(skc), _abi.ptr(idx), _abi.ptr(sc), _abi.ptr(valid), _abi.ptr(top2), _abi.ptr(fill), _abi.ptr(bud),
         mode, float(alpha_max), float(tau_c), int(local_window), int(sink_size), _abi.ptr(k_hat), _abi.ptr(v_hat),
-        _abi.ptr(wkey), _abi.ptr(al), _abi.ptr(weights), _abi.ptr(diag), _abi.ptr(ws), nbytes.value,
+        _abi.ptr(wkey), _abi.ptr(al), _abi.ptr(weights), _abi.ptr(diag), _abi.ptr(stats), _abi.ptr(ws), nbytes.value,
         _abi.stream_of(vc)))
     return {"k_hat": k_hat, "v_hat": v_hat, "write_key": (wkey if mode == 1 else k_hat), "alpha": al,
-            "weights": weights, "diag": diag}
+            "weights": weights, "diag": diag, "stats": stats}
 
 
 def masked_gather_gate(q_ret: Tensor, k: Tensor, v: Tensor, budget_logits: Tensor, top_k: int,
                        attention_mask: Tensor, causal: bool = True, write_mode: str = "direct",
-                       alpha_max: float = 0.25, tau_c: float = 0.1) -> Tuple[Tensor, Tensor, Tensor]:
+                       alpha_max: float = 0.25, tau_c: float = 0.1,
+                       stats: Optional[dict] = None) -> Tuple[Tensor, Tensor, Tensor]:
     """Retrieval half of the SGSA layer under a padding mask [B,T] (the
     retriever's valid = causal & key_valid & query_valid, modeling_sgsa.py:421-428):
-    (write key, v_hat, alpha) for the chunked update."""
+    (write key, v_hat, alpha) for the chunked update.  ``stats`` (a dict) receives
+    "row_stats" as sgsa_layer_fwd_stats writes them."""
     idx, sc, valid, top2, cnt, fill = score_topk_masked(q_ret, k, top_k, key_mask=attention_mask,
                                                         query_mask=attention_mask, causal=causal, sorted=False)
     r = gather_masked(k, v, idx, sc, valid, top2, fill, self_key=k, budget_logits=budget_logits,
-                      write_mode=write_mode, alpha_max=alpha_max, tau_c=tau_c)
+                      write_mode=write_mode, alpha_max=alpha_max, tau_c=tau_c, return_stats=stats is not None)
+    if stats is not None:
+        stats["row_stats"] = r["stats"]
+        stats["alpha"] = r["alpha"]
     return r["write_key"], r["v_hat"], r["alpha"]
 
 

@@ -140,3 +140,32 @@ def test_layer_forward_carries_the_sparse_write(dev):
     gap = (ref - ref0).abs().max()
     assert gap > 0.05 * ref.abs().max(), "the sparse write is too small to test"
     assert (o - ref).abs().max() < 0.25 * gap
+
+
+@pytest.mark.parametrize("dtype,tol,dims", [
+    (torch.float32, 1e-4, (1, 512, 4, 64, 32)),        # direct gather
+    (torch.bfloat16, 2e-2, (1, 1024, 2, 128, 256)),    # threshold form (D = 128)
+])
+@pytest.mark.parametrize("write_mode", ["direct", "residual"])
+def test_layer_stats_match_oracle(dev, dtype, tol, dims, write_mode):
+    # sgsa_layer_fwd_stats / sgsa_layer_retrieve_stats: alpha, each row's largest
+    # weight (max_confidence, modeling_sgsa.py:374) and the write-key norm ratio (:614)
+    B, T, H, D, k = dims
+    x = O.make_inputs(B, T, H, D, dtype=dtype, seed=4)
+    ref = O.sgsa_layer_forward(x["q_f32"], x["k_f32"], x["v_f32"], x["q_f32"], x["beta"], x["gamma"],
+                               x["budget"], k, write_mode=write_mode)
+    g = {n: x[n].to(dev) for n in ("q", "k", "v", "beta", "gamma", "budget")}
+    s1, s2 = {}, {}
+    sgsa_amd.sgsa_layer_forward(g["q"], g["k"], g["v"], g["q"], g["beta"], g["gamma"], g["budget"], k,
+                                write_mode=write_mode, stats=s1)
+    sgsa_amd.sgsa_layer_retrieve(g["q"], g["k"], g["v"], g["budget"], k, write_mode=write_mode, stats=s2)
+    torch.cuda.synchronize()
+    kh = ref["retrieval"]["k_hat"]
+    ratio = (ref["write_key"].norm(dim=-1) / kh.norm(dim=-1).clamp_min(1e-6)).clamp(0, 10).transpose(1, 2)
+    for s in (s1, s2):
+        _close(s["alpha"], ref["alpha"], tol, "alpha")
+        _close(s["row_stats"][0], ref["retrieval"]["diagnostics"]["max_confidence"], tol, "max_confidence")
+        if write_mode == "residual":
+            _close(s["row_stats"][1], ratio, tol, "k_hat_perp ratio")
+        else:
+            assert (s["row_stats"][1] == 0).all()

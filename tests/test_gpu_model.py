@@ -70,3 +70,42 @@ def test_model_deterministic_and_finite_at_config2_width(dev):
     torch.cuda.synchronize()
     assert torch.isfinite(a).all()
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("dtype,tol,D", [(torch.float32, 1e-3, 64), (torch.bfloat16, 4e-2, 128)])
+@pytest.mark.parametrize("write_mode,lam", [("direct", 0.0), ("residual", 0.5)])
+def test_model_padding_labels_and_metrics_match_oracle(dev, dtype, tol, D, write_mode, lam):
+    # SGSAForCausalLM.forward(input_ids, attention_mask, labels) (modeling_sgsa.py:733-767):
+    # masked embeddings and retrieval, the shifted cross entropy, the per-layer metrics
+    H = 2
+    cfg, m = _model(dev, dtype, vocab_size=512, hidden_size=H * D, intermediate_size=384, num_hidden_layers=2,
+                    num_attention_heads=H, num_kv_heads=H, max_position_embeddings=512, top_k=32,
+                    sgsa_write_mode=write_mode, sparse_output_lambda=lam)
+    g = torch.Generator().manual_seed(2)
+    B, T = 3, 260
+    ids = torch.randint(1, 512, (B, T), generator=g)
+    am = torch.ones(B, T, dtype=torch.long)
+    am[1, :40] = 0        # left padding
+    am[2, T - 60:] = 0    # right padding
+    labels = ids.masked_fill(am == 0, -100)
+    with torch.no_grad():
+        out = m(ids.to(dev), attention_mask=am.to(dev), labels=labels.to(dev))
+    torch.cuda.synchronize()
+    params = {k: v.detach().float().cpu() for k, v in m.state_dict().items()}
+    ref, rmet = O.sgsa_model_forward(params, ids, num_layers=2, num_heads=H, top_k=32, write_mode=write_mode,
+                                     sparse_output_lambda=lam, act_dtype=dtype if dtype != torch.float32 else None,
+                                     attention_mask=am, return_metrics=True)
+    err = _rel(out["logits"], ref)
+    assert err <= tol, f"logits: max error {err:.3e} relative to max|ref| exceeds {tol:.1e}"
+    ref_loss = torch.nn.functional.cross_entropy(ref[:, :-1].reshape(-1, 512), labels[:, 1:].reshape(-1),
+                                                 ignore_index=-100)
+    assert abs(out["loss"].item() - ref_loss.item()) <= tol * abs(ref_loss.item()), \
+        f"loss {out['loss'].item()} vs {ref_loss.item()}"
+    names = ("alpha_mean", "k_hat_perp_ratio_mean", "retrieval_confidence_mean", "used_fla_gdn", "used_torch_chunk",
+             "used_recurrent")
+    assert set(out["metrics"]) == {f"layer_{i}_{n}" for i in range(2) for n in names}
+    for i in range(2):
+        for n in ("alpha_mean", "k_hat_perp_ratio_mean", "retrieval_confidence_mean"):
+            got, want = out["metrics"][f"layer_{i}_{n}"].item(), rmet[f"layer_{i}_{n}"].item()
+            assert abs(got - want) <= max(tol, 1e-4) * max(abs(want), 1e-3), f"layer {i} {n}: {got} vs {want}"
+        assert out["metrics"][f"layer_{i}_used_torch_chunk"].item() == 1.0
