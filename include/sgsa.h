@@ -347,6 +347,15 @@ int sgsa_sparse_gather_thresholds(int B, int T, int H, int D, int top_k, const v
                                   float alpha_max, float tau_c, void* k_hat, void* v_hat,
                                   void* write_key, float* alpha, void* stream);
 
+/* Known-answer hook of sgsa_sparse_gather_thresholds: the same kernel with
+ * the same selection, writing instead of the gathered rows each row's
+ * selection summary selection[b,h,t] = {count, sum of the selected key
+ * indices, xor of (index * 2654435761) mod 2^32} as int32 [B,H,T,3], to be
+ * compared exactly with the index lists of sgsa_score_topk. */
+int sgsa_gather_thresholds_selection(int B, int T, int H, int D, int top_k, const void* q, const void* k,
+                                     const void* v, const void* thr, const float* top2,
+                                     const int32_t* counts, int32_t* selection, void* stream);
+
 /* ---- whole SGSA layer forward ------------------------------------------------
  * The attention half of SGSABlock.forward (modelings/modeling_sgsa.py:669-684)
  * with the projections as inputs: token top-k retrieval on (q_ret, k, v)

@@ -14,7 +14,7 @@ The compiled library (libsgsa_hip.so) is required; there is no fallback path.
 
 from .ops import ChunkSGSAFunction, chunk_sgsa, chunk_sgsa_fwd
 from .retrieval import (SparseRetriever, block_retrieve, gather_gate, gather_lists, gather_masked, gather_thresholds,
-                        masked_gather_gate, score_dump, score_topk, score_topk_lists, score_topk_masked,
+                        masked_gather_gate, score_dump, gather_thresholds_selection, selection_summary, score_topk, score_topk_lists, score_topk_masked,
                         score_topk_thresholds, sparse_retrieve)
 from .layer import LayerWorkspace, sgsa_layer_forward, sgsa_layer_retrieve
 from .recurrent import fused_recurrent_sgsa

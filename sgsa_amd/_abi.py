@@ -81,6 +81,7 @@ SIGNATURES = {
     "sgsa_score_topk_thresholds": (_I, [_I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _SZ, _P]),
     "sgsa_sparse_gather_thresholds": (_I, [_I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _I, _F, _F, _P, _P,
                                            _P, _P, _P]),
+    "sgsa_gather_thresholds_selection": (_I, [_I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P]),
     "sgsa_layer_retrieve": (_I, [_I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _F, _F, _P, _P, _P, _P, _SZ, _P]),
 }
 

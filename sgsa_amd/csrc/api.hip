@@ -435,6 +435,23 @@ int sgsa_sparse_gather_thresholds(int B, int T, int H, int D, int top_k, const v
                     "sgsa_sparse_gather_thresholds");
 }
 
+int sgsa_gather_thresholds_selection(int B, int T, int H, int D, int top_k, const void* q, const void* k,
+                                     const void* v, const void* thr, const float* top2, const int32_t* counts,
+                                     int32_t* selection, void* stream) {
+  if (int s = check_dims(B, T, H, D)) return s;
+  if (D != 128) return fail(SGSA_ERR_UNSUPPORTED, "the threshold form needs D == 128 (got %d)", D);
+  if (top_k <= 0) return fail(SGSA_ERR_INVALID_ARG, "top_k=%d must be positive", top_k);
+  if ((long)T * H * D * 2 > 0x7fffffffL) return fail(SGSA_ERR_UNSUPPORTED, "one head's keys exceed 2 GiB of offsets");
+  REQUIRE(q); REQUIRE(k); REQUIRE(v); REQUIRE(thr); REQUIRE(top2); REQUIRE(counts); REQUIRE(selection);
+  sgsa::GatherArgs g{};
+  g.dtype = SGSA_BF16; g.B = B; g.Tq = T; g.Tk = T; g.H = H; g.D = D; g.top_k = top_k < T ? top_k : T;
+  g.q_offset = 0; g.k = k; g.v = v; g.self_key = k; g.top2 = top2; g.counts = counts;
+  g.use_valid = 1; g.eps = 1e-6f; g.sel_dbg = selection;
+  const float ms = sgsa::score_multiplier((float)sqrt((double)D), 0);
+  return hip_status(sgsa::launch_sparse_gather_thr(g, q, reinterpret_cast<const uint2*>(thr), ms, (hipStream_t)stream),
+                    "sgsa_gather_thresholds_selection");
+}
+
 int sgsa_score_dump(int dtype, int B, int Tq, int Tk, int H, int D, int causal, int q_offset, float scale,
                     int scale_mode, const void* q, const void* k, int row0, int rows, float* out, void* stream) {
   if (int s = validate_topk(dtype, B, Tq, Tk, H, D, 1, scale_mode, scale)) return s;

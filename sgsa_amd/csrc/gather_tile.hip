@@ -587,6 +587,10 @@ __device__ __forceinline__ s16x4 lds_read_tr(const uint16_t* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(p));
 }
 
+// DBG: a known-answer variant that writes, instead of the gathered rows, each
+// row's selection summary {count, sum of key indices, xor of (index * 2654435761)}
+// to a.sel_dbg [B,H,Tq,3] -- the selection applied exactly as the gather applies it.
+template <bool DBG>
 __global__ __launch_bounds__(256, 2) void gather_thr_kernel(GatherArgs a, const uint16_t* __restrict__ qg,
                                                          const uint2* __restrict__ thr, float mscale, int nqb2) {
   __shared__ __align__(16) uint16_t K0[KT * RP], V0[KT * RP], K1[KT * RP], V1[KT * RP];
@@ -697,6 +701,7 @@ __global__ __launch_bounds__(256, 2) void gather_thr_kernel(GatherArgs a, const 
     for (int n = 0; n < DP / 16; ++n) { ok_[mt][n] = f4_zero(); ov_[mt][n] = f4_zero(); }
   }
   const uint4 ones4 = make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u);   // bf16 1.0 x 8
+  uint32_t dcnt[2] = {0u, 0u}, dsum[2] = {0u, 0u}, dxor[2] = {0u, 0u};   // DBG only
 
   // score operand: row 32 sp + 16 hf + lr, chunk 4 s + lg -> slot 4 s + (lg ^ (lr >> 3))
   const int s_off = lr * RP + 8 * (lg ^ (lr >> 3));
@@ -738,6 +743,12 @@ __global__ __launch_bounds__(256, 2) void gather_thr_kernel(GatherArgs a, const 
             }
             const float e = __builtin_amdgcn_exp2f(fmaf(c, msl, -mxl[mt]));
             p[i] = sel ? e : 0.f;
+            if constexpr (DBG) {
+              const uint32_t j = (uint32_t)(t0 + 32 * sp + 8 * lg + 4 * hf + i);
+              dcnt[mt] += sel ? 1u : 0u;
+              dsum[mt] += sel ? j : 0u;
+              dxor[mt] ^= sel ? j * 2654435761u : 0u;
+            }
           }
           pw[mt][2 * hf] = pack_bf16x2(p[0], p[1]);
           pw[mt][2 * hf + 1] = pack_bf16x2(p[2], p[3]);
@@ -808,6 +819,26 @@ __global__ __launch_bounds__(256, 2) void gather_thr_kernel(GatherArgs a, const 
     }
   }
 
+  if constexpr (DBG) {
+    // lanes lr, lr + 16, lr + 32, lr + 48 hold row lr's keys
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+      for (int o = 16; o < 64; o <<= 1) {
+        dcnt[mt] += __shfl_xor(dcnt[mt], o, 64);
+        dsum[mt] += __shfl_xor(dsum[mt], o, 64);
+        dxor[mt] ^= __shfl_xor(dxor[mt], o, 64);
+      }
+      const int row = wr0 + 16 * mt + lr;
+      if (lg == 0 && row < Tq) {
+        int32_t* d = a.sel_dbg + ((long)bh * Tq + row) * 3;
+        d[0] = (int32_t)dcnt[mt];
+        d[1] = (int32_t)dsum[mt];
+        d[2] = (int32_t)dxor[mt];
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int mt = 0; mt < 2; ++mt) {
     const float E[4] = {es[mt][0], es[mt][1], es[mt][2], es[mt][3]};
@@ -833,8 +864,12 @@ hipError_t launch_sparse_gather_lists(const GatherArgs& a, const uint2* tl_list,
 hipError_t launch_sparse_gather_thr(const GatherArgs& a, const void* q, const uint2* thr, float mscale,
                                     hipStream_t st) {
   const int nqb2 = (a.Tq + QL - 1) / QL;
-  gather_thr_kernel<<<dim3((unsigned)(a.B * a.H * nqb2)), 256, 0, st>>>(
-      a, reinterpret_cast<const uint16_t*>(q), thr, mscale, nqb2);
+  if (a.sel_dbg)
+    gather_thr_kernel<true><<<dim3((unsigned)(a.B * a.H * nqb2)), 256, 0, st>>>(
+        a, reinterpret_cast<const uint16_t*>(q), thr, mscale, nqb2);
+  else
+    gather_thr_kernel<false><<<dim3((unsigned)(a.B * a.H * nqb2)), 256, 0, st>>>(
+        a, reinterpret_cast<const uint16_t*>(q), thr, mscale, nqb2);
   return hipGetLastError();
 }
 

@@ -161,6 +161,7 @@ struct GatherArgs {
   float* weights;            // [B,H,Tq,top_k] or nullptr
   float* diag;               // [NDIAG,B,H,Tq] or nullptr
   float* stats;              // [2,B,H,Tq] or nullptr: largest weight; |write key| / |k_hat| (residual mode, else 0)
+  int32_t* sel_dbg;          // threshold gather only: [B,H,Tq,3] selection summary instead of the outputs
   int32_t* max_index;        // GATHER_MAXIDX_SLOTS ints of scratch (256 bytes, diagnostics); required with diag
   const float* margin_in;    // [B,H,Tq] score margin to report instead of top-2 (block_only), or nullptr
   float ent_pad;             // zero-weight entries of the row beyond the slots (entropy terms of eps)

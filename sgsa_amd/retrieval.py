@@ -312,6 +312,36 @@ def gather_thresholds(q: Tensor, k: Tensor, v: Tensor, thr: Tensor, top2: Tensor
     return wk, vh, al
 
 
+def gather_thresholds_selection(q: Tensor, k: Tensor, v: Tensor, thr: Tensor, top2: Tensor, cnt: Tensor,
+                                top_k: int) -> Tensor:
+    """The selection K2 applies to ``score_topk_thresholds`` output, summarised per
+    row as int32 [B,H,T,3] = {count, sum of key indices, xor of index * 2654435761}
+    (sgsa_gather_thresholds_selection; compare with ``selection_summary``)."""
+    B, T, H, D = k.shape
+    qc, kc, vc = q.contiguous(), k.contiguous(), v.contiguous()
+    out = torch.empty(B, H, T, 3, device=k.device, dtype=torch.int32)
+    _abi.check(_abi.lib().sgsa_gather_thresholds_selection(
+        B, T, H, D, int(top_k), _abi.ptr(qc), _abi.ptr(kc), _abi.ptr(vc), _abi.ptr(thr), _abi.ptr(top2),
+        _abi.ptr(cnt), _abi.ptr(out), _abi.stream_of(kc)))
+    return out
+
+
+def selection_summary(idx: Tensor, cnt: Tensor) -> Tensor:
+    """{count, sum, xor of index * 2654435761} (mod 2^32, as int32) of the first
+    cnt slots of each row of index lists [..., k] -- the summary
+    ``gather_thresholds_selection`` reports."""
+    k = idx.shape[-1]
+    live = torch.arange(k, device=idx.device) < cnt[..., None]
+    j = idx.long() & 0xFFFFFFFF
+    s = torch.where(live, j, torch.zeros_like(j)).sum(-1) & 0xFFFFFFFF
+    hsh = torch.where(live, (j * 2654435761) & 0xFFFFFFFF, torch.zeros_like(j))
+    x = torch.zeros_like(hsh[..., 0])
+    for bit in range(32):   # xor over the slots, bit by bit (parity of the set bits)
+        x |= (((hsh >> bit) & 1).sum(-1) & 1) << bit
+    to_i32 = lambda t: torch.where(t >= 2 ** 31, t - 2 ** 32, t).to(torch.int32)
+    return torch.stack([cnt.to(torch.int32), to_i32(s), to_i32(x)], dim=-1)
+
+
 def score_dump(q: Tensor, k: Tensor, row0: int, rows: int, causal: bool = True, q_offset: int = 0,
                scale: Optional[float] = None, scale_mode: int = 0) -> Tensor:
     """The exact fp32 scores score_topk selects on, for query rows [row0, row0+rows): [B,H,rows,Tk]."""

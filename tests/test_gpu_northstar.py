@@ -5,6 +5,8 @@ The CPU oracle cannot run all sixteen heads, so the test combines:
   (a) the layer is its two halves: sgsa_layer_retrieve equals the threshold
       entry points (K1 score_thr128_kernel, K2 gather_thr_kernel) bit for bit,
       and sgsa_layer_fwd equals chunk_sgsa fed the retrieval outputs;
+  (a') the gather's own selection (its known-answer variant: per-row count,
+      index sum and index-hash xor) equals the row-list K1's on every row;
   (b) on 32 sampled (head, row) pairs -- rows t < k, t = k-1, t = k, mid
       sequence and the last row -- K1's per-row cut applied to the fp32 scores
       sgsa_score_dump returns selects exactly the lowest-index top-k of those
@@ -58,6 +60,19 @@ def test_layer_is_its_two_halves(ns):
         "sgsa_layer_retrieve differs from the threshold entry points"
     assert torch.equal(o2, ns["o"]), "sgsa_layer_fwd output differs from chunk_sgsa on its retrieval outputs"
     assert torch.equal(st2.float(), ns["st"]), "final states differ"
+
+
+def test_gather_selects_the_row_lists_key_for_key(ns):
+    # every row of every head: K2's selection (its known-answer variant) against
+    # the row-list K1's index lists, exactly
+    g = ns["g"]
+    got = sgsa_amd.gather_thresholds_selection(g["q"], g["k"], g["v"], ns["thr"], ns["t2"], ns["cnt"], K)
+    idx, _, _, cnt = sgsa_amd.score_topk(g["q"], g["k"], K, sorted=False)
+    want = sgsa_amd.selection_summary(idx, cnt)
+    del idx
+    torch.cuda.synchronize()
+    bad = (got != want).any(-1)
+    assert not bad.any(), f"{int(bad.sum())} rows select differently (first {bad.nonzero()[0].tolist()})"
 
 
 def test_counts_on_every_row(ns):

@@ -8,6 +8,9 @@ and applies it.
   fallback blocks), bursts of tied keys (the 128-row kernel's candidate
   staging overflows and the block goes to the fallback) and heavy-tailed
   inputs and a ragged shape.
+* K2's selection, key for key: the known-answer variant of the threshold
+  gather reports each row's {count, index sum, index hash xor} of the keys it
+  weighs, which must equal those of the row lists exactly.
 * K2 on the thresholds gives the outputs of K2 on the tile lists: the same
   selection, and weights that differ only in the rounding of the exponent's
   argument (one fused multiply-add on the raw accumulator instead of the
@@ -96,6 +99,22 @@ def test_thresholds_select_exactly_the_row_lists(dev, case, big):
     assert torch.equal(mask, ref), f"selected sets differ in {(mask != ref).sum().item()} (row, key) pairs"
     if case in ("ties", "mass_ties", "tile_burst"):
         assert (thr[..., 1] != 0x7fffffff).any(), "no row needed a tie cut"
+
+
+@pytest.mark.parametrize("case,big", SIZED, ids=SIZE_IDS)
+def test_threshold_gather_selects_key_for_key(dev, case, big):
+    # K2 recomputes the scores and applies K1's cut: its selection, summarised
+    # per row by the known-answer variant of the same kernel, equals the row
+    # lists' exactly (count, index sum, index hash xor)
+    q, kk, v, _, k = _inputs(case, dev, big)
+    print(f"threshold gather selection: case {case} shape {tuple(q.shape)} k={k}", flush=True)
+    thr, t2t, ct = sgsa_amd.score_topk_thresholds(q, kk, k)
+    got = sgsa_amd.gather_thresholds_selection(q, kk, v, thr, t2t, ct, k)
+    idx, sc, t2, cnt = sgsa_amd.score_topk(q, kk, k, sorted=False)
+    want = sgsa_amd.selection_summary(idx, cnt)
+    torch.cuda.synchronize()
+    bad = (got != want).any(-1)
+    assert not bad.any(), f"{int(bad.sum())} rows select differently (first {bad.nonzero()[0].tolist()})"
 
 
 @pytest.mark.parametrize("write_mode", ["direct", "residual"])
