@@ -8,7 +8,7 @@ swapping the import.  Differences, all deliberate:
   chunk_fwd.py:129);
 * ``use_triton`` is accepted and ignored; ``chunk_size`` is accepted, the
   kernels always use 64-token chunks (the result depends on it only through
-  rounding);
+  rounding), and a value other than 64 draws a warning;
 * decay ratios are exp(log-cumsum differences) rather than ratios of clamped
   prefix products (chunk_fwd.py:86, :110, :121), which follows the recurrent
   definition (naive.py:40) also where a chunk-local prefix falls below 1e-6;
@@ -22,6 +22,7 @@ reference's does (chunk_bwd.py:31-77); see ``backward.py``.
 from __future__ import annotations
 
 import ctypes
+import warnings
 from typing import Optional, Tuple
 
 import torch
@@ -56,6 +57,11 @@ def chunk_sgsa_fwd(
     """Forward body (replaces modelings/sgsa_ops/chunk_fwd.py:12-131)."""
     if not q.is_cuda:
         raise ValueError("chunk_sgsa: the SGSA kernels run on a ROCm GPU; got CPU tensors")
+    if chunk_size <= 0:
+        raise ValueError(f"chunk_size={chunk_size} must be positive")
+    if chunk_size != 64:
+        warnings.warn(f"chunk_sgsa: chunk_size={chunk_size} is accepted for compatibility; the kernels use "
+                      "64-token chunks, whose result differs from other chunkings only by rounding", stacklevel=3)
     B, T, H, D = q.shape
     dev = q.device
     for name, t in (("k", k), ("v", v)):
