@@ -77,6 +77,29 @@ int sgsa_chunk_fwd(int dtype, int B, int T, int H, int D, int chunk_size,
                    void* out, float* final_state,
                    void* workspace, size_t workspace_bytes, void* stream);
 
+/* Backward of sgsa_chunk_fwd: the gradients of <o, d_out> + <final_state,
+ * d_final_state> w.r.t. every input, for the function sgsa_chunk_fwd computes.
+ * Replaces chunk_sgsa_bwd (modelings/sgsa_ops/chunk_bwd.py:12-77), which
+ * recomputes the forward under torch autograd, and the backward the reference
+ * plans in modelings/sgsa_bwd_derivation.md:699-832.  Runs the fp32 chunk form
+ * for bf16 or fp32 inputs: the forward's per-chunk intermediates, a reverse
+ * scan of the state gradient over chunks, then every chunk's gradients in
+ * parallel.  d_out and dq, dk, dv, dsparse_k, dsparse_v are [B,T,H,D] in the
+ * input dtype; dbeta, dgamma, dalpha [B,T,H] fp32; d_final_state and
+ * d_initial_state [B,H,D,D] fp32 (either may be NULL).  The sparse write's
+ * inputs and gradients are given together or not at all.  Needs
+ * sgsa_chunk_bwd_workspace_size() bytes (about 0.8 MB per 64-token chunk and
+ * head with the sparse write). */
+int sgsa_chunk_bwd_workspace_size(int B, int T, int H, int D, int has_sparse, size_t* bytes);
+int sgsa_chunk_bwd(int dtype, int B, int T, int H, int D,
+                   const void* q, const void* k, const void* v,
+                   const float* beta, const float* gamma,
+                   const void* sparse_k, const void* sparse_v, const float* alpha,
+                   const float* initial_state, const void* d_out, const float* d_final_state,
+                   void* dq, void* dk, void* dv, float* dbeta, float* dgamma,
+                   void* dsparse_k, void* dsparse_v, float* dalpha, float* d_initial_state,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- score GEMM + exact token top-k ----------------------------------------
  * Replaces the dense scores and the per-row top-k loop of
  * SparseRetriever.forward / _masked_topk (modelings/modeling_sgsa.py:420-428,

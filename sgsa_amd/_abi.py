@@ -42,6 +42,9 @@ SIGNATURES = {
     "sgsa_last_error": (ctypes.c_char_p, []),
     "sgsa_chunk_fwd_workspace_size": (_I, [_I, _I, _I, _I, _I, ctypes.POINTER(_SZ)]),
     "sgsa_chunk_fwd": (_I, [_I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),
+    "sgsa_chunk_bwd_workspace_size": (_I, [_I, _I, _I, _I, _I, ctypes.POINTER(_SZ)]),
+    "sgsa_chunk_bwd": (_I, [_I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                            _P, _P, _P, _P, _SZ, _P]),
     "sgsa_score_topk_workspace_size": (_I, [_I, _I, _I, ctypes.POINTER(_SZ)]),
     "sgsa_score_topk_fast_workspace_size": (_I, [_I, _I, _I, _I, _I, _I, ctypes.POINTER(_SZ)]),
     "sgsa_score_topk": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _I, _F, _I, _P, _P, _P, _P, _P, _P, _P, _I, _P,

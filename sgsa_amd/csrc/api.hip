@@ -130,6 +130,46 @@ int sgsa_chunk_fwd(int dtype, int B, int T, int H, int D, int chunk_size, const 
   return hip_status(sgsa::launch_chunk_fwd(a, (hipStream_t)stream), "sgsa_chunk_fwd");
 }
 
+int sgsa_chunk_bwd_workspace_size(int B, int T, int H, int D, int has_sparse, size_t* bytes) {
+  if (int s = check_dims(B, T, H, D)) return s;
+  REQUIRE(bytes);
+  *bytes = sgsa::chunk_bwd_workspace_bytes(B, T, H, has_sparse != 0);
+  return SGSA_OK;
+}
+
+int sgsa_chunk_bwd(int dtype, int B, int T, int H, int D, const void* q, const void* k, const void* v,
+                   const float* beta, const float* gamma, const void* sparse_k, const void* sparse_v,
+                   const float* alpha, const float* initial_state, const void* d_out, const float* d_final_state,
+                   void* dq, void* dk, void* dv, float* dbeta, float* dgamma, void* dsparse_k, void* dsparse_v,
+                   float* dalpha, float* d_initial_state, void* workspace, size_t workspace_bytes, void* stream) {
+  if (int s = check_dtype(dtype)) return s;
+  if (int s = check_dims(B, T, H, D)) return s;
+  REQUIRE(q); REQUIRE(k); REQUIRE(v); REQUIRE(beta); REQUIRE(gamma); REQUIRE(d_out);
+  REQUIRE(dq); REQUIRE(dk); REQUIRE(dv); REQUIRE(dbeta); REQUIRE(dgamma); REQUIRE(workspace);
+  const int nsp = (sparse_k != nullptr) + (sparse_v != nullptr) + (alpha != nullptr);
+  if (nsp != 0 && nsp != 3) return fail(SGSA_ERR_INVALID_ARG, "sparse_k, sparse_v and alpha must be given together");
+  if (nsp == 3 && (dsparse_k == nullptr || dsparse_v == nullptr || dalpha == nullptr))
+    return fail(SGSA_ERR_INVALID_ARG, "the sparse write needs dsparse_k, dsparse_v and dalpha outputs");
+  if ((long)T * H > 0x7fffffffL) return fail(SGSA_ERR_UNSUPPORTED, "T*H too large");
+  const size_t need = sgsa::chunk_bwd_workspace_bytes(B, T, H, nsp == 3);
+  if (workspace_bytes < need) return fail(SGSA_ERR_WORKSPACE, "workspace %zu < %zu bytes", workspace_bytes, need);
+  sgsa::ChunkBwdArgs a{};
+  a.f.dtype = dtype; a.f.B = B; a.f.T = T; a.f.H = H; a.f.D = D;
+  a.f.q = q; a.f.k = k; a.f.v = v; a.f.beta = beta; a.f.gamma = gamma;
+  a.f.sparse_k = nsp == 3 ? sparse_k : nullptr;
+  a.f.sparse_v = nsp == 3 ? sparse_v : nullptr;
+  a.f.alpha = nsp == 3 ? alpha : nullptr;
+  a.f.initial_state = initial_state;
+  a.d_out = d_out; a.d_final_state = d_final_state;
+  a.dq = dq; a.dk = dk; a.dv = dv; a.dbeta = dbeta; a.dgamma = dgamma;
+  a.dsk = nsp == 3 ? dsparse_k : nullptr;
+  a.dsv = nsp == 3 ? dsparse_v : nullptr;
+  a.dalpha = nsp == 3 ? dalpha : nullptr;
+  a.d_initial_state = d_initial_state;
+  a.workspace = workspace;
+  return hip_status(sgsa::launch_chunk_bwd(a, (hipStream_t)stream), "sgsa_chunk_bwd");
+}
+
 static int validate_topk(int dtype, int B, int Tq, int Tk, int H, int D, int top_k, int scale_mode, float scale) {
   if (int s = check_dtype(dtype)) return s;
   if (int s = check_dims(B, Tq, H, D)) return s;

@@ -68,7 +68,7 @@ __global__ __launch_bounds__(256) void chunk_intra_kernel(
     const X* __restrict__ k, const X* __restrict__ v, const X* __restrict__ sk, const X* __restrict__ sv,
     const float* __restrict__ beta, const float* __restrict__ alpha, const float* __restrict__ gamma,
     int T, int H, int D, int NT, float* __restrict__ Wout, float* __restrict__ Uout,
-    float* __restrict__ logd_out) {
+    float* __restrict__ logd_out, float* __restrict__ Aout = nullptr) {
   constexpr int M = SP ? 2 * L : L;
   constexpr int NB = M / 16;
   __shared__ float kap[M][PIT];
@@ -180,6 +180,18 @@ __global__ __launch_bounds__(256) void chunk_intra_kernel(
       for (int e = 0; e < 4; ++e) Tm[16 * I + 4 * lg + e][16 * J + lr] = r[e];
     }
     __syncthreads();
+  }
+
+  // A itself (the backward's operand): [M][M] row-major, zero above the diagonal.
+  if (Aout != nullptr) {
+    float* Ac = Aout + ((long)bh * NT + c) * M * M;
+    for (int e = tid; e < M * M; e += 256) {
+      const int i = e / M, j = e % M, I = i >> 4, J = j >> 4;
+      float x = 0.f;
+      if (I == J) x = inv[I][i & 15][j & 15];
+      else if (J < I) x = Tm[i][j];
+      Ac[e] = x;
+    }
   }
 
   // W = A diag(D_tau) kappa, then U = A nu.  Wave w owns output column tiles 2w, 2w+1.
@@ -467,6 +479,35 @@ static hipError_t launch_chunk_t(const ChunkArgs& a, hipStream_t st) {
   chunk_out_kernel<X, SP><<<dim3(NT, BH), 256, 0, st>>>(q, k, sk, a.beta, a.alpha, lgd, Hs, R, a.T, a.H, a.D, NT,
                                                         (X*)a.out);
   return hipGetLastError();
+}
+
+// The forward's intermediates for the backward (chunk_bwd.hip): W, U, R, the
+// chunk-start states, the chunk-local log-decay prefixes and A, for bf16 or
+// fp32 inputs alike (loaded into fp32).
+template <typename X, bool SP>
+static hipError_t launch_recompute_t(const ChunkArgs& a, float* W, float* U, float* R, float* Hs, float* lgd, float* A,
+                                     hipStream_t st) {
+  const int NT = (a.T + L - 1) / L;
+  const int BH = a.B * a.H;
+  const X* k = (const X*)a.k;
+  const X* v = (const X*)a.v;
+  const X* sk = (const X*)a.sparse_k;
+  const X* sv = (const X*)a.sparse_v;
+  chunk_intra_kernel<X, SP><<<dim3(NT, BH), 256, 0, st>>>(k, v, sk, sv, a.beta, a.alpha, a.gamma, a.T, a.H, a.D,
+                                                          NT, W, U, lgd, A);
+  chunk_state_kernel<X, SP><<<dim3(DP / 16, BH), 256, 0, st>>>(k, sk, a.beta, a.alpha, W, U, lgd,
+                                                               a.initial_state, a.T, a.H, a.D, NT, Hs, R, nullptr);
+  return hipGetLastError();
+}
+
+hipError_t launch_chunk_recompute(const ChunkArgs& a, float* W, float* U, float* R, float* Hs, float* lgd, float* A,
+                                  hipStream_t st) {
+  const bool sp = a.sparse_k != nullptr;
+  if (a.dtype == DT_BF16)
+    return sp ? launch_recompute_t<bf16_t, true>(a, W, U, R, Hs, lgd, A, st)
+              : launch_recompute_t<bf16_t, false>(a, W, U, R, Hs, lgd, A, st);
+  return sp ? launch_recompute_t<float, true>(a, W, U, R, Hs, lgd, A, st)
+            : launch_recompute_t<float, false>(a, W, U, R, Hs, lgd, A, st);
 }
 
 hipError_t launch_chunk_fwd(const ChunkArgs& a, hipStream_t st) {

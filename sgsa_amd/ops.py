@@ -15,20 +15,21 @@ swapping the import.  Differences, all deliberate:
 * unsupported input (CPU tensors, float16, D > 128) raises instead of falling
   back to another implementation.
 
-The backward recomputes the forward in torch under autograd, as the
-reference's does (chunk_bwd.py:31-77); see ``backward.py``.
+The backward is native too (sgsa_chunk_bwd, chunk_bwd.hip): the gradient of
+the chunk form written out, where the reference recomputes the forward under
+torch autograd (chunk_bwd.py:31-77).  ``backward.py`` keeps a differentiable
+torch form of the same function, which the tests use as a second reference.
 """
 
 from __future__ import annotations
 
 import ctypes
 import warnings
-from typing import Optional, Tuple
+from typing import List, Optional, Sequence, Tuple
 
 import torch
 
 from . import _abi
-from .backward import recompute_grads
 
 Tensor = torch.Tensor
 
@@ -99,14 +100,66 @@ def chunk_sgsa_fwd(
     return out, ht
 
 
+def chunk_sgsa_bwd(
+    inputs: Sequence[Optional[Tensor]],
+    needs: Sequence[bool],
+    do: Optional[Tensor],
+    dht: Optional[Tensor],
+) -> List[Optional[Tensor]]:
+    """Native backward (sgsa_chunk_bwd): the gradients of <o, do> + <S_T, dht>
+    w.r.t. (q, k, v, beta, gamma, sparse_k, sparse_v, alpha, initial_state) for
+    the function the forward kernels compute -- the role of chunk_sgsa_bwd
+    (modelings/sgsa_ops/chunk_bwd.py:12-77).  ``inputs`` holds those nine
+    tensors (None where absent), ``needs[i]`` whether input i wants a gradient.
+    Returns nine entries, None where absent or not needed; each gradient has its
+    input's dtype (the kernels compute in fp32).
+    """
+    q, k, v, beta, gamma, sk, sv, alpha, h0 = inputs
+    B, T, H, D = q.shape
+    dev = q.device
+    dt = q.dtype
+    code = _abi.dtype_code(dt)
+    has_sparse = sk is not None
+    cast = lambda t: t.to(dt).contiguous()
+    qc, kc, vc = cast(q), cast(k), cast(v)
+    bc, gc = beta.float().contiguous(), gamma.float().contiguous()
+    skc = cast(sk) if has_sparse else None
+    svc = cast(sv) if has_sparse else None
+    ac = alpha.float().contiguous() if has_sparse else None
+    h0c = h0.float().contiguous() if h0 is not None else None
+    doc = cast(do) if do is not None else torch.zeros_like(qc)
+    dhtc = dht.float().contiguous() if dht is not None else None
+    dq, dk, dv = torch.empty_like(qc), torch.empty_like(kc), torch.empty_like(vc)
+    dbeta = torch.empty(B, T, H, device=dev, dtype=torch.float32)
+    dgamma = torch.empty_like(dbeta)
+    dsk = torch.empty_like(skc) if has_sparse else None
+    dsv = torch.empty_like(svc) if has_sparse else None
+    dalpha = torch.empty_like(dbeta) if has_sparse else None
+    dh0 = torch.empty(B, H, D, D, device=dev, dtype=torch.float32) if h0 is not None else None
+    L = _abi.lib()
+    nbytes = ctypes.c_size_t()
+    _abi.check(L.sgsa_chunk_bwd_workspace_size(B, T, H, D, int(has_sparse), ctypes.byref(nbytes)))
+    ws = torch.empty(nbytes.value, device=dev, dtype=torch.uint8)
+    _abi.check(L.sgsa_chunk_bwd(
+        code, B, T, H, D, _abi.ptr(qc), _abi.ptr(kc), _abi.ptr(vc), _abi.ptr(bc), _abi.ptr(gc), _abi.ptr(skc),
+        _abi.ptr(svc), _abi.ptr(ac), _abi.ptr(h0c), _abi.ptr(doc), _abi.ptr(dhtc), _abi.ptr(dq), _abi.ptr(dk),
+        _abi.ptr(dv), _abi.ptr(dbeta), _abi.ptr(dgamma), _abi.ptr(dsk), _abi.ptr(dsv), _abi.ptr(dalpha),
+        _abi.ptr(dh0), _abi.ptr(ws), nbytes.value, _abi.stream_of(qc)))
+    grads = [dq, dk, dv, dbeta, dgamma, dsk, dsv, dalpha, dh0]
+    out: List[Optional[Tensor]] = []
+    for x, g, n in zip(inputs, grads, needs):
+        out.append(g.to(x.dtype) if (x is not None and n and g is not None) else None)
+    return out
+
+
 class ChunkSGSAFunction(torch.autograd.Function):
     """Autograd wrapper with the reference's argument list (modelings/sgsa_ops/chunk.py:13-101).
 
-    The forward runs the HIP kernels.  The backward keeps the reference's
-    recompute semantics (chunk.py:58-101 -> chunk_bwd.py:31-77): the forward is
-    recomputed in torch under autograd (``backward.chunk_sgsa_torch``, the
-    function the kernels compute) and differentiated; it returns the 9 input
-    gradients (None for absent optionals) and None for the 5 flags.
+    The forward runs the HIP kernels; so does the backward (``chunk_sgsa_bwd``,
+    sgsa_chunk_bwd: the gradient of the chunk form, where the reference
+    recomputes the forward under torch autograd, chunk.py:58-101 ->
+    chunk_bwd.py:31-77).  It returns the 9 input gradients (None for absent
+    optionals) and None for the 5 flags.
     """
 
     @staticmethod
@@ -129,7 +182,7 @@ class ChunkSGSAFunction(torch.autograd.Function):
         hs, hi = ctx.has_sparse, ctx.has_initial_state
         inputs = [q, k, v, beta, gamma, sparse_k if hs else None, sparse_v if hs else None, alpha if hs else None,
                   initial_state if hi else None]
-        grads = recompute_grads(inputs, ctx.needs_input_grad[:9], do, dht)
+        grads = chunk_sgsa_bwd(inputs, ctx.needs_input_grad[:9], do, dht)
         return (*grads, None, None, None, None, None)
 
 

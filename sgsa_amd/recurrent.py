@@ -16,7 +16,7 @@ from typing import Optional, Tuple
 import torch
 
 from . import _abi
-from .backward import recompute_grads
+from .ops import chunk_sgsa_bwd
 from .ops import _check_layout
 
 Tensor = torch.Tensor
@@ -73,10 +73,11 @@ def recurrent_sgsa_fwd(
 class FusedRecurrentSGSAFunction(torch.autograd.Function):
     """Autograd wrapper of the recurrent op (modelings/sgsa_ops/recurrent.py:13-135).
 
-    The forward runs the HIP recurrent kernel.  The backward recomputes the
-    forward in torch under autograd and differentiates <o, do> + <S_T, dS_T>,
-    as the reference's does (recurrent.py:78-135); the recompute is the chunk
-    form of the same recurrence (``backward.chunk_sgsa_torch``).
+    The forward runs the HIP recurrent kernel.  The backward is the native
+    chunk-form backward (sgsa_chunk_bwd) of the same function: the recurrence
+    and the chunk form are one map, so its gradient of <o, do> + <S_T, dS_T>
+    is the recurrence's (the reference recomputes under autograd,
+    recurrent.py:78-135).
     """
 
     @staticmethod
@@ -99,7 +100,7 @@ class FusedRecurrentSGSAFunction(torch.autograd.Function):
         hs, hi = ctx.has_sparse, ctx.has_initial_state
         inputs = [q, k, v, beta, gamma, sparse_k if hs else None, sparse_v if hs else None, alpha if hs else None,
                   initial_state if hi else None]
-        grads = recompute_grads(inputs, ctx.needs_input_grad[:9], do, dht)
+        grads = chunk_sgsa_bwd(inputs, ctx.needs_input_grad[:9], do, dht)
         return (*grads, None, None, None)
 
 
@@ -117,7 +118,7 @@ def fused_recurrent_sgsa(
     use_triton: bool = True,
 ) -> Tuple[Tensor, Optional[Tensor]]:
     """q, k, v [B,T,H,D]; beta, gamma [B,T,H]; state [B,H,D,D] (float32 out).
-    Differentiable: the backward recomputes in torch (FusedRecurrentSGSAFunction)."""
+    Differentiable: the backward is the native chunk-form backward (FusedRecurrentSGSAFunction)."""
     if not q.is_cuda:
         raise ValueError("fused_recurrent_sgsa: the SGSA kernels run on a ROCm GPU; got CPU tensors")
     has_sparse = sparse_k is not None and sparse_v is not None and alpha is not None

@@ -1,11 +1,13 @@
 """GPU: backward of chunk_sgsa and fused_recurrent_sgsa through their autograd
-wrappers (HIP forward, torch recompute backward as in
-modelings/sgsa_ops/chunk_bwd.py:31-77 and recurrent.py:78-135), against torch
-autograd through the oracle's token recurrence (naive.py:34-57) in float64 on
-the CPU.  float32 inputs: gradients within 1e-4 of the largest magnitude;
-bfloat16 inputs: gradients come back in bfloat16, within 2e-2.
-The loss follows the reference's tests (tests/test_sgsa_core.py:190, :261):
-out.square().mean() + state.square().mean().
+wrappers (HIP forward, native HIP backward sgsa_chunk_bwd in place of the
+reference's recompute, modelings/sgsa_ops/chunk_bwd.py:31-77 and
+recurrent.py:78-135), against torch autograd through the oracle's token
+recurrence (naive.py:34-57) in float64 on the CPU.  float32 inputs: gradients
+within 1e-4 of the largest magnitude; bfloat16 inputs: gradients come back in
+bfloat16, within 2e-2.  The loss follows the reference's tests
+(tests/test_sgsa_core.py:190, :261): out.square().mean() + state.square().mean().
+At larger shapes the native backward is compared with the torch recompute of
+the same function (sgsa_amd.backward.recompute_grads) on the GPU.
 """
 
 import pytest
@@ -104,3 +106,37 @@ def test_backward_only_some_inputs_and_no_final_state(dev):
         ref = leaves[name].grad
         err = (t.grad.double().cpu() - ref).abs().max() / ref.abs().max()
         assert err <= 1e-4, f"{name}: {err:.3e}"
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-4), (torch.bfloat16, 1e-2)])
+@pytest.mark.parametrize("dims,sparse,init", [((1, 700, 3, 128), True, True), ((2, 333, 2, 40), False, True),
+                                              ((1, 129, 2, 96), True, False)])
+def test_native_backward_matches_torch_recompute(dev, dtype, tol, dims, sparse, init):
+    from sgsa_amd.backward import recompute_grads
+    from sgsa_amd.ops import chunk_sgsa_bwd
+    B, T, H, D = dims
+    x = _inputs(B, T, H, D, sparse, init, seed=21)
+    inputs = []
+    for n in ORDER:
+        t = x[n]
+        if t is not None:
+            t = t.to(dev)
+            t = t.to(dtype) if n in ("q", "k", "v", "sparse_k", "sparse_v") else t.float()
+        inputs.append(t)
+    g = torch.Generator().manual_seed(22)
+    do = torch.randn(B, T, H, D, generator=g).to(dev, dtype)
+    dht = torch.randn(B, H, D, D, generator=g).to(dev)
+    print(f"native backward {dims} sparse={sparse} init={init} {dtype}", flush=True)
+    needs = [t is not None for t in inputs]
+    got = chunk_sgsa_bwd(inputs, needs, do, dht)
+    f32 = [None if t is None else t.float() for t in inputs]
+    want = recompute_grads(f32, needs, do.float(), dht)
+    torch.cuda.synchronize()
+    for n, a, b in zip(ORDER, got, want):
+        if b is None:
+            assert a is None, n
+            continue
+        a, b = a.double().cpu(), b.double().cpu()
+        assert torch.isfinite(a).all(), f"{n}: non-finite"
+        err = (a - b).abs().max() / b.abs().max().clamp_min(1e-12)
+        assert err <= tol, f"{n}: {err:.3e} from the torch recompute"
