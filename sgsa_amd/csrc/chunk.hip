@@ -481,33 +481,23 @@ static hipError_t launch_chunk_t(const ChunkArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
-// The forward's intermediates for the backward (chunk_bwd.hip): W, U, R, the
-// chunk-start states, the chunk-local log-decay prefixes and A, for bf16 or
-// fp32 inputs alike (loaded into fp32).
+// The forward's per-chunk intermediates for the backward (chunk_bwd.hip): W, U,
+// the log-decay prefix and A, for bf16 or fp32 inputs alike (loaded into fp32).
 template <typename X, bool SP>
-static hipError_t launch_recompute_t(const ChunkArgs& a, float* W, float* U, float* R, float* Hs, float* lgd, float* A,
-                                     hipStream_t st) {
+static hipError_t launch_intra_t(const ChunkArgs& a, float* W, float* U, float* lgd, float* A, hipStream_t st) {
   const int NT = (a.T + L - 1) / L;
   const int BH = a.B * a.H;
-  const X* k = (const X*)a.k;
-  const X* v = (const X*)a.v;
-  const X* sk = (const X*)a.sparse_k;
-  const X* sv = (const X*)a.sparse_v;
-  chunk_intra_kernel<X, SP><<<dim3(NT, BH), 256, 0, st>>>(k, v, sk, sv, a.beta, a.alpha, a.gamma, a.T, a.H, a.D,
-                                                          NT, W, U, lgd, A);
-  chunk_state_kernel<X, SP><<<dim3(DP / 16, BH), 256, 0, st>>>(k, sk, a.beta, a.alpha, W, U, lgd,
-                                                               a.initial_state, a.T, a.H, a.D, NT, Hs, R, nullptr);
+  chunk_intra_kernel<X, SP><<<dim3(NT, BH), 256, 0, st>>>((const X*)a.k, (const X*)a.v, (const X*)a.sparse_k,
+                                                          (const X*)a.sparse_v, a.beta, a.alpha, a.gamma, a.T, a.H,
+                                                          a.D, NT, W, U, lgd, A);
   return hipGetLastError();
 }
 
-hipError_t launch_chunk_recompute(const ChunkArgs& a, float* W, float* U, float* R, float* Hs, float* lgd, float* A,
-                                  hipStream_t st) {
+hipError_t launch_chunk_intra(const ChunkArgs& a, float* W, float* U, float* lgd, float* A, hipStream_t st) {
   const bool sp = a.sparse_k != nullptr;
   if (a.dtype == DT_BF16)
-    return sp ? launch_recompute_t<bf16_t, true>(a, W, U, R, Hs, lgd, A, st)
-              : launch_recompute_t<bf16_t, false>(a, W, U, R, Hs, lgd, A, st);
-  return sp ? launch_recompute_t<float, true>(a, W, U, R, Hs, lgd, A, st)
-            : launch_recompute_t<float, false>(a, W, U, R, Hs, lgd, A, st);
+    return sp ? launch_intra_t<bf16_t, true>(a, W, U, lgd, A, st) : launch_intra_t<bf16_t, false>(a, W, U, lgd, A, st);
+  return sp ? launch_intra_t<float, true>(a, W, U, lgd, A, st) : launch_intra_t<float, false>(a, W, U, lgd, A, st);
 }
 
 hipError_t launch_chunk_fwd(const ChunkArgs& a, hipStream_t st) {

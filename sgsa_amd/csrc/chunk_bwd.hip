@@ -3,23 +3,28 @@
 // The reference differentiates chunk_sgsa by recomputing the forward in torch
 // under autograd (modelings/sgsa_ops/chunk_bwd.py:12-77; the plan of a kernel
 // backward is modelings/sgsa_bwd_derivation.md:699-832).  Here the gradient of
-// the chunk form is written out and run as three stages, all on MFMA in fp32:
+// the chunk form is written out and run on fp32 MFMA, for bf16 or fp32 inputs:
 //
-//   1. the forward's intermediates (chunk.hip, launch_chunk_recompute): per
-//      chunk the WY inverse A = (I+T)^-1, W = A diag(D_tau) kappa, U = A nu,
-//      R = U - W S, the chunk-start state S and the log-decay prefix l;
-//   2. chunk_bwd_scan_kernel, sequential over chunks from the last, per
-//      16-column slice of the state: the state gradient G at every chunk end,
-//      and dR = P^T dO + diag(c) kappa G;
-//   3. chunk_bwd_grad_kernel, parallel over chunks: every input gradient of a
-//      chunk from (S, G, dR) and its inputs.
+//   1. chunk_intra_kernel (chunk.hip): per chunk the WY inverse A = (I+T)^-1,
+//      W = A diag(D_tau) kappa, U = A nu and the log-decay prefix l;
+//   2. chunk_bwd_maps_kernel, parallel over chunks: the chunk's affine state
+//      map S' = Phi S + Pm, Phi = e^l_L I - kappa^T diag(c) W,
+//      Pm = kappa^T diag(c) U; chunk_bwd_fscan_kernel, sequential over chunks
+//      per 16-column slice: the chunk-start states;
+//   3. chunk_bwd_pre_kernel, parallel: X1 = P^T dO and the state-independent
+//      part of the state gradient's step, Y2 = Q^T diag(e^l) dO - W^T X1;
+//      chunk_bwd_bscan_kernel, sequential from the last chunk: the state
+//      gradient at every chunk end, G <- Phi^T G + Y2 (Phi^T = e^l_L I -
+//      W^T diag(c) kappa is the adjoint of the state map);
+//   4. chunk_bwd_grad_kernel, parallel over chunks: every input gradient of a
+//      chunk from its start state S, its end gradient G and its inputs.
 //
 // Per chunk (tokens t, samples i at token tau_i, M = 2L samples with the
 // sparse write, lambda = beta / alpha per sample):
 //
 //   P_ti = 1[tau_i <= t] exp(l_t - l_tau_i) lambda_i (q_t . kappa_i)
 //   c_i  = lambda_i exp(l_L - l_tau_i),   l_L the chunk's last prefix
-//   o    = diag(e^l) Q S + P R            S' = e^l_L S + kappa^T diag(c) R
+//   R    = U - W S,   o = diag(e^l) Q S + P R,   S' = e^l_L S + kappa^T diag(c) R
 //
 // and with dO the output gradient of the chunk and G = dS':
 //
@@ -39,7 +44,7 @@
 //   dgamma_p = [gamma_p >= 1e-6] / gamma_p * sum_{t >= p in the chunk} dl_t
 //
 // with dc_i = (kappa G)_i . R_i, and d(initial_state) the scan's dS of chunk 0.
-// The intermediates of stage 3 go through a per-chunk workspace (L2 traffic).
+// The intermediates of stage 4 go through a per-chunk workspace (L2 traffic).
 #include <float.h>
 
 #include "common.h"
@@ -72,141 +77,290 @@ __device__ __forceinline__ f4 mm(f4 acc, int K, FA&& fa, FB&& fb) {
   return acc;
 }
 
-// Stage 2.  grid (DP/16, B*H), 256 threads; block (cs, bh) owns state columns
-// [16 cs, 16 cs + 16); wave w owns state rows [32 w, 32 w + 32).
-template <typename X, bool SP>
-__global__ __launch_bounds__(256) void chunk_bwd_scan_kernel(ChunkBwdArgs a, const float* __restrict__ Wg,
-                                                             const float* __restrict__ lgd, float* __restrict__ Gend,
-                                                             float* __restrict__ dRg, int NT) {
-  constexpr int M = SP ? 2 * L : L;
-  __shared__ float Pm[L][M + 1];
-  __shared__ float Gs[DP][17];
-  __shared__ float dRs[M][17];
-  __shared__ float lam[M], cf[M], logd[L], el[L];
+constexpr int PIT = DP + 4;   // LDS row pitch (floats)
 
-  const int cs = blockIdx.x, bh = blockIdx.y;
-  const int B = a.f.B, T = a.f.T, H = a.f.H, D = a.f.D;
+// Stage 2a, parallel over chunks: Phi = e^l_L I - kappa^T diag(c) W and
+// Pm = kappa^T diag(c) U, [DP][DP] each.  grid (NT, B*H), 256 threads.
+template <typename X, bool SP>
+__global__ __launch_bounds__(256) void chunk_bwd_maps_kernel(ChunkBwdArgs a, const float* __restrict__ Wg,
+                                                             const float* __restrict__ Ug,
+                                                             const float* __restrict__ lgd,
+                                                             float* __restrict__ Phig, float* __restrict__ Pmg,
+                                                             int NT) {
+  constexpr int M = SP ? 2 * L : L;
+  __shared__ float kps[M][PIT];   // c_i kappa_i
+  __shared__ float ws[M][PIT];    // W, then U
+  const int c = blockIdx.x, bh = blockIdx.y;
+  const int T = a.f.T, H = a.f.H, D = a.f.D;
   const int b = bh / H, h = bh % H;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lg = lane >> 4;
+  const int t0 = c * L;
+  const long cb = (long)bh * NT + c;
+  const Rows<X> kk{(const X*)a.f.k, b, h, T, H, D}, ks{(const X*)a.f.sparse_k, b, h, T, H, D};
+  const float* lg_c = lgd + cb * L;
+  const float lL = lg_c[L - 1];
+  for (int e = tid; e < M * DP; e += 256) {
+    const int i = e / DP, d = e % DP;
+    const int tl = SP ? (i >> 1) : i;
+    const int t = t0 + tl;
+    float lm = 0.f;
+    if (t < T) lm = (SP && (i & 1)) ? a.f.alpha[(long)(b * T + t) * H + h] : a.f.beta[(long)(b * T + t) * H + h];
+    const float ci = lm * expf(lL - lg_c[tl]);
+    kps[i][d] = ci * ((SP && (i & 1)) ? ks(t, d) : kk(t, d));
+    ws[i][d] = Wg[cb * M * DP + e];
+  }
+  __syncthreads();
+  const float eL = expf(lL);
+  float* Phi = Phig + cb * DP * DP;
+  for (int tile = w; tile < (DP / 16) * (DP / 16); tile += 4) {
+    const int I = tile / (DP / 16), J = tile % (DP / 16);
+    const f4 x = mm(f4_zero(), M, [&](int r, int k) { return kps[k][16 * I + r]; },
+                    [&](int k, int cc) { return ws[k][16 * J + cc]; });
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int r = 16 * I + 4 * lg + e, cc = 16 * J + (lane & 15);
+      Phi[(long)r * DP + cc] = (r == cc ? eL : 0.f) - x[e];
+    }
+  }
+  __syncthreads();
+  for (int e = tid; e < M * DP; e += 256) ws[e / DP][e % DP] = Ug[cb * M * DP + e];
+  __syncthreads();
+  float* Pm = Pmg + cb * DP * DP;
+  for (int tile = w; tile < (DP / 16) * (DP / 16); tile += 4) {
+    const int I = tile / (DP / 16), J = tile % (DP / 16);
+    const f4 x = mm(f4_zero(), M, [&](int r, int k) { return kps[k][16 * I + r]; },
+                    [&](int k, int cc) { return ws[k][16 * J + cc]; });
+#pragma unroll
+    for (int e = 0; e < 4; ++e) Pm[(long)(16 * I + 4 * lg + e) * DP + 16 * J + (lane & 15)] = x[e];
+  }
+}
+
+// A sequential scan of the affine chunk maps over a 16-column slice: grid
+// (DP/16, B*H), 256 threads; wave w owns rows [32 w, 32 w + 32).  FWD: the
+// state, S_{c+1} = Phi_c S_c + Y_c from the first chunk, storing each S_c;
+// !FWD: the state gradient, G_{c-1} = Phi_c^T G_c + Y_c from the last chunk,
+// storing each G_c.  Phi_c is loaded into registers one chunk ahead and
+// staged in LDS (padded rows: both orientations read without bank conflicts).
+template <bool FWD>
+__global__ __launch_bounds__(256) void chunk_bwd_scan_kernel(const float* __restrict__ Phig,
+                                                             const float* __restrict__ Yg,
+                                                             const float* __restrict__ init, int D,
+                                                             float* __restrict__ out, float* __restrict__ last,
+                                                             int NT) {
+  constexpr int EPT = DP * DP / 256 / 4;   // float4 per thread
+  __shared__ float ph[DP][PIT];
+  __shared__ float xs[DP][17];
+  const int cs = blockIdx.x, bh = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lr = lane & 15, lg = lane >> 4;
   const int col = 16 * cs + lr;
-  (void)B;
-  const Rows<X> q{(const X*)a.f.q, b, h, T, H, D}, dO{(const X*)a.d_out, b, h, T, H, D};
-  const Rows<X> kk{(const X*)a.f.k, b, h, T, H, D}, ks{(const X*)a.f.sparse_k, b, h, T, H, D};
 
-  f4 G[2];
+  float4 pf[EPT];
+  auto prefetch = [&](int c) __attribute__((always_inline)) {
+    const float4* src = reinterpret_cast<const float4*>(Phig + ((long)bh * NT + c) * DP * DP);
+#pragma unroll
+    for (int u = 0; u < EPT; ++u) pf[u] = src[tid + 256 * u];
+  };
+  f4 x[2];
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int row = 16 * (2 * w + u) + 4 * lg + e;
-      float x = 0.f;
-      if (a.d_final_state != nullptr && row < D && col < D) x = a.d_final_state[((long)bh * D + row) * D + col];
-      G[u][e] = x;
+      x[u][e] = (init != nullptr && row < D && col < D) ? init[((long)bh * D + row) * D + col] : 0.f;
     }
   }
-
-  for (int c = NT - 1; c >= 0; --c) {
-    const int t0 = c * L;
-    auto kap = [&](int i, int d) __attribute__((always_inline)) {
-      const int tl = SP ? (i >> 1) : i;
-      return (SP && (i & 1)) ? ks(t0 + tl, d) : kk(t0 + tl, d);
-    };
-    if (tid < L) {
-      const float x = lgd[((long)bh * NT + c) * L + tid];
-      logd[tid] = x;
-      el[tid] = expf(x);
+  prefetch(FWD ? 0 : NT - 1);
+  for (int s = 0; s < NT; ++s) {
+    const int c = FWD ? s : NT - 1 - s;
+    const long cb = (long)bh * NT + c;
+#pragma unroll
+    for (int u = 0; u < EPT; ++u) {
+      const int e4 = tid + 256 * u, r = (4 * e4) / DP, c0 = (4 * e4) % DP;
+      ph[r][c0] = pf[u].x; ph[r][c0 + 1] = pf[u].y; ph[r][c0 + 2] = pf[u].z; ph[r][c0 + 3] = pf[u].w;
     }
-    __syncthreads();
-    if (tid < M) {
-      const int tl = SP ? (tid >> 1) : tid;
-      const int r = SP ? (tid & 1) : 0;
-      const int t = t0 + tl;
-      float lm = 0.f;
-      if (t < T) lm = r ? a.f.alpha[(long)(b * T + t) * H + h] : a.f.beta[(long)(b * T + t) * H + h];
-      lam[tid] = lm;
-      cf[tid] = lm * expf(logd[L - 1] - logd[tl]);
-    }
-    float* Gc = Gend + ((long)bh * NT + c) * DP * DP;
+    float* oc = out + cb * DP * DP;
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int row = 16 * (2 * w + u) + 4 * lg + e;
-        Gs[row][lr] = G[u][e];
-        Gc[(long)row * DP + col] = G[u][e];
+        xs[row][lr] = x[u][e];
+        oc[(long)row * DP + col] = x[u][e];
       }
     }
     __syncthreads();
-
-    // P [L][M]
-    for (int tile = w; tile < (L / 16) * (M / 16); tile += 4) {
-      const int I = tile / (M / 16), J = tile % (M / 16);
-      f4 acc = mm(f4_zero(), DP, [&](int r, int k) { return q(t0 + 16 * I + r, k); },
-                  [&](int k, int cc) { return kap(16 * J + cc, k); });
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int t = 16 * I + 4 * lg + e, i = 16 * J + lr;
-        const int ti = SP ? (i >> 1) : i;
-        Pm[t][i] = ti <= t ? expf(logd[t] - logd[ti]) * lam[i] * acc[e] : 0.f;
-      }
-    }
-    __syncthreads();
-
-    // dR[:, slice] = P^T dO[:, slice] + diag(c) kappa G[:, slice]
-    float* dRc = dRg + ((long)bh * NT + c) * M * DP;
-    for (int I = w; I < M / 16; I += 4) {
-      f4 acc = mm(f4_zero(), L, [&](int r, int k) { return Pm[k][16 * I + r]; },
-                  [&](int k, int cc) { return dO(t0 + k, 16 * cs + cc); });
-      f4 acc2 = mm(f4_zero(), DP, [&](int r, int k) { return kap(16 * I + r, k); },
-                   [&](int k, int cc) { return Gs[k][cc]; });
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int i = 16 * I + 4 * lg + e;
-        const float x = acc[e] + cf[i] * acc2[e];
-        dRs[i][lr] = x;
-        dRc[(long)i * DP + col] = x;
-      }
-    }
-    __syncthreads();
-
-    // G <- e^l_L G + Q^T diag(e^l) dO - W^T dR
-    const float* Wc = Wg + ((long)bh * NT + c) * M * DP;
-    const float eL = el[L - 1];
+    if (s + 1 < NT) prefetch(FWD ? c + 1 : c - 1);
+    const float* Yc = Yg + cb * DP * DP;
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int R0 = 16 * (2 * w + u);
-      f4 acc = mm(G[u] * eL, L, [&](int r, int k) { return q(t0 + k, R0 + r) * el[k]; },
-                  [&](int k, int cc) { return dO(t0 + k, 16 * cs + cc); });
-      f4 acc2 = mm(f4_zero(), M, [&](int r, int k) { return Wc[(long)k * DP + R0 + r]; },
-                   [&](int k, int cc) { return dRs[k][cc]; });
-      G[u] = acc - acc2;
+      const f4 acc = FWD ? mm(f4_zero(), DP, [&](int r, int k) { return ph[R0 + r][k]; },
+                              [&](int k, int cc) { return xs[k][cc]; })
+                         : mm(f4_zero(), DP, [&](int r, int k) { return ph[k][R0 + r]; },
+                              [&](int k, int cc) { return xs[k][cc]; });
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[u][e] = acc[e] + Yc[(long)(R0 + 4 * lg + e) * DP + col];
     }
     __syncthreads();
   }
-
-  if (a.d_initial_state != nullptr) {
+  if (last != nullptr) {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int row = 16 * (2 * w + u) + 4 * lg + e;
-        if (row < D && col < D) a.d_initial_state[((long)bh * D + row) * D + col] = G[u][e];
+        if (row < D && col < D) last[((long)bh * D + row) * D + col] = x[u][e];
       }
     }
   }
 }
 
-// Stage 3.  grid (NT, B*H), 256 threads: every gradient of one chunk.
+// Stage 3a, parallel over chunks: X1 = P^T dO [M][DP] and the state-independent
+// part of the state gradient's step, Y2 = Q^T diag(e^l) dO - W^T X1 [DP][DP].
+// grid (NT, B*H), 256 threads; q, kappa, dO staged in LDS as fp32.
 template <typename X, bool SP>
-__global__ __launch_bounds__(256) void chunk_bwd_grad_kernel(ChunkBwdArgs a, const float* __restrict__ Rg,
+__global__ __launch_bounds__(256) void chunk_bwd_pre_kernel(ChunkBwdArgs a, const float* __restrict__ Wg,
+                                                            const float* __restrict__ lgd,
+                                                            float* __restrict__ X1g, float* __restrict__ Y2g,
+                                                            int NT) {
+  constexpr int M = SP ? 2 * L : L;
+  __shared__ float qs[L][PIT];    // q, later P
+  __shared__ float kps[M][PIT];
+  __shared__ float dos[L][PIT];
+  __shared__ float lam[M], logd[L], el[L];
+
+  const int c = blockIdx.x, bh = blockIdx.y;
+  const int T = a.f.T, H = a.f.H, D = a.f.D;
+  const int b = bh / H, h = bh % H;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lg = lane >> 4;
+  const int t0 = c * L;
+  const long cb = (long)bh * NT + c;
+  const Rows<X> q{(const X*)a.f.q, b, h, T, H, D}, dO{(const X*)a.d_out, b, h, T, H, D};
+  const Rows<X> kk{(const X*)a.f.k, b, h, T, H, D}, ks{(const X*)a.f.sparse_k, b, h, T, H, D};
+  for (int e = tid; e < L * DP; e += 256) {
+    const int t = e / DP, d = e % DP;
+    qs[t][d] = q(t0 + t, d);
+    dos[t][d] = dO(t0 + t, d);
+  }
+  for (int e = tid; e < M * DP; e += 256) {
+    const int i = e / DP, d = e % DP;
+    const int tl = SP ? (i >> 1) : i;
+    kps[i][d] = (SP && (i & 1)) ? ks(t0 + tl, d) : kk(t0 + tl, d);
+  }
+  if (tid < L) {
+    const float x = lgd[cb * L + tid];
+    logd[tid] = x;
+    el[tid] = expf(x);
+  }
+  if (tid < M) {
+    const int tl = SP ? (tid >> 1) : tid;
+    const int r = SP ? (tid & 1) : 0;
+    const int t = t0 + tl;
+    float lm = 0.f;
+    if (t < T) lm = r ? a.f.alpha[(long)(b * T + t) * H + h] : a.f.beta[(long)(b * T + t) * H + h];
+    lam[tid] = lm;
+  }
+  __syncthreads();
+  // P (registers, then over q)
+  constexpr int NPT = (L / 16) * (M / 16) / 4;   // tiles per wave
+  f4 pt[NPT];
+#pragma unroll
+  for (int u = 0; u < NPT; ++u) {
+    const int tile = w + 4 * u, I = tile / (M / 16), J = tile % (M / 16);
+    const f4 x = mm(f4_zero(), DP, [&](int r, int k) { return qs[16 * I + r][k]; },
+                    [&](int k, int cc) { return kps[16 * J + cc][k]; });
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int t = 16 * I + 4 * lg + e, i = 16 * J + (lane & 15);
+      const int ti = SP ? (i >> 1) : i;
+      pt[u][e] = ti <= t ? expf(logd[t] - logd[ti]) * lam[i] * x[e] : 0.f;
+    }
+  }
+  // Y2 = Q^T diag(e^l) dO first (q is still in qs)
+  float* Y2 = Y2g + cb * DP * DP;
+  for (int tile = w; tile < (DP / 16) * (DP / 16); tile += 4) {
+    const int I = tile / (DP / 16), J = tile % (DP / 16);
+    const f4 x = mm(f4_zero(), L, [&](int r, int k) { return qs[k][16 * I + r] * el[k]; },
+                    [&](int k, int cc) { return dos[k][16 * J + cc]; });
+#pragma unroll
+    for (int e = 0; e < 4; ++e) Y2[(long)(16 * I + 4 * lg + e) * DP + 16 * J + (lane & 15)] = x[e];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < NPT; ++u) {
+    const int tile = w + 4 * u, I = tile / (M / 16), J = tile % (M / 16);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) qs[16 * I + 4 * lg + e][16 * J + (lane & 15)] = pt[u][e];
+  }
+  __syncthreads();
+  // X1 = P^T dO, kept in LDS (over kappa) for W^T X1
+  float* X1 = X1g + cb * M * DP;
+  for (int tile = w; tile < (M / 16) * (DP / 16); tile += 4) {
+    const int I = tile / (DP / 16), J = tile % (DP / 16);
+    const f4 x = mm(f4_zero(), L, [&](int r, int k) { return qs[k][16 * I + r]; },
+                    [&](int k, int cc) { return dos[k][16 * J + cc]; });
+#pragma unroll
+    for (int e = 0; e < 4; ++e) X1[(long)(16 * I + 4 * lg + e) * DP + 16 * J + (lane & 15)] = x[e];
+  }
+  __syncthreads();
+  for (int e = tid; e < M * DP; e += 256) kps[e / DP][e % DP] = X1[e];
+  __syncthreads();
+  // Y2 -= W^T X1
+  const float* Wc = Wg + cb * M * DP;
+  for (int tile = w; tile < (DP / 16) * (DP / 16); tile += 4) {
+    const int I = tile / (DP / 16), J = tile % (DP / 16);
+    const f4 x = mm(f4_zero(), M, [&](int r, int k) { return Wc[(long)k * DP + 16 * I + r]; },
+                    [&](int k, int cc) { return kps[k][16 * J + cc]; });
+#pragma unroll
+    for (int e = 0; e < 4; ++e) Y2[(long)(16 * I + 4 * lg + e) * DP + 16 * J + (lane & 15)] -= x[e];
+  }
+}
+
+// One 16 x 16 output tile over K (a multiple of 16) with the sum taken four k at
+// a time per lane: lane (r, g) of the MFMA takes k = k0 + 4g + j in the j-th of
+// four products, so fa4(r, k) / fb4(k, c) return the four consecutive k from k
+// (a float4 load where the operand is contiguous along k).
+template <typename FA, typename FB>
+__device__ __forceinline__ f4 mm4(f4 acc, int K, FA&& fa4, FB&& fb4) {
+  const int lane = threadIdx.x & 63, lr = lane & 15, lg = lane >> 4;
+#pragma unroll 2
+  for (int k0 = 0; k0 < K; k0 += 16) {
+    const float4 a = fa4(lr, k0 + 4 * lg), b = fb4(k0 + 4 * lg, lr);
+    acc = mma_f32(a.x, b.x, acc);
+    acc = mma_f32(a.y, b.y, acc);
+    acc = mma_f32(a.z, b.z, acc);
+    acc = mma_f32(a.w, b.w, acc);
+  }
+  return acc;
+}
+// p[r][k..k+3] (contiguous) and p[k..k+3][c] (a column), for row pitch n
+__device__ __forceinline__ float4 rowv(const float* p, int n, int r, int k) {
+  return *reinterpret_cast<const float4*>(p + (long)r * n + k);
+}
+__device__ __forceinline__ float4 colv(const float* p, int n, int k, int c) {
+  const float* q = p + (long)k * n + c;
+  return make_float4(q[0], q[n], q[2 * n], q[3 * n]);
+}
+
+// Stage 4.  grid (NT, B*H), 256 threads: every gradient of one chunk.  kappa, q
+// and dO stay in LDS as fp32 for the whole kernel; the other operands are
+// read from the workspace (L2).
+template <typename X, bool SP>
+__global__ __launch_bounds__(256) void chunk_bwd_grad_kernel(ChunkBwdArgs a, const float* __restrict__ Wg,
+                                                             const float* __restrict__ Ug,
+                                                             const float* __restrict__ X1g,
                                                              const float* __restrict__ Hs,
                                                              const float* __restrict__ lgd,
                                                              const float* __restrict__ Ag,
-                                                             const float* __restrict__ Gend,
-                                                             const float* __restrict__ dRg, float* __restrict__ scr,
+                                                             const float* __restrict__ Gend, float* __restrict__ scr,
                                                              int NT) {
   constexpr int M = SP ? 2 * L : L;
+  __shared__ __align__(16) float kps[M][PIT];
+  __shared__ __align__(16) float qs[L][PIT];
+  __shared__ __align__(16) float dos[L][PIT];
   __shared__ float lam[M], cf[M], etau[M], dlam[M], dcv[M];
   __shared__ float logd[L], el[L], dl[L];
   __shared__ float red[4];
@@ -220,30 +374,40 @@ __global__ __launch_bounds__(256) void chunk_bwd_grad_kernel(ChunkBwdArgs a, con
   const Rows<X> q{(const X*)a.f.q, b, h, T, H, D}, dO{(const X*)a.d_out, b, h, T, H, D};
   const Rows<X> kk{(const X*)a.f.k, b, h, T, H, D}, ks{(const X*)a.f.sparse_k, b, h, T, H, D};
   const Rows<X> vv{(const X*)a.f.v, b, h, T, H, D}, vs{(const X*)a.f.sparse_v, b, h, T, H, D};
-  auto kap = [&](int i, int d) __attribute__((always_inline)) {
+  auto nu4 = [&](int i, int d) __attribute__((always_inline)) {   // nu[i][d..d+3]
     const int tl = SP ? (i >> 1) : i;
-    return (SP && (i & 1)) ? ks(t0 + tl, d) : kk(t0 + tl, d);
-  };
-  auto nu = [&](int i, int d) __attribute__((always_inline)) {
-    const int tl = SP ? (i >> 1) : i;
-    return (SP && (i & 1)) ? vs(t0 + tl, d) : vv(t0 + tl, d);
+    const Rows<X>& src = (SP && (i & 1)) ? vs : vv;
+    return make_float4(src(t0 + tl, d), src(t0 + tl, d + 1), src(t0 + tl, d + 2), src(t0 + tl, d + 3));
   };
   auto tau = [](int i) { return SP ? (i >> 1) : i; };
+  const float* KS = &kps[0][0];
+  const float* QS = &qs[0][0];
+  const float* DS = &dos[0][0];
 
   const long cb = (long)bh * NT + c;
   const float* S = Hs + cb * DP * DP;      // [DP][DP] chunk-start state
   const float* G = Gend + cb * DP * DP;    // [DP][DP] state gradient at the chunk end
-  const float* R = Rg + cb * M * DP;       // [M][DP]
-  const float* dR = dRg + cb * M * DP;     // [M][DP]
   const float* A = Ag + cb * M * M;        // [M][M]
-  // per-chunk workspace: Y [L][M], dW [M][DP], Z [M][DP], dA [M][M], Tm [M][M], Xm [M][M]
-  float* Y = scr + cb * (size_t)(L * M + 2 * M * DP + 3 * M * M);
-  float* dW = Y + L * M;
+  // per-chunk workspace: R, dR, dW, Z [M][DP], Y [L][M], dA, Tm, Xm [M][M]
+  float* R = scr + cb * (size_t)(L * M + 4 * M * DP + 3 * M * M);
+  float* dR = R + M * DP;
+  float* dW = dR + M * DP;
   float* Z = dW + M * DP;
-  float* dA = Z + M * DP;
+  float* Y = Z + M * DP;
+  float* dA = Y + L * M;
   float* Tm = dA + M * M;
   float* Xm = Tm + M * M;
 
+  for (int e = tid; e < L * DP; e += 256) {
+    const int t = e / DP, d = e % DP;
+    qs[t][d] = q(t0 + t, d);
+    dos[t][d] = dO(t0 + t, d);
+  }
+  for (int e = tid; e < M * DP; e += 256) {
+    const int i = e / DP, d = e % DP;
+    const int tl = tau(i);
+    kps[i][d] = (SP && (i & 1)) ? ks(t0 + tl, d) : kk(t0 + tl, d);
+  }
   if (tid < L) {
     const float x = lgd[cb * L + tid];
     logd[tid] = x;
@@ -265,13 +429,34 @@ __global__ __launch_bounds__(256) void chunk_bwd_grad_kernel(ChunkBwdArgs a, con
   }
   __syncthreads();
 
+  // P0: R = U - W S and dR = X1 + diag(c) kappa G
+  {
+    const float* Wc = Wg + cb * M * DP;
+    const float* Uc = Ug + cb * M * DP;
+    const float* X1 = X1g + cb * M * DP;
+    for (int tile = w; tile < (M / 16) * (DP / 16); tile += 4) {
+      const int I = tile / (DP / 16), J = tile % (DP / 16);
+      const f4 ws = mm4(f4_zero(), DP, [&](int r, int k) { return rowv(Wc, DP, 16 * I + r, k); },
+                        [&](int k, int cc) { return colv(S, DP, k, 16 * J + cc); });
+      const f4 kg = mm4(f4_zero(), DP, [&](int r, int k) { return rowv(KS, PIT, 16 * I + r, k); },
+                        [&](int k, int cc) { return colv(G, DP, k, 16 * J + cc); });
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int i = 16 * I + 4 * lg + e, d = 16 * J + (lane & 15);
+        const long o = (long)i * DP + d;
+        R[o] = Uc[o] - ws[e];
+        dR[o] = X1[o] + cf[i] * kg[e];
+      }
+    }
+  }
+  __syncthreads();
   // P1: Y, and the P-terms of dlambda and dl
   for (int tile = w; tile < (L / 16) * (M / 16); tile += 4) {
     const int I = tile / (M / 16), J = tile % (M / 16);
-    const f4 qk = mm(f4_zero(), DP, [&](int r, int k) { return q(t0 + 16 * I + r, k); },
-                     [&](int k, int cc) { return kap(16 * J + cc, k); });
-    const f4 dp = mm(f4_zero(), DP, [&](int r, int k) { return dO(t0 + 16 * I + r, k); },
-                     [&](int k, int cc) { return R[(long)(16 * J + cc) * DP + k]; });
+    const f4 qk = mm4(f4_zero(), DP, [&](int r, int k) { return rowv(QS, PIT, 16 * I + r, k); },
+                      [&](int k, int cc) { return rowv(KS, PIT, 16 * J + cc, k); });
+    const f4 dp = mm4(f4_zero(), DP, [&](int r, int k) { return rowv(DS, PIT, 16 * I + r, k); },
+                      [&](int k, int cc) { return rowv(R, DP, 16 * J + cc, k); });
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int t = 16 * I + 4 * lg + e, i = 16 * J + (lane & 15);
@@ -289,10 +474,10 @@ __global__ __launch_bounds__(256) void chunk_bwd_grad_kernel(ChunkBwdArgs a, con
   X* dsvo = (X*)a.dsv;
   for (int tile = w; tile < (M / 16) * (DP / 16); tile += 4) {
     const int I = tile / (DP / 16), J = tile % (DP / 16);
-    const f4 x = mm(f4_zero(), DP, [&](int r, int k) { return dR[(long)(16 * I + r) * DP + k]; },
-                    [&](int k, int cc) { return S[(long)(16 * J + cc) * DP + k]; });
-    const f4 y = mm(f4_zero(), M, [&](int r, int k) { return A[(long)k * M + 16 * I + r]; },
-                    [&](int k, int cc) { return dR[(long)k * DP + 16 * J + cc]; });
+    const f4 x = mm4(f4_zero(), DP, [&](int r, int k) { return rowv(dR, DP, 16 * I + r, k); },
+                     [&](int k, int cc) { return rowv(S, DP, 16 * J + cc, k); });
+    const f4 y = mm4(f4_zero(), M, [&](int r, int k) { return colv(A, M, k, 16 * I + r); },
+                     [&](int k, int cc) { return colv(dR, DP, k, 16 * J + cc); });
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int i = 16 * I + 4 * lg + e, d = 16 * J + (lane & 15);
@@ -308,22 +493,33 @@ __global__ __launch_bounds__(256) void chunk_bwd_grad_kernel(ChunkBwdArgs a, con
   // P3: Z = A^T dW; dl_tau += e^l_tau kappa . Z
   for (int tile = w; tile < (M / 16) * (DP / 16); tile += 4) {
     const int I = tile / (DP / 16), J = tile % (DP / 16);
-    const f4 z = mm(f4_zero(), M, [&](int r, int k) { return A[(long)k * M + 16 * I + r]; },
-                    [&](int k, int cc) { return dW[(long)k * DP + 16 * J + cc]; });
+    const f4 z = mm4(f4_zero(), M, [&](int r, int k) { return colv(A, M, k, 16 * I + r); },
+                     [&](int k, int cc) { return colv(dW, DP, k, 16 * J + cc); });
+    float part[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int i = 16 * I + 4 * lg + e, d = 16 * J + (lane & 15);
       Z[(long)i * DP + d] = z[e];
-      atomicAdd(&dl[tau(i)], etau[i] * kap(i, d) * z[e]);
+      part[e] = etau[i] * kps[i][d] * z[e];
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {   // sum over the tile's 16 columns (the 16 lanes of a row)
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) part[e] += __shfl_xor(part[e], o, 64);
+      if ((lane & 15) == 0) atomicAdd(&dl[tau(16 * I + 4 * lg + e)], part[e]);
     }
   }
   // P4: dA = dR nu^T + dW (diag(e^l_tau) kappa)^T
   for (int tile = w; tile < (M / 16) * (M / 16); tile += 4) {
     const int I = tile / (M / 16), J = tile % (M / 16);
-    f4 x = mm(f4_zero(), DP, [&](int r, int k) { return dR[(long)(16 * I + r) * DP + k]; },
-              [&](int k, int cc) { return nu(16 * J + cc, k); });
-    x = mm(x, DP, [&](int r, int k) { return dW[(long)(16 * I + r) * DP + k]; },
-           [&](int k, int cc) { return etau[16 * J + cc] * kap(16 * J + cc, k); });
+    f4 x = mm4(f4_zero(), DP, [&](int r, int k) { return rowv(dR, DP, 16 * I + r, k); },
+               [&](int k, int cc) { return nu4(16 * J + cc, k); });
+    x = mm4(x, DP, [&](int r, int k) { return rowv(dW, DP, 16 * I + r, k); },
+            [&](int k, int cc) {
+              const float4 v = rowv(KS, PIT, 16 * J + cc, k);
+              const float e = etau[16 * J + cc];
+              return make_float4(e * v.x, e * v.y, e * v.z, e * v.w);
+            });
 #pragma unroll
     for (int e = 0; e < 4; ++e) dA[(long)(16 * I + 4 * lg + e) * M + 16 * J + (lane & 15)] = x[e];
   }
@@ -331,8 +527,8 @@ __global__ __launch_bounds__(256) void chunk_bwd_grad_kernel(ChunkBwdArgs a, con
   // P5: Tm = dA A^T
   for (int tile = w; tile < (M / 16) * (M / 16); tile += 4) {
     const int I = tile / (M / 16), J = tile % (M / 16);
-    const f4 x = mm(f4_zero(), M, [&](int r, int k) { return dA[(long)(16 * I + r) * M + k]; },
-                    [&](int k, int cc) { return A[(long)(16 * J + cc) * M + k]; });
+    const f4 x = mm4(f4_zero(), M, [&](int r, int k) { return rowv(dA, M, 16 * I + r, k); },
+                     [&](int k, int cc) { return rowv(A, M, 16 * J + cc, k); });
 #pragma unroll
     for (int e = 0; e < 4; ++e) Tm[(long)(16 * I + 4 * lg + e) * M + 16 * J + (lane & 15)] = x[e];
   }
@@ -341,10 +537,10 @@ __global__ __launch_bounds__(256) void chunk_bwd_grad_kernel(ChunkBwdArgs a, con
   // ratio; the T-terms of dlambda and dl
   for (int tile = w; tile < (M / 16) * (M / 16); tile += 4) {
     const int I = tile / (M / 16), J = tile % (M / 16);
-    const f4 dt = mm(f4_zero(), M, [&](int r, int k) { return A[(long)k * M + 16 * I + r]; },
-                     [&](int k, int cc) { return Tm[(long)k * M + 16 * J + cc]; });
-    const f4 gk = mm(f4_zero(), DP, [&](int r, int k) { return kap(16 * I + r, k); },
-                     [&](int k, int cc) { return kap(16 * J + cc, k); });
+    const f4 dt = mm4(f4_zero(), M, [&](int r, int k) { return colv(A, M, k, 16 * I + r); },
+                      [&](int k, int cc) { return colv(Tm, M, k, 16 * J + cc); });
+    const f4 gk = mm4(f4_zero(), DP, [&](int r, int k) { return rowv(KS, PIT, 16 * I + r, k); },
+                      [&](int k, int cc) { return rowv(KS, PIT, 16 * J + cc, k); });
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int i = 16 * I + 4 * lg + e, j = 16 * J + (lane & 15);
@@ -363,16 +559,20 @@ __global__ __launch_bounds__(256) void chunk_bwd_grad_kernel(ChunkBwdArgs a, con
   X* dsko = (X*)a.dsk;
   for (int tile = w; tile < (M / 16) * (DP / 16); tile += 4) {
     const int I = tile / (DP / 16), J = tile % (DP / 16);
-    f4 x = mm(f4_zero(), L, [&](int r, int k) { return Y[(long)k * M + 16 * I + r]; },
-              [&](int k, int cc) { return q(t0 + k, 16 * J + cc); });
-    const f4 rg = mm(f4_zero(), DP, [&](int r, int k) { return R[(long)(16 * I + r) * DP + k]; },
-                     [&](int k, int cc) { return G[(long)(16 * J + cc) * DP + k]; });
-    x = mm(x, M, [&](int r, int k) { return Xm[(long)(16 * I + r) * M + k] * lam[k]; },
-           [&](int k, int cc) { return kap(k, 16 * J + cc); });
-    const f4 xt = mm(f4_zero(), M, [&](int r, int k) { return Xm[(long)k * M + 16 * I + r]; },
-                     [&](int k, int cc) { return kap(k, 16 * J + cc); });
-    const f4 kg = mm(f4_zero(), DP, [&](int r, int k) { return kap(16 * I + r, k); },
-                     [&](int k, int cc) { return G[(long)k * DP + 16 * J + cc]; });
+    f4 x = mm4(f4_zero(), L, [&](int r, int k) { return colv(Y, M, k, 16 * I + r); },
+               [&](int k, int cc) { return colv(QS, PIT, k, 16 * J + cc); });
+    const f4 rg = mm4(f4_zero(), DP, [&](int r, int k) { return rowv(R, DP, 16 * I + r, k); },
+                      [&](int k, int cc) { return rowv(G, DP, 16 * J + cc, k); });
+    x = mm4(x, M, [&](int r, int k) {
+          const float4 v = rowv(Xm, M, 16 * I + r, k);
+          return make_float4(v.x * lam[k], v.y * lam[k + 1], v.z * lam[k + 2], v.w * lam[k + 3]);
+        },
+        [&](int k, int cc) { return colv(KS, PIT, k, 16 * J + cc); });
+    const f4 xt = mm4(f4_zero(), M, [&](int r, int k) { return colv(Xm, M, k, 16 * I + r); },
+                      [&](int k, int cc) { return colv(KS, PIT, k, 16 * J + cc); });
+    const f4 kg = mm4(f4_zero(), DP, [&](int r, int k) { return rowv(KS, PIT, 16 * I + r, k); },
+                      [&](int k, int cc) { return colv(G, DP, k, 16 * J + cc); });
+    float part[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int i = 16 * I + 4 * lg + e, d = 16 * J + (lane & 15);
@@ -382,23 +582,36 @@ __global__ __launch_bounds__(256) void chunk_bwd_grad_kernel(ChunkBwdArgs a, con
         X* o = (SP && (i & 1)) ? dsko : dko;
         st(o, ((long)(b * T + t) * H + h) * D + d, g);
       }
-      atomicAdd(&dcv[i], kg[e] * R[(long)i * DP + d]);
+      part[e] = kg[e] * R[(long)i * DP + d];
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) part[e] += __shfl_xor(part[e], o, 64);
+      if ((lane & 15) == 0) atomicAdd(&dcv[16 * I + 4 * lg + e], part[e]);
     }
   }
   // P8: dq = diag(e^l) dO S^T + Y kappa; dl_t += e^l_t q_t . (S dO_t)
   X* dqo = (X*)a.dq;
   for (int tile = w; tile < (L / 16) * (DP / 16); tile += 4) {
     const int I = tile / (DP / 16), J = tile % (DP / 16);
-    const f4 ds = mm(f4_zero(), DP, [&](int r, int k) { return dO(t0 + 16 * I + r, k); },
-                     [&](int k, int cc) { return S[(long)(16 * J + cc) * DP + k]; });
-    const f4 yk = mm(f4_zero(), M, [&](int r, int k) { return Y[(long)(16 * I + r) * M + k]; },
-                     [&](int k, int cc) { return kap(k, 16 * J + cc); });
+    const f4 ds = mm4(f4_zero(), DP, [&](int r, int k) { return rowv(DS, PIT, 16 * I + r, k); },
+                      [&](int k, int cc) { return rowv(S, DP, 16 * J + cc, k); });
+    const f4 yk = mm4(f4_zero(), M, [&](int r, int k) { return rowv(Y, M, 16 * I + r, k); },
+                      [&](int k, int cc) { return colv(KS, PIT, k, 16 * J + cc); });
+    float part[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int tl = 16 * I + 4 * lg + e, d = 16 * J + (lane & 15);
       const int t = t0 + tl;
       if (t < T && d < D) st(dqo, ((long)(b * T + t) * H + h) * D + d, el[tl] * ds[e] + yk[e]);
-      atomicAdd(&dl[tl], el[tl] * q(t, d) * ds[e]);
+      part[e] = el[tl] * qs[tl][d] * ds[e];
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) part[e] += __shfl_xor(part[e], o, 64);
+      if ((lane & 15) == 0) atomicAdd(&dl[16 * I + 4 * lg + e], part[e]);
     }
   }
   // P9: <G, S>
@@ -439,8 +652,10 @@ __global__ __launch_bounds__(256) void chunk_bwd_grad_kernel(ChunkBwdArgs a, con
 }
 
 struct BwdWs {
-  float *W, *U, *R, *Hs, *lgd, *A, *Gend, *dR, *scr;
+  float *W, *U, *X1, *A, *lgd, *Phi, *PmY2, *Hs, *Gend, *scr;
 };
+
+size_t bwd_scr_floats(size_t M) { return L * M + 4 * M * DP + 3 * M * M; }
 
 BwdWs bwd_ws(void* base, int B, int T, int H, int sp) {
   const size_t NT = (T + L - 1) / L, M = sp ? 2 * L : L, BH = (size_t)B * H;
@@ -449,12 +664,13 @@ BwdWs bwd_ws(void* base, int B, int T, int H, int sp) {
   BwdWs w;
   w.W = (float*)p; p = al(p + 4 * BH * NT * M * DP);
   w.U = (float*)p; p = al(p + 4 * BH * NT * M * DP);
-  w.R = (float*)p; p = al(p + 4 * BH * NT * M * DP);
-  w.Hs = (float*)p; p = al(p + 4 * BH * NT * DP * DP);
-  w.lgd = (float*)p; p = al(p + 4 * BH * NT * L);
+  w.X1 = (float*)p; p = al(p + 4 * BH * NT * M * DP);
   w.A = (float*)p; p = al(p + 4 * BH * NT * M * M);
+  w.lgd = (float*)p; p = al(p + 4 * BH * NT * L);
+  w.Phi = (float*)p; p = al(p + 4 * BH * NT * DP * DP);
+  w.PmY2 = (float*)p; p = al(p + 4 * BH * NT * DP * DP);
+  w.Hs = (float*)p; p = al(p + 4 * BH * NT * DP * DP);
   w.Gend = (float*)p; p = al(p + 4 * BH * NT * DP * DP);
-  w.dR = (float*)p; p = al(p + 4 * BH * NT * M * DP);
   w.scr = (float*)p;
   return w;
 }
@@ -463,8 +679,13 @@ template <typename X, bool SP>
 hipError_t launch_bwd_t(const ChunkBwdArgs& a, const BwdWs& w, hipStream_t st) {
   const int NT = (a.f.T + L - 1) / L;
   const int BH = a.f.B * a.f.H;
-  chunk_bwd_scan_kernel<X, SP><<<dim3(DP / 16, BH), 256, 0, st>>>(a, w.W, w.lgd, w.Gend, w.dR, NT);
-  chunk_bwd_grad_kernel<X, SP><<<dim3(NT, BH), 256, 0, st>>>(a, w.R, w.Hs, w.lgd, w.A, w.Gend, w.dR, w.scr, NT);
+  const dim3 chunks(NT, BH), slices(DP / 16, BH);
+  chunk_bwd_maps_kernel<X, SP><<<chunks, 256, 0, st>>>(a, w.W, w.U, w.lgd, w.Phi, w.PmY2, NT);
+  chunk_bwd_scan_kernel<true><<<slices, 256, 0, st>>>(w.Phi, w.PmY2, a.f.initial_state, a.f.D, w.Hs, nullptr, NT);
+  chunk_bwd_pre_kernel<X, SP><<<chunks, 256, 0, st>>>(a, w.W, w.lgd, w.X1, w.PmY2, NT);
+  chunk_bwd_scan_kernel<false><<<slices, 256, 0, st>>>(w.Phi, w.PmY2, a.d_final_state, a.f.D, w.Gend,
+                                                       a.d_initial_state, NT);
+  chunk_bwd_grad_kernel<X, SP><<<chunks, 256, 0, st>>>(a, w.W, w.U, w.X1, w.Hs, w.lgd, w.A, w.Gend, w.scr, NT);
   return hipGetLastError();
 }
 
@@ -472,15 +693,14 @@ hipError_t launch_bwd_t(const ChunkBwdArgs& a, const BwdWs& w, hipStream_t st) {
 
 size_t chunk_bwd_workspace_bytes(int B, int T, int H, int has_sparse) {
   const size_t NT = (T + L - 1) / L, M = has_sparse ? 2 * L : L, BH = (size_t)B * H;
-  const size_t per = 4 * (4 * M * DP + 2 * DP * DP + L + M * M) + 6 * 256;
-  const size_t scr = 4 * (L * M + 2 * M * DP + 3 * M * M);
-  return BH * NT * (per + scr) + 256 * 12;
+  const size_t per = 4 * (3 * M * DP + M * M + L + 4 * DP * DP + bwd_scr_floats(M));
+  return BH * NT * per + 256 * 12;
 }
 
 hipError_t launch_chunk_bwd(const ChunkBwdArgs& a, hipStream_t st) {
   const bool sp = a.f.sparse_k != nullptr;
   const BwdWs w = bwd_ws(a.workspace, a.f.B, a.f.T, a.f.H, sp);
-  if (hipError_t e = launch_chunk_recompute(a.f, w.W, w.U, w.R, w.Hs, w.lgd, w.A, st)) return e;
+  if (hipError_t e = launch_chunk_intra(a.f, w.W, w.U, w.lgd, w.A, st)) return e;
   if (a.f.dtype == DT_BF16) return sp ? launch_bwd_t<bf16_t, true>(a, w, st) : launch_bwd_t<bf16_t, false>(a, w, st);
   return sp ? launch_bwd_t<float, true>(a, w, st) : launch_bwd_t<float, false>(a, w, st);
 }

@@ -31,11 +31,10 @@ size_t chunk_workspace_bytes(int B, int T, int H, int has_sparse);   // covers b
 size_t chunk_bf16_workspace_bytes(int B, int T, int H, int has_sparse);
 hipError_t launch_chunk_fwd(const ChunkArgs& a, hipStream_t st);
 hipError_t launch_chunk_bf16(const ChunkArgs& a, hipStream_t st);
-// The fp32 chunk path's intermediates for the backward (chunk.hip): per (b*H + h,
-// chunk) W, U, R [M][128], the chunk-start state [128][128], the log-decay
-// prefix [64] and A [M][M] (M = 128 with the sparse write, else 64).
-hipError_t launch_chunk_recompute(const ChunkArgs& a, float* W, float* U, float* R, float* Hs, float* lgd, float* A,
-                                  hipStream_t st);
+// The fp32 chunk path's per-chunk intermediates for the backward (chunk.hip): per
+// (b*H + h, chunk) W, U [M][128], the log-decay prefix [64] and A [M][M]
+// (M = 128 with the sparse write, else 64).
+hipError_t launch_chunk_intra(const ChunkArgs& a, float* W, float* U, float* lgd, float* A, hipStream_t st);
 
 // Backward of chunk_sgsa (chunk_bwd.hip).
 struct ChunkBwdArgs {
