@@ -78,11 +78,49 @@ __device__ __forceinline__ f4 mm(f4 acc, int K, FA&& fa, FB&& fb) {
 }
 
 constexpr int PIT = DP + 4;   // LDS row pitch (floats)
+// Waves per workgroup of the per-chunk kernels (maps, pre, grad), whose LDS
+// allows one workgroup per CU.
+constexpr int GW = 8;
+
+// One 16 x 16 output tile over K (a multiple of 32) with the sum taken four k at
+// a time per lane: lane (r, g) of the MFMA takes k = k0 + 4g + j in the j-th of
+// four products, so fa4(r, k) / fb4(k, c) return the four consecutive k from k
+// (a float4 load where the operand is contiguous along k).  Two accumulators,
+// for the k-groups at k0 and k0 + 16, keep two MFMA chains in flight.
+template <typename FA, typename FB>
+__device__ __forceinline__ f4 mm4(f4 acc, int K, FA&& fa4, FB&& fb4) {
+  const int lane = threadIdx.x & 63, lr = lane & 15, lg = lane >> 4;
+  f4 acc1 = f4_zero();
+  for (int k0 = 0; k0 < K; k0 += 32) {
+    const float4 a0 = fa4(lr, k0 + 4 * lg), b0 = fb4(k0 + 4 * lg, lr);
+    const float4 a1 = fa4(lr, k0 + 16 + 4 * lg), b1 = fb4(k0 + 16 + 4 * lg, lr);
+    acc = mma_f32(a0.x, b0.x, acc);
+    acc1 = mma_f32(a1.x, b1.x, acc1);
+    acc = mma_f32(a0.y, b0.y, acc);
+    acc1 = mma_f32(a1.y, b1.y, acc1);
+    acc = mma_f32(a0.z, b0.z, acc);
+    acc1 = mma_f32(a1.z, b1.z, acc1);
+    acc = mma_f32(a0.w, b0.w, acc);
+    acc1 = mma_f32(a1.w, b1.w, acc1);
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) acc[e] += acc1[e];
+  return acc;
+}
+// p[r][k..k+3] (contiguous) and p[k..k+3][c] (a column), for row pitch n
+__device__ __forceinline__ float4 rowv(const float* p, int n, int r, int k) {
+  return *reinterpret_cast<const float4*>(p + (long)r * n + k);
+}
+__device__ __forceinline__ float4 colv(const float* p, int n, int k, int c) {
+  const float* q = p + (long)k * n + c;
+  return make_float4(q[0], q[n], q[2 * n], q[3 * n]);
+}
+
 
 // Stage 2a, parallel over chunks: Phi = e^l_L I - kappa^T diag(c) W and
-// Pm = kappa^T diag(c) U, [DP][DP] each.  grid (NT, B*H), 256 threads.
+// Pm = kappa^T diag(c) U, [DP][DP] each.  grid (NT, B*H), GW waves.
 template <typename X, bool SP>
-__global__ __launch_bounds__(256) void chunk_bwd_maps_kernel(ChunkBwdArgs a, const float* __restrict__ Wg,
+__global__ __launch_bounds__(64 * GW) void chunk_bwd_maps_kernel(ChunkBwdArgs a, const float* __restrict__ Wg,
                                                              const float* __restrict__ Ug,
                                                              const float* __restrict__ lgd,
                                                              float* __restrict__ Phig, float* __restrict__ Pmg,
@@ -100,7 +138,7 @@ __global__ __launch_bounds__(256) void chunk_bwd_maps_kernel(ChunkBwdArgs a, con
   const Rows<X> kk{(const X*)a.f.k, b, h, T, H, D}, ks{(const X*)a.f.sparse_k, b, h, T, H, D};
   const float* lg_c = lgd + cb * L;
   const float lL = lg_c[L - 1];
-  for (int e = tid; e < M * DP; e += 256) {
+  for (int e = tid; e < M * DP; e += 64 * GW) {
     const int i = e / DP, d = e % DP;
     const int tl = SP ? (i >> 1) : i;
     const int t = t0 + tl;
@@ -113,10 +151,10 @@ __global__ __launch_bounds__(256) void chunk_bwd_maps_kernel(ChunkBwdArgs a, con
   __syncthreads();
   const float eL = expf(lL);
   float* Phi = Phig + cb * DP * DP;
-  for (int tile = w; tile < (DP / 16) * (DP / 16); tile += 4) {
+  for (int tile = w; tile < (DP / 16) * (DP / 16); tile += GW) {
     const int I = tile / (DP / 16), J = tile % (DP / 16);
-    const f4 x = mm(f4_zero(), M, [&](int r, int k) { return kps[k][16 * I + r]; },
-                    [&](int k, int cc) { return ws[k][16 * J + cc]; });
+    const f4 x = mm4(f4_zero(), M, [&](int r, int k) { return colv(&kps[0][0], PIT, k, 16 * I + r); },
+                     [&](int k, int cc) { return colv(&ws[0][0], PIT, k, 16 * J + cc); });
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int r = 16 * I + 4 * lg + e, cc = 16 * J + (lane & 15);
@@ -124,13 +162,13 @@ __global__ __launch_bounds__(256) void chunk_bwd_maps_kernel(ChunkBwdArgs a, con
     }
   }
   __syncthreads();
-  for (int e = tid; e < M * DP; e += 256) ws[e / DP][e % DP] = Ug[cb * M * DP + e];
+  for (int e = tid; e < M * DP; e += 64 * GW) ws[e / DP][e % DP] = Ug[cb * M * DP + e];
   __syncthreads();
   float* Pm = Pmg + cb * DP * DP;
-  for (int tile = w; tile < (DP / 16) * (DP / 16); tile += 4) {
+  for (int tile = w; tile < (DP / 16) * (DP / 16); tile += GW) {
     const int I = tile / (DP / 16), J = tile % (DP / 16);
-    const f4 x = mm(f4_zero(), M, [&](int r, int k) { return kps[k][16 * I + r]; },
-                    [&](int k, int cc) { return ws[k][16 * J + cc]; });
+    const f4 x = mm4(f4_zero(), M, [&](int r, int k) { return colv(&kps[0][0], PIT, k, 16 * I + r); },
+                     [&](int k, int cc) { return colv(&ws[0][0], PIT, k, 16 * J + cc); });
 #pragma unroll
     for (int e = 0; e < 4; ++e) Pm[(long)(16 * I + 4 * lg + e) * DP + 16 * J + (lane & 15)] = x[e];
   }
@@ -219,16 +257,16 @@ __global__ __launch_bounds__(256) void chunk_bwd_scan_kernel(const float* __rest
 
 // Stage 3a, parallel over chunks: X1 = P^T dO [M][DP] and the state-independent
 // part of the state gradient's step, Y2 = Q^T diag(e^l) dO - W^T X1 [DP][DP].
-// grid (NT, B*H), 256 threads; q, kappa, dO staged in LDS as fp32.
+// grid (NT, B*H), GW waves; q, kappa, dO staged in LDS as fp32.
 template <typename X, bool SP>
-__global__ __launch_bounds__(256) void chunk_bwd_pre_kernel(ChunkBwdArgs a, const float* __restrict__ Wg,
+__global__ __launch_bounds__(64 * GW) void chunk_bwd_pre_kernel(ChunkBwdArgs a, const float* __restrict__ Wg,
                                                             const float* __restrict__ lgd,
                                                             float* __restrict__ X1g, float* __restrict__ Y2g,
                                                             int NT) {
   constexpr int M = SP ? 2 * L : L;
-  __shared__ float qs[L][PIT];    // q, later P
-  __shared__ float kps[M][PIT];
-  __shared__ float dos[L][PIT];
+  __shared__ __align__(16) float qs[L][PIT];    // q, later P
+  __shared__ __align__(16) float kps[M][PIT];
+  __shared__ __align__(16) float dos[L][PIT];
   __shared__ float lam[M], logd[L], el[L];
 
   const int c = blockIdx.x, bh = blockIdx.y;
@@ -240,12 +278,12 @@ __global__ __launch_bounds__(256) void chunk_bwd_pre_kernel(ChunkBwdArgs a, cons
   const long cb = (long)bh * NT + c;
   const Rows<X> q{(const X*)a.f.q, b, h, T, H, D}, dO{(const X*)a.d_out, b, h, T, H, D};
   const Rows<X> kk{(const X*)a.f.k, b, h, T, H, D}, ks{(const X*)a.f.sparse_k, b, h, T, H, D};
-  for (int e = tid; e < L * DP; e += 256) {
+  for (int e = tid; e < L * DP; e += 64 * GW) {
     const int t = e / DP, d = e % DP;
     qs[t][d] = q(t0 + t, d);
     dos[t][d] = dO(t0 + t, d);
   }
-  for (int e = tid; e < M * DP; e += 256) {
+  for (int e = tid; e < M * DP; e += 64 * GW) {
     const int i = e / DP, d = e % DP;
     const int tl = SP ? (i >> 1) : i;
     kps[i][d] = (SP && (i & 1)) ? ks(t0 + tl, d) : kk(t0 + tl, d);
@@ -265,13 +303,13 @@ __global__ __launch_bounds__(256) void chunk_bwd_pre_kernel(ChunkBwdArgs a, cons
   }
   __syncthreads();
   // P (registers, then over q)
-  constexpr int NPT = (L / 16) * (M / 16) / 4;   // tiles per wave
+  constexpr int NPT = (L / 16) * (M / 16) / GW;   // tiles per wave
   f4 pt[NPT];
 #pragma unroll
   for (int u = 0; u < NPT; ++u) {
-    const int tile = w + 4 * u, I = tile / (M / 16), J = tile % (M / 16);
-    const f4 x = mm(f4_zero(), DP, [&](int r, int k) { return qs[16 * I + r][k]; },
-                    [&](int k, int cc) { return kps[16 * J + cc][k]; });
+    const int tile = w + GW * u, I = tile / (M / 16), J = tile % (M / 16);
+    const f4 x = mm4(f4_zero(), DP, [&](int r, int k) { return rowv(&qs[0][0], PIT, 16 * I + r, k); },
+                     [&](int k, int cc) { return rowv(&kps[0][0], PIT, 16 * J + cc, k); });
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int t = 16 * I + 4 * lg + e, i = 16 * J + (lane & 15);
@@ -281,75 +319,53 @@ __global__ __launch_bounds__(256) void chunk_bwd_pre_kernel(ChunkBwdArgs a, cons
   }
   // Y2 = Q^T diag(e^l) dO first (q is still in qs)
   float* Y2 = Y2g + cb * DP * DP;
-  for (int tile = w; tile < (DP / 16) * (DP / 16); tile += 4) {
+  for (int tile = w; tile < (DP / 16) * (DP / 16); tile += GW) {
     const int I = tile / (DP / 16), J = tile % (DP / 16);
-    const f4 x = mm(f4_zero(), L, [&](int r, int k) { return qs[k][16 * I + r] * el[k]; },
-                    [&](int k, int cc) { return dos[k][16 * J + cc]; });
+    const f4 x = mm4(f4_zero(), L,
+                     [&](int r, int k) {
+                       const float4 v = colv(&qs[0][0], PIT, k, 16 * I + r);
+                       return make_float4(v.x * el[k], v.y * el[k + 1], v.z * el[k + 2], v.w * el[k + 3]);
+                     },
+                     [&](int k, int cc) { return colv(&dos[0][0], PIT, k, 16 * J + cc); });
 #pragma unroll
     for (int e = 0; e < 4; ++e) Y2[(long)(16 * I + 4 * lg + e) * DP + 16 * J + (lane & 15)] = x[e];
   }
   __syncthreads();
 #pragma unroll
   for (int u = 0; u < NPT; ++u) {
-    const int tile = w + 4 * u, I = tile / (M / 16), J = tile % (M / 16);
+    const int tile = w + GW * u, I = tile / (M / 16), J = tile % (M / 16);
 #pragma unroll
     for (int e = 0; e < 4; ++e) qs[16 * I + 4 * lg + e][16 * J + (lane & 15)] = pt[u][e];
   }
   __syncthreads();
   // X1 = P^T dO, kept in LDS (over kappa) for W^T X1
   float* X1 = X1g + cb * M * DP;
-  for (int tile = w; tile < (M / 16) * (DP / 16); tile += 4) {
+  for (int tile = w; tile < (M / 16) * (DP / 16); tile += GW) {
     const int I = tile / (DP / 16), J = tile % (DP / 16);
-    const f4 x = mm(f4_zero(), L, [&](int r, int k) { return qs[k][16 * I + r]; },
-                    [&](int k, int cc) { return dos[k][16 * J + cc]; });
+    const f4 x = mm4(f4_zero(), L, [&](int r, int k) { return colv(&qs[0][0], PIT, k, 16 * I + r); },
+                     [&](int k, int cc) { return colv(&dos[0][0], PIT, k, 16 * J + cc); });
 #pragma unroll
     for (int e = 0; e < 4; ++e) X1[(long)(16 * I + 4 * lg + e) * DP + 16 * J + (lane & 15)] = x[e];
   }
   __syncthreads();
-  for (int e = tid; e < M * DP; e += 256) kps[e / DP][e % DP] = X1[e];
+  for (int e = tid; e < M * DP; e += 64 * GW) kps[e / DP][e % DP] = X1[e];
   __syncthreads();
   // Y2 -= W^T X1
   const float* Wc = Wg + cb * M * DP;
-  for (int tile = w; tile < (DP / 16) * (DP / 16); tile += 4) {
+  for (int tile = w; tile < (DP / 16) * (DP / 16); tile += GW) {
     const int I = tile / (DP / 16), J = tile % (DP / 16);
-    const f4 x = mm(f4_zero(), M, [&](int r, int k) { return Wc[(long)k * DP + 16 * I + r]; },
-                    [&](int k, int cc) { return kps[k][16 * J + cc]; });
+    const f4 x = mm4(f4_zero(), M, [&](int r, int k) { return colv(Wc, DP, k, 16 * I + r); },
+                     [&](int k, int cc) { return colv(&kps[0][0], PIT, k, 16 * J + cc); });
 #pragma unroll
     for (int e = 0; e < 4; ++e) Y2[(long)(16 * I + 4 * lg + e) * DP + 16 * J + (lane & 15)] -= x[e];
   }
 }
 
-// One 16 x 16 output tile over K (a multiple of 16) with the sum taken four k at
-// a time per lane: lane (r, g) of the MFMA takes k = k0 + 4g + j in the j-th of
-// four products, so fa4(r, k) / fb4(k, c) return the four consecutive k from k
-// (a float4 load where the operand is contiguous along k).
-template <typename FA, typename FB>
-__device__ __forceinline__ f4 mm4(f4 acc, int K, FA&& fa4, FB&& fb4) {
-  const int lane = threadIdx.x & 63, lr = lane & 15, lg = lane >> 4;
-#pragma unroll 2
-  for (int k0 = 0; k0 < K; k0 += 16) {
-    const float4 a = fa4(lr, k0 + 4 * lg), b = fb4(k0 + 4 * lg, lr);
-    acc = mma_f32(a.x, b.x, acc);
-    acc = mma_f32(a.y, b.y, acc);
-    acc = mma_f32(a.z, b.z, acc);
-    acc = mma_f32(a.w, b.w, acc);
-  }
-  return acc;
-}
-// p[r][k..k+3] (contiguous) and p[k..k+3][c] (a column), for row pitch n
-__device__ __forceinline__ float4 rowv(const float* p, int n, int r, int k) {
-  return *reinterpret_cast<const float4*>(p + (long)r * n + k);
-}
-__device__ __forceinline__ float4 colv(const float* p, int n, int k, int c) {
-  const float* q = p + (long)k * n + c;
-  return make_float4(q[0], q[n], q[2 * n], q[3 * n]);
-}
-
-// Stage 4.  grid (NT, B*H), 256 threads: every gradient of one chunk.  kappa, q
+// Stage 4.  grid (NT, B*H), GW waves: every gradient of one chunk.  kappa, q
 // and dO stay in LDS as fp32 for the whole kernel; the other operands are
 // read from the workspace (L2).
 template <typename X, bool SP>
-__global__ __launch_bounds__(256) void chunk_bwd_grad_kernel(ChunkBwdArgs a, const float* __restrict__ Wg,
+__global__ __launch_bounds__(64 * GW) void chunk_bwd_grad_kernel(ChunkBwdArgs a, const float* __restrict__ Wg,
                                                              const float* __restrict__ Ug,
                                                              const float* __restrict__ X1g,
                                                              const float* __restrict__ Hs,
@@ -363,7 +379,7 @@ __global__ __launch_bounds__(256) void chunk_bwd_grad_kernel(ChunkBwdArgs a, con
   __shared__ __align__(16) float dos[L][PIT];
   __shared__ float lam[M], cf[M], etau[M], dlam[M], dcv[M];
   __shared__ float logd[L], el[L], dl[L];
-  __shared__ float red[4];
+  __shared__ float red[GW];
 
   const int c = blockIdx.x, bh = blockIdx.y;
   const int T = a.f.T, H = a.f.H, D = a.f.D;
@@ -398,12 +414,12 @@ __global__ __launch_bounds__(256) void chunk_bwd_grad_kernel(ChunkBwdArgs a, con
   float* Tm = dA + M * M;
   float* Xm = Tm + M * M;
 
-  for (int e = tid; e < L * DP; e += 256) {
+  for (int e = tid; e < L * DP; e += 64 * GW) {
     const int t = e / DP, d = e % DP;
     qs[t][d] = q(t0 + t, d);
     dos[t][d] = dO(t0 + t, d);
   }
-  for (int e = tid; e < M * DP; e += 256) {
+  for (int e = tid; e < M * DP; e += 64 * GW) {
     const int i = e / DP, d = e % DP;
     const int tl = tau(i);
     kps[i][d] = (SP && (i & 1)) ? ks(t0 + tl, d) : kk(t0 + tl, d);
@@ -434,7 +450,7 @@ __global__ __launch_bounds__(256) void chunk_bwd_grad_kernel(ChunkBwdArgs a, con
     const float* Wc = Wg + cb * M * DP;
     const float* Uc = Ug + cb * M * DP;
     const float* X1 = X1g + cb * M * DP;
-    for (int tile = w; tile < (M / 16) * (DP / 16); tile += 4) {
+    for (int tile = w; tile < (M / 16) * (DP / 16); tile += GW) {
       const int I = tile / (DP / 16), J = tile % (DP / 16);
       const f4 ws = mm4(f4_zero(), DP, [&](int r, int k) { return rowv(Wc, DP, 16 * I + r, k); },
                         [&](int k, int cc) { return colv(S, DP, k, 16 * J + cc); });
@@ -451,7 +467,7 @@ __global__ __launch_bounds__(256) void chunk_bwd_grad_kernel(ChunkBwdArgs a, con
   }
   __syncthreads();
   // P1: Y, and the P-terms of dlambda and dl
-  for (int tile = w; tile < (L / 16) * (M / 16); tile += 4) {
+  for (int tile = w; tile < (L / 16) * (M / 16); tile += GW) {
     const int I = tile / (M / 16), J = tile % (M / 16);
     const f4 qk = mm4(f4_zero(), DP, [&](int r, int k) { return rowv(QS, PIT, 16 * I + r, k); },
                       [&](int k, int cc) { return rowv(KS, PIT, 16 * J + cc, k); });
@@ -472,7 +488,7 @@ __global__ __launch_bounds__(256) void chunk_bwd_grad_kernel(ChunkBwdArgs a, con
   // P2: dW = -dR S^T, and dnu = A^T dR (the v / v-hat gradients)
   X* dvo = (X*)a.dv;
   X* dsvo = (X*)a.dsv;
-  for (int tile = w; tile < (M / 16) * (DP / 16); tile += 4) {
+  for (int tile = w; tile < (M / 16) * (DP / 16); tile += GW) {
     const int I = tile / (DP / 16), J = tile % (DP / 16);
     const f4 x = mm4(f4_zero(), DP, [&](int r, int k) { return rowv(dR, DP, 16 * I + r, k); },
                      [&](int k, int cc) { return rowv(S, DP, 16 * J + cc, k); });
@@ -491,7 +507,7 @@ __global__ __launch_bounds__(256) void chunk_bwd_grad_kernel(ChunkBwdArgs a, con
   }
   __syncthreads();
   // P3: Z = A^T dW; dl_tau += e^l_tau kappa . Z
-  for (int tile = w; tile < (M / 16) * (DP / 16); tile += 4) {
+  for (int tile = w; tile < (M / 16) * (DP / 16); tile += GW) {
     const int I = tile / (DP / 16), J = tile % (DP / 16);
     const f4 z = mm4(f4_zero(), M, [&](int r, int k) { return colv(A, M, k, 16 * I + r); },
                      [&](int k, int cc) { return colv(dW, DP, k, 16 * J + cc); });
@@ -510,7 +526,7 @@ __global__ __launch_bounds__(256) void chunk_bwd_grad_kernel(ChunkBwdArgs a, con
     }
   }
   // P4: dA = dR nu^T + dW (diag(e^l_tau) kappa)^T
-  for (int tile = w; tile < (M / 16) * (M / 16); tile += 4) {
+  for (int tile = w; tile < (M / 16) * (M / 16); tile += GW) {
     const int I = tile / (M / 16), J = tile % (M / 16);
     f4 x = mm4(f4_zero(), DP, [&](int r, int k) { return rowv(dR, DP, 16 * I + r, k); },
                [&](int k, int cc) { return nu4(16 * J + cc, k); });
@@ -525,7 +541,7 @@ __global__ __launch_bounds__(256) void chunk_bwd_grad_kernel(ChunkBwdArgs a, con
   }
   __syncthreads();
   // P5: Tm = dA A^T
-  for (int tile = w; tile < (M / 16) * (M / 16); tile += 4) {
+  for (int tile = w; tile < (M / 16) * (M / 16); tile += GW) {
     const int I = tile / (M / 16), J = tile % (M / 16);
     const f4 x = mm4(f4_zero(), M, [&](int r, int k) { return rowv(dA, M, 16 * I + r, k); },
                      [&](int k, int cc) { return rowv(A, M, 16 * J + cc, k); });
@@ -535,7 +551,7 @@ __global__ __launch_bounds__(256) void chunk_bwd_grad_kernel(ChunkBwdArgs a, con
   __syncthreads();
   // P6: dT = -A^T Tm; X = dT on the strictly lower token blocks, times the decay
   // ratio; the T-terms of dlambda and dl
-  for (int tile = w; tile < (M / 16) * (M / 16); tile += 4) {
+  for (int tile = w; tile < (M / 16) * (M / 16); tile += GW) {
     const int I = tile / (M / 16), J = tile % (M / 16);
     const f4 dt = mm4(f4_zero(), M, [&](int r, int k) { return colv(A, M, k, 16 * I + r); },
                       [&](int k, int cc) { return colv(Tm, M, k, 16 * J + cc); });
@@ -557,7 +573,7 @@ __global__ __launch_bounds__(256) void chunk_bwd_grad_kernel(ChunkBwdArgs a, con
   // P7: dkappa (the k / k-tilde gradients) and dc = (kappa G) . R
   X* dko = (X*)a.dk;
   X* dsko = (X*)a.dsk;
-  for (int tile = w; tile < (M / 16) * (DP / 16); tile += 4) {
+  for (int tile = w; tile < (M / 16) * (DP / 16); tile += GW) {
     const int I = tile / (DP / 16), J = tile % (DP / 16);
     f4 x = mm4(f4_zero(), L, [&](int r, int k) { return colv(Y, M, k, 16 * I + r); },
                [&](int k, int cc) { return colv(QS, PIT, k, 16 * J + cc); });
@@ -593,7 +609,7 @@ __global__ __launch_bounds__(256) void chunk_bwd_grad_kernel(ChunkBwdArgs a, con
   }
   // P8: dq = diag(e^l) dO S^T + Y kappa; dl_t += e^l_t q_t . (S dO_t)
   X* dqo = (X*)a.dq;
-  for (int tile = w; tile < (L / 16) * (DP / 16); tile += 4) {
+  for (int tile = w; tile < (L / 16) * (DP / 16); tile += GW) {
     const int I = tile / (DP / 16), J = tile % (DP / 16);
     const f4 ds = mm4(f4_zero(), DP, [&](int r, int k) { return rowv(DS, PIT, 16 * I + r, k); },
                       [&](int k, int cc) { return rowv(S, DP, 16 * J + cc, k); });
@@ -616,11 +632,16 @@ __global__ __launch_bounds__(256) void chunk_bwd_grad_kernel(ChunkBwdArgs a, con
   }
   // P9: <G, S>
   float gs = 0.f;
-  for (int e = tid; e < DP * DP; e += 256) gs += G[e] * S[e];
+  for (int e = tid; e < DP * DP; e += 64 * GW) gs += G[e] * S[e];
   gs = wave_sum(gs);
   if (lane == 0) red[w] = gs;
   __syncthreads();
-  if (tid == 0) dl[L - 1] += el[L - 1] * (red[0] + red[1] + red[2] + red[3]);
+  if (tid == 0) {
+    float r = 0.f;
+#pragma unroll
+    for (int i = 0; i < GW; ++i) r += red[i];
+    dl[L - 1] += el[L - 1] * r;
+  }
   __syncthreads();
   if (tid < M) {   // the c-terms
     const int ti = tau(tid);
@@ -680,12 +701,12 @@ hipError_t launch_bwd_t(const ChunkBwdArgs& a, const BwdWs& w, hipStream_t st) {
   const int NT = (a.f.T + L - 1) / L;
   const int BH = a.f.B * a.f.H;
   const dim3 chunks(NT, BH), slices(DP / 16, BH);
-  chunk_bwd_maps_kernel<X, SP><<<chunks, 256, 0, st>>>(a, w.W, w.U, w.lgd, w.Phi, w.PmY2, NT);
+  chunk_bwd_maps_kernel<X, SP><<<chunks, 64 * GW, 0, st>>>(a, w.W, w.U, w.lgd, w.Phi, w.PmY2, NT);
   chunk_bwd_scan_kernel<true><<<slices, 256, 0, st>>>(w.Phi, w.PmY2, a.f.initial_state, a.f.D, w.Hs, nullptr, NT);
-  chunk_bwd_pre_kernel<X, SP><<<chunks, 256, 0, st>>>(a, w.W, w.lgd, w.X1, w.PmY2, NT);
+  chunk_bwd_pre_kernel<X, SP><<<chunks, 64 * GW, 0, st>>>(a, w.W, w.lgd, w.X1, w.PmY2, NT);
   chunk_bwd_scan_kernel<false><<<slices, 256, 0, st>>>(w.Phi, w.PmY2, a.d_final_state, a.f.D, w.Gend,
                                                        a.d_initial_state, NT);
-  chunk_bwd_grad_kernel<X, SP><<<chunks, 256, 0, st>>>(a, w.W, w.U, w.X1, w.Hs, w.lgd, w.A, w.Gend, w.scr, NT);
+  chunk_bwd_grad_kernel<X, SP><<<chunks, 64 * GW, 0, st>>>(a, w.W, w.U, w.X1, w.Hs, w.lgd, w.A, w.Gend, w.scr, NT);
   return hipGetLastError();
 }
 
