@@ -2,6 +2,7 @@
 
 Public entry points mirror FAndromedA/sgsa:
   chunk_sgsa            -- modelings/sgsa_ops/chunk.py:104-148
+  chunk_sgsa_bwd        -- its gradients, native (the reference recomputes in torch, chunk_bwd.py:12-77)
   SparseRetriever       -- modelings/modeling_sgsa.py:90-474 (token_only mode)
   sparse_retrieve       -- functional form of SparseRetriever.forward
   sgsa_layer_forward    -- retrieval + write gate + chunked state update in one call
@@ -12,7 +13,7 @@ Public entry points mirror FAndromedA/sgsa:
 The compiled library (libsgsa_hip.so) is required; there is no fallback path.
 """
 
-from .ops import ChunkSGSAFunction, chunk_sgsa, chunk_sgsa_fwd
+from .ops import ChunkSGSAFunction, chunk_sgsa, chunk_sgsa_bwd, chunk_sgsa_fwd
 from .retrieval import (SparseRetriever, block_retrieve, gather_gate, gather_lists, gather_masked, gather_thresholds,
                         masked_gather_gate, score_dump, gather_thresholds_selection, selection_summary, score_topk, score_topk_lists, score_topk_masked,
                         score_topk_thresholds, sparse_retrieve)
@@ -26,6 +27,7 @@ __all__ = [
     "ChunkSGSAFunction",
     "chunk_sgsa",
     "chunk_sgsa_fwd",
+    "chunk_sgsa_bwd",
     "fused_recurrent_sgsa",
     "sgsa_decode_step",
     "SparseRetriever",
