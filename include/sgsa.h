@@ -275,6 +275,23 @@ int sgsa_block_retrieve(int dtype, int B, int T, int H, int D, int top_k, int bl
                         int32_t* indices, int32_t* block_indices, float* block_scores, float* weights,
                         void* k_hat, void* v_hat, float* diag, void* workspace, size_t workspace_bytes,
                         void* stream);
+/* The same with SparseRetriever.forward's attention_mask (modelings/
+ * modeling_sgsa.py:421-428): attention_mask [B,T] uint8, nonzero = real token.
+ * A row sees the causal keys that are real tokens; a padded row sees none.
+ * Block scores take the max over the keys a row sees (-FLT_MAX if none); a
+ * block is valid when it holds one (:188-189); each row keeps k_q = min(eb,
+ * max(1, most valid blocks of any (b, h) at that position)) blocks (:159-160),
+ * its valid ones by score, then its invalid ones (-FLT_MAX) by ascending
+ * index; slots past k_q hold 0.  Candidates = the keys the row sees in its
+ * kept blocks (:313-320); block_token's k_q and fills follow the same rule over
+ * the candidates, block_only's rows with no candidate get zero weights, k_hat
+ * and v_hat.  Same workspace size as sgsa_block_retrieve. */
+int sgsa_block_retrieve_masked(int dtype, int B, int T, int H, int D, int top_k, int block_size, int top_blocks,
+                               int mode, int causal, float tau_c, int local_window, int sink_size,
+                               const void* q, const void* k, const void* v, const uint8_t* attention_mask,
+                               int32_t* indices, int32_t* block_indices, float* block_scores, float* weights,
+                               void* k_hat, void* v_hat, float* diag, void* workspace, size_t workspace_bytes,
+                               void* stream);
 
 /* ---- RMSNorm of the model shells -------------------------------------------
  * y = x * rsqrt(mean(x^2) + eps) * weight over the last dimension, in fp32,

@@ -327,9 +327,11 @@ def block_retrieval(
     local_window: int = 64,
     sink_size: int = 8,
     eps: float = 1e-6,
+    attention_mask: Optional[Tensor] = None,
 ) -> Dict[str, object]:
     """Block retrieval modes of SparseRetriever.forward on its torch path (no flash_moba;
-    modelings/modeling_sgsa.py:444-463), causal or not (:423-424), no padding mask.
+    modelings/modeling_sgsa.py:444-463), causal or not (:423-424), with an optional
+    padding mask [B,T] folded into the valid mask for keys and queries (:425-428).
 
     Scores ``q k^T / sqrt(d)`` (:420).  Block b holds keys [b bs, (b+1) bs)
     (:167-170); its score is the max over its causal keys, finfo.min when it has
@@ -351,6 +353,9 @@ def block_retrieval(
     pos = torch.arange(T)
     valid = (pos[None, :] <= pos[:, None]) if causal else torch.ones(T, T, dtype=torch.bool)
     valid = valid[None, None].expand(B, H, T, T)
+    if attention_mask is not None:
+        am = attention_mask.to(torch.bool)
+        valid = valid & am[:, None, None, :] & am[:, None, :, None]
     fmin = torch.finfo(scores.dtype).min
     block_ids = pos // block_size
     nb = int(block_ids.max().item()) + 1

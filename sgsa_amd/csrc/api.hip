@@ -584,7 +584,8 @@ int sgsa_score_at(int dtype, int B, int Tq, int Tk, int H, int D, int top_k, flo
 // ---- block retrieval -----------------------------------------------------------
 namespace {
 struct BlockWs {
-  size_t bscores, ncand, bmargin, top2, counts, valid, slot_sc, slot_idx, slot_w, maxidx, total;
+  size_t bscores, ncand, bmargin, top2, counts, valid, slot_sc, slot_idx, slot_w, maxidx;
+  size_t mpc, mperm, mnvb, mkqb, mbits, total;   // padding-mask layout (always reserved)
 };
 
 int block_dims(int B, int T, int H, int top_k, int block_size, int top_blocks, int mode, int& nb, int& eb, int& kk,
@@ -621,9 +622,20 @@ BlockWs block_ws(int B, int T, int H, int nb, int kk, int ks, int mode, bool wan
   L.slot_idx = mode == 0 ? take(rows * w * 4) : 0;
   L.slot_w = (mode == 0 && want_weights) ? take(rows * w * 4) : 0;
   L.maxidx = take(256);
+  L.mpc = take((size_t)B * (T + 1) * 4);
+  L.mperm = take((size_t)B * T * 4);
+  L.mnvb = take((size_t)B * T * 4);
+  L.mkqb = take((size_t)T * 4);
+  L.mbits = take((size_t)B * ((T + 31) / 32) * 4);
   L.total = o;
   return L;
 }
+
+int block_retrieve_impl(int dtype, int B, int T, int H, int D, int top_k, int block_size, int top_blocks, int mode,
+                        int causal, float tau_c, int local_window, int sink_size, const void* q, const void* k,
+                        const void* v, const uint8_t* mask, int32_t* indices, int32_t* block_indices,
+                        float* block_scores, float* weights, void* k_hat, void* v_hat, float* diag, void* workspace,
+                        size_t workspace_bytes, void* stream);
 }  // namespace
 
 int sgsa_block_retrieve_workspace_size(int B, int T, int H, int top_k, int block_size, int top_blocks, int mode,
@@ -640,6 +652,30 @@ int sgsa_block_retrieve(int dtype, int B, int T, int H, int D, int top_k, int bl
                         const void* v, int32_t* indices, int32_t* block_indices, float* block_scores, float* weights,
                         void* k_hat, void* v_hat, float* diag, void* workspace, size_t workspace_bytes,
                         void* stream) {
+  return block_retrieve_impl(dtype, B, T, H, D, top_k, block_size, top_blocks, mode, causal, tau_c, local_window,
+                             sink_size, q, k, v, nullptr, indices, block_indices, block_scores, weights, k_hat, v_hat,
+                             diag, workspace, workspace_bytes, stream);
+}
+
+int sgsa_block_retrieve_masked(int dtype, int B, int T, int H, int D, int top_k, int block_size, int top_blocks,
+                               int mode, int causal, float tau_c, int local_window, int sink_size, const void* q,
+                               const void* k, const void* v, const uint8_t* attention_mask, int32_t* indices,
+                               int32_t* block_indices, float* block_scores, float* weights, void* k_hat, void* v_hat,
+                               float* diag, void* workspace, size_t workspace_bytes, void* stream) {
+  REQUIRE(attention_mask);
+  return block_retrieve_impl(dtype, B, T, H, D, top_k, block_size, top_blocks, mode, causal, tau_c, local_window,
+                             sink_size, q, k, v, attention_mask, indices, block_indices, block_scores, weights, k_hat,
+                             v_hat, diag, workspace, workspace_bytes, stream);
+}
+
+}  // extern "C"
+
+namespace {
+int block_retrieve_impl(int dtype, int B, int T, int H, int D, int top_k, int block_size, int top_blocks, int mode,
+                        int causal, float tau_c, int local_window, int sink_size, const void* q, const void* k,
+                        const void* v, const uint8_t* mask, int32_t* indices, int32_t* block_indices,
+                        float* block_scores, float* weights, void* k_hat, void* v_hat, float* diag, void* workspace,
+                        size_t workspace_bytes, void* stream) {
   if (int s = check_dtype(dtype)) return s;
   if (int s = check_dims(B, T, H, D)) return s;
   int nb, eb, kk, ks;
@@ -663,6 +699,13 @@ int sgsa_block_retrieve(int dtype, int B, int T, int H, int D, int top_k, int bl
   a.slot_valid = mode == 1 ? reinterpret_cast<uint8_t*>(base + L.valid) : nullptr;
   a.top2 = reinterpret_cast<float*>(base + L.top2);
   a.counts = reinterpret_cast<int32_t*>(base + L.counts);
+  a.mask = mask;
+  a.nmw = (T + 31) / 32;
+  a.mpc = reinterpret_cast<int32_t*>(base + L.mpc);
+  a.mperm = reinterpret_cast<int32_t*>(base + L.mperm);
+  a.mnvb = reinterpret_cast<int32_t*>(base + L.mnvb);
+  a.mkqb = reinterpret_cast<int32_t*>(base + L.mkqb);
+  a.mbits = reinterpret_cast<uint32_t*>(base + L.mbits);
   hipStream_t st = (hipStream_t)stream;
   if (int s = hip_status(sgsa::launch_block_select(a, st), "sgsa_block_retrieve (select)")) return s;
   if (block_scores != nullptr)
@@ -685,6 +728,9 @@ int sgsa_block_retrieve(int dtype, int B, int T, int H, int D, int top_k, int bl
                       "sgsa_block_retrieve (weights)");
   return SGSA_OK;
 }
+}  // namespace
+
+extern "C" {
 
 int sgsa_rms_norm(int dtype, int weight_f32, long rows, int C, const void* x, const void* weight, float eps, void* y,
                   void* stream) {

@@ -11,6 +11,12 @@
 //                        their scores: block_token sorts them in LDS and emits
 //                        the masked top-k slots; block_only emits them all.
 //
+// With a padding mask (mask [B,T], the same for keys and queries, :421-428)
+// a row sees the valid keys <= its position, a padded query row sees none;
+// block_mask_prep_kernel lays out per batch the valid keys' prefix counts and
+// order, the mask as bits and each row's count of blocks holding a key it sees,
+// from which the rows' k_q (:159-160) follows.
+//
 // Scores here are acc * (1/sqrt(D)).  bf16 inputs with D % 32 == 0: acc from
 // v_mfma_f32_16x16x32_bf16 over d in steps of 32 (the MFMA sweep and scorer);
 // otherwise acc is an fp32 fma chain over d = 0..D-1 in ascending order.  The
@@ -33,6 +39,79 @@ __device__ __forceinline__ void wave_sync_lds() {
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
+
+// ---- padding masks ----------------------------------------------------------
+// One 1024-thread workgroup per batch b, over the positions in tiles of 1024:
+// pass 1 writes pc[t] = valid keys before t (pc[T] = all of them), perm[pc[t]]
+// = t for valid t and the mask bits; pass 2 flags each block's first valid key
+// (a valid t with no valid key in [block start, t)), and the inclusive prefix
+// of the flags is the number of blocks holding a valid key <= t.  nvb[t] is
+// that count (the count over all keys when not causal) for a valid query row,
+// 0 for a padded one.
+__global__ __launch_bounds__(1024) void block_mask_prep_kernel(BlockArgs a) {
+  __shared__ int wsum[16];
+  const int b = blockIdx.x, T = a.T, bs = a.bs;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const uint8_t* m = a.mask + (long)b * T;
+  int32_t* pc = a.mpc + (long)b * (T + 1);
+  int32_t* perm = a.mperm + (long)b * T;
+  int32_t* nvb = a.mnvb + (long)b * T;
+  uint32_t* bits = a.mbits + (long)b * a.nmw;
+  // prefix of a per-position flag over the workgroup: (exclusive count, total)
+  auto scan = [&](bool f, int carry, int& before) {
+    const uint64_t bal = ballot64(f);
+    if (lane == 0) wsum[w] = popc64(bal);
+    __syncthreads();
+    int lo = carry, tot = carry;
+    for (int i = 0; i < 16; ++i) {
+      lo += i < w ? wsum[i] : 0;
+      tot += wsum[i];
+    }
+    before = lo + (int)lane_rank(bal);
+    __syncthreads();
+    return tot;
+  };
+  int carry = 0;
+  for (int t0 = 0; t0 < T; t0 += 1024) {
+    const int t = t0 + tid;
+    const bool v = t < T && m[t] != 0;
+    const uint64_t bal = ballot64(v);
+    if (t < T && (lane & 31) == 0) bits[t >> 5] = (uint32_t)(bal >> (lane & 32));
+    int before;
+    carry = scan(v, carry, before);
+    if (t < T) {
+      pc[t] = before;
+      if (v) perm[before] = t;
+    }
+  }
+  if (tid == 0) pc[T] = carry;
+  __syncthreads();
+  carry = 0;
+  for (int t0 = 0; t0 < T; t0 += 1024) {
+    const int t = t0 + tid;
+    const bool v = t < T && m[t] != 0;
+    const bool first = v && pc[t] == pc[(t / bs) * bs];
+    int before;
+    carry = scan(first, carry, before);
+    if (t < T) nvb[t] = v ? before + (first ? 1 : 0) : 0;
+  }
+  if (!a.causal) {
+    __syncthreads();
+    for (int t = tid; t < T; t += 1024) nvb[t] = m[t] != 0 ? carry : 0;
+  }
+}
+
+// kqb[t] = min(eb, max(1, max over b of nvb[b][t])), the masked top-k's k_q
+// over the block scores of position t (:159-160).
+__global__ __launch_bounds__(256) void block_mask_kq_kernel(BlockArgs a) {
+  const int t = blockIdx.x * 256 + threadIdx.x;
+  if (t >= a.T) return;
+  int mx = 1;
+  for (int b = 0; b < a.B; ++b) mx = max(mx, a.mnvb[(long)b * a.T + t]);
+  a.mkqb[t] = min(a.eb, mx);
+}
+
+__device__ __forceinline__ bool mask_bit(const uint32_t* bits, int j) { return (bits[j >> 5] >> (j & 31)) & 1u; }
 
 // ---- block maxima ----------------------------------------------------------
 // Block scores are held block-major, [B,H,nb,T] (entry (b,h,j,t) at
@@ -59,6 +138,7 @@ __global__ __launch_bounds__(256) void block_max_kernel(BlockArgs a, float mscal
   const int tid = threadIdx.x, ty = tid >> 4, tx = tid & 15;
   const X* Q = reinterpret_cast<const X*>(a.q);
   const X* K = reinterpret_cast<const X*>(a.k);
+  const uint32_t* mb = a.mask ? a.mbits + (long)b * a.nmw : nullptr;
 
   for (int e = tid; e < 64 * D; e += 256) {
     const int r = e / D, d = e % D, t = r0 + r;
@@ -102,7 +182,8 @@ __global__ __launch_bounds__(256) void block_max_kernel(BlockArgs a, float mscal
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int r = ty + 16 * i, c = tx + 16 * j, t = r0 + r, key = k0 + c;
-        const bool ok = t < T && key < T && (!a.causal || key <= t);
+        bool ok = t < T && key < T && (!a.causal || key <= t);
+        if (ok && a.mask) ok = mask_bit(mb, t) && mask_bit(mb, key);
         ss[r * 65 + c] = ok ? block_score(acc[i][j], mscale) : -FLT_MAX;
       }
     __syncthreads();
@@ -174,6 +255,10 @@ __global__ __launch_bounds__(256) void block_max_mfma_kernel(BlockArgs a, float 
       if (t < T) bsc[(fb + e / BMM_ROWS) * T + t] = -FLT_MAX;
     }
   }
+  const uint32_t* mb = a.mask ? a.mbits + (long)b * a.nmw : nullptr;
+  bool qok[2];
+#pragma unroll
+  for (int rs = 0; rs < 2; ++rs) qok[rs] = !mb || (qrow[rs] < T && mask_bit(mb, qrow[rs]));
 
   const int cpr = D / 8;       // 16-byte chunks per key row
   const int nch = 64 * cpr;    // chunks per tile, <= 1024
@@ -198,6 +283,12 @@ __global__ __launch_bounds__(256) void block_max_mfma_kernel(BlockArgs a, float 
     __syncthreads();
     if (k0 + 64 < kend) fetch(k0 + 64);
     const int kt_end = min(k0 + 64, T);
+    // the tile's 64 mask bits (keys k0.., k0 a multiple of 64)
+    uint64_t kbits = ~0ull;
+    if (mb) {
+      const int w0 = k0 >> 5;
+      kbits = (uint64_t)mb[w0] | (w0 + 1 < a.nmw ? (uint64_t)mb[w0 + 1] << 32 : 0ull);
+    }
     float sc[2][4][4];
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
@@ -216,7 +307,8 @@ __global__ __launch_bounds__(256) void block_max_mfma_kernel(BlockArgs a, float 
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int key = k0 + 16 * kb + 4 * lg + i;
-          const bool ok = qrow[rs] < T && key < T && (!a.causal || key <= qrow[rs]);
+          const bool ok = qrow[rs] < T && key < T && (!a.causal || key <= qrow[rs]) && qok[rs] &&
+                          ((kbits >> (key - k0)) & 1ull);
           sc[rs][kb][i] = ok ? v[i] : -FLT_MAX;
         }
       }
@@ -281,6 +373,9 @@ __global__ __launch_bounds__(256) void block_max_mfma_kernel(BlockArgs a, float 
 // (16 consecutive rows per store); blocks never span tiles, and nothing is
 // shared between waves.  Same operands, k-position order and score_of() as
 // block_cand_kernel's scorer, so scores agree bit for bit.
+// MK: the call has a padding mask (a separate instantiation keeps the unmasked
+// sweep's registers as they are).
+template <bool MK>
 __global__ __launch_bounds__(256, 2) void block_max_reg_kernel(BlockArgs a, float mscale) {
   constexpr int QR = BMM_ROWS, NG = QR / 16, TK = 128;
   const int D = a.D, T = a.T, H = a.H, bs = a.bs, nb = a.nb, nks = D / 32;
@@ -314,6 +409,15 @@ __global__ __launch_bounds__(256, 2) void block_max_reg_kernel(BlockArgs a, floa
     }
   }
   const int minvalid = a.causal ? min(T, r0 + 1) : T;   // keys below it are valid for every row
+  const uint32_t* mb = MK ? a.mbits + (long)b * a.nmw : nullptr;
+  uint32_t qok = 0;   // bit g: row r0 + 16 g + lr is a real token
+  if (MK) {
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      const int qr = r0 + 16 * g + lr;
+      if (qr < T && mask_bit(mb, qr)) qok |= 1u << g;
+    }
+  }
   const int ntile = (kend + TK - 1) / TK;
   const int krow = (lr >> 2) + 4 * (lr & 3);
   bf16x8 kf[2][BLK_MAX_D / 32];
@@ -333,7 +437,8 @@ __global__ __launch_bounds__(256, 2) void block_max_reg_kernel(BlockArgs a, floa
   if (ntile > 0) kload(0);
   for (int kt = 0; kt < ntile; ++kt) {
     const int kw = kt * TK + 32 * w;   // the wave's first key
-    const bool full = kw + 32 <= minvalid;
+    const bool full = !MK && kw + 32 <= minvalid;
+    const uint32_t kbits = MK ? (kw < T ? mb[kw >> 5] : 0u) : ~0u;   // keys kw..kw+31
     float m[2][NG];
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
@@ -349,7 +454,8 @@ __global__ __launch_bounds__(256, 2) void block_max_reg_kernel(BlockArgs a, floa
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int key = kw + 16 * u + lg + 4 * i;
-          const bool ok = full || (qr < T && key < T && (!a.causal || key <= qr));
+          bool ok = full || (qr < T && key < T && (!a.causal || key <= qr));
+          if (MK) ok = ok && ((qok >> g) & 1u) && ((kbits >> (key - kw)) & 1u);
           mx = fmaxf(mx, ok ? sc[i] : -FLT_MAX);
         }
         m[u][g] = mx;
@@ -389,11 +495,15 @@ __global__ __launch_bounds__(256) void block_scores_transpose_kernel(const float
 // ---- top blocks per row ----------------------------------------------------
 // One lane per row; the lanes of a wave take consecutive query positions, so
 // each block-score read is coalesced.  Blocks 0..lim/bs hold a key <= lim
-// (lim = t causal, else T-1); they are the valid blocks of :188-189, the same
-// count for every (b, h) of a row, so the masked top-k keeps kqb = min(eb,
-// that count) of them (:159-160) and pads the rest with index 0 (:151-152).
-// A pass keeps, in registers, the best BS_R blocks after the last one taken,
-// in (score desc, index asc) order; passes repeat until kqb are taken.
+// (lim = t causal, else T-1); without a mask they are the valid blocks of
+// :188-189, the same count for every (b, h) of a row, so the masked top-k
+// keeps kqb = min(eb, that count) of them (:159-160) and pads the rest with
+// index 0 (:151-152).  With a mask the valid blocks are those holding a key
+// the row sees (score > -FLT_MAX), kqb comes from block_mask_kq_kernel (at
+// most the lim/bs + 1 blocks scanned), and a row with fewer valid blocks takes
+// its invalid ones, -FLT_MAX, in ascending index.  A pass keeps, in
+// registers, the best BS_R blocks after the last one taken, in (score desc,
+// index asc) order; passes repeat until kqb are taken.
 constexpr int BS_R = 4;
 
 __global__ __launch_bounds__(256) void block_select_kernel(BlockArgs a) {
@@ -404,7 +514,10 @@ __global__ __launch_bounds__(256) void block_select_kernel(BlockArgs a) {
   const long bh = row / T;
   const int lim = a.causal ? t : T - 1;
   const int nvb = lim / bs + 1;
-  const int kqb = min(eb, nvb);
+  const int kqb = a.mask ? a.mkqb[t] : min(eb, nvb);
+  const int b = (int)(bh / a.H);
+  const int32_t* pc = a.mask ? a.mpc + (long)b * (T + 1) : nullptr;
+  const bool qok = !a.mask || a.mask[(long)b * T + t] != 0;
   const float* col = a.block_scores + bh * a.nb * T + t;
   int32_t* bi = a.block_indices + row * eb;
   float ls = INFINITY;
@@ -434,7 +547,8 @@ __global__ __launch_bounds__(256) void block_select_kernel(BlockArgs a) {
         int j = bj[r];
         if (j == 0x7fffffff) j = 0;   // only NaN scores left: keep block 0 so every key stays in range
         bi[got + r] = j;
-        ncand += min(j * bs + bs, lim + 1) - j * bs;
+        const int hi = min(j * bs + bs, lim + 1);
+        ncand += pc ? (qok ? pc[hi] - pc[j * bs] : 0) : hi - j * bs;
         if (got + r == 0) first = j;
         if (got + r == 1) second = j;
         ls = bv[r];
@@ -521,19 +635,26 @@ __global__ __launch_bounds__(64) void block_cand_kernel(BlockArgs a, float mscal
   const int b = (int)(bh / H), h = (int)(bh % H);
   const int lim = a.causal ? t : T - 1;
   const int nvb = lim / bs + 1;
-  const int kqb = min(eb, nvb);
+  const bool masked = a.mask != nullptr;
+  const int kqb = masked ? a.mkqb[t] : min(eb, nvb);
+  const int32_t* pc = masked ? a.mpc + (long)b * (T + 1) : nullptr;
+  const int32_t* perm = masked ? a.mperm + (long)b * T : nullptr;
+  const uint8_t* mrow = masked ? a.mask + (long)b * T : nullptr;
+  const bool qok = !masked || mrow[t] != 0;
   const int32_t* bi = a.block_indices + row * eb;
   const X* Q = reinterpret_cast<const X*>(a.q);
   const X* K = reinterpret_cast<const X*>(a.k);
 
   for (int d = lane; d < D; d += 64) qrow[d] = ld(Q, ((long)(b * T + t) * H + h) * D + d);
+  // candidates of kept block s: its keys <= lim (with a mask, its valid ones)
   int run = 0;
   for (int s0 = 0; s0 < kqb; s0 += 64) {
     const int s = s0 + lane;
     int c = 0;
     if (s < kqb) {
       const int bj = bi[s];
-      c = min(bj * bs + bs, lim + 1) - bj * bs;
+      const int hi = min(bj * bs + bs, lim + 1);
+      c = masked ? (qok ? pc[hi] - pc[bj * bs] : 0) : hi - bj * bs;
     }
     const int inc = (int)wave_incl_scan((uint32_t)c);
     if (s < kqb) pre[s] = run + inc - c;
@@ -549,7 +670,8 @@ __global__ __launch_bounds__(64) void block_cand_kernel(BlockArgs a, float mscal
       if (pre[mid] <= c) lo = mid;
       else hi = mid - 1;
     }
-    return bi[lo] * bs + (c - pre[lo]);
+    // the (c - pre[lo])-th candidate of block bi[lo]
+    return masked ? perm[pc[bi[lo] * bs] + (c - pre[lo])] : bi[lo] * bs + (c - pre[lo]);
   };
   float m1 = -FLT_MAX;
   if (MF) {
@@ -659,7 +781,7 @@ __global__ __launch_bounds__(64) void block_cand_kernel(BlockArgs a, float mscal
     for (int j0 = 0; found < need && j0 < T; j0 += 64) {
       const int j = j0 + lane;
       bool member = false;
-      if (j < T && j <= lim) {
+      if (j < T && j <= lim && (!masked || (qok && mrow[j] != 0))) {
         if (all_kept) {
           member = true;
         } else {
@@ -720,10 +842,17 @@ bool block_uses_mfma(const BlockArgs& a) {
 
 hipError_t launch_block_select(const BlockArgs& a, hipStream_t st) {
   const float ms = score_multiplier((float)sqrt((double)a.D), 0);
+  if (a.mask) {
+    block_mask_prep_kernel<<<dim3((unsigned)a.B), 1024, 0, st>>>(a);
+    block_mask_kq_kernel<<<dim3((unsigned)((a.T + 255) / 256)), 256, 0, st>>>(a);
+  }
   const dim3 g1((unsigned)((a.T + 63) / 64), (unsigned)(a.B * a.H));
   const dim3 g2((unsigned)((a.T + BMM_ROWS - 1) / BMM_ROWS), (unsigned)(a.B * a.H));
   const bool mf = block_uses_mfma(a);
-  if (mf && (a.bs == 16 || a.bs == 32)) block_max_reg_kernel<<<g2, 256, 0, st>>>(a, ms);
+  if (mf && (a.bs == 16 || a.bs == 32)) {
+    if (a.mask) block_max_reg_kernel<true><<<g2, 256, 0, st>>>(a, ms);
+    else block_max_reg_kernel<false><<<g2, 256, 0, st>>>(a, ms);
+  }
   else if (mf && a.bs % 16 == 0) block_max_mfma_kernel<true><<<g2, 256, 0, st>>>(a, ms);
   else if (mf) block_max_mfma_kernel<false><<<g2, 256, 0, st>>>(a, ms);
   else if (a.dtype == DT_F32) block_max_kernel<float><<<g1, 256, 0, st>>>(a, ms);

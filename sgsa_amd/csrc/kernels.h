@@ -226,6 +226,14 @@ struct BlockArgs {
   uint8_t* slot_valid;       // [B,H,T,kk] (block_token)
   float* top2;               // [B,H,T,2]
   int32_t* counts;           // [B,H,T] slots handed to the gather
+  // padding mask (nullptr: none): mask [B,T] nonzero = real token, for keys and queries alike
+  const uint8_t* mask;
+  int nmw;                   // 32-bit words per batch of mbits, ceil(T/32)
+  int32_t* mpc;              // [B,T+1] valid keys before each position
+  int32_t* mperm;            // [B,T] valid keys in ascending order
+  int32_t* mnvb;             // [B,T] blocks holding a valid key the row sees (0 for a padded query)
+  int32_t* mkqb;             // [T] kept blocks per position: min(eb, max(1, max over b of mnvb))
+  uint32_t* mbits;           // [B,nmw] the mask as bits
 };
 
 hipError_t launch_block_select(const BlockArgs& a, hipStream_t st);

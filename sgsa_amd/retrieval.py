@@ -454,9 +454,11 @@ def block_retrieve(
     q,k,v: [B,T,H,D].  k_hat/v_hat [B,T,H,D]; block_indices [B,H,T,min(top_blocks, nb)];
     block_token: indices and weights [B,H,T,min(top_k, T)]; block_only: indices None,
     weights [B,H,T,T], and the diagnostics without the distance statistics (:455-463).
+    attention_mask [B,T] (nonzero = real token) masks keys and query rows alike, as
+    the reference's valid mask does (:421-428): block scores, the rows' k_q over the
+    valid blocks (:188-195, :159-160) and the candidates (:313-320) see only real
+    tokens, and padded rows retrieve nothing (sgsa_block_retrieve_masked).
     """
-    if attention_mask is not None:
-        raise NotImplementedError("block_retrieve: attention_mask is not supported by the HIP retrieval yet")
     if mode not in BLOCK_MODES:
         raise ValueError(f"mode must be one of {sorted(BLOCK_MODES)}, got {mode!r}")
     B, T, H, D = q.shape
@@ -482,11 +484,21 @@ def block_retrieve(
     k_hat = torch.empty(B, T, H, D, device=dev, dtype=q.dtype)
     v_hat = torch.empty_like(k_hat)
     diag = torch.empty(_abi.NDIAG, B, H, T, device=dev, dtype=torch.float32) if return_diagnostics else None
-    _abi.check(lib.sgsa_block_retrieve(
-        _abi.dtype_code(q.dtype), B, T, H, D, int(top_k), int(block_size), int(top_blocks), m, int(causal),
-        float(tau_c), int(local_window), int(sink_size), _abi.ptr(qc), _abi.ptr(kc), _abi.ptr(vc), _abi.ptr(idx),
-        _abi.ptr(bidx), _abi.ptr(bsc), _abi.ptr(weights), _abi.ptr(k_hat), _abi.ptr(v_hat), _abi.ptr(diag),
-        _abi.ptr(ws), ws.numel(), _abi.stream_of(qc)))
+    if attention_mask is None:
+        _abi.check(lib.sgsa_block_retrieve(
+            _abi.dtype_code(q.dtype), B, T, H, D, int(top_k), int(block_size), int(top_blocks), m, int(causal),
+            float(tau_c), int(local_window), int(sink_size), _abi.ptr(qc), _abi.ptr(kc), _abi.ptr(vc), _abi.ptr(idx),
+            _abi.ptr(bidx), _abi.ptr(bsc), _abi.ptr(weights), _abi.ptr(k_hat), _abi.ptr(v_hat), _abi.ptr(diag),
+            _abi.ptr(ws), ws.numel(), _abi.stream_of(qc)))
+    else:
+        if tuple(attention_mask.shape) != (B, T):
+            raise ValueError(f"attention_mask must have shape [batch, seq] = {(B, T)}, got {tuple(attention_mask.shape)}")
+        am = (attention_mask.to(dev) != 0).to(torch.uint8).contiguous()
+        _abi.check(lib.sgsa_block_retrieve_masked(
+            _abi.dtype_code(q.dtype), B, T, H, D, int(top_k), int(block_size), int(top_blocks), m, int(causal),
+            float(tau_c), int(local_window), int(sink_size), _abi.ptr(qc), _abi.ptr(kc), _abi.ptr(vc), _abi.ptr(am),
+            _abi.ptr(idx), _abi.ptr(bidx), _abi.ptr(bsc), _abi.ptr(weights), _abi.ptr(k_hat), _abi.ptr(v_hat),
+            _abi.ptr(diag), _abi.ptr(ws), ws.numel(), _abi.stream_of(qc)))
     names = _abi.DIAG_NAMES if m == 1 else _abi.DIAG_NAMES[:6]
     out = {
         "indices": idx.long() if idx is not None else None,

@@ -26,11 +26,12 @@ def _qkv(B, T, H, D, dt, seed, dup=False):
     return [t.to(dt).float() for t in x]
 
 
-def _check(dev, B, T, H, D, dt, top_k, bs, tb, mode, causal=True, seed=0, dup=False):
+def _check(dev, B, T, H, D, dt, top_k, bs, tb, mode, causal=True, seed=0, dup=False, am=None):
     q, k, v = _qkv(B, T, H, D, dt, seed, dup)
-    ref = O.block_retrieval(q, k, v, top_k, bs, tb, mode=mode, causal=causal)
+    ref = O.block_retrieval(q, k, v, top_k, bs, tb, mode=mode, causal=causal, attention_mask=am)
     got = sgsa_amd.block_retrieve(q.to(dev, dt), k.to(dev, dt), v.to(dev, dt), top_k, bs, tb, mode=mode,
-                                  causal=causal, return_block_scores=True)
+                                  causal=causal, return_block_scores=True,
+                                  attention_mask=None if am is None else am.to(dev))
     torch.cuda.synchronize()
     tol = dict(atol=2e-5, rtol=2e-5) if dt == torch.float32 else dict(atol=2e-2, rtol=2e-2)
     torch.testing.assert_close(got["block_scores"].cpu(), ref["block_scores"], atol=1e-5, rtol=1e-5)
@@ -115,3 +116,47 @@ def test_block_retrieve_rejects_too_many_candidates(dev):
     q = torch.zeros(1, 4096, 1, 16, device=dev)
     with pytest.raises(ValueError, match="candidate keys"):
         sgsa_amd.block_retrieve(q, q, q, 8, 1024, 4, mode="block_only")
+
+
+def _pad(B, T):
+    """Batch 0 all real, batch 1 left-padded with a hole, batch 2 right-padded
+    with every 5th token a pad (padded query rows and rows whose k_q exceeds
+    their own valid count are both present)."""
+    am = torch.ones(B, T, dtype=torch.bool)
+    am[1, :min(19, T - 1)] = False
+    am[1, T // 2:T // 2 + 3] = False
+    if B > 2:
+        am[2, T - T // 4:] = False
+        am[2, ::5] = False
+    return am
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("mode", ["block_token", "block_only"])
+@pytest.mark.parametrize("T,bs,tb,top_k", [(150, 32, 2, 16), (97, 7, 3, 12), (130, 16, 4, 24), (260, 48, 2, 30),
+                                           (40, 1, 5, 6), (64, 64, 2, 8)])
+def test_block_modes_with_padding_mask_match_oracle(dev, dt, mode, T, bs, tb, top_k):
+    """sgsa_block_retrieve_masked against the oracle with the reference's valid
+    mask (causal & real key & real query, modeling_sgsa.py:421-428): block scores,
+    block and token selections (fills included) exactly, values within tolerance.
+    bs 16 / 32 run the register sweep, 48 / 64 the LDS-tiled MFMA sweep, 7 and 1
+    the key-by-key reduction (fp32: the fma sweep)."""
+    print(f"masked block {mode} {dt} T={T} bs={bs} tb={tb} k={top_k}", flush=True)
+    _check(dev, 3, T, 2, 64, dt, top_k, bs, tb, mode, seed=T + bs + 1, am=_pad(3, T))
+
+
+@pytest.mark.parametrize("mode", ["block_token", "block_only"])
+def test_block_modes_with_padding_mask_non_causal_and_d128(dev, mode):
+    _check(dev, 3, 120, 2, 128, torch.bfloat16, 10, 16, 3, mode, causal=False, seed=5, am=_pad(3, 120))
+    _check(dev, 3, 99, 1, 128, torch.bfloat16, 10, 32, 2, mode, causal=True, seed=6, am=_pad(3, 99))
+
+
+def test_block_modes_all_real_mask_equals_unmasked(dev):
+    q, k, v = (t.to(dev, torch.bfloat16) for t in _qkv(2, 200, 2, 64, torch.bfloat16, 9))
+    am = torch.ones(2, 200, dtype=torch.bool, device=dev)
+    for mode in ("block_token", "block_only"):
+        a = sgsa_amd.block_retrieve(q, k, v, 12, 32, 3, mode=mode)
+        b = sgsa_amd.block_retrieve(q, k, v, 12, 32, 3, mode=mode, attention_mask=am)
+        torch.cuda.synchronize()
+        for name in ("block_indices", "k_hat", "v_hat", "weights"):
+            assert torch.equal(a[name], b[name]), (mode, name)
