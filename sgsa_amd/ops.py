@@ -199,6 +199,7 @@ def chunk_sgsa(
     chunk_size: int = 64,
     output_final_state: bool = False,
     use_triton: bool = True,
+    cu_seqlens: Optional[Tensor] = None,
 ) -> Tuple[Tensor, Optional[Tensor]]:
     """Chunked Sparse-Guided State Attention core (modelings/sgsa_ops/chunk.py:104-148).
 
@@ -206,7 +207,20 @@ def chunk_sgsa(
     initial_state: [B,H,D,D].  The sparse write is used iff sparse_k, sparse_v
     and alpha are all given (chunk.py:123).  Returns (o [B,T,H,D] in q.dtype,
     final state [B,H,D,D] float32 or None).
+
+    ``cu_seqlens`` [N+1]: N sequences packed along T of a batch of one (the FLA
+    varlen convention, sgsa_amd.varlen); initial and final states are then
+    [N,H,D,D], one per sequence, and each sequence starts from its own state.
     """
+    if cu_seqlens is not None:
+        from . import varlen
+        lay = varlen.layout(cu_seqlens, q)
+        varlen.check_states(lay, initial_state)
+        pq, pk, pv, pb, pg, psk, psv, pa = varlen.pad_state_inputs(lay, q, k, v, beta, gamma, sparse_k, sparse_v,
+                                                                   alpha)
+        o, ht = chunk_sgsa(pq, pk, pv, pb, pg, psk, psv, pa, initial_state, chunk_size, output_final_state,
+                           use_triton)
+        return lay.unpad(o), ht
     has_sparse = sparse_k is not None and sparse_v is not None and alpha is not None
     has_init = initial_state is not None
     empty = torch.empty(0, device=q.device, dtype=q.dtype)

@@ -116,11 +116,21 @@ def fused_recurrent_sgsa(
     initial_state: Optional[Tensor] = None,
     output_final_state: bool = False,
     use_triton: bool = True,
+    cu_seqlens: Optional[Tensor] = None,
 ) -> Tuple[Tensor, Optional[Tensor]]:
     """q, k, v [B,T,H,D]; beta, gamma [B,T,H]; state [B,H,D,D] (float32 out).
-    Differentiable: the backward is the native chunk-form backward (FusedRecurrentSGSAFunction)."""
+    Differentiable: the backward is the native chunk-form backward (FusedRecurrentSGSAFunction).
+    ``cu_seqlens`` [N+1]: packed sequences in a batch of one, states [N,H,D,D] (sgsa_amd.varlen)."""
     if not q.is_cuda:
         raise ValueError("fused_recurrent_sgsa: the SGSA kernels run on a ROCm GPU; got CPU tensors")
+    if cu_seqlens is not None:
+        from . import varlen
+        lay = varlen.layout(cu_seqlens, q)
+        varlen.check_states(lay, initial_state)
+        pq, pk, pv, pb, pg, psk, psv, pa = varlen.pad_state_inputs(lay, q, k, v, beta, gamma, sparse_k, sparse_v,
+                                                                   alpha)
+        o, ht = fused_recurrent_sgsa(pq, pk, pv, pb, pg, psk, psv, pa, initial_state, output_final_state, use_triton)
+        return lay.unpad(o), ht
     has_sparse = sparse_k is not None and sparse_v is not None and alpha is not None
     has_init = initial_state is not None
     empty = torch.empty(0, device=q.device, dtype=q.dtype)

@@ -370,6 +370,7 @@ def sparse_retrieve(
     sorted: bool = True,
     return_weights: bool = True,
     return_diagnostics: bool = True,
+    cu_seqlens: Optional[Tensor] = None,
 ) -> Dict[str, object]:
     """Token-only retrieval; the dict of SparseRetriever.forward (modeling_sgsa.py:467-474).
 
@@ -378,8 +379,19 @@ def sparse_retrieve(
     masks padded keys and padded queries (:421-428); a row then keeps
     min(top_k, max(1, largest valid count of that row over the batch)) slots,
     its invalid ones pointing at its lowest-index invalid keys with weight 0
-    and the rest index 0 (:144-165).
+    and the rest index 0 (:144-165).  ``cu_seqlens`` [N+1]: N sequences packed
+    along T of a batch of one, each retrieving from itself (sgsa_amd.varlen);
+    outputs come back packed, indices relative to the sequence start.
     """
+    if cu_seqlens is not None:
+        from . import varlen
+        if attention_mask is not None:
+            raise ValueError("sparse_retrieve: pass either cu_seqlens or attention_mask, not both")
+        lay = varlen.layout(cu_seqlens, q)
+        r = sparse_retrieve(lay.pad(q), lay.pad(k), lay.pad(v), top_k, causal=causal, attention_mask=lay.mask,
+                            tau_c=tau_c, local_window=local_window, sink_size=sink_size, sorted=sorted,
+                            return_weights=return_weights, return_diagnostics=return_diagnostics)
+        return varlen.unpad_retrieval(lay, r)
     B, T, H, D = q.shape
     if v.shape != k.shape or v.dtype != k.dtype:
         raise ValueError("v must match k in shape and dtype")
@@ -447,6 +459,7 @@ def block_retrieve(
     return_weights: bool = True,
     return_diagnostics: bool = True,
     return_block_scores: bool = False,
+    cu_seqlens: Optional[Tensor] = None,
 ) -> Dict[str, object]:
     """Block retrieval; the dict of SparseRetriever.forward for ``retrieval_mode``
     "block_only" / "block_token" on the torch path (modelings/modeling_sgsa.py:444-474).
@@ -458,7 +471,20 @@ def block_retrieve(
     the reference's valid mask does (:421-428): block scores, the rows' k_q over the
     valid blocks (:188-195, :159-160) and the candidates (:313-320) see only real
     tokens, and padded rows retrieve nothing (sgsa_block_retrieve_masked).
+    ``cu_seqlens`` [N+1]: packed sequences in a batch of one (sgsa_amd.varlen);
+    blocks start at each sequence's start, outputs come back packed (block_only's
+    dense weights [1,H,total,L_max] over the row's own sequence).
     """
+    if cu_seqlens is not None:
+        from . import varlen
+        if attention_mask is not None:
+            raise ValueError("block_retrieve: pass either cu_seqlens or attention_mask, not both")
+        lay = varlen.layout(cu_seqlens, q)
+        r = block_retrieve(lay.pad(q), lay.pad(k), lay.pad(v), top_k, block_size, top_blocks, mode, causal=causal,
+                           attention_mask=lay.mask, tau_c=tau_c, local_window=local_window, sink_size=sink_size,
+                           return_weights=return_weights, return_diagnostics=return_diagnostics,
+                           return_block_scores=return_block_scores)
+        return varlen.unpad_retrieval(lay, r)
     if mode not in BLOCK_MODES:
         raise ValueError(f"mode must be one of {sorted(BLOCK_MODES)}, got {mode!r}")
     B, T, H, D = q.shape
@@ -537,12 +563,14 @@ class SparseRetriever(nn.Module):
         self.sink_size = getattr(config, "sink_size", 8)
 
     def forward(self, q: Tensor, k: Tensor, v: Tensor, causal: bool = True,
-                attention_mask: Optional[Tensor] = None) -> Dict[str, object]:
+                attention_mask: Optional[Tensor] = None, cu_seqlens: Optional[Tensor] = None) -> Dict[str, object]:
+        """The reference's forward (:407-474); ``cu_seqlens`` additionally takes packed
+        sequences in a batch of one (the varlen layout of the reference's flash_moba calls)."""
         if self.mode != "token_only":
             r = block_retrieve(q, k, v, self.top_k, self.block_size, self.top_blocks, self.mode, causal=causal,
                                attention_mask=attention_mask, tau_c=self.tau_c, local_window=self.local_window,
-                               sink_size=self.sink_size)
+                               sink_size=self.sink_size, cu_seqlens=cu_seqlens)
             return {key: r[key] for key in ("indices", "block_indices", "weights", "k_hat", "v_hat", "diagnostics")}
         r = sparse_retrieve(q, k, v, self.top_k, causal=causal, attention_mask=attention_mask, tau_c=self.tau_c,
-                            local_window=self.local_window, sink_size=self.sink_size)
+                            local_window=self.local_window, sink_size=self.sink_size, cu_seqlens=cu_seqlens)
         return {key: r[key] for key in ("indices", "block_indices", "weights", "k_hat", "v_hat", "diagnostics")}
