@@ -1,7 +1,8 @@
 #!/usr/bin/env python3
 """SGSA layer-forward benchmark on one MI355X.
 
-    python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--no-cpu-baseline] [--workload layer|model|hybrid|block]
+    python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--no-cpu-baseline]
+                    [--workload layer|model|hybrid|block|backward]
 
 A step is one SGSA layer forward over the batch at the north-star shape
 (B=1, H=16, T=32768, d=128, top-k=2048, chunk 64, bf16 inputs, fp32 state),
@@ -287,6 +288,76 @@ def run_block(args) -> int:
     return 0
 
 
+def run_backward(args) -> int:
+    """The native backward of chunk_sgsa (sgsa_chunk_bwd through sgsa_amd.chunk_sgsa_bwd) at the north-star shape
+    with the sparse write: every input gradient from dO, bf16 inputs, fp32 state.  A step is one backward call on
+    resident inputs and output gradient.  --torch-recompute also times, once, the reference's method (the forward
+    recomputed in torch under autograd, modelings/sgsa_ops/chunk_bwd.py:31-77) on the same inputs in fp32."""
+    import sgsa_amd
+    from sgsa_amd.ops import chunk_sgsa_bwd
+    B, T, H, D = NORTH_STAR["B"], args.T, NORTH_STAR["H"], NORTH_STAR["D"]
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+    r = lambda *s: torch.randn(*s, device=dev, generator=g)
+    unit = lambda t: t / t.norm(dim=-1, keepdim=True)
+    bf = torch.bfloat16
+    q, k, v = unit(r(B, T, H, D)).to(bf), unit(r(B, T, H, D)).to(bf), r(B, T, H, D).to(bf)
+    sk, sv = unit(r(B, T, H, D)).to(bf), r(B, T, H, D).to(bf)
+    beta, gamma = torch.sigmoid(r(B, T, H)), torch.sigmoid(r(B, T, H) + 4.0)
+    alpha = 0.25 * torch.sigmoid(r(B, T, H))
+    do = r(B, T, H, D).to(bf)
+    inputs = [q, k, v, beta, gamma, sk, sv, alpha, None]
+    needs = [True] * 8 + [False]
+    cur = torch.cuda.current_stream()
+    for _ in range(args.warmup):
+        grads = chunk_sgsa_bwd(inputs, needs, do, None)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(cur)
+    for _ in range(args.steps):
+        grads = chunk_sgsa_bwd(inputs, needs, do, None)
+    e1.record(cur)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / max(args.steps, 1)
+    if not all(torch.isfinite(t.float()).all() for t in grads if t is not None):
+        log("backward: non-finite gradient")
+        return 1
+    log(f"native backward ms/call {ms:.3f}")
+    # fp32 MFMA multiply-adds per chunk-head (M = 2L samples with the sparse write, L tokens, d dims)
+    M, L, d = 128, 64, 128
+    mac = (3 * M * M * d + M ** 3 // 3                                    # intra: Gram, (I+T)^-1, W, U
+           + 2 * d * d * M                                               # maps: Phi, Pm
+           + 2 * d ** 3                                                  # the two scans, one step each
+           + L * M * d + d * d * L + M * d * L + d * d * M               # pre: P, Q^T dO, P^T dO, W^T X1
+           + 5 * M * d * d + 7 * M * M * d + 2 * M ** 3 + 4 * L * M * d + L * d * d)   # gradient kernel
+    nchunks = B * H * ((T + 63) // 64)
+    flops = 2.0 * mac * nchunks
+    torch_ms = None
+    if args.torch_recompute:
+        from sgsa_amd.backward import recompute_grads
+        f32 = [None if t is None else t.float() for t in inputs]
+        recompute_grads(f32, needs, do.float(), None)
+        torch.cuda.synchronize()
+        t0 = time.time()
+        recompute_grads(f32, needs, do.float(), None)
+        torch.cuda.synchronize()
+        torch_ms = (time.time() - t0) * 1e3
+        log(f"torch recompute ms/call {torch_ms:.1f}")
+    print(json.dumps({
+        "metric": "chunk_sgsa backward tokens/s (bf16, T=32k, H=16, d=128, sparse write)",
+        "value": round(B * T / (ms / 1000.0), 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32 (bf16 inputs and gradients)", "data": "synthetic",
+        "config": {"workload": "chunk_sgsa_backward", "B": B, "T": T, "H": H, "D": D, "chunk": 64,
+                   "sparse_write": True},
+        "mfma_fp32": {"flops": flops, "achieved_tflops": round(flops / (ms / 1000.0) / 1e12, 2),
+                      "peak_tflops": 157.3, "frac": round(flops / (ms / 1000.0) / 1e12 / 157.3, 4)},
+        "torch_recompute_ms": round(torch_ms, 1) if torch_ms is not None else None,
+        "cpu_baseline": None,
+    }), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -304,11 +375,14 @@ def main() -> int:
                     help="timed step: the fused layer path (K1 row thresholds -> K2 recomputing the scores on "
                          "MFMA -> chunk, what sgsa_layer_fwd runs; default), the tile-list form (K1 tile lists -> "
                          "LDS-tiled MFMA K2 -> chunk) or K1 row lists -> per-row 16-byte gathers -> chunk")
-    ap.add_argument("--workload", choices=("layer", "model", "hybrid", "block"), default="layer",
+    ap.add_argument("--torch-recompute", action="store_true",
+                    help="with --workload backward: also time the torch recompute backward once")
+    ap.add_argument("--workload", choices=("layer", "model", "hybrid", "block", "backward"), default="layer",
                     help="layer: the north-star SGSA layer forward (the headline metric, default); model: "
                          "config 2, the 2-layer SGSA causal LM forward at B=16 T=4096; hybrid: config 4, the "
                          "24-layer SGSA / dense-GQA decoder, prefill of 16384 tokens then 256 decode steps at B=8; "
-                         "block: the retriever's block_token / block_only modes at the north-star shape")
+                         "block: the retriever's block_token / block_only modes at the north-star shape; "
+                         "backward: the native backward of chunk_sgsa at the north-star shape")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on exactly one GPU (got --gpus {args.gpus}); the SGSA layer shards by head, "
@@ -320,6 +394,8 @@ def main() -> int:
         return run_hybrid(args)
     if args.workload == "block":
         return run_block(args)
+    if args.workload == "backward":
+        return run_backward(args)
 
     import sgsa_amd
     from sgsa_amd import _abi
