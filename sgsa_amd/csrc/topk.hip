@@ -1588,6 +1588,39 @@ __device__ __forceinline__ float next_down(float x) {
   return __uint_as_float((int32_t)u > 0 ? u - 1u : u + 1u);
 }
 
+// The score of one raw accumulator, as score_of computes it.
+__device__ __forceinline__ float score1(float acc, float mscale) {
+#pragma clang fp contract(off)
+  return acc * mscale + 0.0f;
+}
+
+// For mscale > 0, score1 is non-decreasing in the accumulator, and several
+// accumulators can round to one score.  acc_lo_of(a): the smallest x with
+// score1(x) == score1(a); acc_hi_of(a): the largest.  Bisection over the
+// order-preserving keys between -inf and +inf; a is not NaN.
+__device__ __forceinline__ float acc_lo_of(float a, float mscale) {
+  const float S = score1(a, mscale);
+  if (S == -INFINITY) return -INFINITY;
+  uint32_t lo = 0x007fffffu, hi = f32_order_key(a);   // score1(key -inf) < S <= score1(key hi)
+  while (hi - lo > 1u) {
+    const uint32_t mid = lo + ((hi - lo) >> 1);
+    if (score1(key_to_f32(mid), mscale) >= S) hi = mid;
+    else lo = mid;
+  }
+  return key_to_f32(hi);
+}
+__device__ __forceinline__ float acc_hi_of(float a, float mscale) {
+  const float S = score1(a, mscale);
+  if (S == INFINITY) return INFINITY;
+  uint32_t lo = f32_order_key(a), hi = 0xff800000u;   // score1(key lo) <= S < score1(key +inf)
+  while (hi - lo > 1u) {
+    const uint32_t mid = lo + ((hi - lo) >> 1);
+    if (score1(key_to_f32(mid), mscale) <= S) lo = mid;
+    else hi = mid;
+  }
+  return key_to_f32(lo);
+}
+
 // ---------------------------------------------------------------------------
 // K1, threshold form at 128 query rows per block (the layer path: bf16,
 // D = 128, counts that fit 16 bits).
@@ -1610,12 +1643,16 @@ __device__ __forceinline__ float next_down(float x) {
 __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nqb, float mscale) {
   constexpr int QR = 128;
   constexpr int NG = QR / 16;
-  constexpr int HW = NBIN / 2;   // 16-bit counter pairs per row
   constexpr int CAPL = TOPK_CAP / 64;
-  __shared__ __align__(16) uint32_t hist[QR][HW];
+  // Row histograms, 16-bit counters: rows 16g + r and 16(g + 4) + r (g < 4)
+  // share the words of pair 16g + r, bin b in word b, the first row in the low
+  // half.  64 KB; between the sweeps the same memory holds other per-block data.
+  __shared__ __align__(16) uint32_t hist[QR / 2][NBIN];
   __shared__ RowInfo rinfo[NG][16];
   __shared__ int colcnt[NG][16];
   __shared__ float qnorm[NG][16];
+  __shared__ float ra0[NG][16];   // lower edge a0 of b* (accumulator domain)
+  __shared__ int rcntb[NG][16];   // keys in b*
 
   const int BH = a.B * a.H;
   const int nqr = (a.Tq + QR - 1) / QR;
@@ -1686,7 +1723,9 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
 #pragma unroll
     for (int s = 0; s < 4; ++s) kf[s] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8*>(p + 32 * s));
   };
-  // fn(kt, acc): acc[g][i] = score of row r0 + 16g + lr against key kt*64 + 16w + lg + 4i
+  // fn(kt, acc): acc[g][i] = the raw accumulator of row r0 + 16g + lr against key
+  // kt*64 + 16w + lg + 4i; its score is score1(acc, mscale), non-decreasing in
+  // acc (mscale > 0), so both sweeps bin and test accumulators.
   auto sweep = [&](auto&& fn) __attribute__((always_inline)) {
     if (ntile > 0) kload(0);
     for (int kt = 0; kt < ntile; ++kt) {
@@ -1696,7 +1735,7 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
         f4 c = f4_zero();
 #pragma unroll
         for (int s = 0; s < 4; ++s) c = mma_bf16(kf[s], qf[g][s], c);
-        acc[g] = score_of(c, mscale);
+        acc[g] = c;
       }
       if (kt + 1 < ntile) kload(kt + 1);
       fn(kt, acc);
@@ -1713,7 +1752,7 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
     int nv = 0;
     if (qr < Tq) nv = a.causal ? max(0, min(Tk, qr + a.q_offset + 1)) : Tk;
     RowInfo ri;
-    const float bound = qnorm[g][rr] * kmx * fabsf(mscale) * 1.001f;
+    const float bound = qnorm[g][rr] * kmx * 1.001f;   // of |acc|
     ri.iw = (bound > 0.f && bound < FLT_MAX) ? 128.0f / bound : 0.f;
     ri.bc = BIN_C0;
     ri.bstar = -1;
@@ -1726,6 +1765,7 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
   __syncthreads();
 
   // ---- the bins' range from a sample -------------------------------------------
+  // The bins are a monotone map of the accumulator (so of the score).
   // The bound above spans the Cauchy-Schwarz range; scores typically fill a
   // third of it, so the threshold bin holds several times the keys it needs to.
   // The min and max of each row's scores over 8 tiles spread across the sweep,
@@ -1747,7 +1787,7 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
         f4 c = f4_zero();
 #pragma unroll
         for (int s = 0; s < 4; ++s) c = mma_bf16(kf[s], qf[g][s], c);
-        const f4 sc = score_of(c, mscale);
+        const f4 sc = c;
         const int nv = nv_of(g);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -1790,7 +1830,7 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
     }
     __syncthreads();   // the range sums are read before hist is cleared
   }
-  for (int i = tid; i < QR * HW; i += 256) (&hist[0][0])[i] = 0;
+  for (int i = tid; i < QR / 2 * NBIN; i += 256) (&hist[0][0])[i] = 0;
   __syncthreads();
 
   // ---- pass A: block-shared row histograms and each row's top-2 ---------------
@@ -1808,13 +1848,22 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
       if (r0 + 16 * g + lr < Tq && ri.mode != SELECT_ALL) hmask |= 1u << g;
     }
     const bool any_hist = __syncthreads_or(hmask != 0u);
-    auto bump = [&](int row, uint32_t bits) __attribute__((always_inline)) {
-      // word bin >> 1, half bin & 1; the shift 16 (bin & 1) is (bits << 4) mod 32
-      atomicAdd(&hist[row][__builtin_amdgcn_ubfe(bits, 1, 7)], 1u << ((bits << 4) & 31u));
+    // bits = 2^23 + bin as a float's bits (0x4b000000 + bin), so (bits << 2) mod 2^32
+    // is 0x2c000000 + 4 bin: the byte offset of bin b of pair 16(g & 3) + lr is
+    // hb + (bits << 2) + 16384 (g & 3), and the increment is a constant per g.
+    const uint32_t hb = (uint32_t)lr * (NBIN * 4u) - 0x2c000000u;
+    auto bump = [&](int g, uint32_t bits) __attribute__((always_inline)) {
+      uint32_t* p = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(&hist[0][0]) +
+                                                (hb + (bits << 2) + (uint32_t)(g & 3) * (16u * NBIN * 4u)));
+      atomicAdd(p, g < 4 ? 1u : 0x10000u);
     };
+    // The running max is med3(m1, x, FLT_MAX), one instruction (fmaxf, or med3
+    // against +inf, which the compiler turns into fmaxf, canonicalises both
+    // operands first: two more per score).  It equals max(m1, x) for every finite
+    // accumulator; a q.k product that overflows to +inf is kept as FLT_MAX.
     auto top2 = [&](int g, float x) __attribute__((always_inline)) {
       m2[g] = __builtin_amdgcn_fmed3f(m1[g], m2[g], x);
-      m1[g] = fmaxf(m1[g], x);
+      m1[g] = __builtin_amdgcn_fmed3f(m1[g], x, FLT_MAX);
     };
     // Every block has a live row: the sweep gives the top-2 even where no row
     // needs a histogram.  In full tiles every row's histogram takes the adds
@@ -1827,7 +1876,7 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             top2(g, acc[g][i]);
-            if (any_hist) bump(16 * g + lr, score_bin_bits(acc[g][i], iw[g], bc[g]));
+            if (any_hist) bump(g, score_bin_bits(acc[g][i], iw[g], bc[g]));
           }
         }
       } else {
@@ -1838,7 +1887,7 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
           for (int i = 0; i < 4; ++i) {
             const int j = kt * KT + 16 * w + lg + 4 * i;
             top2(g, j < nv ? acc[g][i] : -FLT_MAX);
-            if (((hmask >> g) & 1u) && j < nv) bump(16 * g + lr, score_bin_bits(acc[g][i], iw[g], bc[g]));
+            if (((hmask >> g) & 1u) && j < nv) bump(g, score_bin_bits(acc[g][i], iw[g], bc[g]));
           }
         }
       }
@@ -1859,15 +1908,17 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
         const int g = w + 4 * (rr >> 4), r = rr & 15;
         RowInfo ri = rinfo[g][r];
         if (ri.mode == SELECT_ALL) continue;
-        const uint32_t* hr = hist[16 * g + r];
+        const uint32_t* hr = hist[16 * (g & 3) + r];
+        const uint32_t sh = 16u * (uint32_t)(g >> 2);
         uint32_t c[4];
-        const uint32_t w0 = hr[127 - 2 * lane], w1 = hr[126 - 2 * lane];
-        c[0] = w0 >> 16; c[1] = w0 & 0xffffu; c[2] = w1 >> 16; c[3] = w1 & 0xffffu;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) c[q] = (hr[255 - 4 * lane - q] >> sh) & 0xffffu;
         int bin;
         uint32_t above, cnt;
         find_bin(c, lane, (uint32_t)ri.need, bin, above, cnt);
         if (lane == 0) {
           ri.bstar = bin;
+          rcntb[g][r] = (int)cnt;
           ri.need -= (int)above;
           if (cnt == (uint32_t)ri.need) ri.mode = BIN_ALL;
           else if (cnt <= (uint32_t)TOPK_CAP) ri.mode = COLLECT;
@@ -1894,7 +1945,7 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
     for (int g = 0; g < NG; ++g) t2s[QR * w + 16 * g + lr] = make_float2(m1[g], m2[g]);
   }
   __syncthreads();
-  float2 t2 = make_float2(-FLT_MAX, -FLT_MAX);   // lane < 32: row 16 (w + 4 (lane / 16)) + lane % 16
+  float2 t2 = make_float2(-FLT_MAX, -FLT_MAX);   // lane < 32: row 16 (w + 4 (lane / 16)) + lane % 16 (accumulators)
   if (lane < 32) {
     const int row = 16 * (w + 4 * (lane >> 4)) + (lane & 15);
 #pragma unroll
@@ -1906,6 +1957,16 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
   }
 
   // ---- thresholds for pass B ---------------------------------------------------
+  // b* spans accumulators [a0, a1).  Accumulators that round to one score can
+  // straddle a0 or a1; the selection is by score with ties to the lowest index,
+  // so a tie at the cut may involve keys on both sides of a bin edge.  The
+  // collection window [th0, th1] therefore reaches out to every accumulator
+  // whose score equals that of a0 or of the largest accumulator below a1.  Keys
+  // above th1 are all selected, keys below th0 none; the resolve takes
+  // need - cntb + (collected keys at or above a0) of the collected ones, which
+  // counts the keys above b* that the window takes in.  A BIN_ALL row takes
+  // everything from a0 up unless a tie straddles a0: then it collects just the
+  // accumulators of a0's score.
   int any_collect = 0;
   if (lane < 32) {
     const int g = w + 4 * (lane >> 4), r = lane & 15;
@@ -1913,9 +1974,16 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
     float t0 = -INFINITY, t1 = -INFINITY;
     if (ri.mode != SELECT_ALL) {
       const float lo_b = ri.bstar > 0 ? bin_lower_edge(ri.bstar, ri.iw, ri.bc) : -INFINITY;
-      const float hi_b = ri.bstar < NBIN - 1 ? bin_lower_edge(ri.bstar + 1, ri.iw, ri.bc) : INFINITY;
-      if (ri.mode == BIN_ALL) { t0 = lo_b; t1 = lo_b; }
-      else { t0 = lo_b; t1 = hi_b; }   // COLLECT
+      const float lo_w = acc_lo_of(lo_b, mscale);
+      ra0[g][r] = lo_b;
+      if (ri.mode == BIN_ALL) {
+        if (lo_w == lo_b) { t0 = lo_b; t1 = lo_b; }   // no tie below a0: s >= score1(a0) selects
+        else { ri.mode = COLLECT; t0 = lo_w; t1 = acc_hi_of(lo_b, mscale); }
+      } else {   // COLLECT
+        t0 = lo_w;
+        t1 = ri.bstar < NBIN - 1 ? acc_hi_of(next_down(bin_lower_edge(ri.bstar + 1, ri.iw, ri.bc)), mscale)
+                                 : INFINITY;
+      }
     }
     ri.th0 = t0; ri.th1 = t1;
     rinfo[g][r] = ri;
@@ -1926,16 +1994,15 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
   const long srowb = (long)bh * Tq + r0;   // global row of the block's row 0
   bool full_col = false;   // pass B: a candidate found no room in its lane's staging column
   if (__syncthreads_or(any_collect)) {
-    // candidate of row 16g + lr: th0 <= s < th1, i.e. med3(s, lo, hi) == s with
-    // lo = th0, hi = the float below th1; rows that collect nothing take
-    // lo = hi = +inf, which no finite score matches
+    // candidate of row 16g + lr: th0 <= acc <= th1, i.e. med3(acc, th0, th1) == acc;
+    // rows that collect nothing take +inf, +inf, which no finite accumulator matches
     float tlo[NG], thi[NG];
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
       const RowInfo ri = rinfo[g][lr];
       const bool col = r0 + 16 * g + lr < Tq && ri.mode == COLLECT;
       tlo[g] = col ? ri.th0 : INFINITY;
-      thi[g] = col ? next_down(ri.th1) : INFINITY;
+      thi[g] = col ? ri.th1 : INFINITY;
     }
     // Candidates are staged in LDS, each lane in a column of its own (entry r of
     // lane l at 64 r + l, 32 entries: the histogram area is free, 32 of its
@@ -1944,12 +2011,12 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
     // after a tile that leaves some lane of the wave holding 16 or more, and
     // after the sweep.  (Flushing every tile put the stores ahead of the next
     // tile's K loads in the memory counter the loads are waited on.)  A tile
-    // starts with at most 15 entries per lane; a lane that still runs out of room
-    // (more than 16 of its 32 scores of one tile in threshold bins) sends the
-    // block to the radix fallback, like an overflowing bin.  Entry: {score bits,
-    // g << 16 | key}: the row is 16g + lr of the lane that staged and flushes it;
-    // keys fit 16 bits (Tk <= 65535 on this path).
-    uint2* ebuf = reinterpret_cast<uint2*>(&hist[32 * w][0]);
+    // starts with at most 15 entries per lane; a lane that reaches 32 (17 or more
+    // of its 32 scores of one tile in the window) sends the block to the radix
+    // fallback, like an overflowing bin.  Entry: {accumulator
+    // bits, g << 16 | key}: the row is 16g + lr of the lane that staged and flushes
+    // it; keys fit 16 bits (Tk <= 65535 on this path).
+    uint2* ebuf = reinterpret_cast<uint2*>(&hist[0][0] + 4096 * w);
     uint32_t* rowcnt = reinterpret_cast<uint32_t*>(&colcnt[0][0]);   // row 16g + lr at 16g + lr
     uint32_t kc = 0;   // this lane's staged entries
     auto flush = [&]() __attribute__((always_inline)) {
@@ -1965,22 +2032,21 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
           if (r0e + u < kc) slot[u] = atomicAdd(rowcnt + 16 * (e[u].y >> 16) + lr, 1u);
 #pragma unroll
         for (int u = 0; u < 4; ++u)
-          if (r0e + u < kc && slot[u] < (uint32_t)TOPK_CAP)
+          if (r0e + u < kc && slot[u] < (uint32_t)TOPK_CAP && r0 + 16 * (int)(e[u].y >> 16) + lr < Tq)
             scratch[(srowb + 16 * (e[u].y >> 16) + lr) * TOPK_CAP + slot[u]] = make_uint2(e[u].x, e[u].y & 0xffffu);
       }
       wave_lds_sync();   // reads done before the buffer is written again
       kc = 0;
     };
     sweep([&](int kt, f4* acc) __attribute__((always_inline)) {
-      // Where any lane of the wave has a candidate, every lane with room writes
-      // its entry at its next position and only candidates keep theirs (advance
-      // kc): the others are overwritten or lie past kc.
+      // Where any lane of the wave has a candidate, every lane writes its entry
+      // at its next position, min(kc, 31), and only candidates keep theirs
+      // (advance kc): the others are overwritten or lie past kc.  kc >= 32 after
+      // the tile means an entry was lost (position 31 written again).
       auto stage = [&](bool cand, int g, float sc, int j) __attribute__((always_inline)) {
         if (ballot64(cand) != 0ull) {
-          const bool room = kc < 32u;
-          if (room) ebuf[64 * kc + lane] = make_uint2(__float_as_uint(sc), ((uint32_t)g << 16) | (uint32_t)j);
-          full_col |= cand & !room;
-          kc += (cand & room) ? 1u : 0u;
+          ebuf[64 * min(kc, 31u) + lane] = make_uint2(__float_as_uint(sc), ((uint32_t)g << 16) | (uint32_t)j);
+          kc += cand ? 1u : 0u;
         }
       };
       if ((kt + 1) * KT <= minvalid) {
@@ -2004,6 +2070,11 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
           }
         }
       }
+      // Positions 0..30 only ever hold candidates; position 31 may hold a later
+      // non-candidate entry once the column is full, so a full lane (block flagged
+      // for the fallback) flushes 31.
+      full_col |= kc >= 32u;
+      kc = min(kc, 31u);
       if (ballot64(kc >= 16u) != 0ull) flush();
     });
     if (ballot64(kc != 0u) != 0ull) flush();
@@ -2015,39 +2086,62 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
     }
     return;
   }
-  __syncthreads();   // candidates and counters of every wave are in place; hist is the resolve's area
+  // A window wider than b* (ties across its edges) can exceed the scratch list.
+  int over = 0;
+  if (lane < 32) {
+    const int g = w + 4 * (lane >> 4), r = lane & 15;
+    over = rinfo[g][r].mode == COLLECT && colcnt[g][r] > TOPK_CAP;
+  }
+  // (also the barrier after which candidates and counters of every wave are in
+  // place and hist is the resolve's area)
+  if (__syncthreads_or(over)) {
+    if (tid < 2) {
+      const int q64 = 2 * qb + tid;
+      if (q64 < nqb) a.flags[(long)(nqb - 1 - q64) * BH + bh] = 1;
+    }
+    return;
+  }
 
   // ---- resolve: the exact cut of every COLLECT row of the wave --------------
-  uint32_t* h256 = &hist[32 * w][0];   // 256 words of the wave's own rows
+  uint32_t* h256 = &hist[0][0] + 4096 * w;   // 256 words of the wave's own staging area
   float thv = -INFINITY;   // lane rr < 32: row (group w + 4 (rr / 16), rr % 16)
   int cutv = 0x7fffffff;
   for (int rr = 0; rr < 32; ++rr) {
     const int g = w + 4 * (rr >> 4), r = rr & 15;
     const RowInfo ri = rinfo[g][r];
-    if (ri.mode == BIN_ALL && lane == rr) thv = ri.th0;   // everything from the bin's lower edge up
+    if (ri.mode == BIN_ALL && lane == rr) thv = score1(ri.th0, mscale);   // everything from a0's score up
     if (ri.mode != COLLECT) continue;
     const long row = srowb + 16 * g + r;
     const int n = min(colcnt[g][r], TOPK_CAP);
     uint32_t key[CAPL];
     int idx[CAPL];
+    uint32_t nin = 0;   // collected keys at or above a0
 #pragma unroll
     for (int m = 0; m < CAPL; ++m) {
       const int p = 64 * m + lane;
       key[m] = 0; idx[m] = 0;
+      float x = -INFINITY;
       if (p < n) {
         const uint2 v = scratch[row * TOPK_CAP + p];
-        key[m] = f32_order_key(__uint_as_float(v.x));
+        x = __uint_as_float(v.x);
+        key[m] = f32_order_key(score1(x, mscale));
         idx[m] = (int)v.y;
       }
+      nin += (uint32_t)__popcll(ballot64(p < n && x >= ra0[g][r]));
     }
-    // every collected key lies in [key(th0), key(th1) - 1]: the bytes those two
-    // share are the same for all of them and need no pass
-    const uint32_t klo = f32_order_key(ri.th0), dif = klo ^ (f32_order_key(ri.th1) - 1u);
+    uint32_t rneed = (uint32_t)(ri.need - rcntb[g][r]) + nin;
+    if (rneed == 0u) {   // none of the window's keys (all tied at a0's score): s > score1(th1)
+      if (lane == rr) thv = next_up(score1(ri.th1, mscale));
+      continue;
+    }
+    // every collected key lies in [key(score1(th0)), key(score1(th1))]: the bytes
+    // those two share are the same for all of them and need no pass
+    const uint32_t klo = f32_order_key(score1(ri.th0, mscale));
+    const uint32_t dif = klo ^ f32_order_key(score1(ri.th1, mscale));
     uint32_t rm = 0;
     int sh = 24;
     while (sh > 0 && (dif >> sh) == 0u) { rm |= 0xffu << sh; sh -= 8; }
     uint32_t rp = klo & rm;
-    uint32_t rneed = (uint32_t)ri.need;
     for (; sh >= 0; sh -= 8) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) h256[4 * lane + q] = 0;
@@ -2116,8 +2210,9 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
       a.thr[rowg] = make_uint2(__float_as_uint(thv), (uint32_t)cutv);
       if (a.counts) a.counts[rowg] = min(topk, nv);
       if (a.split) a.split[rowg] = 0;
-      a.top2[2 * rowg] = t2.x;
-      a.top2[2 * rowg + 1] = t2.y;
+      // scores of the top-2 accumulators (score1 is monotone); -FLT_MAX marks "none"
+      a.top2[2 * rowg] = t2.x == -FLT_MAX ? -FLT_MAX : score1(t2.x, mscale);
+      a.top2[2 * rowg + 1] = t2.y == -FLT_MAX ? -FLT_MAX : score1(t2.y, mscale);
     }
   }
 }
@@ -2169,7 +2264,7 @@ hipError_t launch_score_topk(const TopkArgs& a0, hipStream_t st) {
   const bool t2 = a.top2 != nullptr;
   if (a.thr != nullptr) {   // layer path, threshold mode (bf16, D = 128, top-2 required)
     if (a.dtype != DT_BF16 || !t2 || a.D != DP) return hipErrorInvalidValue;
-    if (c16) {
+    if (c16 && ms > 0.f && ms < FLT_MAX) {   // score_thr128_kernel bins accumulators: needs mscale > 0
       const dim3 grid128((unsigned)(BH * ((a.Tq + 127) / 128)));
       score_thr128_kernel<<<grid128, 256, 0, st>>>(a, nqb, ms);
       score_topk_kernel<bf16_t, false, true, true, true, true, true><<<grid, 256, 0, st>>>(a, nqb, ms);

@@ -6,8 +6,9 @@ and applies it.
   of K1's own fp32 scores, checked against the oracle elsewhere), applied to
   the scores sgsa_score_dump returns -- on random, tied, mass-tied (radix
   fallback blocks), bursts of tied keys (the 128-row kernel's candidate
-  staging overflows and the block goes to the fallback) and heavy-tailed
-  inputs and a ragged shape.
+  staging overflows and the block goes to the fallback), score ties between
+  different accumulators across the 128-row kernel's bin edges (it bins raw
+  accumulators) and heavy-tailed inputs and a ragged shape.
 * K2's selection, key for key: the known-answer variant of the threshold
   gather reports each row's {count, index sum, index hash xor} of the keys it
   weighs, which must equal those of the row lists exactly.
@@ -54,6 +55,18 @@ def _inputs(case, dev, big=False):
         kk = 0.05 * torch.randn(B, T, H, D, generator=g)
         kk[:, is_a] = A
         q = A + 0.01 * torch.randn(B, T, H, D, generator=g)
+    elif case == "straddle":
+        # Every query is (1, 1, 0, ..), every key (1.5, m 2^-23, 0, ..) with m < 256:
+        # accumulators 1.5 + m 2^-23, consecutive fp32 values, which the score scale
+        # 1/sqrt(128) maps two to one score about a third of the time.  Ties by score
+        # then span different accumulators, and the bins (fitted to this narrow
+        # range, about 1.5 accumulator steps wide) put edges between them.
+        q = torch.zeros(B, T, H, D)
+        q[..., 0] = 1.0
+        q[..., 1] = 1.0
+        kk = torch.zeros(B, T, H, D)
+        kk[..., 0] = 1.5
+        kk[..., 1] = torch.randint(0, 256, (B, T, H), generator=g).float() * 2.0 ** -23
     elif case == "heavy_tail":
         x = O.make_inputs(B, T, H, D, dtype=torch.float32, seed=12, heavy_tail=True, with_budget=False)
         q, kk = x["q"], x["k_ret"]
@@ -66,7 +79,7 @@ def _inputs(case, dev, big=False):
     return cast(q), cast(kk), cast(v), bud.to(dev), k
 
 
-CASES = ["random", "ties", "mass_ties", "tile_burst", "heavy_tail", "ragged"]
+CASES = ["random", "ties", "mass_ties", "tile_burst", "straddle", "heavy_tail", "ragged"]
 # (case, big): every case at its own size, and all but tile_burst (a fixed T = 500
 # construction) at top-k 2048 with T = 8192
 SIZED = [(c, False) for c in CASES] + [(c, True) for c in CASES if c != "tile_burst"]
@@ -97,7 +110,7 @@ def test_thresholds_select_exactly_the_row_lists(dev, case, big):
     bi, hi, ri, si = live.nonzero(as_tuple=True)
     ref[bi, hi, ri, ic[bi, hi, ri, si]] = True
     assert torch.equal(mask, ref), f"selected sets differ in {(mask != ref).sum().item()} (row, key) pairs"
-    if case in ("ties", "mass_ties", "tile_burst"):
+    if case in ("ties", "mass_ties", "tile_burst", "straddle"):
         assert (thr[..., 1] != 0x7fffffff).any(), "no row needed a tie cut"
 
 
