@@ -1716,30 +1716,46 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
   // and no select on the loaded data keeps the compiler from waiting for the
   // prefetch right after issuing it.
   const int krow = (lr >> 2) + 4 * (lr & 3);
-  bf16x8 kf[4];
-  auto kload = [&](int kt) __attribute__((always_inline)) {
+  bf16x8 kf[2][4];   // the sweeps: tiles of even / odd index, each loaded two tiles ahead
+  auto kload = [&](bf16x8 (&dst)[4], int kt) __attribute__((always_inline)) {
     const int j = kt * KT + 16 * w + krow;
     const uint16_t* p = kb + ((long)(b * Tk + (j < Tk ? j : 0)) * H + h) * DP + 8 * lg;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) kf[s] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8*>(p + 32 * s));
+    for (int s = 0; s < 4; ++s) dst[s] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8*>(p + 32 * s));
   };
-  // fn(kt, acc): acc[g][i] = the raw accumulator of row r0 + 16g + lr against key
-  // kt*64 + 16w + lg + 4i; its score is score1(acc, mscale), non-decreasing in
-  // acc (mscale > 0), so both sweeps bin and test accumulators.
-  auto sweep = [&](auto&& fn) __attribute__((always_inline)) {
-    if (ntile > 0) kload(0);
-    for (int kt = 0; kt < ntile; ++kt) {
-      f4 acc[NG];
+  // fn(kt, g0, acc): acc[gg][i] = the raw accumulator of row r0 + 16 (g0 + gg) + lr
+  // against key kt*64 + 16w + lg + 4i, for the row groups g0 = 0 and then g0 = 4
+  // of tile kt; its score is score1(acc, mscale), non-decreasing in acc (mscale >
+  // 0), so both sweeps bin and test accumulators.  Half the groups at a time keeps
+  // 16 accumulator VGPRs live instead of 32, which pays for the second K buffer:
+  // a tile's fragments are loaded while the two tiles before it are processed.
+  // fn's last argument is std::true_type in tiles whose keys are valid for every
+  // row of the wave (kt < minvalid / 64: no per-key tests), std::false_type
+  // otherwise; the test is made once per tile, so a full tile is straight-line code.
+  auto tile = [&](bf16x8 (&kfc)[4], int kt, auto&& fn) __attribute__((always_inline)) {
+    auto body = [&](auto full) __attribute__((always_inline)) {
 #pragma unroll
-      for (int g = 0; g < NG; ++g) {
-        f4 c = f4_zero();
+      for (int hh = 0; hh < 2; ++hh) {
+        f4 acc[NG / 2];
 #pragma unroll
-        for (int s = 0; s < 4; ++s) c = mma_bf16(kf[s], qf[g][s], c);
-        acc[g] = c;
+        for (int gg = 0; gg < NG / 2; ++gg) {
+          f4 c = f4_zero();
+#pragma unroll
+          for (int s = 0; s < 4; ++s) c = mma_bf16(kfc[s], qf[NG / 2 * hh + gg][s], c);
+          acc[gg] = c;
+        }
+        // unconditional (the last tile reloads tile ntile - 1): with a conditional
+        // load the compiler waits for every load in flight at the top of a tile
+        if (hh == 1) kload(kfc, min(kt + 1, ntile - 1));
+        fn(kt, NG / 2 * hh, acc, full);
       }
-      if (kt + 1 < ntile) kload(kt + 1);
-      fn(kt, acc);
-    }
+    };
+    if ((kt + 1) * KT <= minvalid) body(std::true_type{});
+    else body(std::false_type{});
+  };
+  auto sweep = [&](auto&& fn) __attribute__((always_inline)) {
+    if (ntile > 0) kload(kf[0], 0);
+    for (int kt = 0; kt < ntile; ++kt) tile(kf[0], kt, fn);
   };
 
   // row set-up (wave w: rows of groups w and w + 4; lane < 32 -> group w + 4 (lane / 16), row lane % 16)
@@ -1781,12 +1797,12 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
     const int ns = min(ntile, NS);
     for (int t = 0; t < ns; ++t) {
       const int kt = (int)(((long)t * ntile) / ns);
-      kload(kt);
+      kload(kf[0], kt);
 #pragma unroll
       for (int g = 0; g < NG; ++g) {
         f4 c = f4_zero();
 #pragma unroll
-        for (int s = 0; s < 4; ++s) c = mma_bf16(kf[s], qf[g][s], c);
+        for (int s = 0; s < 4; ++s) c = mma_bf16(kf[0][s], qf[g][s], c);
         const f4 sc = c;
         const int nv = nv_of(g);
 #pragma unroll
@@ -1868,26 +1884,30 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
     // Every block has a live row: the sweep gives the top-2 even where no row
     // needs a histogram.  In full tiles every row's histogram takes the adds
     // (rows that need none -- past Tq, or taking all their keys -- own rows
-    // nobody reads), so the adds need no per-row branch.
-    sweep([&](int kt, f4* acc) __attribute__((always_inline)) {
-      if ((kt + 1) * KT <= minvalid) {
+    // nobody reads), so the adds need no branch, not even in blocks where no
+    // row needs a histogram: a branch per score would split the tile into basic
+    // blocks the compiler cannot interleave with the next MFMAs.
+    sweep([&](int kt, int g0, f4* acc, auto full) __attribute__((always_inline)) {
+      if constexpr (decltype(full)::value) {
 #pragma unroll
-        for (int g = 0; g < NG; ++g) {
+        for (int gg = 0; gg < NG / 2; ++gg) {
+          const int g = g0 + gg;
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            top2(g, acc[g][i]);
-            if (any_hist) bump(g, score_bin_bits(acc[g][i], iw[g], bc[g]));
+            top2(g, acc[gg][i]);
+            bump(g, score_bin_bits(acc[gg][i], iw[g], bc[g]));
           }
         }
       } else {
 #pragma unroll
-        for (int g = 0; g < NG; ++g) {
+        for (int gg = 0; gg < NG / 2; ++gg) {
+          const int g = g0 + gg;
           const int nv = nv_of(g);   // 0 for rows past Tq
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int j = kt * KT + 16 * w + lg + 4 * i;
-            top2(g, j < nv ? acc[g][i] : -FLT_MAX);
-            if (((hmask >> g) & 1u) && j < nv) bump(g, score_bin_bits(acc[g][i], iw[g], bc[g]));
+            top2(g, j < nv ? acc[gg][i] : -FLT_MAX);
+            if (((hmask >> g) & 1u) && j < nv) bump(g, score_bin_bits(acc[gg][i], iw[g], bc[g]));
           }
         }
       }
@@ -2038,7 +2058,7 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
       wave_lds_sync();   // reads done before the buffer is written again
       kc = 0;
     };
-    sweep([&](int kt, f4* acc) __attribute__((always_inline)) {
+    sweep([&](int kt, int g0, f4* acc, auto full) __attribute__((always_inline)) {
       // Where any lane of the wave has a candidate, every lane writes its entry
       // at its next position, min(kc, 31), and only candidates keep theirs
       // (advance kc): the others are overwritten or lie past kc.  kc >= 32 after
@@ -2049,27 +2069,30 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
           kc += cand ? 1u : 0u;
         }
       };
-      if ((kt + 1) * KT <= minvalid) {
+      if constexpr (decltype(full)::value) {
 #pragma unroll
-        for (int g = 0; g < NG; ++g) {
+        for (int gg = 0; gg < NG / 2; ++gg) {
+          const int g = g0 + gg;
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const float sc = acc[g][i];
+            const float sc = acc[gg][i];
             stage(__builtin_amdgcn_fmed3f(sc, tlo[g], thi[g]) == sc, g, sc, kt * KT + 16 * w + lg + 4 * i);
           }
         }
       } else {
 #pragma unroll
-        for (int g = 0; g < NG; ++g) {
+        for (int gg = 0; gg < NG / 2; ++gg) {
+          const int g = g0 + gg;
           const int nv = nv_of(g);   // 0 for rows past Tq
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int j = kt * KT + 16 * w + lg + 4 * i;
-            const float sc = acc[g][i];
+            const float sc = acc[gg][i];
             stage((__builtin_amdgcn_fmed3f(sc, tlo[g], thi[g]) == sc) & (j < nv), g, sc, j);
           }
         }
       }
+      if (g0 == 0) return;   // the rest once per tile, after its second half
       // Positions 0..30 only ever hold candidates; position 31 may hold a later
       // non-candidate entry once the column is full, so a full lane (block flagged
       // for the fallback) flushes 31.
