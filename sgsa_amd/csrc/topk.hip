@@ -1674,24 +1674,29 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
     return qr < Tq ? nv : 0;
   };
 
-  // B operand: q^T of the block's rows; lane holds row r0 + 16g + lr, dims 32s + 8lg + [0, 8)
+  // B operand: q^T of the block's rows; lane holds row r0 + 16g + lr, dims 32s + 8lg + [0, 8).
+  // All loads first, the norms after.  Rows past Tq load row 0 of the head: their
+  // scores, bins and norms are never used (no output, no histogram or candidate
+  // that anyone reads, no sample range: nv = 0).
   bf16x8 qf[NG][4];
 #pragma unroll
   for (int g = 0; g < NG; ++g) {
     const int qr = r0 + 16 * g + lr;
     const uint16_t* qp = reinterpret_cast<const uint16_t*>(a.q) + ((long)(b * Tq + (qr < Tq ? qr : 0)) * H + h) * DP;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) qf[g][s] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8*>(qp + 32 * s + 8 * lg));
+  }
+#pragma unroll
+  for (int g = 0; g < NG; ++g) {
     float qn2 = 0.f;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      u16x8 raw;
-      if (qr < Tq) raw = *reinterpret_cast<const u16x8*>(qp + 32 * s + 8 * lg);
-      else raw = (u16x8){0, 0, 0, 0, 0, 0, 0, 0};
+      const u16x8 raw = __builtin_bit_cast(u16x8, qf[g][s]);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const float x = bf16_to_f32(raw[j]);
         qn2 = fmaf(x, x, qn2);
       }
-      qf[g][s] = __builtin_bit_cast(bf16x8, raw);
     }
     qn2 += __shfl_xor(qn2, 16, 64);
     qn2 += __shfl_xor(qn2, 32, 64);
@@ -1716,7 +1721,7 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
   // and no select on the loaded data keeps the compiler from waiting for the
   // prefetch right after issuing it.
   const int krow = (lr >> 2) + 4 * (lr & 3);
-  bf16x8 kf[2][4];   // the sweeps: tiles of even / odd index, each loaded two tiles ahead
+  bf16x8 kf[1][4];   // the next tile's fragments, loaded while the current one is processed
   auto kload = [&](bf16x8 (&dst)[4], int kt) __attribute__((always_inline)) {
     const int j = kt * KT + 16 * w + krow;
     const uint16_t* p = kb + ((long)(b * Tk + (j < Tk ? j : 0)) * H + h) * DP + 8 * lg;
@@ -1727,8 +1732,7 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
   // against key kt*64 + 16w + lg + 4i, for the row groups g0 = 0 and then g0 = 4
   // of tile kt; its score is score1(acc, mscale), non-decreasing in acc (mscale >
   // 0), so both sweeps bin and test accumulators.  Half the groups at a time keeps
-  // 16 accumulator VGPRs live instead of 32, which pays for the second K buffer:
-  // a tile's fragments are loaded while the two tiles before it are processed.
+  // 16 accumulator VGPRs live instead of 32.
   // fn's last argument is std::true_type in tiles whose keys are valid for every
   // row of the wave (kt < minvalid / 64: no per-key tests), std::false_type
   // otherwise; the test is made once per tile, so a full tile is straight-line code.
@@ -1795,14 +1799,20 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
 #pragma unroll
     for (int g = 0; g < NG; ++g) { lo[g] = FLT_MAX; hi[g] = -FLT_MAX; }
     const int ns = min(ntile, NS);
-    for (int t = 0; t < ns; ++t) {
-      const int kt = (int)(((long)t * ntile) / ns);
-      kload(kf[0], kt);
+    // sample tile t's fragments in ks[t & 1], the next one's loaded meanwhile
+    auto sample_kt = [&](int t) __attribute__((always_inline)) { return (int)(((long)min(t, ns - 1) * ntile) / ns); };
+    bf16x8 ks[2][4];
+    if (ns > 0) kload(ks[0], sample_kt(0));
+#pragma unroll
+    for (int t = 0; t < NS; ++t) {
+      if (t >= ns) break;   // uniform
+      const int kt = sample_kt(t);
+      kload(ks[(t + 1) & 1], sample_kt(t + 1));
 #pragma unroll
       for (int g = 0; g < NG; ++g) {
         f4 c = f4_zero();
 #pragma unroll
-        for (int s = 0; s < 4; ++s) c = mma_bf16(kf[0][s], qf[g][s], c);
+        for (int s = 0; s < 4; ++s) c = mma_bf16(ks[t & 1][s], qf[g][s], c);
         const f4 sc = c;
         const int nv = nv_of(g);
 #pragma unroll
