@@ -2139,12 +2139,31 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
   uint32_t* h256 = &hist[0][0] + 4096 * w;   // 256 words of the wave's own staging area
   float thv = -INFINITY;   // lane rr < 32: row (group w + 4 (rr / 16), rr % 16)
   int cutv = 0x7fffffff;
-  for (int rr = 0; rr < 32; ++rr) {
+  // The wave's COLLECT rows (bit rr), resolved in turn; each row's candidates
+  // are loaded while the row before it is resolved.  All CAPL loads of a row are
+  // issued (slots past its count re-read slot 0, which every COLLECT row has), so
+  // the number of loads in flight is the same on every path.
+  uint32_t cmask = 0;
+  if (lane < 32) {
+    const RowInfo ri = rinfo[w + 4 * (lane >> 4)][lane & 15];
+    if (ri.mode == BIN_ALL) thv = score1(ri.th0, mscale);   // everything from a0's score up
+    cmask = ri.mode == COLLECT;
+  }
+  cmask = (uint32_t)ballot64(cmask != 0u);
+  auto load_row = [&](int rr, uint2 (&buf)[CAPL]) __attribute__((always_inline)) {
+    const int g = w + 4 * (rr >> 4), r = rr & 15;
+    const long row = srowb + 16 * g + r;
+    const int n = min(colcnt[g][r], TOPK_CAP);
+#pragma unroll
+    for (int m = 0; m < CAPL; ++m) {
+      const int p = 64 * m + lane;
+      buf[m] = scratch[row * TOPK_CAP + (p < n ? p : 0)];
+    }
+  };
+  uint2 cbA[CAPL], cbB[CAPL];
+  auto resolve_row = [&](int rr, const uint2 (&cb)[CAPL]) __attribute__((always_inline)) {
     const int g = w + 4 * (rr >> 4), r = rr & 15;
     const RowInfo ri = rinfo[g][r];
-    if (ri.mode == BIN_ALL && lane == rr) thv = score1(ri.th0, mscale);   // everything from a0's score up
-    if (ri.mode != COLLECT) continue;
-    const long row = srowb + 16 * g + r;
     const int n = min(colcnt[g][r], TOPK_CAP);
     uint32_t key[CAPL];
     int idx[CAPL];
@@ -2155,17 +2174,16 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
       key[m] = 0; idx[m] = 0;
       float x = -INFINITY;
       if (p < n) {
-        const uint2 v = scratch[row * TOPK_CAP + p];
-        x = __uint_as_float(v.x);
+        x = __uint_as_float(cb[m].x);
         key[m] = f32_order_key(score1(x, mscale));
-        idx[m] = (int)v.y;
+        idx[m] = (int)cb[m].y;
       }
       nin += (uint32_t)__popcll(ballot64(p < n && x >= ra0[g][r]));
     }
     uint32_t rneed = (uint32_t)(ri.need - rcntb[g][r]) + nin;
     if (rneed == 0u) {   // none of the window's keys (all tied at a0's score): s > score1(th1)
       if (lane == rr) thv = next_up(score1(ri.th1, mscale));
-      continue;
+      return;
     }
     // every collected key lies in [key(score1(th0)), key(score1(th1))]: the bytes
     // those two share are the same for all of them and need no pass
@@ -2233,6 +2251,21 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
       thv = threshold_of_key(rp);
       cutv = neq > rneed ? (int)~ip : 0x7fffffff;
     }
+  };
+  // Two buffers in turn.  The prefetch is unconditional (with no next row it
+  // reloads the current one): a conditional load would make the compiler wait for
+  // both buffers before using the first.
+  if (cmask != 0u) load_row(__builtin_ctz(cmask), cbA);
+  while (cmask != 0u) {
+    const int ra = __builtin_ctz(cmask);
+    cmask &= cmask - 1u;
+    load_row(cmask != 0u ? __builtin_ctz(cmask) : ra, cbB);
+    resolve_row(ra, cbA);
+    if (cmask == 0u) break;
+    const int rb = __builtin_ctz(cmask);
+    cmask &= cmask - 1u;
+    load_row(cmask != 0u ? __builtin_ctz(cmask) : rb, cbA);
+    resolve_row(rb, cbB);
   }
   if (lane < 32) {
     const int g = w + 4 * (lane >> 4), r = lane & 15;
