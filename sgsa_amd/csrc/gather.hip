@@ -63,6 +63,22 @@ __device__ __forceinline__ void load_row(const X* __restrict__ base, long rowoff
   }
 }
 
+// The elements of one 16-byte piece of a row, as load_row<X, true> reads them.
+template <typename X>
+__device__ __forceinline__ void unpack_row(const uint4 raw, float (&x)[16 / (int)sizeof(X)]) {
+  if constexpr (sizeof(X) == 2) {
+    const uint32_t u[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[2 * i] = __uint_as_float(u[i] << 16);
+      x[2 * i + 1] = __uint_as_float(u[i] & 0xffff0000u);
+    }
+  } else {
+    x[0] = __uint_as_float(raw.x); x[1] = __uint_as_float(raw.y);
+    x[2] = __uint_as_float(raw.z); x[3] = __uint_as_float(raw.w);
+  }
+}
+
 template <typename X, bool VEC>
 __device__ __forceinline__ int elem_d(int sub, int m, int lpr) {
   return VEC ? sub * GatherShape<X, VEC>::NE + m : sub + lpr * m;
@@ -73,6 +89,75 @@ __device__ __forceinline__ int elem_d(int sub, int m, int lpr) {
 // Element offset of key / value row j of (b, h): [B,Tk,H,D] or, with kv_hm, [B,H,Tk,D].
 __device__ __forceinline__ long kv_row_offset(const GatherArgs& a, int b, int h, int j) {
   return a.kv_hm ? (((long)b * a.H + h) * a.Tk + j) * a.D : (((long)b * a.Tk + j) * a.H + h) * a.D;
+}
+
+// Adds slots [base, base + nstep) of a row (their key indices in lane j, weights
+// in wgt, lane order) into ak / av: the lane group grp takes slots it, it + 1, ..
+// of each step of rpi = 64 / lpr.
+template <typename X, bool VEC>
+__device__ __forceinline__ void gather_step(const GatherArgs& a, int j, float wgt, int nstep, const X* K, const X* V,
+                                            int b, int h, int grp, int sub, int lpr,
+                                            float (&ak)[GatherShape<X, VEC>::NE],
+                                            float (&av)[GatherShape<X, VEC>::NE]) {
+  constexpr int NE = GatherShape<X, VEC>::NE;
+  const int D = a.D;
+  const int rpi = 64 / lpr;
+  if constexpr (VEC) {
+    // U slots per lane group at a time: every load issued before any is used
+    // (no branch around them, so the compiler keeps them all in flight).
+    // Slots past the step read slot 0's row (index 0 past kq) with weight 0;
+    // lanes past D read dims from 0 and weigh them 0.
+    constexpr int U = 4;
+    const int d0 = sub * NE < D ? sub * NE : 0;
+    const float lw = sub * NE < D ? 1.f : 0.f;
+    for (int it0 = 0; it0 * rpi < nstep; it0 += U) {
+      uint4 rk[U], rv[U];
+      float wv[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int src = (it0 + u) * rpi + grp;
+        const int jj = __shfl(j, src & 63, 64);
+        const float ww = __shfl(wgt, src & 63, 64);
+        wv[u] = src < nstep ? ww * lw : 0.f;
+        const long off = kv_row_offset(a, b, h, src < nstep ? jj : 0) + d0;
+        rv[u] = *reinterpret_cast<const uint4*>(V + off);
+        if (K) rk[u] = *reinterpret_cast<const uint4*>(K + off);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        float xv[NE];
+        unpack_row<X>(rv[u], xv);
+#pragma unroll
+        for (int i = 0; i < NE; ++i) av[i] += wv[u] * xv[i];
+        if (K) {
+          float xk[NE];
+          unpack_row<X>(rk[u], xk);
+#pragma unroll
+          for (int i = 0; i < NE; ++i) ak[i] += wv[u] * xk[i];
+        }
+      }
+    }
+  } else {
+#pragma unroll 4
+    for (int it = 0; it * rpi < nstep; ++it) {
+      const int src = it * rpi + grp;
+      const int jj = __shfl(j, src, 64);
+      const float ww = __shfl(wgt, src, 64);
+      if (src < nstep && ww != 0.f) {
+        const long off = kv_row_offset(a, b, h, jj);
+        float xv[NE];
+        load_row<X, VEC>(V, off, sub, D, lpr, xv);
+        if (K) {
+          float xk[NE];
+          load_row<X, VEC>(K, off, sub, D, lpr, xk);
+#pragma unroll
+          for (int i = 0; i < NE; ++i) ak[i] += ww * xk[i];
+        }
+#pragma unroll
+        for (int i = 0; i < NE; ++i) av[i] += ww * xv[i];
+      }
+    }
+  }
 }
 
 // Accumulates slots [s0, s1) of one row into (ak, av, esum) with weights
@@ -87,8 +172,6 @@ __device__ __forceinline__ void gather_slots(const GatherArgs& a, int s0, int s1
                                              float (&av)[GatherShape<X, VEC>::NE]) {
   constexpr int NE = GatherShape<X, VEC>::NE;
   const int lane = threadIdx.x & 63;
-  const int D = a.D;
-  const int rpi = 64 / lpr;
   for (int base = s0; base < s1; base += 64) {
     const int slot = base + lane;
     int j = 0;
@@ -115,25 +198,7 @@ __device__ __forceinline__ void gather_slots(const GatherArgs& a, int s0, int s1
     const float wgt = sc == -INFINITY ? 0.f : __expf(sc - mrun);
     esum += wgt;
     const int nstep = min(64, s1 - base);
-#pragma unroll 4
-    for (int it = 0; it * rpi < nstep; ++it) {
-      const int src = it * rpi + grp;
-      const int jj = __shfl(j, src, 64);
-      const float ww = __shfl(wgt, src, 64);
-      if (src < nstep && ww != 0.f) {
-        const long off = kv_row_offset(a, b, h, jj);
-        float xv[NE];
-        load_row<X, VEC>(V, off, sub, D, lpr, xv);
-        if (K) {
-          float xk[NE];
-          load_row<X, VEC>(K, off, sub, D, lpr, xk);
-#pragma unroll
-          for (int i = 0; i < NE; ++i) ak[i] += ww * xk[i];
-        }
-#pragma unroll
-        for (int i = 0; i < NE; ++i) av[i] += ww * xv[i];
-      }
-    }
+    gather_step<X, VEC>(a, j, wgt, nstep, K, V, b, h, grp, sub, lpr, ak, av);
   }
 }
 
@@ -149,7 +214,6 @@ __global__ __launch_bounds__(256) void sparse_gather_kernel(GatherArgs a, int lp
   const int b = bh / H, h = bh % H;
   const int pos = qr + a.q_offset;
   const int grp = lane / lpr, sub = lane % lpr;
-  const int rpi = 64 / lpr;    // key rows per step
 
   const int kq = a.counts[row];
   const bool fixed_max = a.top2 != nullptr;
@@ -193,25 +257,7 @@ __global__ __launch_bounds__(256) void sparse_gather_kernel(GatherArgs a, int lp
       const float wgt = sc == -INFINITY ? 0.f : __expf(sc - mrun);
       esum += wgt;
       const int nstep = min(64, kq - base);
-  #pragma unroll 4
-      for (int it = 0; it * rpi < nstep; ++it) {
-        const int src = it * rpi + grp;
-        const int jj = __shfl(j, src, 64);
-        const float ww = __shfl(wgt, src, 64);
-        if (src < nstep && ww != 0.f) {
-          const long off = kv_row_offset(a, b, h, jj);
-          float xv[NE];
-          load_row<X, VEC>(V, off, sub, D, lpr, xv);
-          if (K) {
-            float xk[NE];
-            load_row<X, VEC>(K, off, sub, D, lpr, xk);
-  #pragma unroll
-            for (int i = 0; i < NE; ++i) ak[i] += ww * xk[i];
-          }
-  #pragma unroll
-          for (int i = 0; i < NE; ++i) av[i] += ww * xv[i];
-        }
-      }
+      gather_step<X, VEC>(a, j, wgt, nstep, K, V, b, h, grp, sub, lpr, ak, av);
     }
   } else {
     // merge the row's partials (gather_part_kernel) in split order
