@@ -156,6 +156,55 @@ __device__ __forceinline__ void find_bin(const uint32_t (&c)[4], int lane, uint3
   cnt = (uint32_t)__builtin_amdgcn_readlane((int)ct, src);
 }
 
+
+// Inclusive prefix sum within each aligned group of 16 lanes (row_shr 1/2/4/8,
+// lanes past the row edge read 0).
+__device__ __forceinline__ uint32_t row16_incl_scan(uint32_t x) {
+  int v = (int)x;
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, true);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, true);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, true);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, true);
+  return (uint32_t)v;
+}
+// Sum over the aligned group of 16 lanes, in every lane of the group.
+__device__ __forceinline__ uint32_t row16_sum(uint32_t x, int lane) {
+  return (uint32_t)__shfl((int)row16_incl_scan(x), lane | 15, 64);
+}
+
+// find_bin for four independent histograms, one per group of 16 lanes: lane
+// 16s + u holds bins 255-16u .. 240-16u (descending) of group s, and need is the
+// group's.  Results are uniform within each group.
+__device__ __forceinline__ void find_bin16(const uint32_t (&c)[16], int lane, uint32_t need, int& bin,
+                                           uint32_t& above, uint32_t& cnt) {
+  const int u = lane & 15;
+  uint32_t loc = 0;
+#pragma unroll
+  for (int q = 0; q < 16; ++q) loc += c[q];
+  const uint32_t inc = row16_incl_scan(loc);
+  const uint32_t exc = inc - loc;
+  const bool hit = exc < need && need <= inc;
+  const uint32_t rowbits = (uint32_t)(ballot64(hit) >> (lane & 48)) & 0xffffu;
+  const int src = (lane & 48) + (rowbits ? (int)__builtin_ctz(rowbits) : 0);
+  int b = 0;
+  uint32_t ab = 0, ct = 0;
+  if (hit) {
+    uint32_t cum = exc;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      if (ct == 0 && cum + c[q] >= need) {
+        b = 255 - 16 * u - q;
+        ab = cum;
+        ct = c[q];
+      }
+      if (ct == 0) cum += c[q];
+    }
+  }
+  bin = __shfl(b, src, 64);
+  above = (uint32_t)__shfl((int)ab, src, 64);
+  cnt = (uint32_t)__shfl((int)ct, src, 64);
+}
+
 }  // namespace
 
 // Max |k_j| per (b,h): the denominator of the pass-A bin scale.  grid (B*H), 256 threads.
@@ -2150,6 +2199,144 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
     cmask = ri.mode == COLLECT;
   }
   cmask = (uint32_t)ballot64(cmask != 0u);
+  // Four rows at a time first: lanes 16s..16s+15 take the s-th of the four
+  // lowest rows left, lane u its candidates 16m + u (m < CAPQ), and each group
+  // runs the byte radix below on a 256-bin histogram of its own (words 256s.. of
+  // the wave's area).  Rows with more than 16 CAPQ candidates, and rows whose
+  // cut key is shared by more candidates than it takes (the index tie-break),
+  // stay in cmask for the one-row resolve.
+  {
+    constexpr int CAPQ = 16;
+    const int qs = lane >> 4, qu = lane & 15;
+    uint32_t big = 0;
+    if (lane < 32 && ((cmask >> lane) & 1u)) big = colcnt[w + 4 * (lane >> 4)][lane & 15] > 16 * CAPQ;
+    const uint32_t bigm = (uint32_t)ballot64(big != 0u);
+    uint32_t todo = cmask & ~bigm;
+    cmask &= bigm;
+    // A quad is four rows packed in bytes (row id, 0xff for none), wave-uniform;
+    // lanes of an empty group take group 0's row.
+    auto quad_rows = [&](uint32_t m) __attribute__((always_inline)) {
+      uint32_t rq = 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        rq |= (m != 0u ? (uint32_t)__builtin_ctz(m) : 0xffu) << (8 * q);
+        m &= m - 1u;
+      }
+      return rq;
+    };
+    auto load_quad = [&](uint32_t rq, uint2 (&buf)[CAPQ]) __attribute__((always_inline)) {
+      const uint32_t rsel = (rq >> (8 * qs)) & 0xffu;
+      const int rr = (int)(rsel != 0xffu ? rsel : rq & 0xffu);
+      const int g = w + 4 * (rr >> 4), r = rr & 15;
+      const long row = srowb + 16 * g + r;
+      const int n = min(colcnt[g][r], TOPK_CAP);
+#pragma unroll
+      for (int m = 0; m < CAPQ; ++m) {
+        const int p = 16 * m + qu;
+        buf[m] = scratch[row * TOPK_CAP + (p < n ? p : 0)];
+      }
+    };
+    uint32_t* hq = h256 + 256 * qs;
+    auto resolve_quad = [&](uint32_t rq, const uint2 (&cb)[CAPQ]) __attribute__((always_inline)) {
+      const uint32_t rsel = (rq >> (8 * qs)) & 0xffu;
+      const bool live = rsel != 0xffu;
+      const int rr = (int)(live ? rsel : rq & 0xffu);
+      const int g = w + 4 * (rr >> 4), r = rr & 15;
+      const RowInfo ri = rinfo[g][r];
+      const int n = live ? min(colcnt[g][r], TOPK_CAP) : 0;
+      const float a0 = ra0[g][r];
+      uint32_t key[CAPQ];
+      uint32_t nin = 0;   // collected keys at or above a0
+#pragma unroll
+      for (int m = 0; m < CAPQ; ++m) {
+        const bool ok = 16 * m + qu < n;
+        const float x = __uint_as_float(cb[m].x);
+        key[m] = ok ? f32_order_key(score1(x, mscale)) : 0u;
+        nin += (ok && x >= a0) ? 1u : 0u;
+      }
+      nin = row16_sum(nin, lane);
+      uint32_t rneed = (uint32_t)(ri.need - rcntb[g][r]) + nin;
+      float thq = -INFINITY;
+      bool done = !live, radix = false;
+      if (live && rneed == 0u) {   // none of the window's keys: s > score1(th1)
+        thq = next_up(score1(ri.th1, mscale));
+        done = true;
+      }
+      radix = !done;
+      // bytes that key(score1(th0)) and key(score1(th1)) share need no pass
+      const uint32_t klo = f32_order_key(score1(ri.th0, mscale));
+      const uint32_t dif = klo ^ f32_order_key(score1(ri.th1, mscale));
+      uint32_t rm = 0;
+      int sh = 24;
+      while (sh > 0 && (dif >> sh) == 0u) { rm |= 0xffu << sh; sh -= 8; }
+      uint32_t rp = klo & rm;
+      while (ballot64(!done) != 0ull) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) reinterpret_cast<uint4*>(hq)[4 * qu + q] = make_uint4(0u, 0u, 0u, 0u);
+        wave_lds_sync();
+#pragma unroll
+        for (int m = 0; m < CAPQ; ++m) {
+          if (!done && 16 * m + qu < n && (key[m] & rm) == rp) atomicAdd(&hq[(key[m] >> sh) & 255u], 1u);
+        }
+        wave_lds_sync();
+        uint32_t c[16];
+        {
+          const uint4* hr = reinterpret_cast<const uint4*>(hq + 240 - 16 * qu);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const uint4 v4 = hr[q];
+            c[15 - 4 * q] = v4.x; c[14 - 4 * q] = v4.y; c[13 - 4 * q] = v4.z; c[12 - 4 * q] = v4.w;
+          }
+        }
+        int bin;
+        uint32_t above, cnt;
+        find_bin16(c, lane, rneed, bin, above, cnt);
+        wave_lds_sync();   // counts read before the next pass clears them
+        if (!done) {
+          rp |= (uint32_t)bin << sh;
+          rm |= 0xffu << sh;
+          rneed -= above;
+          if (cnt == rneed) done = true;
+          else if ((sh -= 8) < 0) done = true;
+        }
+      }
+      uint32_t neq = 0;
+#pragma unroll
+      for (int m = 0; m < CAPQ; ++m) neq += (16 * m + qu < n && (key[m] & rm) == rp) ? 1u : 0u;
+      neq = row16_sum(neq, lane);
+      const bool tie = radix && neq > rneed;   // index tie-break: the one-row resolve
+      if (radix) thq = threshold_of_key(rp);
+      // results to lane rr (rows < 32 of this wave)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t rq_q = (rq >> (8 * q)) & 0xffu;
+        if (rq_q == 0xffu) continue;   // uniform
+        const float tq = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(thq), 16 * q));
+        const bool tie_q = __builtin_amdgcn_readlane((int)tie, 16 * q) != 0;
+        if (tie_q) cmask |= 1u << rq_q;
+        else if (lane == (int)rq_q) { thv = tq; cutv = 0x7fffffff; }
+      }
+    };
+    // two buffers in turn, the next quad's candidates loaded while one is resolved
+    auto drop4 = [](uint32_t m) __attribute__((always_inline)) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) m &= m - 1u;
+      return m;
+    };
+    uint2 qA[CAPQ], qB[CAPQ];
+    if (todo != 0u) load_quad(quad_rows(todo), qA);
+    while (todo != 0u) {
+      const uint32_t ra = quad_rows(todo);
+      todo = drop4(todo);
+      const uint32_t rb = todo != 0u ? quad_rows(todo) : ra;
+      load_quad(rb, qB);
+      resolve_quad(ra, qA);
+      if (todo == 0u) break;
+      todo = drop4(todo);
+      load_quad(todo != 0u ? quad_rows(todo) : rb, qA);
+      resolve_quad(rb, qB);
+    }
+  }
   auto load_row = [&](int rr, uint2 (&buf)[CAPL]) __attribute__((always_inline)) {
     const int g = w + 4 * (rr >> 4), r = rr & 15;
     const long row = srowb + 16 * g + r;
