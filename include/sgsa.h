@@ -320,6 +320,32 @@ int sgsa_rope_qk(int dtype, int B, int T, int Hq, int Hk, int D, int pos0, int t
 int sgsa_layer_gates(int dtype, long rows, int H, const void* logits, long row_stride, float* beta, float* gamma,
                      float* budget, void* stream);
 
+/* The hybrid decoder's dense GQA attention for one decode token per sequence
+ * (modelings/hybrid_dense_delta_topk.py:178-192 at q_len = 1, the query at
+ * position kend - 1): o = softmax(q K^T / sqrt(D)) V over cache rows
+ * [0, kend), with the reference's rounding points in bf16 (score product and
+ * its scaling rounded to bf16, softmax in fp32, probabilities rounded to bf16,
+ * fp32 accumulation with V).  q, out [B, H, 1, D]; k_cache, v_cache
+ * [B, Hkv, cache_len, D], all contiguous in dtype; D = 128, H / Hkv in
+ * {1, 2, 4, 8}.  Workspace from sgsa_decode_attention_workspace_size. */
+int sgsa_decode_attention_workspace_size(int dtype, int B, int H, int kend, size_t* bytes);
+int sgsa_decode_attention(int dtype, int B, int H, int Hkv, int D, const void* q, const void* k_cache,
+                          const void* v_cache, long cache_len, int kend, void* out, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
+/* One SGSA decode step's projections, split for the decode kernels: the
+ * strided views and casts of SGSABlock's projections and gates
+ * (modelings/modeling_sgsa.py:480-482, :543-544) and the KV-cache append of
+ * one token, in one launch.  Row b of proj (row_stride elements of dtype)
+ * holds q, k, v, q_ret (H*D each) then the gate logits b, g, u (H each).
+ * Writes q, k, v, q_ret contiguous [B, H*D] in dtype and beta, gamma, budget
+ * fp32 [B, H] as sgsa_layer_gates does; with k_cache / v_cache
+ * ([B, cache_len, H, D] contiguous, dtype; both or neither) also k and v into
+ * cache row pos (0 <= pos < cache_len).  row_stride >= 4*H*D + 3*H. */
+int sgsa_decode_split(int dtype, int B, int H, int D, const void* proj, long row_stride, void* q, void* k, void* v,
+                      void* q_ret, float* beta, float* gamma, float* budget, void* k_cache, void* v_cache,
+                      long cache_len, long pos, void* stream);
+
 int sgsa_sparse_gather_tiled(int B, int T, int H, int D, int top_k, const void* k, const void* v,
                              const int32_t* indices, const float* scores, const float* top2,
                              const int32_t* counts, const int32_t* split, const float* budget,

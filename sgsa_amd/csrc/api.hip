@@ -772,6 +772,53 @@ int sgsa_layer_gates(int dtype, long rows, int H, const void* logits, long row_s
                     "sgsa_layer_gates");
 }
 
+int sgsa_decode_attention_workspace_size(int dtype, int B, int H, int kend, size_t* bytes) {
+  REQUIRE(bytes);
+  if (int s = check_dtype(dtype)) return s;
+  if (B < 0 || H <= 0 || kend < 0) return fail(SGSA_ERR_INVALID_ARG, "B=%d H=%d kend=%d", B, H, kend);
+  *bytes = sgsa::decode_attn_workspace_bytes(dtype, B, H, kend);
+  return SGSA_OK;
+}
+
+int sgsa_decode_attention(int dtype, int B, int H, int Hkv, int D, const void* q, const void* k_cache,
+                          const void* v_cache, long cache_len, int kend, void* out, void* workspace,
+                          size_t workspace_bytes, void* stream) {
+  if (int s = check_dtype(dtype)) return s;
+  if (B < 0 || H <= 0 || Hkv <= 0 || H % Hkv != 0) return fail(SGSA_ERR_INVALID_ARG, "B=%d H=%d Hkv=%d", B, H, Hkv);
+  const int G = H / Hkv;
+  if (D != 128 || (G != 1 && G != 2 && G != 4 && G != 8))
+    return fail(SGSA_ERR_UNSUPPORTED, "decode attention needs D == 128 and H / Hkv in {1, 2, 4, 8} (D=%d, G=%d)", D, G);
+  if (kend < 1 || kend > cache_len) return fail(SGSA_ERR_INVALID_ARG, "kend=%d must be in [1, cache_len=%ld]", kend, cache_len);
+  if ((long)B * Hkv > 65535) return fail(SGSA_ERR_UNSUPPORTED, "B * Hkv exceeds the grid");
+  if (B == 0) return SGSA_OK;
+  REQUIRE(q); REQUIRE(k_cache); REQUIRE(v_cache); REQUIRE(out); REQUIRE(workspace);
+  if (workspace_bytes < sgsa::decode_attn_workspace_bytes(dtype, B, H, kend))
+    return fail(SGSA_ERR_WORKSPACE, "workspace of %zu bytes, need %zu", workspace_bytes,
+                sgsa::decode_attn_workspace_bytes(dtype, B, H, kend));
+  return hip_status(sgsa::launch_decode_attn(dtype, B, H, Hkv, q, k_cache, v_cache, cache_len, kend, out, workspace,
+                                             (hipStream_t)stream),
+                    "sgsa_decode_attention");
+}
+
+int sgsa_decode_split(int dtype, int B, int H, int D, const void* proj, long row_stride, void* q, void* k, void* v,
+                      void* q_ret, float* beta, float* gamma, float* budget, void* k_cache, void* v_cache,
+                      long cache_len, long pos, void* stream) {
+  if (int s = check_dtype(dtype)) return s;
+  if (B < 0 || H <= 0 || D <= 0) return fail(SGSA_ERR_INVALID_ARG, "B=%d H=%d D=%d", B, H, D);
+  if (row_stride < 4L * H * D + 3L * H)
+    return fail(SGSA_ERR_INVALID_ARG, "row_stride=%ld < 4*H*D + 3*H", row_stride);
+  if ((k_cache == nullptr) != (v_cache == nullptr))
+    return fail(SGSA_ERR_INVALID_ARG, "k_cache and v_cache must both be given or both be NULL");
+  if (k_cache != nullptr && (pos < 0 || pos >= cache_len))
+    return fail(SGSA_ERR_INVALID_ARG, "pos=%ld outside the cache [0, %ld)", pos, cache_len);
+  if (4L * B * H * D + (long)B * H > 0x7fffffffL * 256L) return fail(SGSA_ERR_UNSUPPORTED, "too many elements");
+  if (B == 0) return SGSA_OK;
+  REQUIRE(proj); REQUIRE(q); REQUIRE(k); REQUIRE(v); REQUIRE(q_ret); REQUIRE(beta); REQUIRE(gamma); REQUIRE(budget);
+  return hip_status(sgsa::launch_decode_split(dtype, proj, row_stride, B, H, D, q, k, v, q_ret, beta, gamma, budget,
+                                              k_cache, v_cache, cache_len, pos, (hipStream_t)stream),
+                    "sgsa_decode_split");
+}
+
 int sgsa_sparse_gather_tiled(int B, int T, int H, int D, int top_k, const void* k, const void* v,
                              const int32_t* indices, const float* scores, const float* top2,
                              const int32_t* counts, const int32_t* split, const float* budget, int write_mode,

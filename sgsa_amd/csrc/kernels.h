@@ -247,6 +247,12 @@ hipError_t launch_rope_qk(int dtype, const void* src, long stride, int B, int T,
 // The SGSA layer's gates from the logit groups of a projection row (norm.hip).
 hipError_t launch_gates(int dtype, const void* src, long stride, long rows, int H, float* beta, float* gamma,
                         float* budget, hipStream_t st);
+hipError_t launch_decode_split(int dtype, const void* src, long stride, int B, int H, int D, void* q, void* k, void* v,
+                               void* qr, float* beta, float* gamma, float* budget, void* kc, void* vc, long cache_len,
+                               long pos, hipStream_t st);
+size_t decode_attn_workspace_bytes(int dtype, int B, int H, int kend);
+hipError_t launch_decode_attn(int dtype, int B, int H, int Hkv, const void* q, const void* kc, const void* vc,
+                              long Tmax, int kend, void* out, void* ws, hipStream_t st);
 hipError_t launch_block_scores_transpose(const float* src, int B, int H, int T, int nb, float* dst, hipStream_t st);
 hipError_t launch_block_dense_weights(int B, int H, int T, int ks, const int32_t* idx, const float* w,
                                       const int32_t* counts, float* dense, hipStream_t st);

@@ -62,6 +62,60 @@ hipError_t launch_gates(int dtype, const void* src, long stride, long rows, int 
   return hipGetLastError();
 }
 
+// One decode token's projection row per sequence, split for the kernels: row b
+// (src + b * stride) holds q, k, v, q_ret (HD = H * D each), then the gate
+// logits b, g, u (H each).  Threads i < 4 B HD copy one element each into the
+// contiguous [B, HD] outputs (k and v also into cache row pos of their
+// sequence when the caches are given); the next B H threads make the gates as
+// gates_kernel does.
+template <typename X>
+__global__ __launch_bounds__(256) void decode_split_kernel(const X* __restrict__ src, long stride, int B, int H, int D,
+                                                           X* __restrict__ q, X* __restrict__ k, X* __restrict__ v,
+                                                           X* __restrict__ qr, float* __restrict__ beta,
+                                                           float* __restrict__ gamma, float* __restrict__ budget,
+                                                           X* __restrict__ kc, X* __restrict__ vc, long cache_len,
+                                                           long pos) {
+  const long HD = (long)H * D;
+  const long ncopy = 4L * B * HD;
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i < ncopy) {
+    const long b = i / (4 * HD), j = i % (4 * HD);
+    const int grp = (int)(j / HD);
+    const long e = j % HD;
+    const X x = src[b * stride + j];
+    X* dst = grp == 0 ? q : grp == 1 ? k : grp == 2 ? v : qr;
+    dst[b * HD + e] = x;
+    if (grp == 1 && kc != nullptr) kc[(b * cache_len + pos) * HD + e] = x;
+    if (grp == 2 && vc != nullptr) vc[(b * cache_len + pos) * HD + e] = x;
+    return;
+  }
+  const long g = i - ncopy;
+  if (g >= (long)B * H) return;
+  const long b = g / H;
+  const int h = (int)(g % H);
+  const X* p = src + b * stride + 4 * HD + h;
+  const float bl = ld(p, 0), gl = ld(p, H), ul = ld(p, 2 * H);
+  beta[g] = fmaxf(1.0f / (1.0f + expf(-bl)), 1e-4f);
+  gamma[g] = 1.0f / (1.0f + expf(-gl));
+  budget[g] = ul;
+}
+
+hipError_t launch_decode_split(int dtype, const void* src, long stride, int B, int H, int D, void* q, void* k, void* v,
+                               void* qr, float* beta, float* gamma, float* budget, void* kc, void* vc, long cache_len,
+                               long pos, hipStream_t st) {
+  const long n = 4L * B * H * D + (long)B * H;
+  const dim3 grid((unsigned)((n + 255) / 256));
+  if (dtype == DT_F32)
+    decode_split_kernel<float><<<grid, 256, 0, st>>>((const float*)src, stride, B, H, D, (float*)q, (float*)k,
+                                                     (float*)v, (float*)qr, beta, gamma, budget, (float*)kc,
+                                                     (float*)vc, cache_len, pos);
+  else
+    decode_split_kernel<bf16_t><<<grid, 256, 0, st>>>((const bf16_t*)src, stride, B, H, D, (bf16_t*)q, (bf16_t*)k,
+                                                      (bf16_t*)v, (bf16_t*)qr, beta, gamma, budget, (bf16_t*)kc,
+                                                      (bf16_t*)vc, cache_len, pos);
+  return hipGetLastError();
+}
+
 // One thread per output element.  Row (b, t) of the projection output starts at
 // src + (b T + t) stride: q's Hq heads of D, then k's Hk heads.
 __device__ __forceinline__ float round_to(float v, float) { return v; }

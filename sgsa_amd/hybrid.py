@@ -29,6 +29,7 @@ Inference only.
 
 from __future__ import annotations
 
+import ctypes
 import math
 from dataclasses import dataclass
 from typing import List, Optional, Tuple
@@ -40,7 +41,7 @@ import torch.nn.functional as F
 from .decode import sgsa_decode_step
 from .layer import LayerWorkspace, sgsa_layer_forward
 from . import _abi
-from .model import GatedMLP, RMSNorm, SGSABlock, SGSAConfig, fused_linear
+from .model import GatedMLP, RMSNorm, SGSABlock, SGSAConfig, fused_linear, fused_linear_out
 from .retrieval import gather_masked, score_topk_masked
 
 Tensor = torch.Tensor
@@ -110,6 +111,8 @@ def gqa_attention(q: Tensor, k: Tensor, v: Tensor, pos0: int, block: int = 1024)
     B, H, Tq, D = q.shape
     Hkv = k.shape[1]
     G = H // Hkv
+    if Tq == 1 and _decode_attention_fits(q, k, v, pos0):
+        return _decode_attention(q, k, v)
     out = torch.empty_like(q)
     qg = q.reshape(B, Hkv, G, Tq, D)
     kpos = torch.arange(k.shape[2], device=q.device)
@@ -138,6 +141,43 @@ def gqa_attention(q: Tensor, k: Tensor, v: Tensor, pos0: int, block: int = 1024)
         p = torch.softmax(s, dim=-2).to(q.dtype).transpose(-1, -2).contiguous()             # [B,Hkv,G*n,kend]
         o = torch.matmul(p, v[:, :, :kend])   # [B,Hkv,G*n,D]; a row-major slice, not a transposed view
         out[:, :, r0:r1] = o.view(B, Hkv, G, n, D).reshape(B, H, n, D)
+    return out
+
+
+def _cache_view_len(t: Tensor) -> int:
+    """cache_len of a [B, Hkv, kend, D] view of a contiguous [B, Hkv, cache_len, D] cache, or 0."""
+    B, Hkv, _, D = t.shape
+    if t.stride(3) != 1 or t.stride(2) != D or t.stride(1) % D != 0:
+        return 0
+    n = t.stride(1) // D
+    return n if t.stride(0) == Hkv * n * D and n >= t.shape[2] else 0
+
+
+def _decode_attention_fits(q: Tensor, k: Tensor, v: Tensor, pos0: int) -> bool:
+    """Whether sgsa_decode_attention takes this call: one query row per sequence at the
+    last cached position, no autograd, D = 128, H / Hkv in {1, 2, 4, 8}, q contiguous and
+    k / v views of contiguous caches of q's dtype."""
+    B, H, _, D = q.shape
+    Hkv = k.shape[1]
+    return (not torch.is_grad_enabled() and q.is_cuda and q.dtype in (torch.float32, torch.bfloat16) and D == 128
+            and H % Hkv == 0 and H // Hkv in (1, 2, 4, 8) and k.dtype == q.dtype and v.dtype == q.dtype
+            and q.is_contiguous() and k.shape == v.shape and k.shape[2] == pos0 + 1
+            and _cache_view_len(k) > 0 and _cache_view_len(k) == _cache_view_len(v))
+
+
+def _decode_attention(q: Tensor, k: Tensor, v: Tensor) -> Tensor:
+    """gqa_attention for one query row per sequence, in one HIP pass over the cache
+    (sgsa_decode_attention): the same rounding points as the torch form."""
+    B, H, _, D = q.shape
+    Hkv, kend = k.shape[1], k.shape[2]
+    code = _abi.dtype_code(q.dtype)
+    nb = ctypes.c_size_t()
+    L = _abi.lib()
+    _abi.check(L.sgsa_decode_attention_workspace_size(code, B, H, kend, ctypes.byref(nb)))
+    ws = torch.empty(nb.value, device=q.device, dtype=torch.uint8)
+    out = torch.empty_like(q)
+    _abi.check(L.sgsa_decode_attention(code, B, H, Hkv, D, _abi.ptr(q), _abi.ptr(k), _abi.ptr(v), _cache_view_len(k),
+                                       kend, _abi.ptr(out), _abi.ptr(ws), nb.value, _abi.stream_of(q)))
     return out
 
 
@@ -206,12 +246,35 @@ class SGSADecoderBlock(SGSABlock):
         cache["cand"] = None
         return self._finish(h, att)
 
+    _PROJ = ("q_proj", "k_proj", "v_proj", "q_ret_proj", "beta_proj", "gamma_proj", "budget_proj")
+
+    def _project_decode(self, h: Tensor, pos: int, cache: dict):
+        """_project for one token per sequence, appending its k and v to the cache.  Without
+        autograd, one launch (sgsa_decode_split) splits the fused projection row into
+        contiguous q, k, v, q_ret, makes the gates and writes the cache row, in place of
+        the strided copies the kernels would otherwise take."""
+        kc, vc = cache["k"], cache["v"]
+        if torch.is_grad_enabled() or kc.dtype != h.dtype or vc.dtype != h.dtype or not kc.is_contiguous() \
+                or not vc.is_contiguous():
+            q, k, v, q_ret, beta, gamma, budget = self._project(h)
+            kc[:, pos:pos + 1] = k
+            vc[:, pos:pos + 1] = v
+            return q, k, v, q_ret, beta, gamma, budget
+        B = h.shape[0]
+        H, D = self.num_heads, self.head_dim
+        y = fused_linear_out(self, self.input_norm(h), self._PROJ)   # [B, 1, 4HD + 3H], contiguous
+        q, k, v, q_ret = (torch.empty(B, 1, H, D, device=h.device, dtype=h.dtype) for _ in range(4))
+        beta, gamma, budget = (torch.empty(B, 1, H, device=h.device, dtype=torch.float32) for _ in range(3))
+        _abi.check(_abi.lib().sgsa_decode_split(
+            _abi.dtype_code(h.dtype), B, H, D, _abi.ptr(y), y.stride(0), _abi.ptr(q), _abi.ptr(k), _abi.ptr(v),
+            _abi.ptr(q_ret), _abi.ptr(beta), _abi.ptr(gamma), _abi.ptr(budget), _abi.ptr(kc), _abi.ptr(vc),
+            kc.shape[1], pos, _abi.stream_of(y)))
+        return q, k, v, q_ret, beta, gamma, budget
+
     def decode(self, h: Tensor, pos: int, cache: dict, select: bool) -> Tensor:
         """h [B, 1, C] at position pos; select: recompute the top-k (else re-score the kept set)."""
         cfg = self.config
-        q, k, v, q_ret, beta, gamma, budget = self._project(h)
-        cache["k"][:, pos:pos + 1] = k
-        cache["v"][:, pos:pos + 1] = v
+        q, k, v, q_ret, beta, gamma, budget = self._project_decode(h, pos, cache)
         cand = None if (select or cache["cand"] is None) else cache["cand"]
         att, st, cand = sgsa_decode_step(q, k, v, q_ret, beta, gamma, budget, cache["k"], cache["v"],
                                          cache["state"], cfg.top_k, write_mode=cfg.sgsa_write_mode,

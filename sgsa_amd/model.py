@@ -112,6 +112,14 @@ def fused_linear(module: nn.Module, x: Tensor, names) -> list:
     lins = [getattr(module, n) for n in names]
     if torch.is_grad_enabled():
         return [lin(x) for lin in lins]
+    y = fused_linear_out(module, x, names)
+    return list(torch.split(y, [l.out_features for l in lins], dim=-1))
+
+
+def fused_linear_out(module: nn.Module, x: Tensor, names) -> Tensor:
+    """The one GEMM of fused_linear (no autograd): the outputs of the nn.Linear children
+    ``names`` side by side along the last dimension of one contiguous tensor."""
+    lins = [getattr(module, n) for n in names]
     key = tuple((l.weight.data_ptr(), l.weight._version,
                  None if l.bias is None else (l.bias.data_ptr(), l.bias._version)) for l in lins)
     cached = module.__dict__.get("_fused_" + "_".join(names))
@@ -122,8 +130,7 @@ def fused_linear(module: nn.Module, x: Tensor, names) -> list:
             b = torch.cat([l.bias if l.bias is not None else l.weight.new_zeros(l.out_features) for l in lins])
         cached = (key, w, b)
         module.__dict__["_fused_" + "_".join(names)] = cached
-    y = F.linear(x, cached[1], cached[2])
-    return list(torch.split(y, [l.out_features for l in lins], dim=-1))
+    return F.linear(x, cached[1], cached[2])
 
 
 class GatedMLP(nn.Module):

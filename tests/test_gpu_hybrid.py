@@ -93,3 +93,33 @@ def test_hybrid_bf16_prompt_logits_near_the_oracle(dev):
     for s in range(n):
         out = m.decode_step(dec[:, s].to(dev), T + s, s, caches, rope)
         close(out, ref_d[:, s], 2e-2, f"bf16 decode step {s}")
+
+
+@pytest.mark.parametrize("dt,tol", [(torch.float32, 1e-5), (torch.bfloat16, 1e-2)])
+@pytest.mark.parametrize("G", [1, 2, 4, 8])
+@pytest.mark.parametrize("kend", [1, 255, 257, 1000])
+def test_decode_attention_equals_torch_form(dev, dt, tol, G, kend):
+    # one query row per sequence over a cache view: the HIP pass (sgsa_decode_attention, taken by
+    # gqa_attention at Tq = 1) against the torch form with the same rounding points (scores and
+    # scaling in dtype, softmax in fp32, probabilities in dtype); relative to max |o|
+    from sgsa_amd.hybrid import _decode_attention, _decode_attention_fits, gqa_attention
+    import math
+    B, Hkv, D, Tmax = 3, 2, 128, 1040
+    H = G * Hkv
+    g = torch.Generator().manual_seed(kend * 10 + G)
+    q = torch.randn(B, H, 1, D, generator=g).to(dt).to(dev)
+    kc = torch.randn(B, Hkv, Tmax, D, generator=g).to(dt).to(dev)
+    vc = torch.randn(B, Hkv, Tmax, D, generator=g).to(dt).to(dev)
+    k, v = kc[:, :, :kend], vc[:, :, :kend]
+    with torch.no_grad():
+        assert _decode_attention_fits(q, k, v, kend - 1)
+        got = _decode_attention(q, k, v)
+        via = gqa_attention(q, k, v, kend - 1)
+    qg = q.reshape(B, Hkv, G, D)
+    s = (torch.matmul(qg, k.transpose(-1, -2).contiguous()) * (1.0 / math.sqrt(D))).float()   # [B,Hkv,G,kend]
+    p = torch.softmax(s, dim=-1).to(dt)
+    want = torch.matmul(p, v.contiguous()).reshape(B, H, 1, D)
+    torch.cuda.synchronize()
+    assert torch.equal(got, via)
+    err = ((got.float() - want.float()).abs().max() / want.float().abs().max()).item()
+    assert err <= tol, f"{err:.3e}"

@@ -98,3 +98,46 @@ def test_rope_qk_equals_torch_rope(dev, dt, T, pos0):
     c, s = cos[pos0:pos0 + T], sin[pos0:pos0 + T]
     torch.cuda.synchronize()
     assert torch.equal(q, apply_rope(qr, c, s)) and torch.equal(k, apply_rope(kr, c, s))
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("B,H,D,pad", [(8, 4, 64, 0), (3, 5, 48, 7), (1, 2, 128, 0)])
+def test_decode_split_equals_views_and_gates(dev, dt, B, H, D, pad):
+    # one decode token per sequence: the fused projection row [q | k | v | q_ret | b | g | u | pad]
+    # split into contiguous q, k, v, q_ret (bit for bit), the gates of sgsa_layer_gates' formula,
+    # and k, v appended at cache row pos with every other cache row untouched
+    from sgsa_amd import _abi
+    HD = H * D
+    X = 4 * HD + 3 * H + pad
+    g = torch.Generator().manual_seed(B * 100 + H)
+    y = (3.0 * torch.randn(B, 1, X, generator=g)).to(dt).to(dev)
+    Tc, pos = 11, 6
+    kc = torch.randn(B, Tc, H, D, generator=g).to(dt).to(dev)
+    vc = torch.randn(B, Tc, H, D, generator=g).to(dt).to(dev)
+    kc0, vc0 = kc.clone(), vc.clone()
+    q, k, v, qr = (torch.empty(B, 1, H, D, device=dev, dtype=dt) for _ in range(4))
+    beta, gamma, budget = (torch.empty(B, 1, H, device=dev) for _ in range(3))
+    _abi.check(_abi.lib().sgsa_decode_split(
+        _abi.dtype_code(dt), B, H, D, _abi.ptr(y), y.stride(0), _abi.ptr(q), _abi.ptr(k), _abi.ptr(v), _abi.ptr(qr),
+        _abi.ptr(beta), _abi.ptr(gamma), _abi.ptr(budget), _abi.ptr(kc), _abi.ptr(vc), Tc, pos, _abi.stream_of(y)))
+    torch.cuda.synchronize()
+    parts = torch.split(y, [HD, HD, HD, HD, H, H, H, pad], dim=-1)
+    for name, got, want in zip(("q", "k", "v", "q_ret"), (q, k, v, qr), parts[:4]):
+        assert torch.equal(got, want.reshape(B, 1, H, D)), name
+    want = (torch.sigmoid(parts[4].float()).clamp_min(1e-4), torch.sigmoid(parts[5].float()), parts[6].float())
+    for name, o, w in zip(("beta", "gamma", "budget"), (beta, gamma, budget), want):
+        torch.testing.assert_close(o, w, atol=1e-6, rtol=1e-5, msg=name)
+    kw, vw = kc0.clone(), vc0.clone()
+    kw[:, pos] = parts[1].reshape(B, H, D)
+    vw[:, pos] = parts[2].reshape(B, H, D)
+    assert torch.equal(kc, kw) and torch.equal(vc, vw)
+    # without caches nothing else is written; a pos outside the cache is an error
+    _abi.check(_abi.lib().sgsa_decode_split(
+        _abi.dtype_code(dt), B, H, D, _abi.ptr(y), y.stride(0), _abi.ptr(q), _abi.ptr(k), _abi.ptr(v), _abi.ptr(qr),
+        _abi.ptr(beta), _abi.ptr(gamma), _abi.ptr(budget), None, None, 0, 0, _abi.stream_of(y)))
+    rc = _abi.lib().sgsa_decode_split(
+        _abi.dtype_code(dt), B, H, D, _abi.ptr(y), y.stride(0), _abi.ptr(q), _abi.ptr(k), _abi.ptr(v), _abi.ptr(qr),
+        _abi.ptr(beta), _abi.ptr(gamma), _abi.ptr(budget), _abi.ptr(kc), _abi.ptr(vc), Tc, Tc, _abi.stream_of(y))
+    assert rc != 0
+    torch.cuda.synchronize()
+    assert torch.equal(kc, kw) and torch.equal(vc, vw)
