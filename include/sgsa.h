@@ -302,6 +302,19 @@ int sgsa_block_retrieve_masked(int dtype, int B, int T, int H, int D, int top_k,
 int sgsa_rms_norm(int dtype, int weight_f32, long rows, int C, const void* x, const void* weight, float eps, void* y,
                   void* stream);
 
+/* The residual add before a block's second norm (SGSABlock.forward,
+ * modelings/modeling_sgsa.py:684-686; hybrid_dense_delta_topk.py:240-244)
+ * in one launch: sum = a + b (rounded to dtype), y = sgsa_rms_norm(sum).
+ * a, b, sum, y [rows, C] contiguous in dtype; sum may not alias a or b. */
+int sgsa_add_rms_norm(int dtype, int weight_f32, long rows, int C, const void* a, const void* b, void* sum,
+                      const void* weight, float eps, void* y, void* stream);
+
+/* The gated MLP's activation (down(silu(gate(x)) * up(x)), modeling_sgsa.py's
+ * and the hybrid's MLP) on a fused gate | up projection: row r of gate_up
+ * (row_stride elements) holds gate's I values then up's.  y [rows, I]
+ * contiguous = silu(gate) rounded to dtype, times up, rounded to dtype. */
+int sgsa_silu_mul(int dtype, long rows, int I, const void* gate_up, long row_stride, void* y, void* stream);
+
 /* Rotary embedding of a dense attention layer's q and k (rotate-half form,
  * modelings/hybrid_dense_delta_topk.py:140-150), in x's dtype with a rounding
  * after each product and the sum (torch's elementwise semantics).  Row (b, t)

@@ -67,6 +67,8 @@ SIGNATURES = {
                                 _I, _I, _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),
     "sgsa_sparse_gather_workspace_size": (_I, [_I, _I, _I, _I, _I, ctypes.POINTER(_SZ)]),
     "sgsa_rms_norm": (_I, [_I, _I, ctypes.c_long, _I, _P, _P, _F, _P, _P]),
+    "sgsa_add_rms_norm": (_I, [_I, _I, ctypes.c_long, _I, _P, _P, _P, _P, _F, _P, _P]),
+    "sgsa_silu_mul": (_I, [_I, ctypes.c_long, _I, _P, ctypes.c_long, _P, _P]),
     "sgsa_layer_gates": (_I, [_I, ctypes.c_long, _I, _P, ctypes.c_long, _P, _P, _P, _P]),
     "sgsa_rope_qk": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _P, ctypes.c_long, _P, _P, _P, _P, _P]),
     "sgsa_decode_attention_workspace_size": (_I, [_I, _I, _I, _I, ctypes.POINTER(ctypes.c_size_t)]),

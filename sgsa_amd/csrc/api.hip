@@ -761,6 +761,29 @@ int sgsa_rope_qk(int dtype, int B, int T, int Hq, int Hk, int D, int pos0, int t
                     "sgsa_rope_qk");
 }
 
+int sgsa_add_rms_norm(int dtype, int weight_f32, long rows, int C, const void* a, const void* b, void* sum,
+                      const void* weight, float eps, void* y, void* stream) {
+  if (int s = check_dtype(dtype)) return s;
+  if (rows < 0 || C <= 0) return fail(SGSA_ERR_INVALID_ARG, "rows=%ld C=%d", rows, C);
+  if (rows > 0x7fffffffL) return fail(SGSA_ERR_UNSUPPORTED, "rows=%ld exceeds the grid", rows);
+  if (dtype == SGSA_F32 && !weight_f32) return fail(SGSA_ERR_INVALID_ARG, "fp32 input needs an fp32 weight");
+  if (!(eps >= 0.f)) return fail(SGSA_ERR_INVALID_ARG, "eps must be >= 0");
+  if (rows == 0) return SGSA_OK;
+  REQUIRE(a); REQUIRE(b); REQUIRE(sum); REQUIRE(weight); REQUIRE(y);
+  return hip_status(sgsa::launch_add_rms_norm(dtype, weight_f32 ? 1 : 0, rows, C, a, b, sum, weight, eps, y,
+                                              (hipStream_t)stream),
+                    "sgsa_add_rms_norm");
+}
+
+int sgsa_silu_mul(int dtype, long rows, int I, const void* gate_up, long row_stride, void* y, void* stream) {
+  if (int s = check_dtype(dtype)) return s;
+  if (rows < 0 || I <= 0 || row_stride < 2L * I) return fail(SGSA_ERR_INVALID_ARG, "rows=%ld I=%d row_stride=%ld", rows, I, row_stride);
+  if (rows * I > 0x7fffffffL * 256L) return fail(SGSA_ERR_UNSUPPORTED, "rows * I exceeds the grid");
+  if (rows == 0) return SGSA_OK;
+  REQUIRE(gate_up); REQUIRE(y);
+  return hip_status(sgsa::launch_silu_mul(dtype, gate_up, row_stride, rows, I, y, (hipStream_t)stream), "sgsa_silu_mul");
+}
+
 int sgsa_layer_gates(int dtype, long rows, int H, const void* logits, long row_stride, float* beta, float* gamma,
                      float* budget, void* stream) {
   if (int s = check_dtype(dtype)) return s;

@@ -241,6 +241,9 @@ hipError_t launch_block_select(const BlockArgs& a, hipStream_t st);
 // RMSNorm of the model shells (norm.hip): x, y [rows, C] in dtype; weight [C] in dtype or fp32.
 hipError_t launch_rms_norm(int dtype, int w_f32, long rows, int C, const void* x, const void* w, float eps, void* y,
                            hipStream_t st);
+hipError_t launch_add_rms_norm(int dtype, int w_f32, long rows, int C, const void* a, const void* b, void* sum,
+                               const void* w, float eps, void* y, hipStream_t st);
+hipError_t launch_silu_mul(int dtype, const void* src, long stride, long rows, int I, void* y, hipStream_t st);
 // RoPE of a dense layer's q and k from the fused projection rows (norm.hip).
 hipError_t launch_rope_qk(int dtype, const void* src, long stride, int B, int T, int Hq, int Hk, int D, int pos0,
                           const float* cosv, const float* sinv, void* qo, void* ko, hipStream_t st);

@@ -16,17 +16,31 @@
 
 namespace sgsa {
 
-// One workgroup of 256 threads per row.
-template <typename X, typename W>
+// One workgroup of 256 threads per row.  ADD: the row is first a + b, rounded
+// to X and stored to sum (the residual add before the norm); each thread reads
+// back only the elements it stored.
+template <typename X, typename W, bool ADD = false>
 __global__ __launch_bounds__(256) void rms_norm_kernel(const X* __restrict__ x, const W* __restrict__ w, int C,
-                                                       float eps, X* __restrict__ y) {
+                                                       float eps, X* __restrict__ y, const X* __restrict__ b = nullptr,
+                                                       X* __restrict__ sum = nullptr) {
   __shared__ float part[4];
   const long row = blockIdx.x;
   const X* xr = x + row * C;
   float ss = 0.f;
-  for (int c = threadIdx.x; c < C; c += 256) {
-    const float v = ld(xr, c);
-    ss = fmaf(v, v, ss);
+  if constexpr (ADD) {
+    const X* br = b + row * C;
+    X* sr = sum + row * C;
+    for (int c = threadIdx.x; c < C; c += 256) {
+      st(sr, c, ld(xr, c) + ld(br, c));
+      const float v = ld(sr, c);
+      ss = fmaf(v, v, ss);
+    }
+    xr = sr;
+  } else {
+    for (int c = threadIdx.x; c < C; c += 256) {
+      const float v = ld(xr, c);
+      ss = fmaf(v, v, ss);
+    }
   }
   ss = wave_sum(ss);
   if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
@@ -157,6 +171,43 @@ hipError_t launch_rope_qk(int dtype, const void* src, long stride, int B, int T,
   else
     rope_qk_kernel<bf16_t><<<grid, 256, 0, st>>>((const bf16_t*)src, stride, B, T, Hq, Hk, D, pos0, cosv, sinv,
                                                  (bf16_t*)qo, (bf16_t*)ko);
+  return hipGetLastError();
+}
+
+hipError_t launch_add_rms_norm(int dtype, int w_f32, long rows, int C, const void* a, const void* b, void* sum,
+                               const void* w, float eps, void* y, hipStream_t st) {
+  const dim3 grid((unsigned)rows);
+  if (dtype == DT_F32) {
+    rms_norm_kernel<float, float, true><<<grid, 256, 0, st>>>((const float*)a, (const float*)w, C, eps, (float*)y,
+                                                              (const float*)b, (float*)sum);
+  } else if (w_f32) {
+    rms_norm_kernel<bf16_t, float, true><<<grid, 256, 0, st>>>((const bf16_t*)a, (const float*)w, C, eps,
+                                                               (bf16_t*)y, (const bf16_t*)b, (bf16_t*)sum);
+  } else {
+    rms_norm_kernel<bf16_t, bf16_t, true><<<grid, 256, 0, st>>>((const bf16_t*)a, (const bf16_t*)w, C, eps,
+                                                                (bf16_t*)y, (const bf16_t*)b, (bf16_t*)sum);
+  }
+  return hipGetLastError();
+}
+
+// silu(gate) * up of a fused gate | up projection row, in X's roundings: silu
+// rounded to X, then the product rounded to X.  One thread per output element.
+template <typename X>
+__global__ __launch_bounds__(256) void silu_mul_kernel(const X* __restrict__ src, long stride, long rows, int I,
+                                                       X* __restrict__ y) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= rows * I) return;
+  const long r = i / I;
+  const int c = (int)(i % I);
+  const X tag{};
+  const float g = ld(src, r * stride + c), u = ld(src, r * stride + I + c);
+  st(y, i, round_to(g / (1.0f + expf(-g)), tag) * u);
+}
+
+hipError_t launch_silu_mul(int dtype, const void* src, long stride, long rows, int I, void* y, hipStream_t st) {
+  const dim3 grid((unsigned)((rows * I + 255) / 256));
+  if (dtype == DT_F32) silu_mul_kernel<float><<<grid, 256, 0, st>>>((const float*)src, stride, rows, I, (float*)y);
+  else silu_mul_kernel<bf16_t><<<grid, 256, 0, st>>>((const bf16_t*)src, stride, rows, I, (bf16_t*)y);
   return hipGetLastError();
 }
 

@@ -221,8 +221,8 @@ class DenseGQABlock(nn.Module):
         cache["k"][:, :, pos0:pos0 + T] = k
         cache["v"][:, :, pos0:pos0 + T] = v
         att = gqa_attention(q, cache["k"][:, :, :pos0 + T], cache["v"][:, :, :pos0 + T], pos0)
-        h = h + self.o_proj(att.transpose(1, 2).reshape(B, T, self.H * self.D))
-        return h + self.mlp(self.post_attn_norm(h))
+        h, n = self.post_attn_norm.add_forward(h, self.o_proj(att.transpose(1, 2).reshape(B, T, self.H * self.D)))
+        return h + self.mlp(n)
 
 
 class SGSADecoderBlock(SGSABlock):
@@ -230,8 +230,8 @@ class SGSADecoderBlock(SGSABlock):
 
     def _finish(self, h: Tensor, att: Tensor) -> Tensor:
         B, T, C = h.shape
-        h = h + self.o_proj(att.reshape(B, T, C))
-        return h + self.mlp(self.post_attn_norm(h))
+        h, n = self.post_attn_norm.add_forward(h, self.o_proj(att.reshape(B, T, C)))
+        return h + self.mlp(n)
 
     def prefill(self, h: Tensor, cache: dict) -> Tensor:
         cfg = self.config

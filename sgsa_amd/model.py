@@ -100,6 +100,24 @@ class RMSNorm(nn.Module):
                                             _abi.ptr(y), _abi.stream_of(xc)))
         return y
 
+    def add_forward(self, a: Tensor, b: Tensor) -> Tuple[Tensor, Tensor]:
+        """(a + b, self(a + b)): the residual add and this norm; without autograd in one
+        launch (sgsa_add_rms_norm) with the same roundings as the two steps."""
+        if torch.is_grad_enabled() or a.shape != b.shape or a.dtype != b.dtype or not a.is_cuda:
+            h = a + b
+            return h, self(h)
+        ac, bc = a.contiguous(), b.contiguous()
+        C = ac.shape[-1]
+        w = self.weight
+        if w.dtype != a.dtype and w.dtype != torch.float32:
+            w = w.float()
+        w = w.contiguous()
+        h, y = torch.empty_like(ac), torch.empty_like(ac)
+        _abi.check(_abi.lib().sgsa_add_rms_norm(_abi.dtype_code(a.dtype), int(w.dtype == torch.float32),
+                                                ac.numel() // C, C, _abi.ptr(ac), _abi.ptr(bc), _abi.ptr(h),
+                                                _abi.ptr(w), float(self.eps), _abi.ptr(y), _abi.stream_of(ac)))
+        return h, y
+
 
 def fused_linear(module: nn.Module, x: Tensor, names) -> list:
     """The outputs of the nn.Linear children ``names`` of ``module`` on the same input x.
@@ -143,8 +161,17 @@ class GatedMLP(nn.Module):
         self.down_proj = nn.Linear(intermediate_size, hidden_size, bias=False)
 
     def forward(self, x: Tensor) -> Tensor:
-        gate, up = fused_linear(self, x, ("gate_proj", "up_proj"))
-        return self.down_proj(F.silu(gate) * up)
+        if torch.is_grad_enabled() or x.dtype not in (torch.float32, torch.bfloat16) or not x.is_cuda:
+            gate, up = fused_linear(self, x, ("gate_proj", "up_proj"))
+            return self.down_proj(F.silu(gate) * up)
+        # one launch for silu(gate) * up on the fused projection (sgsa_silu_mul)
+        gu = fused_linear_out(self, x, ("gate_proj", "up_proj"))
+        I = self.gate_proj.out_features
+        act = torch.empty(*gu.shape[:-1], I, device=gu.device, dtype=gu.dtype)
+        _abi.check(_abi.lib().sgsa_silu_mul(_abi.dtype_code(gu.dtype), gu.numel() // (2 * I), I, _abi.ptr(gu),
+                                            gu.stride(-2) if gu.dim() > 1 else 2 * I, _abi.ptr(act),
+                                            _abi.stream_of(gu)))
+        return self.down_proj(act)
 
 
 class SGSABlock(nn.Module):
@@ -222,8 +249,8 @@ class SGSABlock(nn.Module):
         out = self.o_proj(att.reshape(B, T, C))
         if cfg.sparse_output_lambda > 0:
             out = out + cfg.sparse_output_lambda * self.sparse_out_proj(vh.reshape(B, T, C))
-        h = h + out
-        h = h + self.mlp(self.post_attn_norm(h))
+        h, n = self.post_attn_norm.add_forward(h, out)
+        h = h + self.mlp(n)
         rs = stats["row_stats"]
         zero = torch.zeros((), device=h.device)
         metrics = {

@@ -141,3 +141,41 @@ def test_decode_split_equals_views_and_gates(dev, dt, B, H, D, pad):
     assert rc != 0
     torch.cuda.synchronize()
     assert torch.equal(kc, kw) and torch.equal(vc, vw)
+
+
+@pytest.mark.parametrize("dt,wdt", [(torch.float32, torch.float32), (torch.bfloat16, torch.bfloat16),
+                                    (torch.bfloat16, torch.float32)])
+@pytest.mark.parametrize("shape", [(8, 1, 2048), (3, 77, 1000)])
+def test_add_rms_norm_equals_the_two_steps(dev, dt, wdt, shape):
+    # sgsa_add_rms_norm (RMSNorm.add_forward without autograd) = (a + b, RMSNorm(a + b)) bit for bit
+    g = torch.Generator().manual_seed(shape[1])
+    a = (2.0 * torch.randn(*shape, generator=g)).to(dt).to(dev)
+    b = (2.0 * torch.randn(*shape, generator=g)).to(dt).to(dev)
+    norm = RMSNorm(shape[-1], 1e-6)
+    with torch.no_grad():
+        norm.weight.copy_(1.0 + 0.1 * torch.randn(shape[-1], generator=g))
+    norm = norm.to(device=dev, dtype=wdt)
+    with torch.no_grad():
+        h, y = norm.add_forward(a, b)
+        h2 = a + b
+        y2 = norm(h2)
+    torch.cuda.synchronize()
+    assert torch.equal(h, h2) and torch.equal(y, y2)
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_gated_mlp_silu_mul_equals_torch(dev, dt):
+    # GatedMLP without autograd (one sgsa_silu_mul launch on the fused gate | up projection)
+    # against silu(gate) * up in torch on the same projection: within one rounding of dt
+    from sgsa_amd.model import GatedMLP
+    torch.manual_seed(3)
+    mlp = GatedMLP(256, 640).to(device=dev, dtype=dt)
+    x = torch.randn(4, 3, 256, device=dev).to(dt)
+    with torch.no_grad():
+        got = mlp(x)
+        gate, up = mlp.gate_proj(x), mlp.up_proj(x)
+        act = torch.nn.functional.silu(gate) * up
+        want = mlp.down_proj(act)
+    torch.cuda.synchronize()
+    err = ((got.float() - want.float()).abs().max() / want.float().abs().max()).item()
+    assert err <= (1e-5 if dt == torch.float32 else 1.6e-2), f"{err:.3e}"
