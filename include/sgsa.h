@@ -309,6 +309,15 @@ int sgsa_rms_norm(int dtype, int weight_f32, long rows, int C, const void* x, co
 int sgsa_add_rms_norm(int dtype, int weight_f32, long rows, int C, const void* a, const void* b, void* sum,
                       const void* weight, float eps, void* y, void* stream);
 
+/* nn.Linear on a few rows, for the decode step's projections (the model
+ * shells' q/k/v, output, MLP and LM-head linears at B <= 16 tokens):
+ * y = x weight^T (+ bias), bf16 in and out, fp32 accumulation.  x [M, K]
+ * (row stride x_row_stride elements, a multiple of 8), weight [N, K]
+ * contiguous, bias [N] or NULL, y [M, N] (row stride y_row_stride);
+ * M <= 16, K a multiple of 32, x and weight 16-byte aligned. */
+int sgsa_linear_rows(int dtype, int M, int N, int K, const void* x, long x_row_stride, const void* weight,
+                     const void* bias, void* y, long y_row_stride, void* stream);
+
 /* The gated MLP's activation (down(silu(gate(x)) * up(x)), modeling_sgsa.py's
  * and the hybrid's MLP) on a fused gate | up projection: row r of gate_up
  * (row_stride elements) holds gate's I values then up's.  y [rows, I]

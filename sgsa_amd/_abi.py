@@ -68,6 +68,7 @@ SIGNATURES = {
     "sgsa_sparse_gather_workspace_size": (_I, [_I, _I, _I, _I, _I, ctypes.POINTER(_SZ)]),
     "sgsa_rms_norm": (_I, [_I, _I, ctypes.c_long, _I, _P, _P, _F, _P, _P]),
     "sgsa_add_rms_norm": (_I, [_I, _I, ctypes.c_long, _I, _P, _P, _P, _P, _F, _P, _P]),
+    "sgsa_linear_rows": (_I, [_I, _I, _I, _I, _P, ctypes.c_long, _P, _P, _P, ctypes.c_long, _P]),
     "sgsa_silu_mul": (_I, [_I, ctypes.c_long, _I, _P, ctypes.c_long, _P, _P]),
     "sgsa_layer_gates": (_I, [_I, ctypes.c_long, _I, _P, ctypes.c_long, _P, _P, _P, _P]),
     "sgsa_rope_qk": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _P, ctypes.c_long, _P, _P, _P, _P, _P]),
@@ -132,8 +133,15 @@ def ptr(t: Optional[torch.Tensor]):
     return None if t is None else ctypes.c_void_p(t.data_ptr())
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(t: torch.Tensor):
+    """The current stream of t's device (torch's raw-stream query when present: the
+    Stream object of torch.cuda.current_stream costs several microseconds per call)."""
     if t.is_cuda:
+        if _raw_stream is not None:
+            return ctypes.c_void_p(_raw_stream(t.device.index))
         return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
     return None
 

@@ -111,6 +111,7 @@ __global__ __launch_bounds__(256) void dattn_pv_kernel(const X* __restrict__ sws
                                                        const X* __restrict__ vc, int H, int Hkv, long Tmax, int kend,
                                                        int nblk, float* __restrict__ opart) {
   __shared__ float pl[G][DA_KB];
+  __shared__ float wsum[4 * G * DA_D];   // the waves' partial sums [w][g][d]
   __shared__ float nm[G][2];
   const int blk = blockIdx.x, bk = blockIdx.y;
   const int b = bk / Hkv, kh = bk % Hkv;
@@ -154,15 +155,16 @@ __global__ __launch_bounds__(256) void dattn_pv_kernel(const X* __restrict__ sws
     pl[g][tid] = p;
   }
   __syncthreads();
-  // thread t: dimensions 2 (t % 64) .. +1 of heads g = t / 64 (+4)
-  const int dp = 2 * (tid & 63), g0 = tid >> 6;
+  // wave w: keys 64 w .. 64 w + 63 of the block for every head; lane l: dimensions 2l, 2l + 1.
+  // Each value pair is loaded once and used by all G heads; the waves' sums meet in LDS.
+  const int dp = 2 * lane;
   const int nk = min(DA_KB, kend - blk * DA_KB);
+  const int j0 = 64 * w, j1 = min(nk, j0 + 64);
   const X* vr = vc + ((long)bk * Tmax + blk * DA_KB) * DA_D + dp;
-  float o0[(G + 3) / 4], o1[(G + 3) / 4];
+  float o0[G], o1[G];
 #pragma unroll
-  for (int u = 0; u < (G + 3) / 4; ++u) { o0[u] = 0.f; o1[u] = 0.f; }
-  for (int jj = 0; jj < nk; ++jj) {
-    float v0, v1;
+  for (int g = 0; g < G; ++g) { o0[g] = 0.f; o1[g] = 0.f; }
+  auto vload = [&](int jj, float& v0, float& v1) __attribute__((always_inline)) {
     if constexpr (sizeof(X) == 2) {
       const uint32_t u2 = *reinterpret_cast<const uint32_t*>(vr + (long)jj * DA_D);
       v0 = __uint_as_float(u2 << 16);
@@ -171,24 +173,43 @@ __global__ __launch_bounds__(256) void dattn_pv_kernel(const X* __restrict__ sws
       const float2 f2 = *reinterpret_cast<const float2*>(vr + (long)jj * DA_D);
       v0 = f2.x; v1 = f2.y;
     }
+  };
+  int jj = j0;
+  for (; jj + 8 <= j1; jj += 8) {   // eight rows' loads in flight at a time
+    float v0[8], v1[8];
 #pragma unroll
-    for (int u = 0; u < (G + 3) / 4; ++u) {
-      const int g = g0 + 4 * u;
-      if (g < G) {
-        const float p = pl[g][jj];
-        o0[u] = fmaf(p, v0, o0[u]);
-        o1[u] = fmaf(p, v1, o1[u]);
+    for (int u = 0; u < 8; ++u) vload(jj + u, v0[u], v1[u]);
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float p = pl[g][jj + u];
+        o0[g] = fmaf(p, v0[u], o0[g]);
+        o1[g] = fmaf(p, v1[u], o1[g]);
       }
+  }
+  for (; jj < j1; ++jj) {
+    float v0, v1;
+    vload(jj, v0, v1);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float p = pl[g][jj];
+      o0[g] = fmaf(p, v0, o0[g]);
+      o1[g] = fmaf(p, v1, o1[g]);
     }
   }
 #pragma unroll
-  for (int u = 0; u < (G + 3) / 4; ++u) {
-    const int g = g0 + 4 * u;
-    if (g < G) {
-      float* op = opart + (((long)b * H + kh * G + g) * nblk + blk) * DA_D + dp;
-      op[0] = o0[u];
-      op[1] = o1[u];
-    }
+  for (int g = 0; g < G; ++g) {
+    wsum[(w * G + g) * DA_D + dp] = o0[g];
+    wsum[(w * G + g) * DA_D + dp + 1] = o1[g];
+  }
+  __syncthreads();
+  // thread t: element t of the G x 128 block output, the waves' sums in wave order
+  for (int e = tid; e < G * DA_D; e += 256) {
+    const int g = e / DA_D, d = e % DA_D;
+    const float o = (wsum[(0 * G + g) * DA_D + d] + wsum[(1 * G + g) * DA_D + d]) +
+                    (wsum[(2 * G + g) * DA_D + d] + wsum[(3 * G + g) * DA_D + d]);
+    opart[(((long)b * H + kh * G + g) * nblk + blk) * DA_D + d] = o;
   }
 }
 
@@ -197,8 +218,17 @@ __global__ __launch_bounds__(128) void dattn_reduce_kernel(const float* __restri
                                                            X* __restrict__ out) {
   const long bh = blockIdx.x;
   const int d = threadIdx.x;
+  const float* op = opart + bh * nblk * DA_D + d;
   float o = 0.f;
-  for (int i = 0; i < nblk; ++i) o += opart[(bh * nblk + i) * DA_D + d];
+  int i = 0;
+  for (; i + 8 <= nblk; i += 8) {   // eight loads in flight, summed in block order
+    float x[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) x[u] = op[(long)(i + u) * DA_D];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) o += x[u];
+  }
+  for (; i < nblk; ++i) o += op[(long)i * DA_D];
   st(out, bh * DA_D + d, o);
 }
 

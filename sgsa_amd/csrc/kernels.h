@@ -244,6 +244,8 @@ hipError_t launch_rms_norm(int dtype, int w_f32, long rows, int C, const void* x
 hipError_t launch_add_rms_norm(int dtype, int w_f32, long rows, int C, const void* a, const void* b, void* sum,
                                const void* w, float eps, void* y, hipStream_t st);
 hipError_t launch_silu_mul(int dtype, const void* src, long stride, long rows, int I, void* y, hipStream_t st);
+hipError_t launch_small_gemm(const void* x, long xs, const void* W, const void* bias, int M, int N, int K, void* y,
+                             long ys, hipStream_t st);
 // RoPE of a dense layer's q and k from the fused projection rows (norm.hip).
 hipError_t launch_rope_qk(int dtype, const void* src, long stride, int B, int T, int Hq, int Hk, int D, int pos0,
                           const float* cosv, const float* sinv, void* qo, void* ko, hipStream_t st);

@@ -41,7 +41,7 @@ import torch.nn.functional as F
 from .decode import sgsa_decode_step
 from .layer import LayerWorkspace, sgsa_layer_forward
 from . import _abi
-from .model import GatedMLP, RMSNorm, SGSABlock, SGSAConfig, fused_linear, fused_linear_out
+from .model import GatedMLP, RMSNorm, SGSABlock, SGSAConfig, fused_linear, fused_linear_out, lin
 from .retrieval import gather_masked, score_topk_masked
 
 Tensor = torch.Tensor
@@ -221,7 +221,7 @@ class DenseGQABlock(nn.Module):
         cache["k"][:, :, pos0:pos0 + T] = k
         cache["v"][:, :, pos0:pos0 + T] = v
         att = gqa_attention(q, cache["k"][:, :, :pos0 + T], cache["v"][:, :, :pos0 + T], pos0)
-        h, n = self.post_attn_norm.add_forward(h, self.o_proj(att.transpose(1, 2).reshape(B, T, self.H * self.D)))
+        h, n = self.post_attn_norm.add_forward(h, lin(self.o_proj, att.transpose(1, 2).reshape(B, T, self.H * self.D)))
         return h + self.mlp(n)
 
 
@@ -230,7 +230,7 @@ class SGSADecoderBlock(SGSABlock):
 
     def _finish(self, h: Tensor, att: Tensor) -> Tensor:
         B, T, C = h.shape
-        h, n = self.post_attn_norm.add_forward(h, self.o_proj(att.reshape(B, T, C)))
+        h, n = self.post_attn_norm.add_forward(h, lin(self.o_proj, att.reshape(B, T, C)))
         return h + self.mlp(n)
 
     def prefill(self, h: Tensor, cache: dict) -> Tensor:
@@ -337,7 +337,7 @@ class HybridForCausalLM(nn.Module):
         return caches
 
     def _head(self, h: Tensor) -> Tensor:
-        return self.lm_head(self.norm(h))
+        return lin(self.lm_head, self.norm(h))
 
     @torch.no_grad()
     def prefill(self, input_ids: Tensor, caches: List[dict], rope: Tuple[Tensor, Tensor]) -> Tensor:

@@ -119,6 +119,31 @@ class RMSNorm(nn.Module):
         return h, y
 
 
+def linear_rows(x: Tensor, weight: Tensor, bias: Optional[Tensor] = None) -> Tensor:
+    """F.linear(x, weight, bias).  Without autograd, for bf16 x of at most 16 rows (a decode
+    step's tokens), one sgsa_linear_rows launch: a library GEMM's host dispatch costs more
+    than such a product."""
+    K = x.shape[-1]
+    M = x.numel() // K if K else 0
+    if torch.is_grad_enabled() or not x.is_cuda or x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16 \
+            or not 1 <= M <= 16 or K % 32 != 0 or not weight.is_contiguous() \
+            or (bias is not None and (bias.dtype != torch.bfloat16 or not bias.is_contiguous())):
+        return F.linear(x, weight, bias)
+    x2 = x.reshape(M, K)
+    if x2.stride(-1) != 1 or x2.stride(0) % 8 != 0 or x2.data_ptr() % 16 != 0 or weight.data_ptr() % 16 != 0:
+        return F.linear(x, weight, bias)
+    N = weight.shape[0]
+    y = torch.empty(*x.shape[:-1], N, device=x.device, dtype=x.dtype)
+    _abi.check(_abi.lib().sgsa_linear_rows(_abi.dtype_code(x.dtype), M, N, K, _abi.ptr(x2), x2.stride(0),
+                                           _abi.ptr(weight), _abi.ptr(bias), _abi.ptr(y), N, _abi.stream_of(x)))
+    return y
+
+
+def lin(module: nn.Linear, x: Tensor) -> Tensor:
+    """module(x) through linear_rows."""
+    return linear_rows(x, module.weight, module.bias)
+
+
 def fused_linear(module: nn.Module, x: Tensor, names) -> list:
     """The outputs of the nn.Linear children ``names`` of ``module`` on the same input x.
 
@@ -148,7 +173,7 @@ def fused_linear_out(module: nn.Module, x: Tensor, names) -> Tensor:
             b = torch.cat([l.bias if l.bias is not None else l.weight.new_zeros(l.out_features) for l in lins])
         cached = (key, w, b)
         module.__dict__["_fused_" + "_".join(names)] = cached
-    return F.linear(x, cached[1], cached[2])
+    return linear_rows(x, cached[1], cached[2])
 
 
 class GatedMLP(nn.Module):
@@ -171,7 +196,7 @@ class GatedMLP(nn.Module):
         _abi.check(_abi.lib().sgsa_silu_mul(_abi.dtype_code(gu.dtype), gu.numel() // (2 * I), I, _abi.ptr(gu),
                                             gu.stride(-2) if gu.dim() > 1 else 2 * I, _abi.ptr(act),
                                             _abi.stream_of(gu)))
-        return self.down_proj(act)
+        return lin(self.down_proj, act)
 
 
 class SGSABlock(nn.Module):

@@ -179,3 +179,23 @@ def test_gated_mlp_silu_mul_equals_torch(dev, dt):
     torch.cuda.synchronize()
     err = ((got.float() - want.float()).abs().max() / want.float().abs().max()).item()
     assert err <= (1e-5 if dt == torch.float32 else 1.6e-2), f"{err:.3e}"
+
+
+@pytest.mark.parametrize("M", [1, 3, 8, 16])
+@pytest.mark.parametrize("N,K,bias", [(16, 64, False), (100, 2048, True), (2096, 2048, False), (48, 5632, True)])
+def test_linear_rows_equals_f_linear(dev, M, N, K, bias):
+    # sgsa_linear_rows (model.linear_rows at <= 16 bf16 rows) against F.linear in fp32 on the same
+    # bf16 operands: within one bf16 rounding of the largest output; x as a strided view of a wider row
+    from sgsa_amd.model import linear_rows
+    g = torch.Generator().manual_seed(M * 7 + N)
+    xw = torch.randn(M, K + 32, generator=g).to(torch.bfloat16).to(dev)
+    x = xw[:, 16:16 + K]
+    w = (torch.randn(N, K, generator=g) / K ** 0.5).to(torch.bfloat16).to(dev)
+    b = torch.randn(N, generator=g).to(torch.bfloat16).to(dev) if bias else None
+    with torch.no_grad():
+        got = linear_rows(x, w, b)
+    want = torch.nn.functional.linear(x.float(), w.float(), None if b is None else b.float())
+    torch.cuda.synchronize()
+    assert got.shape == (M, N) and got.dtype == torch.bfloat16
+    err = ((got.float() - want).abs().max() / want.abs().max()).item()
+    assert err <= 8e-3, f"{err:.3e}"
