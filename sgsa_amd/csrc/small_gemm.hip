@@ -2,7 +2,7 @@
 // (nn.Linear at B <= 16 tokens), where a library GEMM's host dispatch costs
 // more than the kernel.  bf16 in, fp32 accumulation, bf16 out.
 //
-// One workgroup per 16 output columns, its four waves splitting K in four
+// One workgroup per 16 output columns, its eight waves splitting K in eight
 // interleaved ranges of 32-element steps; each wave runs
 // v_mfma_f32_16x16x32_bf16 with the x rows (zero past M) as the A operand and
 // 16 weight rows as the B operand, both loaded from global memory straight
@@ -16,10 +16,12 @@ namespace {
 
 typedef uint16_t sg_u16x8 __attribute__((ext_vector_type(8)));
 
-__global__ __launch_bounds__(256) void small_gemm_kernel(const bf16_t* __restrict__ x, long xs, const bf16_t* __restrict__ W,
+constexpr int SG_W = 8;   // waves per workgroup
+
+__global__ __launch_bounds__(64 * SG_W) void small_gemm_kernel(const bf16_t* __restrict__ x, long xs, const bf16_t* __restrict__ W,
                                                          const bf16_t* __restrict__ bias, int M, int N, int K,
                                                          bf16_t* __restrict__ y, long ys) {
-  __shared__ f4 red[4][64];
+  __shared__ f4 red[SG_W][64];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int lr = lane & 15, lg = lane >> 4;
   const int n0 = blockIdx.x * 16;
@@ -30,14 +32,14 @@ __global__ __launch_bounds__(256) void small_gemm_kernel(const bf16_t* __restric
   const uint16_t* wr = reinterpret_cast<const uint16_t*>(W) + (long)n * K + 8 * lg;
   const int nsteps = K / 32;
   f4 acc = f4_zero();
-  // wave w takes steps w, w + 4, ...
+  // wave w takes steps w, w + SG_W, ...
   int s = w;
-  for (; s + 12 < nsteps; s += 16) {
+  for (; s + 3 * SG_W < nsteps; s += 4 * SG_W) {
     sg_u16x8 a[4], b[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      a[u] = *reinterpret_cast<const sg_u16x8*>(xr + 32 * (s + 4 * u));
-      b[u] = *reinterpret_cast<const sg_u16x8*>(wr + 32 * (s + 4 * u));
+      a[u] = *reinterpret_cast<const sg_u16x8*>(xr + 32 * (s + SG_W * u));
+      b[u] = *reinterpret_cast<const sg_u16x8*>(wr + 32 * (s + SG_W * u));
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -45,7 +47,7 @@ __global__ __launch_bounds__(256) void small_gemm_kernel(const bf16_t* __restric
       acc = mma_bf16(__builtin_bit_cast(bf16x8, av), __builtin_bit_cast(bf16x8, b[u]), acc);
     }
   }
-  for (; s < nsteps; s += 4) {
+  for (; s < nsteps; s += SG_W) {
     sg_u16x8 a = *reinterpret_cast<const sg_u16x8*>(xr + 32 * s);
     const sg_u16x8 b = *reinterpret_cast<const sg_u16x8*>(wr + 32 * s);
     if (!live) a = (sg_u16x8){0, 0, 0, 0, 0, 0, 0, 0};
@@ -57,7 +59,7 @@ __global__ __launch_bounds__(256) void small_gemm_kernel(const bf16_t* __restric
     // acc element i of lane (lr, lg): output row 4 lg + i, column n0 + lr
     f4 t = red[0][lane];
 #pragma unroll
-    for (int v = 1; v < 4; ++v) {
+    for (int v = 1; v < SG_W; ++v) {
       const f4 o = red[v][lane];
       t[0] += o[0]; t[1] += o[1]; t[2] += o[2]; t[3] += o[3];
     }
@@ -77,7 +79,7 @@ __global__ __launch_bounds__(256) void small_gemm_kernel(const bf16_t* __restric
 
 hipError_t launch_small_gemm(const void* x, long xs, const void* W, const void* bias, int M, int N, int K, void* y,
                              long ys, hipStream_t st) {
-  small_gemm_kernel<<<dim3((unsigned)((N + 15) / 16)), 256, 0, st>>>((const bf16_t*)x, xs, (const bf16_t*)W,
+  small_gemm_kernel<<<dim3((unsigned)((N + 15) / 16)), 64 * SG_W, 0, st>>>((const bf16_t*)x, xs, (const bf16_t*)W,
                                                                      (const bf16_t*)bias, M, N, K, (bf16_t*)y, ys);
   return hipGetLastError();
 }
