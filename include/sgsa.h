@@ -342,6 +342,19 @@ int sgsa_rope_qk(int dtype, int B, int T, int Hq, int Hk, int D, int pos0, int t
 int sgsa_layer_gates(int dtype, long rows, int H, const void* logits, long row_stride, float* beta, float* gamma,
                      float* budget, void* stream);
 
+/* The hybrid decoder's dense causal GQA attention for a block of query rows
+ * (prefill; modelings/hybrid_dense_delta_topk.py:178-192): query row t sits at
+ * position pos0 + t and attends to cache rows [0, pos0 + t].  The reference's
+ * rounding points in bf16: the score product and its 1/sqrt(D) scaling rounded
+ * to bf16, the softmax in fp32, the probabilities rounded to bf16 after
+ * normalisation, fp32 accumulation with V.  bf16 only.  q, out [B, H, Tq, D];
+ * k_cache, v_cache [B, Hkv, cache_len, D] contiguous with rows
+ * [0, pos0 + Tq) filled; D = 128, H a multiple of Hkv.  workspace: B*H*Tq*8
+ * bytes (each row's softmax maximum and sum). */
+int sgsa_dense_attention(int dtype, int B, int H, int Hkv, int D, int Tq, int pos0, const void* q,
+                         const void* k_cache, const void* v_cache, long cache_len, void* out, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
 /* The hybrid decoder's dense GQA attention for one decode token per sequence
  * (modelings/hybrid_dense_delta_topk.py:178-192 at q_len = 1, the query at
  * position kend - 1): o = softmax(q K^T / sqrt(D)) V over cache rows

@@ -72,6 +72,7 @@ SIGNATURES = {
     "sgsa_silu_mul": (_I, [_I, ctypes.c_long, _I, _P, ctypes.c_long, _P, _P]),
     "sgsa_layer_gates": (_I, [_I, ctypes.c_long, _I, _P, ctypes.c_long, _P, _P, _P, _P]),
     "sgsa_rope_qk": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _P, ctypes.c_long, _P, _P, _P, _P, _P]),
+    "sgsa_dense_attention": (_I, [_I, _I, _I, _I, _I, _I, _I, _P, _P, _P, ctypes.c_long, _P, _P, ctypes.c_size_t, _P]),
     "sgsa_decode_attention_workspace_size": (_I, [_I, _I, _I, _I, ctypes.POINTER(ctypes.c_size_t)]),
     "sgsa_decode_attention": (_I, [_I, _I, _I, _I, _I, _P, _P, _P, ctypes.c_long, _I, _P, _P, ctypes.c_size_t, _P]),
     "sgsa_decode_split": (_I, [_I, _I, _I, _I, _P, ctypes.c_long, _P, _P, _P, _P, _P, _P, _P, _P, _P,

@@ -811,6 +811,27 @@ int sgsa_layer_gates(int dtype, long rows, int H, const void* logits, long row_s
                     "sgsa_layer_gates");
 }
 
+int sgsa_dense_attention(int dtype, int B, int H, int Hkv, int D, int Tq, int pos0, const void* q,
+                         const void* k_cache, const void* v_cache, long cache_len, void* out, void* workspace,
+                         size_t workspace_bytes, void* stream) {
+  if (int s = check_dtype(dtype)) return s;
+  if (dtype != SGSA_BF16) return fail(SGSA_ERR_UNSUPPORTED, "sgsa_dense_attention takes bf16");
+  if (B < 0 || Tq < 0 || pos0 < 0 || H <= 0 || Hkv <= 0 || H % Hkv != 0)
+    return fail(SGSA_ERR_INVALID_ARG, "B=%d H=%d Hkv=%d Tq=%d pos0=%d", B, H, Hkv, Tq, pos0);
+  if (D != 128) return fail(SGSA_ERR_UNSUPPORTED, "sgsa_dense_attention needs D == 128 (got %d)", D);
+  if ((long)pos0 + Tq > cache_len) return fail(SGSA_ERR_INVALID_ARG, "pos0 + Tq = %ld exceeds cache_len %ld", (long)pos0 + Tq, cache_len);
+  if (((long)pos0 + Tq) * 256L >= 0x7fffffffL) return fail(SGSA_ERR_UNSUPPORTED, "too many cached keys for 32-bit offsets");
+  const long nqb2 = (Tq + 127) / 128;
+  if ((long)B * H * nqb2 > 0x7fffffffL) return fail(SGSA_ERR_UNSUPPORTED, "grid too large");
+  if (B == 0 || Tq == 0) return SGSA_OK;
+  REQUIRE(q); REQUIRE(k_cache); REQUIRE(v_cache); REQUIRE(out); REQUIRE(workspace);
+  const size_t need = (size_t)B * H * Tq * 8;
+  if (workspace_bytes < need) return fail(SGSA_ERR_WORKSPACE, "workspace of %zu bytes, need %zu", workspace_bytes, need);
+  return hip_status(sgsa::launch_dense_attn(q, k_cache, v_cache, B, H, Hkv, Tq, pos0, cache_len, (float2*)workspace, out,
+                                            (hipStream_t)stream),
+                    "sgsa_dense_attention");
+}
+
 int sgsa_decode_attention_workspace_size(int dtype, int B, int H, int kend, size_t* bytes) {
   REQUIRE(bytes);
   if (int s = check_dtype(dtype)) return s;

@@ -846,6 +846,257 @@ __global__ __launch_bounds__(256, 2) void gather_thr_kernel(GatherArgs a, const 
   }
 }
 
+// ---------------------------------------------------------------------------
+// Dense causal GQA attention for prefill (the hybrid decoder's dense layers,
+// modelings/hybrid_dense_delta_topk.py:178-192) with the reference's rounding
+// points: s = bf16(bf16(q.k) * 1/sqrt(d)), p = bf16(exp(s - max) / sum) with
+// the softmax in fp32 over every causal key, o = bf16(sum p v) in fp32.
+// Because p is rounded after normalisation, the row maximum and sum come
+// first: PASS 1 walks the causal keys for them (scores only, K tiles only);
+// PASS 2 walks them again, forms p and accumulates p V.  The K/V tiles, the
+// score operand layout and the transposing reads are those of
+// gather_thr_kernel: 128 query rows per block, 32 per wave.
+//   q, out [B, H, Tq, D]; k, v [B, Hkv, L, D] (a cache of L rows, keys
+//   [0, pos0 + Tq) valid); query row t sits at key position pos0 + t.
+struct DenseAttnArgs {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  int B, H, Hkv, Tq, pos0;
+  long L;
+  float scale;
+  float2* stats;   // [B, H, Tq]: (max, sum of exp(s - max))
+  uint16_t* out;
+};
+
+template <int PASS>
+__global__ __launch_bounds__(256, 2) void dense_attn_kernel(DenseAttnArgs a, int nqb2) {
+  __shared__ __align__(16) uint16_t K0[KT * RP], V0[PASS == 2 ? KT * RP : 8], K1[KT * RP], V1[PASS == 2 ? KT * RP : 8];
+
+  const int BH = a.B * a.H;
+  const int bid = blockIdx.x;
+  const int bh = bid % BH;
+  const int qb2 = nqb2 - 1 - bid / BH;   // heaviest row blocks first
+  const int b = bh / a.H, h = bh % a.H, kh = h / (a.H / a.Hkv);
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lr = lane & 15, lg = lane >> 4;
+  const int Tq = a.Tq;
+  const int Tk = a.pos0 + Tq;   // valid keys
+  const int r0 = qb2 * QL;
+  const int wr0 = r0 + 32 * w;
+  const int kend = min(Tk, min(Tq, r0 + QL) + a.pos0);
+  const int ntile = (kend + KT - 1) / KT;
+
+  const long hbase = ((long)(b * a.Hkv + kh) * a.L) * DP;
+  const int rbytes = DP * 2;
+  const int nrec = Tk * rbytes;
+  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.k + hbase), 0, nrec, 0x00020000);
+  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.v + hbase), 0, nrec, 0x00020000);
+  int doff[5];
+#pragma unroll
+  for (int t = 0; t < 5; ++t) {
+    const int slot = 64 * (w + 4 * t) + lane;
+    const int r = slot / 18, p = slot % 18;
+    const int c = p < 16 ? p ^ ((r >> 3) & 1) : 0;
+    doff[t] = tile_row_key(min(r, KT - 1)) * rbytes + 16 * c;
+  }
+  auto dma = [&](int kt, uint16_t* Kd, uint16_t* Vd) __attribute__((always_inline)) {
+    const int toff = kt * KT * rbytes;
+#pragma unroll
+    for (int t = 0; t < 5; ++t) {
+      const int i = w + 4 * t;
+      if (i < TILE_SLOTS / 64) {   // wave-uniform
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (__attribute__((address_space(3))) void*)(Kd + 512 * i), 16,
+                                                 doff[t] + toff, 0, 0, 0);
+        if constexpr (PASS == 2)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (__attribute__((address_space(3))) void*)(Vd + 512 * i), 16,
+                                                   doff[t] + toff, 0, 0, 0);
+      }
+    }
+  };
+  // a tile reaching past the valid keys: those LDS rows must hold finite values (their weights are 0)
+  if (Tk % KT != 0) {
+    uint4* z[2] = {reinterpret_cast<uint4*>(K0), reinterpret_cast<uint4*>(K1)};
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+      for (int i = tid; i < KT * RP / 8; i += 256) z[u][i] = make_uint4(0, 0, 0, 0);
+    if constexpr (PASS == 2) {
+      uint4* zv[2] = {reinterpret_cast<uint4*>(V0), reinterpret_cast<uint4*>(V1)};
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+        for (int i = tid; i < KT * RP / 8; i += 256) zv[u][i] = make_uint4(0, 0, 0, 0);
+    }
+    __syncthreads();
+  }
+
+  // the lane's rows wr0 + 16 mt + lr: q (B operand of the score product) and the causal end
+  bf16x8 qf[2][4];
+  int nv[2];
+  float mrow[2], ilrow[2];   // PASS 2: the row's maximum and 1 / sum
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt) {
+    const int row = wr0 + 16 * mt + lr;
+    const bool live = row < Tq;
+    const uint16_t* qp = a.q + (((long)b * a.H + h) * Tq + (live ? row : 0)) * DP + 8 * lg;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      u16x8 raw = *reinterpret_cast<const u16x8*>(qp + 32 * s);
+      if (!live) raw = (u16x8){0, 0, 0, 0, 0, 0, 0, 0};
+      qf[mt][s] = __builtin_bit_cast(bf16x8, raw);
+    }
+    nv[mt] = live ? min(Tk, row + a.pos0 + 1) : 0;
+    mrow[mt] = 0.f;
+    ilrow[mt] = 0.f;
+    if constexpr (PASS == 2) {
+      if (live) {
+        const float2 st = a.stats[((long)b * a.H + h) * Tq + row];
+        mrow[mt] = st.x;
+        ilrow[mt] = 1.0f / st.y;
+      }
+    }
+  }
+  const int wmin = wr0 + 31 < Tq ? min(Tk, wr0 + a.pos0 + 1) : 0;   // keys below are causal for every row of the wave
+
+  float ml[2] = {-INFINITY, -INFINITY}, ll[2] = {0.f, 0.f};   // PASS 1: the lane's running max and sum
+  f4 ov_[2][PASS == 2 ? DP / 16 : 1];
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int n = 0; n < (PASS == 2 ? DP / 16 : 1); ++n) ov_[mt][n] = f4_zero();
+
+  const int s_off = lr * RP + 8 * (lg ^ (lr >> 3));
+  const int t_off = (4 * lg + (lr >> 2)) * RP + 8 * (((lr & 3) >> 1) ^ (lg >> 1)) + 4 * (lr & 1);
+  const float scale = a.scale;
+
+  auto chunk = [&](bool full, const uint16_t* Kc, const uint16_t* Vc, int sp, int t0) __attribute__((always_inline)) {
+    uint32_t pw[2][4];
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      f4 sc[2] = {f4_zero(), f4_zero()};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const uint4 kf = *reinterpret_cast<const uint4*>(&Kc[(32 * sp + 16 * hf) * RP + s_off + 32 * s]);
+        sc[0] = mma_bf16(as_bf8(kf), qf[0][s], sc[0]);
+        sc[1] = mma_bf16(as_bf8(kf), qf[1][s], sc[1]);
+      }
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        float sv[4];
+        bool ok[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int j = t0 + 32 * sp + 8 * lg + 4 * hf + i;
+          ok[i] = full || j < nv[mt];
+          // the product rounded to bf16, scaled, rounded again (the reference's bf16 matmul and scaling)
+          sv[i] = bf16_to_f32(f32_to_bf16(bf16_to_f32(f32_to_bf16(sc[mt][i])) * scale));
+        }
+        if constexpr (PASS == 1) {
+          float tm = -INFINITY;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) tm = fmaxf(tm, ok[i] ? sv[i] : -INFINITY);
+          const float mn = fmaxf(ml[mt], tm);
+          if (mn > -INFINITY) {
+            float acc = ll[mt] * expf(ml[mt] - mn);   // ml = -inf: exp(-inf) = 0
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc += ok[i] ? expf(sv[i] - mn) : 0.f;
+            ll[mt] = acc;
+            ml[mt] = mn;
+          }
+        } else {
+          float p[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) p[i] = ok[i] ? expf(sv[i] - mrow[mt]) * ilrow[mt] : 0.f;
+          pw[mt][2 * hf] = pack_bf16x2(p[0], p[1]);
+          pw[mt][2 * hf + 1] = pack_bf16x2(p[2], p[3]);
+        }
+      }
+    }
+    if constexpr (PASS == 2) {
+      const uint4 pa[2] = {make_uint4(pw[0][0], pw[0][1], pw[0][2], pw[0][3]),
+                           make_uint4(pw[1][0], pw[1][1], pw[1][2], pw[1][3])};
+      __builtin_amdgcn_sched_barrier(0);
+      const uint16_t* vt_ = Vc + 32 * sp * RP + t_off;
+      auto operands = [&](int n, bf16x8& vb) __attribute__((always_inline)) {
+        const s16x4 v0 = lds_read_tr(vt_ + 16 * n), v1 = lds_read_tr(vt_ + 16 * RP + 16 * n);
+        vb = __builtin_bit_cast(bf16x8, __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7));
+      };
+      bf16x8 vb[2];
+      operands(0, vb[0]);
+#pragma unroll
+      for (int n = 0; n < DP / 16; ++n) {
+        if (n + 1 < DP / 16) operands(n + 1, vb[(n + 1) & 1]);
+        ov_[0][n] = mma_bf16(as_bf8(pa[0]), vb[n & 1], ov_[0][n]);
+        ov_[1][n] = mma_bf16(as_bf8(pa[1]), vb[n & 1], ov_[1][n]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  };
+  auto tile = [&](int kt, const uint16_t* Kc, const uint16_t* Vc) __attribute__((always_inline)) {
+    const int t0 = kt * KT;
+    const bool full = t0 + KT <= wmin;
+#pragma unroll
+    for (int sp = 0; sp < KT / 32; ++sp) chunk(full, Kc, Vc, sp, t0);
+  };
+
+  dma(0, K0, V0);
+  for (int kt = 0; kt < ntile; kt += 2) {
+    __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): this wave's loads of tile kt are done
+    __syncthreads();                      // ... every wave's; buffer 1 is free
+    if (kt + 1 < ntile) dma(kt + 1, K1, V1);
+    tile(kt, K0, V0);
+    if (kt + 1 < ntile) {
+      __builtin_amdgcn_s_waitcnt(0x0f70);
+      __syncthreads();
+      if (kt + 2 < ntile) dma(kt + 2, K0, V0);
+      tile(kt + 1, K1, V1);
+    }
+  }
+
+  if constexpr (PASS == 1) {
+    // lanes lr, lr + 16, lr + 32, lr + 48 hold row lr's keys
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      float m = ml[mt], l = ll[mt];
+#pragma unroll
+      for (int o = 16; o < 64; o <<= 1) {
+        const float m2 = __shfl_xor(m, o, 64), l2 = __shfl_xor(l, o, 64);
+        const float mn = fmaxf(m, m2);
+        l = (m > -INFINITY ? l * expf(m - mn) : 0.f) + (m2 > -INFINITY ? l2 * expf(m2 - mn) : 0.f);
+        m = mn;
+      }
+      const int row = wr0 + 16 * mt + lr;
+      if (lg == 0 && row < Tq) a.stats[((long)b * a.H + h) * Tq + row] = make_float2(m, l);
+    }
+  } else {
+    // accumulator element e of lane (lr, lg): row 16 mt + 4 lg + e of the wave, dim 16 n + lr
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = wr0 + 16 * mt + 4 * lg + e;
+        if (row < Tq) {
+          uint16_t* op = a.out + (((long)b * a.H + h) * Tq + row) * DP + lr;
+#pragma unroll
+          for (int n = 0; n < DP / 16; ++n) op[16 * n] = f32_to_bf16(ov_[mt][n][e]);
+        }
+      }
+  }
+}
+
+hipError_t launch_dense_attn(const void* q, const void* k, const void* v, int B, int H, int Hkv, int Tq, int pos0,
+                             long L, float2* stats, void* out, hipStream_t st) {
+  DenseAttnArgs a{};
+  a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v;
+  a.B = B; a.H = H; a.Hkv = Hkv; a.Tq = Tq; a.pos0 = pos0; a.L = L;
+  a.scale = (float)(1.0 / 11.313708498984761);   // 1 / sqrt(128), as the fp32 of the double
+  a.stats = stats; a.out = (uint16_t*)out;
+  const int nqb2 = (Tq + QL - 1) / QL;
+  const dim3 grid((unsigned)(B * H * nqb2));
+  dense_attn_kernel<1><<<grid, 256, 0, st>>>(a, nqb2);
+  dense_attn_kernel<2><<<grid, 256, 0, st>>>(a, nqb2);
+  return hipGetLastError();
+}
+
 hipError_t launch_sparse_gather_staged(const GatherArgs& a, const int32_t* split, hipStream_t st) {
   const int nqb = (a.Tq + QB - 1) / QB;
   gather_tile_kernel<<<dim3((unsigned)(a.B * a.H * nqb)), 256, 0, st>>>(a, split, nqb);

@@ -277,5 +277,7 @@ hipError_t launch_sparse_gather_lists(const GatherArgs& a, const uint2* tl_list,
 // cut (score threshold, tie index) left by the threshold-mode K1.
 hipError_t launch_sparse_gather_thr(const GatherArgs& a, const void* q, const uint2* thr, float mscale,
                                     hipStream_t st);
+hipError_t launch_dense_attn(const void* q, const void* k, const void* v, int B, int H, int Hkv, int Tq, int pos0,
+                             long L, float2* stats, void* out, hipStream_t st);
 
 }  // namespace sgsa

@@ -113,6 +113,8 @@ def gqa_attention(q: Tensor, k: Tensor, v: Tensor, pos0: int, block: int = 1024)
     G = H // Hkv
     if Tq == 1 and _decode_attention_fits(q, k, v, pos0):
         return _decode_attention(q, k, v)
+    if Tq > 1 and _dense_attention_fits(q, k, v, pos0):
+        return _dense_attention(q, k, v, pos0)
     out = torch.empty_like(q)
     qg = q.reshape(B, Hkv, G, Tq, D)
     kpos = torch.arange(k.shape[2], device=q.device)
@@ -178,6 +180,30 @@ def _decode_attention(q: Tensor, k: Tensor, v: Tensor) -> Tensor:
     out = torch.empty_like(q)
     _abi.check(L.sgsa_decode_attention(code, B, H, Hkv, D, _abi.ptr(q), _abi.ptr(k), _abi.ptr(v), _cache_view_len(k),
                                        kend, _abi.ptr(out), _abi.ptr(ws), nb.value, _abi.stream_of(q)))
+    return out
+
+
+def _dense_attention_fits(q: Tensor, k: Tensor, v: Tensor, pos0: int) -> bool:
+    """Whether sgsa_dense_attention takes this call: bf16, no autograd, D = 128, q contiguous,
+    k / v views of contiguous caches ending at the block's last position."""
+    B, H, Tq, D = q.shape
+    Hkv = k.shape[1]
+    return (not torch.is_grad_enabled() and q.is_cuda and q.dtype == torch.bfloat16 and D == 128 and H % Hkv == 0
+            and k.dtype == q.dtype and v.dtype == q.dtype and q.is_contiguous() and k.shape == v.shape
+            and k.shape[2] == pos0 + Tq and _cache_view_len(k) > 0 and _cache_view_len(k) == _cache_view_len(v)
+            and (pos0 + Tq) * 256 < 2 ** 31 - 1)
+
+
+def _dense_attention(q: Tensor, k: Tensor, v: Tensor, pos0: int) -> Tensor:
+    """gqa_attention for a block of query rows in two HIP passes over the cache
+    (sgsa_dense_attention): each row's softmax maximum and sum, then p V with the
+    probabilities rounded after normalisation, as the torch form does."""
+    B, H, Tq, D = q.shape
+    ws = torch.empty(B * H * Tq * 8, device=q.device, dtype=torch.uint8)
+    out = torch.empty_like(q)
+    _abi.check(_abi.lib().sgsa_dense_attention(_abi.dtype_code(q.dtype), B, H, k.shape[1], D, Tq, pos0, _abi.ptr(q),
+                                               _abi.ptr(k), _abi.ptr(v), _cache_view_len(k), _abi.ptr(out),
+                                               _abi.ptr(ws), ws.numel(), _abi.stream_of(q)))
     return out
 
 

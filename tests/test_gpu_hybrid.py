@@ -123,3 +123,36 @@ def test_decode_attention_equals_torch_form(dev, dt, tol, G, kend):
     assert torch.equal(got, via)
     err = ((got.float() - want.float()).abs().max() / want.float().abs().max()).item()
     assert err <= tol, f"{err:.3e}"
+
+
+@pytest.mark.parametrize("G", [1, 4])
+@pytest.mark.parametrize("Tq,pos0", [(64, 0), (200, 0), (130, 57), (1000, 300)])
+def test_dense_attention_equals_torch_form(dev, G, Tq, pos0):
+    # a block of query rows at positions pos0 .. over a cache view: the two HIP passes
+    # (sgsa_dense_attention, taken by gqa_attention in bf16) against the torch form with the same
+    # rounding points (bf16 scores and scaling, fp32 softmax, bf16 probabilities); relative to max |o|
+    from sgsa_amd.hybrid import _dense_attention, _dense_attention_fits, gqa_attention
+    import math
+    B, Hkv, D, L = 2, 2, 128, 1400
+    H = G * Hkv
+    dt = torch.bfloat16
+    g = torch.Generator().manual_seed(Tq + pos0 + G)
+    q = torch.randn(B, H, Tq, D, generator=g).to(dt).to(dev)
+    kc = torch.randn(B, Hkv, L, D, generator=g).to(dt).to(dev)
+    vc = torch.randn(B, Hkv, L, D, generator=g).to(dt).to(dev)
+    kend = pos0 + Tq
+    k, v = kc[:, :, :kend], vc[:, :, :kend]
+    with torch.no_grad():
+        assert _dense_attention_fits(q, k, v, pos0)
+        got = _dense_attention(q, k, v, pos0)
+        via = gqa_attention(q, k, v, pos0)
+    qg = q.reshape(B, Hkv, G * Tq, D)
+    s = (torch.matmul(qg, k.transpose(-1, -2).contiguous()) * (1.0 / math.sqrt(D))).float()   # [B,Hkv,G*Tq,kend]
+    qpos = (pos0 + torch.arange(Tq, device=dev)).repeat(G)
+    s = s.masked_fill(torch.arange(kend, device=dev)[None, :] > qpos[:, None], float("-inf"))
+    p = torch.softmax(s, dim=-1).to(dt)
+    want = torch.matmul(p, v.contiguous()).reshape(B, H, Tq, D)
+    torch.cuda.synchronize()
+    assert torch.equal(got, via)
+    err = ((got.float() - want.float()).abs().max() / want.float().abs().max()).item()
+    assert err <= 1e-2, f"{err:.3e}"
