@@ -27,7 +27,7 @@ from typing import Optional, Tuple
 import torch
 
 from . import _abi
-from .recurrent import fused_recurrent_sgsa
+from .recurrent import fused_recurrent_sgsa, recurrent_sgsa_fwd
 
 Tensor = torch.Tensor
 
@@ -130,6 +130,8 @@ def sgsa_decode_step(
         _abi.ptr(sc), _abi.ptr(top2), _abi.ptr(cnt), _abi.ptr(bud), mode, float(alpha_max), float(tau_c), 64, 8,
         _abi.ptr(wk if mode == 0 else None), _abi.ptr(vh), _abi.ptr(wk if mode == 1 else None), _abi.ptr(al),
         None, None, _abi.ptr(gws), gn, _abi.stream_of(kc)))
-    # 3. the recurrent update for this token
-    o, st = fused_recurrent_sgsa(q, k, v, beta, gamma, wk, vh, al, state, output_final_state=True)
+    # 3. the recurrent update for this token (without autograd, the forward itself: the autograd
+    # Function's dispatch costs more host time than the kernel)
+    rec = fused_recurrent_sgsa if torch.is_grad_enabled() else recurrent_sgsa_fwd
+    o, st = rec(q, k, v, beta, gamma, wk, vh, al, state, output_final_state=True)
     return (o, st, (idx, cnt)) if return_candidates else (o, st)

@@ -25,6 +25,7 @@ restatement of modelings/hybrid_dense_delta_topk.py:94-117.  Forward only.
 from __future__ import annotations
 
 from dataclasses import dataclass
+import ctypes
 from typing import Dict, Optional, Tuple
 
 import torch
@@ -123,20 +124,44 @@ def linear_rows(x: Tensor, weight: Tensor, bias: Optional[Tensor] = None) -> Ten
     """F.linear(x, weight, bias).  Without autograd, for bf16 x of at most 16 rows (a decode
     step's tokens), one sgsa_linear_rows launch: a library GEMM's host dispatch costs more
     than such a product."""
-    K = x.shape[-1]
+    shape = x.shape
+    K = shape[-1]
     M = x.numel() // K if K else 0
-    if torch.is_grad_enabled() or not x.is_cuda or x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16 \
-            or not 1 <= M <= 16 or K % 32 != 0 or not weight.is_contiguous() \
-            or (bias is not None and (bias.dtype != torch.bfloat16 or not bias.is_contiguous())):
+    if M > 16 or M < 1 or K % 32 != 0 or x.dtype != _BF16 or weight.dtype != _BF16 or torch.is_grad_enabled() \
+            or not x.is_cuda or not _weight_ok(weight, bias):
         return F.linear(x, weight, bias)
-    x2 = x.reshape(M, K)
-    if x2.stride(-1) != 1 or x2.stride(0) % 8 != 0 or x2.data_ptr() % 16 != 0 or weight.data_ptr() % 16 != 0:
+    x2 = x if x.dim() == 2 else x.reshape(M, K)
+    xs = x2.stride(0) if M > 1 else K
+    xp = x2.data_ptr()
+    if x2.stride(-1) != 1 or xs % 8 != 0 or xp % 16 != 0:
         return F.linear(x, weight, bias)
     N = weight.shape[0]
-    y = torch.empty(*x.shape[:-1], N, device=x.device, dtype=x.dtype)
-    _abi.check(_abi.lib().sgsa_linear_rows(_abi.dtype_code(x.dtype), M, N, K, _abi.ptr(x2), x2.stride(0),
-                                           _abi.ptr(weight), _abi.ptr(bias), _abi.ptr(y), N, _abi.stream_of(x)))
+    y = torch.empty(shape[:-1] + (N,), device=x.device, dtype=_BF16)
+    _abi.check(_LINEAR_ROWS(_abi.SGSA_BF16, M, N, K, ctypes.c_void_p(xp), xs, ctypes.c_void_p(weight.data_ptr()),
+                            _abi.ptr(bias), ctypes.c_void_p(y.data_ptr()), N, _abi.stream_of(x)))
     return y
+
+
+_BF16 = torch.bfloat16
+_LINEAR_ROWS = None
+_WEIGHT_OK: dict = {}
+
+
+def _weight_ok(weight: Tensor, bias: Optional[Tensor]) -> bool:
+    """weight (and bias) fit sgsa_linear_rows: bf16, contiguous, 16-byte aligned; remembered per
+    (storage, version) pair, and the library's entry point looked up once."""
+    global _LINEAR_ROWS
+    key = (weight.data_ptr(), weight._version, None if bias is None else (bias.data_ptr(), bias._version))
+    ok = _WEIGHT_OK.get(key)
+    if ok is None:
+        ok = weight.is_contiguous() and weight.data_ptr() % 16 == 0 and \
+            (bias is None or (bias.dtype == _BF16 and bias.is_contiguous()))
+        if len(_WEIGHT_OK) > 4096:
+            _WEIGHT_OK.clear()
+        _WEIGHT_OK[key] = ok
+        if _LINEAR_ROWS is None:
+            _LINEAR_ROWS = _abi.lib().sgsa_linear_rows
+    return ok
 
 
 def lin(module: nn.Linear, x: Tensor) -> Tensor:
