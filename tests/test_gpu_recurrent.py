@@ -154,9 +154,11 @@ def test_decode_with_topk_reuse_matches_the_oracle(dev, dtype, tol, D):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_score_at_is_the_dot_product(dev, dtype):
+@pytest.mark.parametrize("D,n", [(96, 40), (128, 300)])
+def test_score_at_is_the_dot_product(dev, dtype, D, n):
     # sgsa_score_at: q . k[idx] / sqrt(D) at given keys, slots past the count untouched
-    B, Tq, Tk, H, D, n = 2, 3, 300, 2, 96, 40
+    # (bf16 at D = 128 takes the 16-byte-load path, 16 keys in flight per wave)
+    B, Tq, Tk, H = 2, 3, 300, 2
     g = torch.Generator().manual_seed(12)
     q = torch.randn(B, Tq, H, D, generator=g).to(dtype)
     kk = torch.randn(B, Tk, H, D, generator=g).to(dtype)
