@@ -858,6 +858,10 @@ __global__ __launch_bounds__(256, 2) void gather_thr_kernel(GatherArgs a, const 
 // gather_thr_kernel: 128 query rows per block, 32 per wave.
 //   q, out [B, H, Tq, D]; k, v [B, Hkv, L, D] (a cache of L rows, keys
 //   [0, pos0 + Tq) valid); query row t sits at key position pos0 + t.
+// e^x as 2^(x log2 e) on v_exp_f32 (relative error below 1e-5 for the |x| < 100 a softmax
+// meets, far inside the bf16 rounding of the probabilities); e^-inf = 0.
+__device__ __forceinline__ float dexp(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
+
 struct DenseAttnArgs {
   const uint16_t* q;
   const uint16_t* k;
@@ -996,16 +1000,16 @@ __global__ __launch_bounds__(256, 2) void dense_attn_kernel(DenseAttnArgs a, int
           for (int i = 0; i < 4; ++i) tm = fmaxf(tm, ok[i] ? sv[i] : -INFINITY);
           const float mn = fmaxf(ml[mt], tm);
           if (mn > -INFINITY) {
-            float acc = ll[mt] * expf(ml[mt] - mn);   // ml = -inf: exp(-inf) = 0
+            float acc = ll[mt] * dexp(ml[mt] - mn);   // ml = -inf: exp(-inf) = 0
 #pragma unroll
-            for (int i = 0; i < 4; ++i) acc += ok[i] ? expf(sv[i] - mn) : 0.f;
+            for (int i = 0; i < 4; ++i) acc += ok[i] ? dexp(sv[i] - mn) : 0.f;
             ll[mt] = acc;
             ml[mt] = mn;
           }
         } else {
           float p[4];
 #pragma unroll
-          for (int i = 0; i < 4; ++i) p[i] = ok[i] ? expf(sv[i] - mrow[mt]) * ilrow[mt] : 0.f;
+          for (int i = 0; i < 4; ++i) p[i] = ok[i] ? dexp(sv[i] - mrow[mt]) * ilrow[mt] : 0.f;
           pw[mt][2 * hf] = pack_bf16x2(p[0], p[1]);
           pw[mt][2 * hf + 1] = pack_bf16x2(p[2], p[3]);
         }
@@ -1061,7 +1065,7 @@ __global__ __launch_bounds__(256, 2) void dense_attn_kernel(DenseAttnArgs a, int
       for (int o = 16; o < 64; o <<= 1) {
         const float m2 = __shfl_xor(m, o, 64), l2 = __shfl_xor(l, o, 64);
         const float mn = fmaxf(m, m2);
-        l = (m > -INFINITY ? l * expf(m - mn) : 0.f) + (m2 > -INFINITY ? l2 * expf(m2 - mn) : 0.f);
+        l = (m > -INFINITY ? l * dexp(m - mn) : 0.f) + (m2 > -INFINITY ? l2 * dexp(m2 - mn) : 0.f);
         m = mn;
       }
       const int row = wr0 + 16 * mt + lr;
