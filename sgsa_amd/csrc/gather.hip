@@ -260,31 +260,35 @@ __global__ __launch_bounds__(256) void sparse_gather_kernel(GatherArgs a, int lp
       gather_step<X, VEC>(a, j, wgt, nstep, K, V, b, h, grp, sub, lpr, ak, av);
     }
   } else {
-    // merge the row's partials (gather_part_kernel) in split order
-    const float* P = a.part + row * (long)a.nsplit * (4 + 2 * D);
+    // merge the row's partials (gather_part_kernel): lane c takes partials c, c + 64, .. for the
+    // sums and top-2 pairs; lane group g adds partials g, g + 64 / lpr, .. to the row vectors
+    // (the groups are summed below).  Every load after the maximum is independent of the others.
+    const long pst = 4 + 2 * (long)D;
+    const int ns = a.nsplit;
+    const float* P = a.part + row * (long)ns * pst;
     if (!fixed_max) {
       float mc = -INFINITY;
-      for (int c = lane; c < a.nsplit; c += 64) mc = fmaxf(mc, P[(long)c * (4 + 2 * D)]);
+      for (int c = lane; c < ns; c += 64) mc = fmaxf(mc, P[c * pst]);
       mrun = wave_max(mc);
     }
-    for (int c = 0; c < a.nsplit; ++c) {
-      const float* pc = P + (long)c * (4 + 2 * D);
+    for (int c = lane; c < ns; c += 64) {
+      const float* pc = P + c * pst;
       const float f = pc[0] == -INFINITY ? 0.f : __expf(pc[0] - mrun);
-      if (lane == 0) {
-        esum += pc[1] * f;
-        const float u1 = pc[2], u2 = pc[3];
-        const float hi = fmaxf(t1, u1), lo = fmaxf(fminf(t1, u1), fmaxf(t2, u2));
-        t1 = hi;
-        t2 = lo;
-      }
-      if (grp == 0) {
+      esum += pc[1] * f;
+      const float u1 = pc[2], u2 = pc[3];
+      const float hi = fmaxf(t1, u1), lo = fmaxf(fminf(t1, u1), fmaxf(t2, u2));
+      t1 = hi;
+      t2 = lo;
+    }
+    for (int c = grp; c < ns; c += 64 / lpr) {
+      const float* pc = P + c * pst;
+      const float f = pc[0] == -INFINITY ? 0.f : __expf(pc[0] - mrun);
 #pragma unroll
-        for (int i = 0; i < NE; ++i) {
-          const int d = elem_d<X, VEC>(sub, i, lpr);
-          if (d < D) {
-            ak[i] += pc[4 + d] * f;
-            av[i] += pc[4 + D + d] * f;
-          }
+      for (int i = 0; i < NE; ++i) {
+        const int d = elem_d<X, VEC>(sub, i, lpr);
+        if (d < D) {
+          ak[i] += pc[4 + d] * f;
+          av[i] += pc[4 + D + d] * f;
         }
       }
     }
@@ -473,7 +477,7 @@ __global__ void zero_int_kernel(int32_t* p) {
 // wave (row, c) accumulates slots [c*split_len, (c+1)*split_len) of the row
 // and writes its partial {max, sum, top-1, top-2, ak[D], av[D]}
 // (unnormalised, relative to that max); sparse_gather_kernel merges a row's
-// partials in split order, then runs its epilogue unchanged.
+// partials in a fixed order, then runs its epilogue unchanged.
 template <typename X, bool VEC>
 __global__ __launch_bounds__(256) void gather_part_kernel(GatherArgs a, int lpr) {
   constexpr int NE = GatherShape<X, VEC>::NE;
