@@ -17,7 +17,7 @@ from oracle import sgsa_oracle as O
 
 pytestmark = pytest.mark.gpu
 
-sgsa_amd = pytest.importorskip("sgsa_amd")
+import sgsa_amd  # noqa: E402  (pure Python; the HIP library loads on first call and raises if missing)
 
 ORDER = ["q", "k", "v", "beta", "gamma", "sparse_k", "sparse_v", "alpha", "initial_state"]
 

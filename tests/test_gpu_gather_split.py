@@ -14,7 +14,7 @@ import torch
 
 pytestmark = pytest.mark.gpu
 
-sgsa_amd = pytest.importorskip("sgsa_amd")
+import sgsa_amd  # noqa: E402  (pure Python; the HIP library loads on first call and raises if missing)
 from sgsa_amd import _abi  # noqa: E402
 from sgsa_amd.retrieval import score_topk  # noqa: E402
 

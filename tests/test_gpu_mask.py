@@ -24,7 +24,7 @@ from tolerance import close
 
 pytestmark = pytest.mark.gpu
 
-sgsa_amd = pytest.importorskip("sgsa_amd")
+import sgsa_amd  # noqa: E402  (pure Python; the HIP library loads on first call and raises if missing)
 
 FMIN = torch.finfo(torch.float32).min
 

@@ -28,7 +28,7 @@ from tolerance import close, scalar_close
 
 pytestmark = pytest.mark.gpu
 
-sgsa_amd = pytest.importorskip("sgsa_amd")
+import sgsa_amd  # noqa: E402  (pure Python; the HIP library loads on first call and raises if missing)
 
 B, T, H, D, K = 1, 32768, 16, 128, 2048
 # (head, row): two rows per head, covering t < k, the k boundary, mid sequence and the end
