@@ -24,6 +24,8 @@
 // candidate's score is bit-identical to the value its block max was taken on.
 #include <float.h>
 
+#include <type_traits>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -374,11 +376,13 @@ __global__ __launch_bounds__(256) void block_max_mfma_kernel(BlockArgs a, float 
 // shared between waves.  Same operands, k-position order and score_of() as
 // block_cand_kernel's scorer, so scores agree bit for bit.
 // MK: the call has a padding mask (a separate instantiation keeps the unmasked
-// sweep's registers as they are).
-template <bool MK>
+// sweep's registers as they are).  NKS = D / 32 is a template argument: with D
+// known, the k-steps' loads and MFMAs are straight-line code with no branch
+// each, and the compiler interleaves them.
+template <bool MK, int NKS>
 __global__ __launch_bounds__(256, 2) void block_max_reg_kernel(BlockArgs a, float mscale) {
   constexpr int QR = BMM_ROWS, NG = QR / 16, TK = 128;
-  const int D = a.D, T = a.T, H = a.H, bs = a.bs, nb = a.nb, nks = D / 32;
+  const int D = NKS * 32, T = a.T, H = a.H, bs = a.bs, nb = a.nb;
   const int nrb = (T + QR - 1) / QR;
   const int bh = blockIdx.y, b = bh / H, h = bh % H;
   const int r0 = (nrb - 1 - (int)blockIdx.x) * QR;
@@ -388,14 +392,14 @@ __global__ __launch_bounds__(256, 2) void block_max_reg_kernel(BlockArgs a, floa
   const uint16_t* K = reinterpret_cast<const uint16_t*>(a.k) + ((long)b * T * H + h) * D;
   const long kstride = (long)H * D;
 
-  bf16x8 qf[NG][BLK_MAX_D / 32];
+  bf16x8 qf[NG][NKS];
 #pragma unroll
   for (int g = 0; g < NG; ++g) {
     const int qr = r0 + 16 * g + lr;
 #pragma unroll
-    for (int s = 0; s < BLK_MAX_D / 32; ++s) {
+    for (int s = 0; s < NKS; ++s) {
       u16x8 raw = {0, 0, 0, 0, 0, 0, 0, 0};
-      if (s < nks && qr < T) raw = *reinterpret_cast<const u16x8*>(Q + ((long)(b * T + qr) * H + h) * D + 32 * s + 8 * lg);
+      if (qr < T) raw = *reinterpret_cast<const u16x8*>(Q + ((long)(b * T + qr) * H + h) * D + 32 * s + 8 * lg);
       qf[g][s] = __builtin_bit_cast(bf16x8, raw);
     }
   }
@@ -420,48 +424,56 @@ __global__ __launch_bounds__(256, 2) void block_max_reg_kernel(BlockArgs a, floa
   }
   const int ntile = (kend + TK - 1) / TK;
   const int krow = (lr >> 2) + 4 * (lr & 3);
-  bf16x8 kf[2][BLK_MAX_D / 32];
-  auto kload = [&](int kt) __attribute__((always_inline)) {
+  // key operands of one tile; without a mask two of them, the next tile's loads issued before
+  // the current tile's MFMAs (the masked form has no registers to spare for it)
+  bf16x8 kf[2][NKS], kn[2][NKS];
+  auto kload = [&](bf16x8 (&kb)[2][NKS], int kt) __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int j = kt * TK + 32 * w + 16 * u + krow;
       const uint16_t* p = K + (long)(j < T ? j : 0) * kstride + 8 * lg;
 #pragma unroll
-      for (int s = 0; s < BLK_MAX_D / 32; ++s) {
-        u16x8 raw = {0, 0, 0, 0, 0, 0, 0, 0};
-        if (s < nks) raw = *reinterpret_cast<const u16x8*>(p + 32 * s);
-        kf[u][s] = __builtin_bit_cast(bf16x8, raw);
-      }
+      for (int s = 0; s < NKS; ++s) kb[u][s] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8*>(p + 32 * s));
     }
   };
-  if (ntile > 0) kload(0);
-  for (int kt = 0; kt < ntile; ++kt) {
-    const int kw = kt * TK + 32 * w;   // the wave's first key
-    const bool full = !MK && kw + 32 <= minvalid;
-    const uint32_t kbits = MK ? (kw < T ? mb[kw >> 5] : 0u) : ~0u;   // keys kw..kw+31
-    float m[2][NG];
+  float m[2][NG];
+  // the block maxima of the wave's keys for each row; FULL: every key of the wave is valid for every row
+  auto tile = [&](const bf16x8 (&kb)[2][NKS], int kw, uint32_t kbits, auto fullt) __attribute__((always_inline)) {
+    constexpr bool FULL = decltype(fullt)::value;
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
 #pragma unroll
       for (int g = 0; g < NG; ++g) {
         f4 c = f4_zero();
 #pragma unroll
-        for (int s = 0; s < BLK_MAX_D / 32; ++s)
-          if (s < nks) c = mma_bf16(kf[u][s], qf[g][s], c);
+        for (int s = 0; s < NKS; ++s) c = mma_bf16(kb[u][s], qf[g][s], c);
         const f4 sc = score_of(c, mscale);
-        const int qr = r0 + 16 * g + lr;
         float mx = -FLT_MAX;
+        if constexpr (FULL) {
+          mx = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), sc[2]), sc[3]);   // the masked chain's order
+        } else {
+          const int qr = r0 + 16 * g + lr;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int key = kw + 16 * u + lg + 4 * i;
-          bool ok = full || (qr < T && key < T && (!a.causal || key <= qr));
-          if (MK) ok = ok && ((qok >> g) & 1u) && ((kbits >> (key - kw)) & 1u);
-          mx = fmaxf(mx, ok ? sc[i] : -FLT_MAX);
+          for (int i = 0; i < 4; ++i) {
+            const int key = kw + 16 * u + lg + 4 * i;
+            bool ok = qr < T && key < T && (!a.causal || key <= qr);
+            if (MK) ok = ok && ((qok >> g) & 1u) && ((kbits >> (key - kw)) & 1u);
+            mx = fmaxf(mx, ok ? sc[i] : -FLT_MAX);
+          }
         }
         m[u][g] = mx;
       }
     }
-    if (kt + 1 < ntile) kload(kt + 1);
+  };
+  auto sweep = [&](const bf16x8 (&kb)[2][NKS], int kt) __attribute__((always_inline)) {
+    const int kw = kt * TK + 32 * w;   // the wave's first key
+    const bool full = !MK && kw + 32 <= minvalid;
+    const uint32_t kbits = MK ? (kw < T ? mb[kw >> 5] : 0u) : ~0u;   // keys kw..kw+31
+    if (full) tile(kb, kw, kbits, std::true_type{});
+    else tile(kb, kw, kbits, std::false_type{});
+    return kw;
+  };
+  auto store = [&](int kw) __attribute__((always_inline)) {
     if (kw < kend) {   // wave-uniform: the wave's keys hold a block the rows may see
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
@@ -476,6 +488,22 @@ __global__ __launch_bounds__(256, 2) void block_max_reg_kernel(BlockArgs a, floa
           if (lg == 0 && t < T && kw + 16 * u < kend) bsc[(long)bb * T + t] = v;
         }
       }
+    }
+  };
+  if (ntile > 0) kload(kf, 0);
+  if constexpr (!MK) {
+    for (int kt = 0; kt < ntile; kt += 2) {
+      if (kt + 1 < ntile) kload(kn, kt + 1);
+      store(sweep(kf, kt));
+      if (kt + 1 >= ntile) break;
+      if (kt + 2 < ntile) kload(kf, kt + 2);
+      store(sweep(kn, kt + 1));
+    }
+  } else {
+    for (int kt = 0; kt < ntile; ++kt) {
+      const int kw = sweep(kf, kt);
+      if (kt + 1 < ntile) kload(kf, kt + 1);
+      store(kw);
     }
   }
 }
@@ -850,8 +878,18 @@ hipError_t launch_block_select(const BlockArgs& a, hipStream_t st) {
   const dim3 g2((unsigned)((a.T + BMM_ROWS - 1) / BMM_ROWS), (unsigned)(a.B * a.H));
   const bool mf = block_uses_mfma(a);
   if (mf && (a.bs == 16 || a.bs == 32)) {
-    if (a.mask) block_max_reg_kernel<true><<<g2, 256, 0, st>>>(a, ms);
-    else block_max_reg_kernel<false><<<g2, 256, 0, st>>>(a, ms);
+    // D is a multiple of 32 and at most BLK_MAX_D (block_uses_mfma, the entry points' checks)
+    switch ((a.mask ? 8 : 0) + a.D / 32) {
+      case 1: block_max_reg_kernel<false, 1><<<g2, 256, 0, st>>>(a, ms); break;
+      case 2: block_max_reg_kernel<false, 2><<<g2, 256, 0, st>>>(a, ms); break;
+      case 3: block_max_reg_kernel<false, 3><<<g2, 256, 0, st>>>(a, ms); break;
+      case 4: block_max_reg_kernel<false, 4><<<g2, 256, 0, st>>>(a, ms); break;
+      case 9: block_max_reg_kernel<true, 1><<<g2, 256, 0, st>>>(a, ms); break;
+      case 10: block_max_reg_kernel<true, 2><<<g2, 256, 0, st>>>(a, ms); break;
+      case 11: block_max_reg_kernel<true, 3><<<g2, 256, 0, st>>>(a, ms); break;
+      case 12: block_max_reg_kernel<true, 4><<<g2, 256, 0, st>>>(a, ms); break;
+      default: return hipErrorInvalidValue;
+    }
   }
   else if (mf && a.bs % 16 == 0) block_max_mfma_kernel<true><<<g2, 256, 0, st>>>(a, ms);
   else if (mf) block_max_mfma_kernel<false><<<g2, 256, 0, st>>>(a, ms);
