@@ -27,9 +27,11 @@ namespace sgsa {
 
 constexpr int TR_THREADS = 512;
 
+// NKS = D / 32 as a template argument keeps the k-steps' loads and MFMAs free of branches.
+template <int NKS>
 __global__ __launch_bounds__(256) void rows_score_kernel(TopkArgs a, float mscale, float* __restrict__ sbuf) {
   const long row = blockIdx.y;
-  const int Tq = a.Tq, Tk = a.Tk, H = a.H, D = a.D, nks = D / 32;
+  const int Tq = a.Tq, Tk = a.Tk, H = a.H, D = NKS * 32;
   const int qr = (int)(row % Tq);
   const long bh = row / Tq;
   const int b = (int)(bh / H), h = (int)(bh % H);
@@ -40,31 +42,22 @@ __global__ __launch_bounds__(256) void rows_score_kernel(TopkArgs a, float mscal
   const uint16_t* qp = reinterpret_cast<const uint16_t*>(a.q) + ((long)(b * Tq + qr) * H + h) * D;
   const uint16_t* kb = reinterpret_cast<const uint16_t*>(a.k) + ((long)b * Tk * H + h) * D;
   const long kstride = (long)H * D;
-  bf16x8 qf[DP_ROWS / 32];
+  bf16x8 qf[NKS];
 #pragma unroll
-  for (int s = 0; s < DP_ROWS / 32; ++s) {
-    u16x8 raw = {0, 0, 0, 0, 0, 0, 0, 0};
-    if (s < nks) raw = *reinterpret_cast<const u16x8*>(qp + 32 * s + 8 * lg);
-    qf[s] = __builtin_bit_cast(bf16x8, raw);
-  }
-  u16x8 kr[4][DP_ROWS / 32];
+  for (int s = 0; s < NKS; ++s) qf[s] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8*>(qp + 32 * s + 8 * lg));
+  u16x8 kr[4][NKS];
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
     const int key = min(k0 + 16 * g + lc, nv - 1);
 #pragma unroll
-    for (int s = 0; s < DP_ROWS / 32; ++s) {
-      u16x8 raw = {0, 0, 0, 0, 0, 0, 0, 0};
-      if (s < nks) raw = *reinterpret_cast<const u16x8*>(kb + key * kstride + 32 * s + 8 * lg);
-      kr[g][s] = raw;
-    }
+    for (int s = 0; s < NKS; ++s) kr[g][s] = *reinterpret_cast<const u16x8*>(kb + key * kstride + 32 * s + 8 * lg);
   }
   float* out = sbuf + row * (long)Tk;
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
     f4 c = f4_zero();
 #pragma unroll
-    for (int s = 0; s < DP_ROWS / 32; ++s)
-      if (s < nks) c = mma_bf16(qf[s], __builtin_bit_cast(bf16x8, kr[g][s]), c);
+    for (int s = 0; s < NKS; ++s) c = mma_bf16(qf[s], __builtin_bit_cast(bf16x8, kr[g][s]), c);
     const float sv = score_of(c, mscale)[0];
     const int key = k0 + 16 * g + lc;
     if (lg == 0 && key < nv) out[key] = sv;
@@ -202,7 +195,14 @@ size_t topk_rows_bytes(const TopkArgs& a) {
 hipError_t launch_score_topk_rows(const TopkArgs& a, float* sbuf, hipStream_t st) {
   const float ms = score_multiplier(a.scale, a.scale_mode);
   const long rows = (long)a.B * a.H * a.Tq;
-  rows_score_kernel<<<dim3((unsigned)((a.Tk + 255) / 256), (unsigned)rows), 256, 0, st>>>(a, ms, sbuf);
+  const dim3 grid((unsigned)((a.Tk + 255) / 256), (unsigned)rows);
+  switch (a.D / 32) {   // D is a multiple of 32, at most DP_ROWS (topk_rows_bytes)
+    case 1: rows_score_kernel<1><<<grid, 256, 0, st>>>(a, ms, sbuf); break;
+    case 2: rows_score_kernel<2><<<grid, 256, 0, st>>>(a, ms, sbuf); break;
+    case 3: rows_score_kernel<3><<<grid, 256, 0, st>>>(a, ms, sbuf); break;
+    case 4: rows_score_kernel<4><<<grid, 256, 0, st>>>(a, ms, sbuf); break;
+    default: return hipErrorInvalidValue;
+  }
   rows_select_kernel<<<dim3((unsigned)rows), TR_THREADS, 0, st>>>(a, sbuf);
   return hipGetLastError();
 }
