@@ -716,29 +716,35 @@ __global__ __launch_bounds__(64) void block_cand_kernel(BlockArgs a, float mscal
       if (s < nks) raw = *reinterpret_cast<const u16x8*>(Qb + 32 * s + 8 * lg);
       qa[s] = __builtin_bit_cast(bf16x8, raw);
     }
-    for (int c0 = 0; c0 < ncand; c0 += 16) {
-      const int ca = c0 + lc;   // the candidate this lane loads as A row lc
-      const int key = ca < ncand ? key_of(ca) : 0;
-      const uint16_t* kp = Kb + ((long)(b * T + key) * H + h) * D;
-      f4 acc = f4_zero();
+    // NK = D / 32 when it is 4 (straight-line k-steps), 0 for D / 32 at run time
+    auto score_groups = [&](auto nkt) __attribute__((always_inline)) {
+      constexpr int NK = decltype(nkt)::value;
+      for (int c0 = 0; c0 < ncand; c0 += 16) {
+        const int ca = c0 + lc;   // the candidate this lane loads as A row lc
+        const int key = ca < ncand ? key_of(ca) : 0;
+        const uint16_t* kp = Kb + ((long)(b * T + key) * H + h) * D;
+        f4 acc = f4_zero();
 #pragma unroll
-      for (int s = 0; s < BLK_MAX_D / 32; ++s)
-        if (s < nks) acc = mma_bf16(__builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8*>(kp + 32 * s + 8 * lg)), qa[s], acc);
-      // accumulator element i holds A row 4lg+i, i.e. candidate c0+4lg+i; lane lc == i reports it
-      const f4 sv4 = score_of(acc, mscale);
-      const float sv = lc == 0 ? sv4[0] : lc == 1 ? sv4[1] : lc == 2 ? sv4[2] : sv4[3];
-      const int c = c0 + 4 * lg + lc;
-      const int ckey = __shfl(key, 4 * lg + lc, 64);   // key of candidate c (lane 4lg+lc loaded it)
-      if (lc < 4 && c < ncand) {
-        if (TOKEN) {
-          keys[c] = ((uint64_t)(~f32_order_key(sv)) << 32) | (uint32_t)ckey;
-        } else {
-          a.slot_idx[row * a.ks + c] = ckey;
-          a.slot_sc[row * a.ks + c] = sv;
-          m1 = fmaxf(m1, sv);
+        for (int s = 0; s < BLK_MAX_D / 32; ++s)
+          if (NK ? s < NK : s < nks) acc = mma_bf16(__builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8*>(kp + 32 * s + 8 * lg)), qa[s], acc);
+        // accumulator element i holds A row 4lg+i, i.e. candidate c0+4lg+i; lane lc == i reports it
+        const f4 sv4 = score_of(acc, mscale);
+        const float sv = lc == 0 ? sv4[0] : lc == 1 ? sv4[1] : lc == 2 ? sv4[2] : sv4[3];
+        const int c = c0 + 4 * lg + lc;
+        const int ckey = __shfl(key, 4 * lg + lc, 64);   // key of candidate c (lane 4lg+lc loaded it)
+        if (lc < 4 && c < ncand) {
+          if (TOKEN) {
+            keys[c] = ((uint64_t)(~f32_order_key(sv)) << 32) | (uint32_t)ckey;
+          } else {
+            a.slot_idx[row * a.ks + c] = ckey;
+            a.slot_sc[row * a.ks + c] = sv;
+            m1 = fmaxf(m1, sv);
+          }
         }
       }
-    }
+    };
+    if (nks == 4) score_groups(std::integral_constant<int, 4>{});
+    else score_groups(std::integral_constant<int, 0>{});
   }
   for (int c = MF ? ncand : lane; c < ncand; c += 64) {
     const int key = key_of(c);
