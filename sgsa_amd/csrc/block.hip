@@ -533,6 +533,7 @@ __global__ __launch_bounds__(256) void block_scores_transpose_kernel(const float
 // registers, the best BS_R blocks after the last one taken, in (score desc,
 // index asc) order; passes repeat until kqb are taken.
 constexpr int BS_R = 4;
+constexpr int BS_AHEAD = 16;   // block scores a lane loads before inserting them
 
 __global__ __launch_bounds__(256) void block_select_kernel(BlockArgs a) {
   const long row = (long)blockIdx.x * 256 + threadIdx.x;
@@ -555,10 +556,9 @@ __global__ __launch_bounds__(256) void block_select_kernel(BlockArgs a) {
     int bj[BS_R];
 #pragma unroll
     for (int r = 0; r < BS_R; ++r) { bv[r] = -INFINITY; bj[r] = 0x7fffffff; }
-    for (int j = 0; j < nvb; ++j) {
-      float cv = col[(long)j * T];
-      if (!(cv < ls || (cv == ls && j > lj))) continue;
-      int cj = j;
+    // block j's score into the kept list if it ranks after the last block taken
+    auto insert = [&](float cv, int cj) __attribute__((always_inline)) {
+      if (!(cv < ls || (cv == ls && cj > lj))) return;
 #pragma unroll
       for (int r = 0; r < BS_R; ++r) {
         if (cv > bv[r] || (cv == bv[r] && cj < bj[r])) {
@@ -567,7 +567,17 @@ __global__ __launch_bounds__(256) void block_select_kernel(BlockArgs a) {
           bv[r] = cv; bj[r] = cj; cv = tv; cj = tj;
         }
       }
+    };
+    // BS_AHEAD scores loaded ahead of their insertions (one load at a time leaves the loop latency-bound)
+    int j = 0;
+    for (; j + BS_AHEAD <= nvb; j += BS_AHEAD) {
+      float cvs[BS_AHEAD];
+#pragma unroll
+      for (int u = 0; u < BS_AHEAD; ++u) cvs[u] = col[(long)(j + u) * T];
+#pragma unroll
+      for (int u = 0; u < BS_AHEAD; ++u) insert(cvs[u], j + u);
     }
+    for (; j < nvb; ++j) insert(col[(long)j * T], j);
     const int take = min(BS_R, kqb - got);
 #pragma unroll
     for (int r = 0; r < BS_R; ++r) {
