@@ -97,11 +97,24 @@ __global__ __launch_bounds__(TR_THREADS) void rows_select_kernel(TopkArgs a, con
   const float* sr = sbuf + row * (long)Tk;
 
   float t1 = -FLT_MAX, t2 = -FLT_MAX;
-  for (int j = tid; j < nv; j += TR_THREADS) {
-    const float s = sr[j];
-    key[j] = f32_order_key(s);
-    t2 = fmaxf(t2, fminf(t1, s));
-    t1 = fmaxf(t1, s);
+  // eight scores per thread loaded before they are used (one load at a time leaves the pass latency-bound)
+  for (int j0 = 0; j0 < nv; j0 += 8 * TR_THREADS) {
+    float sv[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int j = j0 + u * TR_THREADS + tid;
+      sv[u] = j < nv ? sr[j] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int j = j0 + u * TR_THREADS + tid;
+      if (j < nv) {
+        const float s = sv[u];
+        key[j] = f32_order_key(s);
+        t2 = fmaxf(t2, fminf(t1, s));
+        t1 = fmaxf(t1, s);
+      }
+    }
   }
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
