@@ -384,8 +384,10 @@ __global__ __launch_bounds__(256, 2) void block_max_reg_kernel(BlockArgs a, floa
   constexpr int QR = BMM_ROWS, NG = QR / 16, TK = 128;
   const int D = NKS * 32, T = a.T, H = a.H, bs = a.bs, nb = a.nb;
   const int nrb = (T + QR - 1) / QR;
-  const int bh = blockIdx.y, b = bh / H, h = bh % H;
-  const int r0 = (nrb - 1 - (int)blockIdx.x) * QR;
+  // grid (B*H, row blocks): consecutive workgroups take different heads, so the XCDs they are dealt
+  // to in turn each see a few heads' keys in their L2; the latest (heaviest) row blocks go first
+  const int bh = blockIdx.x, b = bh / H, h = bh % H;
+  const int r0 = (nrb - 1 - (int)blockIdx.y) * QR;
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lr = lane & 15, lg = lane >> 4;
   const uint16_t* Q = reinterpret_cast<const uint16_t*>(a.q);
@@ -895,15 +897,16 @@ hipError_t launch_block_select(const BlockArgs& a, hipStream_t st) {
   const bool mf = block_uses_mfma(a);
   if (mf && (a.bs == 16 || a.bs == 32)) {
     // D is a multiple of 32 and at most BLK_MAX_D (block_uses_mfma, the entry points' checks)
+    const dim3 gh(g2.y, g2.x);   // (B*H, row blocks)
     switch ((a.mask ? 8 : 0) + a.D / 32) {
-      case 1: block_max_reg_kernel<false, 1><<<g2, 256, 0, st>>>(a, ms); break;
-      case 2: block_max_reg_kernel<false, 2><<<g2, 256, 0, st>>>(a, ms); break;
-      case 3: block_max_reg_kernel<false, 3><<<g2, 256, 0, st>>>(a, ms); break;
-      case 4: block_max_reg_kernel<false, 4><<<g2, 256, 0, st>>>(a, ms); break;
-      case 9: block_max_reg_kernel<true, 1><<<g2, 256, 0, st>>>(a, ms); break;
-      case 10: block_max_reg_kernel<true, 2><<<g2, 256, 0, st>>>(a, ms); break;
-      case 11: block_max_reg_kernel<true, 3><<<g2, 256, 0, st>>>(a, ms); break;
-      case 12: block_max_reg_kernel<true, 4><<<g2, 256, 0, st>>>(a, ms); break;
+      case 1: block_max_reg_kernel<false, 1><<<gh, 256, 0, st>>>(a, ms); break;
+      case 2: block_max_reg_kernel<false, 2><<<gh, 256, 0, st>>>(a, ms); break;
+      case 3: block_max_reg_kernel<false, 3><<<gh, 256, 0, st>>>(a, ms); break;
+      case 4: block_max_reg_kernel<false, 4><<<gh, 256, 0, st>>>(a, ms); break;
+      case 9: block_max_reg_kernel<true, 1><<<gh, 256, 0, st>>>(a, ms); break;
+      case 10: block_max_reg_kernel<true, 2><<<gh, 256, 0, st>>>(a, ms); break;
+      case 11: block_max_reg_kernel<true, 3><<<gh, 256, 0, st>>>(a, ms); break;
+      case 12: block_max_reg_kernel<true, 4><<<gh, 256, 0, st>>>(a, ms); break;
       default: return hipErrorInvalidValue;
     }
   }
