@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """SGSA layer-forward benchmark on one MI355X.
 
-    python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--no-cpu-baseline] [--no-other-configs]
                     [--workload layer|model|hybrid|block|backward]
 
 A step is one SGSA layer forward over the batch at the north-star shape
@@ -63,6 +63,92 @@ def synth_inputs(B, T, H, D, seed=0):
     q = q / q.norm(dim=-1, keepdim=True)
     k = k / k.norm(dim=-1, keepdim=True)
     return q, k, v, beta, gamma, budget
+
+
+def heavy_tail_keys(k, seed=0, frac=0.01, mult=8.0):
+    """Config 3's retrieval keys: for each (b, h), round(frac * T) key positions (randperm on a
+    generator seeded ``seed``) scaled by ``mult``; the state update keeps the unit-norm keys."""
+    B, T, H, _ = k.shape
+    g = torch.Generator().manual_seed(seed + 1)
+    kr = k.clone()
+    n = int(round(frac * T))
+    for b in range(B):
+        for h in range(H):
+            kr[b, torch.randperm(T, generator=g)[:n], h] *= mult
+    return kr
+
+
+def time_config(name, B, T, H, D, top_k, dtype, heavy=False, reps=3):
+    """One BASELINE.json configuration through the layer path, outside the timed steps:
+    K1 -> K2 -> chunk update as sgsa_layer_fwd runs them (bf16, d = 128: the threshold
+    form, per stage; otherwise the whole sgsa_layer_fwd call).  Config 3 retrieves over
+    the heavy-tailed keys and updates the state with the unit-norm ones.  Returns ms per
+    layer forward (mean of ``reps`` after one warm-up), tokens/s and the stage split."""
+    import sgsa_amd
+    from sgsa_amd import _abi
+    dev = torch.device("cuda:0")
+    q, k, v, beta, gamma, budget = synth_inputs(B, T, H, D)
+    kr = heavy_tail_keys(k) if heavy else k
+    qd, kd, vd, krd = (t.to(dev, dtype).contiguous() for t in (q, k, v, kr))
+    bd, gd, ud = (t.to(dev).contiguous() for t in (beta, gamma, budget))
+    del q, k, v, kr
+    L, P = _abi.lib(), _abi.ptr
+    stream = _abi.stream_of(qd)
+    dc = _abi.dtype_code(dtype)
+    kk = min(top_k, T)
+    out = torch.empty_like(qd)
+    ht = torch.empty(B, H, D, D, device=dev, dtype=torch.float32)
+    thr_form = dtype == torch.bfloat16 and D == 128
+    if thr_form:
+        n = ctypes.c_size_t()
+        _abi.check(L.sgsa_score_topk_workspace_size(B, T, H, ctypes.byref(n)))
+        tws = torch.empty(n.value, device=dev, dtype=torch.uint8)
+        _abi.check(L.sgsa_chunk_fwd_workspace_size(B, T, H, D, 1, ctypes.byref(n)))
+        cws = torch.empty(n.value, device=dev, dtype=torch.uint8)
+        thr = torch.empty(B, H, T, 2, device=dev, dtype=torch.int32)
+        top2 = torch.empty(B, H, T, 2, device=dev, dtype=torch.float32)
+        cnt = torch.empty(B, H, T, device=dev, dtype=torch.int32)
+        wk, vh = torch.empty_like(qd), torch.empty_like(qd)
+        al = torch.empty(B, T, H, device=dev, dtype=torch.float32)
+        stages = (
+            ("score_topk", lambda: _abi.check(L.sgsa_score_topk_thresholds(
+                B, T, H, D, kk, P(qd), P(krd), P(thr), P(top2), P(cnt), P(tws), tws.numel(), stream))),
+            ("gather_gate", lambda: _abi.check(L.sgsa_sparse_gather_thresholds(
+                B, T, H, D, kk, P(qd), P(krd), P(vd), P(thr), P(top2), P(cnt), P(ud), 0, 0.25, 0.1, P(wk), P(vh),
+                None, P(al), stream))),
+            ("chunk", lambda: _abi.check(L.sgsa_chunk_fwd(
+                dc, B, T, H, D, 64, P(qd), P(kd), P(vd), P(bd), P(gd), P(wk), P(vh), P(al), None, P(out), P(ht),
+                P(cws), cws.numel(), stream))),
+        )
+    else:
+        n = ctypes.c_size_t()
+        _abi.check(L.sgsa_layer_fwd_workspace_size(dc, B, T, H, D, kk, ctypes.byref(n)))
+        lws = torch.empty(n.value, device=dev, dtype=torch.uint8)
+        stages = (("layer", lambda: _abi.check(L.sgsa_layer_fwd(
+            dc, B, T, H, D, kk, 64, P(qd), P(kd), P(vd), P(qd), P(bd), P(gd), P(ud), None, 0, 0.25, 0.1, P(out),
+            P(ht), P(lws), lws.numel(), stream))),)
+    cur = torch.cuda.current_stream(dev)
+    for _, fn in stages:
+        fn()
+    torch.cuda.synchronize()
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(stages) + 1)] for _ in range(reps)]
+    for r in range(reps):
+        for i, (_, fn) in enumerate(stages):
+            ev[r][i].record(cur)
+            fn()
+        ev[r][-1].record(cur)
+    torch.cuda.synchronize()
+    st = {nm: sum(ev[r][i].elapsed_time(ev[r][i + 1]) for r in range(reps)) / reps for i, (nm, _) in enumerate(stages)}
+    ms = sum(st.values())
+    ok = bool(torch.isfinite(out.float()).all() and torch.isfinite(ht).all())
+    f_score = B * H * T * (T + 1) * D
+    res = {"config": name, "B": B, "T": T, "H": H, "D": D, "top_k": top_k, "dtype": str(dtype).split(".")[-1],
+           "heavy_tail_keys": heavy, "ms": round(ms, 3), "tokens_per_s": round(B * T / (ms / 1000.0), 1),
+           "stage_ms": {nm: round(v, 3) for nm, v in st.items()}, "finite": ok}
+    if "score_topk" in st:
+        res["score_topk_mfma_frac"] = round(f_score / (st["score_topk"] / 1000.0) / 2.5e15, 4)
+    log(f"{name}: {json.dumps(res)}")
+    return res
 
 
 def gather_bytes(B, H, T, D, k, elem=2):
@@ -147,42 +233,54 @@ def recall_batch(B: int, T: int, vocab: int, seed: int = 0) -> torch.Tensor:
 
 
 def run_model(args) -> int:
-    """Config 2: the 2-layer SGSA causal LM forward (sgsa_amd.SGSAForCausalLM)."""
+    """Config 2: the 2-layer SGSA causal LM forward (sgsa_amd.SGSAForCausalLM).  The value is the
+    reference config's default retrieval (block_token, top-k 16, blocks of 32, 2 kept;
+    modelings/modeling_sgsa.py:58-61); token_only at top-k 16 is timed beside it."""
     import sgsa_amd
     B, T = 16, 4096
-    cfg = sgsa_amd.SGSAConfig(vocab_size=8192, hidden_size=1024, intermediate_size=2816, num_hidden_layers=2,
-                              num_attention_heads=8, num_kv_heads=8, max_position_embeddings=T, top_k=16)
     dev = torch.device("cuda:0")
-    model = sgsa_amd.SGSAForCausalLM(cfg)
-    model.init_weights(std=0.02, qk_std=1.0 / math.sqrt(cfg.hidden_size * cfg.head_dim),
-                       generator=torch.Generator().manual_seed(0))
-    model = model.to(device=dev, dtype=torch.bfloat16).eval()
-    ids = recall_batch(B, T, cfg.vocab_size).to(dev)
-    log(f"model: config 2, B={B} T={T}, warmup {args.warmup}")
-    with torch.no_grad():
-        for _ in range(args.warmup):
-            logits = model(ids)["logits"]
-        torch.cuda.synchronize()
-        cur = torch.cuda.current_stream()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(cur)
-        for _ in range(args.steps):
-            logits = model(ids)["logits"]
-        e1.record(cur)
-        torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / max(args.steps, 1)
-    if not torch.isfinite(logits).all():
-        log("non-finite logits")
-        return 1
-    log(f"model ms/step {ms:.3f}")
+    ids = recall_batch(B, T, 8192).to(dev)
+    res = {}
+    for mode in ("block_token", "token_only"):
+        cfg = sgsa_amd.SGSAConfig(vocab_size=8192, hidden_size=1024, intermediate_size=2816, num_hidden_layers=2,
+                                  num_attention_heads=8, num_kv_heads=8, max_position_embeddings=T, top_k=16,
+                                  retrieval_mode=mode)
+        model = sgsa_amd.SGSAForCausalLM(cfg)
+        model.init_weights(std=0.02, qk_std=1.0 / math.sqrt(cfg.hidden_size * cfg.head_dim),
+                           generator=torch.Generator().manual_seed(0))
+        model = model.to(device=dev, dtype=torch.bfloat16).eval()
+        log(f"model: config 2 ({mode}), B={B} T={T}, warmup {args.warmup}")
+        with torch.no_grad():
+            for _ in range(args.warmup):
+                logits = model(ids)["logits"]
+            torch.cuda.synchronize()
+            cur = torch.cuda.current_stream()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(cur)
+            for _ in range(args.steps):
+                logits = model(ids)["logits"]
+            e1.record(cur)
+            torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / max(args.steps, 1)
+        if not torch.isfinite(logits).all():
+            log("non-finite logits")
+            return 1
+        log(f"model ({mode}) ms/step {ms:.3f}")
+        res[mode] = ms
+        del model, logits
+        torch.cuda.empty_cache()
+    ms = res["block_token"]
     print(json.dumps({
         "metric": MODEL_METRIC, "value": round(B * T / (ms / 1000.0), 1), "unit": "tokens/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 3), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic associative-recall token ids, random-init weights",
         "config": {"workload": "sgsa_model_fwd", "B": B, "T": T, "hidden": 1024, "heads": 8, "head_dim": 128,
-                   "vocab": 8192, "layers": 2, "intermediate": 2816, "top_k": 16,
+                   "vocab": 8192, "layers": 2, "intermediate": 2816, "top_k": 16, "retrieval_mode": "block_token",
+                   "block_size": 32, "top_blocks": 2,
                    "init": "normal std 0.02; q/k/q_ret projections std 1/sqrt(hidden*head_dim)"},
+        "token_only": {"ms_per_step": round(res["token_only"], 3),
+                       "value": round(B * T / (res["token_only"] / 1000.0), 1)},
         "cpu_baseline": None,
     }), flush=True)
     return 0
@@ -365,6 +463,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--T", type=int, default=NORTH_STAR["T"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-other-configs", action="store_true",
+                    help="skip timing configs 0, 1 and 3 beside the headline (outside the timed steps)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run one plain 256 MiB fp32 copy kernel (torch.neg) first; its PMC byte counters "
                          "give the scale factor for the traffic of the SGSA kernels")
@@ -649,6 +749,16 @@ def main() -> int:
         "rooflines": rooflines,
         "cpu_baseline": None,
     }
+    if not args.no_other_configs and (B, T, H, D, kk) == (1, 32768, 16, 128, 2048):
+        # BASELINE.json's other single-GPU configurations through the same layer path, outside the timed steps
+        del idx, sc, tl, toff, tws
+        torch.cuda.empty_cache()
+        result["other_configs"] = [
+            time_config("config 0", 1, 512, 4, 64, 32, torch.float32),
+            time_config("config 1", 4, 8192, 16, 128, 256, torch.bfloat16),
+            time_config("config 3", 1, 65536, 16, 128, 2048, torch.bfloat16, heavy=True),
+        ]
+        torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
         log("cpu baseline (bounded sample)")
         result["cpu_baseline"] = cpu_baseline(q.to(bf), k.to(bf), v.to(bf), beta, gamma, budget, cfg)

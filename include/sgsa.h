@@ -293,6 +293,29 @@ int sgsa_block_retrieve_masked(int dtype, int B, int T, int H, int D, int top_k,
                                void* k_hat, void* v_hat, float* diag, void* workspace, size_t workspace_bytes,
                                void* stream);
 
+/* ---- block retrieval inside the SGSA block (the layer's retrieval half) --------
+ * Replaces the retrieval + gate of SGSABlock.forward in the block modes
+ * (modelings/modeling_sgsa.py:669-684 with SparseRetriever.forward :444-463 and
+ * SGSAStateLayer :543-552, _compute_alpha :497-504; retrieval_mode
+ * "block_token" is the reference config's default, :61): the block retrieval of
+ * sgsa_block_retrieve(_masked) on (q_ret, k, v), causal, then the write key
+ * (write_mode 0 direct: k_hat; 1 residual: k_hat - (k_hat.k / max(|k|^2, 1e-6)) k)
+ * and alpha = alpha_max * concentration * clamp(novelty, 0, 1) * sigmoid(budget),
+ * clipped by 1 / max(alpha |v_hat| |write key|, 1).  block_only's concentration
+ * reads the kept block indices' difference as the reference's does (:455-463).
+ * attention_mask [B,T] uint8 or NULL.  budget [B,T,H] fp32 logits.  Outputs:
+ * write_key, v_hat [B,T,H,D] in dtype, alpha [B,T,H] fp32, row_stats [2,B,H,T]
+ * (largest weight; |write key| / |k_hat| clamped to [0, 10] in residual mode,
+ * else 0) or NULL.  Index lists stay in the workspace:
+ * sgsa_block_layer_retrieve_workspace_size() bytes. */
+int sgsa_block_layer_retrieve_workspace_size(int B, int T, int H, int top_k, int block_size, int top_blocks,
+                                             int mode, size_t* bytes);
+int sgsa_block_layer_retrieve(int dtype, int B, int T, int H, int D, int top_k, int block_size, int top_blocks,
+                              int mode, float tau_c, const void* q_ret, const void* k, const void* v,
+                              const uint8_t* attention_mask, const float* budget, int write_mode, float alpha_max,
+                              void* write_key, void* v_hat, float* alpha, float* row_stats, void* workspace,
+                              size_t workspace_bytes, void* stream);
+
 /* ---- RMSNorm of the model shells -------------------------------------------
  * y = x * rsqrt(mean(x^2) + eps) * weight over the last dimension, in fp32,
  * stored in x's dtype: the RMSNorm of the SGSA and hybrid stacks

@@ -500,28 +500,39 @@ def sgsa_layer_forward(
     chunk_size: int = 64,
     block_rows: int = 256,
     attention_mask: Optional[Tensor] = None,
+    retrieval_mode: str = "token_only",
+    block_size: int = 32,
+    top_blocks: int = 2,
 ) -> Dict[str, Tensor]:
     """Op-level SGSA layer forward: retrieval -> gate -> state update.
 
     Mirrors SGSABlock.forward's attention half (modelings/modeling_sgsa.py:669-684)
     with the projections taken as inputs: retrieval on (q_ret, k, v) under the
-    optional padding mask [B,T] (:672-675 pass it to the retriever only), write
-    key and alpha (:546-552), then the recurrent state update (naive.py, or the
-    chunk form when ``use_chunk``).  Inputs are upcast to fp32.
+    optional padding mask [B,T] (:672-675 pass it to the retriever only) --
+    ``retrieval_mode`` token_only (:430-431) or block_only / block_token
+    (``block_retrieval``, :432-463) -- write key and alpha (:543-552), then the
+    recurrent state update (naive.py, or the chunk form when ``use_chunk``).
+    ``write_mode`` "none" keeps the write key k_hat for alpha (:546-550) and
+    leaves the sparse write out of the update (:557-609).  Inputs are upcast to fp32.
     """
     f = lambda x: None if x is None else x.float()
     q, k, v, q_ret, beta, gamma, budget_logits = map(f, (q, k, v, q_ret, beta, gamma, budget_logits))
-    ret = token_topk_retrieval(q_ret, k, v, top_k, tau_c=tau_c, block_rows=block_rows,
-                               attention_mask=attention_mask)
-    wk = write_key(ret["k_hat"], k, write_mode)
+    if retrieval_mode == "token_only":
+        ret = token_topk_retrieval(q_ret, k, v, top_k, tau_c=tau_c, block_rows=block_rows,
+                                   attention_mask=attention_mask)
+    else:
+        ret = block_retrieval(q_ret, k, v, top_k, block_size, top_blocks, retrieval_mode, causal=True,
+                              tau_c=tau_c, attention_mask=attention_mask)
+    if write_mode not in ("none", "direct", "residual"):
+        raise ValueError(f"unknown write mode {write_mode!r}")
+    wk = write_key(ret["k_hat"], k, "residual" if write_mode == "residual" else "direct")
     alpha = compute_alpha(ret["diagnostics"]["concentration"], ret["diagnostics"]["novelty"],
                           budget_logits, wk, ret["v_hat"], alpha_max)
+    sp = (wk, ret["v_hat"], alpha) if write_mode != "none" else (None, None, None)
     if use_chunk:
-        o, st = chunk_sgsa_fwd(q, k, v, beta, gamma, wk, ret["v_hat"], alpha,
-                               f(initial_state), chunk_size, True)
+        o, st = chunk_sgsa_fwd(q, k, v, beta, gamma, *sp, f(initial_state), chunk_size, True)
     else:
-        o, st = naive_recurrent_sgsa(q, k, v, beta, gamma, wk, ret["v_hat"], alpha,
-                                     f(initial_state), True)
+        o, st = naive_recurrent_sgsa(q, k, v, beta, gamma, *sp, f(initial_state), True)
     return {"o": o, "final_state": st, "write_key": wk, "v_hat": ret["v_hat"],
             "alpha": alpha, "retrieval": ret}
 
@@ -615,14 +626,17 @@ def sgsa_model_forward(params: Dict[str, Tensor], input_ids: Tensor, *, num_laye
                        top_k: int, eps: float = 1e-6, write_mode: str = "direct", alpha_max: float = 0.25,
                        tau_c: float = 0.1, sparse_output_lambda: float = 0.0,
                        act_dtype: Optional[torch.dtype] = None, attention_mask: Optional[Tensor] = None,
-                       return_metrics: bool = False):
+                       return_metrics: bool = False, retrieval_mode: str = "token_only", block_size: int = 32,
+                       top_blocks: int = 2):
     """Logits of SGSAForCausalLM.forward (modelings/modeling_sgsa.py:735-749) in fp32.
 
     ``params`` uses the parameter names of sgsa_amd.model.SGSAForCausalLM, which follow
     the reference's modules: embedding + learned position embedding (:739), per block
     (:669-709) RMSNorm, q/k/v/q_ret projections, the gates of SGSAStateLayer
     (beta = sigmoid(.).clamp_min(1e-4), gamma = sigmoid(.), budget logits; :584-585,
-    :501), the token_only retrieval and state update (``sgsa_layer_forward``), o_proj,
+    :501), the retrieval in ``retrieval_mode`` (token_only, block_only, block_token with
+    ``block_size`` / ``top_blocks``) and the state update (``sgsa_layer_forward``; every
+    linear_backend of :554-609 computes this recurrence), o_proj,
     the optional sparse output (:689-692), the residual MLP (:695), then the final
     RMSNorm and lm_head (:746).
 
@@ -658,7 +672,8 @@ def sgsa_model_forward(params: Dict[str, Tensor], input_ids: Tensor, *, num_laye
         gamma = torch.sigmoid(r(n @ w("gamma_proj.weight").T + w("gamma_proj.bias")))
         budget = r(n @ w("budget_proj.weight").T + w("budget_proj.bias"))
         lay = sgsa_layer_forward(q, k, v, q_ret, beta, gamma, budget, top_k, write_mode=write_mode,
-                                 alpha_max=alpha_max, tau_c=tau_c, attention_mask=attention_mask)
+                                 alpha_max=alpha_max, tau_c=tau_c, attention_mask=attention_mask,
+                                 retrieval_mode=retrieval_mode, block_size=block_size, top_blocks=top_blocks)
         kh = lay["retrieval"]["k_hat"]
         metrics[f"layer_{i}_alpha_mean"] = lay["alpha"].mean()
         metrics[f"layer_{i}_k_hat_perp_ratio_mean"] = (
@@ -682,33 +697,45 @@ def sgsa_model_forward(params: Dict[str, Tensor], input_ids: Tensor, *, num_laye
 # Config 4: the hybrid decoder (SGSA blocks and dense GQA attention blocks)
 # ---------------------------------------------------------------------------
 
-def rope_apply(x: Tensor, pos: Tensor, theta: float = 10000.0) -> Tensor:
+def rope_apply(x: Tensor, pos: Tensor, theta: float = 10000.0, act_dtype=None) -> Tensor:
     """Rotary embedding of x [B, heads, T, D] at positions pos [T], in the rotate-half
-    form of modelings/hybrid_dense_delta_topk.py:124-150 (fp32)."""
+    form of modelings/hybrid_dense_delta_topk.py:124-150 (fp32).  ``act_dtype``: a model
+    in that dtype -- the cos / sin tables stored in it (:134-136) and each product and
+    the sum rounded to it (:150)."""
     D = x.shape[-1]
     inv_freq = 1.0 / (theta ** (torch.arange(0, D, 2).float() / D))
     f = torch.outer(pos.float(), inv_freq)
     emb = torch.cat((f, f), dim=-1)
     rot = torch.cat((-x[..., D // 2:], x[..., :D // 2]), dim=-1)
-    return x * emb.cos() + rot * emb.sin()
+    if act_dtype is None:
+        return x * emb.cos() + rot * emb.sin()
+    r = lambda t: t.to(act_dtype).float()
+    return r(r(x * r(emb.cos())) + r(rot * r(emb.sin())))
 
 
-def dense_gqa_attention(q: Tensor, k: Tensor, v: Tensor, q_pos: Tensor) -> Tensor:
+def dense_gqa_attention(q: Tensor, k: Tensor, v: Tensor, q_pos: Tensor, act_dtype=None) -> Tensor:
     """Causal softmax attention (:178-192) with grouped key/value heads: q [B, H, Tq, D]
     at positions q_pos [Tq]; k, v [B, Hkv, Tk, D] at positions 0 .. Tk-1; query head h
-    reads key/value head h // (H / Hkv)."""
+    reads key/value head h // (H / Hkv).  ``act_dtype``: the roundings of a model in that
+    dtype -- the product q k^T and its scaling by 1/sqrt(D) each rounded (:186-187), the
+    fp32 softmax's probabilities rounded (:190), the output rounded."""
     H, Hkv, D = q.shape[1], k.shape[1], q.shape[-1]
+    r = (lambda x: x) if act_dtype is None else (lambda x: x.to(act_dtype).float())
     kk = k.repeat_interleave(H // Hkv, dim=1)
     vv = v.repeat_interleave(H // Hkv, dim=1)
-    s = torch.matmul(q, kk.transpose(-1, -2)) / math.sqrt(D)
+    if act_dtype is None:
+        s = torch.matmul(q, kk.transpose(-1, -2)) / math.sqrt(D)
+    else:   # a low-precision tensor times a Python float: the product in fp32, rounded once
+        s = r(r(torch.matmul(q, kk.transpose(-1, -2))) * (1.0 / math.sqrt(D)))
     s = s.masked_fill(torch.arange(k.shape[2])[None, :] > q_pos[:, None], float("-inf"))
-    return torch.matmul(torch.softmax(s, dim=-1), vv)
+    return r(torch.matmul(r(torch.softmax(s, dim=-1)), vv))
 
 
 def hybrid_generate(params: Dict[str, Tensor], prompt_ids: Tensor, decode_ids: Tensor, *, num_layers: int,
                     num_heads: int, num_kv_heads: int, dense_every: int, top_k: int, recompute_every: int,
                     rope_theta: float = 10000.0, eps: float = 1e-6, write_mode: str = "direct",
-                    alpha_max: float = 0.25, tau_c: float = 0.1) -> Tuple[Tensor, Tensor]:
+                    alpha_max: float = 0.25, tau_c: float = 0.1,
+                    act_dtype: Optional[torch.dtype] = None) -> Tuple[Tensor, Tensor]:
     """Logits of the config-4 hybrid decoder in fp32: the prompt [B, T] in one pass, then
     the tokens decode_ids [B, n] one at a time (token s at position T + s).
 
@@ -720,8 +747,14 @@ def hybrid_generate(params: Dict[str, Tensor], prompt_ids: Tensor, decode_ids: T
     re-scores the layer's kept candidates otherwise.  ``params`` uses the names of
     sgsa_amd.hybrid.HybridForCausalLM.  Returns (prompt logits [B, T, V], decode
     logits [B, n, V]).
+
+    ``act_dtype`` (e.g. bfloat16) rounds every activation a model in that dtype
+    stores -- embeddings, norms, projections, the rotary embedding, the attention's
+    scores, probabilities and output, the SGSA layer's output, the MLP's products and
+    each residual sum -- while the arithmetic stays fp32, as sgsa_model_forward does.
     """
     P = {k: v.float() for k, v in params.items()}
+    r = (lambda x: x) if act_dtype is None else (lambda x: x.to(act_dtype).float())
     B, T = prompt_ids.shape
     C = P["embed_tokens.weight"].shape[1]
     H, Hkv = num_heads, num_kv_heads
@@ -731,34 +764,36 @@ def hybrid_generate(params: Dict[str, Tensor], prompt_ids: Tensor, decode_ids: T
 
     def mlp(i, h):
         w = lambda n: P[f"layers.{i}.{n}"]
-        m = rms_norm(h, w("post_attn_norm.weight"), eps)
-        return h + (F.silu(m @ w("mlp.gate_proj.weight").T) * (m @ w("mlp.up_proj.weight").T)) @ \
-            w("mlp.down_proj.weight").T
+        m = r(rms_norm(h, w("post_attn_norm.weight"), eps))
+        gate, up = r(m @ w("mlp.gate_proj.weight").T), r(m @ w("mlp.up_proj.weight").T)
+        return r(h + r(r(r(F.silu(gate)) * up) @ w("mlp.down_proj.weight").T))
 
     def run(ids: Tensor, pos0: int, step: Optional[int]) -> Tensor:
         n_t = ids.shape[1]
-        h = P["embed_tokens.weight"][ids]
+        h = r(P["embed_tokens.weight"][ids])
         pos = torch.arange(pos0, pos0 + n_t)
         for i in range(num_layers):
             w = lambda n: P[f"layers.{i}.{n}"]
             c = caches[i]
-            nrm = rms_norm(h, w("input_norm.weight"), eps)
+            nrm = r(rms_norm(h, w("input_norm.weight"), eps))
             if i % dense_every == 0:
-                q = rope_apply((nrm @ w("q_proj.weight").T).view(B, n_t, H, D).transpose(1, 2), pos, rope_theta)
-                k = rope_apply((nrm @ w("k_proj.weight").T).view(B, n_t, Hkv, D).transpose(1, 2), pos, rope_theta)
-                v = (nrm @ w("v_proj.weight").T).view(B, n_t, Hkv, D).transpose(1, 2)
+                q = rope_apply(r(nrm @ w("q_proj.weight").T).view(B, n_t, H, D).transpose(1, 2), pos, rope_theta,
+                               act_dtype)
+                k = rope_apply(r(nrm @ w("k_proj.weight").T).view(B, n_t, Hkv, D).transpose(1, 2), pos, rope_theta,
+                               act_dtype)
+                v = r(nrm @ w("v_proj.weight").T).view(B, n_t, Hkv, D).transpose(1, 2)
                 c["k"] = k if step is None else torch.cat((c["k"], k), dim=2)
                 c["v"] = v if step is None else torch.cat((c["v"], v), dim=2)
-                att = dense_gqa_attention(q, c["k"], c["v"], pos)
-                h = h + att.transpose(1, 2).reshape(B, n_t, C) @ w("o_proj.weight").T
+                att = dense_gqa_attention(q, c["k"], c["v"], pos, act_dtype)
+                h = r(h + r(att.transpose(1, 2).reshape(B, n_t, C) @ w("o_proj.weight").T))
             else:
-                q = (nrm @ w("q_proj.weight").T).view(B, n_t, H, D)
-                k = (nrm @ w("k_proj.weight").T).view(B, n_t, H, D)
-                v = (nrm @ w("v_proj.weight").T).view(B, n_t, H, D)
-                q_ret = (nrm @ w("q_ret_proj.weight").T).view(B, n_t, H, D)
-                beta = torch.sigmoid(nrm @ w("beta_proj.weight").T + w("beta_proj.bias")).clamp_min(1e-4)
-                gamma = torch.sigmoid(nrm @ w("gamma_proj.weight").T + w("gamma_proj.bias"))
-                budget = nrm @ w("budget_proj.weight").T + w("budget_proj.bias")
+                q = r(nrm @ w("q_proj.weight").T).view(B, n_t, H, D)
+                k = r(nrm @ w("k_proj.weight").T).view(B, n_t, H, D)
+                v = r(nrm @ w("v_proj.weight").T).view(B, n_t, H, D)
+                q_ret = r(nrm @ w("q_ret_proj.weight").T).view(B, n_t, H, D)
+                beta = torch.sigmoid(r(nrm @ w("beta_proj.weight").T + w("beta_proj.bias"))).clamp_min(1e-4)
+                gamma = torch.sigmoid(r(nrm @ w("gamma_proj.weight").T + w("gamma_proj.bias")))
+                budget = r(nrm @ w("budget_proj.weight").T + w("budget_proj.bias"))
                 if step is None:
                     lay = sgsa_layer_forward(q, k, v, q_ret, beta, gamma, budget, top_k, write_mode=write_mode,
                                              alpha_max=alpha_max, tau_c=tau_c)
@@ -771,9 +806,9 @@ def hybrid_generate(params: Dict[str, Tensor], prompt_ids: Tensor, decode_ids: T
                     o, c["state"], c["cand"] = sgsa_decode_step(
                         q, k, v, q_ret, beta, gamma, budget, c["k"], c["v"], c["state"], top_k, write_mode,
                         alpha_max, tau_c, candidates=None if select else c["cand"])
-                h = h + o.reshape(B, n_t, C) @ w("o_proj.weight").T
+                h = r(h + r(r(o).reshape(B, n_t, C) @ w("o_proj.weight").T))
             h = mlp(i, h)
-        return rms_norm(h, P["norm.weight"], eps) @ head.T
+        return r(r(rms_norm(h, P["norm.weight"], eps)) @ head.T)
 
     prompt_logits = run(prompt_ids, 0, None)
     dec = [run(decode_ids[:, s:s + 1], T + s, s) for s in range(decode_ids.shape[1])]

@@ -585,7 +585,20 @@ int sgsa_score_at(int dtype, int B, int Tq, int Tk, int H, int D, int top_k, flo
 namespace {
 struct BlockWs {
   size_t bscores, ncand, bmargin, top2, counts, valid, slot_sc, slot_idx, slot_w, maxidx;
-  size_t mpc, mperm, mnvb, mkqb, mbits, total;   // padding-mask layout (always reserved)
+  size_t mpc, mperm, mnvb, mkqb, mbits;   // padding-mask layout (always reserved)
+  size_t own_idx, own_bidx;               // the layer form's token and block index lists
+  size_t total;
+};
+
+// The write gate of SGSAStateLayer (modeling_sgsa.py:497-504, :543-552) folded into the block
+// retrieval's gather, for the layer form (sgsa_block_layer_retrieve); all NULL for the retriever.
+struct BlockGate {
+  const float* budget = nullptr;   // [B,T,H] budget logits
+  int write_mode = 0;              // 0 direct, 1 residual
+  float alpha_max = 0.f;
+  void* write_key = nullptr;       // [B,T,H,D] dtype
+  float* alpha = nullptr;          // [B,T,H]
+  float* stats = nullptr;          // [2,B,H,T] largest weight, |write key| / |k_hat|, or NULL
 };
 
 int block_dims(int B, int T, int H, int top_k, int block_size, int top_blocks, int mode, int& nb, int& eb, int& kk,
@@ -606,7 +619,8 @@ int block_dims(int B, int T, int H, int top_k, int block_size, int top_blocks, i
   return SGSA_OK;
 }
 
-BlockWs block_ws(int B, int T, int H, int nb, int kk, int ks, int mode, bool want_weights) {
+BlockWs block_ws(int B, int T, int H, int nb, int kk, int ks, int mode, bool want_weights, int eb = 0,
+                 bool own_lists = false) {
   const size_t rows = (size_t)B * H * T;
   const size_t w = mode == 1 ? (size_t)kk : (size_t)ks;
   BlockWs L{};
@@ -627,6 +641,8 @@ BlockWs block_ws(int B, int T, int H, int nb, int kk, int ks, int mode, bool wan
   L.mnvb = take((size_t)B * T * 4);
   L.mkqb = take((size_t)T * 4);
   L.mbits = take((size_t)B * ((T + 31) / 32) * 4);
+  L.own_idx = (own_lists && mode == 1) ? take(rows * kk * 4) : 0;
+  L.own_bidx = own_lists ? take(rows * eb * 4) : 0;
   L.total = o;
   return L;
 }
@@ -635,7 +651,7 @@ int block_retrieve_impl(int dtype, int B, int T, int H, int D, int top_k, int bl
                         int causal, float tau_c, int local_window, int sink_size, const void* q, const void* k,
                         const void* v, const uint8_t* mask, int32_t* indices, int32_t* block_indices,
                         float* block_scores, float* weights, void* k_hat, void* v_hat, float* diag, void* workspace,
-                        size_t workspace_bytes, void* stream);
+                        size_t workspace_bytes, void* stream, const BlockGate* gate = nullptr);
 }  // namespace
 
 int sgsa_block_retrieve_workspace_size(int B, int T, int H, int top_k, int block_size, int top_blocks, int mode,
@@ -668,6 +684,28 @@ int sgsa_block_retrieve_masked(int dtype, int B, int T, int H, int D, int top_k,
                              v_hat, diag, workspace, workspace_bytes, stream);
 }
 
+int sgsa_block_layer_retrieve_workspace_size(int B, int T, int H, int top_k, int block_size, int top_blocks,
+                                             int mode, size_t* bytes) {
+  int nb, eb, kk, ks;
+  if (int s = block_dims(B, T, H, top_k, block_size, top_blocks, mode, nb, eb, kk, ks)) return s;
+  REQUIRE(bytes);
+  *bytes = block_ws(B, T, H, nb, kk, ks, mode, false, eb, true).total;
+  return SGSA_OK;
+}
+
+int sgsa_block_layer_retrieve(int dtype, int B, int T, int H, int D, int top_k, int block_size, int top_blocks,
+                              int mode, float tau_c, const void* q_ret, const void* k, const void* v,
+                              const uint8_t* attention_mask, const float* budget, int write_mode, float alpha_max,
+                              void* write_key, void* v_hat, float* alpha, float* row_stats, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  BlockGate gate;
+  gate.budget = budget; gate.write_mode = write_mode; gate.alpha_max = alpha_max;
+  gate.write_key = write_key; gate.alpha = alpha; gate.stats = row_stats;
+  return block_retrieve_impl(dtype, B, T, H, D, top_k, block_size, top_blocks, mode, 1, tau_c, 64, 8, q_ret, k, v,
+                             attention_mask, nullptr, nullptr, nullptr, nullptr, nullptr, v_hat, nullptr, workspace,
+                             workspace_bytes, stream, &gate);
+}
+
 }  // extern "C"
 
 namespace {
@@ -675,17 +713,29 @@ int block_retrieve_impl(int dtype, int B, int T, int H, int D, int top_k, int bl
                         int causal, float tau_c, int local_window, int sink_size, const void* q, const void* k,
                         const void* v, const uint8_t* mask, int32_t* indices, int32_t* block_indices,
                         float* block_scores, float* weights, void* k_hat, void* v_hat, float* diag, void* workspace,
-                        size_t workspace_bytes, void* stream) {
+                        size_t workspace_bytes, void* stream, const BlockGate* gate) {
   if (int s = check_dtype(dtype)) return s;
   if (int s = check_dims(B, T, H, D)) return s;
   int nb, eb, kk, ks;
   if (int s = block_dims(B, T, H, top_k, block_size, top_blocks, mode, nb, eb, kk, ks)) return s;
-  REQUIRE(q); REQUIRE(k); REQUIRE(v); REQUIRE(block_indices); REQUIRE(k_hat); REQUIRE(v_hat); REQUIRE(workspace);
-  if (mode == 1 && indices == nullptr) return fail(SGSA_ERR_INVALID_ARG, "block_token needs the indices output");
+  REQUIRE(q); REQUIRE(k); REQUIRE(v); REQUIRE(v_hat); REQUIRE(workspace);
+  if (gate == nullptr) {
+    REQUIRE(block_indices); REQUIRE(k_hat);
+    if (mode == 1 && indices == nullptr) return fail(SGSA_ERR_INVALID_ARG, "block_token needs the indices output");
+  } else {
+    if (gate->budget == nullptr || gate->write_key == nullptr || gate->alpha == nullptr)
+      return fail(SGSA_ERR_INVALID_ARG, "budget logits, write_key and alpha must not be NULL");
+    if (gate->write_mode != 0 && gate->write_mode != 1)
+      return fail(SGSA_ERR_INVALID_ARG, "write_mode must be 0 (direct) or 1 (residual)");
+  }
   if ((long)T * H * D * 4 > 0x7fffffffL) return fail(SGSA_ERR_UNSUPPORTED, "one head's keys exceed 2 GiB of offsets");
-  const BlockWs L = block_ws(B, T, H, nb, kk, ks, mode, weights != nullptr);
+  const BlockWs L = block_ws(B, T, H, nb, kk, ks, mode, weights != nullptr, eb, gate != nullptr);
   if (workspace_bytes < L.total) return fail(SGSA_ERR_WORKSPACE, "workspace %zu < %zu bytes", workspace_bytes, L.total);
   char* base = static_cast<char*>(workspace);
+  if (gate != nullptr) {
+    block_indices = reinterpret_cast<int32_t*>(base + L.own_bidx);
+    if (mode == 1) indices = reinterpret_cast<int32_t*>(base + L.own_idx);
+  }
   sgsa::BlockArgs a{};
   a.dtype = dtype; a.B = B; a.T = T; a.H = H; a.D = D;
   a.bs = block_size; a.nb = nb; a.eb = eb; a.mode = mode; a.kk = kk; a.ks = ks; a.causal = causal ? 1 : 0;
@@ -722,6 +772,10 @@ int block_retrieve_impl(int dtype, int B, int T, int H, int D, int top_k, int bl
   g.diag = diag; g.max_index = reinterpret_cast<int32_t*>(base + L.maxidx);
   g.margin_in = a.bmargin;
   g.ent_pad = mode == 0 ? (float)(T - ks) : 0.f;
+  if (gate != nullptr) {
+    g.budget = gate->budget; g.write_mode = gate->write_mode; g.alpha_max = gate->alpha_max;
+    g.write_key = gate->write_key; g.alpha = gate->alpha; g.stats = gate->stats;
+  }
   if (int s = hip_status(sgsa::launch_sparse_gather(g, st), "sgsa_block_retrieve (gather)")) return s;
   if (mode == 0 && weights != nullptr)
     return hip_status(sgsa::launch_block_dense_weights(B, H, T, ks, a.slot_idx, g.weights, a.counts, weights, st),

@@ -82,7 +82,7 @@ class HybridConfig:
         return SGSAConfig(vocab_size=self.vocab_size, hidden_size=self.hidden_size,
                           intermediate_size=self.intermediate_size, num_hidden_layers=1,
                           num_attention_heads=self.num_attention_heads, num_kv_heads=self.num_attention_heads,
-                          layer_norm_eps=self.layer_norm_eps, top_k=self.top_k,
+                          layer_norm_eps=self.layer_norm_eps, top_k=self.top_k, retrieval_mode="token_only",
                           sgsa_write_mode=self.sgsa_write_mode, alpha_max=self.alpha_max, tau_c=self.tau_c)
 
 

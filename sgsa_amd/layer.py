@@ -162,3 +162,72 @@ def sgsa_layer_retrieve(
         _abi.ptr(uc), _WRITE_MODES[write_mode], float(alpha_max), float(tau_c), _abi.ptr(wk), _abi.ptr(vh),
         _abi.ptr(al), _abi.ptr(rs), _abi.ptr(ws), ws.numel(), _abi.stream_of(rc)))
     return wk, vh, al
+
+
+_BLOCK_MODES = {"block_only": 0, "block_token": 1}
+
+
+def sgsa_block_layer_retrieve(
+    q_ret: Tensor,
+    k: Tensor,
+    v: Tensor,
+    budget_logits: Tensor,
+    top_k: int,
+    block_size: int,
+    top_blocks: int,
+    mode: str = "block_token",
+    write_mode: str = "direct",
+    alpha_max: float = 0.25,
+    tau_c: float = 0.1,
+    workspace: Optional[LayerWorkspace] = None,
+    attention_mask: Optional[Tensor] = None,
+    stats: Optional[dict] = None,
+) -> Tuple[Tensor, Tensor, Tensor]:
+    """The retrieval half of SGSABlock.forward in the block modes (sgsa_block_layer_retrieve):
+    SparseRetriever's block_only / block_token retrieval (modelings/modeling_sgsa.py:444-463,
+    causal, with the optional padding mask of :421-428), then the write key and alpha gate
+    of SGSAStateLayer (:543-552, :497-504).
+
+    q_ret, k, v [B,T,H,D] (float32 or bfloat16); budget_logits [B,T,H].  Returns write_key /
+    v_hat [B,T,H,D] in the input dtype and alpha [B,T,H] float32.  ``stats`` receives
+    "alpha" and "row_stats" [2,B,H,T] (largest weight; |write key| / |k_hat| in residual mode).
+    """
+    if not q_ret.is_cuda:
+        raise ValueError("sgsa_block_layer_retrieve: the SGSA kernels run on a ROCm GPU; got CPU tensors")
+    if mode not in _BLOCK_MODES:
+        raise ValueError(f"mode must be one of {sorted(_BLOCK_MODES)}, got {mode!r}")
+    if write_mode not in _WRITE_MODES:
+        raise ValueError(f"write_mode must be one of {sorted(_WRITE_MODES)}")
+    B, T, H, D = q_ret.shape
+    for name, t in (("k", k), ("v", v)):
+        if t.shape != q_ret.shape or t.dtype != q_ret.dtype:
+            raise ValueError(f"{name} must match q_ret in shape and dtype")
+    if budget_logits.shape != (B, T, H):
+        raise ValueError(f"budget_logits has shape {tuple(budget_logits.shape)}, expected {(B, T, H)}")
+    dev = q_ret.device
+    m = _BLOCK_MODES[mode]
+    rc, kc, vc = (t.contiguous() for t in (q_ret, k, v))
+    uc = budget_logits.float().contiguous()
+    am = None
+    if attention_mask is not None:
+        if tuple(attention_mask.shape) != (B, T):
+            raise ValueError(f"attention_mask must have shape [batch, seq] = {(B, T)}, got "
+                             f"{tuple(attention_mask.shape)}")
+        am = (attention_mask.to(dev) != 0).to(torch.uint8).contiguous()
+    n = ctypes.c_size_t()
+    _abi.check(_abi.lib().sgsa_block_layer_retrieve_workspace_size(B, T, H, int(top_k), int(block_size),
+                                                                   int(top_blocks), m, ctypes.byref(n)))
+    ws = (workspace or LayerWorkspace()).get(max(n.value, 1), dev)
+    wk = torch.empty_like(kc)
+    vh = torch.empty_like(kc)
+    al = torch.empty(B, T, H, device=dev, dtype=torch.float32)
+    rs = None
+    if stats is not None:
+        stats["alpha"] = al
+        rs = stats["row_stats"] = torch.empty(2, B, H, T, device=dev, dtype=torch.float32)
+    _abi.check(_abi.lib().sgsa_block_layer_retrieve(
+        _abi.dtype_code(q_ret.dtype), B, T, H, D, int(top_k), int(block_size), int(top_blocks), m, float(tau_c),
+        _abi.ptr(rc), _abi.ptr(kc), _abi.ptr(vc), _abi.ptr(am), _abi.ptr(uc), _WRITE_MODES[write_mode],
+        float(alpha_max), _abi.ptr(wk), _abi.ptr(vh), _abi.ptr(al), _abi.ptr(rs), _abi.ptr(ws), ws.numel(),
+        _abi.stream_of(rc)))
+    return wk, vh, al

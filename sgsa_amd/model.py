@@ -1,7 +1,7 @@
 """The SGSA causal LM around the layer kernels: SGSABlock and SGSAForCausalLM.
 
-Mirrors modelings/modeling_sgsa.py:634-767 (SGSABlock, SGSAForCausalLM) for the
-token_only retrieval mode with the chunked state backend:
+Mirrors modelings/modeling_sgsa.py:634-767 (SGSABlock, SGSAForCausalLM) in every
+retrieval mode (token_only, block_only, block_token) and state backend:
 
   h   = (embed(ids) + pos_embed(positions)) * attention_mask         (:739-743)
   per block (:669-709):
@@ -15,11 +15,19 @@ token_only retrieval mode with the chunked state backend:
   metrics: per layer alpha_mean, k_hat_perp_ratio_mean, retrieval_confidence_mean
            and the path flags (:697-708, :744-752)
 
-The layer core runs in the HIP library (sgsa_layer_forward); the projections,
-norms and the MLP are plain GEMMs and elementwise ops left to PyTorch
-(rocBLAS / hipBLASLt).  RMSNorm and GatedMLP are the fla-core modules the
-reference imports (modeling_sgsa.py:40-41); their arithmetic is the in-tree
-restatement of modelings/hybrid_dense_delta_topk.py:94-117.  Forward only.
+The layer core runs in the HIP library: sgsa_layer_forward for token_only with
+the chunked backend, else the retrieval half (sgsa_layer_retrieve or, in the
+block modes, sgsa_block_layer_retrieve) followed by chunk_sgsa or
+fused_recurrent_sgsa as ``linear_backend`` selects (:554-609).  The projections
+and the MLP are GEMMs left to PyTorch (hipBLASLt); norms, gates and the MLP
+activation are one HIP launch each.  RMSNorm and GatedMLP are the fla-core
+modules the reference imports (modeling_sgsa.py:40-41); their arithmetic is the
+in-tree restatement of modelings/hybrid_dense_delta_topk.py:94-117.
+
+Forward only: the retrieval half has no backward, so SGSABlock and
+SGSAForCausalLM raise when autograd would record them (run them under
+torch.no_grad() or torch.inference_mode()) instead of returning a loss whose
+gradients silently miss the attention parameters.
 """
 
 from __future__ import annotations
@@ -34,15 +42,16 @@ import torch.nn.functional as F
 
 from . import _abi
 
-from .layer import LayerWorkspace, sgsa_layer_forward, sgsa_layer_retrieve
+from .layer import LayerWorkspace, sgsa_block_layer_retrieve, sgsa_layer_forward, sgsa_layer_retrieve
 from .ops import chunk_sgsa
+from .recurrent import fused_recurrent_sgsa
 
 Tensor = torch.Tensor
 
 
 @dataclass
 class SGSAConfig:
-    """The fields of modelings/modeling_sgsa.py:47-78 that the token_only path reads."""
+    """SGSAConfig of modelings/modeling_sgsa.py:47-78: the same fields and defaults."""
 
     vocab_size: int = 32000
     hidden_size: int = 256
@@ -55,12 +64,18 @@ class SGSAConfig:
     layer_norm_eps: float = 1e-6
     pad_token_id: int = 0
     top_k: int = 16
-    retrieval_mode: str = "token_only"
-    sgsa_write_mode: str = "direct"   # direct | residual
+    block_size: int = 32
+    top_blocks: int = 2
+    retrieval_mode: str = "block_token"   # token_only | block_only | block_token
+    sgsa_write_mode: str = "direct"       # none | direct | residual
     alpha_max: float = 0.25
     tau_c: float = 0.1
+    local_window: int = 64
+    sink_size: int = 8
     sparse_output_lambda: float = 0.0
     tie_word_embeddings: bool = True
+    linear_backend: str = "auto"   # auto | python | torch_chunk | recurrent | triton_recurrent | fla_gdn
+    retrieval_backend: str = "auto"   # auto | torch | flash_moba (flash_moba absent: the torch path's semantics)
     chunk_size: int = 64
 
     @property
@@ -149,9 +164,11 @@ _WEIGHT_OK: dict = {}
 
 def _weight_ok(weight: Tensor, bias: Optional[Tensor]) -> bool:
     """weight (and bias) fit sgsa_linear_rows: bf16, contiguous, 16-byte aligned; remembered per
-    (storage, version) pair, and the library's entry point looked up once."""
+    (address, version, shape, strides, dtype) of each, so that a strided view of a checked
+    weight is checked on its own, and the library's entry point looked up once."""
     global _LINEAR_ROWS
-    key = (weight.data_ptr(), weight._version, None if bias is None else (bias.data_ptr(), bias._version))
+    key = (weight.data_ptr(), weight._version, tuple(weight.shape), weight.stride(), weight.dtype,
+           None if bias is None else (bias.data_ptr(), bias._version, tuple(bias.shape), bias.stride(), bias.dtype))
     ok = _WEIGHT_OK.get(key)
     if ok is None:
         ok = weight.is_contiguous() and weight.data_ptr() % 16 == 0 and \
@@ -224,15 +241,42 @@ class GatedMLP(nn.Module):
         return lin(self.down_proj, act)
 
 
+# linear_backend -> the state update SGSAStateLayer.forward runs (modeling_sgsa.py:554-609).  fla is
+# not part of this build, so "fla_gdn" and "python" take the reference's last branch, the token
+# recurrence naive_recurrent_sgsa, whose semantics the recurrent kernel computes.
+_STATE_BACKENDS = {"auto": "chunk", "torch_chunk": "chunk", "recurrent": "recurrent",
+                   "triton_recurrent": "recurrent", "fused_recurrent": "recurrent", "python": "naive",
+                   "fla_gdn": "naive"}
+_RETRIEVAL_MODES = ("token_only", "block_only", "block_token")
+
+
+def refuse_autograd(module: nn.Module, *inputs: Tensor) -> None:
+    """Raise when autograd would record ``module`` on ``inputs``: the SGSA retrieval (top-k
+    select, weights, gathers, gate) has no backward here, so a loss through it would leave
+    the q/k/v/q_ret projections and the gates without gradients."""
+    if not torch.is_grad_enabled():
+        return
+    if any(t.requires_grad for t in inputs) or any(p.requires_grad for p in module.parameters()):
+        raise RuntimeError(
+            f"{type(module).__name__}.forward is forward-only: the SGSA retrieval half has no backward in this "
+            "build, so gradients would silently miss its projections. Run it under torch.no_grad() or "
+            "torch.inference_mode(), or freeze its parameters (requires_grad_(False)); chunk_sgsa and "
+            "fused_recurrent_sgsa themselves are differentiable.")
+
+
 class SGSABlock(nn.Module):
     def __init__(self, config: SGSAConfig) -> None:
         super().__init__()
-        if config.retrieval_mode != "token_only":
-            raise ValueError("only retrieval_mode='token_only' runs on the SGSA kernels")
+        if config.retrieval_mode not in _RETRIEVAL_MODES:
+            raise ValueError(f"retrieval_mode must be one of {_RETRIEVAL_MODES}, got {config.retrieval_mode!r}")
         if config.num_kv_heads != config.num_attention_heads:
             raise ValueError("the SGSA block uses one key/value head per query head")
-        if config.sgsa_write_mode not in ("direct", "residual"):
-            raise ValueError("sgsa_write_mode must be 'direct' or 'residual'")
+        if config.sgsa_write_mode not in ("none", "direct", "residual"):
+            raise ValueError("sgsa_write_mode must be 'none', 'direct' or 'residual'")
+        if config.linear_backend not in _STATE_BACKENDS:
+            raise ValueError(f"linear_backend must be one of {sorted(_STATE_BACKENDS)}, got {config.linear_backend!r}")
+        if config.retrieval_backend not in ("auto", "torch", "flash_moba"):
+            raise ValueError(f"retrieval_backend must be auto, torch or flash_moba, got {config.retrieval_backend!r}")
         if config.dropout != 0.0:
             raise ValueError("dropout is a training feature; the forward here is inference only")
         self.config = config
@@ -277,25 +321,43 @@ class SGSABlock(nn.Module):
         """SGSABlock.forward (modeling_sgsa.py:660-709): (hidden states, metrics).
 
         attention_mask [B,T] (nonzero = real token) reaches the retrieval only
-        (:668-674).  The metrics are the reference's: alpha_mean,
-        k_hat_perp_ratio_mean (residual write mode, else 0),
-        retrieval_confidence_mean (mean largest retrieval weight) and the path
-        flags, of which used_torch_chunk is 1 -- the chunked update runs.
+        (:668-674).  ``retrieval_mode`` picks the token or block retrieval
+        (:430-463), ``sgsa_write_mode`` "none" drops the sparse write from the
+        state update while alpha is still reported (:543-552, :557-609), and
+        ``linear_backend`` the chunked or the token-recurrent update (:554-609).
+        The metrics are the reference's: alpha_mean, k_hat_perp_ratio_mean
+        (residual write mode, else 0), retrieval_confidence_mean (mean largest
+        retrieval weight) and the path flags.  Raises under autograd (no
+        retrieval backward).
         """
+        refuse_autograd(self, h)
         cfg = self.config
         B, T, C = h.shape
         q, k, v, q_ret, beta, gamma, budget = self._project(h)
         stats: Dict[str, Tensor] = {}
-        if cfg.sparse_output_lambda > 0:
-            wk, vh, al = sgsa_layer_retrieve(q_ret, k, v, budget, cfg.top_k, cfg.sgsa_write_mode, cfg.alpha_max,
-                                             cfg.tau_c, workspace=self._ws, attention_mask=attention_mask,
-                                             stats=stats)
-            att, _ = chunk_sgsa(q, k, v, beta, gamma, wk, vh, al)
+        backend = _STATE_BACKENDS[cfg.linear_backend]
+        sparse = cfg.sgsa_write_mode != "none"
+        # with write_mode "none" the reference's write key is k_hat (:546-550): alpha as "direct"
+        wm = "residual" if cfg.sgsa_write_mode == "residual" else "direct"
+        vh = None
+        if cfg.retrieval_mode == "token_only" and backend == "chunk" and sparse and cfg.sparse_output_lambda <= 0:
+            att, _ = sgsa_layer_forward(q, k, v, q_ret, beta, gamma, budget, cfg.top_k, write_mode=wm,
+                                        alpha_max=cfg.alpha_max, tau_c=cfg.tau_c, output_final_state=False,
+                                        workspace=self._ws, attention_mask=attention_mask, stats=stats)
         else:
-            att, _ = sgsa_layer_forward(q, k, v, q_ret, beta, gamma, budget, cfg.top_k,
-                                        write_mode=cfg.sgsa_write_mode, alpha_max=cfg.alpha_max, tau_c=cfg.tau_c,
-                                        output_final_state=False, workspace=self._ws,
-                                        attention_mask=attention_mask, stats=stats)
+            if cfg.retrieval_mode == "token_only":
+                wk, vh, al = sgsa_layer_retrieve(q_ret, k, v, budget, cfg.top_k, wm, cfg.alpha_max, cfg.tau_c,
+                                                 workspace=self._ws, attention_mask=attention_mask, stats=stats)
+            else:
+                wk, vh, al = sgsa_block_layer_retrieve(q_ret, k, v, budget, cfg.top_k, cfg.block_size,
+                                                       cfg.top_blocks, cfg.retrieval_mode, wm, cfg.alpha_max,
+                                                       cfg.tau_c, workspace=self._ws, attention_mask=attention_mask,
+                                                       stats=stats)
+            sk, sv, sa = (wk, vh, al) if sparse else (None, None, None)
+            if backend == "chunk":
+                att, _ = chunk_sgsa(q, k, v, beta, gamma, sk, sv, sa)
+            else:
+                att, _ = fused_recurrent_sgsa(q, k, v, beta, gamma, sk, sv, sa)
         out = self.o_proj(att.reshape(B, T, C))
         if cfg.sparse_output_lambda > 0:
             out = out + cfg.sparse_output_lambda * self.sparse_out_proj(vh.reshape(B, T, C))
@@ -303,13 +365,14 @@ class SGSABlock(nn.Module):
         h = h + self.mlp(n)
         rs = stats["row_stats"]
         zero = torch.zeros((), device=h.device)
+        one = torch.ones((), device=h.device)
         metrics = {
             "alpha_mean": stats["alpha"].mean(),
             "k_hat_perp_ratio_mean": rs[1].mean() if cfg.sgsa_write_mode == "residual" else h.new_zeros(()),
             "retrieval_confidence_mean": rs[0].mean(),
             "used_fla_gdn": zero,
-            "used_torch_chunk": torch.ones((), device=h.device),
-            "used_recurrent": zero,
+            "used_torch_chunk": one if backend == "chunk" else zero,
+            "used_recurrent": one if backend == "recurrent" else zero,
         }
         return h, metrics
 
@@ -353,6 +416,7 @@ class SGSAForCausalLM(nn.Module):
         and, with labels, "loss" -- the next-token cross entropy with ignore_index
         -100 (:758-766).  attention_mask [B,T] zeroes the padded embeddings
         (:740-741) and masks padded keys and queries in every retrieval."""
+        refuse_autograd(self)
         B, T = input_ids.shape
         if T > self.config.max_position_embeddings:
             raise ValueError("sequence length exceeds max_position_embeddings")

@@ -24,15 +24,6 @@ pytestmark = pytest.mark.gpu
 import sgsa_amd  # noqa: E402  (pure Python; the HIP library loads on first call and raises if missing)
 
 
-def _close(got, ref, rel, name=""):
-    got = got.detach().float().cpu()
-    ref = ref.detach().float().cpu()
-    scale = ref.abs().max().clamp_min(1e-12)
-    err = (got - ref).abs().max() / scale
-    assert torch.isfinite(got).all(), f"{name}: non-finite"
-    assert err <= rel, f"{name}: max error {err:.3e} relative to max|ref| {scale:.3e} exceeds {rel:.1e}"
-
-
 @pytest.fixture(scope="module")
 def config1(dev):
     B, T, H, D, k = 4, 8192, 16, 128, 256
@@ -43,14 +34,20 @@ def config1(dev):
     return x, g, k, o, st
 
 
-@pytest.mark.parametrize("b,h", [(0, 0), (3, 11)])
-def test_config1_slice_matches_oracle(config1, b, h):
-    x, _, k, o, st = config1
+@pytest.mark.parametrize("b,h,write_mode", [(0, 0, "direct"), (3, 11, "direct"), (2, 5, "residual")])
+def test_config1_slice_matches_oracle(config1, b, h, write_mode):
+    # max-norm 2e-2 of the largest magnitude, and 99% of the entries above 1% of it
+    # within 2e-2 of their own magnitude
+    x, g, k, o, st = config1
+    if write_mode != "direct":
+        o, st = sgsa_amd.sgsa_layer_forward(g["q"], g["k"], g["v"], g["q"], g["beta"], g["gamma"], g["budget"], k,
+                                            write_mode=write_mode)
+        torch.cuda.synchronize()
     sl = lambda t: t[b:b + 1, :, h:h + 1].contiguous()
     ref = O.sgsa_layer_forward(sl(x["q_f32"]), sl(x["k_f32"]), sl(x["v_f32"]), sl(x["q_f32"]), sl(x["beta"]),
-                               sl(x["gamma"]), sl(x["budget"]), k)
-    _close(o[b:b + 1, :, h:h + 1], ref["o"], 2e-2, "o")
-    _close(st[b:b + 1, h:h + 1], ref["final_state"], 2e-2, "final_state")
+                               sl(x["gamma"]), sl(x["budget"]), k, write_mode=write_mode)
+    close(o[b:b + 1, :, h:h + 1], ref["o"], 2e-2, f"o ({write_mode})", elem_p99=2e-2)
+    close(st[b:b + 1, h:h + 1], ref["final_state"], 2e-2, f"final_state ({write_mode})", elem_p99=2e-2)
 
 
 def test_config1_chunk_equals_recurrence(config1):
@@ -59,8 +56,8 @@ def test_config1_chunk_equals_recurrence(config1):
     o2, st2 = sgsa_amd.fused_recurrent_sgsa(g["q"], g["k"], g["v"], g["beta"], g["gamma"], wk, vh, al,
                                             output_final_state=True)
     torch.cuda.synchronize()
-    _close(o, o2, 2e-2, "o")
-    _close(st, st2, 2e-2, "final_state")
+    close(o, o2, 2e-2, "o", elem_p99=2e-2)
+    close(st, st2, 2e-2, "final_state", elem_p99=2e-2)
 
 
 def test_config3_tile_lists_on_sampled_rows(dev):

@@ -7,17 +7,20 @@ The CPU oracle cannot run all sixteen heads, so the test combines:
       and sgsa_layer_fwd equals chunk_sgsa fed the retrieval outputs;
   (a') the gather's own selection (its known-answer variant: per-row count,
       index sum and index-hash xor) equals the row-list K1's on every row;
-  (b) on 32 sampled (head, row) pairs -- rows t < k, t = k-1, t = k, mid
-      sequence and the last row -- K1's per-row cut applied to the fp32 scores
-      sgsa_score_dump returns selects exactly the lowest-index top-k of those
-      scores (oracle.topk_lowest_index), with the same count and top-2;
+  (b) on 256 sampled (head, row) pairs -- 32 chosen rows (t < k, t = k-1,
+      t = k, mid sequence, the last row) and 14 more per head, one from each
+      of 14 equal strata of [0, T) -- K1's per-row cut applied to the fp32
+      scores sgsa_score_dump returns selects exactly the lowest-index top-k of
+      those scores (oracle.topk_lowest_index), with the same count and top-2;
   (c) on those rows the write key, v_hat and alpha match the oracle's
       token_topk_retrieval / write_key / compute_alpha (modeling_sgsa.py:126-134,
-      :361-405, :497-504, :546-551) within 2e-2;
-  (d) the output and final state of two whole heads match the oracle's layer
+      :361-405, :497-504, :546-551) within 2e-2, in both write modes (direct
+      and residual);
+  (d) the output and final state of whole heads match the oracle's layer
       (fp32 recurrence, naive.py:34-57) run on that head alone within 2e-2 of
       the largest magnitude, and 99% of their entries above 1% of it within
-      2e-2 of their own magnitude -- heads are independent in the layer.
+      2e-2 of their own magnitude -- heads are independent in the layer; two
+      heads in the direct write mode, one in the residual mode.
 """
 
 import pytest
@@ -38,6 +41,20 @@ PAIRS = [(0, 0), (0, 32767), (1, 1), (1, 16384), (2, 63), (2, 2047), (3, 64), (3
          (12, 5000), (12, 31000), (13, 2050), (13, 16385), (14, 10000), (14, 32700), (15, 2047), (15, 32767)]
 
 
+def _stratified_pairs(per_head=14, seed=7):
+    """per_head rows for every head, row i drawn uniformly from stratum i of [0, T)."""
+    g = torch.Generator().manual_seed(seed)
+    out = []
+    for h in range(H):
+        for i in range(per_head):
+            lo, hi = i * T // per_head, (i + 1) * T // per_head
+            out.append((h, lo + int(torch.randint(0, hi - lo, (1,), generator=g))))
+    return out
+
+
+PAIRS = PAIRS + [p for p in _stratified_pairs() if p not in PAIRS]
+
+
 @pytest.fixture(scope="module")
 def ns(dev):
     x = O.make_inputs(B, T, H, D, dtype=torch.bfloat16, seed=0)
@@ -46,8 +63,12 @@ def ns(dev):
     o, st = sgsa_amd.sgsa_layer_forward(g["q"], g["k"], g["v"], g["q"], g["beta"], g["gamma"], g["budget"], K)
     wk, vh, al = sgsa_amd.sgsa_layer_retrieve(g["q"], g["k"], g["v"], g["budget"], K)
     thr, t2, cnt = sgsa_amd.score_topk_thresholds(g["q"], g["k"], K)
+    o_r, st_r = sgsa_amd.sgsa_layer_forward(g["q"], g["k"], g["v"], g["q"], g["beta"], g["gamma"], g["budget"], K,
+                                            write_mode="residual")
+    wk_r, vh_r, al_r = sgsa_amd.sgsa_layer_retrieve(g["q"], g["k"], g["v"], g["budget"], K, write_mode="residual")
     torch.cuda.synchronize()
-    return {"x": x, "g": g, "o": o, "st": st, "wk": wk, "vh": vh, "al": al, "thr": thr, "t2": t2, "cnt": cnt}
+    return {"x": x, "g": g, "o": o, "st": st, "wk": wk, "vh": vh, "al": al, "thr": thr, "t2": t2, "cnt": cnt,
+            "residual": {"o": o_r, "st": st_r, "wk": wk_r, "vh": vh_r, "al": al_r}}
 
 
 def test_layer_is_its_two_halves(ns):
@@ -102,31 +123,43 @@ def test_cut_selects_the_lowest_index_topk_of_the_dumped_scores(ns):
                 assert t2[0, h, r, 1] == ov[0, 0, 0, 1], f"head {h} row {r}: top-2"
 
 
-@pytest.mark.parametrize("write_mode", ["direct"])
+def test_sample_covers_every_head_and_stratum():
+    assert len(PAIRS) >= 256
+    assert {h for h, _ in PAIRS} == set(range(H))
+    assert len({r * 16 // T for _, r in PAIRS}) == 16
+
+
+@pytest.mark.parametrize("write_mode", ["direct", "residual"])
 def test_sampled_rows_match_oracle_retrieval(ns, write_mode):
     x = ns["x"]
+    out = ns if write_mode == "direct" else ns["residual"]
+    # the residual mode's v_hat is the direct mode's: the write key changes, the retrieval does not
+    if write_mode == "residual":
+        assert torch.equal(out["vh"], ns["vh"])
     for h, r in PAIRS:
         sl = lambda t: t[:, :, h:h + 1].contiguous()
         ret = O.token_topk_retrieval(sl(x["q_f32"]), sl(x["k_f32"]), sl(x["v_f32"]), K, rows=(r, r + 1))
         wk = O.write_key(ret["k_hat"], sl(x["k_f32"])[:, r:r + 1], write_mode)
         al = O.compute_alpha(ret["diagnostics"]["concentration"], ret["diagnostics"]["novelty"],
                              sl(x["budget"])[:, r:r + 1], wk, ret["v_hat"])
-        for name, got, want in (("write key", ns["wk"][0, r, h], wk[0, 0, 0]),
-                                ("v_hat", ns["vh"][0, r, h], ret["v_hat"][0, 0, 0])):
-            close(got, want, 2e-2, f"{name} head {h} row {r}")
-        scalar_close(ns["al"][0, r, h].item(), al[0, 0, 0].item(), 2e-2, 1e-4, f"alpha head {h} row {r}")
+        for name, got, want in (("write key", out["wk"][0, r, h], wk[0, 0, 0]),
+                                ("v_hat", out["vh"][0, r, h], ret["v_hat"][0, 0, 0])):
+            close(got, want, 2e-2, f"{write_mode} {name} head {h} row {r}")
+        scalar_close(out["al"][0, r, h].item(), al[0, 0, 0].item(), 2e-2, 1e-4,
+                     f"{write_mode} alpha head {h} row {r}")
 
 
-@pytest.mark.parametrize("h", [0, 13])
-def test_whole_head_matches_oracle_layer(ns, h):
+@pytest.mark.parametrize("h,write_mode", [(0, "direct"), (13, "direct"), (6, "residual")])
+def test_whole_head_matches_oracle_layer(ns, h, write_mode):
     x = ns["x"]
+    out = ns if write_mode == "direct" else ns["residual"]
     sl = lambda t: t[:, :, h:h + 1].contiguous()
-    print(f"oracle layer on head {h} (T={T})", flush=True)
+    print(f"oracle layer on head {h} (T={T}, {write_mode})", flush=True)
     ref = O.sgsa_layer_forward(sl(x["q_f32"]), sl(x["k_f32"]), sl(x["v_f32"]), sl(x["q_f32"]), sl(x["beta"]),
-                               sl(x["gamma"]), sl(x["budget"]), K)
+                               sl(x["gamma"]), sl(x["budget"]), K, write_mode=write_mode)
     # elementwise as well: 99% of the entries above 1% of the largest within 2e-2 of their own magnitude
-    close(ns["o"][:, :, h:h + 1], ref["o"], 2e-2, f"o head {h}", elem_p99=2e-2)
-    close(ns["st"][:, h:h + 1], ref["final_state"], 2e-2, f"final_state head {h}", elem_p99=2e-2)
-    close(ns["wk"][:, :, h:h + 1], ref["write_key"], 2e-2, f"write key head {h}")
-    close(ns["vh"][:, :, h:h + 1], ref["v_hat"], 2e-2, f"v_hat head {h}")
-    close(ns["al"][:, :, h:h + 1], ref["alpha"], 2e-2, f"alpha head {h}")
+    close(out["o"][:, :, h:h + 1], ref["o"], 2e-2, f"o head {h}", elem_p99=2e-2)
+    close(out["st"][:, h:h + 1], ref["final_state"], 2e-2, f"final_state head {h}", elem_p99=2e-2)
+    close(out["wk"][:, :, h:h + 1], ref["write_key"], 2e-2, f"write key head {h}")
+    close(out["vh"][:, :, h:h + 1], ref["v_hat"], 2e-2, f"v_hat head {h}")
+    close(out["al"][:, :, h:h + 1], ref["alpha"], 2e-2, f"alpha head {h}")

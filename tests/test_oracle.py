@@ -13,6 +13,7 @@ import math
 
 import pytest
 import torch
+import torch.nn.functional as F
 
 from oracle import sgsa_oracle as O
 
@@ -496,3 +497,55 @@ def test_model_residual_structure():
     Z2 = dict(Z)
     Z2["layers.0.q_ret_proj.weight"] = P["layers.0.q_proj.weight"] * -1.0
     assert not torch.allclose(O.sgsa_model_forward(Z2, ids, num_layers=1, num_heads=2, top_k=3), head(h1))
+
+
+def test_layer_block_modes_reduce_to_known_forms():
+    # block_token with unit blocks, every block kept: the token_only layer (the same
+    # candidates, the same masked top-k); block_only with every block kept: v_hat is causal
+    # softmax attention (modeling_sgsa.py:346-359), and the write gate reads it
+    g = torch.Generator().manual_seed(11)
+    B, T, H, D, k = 2, 13, 2, 8, 4
+    q, kk, v, qr = (torch.randn(B, T, H, D, generator=g) for _ in range(4))
+    beta, gamma, bud = torch.rand(B, T, H, generator=g), torch.rand(B, T, H, generator=g), torch.randn(B, T, H, generator=g)
+    args = (q, kk, v, qr, beta, gamma, bud, k)
+    for wm in ("direct", "residual"):
+        tok = O.sgsa_layer_forward(*args, write_mode=wm)
+        blk = O.sgsa_layer_forward(*args, write_mode=wm, retrieval_mode="block_token", block_size=1, top_blocks=T)
+        for name in ("o", "final_state", "write_key", "v_hat", "alpha"):
+            torch.testing.assert_close(blk[name], tok[name], msg=name)
+    only = O.sgsa_layer_forward(*args, retrieval_mode="block_only", block_size=4, top_blocks=4)
+    sdpa = F.scaled_dot_product_attention(qr.transpose(1, 2), kk.transpose(1, 2), v.transpose(1, 2), is_causal=True)
+    torch.testing.assert_close(only["v_hat"], sdpa.transpose(1, 2))
+    ret = O.block_retrieval(qr, kk, v, k, 4, 4, "block_only")
+    want_alpha = O.compute_alpha(ret["diagnostics"]["concentration"], ret["diagnostics"]["novelty"], bud,
+                                 ret["k_hat"], ret["v_hat"])
+    torch.testing.assert_close(only["alpha"], want_alpha)
+
+
+def test_layer_write_mode_none_drops_the_sparse_write():
+    # write_mode "none": the state update without the sparse write equals the direct mode
+    # with alpha forced to 0; alpha itself is still the direct mode's (reported, not applied)
+    g = torch.Generator().manual_seed(12)
+    B, T, H, D, k = 1, 11, 2, 8, 3
+    q, kk, v, qr = (torch.randn(B, T, H, D, generator=g) for _ in range(4))
+    beta, gamma, bud = torch.rand(B, T, H, generator=g), torch.rand(B, T, H, generator=g), torch.randn(B, T, H, generator=g)
+    none = O.sgsa_layer_forward(q, kk, v, qr, beta, gamma, bud, k, write_mode="none")
+    direct = O.sgsa_layer_forward(q, kk, v, qr, beta, gamma, bud, k, write_mode="direct")
+    zero = O.sgsa_layer_forward(q, kk, v, qr, beta, gamma, bud, k, write_mode="direct", alpha_max=0.0)
+    torch.testing.assert_close(none["o"], zero["o"])
+    torch.testing.assert_close(none["final_state"], zero["final_state"])
+    torch.testing.assert_close(none["alpha"], direct["alpha"])
+    assert (direct["alpha"] > 0).any() and not torch.allclose(none["o"], direct["o"])
+
+
+def test_model_block_token_with_unit_blocks_is_token_only():
+    g = torch.Generator().manual_seed(13)
+    P = _model_params(2, 8, 2, 11, 16, 12, g)
+    ids = torch.randint(0, 11, (2, 9), generator=g)
+    tok = O.sgsa_model_forward(P, ids, num_layers=2, num_heads=2, top_k=3)
+    blk = O.sgsa_model_forward(P, ids, num_layers=2, num_heads=2, top_k=3, retrieval_mode="block_token",
+                               block_size=1, top_blocks=9)
+    torch.testing.assert_close(blk, tok)
+    other = O.sgsa_model_forward(P, ids, num_layers=2, num_heads=2, top_k=3, retrieval_mode="block_token",
+                                 block_size=4, top_blocks=1)
+    assert not torch.allclose(other, tok)

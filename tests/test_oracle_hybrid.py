@@ -58,3 +58,24 @@ def test_decode_steps_reproduce_the_full_pass():
     full, _ = O.hybrid_generate(params, torch.cat([prompt, dec], 1), dec[:, :0], **kw)
     torch.testing.assert_close(pl, full[:, :T], atol=1e-5, rtol=1e-5)
     torch.testing.assert_close(dl, full[:, T:T + n], atol=1e-5, rtol=1e-5)
+
+
+def test_activation_rounding_is_identity_in_fp32_and_small_in_bf16():
+    # act_dtype=float32 rounds nothing: the unrounded decoder exactly; bfloat16 stays within a few
+    # bf16 ulps of it on this 5-layer model
+    from sgsa_amd.hybrid import HybridConfig, HybridForCausalLM
+    cfg = HybridConfig(vocab_size=256, hidden_size=128, intermediate_size=256, num_hidden_layers=5,
+                       num_attention_heads=2, num_kv_heads=1, top_k=16)
+    m = HybridForCausalLM(cfg)
+    g = torch.Generator().manual_seed(2)
+    m.init_weights(0.02, qk_std=(cfg.hidden_size * cfg.head_dim) ** -0.5, generator=g)
+    params = {k: v.detach().float() for k, v in m.state_dict().items()}
+    prompt = torch.randint(0, 256, (1, 40), generator=g)
+    dec = torch.randint(0, 256, (1, 3), generator=g)
+    kw = dict(num_layers=5, num_heads=2, num_kv_heads=1, dense_every=4, top_k=16, recompute_every=2)
+    pl, dl = O.hybrid_generate(params, prompt, dec, **kw)
+    p32, d32 = O.hybrid_generate(params, prompt, dec, act_dtype=torch.float32, **kw)
+    assert torch.equal(pl, p32) and torch.equal(dl, d32)
+    p16, d16 = O.hybrid_generate(params, prompt, dec, act_dtype=torch.bfloat16, **kw)
+    assert ((p16 - pl).abs().max() / pl.abs().max()).item() < 3e-2
+    assert not torch.equal(p16, pl)

@@ -87,8 +87,20 @@ def test_noalloc_row_kernel_then_smaller(dev, dtype):
 
 
 def test_noalloc_refuses_beyond_its_scratch(dev):
-    # 16 heads x 8192 rows need 512 MiB of candidate lists: refused before any launch
+    # 16 heads x 8192 rows need 512 MiB of candidate lists: refused before any launch.  The
+    # operands are real device buffers of the stated shape, so a guard that stopped refusing
+    # would show as a wrong status, not as a kernel reading a bogus address.
     L = _abi.lib()
-    p = ctypes.c_void_p(16)
-    s = L.sgsa_score_topk_noalloc(1, 1, 8192, 8192, 16, 128, 256, 1, 0, 11.3, 0, p, p, p, p, p, p, None, 0, None)
+    B, T, H, D, kk = 1, 8192, 16, 128, 256
+    q, k = _inputs(B, T, T, H, D, torch.bfloat16, 5)
+    idx = torch.zeros(B, H, T, kk, device=dev, dtype=torch.int32)
+    sc = torch.zeros(B, H, T, kk, device=dev, dtype=torch.float32)
+    top2 = torch.zeros(B, H, T, 2, device=dev, dtype=torch.float32)
+    cnt = torch.zeros(B, H, T, device=dev, dtype=torch.int32)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    s = L.sgsa_score_topk_noalloc(1, B, T, T, H, D, kk, 1, 0, 11.3, 0, P(q), P(k), P(idx), P(sc), P(top2), P(cnt),
+                                  None, 0, st)
+    torch.cuda.synchronize()
     assert s == 4 and b"SGSA_NOALLOC_SCRATCH_BYTES" in L.sgsa_last_error()
+    assert not cnt.any(), "a refused call wrote its outputs"
