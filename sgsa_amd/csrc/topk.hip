@@ -1702,6 +1702,8 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
   __shared__ float qnorm[NG][16];
   __shared__ float ra0[NG][16];   // lower edge a0 of b* (accumulator domain)
   __shared__ int rcntb[NG][16];   // keys in b*
+  __shared__ int force_fb;        // a row's 16-bit bin counter could overflow: radix fallback
+  __shared__ float2 smap[NG][16]; // the sample histogram's map (iws, bcs) per row
 
   const int BH = a.B * a.H;
   const int nqr = (a.Tq + QR - 1) / QR;
@@ -1831,79 +1833,226 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
     rinfo[g][rr] = ri;
     colcnt[g][rr] = 0;
   }
+  if (tid == 0) force_fb = 0;
   __syncthreads();
 
   // ---- the bins' range from a sample -------------------------------------------
-  // The bins are a monotone map of the accumulator (so of the score).
-  // The bound above spans the Cauchy-Schwarz range; scores typically fill a
-  // third of it, so the threshold bin holds several times the keys it needs to.
-  // The min and max of each row's scores over 8 tiles spread across the sweep,
-  // widened by a quarter of their span on each side, set finer bins where they
-  // are finer than the bound's.  Any monotone map keeps the selection exact; a
-  // row it misjudges (a bin with more than TOPK_CAP keys) goes to the radix
-  // fallback like any other.
+  // The bins are a monotone map of the accumulator (so of the score); any monotone
+  // map keeps the selection exact, and a row the map misjudges (a bin with more
+  // than TOPK_CAP keys) goes to the radix fallback like any other.  The bound above
+  // spans the Cauchy-Schwarz range, several times what the scores fill, so the
+  // threshold bin would hold several times the keys it needs to.  Instead each
+  // row's accumulators over 8 tiles spread across its sweep (about 512 keys) fit
+  // the bins in two steps:
+  //  1. min l and max h: bins over [l, h] widened by a quarter of h - l on each
+  //     side, used where finer than the bound's;
+  //  2. where the sample is outlying (its span above 9 standard deviations, as a
+  //     heavy tail of keys makes it), a 256-bin histogram of the same sample over
+  //     [l, h] gives approximate order statistics: the bins then span [x16 - (u - x16) / 4, u], where x16 is the
+  //     16th smallest sampled accumulator and u = 2 x(r/2) - x(2r), x(i) the i-th
+  //     largest and r = n k / nv the expected rank of the row's cut among the n
+  //     sampled keys (bin edges taken on the safe side).  A few far-out keys (a
+  //     heavy tail) then no longer stretch the bins: the keys above u share the top
+  //     bin, the rare ones below the lower end the bottom bin, and the cut lies
+  //     below u except with a small probability.
+  // 16-bit counters: a row's bin count stays below 65536 while it has at most 65535
+  // keys, and also with 65536 keys once two of them are known to fall in different
+  // bins -- the sample's lowest and highest accumulators, checked under the final
+  // map.  A row of 65536 keys without such a pair sends its block to the radix
+  // fallback, whose counters are 32-bit.
   {
     constexpr int NS = 8;
-    float lo[NG], hi[NG];
+    float lo[NG], hi[NG], sm[NG], sq[NG];   // min, max, sum and sum of squares of the sampled accumulators
+    int cn[NG];
 #pragma unroll
-    for (int g = 0; g < NG; ++g) { lo[g] = FLT_MAX; hi[g] = -FLT_MAX; }
+    for (int g = 0; g < NG; ++g) { lo[g] = FLT_MAX; hi[g] = -FLT_MAX; sm[g] = 0.f; sq[g] = 0.f; cn[g] = 0; }
     const int ns = min(ntile, NS);
-    // sample tile t's fragments in ks[t & 1], the next one's loaded meanwhile
     auto sample_kt = [&](int t) __attribute__((always_inline)) { return (int)(((long)min(t, ns - 1) * ntile) / ns); };
-    bf16x8 ks[2][4];
-    if (ns > 0) kload(ks[0], sample_kt(0));
+    {
+      // sample tile t's fragments in ks[t & 1], the next one's loaded meanwhile
+      bf16x8 ks[2][4];
+      if (ns > 0) kload(ks[0], sample_kt(0));
 #pragma unroll
-    for (int t = 0; t < NS; ++t) {
-      if (t >= ns) break;   // uniform
-      const int kt = sample_kt(t);
-      kload(ks[(t + 1) & 1], sample_kt(t + 1));
+      for (int t = 0; t < NS; ++t) {
+        if (t >= ns) break;   // uniform
+        const int kt = sample_kt(t);
+        kload(ks[(t + 1) & 1], sample_kt(t + 1));
 #pragma unroll
-      for (int g = 0; g < NG; ++g) {
-        f4 c = f4_zero();
+        for (int g = 0; g < NG; ++g) {
+          f4 c = f4_zero();
 #pragma unroll
-        for (int s = 0; s < 4; ++s) c = mma_bf16(ks[t & 1][s], qf[g][s], c);
-        const f4 sc = c;
-        const int nv = nv_of(g);
+          for (int s = 0; s < 4; ++s) c = mma_bf16(ks[t & 1][s], qf[g][s], c);
+          const int nv = nv_of(g);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const bool ok = kt * KT + 16 * w + lg + 4 * i < nv;
-          lo[g] = fminf(lo[g], ok ? sc[i] : FLT_MAX);
-          hi[g] = fmaxf(hi[g], ok ? sc[i] : -FLT_MAX);
+          for (int i = 0; i < 4; ++i) {
+            const bool ok = kt * KT + 16 * w + lg + 4 * i < nv;
+            const float x = ok ? c[i] : 0.f;
+            lo[g] = fminf(lo[g], ok ? c[i] : FLT_MAX);
+            hi[g] = fmaxf(hi[g], ok ? c[i] : -FLT_MAX);
+            sm[g] += x;
+            sq[g] = fmaf(x, x, sq[g]);
+            cn[g] += ok ? 1 : 0;
+          }
         }
       }
     }
+    // the fitted bins' sample pass: fn(g, kt, c) for the accumulators c of row group g
+    // against sample tile kt.  A rolled loop, one tile at a time: it runs only in
+    // blocks with an outlying sample, and unrolled copies would crowd the registers
+    // of the sweeps.
+    auto sample = [&](auto&& fn) __attribute__((always_inline)) {
+#pragma unroll 1
+      for (int t = 0; t < ns; ++t) {
+        const int kt = sample_kt(t);
+        bf16x8 ks[4];
+        kload(ks, kt);
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+          f4 c = f4_zero();
+#pragma unroll
+          for (int s = 0; s < 4; ++s) c = mma_bf16(ks[s], qf[g][s], c);
+          fn(g, kt, c);
+        }
+      }
+    };
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
 #pragma unroll
       for (int o = 16; o < 64; o <<= 1) {
         lo[g] = fminf(lo[g], __shfl_xor(lo[g], o, 64));
         hi[g] = fmaxf(hi[g], __shfl_xor(hi[g], o, 64));
+        sm[g] += __shfl_xor(sm[g], o, 64);
+        sq[g] += __shfl_xor(sq[g], o, 64);
+        cn[g] += __shfl_xor(cn[g], o, 64);
       }
     }
-    float2* rg = reinterpret_cast<float2*>(&hist[0][0]);   // [wave][128 rows]
+    float4* rg = reinterpret_cast<float4*>(&hist[0][0]);   // [wave][128 rows][2]
     if (lg == 0) {
 #pragma unroll
-      for (int g = 0; g < NG; ++g) rg[QR * w + 16 * g + lr] = make_float2(lo[g], hi[g]);
+      for (int g = 0; g < NG; ++g) {
+        rg[2 * (QR * w + 16 * g + lr)] = make_float4(lo[g], hi[g], (float)cn[g], 0.f);
+        rg[2 * (QR * w + 16 * g + lr) + 1] = make_float4(sm[g], sq[g], 0.f, 0.f);
+      }
     }
     __syncthreads();
+    // step 1, and the sample histogram's map (iws, bcs: bin 0 at l, bin 255 at h)
     if (lane < 32) {
       const int g = w + 4 * (lane >> 4), r = lane & 15;
-      float l = FLT_MAX, h = -FLT_MAX;
+      float l = FLT_MAX, h = -FLT_MAX, n = 0.f, s1 = 0.f, s2 = 0.f;
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const float2 o = rg[QR * v + 16 * g + r];
-        l = fminf(l, o.x); h = fmaxf(h, o.y);
+        const float4 o = rg[2 * (QR * v + 16 * g + r)], p = rg[2 * (QR * v + 16 * g + r) + 1];
+        l = fminf(l, o.x); h = fmaxf(h, o.y); n += o.z; s1 += p.x; s2 += p.y;
       }
       RowInfo ri = rinfo[g][r];
       const float sp = h - l;
+      float iws = 0.f, bcs = 0.f;
       if (l < h && sp < FLT_MAX) {
         const float l2 = l - 0.25f * sp, iw2 = 255.0f / (1.5f * sp);
         const float bc2 = 8388608.0f - l2 * iw2;
         if (iw2 > ri.iw && iw2 < FLT_MAX && fabsf(bc2) < 1.0e30f) { ri.iw = iw2; ri.bc = bc2; }
+        // an outlying sample (a span above 9 standard deviations: about 6.5 for 512
+        // normal scores) gets the fitted bins of step 2
+        const float mean = s1 / fmaxf(n, 1.f);
+        const float var = fmaxf(s2 / fmaxf(n, 1.f) - mean * mean, 0.f);
+        if (ri.mode != SELECT_ALL && n >= 64.f && sp * sp > 81.f * var) {
+          iws = 255.0f / sp;
+          bcs = 8388608.0f - l * iws;
+          if (!(iws < FLT_MAX && fabsf(bcs) < 1.0e30f)) iws = 0.f;
+        }
       }
+      ri.th0 = h;   // l and h for the overflow check below (th0 and colcnt are reset there)
       rinfo[g][r] = ri;
+      smap[g][r] = make_float2(iws, bcs);
+      rcntb[g][r] = (int)n;
+      colcnt[g][r] = __float_as_int(l);
     }
     __syncthreads();   // the range sums are read before hist is cleared
+    for (int i = tid; i < QR / 2 * NBIN; i += 256) (&hist[0][0])[i] = 0;
+    __syncthreads();
+    // step 2: the sample's 256-bin histograms (rows with keys to select and a sample span)
+    {
+      const uint32_t hb = (uint32_t)lr * (NBIN * 4u) - 0x2c000000u;
+      float iws[NG], bcs[NG];
+      uint32_t smask = 0;
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        const float2 m = smap[g][lr];
+        iws[g] = m.x; bcs[g] = m.y;
+        if (m.x > 0.f && rinfo[g][lr].mode != SELECT_ALL) smask |= 1u << g;
+      }
+      if (__syncthreads_or(smask != 0u)) {
+        sample([&](int g, int kt, f4 c) __attribute__((always_inline)) {
+          const int nv = nv_of(g);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            if (((smask >> g) & 1u) && kt * KT + 16 * w + lg + 4 * i < nv) {
+              const uint32_t bits = score_bin_bits(c[i], iws[g], bcs[g]);
+              atomicAdd(reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(&hist[0][0]) +
+                                                    (hb + (bits << 2) + (uint32_t)(g & 3) * (16u * NBIN * 4u))),
+                        g < 4 ? 1u : 0x10000u);
+            }
+          }
+        });
+        __syncthreads();
+        // step 3: wave w fits the bins of its rows (groups w and w + 4) in turn
+        for (int rr = 0; rr < 32; ++rr) {
+          const int g = w + 4 * (rr >> 4), r = rr & 15;
+          RowInfo ri = rinfo[g][r];
+          const float2 m = smap[g][r];
+          const int n = rcntb[g][r];
+          if (!(m.x > 0.f)) continue;   // wave-uniform: no fit for this row
+          const int qr = r0 + 16 * g + r;
+          const int nv = a.causal ? max(0, min(Tk, qr + a.q_offset + 1)) : Tk;
+          const uint32_t* hr = hist[16 * (g & 3) + r];
+          const uint32_t sh = 16u * (uint32_t)(g >> 2);
+          uint32_t c[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) c[q] = (hr[255 - 4 * lane - q] >> sh) & 0xffffu;
+          const float rexp = (float)n * (float)ri.need / (float)max(nv, 1);
+          const int rA = min(n, max(1, (int)(0.5f * rexp)));
+          const int rB = min(n, max(rA + 1, (int)(2.0f * rexp)));
+          const int rL = max(1, n - 15);
+          int bA, bB, bL;
+          uint32_t ab, ct;
+          find_bin(c, lane, (uint32_t)rA, bA, ab, ct);
+          find_bin(c, lane, (uint32_t)rB, bB, ab, ct);
+          find_bin(c, lane, (uint32_t)rL, bL, ab, ct);
+          if (lane == 0) {
+            const float l = __int_as_float(colcnt[g][r]);
+            const float inv = 1.0f / m.x;
+            const float a_hi = l + ((float)bA + 0.5f) * inv;   // >= x(rA)
+            const float b_lo = l + ((float)bB - 0.5f) * inv;   // <= x(rB)
+            const float x16 = l + ((float)bL - 0.5f) * inv;    // <= the 16th smallest
+            const float up = a_hi + (a_hi - b_lo);
+            const float low = x16 - 0.25f * (up - x16);
+            if (up > low) {
+              const float iw3 = 255.0f / (up - low);
+              const float bc3 = 8388608.0f - low * iw3;
+              if (iw3 > ri.iw && iw3 < FLT_MAX && fabsf(bc3) < 1.0e30f) {
+                ri.iw = iw3;
+                ri.bc = bc3;
+                rinfo[g][r].iw = iw3;
+                rinfo[g][r].bc = bc3;
+              }
+            }
+          }
+        }
+      }
+    }
+    __syncthreads();
+    // rows of 65536 keys: the sample's lowest and highest accumulators in different bins
+    if (lane < 32) {
+      const int g = w + 4 * (lane >> 4), r = lane & 15;
+      const RowInfo ri = rinfo[g][r];
+      const float l = __int_as_float(colcnt[g][r]), h = ri.th0;
+      if (ri.mode != SELECT_ALL && nv_of(g) > 65535 &&
+          !(l < h && score_bin_bits(l, ri.iw, ri.bc) != score_bin_bits(h, ri.iw, ri.bc)))
+        force_fb = 1;
+      rinfo[g][r].th0 = -INFINITY;
+      colcnt[g][r] = 0;
+    }
+    __syncthreads();   // the sample's words are read before hist is cleared
   }
   for (int i = tid; i < QR / 2 * NBIN; i += 256) (&hist[0][0])[i] = 0;
   __syncthreads();
@@ -2007,8 +2156,8 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
       }
     }
     __syncthreads();
-    int overflow = 0;
-    if (lane < 32) overflow = rinfo[w + 4 * (lane >> 4)][lane & 15].mode == RADIX;
+    int overflow = force_fb;
+    if (lane < 32) overflow |= rinfo[w + 4 * (lane >> 4)][lane & 15].mode == RADIX;
     overflow = __syncthreads_or(overflow);
     if (tid < 2) {   // both 64-row halves, as the fallback launch indexes its blocks
       const int q64 = 2 * qb + tid;
@@ -2094,7 +2243,7 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
     // of its 32 scores of one tile in the window) sends the block to the radix
     // fallback, like an overflowing bin.  Entry: {accumulator
     // bits, g << 16 | key}: the row is 16g + lr of the lane that staged and flushes
-    // it; keys fit 16 bits (Tk <= 65535 on this path).
+    // it; keys fit 16 bits (Tk <= 65536 on this path).
     uint2* ebuf = reinterpret_cast<uint2*>(&hist[0][0] + 4096 * w);
     uint32_t* rowcnt = reinterpret_cast<uint32_t*>(&colcnt[0][0]);   // row 16g + lr at 16g + lr
     uint32_t kc = 0;   // this lane's staged entries
@@ -2517,10 +2666,14 @@ hipError_t launch_score_topk(const TopkArgs& a0, hipStream_t st) {
   const bool t2 = a.top2 != nullptr;
   if (a.thr != nullptr) {   // layer path, threshold mode (bf16, D = 128, top-2 required)
     if (a.dtype != DT_BF16 || !t2 || a.D != DP) return hipErrorInvalidValue;
-    if (c16 && ms > 0.f && ms < FLT_MAX) {   // score_thr128_kernel bins accumulators: needs mscale > 0
+    // score_thr128_kernel bins accumulators (needs mscale > 0) and holds key indices in 16
+    // bits; at Tk = 65536 it sends rows whose counters could overflow to the fallback,
+    // which then counts in 32 bits
+    if (a.Tk <= 65536 && ms > 0.f && ms < FLT_MAX) {
       const dim3 grid128((unsigned)(BH * ((a.Tq + 127) / 128)));
       score_thr128_kernel<<<grid128, 256, 0, st>>>(a, nqb, ms);
-      score_topk_kernel<bf16_t, false, true, true, true, true, true><<<grid, 256, 0, st>>>(a, nqb, ms);
+      if (c16) score_topk_kernel<bf16_t, false, true, true, true, true, true><<<grid, 256, 0, st>>>(a, nqb, ms);
+      else score_topk_kernel<bf16_t, false, false, true, true, true, true><<<grid, 256, 0, st>>>(a, nqb, ms);
     } else {
       score_topk_tiles_kernel<false, true><<<grid, 256, 0, st>>>(a, nqb, ms);
       score_topk_kernel<bf16_t, false, false, true, true, true, true><<<grid, 256, 0, st>>>(a, nqb, ms);

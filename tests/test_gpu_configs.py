@@ -196,19 +196,24 @@ def test_config3_state_path(config3):
     close(c["st"][:, h:h + 1], rs, 2e-2, f"final_state head {h} vs oracle recurrence")
 
 
-@pytest.mark.parametrize("case", ["heavy_tail", "mass_ties"])
+@pytest.mark.parametrize("case", ["heavy_tail", "mass_ties", "all_equal_65536", "heavy_tail_65536"])
 def test_thresholds_past_65535_keys(dev, case):
-    # Tk > 65535 takes score_topk_tiles_kernel<C16=false, THR=true> and, for blocks
+    # Tk > 65536 takes score_topk_tiles_kernel<C16=false, THR=true> and, for blocks
     # whose threshold bin overflows, the 32-bit-counter radix fallback; mass ties
-    # (keys drawn from two rows) send every block there.
+    # (keys drawn from two rows) send every block there.  Tk = 65536 takes the 128-row
+    # kernel with 16-bit counters: a row of 65536 keys whose sample shows a single
+    # score (all keys equal) sends its block to the 32-bit fallback.
     B, T, H, D, k = 1, 65600, 2, 128, 2048
-    if case == "heavy_tail":
+    if case.endswith("65536"):
+        T = 65536
+    if case.startswith("heavy_tail"):
         x = O.make_inputs(B, T, H, D, dtype=torch.bfloat16, seed=5, heavy_tail=True)
         q, kr, v, bud = x["q"], x["k_ret"], x["v"], x["budget"]
     else:
         gen = torch.Generator().manual_seed(6)
         base = torch.randn(2, H, D, generator=gen)
-        kr = base[torch.randint(0, 2, (T,), generator=gen)][None].to(torch.bfloat16)
+        kr = base[torch.randint(0, 2, (T,), generator=gen) if case == "mass_ties" else torch.zeros(T, dtype=torch.long)]
+        kr = kr[None].to(torch.bfloat16)
         q = torch.randn(B, T, H, D, generator=gen).to(torch.bfloat16)
         v = torch.randn(B, T, H, D, generator=gen).to(torch.bfloat16)
         bud = torch.randn(B, T, H, generator=gen)
@@ -221,10 +226,12 @@ def test_thresholds_past_65535_keys(dev, case):
     assert torch.equal(cnt, cntr), "counts differ from the row lists"
     assert torch.equal(t2, t2r), "top-2 differs from the row lists"
     thr_c = thr.cpu()
-    if case == "mass_ties":
+    if case in ("mass_ties", "all_equal_65536"):
         assert (thr[..., 1] != 0x7fffffff).any(), "no row needed a tie cut"
     kf, vf = kr.float(), v.float()
     for h, r in [(0, 0), (1, 2047), (0, 2048), (1, 30000), (0, 65535), (1, 65536), (0, 65599), (1, 65599)]:
+        if r >= T:
+            r = T - 1 - h
         dump = sgsa_amd.score_dump(qd, kd, r, 1)[0, h, 0, :r + 1].cpu()
         sel = _check_cut(thr_c, dump, h, r, k)
         n = int(cntr[0, h, r])
