@@ -19,8 +19,8 @@
 //                        blocked inversion on fp32 MFMA: each 16x16 diagonal block as the product
 //                        (I - T)(I + T^2)(I + T^4)(I + T^8) (T^16 = 0 in a block), then the
 //                        off-diagonal blocks by doubling, A_RC = -A_RR T_RC A_CC for 16-, 32- and
-//                        64-row halves.  A goes to the workspace as bf16 hi + lo planes of its
-//                        lower 16x16 tiles (36 KB per chunk), the only intermediate of the chunk.
+//                        64-row halves.  A goes to the workspace as the bf16 rounding of its
+//                        lower 16x16 tiles (18 KB per chunk), the only intermediate of the chunk.
 // K4 chunk_maps_bf16     grid (B*H, G)   the affine maps S_end = Phi S_start + P of G segments of
 //                        consecutive chunks (Phi: from I with nu = 0; P: from 0)
 //    chunk_seg_scan_bf16 grid (B*H)      the segment start states
@@ -35,10 +35,16 @@
 // rows 32s + 4lg + e and 32s + 16 + 4lg + e (e = 0..3); the A operand of such a product
 // is read in the same k order.  The shared operands of a chunk (kappa, nu and q rows, the
 // A tiles) are staged in LDS once per chunk; kappa^T operands are read from the kappa
-// rows with ds_read_b64_tr_b16.  fp32 operands (S, B, R, P, A) enter the bf16 MFMAs as
-// hi + lo bf16 pairs -- hi.Y + lo.Y against an exact bf16 Y, hi.hi + hi.lo + lo.hi
-// between two of them -- which keeps about 16 mantissa bits; the state stays fp32 in
-// registers.
+// rows with ds_read_b64_tr_b16.  The state stays fp32 in registers.  fp32 operands enter
+// the bf16 MFMAs as hi + lo bf16 pairs, which keeps about 16 mantissa bits -- hi.Y + lo.Y
+// against a bf16 Y, hi.hi + hi.lo + lo.hi between two fp32 ones -- where the result carries
+// the state or the output: S in q S, R' in the update kappa^T R', B in A B (against A's bf16
+// rounding), P and R in P R.  Two products take one bf16 operand: X = kappa S reads S's bf16
+// rounding, and A is stored as bf16.  Measured on a CPU emulation of these roundings (one
+// head, T = 2048 and 8192, the north-star input distribution): output and final state within
+// 7e-4 of the fp64 recurrence, against 8e-6 and 4e-6 with hi + lo in every product and the
+// 2e-2 bound for bf16 inputs; X and A B with all hi + lo terms cost 52 more MFMAs per wave
+// and chunk and twice the A staging.
 #include <type_traits>
 
 #include "common.h"
@@ -314,18 +320,12 @@ __global__ __launch_bounds__(256) void chunk_inv_bf16(const bf16_t* __restrict__
     __syncthreads();
   }
 
-  // A -> workspace: [NTL tiles][hi, lo][16][16] bf16
-  uint16_t* dst = Aout + ((long)bh * NT + c) * NTL * 512;
+  // A -> workspace: [NTL tiles][16][16] bf16 (round to nearest)
+  uint16_t* dst = Aout + ((long)bh * NT + c) * NTL * 256;
   for (int e = tid; e < NTL * 64; e += 256) {
     const int tl = e >> 6, r = (e >> 2) & 15, cg = e & 3;
     const float* src = Tt + tl * 16 * TP + r * TP + 4 * cg;
-    f4 x;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) x[q] = src[q];
-    uint2 hi, lo;
-    split4(x, hi, lo);
-    *reinterpret_cast<uint2*>(dst + tl * 512 + r * 16 + 4 * cg) = hi;
-    *reinterpret_cast<uint2*>(dst + tl * 512 + 256 + r * 16 + 4 * cg) = lo;
+    *reinterpret_cast<uint2*>(dst + tl * 256 + r * 16 + 4 * cg) = make_uint2(pack2(src[0], src[1]), pack2(src[2], src[3]));
   }
 }
 
@@ -352,6 +352,47 @@ struct GateTab {
   float lam[M];
   float fac[M];
 };
+
+// The gate inputs of chunk token t0 + lane (wave 0, one token per lane), loaded into
+// registers ahead of use: gamma, beta and alpha (tokens past T: gamma 1, no write).
+struct GateIn {
+  float g, b, a;
+};
+template <bool SP>
+__device__ __forceinline__ GateIn load_gates(const float* __restrict__ beta, const float* __restrict__ alpha,
+                                             const float* __restrict__ gamma, int T, int H, int b, int h, int t0,
+                                             int lane) {
+  GateIn gi{1.f, 0.f, 0.f};
+  const int t = t0 + lane;
+  if (t < T) {
+    const long o = (long)(b * T + t) * H + h;
+    gi.g = gamma[o];
+    gi.b = beta[o];
+    if (SP) gi.a = alpha[o];
+  }
+  return gi;
+}
+// Fills the tables from load_gates' registers (wave 0).
+template <int M>
+__device__ __forceinline__ void store_gates(const GateIn& gi, int lane, GateTab<M>& gt) {
+  constexpr bool SP = M == 2 * L;
+  float x = __logf(fmaxf(gi.g, 1e-6f));
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const float n = __shfl_up(x, o, 64);
+    if (lane >= o) x += n;
+  }
+  gt.logd[lane] = x;
+  gt.el[lane] = fexp(x);
+  const float dec = fexp(__shfl(x, 63, 64) - x);   // e^{l_L - l_t}
+#pragma unroll
+  for (int r = 0; r < (SP ? 2 : 1); ++r) {
+    const int i = SP ? 2 * lane + r : lane;
+    const float lm = r ? gi.a : gi.b;
+    gt.lam[i] = lm;
+    gt.fac[i] = lm * dec;
+  }
+}
 
 // Fills the tables (tokens past T: no decay, no write); wave 0 does it all, one token per
 // lane, so the factors come from the scan in registers.
@@ -404,17 +445,17 @@ __device__ __forceinline__ void stage_chunk(const bf16_t* __restrict__ q, const 
   constexpr int NTL = NB * (NB + 1) / 2;
   constexpr int NK = M * (DP / 8) / NTHR;              // 16-byte row pieces per thread
   constexpr int NQ = L * (DP / 8) / NTHR;
-  constexpr int NA = (NTL * 64 + NTHR - 1) / NTHR;     // 16-byte A tile pieces per thread
+  constexpr int NA = (NTL * 32 + NTHR - 1) / NTHR;     // 16-byte A tile pieces per thread
   static_assert(NK * NTHR == M * (DP / 8) && NQ * NTHR == L * (DP / 8), "row pieces must divide evenly");
   const int t0 = c * L;
   uint4 kx[NK], nx[USE_NU ? NK : 1], qx[USE_Q ? NQ : 1], ax[NA];
-  const uint16_t* src = Ain + ((long)bh * NT + c) * NTL * 512;
+  const uint16_t* src = Ain + ((long)bh * NT + c) * NTL * 256;
 #pragma unroll
   for (int j = 0; j < NA; ++j) {
-    const int e = tid + j * NTHR;   // tp = 2 * tile + plane, row r, 16-byte half hf
+    const int e = tid + j * NTHR;   // tile tp, row r, 16-byte half hf
     const int tp = e >> 5, r = (e >> 1) & 15, hf = e & 1;
-    if constexpr (NTL * 64 % NTHR == 0) ax[j] = *reinterpret_cast<const uint4*>(src + tp * 256 + r * 16 + 8 * hf);
-    else ax[j] = e < NTL * 64 ? *reinterpret_cast<const uint4*>(src + tp * 256 + r * 16 + 8 * hf) : zero4();
+    if constexpr (NTL * 32 % NTHR == 0) ax[j] = *reinterpret_cast<const uint4*>(src + tp * 256 + r * 16 + 8 * hf);
+    else ax[j] = e < NTL * 32 ? *reinterpret_cast<const uint4*>(src + tp * 256 + r * 16 + 8 * hf) : zero4();
   }
 #pragma unroll
   for (int j = 0; j < NK; ++j) {
@@ -447,7 +488,7 @@ __device__ __forceinline__ void stage_chunk(const bf16_t* __restrict__ q, const 
   for (int j = 0; j < NA; ++j) {
     const int e = tid + j * NTHR;
     const int tp = e >> 5, r = (e >> 1) & 15, hf = e & 1;
-    if (e < NTL * 64) *reinterpret_cast<uint4*>(&At[(tp * 16 + r) * AP + 8 * hf]) = ax[j];
+    if (e < NTL * 32) *reinterpret_cast<uint4*>(&At[(tp * 16 + r) * AP + 8 * hf]) = ax[j];
   }
 #pragma unroll
   for (int j = 0; j < NK; ++j) {
@@ -468,64 +509,60 @@ __device__ __forceinline__ void stage_chunk(const bf16_t* __restrict__ q, const 
 
 // The staging of stage_chunk for D = DP as direct-to-LDS buffer loads (buffer_load_dwordx4
 // ... lds: lane l of an instruction fills the 16 bytes at its LDS base + 16 l), which
-// hold no data registers, so all of a chunk's loads are issued back to back.  One buffer
+// hold no data registers, so all of a chunk's loads are issued back to back; in pieces, so
+// that a chunk's operands can load while the previous chunk still computes.  One buffer
 // resource per input covers its head's rows [0, T): a token past T reads as zeros.  A
 // 272-byte kappa / nu / q row is 17 slots (the 17th is its pad and re-reads the first);
 // a 48-byte A tile row is 3 (2 data, 1 pad).  The caller waits for the loads (vmcnt) and
-// then synchronises the block.
-template <int M, int NTHR, bool USE_NU, bool USE_Q>
-__device__ __forceinline__ void stage_chunk_dma(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
-                                                const bf16_t* __restrict__ v, const bf16_t* __restrict__ sk,
-                                                const bf16_t* __restrict__ sv, const float* __restrict__ beta,
-                                                const float* __restrict__ alpha, const float* __restrict__ gamma,
-                                                const uint16_t* __restrict__ Ain, int T, int H, int NT, int b, int h,
-                                                int bh, int c, int tid, uint16_t* kap, uint16_t* nuv, uint16_t* qr,
-                                                uint16_t* At, GateTab<M>& gt) {
-  constexpr bool SP = M == 2 * L;
+// then publishes them with a barrier.
+struct DmaCtx {
+  int T, H, NT, b, h, bh, lane, w;
+};
+// 64 rows of one input, tokens c L .. c L + 63, into dst (rows of PK elements)
+template <int NW>
+__device__ __forceinline__ void dma_rows(const DmaCtx& x, const bf16_t* base, int c, uint16_t* dst) {
+  constexpr int RI = L * 17 / 64;
+  const long hoff = ((long)x.b * x.T * x.H + x.h) * DP;
+  const int rbytes = x.H * DP * 2;
+  const int nrec = (x.T - 1) * rbytes + DP * 2;
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t*>(base + hoff), 0, nrec, 0x00020000);
+  for (int i = x.w; i < RI; i += NW) {
+    const int sl = 64 * i + x.lane;
+    const int row = sl / 17, pc = sl % 17;
+    const unsigned voff = (unsigned)((c * L + row) * rbytes + 16 * (pc < 16 ? pc : 0));
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(dst + 512 * i), 16, voff,
+                                             0, 0, 0);
+  }
+}
+// kappa (or nu) rows of chunk c: the local rows, then (SP) the sparse rows 16 bytes on
+template <int M, int NW>
+__device__ __forceinline__ void dma_pair(const DmaCtx& x, const bf16_t* a, const bf16_t* sa, int c, uint16_t* dst) {
+  dma_rows<NW>(x, a, c, dst);
+  if constexpr (M == 2 * L) dma_rows<NW>(x, sa, c, dst + 64 * PK + 8);
+}
+// The A tile area: the tiles' rows, rounded up to whole DMA instructions (every lane of
+// the last one writes; its slots past the tiles read past the buffer, as zeros).
+template <int M> constexpr int a_instr() { return ((M / 16) * (M / 16 + 1) / 2 * 16 * 3 + 63) / 64; }
+template <int M> constexpr int at_elems() {
+  return a_instr<M>() * 512 > (M / 16) * (M / 16 + 1) / 2 * 16 * AP ? a_instr<M>() * 512
+                                                                      : (M / 16) * (M / 16 + 1) / 2 * 16 * AP;
+}
+// the A tiles of chunk c
+template <int M, int NW>
+__device__ __forceinline__ void dma_A(const DmaCtx& x, const uint16_t* Ain, int c, uint16_t* At) {
   constexpr int NB = M / 16;
   constexpr int NTL = NB * (NB + 1) / 2;
-  constexpr int NW = NTHR / 64;
-  constexpr int RI = L * 17 / 64;            // instructions per 64 rows (17)
-  constexpr int AI = NTL * 2 * 16 * 3 / 64;  // instructions for the A tiles
-  static_assert(NTL * 2 * 16 * 3 % 64 == 0, "A tile rows must fill whole instructions");
-  const int t0 = c * L;
-  const int lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const long hoff = ((long)b * T * H + h) * DP;   // row 0 of this head
-  const int rbytes = H * DP * 2;
-  const int nrec = (T - 1) * rbytes + DP * 2;
-  auto rsrc = [&](const bf16_t* base) __attribute__((always_inline)) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t*>(base + hoff), 0, nrec, 0x00020000);
-  };
-  // rows of 64 tokens from one input into dst (64 rows x PK)
-  auto rows64 = [&](__amdgpu_buffer_rsrc_t rs, uint16_t* dst) __attribute__((always_inline)) {
-    for (int i = w; i < RI; i += NW) {
-      const int sl = 64 * i + lane;
-      const int row = sl / 17, pc = sl % 17;
-      const unsigned voff = (unsigned)((t0 + row) * rbytes + 16 * (pc < 16 ? pc : 0));
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(dst + 512 * i), 16,
-                                               voff, 0, 0, 0);
-    }
-  };
-  rows64(rsrc(k), kap);
-  if constexpr (SP) rows64(rsrc(sk), kap + 64 * PK + 8);
-  if constexpr (USE_NU) {
-    rows64(rsrc(v), nuv);
-    if constexpr (SP) rows64(rsrc(sv), nuv + 64 * PK + 8);
+  constexpr int AI = a_instr<M>();
+  const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(Ain + ((long)x.bh * x.NT + c) * NTL * 256), 0, NTL * 512, 0x00020000);
+  for (int i = x.w; i < AI; i += NW) {
+    const int sl = 64 * i + x.lane;
+    const int row = sl / 3, pc = sl % 3;
+    const unsigned voff = (unsigned)(row * 32 + 16 * (pc < 2 ? pc : 0));
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(ars, (__attribute__((address_space(3))) void*)(At + 512 * i), 16, voff,
+                                             0, 0, 0);
   }
-  if constexpr (USE_Q) rows64(rsrc(q), qr);
-  {
-    const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint16_t*>(Ain + ((long)bh * NT + c) * NTL * 512), 0, NTL * 1024, 0x00020000);
-    for (int i = w; i < AI; i += NW) {
-      const int sl = 64 * i + lane;
-      const int row = sl / 3, pc = sl % 3;   // row = (2 tile + plane) 16 + r
-      const unsigned voff = (unsigned)(row * 32 + 16 * (pc < 2 ? pc : 0));
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(ars, (__attribute__((address_space(3))) void*)(At + 512 * i), 16,
-                                               voff, 0, 0, 0);
-    }
-  }
-  stage_gates<M>(beta, alpha, gamma, T, H, b, h, t0, tid, gt);
 }
 
 // A wave's state is kept in 16-column tiles: S[r] holds S[16r + 4lg + e][col + lr] of the
@@ -567,11 +604,7 @@ __device__ __forceinline__ void tile_residual(const Op (&Sop)[DP / 32], const ui
       f4 x = f4_zero();
       const uint16_t* kr = kap + krow<SP>(16 * I + lr);
 #pragma unroll
-      for (int s = 0; s < DP / 32; ++s) {
-        const bf16x8 a = rowop_p(kr, s, lg);
-        x = mma_bf16(a, as_bf8(Sop[s].h), x);
-        x = mma_bf16(a, as_bf8(Sop[s].l), x);
-      }
+      for (int s = 0; s < DP / 32; ++s) x = mma_bf16(rowop_p(kr, s, lg), as_bf8(Sop[s].h), x);
       float ef[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) ef[e] = el[samp_t<SP>(16 * I + 4 * lg + e)];
@@ -597,19 +630,12 @@ __device__ __forceinline__ void tile_residual(const Op (&Sop)[DP / 32], const ui
     R[I] = f4_zero();
 #pragma unroll
     for (int s = 0; 2 * s <= I; ++s) {
-      const uint16_t* a0 = At + tri(I, 2 * s) * 2 * 16 * AP + lr * AP + 4 * lg;
-      const uint2 h0 = *reinterpret_cast<const uint2*>(a0);
-      const uint2 l0 = *reinterpret_cast<const uint2*>(a0 + 16 * AP);
-      uint2 h1 = make_uint2(0, 0), l1 = make_uint2(0, 0);
-      if (2 * s + 1 <= I) {
-        const uint16_t* a1 = At + tri(I, 2 * s + 1) * 2 * 16 * AP + lr * AP + 4 * lg;
-        h1 = *reinterpret_cast<const uint2*>(a1);
-        l1 = *reinterpret_cast<const uint2*>(a1 + 16 * AP);
-      }
-      const bf16x8 ah = cat(h0, h1), al = cat(l0, l1);
+      const uint2 h0 = *reinterpret_cast<const uint2*>(At + tri(I, 2 * s) * 16 * AP + lr * AP + 4 * lg);
+      uint2 h1 = make_uint2(0, 0);
+      if (2 * s + 1 <= I) h1 = *reinterpret_cast<const uint2*>(At + tri(I, 2 * s + 1) * 16 * AP + lr * AP + 4 * lg);
+      const bf16x8 ah = cat(h0, h1);
       R[I] = mma_bf16(ah, as_bf8(Bop[s].h), R[I]);
       R[I] = mma_bf16(ah, as_bf8(Bop[s].l), R[I]);
-      R[I] = mma_bf16(al, as_bf8(Bop[s].h), R[I]);
     }
     __builtin_amdgcn_sched_barrier(0);
   }
@@ -649,15 +675,20 @@ __device__ __forceinline__ void tile_update(f4 (&S)[DP / 16], const Op (&Rop)[M 
 }
 
 // The chunks of segment g for one state: PHI = false runs P (start 0, with nu), PHI = true
-// runs Phi (start I, nu = 0), each wave over one 16-column tile of the state.
+// runs Phi (start I, nu = 0), each wave over one 16-column tile of the state.  kapb holds
+// two kappa buffers and gtb two gate tables: with D = DP the next chunk's kappa rows and
+// gates load while the current chunk computes, and its nu rows and A tiles as soon as
+// every wave has formed R (their buffers are free then); D < DP stages each chunk in turn.
 template <int M, bool FULL, bool PHI>
 __device__ __forceinline__ void maps_pass(const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
                                           const bf16_t* __restrict__ sk, const bf16_t* __restrict__ sv,
                                           const float* __restrict__ beta, const float* __restrict__ alpha,
                                           const float* __restrict__ gamma, int T, int H, int D, int NT, int CPS,
-                                          const uint16_t* __restrict__ Ain, float* __restrict__ dst, uint16_t* kap,
-                                          uint16_t* nuv, uint16_t* At, GateTab<M>& gt, int bh, int g) {
+                                          const uint16_t* __restrict__ Ain, float* __restrict__ dst, uint16_t* kapb,
+                                          uint16_t* nuv, uint16_t* At, GateTab<M>* gtb, int bh, int g) {
+  constexpr bool SP = M == 2 * L;
   constexpr int NB = M / 16;
+  constexpr int KE = krows_elems<M>();
   const int b = bh / H, h = bh % H;
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform
   const int lr = lane & 15, lg = lane >> 4;
@@ -670,24 +701,57 @@ __device__ __forceinline__ void maps_pass(const bf16_t* __restrict__ k, const bf
 #pragma unroll
     for (int e = 0; e < 4; ++e) S[r][e] = (PHI && 16 * r + 4 * lg + e == col + lr) ? 1.f : 0.f;
 
-  for (int c = cb; c < ce; ++c) {
-    __syncthreads();   // every wave is done with the previous chunk's operands
-    if constexpr (FULL) {
-      stage_chunk_dma<M, 512, !PHI, false>(nullptr, k, v, sk, sv, beta, alpha, gamma, Ain, T, H, NT, b, h, bh, c,
-                                           tid, kap, nuv, nullptr, At, gt);
+  if constexpr (FULL) {
+    const DmaCtx x{T, H, NT, b, h, bh, lane, w};
+    if (cb < ce) {
+      dma_pair<M, 8>(x, k, sk, cb, kapb);
+      if constexpr (!PHI) dma_pair<M, 8>(x, v, sv, cb, nuv);
+      dma_A<M, 8>(x, Ain, cb, At);
+      if (w == 0) store_gates<M>(load_gates<SP>(beta, alpha, gamma, T, H, b, h, cb * L, lane), lane, gtb[0]);
       __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): this wave's loads have landed in LDS
-    } else {
-      stage_chunk<M, 512, !PHI, false, FULL>(nullptr, k, v, sk, sv, beta, alpha, gamma, Ain, T, H, D, NT, b, h, bh,
-                                             c, tid, kap, nuv, nullptr, At, gt);
     }
     __syncthreads();
-    Op Sop[DP / 32];
-    pack_ops<DP / 16>(S, Sop);
-    f4 R[NB];
-    tile_residual<M, !PHI>(Sop, kap, nuv, At, gt.el, col, lr, lg, R);
-    Op Rop[NB / 2];
-    scaled_ops<M>(R, gt.fac, lg, Rop);
-    tile_update<M>(S, Rop, kap, gt.el[L - 1], lr, lg);
+    for (int c = cb; c < ce; ++c) {
+      const int cur = (c - cb) & 1;
+      const uint16_t* kap = kapb + cur * KE;
+      const GateTab<M>& gt = gtb[cur];
+      const bool more = c + 1 < ce;   // block-uniform
+      GateIn gn{1.f, 0.f, 0.f};
+      if (more) {
+        dma_pair<M, 8>(x, k, sk, c + 1, kapb + (cur ^ 1) * KE);
+        if (w == 0) gn = load_gates<SP>(beta, alpha, gamma, T, H, b, h, (c + 1) * L, lane);
+      }
+      Op Sop[DP / 32];
+      pack_ops<DP / 16>(S, Sop);
+      f4 R[NB];
+      tile_residual<M, !PHI>(Sop, kap, nuv, At, gt.el, col, lr, lg, R);
+      __syncthreads();   // every wave is done with nu and the A tiles
+      if (more) {
+        if constexpr (!PHI) dma_pair<M, 8>(x, v, sv, c + 1, nuv);
+        dma_A<M, 8>(x, Ain, c + 1, At);
+      }
+      Op Rop[NB / 2];
+      scaled_ops<M>(R, gt.fac, lg, Rop);
+      tile_update<M>(S, Rop, kap, gt.el[L - 1], lr, lg);
+      if (more && w == 0) store_gates<M>(gn, lane, gtb[cur ^ 1]);
+      __builtin_amdgcn_s_waitcnt(0x0f70);
+      __syncthreads();   // the next chunk's operands are in place; this chunk's are free
+    }
+  } else {
+    GateTab<M>& gt = gtb[0];
+    for (int c = cb; c < ce; ++c) {
+      __syncthreads();   // every wave is done with the previous chunk's operands
+      stage_chunk<M, 512, !PHI, false, FULL>(nullptr, k, v, sk, sv, beta, alpha, gamma, Ain, T, H, D, NT, b, h, bh,
+                                             c, tid, kapb, nuv, nullptr, At, gt);
+      __syncthreads();
+      Op Sop[DP / 32];
+      pack_ops<DP / 16>(S, Sop);
+      f4 R[NB];
+      tile_residual<M, !PHI>(Sop, kapb, nuv, At, gt.el, col, lr, lg, R);
+      Op Rop[NB / 2];
+      scaled_ops<M>(R, gt.fac, lg, Rop);
+      tile_update<M>(S, Rop, kapb, gt.el[L - 1], lr, lg);
+    }
   }
 #pragma unroll
   for (int r = 0; r < DP / 16; ++r)
@@ -708,11 +772,10 @@ __global__ __launch_bounds__(512, 1) void chunk_maps_bf16(const bf16_t* __restri
                                                         int CPS, int BH, int G, const uint16_t* __restrict__ Ain,
                                                         float* __restrict__ sout) {
   constexpr int NB = M / 16;
-  constexpr int NTL = NB * (NB + 1) / 2;
-  __shared__ __align__(16) uint16_t kap[krows_elems<M>()];
+  __shared__ __align__(16) uint16_t kap[(FULL ? 2 : 1) * krows_elems<M>()];
   __shared__ __align__(16) uint16_t nuv[krows_elems<M>()];
-  __shared__ __align__(16) uint16_t At[NTL * 2 * 16 * AP];
-  __shared__ __align__(16) GateTab<M> gt;
+  __shared__ __align__(16) uint16_t At[at_elems<M>()];
+  __shared__ __align__(16) GateTab<M> gt[FULL ? 2 : 1];
   const int pid = blockIdx.x;
   const int z = (pid >> 3) & 1;                       // 0: P, 1: Phi
   const int pair = (pid >> 4) * 8 + (pid & 7);        // (b*h, segment) pair, b*h fastest
@@ -818,7 +881,10 @@ __global__ __launch_bounds__(256) void chunk_seg_scan_bf16(int G, int D, const f
 // Segment g reruns its chunks from its start state (sinit[bh*G + g], leading dimension
 // sld; rows / columns >= sld read as 0) and writes the output rows; the last segment
 // writes the final state to ht ([B*H][D][D], rows / columns < D).  Eight waves, one
-// 16-column tile of the state (and of the output) each.
+// 16-column tile of the state (and of the output) each.  With D = DP the next chunk's
+// operands load while the current one computes: its kappa rows (a second buffer) and
+// gates from the start, its nu rows once every wave has formed R, its q rows once the P
+// operands are built and its A tiles once the output rows are done.
 template <int M, bool FULL>
 __global__ __launch_bounds__(512, 1) void chunk_replay_bf16(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
@@ -828,12 +894,13 @@ __global__ __launch_bounds__(512, 1) void chunk_replay_bf16(
     bf16_t* __restrict__ out) {
   constexpr bool SP = M == 2 * L;
   constexpr int NB = M / 16;
-  constexpr int NTL = NB * (NB + 1) / 2;
-  __shared__ __align__(16) uint16_t kap[krows_elems<M>()];
-  __shared__ __align__(16) uint16_t nuv[krows_elems<M>()];
+  constexpr int KE = krows_elems<M>();
+  __shared__ __align__(16) uint16_t kapb[(FULL ? 2 : 1) * KE];
+  __shared__ __align__(16) uint16_t nuv[KE];
   __shared__ __align__(16) uint16_t qr[L * PK];
-  __shared__ __align__(16) uint16_t At[NTL * 2 * 16 * AP];
-  __shared__ __align__(16) GateTab<M> gt;
+  constexpr int NCBX = SP ? 10 : 6;   // the P operand blocks that later pass through At
+  __shared__ __align__(16) uint16_t At[(at_elems<M>() > NCBX * 1024) ? at_elems<M>() : NCBX * 1024];
+  __shared__ __align__(16) GateTab<M> gtb[FULL ? 2 : 1];
 
   const int bh = blockIdx.x, g = blockIdx.y, G = gridDim.y;
   const int b = bh / H, h = bh % H;
@@ -841,6 +908,7 @@ __global__ __launch_bounds__(512, 1) void chunk_replay_bf16(
   const int lr = lane & 15, lg = lane >> 4;
   const int col = 16 * w;
   const int cb = g * CPS, ce = min(NT, cb + CPS);
+  const DmaCtx x{T, H, NT, b, h, bh, lane, w};
 
   f4 S[DP / 16];
   {
@@ -854,17 +922,34 @@ __global__ __launch_bounds__(512, 1) void chunk_replay_bf16(
       }
   }
 
-  for (int c = cb; c < ce; ++c) {
-    __syncthreads();   // every wave is done with the previous chunk's operands
-    if constexpr (FULL) {
-      stage_chunk_dma<M, 512, true, true>(q, k, v, sk, sv, beta, alpha, gamma, Ain, T, H, NT, b, h, bh, c, tid, kap,
-                                          nuv, qr, At, gt);
+  if constexpr (FULL) {
+    if (cb < ce) {
+      dma_pair<M, 8>(x, k, sk, cb, kapb);
+      dma_pair<M, 8>(x, v, sv, cb, nuv);
+      dma_rows<8>(x, q, cb, qr);
+      dma_A<M, 8>(x, Ain, cb, At);
+      if (w == 0) store_gates<M>(load_gates<SP>(beta, alpha, gamma, T, H, b, h, cb * L, lane), lane, gtb[0]);
       __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): this wave's loads have landed in LDS
-    } else {
-      stage_chunk<M, 512, true, true, FULL>(q, k, v, sk, sv, beta, alpha, gamma, Ain, T, H, D, NT, b, h, bh, c, tid,
-                                            kap, nuv, qr, At, gt);
     }
     __syncthreads();
+  }
+  for (int c = cb; c < ce; ++c) {
+    const int cur = FULL ? (c - cb) & 1 : 0;
+    const uint16_t* kap = kapb + cur * KE;
+    const GateTab<M>& gt = gtb[cur];
+    const bool more = FULL && c + 1 < ce;   // block-uniform
+    GateIn gn{1.f, 0.f, 0.f};
+    if constexpr (FULL) {
+      if (more) {
+        dma_pair<M, 8>(x, k, sk, c + 1, kapb + (cur ^ 1) * KE);
+        if (w == 0) gn = load_gates<SP>(beta, alpha, gamma, T, H, b, h, (c + 1) * L, lane);
+      }
+    } else {
+      __syncthreads();   // every wave is done with the previous chunk's operands
+      stage_chunk<M, 512, true, true, FULL>(q, k, v, sk, sv, beta, alpha, gamma, Ain, T, H, D, NT, b, h, bh, c, tid,
+                                            kapb, nuv, qr, At, gtb[0]);
+      __syncthreads();
+    }
     Op Sop[DP / 32];
     pack_ops<DP / 16>(S, Sop);
     // q S for the chunk's 64 rows (rows 16 tt + 4 lg + e of the accumulator)
@@ -892,8 +977,10 @@ __global__ __launch_bounds__(512, 1) void chunk_replay_bf16(
     // accumulator layout is P's A operand layout) -- and pass them through the A tile
     // area, free once every wave has formed R.
     constexpr int NCB = SP ? 10 : 6;   // (tt, s) pairs: s < tt + 1 (SP) or s < tt / 2 + 1
+    static_assert(NCB == NCBX, "the P operand area must fit At");
     uint4* pst = reinterpret_cast<uint4*>(At);   // [NCB][64 lanes][hi, lo]
-    __syncthreads();   // every wave is done with the A tiles
+    __syncthreads();   // every wave is done with the A tiles and nu
+    if (more) dma_pair<M, 8>(x, v, sv, c + 1, nuv);
     for (int cb2 = w; cb2 < NCB; cb2 += 8) {
       int tt = 0, s0 = cb2;
       while (s0 >= (SP ? tt + 1 : tt / 2 + 1)) { s0 -= (SP ? tt + 1 : tt / 2 + 1); ++tt; }
@@ -918,7 +1005,8 @@ __global__ __launch_bounds__(512, 1) void chunk_replay_bf16(
       pst[(cb2 * 64 + lane) * 2] = Pop[0].h;
       pst[(cb2 * 64 + lane) * 2 + 1] = Pop[0].l;
     }
-    __syncthreads();
+    __syncthreads();   // the P operands are in place; q is free
+    if (more) dma_rows<8>(x, q, c + 1, qr);
     const int t0 = c * L;
     const bool whole = t0 + L <= T;   // block-uniform: every output row of the chunk exists
     bf16_t* orow = out + ((long)(b * T + t0) * H + h) * D + col + lr;
@@ -951,6 +1039,10 @@ __global__ __launch_bounds__(512, 1) void chunk_replay_bf16(
       }
       __builtin_amdgcn_sched_barrier(0);
     }
+    if (more) {
+      __syncthreads();   // every wave is done with the P operands: the A area is free
+      dma_A<M, 8>(x, Ain, c + 1, At);
+    }
 
     // R' from the residual operands (R = hi + lo to about 16 bits)
 #pragma unroll
@@ -966,6 +1058,11 @@ __global__ __launch_bounds__(512, 1) void chunk_replay_bf16(
       Rop[sp] = o1[0];
     }
     tile_update<M>(S, Rop, kap, gt.el[L - 1], lr, lg);
+    if constexpr (FULL) {
+      if (more && w == 0) store_gates<M>(gn, lane, gtb[cur ^ 1]);
+      __builtin_amdgcn_s_waitcnt(0x0f70);
+      __syncthreads();   // the next chunk's operands are in place; this chunk's are free
+    }
   }
 
   if (ht != nullptr && g == G - 1) {
@@ -990,7 +1087,7 @@ size_t chunk_bf16_workspace_bytes(int B, int T, int H, int has_sparse) {
   const size_t NB = has_sparse ? 2 * L / 16 : L / 16;
   const size_t ntl = NB * (NB + 1) / 2;
   const size_t n = (size_t)B * H * NT;
-  size_t total = n * ntl * 1024;   // A tiles, hi + lo
+  size_t total = n * ntl * 512;    // A tiles, bf16
   const size_t G = seg_count(B * H, (int)NT);
   if (G > 1) total += 3 * (size_t)B * H * G * DP * DP * 4;   // segment maps P, Phi and start states
   return total + 256 * 4;
@@ -1005,7 +1102,7 @@ static hipError_t launch_bf16_t(const ChunkArgs& a, hipStream_t st) {
   auto align = [](char* p) { return (char*)(((uintptr_t)p + 255) & ~(uintptr_t)255); };
   char* p = align((char*)a.workspace);
   uint16_t* Aws = (uint16_t*)p;
-  p = align(p + n * NTL * 1024);
+  p = align(p + n * NTL * 512);
   const int BH = a.B * a.H;
   const int G = seg_count(BH, NT);
   const int CPS = (NT + G - 1) / G;
