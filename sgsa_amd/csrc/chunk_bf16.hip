@@ -15,7 +15,7 @@
 // which is chunk_fwd.py:70-126 with the UT/WY inverse kept as A (R = U - W S for
 // W = A e^{l_tau} kappa and U = A nu).
 //
-// K3 chunk_inv_bf16      grid (NT, B*H)  Gram of kappa (bf16 MFMA, exact in fp32), T, and A by
+// K3 chunk_inv_bf16      grid (NT, B*H), 8 waves: Gram of kappa (bf16 MFMA, exact in fp32), T, and A by
 //                        blocked inversion on fp32 MFMA: each 16x16 diagonal block as the product
 //                        (I - T)(I + T^2)(I + T^4)(I + T^8) (T^16 = 0 in a block), then the
 //                        off-diagonal blocks by doubling, A_RC = -A_RR T_RC A_CC for 16-, 32- and
@@ -181,8 +181,10 @@ __device__ __forceinline__ f4 ld16(const float* Z, int lr, int lg) {
   return v;
 }
 
+constexpr int K3W = 8;   // waves of a chunk_inv_bf16 block
+
 template <int M, bool FULL>
-__global__ __launch_bounds__(256) void chunk_inv_bf16(const bf16_t* __restrict__ k, const bf16_t* __restrict__ sk,
+__global__ __launch_bounds__(64 * K3W) void chunk_inv_bf16(const bf16_t* __restrict__ k, const bf16_t* __restrict__ sk,
                                                     const float* __restrict__ beta, const float* __restrict__ alpha,
                                                     const float* __restrict__ gamma, int T, int H, int D, int NT,
                                                     uint16_t* __restrict__ Aout) {
@@ -190,7 +192,8 @@ __global__ __launch_bounds__(256) void chunk_inv_bf16(const bf16_t* __restrict__
   constexpr int NB = M / 16;
   constexpr int NTL = NB * (NB + 1) / 2;
   constexpr int UNION = M * PK * 2;                      // bytes: kappa rows; later the product scratch
-  static_assert(4 * 4 * 16 * TP * 4 <= UNION && 16 * 16 * TP * 4 <= UNION, "scratch exceeds the union");
+  constexpr int NDW = K3W < NB ? K3W : NB;               // waves holding a diagonal block
+  static_assert(NDW * 4 * 16 * TP * 4 <= UNION && 16 * 16 * TP * 4 <= UNION, "scratch exceeds the union");
   __shared__ __align__(16) unsigned char un[UNION];
   __shared__ __align__(16) float Tt[NTL * 16 * TP];      // lower tiles of T, then of A
   __shared__ float lam[M];
@@ -221,11 +224,11 @@ __global__ __launch_bounds__(256) void chunk_inv_bf16(const bf16_t* __restrict__
     lam[tid] = lm;
   }
   {
-    constexpr int NK = M * (DP / 8) / 256;   // all of a thread's loads in flight before its stores
+    constexpr int NK = M * (DP / 8) / (64 * K3W);   // all of a thread's loads in flight before its stores
     uint4 kx[NK];
 #pragma unroll
     for (int j = 0; j < NK; ++j) {
-      const int e = tid + 256 * j;
+      const int e = tid + 64 * K3W * j;
       const int i = e / (DP / 8), cv = e % (DP / 8);
       const int t = t0 + samp_t<SP>(i);
       const bf16_t* src = samp_r<SP>(i) ? sk : k;
@@ -235,14 +238,14 @@ __global__ __launch_bounds__(256) void chunk_inv_bf16(const bf16_t* __restrict__
     }
 #pragma unroll
     for (int j = 0; j < NK; ++j) {
-      const int e = tid + 256 * j;
+      const int e = tid + 64 * K3W * j;
       *reinterpret_cast<uint4*>(&kap[(e / (DP / 8)) * PK + 8 * (e % (DP / 8))]) = kx[j];
     }
   }
   __syncthreads();
 
   // Gram on the lower tiles -> T
-  for (int ti = w; ti < NTL; ti += 4) {
+  for (int ti = w; ti < NTL; ti += K3W) {
     int I = 0;
     while (tri(I + 1, 0) <= ti) ++I;
     const int J = ti - tri(I, 0);
@@ -267,7 +270,7 @@ __global__ __launch_bounds__(256) void chunk_inv_bf16(const bf16_t* __restrict__
     float* s1 = sc + 16 * TP;
     float* s2 = sc + 2 * 16 * TP;
     float* s3 = sc + 3 * 16 * TP;
-    for (int Ib = w; Ib < NB; Ib += 4) {
+    for (int Ib = w; Ib < NB; Ib += K3W) {
       float* Tb = Tt + tri(Ib, Ib) * 16 * TP;
       const f4 t1 = ld16(Tb, lr, lg);
       const f4 t2 = mm16(Tb, Tb, f4_zero(), lr, lg);
@@ -300,7 +303,7 @@ __global__ __launch_bounds__(256) void chunk_inv_bf16(const bf16_t* __restrict__
   for (int nb = 1; nb < NB; nb <<= 1) {
     const int npair = NB / (2 * nb);
     const int items = npair * nb * nb;
-    for (int it = w; it < items; it += 4) {
+    for (int it = w; it < items; it += K3W) {
       const int p = it / (nb * nb), i = (it / nb) % nb, j = it % nb;
       const int Ri = (2 * p + 1) * nb + i, C0 = 2 * p * nb;
       f4 z = f4_zero();
@@ -309,7 +312,7 @@ __global__ __launch_bounds__(256) void chunk_inv_bf16(const bf16_t* __restrict__
       st16(Zs + it * 16 * TP, z, lr, lg);
     }
     __syncthreads();
-    for (int it = w; it < items; it += 4) {
+    for (int it = w; it < items; it += K3W) {
       const int p = it / (nb * nb), i = (it / nb) % nb, j = it % nb;
       const int R0 = (2 * p + 1) * nb, C0 = 2 * p * nb;
       f4 a = f4_zero();
@@ -322,7 +325,7 @@ __global__ __launch_bounds__(256) void chunk_inv_bf16(const bf16_t* __restrict__
 
   // A -> workspace: [NTL tiles][16][16] bf16 (round to nearest)
   uint16_t* dst = Aout + ((long)bh * NT + c) * NTL * 256;
-  for (int e = tid; e < NTL * 64; e += 256) {
+  for (int e = tid; e < NTL * 64; e += 64 * K3W) {
     const int tl = e >> 6, r = (e >> 2) & 15, cg = e & 3;
     const float* src = Tt + tl * 16 * TP + r * TP + 4 * cg;
     *reinterpret_cast<uint2*>(dst + tl * 256 + r * 16 + 4 * cg) = make_uint2(pack2(src[0], src[1]), pack2(src[2], src[3]));
@@ -1113,7 +1116,7 @@ static hipError_t launch_bf16_t(const ChunkArgs& a, hipStream_t st) {
   const bf16_t* v = (const bf16_t*)a.v;
   const bf16_t* sk = (const bf16_t*)a.sparse_k;
   const bf16_t* sv = (const bf16_t*)a.sparse_v;
-  chunk_inv_bf16<M, FULL><<<dim3(NT, BH), 256, 0, st>>>(k, sk, a.beta, a.alpha, a.gamma, a.T, a.H, a.D, NT, Aws);
+  chunk_inv_bf16<M, FULL><<<dim3(NT, BH), 64 * K3W, 0, st>>>(k, sk, a.beta, a.alpha, a.gamma, a.T, a.H, a.D, NT, Aws);
   if (G == 1) {
     chunk_replay_bf16<M, FULL><<<dim3(BH, 1), 512, 0, st>>>(q, k, v, sk, sv, a.beta, a.alpha, a.gamma, a.T, a.H, a.D, NT,
                                                       NT, Aws, a.initial_state, a.D, a.final_state, (bf16_t*)a.out);
