@@ -151,6 +151,63 @@ def time_config(name, B, T, H, D, top_k, dtype, heavy=False, reps=3):
     return res
 
 
+def time_masked(B, T, H, D, top_k, pad, reps=3):
+    """The layer under a padding mask (bf16, d = 128): the first ``pad`` positions of
+    every sequence are padding.  sgsa_layer_retrieve_masked (per-row valid prefixes,
+    keys and values compacted valid-first, the threshold K1 and K2 over them) then the
+    chunk update, outside the timed steps.  Returns ms per layer forward (mean of
+    ``reps`` after one warm-up) and the stage split."""
+    from sgsa_amd import _abi
+    dev = torch.device("cuda:0")
+    dtype = torch.bfloat16
+    q, k, v, beta, gamma, budget = synth_inputs(B, T, H, D)
+    qd, kd, vd = (t.to(dev, dtype).contiguous() for t in (q, k, v))
+    bd, gd, ud = (t.to(dev).contiguous() for t in (beta, gamma, budget))
+    del q, k, v
+    am = torch.ones(B, T, device=dev, dtype=torch.uint8)
+    am[:, :pad] = 0
+    L, P = _abi.lib(), _abi.ptr
+    stream = _abi.stream_of(qd)
+    kk = min(top_k, T)
+    n = ctypes.c_size_t()
+    _abi.check(L.sgsa_layer_retrieve_masked_workspace_size(1, B, T, H, D, kk, ctypes.byref(n)))
+    rws = torch.empty(n.value, device=dev, dtype=torch.uint8)
+    _abi.check(L.sgsa_chunk_fwd_workspace_size(B, T, H, D, 1, ctypes.byref(n)))
+    cws = torch.empty(n.value, device=dev, dtype=torch.uint8)
+    wk, vh, out = torch.empty_like(qd), torch.empty_like(qd), torch.empty_like(qd)
+    al = torch.empty(B, T, H, device=dev, dtype=torch.float32)
+    ht = torch.empty(B, H, D, D, device=dev, dtype=torch.float32)
+    stages = (
+        ("retrieve_masked", lambda: _abi.check(L.sgsa_layer_retrieve_masked(
+            1, B, T, H, D, kk, P(qd), P(kd), P(vd), P(am), P(ud), 0, 0.25, 0.1, P(wk), P(vh), P(al), None,
+            P(rws), rws.numel(), stream))),
+        ("chunk", lambda: _abi.check(L.sgsa_chunk_fwd(
+            1, B, T, H, D, 64, P(qd), P(kd), P(vd), P(bd), P(gd), P(wk), P(vh), P(al), None, P(out), P(ht),
+            P(cws), cws.numel(), stream))),
+    )
+    cur = torch.cuda.current_stream(dev)
+    for _, fn in stages:
+        fn()
+    torch.cuda.synchronize()
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(stages) + 1)] for _ in range(reps)]
+    for r in range(reps):
+        for i, (_, fn) in enumerate(stages):
+            ev[r][i].record(cur)
+            fn()
+        ev[r][-1].record(cur)
+    torch.cuda.synchronize()
+    st = {nm: sum(ev[r][i].elapsed_time(ev[r][i + 1]) for r in range(reps)) / reps for i, (nm, _) in enumerate(stages)}
+    ms = sum(st.values())
+    pad_rows = vh[:, :pad].float().abs().max().item() if pad > 0 else 0.0
+    res = {"config": "north star, left-padded", "B": B, "T": T, "H": H, "D": D, "top_k": top_k, "pad": pad,
+           "dtype": "bfloat16", "ms": round(ms, 3), "tokens_per_s": round(B * T / (ms / 1000.0), 1),
+           "stage_ms": {nm: round(v, 3) for nm, v in st.items()},
+           "finite": bool(torch.isfinite(out.float()).all() and torch.isfinite(ht).all()),
+           "padded_rows_retrieve_nothing": pad_rows == 0.0}
+    log(f"masked: {json.dumps(res)}")
+    return res
+
+
 def gather_bytes(B, H, T, D, k, elem=2):
     """Algorithmic bytes of the K/V gather: B*H*sum_t min(k, t+1) * 2 rows * D * elem."""
     rows = k * (T - k) + k * (k + 1) // 2 if T > k else T * (T + 1) // 2
@@ -758,6 +815,9 @@ def main() -> int:
             time_config("config 1", 4, 8192, 16, 128, 256, torch.bfloat16),
             time_config("config 3", 1, 65536, 16, 128, 2048, torch.bfloat16, heavy=True),
         ]
+        torch.cuda.empty_cache()
+        # the headline shape with its first eighth of positions padded
+        result["masked"] = time_masked(B, T, H, D, top_k, T // 8)
         torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
         log("cpu baseline (bounded sample)")

@@ -506,6 +506,23 @@ int sgsa_layer_retrieve(int dtype, int B, int T, int H, int D, int top_k,
                         void* write_key, void* v_hat, float* alpha,
                         void* workspace, size_t workspace_bytes, void* stream);
 
+/* The retrieval half of the layer with SparseRetriever.forward's attention_mask
+ * (modelings/modeling_sgsa.py:421-428; SGSABlock.forward passes it to the retriever,
+ * :668-675) on the threshold form: bf16, D = 128, T <= 65536.  attention_mask [B,T]
+ * uint8, nonzero = real token.  A query row sees the real tokens at or before it and
+ * takes k_q = min(top_k, max(1, most real tokens any batch row sees at that position))
+ * slots (:159-160); slots past its own real tokens hold nothing (weight 0), and a
+ * padded query row retrieves nothing (write key, v_hat and alpha 0).  The keys and
+ * values are copied in valid-first order into the workspace, then K1 cuts each row
+ * and K2 recomputes and weighs the scores as in sgsa_layer_retrieve.  Outputs as
+ * sgsa_layer_retrieve_stats.  Workspace: sgsa_layer_retrieve_masked_workspace_size()
+ * bytes (it returns SGSA_ERR_UNSUPPORTED outside bf16 / D = 128 / T <= 65536). */
+int sgsa_layer_retrieve_masked_workspace_size(int dtype, int B, int T, int H, int D, int top_k, size_t* bytes);
+int sgsa_layer_retrieve_masked(int dtype, int B, int T, int H, int D, int top_k, const void* q_ret, const void* k,
+                               const void* v, const uint8_t* attention_mask, const float* budget, int write_mode,
+                               float alpha_max, float tau_c, void* write_key, void* v_hat, float* alpha,
+                               float* row_stats, void* workspace, size_t workspace_bytes, void* stream);
+
 /* sgsa_layer_fwd / sgsa_layer_retrieve with the per-row figures behind
  * SGSABlock.forward's metrics (modelings/modeling_sgsa.py:697-708):
  * alpha_out [B,T,H] fp32 (may be NULL) receives alpha ("alpha_mean");

@@ -86,6 +86,9 @@ SIGNATURES = {
     "sgsa_block_layer_retrieve_workspace_size": (_I, [_I, _I, _I, _I, _I, _I, _I, ctypes.POINTER(_SZ)]),
     "sgsa_block_layer_retrieve": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _I, _F, _P, _P, _P, _P, _P, _I, _F, _P,
                                        _P, _P, _P, _P, _SZ, _P]),
+    "sgsa_layer_retrieve_masked_workspace_size": (_I, [_I, _I, _I, _I, _I, _I, ctypes.POINTER(_SZ)]),
+    "sgsa_layer_retrieve_masked": (_I, [_I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _I, _F, _F, _P, _P, _P, _P,
+                                        _P, _SZ, _P]),
     "sgsa_layer_fwd_workspace_size": (_I, [_I, _I, _I, _I, _I, _I, ctypes.POINTER(_SZ)]),
     "sgsa_layer_fwd": (_I, [_I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _I, _F, _F, _P, _P,
                             _P, _SZ, _P]),

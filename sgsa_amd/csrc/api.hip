@@ -969,11 +969,20 @@ int sgsa_layer_fwd_workspace_size(int dtype, int B, int T, int H, int D, int top
 
 namespace {
 
+// A padding mask for the threshold form: the keys and values in valid-first order and each
+// row's valid prefix and slot count (mask.hip); nullptr members for an unmasked layer.
+struct LayerMask {
+  const int32_t* row_nv = nullptr;
+  const int32_t* row_kq = nullptr;
+  const void* kc = nullptr;
+  const void* vc = nullptr;
+};
+
 // K1 + K2 of the layer path into (wk, vh, al); the workspace is laid out by layer_ws.
 int layer_retrieve_impl(const LayerWs& L, char* base, int dtype, int B, int T, int H, int D, int top_k,
                         const void* q_ret, const void* k, const void* v, const float* budget, int write_mode,
                         float alpha_max, float tau_c, void* wk, void* vh, float* al, float* stats,
-                        hipStream_t st, const char* who) {
+                        hipStream_t st, const char* who, const LayerMask& mk = LayerMask{}) {
   const int kk = top_k < T ? top_k : T;
   int32_t* cnt = (int32_t*)(base + L.cnt);
   float* t2 = (float*)(base + L.top2);
@@ -981,7 +990,8 @@ int layer_retrieve_impl(const LayerWs& L, char* base, int dtype, int B, int T, i
   sgsa::TopkArgs ta{};
   ta.dtype = dtype; ta.B = B; ta.Tq = T; ta.Tk = T; ta.H = H; ta.D = D; ta.top_k = kk; ta.causal = 1;
   ta.q_offset = 0; ta.scale = (float)sqrt((double)D); ta.scale_mode = 0;
-  ta.q = q_ret; ta.k = k; ta.counts = cnt;
+  ta.q = q_ret; ta.k = mk.kc != nullptr ? mk.kc : k; ta.counts = cnt;
+  ta.row_nv = mk.row_nv; ta.row_kq = mk.row_kq;
   if (L.thr) {
     ta.thr = reinterpret_cast<uint2*>(base + L.idx);
     ta.top2 = t2;
@@ -993,7 +1003,8 @@ int layer_retrieve_impl(const LayerWs& L, char* base, int dtype, int B, int T, i
 
   sgsa::GatherArgs ga{};
   ga.dtype = dtype; ga.B = B; ga.Tq = T; ga.Tk = T; ga.H = H; ga.D = D; ga.top_k = kk; ga.q_offset = 0;
-  ga.k = k; ga.v = v; ga.self_key = k; ga.counts = cnt;
+  ga.k = mk.kc != nullptr ? mk.kc : k; ga.v = mk.vc != nullptr ? mk.vc : v; ga.self_key = k; ga.counts = cnt;
+  ga.row_nv = mk.row_nv;
   ga.use_valid = 1; ga.tau_c = tau_c; ga.eps = 1e-6f; ga.local_window = 64; ga.sink_size = 8;
   ga.budget = budget; ga.write_mode = write_mode; ga.alpha_max = alpha_max;
   ga.k_hat = write_mode == 0 ? wk : nullptr; ga.v_hat = vh; ga.write_key = write_mode == 1 ? wk : nullptr;
@@ -1040,6 +1051,46 @@ int sgsa_layer_retrieve_stats(int dtype, int B, int T, int H, int D, int top_k, 
   char* base = (char*)(((uintptr_t)workspace + kAlign - 1) & ~(uintptr_t)(kAlign - 1));
   return layer_retrieve_impl(L, base, dtype, B, T, H, D, top_k, q_ret, k, v, budget, write_mode, alpha_max, tau_c,
                              write_key, v_hat, alpha, row_stats, (hipStream_t)stream, "sgsa_layer_retrieve");
+}
+
+int sgsa_layer_retrieve_masked_workspace_size(int dtype, int B, int T, int H, int D, int top_k, size_t* bytes) {
+  REQUIRE(bytes);
+  if (int s = layer_check(dtype, B, T, H, D, top_k, 0)) return s;
+  const LayerWs L = layer_ws(dtype, B, T, H, D, top_k);
+  if (!L.thr || T > 65536)
+    return fail(SGSA_ERR_UNSUPPORTED, "the masked threshold form needs bf16, D == 128 and T <= 65536");
+  *bytes = align_up(sgsa::mask_workspace_bytes(dtype, B, T, T, H, D, 1)) +
+           align_up((size_t)B * T * H * D * dtype_size(dtype)) + L.total + kAlign;
+  return SGSA_OK;
+}
+
+int sgsa_layer_retrieve_masked(int dtype, int B, int T, int H, int D, int top_k, const void* q_ret, const void* k,
+                               const void* v, const uint8_t* attention_mask, const float* budget, int write_mode,
+                               float alpha_max, float tau_c, void* write_key, void* v_hat, float* alpha,
+                               float* row_stats, void* workspace, size_t workspace_bytes, void* stream) {
+  size_t need = 0;
+  if (int s = sgsa_layer_retrieve_masked_workspace_size(dtype, B, T, H, D, top_k, &need)) return s;
+  if (write_mode != 0 && write_mode != 1) return fail(SGSA_ERR_INVALID_ARG, "write_mode must be 0 (direct) or 1 (residual)");
+  REQUIRE(q_ret); REQUIRE(k); REQUIRE(v); REQUIRE(attention_mask); REQUIRE(budget); REQUIRE(write_key);
+  REQUIRE(v_hat); REQUIRE(alpha); REQUIRE(workspace);
+  if (workspace_bytes < need) return fail(SGSA_ERR_WORKSPACE, "workspace %zu < %zu bytes", workspace_bytes, need);
+  const hipStream_t st = (hipStream_t)stream;
+  char* base = (char*)(((uintptr_t)workspace + kAlign - 1) & ~(uintptr_t)(kAlign - 1));
+  const int kk = top_k < T ? top_k : T;
+  sgsa::MaskArgs m{};
+  m.dtype = dtype; m.B = B; m.Tq = T; m.Tk = T; m.H = H; m.D = D;
+  m.causal = 1; m.q_offset = 0; m.top_k = kk; m.kq_rule = 0; m.kv_hm = 0; m.compacted = 1;
+  m.key_mask = attention_mask; m.query_mask = attention_mask; m.k = k;
+  sgsa::mask_carve(m, base);
+  char* vc = base + align_up(sgsa::mask_workspace_bytes(dtype, B, T, T, H, D, 1));
+  char* lbase = vc + align_up((size_t)B * T * H * D * dtype_size(dtype));
+  if (int s = hip_status(sgsa::launch_mask_prepare(m, st), "sgsa_layer_retrieve_masked (mask)")) return s;
+  if (int s = hip_status(sgsa::launch_mask_compact(m, v, vc, st), "sgsa_layer_retrieve_masked (values)")) return s;
+  LayerMask mk;
+  mk.row_nv = m.nv; mk.row_kq = m.kq; mk.kc = m.kc; mk.vc = vc;
+  const LayerWs L = layer_ws(dtype, B, T, H, D, top_k);
+  return layer_retrieve_impl(L, lbase, dtype, B, T, H, D, top_k, q_ret, k, v, budget, write_mode, alpha_max, tau_c,
+                             write_key, v_hat, alpha, row_stats, st, "sgsa_layer_retrieve_masked", mk);
 }
 
 int sgsa_layer_fwd(int dtype, int B, int T, int H, int D, int top_k, int chunk_size, const void* q, const void* k,

@@ -684,14 +684,21 @@ __global__ __launch_bounds__(256, 2) void gather_thr_kernel(GatherArgs a, const 
       th = __uint_as_float(t.x);
       cut[mt] = (int)t.y;
       mx = a.top2[2 * rg];
-      nv[mt] = max(0, min(Tk, row + a.q_offset + 1));
+      nv[mt] = a.row_nv != nullptr ? a.row_nv[(long)b * Tq + row] : max(0, min(Tk, row + a.q_offset + 1));
     }
     ce[mt] = acc_bound(th, mscale);
     cg[mt] = acc_bound(next_up(th), mscale);
     mxl[mt] = mx * 1.44269504f;
   }
-  // every key below wmin is causal for every row of the wave
-  const int wmin = wr0 + 31 < Tq ? max(0, min(Tk, wr0 + a.q_offset + 1)) : 0;
+  // every key below wmin is valid for every row of the wave (the causal range; with a
+  // padding mask the least of the rows' valid prefixes)
+  int wmin = wr0 + 31 < Tq ? max(0, min(Tk, wr0 + a.q_offset + 1)) : 0;
+  if (a.row_nv != nullptr) {
+    int m = min(nv[0], nv[1]);
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) m = min(m, __shfl_xor(m, o, 64));
+    wmin = wr0 + 31 < Tq ? __builtin_amdgcn_readfirstlane(m) : 0;
+  }
 
   f4 ok_[2][DP / 16], ov_[2][DP / 16], es[2];
 #pragma unroll

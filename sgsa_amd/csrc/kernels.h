@@ -122,6 +122,8 @@ struct MaskArgs {
 size_t mask_workspace_bytes(int dtype, int B, int Tq, int Tk, int H, int D, int compact);
 void mask_carve(MaskArgs& m, void* ws);
 hipError_t launch_mask_prepare(const MaskArgs& m, hipStream_t st);
+// Another [B,Tk,H,D] (or kv_hm [B,H,Tk,D]) tensor in the valid-first key order of m (after launch_mask_prepare).
+hipError_t launch_mask_compact(const MaskArgs& m, const void* src, void* dst, hipStream_t st);
 hipError_t launch_mask_finish(const MaskArgs& m, int32_t* indices, float* scores, uint8_t* slot_valid,
                               const int32_t* counts, int32_t* fill, hipStream_t st);
 
@@ -181,6 +183,8 @@ struct GatherArgs {
   int32_t* sel_dbg;          // threshold gather only: [B,H,Tq,3] selection summary instead of the outputs
   int32_t* max_index;        // GATHER_MAXIDX_SLOTS ints of scratch (256 bytes, diagnostics); required with diag
   const float* margin_in;    // [B,H,Tq] score margin to report instead of top-2 (block_only), or nullptr
+  const int32_t* row_nv;     // threshold gather: [B,Tq] valid-key prefix per row (keys compacted valid-first
+                             // under a padding mask), or nullptr for the causal range
   float ent_pad;             // zero-weight entries of the row beyond the slots (entropy terms of eps)
   int nsplit;                // > 0: split-row form, nsplit partials of split_len slots per row
   int split_len;

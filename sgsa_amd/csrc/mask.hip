@@ -172,27 +172,31 @@ void mask_carve(MaskArgs& m, void* ws) {
   m.kc = m.compacted ? p : nullptr;
 }
 
+hipError_t launch_mask_compact(const MaskArgs& m, const void* src, void* dst, hipStream_t st) {
+  const size_t es = m.dtype == DT_F32 ? 4 : 2;
+  const size_t row_bytes = (size_t)m.D * es;
+  const bool vec = row_bytes % 16 == 0 && ((uintptr_t)src & 15u) == 0 && ((uintptr_t)dst & 15u) == 0;
+  const int upr = (int)(vec ? row_bytes / 16 : (size_t)m.D);
+  const long n = (long)m.B * m.Tk * m.H * upr;
+  const unsigned grid = (unsigned)std::min<long>((n + 255) / 256, 65536L);
+  if (vec)
+    mask_compact_kernel<uint4><<<grid, 256, 0, st>>>((const uint4*)src, (uint4*)dst, m.perm, m.pc, m.B, m.Tk, m.H,
+                                                     upr, m.kv_hm);
+  else if (es == 4)
+    mask_compact_kernel<float><<<grid, 256, 0, st>>>((const float*)src, (float*)dst, m.perm, m.pc, m.B, m.Tk, m.H,
+                                                     upr, m.kv_hm);
+  else
+    mask_compact_kernel<uint16_t><<<grid, 256, 0, st>>>((const uint16_t*)src, (uint16_t*)dst, m.perm, m.pc, m.B,
+                                                        m.Tk, m.H, upr, m.kv_hm);
+  return hipGetLastError();
+}
+
 hipError_t launch_mask_prepare(const MaskArgs& m, hipStream_t st) {
   mask_scan_kernel<<<dim3((unsigned)m.B), 1024, 0, st>>>(m.key_mask, m.Tk, m.pc, m.perm, m.inv);
   mask_rows_kernel<<<dim3((unsigned)((m.Tq + 255) / 256)), 256, 0, st>>>(
       m.query_mask, m.pc, m.B, m.Tq, m.Tk, m.causal, m.q_offset, m.top_k, m.kq_rule, m.nv, m.kq);
   if (!m.compacted) return hipGetLastError();
-  const size_t es = m.dtype == DT_F32 ? 4 : 2;
-  const size_t row_bytes = (size_t)m.D * es;
-  const bool vec = row_bytes % 16 == 0 && ((uintptr_t)m.k & 15u) == 0 && ((uintptr_t)m.kc & 15u) == 0;
-  const int upr = (int)(vec ? row_bytes / 16 : (size_t)m.D);
-  const long n = (long)m.B * m.Tk * m.H * upr;
-  const unsigned grid = (unsigned)std::min<long>((n + 255) / 256, 65536L);
-  if (vec)
-    mask_compact_kernel<uint4><<<grid, 256, 0, st>>>((const uint4*)m.k, (uint4*)m.kc, m.perm, m.pc, m.B, m.Tk, m.H,
-                                                     upr, m.kv_hm);
-  else if (es == 4)
-    mask_compact_kernel<float><<<grid, 256, 0, st>>>((const float*)m.k, (float*)m.kc, m.perm, m.pc, m.B, m.Tk, m.H,
-                                                     upr, m.kv_hm);
-  else
-    mask_compact_kernel<uint16_t><<<grid, 256, 0, st>>>((const uint16_t*)m.k, (uint16_t*)m.kc, m.perm, m.pc, m.B,
-                                                        m.Tk, m.H, upr, m.kv_hm);
-  return hipGetLastError();
+  return launch_mask_compact(m, m.k, m.kc, st);
 }
 
 hipError_t launch_mask_finish(const MaskArgs& m, int32_t* indices, float* scores, uint8_t* slot_valid,

@@ -329,7 +329,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LIST && !FB
 
   // rows this lane holds in the accumulator: 4*lg + e
   // valid keys of query row qr (< Tq): a prefix of the keys
-  const bool masked = !DUMP && !LIST && a.row_nv != nullptr;
+  const bool masked = !DUMP && (!LIST || THR) && a.row_nv != nullptr;   // not in tile-list mode
   auto row_valid = [&](int qr) __attribute__((always_inline)) {
     if (masked) return a.row_nv[(long)b * Tq + qr];
     return a.causal ? max(0, min(Tk, qr + a.q_offset + 1)) : Tk;
@@ -933,8 +933,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LIST && !FB
         a.thr[rowg] = make_uint2(__float_as_uint(th), (uint32_t)cut);
       }
     }
-    // LIST: every row selects exactly min(top_k, valid keys)
-    const int oc = LIST ? min(topk, nvalid[e]) : min(rowcnt[w][4 * lg + e][0], topk);
+    // LIST: every row selects exactly min(its slots, valid keys)
+    const int qre = r0 + 16 * w + 4 * lg + e;
+    const int kre = (masked && a.row_kq != nullptr) ? min(topk, a.row_kq[qre]) : topk;
+    const int oc = LIST ? min(kre, nvalid[e]) : min(rowcnt[w][4 * lg + e][0], topk);
     if (!LIST) for (int p = oc + lr; p < topk; p += 16) {
       a.indices[rowg * topk + p] = 0;
       a.scores[rowg * topk + p] = -FLT_MAX;
@@ -1689,6 +1691,9 @@ __device__ __forceinline__ float acc_hi_of(float a, float mscale) {
 // both of its 64-row halves for the radix fallback launch of
 // score_topk_kernel<..., FB, LIST, THR>, which writes the same outputs.
 // ---------------------------------------------------------------------------
+// MASKED: rows carry a valid prefix and slot count (a.row_nv / a.row_kq, keys
+// compacted valid-first); the unmasked instantiation computes the causal range.
+template <bool MASKED>
 __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nqb, float mscale) {
   constexpr int QR = 128;
   constexpr int NG = QR / 16;
@@ -1704,6 +1709,7 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
   __shared__ int rcntb[NG][16];   // keys in b*
   __shared__ int force_fb;        // a row's 16-bit bin counter could overflow: radix fallback
   __shared__ float2 smap[NG][16]; // the sample histogram's map (iws, bcs) per row
+  __shared__ int rnv[MASKED ? NG : 1][16];   // MASKED: valid keys per row (0 past Tq)
 
   const int BH = a.B * a.H;
   const int nqr = (a.Tq + QR - 1) / QR;
@@ -1717,13 +1723,32 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
   const int Tq = a.Tq, Tk = a.Tk, H = a.H;
   const uint16_t* kb = reinterpret_cast<const uint16_t*>(a.k);
   const int topk = a.top_k;
-  // valid keys of row r0 + 16g + lr (0 for rows past Tq)
-  auto nv_of = [&](int g) __attribute__((always_inline)) {
-    const int qr = r0 + 16 * g + lr;
-    int nv = Tk;
-    if (a.causal) nv = max(0, min(Tk, qr + a.q_offset + 1));
-    return qr < Tq ? nv : 0;
+  // valid keys of query row qr < Tq: the causal (or full) range, or with a padding mask
+  // (row_nv, keys compacted valid-first) the row's valid prefix; and its slots
+  auto nv_row = [&](int qr) __attribute__((always_inline)) {
+    if constexpr (MASKED) return a.row_nv[(long)b * Tq + qr];
+    return a.causal ? max(0, min(Tk, qr + a.q_offset + 1)) : Tk;
   };
+  auto kq_row = [&](int qr) __attribute__((always_inline)) {
+    if constexpr (MASKED) return a.row_kq != nullptr ? min(topk, a.row_kq[qr]) : topk;
+    return topk;
+  };
+  // valid keys of row r0 + 16g + lr (0 for rows past Tq); the masked rows' counts
+  // come from LDS in the sweeps (rnv, written below and visible after the row set-up)
+  auto nv_direct = [&](int g) __attribute__((always_inline)) {
+    const int qr = r0 + 16 * g + lr;
+    return qr < Tq ? nv_row(qr) : 0;
+  };
+  auto nv_of = [&](int g) __attribute__((always_inline)) {
+    if constexpr (MASKED) return rnv[g][lr];
+    return nv_direct(g);
+  };
+  if constexpr (MASKED) {
+    if (tid < QR) {
+      const int qr = r0 + tid;
+      rnv[tid >> 4][tid & 15] = qr < Tq ? nv_row(qr) : 0;
+    }
+  }
 
   // B operand: q^T of the block's rows; lane holds row r0 + 16g + lr, dims 32s + 8lg + [0, 8).
   // All loads first, the norms after.  Rows past Tq load row 0 of the head: their
@@ -1758,7 +1783,7 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
   int minvalid = 0x7fffffff;
 #pragma unroll
   for (int g = 0; g < NG; ++g)
-    if (r0 + 16 * g + lr < Tq) minvalid = min(minvalid, nv_of(g));
+    if (r0 + 16 * g + lr < Tq) minvalid = min(minvalid, nv_direct(g));
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) minvalid = min(minvalid, __shfl_xor(minvalid, o, 64));
   minvalid = __builtin_amdgcn_readfirstlane(minvalid);   // block-uniform: tile tests branch on the scalar unit
@@ -1820,15 +1845,15 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
   if (lane < 32) {
     const int g = w + 4 * (lane >> 4), rr = lane & 15;
     const int qr = r0 + 16 * g + rr;
-    int nv = 0;
-    if (qr < Tq) nv = a.causal ? max(0, min(Tk, qr + a.q_offset + 1)) : Tk;
+    const int nv = qr < Tq ? nv_row(qr) : 0;
+    const int kr = qr < Tq ? kq_row(qr) : topk;
     RowInfo ri;
     const float bound = qnorm[g][rr] * kmx * 1.001f;   // of |acc|
     ri.iw = (bound > 0.f && bound < FLT_MAX) ? 128.0f / bound : 0.f;
     ri.bc = BIN_C0;
     ri.bstar = -1;
-    ri.need = min(topk, nv);
-    ri.mode = (nv <= topk) ? SELECT_ALL : BIN_ALL;
+    ri.need = min(kr, nv);
+    ri.mode = (nv <= kr) ? SELECT_ALL : BIN_ALL;
     ri.pfx = 0; ri.msk = 0; ri.done = 1; ri.th0 = -INFINITY; ri.th1 = -INFINITY;
     rinfo[g][rr] = ri;
     colcnt[g][rr] = 0;
@@ -2002,8 +2027,7 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
           const float2 m = smap[g][r];
           const int n = rcntb[g][r];
           if (!(m.x > 0.f)) continue;   // wave-uniform: no fit for this row
-          const int qr = r0 + 16 * g + r;
-          const int nv = a.causal ? max(0, min(Tk, qr + a.q_offset + 1)) : Tk;
+          const int nv = nv_row(r0 + 16 * g + r);
           const uint32_t* hr = hist[16 * (g & 3) + r];
           const uint32_t sh = 16u * (uint32_t)(g >> 2);
           uint32_t c[4];
@@ -2608,9 +2632,8 @@ __global__ __launch_bounds__(256, 2) void score_thr128_kernel(TopkArgs a, int nq
     const int qr = r0 + 16 * g + r;
     if (qr < Tq) {
       const long rowg = srowb + 16 * g + r;
-      const int nv = a.causal ? max(0, min(Tk, qr + a.q_offset + 1)) : Tk;
       a.thr[rowg] = make_uint2(__float_as_uint(thv), (uint32_t)cutv);
-      if (a.counts) a.counts[rowg] = min(topk, nv);
+      if (a.counts) a.counts[rowg] = min(kq_row(qr), nv_row(qr));
       if (a.split) a.split[rowg] = 0;
       // scores of the top-2 accumulators (score1 is monotone); -FLT_MAX marks "none"
       a.top2[2 * rowg] = t2.x == -FLT_MAX ? -FLT_MAX : score1(t2.x, mscale);
@@ -2671,7 +2694,8 @@ hipError_t launch_score_topk(const TopkArgs& a0, hipStream_t st) {
     // which then counts in 32 bits
     if (a.Tk <= 65536 && ms > 0.f && ms < FLT_MAX) {
       const dim3 grid128((unsigned)(BH * ((a.Tq + 127) / 128)));
-      score_thr128_kernel<<<grid128, 256, 0, st>>>(a, nqb, ms);
+      if (a.row_nv != nullptr) score_thr128_kernel<true><<<grid128, 256, 0, st>>>(a, nqb, ms);
+      else score_thr128_kernel<false><<<grid128, 256, 0, st>>>(a, nqb, ms);
       if (c16) score_topk_kernel<bf16_t, false, true, true, true, true, true><<<grid, 256, 0, st>>>(a, nqb, ms);
       else score_topk_kernel<bf16_t, false, false, true, true, true, true><<<grid, 256, 0, st>>>(a, nqb, ms);
     } else {

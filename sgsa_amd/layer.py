@@ -41,6 +41,40 @@ def layer_workspace_bytes(dtype: torch.dtype, B: int, T: int, H: int, D: int, to
     return n.value
 
 
+def _masked_threshold_form(q: Tensor) -> bool:
+    """A padded bf16 layer with d = 128 and T <= 65536 runs the threshold form on its
+    valid-first keys (sgsa_layer_retrieve_masked); anything else the masked row path."""
+    return q.dtype == torch.bfloat16 and q.shape[-1] == 128 and q.shape[1] <= 65536
+
+
+def _retrieve_masked_thr(q_ret: Tensor, k: Tensor, v: Tensor, budget_logits: Tensor, top_k: int,
+                         attention_mask: Tensor, write_mode: str, alpha_max: float, tau_c: float,
+                         workspace: Optional["LayerWorkspace"], stats: Optional[dict]):
+    B, T, H, D = q_ret.shape
+    dev = q_ret.device
+    if tuple(attention_mask.shape) != (B, T):
+        raise ValueError(f"attention_mask must have shape [batch, seq] = {(B, T)}, got {tuple(attention_mask.shape)}")
+    am = (attention_mask.to(dev) != 0).to(torch.uint8).contiguous()
+    rc, kc, vc = (t.contiguous() for t in (q_ret, k, v))
+    uc = budget_logits.float().contiguous()
+    n = ctypes.c_size_t()
+    _abi.check(_abi.lib().sgsa_layer_retrieve_masked_workspace_size(_abi.dtype_code(q_ret.dtype), B, T, H, D,
+                                                                    int(top_k), ctypes.byref(n)))
+    ws = (workspace or LayerWorkspace()).get(n.value, dev)
+    wk = torch.empty_like(kc)
+    vh = torch.empty_like(kc)
+    al = torch.empty(B, T, H, device=dev, dtype=torch.float32)
+    rs = None
+    if stats is not None:
+        stats["alpha"] = al
+        rs = stats["row_stats"] = torch.empty(2, B, H, T, device=dev, dtype=torch.float32)
+    _abi.check(_abi.lib().sgsa_layer_retrieve_masked(
+        _abi.dtype_code(q_ret.dtype), B, T, H, D, int(top_k), _abi.ptr(rc), _abi.ptr(kc), _abi.ptr(vc), _abi.ptr(am),
+        _abi.ptr(uc), _WRITE_MODES[write_mode], float(alpha_max), float(tau_c), _abi.ptr(wk), _abi.ptr(vh),
+        _abi.ptr(al), _abi.ptr(rs), _abi.ptr(ws), ws.numel(), _abi.stream_of(rc)))
+    return wk, vh, al
+
+
 def sgsa_layer_forward(
     q: Tensor,
     k: Tensor,
@@ -66,8 +100,10 @@ def sgsa_layer_forward(
     Returns (o [B,T,H,D] in q.dtype, final state [B,H,D,D] float32 or None).
     attention_mask [B,T] (nonzero = real token): the retrieval masks padded
     keys and queries (SparseRetriever.forward, modeling_sgsa.py:421-428); the
-    state update itself takes no mask (:584-596).  The masked layer runs as
-    its three entry points (masked select, masked gather + gate, chunked update).
+    state update itself takes no mask (:584-596).  The masked layer runs its
+    retrieval on the threshold form over valid-first keys (bf16, d = 128,
+    T <= 65536: sgsa_layer_retrieve_masked) or else as the masked select and
+    gather, then the chunked update.
     ``stats`` (a dict) receives "alpha" [B,T,H] and "row_stats" [2,B,H,T]
     (sgsa_layer_fwd_stats: largest weight, write-key norm ratio per row).
     """
@@ -83,8 +119,12 @@ def sgsa_layer_forward(
     if write_mode not in _WRITE_MODES:
         raise ValueError(f"write_mode must be one of {sorted(_WRITE_MODES)}")
     if attention_mask is not None:
-        wk, vh, al = masked_gather_gate(q_ret, k, v, budget_logits, top_k, attention_mask, write_mode=write_mode,
-                                        alpha_max=alpha_max, tau_c=tau_c, stats=stats)
+        if _masked_threshold_form(q):
+            wk, vh, al = _retrieve_masked_thr(q_ret, k, v, budget_logits, top_k, attention_mask, write_mode,
+                                              alpha_max, tau_c, workspace, stats)
+        else:
+            wk, vh, al = masked_gather_gate(q_ret, k, v, budget_logits, top_k, attention_mask, write_mode=write_mode,
+                                            alpha_max=alpha_max, tau_c=tau_c, stats=stats)
         o, ht = chunk_sgsa_fwd(q, k, v, beta, gamma, wk, vh, al, initial_state=initial_state,
                                chunk_size=chunk_size, output_final_state=output_final_state)
         if out is not None:
@@ -143,6 +183,9 @@ def sgsa_layer_retrieve(
     if write_mode not in _WRITE_MODES:
         raise ValueError(f"write_mode must be one of {sorted(_WRITE_MODES)}")
     if attention_mask is not None:
+        if _masked_threshold_form(q_ret):
+            return _retrieve_masked_thr(q_ret, k, v, budget_logits, top_k, attention_mask, write_mode, alpha_max,
+                                        tau_c, workspace, stats)
         return masked_gather_gate(q_ret, k, v, budget_logits, top_k, attention_mask, write_mode=write_mode,
                                   alpha_max=alpha_max, tau_c=tau_c, stats=stats)
     dev = q_ret.device

@@ -9,6 +9,11 @@ merged mask (modelings/hybrid_dense_delta_topk.py:153-175, :343-356).
 * Values: k_hat / v_hat / weights / diagnostics of the masked retrieval, the
   masked layer (write key, v_hat, alpha, output, final state) and the KV-reuse
   attention against the oracle within the stated tolerances.
+* The threshold form under a mask (bf16, d = 128: the layer's keys compacted
+  valid-first, per-row valid prefix and slot count in score_thr128_kernel, its
+  radix fallback and gather_thr_kernel) against the oracle layer, bit-equal to
+  the unmasked form under an all-ones mask, and on mass ties that send blocks to
+  the fallback.
 
 Masks: batch 0 all real tokens, batch 1 left-padded, batch 2 right-padded with
 holes; padded query rows and rows with fewer valid keys than k_q are included.
@@ -153,6 +158,73 @@ def test_masked_layer_matches_oracle(dev, dtype, tol):
     close(al, ref["alpha"], tol, "alpha")
     close(o, ref["o"], tol, "o")
     close(st, ref["final_state"], tol, "final state")
+
+
+@pytest.mark.parametrize("shape", [(3, 640, 2, 32), (2, 1500, 2, 300)])
+def test_masked_threshold_layer_matches_oracle(dev, shape):
+    # bf16, d = 128: the masked layer runs the threshold form (score_thr128_kernel and
+    # gather_thr_kernel over keys compacted valid-first, per-row valid prefix and slots)
+    B, T, H, k = shape
+    D = 128
+    x = O.make_inputs(B, T, H, D, dtype=torch.bfloat16, seed=8)
+    am = _mask(B, T)
+    assert sgsa_amd.layer._masked_threshold_form(x["q"])
+    print(f"masked threshold layer B={B} T={T} H={H} D={D} k={k}", flush=True)
+    ref = O.sgsa_layer_forward(x["q_f32"], x["k_f32"], x["v_f32"], x["q_f32"], x["beta"], x["gamma"],
+                               x["budget"], k, attention_mask=am)
+    g = {n: x[n].to(dev) for n in ("q", "k", "v", "beta", "gamma", "budget")}
+    st_ = {}
+    o, st = sgsa_amd.sgsa_layer_forward(g["q"], g["k"], g["v"], g["q"], g["beta"], g["gamma"], g["budget"], k,
+                                        attention_mask=am.to(dev), stats=st_)
+    wk, vh, al = sgsa_amd.sgsa_layer_retrieve(g["q"], g["k"], g["v"], g["budget"], k, attention_mask=am.to(dev))
+    torch.cuda.synchronize()
+    assert "row_stats" in st_, "the threshold form did not run"
+    assert torch.equal(al, st_["alpha"])
+    close(wk, ref["write_key"], 2e-2, "write key")
+    close(vh, ref["v_hat"], 2e-2, "v_hat")
+    close(al, ref["alpha"], 2e-2, "alpha")
+    close(o, ref["o"], 2e-2, "o", elem_p99=2e-2)
+    close(st, ref["final_state"], 2e-2, "final state", elem_p99=2e-2)
+    pad = ~am.to(dev)
+    assert vh[pad].abs().max() == 0 and al[pad].abs().max() == 0, "padded query rows retrieve nothing"
+
+
+def test_masked_threshold_all_ones_mask_equals_unmasked(dev):
+    B, T, H, D, k = 2, 1200, 2, 128, 256
+    x = O.make_inputs(B, T, H, D, dtype=torch.bfloat16, seed=9)
+    g = {n: x[n].to(dev) for n in ("q", "k", "v", "budget")}
+    am = torch.ones(B, T, dtype=torch.bool, device=dev)
+    for mode in ("direct", "residual"):
+        got = sgsa_amd.sgsa_layer_retrieve(g["q"], g["k"], g["v"], g["budget"], k, attention_mask=am,
+                                           write_mode=mode)
+        want = sgsa_amd.sgsa_layer_retrieve(g["q"], g["k"], g["v"], g["budget"], k, write_mode=mode)
+        torch.cuda.synchronize()
+        for name, a_, b_ in zip(("write key", "v_hat", "alpha"), got, want):
+            assert torch.equal(a_, b_), f"{mode} {name}: an all-ones mask changes the threshold form"
+
+
+def test_masked_threshold_ties_take_the_fallback(dev):
+    # keys drawn from two rows: a row's threshold bin holds every valid key equal to its
+    # better row, more than the collect capacity past ~1100 rows, so those blocks take the
+    # masked radix fallback; ties resolve to the lowest-index valid keys, as in the oracle
+    B, T, H, D, k = 3, 1600, 2, 128, 64
+    gen = torch.Generator().manual_seed(10)
+    base = torch.randn(2, H, D, generator=gen)
+    kr = base[torch.randint(0, 2, (B, T), generator=gen)].to(torch.bfloat16)
+    q = torch.randn(B, T, H, D, generator=gen).to(torch.bfloat16)
+    v = torch.randn(B, T, H, D, generator=gen).to(torch.bfloat16)
+    bud = torch.randn(B, T, H, generator=gen)
+    am = _mask(B, T)
+    print(f"masked threshold ties B={B} T={T} H={H} k={k}", flush=True)
+    ret = O.token_topk_retrieval(q.float(), kr.float(), v.float(), k, attention_mask=am)
+    wk, vh, al = sgsa_amd.sgsa_layer_retrieve(q.to(dev), kr.to(dev), v.to(dev), bud.to(dev), k,
+                                              attention_mask=am.to(dev))
+    torch.cuda.synchronize()
+    close(vh, ret["v_hat"], 2e-2, "v_hat")
+    wko = O.write_key(ret["k_hat"], kr.float(), "direct")
+    close(wk, wko, 2e-2, "write key")
+    alo = O.compute_alpha(ret["diagnostics"]["concentration"], ret["diagnostics"]["novelty"], bud, wko, ret["v_hat"])
+    close(al, alo, 2e-2, "alpha")
 
 
 @pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-4), (torch.bfloat16, 2e-2)])
