@@ -736,7 +736,7 @@ def main() -> int:
     f_chunk = B * H * ((T + 63) // 64) * 23.77e6     # chunk contractions (K3 + K5 + K4)
     gather_kernel = {"threshold": "gather_thr_kernel<false>", "tiled": "gather_list_kernel",
                      "direct": "sparse_gather_kernel<bf16_t, true, false>"}[args.gather]
-    topk_kernel = {"threshold": "score_thr128_kernel", "tiled": "score_topk_tiles_kernel<true, false>",
+    topk_kernel = {"threshold": "score_thr128_kernel<false>", "tiled": "score_topk_tiles_kernel<true, false>",
                    "direct": "score_topk_kernel<bf16_t, false, true, true, false, false, false>"}[args.gather]
     rooflines = {
         "score_topk": {"kernel": f"{topk_kernel} (K1)", "bound": "mfma",
