@@ -78,12 +78,13 @@ def heavy_tail_keys(k, seed=0, frac=0.01, mult=8.0):
     return kr
 
 
-def time_config(name, B, T, H, D, top_k, dtype, heavy=False, reps=3):
+def time_config(name, B, T, H, D, top_k, dtype, heavy=False, reps=3, cpu=False):
     """One BASELINE.json configuration through the layer path, outside the timed steps:
     K1 -> K2 -> chunk update as sgsa_layer_fwd runs them (bf16, d = 128: the threshold
     form, per stage; otherwise the whole sgsa_layer_fwd call).  Config 3 retrieves over
     the heavy-tailed keys and updates the state with the unit-norm ones.  Returns ms per
-    layer forward (mean of ``reps`` after one warm-up), tokens/s and the stage split."""
+    layer forward (mean of ``reps`` after one warm-up), tokens/s and the stage split, and
+    with ``cpu`` the CPU oracle's rate on a bounded sample of the same inputs."""
     import sgsa_amd
     from sgsa_amd import _abi
     dev = torch.device("cuda:0")
@@ -91,6 +92,7 @@ def time_config(name, B, T, H, D, top_k, dtype, heavy=False, reps=3):
     kr = heavy_tail_keys(k) if heavy else k
     qd, kd, vd, krd = (t.to(dev, dtype).contiguous() for t in (q, k, v, kr))
     bd, gd, ud = (t.to(dev).contiguous() for t in (beta, gamma, budget))
+    cpu_in = (q.to(dtype), kr.to(dtype), v.to(dtype), beta, gamma, budget) if cpu else None
     del q, k, v, kr
     L, P = _abi.lib(), _abi.ptr
     stream = _abi.stream_of(qd)
@@ -147,6 +149,8 @@ def time_config(name, B, T, H, D, top_k, dtype, heavy=False, reps=3):
            "stage_ms": {nm: round(v, 3) for nm, v in st.items()}, "finite": ok}
     if "score_topk" in st:
         res["score_topk_mfma_frac"] = round(f_score / (st["score_topk"] / 1000.0) / 2.5e15, 4)
+    if cpu_in is not None:
+        res["cpu_baseline"] = cpu_baseline(*cpu_in, dict(B=B, T=T, H=H, D=D, top_k=top_k, chunk=64))
     log(f"{name}: {json.dumps(res)}")
     return res
 
@@ -810,10 +814,11 @@ def main() -> int:
         # BASELINE.json's other single-GPU configurations through the same layer path, outside the timed steps
         del idx, sc, tl, toff, tws
         torch.cuda.empty_cache()
+        cpu = not args.no_cpu_baseline
         result["other_configs"] = [
-            time_config("config 0", 1, 512, 4, 64, 32, torch.float32),
-            time_config("config 1", 4, 8192, 16, 128, 256, torch.bfloat16),
-            time_config("config 3", 1, 65536, 16, 128, 2048, torch.bfloat16, heavy=True),
+            time_config("config 0", 1, 512, 4, 64, 32, torch.float32, cpu=cpu),
+            time_config("config 1", 4, 8192, 16, 128, 256, torch.bfloat16, cpu=cpu),
+            time_config("config 3", 1, 65536, 16, 128, 2048, torch.bfloat16, heavy=True, cpu=cpu),
         ]
         torch.cuda.empty_cache()
         # the headline shape with its first eighth of positions padded
