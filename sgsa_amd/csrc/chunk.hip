@@ -495,8 +495,7 @@ static hipError_t launch_intra_t(const ChunkArgs& a, float* W, float* U, float* 
 
 hipError_t launch_chunk_intra(const ChunkArgs& a, float* W, float* U, float* lgd, float* A, hipStream_t st) {
   const bool sp = a.sparse_k != nullptr;
-  if (a.dtype == DT_BF16)
-    return sp ? launch_intra_t<bf16_t, true>(a, W, U, lgd, A, st) : launch_intra_t<bf16_t, false>(a, W, U, lgd, A, st);
+  if (a.dtype == DT_BF16) return launch_chunk_intra_bf16(a, W, U, lgd, A, st);
   return sp ? launch_intra_t<float, true>(a, W, U, lgd, A, st) : launch_intra_t<float, false>(a, W, U, lgd, A, st);
 }
 

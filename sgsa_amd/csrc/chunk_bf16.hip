@@ -183,11 +183,25 @@ __device__ __forceinline__ f4 ld16(const float* Z, int lr, int lg) {
 
 constexpr int K3W = 8;   // waves of a chunk_inv_bf16 block
 
-template <int M, bool FULL>
+// The backward's per-chunk operands (chunk_bwd.hip), fp32: A [M][M] row-major (zero
+// above the diagonal), W = A diag(e^{l_tau}) kappa and U = A nu [M][DP], the log-decay
+// prefix [L].  Samples past T have zero kappa and nu rows.
+struct K3Bwd {
+  float* A;
+  float* W;
+  float* U;
+  float* logd;
+  const bf16_t* v;
+  const bf16_t* sv;
+};
+
+// BWD: the backward's form -- the same Gram and inverse, then K3Bwd's outputs in place
+// of the bf16 A tiles.
+template <int M, bool FULL, bool BWD = false>
 __global__ __launch_bounds__(64 * K3W) void chunk_inv_bf16(const bf16_t* __restrict__ k, const bf16_t* __restrict__ sk,
                                                     const float* __restrict__ beta, const float* __restrict__ alpha,
                                                     const float* __restrict__ gamma, int T, int H, int D, int NT,
-                                                    uint16_t* __restrict__ Aout) {
+                                                    uint16_t* __restrict__ Aout, K3Bwd bw = K3Bwd{}) {
   constexpr bool SP = M == 2 * L;
   constexpr int NB = M / 16;
   constexpr int NTL = NB * (NB + 1) / 2;
@@ -198,6 +212,7 @@ __global__ __launch_bounds__(64 * K3W) void chunk_inv_bf16(const bf16_t* __restr
   __shared__ __align__(16) float Tt[NTL * 16 * TP];      // lower tiles of T, then of A
   __shared__ float lam[M];
   __shared__ float logd[L];
+  __shared__ float dtau[BWD ? M : 1];   // BWD: e^{l_tau_i} per sample
   uint16_t* kap = reinterpret_cast<uint16_t*>(un);
 
   const int c = blockIdx.x, bh = blockIdx.y;
@@ -323,12 +338,59 @@ __global__ __launch_bounds__(64 * K3W) void chunk_inv_bf16(const bf16_t* __restr
     __syncthreads();
   }
 
-  // A -> workspace: [NTL tiles][16][16] bf16 (round to nearest)
-  uint16_t* dst = Aout + ((long)bh * NT + c) * NTL * 256;
-  for (int e = tid; e < NTL * 64; e += 64 * K3W) {
-    const int tl = e >> 6, r = (e >> 2) & 15, cg = e & 3;
-    const float* src = Tt + tl * 16 * TP + r * TP + 4 * cg;
-    *reinterpret_cast<uint2*>(dst + tl * 256 + r * 16 + 4 * cg) = make_uint2(pack2(src[0], src[1]), pack2(src[2], src[3]));
+  if constexpr (!BWD) {
+    // A -> workspace: [NTL tiles][16][16] bf16 (round to nearest)
+    uint16_t* dst = Aout + ((long)bh * NT + c) * NTL * 256;
+    for (int e = tid; e < NTL * 64; e += 64 * K3W) {
+      const int tl = e >> 6, r = (e >> 2) & 15, cg = e & 3;
+      const float* src = Tt + tl * 16 * TP + r * TP + 4 * cg;
+      *reinterpret_cast<uint2*>(dst + tl * 256 + r * 16 + 4 * cg) = make_uint2(pack2(src[0], src[1]), pack2(src[2], src[3]));
+    }
+  } else {
+    const long cid = (long)bh * NT + c;
+    if (tid < L) bw.logd[cid * L + tid] = logd[tid];
+    // A: [M][M] fp32, row-major, zero above the diagonal
+    float* Ac = bw.A + cid * M * M;
+    for (int e = tid; e < M * M; e += 64 * K3W) {
+      const int i = e / M, j = e % M, I = i >> 4, J = j >> 4;
+      Ac[e] = (J < I || (J == I && (j & 15) <= (i & 15))) ? Tt[tri(I, J) * 16 * TP + (i & 15) * TP + (j & 15)] : 0.f;
+    }
+    // W = A diag(e^{l_tau}) kappa, then U = A nu: the rows staged again in the union
+    // (zero past T and past D), fp32 MFMA (A fp32, the bf16 rows exact in fp32).
+    // Output tile (I, n), I < NB, n < DP / 16: wave w takes tiles w, w + K3W, ..
+    float* dt = dtau;
+    for (int pass = 0; pass < 2; ++pass) {
+      __syncthreads();   // the union's previous contents are no longer read
+      const bf16_t* lo_src = pass == 0 ? k : bw.v;
+      const bf16_t* sp_src = pass == 0 ? sk : bw.sv;
+      for (int e = tid; e < M * (DP / 8); e += 64 * K3W) {
+        const int i = e / (DP / 8), cv = e % (DP / 8);
+        const int t = t0 + samp_t<SP>(i);
+        const bf16_t* src = samp_r<SP>(i) ? sp_src : lo_src;
+        *reinterpret_cast<uint4*>(&kap[i * PK + 8 * cv]) =
+            load8(src + ((long)(b * T + (t < T ? t : 0)) * H + h) * D, 8 * cv, D, t < T);
+      }
+      if (pass == 0 && tid < M) dt[tid] = expf(logd[samp_t<SP>(tid)]);
+      __syncthreads();
+      float* dst = (pass == 0 ? bw.W : bw.U) + cid * M * DP;
+      for (int ot = w; ot < NB * (DP / 16); ot += K3W) {
+        const int I = ot / (DP / 16), n = ot % (DP / 16);
+        f4 acc = f4_zero();
+        for (int J = 0; J <= I; ++J) {
+          const float* At = Tt + tri(I, J) * 16 * TP;
+#pragma unroll
+          for (int s4 = 0; s4 < 4; ++s4) {
+            const int kk = 16 * J + 4 * s4 + lg;
+            float bb = bf16_to_f32(kap[kk * PK + 16 * n + lr]);
+            if (pass == 0) bb *= dt[kk];
+            const float aa = (J == I && 4 * s4 + lg > lr) ? 0.f : At[lr * TP + 4 * s4 + lg];
+            acc = mma_f32(aa, bb, acc);
+          }
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) dst[(long)(16 * I + 4 * lg + e) * DP + 16 * n + lr] = acc[e];
+      }
+    }
   }
 }
 
@@ -1094,6 +1156,22 @@ size_t chunk_bf16_workspace_bytes(int B, int T, int H, int has_sparse) {
   const size_t G = seg_count(B * H, (int)NT);
   if (G > 1) total += 3 * (size_t)B * H * G * DP * DP * 4;   // segment maps P, Phi and start states
   return total + 256 * 4;
+}
+
+template <int M, bool FULL>
+static hipError_t launch_intra_bwd_t(const ChunkArgs& a, float* W, float* U, float* lgd, float* A, hipStream_t st) {
+  const int NT = (a.T + L - 1) / L;
+  const K3Bwd bw{A, W, U, lgd, (const bf16_t*)a.v, (const bf16_t*)a.sparse_v};
+  chunk_inv_bf16<M, FULL, true><<<dim3(NT, a.B * a.H), 64 * K3W, 0, st>>>(
+      (const bf16_t*)a.k, (const bf16_t*)a.sparse_k, a.beta, a.alpha, a.gamma, a.T, a.H, a.D, NT, nullptr, bw);
+  return hipGetLastError();
+}
+
+// The backward's per-chunk operands for bf16 inputs (see K3Bwd).
+hipError_t launch_chunk_intra_bf16(const ChunkArgs& a, float* W, float* U, float* lgd, float* A, hipStream_t st) {
+  const bool sp = a.sparse_k != nullptr, full = a.D == DP;
+  if (sp) return full ? launch_intra_bwd_t<2 * L, true>(a, W, U, lgd, A, st) : launch_intra_bwd_t<2 * L, false>(a, W, U, lgd, A, st);
+  return full ? launch_intra_bwd_t<L, true>(a, W, U, lgd, A, st) : launch_intra_bwd_t<L, false>(a, W, U, lgd, A, st);
 }
 
 template <int M, bool FULL>

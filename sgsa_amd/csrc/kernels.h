@@ -35,6 +35,8 @@ hipError_t launch_chunk_bf16(const ChunkArgs& a, hipStream_t st);
 // (b*H + h, chunk) W, U [M][128], the log-decay prefix [64] and A [M][M]
 // (M = 128 with the sparse write, else 64).
 hipError_t launch_chunk_intra(const ChunkArgs& a, float* W, float* U, float* lgd, float* A, hipStream_t st);
+// The same operands for bf16 inputs from the forward's K3 (chunk_inv_bf16 in its backward form).
+hipError_t launch_chunk_intra_bf16(const ChunkArgs& a, float* W, float* U, float* lgd, float* A, hipStream_t st);
 
 // Backward of chunk_sgsa (chunk_bwd.hip).
 struct ChunkBwdArgs {
