@@ -9,13 +9,13 @@
 //      W = A diag(D_tau) kappa, U = A nu and the log-decay prefix l;
 //   2. chunk_bwd_maps_kernel, parallel over chunks: the chunk's affine state
 //      map S' = Phi S + Pm, Phi = e^l_L I - kappa^T diag(c) W,
-//      Pm = kappa^T diag(c) U; chunk_bwd_fscan_kernel, sequential over chunks
-//      per 16-column slice: the chunk-start states;
+//      Pm = kappa^T diag(c) U; a segmented scan (sscan_kernel) over the
+//      chunks: the chunk-start states;
 //   3. chunk_bwd_pre_kernel, parallel: X1 = P^T dO and the state-independent
 //      part of the state gradient's step, Y2 = Q^T diag(e^l) dO - W^T X1;
-//      chunk_bwd_bscan_kernel, sequential from the last chunk: the state
-//      gradient at every chunk end, G <- Phi^T G + Y2 (Phi^T = e^l_L I -
-//      W^T diag(c) kappa is the adjoint of the state map);
+//      a segmented scan from the last chunk: the state gradient at every
+//      chunk end, G <- Phi^T G + Y2 (Phi^T = e^l_L I - W^T diag(c) kappa is
+//      the adjoint of the state map);
 //   4. chunk_bwd_grad_kernel, parallel over chunks: every input gradient of a
 //      chunk from its start state S, its end gradient G and its inputs.
 //
@@ -171,87 +171,6 @@ __global__ __launch_bounds__(64 * GW) void chunk_bwd_maps_kernel(ChunkBwdArgs a,
                      [&](int k, int cc) { return colv(&ws[0][0], PIT, k, 16 * J + cc); });
 #pragma unroll
     for (int e = 0; e < 4; ++e) Pm[(long)(16 * I + 4 * lg + e) * DP + 16 * J + (lane & 15)] = x[e];
-  }
-}
-
-// A sequential scan of the affine chunk maps over a 16-column slice: grid
-// (DP/16, B*H), 256 threads; wave w owns rows [32 w, 32 w + 32).  FWD: the
-// state, S_{c+1} = Phi_c S_c + Y_c from the first chunk, storing each S_c;
-// !FWD: the state gradient, G_{c-1} = Phi_c^T G_c + Y_c from the last chunk,
-// storing each G_c.  Phi_c is loaded into registers one chunk ahead and
-// staged in LDS (padded rows: both orientations read without bank conflicts).
-template <bool FWD>
-__global__ __launch_bounds__(256) void chunk_bwd_scan_kernel(const float* __restrict__ Phig,
-                                                             const float* __restrict__ Yg,
-                                                             const float* __restrict__ init, int D,
-                                                             float* __restrict__ out, float* __restrict__ last,
-                                                             int NT) {
-  constexpr int EPT = DP * DP / 256 / 4;   // float4 per thread
-  __shared__ float ph[DP][PIT];
-  __shared__ float xs[DP][17];
-  const int cs = blockIdx.x, bh = blockIdx.y;
-  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int lr = lane & 15, lg = lane >> 4;
-  const int col = 16 * cs + lr;
-
-  float4 pf[EPT];
-  auto prefetch = [&](int c) __attribute__((always_inline)) {
-    const float4* src = reinterpret_cast<const float4*>(Phig + ((long)bh * NT + c) * DP * DP);
-#pragma unroll
-    for (int u = 0; u < EPT; ++u) pf[u] = src[tid + 256 * u];
-  };
-  f4 x[2];
-#pragma unroll
-  for (int u = 0; u < 2; ++u) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int row = 16 * (2 * w + u) + 4 * lg + e;
-      x[u][e] = (init != nullptr && row < D && col < D) ? init[((long)bh * D + row) * D + col] : 0.f;
-    }
-  }
-  prefetch(FWD ? 0 : NT - 1);
-  for (int s = 0; s < NT; ++s) {
-    const int c = FWD ? s : NT - 1 - s;
-    const long cb = (long)bh * NT + c;
-#pragma unroll
-    for (int u = 0; u < EPT; ++u) {
-      const int e4 = tid + 256 * u, r = (4 * e4) / DP, c0 = (4 * e4) % DP;
-      ph[r][c0] = pf[u].x; ph[r][c0 + 1] = pf[u].y; ph[r][c0 + 2] = pf[u].z; ph[r][c0 + 3] = pf[u].w;
-    }
-    float* oc = out + cb * DP * DP;
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int row = 16 * (2 * w + u) + 4 * lg + e;
-        xs[row][lr] = x[u][e];
-        oc[(long)row * DP + col] = x[u][e];
-      }
-    }
-    __syncthreads();
-    if (s + 1 < NT) prefetch(FWD ? c + 1 : c - 1);
-    const float* Yc = Yg + cb * DP * DP;
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int R0 = 16 * (2 * w + u);
-      const f4 acc = FWD ? mm(f4_zero(), DP, [&](int r, int k) { return ph[R0 + r][k]; },
-                              [&](int k, int cc) { return xs[k][cc]; })
-                         : mm(f4_zero(), DP, [&](int r, int k) { return ph[k][R0 + r]; },
-                              [&](int k, int cc) { return xs[k][cc]; });
-#pragma unroll
-      for (int e = 0; e < 4; ++e) x[u][e] = acc[e] + Yc[(long)(R0 + 4 * lg + e) * DP + col];
-    }
-    __syncthreads();
-  }
-  if (last != nullptr) {
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int row = 16 * (2 * w + u) + 4 * lg + e;
-        if (row < D && col < D) last[((long)bh * D + row) * D + col] = x[u][e];
-      }
-    }
   }
 }
 
@@ -672,8 +591,187 @@ __global__ __launch_bounds__(64 * GW) void chunk_bwd_grad_kernel(ChunkBwdArgs a,
   }
 }
 
+// ---------------------------------------------------------------------------
+// Segmented scans of the state maps (the chunk-start states and the end-of-chunk
+// state gradients).  x <- Phi_c x + Y_c over the chunks of a head (TR: Phi_c^T,
+// in decreasing chunk order) is split into G segments of CPS chunks:
+//   1. each segment's composed map, run from I without Y and from 0 with Y
+//      (sscan_kernel over the segment's chunks, all segments in parallel);
+//   2. the segment-level scan over those G maps from the initial state, which
+//      gives every segment's entering state;
+//   3. every segment rerun from its entering state, writing x before each chunk.
+// That takes 2 CPS + G dependent steps instead of NT.  A block (512 threads)
+// holds the whole DP x DP state, wave w its 16-column tile in the accumulator
+// layout (32 VGPRs), so each Phi_c is read once per step; the product runs on
+// v_mfma_f32_16x16x4_f32 with Phi_c staged in LDS from registers loaded one step
+// ahead and the wave's columns of x staged as the B operand.
+// ---------------------------------------------------------------------------
+struct SScanArgs {
+  const float* phi;   // [BH][NP][DP][DP] row-major
+  const float* y;     // same layout, or nullptr
+  int NP, CPS, G;
+  int init_mode;      // 0: zero, 1: identity, 2: per segment [BH][G][DP][DP], 3: [BH][D][D] (zero past D)
+  const float* init;
+  int D;
+  float* out;         // [BH][NP][DP][DP]: x before each step, or nullptr
+  int last_mode;      // 0: none, 1: per segment [BH][G][DP][DP], 2: [BH][D][D] from the scan's last segment
+  float* last;
+};
+
+template <bool TR, bool INC>
+__global__ __launch_bounds__(512) void sscan_kernel(SScanArgs a) {
+  constexpr int NW = 8;
+  constexpr int EPT = DP * DP / (64 * NW) / 4;   // float4 of Phi per thread
+  constexpr int MB = DP * DP * 4;                // bytes of one matrix
+  __shared__ __align__(16) float ph[DP][PIT];
+  __shared__ float xs[NW][DP][17];
+  const int z = blockIdx.x, bh = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lr = lane & 15, lg = lane >> 4;
+  const int col = 16 * w + lr;
+  const int cbeg = z * a.CPS, cend = min(a.NP, cbeg + a.CPS);
+  const int nst = cend - cbeg;
+  // element (16 rt + 4 lg + e, col) of a matrix: byte offset xoff + 4 DP (16 rt + e), the
+  // row part a compile-time constant (scalar offsets of buffer loads and stores)
+  const int xoff = 4 * (4 * lg * DP + col);
+  auto rsrc = [](const float* base) __attribute__((always_inline)) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, MB, 0x00020000);
+  };
+
+  f4 x[DP / 16];
+  {
+    const bool seg_in = a.init_mode == 2;
+    const auto ir = rsrc(seg_in ? a.init + ((long)bh * a.G + z) * DP * DP : a.phi);
+#pragma unroll
+    for (int rt = 0; rt < DP / 16; ++rt) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = 16 * rt + 4 * lg + e;
+        float v = 0.f;
+        if (a.init_mode == 1) v = row == col ? 1.f : 0.f;
+        else if (seg_in) v = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ir, xoff, 4 * DP * (16 * rt + e), 0));
+        else if (a.init_mode == 3) v = (row < a.D && col < a.D) ? a.init[((long)bh * a.D + row) * a.D + col] : 0.f;
+        x[rt][e] = v;
+      }
+    }
+  }
+  uint4 pf[EPT];
+  auto prefetch = [&](int c) __attribute__((always_inline)) {
+    const auto pr = rsrc(a.phi + ((long)bh * a.NP + c) * DP * DP);
+#pragma unroll
+    for (int u = 0; u < EPT; ++u) pf[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(pr, 16 * tid, 16 * 64 * NW * u, 0));
+  };
+  if (nst > 0) prefetch(INC ? cbeg : cend - 1);
+  for (int s = 0; s < nst; ++s) {
+    const int c = INC ? cbeg + s : cend - 1 - s;
+    const long cb = (long)bh * a.NP + c;
+#pragma unroll
+    for (int u = 0; u < EPT; ++u) {
+      const int e4 = tid + 64 * NW * u, r = (4 * e4) / DP, c0 = (4 * e4) % DP;
+      *reinterpret_cast<uint4*>(&ph[r][c0]) = pf[u];
+    }
+#pragma unroll
+    for (int rt = 0; rt < DP / 16; ++rt) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) xs[w][16 * rt + 4 * lg + e][lr] = x[rt][e];
+    }
+    if (a.out != nullptr) {   // block-uniform
+      float* ob = a.out + cb * DP * DP + (long)(4 * lg) * DP + col;
+#pragma unroll
+      for (int rt = 0; rt < DP / 16; ++rt) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ob[(16 * rt + e) * DP] = x[rt][e];
+      }
+    }
+    __syncthreads();
+    if (s + 1 < nst) prefetch(INC ? c + 1 : c - 1);
+    const bool hy = a.y != nullptr;
+    const auto yr = rsrc(hy ? a.y + cb * DP * DP : a.phi);
+#pragma unroll
+    for (int rt = 0; rt < DP / 16; ++rt) {
+      f4 acc0 = f4_zero(), acc1 = f4_zero();
+#pragma unroll 1
+      for (int k0 = 0; k0 < DP; k0 += 32) {
+        float av0[4], av1[4];
+        if constexpr (TR) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            av0[j] = ph[k0 + 4 * lg + j][16 * rt + lr];
+            av1[j] = ph[k0 + 16 + 4 * lg + j][16 * rt + lr];
+          }
+        } else {
+          const float4 p0 = *reinterpret_cast<const float4*>(&ph[16 * rt + lr][k0 + 4 * lg]);
+          const float4 p1 = *reinterpret_cast<const float4*>(&ph[16 * rt + lr][k0 + 16 + 4 * lg]);
+          av0[0] = p0.x; av0[1] = p0.y; av0[2] = p0.z; av0[3] = p0.w;
+          av1[0] = p1.x; av1[1] = p1.y; av1[2] = p1.z; av1[3] = p1.w;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          acc0 = mma_f32(av0[j], xs[w][k0 + 4 * lg + j][lr], acc0);
+          acc1 = mma_f32(av1[j], xs[w][k0 + 16 + 4 * lg + j][lr], acc1);
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float yv = hy ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(yr, xoff, 4 * DP * (16 * rt + e), 0)) : 0.f;
+        x[rt][e] = acc0[e] + acc1[e] + yv;
+      }
+    }
+    __syncthreads();   // ph is restaged by the next step
+  }
+  const bool final_seg = INC ? z == a.G - 1 : z == 0;
+  if (a.last_mode == 1 || (a.last_mode == 2 && final_seg)) {
+#pragma unroll
+    for (int rt = 0; rt < DP / 16; ++rt) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = 16 * rt + 4 * lg + e;
+        if (a.last_mode == 1) a.last[((long)bh * a.G + z) * DP * DP + (long)row * DP + col] = x[rt][e];
+        else if (row < a.D && col < a.D) a.last[((long)bh * a.D + row) * a.D + col] = x[rt][e];
+      }
+    }
+  }
+}
+
+// Segments of a head's NT chunks for the segmented scans: up to 16 of at least 8 chunks.
+inline void sscan_segments(int NT, int& G, int& CPS) {
+  G = NT / 8 < 16 ? NT / 8 : 16;
+  if (G < 1) G = 1;
+  CPS = (NT + G - 1) / G;
+  G = (NT + CPS - 1) / CPS;
+}
+
+// One scan (TR, INC as above) by the three launches; seg: 3 x [BH][G][DP][DP] floats.
+template <bool TR, bool INC>
+hipError_t launch_sscan(const float* phi, const float* y, int BH, int NT, const float* init, int D, float* out,
+                        float* last, float* seg, hipStream_t st) {
+  int G, CPS;
+  sscan_segments(NT, G, CPS);
+  const size_t segsz = (size_t)BH * G * DP * DP;
+  float* smap = seg;               // the segments' composed maps (from I, no Y)
+  float* soff = seg + segsz;       // their offsets (from 0, with Y)
+  float* sin = seg + 2 * segsz;    // the segments' entering states
+  const dim3 gs(G, BH), g1(1, BH);
+  SScanArgs a{};
+  a.phi = phi; a.NP = NT; a.CPS = CPS; a.G = G; a.D = D;
+  // 1. composed maps and offsets
+  a.y = nullptr; a.init_mode = 1; a.init = nullptr; a.out = nullptr; a.last_mode = 1; a.last = smap;
+  sscan_kernel<TR, INC><<<gs, 512, 0, st>>>(a);
+  a.y = y; a.init_mode = 0; a.last = soff;
+  sscan_kernel<TR, INC><<<gs, 512, 0, st>>>(a);
+  // 2. the segment-level scan: entering states (the composed maps apply as they are)
+  SScanArgs b{};
+  b.phi = smap; b.y = soff; b.NP = G; b.CPS = G; b.G = 1; b.D = D;
+  b.init_mode = init != nullptr ? 3 : 0; b.init = init; b.out = sin; b.last_mode = 0;
+  sscan_kernel<false, INC><<<g1, 512, 0, st>>>(b);
+  // 3. every segment from its entering state, x before each chunk
+  a.y = y; a.init_mode = 2; a.init = sin; a.out = out; a.last_mode = last != nullptr ? 2 : 0; a.last = last;
+  sscan_kernel<TR, INC><<<gs, 512, 0, st>>>(a);
+  return hipGetLastError();
+}
+
 struct BwdWs {
-  float *W, *U, *X1, *A, *lgd, *Phi, *PmY2, *Hs, *Gend, *scr;
+  float *W, *U, *X1, *A, *lgd, *Phi, *PmY2, *Hs, *Gend, *seg, *scr;
 };
 
 size_t bwd_scr_floats(size_t M) { return L * M + 4 * M * DP + 3 * M * M; }
@@ -692,6 +790,7 @@ BwdWs bwd_ws(void* base, int B, int T, int H, int sp) {
   w.PmY2 = (float*)p; p = al(p + 4 * BH * NT * DP * DP);
   w.Hs = (float*)p; p = al(p + 4 * BH * NT * DP * DP);
   w.Gend = (float*)p; p = al(p + 4 * BH * NT * DP * DP);
+  w.seg = (float*)p; p = al(p + 4 * 3 * BH * 16 * DP * DP);   // the segmented scans' maps and states (G <= 16)
   w.scr = (float*)p;
   return w;
 }
@@ -700,12 +799,15 @@ template <typename X, bool SP>
 hipError_t launch_bwd_t(const ChunkBwdArgs& a, const BwdWs& w, hipStream_t st) {
   const int NT = (a.f.T + L - 1) / L;
   const int BH = a.f.B * a.f.H;
-  const dim3 chunks(NT, BH), slices(DP / 16, BH);
+  const dim3 chunks(NT, BH);
   chunk_bwd_maps_kernel<X, SP><<<chunks, 64 * GW, 0, st>>>(a, w.W, w.U, w.lgd, w.Phi, w.PmY2, NT);
-  chunk_bwd_scan_kernel<true><<<slices, 256, 0, st>>>(w.Phi, w.PmY2, a.f.initial_state, a.f.D, w.Hs, nullptr, NT);
+  if (hipError_t e = launch_sscan<false, true>(w.Phi, w.PmY2, BH, NT, a.f.initial_state, a.f.D, w.Hs, nullptr,
+                                                 w.seg, st))
+    return e;
   chunk_bwd_pre_kernel<X, SP><<<chunks, 64 * GW, 0, st>>>(a, w.W, w.lgd, w.X1, w.PmY2, NT);
-  chunk_bwd_scan_kernel<false><<<slices, 256, 0, st>>>(w.Phi, w.PmY2, a.d_final_state, a.f.D, w.Gend,
-                                                       a.d_initial_state, NT);
+  if (hipError_t e = launch_sscan<true, false>(w.Phi, w.PmY2, BH, NT, a.d_final_state, a.f.D, w.Gend,
+                                                 a.d_initial_state, w.seg, st))
+    return e;
   chunk_bwd_grad_kernel<X, SP><<<chunks, 64 * GW, 0, st>>>(a, w.W, w.U, w.X1, w.Hs, w.lgd, w.A, w.Gend, w.scr, NT);
   return hipGetLastError();
 }
@@ -715,7 +817,7 @@ hipError_t launch_bwd_t(const ChunkBwdArgs& a, const BwdWs& w, hipStream_t st) {
 size_t chunk_bwd_workspace_bytes(int B, int T, int H, int has_sparse) {
   const size_t NT = (T + L - 1) / L, M = has_sparse ? 2 * L : L, BH = (size_t)B * H;
   const size_t per = 4 * (3 * M * DP + M * M + L + 4 * DP * DP + bwd_scr_floats(M));
-  return BH * NT * per + 256 * 12;
+  return BH * NT * per + 4 * 3 * BH * 16 * DP * DP + 256 * 13;
 }
 
 hipError_t launch_chunk_bwd(const ChunkBwdArgs& a, hipStream_t st) {
