@@ -722,17 +722,21 @@ __global__ __launch_bounds__(256, 2) void gather_thr_kernel(GatherArgs a, const 
   // acc >= the[mt] decides; only the weights depend on it.
   auto chunk = [&](bool fast, const uint16_t* Kc, const uint16_t* Vc, int sp, int t0, const float (&the)[2])
       __attribute__((always_inline)) {
-    // scores and weights one half (16 keys) at a time: A operand rows
-    // 32 sp + 16 hf + lr of the tile, the weights of keys 8 lg + 4 hf + i
+    // scores of both halves (16 keys each) first, then the weights of each: a half's
+    // weights read accumulators that finished while the other half's products ran.
+    // A operand rows 32 sp + 16 hf + lr of the tile; the weights of keys 8 lg + 4 hf + i
     uint32_t pw[2][4];
-    auto half = [&](int hf) __attribute__((always_inline)) {
-      f4 sc[2] = {f4_zero(), f4_zero()};
+    f4 sc[2][2] = {{f4_zero(), f4_zero()}, {f4_zero(), f4_zero()}};
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         const uint4 kf = *reinterpret_cast<const uint4*>(&Kc[(32 * sp + 16 * hf) * RP + s_off + 32 * s]);
-        sc[0] = mma_bf16(as_bf8(kf), qf[0][s], sc[0]);
-        sc[1] = mma_bf16(as_bf8(kf), qf[1][s], sc[1]);
+        sc[hf][0] = mma_bf16(as_bf8(kf), qf[0][s], sc[hf][0]);
+        sc[hf][1] = mma_bf16(as_bf8(kf), qf[1][s], sc[hf][1]);
       }
+    }
+    auto half = [&](int hf) __attribute__((always_inline)) {
       auto weights = [&](auto fast_t) __attribute__((always_inline)) {
         constexpr bool FAST = decltype(fast_t)::value;
 #pragma unroll
@@ -740,7 +744,7 @@ __global__ __launch_bounds__(256, 2) void gather_thr_kernel(GatherArgs a, const 
           float p[4];
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const float c = sc[mt][i];
+            const float c = sc[hf][mt][i];
             bool sel;
             if constexpr (FAST) {
               sel = c >= the[mt];
