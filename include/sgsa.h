@@ -543,6 +543,74 @@ int sgsa_layer_retrieve_stats(int dtype, int B, int T, int H, int D, int top_k,
                               void* write_key, void* v_hat, float* alpha, float* row_stats,
                               void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---- hybrid decoder: one decode step of the whole layer stack -----------------
+ * HybridForCausalLM.decode_step's layer loop (the reference's hybrid stack,
+ * modelings/hybrid_dense_delta_topk.py:394-437, one greedy decode token per
+ * sequence, :510-532) in one host call, so that a step costs one call rather
+ * than several hundred Python dispatches.  Each layer runs the same launches,
+ * in the same order, as sgsa_amd.hybrid's per-layer decode:
+ *   SGSA layer (kind 0; SGSABlock, modeling_sgsa.py:660-709, with the
+ *   recurrent backend and top-k reuse): RMSNorm, the fused projection
+ *   q|k|v|q_ret|beta|gamma|budget (sgsa_linear_rows), sgsa_decode_split (the
+ *   k, v cache row at pos), the selection (sgsa_score_topk over cache rows
+ *   [0, pos], written to cand_idx / cand_cnt) when select != 0, else the
+ *   re-score of the kept candidates (sgsa_score_at), sgsa_sparse_gather (the
+ *   write key, v_hat, alpha), sgsa_recurrent_fwd (state updated in place),
+ *   then the shell;
+ *   dense layer (kind 1; :195-244): RMSNorm, the fused q|k|v projection, RoPE
+ *   of q and k at position pos with k and v written to cache row pos
+ *   (sgsa_rope_qk's arithmetic), sgsa_decode_attention over cache rows
+ *   [0, pos], then the shell;
+ *   shell: o projection, the residual add and second RMSNorm
+ *   (sgsa_add_rms_norm), the gated MLP (the gate/up projection with
+ *   sgsa_silu_mul's silu(gate) * up in its epilogue, the down projection with
+ *   the residual add in its epilogue).
+ * h [B, C] bf16 is the residual stream, updated in place.  All tensors bf16
+ * except state (fp32), the rope tables (fp32 [rope_len, D]) and the norm
+ * weights (bf16, or fp32 with norm_w_f32 = 1).  Weights are row-major
+ * [out, in]: w_in [4HD + 3H, C] (SGSA) or [(H + 2Hkv) D, C] (dense), w_o
+ * [C, HD], w_gu [2I, C] with gate and up rows interleaved in groups of 8
+ * (rows 16b .. 16b + 7 = gate rows 8b .. 8b + 7, rows 16b + 8 .. 16b + 15 =
+ * up rows 8b .. 8b + 7), w_down [C, I]; biases
+ * [out] or NULL (w_gu and w_down take none).  Caches: SGSA k/v [B, cache_len,
+ * H, D], dense k/v [B, Hkv, cache_len, D], contiguous; cand_idx [B, H, top_k]
+ * int32, cand_cnt [B, H] int32.  Limits: B <= 16, D = 128, C, HD and I
+ * multiples of 32, H / Hkv in {1, 2, 4, 8}, top_k <= pos + 1 <= cache_len
+ * (the candidate rows hold top_k slots), rope_len > pos; select must be set
+ * on a layer stack's first step (there are no candidates to re-score).
+ * Workspace: sgsa_decode_stack_workspace_size() bytes, 256-byte aligned. */
+typedef struct SgsaDecodeConfig {
+  int B, C, H, Hkv, D, I;
+  int top_k, write_mode;      /* write_mode 0 direct, 1 residual */
+  float alpha_max, tau_c, eps;
+  int norm_w_f32;
+  long cache_len;
+  const float* rope_cos;      /* dense layers: [rope_len, D] */
+  const float* rope_sin;
+  int rope_len;
+} SgsaDecodeConfig;
+
+typedef struct SgsaDecodeLayer {
+  int kind;                   /* 0 SGSA, 1 dense */
+  const void* input_norm;
+  const void* post_norm;
+  const void* w_in;
+  const void* b_in;
+  const void* w_o;
+  const void* b_o;
+  const void* w_gu;
+  const void* w_down;
+  void* k_cache;
+  void* v_cache;
+  float* state;               /* SGSA */
+  int32_t* cand_idx;          /* SGSA */
+  int32_t* cand_cnt;          /* SGSA */
+} SgsaDecodeLayer;
+
+int sgsa_decode_stack_workspace_size(const SgsaDecodeConfig* cfg, size_t* bytes);
+int sgsa_decode_stack(const SgsaDecodeConfig* cfg, int n_layers, const SgsaDecodeLayer* layers, void* h, int pos,
+                      int select, void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

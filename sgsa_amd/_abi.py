@@ -104,6 +104,24 @@ SIGNATURES = {
     "sgsa_layer_retrieve": (_I, [_I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _F, _F, _P, _P, _P, _P, _SZ, _P]),
 }
 
+class SgsaDecodeConfig(ctypes.Structure):
+    """struct SgsaDecodeConfig of include/sgsa.h."""
+    _fields_ = [("B", _I), ("C", _I), ("H", _I), ("Hkv", _I), ("D", _I), ("I", _I), ("top_k", _I),
+                ("write_mode", _I), ("alpha_max", _F), ("tau_c", _F), ("eps", _F), ("norm_w_f32", _I),
+                ("cache_len", ctypes.c_long), ("rope_cos", _P), ("rope_sin", _P), ("rope_len", _I)]
+
+
+class SgsaDecodeLayer(ctypes.Structure):
+    """struct SgsaDecodeLayer of include/sgsa.h."""
+    _fields_ = [("kind", _I), ("input_norm", _P), ("post_norm", _P), ("w_in", _P), ("b_in", _P), ("w_o", _P),
+                ("b_o", _P), ("w_gu", _P), ("w_down", _P), ("k_cache", _P), ("v_cache", _P), ("state", _P),
+                ("cand_idx", _P), ("cand_cnt", _P)]
+
+
+SIGNATURES["sgsa_decode_stack_workspace_size"] = (_I, [ctypes.POINTER(SgsaDecodeConfig), ctypes.POINTER(_SZ)])
+SIGNATURES["sgsa_decode_stack"] = (_I, [ctypes.POINTER(SgsaDecodeConfig), _I, ctypes.POINTER(SgsaDecodeLayer), _P, _I,
+                                        _I, _P, _SZ, _P])
+
 _lib: Optional[ctypes.CDLL] = None
 
 

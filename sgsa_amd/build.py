@@ -19,7 +19,7 @@ ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libsgsa_hip.so")
-SOURCES = ["api.hip", "chunk.hip", "chunk_bf16.hip", "topk.hip", "gather.hip", "gather_tile.hip", "recurrent.hip", "block.hip", "topk_rows.hip", "norm.hip", "mask.hip", "chunk_bwd.hip", "decode_attn.hip", "small_gemm.hip"]
+SOURCES = ["api.hip", "chunk.hip", "chunk_bf16.hip", "topk.hip", "gather.hip", "gather_tile.hip", "recurrent.hip", "block.hip", "topk_rows.hip", "norm.hip", "mask.hip", "chunk_bwd.hip", "decode_attn.hip", "small_gemm.hip", "decode_stack.hip"]
 ARCH = os.environ.get("SGSA_OFFLOAD_ARCH", "gfx950")
 
 

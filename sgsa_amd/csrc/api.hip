@@ -101,6 +101,18 @@ const char* sgsa_status_string(int status) {
 
 const char* sgsa_last_error(void) { return g_last_error.c_str(); }
 
+}  // extern "C"
+
+namespace sgsa {
+// The last-error hook for entry points defined in other translation units.
+int abi_set_error(int status, const char* msg) {
+  g_last_error = msg;
+  return status;
+}
+}  // namespace sgsa
+
+extern "C" {
+
 int sgsa_chunk_fwd_workspace_size(int B, int T, int H, int D, int has_sparse, size_t* bytes) {
   REQUIRE(bytes);
   if (int s = check_dims(B, T, H, D)) return s;

@@ -250,11 +250,29 @@ hipError_t launch_rms_norm(int dtype, int w_f32, long rows, int C, const void* x
 hipError_t launch_add_rms_norm(int dtype, int w_f32, long rows, int C, const void* a, const void* b, void* sum,
                                const void* w, float eps, void* y, hipStream_t st);
 hipError_t launch_silu_mul(int dtype, const void* src, long stride, long rows, int I, void* y, hipStream_t st);
+// y = x W^T (+ bias) on <= 16 bf16 rows (small_gemm.hip); with res, y = that rounded to bf16 plus res
+// [M, N] (row stride rs), rounded again: a residual add after the product.
 hipError_t launch_small_gemm(const void* x, long xs, const void* W, const void* bias, int M, int N, int K, void* y,
-                             long ys, hipStream_t st);
-// RoPE of a dense layer's q and k from the fused projection rows (norm.hip).
+                             long ys, hipStream_t st, const void* res = nullptr, long rs = 0);
+// The SGSA decode projection's outputs (launch_small_gemm_split): bf16 q, k, v, q_ret [M, HD], the k and
+// v rows of cache row pos ([M, cache_len, HD]) and the fp32 gates [M, H], as launch_decode_split writes them.
+struct SgSplit {
+  uint16_t *q, *k, *v, *qr;
+  float *beta, *gamma, *budget;
+  uint16_t *kc, *vc;
+  long cache_len, pos, HD;
+  int H;
+};
+hipError_t launch_small_gemm_split(const void* x, long xs, const void* W, const void* bias, int M, int N, int K,
+                                   const SgSplit& sp, hipStream_t st);
+// y [M, N / 2] = silu(gate) * up from a projection whose W rows interleave gate and up in groups of 8.
+hipError_t launch_small_gemm_swiglu(const void* x, long xs, const void* W, int M, int N, int K, void* y, long ys,
+                                    hipStream_t st);
+// RoPE of a dense layer's q and k from the fused projection rows (norm.hip); k (and, with vo, the
+// unrotated v heads after it) to rows koff .. of a [B, Hk, klen, D] buffer (klen < 0: T).
 hipError_t launch_rope_qk(int dtype, const void* src, long stride, int B, int T, int Hq, int Hk, int D, int pos0,
-                          const float* cosv, const float* sinv, void* qo, void* ko, hipStream_t st);
+                          const float* cosv, const float* sinv, void* qo, void* ko, hipStream_t st, long klen = -1,
+                          long koff = 0, void* vo = nullptr);
 // The SGSA layer's gates from the logit groups of a projection row (norm.hip).
 hipError_t launch_gates(int dtype, const void* src, long stride, long rows, int H, float* beta, float* gamma,
                         float* budget, hipStream_t st);

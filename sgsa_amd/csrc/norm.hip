@@ -16,17 +16,57 @@
 
 namespace sgsa {
 
+__device__ __forceinline__ float round_to(float v, float) { return v; }
+__device__ __forceinline__ float round_to(float v, bf16_t) { return bf16_to_f32(f32_to_bf16(v)); }
+
 // One workgroup of 256 threads per row.  ADD: the row is first a + b, rounded
-// to X and stored to sum (the residual add before the norm); each thread reads
-// back only the elements it stored.
-template <typename X, typename W, bool ADD = false>
+// to X and stored to sum (the residual add before the norm).  NE > 0: thread t
+// holds its elements t, t + 256, ... (at most NE of them, C <= 256 NE) and
+// their weights in registers, loaded before the reduction; NE = 0 walks the row
+// twice.  Both forms sum the squares in the same order and round alike.
+template <typename X, typename W, bool ADD = false, int NE = 0>
 __global__ __launch_bounds__(256) void rms_norm_kernel(const X* __restrict__ x, const W* __restrict__ w, int C,
                                                        float eps, X* __restrict__ y, const X* __restrict__ b = nullptr,
                                                        X* __restrict__ sum = nullptr) {
   __shared__ float part[4];
   const long row = blockIdx.x;
   const X* xr = x + row * C;
+  X* yr = y + row * C;
   float ss = 0.f;
+  if constexpr (NE > 0) {
+    float v[NE], wv[NE];
+    const X tag{};
+#pragma unroll
+    for (int j = 0; j < NE; ++j) {
+      const int c = threadIdx.x + 256 * j;
+      v[j] = 0.f;
+      wv[j] = 0.f;
+      if (c < C) {
+        v[j] = ld(xr, c);
+        if constexpr (ADD) v[j] = round_to(v[j] + ld(b + row * C, c), tag);
+        wv[j] = ld(w, c);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NE; ++j) {
+      const int c = threadIdx.x + 256 * j;
+      if (c < C) {
+        if constexpr (ADD) st(sum + row * C, c, v[j]);
+        ss = fmaf(v[j], v[j], ss);
+      }
+    }
+    ss = wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float mean = (part[0] + part[1] + part[2] + part[3]) / (float)C;
+    const float r = 1.0f / sqrtf(mean + eps);
+#pragma unroll
+    for (int j = 0; j < NE; ++j) {
+      const int c = threadIdx.x + 256 * j;
+      if (c < C) st(yr, c, v[j] * r * wv[j]);
+    }
+    return;
+  }
   if constexpr (ADD) {
     const X* br = b + row * C;
     X* sr = sum + row * C;
@@ -47,8 +87,18 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const X* __restrict__ x, 
   __syncthreads();
   const float mean = (part[0] + part[1] + part[2] + part[3]) / (float)C;
   const float r = 1.0f / sqrtf(mean + eps);
-  X* yr = y + row * C;
   for (int c = threadIdx.x; c < C; c += 256) st(yr, c, ld(xr, c) * r * ld(w, c));
+}
+
+// The row form for C: registers for C <= 4096, else the two walks.
+template <typename X, typename W, bool ADD>
+hipError_t launch_norm_rows(long rows, int C, const X* x, const W* w, float eps, X* y, const X* b, X* sum,
+                            hipStream_t st) {
+  const dim3 grid((unsigned)rows);
+  if (C <= 256 * 8) rms_norm_kernel<X, W, ADD, 8><<<grid, 256, 0, st>>>(x, w, C, eps, y, b, sum);
+  else if (C <= 256 * 16) rms_norm_kernel<X, W, ADD, 16><<<grid, 256, 0, st>>>(x, w, C, eps, y, b, sum);
+  else rms_norm_kernel<X, W, ADD, 0><<<grid, 256, 0, st>>>(x, w, C, eps, y, b, sum);
+  return hipGetLastError();
 }
 
 // One thread per (row, head).  Row r's logits start at src + r * stride: beta's
@@ -131,25 +181,31 @@ hipError_t launch_decode_split(int dtype, const void* src, long stride, int B, i
 }
 
 // One thread per output element.  Row (b, t) of the projection output starts at
-// src + (b T + t) stride: q's Hq heads of D, then k's Hk heads.
-__device__ __forceinline__ float round_to(float v, float) { return v; }
-__device__ __forceinline__ float round_to(float v, bf16_t) { return bf16_to_f32(f32_to_bf16(v)); }
+// src + (b T + t) stride: q's Hq heads of D, then k's Hk heads (then, when vo is
+// given, v's Hk heads, copied unrotated).  q goes to qo [B, Hq, T, D]; k (and v)
+// to row koff + t of a [B, Hk, klen, D] buffer: the k_out tensor itself (klen =
+// T, koff = 0) or a decode step's cache (klen = cache_len, koff = pos).
 
 template <typename X>
 __global__ __launch_bounds__(256) void rope_qk_kernel(const X* __restrict__ src, long stride, int B, int T, int Hq,
                                                       int Hk, int D, int pos0, const float* __restrict__ cosv,
                                                       const float* __restrict__ sinv, X* __restrict__ qo,
-                                                      X* __restrict__ ko) {
+                                                      X* __restrict__ ko, long klen, long koff, X* __restrict__ vo) {
 #pragma clang fp contract(off)
-  const long n = (long)B * T * (Hq + Hk) * D;
+  const int nh = Hq + Hk + (vo != nullptr ? Hk : 0);
+  const long n = (long)B * T * nh * D;
   const long i = (long)blockIdx.x * 256 + threadIdx.x;
   if (i >= n) return;
   const int d = (int)(i % D);
   const long r = i / D;
-  const int hh = (int)(r % (Hq + Hk));
-  const long bt = r / (Hq + Hk);
+  const int hh = (int)(r % nh);
+  const long bt = r / nh;
   const int t = (int)(bt % T), b = (int)(bt / T);
   const X* xr = src + bt * stride + (long)hh * D;
+  if (hh >= Hq + Hk) {   // v: copied as it is
+    vo[(((long)b * Hk + (hh - Hq - Hk)) * klen + koff + t) * D + d] = xr[d];
+    return;
+  }
   const int half = D / 2;
   const float x = ld(xr, d);
   const float xr_ = d < half ? -ld(xr, d + half) : ld(xr, d - half);
@@ -158,36 +214,34 @@ __global__ __launch_bounds__(256) void rope_qk_kernel(const X* __restrict__ src,
   const float s = round_to(sinv[(long)(pos0 + t) * D + d], tag);
   const float y = round_to(round_to(x * c, tag) + round_to(xr_ * s, tag), tag);
   if (hh < Hq) st(qo, (((long)b * Hq + hh) * T + t) * D + d, y);
-  else st(ko, (((long)b * Hk + (hh - Hq)) * T + t) * D + d, y);
+  else st(ko, (((long)b * Hk + (hh - Hq)) * klen + koff + t) * D + d, y);
 }
 
 hipError_t launch_rope_qk(int dtype, const void* src, long stride, int B, int T, int Hq, int Hk, int D, int pos0,
-                          const float* cosv, const float* sinv, void* qo, void* ko, hipStream_t st) {
-  const long n = (long)B * T * (Hq + Hk) * D;
+                          const float* cosv, const float* sinv, void* qo, void* ko, hipStream_t st, long klen,
+                          long koff, void* vo) {
+  if (klen < 0) klen = T;
+  const long n = (long)B * T * (Hq + Hk + (vo != nullptr ? Hk : 0)) * D;
   const dim3 grid((unsigned)((n + 255) / 256));
   if (dtype == DT_F32)
     rope_qk_kernel<float><<<grid, 256, 0, st>>>((const float*)src, stride, B, T, Hq, Hk, D, pos0, cosv, sinv,
-                                                (float*)qo, (float*)ko);
+                                                (float*)qo, (float*)ko, klen, koff, (float*)vo);
   else
     rope_qk_kernel<bf16_t><<<grid, 256, 0, st>>>((const bf16_t*)src, stride, B, T, Hq, Hk, D, pos0, cosv, sinv,
-                                                 (bf16_t*)qo, (bf16_t*)ko);
+                                                 (bf16_t*)qo, (bf16_t*)ko, klen, koff, (bf16_t*)vo);
   return hipGetLastError();
 }
 
 hipError_t launch_add_rms_norm(int dtype, int w_f32, long rows, int C, const void* a, const void* b, void* sum,
                                const void* w, float eps, void* y, hipStream_t st) {
-  const dim3 grid((unsigned)rows);
-  if (dtype == DT_F32) {
-    rms_norm_kernel<float, float, true><<<grid, 256, 0, st>>>((const float*)a, (const float*)w, C, eps, (float*)y,
-                                                              (const float*)b, (float*)sum);
-  } else if (w_f32) {
-    rms_norm_kernel<bf16_t, float, true><<<grid, 256, 0, st>>>((const bf16_t*)a, (const float*)w, C, eps,
-                                                               (bf16_t*)y, (const bf16_t*)b, (bf16_t*)sum);
-  } else {
-    rms_norm_kernel<bf16_t, bf16_t, true><<<grid, 256, 0, st>>>((const bf16_t*)a, (const bf16_t*)w, C, eps,
-                                                                (bf16_t*)y, (const bf16_t*)b, (bf16_t*)sum);
-  }
-  return hipGetLastError();
+  if (dtype == DT_F32)
+    return launch_norm_rows<float, float, true>(rows, C, (const float*)a, (const float*)w, eps, (float*)y,
+                                                (const float*)b, (float*)sum, st);
+  if (w_f32)
+    return launch_norm_rows<bf16_t, float, true>(rows, C, (const bf16_t*)a, (const float*)w, eps, (bf16_t*)y,
+                                                 (const bf16_t*)b, (bf16_t*)sum, st);
+  return launch_norm_rows<bf16_t, bf16_t, true>(rows, C, (const bf16_t*)a, (const bf16_t*)w, eps, (bf16_t*)y,
+                                                (const bf16_t*)b, (bf16_t*)sum, st);
 }
 
 // silu(gate) * up of a fused gate | up projection row, in X's roundings: silu
@@ -213,15 +267,14 @@ hipError_t launch_silu_mul(int dtype, const void* src, long stride, long rows, i
 
 hipError_t launch_rms_norm(int dtype, int w_f32, long rows, int C, const void* x, const void* w, float eps, void* y,
                            hipStream_t st) {
-  const dim3 grid((unsigned)rows);
-  if (dtype == DT_F32) {
-    rms_norm_kernel<float, float><<<grid, 256, 0, st>>>((const float*)x, (const float*)w, C, eps, (float*)y);
-  } else if (w_f32) {
-    rms_norm_kernel<bf16_t, float><<<grid, 256, 0, st>>>((const bf16_t*)x, (const float*)w, C, eps, (bf16_t*)y);
-  } else {
-    rms_norm_kernel<bf16_t, bf16_t><<<grid, 256, 0, st>>>((const bf16_t*)x, (const bf16_t*)w, C, eps, (bf16_t*)y);
-  }
-  return hipGetLastError();
+  if (dtype == DT_F32)
+    return launch_norm_rows<float, float, false>(rows, C, (const float*)x, (const float*)w, eps, (float*)y, nullptr,
+                                                 nullptr, st);
+  if (w_f32)
+    return launch_norm_rows<bf16_t, float, false>(rows, C, (const bf16_t*)x, (const float*)w, eps, (bf16_t*)y,
+                                                  nullptr, nullptr, st);
+  return launch_norm_rows<bf16_t, bf16_t, false>(rows, C, (const bf16_t*)x, (const bf16_t*)w, eps, (bf16_t*)y,
+                                                 nullptr, nullptr, st);
 }
 
 }  // namespace sgsa

@@ -2,11 +2,33 @@
 // (nn.Linear at B <= 16 tokens), where a library GEMM's host dispatch costs
 // more than the kernel.  bf16 in, fp32 accumulation, bf16 out.
 //
-// One workgroup per 16 output columns, its eight waves splitting K in eight
-// interleaved ranges of 32-element steps; each wave runs
-// v_mfma_f32_16x16x32_bf16 with the x rows (zero past M) as the A operand and
-// 16 weight rows as the B operand, both loaded from global memory straight
-// into registers, four steps ahead.  The waves' 16x16 tiles meet in LDS.
+// The product reads W once and is bound by that read (N K bf16).  One
+// workgroup per 16 output columns, its 16 waves splitting K in interleaved
+// 32-element steps: wave w takes steps w, w + 16, ...  Each wave issues the
+// loads of up to D steps (W rows and the x rows, straight into registers)
+// before the first product, so a workgroup pays about one memory latency per
+// D steps rather than one per step; steps past K re-read the last step with
+// the x operand zeroed, which keeps the loads free of branches.  (Measured at
+// the decode shapes: 16 waves with every load in one batch beat 8 waves with
+// one batch and 8 waves with two batches at twice the occupancy.)  The
+// products run on v_mfma_f32_16x16x32_bf16 (A operand: the x rows, zero past
+// M; B operand: 16 rows of W), and the 16 waves' partial 16x16 tiles meet in
+// LDS, where 256 threads sum one output element each and apply the epilogue:
+//   plain     y = bf16(acc + bias), then with a residual operand
+//             bf16(y + res) (the model's h + mlp(x), as two bf16 tensor ops
+//             compute it);
+//   split     the SGSA decode projection's row q | k | v | q_ret | b | g | u
+//             routed as sgsa_decode_split routes it: the bf16 values to the
+//             contiguous q, k, v, q_ret and to cache row pos, the gates
+//             beta = max(sigmoid(b), 1e-4), gamma = sigmoid(g), budget = u in
+//             fp32 from the bf16 logits;
+//   swiglu    W's rows interleaved in groups of 8 (gate rows 8b .. 8b + 7,
+//             then the up rows 8b .. 8b + 7), so a workgroup's 16 columns
+//             hold 8 gate and the matching 8 up values; it writes
+//             bf16(bf16(silu(gate)) * up) for those 8 columns of y [M, N / 2]
+//             (sgsa_silu_mul's roundings on the bf16 projection values).
+
+#include <math.h>
 
 #include "common.h"
 #include "kernels.h"
@@ -16,72 +38,117 @@ namespace {
 
 typedef uint16_t sg_u16x8 __attribute__((ext_vector_type(8)));
 
-constexpr int SG_W = 8;   // waves per workgroup
+constexpr int SG_W = 16;   // waves per workgroup
 
-__global__ __launch_bounds__(64 * SG_W) void small_gemm_kernel(const bf16_t* __restrict__ x, long xs, const bf16_t* __restrict__ W,
-                                                         const bf16_t* __restrict__ bias, int M, int N, int K,
-                                                         bf16_t* __restrict__ y, long ys) {
+template <int D, int EPI>
+__global__ __launch_bounds__(64 * SG_W) void small_gemm_kernel(const bf16_t* __restrict__ x, long xs,
+                                                               const bf16_t* __restrict__ W,
+                                                               const bf16_t* __restrict__ bias, int M, int N, int K,
+                                                               bf16_t* __restrict__ y, long ys,
+                                                               const bf16_t* __restrict__ res, long rs, SgSplit sp) {
   __shared__ f4 red[SG_W][64];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int lr = lane & 15, lg = lane >> 4;
   const int n0 = blockIdx.x * 16;
   const int n = min(n0 + lr, N - 1);    // columns past N re-read the last row and are not stored
-  const int row = lr;                   // A operand row; rows >= M read row 0 and are zeroed
-  const bool live = row < M;
-  const uint16_t* xr = reinterpret_cast<const uint16_t*>(x) + (long)(live ? row : 0) * xs + 8 * lg;
+  const bool live = lr < M;             // A operand row lr; rows >= M read row 0 and are zeroed
+  const uint16_t* xr = reinterpret_cast<const uint16_t*>(x) + (long)(live ? lr : 0) * xs + 8 * lg;
   const uint16_t* wr = reinterpret_cast<const uint16_t*>(W) + (long)n * K + 8 * lg;
   const int nsteps = K / 32;
   f4 acc = f4_zero();
-  // wave w takes steps w, w + SG_W, ...
-  int s = w;
-  for (; s + 3 * SG_W < nsteps; s += 4 * SG_W) {
-    sg_u16x8 a[4], b[4];
+  for (int s0 = w; s0 < nsteps; s0 += SG_W * D) {
+    sg_u16x8 a[D], b[D];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      a[u] = *reinterpret_cast<const sg_u16x8*>(xr + 32 * (s + SG_W * u));
-      b[u] = *reinterpret_cast<const sg_u16x8*>(wr + 32 * (s + SG_W * u));
+    for (int u = 0; u < D; ++u) {
+      const int s = min(s0 + SG_W * u, nsteps - 1);
+      a[u] = *reinterpret_cast<const sg_u16x8*>(xr + 32 * s);
+      b[u] = *reinterpret_cast<const sg_u16x8*>(wr + 32 * s);
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const sg_u16x8 av = live ? a[u] : (sg_u16x8){0, 0, 0, 0, 0, 0, 0, 0};
+    for (int u = 0; u < D; ++u) {
+      const bool on = live && s0 + SG_W * u < nsteps;
+      const sg_u16x8 av = on ? a[u] : (sg_u16x8){0, 0, 0, 0, 0, 0, 0, 0};
       acc = mma_bf16(__builtin_bit_cast(bf16x8, av), __builtin_bit_cast(bf16x8, b[u]), acc);
     }
   }
-  for (; s < nsteps; s += SG_W) {
-    sg_u16x8 a = *reinterpret_cast<const sg_u16x8*>(xr + 32 * s);
-    const sg_u16x8 b = *reinterpret_cast<const sg_u16x8*>(wr + 32 * s);
-    if (!live) a = (sg_u16x8){0, 0, 0, 0, 0, 0, 0, 0};
-    acc = mma_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), acc);
-  }
   red[w][lane] = acc;
   __syncthreads();
-  if (w == 0) {
-    // acc element i of lane (lr, lg): output row 4 lg + i, column n0 + lr
-    f4 t = red[0][lane];
+  if (tid >= 256) return;
+  // output row r, column n0 + c: element r % 4 of lane c + 16 (r / 4) in every wave's tile
+  const int r = tid >> 4, c = tid & 15;
+  const int l = c + 16 * (r >> 2), e = r & 3;
+  float t = 0.f;
 #pragma unroll
-    for (int v = 1; v < SG_W; ++v) {
-      const f4 o = red[v][lane];
-      t[0] += o[0]; t[1] += o[1]; t[2] += o[2]; t[3] += o[3];
+  for (int v = 0; v < SG_W; ++v) t += red[v][l][e];
+  const int col = n0 + c;
+  const float bv = (bias != nullptr && col < N) ? bf16_to_f32(bias[col].bits) : 0.f;
+  const uint16_t o = f32_to_bf16(t + bv);
+  if constexpr (EPI == 2) {
+    // c < 8: gate column 8 blockIdx.x + c; its up value is column c + 8 of the same
+    // row, held by the lane 8 on (lanes 16 r' + c of one wave hold row r')
+    const float up = __shfl_down(bf16_to_f32(o), 8, 16);
+    if (c < 8 && r < M && col < N) {
+      const float g = bf16_to_f32(o);
+      const float sg = bf16_to_f32(f32_to_bf16(g / (1.0f + expf(-g))));
+      y[(long)r * ys + 8 * blockIdx.x + c].bits = f32_to_bf16(sg * up);
     }
-    const int col = n0 + lr;
-    if (col < N) {
-      const float bv = bias != nullptr ? bf16_to_f32(bias[col].bits) : 0.f;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = 4 * lg + i;
-        if (r < M) y[(long)r * ys + col].bits = f32_to_bf16(t[i] + bv);
-      }
+    return;
+  }
+  if (r >= M || col >= N) return;
+  if constexpr (EPI == 0) {
+    uint16_t ov = o;
+    if (res != nullptr) ov = f32_to_bf16(bf16_to_f32(o) + bf16_to_f32(res[(long)r * rs + col].bits));
+    y[(long)r * ys + col].bits = ov;
+  } else {
+    const long HD = sp.HD;
+    if (col < 4 * HD) {
+      const int grp = (int)(col / HD);
+      const long e2 = col % HD;
+      uint16_t* dst = grp == 0 ? sp.q : grp == 1 ? sp.k : grp == 2 ? sp.v : sp.qr;
+      dst[(long)r * HD + e2] = o;
+      if (grp == 1) sp.kc[((long)r * sp.cache_len + sp.pos) * HD + e2] = o;
+      if (grp == 2) sp.vc[((long)r * sp.cache_len + sp.pos) * HD + e2] = o;
+    } else {
+      const int j = (int)(col - 4 * HD), H = sp.H;
+      const float lv = bf16_to_f32(o);
+      if (j < H) sp.beta[(long)r * H + j] = fmaxf(1.0f / (1.0f + expf(-lv)), 1e-4f);
+      else if (j < 2 * H) sp.gamma[(long)r * H + j - H] = 1.0f / (1.0f + expf(-lv));
+      else sp.budget[(long)r * H + j - 2 * H] = lv;
     }
   }
+}
+
+template <int EPI>
+hipError_t launch_gemm(const void* x, long xs, const void* W, const void* bias, int M, int N, int K, void* y, long ys,
+                       hipStream_t st, const void* res, long rs, const SgSplit& sp) {
+  const dim3 grid((unsigned)((N + 15) / 16));
+  const int spw = (K / 32 + SG_W - 1) / SG_W;   // steps per wave
+  const bf16_t* xp = (const bf16_t*)x;
+  const bf16_t* wp = (const bf16_t*)W;
+  const bf16_t* bp = (const bf16_t*)bias;
+  const bf16_t* rp = (const bf16_t*)res;
+  bf16_t* yp = (bf16_t*)y;
+  if (spw <= 4) small_gemm_kernel<4, EPI><<<grid, 64 * SG_W, 0, st>>>(xp, xs, wp, bp, M, N, K, yp, ys, rp, rs, sp);
+  else if (spw <= 8) small_gemm_kernel<8, EPI><<<grid, 64 * SG_W, 0, st>>>(xp, xs, wp, bp, M, N, K, yp, ys, rp, rs, sp);
+  else small_gemm_kernel<11, EPI><<<grid, 64 * SG_W, 0, st>>>(xp, xs, wp, bp, M, N, K, yp, ys, rp, rs, sp);
+  return hipGetLastError();
 }
 
 }  // namespace
 
 hipError_t launch_small_gemm(const void* x, long xs, const void* W, const void* bias, int M, int N, int K, void* y,
-                             long ys, hipStream_t st) {
-  small_gemm_kernel<<<dim3((unsigned)((N + 15) / 16)), 64 * SG_W, 0, st>>>((const bf16_t*)x, xs, (const bf16_t*)W,
-                                                                     (const bf16_t*)bias, M, N, K, (bf16_t*)y, ys);
-  return hipGetLastError();
+                             long ys, hipStream_t st, const void* res, long rs) {
+  return launch_gemm<0>(x, xs, W, bias, M, N, K, y, ys, st, res, rs, SgSplit{});
+}
+
+hipError_t launch_small_gemm_split(const void* x, long xs, const void* W, const void* bias, int M, int N, int K,
+                                   const SgSplit& sp, hipStream_t st) {
+  return launch_gemm<1>(x, xs, W, bias, M, N, K, nullptr, 0, st, nullptr, 0, sp);
+}
+
+hipError_t launch_small_gemm_swiglu(const void* x, long xs, const void* W, int M, int N, int K, void* y, long ys,
+                                    hipStream_t st) {
+  return launch_gemm<2>(x, xs, W, nullptr, M, N, K, y, ys, st, nullptr, 0, SgSplit{});
 }
 
 }  // namespace sgsa

@@ -41,7 +41,7 @@ import torch.nn.functional as F
 from .decode import sgsa_decode_step
 from .layer import LayerWorkspace, sgsa_layer_forward
 from . import _abi
-from .model import GatedMLP, RMSNorm, SGSABlock, SGSAConfig, fused_linear, fused_linear_out, lin
+from .model import GatedMLP, RMSNorm, SGSABlock, SGSAConfig, fused_linear, fused_linear_out, fused_weight, lin
 from .retrieval import gather_masked, score_topk_masked
 
 Tensor = torch.Tensor
@@ -326,6 +326,8 @@ class HybridForCausalLM(nn.Module):
                 layer._ws = shared
         self.norm = RMSNorm(config.hidden_size, config.layer_norm_eps)
         self.lm_head = nn.Linear(config.hidden_size, config.vocab_size, bias=False)
+        # decode steps go through sgsa_decode_stack where it applies (False: always the per-layer path)
+        self.decode_stack = True
         if config.tie_word_embeddings:
             self.lm_head.weight = self.embed_tokens.weight
 
@@ -377,15 +379,122 @@ class HybridForCausalLM(nn.Module):
     def decode_step(self, tokens: Tensor, pos: int, step: int, caches: List[dict],
                     rope: Tuple[Tensor, Tensor]) -> Tensor:
         """tokens [B] at position pos, the step-th generated token; returns logits [B, V].
-        SGSA layers select their top-k when step % topk_recompute_every == 0."""
+        SGSA layers select their top-k when step % topk_recompute_every == 0.
+
+        Where the stack and its caches fit sgsa_decode_stack (bf16, head_dim 128, B <= 16,
+        contiguous caches, top_k <= pos + 1), the whole layer loop is that one call: the
+        same launches as the per-layer path below, without its Python dispatch.  That
+        call keeps its own candidate sets (it selects on its first step) and updates
+        the SGSA states in place."""
         select = step % self.config.topk_recompute_every == 0
         h = self.embed_tokens(tokens[:, None])
-        for layer, cache in zip(self.layers, caches):
-            if isinstance(layer, DenseGQABlock):
-                h = layer.forward_cached(h, pos, cache, rope)
-            else:
-                h = layer.decode(h, pos, cache, select)
+        plan = self._stack_plan(caches, rope, h, pos)
+        if plan is not None:
+            B, C = h.shape[0], h.shape[-1]
+            hb = h.view(B, C)
+            _abi.check(_abi.lib().sgsa_decode_stack(
+                ctypes.byref(plan["cfg"]), len(plan["layers"]), plan["layers"], _abi.ptr(hb), pos,
+                int(select or not plan["primed"]), ctypes.c_void_p(plan["ws_ptr"]), plan["ws_bytes"],
+                _abi.stream_of(hb)))
+            plan["primed"] = True
+        else:
+            for layer, cache in zip(self.layers, caches):
+                if isinstance(layer, DenseGQABlock):
+                    h = layer.forward_cached(h, pos, cache, rope)
+                else:
+                    h = layer.decode(h, pos, cache, select)
         return self._head(h)[:, 0]
+
+    def _stack_plan(self, caches: List[dict], rope: Tuple[Tensor, Tensor], h: Tensor, pos: int) -> Optional[dict]:
+        """sgsa_decode_stack's arguments for these caches (built on first use and kept while the
+        caches, states and parameters stay the same objects and versions), or None when the
+        stack does not fit it and the per-layer path runs."""
+        cfg = self.config
+        B = h.shape[0]
+        if not self.decode_stack or torch.is_grad_enabled() or not h.is_cuda or h.dtype != torch.bfloat16 or not h.is_contiguous() \
+                or B > 16 or cfg.head_dim != 128 or pos + 1 < cfg.top_k:
+            return None
+        state_key = tuple(id(c.get("state")) for c in caches)
+        pkey = tuple((id(p), p._version) for p in self.parameters())
+        plan = self.__dict__.get("_decode_plan")
+        if plan is not None and plan["caches"] is caches and plan["state_key"] == state_key \
+                and plan["pkey"] == pkey and plan["rope"] is rope and plan["B"] == B:
+            return plan
+        self.__dict__["_decode_plan"] = None
+        plan = self._build_stack_plan(caches, rope, B)
+        if plan is not None:
+            # a new plan selects on its first step; the per-layer path's candidate sets are
+            # dropped, so that it also selects afresh should it take over later
+            plan.update(caches=caches, state_key=state_key, pkey=pkey, rope=rope, B=B, primed=False)
+            for c in caches:
+                if "cand" in c:
+                    c["cand"] = None
+            self.__dict__["_decode_plan"] = plan
+        return plan
+
+    def _build_stack_plan(self, caches: List[dict], rope: Tuple[Tensor, Tensor], B: int) -> Optional[dict]:
+        cfg = self.config
+        C, H, Hkv, D, I = cfg.hidden_size, cfg.num_attention_heads, cfg.num_kv_heads, cfg.head_dim, \
+            cfg.intermediate_size
+        if C % 32 or I % 32 or H % Hkv or H // Hkv not in (1, 2, 4, 8) or cfg.sgsa_write_mode not in ("direct", "residual"):
+            return None
+        bf = torch.bfloat16
+        norms = [m.weight for l in self.layers for m in (l.input_norm, l.post_attn_norm)]
+        if any(w.dtype != norms[0].dtype or not w.is_contiguous() for w in norms) or norms[0].dtype not in (bf, torch.float32):
+            return None
+        T_max = caches[0]["k"].shape[1] if not self.config.is_dense(0) else caches[0]["k"].shape[2]
+
+        def ok(t, shape, dt=bf):
+            return t is not None and t.is_cuda and t.dtype == dt and t.is_contiguous() and tuple(t.shape) == shape
+
+        keep, layers = [], (_abi.SgsaDecodeLayer * len(self.layers))()
+        for i, (layer, cache) in enumerate(zip(self.layers, caches)):
+            dense = isinstance(layer, DenseGQABlock)
+            names = ("q_proj", "k_proj", "v_proj") if dense else SGSADecoderBlock._PROJ
+            w_in, b_in = fused_weight(layer, names)
+            w_gu, b_gu = fused_weight(layer.mlp, ("gate_proj", "up_proj"))
+            # gate and up rows interleaved in groups of 8 (the swiglu epilogue's layout)
+            w_gu = torch.stack([w_gu[:I].view(I // 8, 8, C), w_gu[I:].view(I // 8, 8, C)], 1).reshape(2 * I, C)
+            w_o, b_o, w_down = layer.o_proj.weight, layer.o_proj.bias, layer.mlp.down_proj.weight
+            if b_gu is not None or layer.mlp.down_proj.bias is not None:
+                return None
+            n_in = (H + 2 * Hkv) * D if dense else 4 * H * D + 3 * H
+            if not (ok(w_in, (n_in, C)) and ok(w_o, (C, H * D)) and ok(w_gu, (2 * I, C)) and ok(w_down, (C, I))
+                    and (b_in is None or ok(b_in, (n_in,))) and (b_o is None or ok(b_o, (C,)))):
+                return None
+            L = layers[i]
+            L.kind = 1 if dense else 0
+            L.input_norm, L.post_norm = layer.input_norm.weight.data_ptr(), layer.post_attn_norm.weight.data_ptr()
+            L.w_in, L.b_in = w_in.data_ptr(), (b_in.data_ptr() if b_in is not None else None)
+            L.w_o, L.b_o = w_o.data_ptr(), (b_o.data_ptr() if b_o is not None else None)
+            L.w_gu, L.w_down = w_gu.data_ptr(), w_down.data_ptr()
+            keep += [w_in, b_in, w_gu]
+            if dense:
+                if not (ok(cache["k"], (B, Hkv, T_max, D)) and ok(cache["v"], (B, Hkv, T_max, D))):
+                    return None
+            else:
+                st = cache.get("state")
+                if not (ok(cache["k"], (B, T_max, H, D)) and ok(cache["v"], (B, T_max, H, D))
+                        and ok(st, (B, H, D, D), torch.float32)):
+                    return None
+                idx = torch.zeros(B, H, cfg.top_k, device=st.device, dtype=torch.int32)
+                cnt = torch.zeros(B, H, device=st.device, dtype=torch.int32)
+                keep += [idx, cnt]
+                L.state, L.cand_idx, L.cand_cnt = st.data_ptr(), idx.data_ptr(), cnt.data_ptr()
+            L.k_cache, L.v_cache = cache["k"].data_ptr(), cache["v"].data_ptr()
+        cos, sin = rope[0].float().contiguous(), rope[1].float().contiguous()
+        keep += [cos, sin]
+        c = _abi.SgsaDecodeConfig(B=B, C=C, H=H, Hkv=Hkv, D=D, I=I, top_k=cfg.top_k,
+                                  write_mode=0 if cfg.sgsa_write_mode == "direct" else 1, alpha_max=cfg.alpha_max,
+                                  tau_c=cfg.tau_c, eps=self.layers[0].input_norm.eps,
+                                  norm_w_f32=int(norms[0].dtype == torch.float32), cache_len=T_max,
+                                  rope_cos=cos.data_ptr(), rope_sin=sin.data_ptr(), rope_len=cos.shape[0])
+        nb = ctypes.c_size_t()
+        _abi.check(_abi.lib().sgsa_decode_stack_workspace_size(ctypes.byref(c), ctypes.byref(nb)))
+        ws = torch.empty(nb.value + 256, device=caches[0]["k"].device, dtype=torch.uint8)
+        keep.append(ws)
+        return {"cfg": c, "layers": layers, "keep": keep, "ws_ptr": (ws.data_ptr() + 255) // 256 * 256,
+                "ws_bytes": nb.value}
 
 
 def expand_caches(caches: List[dict], B: int) -> List[dict]:

@@ -201,9 +201,10 @@ def fused_linear(module: nn.Module, x: Tensor, names) -> list:
     return list(torch.split(y, [l.out_features for l in lins], dim=-1))
 
 
-def fused_linear_out(module: nn.Module, x: Tensor, names) -> Tensor:
-    """The one GEMM of fused_linear (no autograd): the outputs of the nn.Linear children
-    ``names`` side by side along the last dimension of one contiguous tensor."""
+def fused_weight(module: nn.Module, names) -> Tuple[Tensor, Optional[Tensor]]:
+    """(weight, bias) of the nn.Linear children ``names`` of ``module`` concatenated along the
+    output dimension (bias None when none has one; zeros for those without), cached on the
+    module and rebuilt when any weight or bias changes (storage or in-place version)."""
     lins = [getattr(module, n) for n in names]
     key = tuple((l.weight.data_ptr(), l.weight._version,
                  None if l.bias is None else (l.bias.data_ptr(), l.bias._version)) for l in lins)
@@ -215,7 +216,14 @@ def fused_linear_out(module: nn.Module, x: Tensor, names) -> Tensor:
             b = torch.cat([l.bias if l.bias is not None else l.weight.new_zeros(l.out_features) for l in lins])
         cached = (key, w, b)
         module.__dict__["_fused_" + "_".join(names)] = cached
-    return linear_rows(x, cached[1], cached[2])
+    return cached[1], cached[2]
+
+
+def fused_linear_out(module: nn.Module, x: Tensor, names) -> Tensor:
+    """The one GEMM of fused_linear (no autograd): the outputs of the nn.Linear children
+    ``names`` side by side along the last dimension of one contiguous tensor."""
+    w, b = fused_weight(module, names)
+    return linear_rows(x, w, b)
 
 
 class GatedMLP(nn.Module):

@@ -7,7 +7,11 @@ selecting its top-2048 every 4 steps and re-scoring that set in between.
 
 The CPU oracle cannot run 24 layers over 16K tokens, so the full workload is
 checked through properties that do not depend on size:
-  * the logits are finite and a second run gives the same tokens and logits;
+  * the logits are finite, and a second run gives the same tokens and logits:
+    the first decodes layer by layer from Python (where the selections below are
+    recorded), the second through sgsa_decode_stack (the whole layer loop of a
+    step in one call), so this also shows the two paths equal bit for bit over
+    all 256 steps;
   * the 8 sequences start from one prompt and stay identical;
   * on selecting steps, the candidate set a layer keeps is exactly the row
     kernel's top-k (sgsa_score_topk) of that step's retrieval query over the
@@ -69,6 +73,7 @@ def config4(dev):
 
     HY.sgsa_decode_step = recording
     HY.SGSADecoderBlock.decode = decode
+    m.decode_stack = False   # the recorded run takes the per-layer path
     try:
         print(f"config 4: prefill T={T} at B=1, {STEPS} decode steps at B={B}", flush=True)
         with torch.no_grad():
@@ -90,6 +95,7 @@ def config4(dev):
     finally:
         HY.sgsa_decode_step = real
         HY.SGSADecoderBlock.decode = orig_decode
+        m.decode_stack = True
     return {"cfg": cfg, "m": m, "prompt": prompt, "logits": logits, "toks": torch.stack(toks, 1),
             "step_logits": step_logits, "rec": rec, "caches": caches}
 
@@ -102,11 +108,13 @@ def test_config4_finite_identical_sequences_and_deterministic(config4):
     toks = c["toks"]
     assert toks.shape == (B, STEPS)
     assert (toks == toks[0:1]).all(), "sequences decoded from one prompt diverged"
-    print("second run", flush=True)
+    print("second run (sgsa_decode_stack)", flush=True)
+    assert c["m"].decode_stack
     logits2, toks2 = HY.generate(c["m"], c["prompt"], steps=STEPS, batch=B)
     torch.cuda.synchronize()
+    assert c["m"].__dict__.get("_decode_plan") is not None, "the second run did not take sgsa_decode_stack"
     assert torch.equal(logits2, c["logits"]), "prefill not deterministic"
-    assert torch.equal(toks2, toks), "decode not deterministic"
+    assert torch.equal(toks2, toks), "sgsa_decode_stack's tokens differ from the per-layer path's"
 
 
 @pytest.mark.parametrize("layer", CHECK_LAYERS)

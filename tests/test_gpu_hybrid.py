@@ -70,6 +70,36 @@ def test_hybrid_bf16_greedy_generation(dev):
     assert torch.equal(toks, toks2) and torch.equal(logits, logits2), "not deterministic"
 
 
+def test_decode_stack_equals_the_per_layer_path(dev):
+    # sgsa_decode_stack (one call per step) against the per-layer Python path on copies of
+    # the same prefilled caches: logits equal bit for bit on selecting and re-scoring steps,
+    # and so are the SGSA states and caches after the last step
+    import sgsa_amd.hybrid as HY
+    cfg, m = _model(dev, torch.bfloat16, seed=6)
+    g = torch.Generator().manual_seed(7)
+    B, T, n = 3, 160, 9
+    prompt = torch.randint(0, cfg.vocab_size, (B, T), generator=g).to(dev)
+    toks = torch.randint(0, cfg.vocab_size, (B, n), generator=g).to(dev)
+    rope = HY.rope_tables(T + n, cfg.head_dim, cfg.rope_theta, dev)
+    with torch.no_grad():
+        caches = m.new_cache(B, T + n, dev, torch.bfloat16)
+        m.prefill(prompt, caches, rope)
+        copy = [{k: (v.clone() if torch.is_tensor(v) else v) for k, v in c.items()} for c in caches]
+        m.decode_stack = False
+        ref = [m.decode_step(toks[:, s], T + s, s, caches, rope) for s in range(n)]
+        assert m.__dict__.get("_decode_plan") is None
+        m.decode_stack = True
+        got = [m.decode_step(toks[:, s], T + s, s, copy, rope) for s in range(n)]
+        assert m.__dict__.get("_decode_plan") is not None, "sgsa_decode_stack was not used"
+    torch.cuda.synchronize()
+    for s in range(n):
+        assert torch.equal(got[s], ref[s]), f"step {s} ({'select' if s % 4 == 0 else 'reuse'}): logits differ"
+    for i, (a, b) in enumerate(zip(copy, caches)):
+        for name in ("k", "v", "state"):
+            if name in a:
+                assert torch.equal(a[name], b[name]), f"layer {i}: {name} differs"
+
+
 def test_hybrid_bf16_prompt_logits_near_the_oracle(dev):
     # bf16 activations (dense scores scaled in bf16 as hybrid_dense_delta_topk.py:186-187
     # does) against the fp32 oracle on the same bf16 parameters: prompt and three
