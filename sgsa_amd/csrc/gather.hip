@@ -229,6 +229,16 @@ __global__ __launch_bounds__(256) void sparse_gather_kernel(GatherArgs a, int lp
 #pragma unroll
   for (int i = 0; i < NE; ++i) { ak[i] = 0.f; av[i] = 0.f; }
   float esum = 0.f;
+  // the epilogue's own inputs, loaded first (they do not depend on the slots)
+  const long qoff = ((long)(b * Tq + qr) * H + h) * D;
+  float kt[NE];
+  if (a.self_key != nullptr && (a.diag != nullptr || a.budget != nullptr)) {
+    load_row<X, VEC>(reinterpret_cast<const X*>(a.self_key), qoff, sub, D, lpr, kt);
+  } else {
+#pragma unroll
+    for (int i = 0; i < NE; ++i) kt[i] = 0.f;
+  }
+  const float bud = a.budget != nullptr ? a.budget[(long)(b * Tq + qr) * H + h] : 0.f;
 
   if constexpr (!SPLIT) {
     for (int base = 0; base < kq; base += 64) {
@@ -266,6 +276,53 @@ __global__ __launch_bounds__(256) void sparse_gather_kernel(GatherArgs a, int lp
     const long pst = 4 + 2 * (long)D;
     const int ns = a.nsplit;
     const float* P = a.part + row * (long)ns * pst;
+    constexpr int SPG = 4;
+    const int ng = 64 / lpr;
+    if (ns <= ng * SPG) {
+      // every load first: lane c < ns the header of partial c; lane group g the row-vector
+      // pieces of partials g, g + ng, .. (at most SPG); then the same sums in the same
+      // order as the loops below
+      float hm = -INFINITY, hs = 0.f, h1 = -FLT_MAX, h2 = -FLT_MAX;
+      if (lane < ns) {
+        const float* pc = P + lane * pst;
+        hm = pc[0]; hs = pc[1]; h1 = pc[2]; h2 = pc[3];
+      }
+      float pk[SPG][NE], pvv[SPG][NE];
+#pragma unroll
+      for (int u = 0; u < SPG; ++u) {
+        const int c = min(grp + ng * u, ns - 1);
+        const float* pc = P + c * pst;
+#pragma unroll
+        for (int i = 0; i < NE; ++i) {
+          const int d = min(elem_d<X, VEC>(sub, i, lpr), D - 1);
+          pk[u][i] = pc[4 + d];
+          pvv[u][i] = pc[4 + D + d];
+        }
+      }
+      if (!fixed_max) mrun = wave_max(hm);
+      if (lane < ns) {
+        const float f = hm == -INFINITY ? 0.f : __expf(hm - mrun);
+        esum += hs * f;
+        const float hi = fmaxf(t1, h1), lo = fmaxf(fminf(t1, h1), fmaxf(t2, h2));
+        t1 = hi;
+        t2 = lo;
+      }
+#pragma unroll
+      for (int u = 0; u < SPG; ++u) {
+        const int c = grp + ng * u;
+        const float pm = __shfl(hm, min(c, 63), 64);
+        if (c < ns) {
+          const float f = pm == -INFINITY ? 0.f : __expf(pm - mrun);
+#pragma unroll
+          for (int i = 0; i < NE; ++i) {
+            if (elem_d<X, VEC>(sub, i, lpr) < D) {
+              ak[i] += pk[u][i] * f;
+              av[i] += pvv[u][i] * f;
+            }
+          }
+        }
+      }
+    } else {
     if (!fixed_max) {
       float mc = -INFINITY;
       for (int c = lane; c < ns; c += 64) mc = fmaxf(mc, P[c * pst]);
@@ -291,6 +348,7 @@ __global__ __launch_bounds__(256) void sparse_gather_kernel(GatherArgs a, int lp
           av[i] += pc[4 + D + d] * f;
         }
       }
+    }
     }
   }
   // combine the groups (lanes with equal `sub`)
@@ -320,14 +378,6 @@ __global__ __launch_bounds__(256) void sparse_gather_kernel(GatherArgs a, int lp
   for (int i = 0; i < NE; ++i) { ak[i] *= inv; av[i] *= inv; }
 
   // ---- per-row scalars (group 0 lanes hold the row vectors) ----
-  const long qoff = ((long)(b * Tq + qr) * H + h) * D;
-  float kt[NE];
-  if (a.self_key != nullptr && (a.diag != nullptr || a.budget != nullptr)) {
-    load_row<X, VEC>(reinterpret_cast<const X*>(a.self_key), qoff, sub, D, lpr, kt);
-  } else {
-#pragma unroll
-    for (int i = 0; i < NE; ++i) kt[i] = 0.f;
-  }
   float pdot = 0.f, pkk = 0.f, phh = 0.f, pvv = 0.f;
   if (grp == 0) {
 #pragma unroll
@@ -377,7 +427,6 @@ __global__ __launch_bounds__(256) void sparse_gather_kernel(GatherArgs a, int lp
       wnorm2 = wave_sum(pw);
       perp_ratio = fminf(fmaxf(sqrtf(wnorm2) / kh_norm, 0.f), 10.f);
     }
-    const float bud = a.budget[(long)(b * Tq + qr) * H + h];
     float al = a.alpha_max * conc * novelty * (1.f / (1.f + expf(-bud)));
     const float prox = al * sqrtf(vv2) * sqrtf(wnorm2);
     const float clip = fminf(1.f / fmaxf(prox, 1.f), 1.f);

@@ -61,7 +61,8 @@ __global__ __launch_bounds__(64 * SG_W) void small_gemm_kernel(const bf16_t* __r
 #pragma unroll
     for (int u = 0; u < D; ++u) {
       const int s = min(s0 + SG_W * u, nsteps - 1);
-      a[u] = *reinterpret_cast<const sg_u16x8*>(xr + 32 * s);
+      a[u] = (sg_u16x8){0, 0, 0, 0, 0, 0, 0, 0};
+      if (live) a[u] = *reinterpret_cast<const sg_u16x8*>(xr + 32 * s);   // rows past M load nothing
       b[u] = *reinterpret_cast<const sg_u16x8*>(wr + 32 * s);
     }
 #pragma unroll
