@@ -160,21 +160,49 @@ __global__ __launch_bounds__(TR_THREADS) void rows_select_kernel(TopkArgs a, con
 
   int32_t* oi = a.indices + row * top_k;
   float* os = a.scores + row * top_k;
-  uint32_t base = 0, eqbase = 0;
-  for (int j0 = 0; j0 < nv; j0 += TR_THREADS) {
-    const int j = j0 + tid;
-    const uint32_t kv = j < nv ? key[j] : 0u;
-    const bool eq = j < nv && !all && kv == thr;
-    uint32_t ntot;
-    const uint32_t eqrank = eqbase + block_excl_scan(eq ? 1u : 0u, wsum, &ntot);
-    eqbase += ntot;
-    const bool sel = j < nv && (all || kv > thr || (eq && eqrank < need));
-    const uint32_t pos = base + block_excl_scan(sel ? 1u : 0u, wsum, &ntot);
-    base += ntot;
-    if (sel) {
-      oi[pos] = j;
-      os[pos] = key_to_f32(kv);
+  // emission in ascending key index: thread t owns keys [t CH, t CH + CH) (CH odd, so the
+  // strided LDS reads hit distinct banks; CH <= 65 since nv <= 32768), marks them in
+  // 64-bit masks, and two block scans give the ties' ranks and the output positions
+  const int CH = ((nv + TR_THREADS - 1) / TR_THREADS) | 1;
+  const int c0 = tid * CH;
+  uint64_t gtm = 0, eqm = 0, hi_gt = 0, hi_eq = 0;   // bits of keys c0 + i (i < 64), then i = 64
+  for (int i = 0; i < CH; ++i) {
+    const int j = c0 + i;
+    if (j < nv) {
+      const uint32_t kv = key[j];
+      const bool g = all || kv > thr, e = !all && kv == thr;
+      if (i < 64) {
+        gtm |= (uint64_t)g << i;
+        eqm |= (uint64_t)e << i;
+      } else {
+        hi_gt = g;
+        hi_eq = e;
+      }
     }
+  }
+  uint32_t ntot;
+  const uint32_t neq = (uint32_t)(__popcll(eqm) + hi_eq);
+  const uint32_t eqbase = block_excl_scan(neq, wsum, &ntot);
+  // ties at the cut go to the lowest indices: this chunk takes the first `take` of its equal keys
+  uint32_t take = eqbase < need ? min(neq, need - eqbase) : 0u;
+  uint64_t selm = gtm, hi_sel = hi_gt;
+  for (uint64_t m = eqm; take > 0 && m != 0; --take) {
+    const uint64_t lowbit = m & (~m + 1);
+    selm |= lowbit;
+    m ^= lowbit;
+  }
+  if (take > 0 && hi_eq) hi_sel = 1;
+  const uint32_t nsel = (uint32_t)(__popcll(selm) + hi_sel);
+  uint32_t pos = block_excl_scan(nsel, wsum, &ntot);
+  for (uint64_t m = selm; m != 0; m &= m - 1) {
+    const int i = __ffsll((long long)m) - 1;
+    oi[pos] = c0 + i;
+    os[pos] = key_to_f32(key[c0 + i]);
+    ++pos;
+  }
+  if (hi_sel) {
+    oi[pos] = c0 + 64;
+    os[pos] = key_to_f32(key[c0 + 64]);
   }
   for (int i = kq + tid; i < top_k; i += TR_THREADS) {
     oi[i] = 0;
