@@ -668,34 +668,33 @@ __global__ __launch_bounds__(256) void rescore_kernel(int B, int Tq, int Tk, int
   const int nend = min(kq, base + 64);
   if constexpr (VEC && sizeof(X) == 2) {
     if (D == 128) {
-      // the wave's 64 indices in one load (lane l: slot base + l); 16 keys per step, their 16-byte
-      // pieces all loaded before the first is used
+      // the wave's 64 indices in one load (lane l: slot base + l), then the 16-byte pieces of all
+      // 64 keys (lane group g: keys base + 4u + g) loaded before the first is used: two memory
+      // round trips per wave
       const int jl = base + lane < nend ? ip[base + lane] : -1;
-      for (int i0 = base; i0 < nend; i0 += 16) {
-        uint4 kv[4];
-        bool ok[4];
+      uint4 kv[16];
+      bool ok[16];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int i = i0 + 4 * u + grp;
-          const int j = __shfl(jl, (i - base) & 63, 64);
-          ok[u] = i < nend && j >= 0 && j < Tk;
-          const long koff = ((long)(b * Tk + (ok[u] ? j : 0)) * H + h) * 128 + 8 * l16;
-          kv[u] = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(k) + koff);
+      for (int u = 0; u < 16; ++u) {
+        const int i = base + 4 * u + grp;
+        const int j = __shfl(jl, 4 * u + grp, 64);
+        ok[u] = i < nend && j >= 0 && j < Tk;
+        const long koff = ((long)(b * Tk + (ok[u] ? j : 0)) * H + h) * 128 + 8 * l16;
+        kv[u] = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(k) + koff);
+      }
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const uint32_t wv[4] = {kv[u].x, kv[u].y, kv[u].z, kv[u].w};
+        float acc = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          acc = fmaf(qv[2 * e], __uint_as_float(wv[e] << 16), acc);
+          acc = fmaf(qv[2 * e + 1], __uint_as_float(wv[e] & 0xffff0000u), acc);
         }
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const uint32_t wv[4] = {kv[u].x, kv[u].y, kv[u].z, kv[u].w};
-          float acc = 0.f;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            acc = fmaf(qv[2 * e], __uint_as_float(wv[e] << 16), acc);
-            acc = fmaf(qv[2 * e + 1], __uint_as_float(wv[e] & 0xffff0000u), acc);
-          }
-#pragma unroll
-          for (int o = 1; o < 16; o <<= 1) acc += __shfl_xor(acc, o, 64);
-          const int i = i0 + 4 * u + grp;
-          if (i < nend && l16 == 0) sp[i] = ok[u] ? acc * mscale : 0.f;
-        }
+        for (int o = 1; o < 16; o <<= 1) acc += __shfl_xor(acc, o, 64);
+        const int i = base + 4 * u + grp;
+        if (i < nend && l16 == 0) sp[i] = ok[u] ? acc * mscale : 0.f;
       }
       return;
     }

@@ -20,10 +20,12 @@ __device__ __forceinline__ float round_to(float v, float) { return v; }
 __device__ __forceinline__ float round_to(float v, bf16_t) { return bf16_to_f32(f32_to_bf16(v)); }
 
 // One workgroup of 256 threads per row.  ADD: the row is first a + b, rounded
-// to X and stored to sum (the residual add before the norm).  NE > 0: thread t
-// holds its elements t, t + 256, ... (at most NE of them, C <= 256 NE) and
-// their weights in registers, loaded before the reduction; NE = 0 walks the row
-// twice.  Both forms sum the squares in the same order and round alike.
+// to X and stored to sum (the residual add before the norm).
+//   NE > 0 (bf16 rows, C a multiple of 8, 16-byte aligned, C <= 2048 NE / 8):
+//     thread t holds elements 2048 j + 8 t + e (j < NE / 8, e < 8), read as one
+//     16-byte load per j, and its weights, all loaded before the reduction; the
+//     squares are summed in (j, e) order, then over the wave and the 4 waves.
+//   NE = 0 walks the row twice (thread t: elements t, t + 256, ..).
 template <typename X, typename W, bool ADD = false, int NE = 0>
 __global__ __launch_bounds__(256) void rms_norm_kernel(const X* __restrict__ x, const W* __restrict__ w, int C,
                                                        float eps, X* __restrict__ y, const X* __restrict__ b = nullptr,
@@ -34,25 +36,41 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const X* __restrict__ x, 
   X* yr = y + row * C;
   float ss = 0.f;
   if constexpr (NE > 0) {
-    float v[NE], wv[NE];
+    constexpr int NJ = NE / 8;
+    float v[NJ][8], wv[NJ][8];
     const X tag{};
 #pragma unroll
-    for (int j = 0; j < NE; ++j) {
-      const int c = threadIdx.x + 256 * j;
-      v[j] = 0.f;
-      wv[j] = 0.f;
-      if (c < C) {
-        v[j] = ld(xr, c);
-        if constexpr (ADD) v[j] = round_to(v[j] + ld(b + row * C, c), tag);
-        wv[j] = ld(w, c);
+    for (int jj = 0; jj < NJ; ++jj) {
+      const int c0 = 2048 * jj + 8 * threadIdx.x;
+      if (c0 < C) {
+        const uint4 xv = *reinterpret_cast<const uint4*>(xr + c0);
+        uint4 bv = make_uint4(0, 0, 0, 0);
+        if constexpr (ADD) bv = *reinterpret_cast<const uint4*>(b + row * C + c0);
+        const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w}, bw[4] = {bv.x, bv.y, bv.z, bv.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t xs_ = (e & 1) ? (xw[e >> 1] & 0xffff0000u) : (xw[e >> 1] << 16);
+          v[jj][e] = __uint_as_float(xs_);
+          if constexpr (ADD) {
+            const uint32_t bs_ = (e & 1) ? (bw[e >> 1] & 0xffff0000u) : (bw[e >> 1] << 16);
+            v[jj][e] = round_to(v[jj][e] + __uint_as_float(bs_), tag);
+          }
+          wv[jj][e] = ld(w, c0 + e);
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) { v[jj][e] = 0.f; wv[jj][e] = 0.f; }
       }
     }
 #pragma unroll
-    for (int j = 0; j < NE; ++j) {
-      const int c = threadIdx.x + 256 * j;
-      if (c < C) {
-        if constexpr (ADD) st(sum + row * C, c, v[j]);
-        ss = fmaf(v[j], v[j], ss);
+    for (int jj = 0; jj < NJ; ++jj) {
+      const int c0 = 2048 * jj + 8 * threadIdx.x;
+      if (c0 < C) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          if constexpr (ADD) st(sum + row * C, c0 + e, v[jj][e]);
+          ss = fmaf(v[jj][e], v[jj][e], ss);
+        }
       }
     }
     ss = wave_sum(ss);
@@ -61,9 +79,12 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const X* __restrict__ x, 
     const float mean = (part[0] + part[1] + part[2] + part[3]) / (float)C;
     const float r = 1.0f / sqrtf(mean + eps);
 #pragma unroll
-    for (int j = 0; j < NE; ++j) {
-      const int c = threadIdx.x + 256 * j;
-      if (c < C) st(yr, c, v[j] * r * wv[j]);
+    for (int jj = 0; jj < NJ; ++jj) {
+      const int c0 = 2048 * jj + 8 * threadIdx.x;
+      if (c0 < C) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) st(yr, c0 + e, v[jj][e] * r * wv[jj][e]);
+      }
     }
     return;
   }
@@ -90,13 +111,15 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const X* __restrict__ x, 
   for (int c = threadIdx.x; c < C; c += 256) st(yr, c, ld(xr, c) * r * ld(w, c));
 }
 
-// The row form for C: registers for C <= 4096, else the two walks.
+// The row form: 16-byte register chunks for bf16 rows with C % 8 == 0 (16-byte aligned
+// rows) and C <= 4096, else the two walks.
 template <typename X, typename W, bool ADD>
 hipError_t launch_norm_rows(long rows, int C, const X* x, const W* w, float eps, X* y, const X* b, X* sum,
                             hipStream_t st) {
   const dim3 grid((unsigned)rows);
-  if (C <= 256 * 8) rms_norm_kernel<X, W, ADD, 8><<<grid, 256, 0, st>>>(x, w, C, eps, y, b, sum);
-  else if (C <= 256 * 16) rms_norm_kernel<X, W, ADD, 16><<<grid, 256, 0, st>>>(x, w, C, eps, y, b, sum);
+  const bool chunks = sizeof(X) == 2 && C % 8 == 0 && ((uintptr_t)x | (uintptr_t)b) % 16 == 0;
+  if (chunks && C <= 2048) rms_norm_kernel<X, W, ADD, 8><<<grid, 256, 0, st>>>(x, w, C, eps, y, b, sum);
+  else if (chunks && C <= 4096) rms_norm_kernel<X, W, ADD, 16><<<grid, 256, 0, st>>>(x, w, C, eps, y, b, sum);
   else rms_norm_kernel<X, W, ADD, 0><<<grid, 256, 0, st>>>(x, w, C, eps, y, b, sum);
   return hipGetLastError();
 }
