@@ -348,9 +348,12 @@ def run_model(args) -> int:
 
 
 def run_hybrid(args) -> int:
-    """Config 4: the 24-layer hybrid decoder (sgsa_amd.hybrid), prefill then greedy decode."""
+    """Config 4: the 24-layer hybrid decoder (sgsa_amd.hybrid), prefill then greedy decode: a warm-up
+    prefill, the timed prefill, 4 untimed decode steps (where the decode plan is built), then the 256
+    timed decode steps."""
     from sgsa_amd.hybrid import HybridConfig, HybridForCausalLM, expand_caches, rope_tables
     T, B, steps = 16384, 8, 256
+    wsteps = 4   # untimed decode steps first (one selecting, three re-scoring): the decode plan is built there
     cfg = HybridConfig()
     dev = torch.device("cuda:0")
     model = HybridForCausalLM(cfg)
@@ -358,12 +361,12 @@ def run_hybrid(args) -> int:
                        generator=torch.Generator().manual_seed(0))
     model = model.to(device=dev, dtype=torch.bfloat16).eval()
     ids = torch.randint(0, cfg.vocab_size, (1, T), generator=torch.Generator().manual_seed(1)).to(dev)
-    rope = rope_tables(T + steps, cfg.head_dim, cfg.rope_theta, dev)
+    rope = rope_tables(T + wsteps + steps, cfg.head_dim, cfg.rope_theta, dev)
     cur = torch.cuda.current_stream()
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
-    log(f"hybrid: config 4, prefill T={T} at B=1, then {steps} decode steps at B={B}")
+    log(f"hybrid: config 4, prefill T={T} at B=1, then {wsteps} untimed and {steps} timed decode steps at B={B}")
     with torch.no_grad():
-        caches = model.new_cache(1, T + steps, dev, torch.bfloat16)
+        caches = model.new_cache(1, T + wsteps + steps, dev, torch.bfloat16)
         model.prefill(ids, caches, rope)   # warm-up: kernels, workspaces, GEMM plans
         torch.cuda.synchronize()
         ev[0].record(cur)
@@ -373,11 +376,14 @@ def run_hybrid(args) -> int:
         log(f"prefill {ev[0].elapsed_time(ev[1]):.1f} ms")
         caches = expand_caches(caches, B)
         tok = logits[:, -1].argmax(-1).expand(B).contiguous()
-        ev[2].record(cur)
-        for s in range(steps):
+        for s in range(wsteps):
             tok = model.decode_step(tok, T + s, s, caches, rope).argmax(-1)
-            if (s + 1) % 64 == 0:
-                log(f"decode step {s + 1}")
+        torch.cuda.synchronize()
+        ev[2].record(cur)
+        for s in range(wsteps, wsteps + steps):
+            tok = model.decode_step(tok, T + s, s, caches, rope).argmax(-1)
+            if (s + 1 - wsteps) % 64 == 0:
+                log(f"decode step {s + 1 - wsteps}")
         ev[3].record(cur)
         torch.cuda.synchronize()
     pre_ms, dec_ms = ev[0].elapsed_time(ev[1]), ev[2].elapsed_time(ev[3])
@@ -387,7 +393,7 @@ def run_hybrid(args) -> int:
     log(f"decode {dec_ms:.1f} ms for {steps} steps")
     print(json.dumps({
         "metric": HYBRID_METRIC, "value": round(B * steps / (dec_ms / 1000.0), 1), "unit": "tokens/s", "n_gpus": 1,
-        "steps": steps, "warmup": 1, "ms_per_step": round(dec_ms / steps, 3), "higher_is_better": True,
+        "steps": steps, "warmup": wsteps, "ms_per_step": round(dec_ms / steps, 3), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "uniform-random token ids, random-init weights",
         "prefill": {"T": T, "B": 1, "ms": round(pre_ms, 1), "tokens_per_s": round(T / (pre_ms / 1000.0), 1)},
