@@ -268,7 +268,9 @@ hipError_t launch_add_rms_norm(int dtype, int w_f32, long rows, int C, const voi
 }
 
 // silu(gate) * up of a fused gate | up projection row, in X's roundings: silu
-// rounded to X, then the product rounded to X.  One thread per output element.
+// rounded to X, then the product rounded to X.  One thread per output element;
+// VEC (bf16, I % 8 == 0, 16-byte aligned rows): eight elements per thread, read
+// and written as 16-byte pieces.
 template <typename X>
 __global__ __launch_bounds__(256) void silu_mul_kernel(const X* __restrict__ src, long stride, long rows, int I,
                                                        X* __restrict__ y) {
@@ -281,7 +283,33 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const X* __restrict__ src
   st(y, i, round_to(g / (1.0f + expf(-g)), tag) * u);
 }
 
+__global__ __launch_bounds__(256) void silu_mul8_kernel(const bf16_t* __restrict__ src, long stride, long rows, int I,
+                                                        bf16_t* __restrict__ y) {
+  const long i = ((long)blockIdx.x * 256 + threadIdx.x) * 8;
+  if (i >= rows * I) return;
+  const long r = i / I;
+  const int c = (int)(i % I);
+  const uint4 gv = *reinterpret_cast<const uint4*>(src + r * stride + c);
+  const uint4 uv = *reinterpret_cast<const uint4*>(src + r * stride + I + c);
+  const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w}, uw[4] = {uv.x, uv.y, uv.z, uv.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int e2 = 0; e2 < 4; ++e2) {
+    const float g0 = __uint_as_float(gw[e2] << 16), g1 = __uint_as_float(gw[e2] & 0xffff0000u);
+    const float u0 = __uint_as_float(uw[e2] << 16), u1 = __uint_as_float(uw[e2] & 0xffff0000u);
+    const float s0 = bf16_to_f32(f32_to_bf16(g0 / (1.0f + expf(-g0))));
+    const float s1 = bf16_to_f32(f32_to_bf16(g1 / (1.0f + expf(-g1))));
+    o[e2] = (uint32_t)f32_to_bf16(s0 * u0) | ((uint32_t)f32_to_bf16(s1 * u1) << 16);
+  }
+  *reinterpret_cast<uint4*>(y + i) = make_uint4(o[0], o[1], o[2], o[3]);
+}
+
 hipError_t launch_silu_mul(int dtype, const void* src, long stride, long rows, int I, void* y, hipStream_t st) {
+  if (dtype != DT_F32 && I % 8 == 0 && stride % 8 == 0 && ((uintptr_t)src | (uintptr_t)y) % 16 == 0) {
+    const dim3 grid((unsigned)((rows * I / 8 + 255) / 256));
+    silu_mul8_kernel<<<grid, 256, 0, st>>>((const bf16_t*)src, stride, rows, I, (bf16_t*)y);
+    return hipGetLastError();
+  }
   const dim3 grid((unsigned)((rows * I + 255) / 256));
   if (dtype == DT_F32) silu_mul_kernel<float><<<grid, 256, 0, st>>>((const float*)src, stride, rows, I, (float*)y);
   else silu_mul_kernel<bf16_t><<<grid, 256, 0, st>>>((const bf16_t*)src, stride, rows, I, (bf16_t*)y);
