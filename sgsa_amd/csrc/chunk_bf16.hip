@@ -21,8 +21,9 @@
 //                        off-diagonal blocks by doubling, A_RC = -A_RR T_RC A_CC for 16-, 32- and
 //                        64-row halves.  A goes to the workspace as the bf16 rounding of its
 //                        lower 16x16 tiles (18 KB per chunk), the only intermediate of the chunk.
-// K4 chunk_maps_bf16     grid (B*H, G)   the affine maps S_end = Phi S_start + P of G segments of
-//                        consecutive chunks (Phi: from I with nu = 0; P: from 0)
+// K4 chunk_maps2_bf16    grid (B*H*G)    the affine maps S_end = Phi S_start + P of G segments of
+//                        consecutive chunks (Phi: from I with nu = 0; P: from 0), both in one
+//                        block (D = 128; chunk_maps_bf16 builds them in two blocks for D < 128)
 //    chunk_seg_scan_bf16 grid (B*H)      the segment start states
 //    chunk_replay_bf16   grid (B*H, G)   each segment reruns its chunks from its start state and
 //                        writes the output rows; the last segment writes the final state.
@@ -582,22 +583,45 @@ __device__ __forceinline__ void stage_chunk(const bf16_t* __restrict__ q, const 
 // then publishes them with a barrier.
 struct DmaCtx {
   int T, H, NT, b, h, bh, lane, w;
+  // per-lane byte offsets, the same for every chunk: row slots of load i = w + 8 u
+  // (row (64 i + lane) / 17 of the chunk, 16-byte piece (64 i + lane) % 17) and A
+  // tile slots (row (64 i + lane) / 3, piece (64 i + lane) % 3); the chunk's start
+  // is added per load (rows) or is the buffer's base (A tiles)
+  unsigned ro[3], ao[4];
+  __device__ DmaCtx(int T_, int H_, int NT_, int b_, int h_, int bh_, int lane_, int w_)
+      : T(T_), H(H_), NT(NT_), b(b_), h(h_), bh(bh_), lane(lane_), w(w_) {
+    const int rbytes = H * DP * 2;
+#pragma unroll
+    for (int u = 0; u < 3; ++u) {
+      const int sl = 64 * (w + 8 * u) + lane;
+      const int row = sl / 17, pc = sl % 17;
+      ro[u] = (unsigned)(row * rbytes + 16 * (pc < 16 ? pc : 0));
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int sl = 64 * (w + 8 * u) + lane;
+      const int row = sl / 3, pc = sl % 3;
+      ao[u] = (unsigned)(row * 32 + 16 * (pc < 2 ? pc : 0));
+    }
+  }
 };
 // 64 rows of one input, tokens c L .. c L + 63, into dst (rows of PK elements)
 template <int NW>
 __device__ __forceinline__ void dma_rows(const DmaCtx& x, const bf16_t* base, int c, uint16_t* dst) {
+  static_assert(NW == 8, "the per-lane offsets are laid out for 8 waves");
   constexpr int RI = L * 17 / 64;
   const long hoff = ((long)x.b * x.T * x.H + x.h) * DP;
   const int rbytes = x.H * DP * 2;
   const int nrec = (x.T - 1) * rbytes + DP * 2;
   const __amdgpu_buffer_rsrc_t rs =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t*>(base + hoff), 0, nrec, 0x00020000);
-  for (int i = x.w; i < RI; i += NW) {
-    const int sl = 64 * i + x.lane;
-    const int row = sl / 17, pc = sl % 17;
-    const unsigned voff = (unsigned)((c * L + row) * rbytes + 16 * (pc < 16 ? pc : 0));
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(dst + 512 * i), 16, voff,
-                                             0, 0, 0);
+  const unsigned coff = (unsigned)(c * L * rbytes);
+#pragma unroll
+  for (int u = 0; u < 3; ++u) {
+    const int i = x.w + NW * u;
+    if (i < RI)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(dst + 512 * i), 16,
+                                               x.ro[u] + coff, 0, 0, 0);
   }
 }
 // kappa (or nu) rows of chunk c: the local rows, then (SP) the sparse rows 16 bytes on
@@ -616,17 +640,19 @@ template <int M> constexpr int at_elems() {
 // the A tiles of chunk c
 template <int M, int NW>
 __device__ __forceinline__ void dma_A(const DmaCtx& x, const uint16_t* Ain, int c, uint16_t* At) {
+  static_assert(NW == 8, "the per-lane offsets are laid out for 8 waves");
   constexpr int NB = M / 16;
   constexpr int NTL = NB * (NB + 1) / 2;
   constexpr int AI = a_instr<M>();
+  static_assert(AI <= 4 * NW, "A tiles beyond the per-lane offsets");
   const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(Ain + ((long)x.bh * x.NT + c) * NTL * 256), 0, NTL * 512, 0x00020000);
-  for (int i = x.w; i < AI; i += NW) {
-    const int sl = 64 * i + x.lane;
-    const int row = sl / 3, pc = sl % 3;
-    const unsigned voff = (unsigned)(row * 32 + 16 * (pc < 2 ? pc : 0));
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(ars, (__attribute__((address_space(3))) void*)(At + 512 * i), 16, voff,
-                                             0, 0, 0);
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int i = x.w + NW * u;
+    if (i < AI)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ars, (__attribute__((address_space(3))) void*)(At + 512 * i), 16,
+                                               x.ao[u], 0, 0, 0);
   }
 }
 
@@ -851,6 +877,100 @@ __global__ __launch_bounds__(512, 1) void chunk_maps_bf16(const bf16_t* __restri
     maps_pass<M, FULL, true>(k, v, sk, sv, beta, alpha, gamma, T, H, D, NT, CPS, Ain, dst, kap, nuv, At, gt, bh, g);
   else
     maps_pass<M, FULL, false>(k, v, sk, sv, beta, alpha, gamma, T, H, D, NT, CPS, Ain, dst, kap, nuv, At, gt, bh, g);
+}
+
+// Both maps of a (b*h, segment) pair in one block (D = DP): P (from 0, with nu) and
+// Phi (from I, nu = 0) share every chunk's staged kappa, nu and A tiles, so a chunk's
+// operands are loaded and published once for the two states, and the pairs run in
+// one round of workgroups.  Each wave carries its 16-column tile of both states;
+// per chunk: P's residual and update, Phi's residual, the barrier that frees nu and
+// the A tiles for the next chunk's loads, then Phi's update.  1-D grid of B*H*G
+// blocks; sout as chunk_maps_bf16.
+template <int M>
+__global__ __launch_bounds__(512, 1) void chunk_maps2_bf16(const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
+                                                         const bf16_t* __restrict__ sk, const bf16_t* __restrict__ sv,
+                                                         const float* __restrict__ beta, const float* __restrict__ alpha,
+                                                         const float* __restrict__ gamma, int T, int H, int NT, int CPS,
+                                                         int BH, int G, const uint16_t* __restrict__ Ain,
+                                                         float* __restrict__ sout) {
+  constexpr bool SP = M == 2 * L;
+  constexpr int NB = M / 16;
+  constexpr int KE = krows_elems<M>();
+  __shared__ __align__(16) uint16_t kapb[2 * KE];
+  __shared__ __align__(16) uint16_t nuv[KE];
+  __shared__ __align__(16) uint16_t At[at_elems<M>()];
+  __shared__ __align__(16) GateTab<M> gtb[2];
+  const int pair = blockIdx.x;
+  if (pair >= BH * G) return;   // block-uniform
+  const int bh = pair % BH, g = pair / BH;
+  const int b = bh / H, h = bh % H;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform
+  const int lr = lane & 15, lg = lane >> 4;
+  const int col = 16 * w;
+  const int cb = g * CPS, ce = min(NT, cb + CPS);
+
+  f4 S0[DP / 16], S1[DP / 16];   // P (from 0) and Phi (from I)
+#pragma unroll
+  for (int r = 0; r < DP / 16; ++r)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      S0[r][e] = 0.f;
+      S1[r][e] = (16 * r + 4 * lg + e == col + lr) ? 1.f : 0.f;
+    }
+
+  const DmaCtx x{T, H, NT, b, h, bh, lane, w};
+  if (cb < ce) {
+    dma_pair<M, 8>(x, k, sk, cb, kapb);
+    dma_pair<M, 8>(x, v, sv, cb, nuv);
+    dma_A<M, 8>(x, Ain, cb, At);
+    if (w == 0) store_gates<M>(load_gates<SP>(beta, alpha, gamma, T, H, b, h, cb * L, lane), lane, gtb[0]);
+    __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): this wave's loads have landed in LDS
+  }
+  __syncthreads();
+  for (int c = cb; c < ce; ++c) {
+    const int cur = (c - cb) & 1;
+    const uint16_t* kap = kapb + cur * KE;
+    const GateTab<M>& gt = gtb[cur];
+    const bool more = c + 1 < ce;   // block-uniform
+    GateIn gn{1.f, 0.f, 0.f};
+    if (more) {
+      dma_pair<M, 8>(x, k, sk, c + 1, kapb + (cur ^ 1) * KE);
+      if (w == 0) gn = load_gates<SP>(beta, alpha, gamma, T, H, b, h, (c + 1) * L, lane);
+    }
+    f4 R[NB];
+    Op Rop[NB / 2];
+    {
+      Op Sop[DP / 32];
+      pack_ops<DP / 16>(S0, Sop);
+      tile_residual<M, true>(Sop, kap, nuv, At, gt.el, col, lr, lg, R);
+    }
+    scaled_ops<M>(R, gt.fac, lg, Rop);
+    tile_update<M>(S0, Rop, kap, gt.el[L - 1], lr, lg);
+    {
+      Op Sop[DP / 32];
+      pack_ops<DP / 16>(S1, Sop);
+      tile_residual<M, false>(Sop, kap, nuv, At, gt.el, col, lr, lg, R);
+    }
+    __syncthreads();   // every wave is done with nu and the A tiles
+    if (more) {
+      dma_pair<M, 8>(x, v, sv, c + 1, nuv);
+      dma_A<M, 8>(x, Ain, c + 1, At);
+    }
+    scaled_ops<M>(R, gt.fac, lg, Rop);
+    tile_update<M>(S1, Rop, kap, gt.el[L - 1], lr, lg);
+    if (more && w == 0) store_gates<M>(gn, lane, gtb[cur ^ 1]);
+    __builtin_amdgcn_s_waitcnt(0x0f70);
+    __syncthreads();   // the next chunk's operands are in place; this chunk's are free
+  }
+  float* d0 = sout + (long)(bh * G + g) * DP * DP;
+  float* d1 = sout + (long)((BH + bh) * G + g) * DP * DP;
+#pragma unroll
+  for (int r = 0; r < DP / 16; ++r)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      d0[(long)(16 * r + 4 * lg + e) * DP + col + lr] = S0[r][e];
+      d1[(long)(16 * r + 4 * lg + e) * DP + col + lr] = S1[r][e];
+    }
 }
 
 // The segment start states: sinit[bh*G + g] for g < G, from h0 ([B*H][D][D] or
@@ -1199,8 +1319,12 @@ static hipError_t launch_bf16_t(const ChunkArgs& a, hipStream_t st) {
     chunk_replay_bf16<M, FULL><<<dim3(BH, 1), 512, 0, st>>>(q, k, v, sk, sv, a.beta, a.alpha, a.gamma, a.T, a.H, a.D, NT,
                                                       NT, Aws, a.initial_state, a.D, a.final_state, (bf16_t*)a.out);
   } else {
-    chunk_maps_bf16<M, FULL><<<dim3(16 * ((BH * G + 7) / 8)), 512, 0, st>>>(
-        k, v, sk, sv, a.beta, a.alpha, a.gamma, a.T, a.H, a.D, NT, CPS, BH, G, Aws, maps);
+    if constexpr (FULL)
+      chunk_maps2_bf16<M><<<dim3(BH * G), 512, 0, st>>>(k, v, sk, sv, a.beta, a.alpha, a.gamma, a.T, a.H, NT, CPS, BH,
+                                                        G, Aws, maps);
+    else
+      chunk_maps_bf16<M, FULL><<<dim3(16 * ((BH * G + 7) / 8)), 512, 0, st>>>(
+          k, v, sk, sv, a.beta, a.alpha, a.gamma, a.T, a.H, a.D, NT, CPS, BH, G, Aws, maps);
     chunk_seg_scan_bf16<<<dim3(BH, DP / 16), 256, 0, st>>>(G, a.D, a.initial_state, maps, sinit);
     chunk_replay_bf16<M, FULL><<<dim3(BH, G), 512, 0, st>>>(q, k, v, sk, sv, a.beta, a.alpha, a.gamma, a.T, a.H, a.D, NT,
                                                       CPS, Aws, sinit, DP, a.final_state, (bf16_t*)a.out);
