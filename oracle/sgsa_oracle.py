@@ -30,6 +30,8 @@ How each function is pinned (tests/test_oracle.py):
   mistake (sparse residual read from the updated state) that must fail;
 * chunk form: equality with the recurrence for several chunk sizes including
   a ragged tail (the reference's own 1e-5 test), and state continuation;
+  ``carry_dtype`` (the reference's bf16 state between chunks): the run equals
+  its chunks run one at a time with the state rounded in between, bit for bit;
 * top-k: brute force with Python ``sorted`` on tiny rows with ties and -0.0,
   causality, the t<k row counts and the padded-slot convention;
 * retrieval/diagnostics/gate: explicit Python loops on tiny inputs, sums of
@@ -122,6 +124,7 @@ def chunk_sgsa_fwd(
     initial_state: Optional[Tensor] = None,
     chunk_size: int = 64,
     output_final_state: bool = False,
+    carry_dtype: Optional[torch.dtype] = None,
 ) -> Tuple[Tensor, Optional[Tensor]]:
     """Chunked SGSA forward, torch branch of modelings/sgsa_ops/chunk_fwd.py:12-131.
 
@@ -130,8 +133,16 @@ def chunk_sgsa_fwd(
     (:46, :70-71); ``rhs = nu - D_tau * (kappa S0)`` (:73-74); the transition
     ``T_ij = 1[tau_j < tau_i] lam_j D_tau_i / max(D_tau_j, 1e-6) (kappa_i . kappa_j)``
     (:86-87) is solved with ``solve_triangular`` (:89); readout uses the
-    ``tau_i <= t`` mask (:120); the final state is :109-115.  The state is
-    carried in the compute dtype (fp32 for low-precision inputs).
+    ``tau_i <= t`` mask (:120); the final state is :109-115.
+
+    By default the state is carried between chunks in the compute dtype (fp32
+    for low-precision inputs), as the kernels carry it.  ``carry_dtype``
+    rounds it to that dtype after every chunk, which is what the reference
+    does with q.dtype (the zero start state made in it, :34; ``state =
+    state_h.to(q.dtype)`` after each chunk, :129): pass the inputs' dtype
+    (bfloat16) to get the reference's own roundings of the carried state.  An
+    initial state is taken as given (:34, :48) and the returned final state
+    is the rounded one, upcast to the compute dtype.
     """
     bsz, seq_len, heads, dk = q.shape
     dv = v.shape[-1]
@@ -177,6 +188,8 @@ def chunk_sgsa_fwd(
         final = prefix[..., -1]
         tail = final[..., None] / ptau.clamp_min(1e-6)
         state = final[..., None, None] * state + kap.transpose(-1, -2) @ (resid * (lam * tail)[..., None])
+        if carry_dtype is not None:
+            state = state.to(carry_dtype).to(cdt)
     out = torch.cat(outs, dim=1) if outs else q.new_zeros(bsz, 0, heads, dv)
     return out, (state if output_final_state else None)
 

@@ -4,8 +4,11 @@ Same signature and return as modelings/sgsa_ops/chunk.py:104-148, so callers
 such as SGSAStateLayer.forward (modelings/modeling_sgsa.py:584-596) work by
 swapping the import.  Differences, all deliberate:
 
-* the final state is returned in float32 (the reference casts it to q.dtype,
-  chunk_fwd.py:129);
+* the state is carried between chunks in float32 and the final state is
+  returned in float32 (the reference holds it in q.dtype between chunks and
+  returns it so, chunk_fwd.py:34, :129: with bf16 inputs a rounding of the
+  state after every chunk, worth about 1e-3 of o's largest magnitude at
+  T = 32768);
 * ``use_triton`` is accepted and ignored; ``chunk_size`` is accepted, the
   kernels always use 64-token chunks (the result depends on it only through
   rounding), and a value other than 64 draws a warning;

@@ -20,7 +20,9 @@ The CPU oracle cannot run all sixteen heads, so the test combines:
       (fp32 recurrence, naive.py:34-57) run on that head alone within 2e-2 of
       the largest magnitude, and 99% of their entries above 1% of it within
       2e-2 of their own magnitude -- heads are independent in the layer; two
-      heads in the direct write mode, one in the residual mode.
+      heads in the direct write mode, one in the residual mode; and the same
+      bounds hold against the reference's chunk form with its own roundings
+      of the carried state (bf16 between chunks, chunk_fwd.py:34, :129).
 """
 
 import pytest
@@ -163,3 +165,12 @@ def test_whole_head_matches_oracle_layer(ns, h, write_mode):
     close(out["wk"][:, :, h:h + 1], ref["write_key"], 2e-2, f"write key head {h}")
     close(out["vh"][:, :, h:h + 1], ref["v_hat"], 2e-2, f"v_hat head {h}")
     close(out["al"][:, :, h:h + 1], ref["alpha"], 2e-2, f"alpha head {h}")
+    # the reference's own roundings of the carried state: chunk_fwd.py holds it in q.dtype
+    # (bf16) between chunks (:34, :129), which moves o by about 1e-3 of its largest
+    # magnitude from the fp32 recurrence above; the kernels carry fp32 and must sit within
+    # the same bounds of that form too (same retrieval outputs, chunk form of 64 tokens)
+    o16, s16 = O.chunk_sgsa_fwd(sl(x["q_f32"]), sl(x["k_f32"]), sl(x["v_f32"]), sl(x["beta"]), sl(x["gamma"]),
+                                ref["write_key"], ref["v_hat"], ref["alpha"], None, 64, True,
+                                carry_dtype=torch.bfloat16)
+    close(out["o"][:, :, h:h + 1], o16, 2e-2, f"o head {h} vs bf16-carried state", elem_p99=2e-2)
+    close(out["st"][:, h:h + 1], s16, 2e-2, f"final_state head {h} vs bf16-carried state", elem_p99=2e-2)

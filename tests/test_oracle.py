@@ -141,6 +141,30 @@ def test_chunk_matches_recurrent_fp32_reference_tolerance():
     torch.testing.assert_close(cs, rs, rtol=1e-5, atol=1e-5)
 
 
+def test_chunk_carry_dtype_rounds_the_state_between_chunks_only():
+    # chunk_fwd.py:129 holds the state in q.dtype between chunks; within a chunk everything
+    # is fp32.  Restated piecewise: each chunk run alone from the previous chunk's final
+    # state with no carry rounding, that state rounded to bf16 in between, must give the
+    # carry_dtype run bit for bit (T=10, chunks of 4: a ragged last chunk).
+    q, k, v, sk, sv, beta, gamma, alpha = (x.to(torch.bfloat16) for x in _inputs(seed=5, T=10, D=8))
+    o, s = O.chunk_sgsa_fwd(q, k, v, beta, gamma, sk, sv, alpha, None, 4, True, carry_dtype=torch.bfloat16)
+    pieces, st = [], None
+    for a, b in ((0, 4), (4, 8), (8, 10)):
+        sl = lambda x: x[:, a:b]
+        oi, si = O.chunk_sgsa_fwd(*(sl(x) for x in (q, k, v, beta, gamma, sk, sv, alpha)), st, 4, True)
+        pieces.append(oi)
+        st = si.to(torch.bfloat16).float()
+    assert torch.equal(torch.cat(pieces, 1), o)
+    assert torch.equal(st, s)
+    # the rounding changes the later chunks and leaves the first chunk's outputs alone
+    o32, s32 = O.chunk_sgsa_fwd(q, k, v, beta, gamma, sk, sv, alpha, None, 4, True)
+    assert torch.equal(o32[:, :4], o[:, :4])
+    assert not torch.equal(o32[:, 4:], o[:, 4:]) and not torch.equal(s32, s)
+    # carrying in the compute dtype is the default
+    o2, s2 = O.chunk_sgsa_fwd(q, k, v, beta, gamma, sk, sv, alpha, None, 4, True, carry_dtype=torch.float32)
+    assert torch.equal(o2, o32) and torch.equal(s2, s32)
+
+
 # ---------------------------------------------------------------- top-k
 
 def _brute_topk(row, k):
