@@ -528,13 +528,17 @@ int sgsa_sparse_gather(int dtype, int B, int Tq, int Tk, int H, int D, int top_k
                                    workspace_bytes, stream);
 }
 
-int sgsa_sparse_gather_masked(int dtype, int B, int Tq, int Tk, int H, int D, int top_k, int q_offset,
+// sgsa_sparse_gather_masked; with rq, the slot scores are (rq . k) * rq_ms at the slots' keys,
+// computed inside the split-row gather where its form allows (bf16, D = 128, [B,Tk,H,D], no slot
+// mask), else by launch_rescore into scores first: the same values either way.
+static int sparse_gather_impl(int dtype, int B, int Tq, int Tk, int H, int D, int top_k, int q_offset,
                               int kv_layout, const void* k, const void* v, const void* self_key,
                               const int32_t* indices, const float* scores, const uint8_t* slot_valid,
                               const float* top2, const int32_t* counts, const float* budget, int write_mode,
                               float alpha_max, float tau_c, int local_window, int sink_size, void* k_hat,
                               void* v_hat, void* write_key, float* alpha, float* weights, float* diag,
-                              float* row_stats, void* workspace, size_t workspace_bytes, void* stream) {
+                              float* row_stats, void* workspace, size_t workspace_bytes, void* stream,
+                              const void* rq, float rq_ms) {
   if (kv_layout != 0 && kv_layout != 1) return fail(SGSA_ERR_INVALID_ARG, "kv_layout must be 0 ([B,Tk,H,D]) or 1 ([B,H,Tk,D])");
   if (int s = check_dtype(dtype)) return s;
   if (int s = check_dims(B, Tq, H, D)) return s;
@@ -568,8 +572,53 @@ int sgsa_sparse_gather_masked(int dtype, int B, int Tq, int Tk, int H, int D, in
     a.split_len = sgsa::GATHER_SPLIT_LEN;
     a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + 256);
   }
+  if (rq != nullptr) {
+    auto aligned = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
+    if (dtype == SGSA_BF16 && D == 128 && kv_layout == 0 && slot_valid == nullptr && a.nsplit > 0 && k != nullptr &&
+        aligned(k) && aligned(v) && aligned(rq) && (self_key == nullptr || aligned(self_key))) {
+      a.rq = rq;
+      a.rq_ms = rq_ms;
+    } else if (int s = hip_status(sgsa::launch_rescore(dtype, B, Tq, Tk, H, D, top_k, rq, k, indices, counts, rq_ms,
+                                                       const_cast<float*>(scores), (hipStream_t)stream),
+                                  "sgsa_sparse_gather (scores)")) {
+      return s;
+    }
+  }
   return hip_status(sgsa::launch_sparse_gather(a, (hipStream_t)stream), "sgsa_sparse_gather");
 }
+
+int sgsa_sparse_gather_masked(int dtype, int B, int Tq, int Tk, int H, int D, int top_k, int q_offset,
+                              int kv_layout, const void* k, const void* v, const void* self_key,
+                              const int32_t* indices, const float* scores, const uint8_t* slot_valid,
+                              const float* top2, const int32_t* counts, const float* budget, int write_mode,
+                              float alpha_max, float tau_c, int local_window, int sink_size, void* k_hat,
+                              void* v_hat, void* write_key, float* alpha, float* weights, float* diag,
+                              float* row_stats, void* workspace, size_t workspace_bytes, void* stream) {
+  return sparse_gather_impl(dtype, B, Tq, Tk, H, D, top_k, q_offset, kv_layout, k, v, self_key, indices, scores,
+                            slot_valid, top2, counts, budget, write_mode, alpha_max, tau_c, local_window, sink_size,
+                            k_hat, v_hat, write_key, alpha, weights, diag, row_stats, workspace, workspace_bytes,
+                            stream, nullptr, 0.f);
+}
+
+}  // extern "C"
+
+namespace sgsa {
+int sparse_gather_rescored(int dtype, int B, int Tq, int Tk, int H, int D, int top_k, int q_offset, float scale,
+                           int scale_mode, const void* q, const void* k, const void* v, const void* self_key,
+                           const int32_t* indices, float* scores, const int32_t* counts, const float* budget,
+                           int write_mode, float alpha_max, float tau_c, int local_window, int sink_size,
+                           void* k_hat, void* v_hat, void* write_key, float* alpha, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+  if (scale_mode != 0 && scale_mode != 1) return fail(SGSA_ERR_INVALID_ARG, "scale_mode must be 0 or 1");
+  REQUIRE(q);
+  return sparse_gather_impl(dtype, B, Tq, Tk, H, D, top_k, q_offset, 0, k, v, self_key, indices, scores, nullptr,
+                            nullptr, counts, budget, write_mode, alpha_max, tau_c, local_window, sink_size, k_hat,
+                            v_hat, write_key, alpha, nullptr, nullptr, nullptr, workspace, workspace_bytes, stream, q,
+                            score_multiplier(scale, scale_mode));
+}
+}  // namespace sgsa
+
+extern "C" {
 
 int sgsa_sparse_gather_workspace_size(int B, int Tq, int H, int D, int top_k, size_t* bytes) {
   if (int s = check_dims(B, Tq, H, D)) return s;

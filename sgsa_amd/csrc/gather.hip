@@ -202,6 +202,96 @@ __device__ __forceinline__ void gather_slots(const GatherArgs& a, int s0, int s1
   }
 }
 
+// gather_slots for bf16 rows of D = 128 ([B,Tk,H,D], 16 lanes per row) whose slot scores
+// are computed here, from the query's 8 elements of the lane (qv) and the key rows the
+// gather loads anyway: each 64-slot block loads its 64 key and value rows (lane group g:
+// slots 4u + g, u = 0..15) before using any, scores them as rescore_kernel does (the same
+// fused multiply-adds, lane swaps and multiplier, 0 for an index outside [0, Tk)), hands
+// slot l's score to lane l, and then weighs and sums as gather_slots and gather_step do,
+// in the same order: the results equal rescore_kernel followed by gather_slots bit for
+// bit, with one read of the key rows instead of two.
+__device__ __forceinline__ void gather_slots_rescored(const GatherArgs& a, int s0, int s1, const int32_t* idxp,
+                                                      const float (&qv)[8], float ms, const uint16_t* K,
+                                                      const uint16_t* V, int b, int h, int grp, int sub,
+                                                      bool fixed_max, float& mrun, float& t1, float& t2,
+                                                      float& esum, float (&ak)[8], float (&av)[8]) {
+  const int lane = threadIdx.x & 63;
+  const int Tk = a.Tk;
+  // the (b, h) rows from one base; a row's offset from it fits 32 bits (j H D + D < 2^31 elements)
+  const long hb = kv_row_offset(a, b, h, 0);
+  const uint16_t* Kb = K + hb;
+  const uint16_t* Vb = V + hb;
+  const uint32_t rstride = (uint32_t)a.H * 128u;
+  for (int base = s0; base < s1; base += 64) {
+    const int slot = base + lane;
+    const int jl = slot < s1 ? idxp[slot] : 0;
+    const int nstep = min(64, s1 - base);
+    uint4 rk[16], rv[16];
+    uint32_t okm = 0;   // bit u: slot 4u + grp is in the block and its index in [0, Tk)
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int src = 4 * u + grp;
+      const int jj = __shfl(jl, src, 64);
+      const bool ok = src < nstep && jj >= 0 && jj < Tk;
+      okm |= ok ? 1u << u : 0u;
+      const uint32_t off = (ok ? (uint32_t)jj : 0u) * rstride + 8u * (uint32_t)sub;
+      rk[u] = *reinterpret_cast<const uint4*>(Kb + off);
+      rv[u] = *reinterpret_cast<const uint4*>(Vb + off);
+    }
+    // the scores: all 16 lanes of group g hold slot 4u + g's in sco[u]; lane 16g + u then
+    // offers sco[u], which lane 4u + g takes
+    float mine = 0.f;
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const uint32_t wv[4] = {rk[u].x, rk[u].y, rk[u].z, rk[u].w};
+      float acc = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        acc = fmaf(qv[2 * e], __uint_as_float(wv[e] << 16), acc);
+        acc = fmaf(qv[2 * e + 1], __uint_as_float(wv[e] & 0xffff0000u), acc);
+      }
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) acc += __shfl_xor(acc, o, 64);
+      const float sco = (okm >> u) & 1u ? acc * ms : 0.f;
+      mine = sub == u ? sco : mine;
+    }
+    // the key rows stay packed until the sums: the unpacked copies of the scoring loop are
+    // not kept for them (128 more registers live), they are unpacked again
+#pragma unroll
+    for (int u = 0; u < 16; ++u) asm volatile("" : "+v"(rk[u].x), "+v"(rk[u].y), "+v"(rk[u].z), "+v"(rk[u].w));
+    const float got = __shfl(mine, 16 * (lane & 3) + (lane >> 2), 64);
+    const float sc = slot < s1 ? got : -INFINITY;
+    if (!fixed_max) {
+      const float bm = wave_max(sc);
+      if (bm > mrun) {
+        const float f = (mrun == -INFINITY) ? 0.f : __expf(mrun - bm);
+        esum *= f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) { ak[i] *= f; av[i] *= f; }
+        mrun = bm;
+      }
+      const float so = sc == -INFINITY ? -FLT_MAX : sc;
+      t2 = fmaxf(t2, fminf(t1, so));
+      t1 = fmaxf(t1, so);
+    }
+    const float wgt = sc == -INFINITY ? 0.f : __expf(sc - mrun);
+    esum += wgt;
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int src = 4 * u + grp;
+      const float ww = __shfl(wgt, src, 64);
+      const float wv = src < nstep ? ww : 0.f;
+      float xv[8], xk[8];
+      unpack_row<bf16_t>(rv[u], xv);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) av[i] += wv * xv[i];
+      unpack_row<bf16_t>(rk[u], xk);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ak[i] += wv * xk[i];
+    }
+  }
+}
+
 template <typename X, bool VEC, bool SPLIT>
 __global__ __launch_bounds__(256) void sparse_gather_kernel(GatherArgs a, int lpr) {
   constexpr int NE = GatherShape<X, VEC>::NE;
@@ -526,8 +616,9 @@ __global__ void zero_int_kernel(int32_t* p) {
 // wave (row, c) accumulates slots [c*split_len, (c+1)*split_len) of the row
 // and writes its partial {max, sum, top-1, top-2, ak[D], av[D]}
 // (unnormalised, relative to that max); sparse_gather_kernel merges a row's
-// partials in a fixed order, then runs its epilogue unchanged.
-template <typename X, bool VEC>
+// partials in a fixed order, then runs its epilogue unchanged.  RS: the slot scores are
+// computed from a.rq and the gathered key rows (gather_slots_rescored; bf16, D = 128).
+template <typename X, bool VEC, bool RS>
 __global__ __launch_bounds__(256) void gather_part_kernel(GatherArgs a, int lpr) {
   constexpr int NE = GatherShape<X, VEC>::NE;
   const int lane = threadIdx.x & 63;
@@ -549,9 +640,21 @@ __global__ __launch_bounds__(256) void gather_part_kernel(GatherArgs a, int lpr)
   for (int i = 0; i < NE; ++i) { ak[i] = 0.f; av[i] = 0.f; }
   float esum = 0.f;
   const int s0 = c * a.split_len, s1 = min(kq, s0 + a.split_len);
-  gather_slots<X, VEC>(a, s0, s1, a.indices + row * topk, a.scores + row * topk,
-                       a.slot_valid ? a.slot_valid + row * topk : nullptr, reinterpret_cast<const X*>(a.k),
-                       reinterpret_cast<const X*>(a.v), b, h, grp, sub, lpr, fixed_max, mrun, t1, t2, esum, ak, av);
+  if constexpr (RS) {
+    static_assert(VEC && sizeof(X) == 2 && NE == 8, "the rescored partials take bf16 rows of 16-byte pieces");
+    const long qoff = ((long)(b * Tq + (int)(row % Tq)) * H + h) * D;
+    float qv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qv[e] = ld(reinterpret_cast<const X*>(a.rq), qoff + 8 * sub + e);
+    gather_slots_rescored(a, s0, s1, a.indices + row * topk, qv, a.rq_ms, reinterpret_cast<const uint16_t*>(a.k),
+                          reinterpret_cast<const uint16_t*>(a.v), b, h, grp, sub, fixed_max, mrun, t1, t2, esum, ak,
+                          av);
+  } else {
+    gather_slots<X, VEC>(a, s0, s1, a.indices + row * topk, a.scores + row * topk,
+                         a.slot_valid ? a.slot_valid + row * topk : nullptr, reinterpret_cast<const X*>(a.k),
+                         reinterpret_cast<const X*>(a.v), b, h, grp, sub, lpr, fixed_max, mrun, t1, t2, esum, ak,
+                         av);
+  }
   for (int o = lpr; o < 64; o <<= 1) {
 #pragma unroll
     for (int i = 0; i < NE; ++i) {
@@ -595,14 +698,19 @@ hipError_t launch_sparse_gather(const GatherArgs& a, hipStream_t st) {
   vec = vec && aligned(a.v) && (a.k == nullptr || aligned(a.k)) && (a.self_key == nullptr || aligned(a.self_key));
   if (a.nsplit > 0) {
     const dim3 pgrid((unsigned)((nrows * a.nsplit + 3) / 4));
-    if (vec) {
+    if (a.rq != nullptr) {
+      // the caller checked the form: bf16, D = 128, [B,Tk,H,D] keys, no slot mask, aligned rows
+      if (a.dtype != DT_BF16 || a.D != 128 || a.kv_hm != 0 || a.slot_valid != nullptr || !vec || a.k == nullptr)
+        return hipErrorInvalidValue;
+      gather_part_kernel<bf16_t, true, true><<<pgrid, 256, 0, st>>>(a, 16);
+    } else if (vec) {
       int lpr = 1;
       while (lpr * epv < a.D) lpr <<= 1;
-      if (a.dtype == DT_F32) gather_part_kernel<float, true><<<pgrid, 256, 0, st>>>(a, lpr);
-      else gather_part_kernel<bf16_t, true><<<pgrid, 256, 0, st>>>(a, lpr);
+      if (a.dtype == DT_F32) gather_part_kernel<float, true, false><<<pgrid, 256, 0, st>>>(a, lpr);
+      else gather_part_kernel<bf16_t, true, false><<<pgrid, 256, 0, st>>>(a, lpr);
     } else {
-      if (a.dtype == DT_F32) gather_part_kernel<float, false><<<pgrid, 256, 0, st>>>(a, 64);
-      else gather_part_kernel<bf16_t, false><<<pgrid, 256, 0, st>>>(a, 64);
+      if (a.dtype == DT_F32) gather_part_kernel<float, false, false><<<pgrid, 256, 0, st>>>(a, 64);
+      else gather_part_kernel<bf16_t, false, false><<<pgrid, 256, 0, st>>>(a, 64);
     }
   }
   const bool sp = a.nsplit > 0;

@@ -191,6 +191,10 @@ struct GatherArgs {
   int nsplit;                // > 0: split-row form, nsplit partials of split_len slots per row
   int split_len;
   float* part;               // [B,H,Tq,nsplit,4+2D] partials (split-row form)
+  const void* rq;            // split-row form, bf16, D = 128, [B,Tk,H,D] keys: [B,Tq,H,D] queries whose slot
+                             // scores (q . k) * rq_ms the partial kernel computes from the key rows it gathers
+                             // (scores is then not read), or nullptr
+  float rq_ms;
 };
 
 // Split-row gather: used for at most GATHER_SPLIT_ROWS rows with more than

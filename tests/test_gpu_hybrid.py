@@ -21,10 +21,10 @@ pytestmark = pytest.mark.gpu
 import sgsa_amd  # noqa: E402  (pure Python; the HIP library loads on first call and raises if missing)
 
 
-def _model(dev, dtype, seed=0):
+def _model(dev, dtype, seed=0, top_k=32):
     from sgsa_amd.hybrid import HybridConfig, HybridForCausalLM
     cfg = HybridConfig(vocab_size=512, hidden_size=256, intermediate_size=512, num_hidden_layers=5,
-                       num_attention_heads=2, num_kv_heads=1, top_k=32, topk_recompute_every=4)
+                       num_attention_heads=2, num_kv_heads=1, top_k=top_k, topk_recompute_every=4)
     m = HybridForCausalLM(cfg)
     m.init_weights(0.02, qk_std=(cfg.hidden_size * cfg.head_dim) ** -0.5, generator=torch.Generator().manual_seed(seed))
     return cfg, m.to(dev, dtype).eval()
@@ -70,14 +70,17 @@ def test_hybrid_bf16_greedy_generation(dev):
     assert torch.equal(toks, toks2) and torch.equal(logits, logits2), "not deterministic"
 
 
-def test_decode_stack_equals_the_per_layer_path(dev):
+@pytest.mark.parametrize("top_k,T", [(32, 160), (320, 600)])
+def test_decode_stack_equals_the_per_layer_path(dev, top_k, T):
     # sgsa_decode_stack (one call per step) against the per-layer Python path on copies of
     # the same prefilled caches: logits equal bit for bit on selecting and re-scoring steps,
-    # and so are the SGSA states and caches after the last step
+    # and so are the SGSA states and caches after the last step.  top_k 320 takes the
+    # split-row gather (3 partials per row, the last one short), where the stack re-scores
+    # the kept candidates inside the gather and the per-layer path scores them first
     import sgsa_amd.hybrid as HY
-    cfg, m = _model(dev, torch.bfloat16, seed=6)
+    cfg, m = _model(dev, torch.bfloat16, seed=6, top_k=top_k)
     g = torch.Generator().manual_seed(7)
-    B, T, n = 3, 160, 9
+    B, n = 3, 9
     prompt = torch.randint(0, cfg.vocab_size, (B, T), generator=g).to(dev)
     toks = torch.randint(0, cfg.vocab_size, (B, n), generator=g).to(dev)
     rope = HY.rope_tables(T + n, cfg.head_dim, cfg.rope_theta, dev)
