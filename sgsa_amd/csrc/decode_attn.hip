@@ -7,7 +7,8 @@
 //
 // Split over key blocks of 256, three launches:
 //   scores  (block, b*Hkv + kh): the G = H / Hkv query heads sharing kv head kh
-//           against the block's keys, one key per thread; the rounded scores go
+//           against the block's keys (bf16: on MFMA, 16 keys per product; fp32:
+//           one key per thread); the rounded scores go
 //           to the workspace, and each head's block maximum and sum of
 //           exp(s - max) to a partial.
 //   pv      (block, b*Hkv + kh): each head's softmax normaliser from all the
@@ -96,6 +97,89 @@ __global__ __launch_bounds__(256) void dattn_scores_kernel(const X* __restrict__
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) e += __shfl_xor(e, o, 64);
     if (lane == 0) red[g][w][1] = e;
+  }
+  __syncthreads();
+  if (tid < G) {
+    const int g = tid;
+    const float mx = fmaxf(fmaxf(red[g][0][0], red[g][1][0]), fmaxf(red[g][2][0], red[g][3][0]));
+    const float l = (red[g][0][1] + red[g][1][1]) + (red[g][2][1] + red[g][3][1]);
+    part[((long)b * H + kh * G + g) * nblk + blk] = make_float2(mx, l);
+  }
+}
+
+// bf16 form of dattn_scores_kernel, the products on v_mfma_f32_16x16x32_bf16: A = the
+// group's G query heads (rows past G zero), B = 16 keys, dims 32 s + 8 lg + e at
+// k-position 8 lg + e of step s.  Lane (lc, lg) loads 64-byte pieces of 16 key rows per
+// instruction (16 rows x 64 B) where the one-key-per-thread form touches 64 rows x 16 B,
+// and holds C[4 lg + e][lc], head 4 lg + e's score of key 16 kg + lc.  The rounding
+// points, the stores and the per-head block statistics are those of the fp32 form.
+template <int G>
+__global__ __launch_bounds__(256) void dattn_scores_mfma_kernel(const bf16_t* __restrict__ q,
+                                                                const bf16_t* __restrict__ kc, int H, int Hkv,
+                                                                long Tmax, int kend, int nblk, float scale,
+                                                                bf16_t* __restrict__ sws, float2* __restrict__ part) {
+  static_assert(G <= 16, "one 16-row A operand holds the group's heads");
+  __shared__ float red[G][4][2];
+  const int blk = blockIdx.x, bk = blockIdx.y;
+  const int b = bk / Hkv, kh = bk % Hkv;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int lc = lane & 15, lg = lane >> 4;
+  const bf16_t tag{};
+  const uint16_t* qh = reinterpret_cast<const uint16_t*>(q) + ((long)b * H + kh * G + min(lc, G - 1)) * DA_D + 8 * lg;
+  const uint16_t* kb = reinterpret_cast<const uint16_t*>(kc) + (long)bk * Tmax * DA_D + 8 * lg;
+  const int j0 = blk * DA_KB + 64 * w;   // the wave's 64 keys, 16 kg + lc
+  u16x8 kr[4][4];
+#pragma unroll
+  for (int kg = 0; kg < 4; ++kg) {
+    const int j = min(j0 + 16 * kg + lc, kend - 1);   // keys past kend re-read the last one and are not used
+#pragma unroll
+    for (int s = 0; s < 4; ++s) kr[kg][s] = *reinterpret_cast<const u16x8*>(kb + (long)j * DA_D + 32 * s);
+  }
+  bf16x8 qa[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const u16x8 z = {0, 0, 0, 0, 0, 0, 0, 0};
+    qa[s] = __builtin_bit_cast(bf16x8, lc < G ? *reinterpret_cast<const u16x8*>(qh + 32 * s) : z);
+  }
+  constexpr int NE = G < 4 ? G : 4;   // heads 4 lg + e < G held per lane
+  float sc[4][NE], mh[NE];
+#pragma unroll
+  for (int e = 0; e < NE; ++e) mh[e] = -INFINITY;
+  const bool hl = 4 * lg < G;          // lanes whose rows are real heads
+#pragma unroll
+  for (int kg = 0; kg < 4; ++kg) {
+    f4 c = f4_zero();
+#pragma unroll
+    for (int s = 0; s < 4; ++s) c = mma_bf16(qa[s], __builtin_bit_cast(bf16x8, kr[kg][s]), c);
+    const int j = j0 + 16 * kg + lc;
+    const bool valid = j < kend;
+#pragma unroll
+    for (int e = 0; e < NE; ++e) {
+      const int g = 4 * lg + e;
+      const float s = da_round(da_round(c[e], tag) * scale, tag);
+      sc[kg][e] = s;
+      if (hl && valid) st(sws, ((long)b * H + kh * G + g) * kend + j, s);
+      mh[e] = valid ? fmaxf(mh[e], s) : mh[e];
+    }
+  }
+  // head g = 4 lg + e: its 64 scores of the wave sit in lanes 16 lg .. 16 lg + 15 (4 each)
+#pragma unroll
+  for (int e = 0; e < NE; ++e) {
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) mh[e] = fmaxf(mh[e], __shfl_xor(mh[e], o, 64));
+    if (hl && lc == 0) red[4 * lg + e][w][0] = mh[e];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int e = 0; e < NE; ++e) {
+    const int g = min(4 * lg + e, G - 1);
+    const float m = fmaxf(fmaxf(red[g][0][0], red[g][1][0]), fmaxf(red[g][2][0], red[g][3][0]));
+    float x = 0.f;
+#pragma unroll
+    for (int kg = 0; kg < 4; ++kg) x += j0 + 16 * kg + lc < kend ? expf(sc[kg][e] - m) : 0.f;
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) x += __shfl_xor(x, o, 64);
+    if (hl && lc == 0) red[4 * lg + e][w][1] = x;
   }
   __syncthreads();
   if (tid < G) {
@@ -244,7 +328,18 @@ hipError_t launch_t(int B, int H, int Hkv, const void* q, const void* kc, const 
   float* opart = reinterpret_cast<float*>(p);
   const dim3 grid((unsigned)nblk, (unsigned)(B * Hkv));
   const float scale = (float)(1.0 / 11.313708498984761);   // 1 / sqrt(128), as the fp32 of the double
-  dattn_scores_kernel<X, G><<<grid, 256, 0, st>>>((const X*)q, (const X*)kc, H, Hkv, Tmax, kend, nblk, scale, sws, part);
+  const bool al16 = (((uintptr_t)q | (uintptr_t)kc) & 15u) == 0;
+  if constexpr (sizeof(X) == 2) {
+    if (al16)
+      dattn_scores_mfma_kernel<G><<<grid, 256, 0, st>>>((const bf16_t*)q, (const bf16_t*)kc, H, Hkv, Tmax, kend, nblk,
+                                                         scale, sws, part);
+    else
+      dattn_scores_kernel<X, G><<<grid, 256, 0, st>>>((const X*)q, (const X*)kc, H, Hkv, Tmax, kend, nblk, scale, sws,
+                                                      part);
+  } else {
+    dattn_scores_kernel<X, G><<<grid, 256, 0, st>>>((const X*)q, (const X*)kc, H, Hkv, Tmax, kend, nblk, scale, sws,
+                                                    part);
+  }
   dattn_pv_kernel<X, G><<<grid, 256, 0, st>>>(sws, part, (const X*)vc, H, Hkv, Tmax, kend, nblk, opart);
   dattn_reduce_kernel<X><<<dim3((unsigned)BH), 128, 0, st>>>(opart, nblk, (X*)out);
   return hipGetLastError();
