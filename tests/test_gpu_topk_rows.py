@@ -25,6 +25,8 @@ def _inputs(dev, B, Tq, Tk, H, D, seed, dup=False):
 
 @pytest.mark.parametrize("B,Tq,Tk,H,D,top_k,q_offset,causal,dup", [
     (8, 1, 16640, 16, 128, 2048, 16383, True, False),   # config-4 decode: 16384 valid of a 16640 buffer
+    (3, 1, 4000, 16, 128, 300, 1000, True, True),        # 1001 valid keys (not a multiple of 16), ties
+    (2, 1, 3001, 16, 128, 512, 0, False, False),         # not causal, Tk % 16 = 9
     (2, 1, 5000, 4, 64, 700, 4999, True, True),          # ties at the cut
     (1, 4, 3000, 2, 96, 512, 100, True, False),          # rows with fewer valid keys than top_k
     (2, 3, 2048, 2, 32, 64, 0, False, False),            # not causal
