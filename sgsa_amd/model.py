@@ -24,10 +24,14 @@ activation are one HIP launch each.  RMSNorm and GatedMLP are the fla-core
 modules the reference imports (modeling_sgsa.py:40-41); their arithmetic is the
 in-tree restatement of modelings/hybrid_dense_delta_topk.py:94-117.
 
-Forward only: the retrieval half has no backward, so SGSABlock and
-SGSAForCausalLM raise when autograd would record them (run them under
-torch.no_grad() or torch.inference_mode()) instead of returning a loss whose
-gradients silently miss the attention parameters.
+Training (token_only): under autograd the block selects with K1 on the GPU as
+above, then computes the weights, gathers, diagnostics and write gate of the
+selected rows as differentiable torch ops (``retrieval_grad.py``, the
+reference's own structure over the k slots) and runs the state update through
+chunk_sgsa / fused_recurrent_sgsa, whose backward is native; every parameter
+gets its gradient.  The block retrieval modes have no backward: under autograd
+they raise instead of returning a loss whose gradients silently miss their
+projections.
 """
 
 from __future__ import annotations
@@ -45,6 +49,7 @@ from . import _abi
 from .layer import LayerWorkspace, sgsa_block_layer_retrieve, sgsa_layer_forward, sgsa_layer_retrieve
 from .ops import chunk_sgsa
 from .recurrent import fused_recurrent_sgsa
+from .retrieval_grad import retrieve_differentiable
 
 Tensor = torch.Tensor
 
@@ -258,18 +263,22 @@ _STATE_BACKENDS = {"auto": "chunk", "torch_chunk": "chunk", "recurrent": "recurr
 _RETRIEVAL_MODES = ("token_only", "block_only", "block_token")
 
 
+def needs_grad(module: nn.Module, *inputs: Tensor) -> bool:
+    """Whether autograd records ``module`` on ``inputs``."""
+    return torch.is_grad_enabled() and (any(t.requires_grad for t in inputs) or
+                                        any(p.requires_grad for p in module.parameters()))
+
+
 def refuse_autograd(module: nn.Module, *inputs: Tensor) -> None:
-    """Raise when autograd would record ``module`` on ``inputs``: the SGSA retrieval (top-k
-    select, weights, gathers, gate) has no backward here, so a loss through it would leave
-    the q/k/v/q_ret projections and the gates without gradients."""
-    if not torch.is_grad_enabled():
-        return
-    if any(t.requires_grad for t in inputs) or any(p.requires_grad for p in module.parameters()):
+    """Raise when autograd would record ``module`` on ``inputs`` and the module has no
+    differentiable form there, so a loss through it cannot leave parameters without
+    gradients."""
+    if needs_grad(module, *inputs):
         raise RuntimeError(
-            f"{type(module).__name__}.forward is forward-only: the SGSA retrieval half has no backward in this "
-            "build, so gradients would silently miss its projections. Run it under torch.no_grad() or "
-            "torch.inference_mode(), or freeze its parameters (requires_grad_(False)); chunk_sgsa and "
-            "fused_recurrent_sgsa themselves are differentiable.")
+            f"{type(module).__name__}.forward is forward-only in this configuration: the block retrieval modes "
+            "have no backward in this build, so gradients would silently miss their projections. Use "
+            "retrieval_mode='token_only' to train, or run under torch.no_grad() / torch.inference_mode(), or "
+            "freeze the parameters (requires_grad_(False)).")
 
 
 class SGSABlock(nn.Module):
@@ -335,10 +344,17 @@ class SGSABlock(nn.Module):
         ``linear_backend`` the chunked or the token-recurrent update (:554-609).
         The metrics are the reference's: alpha_mean, k_hat_perp_ratio_mean
         (residual write mode, else 0), retrieval_confidence_mean (mean largest
-        retrieval weight) and the path flags.  Raises under autograd (no
-        retrieval backward).
+        retrieval weight) and the path flags.
+
+        Under autograd (token_only) the retrieval and the write gate take their
+        differentiable form (``retrieve_differentiable``: K1's selection, then
+        the weights, gathers and gate as torch ops on the selected rows) and the
+        state update its native backward, so every projection gets its
+        gradient; the block retrieval modes raise there.
         """
-        refuse_autograd(self, h)
+        grad = needs_grad(self, h)
+        if grad and self.config.retrieval_mode != "token_only":
+            refuse_autograd(self, h)
         cfg = self.config
         B, T, C = h.shape
         q, k, v, q_ret, beta, gamma, budget = self._project(h)
@@ -348,7 +364,15 @@ class SGSABlock(nn.Module):
         # with write_mode "none" the reference's write key is k_hat (:546-550): alpha as "direct"
         wm = "residual" if cfg.sgsa_write_mode == "residual" else "direct"
         vh = None
-        if cfg.retrieval_mode == "token_only" and backend == "chunk" and sparse and cfg.sparse_output_lambda <= 0:
+        if grad:
+            wk, vh, al, stats = retrieve_differentiable(q_ret, k, v, budget, cfg.top_k, wm, cfg.alpha_max, cfg.tau_c,
+                                                        attention_mask=attention_mask)
+            sk, sv, sa = (wk, vh, al) if sparse else (None, None, None)
+            if backend == "chunk":
+                att, _ = chunk_sgsa(q, k, v, beta, gamma, sk, sv, sa)
+            else:
+                att, _ = fused_recurrent_sgsa(q, k, v, beta, gamma, sk, sv, sa)
+        elif cfg.retrieval_mode == "token_only" and backend == "chunk" and sparse and cfg.sparse_output_lambda <= 0:
             att, _ = sgsa_layer_forward(q, k, v, q_ret, beta, gamma, budget, cfg.top_k, write_mode=wm,
                                         alpha_max=cfg.alpha_max, tau_c=cfg.tau_c, output_final_state=False,
                                         workspace=self._ws, attention_mask=attention_mask, stats=stats)
@@ -423,8 +447,8 @@ class SGSAForCausalLM(nn.Module):
         """SGSAForCausalLM.forward (modeling_sgsa.py:733-767): {"logits", "metrics"}
         and, with labels, "loss" -- the next-token cross entropy with ignore_index
         -100 (:758-766).  attention_mask [B,T] zeroes the padded embeddings
-        (:740-741) and masks padded keys and queries in every retrieval."""
-        refuse_autograd(self)
+        (:740-741) and masks padded keys and queries in every retrieval.  Trains
+        (autograd through every layer) with retrieval_mode token_only."""
         B, T = input_ids.shape
         if T > self.config.max_position_embeddings:
             raise ValueError("sequence length exceeds max_position_embeddings")

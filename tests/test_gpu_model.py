@@ -4,8 +4,9 @@ parameters, rounded to the model's dtype; for a bf16 model the oracle also
 rounds each stored activation to bf16, so each layer is compared on the
 inputs the model actually feeds it.  Every retrieval mode (token_only and the
 reference config's default block_token, block_only), write mode (none, direct,
-residual) and state backend (chunked, recurrent) is covered; forward only, so
-the model refuses to run while autograd records it.
+residual) and state backend (chunked, recurrent) is covered; token_only also
+under autograd, every parameter's gradient against autograd through the oracle
+(the block modes have no backward and refuse to run while autograd records them).
 
 The projections use the reference's init (normal, std 0.02) except q/k/q_ret,
 whose std 1/sqrt(C*D) keeps |k| ~ 1: at std 0.02 the delta-rule transition
@@ -179,11 +180,58 @@ def test_model_state_backends_and_write_mode_none(dev, backend, flag, write_mode
             assert out["metrics"][f"layer_{i}_{name}"].item() == (1.0 if name == flag else 0.0), name
 
 
-def test_model_refuses_autograd(dev):
-    # the retrieval half has no backward: a loss through the model under autograd would
-    # leave q/k/v/q_ret and the gates without gradients, so the forward raises instead
+@pytest.mark.parametrize("write_mode,lam,mask", [("direct", 0.0, False), ("residual", 0.5, False),
+                                                 ("direct", 0.0, True)])
+def test_model_gradients_match_oracle(dev, write_mode, lam, mask):
+    # training through the token_only model: every parameter's gradient of the next-token loss
+    # against torch autograd through the fp32 oracle model (the reference's structure: top-k
+    # values, softmax weights, gathers, diagnostics and gate all differentiable) on the same
+    # parameters, relative to each gradient's largest magnitude
+    H, D, L, T, V = 2, 64, 2, 48, 64
+    cfg, m = _model(dev, torch.float32, vocab_size=V, hidden_size=H * D, intermediate_size=192, num_hidden_layers=L,
+                    num_attention_heads=H, num_kv_heads=H, max_position_embeddings=64, top_k=8,
+                    sgsa_write_mode=write_mode, sparse_output_lambda=lam, retrieval_mode="token_only",
+                    tie_word_embeddings=False)
+    m.train()
+    g = torch.Generator().manual_seed(2)
+    ids = torch.randint(1, V, (2, T), generator=g)
+    am = None
+    if mask:   # left padding of 5 and 0 tokens
+        am = torch.ones(2, T, dtype=torch.int64)
+        am[0, :5] = 0
+    labels = ids.clone()
+    if am is not None:
+        labels[am == 0] = -100
+    out = m(ids.to(dev), attention_mask=None if am is None else am.to(dev), labels=labels.to(dev))
+    out["loss"].backward()
+    torch.cuda.synchronize()
+    params = {k: v.detach().float().cpu().clone().requires_grad_(True) for k, v in m.state_dict().items()}
+    logits = O.sgsa_model_forward(params, ids, num_layers=L, num_heads=H, top_k=8, write_mode=write_mode,
+                                  sparse_output_lambda=lam, attention_mask=am)
+    loss = torch.nn.functional.cross_entropy(logits[:, :-1].reshape(-1, V), labels[:, 1:].reshape(-1),
+                                             ignore_index=-100)
+    loss.backward()
+    assert abs(out["loss"].item() - loss.item()) <= 1e-4 * abs(loss.item())
+    named = dict(m.named_parameters())
+    for name, p in params.items():
+        got = named[name].grad
+        if p.grad is None:
+            assert got is None or float(got.abs().max()) == 0.0, name
+            continue
+        assert got is not None, f"{name}: no gradient"
+        err = _rel(got, p.grad)
+        assert err <= 2e-3, f"{name}: gradient error {err:.3e} relative to its largest magnitude"
+    for i in range(L):   # the retrieval half's own parameters are reached
+        for proj in ("q_ret_proj", "budget_proj", "k_proj", "v_proj"):
+            assert float(named[f"layers.{i}.{proj}.weight"].grad.abs().max()) > 0, proj
+
+
+def test_block_modes_refuse_autograd(dev):
+    # the block retrieval modes have no backward: a loss through them under autograd would
+    # leave their projections without gradients, so the forward raises instead
     cfg, m = _model(dev, torch.float32, vocab_size=64, hidden_size=128, intermediate_size=128, num_hidden_layers=1,
-                    num_attention_heads=2, num_kv_heads=2, max_position_embeddings=64, top_k=4)
+                    num_attention_heads=2, num_kv_heads=2, max_position_embeddings=64, top_k=4,
+                    retrieval_mode="block_token", block_size=8, top_blocks=2)
     ids = torch.randint(1, 64, (1, 16)).to(dev)
     with pytest.raises(RuntimeError, match="forward-only"):
         m(ids, labels=ids)
