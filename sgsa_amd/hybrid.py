@@ -561,15 +561,48 @@ def topk_kv_reuse_attention(query: Tensor, key: Tensor, value: Tensor, top_k: in
     return r["v_hat"], idx.long(), r["weights"]
 
 
+def topk_kv_reuse_attention_grad(query: Tensor, key: Tensor, value: Tensor, top_k: int,
+                                 attention_mask: Optional[Tensor] = None) -> Tensor:
+    """``topk_kv_reuse_attention``'s attended [B,Q,H,D] in a form autograd differentiates
+    in query, key and value: the masked select on the GPU under no_grad (the same kernel,
+    slot rule and tie order; the indices are constants of the step, as torch.topk's are to
+    autograd in the reference), then the selected slots' scores q.k / sqrt(D) (finfo.min on
+    masked slots, :346), their fp32 softmax (:350) and the probability-weighted value rows
+    (:351-356) as torch ops on the [B,H,Q,k,D] selected rows."""
+    B, Q, H, D = query.shape
+    K = key.shape[2]
+    if key.shape != (B, H, K, D) or value.shape != key.shape:
+        raise ValueError(f"key/value must be [B,H,K,D] = {(B, H, K, D)}; got {tuple(key.shape)} / {tuple(value.shape)}")
+    if Q > K:
+        raise ValueError(f"{Q} queries over {K} keys: the queries are the last Q positions of the KV")
+    with torch.no_grad():
+        idx, _, valid, _, _, _ = score_topk_masked(query.detach(), key.detach(), top_k, key_mask=attention_mask,
+                                                   causal=True, q_offset=K - Q, scale_mode=1, kq_rule=1,
+                                                   kv_layout=1, sorted=True)
+        kk = idx.shape[-1]
+        rows = (torch.arange(B * H, device=idx.device, dtype=torch.long).view(B, H, 1, 1) * K
+                + idx.long()).reshape(-1)
+        valid = valid.to(torch.bool)
+    qh = query.float().transpose(1, 2).contiguous()                       # [B,H,Q,D]
+    ksel = key.float().reshape(B * H * K, D).index_select(0, rows).view(B, H, Q, kk, D)
+    vsel = value.float().reshape(B * H * K, D).index_select(0, rows).view(B, H, Q, kk, D)
+    sc = torch.matmul(ksel, qh.unsqueeze(-1)).squeeze(-1) * (1.0 / math.sqrt(D))
+    sc = torch.where(valid, sc, torch.full_like(sc, torch.finfo(torch.float32).min))
+    p = torch.softmax(sc, dim=-1)
+    out = torch.matmul(p.unsqueeze(-2), vsel).squeeze(-2)                 # [B,H,Q,D]
+    return out.transpose(1, 2).to(value.dtype)
+
+
 class TopKSparseKVReuseAttention(nn.Module):
     """Top-k sparse attention over the nearest previous dense layer's KV cache
     (modelings/hybrid_dense_delta_topk.py:317-358): q_proj, RoPE at offset
     K-Q, the masked top-k select and V-only gather of ``topk_kv_reuse_attention``,
     o_proj.  Same constructor config fields (num_attention_heads, head_dim or
-    hidden_size, top_k, dropout) and forward signature.  Forward only: the
-    kernels' outputs carry no autograd graph, so the module refuses to run
-    where gradients are being recorded, and dropout on the probabilities
-    (training with dropout > 0) is not supported.
+    hidden_size, top_k, dropout) and forward signature.  Where autograd records
+    it, the select stays on the GPU kernels and the softmax and the value sum
+    take their differentiable form (``topk_kv_reuse_attention_grad``), so q_proj,
+    o_proj, the hidden states and the dense KV get their gradients; dropout on
+    the probabilities (training with dropout > 0) is not supported.
     """
 
     def __init__(self, config) -> None:
@@ -584,9 +617,6 @@ class TopKSparseKVReuseAttention(nn.Module):
 
     def forward(self, hidden_states: Tensor, dense_kv: Tuple[Tensor, Tensor], rope: Tuple[Tensor, Tensor],
                 attention_mask: Optional[Tensor]) -> Tensor:
-        if torch.is_grad_enabled() and any(p.requires_grad for p in self.parameters()):
-            raise RuntimeError("TopKSparseKVReuseAttention runs forward-only HIP kernels; call it under "
-                               "torch.no_grad() / torch.inference_mode()")
         if self.training and self.dropout_p > 0:
             raise NotImplementedError("dropout on the top-k probabilities is not supported")
         B, Q, _ = hidden_states.shape
@@ -607,6 +637,12 @@ class TopKSparseKVReuseAttention(nn.Module):
         s = sin[off:off + Q].to(query.dtype)[None, :, None, :]
         half = D // 2
         query = query * c + torch.cat((-query[..., half:], query[..., :half]), dim=-1) * s
-        attended, _, _ = topk_kv_reuse_attention(query.contiguous(), key.to(query.dtype), value.to(query.dtype),
-                                                 self.top_k, attention_mask)
+        grad = torch.is_grad_enabled() and (hidden_states.requires_grad or key.requires_grad or
+                                            value.requires_grad or any(p.requires_grad for p in self.parameters()))
+        if grad:
+            attended = topk_kv_reuse_attention_grad(query, key.to(query.dtype), value.to(query.dtype), self.top_k,
+                                                    attention_mask)
+        else:
+            attended, _, _ = topk_kv_reuse_attention(query.contiguous(), key.to(query.dtype), value.to(query.dtype),
+                                                     self.top_k, attention_mask)
         return self.o_proj(attended.reshape(B, Q, H * D))

@@ -8,7 +8,8 @@ merged mask (modelings/hybrid_dense_delta_topk.py:153-175, :343-356).
   valid flags, counts and each row's k_q.
 * Values: k_hat / v_hat / weights / diagnostics of the masked retrieval, the
   masked layer (write key, v_hat, alpha, output, final state) and the KV-reuse
-  attention against the oracle within the stated tolerances.
+  attention against the oracle within the stated tolerances; the KV-reuse
+  module's gradients under autograd against autograd through the oracle.
 * The threshold form under a mask (bf16, d = 128: the layer's keys compacted
   valid-first, per-row valid prefix and slot count in score_thr128_kernel, its
   radix fallback and gather_thr_kernel) against the oracle layer, bit-equal to
@@ -275,5 +276,23 @@ def test_kv_reuse_module_matches_reference_formula(dev):
         ref = m.o_proj(att.transpose(1, 2).reshape(2, Q, C).to(dev))
     torch.cuda.synchronize()
     close(y, ref, 1e-4, "module output")
-    with pytest.raises(RuntimeError):
-        m(hs, (key, val), rope, am.to(dev))   # gradients being recorded
+    # under autograd: gradients of q_proj, o_proj, the hidden states and the dense KV
+    # against torch autograd through the oracle's formula on the CPU (fp32)
+    hs_g, key_g, val_g = (t.clone().requires_grad_(True) for t in (hs, key, val))
+    wout = torch.randn(2, Q, C, generator=g)
+    y = m(hs_g, (key_g, val_g), rope, am.to(dev))
+    (y * wout.to(dev)).sum().backward()
+    torch.cuda.synchronize()
+    qw, ow = (m.q_proj.weight.detach().cpu().requires_grad_(True), m.o_proj.weight.detach().cpu().requires_grad_(True))
+    hs_c, key_c, val_c = (t.detach().cpu().requires_grad_(True) for t in (hs, key, val))
+    qh = (hs_c @ qw.T).view(2, Q, H, D).transpose(1, 2)
+    qh = qh * c + torch.cat((-qh[..., D // 2:], qh[..., :D // 2]), dim=-1) * s
+    att, _, _ = O.topk_kv_reuse_attention(qh, key_c, val_c, k, attention_mask=am)
+    yr = att.transpose(1, 2).reshape(2, Q, C) @ ow.T
+    close(y.detach(), yr.detach(), 1e-4, "module output under autograd")
+    (yr * wout).sum().backward()
+    for name, got, want in (("q_proj", m.q_proj.weight.grad, qw.grad), ("o_proj", m.o_proj.weight.grad, ow.grad),
+                            ("hidden states", hs_g.grad, hs_c.grad), ("key", key_g.grad, key_c.grad),
+                            ("value", val_g.grad, val_c.grad)):
+        assert got is not None, f"{name}: no gradient"
+        close(got, want, 1e-4, f"gradient of {name}")
