@@ -24,14 +24,12 @@ activation are one HIP launch each.  RMSNorm and GatedMLP are the fla-core
 modules the reference imports (modeling_sgsa.py:40-41); their arithmetic is the
 in-tree restatement of modelings/hybrid_dense_delta_topk.py:94-117.
 
-Training (token_only): under autograd the block selects with K1 on the GPU as
-above, then computes the weights, gathers, diagnostics and write gate of the
-selected rows as differentiable torch ops (``retrieval_grad.py``, the
-reference's own structure over the k slots) and runs the state update through
-chunk_sgsa / fused_recurrent_sgsa, whose backward is native; every parameter
-gets its gradient.  The block retrieval modes have no backward: under autograd
-they raise instead of returning a loss whose gradients silently miss their
-projections.
+Training: under autograd the block selects on the GPU as above (K1, or the
+block retrieval), then computes the weights, gathers, diagnostics and write
+gate of the selected rows as differentiable torch ops (``retrieval_grad.py``,
+the reference's own structure over the selected slots) and runs the state
+update through chunk_sgsa / fused_recurrent_sgsa, whose backward is native;
+every parameter gets its gradient, in every retrieval mode.
 """
 
 from __future__ import annotations
@@ -49,7 +47,7 @@ from . import _abi
 from .layer import LayerWorkspace, sgsa_block_layer_retrieve, sgsa_layer_forward, sgsa_layer_retrieve
 from .ops import chunk_sgsa
 from .recurrent import fused_recurrent_sgsa
-from .retrieval_grad import retrieve_differentiable
+from .retrieval_grad import retrieve_block_differentiable, retrieve_differentiable
 
 Tensor = torch.Tensor
 
@@ -269,18 +267,6 @@ def needs_grad(module: nn.Module, *inputs: Tensor) -> bool:
                                         any(p.requires_grad for p in module.parameters()))
 
 
-def refuse_autograd(module: nn.Module, *inputs: Tensor) -> None:
-    """Raise when autograd would record ``module`` on ``inputs`` and the module has no
-    differentiable form there, so a loss through it cannot leave parameters without
-    gradients."""
-    if needs_grad(module, *inputs):
-        raise RuntimeError(
-            f"{type(module).__name__}.forward is forward-only in this configuration: the block retrieval modes "
-            "have no backward in this build, so gradients would silently miss their projections. Use "
-            "retrieval_mode='token_only' to train, or run under torch.no_grad() / torch.inference_mode(), or "
-            "freeze the parameters (requires_grad_(False)).")
-
-
 class SGSABlock(nn.Module):
     def __init__(self, config: SGSAConfig) -> None:
         super().__init__()
@@ -346,15 +332,13 @@ class SGSABlock(nn.Module):
         (residual write mode, else 0), retrieval_confidence_mean (mean largest
         retrieval weight) and the path flags.
 
-        Under autograd (token_only) the retrieval and the write gate take their
-        differentiable form (``retrieve_differentiable``: K1's selection, then
-        the weights, gathers and gate as torch ops on the selected rows) and the
-        state update its native backward, so every projection gets its
-        gradient; the block retrieval modes raise there.
+        Under autograd the retrieval and the write gate take their
+        differentiable form (``retrieval_grad.py``: the selection on the GPU,
+        then the weights, gathers and gate as torch ops on the selected rows)
+        and the state update its native backward, so every projection gets its
+        gradient, in every retrieval mode.
         """
         grad = needs_grad(self, h)
-        if grad and self.config.retrieval_mode != "token_only":
-            refuse_autograd(self, h)
         cfg = self.config
         B, T, C = h.shape
         q, k, v, q_ret, beta, gamma, budget = self._project(h)
@@ -365,8 +349,14 @@ class SGSABlock(nn.Module):
         wm = "residual" if cfg.sgsa_write_mode == "residual" else "direct"
         vh = None
         if grad:
-            wk, vh, al, stats = retrieve_differentiable(q_ret, k, v, budget, cfg.top_k, wm, cfg.alpha_max, cfg.tau_c,
-                                                        attention_mask=attention_mask)
+            if cfg.retrieval_mode == "token_only":
+                wk, vh, al, stats = retrieve_differentiable(q_ret, k, v, budget, cfg.top_k, wm, cfg.alpha_max,
+                                                            cfg.tau_c, attention_mask=attention_mask)
+            else:
+                wk, vh, al, stats = retrieve_block_differentiable(q_ret, k, v, budget, cfg.top_k, cfg.block_size,
+                                                                  cfg.top_blocks, cfg.retrieval_mode, wm,
+                                                                  cfg.alpha_max, cfg.tau_c,
+                                                                  attention_mask=attention_mask)
             sk, sv, sa = (wk, vh, al) if sparse else (None, None, None)
             if backend == "chunk":
                 att, _ = chunk_sgsa(q, k, v, beta, gamma, sk, sv, sa)

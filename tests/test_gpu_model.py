@@ -4,9 +4,9 @@ parameters, rounded to the model's dtype; for a bf16 model the oracle also
 rounds each stored activation to bf16, so each layer is compared on the
 inputs the model actually feeds it.  Every retrieval mode (token_only and the
 reference config's default block_token, block_only), write mode (none, direct,
-residual) and state backend (chunked, recurrent) is covered; token_only also
-under autograd, every parameter's gradient against autograd through the oracle
-(the block modes have no backward and refuse to run while autograd records them).
+residual) and state backend (chunked, recurrent) is covered, and every mode
+also under autograd: every parameter's gradient against autograd through the
+oracle.
 
 The projections use the reference's init (normal, std 0.02) except q/k/q_ret,
 whose std 1/sqrt(C*D) keeps |k| ~ 1: at std 0.02 the delta-rule transition
@@ -180,18 +180,20 @@ def test_model_state_backends_and_write_mode_none(dev, backend, flag, write_mode
             assert out["metrics"][f"layer_{i}_{name}"].item() == (1.0 if name == flag else 0.0), name
 
 
-@pytest.mark.parametrize("write_mode,lam,mask", [("direct", 0.0, False), ("residual", 0.5, False),
-                                                 ("direct", 0.0, True)])
-def test_model_gradients_match_oracle(dev, write_mode, lam, mask):
-    # training through the token_only model: every parameter's gradient of the next-token loss
-    # against torch autograd through the fp32 oracle model (the reference's structure: top-k
-    # values, softmax weights, gathers, diagnostics and gate all differentiable) on the same
+@pytest.mark.parametrize("mode,write_mode,lam,mask", [
+    ("token_only", "direct", 0.0, False), ("token_only", "residual", 0.5, False), ("token_only", "direct", 0.0, True),
+    ("block_token", "direct", 0.0, False), ("block_token", "residual", 0.5, True),
+    ("block_only", "direct", 0.0, False), ("block_only", "direct", 0.0, True)])
+def test_model_gradients_match_oracle(dev, mode, write_mode, lam, mask):
+    # training through the model: every parameter's gradient of the next-token loss against
+    # torch autograd through the fp32 oracle model (the reference's structure: top-k values,
+    # softmax weights, gathers, diagnostics and gate all differentiable) on the same
     # parameters, relative to each gradient's largest magnitude
     H, D, L, T, V = 2, 64, 2, 48, 64
     cfg, m = _model(dev, torch.float32, vocab_size=V, hidden_size=H * D, intermediate_size=192, num_hidden_layers=L,
                     num_attention_heads=H, num_kv_heads=H, max_position_embeddings=64, top_k=8,
-                    sgsa_write_mode=write_mode, sparse_output_lambda=lam, retrieval_mode="token_only",
-                    tie_word_embeddings=False)
+                    sgsa_write_mode=write_mode, sparse_output_lambda=lam, retrieval_mode=mode, block_size=8,
+                    top_blocks=2, tie_word_embeddings=False)
     m.train()
     g = torch.Generator().manual_seed(2)
     ids = torch.randint(1, V, (2, T), generator=g)
@@ -207,7 +209,8 @@ def test_model_gradients_match_oracle(dev, write_mode, lam, mask):
     torch.cuda.synchronize()
     params = {k: v.detach().float().cpu().clone().requires_grad_(True) for k, v in m.state_dict().items()}
     logits = O.sgsa_model_forward(params, ids, num_layers=L, num_heads=H, top_k=8, write_mode=write_mode,
-                                  sparse_output_lambda=lam, attention_mask=am)
+                                  sparse_output_lambda=lam, attention_mask=am, retrieval_mode=mode, block_size=8,
+                                  top_blocks=2)
     loss = torch.nn.functional.cross_entropy(logits[:, :-1].reshape(-1, V), labels[:, 1:].reshape(-1),
                                              ignore_index=-100)
     loss.backward()
@@ -225,22 +228,3 @@ def test_model_gradients_match_oracle(dev, write_mode, lam, mask):
         for proj in ("q_ret_proj", "budget_proj", "k_proj", "v_proj"):
             assert float(named[f"layers.{i}.{proj}.weight"].grad.abs().max()) > 0, proj
 
-
-def test_block_modes_refuse_autograd(dev):
-    # the block retrieval modes have no backward: a loss through them under autograd would
-    # leave their projections without gradients, so the forward raises instead
-    cfg, m = _model(dev, torch.float32, vocab_size=64, hidden_size=128, intermediate_size=128, num_hidden_layers=1,
-                    num_attention_heads=2, num_kv_heads=2, max_position_embeddings=64, top_k=4,
-                    retrieval_mode="block_token", block_size=8, top_blocks=2)
-    ids = torch.randint(1, 64, (1, 16)).to(dev)
-    with pytest.raises(RuntimeError, match="forward-only"):
-        m(ids, labels=ids)
-    with pytest.raises(RuntimeError, match="forward-only"):
-        m.layers[0](torch.randn(1, 16, 128, device=dev))
-    with torch.no_grad():
-        out = m(ids, labels=ids)
-    assert torch.isfinite(out["loss"])
-    # parameters frozen and an input that needs no gradient: nothing to lose, it runs
-    m.requires_grad_(False)
-    out = m(ids, labels=ids)
-    assert torch.isfinite(out["loss"]) and out["loss"].grad_fn is None
