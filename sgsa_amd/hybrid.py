@@ -562,13 +562,14 @@ def topk_kv_reuse_attention(query: Tensor, key: Tensor, value: Tensor, top_k: in
 
 
 def topk_kv_reuse_attention_grad(query: Tensor, key: Tensor, value: Tensor, top_k: int,
-                                 attention_mask: Optional[Tensor] = None) -> Tensor:
+                                 attention_mask: Optional[Tensor] = None, dropout_p: float = 0.0) -> Tensor:
     """``topk_kv_reuse_attention``'s attended [B,Q,H,D] in a form autograd differentiates
     in query, key and value: the masked select on the GPU under no_grad (the same kernel,
     slot rule and tie order; the indices are constants of the step, as torch.topk's are to
     autograd in the reference), then the selected slots' scores q.k / sqrt(D) (finfo.min on
     masked slots, :346), their fp32 softmax (:350) and the probability-weighted value rows
-    (:351-356) as torch ops on the [B,H,Q,k,D] selected rows."""
+    (:351-356) as torch ops on the [B,H,Q,k,D] selected rows; ``dropout_p`` > 0 drops
+    probabilities as training does (:351)."""
     B, Q, H, D = query.shape
     K = key.shape[2]
     if key.shape != (B, H, K, D) or value.shape != key.shape:
@@ -589,6 +590,8 @@ def topk_kv_reuse_attention_grad(query: Tensor, key: Tensor, value: Tensor, top_
     sc = torch.matmul(ksel, qh.unsqueeze(-1)).squeeze(-1) * (1.0 / math.sqrt(D))
     sc = torch.where(valid, sc, torch.full_like(sc, torch.finfo(torch.float32).min))
     p = torch.softmax(sc, dim=-1)
+    if dropout_p > 0:
+        p = torch.nn.functional.dropout(p, p=dropout_p, training=True)
     out = torch.matmul(p.unsqueeze(-2), vsel).squeeze(-2)                 # [B,H,Q,D]
     return out.transpose(1, 2).to(value.dtype)
 
@@ -601,8 +604,8 @@ class TopKSparseKVReuseAttention(nn.Module):
     hidden_size, top_k, dropout) and forward signature.  Where autograd records
     it, the select stays on the GPU kernels and the softmax and the value sum
     take their differentiable form (``topk_kv_reuse_attention_grad``), so q_proj,
-    o_proj, the hidden states and the dense KV get their gradients; dropout on
-    the probabilities (training with dropout > 0) is not supported.
+    o_proj, the hidden states and the dense KV get their gradients; in training
+    mode with dropout > 0 the probabilities are dropped there as in the reference.
     """
 
     def __init__(self, config) -> None:
@@ -617,8 +620,6 @@ class TopKSparseKVReuseAttention(nn.Module):
 
     def forward(self, hidden_states: Tensor, dense_kv: Tuple[Tensor, Tensor], rope: Tuple[Tensor, Tensor],
                 attention_mask: Optional[Tensor]) -> Tensor:
-        if self.training and self.dropout_p > 0:
-            raise NotImplementedError("dropout on the top-k probabilities is not supported")
         B, Q, _ = hidden_states.shape
         key, value = dense_kv
         K = key.shape[-2]
@@ -639,9 +640,10 @@ class TopKSparseKVReuseAttention(nn.Module):
         query = query * c + torch.cat((-query[..., half:], query[..., :half]), dim=-1) * s
         grad = torch.is_grad_enabled() and (hidden_states.requires_grad or key.requires_grad or
                                             value.requires_grad or any(p.requires_grad for p in self.parameters()))
-        if grad:
+        drop = self.dropout_p if self.training else 0.0
+        if grad or drop > 0:
             attended = topk_kv_reuse_attention_grad(query, key.to(query.dtype), value.to(query.dtype), self.top_k,
-                                                    attention_mask)
+                                                    attention_mask, dropout_p=drop)
         else:
             attended, _, _ = topk_kv_reuse_attention(query.contiguous(), key.to(query.dtype), value.to(query.dtype),
                                                      self.top_k, attention_mask)

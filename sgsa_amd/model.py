@@ -280,8 +280,8 @@ class SGSABlock(nn.Module):
             raise ValueError(f"linear_backend must be one of {sorted(_STATE_BACKENDS)}, got {config.linear_backend!r}")
         if config.retrieval_backend not in ("auto", "torch", "flash_moba"):
             raise ValueError(f"retrieval_backend must be auto, torch or flash_moba, got {config.retrieval_backend!r}")
-        if config.dropout != 0.0:
-            raise ValueError("dropout is a training feature; the forward here is inference only")
+        if not 0.0 <= config.dropout < 1.0:
+            raise ValueError(f"dropout must be in [0, 1), got {config.dropout}")
         self.config = config
         H, D, C = config.num_attention_heads, config.head_dim, config.hidden_size
         self.num_heads, self.head_dim = H, D
@@ -383,6 +383,8 @@ class SGSABlock(nn.Module):
         out = self.o_proj(att.reshape(B, T, C))
         if cfg.sparse_output_lambda > 0:
             out = out + cfg.sparse_output_lambda * self.sparse_out_proj(vh.reshape(B, T, C))
+        if self.training and cfg.dropout > 0:   # the residual branch's dropout (:651, :695)
+            out = F.dropout(out, p=cfg.dropout, training=True)
         h, n = self.post_attn_norm.add_forward(h, out)
         h = h + self.mlp(n)
         rs = stats["row_stats"]

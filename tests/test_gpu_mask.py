@@ -296,3 +296,16 @@ def test_kv_reuse_module_matches_reference_formula(dev):
                             ("value", val_g.grad, val_c.grad)):
         assert got is not None, f"{name}: no gradient"
         close(got, want, 1e-4, f"gradient of {name}")
+    # dropout on the probabilities in training mode (hybrid_dense_delta_topk.py:351): eval
+    # unchanged, training random but reproducible under a seed
+    md = sgsa_amd.TopKSparseKVReuseAttention(SimpleNamespace(num_attention_heads=H, head_dim=D, hidden_size=C,
+                                                             top_k=k, dropout=0.5)).to(dev)
+    md.load_state_dict(m.state_dict())
+    with torch.no_grad():
+        assert torch.equal(md.eval()(hs, (key, val), rope, am.to(dev)), m(hs, (key, val), rope, am.to(dev)))
+        md.train()
+        ys = []
+        for seed in (1, 1, 2):
+            torch.manual_seed(seed)
+            ys.append(md(hs, (key, val), rope, am.to(dev)))
+    assert torch.isfinite(ys[0]).all() and torch.equal(ys[0], ys[1]) and not torch.equal(ys[0], ys[2])

@@ -228,3 +228,26 @@ def test_model_gradients_match_oracle(dev, mode, write_mode, lam, mask):
         for proj in ("q_ret_proj", "budget_proj", "k_proj", "v_proj"):
             assert float(named[f"layers.{i}.{proj}.weight"].grad.abs().max()) > 0, proj
 
+
+
+def test_model_dropout_on_the_attention_branch(dev):
+    # config.dropout drops the attention branch before the residual add in training mode
+    # (modeling_sgsa.py:651, :695); eval mode is the dropout-free model bit for bit
+    kw = dict(vocab_size=64, hidden_size=128, intermediate_size=128, num_hidden_layers=2, num_attention_heads=2,
+              num_kv_heads=2, max_position_embeddings=64, top_k=8, retrieval_mode="token_only")
+    _, m0 = _model(dev, torch.float32, **kw)
+    _, md = _model(dev, torch.float32, dropout=0.3, **kw)
+    md.load_state_dict(m0.state_dict())
+    ids = torch.randint(1, 64, (2, 40), generator=torch.Generator().manual_seed(3)).to(dev)
+    with torch.no_grad():
+        assert torch.equal(md.eval()(ids)["logits"], m0.eval()(ids)["logits"])
+    md.train()
+    losses = []
+    for seed in (5, 5, 6):
+        torch.manual_seed(seed)
+        md.zero_grad()
+        out = md(ids, labels=ids)
+        out["loss"].backward()
+        assert torch.isfinite(out["loss"]) and md.layers[0].q_ret_proj.weight.grad is not None
+        losses.append(out["loss"].item())
+    assert losses[0] == losses[1] and losses[0] != losses[2], losses
