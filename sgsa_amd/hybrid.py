@@ -24,7 +24,8 @@ sgsa_amd.model.SGSABlock on the HIP kernels) as the sparse layer.
 No right-hand operand of an attention product is a transposed view: scores
 are Q K^T with K^T copied contiguous (prefill) or K Q^T with Q^T copied
 contiguous (decode), and the values are a row-major slice of the cache.
-Inference only.
+The decoder (prefill, decode) is inference only; TopKSparseKVReuseAttention
+also trains (its differentiable form under autograd).
 """
 
 from __future__ import annotations
