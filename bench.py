@@ -2,7 +2,7 @@
 """SGSA layer-forward benchmark on one MI355X.
 
     python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--no-cpu-baseline] [--no-other-configs]
-                    [--workload layer|model|hybrid|block|backward]
+                    [--workload layer|model|hybrid|block|backward|train]
 
 A step is one SGSA layer forward over the batch at the north-star shape
 (B=1, H=16, T=32768, d=128, top-k=2048, chunk 64, bf16 inputs, fp32 state),
@@ -347,6 +347,91 @@ def run_model(args) -> int:
     return 0
 
 
+TRAIN_METRIC = ("SGSA 2-layer model training tokens/s (config-2 shape: fp32, AdamW, B=16, T=4096, hidden 1024, "
+                "8x128 heads, vocab 8192, block_token)")
+
+
+def run_train(args) -> int:
+    """Training steps of the config-2 model as the reference's experiment runs them
+    (experiments/run_sgsa_synthetic_retrieval.py:100-117: fp32 parameters, AdamW, forward with
+    labels, backward, optimizer step), with the reference config's default block_token
+    retrieval: per step the forward, the backward through the retrieval's differentiable form
+    and the native chunk backward, and the AdamW update."""
+    import sgsa_amd
+    B, T = 16, 4096
+    dev = torch.device("cuda:0")
+    ids = recall_batch(B, T, 8192).to(dev)
+    cfg = sgsa_amd.SGSAConfig(vocab_size=8192, hidden_size=1024, intermediate_size=2816, num_hidden_layers=2,
+                              num_attention_heads=8, num_kv_heads=8, max_position_embeddings=T, top_k=16,
+                              retrieval_mode="block_token")
+    model = sgsa_amd.SGSAForCausalLM(cfg)
+    model.init_weights(std=0.02, qk_std=1.0 / math.sqrt(cfg.hidden_size * cfg.head_dim),
+                       generator=torch.Generator().manual_seed(0))
+    model = model.to(device=dev).train()
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-4)
+
+    def step():
+        loss = model(ids, labels=ids)["loss"]
+        opt.zero_grad(set_to_none=True)
+        loss.backward()
+        opt.step()
+        return loss
+
+    log(f"train: config-2 shape, fp32, B={B} T={T}, warmup {args.warmup}")
+    for _ in range(args.warmup):
+        loss = step()
+    torch.cuda.synchronize()
+    cur = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(cur)
+    for _ in range(args.steps):
+        loss = step()
+    e1.record(cur)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / max(args.steps, 1)
+    if not torch.isfinite(loss):
+        log("non-finite loss")
+        return 1
+    log(f"train ms/step {ms:.3f} loss {loss.item():.4f}")
+    peak = torch.cuda.max_memory_allocated() / 2**30
+    # the same steps under bf16 autocast (fp32 parameters and optimizer; the projections, the
+    # retrieval's selection and the state update in bf16)
+    for _ in range(args.warmup):
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            loss = model(ids, labels=ids)["loss"]
+        opt.zero_grad(set_to_none=True)
+        loss.backward()
+        opt.step()
+    torch.cuda.synchronize()
+    e0.record(cur)
+    for _ in range(args.steps):
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            loss = model(ids, labels=ids)["loss"]
+        opt.zero_grad(set_to_none=True)
+        loss.backward()
+        opt.step()
+    e1.record(cur)
+    torch.cuda.synchronize()
+    ms_ac = e0.elapsed_time(e1) / max(args.steps, 1)
+    if not torch.isfinite(loss):
+        log("non-finite loss under autocast")
+        return 1
+    log(f"train (bf16 autocast) ms/step {ms_ac:.3f} loss {loss.item():.4f}")
+    print(json.dumps({
+        "metric": TRAIN_METRIC, "value": round(B * T / (ms / 1000.0), 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 3), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
+        "data": "synthetic associative-recall token ids, random-init weights",
+        "config": {"workload": "sgsa_model_train", "B": B, "T": T, "hidden": 1024, "heads": 8, "head_dim": 128,
+                   "vocab": 8192, "layers": 2, "intermediate": 2816, "top_k": 16, "retrieval_mode": "block_token",
+                   "block_size": 32, "top_blocks": 2, "optimizer": "AdamW lr 1e-4",
+                   "peak_memory_gb": round(peak, 1)},
+        "bf16_autocast": {"ms_per_step": round(ms_ac, 3), "value": round(B * T / (ms_ac / 1000.0), 1)},
+        "cpu_baseline": None,
+    }), flush=True)
+    return 0
+
+
 def run_hybrid(args) -> int:
     """Config 4: the 24-layer hybrid decoder (sgsa_amd.hybrid), prefill then greedy decode: a warm-up
     prefill, the timed prefill, 4 untimed decode steps (where the decode plan is built), then the 256
@@ -544,12 +629,13 @@ def main() -> int:
                          "LDS-tiled MFMA K2 -> chunk) or K1 row lists -> per-row 16-byte gathers -> chunk")
     ap.add_argument("--torch-recompute", action="store_true",
                     help="with --workload backward: also time the torch recompute backward once")
-    ap.add_argument("--workload", choices=("layer", "model", "hybrid", "block", "backward"), default="layer",
+    ap.add_argument("--workload", choices=("layer", "model", "hybrid", "block", "backward", "train"), default="layer",
                     help="layer: the north-star SGSA layer forward (the headline metric, default); model: "
                          "config 2, the 2-layer SGSA causal LM forward at B=16 T=4096; hybrid: config 4, the "
                          "24-layer SGSA / dense-GQA decoder, prefill of 16384 tokens then 256 decode steps at B=8; "
                          "block: the retriever's block_token / block_only modes at the north-star shape; "
-                         "backward: the native backward of chunk_sgsa at the north-star shape")
+                         "backward: the native backward of chunk_sgsa at the north-star shape; train: config 2's "
+                         "model trained as the reference's experiment trains it (fp32, AdamW)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on exactly one GPU (got --gpus {args.gpus}); the SGSA layer shards by head, "
@@ -563,6 +649,8 @@ def main() -> int:
         return run_block(args)
     if args.workload == "backward":
         return run_backward(args)
+    if args.workload == "train":
+        return run_train(args)
 
     import sgsa_amd
     from sgsa_amd import _abi

@@ -585,15 +585,16 @@ def topk_kv_reuse_attention_grad(query: Tensor, key: Tensor, value: Tensor, top_
         rows = (torch.arange(B * H, device=idx.device, dtype=torch.long).view(B, H, 1, 1) * K
                 + idx.long()).reshape(-1)
         valid = valid.to(torch.bool)
-    qh = query.float().transpose(1, 2).contiguous()                       # [B,H,Q,D]
-    ksel = key.float().reshape(B * H * K, D).index_select(0, rows).view(B, H, Q, kk, D)
-    vsel = value.float().reshape(B * H * K, D).index_select(0, rows).view(B, H, Q, kk, D)
-    sc = torch.matmul(ksel, qh.unsqueeze(-1)).squeeze(-1) * (1.0 / math.sqrt(D))
-    sc = torch.where(valid, sc, torch.full_like(sc, torch.finfo(torch.float32).min))
-    p = torch.softmax(sc, dim=-1)
-    if dropout_p > 0:
-        p = torch.nn.functional.dropout(p, p=dropout_p, training=True)
-    out = torch.matmul(p.unsqueeze(-2), vsel).squeeze(-2)                 # [B,H,Q,D]
+    with torch.autocast("cuda", enabled=False):   # fp32 arithmetic also inside an autocast region
+        qh = query.float().transpose(1, 2).contiguous()                       # [B,H,Q,D]
+        ksel = key.float().reshape(B * H * K, D).index_select(0, rows).view(B, H, Q, kk, D)
+        vsel = value.float().reshape(B * H * K, D).index_select(0, rows).view(B, H, Q, kk, D)
+        sc = torch.matmul(ksel, qh.unsqueeze(-1)).squeeze(-1) * (1.0 / math.sqrt(D))
+        sc = torch.where(valid, sc, torch.full_like(sc, torch.finfo(torch.float32).min))
+        p = torch.softmax(sc, dim=-1)
+        if dropout_p > 0:
+            p = torch.nn.functional.dropout(p, p=dropout_p, training=True)
+        out = torch.matmul(p.unsqueeze(-2), vsel).squeeze(-2)                 # [B,H,Q,D]
     return out.transpose(1, 2).to(value.dtype)
 
 

@@ -138,9 +138,10 @@ def retrieve_differentiable(q_ret: Tensor, k: Tensor, v: Tensor, budget_logits: 
             idx, _, vmask, _, _, _ = score_topk_masked(q_ret.detach(), k.detach(), kk, key_mask=m, query_mask=m,
                                                        causal=True, kq_rule=0, sorted=True)
             valid = vmask.to(torch.bool)
-    s, w, k_hat, v_hat, kh = _weigh(q_ret, k, v, idx, valid, eps)
-    return _gate(k, v, kh, w, k_hat, v_hat, _top2_margin(s, valid), budget_logits, write_mode, alpha_max, tau_c,
-                 eps)
+    with torch.autocast("cuda", enabled=False):   # fp32 arithmetic also inside an autocast region
+        s, w, k_hat, v_hat, kh = _weigh(q_ret, k, v, idx, valid, eps)
+        return _gate(k, v, kh, w, k_hat, v_hat, _top2_margin(s, valid), budget_logits, write_mode, alpha_max,
+                     tau_c, eps)
 
 
 def retrieve_block_differentiable(q_ret: Tensor, k: Tensor, v: Tensor, budget_logits: Tensor, top_k: int,
@@ -188,9 +189,10 @@ def retrieve_block_differentiable(q_ret: Tensor, k: Tensor, v: Tensor, budget_lo
             for i in range(1, eb):
                 dup[..., i] = (bidx[..., :i] == bidx[..., i:i + 1]).any(dim=-1)
             valid &= ~dup.repeat_interleave(block_size, dim=-1)
-    s, w, k_hat, v_hat, kh = _weigh(q_ret, k, v, idx, valid, eps)
-    if mode == "block_token":
-        margin = _top2_margin(s, valid)
-    else:
-        margin = (bidx[..., 0] - bidx[..., 1]).float() if eb >= 2 else torch.zeros(B, H, T, device=dev)
-    return _gate(k, v, kh, w, k_hat, v_hat, margin, budget_logits, write_mode, alpha_max, tau_c, eps)
+    with torch.autocast("cuda", enabled=False):   # fp32 arithmetic also inside an autocast region
+        s, w, k_hat, v_hat, kh = _weigh(q_ret, k, v, idx, valid, eps)
+        if mode == "block_token":
+            margin = _top2_margin(s, valid)
+        else:
+            margin = (bidx[..., 0] - bidx[..., 1]).float() if eb >= 2 else torch.zeros(B, H, T, device=dev)
+        return _gate(k, v, kh, w, k_hat, v_hat, margin, budget_logits, write_mode, alpha_max, tau_c, eps)

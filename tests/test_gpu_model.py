@@ -251,3 +251,25 @@ def test_model_dropout_on_the_attention_branch(dev):
         assert torch.isfinite(out["loss"]) and md.layers[0].q_ret_proj.weight.grad is not None
         losses.append(out["loss"].item())
     assert losses[0] == losses[1] and losses[0] != losses[2], losses
+
+
+@pytest.mark.parametrize("mode", ["token_only", "block_token"])
+def test_model_trains_under_bf16_autocast(dev, mode):
+    # fp32 parameters, bf16 autocast: the projections and the retrieval's selection and state
+    # update run in bf16, the retrieval's weights and gate in fp32; loss and every gradient finite
+    kw = dict(vocab_size=64, hidden_size=256, intermediate_size=256, num_hidden_layers=2, num_attention_heads=2,
+              num_kv_heads=2, max_position_embeddings=128, top_k=16, retrieval_mode=mode, block_size=16,
+              top_blocks=2, tie_word_embeddings=False)
+    _, m = _model(dev, torch.float32, **kw)
+    m.train()
+    ids = torch.randint(1, 64, (2, 96), generator=torch.Generator().manual_seed(4)).to(dev)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        out = m(ids, labels=ids)
+    out["loss"].backward()
+    torch.cuda.synchronize()
+    assert torch.isfinite(out["loss"])
+    for name, p in m.named_parameters():
+        if "sparse_out_proj" in name:   # unused at sparse_output_lambda 0
+            continue
+        assert p.grad is not None and torch.isfinite(p.grad).all(), name
+    assert float(m.layers[0].q_ret_proj.weight.grad.abs().max()) > 0
