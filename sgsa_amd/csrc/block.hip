@@ -19,7 +19,9 @@
 //
 // Scores here are acc * (1/sqrt(D)).  bf16 inputs with D % 32 == 0: acc from
 // v_mfma_f32_16x16x32_bf16 over d in steps of 32 (the MFMA sweep and scorer);
-// otherwise acc is an fp32 fma chain over d = 0..D-1 in ascending order.  The
+// fp32 inputs with D % 16 == 0: acc from v_mfma_f32_16x16x4_f32 in the steps of
+// block_max_f32mfma_kernel; otherwise acc is an fp32 fma chain over d = 0..D-1
+// in ascending order.  The
 // block sweep and the candidate scorer of one call use the same form, so a
 // candidate's score is bit-identical to the value its block max was taken on.
 #include <float.h>
@@ -221,6 +223,162 @@ __global__ __launch_bounds__(256) void block_max_kernel(BlockArgs a, float mscal
 // select kernel never reads them.
 constexpr int BMM_KP = BLK_MAX_D + 8;
 constexpr int BMM_ROWS = 128;
+
+// fp32 form of the MFMA sweep (v_mfma_f32_16x16x4_f32), D % 16 == 0: the bf16 kernel's
+// tiles, rows, operand roles and reductions with one fp32 element per lane and k-step.
+// Step s = 4j + e of a 16x16 tile multiplies dimension 16j + 4lg + e in lane group lg, so
+// a lane's four consecutive steps read four consecutive floats of its key row (one 16-byte
+// LDS read) and of its query row (registers).  block_cand_kernel's fp32 scorer runs the
+// same steps in the same order, so a candidate's score is bit for bit the value its
+// block max was taken on.
+constexpr int BMF_KP = BLK_MAX_D + 4;   // key tile row pitch, floats
+
+template <bool REG>
+__global__ __launch_bounds__(256) void block_max_f32mfma_kernel(BlockArgs a, float mscale) {
+  __shared__ __attribute__((aligned(16))) float kt[64 * BMF_KP];
+  __shared__ float ss[REG ? 1 : 128 * 65];
+  constexpr int ROWS = 128;
+  const int D = a.D, T = a.T, H = a.H, bs = a.bs, nb = a.nb, nj = D / 16;
+  const int nrb = (T + ROWS - 1) / ROWS;
+  const int bh = blockIdx.y, b = bh / H, h = bh % H;
+  const int r0 = (nrb - 1 - (int)blockIdx.x) * ROWS;
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, lg = l >> 4, lc = l & 15;
+  const float* Q = reinterpret_cast<const float*>(a.q);
+  const float* K = reinterpret_cast<const float*>(a.k) + ((long)b * T * H + h) * D;
+  const long kstride = (long)H * D;
+
+  float4 qf[2][BLK_MAX_D / 16];
+  int qrow[2];
+#pragma unroll
+  for (int rs = 0; rs < 2; ++rs) {
+    qrow[rs] = r0 + 32 * w + 16 * rs + lc;
+#pragma unroll
+    for (int j = 0; j < BLK_MAX_D / 16; ++j) {
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (j < nj && qrow[rs] < T)
+        v = *reinterpret_cast<const float4*>(Q + ((long)(b * T + qrow[rs]) * H + h) * D + 16 * j + 4 * lg);
+      qf[rs][j] = v;
+    }
+  }
+  float* bsc = a.block_scores + (long)bh * nb * T;
+  const int kend = a.causal ? min(T, r0 + ROWS) : T;
+  if (a.fill_invalid) {
+    const int fb = (kend + bs - 1) / bs, nfill = nb - fb;
+    for (long e = tid; e < (long)ROWS * nfill; e += 256) {
+      const int t = r0 + (int)(e % ROWS);
+      if (t < T) bsc[(fb + e / ROWS) * T + t] = -FLT_MAX;
+    }
+  }
+  const uint32_t* mb = a.mask ? a.mbits + (long)b * a.nmw : nullptr;
+  bool qok[2];
+#pragma unroll
+  for (int rs = 0; rs < 2; ++rs) qok[rs] = !mb || (qrow[rs] < T && mask_bit(mb, qrow[rs]));
+
+  const int cpr = D / 4;       // 16-byte chunks per key row
+  const int nch = 64 * cpr;    // chunks per tile, <= 2048
+  float4 pf[8];
+  auto fetch = [&](int k0) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int e = tid + 256 * u, r = e / cpr, c = e % cpr, key = k0 + r;
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (e < nch && key < T) v = *reinterpret_cast<const float4*>(K + key * kstride + 4 * c);
+      pf[u] = v;
+    }
+  };
+  fetch(0);
+  for (int k0 = 0; k0 < kend; k0 += 64) {
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int e = tid + 256 * u;
+      if (e < nch) *reinterpret_cast<float4*>(kt + (e / cpr) * BMF_KP + 4 * (e % cpr)) = pf[u];
+    }
+    __syncthreads();
+    if (k0 + 64 < kend) fetch(k0 + 64);
+    const int kt_end = min(k0 + 64, T);
+    uint64_t kbits = ~0ull;
+    if (mb) {
+      const int w0 = k0 >> 5;
+      kbits = (uint64_t)mb[w0] | (w0 + 1 < a.nmw ? (uint64_t)mb[w0 + 1] << 32 : 0ull);
+    }
+    float sc[2][4][4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      f4 acc[2] = {f4_zero(), f4_zero()};
+#pragma unroll
+      for (int j = 0; j < BLK_MAX_D / 16; ++j) {
+        if (j < nj) {
+          const float4 kv = *reinterpret_cast<const float4*>(kt + (16 * kb + lc) * BMF_KP + 16 * j + 4 * lg);
+#pragma unroll
+          for (int rs = 0; rs < 2; ++rs) {
+            acc[rs] = mma_f32(kv.x, qf[rs][j].x, acc[rs]);
+            acc[rs] = mma_f32(kv.y, qf[rs][j].y, acc[rs]);
+            acc[rs] = mma_f32(kv.z, qf[rs][j].z, acc[rs]);
+            acc[rs] = mma_f32(kv.w, qf[rs][j].w, acc[rs]);
+          }
+        }
+      }
+#pragma unroll
+      for (int rs = 0; rs < 2; ++rs) {
+        const f4 v = score_of(acc[rs], mscale);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int key = k0 + 16 * kb + 4 * lg + i;
+          const bool ok = qrow[rs] < T && key < T && (!a.causal || key <= qrow[rs]) && qok[rs] &&
+                          ((kbits >> (key - k0)) & 1ull);
+          sc[rs][kb][i] = ok ? v[i] : -FLT_MAX;
+        }
+      }
+    }
+    if (REG) {
+#pragma unroll
+      for (int rs = 0; rs < 2; ++rs) {
+        float run = -FLT_MAX;
+        int cur = k0 / bs;
+        auto flush = [&](int bb) {
+          float m = fmaxf(run, __shfl_xor(run, 16, 64));
+          m = fmaxf(m, __shfl_xor(m, 32, 64));
+          if (lg == 0 && qrow[rs] < T) {
+            float* p = bsc + (long)bb * T + qrow[rs];
+            *p = bb * bs >= k0 ? m : fmaxf(*p, m);
+          }
+        };
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+          const int c0 = k0 + 16 * kb;
+          if (c0 >= kt_end) break;
+          const int bb = c0 / bs;
+          if (bb != cur) {
+            flush(cur);
+            run = -FLT_MAX;
+            cur = bb;
+          }
+          run = fmaxf(run, fmaxf(fmaxf(sc[rs][kb][0], sc[rs][kb][1]), fmaxf(sc[rs][kb][2], sc[rs][kb][3])));
+        }
+        flush(cur);
+      }
+    } else {
+#pragma unroll
+      for (int rs = 0; rs < 2; ++rs)
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) ss[(32 * w + 16 * rs + lc) * 65 + 16 * kb + 4 * lg + i] = sc[rs][kb][i];
+      __syncthreads();
+      const int bA = k0 / bs, nbt = (kt_end - 1) / bs - bA + 1;
+      for (int it = tid; it < ROWS * nbt; it += 256) {
+        const int r = it % ROWS, bb = bA + it / ROWS, t = r0 + r;
+        if (t >= T) continue;
+        const int lo = max(bb * bs, k0), hi = min(bb * bs + bs, kt_end);
+        float m = -FLT_MAX;
+        for (int key = lo; key < hi; ++key) m = fmaxf(m, ss[r * 65 + key - k0]);
+        float* p = bsc + (long)bb * T + t;
+        *p = bb * bs >= k0 ? m : fmaxf(*p, m);
+      }
+    }
+  }
+}
 
 template <bool REG>
 __global__ __launch_bounds__(256) void block_max_mfma_kernel(BlockArgs a, float mscale) {
@@ -714,7 +872,46 @@ __global__ __launch_bounds__(64) void block_cand_kernel(BlockArgs a, float mscal
     return masked ? perm[pc[bi[lo] * bs] + (c - pre[lo])] : bi[lo] * bs + (c - pre[lo]);
   };
   float m1 = -FLT_MAX;
-  if (MF) {
+  if constexpr (MF && sizeof(X) == 4) {
+    // fp32: block_max_f32mfma_kernel's steps -- step 4j + e multiplies dimension 16j + 4lg + e,
+    // A row lc = candidate c0 + lc, every B column the query -- so the scores agree bit for bit
+    const int nj = D / 16, lg = lane >> 4, lc = lane & 15;
+    const float* Qf = reinterpret_cast<const float*>(a.q) + ((long)(b * T + t) * H + h) * D;
+    const float* Kf = reinterpret_cast<const float*>(a.k);
+    float4 qa[BLK_MAX_D / 16];
+#pragma unroll
+    for (int j = 0; j < BLK_MAX_D / 16; ++j)
+      qa[j] = j < nj ? *reinterpret_cast<const float4*>(Qf + 16 * j + 4 * lg) : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int c0 = 0; c0 < ncand; c0 += 16) {
+      const int ca = c0 + lc;
+      const int key = ca < ncand ? key_of(ca) : 0;
+      const float* kp = Kf + ((long)(b * T + key) * H + h) * D;
+      f4 acc = f4_zero();
+#pragma unroll
+      for (int j = 0; j < BLK_MAX_D / 16; ++j) {
+        if (j < nj) {
+          const float4 kv = *reinterpret_cast<const float4*>(kp + 16 * j + 4 * lg);
+          acc = mma_f32(kv.x, qa[j].x, acc);
+          acc = mma_f32(kv.y, qa[j].y, acc);
+          acc = mma_f32(kv.z, qa[j].z, acc);
+          acc = mma_f32(kv.w, qa[j].w, acc);
+        }
+      }
+      const f4 sv4 = score_of(acc, mscale);
+      const float sv = lc == 0 ? sv4[0] : lc == 1 ? sv4[1] : lc == 2 ? sv4[2] : sv4[3];
+      const int c = c0 + 4 * lg + lc;
+      const int ckey = __shfl(key, 4 * lg + lc, 64);
+      if (lc < 4 && c < ncand) {
+        if (TOKEN) {
+          keys[c] = ((uint64_t)(~f32_order_key(sv)) << 32) | (uint32_t)ckey;
+        } else {
+          a.slot_idx[row * a.ks + c] = ckey;
+          a.slot_sc[row * a.ks + c] = sv;
+          m1 = fmaxf(m1, sv);
+        }
+      }
+    }
+  } else if (MF) {
     // 16 candidates per MFMA group as the A operand (row lc = candidate c0+lc),
     // every B column the query: the same operand roles and instruction
     // sequence as block_max_mfma_kernel, so the scores agree bit for bit.
@@ -886,6 +1083,12 @@ bool block_uses_mfma(const BlockArgs& a) {
   return a.dtype == DT_BF16 && a.D % 32 == 0 && aligned(a.q) && aligned(a.k);
 }
 
+// fp32 inputs with D % 16 == 0 (at most BLK_MAX_D) take the fp32 MFMA sweep and scorer
+static bool block_uses_f32_mfma(const BlockArgs& a) {
+  auto aligned = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
+  return a.dtype == DT_F32 && a.D % 16 == 0 && a.D <= BLK_MAX_D && aligned(a.q) && aligned(a.k);
+}
+
 hipError_t launch_block_select(const BlockArgs& a, hipStream_t st) {
   const float ms = score_multiplier((float)sqrt((double)a.D), 0);
   if (a.mask) {
@@ -894,7 +1097,7 @@ hipError_t launch_block_select(const BlockArgs& a, hipStream_t st) {
   }
   const dim3 g1((unsigned)((a.T + 63) / 64), (unsigned)(a.B * a.H));
   const dim3 g2((unsigned)((a.T + BMM_ROWS - 1) / BMM_ROWS), (unsigned)(a.B * a.H));
-  const bool mf = block_uses_mfma(a);
+  const bool mf = block_uses_mfma(a), mf32 = block_uses_f32_mfma(a);
   if (mf && (a.bs == 16 || a.bs == 32)) {
     // D is a multiple of 32 and at most BLK_MAX_D (block_uses_mfma, the entry points' checks)
     const dim3 gh(g2.y, g2.x);   // (B*H, row blocks)
@@ -912,6 +1115,8 @@ hipError_t launch_block_select(const BlockArgs& a, hipStream_t st) {
   }
   else if (mf && a.bs % 16 == 0) block_max_mfma_kernel<true><<<g2, 256, 0, st>>>(a, ms);
   else if (mf) block_max_mfma_kernel<false><<<g2, 256, 0, st>>>(a, ms);
+  else if (mf32 && a.bs % 16 == 0) block_max_f32mfma_kernel<true><<<g2, 256, 0, st>>>(a, ms);
+  else if (mf32) block_max_f32mfma_kernel<false><<<g2, 256, 0, st>>>(a, ms);
   else if (a.dtype == DT_F32) block_max_kernel<float><<<g1, 256, 0, st>>>(a, ms);
   else block_max_kernel<bf16_t><<<g1, 256, 0, st>>>(a, ms);
   const long rows = (long)a.B * a.H * a.T;
@@ -919,6 +1124,7 @@ hipError_t launch_block_select(const BlockArgs& a, hipStream_t st) {
   const int epv = a.dtype == DT_F32 ? 4 : 8;
   const bool vec = a.D % epv == 0 && ((uintptr_t)a.k & 15u) == 0;
   if (mf) launch_cand<bf16_t, true>(a, ms, vec, st);
+  else if (mf32) launch_cand<float, true>(a, ms, vec, st);
   else if (a.dtype == DT_F32) launch_cand<float, false>(a, ms, vec, st);
   else launch_cand<bf16_t, false>(a, ms, vec, st);
   return hipGetLastError();
