@@ -44,6 +44,7 @@ from .layer import LayerWorkspace, sgsa_layer_forward
 from . import _abi
 from .model import GatedMLP, RMSNorm, SGSABlock, SGSAConfig, fused_linear, fused_linear_out, fused_weight, lin
 from .retrieval import gather_masked, score_topk_masked
+from .retrieval_grad import MAX_SELECTED_ELEMS
 
 Tensor = torch.Tensor
 
@@ -577,6 +578,10 @@ def topk_kv_reuse_attention_grad(query: Tensor, key: Tensor, value: Tensor, top_
         raise ValueError(f"key/value must be [B,H,K,D] = {(B, H, K, D)}; got {tuple(key.shape)} / {tuple(value.shape)}")
     if Q > K:
         raise ValueError(f"{Q} queries over {K} keys: the queries are the last Q positions of the KV")
+    n = B * H * Q * min(int(top_k), K) * D
+    if n > MAX_SELECTED_ELEMS:
+        raise ValueError(f"topk_kv_reuse_attention_grad: B*H*Q*k*D = {n} selected elements exceed "
+                         f"{MAX_SELECTED_ELEMS}; train on shorter sequences or a smaller top_k")
     with torch.no_grad():
         idx, _, valid, _, _, _ = score_topk_masked(query.detach(), key.detach(), top_k, key_mask=attention_mask,
                                                    causal=True, q_offset=K - Q, scale_mode=1, kq_rule=1,
