@@ -538,7 +538,7 @@ static int sparse_gather_impl(int dtype, int B, int Tq, int Tk, int H, int D, in
                               float alpha_max, float tau_c, int local_window, int sink_size, void* k_hat,
                               void* v_hat, void* write_key, float* alpha, float* weights, float* diag,
                               float* row_stats, void* workspace, size_t workspace_bytes, void* stream,
-                              const void* rq, float rq_ms) {
+                              const void* rq, float rq_ms, const sgsa::RecurrentArgs* rec = nullptr) {
   if (kv_layout != 0 && kv_layout != 1) return fail(SGSA_ERR_INVALID_ARG, "kv_layout must be 0 ([B,Tk,H,D]) or 1 ([B,H,Tk,D])");
   if (int s = check_dtype(dtype)) return s;
   if (int s = check_dims(B, Tq, H, D)) return s;
@@ -584,7 +584,19 @@ static int sparse_gather_impl(int dtype, int B, int Tq, int Tk, int H, int D, in
       return s;
     }
   }
-  return hip_status(sgsa::launch_sparse_gather(a, (hipStream_t)stream), "sgsa_sparse_gather");
+  if (rec == nullptr) return hip_status(sgsa::launch_sparse_gather(a, (hipStream_t)stream), "sgsa_sparse_gather");
+  // K6 at T = 1 on the outputs: in the launch that merges the split rows where that form
+  // applies, else after the gather
+  auto aligned16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
+  if (a.nsplit > 0 && dtype == SGSA_BF16 && D == 128 && Tq == 1 && rec->T == 1 && diag == nullptr &&
+      weights == nullptr && aligned16(v) && (k == nullptr || aligned16(k)) &&
+      (self_key == nullptr || aligned16(self_key))) {
+    a.pieces_only = 1;
+    if (int s = hip_status(sgsa::launch_sparse_gather(a, (hipStream_t)stream), "sgsa_sparse_gather")) return s;
+    return hip_status(sgsa::launch_merge_recurrent(a, *rec, (hipStream_t)stream), "sgsa_sparse_gather (merge, K6)");
+  }
+  if (int s = hip_status(sgsa::launch_sparse_gather(a, (hipStream_t)stream), "sgsa_sparse_gather")) return s;
+  return hip_status(sgsa::launch_recurrent(*rec, (hipStream_t)stream), "sgsa_recurrent_fwd");
 }
 
 int sgsa_sparse_gather_masked(int dtype, int B, int Tq, int Tk, int H, int D, int top_k, int q_offset,
@@ -603,18 +615,19 @@ int sgsa_sparse_gather_masked(int dtype, int B, int Tq, int Tk, int H, int D, in
 }  // extern "C"
 
 namespace sgsa {
-int sparse_gather_rescored(int dtype, int B, int Tq, int Tk, int H, int D, int top_k, int q_offset, float scale,
-                           int scale_mode, const void* q, const void* k, const void* v, const void* self_key,
-                           const int32_t* indices, float* scores, const int32_t* counts, const float* budget,
-                           int write_mode, float alpha_max, float tau_c, int local_window, int sink_size,
-                           void* k_hat, void* v_hat, void* write_key, float* alpha, void* workspace,
-                           size_t workspace_bytes, void* stream) {
+int sparse_gather_stack(int dtype, int B, int Tq, int Tk, int H, int D, int top_k, int q_offset, float scale,
+                        int scale_mode, const void* q, const void* k, const void* v, const void* self_key,
+                        const int32_t* indices, float* scores, const float* top2, const int32_t* counts,
+                        const float* budget, int write_mode, float alpha_max, float tau_c, int local_window,
+                        int sink_size, void* k_hat, void* v_hat, void* write_key, float* alpha, void* workspace,
+                        size_t workspace_bytes, const RecurrentArgs* rec, void* stream) {
   if (scale_mode != 0 && scale_mode != 1) return fail(SGSA_ERR_INVALID_ARG, "scale_mode must be 0 or 1");
-  REQUIRE(q);
+  if (rec != nullptr && (rec->B != B || rec->T != Tq || rec->H != H || rec->D != D || rec->dtype != dtype))
+    return fail(SGSA_ERR_INVALID_ARG, "the recurrent update's shape differs from the gather's");
   return sparse_gather_impl(dtype, B, Tq, Tk, H, D, top_k, q_offset, 0, k, v, self_key, indices, scores, nullptr,
-                            nullptr, counts, budget, write_mode, alpha_max, tau_c, local_window, sink_size, k_hat,
+                            top2, counts, budget, write_mode, alpha_max, tau_c, local_window, sink_size, k_hat,
                             v_hat, write_key, alpha, nullptr, nullptr, nullptr, workspace, workspace_bytes, stream, q,
-                            score_multiplier(scale, scale_mode));
+                            q != nullptr ? score_multiplier(scale, scale_mode) : 0.f, rec);
 }
 }  // namespace sgsa
 

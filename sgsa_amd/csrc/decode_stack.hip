@@ -19,14 +19,17 @@
 
 namespace sgsa {
 int abi_set_error(int status, const char* msg);
-// sgsa_score_at followed by sgsa_sparse_gather (no mask), the scores computed inside the
-// split-row gather where its form allows: the same results bit for bit (api.hip)
-int sparse_gather_rescored(int dtype, int B, int Tq, int Tk, int H, int D, int top_k, int q_offset, float scale,
-                           int scale_mode, const void* q, const void* k, const void* v, const void* self_key,
-                           const int32_t* indices, float* scores, const int32_t* counts, const float* budget,
-                           int write_mode, float alpha_max, float tau_c, int local_window, int sink_size,
-                           void* k_hat, void* v_hat, void* write_key, float* alpha, void* workspace,
-                           size_t workspace_bytes, void* stream);
+// sgsa_sparse_gather (no mask) then, with rec, sgsa_recurrent_fwd on its outputs (api.hip).
+// With q, the slot scores are (q . k) * scale at the slots' keys, computed inside the
+// split-row gather where its form allows (written to scores first otherwise); where the
+// split form applies, the update runs in the launch that merges the split rows.  The results
+// equal sgsa_score_at + sgsa_sparse_gather + sgsa_recurrent_fwd bit for bit.
+int sparse_gather_stack(int dtype, int B, int Tq, int Tk, int H, int D, int top_k, int q_offset, float scale,
+                        int scale_mode, const void* q, const void* k, const void* v, const void* self_key,
+                        const int32_t* indices, float* scores, const float* top2, const int32_t* counts,
+                        const float* budget, int write_mode, float alpha_max, float tau_c, int local_window,
+                        int sink_size, void* k_hat, void* v_hat, void* write_key, float* alpha, void* workspace,
+                        size_t workspace_bytes, const RecurrentArgs* rec, void* stream);
 }
 
 namespace {
@@ -191,23 +194,20 @@ int sgsa_decode_stack(const SgsaDecodeConfig* cfg, int n_layers, const SgsaDecod
         if (int s = sgsa_score_topk(SGSA_BF16, B, 1, (int)c.cache_len, H, D, c.top_k, 1, pos, scale, 0, qr, L.k_cache,
                                     L.cand_idx, sc, top2, L.cand_cnt, nullptr, 0, ws + w.tws, w.tws_bytes, stream))
           return s;
-        if (int s = sgsa_sparse_gather(SGSA_BF16, B, 1, (int)c.cache_len, H, D, c.top_k, pos, L.k_cache, L.v_cache, k,
-                                       L.cand_idx, sc, top2, L.cand_cnt, budget, c.write_mode, c.alpha_max, c.tau_c,
-                                       64, 8, c.write_mode == 0 ? wk : nullptr, vh, c.write_mode == 1 ? wk : nullptr,
-                                       alpha, nullptr, nullptr, ws + w.gws, w.gws_bytes, stream))
-          return s;
-      } else {
-        // the kept candidates re-scored against this step's query inside the gather
-        if (int s = sgsa::sparse_gather_rescored(SGSA_BF16, B, 1, (int)c.cache_len, H, D, c.top_k, pos, scale, 0, qr,
-                                                 L.k_cache, L.v_cache, k, L.cand_idx, sc, L.cand_cnt, budget,
-                                                 c.write_mode, c.alpha_max, c.tau_c, 64, 8,
-                                                 c.write_mode == 0 ? wk : nullptr, vh,
-                                                 c.write_mode == 1 ? wk : nullptr, alpha, ws + w.gws, w.gws_bytes,
-                                                 stream))
-          return s;
       }
-      if (int s = sgsa_recurrent_fwd(SGSA_BF16, B, 1, H, D, q, k, v, beta, gamma, wk, vh, alpha, L.state, o, L.state,
-                                     stream))
+      // the gather (the kept candidates re-scored against this step's query inside it on
+      // steps that keep them), then K6 on its outputs, the state updated in place
+      sgsa::RecurrentArgs r{};
+      r.dtype = sgsa::DT_BF16; r.B = B; r.T = 1; r.H = H; r.D = D;
+      r.q = q; r.k = k; r.v = v; r.beta = beta; r.gamma = gamma;
+      r.sparse_k = wk; r.sparse_v = vh; r.alpha = alpha;
+      r.initial_state = L.state; r.out = o; r.final_state = L.state;
+      if (int s = sgsa::sparse_gather_stack(SGSA_BF16, B, 1, (int)c.cache_len, H, D, c.top_k, pos, scale, 0,
+                                            select ? nullptr : qr, L.k_cache, L.v_cache, k, L.cand_idx, sc,
+                                            select ? top2 : nullptr, L.cand_cnt, budget, c.write_mode, c.alpha_max,
+                                            c.tau_c, 64, 8, c.write_mode == 0 ? wk : nullptr, vh,
+                                            c.write_mode == 1 ? wk : nullptr, alpha, ws + w.gws, w.gws_bytes, &r,
+                                            stream))
         return s;
     } else {
       if (hipError_t e = sgsa::launch_small_gemm(n, C, L.w_in, L.b_in, B, n_dense, C, y, n_dense, st))

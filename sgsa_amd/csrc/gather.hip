@@ -20,6 +20,7 @@
 // wave keeps 2 x 16 rows of 16 B loads in flight per unrolled step.
 #include "common.h"
 #include "kernels.h"
+#include "recurrent_body.h"
 
 #include <float.h>
 
@@ -292,11 +293,12 @@ __device__ __forceinline__ void gather_slots_rescored(const GatherArgs& a, int s
   }
 }
 
+// One wave's row (over B*H*Tq) of the gather: its slots (or, SPLIT, its partials), then the
+// epilogue.  Wave-local: no LDS and no block barrier.
 template <typename X, bool VEC, bool SPLIT>
-__global__ __launch_bounds__(256) void sparse_gather_kernel(GatherArgs a, int lpr) {
+__device__ __forceinline__ void gather_row(const GatherArgs& a, long row, int lpr) {
   constexpr int NE = GatherShape<X, VEC>::NE;
   const int lane = threadIdx.x & 63;
-  const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);     // over B*H*Tq
   const long nrows = (long)a.B * a.H * a.Tq;
   if (row >= nrows) return;
   const int Tq = a.Tq, H = a.H, D = a.D, topk = a.top_k;
@@ -592,6 +594,11 @@ __global__ __launch_bounds__(256) void sparse_gather_kernel(GatherArgs a, int lp
   }
 }
 
+template <typename X, bool VEC, bool SPLIT>
+__global__ __launch_bounds__(256) void sparse_gather_kernel(GatherArgs a, int lpr) {
+  gather_row<X, VEC, SPLIT>(a, (long)blockIdx.x * 4 + (threadIdx.x >> 6), lpr);
+}
+
 // avg_distance /= max(max_index + 1, 1)  (modelings/modeling_sgsa.py:395, :401); the largest index is the
 // max over the GATHER_MAXIDX_SLOTS words the rows spread their atomics over.
 __global__ __launch_bounds__(256) void finish_diag_kernel(float* __restrict__ avgd, long n,
@@ -688,6 +695,26 @@ __global__ __launch_bounds__(256) void gather_part_kernel(GatherArgs a, int lpr)
   }
 }
 
+// Decode step (T = 1): wave 0 of each block merges its row's partials and writes the write
+// key, v_hat and alpha (gather_row: the merge kernel's arithmetic; the CS column blocks of a
+// row write the same values), then the block runs K6's update of its state columns on them
+// (recurrent_body), as sparse_gather_kernel followed by recurrent_kernel compute them.
+template <int CS>
+__global__ __launch_bounds__(256) void merge_recurrent_kernel(GatherArgs g, RecurrentArgs r) {
+  if (threadIdx.x < 64) gather_row<bf16_t, true, true>(g, (long)blockIdx.x, 16);
+  __syncthreads();
+  recurrent_body<bf16_t, true, CS>(r);
+}
+
+hipError_t launch_merge_recurrent(const GatherArgs& g, const RecurrentArgs& r, hipStream_t st) {
+  if (g.dtype != DT_BF16 || g.D != 128 || g.Tq != 1 || g.nsplit <= 0 || r.T != 1 || r.dtype != DT_BF16 ||
+      r.D != 128 || r.B != g.B || r.H != g.H || r.sparse_k == nullptr || g.diag != nullptr || g.weights != nullptr)
+    return hipErrorInvalidValue;
+  if (r.B * r.H < 256) merge_recurrent_kernel<4><<<dim3((unsigned)(r.B * r.H), 4), 256, 0, st>>>(g, r);
+  else merge_recurrent_kernel<1><<<dim3((unsigned)(r.B * r.H), 1), 256, 0, st>>>(g, r);
+  return hipGetLastError();
+}
+
 hipError_t launch_sparse_gather(const GatherArgs& a, hipStream_t st) {
   const long nrows = (long)a.B * a.H * a.Tq;
   const dim3 grid((unsigned)((nrows + 3) / 4));
@@ -714,6 +741,7 @@ hipError_t launch_sparse_gather(const GatherArgs& a, hipStream_t st) {
     }
   }
   const bool sp = a.nsplit > 0;
+  if (sp && a.pieces_only) return hipGetLastError();
   if (vec) {
     int lpr = 1;
     while (lpr * epv < a.D) lpr <<= 1;

@@ -195,6 +195,7 @@ struct GatherArgs {
                              // scores (q . k) * rq_ms the partial kernel computes from the key rows it gathers
                              // (scores is then not read), or nullptr
   float rq_ms;
+  int pieces_only;           // split-row form: launch the partial kernel only (the caller merges)
 };
 
 // Split-row gather: used for at most GATHER_SPLIT_ROWS rows with more than
@@ -289,6 +290,9 @@ hipError_t launch_decode_attn(int dtype, int B, int H, int Hkv, const void* q, c
 hipError_t launch_block_scores_transpose(const float* src, int B, int H, int T, int nb, float* dst, hipStream_t st);
 hipError_t launch_block_dense_weights(int B, int H, int T, int ks, const int32_t* idx, const float* w,
                                       const int32_t* counts, float* dense, hipStream_t st);
+// The split-row gather's merge of each row, then K6 at T = 1 on its outputs, in one launch
+// (bf16, D = 128, r.sparse_k / sparse_v / alpha = g.write_key or k_hat / v_hat / alpha).
+hipError_t launch_merge_recurrent(const GatherArgs& g, const RecurrentArgs& r, hipStream_t st);
 hipError_t launch_sparse_gather(const GatherArgs& a, hipStream_t st);
 // Scores of given keys (top-k reuse across decode steps): scores[r, i] =
 // (q_r . k[indices[r, i]]) * mscale for i < counts[r].
