@@ -69,6 +69,8 @@ SIGNATURES = {
     "sgsa_rms_norm": (_I, [_I, _I, ctypes.c_long, _I, _P, _P, _F, _P, _P]),
     "sgsa_add_rms_norm": (_I, [_I, _I, ctypes.c_long, _I, _P, _P, _P, _P, _F, _P, _P]),
     "sgsa_linear_rows": (_I, [_I, _I, _I, _I, _P, ctypes.c_long, _P, _P, _P, ctypes.c_long, _P]),
+    "sgsa_linear_rows_tile": (_I, [_I, _I, _I, _P, _P, _P]),
+    "sgsa_linear_rows_tiled": (_I, [_I, _I, _I, _I, _P, ctypes.c_long, _P, _P, _P, ctypes.c_long, _P]),
     "sgsa_silu_mul": (_I, [_I, ctypes.c_long, _I, _P, ctypes.c_long, _P, _P]),
     "sgsa_layer_gates": (_I, [_I, ctypes.c_long, _I, _P, ctypes.c_long, _P, _P, _P, _P]),
     "sgsa_rope_qk": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _P, ctypes.c_long, _P, _P, _P, _P, _P]),

@@ -919,6 +919,35 @@ int sgsa_linear_rows(int dtype, int M, int N, int K, const void* x, long x_row_s
                     "sgsa_linear_rows");
 }
 
+int sgsa_linear_rows_tile(int dtype, int N, int K, const void* weight, void* tiled, void* stream) {
+  if (int s = check_dtype(dtype)) return s;
+  if (dtype != SGSA_BF16) return fail(SGSA_ERR_UNSUPPORTED, "sgsa_linear_rows_tile takes bf16");
+  if (N <= 0 || K <= 0) return fail(SGSA_ERR_INVALID_ARG, "N=%d K=%d must be positive", N, K);
+  if (K % 32 != 0) return fail(SGSA_ERR_UNSUPPORTED, "K=%d must be a multiple of 32", K);
+  if ((long)((N + 15) / 16) * (K / 32) * 64 > 0x7fffffffL * 256L) return fail(SGSA_ERR_UNSUPPORTED, "N * K exceeds the grid");
+  REQUIRE(weight); REQUIRE(tiled);
+  if (((uintptr_t)weight | (uintptr_t)tiled) % 16 != 0)
+    return fail(SGSA_ERR_INVALID_ARG, "weight and tiled must be 16-byte aligned");
+  return hip_status(sgsa::launch_tile_rows(weight, N, K, tiled, (hipStream_t)stream), "sgsa_linear_rows_tile");
+}
+
+int sgsa_linear_rows_tiled(int dtype, int M, int N, int K, const void* x, long x_row_stride, const void* tiled,
+                           const void* bias, void* y, long y_row_stride, void* stream) {
+  if (int s = check_dtype(dtype)) return s;
+  if (dtype != SGSA_BF16) return fail(SGSA_ERR_UNSUPPORTED, "sgsa_linear_rows_tiled takes bf16");
+  if (M < 0 || M > 16 || N <= 0 || K <= 0) return fail(SGSA_ERR_INVALID_ARG, "M=%d (<= 16) N=%d K=%d", M, N, K);
+  if (K % 32 != 0) return fail(SGSA_ERR_UNSUPPORTED, "K=%d must be a multiple of 32", K);
+  if (x_row_stride < K || x_row_stride % 8 != 0 || y_row_stride < N)
+    return fail(SGSA_ERR_INVALID_ARG, "x_row_stride=%ld (>= K, multiple of 8) y_row_stride=%ld (>= N)", x_row_stride,
+                y_row_stride);
+  if (M == 0) return SGSA_OK;
+  REQUIRE(x); REQUIRE(tiled); REQUIRE(y);
+  if (((uintptr_t)x | (uintptr_t)tiled) % 16 != 0) return fail(SGSA_ERR_INVALID_ARG, "x and tiled must be 16-byte aligned");
+  return hip_status(sgsa::launch_small_gemm(x, x_row_stride, tiled, bias, M, N, K, y, y_row_stride, (hipStream_t)stream,
+                                            nullptr, 0, true),
+                    "sgsa_linear_rows_tiled");
+}
+
 int sgsa_silu_mul(int dtype, long rows, int I, const void* gate_up, long row_stride, void* y, void* stream) {
   if (int s = check_dtype(dtype)) return s;
   if (rows < 0 || I <= 0 || row_stride < 2L * I) return fail(SGSA_ERR_INVALID_ARG, "rows=%ld I=%d row_stride=%ld", rows, I, row_stride);

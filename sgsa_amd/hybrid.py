@@ -399,6 +399,7 @@ class HybridForCausalLM(nn.Module):
                 int(select or not plan["primed"]), ctypes.c_void_p(plan["ws_ptr"]), plan["ws_bytes"],
                 _abi.stream_of(hb)))
             plan["primed"] = True
+            return self._head_tiled(h, plan)[:, 0]
         else:
             for layer, cache in zip(self.layers, caches):
                 if isinstance(layer, DenseGQABlock):
@@ -467,10 +468,12 @@ class HybridForCausalLM(nn.Module):
             L = layers[i]
             L.kind = 1 if dense else 0
             L.input_norm, L.post_norm = layer.input_norm.weight.data_ptr(), layer.post_attn_norm.weight.data_ptr()
+            # the stack's linears read their weights tiled (one wave step's operand in one 1 KB piece)
+            w_in, w_o, w_gu, w_down = (_tile_rows(w) for w in (w_in, w_o, w_gu, w_down))
             L.w_in, L.b_in = w_in.data_ptr(), (b_in.data_ptr() if b_in is not None else None)
             L.w_o, L.b_o = w_o.data_ptr(), (b_o.data_ptr() if b_o is not None else None)
             L.w_gu, L.w_down = w_gu.data_ptr(), w_down.data_ptr()
-            keep += [w_in, b_in, w_gu]
+            keep += [w_in, b_in, w_o, b_o, w_gu, w_down]
             if dense:
                 if not (ok(cache["k"], (B, Hkv, T_max, D)) and ok(cache["v"], (B, Hkv, T_max, D))):
                     return None
@@ -486,6 +489,10 @@ class HybridForCausalLM(nn.Module):
             L.k_cache, L.v_cache = cache["k"].data_ptr(), cache["v"].data_ptr()
         cos, sin = rope[0].float().contiguous(), rope[1].float().contiguous()
         keep += [cos, sin]
+        lm_w, lm_b = self.lm_head.weight, self.lm_head.bias
+        lm = None
+        if ok(lm_w, (cfg.vocab_size, C)) and (lm_b is None or ok(lm_b, (cfg.vocab_size,))):
+            lm = _tile_rows(lm_w)
         c = _abi.SgsaDecodeConfig(B=B, C=C, H=H, Hkv=Hkv, D=D, I=I, top_k=cfg.top_k,
                                   write_mode=0 if cfg.sgsa_write_mode == "direct" else 1, alpha_max=cfg.alpha_max,
                                   tau_c=cfg.tau_c, eps=self.layers[0].input_norm.eps,
@@ -496,7 +503,28 @@ class HybridForCausalLM(nn.Module):
         ws = torch.empty(nb.value + 256, device=caches[0]["k"].device, dtype=torch.uint8)
         keep.append(ws)
         return {"cfg": c, "layers": layers, "keep": keep, "ws_ptr": (ws.data_ptr() + 255) // 256 * 256,
-                "ws_bytes": nb.value}
+                "ws_bytes": nb.value, "lm": lm}
+
+    def _head_tiled(self, h: Tensor, plan: dict) -> Tensor:
+        """_head on the plan's tiled LM-head weight (sgsa_linear_rows_tiled: the same bits)."""
+        if plan["lm"] is None:
+            return self._head(h)
+        n = self.norm(h)
+        B, C = n.shape[0], n.shape[-1]
+        V = self.lm_head.out_features
+        y = torch.empty(B, 1, V, device=n.device, dtype=n.dtype)
+        _abi.check(_abi.lib().sgsa_linear_rows_tiled(
+            _abi.SGSA_BF16, B, V, C, _abi.ptr(n), C, _abi.ptr(plan["lm"]), _abi.ptr(self.lm_head.bias), _abi.ptr(y),
+            V, _abi.stream_of(n)))
+        return y
+
+
+def _tile_rows(w: Tensor) -> Tensor:
+    """w [N, K] bf16 in sgsa_linear_rows_tile's layout (16 ceil(N / 16) K elements)."""
+    N, K = w.shape
+    out = torch.empty(16 * ((N + 15) // 16) * K, device=w.device, dtype=w.dtype)
+    _abi.check(_abi.lib().sgsa_linear_rows_tile(_abi.SGSA_BF16, N, K, _abi.ptr(w), _abi.ptr(out), _abi.stream_of(w)))
+    return out
 
 
 def expand_caches(caches: List[dict], B: int) -> List[dict]:

@@ -199,3 +199,33 @@ def test_linear_rows_equals_f_linear(dev, M, N, K, bias):
     assert got.shape == (M, N) and got.dtype == torch.bfloat16
     err = ((got.float() - want).abs().max() / want.abs().max()).item()
     assert err <= 8e-3, f"{err:.3e}"
+
+
+@pytest.mark.parametrize("M", [1, 8, 16])
+@pytest.mark.parametrize("N,K,bias", [(16, 64, False), (100, 2048, True), (2096, 2048, False), (2048, 5632, False),
+                                      (40, 5632, True)])
+def test_linear_rows_tiled_equals_linear_rows(dev, M, N, K, bias):
+    # sgsa_linear_rows_tile's layout against a torch permutation of the zero-padded weight
+    # ([tiles, 16 rows, K/32 steps, 4 pieces, 8] -> [tiles, steps, pieces, rows, 8]), and
+    # sgsa_linear_rows_tiled against sgsa_linear_rows bit for bit
+    from sgsa_amd import _abi
+    from sgsa_amd.model import linear_rows
+    g = torch.Generator().manual_seed(M * 13 + N + K)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16).to(dev)
+    w = (torch.randn(N, K, generator=g) / K ** 0.5).to(torch.bfloat16).to(dev)
+    b = torch.randn(N, generator=g).to(torch.bfloat16).to(dev) if bias else None
+    tiles = (N + 15) // 16
+    tiled = torch.full((16 * tiles * K,), 7.0, device=dev, dtype=torch.bfloat16)
+    lib = _abi.lib()
+    _abi.check(lib.sgsa_linear_rows_tile(_abi.SGSA_BF16, N, K, _abi.ptr(w), _abi.ptr(tiled), _abi.stream_of(w)))
+    wp = torch.zeros(16 * tiles, K, device=dev, dtype=torch.bfloat16)
+    wp[:N] = w
+    want_t = wp.view(tiles, 16, K // 32, 4, 8).permute(0, 2, 3, 1, 4).reshape(-1)
+    y = torch.full((M, N), 3.0, device=dev, dtype=torch.bfloat16)
+    _abi.check(lib.sgsa_linear_rows_tiled(_abi.SGSA_BF16, M, N, K, _abi.ptr(x), K, _abi.ptr(tiled), _abi.ptr(b),
+                                          _abi.ptr(y), N, _abi.stream_of(x)))
+    with torch.no_grad():
+        want = linear_rows(x, w, b)
+    torch.cuda.synchronize()
+    assert torch.equal(tiled, want_t)
+    assert torch.equal(y, want)
