@@ -295,7 +295,9 @@ __device__ __forceinline__ void gather_slots_rescored(const GatherArgs& a, int s
 
 // One wave's row (over B*H*Tq) of the gather: its slots (or, SPLIT, its partials), then the
 // epilogue.  Wave-local: no LDS and no block barrier.
-template <typename X, bool VEC, bool SPLIT>
+// PA: the split partials are 16-byte aligned (the launcher checks a.part), so their row pieces
+// load 16 bytes at a time.
+template <typename X, bool VEC, bool SPLIT, bool PA = false>
 __device__ __forceinline__ void gather_row(const GatherArgs& a, long row, int lpr) {
   constexpr int NE = GatherShape<X, VEC>::NE;
   const int lane = threadIdx.x & 63;
@@ -374,21 +376,48 @@ __device__ __forceinline__ void gather_row(const GatherArgs& a, long row, int lp
       // every load first: lane c < ns the header of partial c; lane group g the row-vector
       // pieces of partials g, g + ng, .. (at most SPG); then the same sums in the same
       // order as the loops below
+      // 16-byte loads where the partials allow them (PA; VEC: a lane's NE elements are
+      // consecutive, D and the partial stride multiples of 4); the same values either way
+      constexpr bool f4 = PA && VEC && NE % 4 == 0;
       float hm = -INFINITY, hs = 0.f, h1 = -FLT_MAX, h2 = -FLT_MAX;
       if (lane < ns) {
         const float* pc = P + lane * pst;
-        hm = pc[0]; hs = pc[1]; h1 = pc[2]; h2 = pc[3];
+        if constexpr (f4) {
+          const float4 hv = *reinterpret_cast<const float4*>(pc);
+          hm = hv.x; hs = hv.y; h1 = hv.z; h2 = hv.w;
+        } else {
+          hm = pc[0]; hs = pc[1]; h1 = pc[2]; h2 = pc[3];
+        }
       }
       float pk[SPG][NE], pvv[SPG][NE];
+      if constexpr (f4) {
+        const int d0 = elem_d<X, VEC>(sub, 0, lpr);   // the lane's NE elements d0 .. d0 + NE - 1
+        const bool in = d0 < D;
 #pragma unroll
-      for (int u = 0; u < SPG; ++u) {
-        const int c = min(grp + ng * u, ns - 1);
-        const float* pc = P + c * pst;
+        for (int u = 0; u < SPG; ++u) {
+          const int c = min(grp + ng * u, ns - 1);
+          const float* pc = P + c * pst + 4 + (in ? d0 : 0);
 #pragma unroll
-        for (int i = 0; i < NE; ++i) {
-          const int d = min(elem_d<X, VEC>(sub, i, lpr), D - 1);
-          pk[u][i] = pc[4 + d];
-          pvv[u][i] = pc[4 + D + d];
+          for (int i4 = 0; i4 < NE / 4; ++i4) {
+            const uint4 kv = *reinterpret_cast<const uint4*>(pc + 4 * i4);
+            const uint4 vv = *reinterpret_cast<const uint4*>(pc + D + 4 * i4);
+            pk[u][4 * i4] = __uint_as_float(kv.x); pk[u][4 * i4 + 1] = __uint_as_float(kv.y);
+            pk[u][4 * i4 + 2] = __uint_as_float(kv.z); pk[u][4 * i4 + 3] = __uint_as_float(kv.w);
+            pvv[u][4 * i4] = __uint_as_float(vv.x); pvv[u][4 * i4 + 1] = __uint_as_float(vv.y);
+            pvv[u][4 * i4 + 2] = __uint_as_float(vv.z); pvv[u][4 * i4 + 3] = __uint_as_float(vv.w);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int u = 0; u < SPG; ++u) {
+          const int c = min(grp + ng * u, ns - 1);
+          const float* pc = P + c * pst;
+#pragma unroll
+          for (int i = 0; i < NE; ++i) {
+            const int d = min(elem_d<X, VEC>(sub, i, lpr), D - 1);
+            pk[u][i] = pc[4 + d];
+            pvv[u][i] = pc[4 + D + d];
+          }
         }
       }
       if (!fixed_max) mrun = wave_max(hm);
@@ -594,9 +623,9 @@ __device__ __forceinline__ void gather_row(const GatherArgs& a, long row, int lp
   }
 }
 
-template <typename X, bool VEC, bool SPLIT>
+template <typename X, bool VEC, bool SPLIT, bool PA = false>
 __global__ __launch_bounds__(256) void sparse_gather_kernel(GatherArgs a, int lpr) {
-  gather_row<X, VEC, SPLIT>(a, (long)blockIdx.x * 4 + (threadIdx.x >> 6), lpr);
+  gather_row<X, VEC, SPLIT, PA>(a, (long)blockIdx.x * 4 + (threadIdx.x >> 6), lpr);
 }
 
 // avg_distance /= max(max_index + 1, 1)  (modelings/modeling_sgsa.py:395, :401); the largest index is the
@@ -699,9 +728,9 @@ __global__ __launch_bounds__(256) void gather_part_kernel(GatherArgs a, int lpr)
 // key, v_hat and alpha (gather_row: the merge kernel's arithmetic; the CS column blocks of a
 // row write the same values), then the block runs K6's update of its state columns on them
 // (recurrent_body), as sparse_gather_kernel followed by recurrent_kernel compute them.
-template <int CS>
+template <int CS, bool PA>
 __global__ __launch_bounds__(256) void merge_recurrent_kernel(GatherArgs g, RecurrentArgs r) {
-  if (threadIdx.x < 64) gather_row<bf16_t, true, true>(g, (long)blockIdx.x, 16);
+  if (threadIdx.x < 64) gather_row<bf16_t, true, true, PA>(g, (long)blockIdx.x, 16);
   __syncthreads();
   recurrent_body<bf16_t, true, CS>(r);
 }
@@ -710,8 +739,15 @@ hipError_t launch_merge_recurrent(const GatherArgs& g, const RecurrentArgs& r, h
   if (g.dtype != DT_BF16 || g.D != 128 || g.Tq != 1 || g.nsplit <= 0 || r.T != 1 || r.dtype != DT_BF16 ||
       r.D != 128 || r.B != g.B || r.H != g.H || r.sparse_k == nullptr || g.diag != nullptr || g.weights != nullptr)
     return hipErrorInvalidValue;
-  if (r.B * r.H < 256) merge_recurrent_kernel<4><<<dim3((unsigned)(r.B * r.H), 4), 256, 0, st>>>(g, r);
-  else merge_recurrent_kernel<1><<<dim3((unsigned)(r.B * r.H), 1), 256, 0, st>>>(g, r);
+  const bool pa = ((uintptr_t)g.part & 15u) == 0;
+  const dim3 grid4((unsigned)(r.B * r.H), 4), grid1((unsigned)(r.B * r.H), 1);
+  if (r.B * r.H < 256) {
+    if (pa) merge_recurrent_kernel<4, true><<<grid4, 256, 0, st>>>(g, r);
+    else merge_recurrent_kernel<4, false><<<grid4, 256, 0, st>>>(g, r);
+  } else {
+    if (pa) merge_recurrent_kernel<1, true><<<grid1, 256, 0, st>>>(g, r);
+    else merge_recurrent_kernel<1, false><<<grid1, 256, 0, st>>>(g, r);
+  }
   return hipGetLastError();
 }
 
@@ -745,11 +781,14 @@ hipError_t launch_sparse_gather(const GatherArgs& a, hipStream_t st) {
   if (vec) {
     int lpr = 1;
     while (lpr * epv < a.D) lpr <<= 1;
+    const bool pa = sp && ((uintptr_t)a.part & 15u) == 0;
     if (a.dtype == DT_F32) {
-      if (sp) sparse_gather_kernel<float, true, true><<<grid, 256, 0, st>>>(a, lpr);
+      if (pa) sparse_gather_kernel<float, true, true, true><<<grid, 256, 0, st>>>(a, lpr);
+      else if (sp) sparse_gather_kernel<float, true, true><<<grid, 256, 0, st>>>(a, lpr);
       else sparse_gather_kernel<float, true, false><<<grid, 256, 0, st>>>(a, lpr);
     } else {
-      if (sp) sparse_gather_kernel<bf16_t, true, true><<<grid, 256, 0, st>>>(a, lpr);
+      if (pa) sparse_gather_kernel<bf16_t, true, true, true><<<grid, 256, 0, st>>>(a, lpr);
+      else if (sp) sparse_gather_kernel<bf16_t, true, true><<<grid, 256, 0, st>>>(a, lpr);
       else sparse_gather_kernel<bf16_t, true, false><<<grid, 256, 0, st>>>(a, lpr);
     }
   } else {
