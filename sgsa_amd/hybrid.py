@@ -385,9 +385,10 @@ class HybridForCausalLM(nn.Module):
 
         Where the stack and its caches fit sgsa_decode_stack (bf16, head_dim 128, B <= 16,
         contiguous caches, top_k <= pos + 1), the whole layer loop is that one call: the
-        same launches as the per-layer path below, without its Python dispatch.  That
-        call keeps its own candidate sets (it selects on its first step) and updates
-        the SGSA states in place."""
+        same launches as the per-layer path below, without its Python dispatch, on copies
+        of the weights tiled for the few-row products (made once per plan, about the size
+        of the linears' weights; the same results bit for bit).  That call keeps its own
+        candidate sets (it selects on its first step) and updates the SGSA states in place."""
         select = step % self.config.topk_recompute_every == 0
         h = self.embed_tokens(tokens[:, None])
         plan = self._stack_plan(caches, rope, h, pos)
