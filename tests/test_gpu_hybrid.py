@@ -21,10 +21,10 @@ pytestmark = pytest.mark.gpu
 import sgsa_amd  # noqa: E402  (pure Python; the HIP library loads on first call and raises if missing)
 
 
-def _model(dev, dtype, seed=0, top_k=32):
+def _model(dev, dtype, seed=0, top_k=32, heads=2):
     from sgsa_amd.hybrid import HybridConfig, HybridForCausalLM
-    cfg = HybridConfig(vocab_size=512, hidden_size=256, intermediate_size=512, num_hidden_layers=5,
-                       num_attention_heads=2, num_kv_heads=1, top_k=top_k, topk_recompute_every=4)
+    cfg = HybridConfig(vocab_size=512, hidden_size=128 * heads, intermediate_size=512, num_hidden_layers=5,
+                       num_attention_heads=heads, num_kv_heads=heads // 2, top_k=top_k, topk_recompute_every=4)
     m = HybridForCausalLM(cfg)
     m.init_weights(0.02, qk_std=(cfg.hidden_size * cfg.head_dim) ** -0.5, generator=torch.Generator().manual_seed(seed))
     return cfg, m.to(dev, dtype).eval()
@@ -70,17 +70,19 @@ def test_hybrid_bf16_greedy_generation(dev):
     assert torch.equal(toks, toks2) and torch.equal(logits, logits2), "not deterministic"
 
 
-@pytest.mark.parametrize("top_k,T", [(32, 160), (320, 600)])
-def test_decode_stack_equals_the_per_layer_path(dev, top_k, T):
+@pytest.mark.parametrize("top_k,T,B,heads", [(32, 160, 3, 2), (320, 600, 3, 2), (320, 600, 16, 16)])
+def test_decode_stack_equals_the_per_layer_path(dev, top_k, T, B, heads):
     # sgsa_decode_stack (one call per step) against the per-layer Python path on copies of
     # the same prefilled caches: logits equal bit for bit on selecting and re-scoring steps,
     # and so are the SGSA states and caches after the last step.  top_k 320 takes the
     # split-row gather (3 partials per row, the last one short), where the stack re-scores
-    # the kept candidates inside the gather and the per-layer path scores them first
+    # the kept candidates inside the gather and merges the rows in the state update's
+    # launch, and the per-layer path scores them first; at B * heads = 256 the state
+    # update runs one workgroup per head (all columns) instead of four
     import sgsa_amd.hybrid as HY
-    cfg, m = _model(dev, torch.bfloat16, seed=6, top_k=top_k)
+    cfg, m = _model(dev, torch.bfloat16, seed=6, top_k=top_k, heads=heads)
     g = torch.Generator().manual_seed(7)
-    B, n = 3, 9
+    n = 9
     prompt = torch.randint(0, cfg.vocab_size, (B, T), generator=g).to(dev)
     toks = torch.randint(0, cfg.vocab_size, (B, n), generator=g).to(dev)
     rope = HY.rope_tables(T + n, cfg.head_dim, cfg.rope_theta, dev)
