@@ -98,6 +98,12 @@ def test_workspace_size_queries():
      "D == 128"),
     (lambda L, p: L.sgsa_score_topk_lists(1, 16, 2, 64, 4, p, p, p, p, p, p, p, 16, None),
      "workspace"),
+    (lambda L, p: L.sgsa_linear_rows_tile(1, 64, 48, p, p, None), "K=48"),
+    (lambda L, p: L.sgsa_linear_rows_tile(0, 64, 64, p, p, None), "bf16"),
+    (lambda L, p: L.sgsa_linear_rows_tile(1, 64, 64, ctypes.c_void_p(0x1008), p, None), "16-byte"),
+    (lambda L, p: L.sgsa_linear_rows_tiled(1, 17, 64, 64, p, 64, p, None, p, 64, None), "M=17"),
+    (lambda L, p: L.sgsa_linear_rows_tiled(1, 8, 64, 64, p, 60, p, None, p, 64, None), "x_row_stride"),
+    (lambda L, p: L.sgsa_linear_rows_tiled(1, 8, 64, 64, p, 64, None, None, p, 64, None), "tiled must not be NULL"),
 ])
 def test_argument_validation(call, needle):
     abi, L = _lib()
