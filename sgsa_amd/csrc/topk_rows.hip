@@ -25,7 +25,7 @@
 
 namespace sgsa {
 
-constexpr int TR_THREADS = 512;
+constexpr int TR_THREADS = 1024;
 
 // NKS = D / 32 as a template argument keeps the k-steps' loads and MFMAs free of branches.
 template <int NKS>
