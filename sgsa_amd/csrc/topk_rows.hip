@@ -3,8 +3,9 @@
 // with B*H*Tq ~ 128 rows occupies only 128 workgroups.  Here the keys of a row
 // are spread over many workgroups:
 //
-//   rows_score_kernel   grid (key chunks of 256, rows): each wave scores 64
-//                       keys on v_mfma_f32_16x16x32_bf16 with the row
+//   rows_score_kernel   grid (key chunks of 512, rows): each wave loads its 128
+//                       keys first, then scores them 16 at a time on
+//                       v_mfma_f32_16x16x32_bf16 with the row
 //                       kernel's operand roles (A = query, B = keys, d at
 //                       k-position 32s + 8lg + j, steps s in order) and its
 //                       score_of(), so the scores are bit-identical to the row
@@ -26,6 +27,7 @@
 namespace sgsa {
 
 constexpr int TR_THREADS = 1024;
+constexpr int TR_KG = 8;   // 16-key groups per wave of rows_score_kernel (all loads issued first)
 
 // NKS = D / 32 as a template argument keeps the k-steps' loads and MFMAs free of branches.
 template <int NKS>
@@ -37,7 +39,7 @@ __global__ __launch_bounds__(256) void rows_score_kernel(TopkArgs a, float mscal
   const int b = (int)(bh / H), h = (int)(bh % H);
   const int nv = a.causal ? min(Tk, qr + a.q_offset + 1) : Tk;
   const int lane = threadIdx.x & 63, lg = lane >> 4, lc = lane & 15;
-  const int k0 = blockIdx.x * 256 + 64 * (threadIdx.x >> 6);
+  const int k0 = blockIdx.x * (64 * TR_KG) + 16 * TR_KG * (threadIdx.x >> 6);
   if (k0 >= nv) return;
   const uint16_t* qp = reinterpret_cast<const uint16_t*>(a.q) + ((long)(b * Tq + qr) * H + h) * D;
   const uint16_t* kb = reinterpret_cast<const uint16_t*>(a.k) + ((long)b * Tk * H + h) * D;
@@ -45,16 +47,16 @@ __global__ __launch_bounds__(256) void rows_score_kernel(TopkArgs a, float mscal
   bf16x8 qf[NKS];
 #pragma unroll
   for (int s = 0; s < NKS; ++s) qf[s] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8*>(qp + 32 * s + 8 * lg));
-  u16x8 kr[4][NKS];
+  u16x8 kr[TR_KG][NKS];
 #pragma unroll
-  for (int g = 0; g < 4; ++g) {
+  for (int g = 0; g < TR_KG; ++g) {
     const int key = min(k0 + 16 * g + lc, nv - 1);
 #pragma unroll
     for (int s = 0; s < NKS; ++s) kr[g][s] = *reinterpret_cast<const u16x8*>(kb + key * kstride + 32 * s + 8 * lg);
   }
   float* out = sbuf + row * (long)Tk;
 #pragma unroll
-  for (int g = 0; g < 4; ++g) {
+  for (int g = 0; g < TR_KG; ++g) {
     f4 c = f4_zero();
 #pragma unroll
     for (int s = 0; s < NKS; ++s) c = mma_bf16(qf[s], __builtin_bit_cast(bf16x8, kr[g][s]), c);
@@ -236,7 +238,7 @@ size_t topk_rows_bytes(const TopkArgs& a) {
 hipError_t launch_score_topk_rows(const TopkArgs& a, float* sbuf, hipStream_t st) {
   const float ms = score_multiplier(a.scale, a.scale_mode);
   const long rows = (long)a.B * a.H * a.Tq;
-  const dim3 grid((unsigned)((a.Tk + 255) / 256), (unsigned)rows);
+  const dim3 grid((unsigned)((a.Tk + 64 * TR_KG - 1) / (64 * TR_KG)), (unsigned)rows);
   switch (a.D / 32) {   // D is a multiple of 32, at most DP_ROWS (topk_rows_bytes)
     case 1: rows_score_kernel<1><<<grid, 256, 0, st>>>(a, ms, sbuf); break;
     case 2: rows_score_kernel<2><<<grid, 256, 0, st>>>(a, ms, sbuf); break;
